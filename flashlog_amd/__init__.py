@@ -1,0 +1,20 @@
+"""flashlog_amd: FlashLog's sparse rule-propagation hot path for MI355X (gfx950).
+
+``flashlog_amd.flashlog_kernel`` mirrors the reference package
+``flashlog_kernel`` (same public names and signatures).  ``install()``
+registers it under the reference's module names so unchanged model files
+(``from flashlog_kernel.flashlog_kernel import dense_csr_sum_cuda``) use it.
+"""
+import sys
+
+__version__ = "0.1.0"
+
+
+def install():
+    """Alias ``flashlog_kernel`` and ``flashlog_kernel.flashlog_kernel`` to
+    this package's mirror (drop-in replacement of the reference package)."""
+    from . import flashlog_kernel as pkg
+    from .flashlog_kernel import flashlog_kernel as mod
+    sys.modules["flashlog_kernel"] = pkg
+    sys.modules["flashlog_kernel.flashlog_kernel"] = mod
+    return pkg

@@ -1,0 +1,99 @@
+"""ctypes binding of libflashlog_hip.so (the C-ABI declared in
+include/flashlog_hip.h).
+
+The library is loaded from this package directory only.  There is no
+fallback: if the library is missing or fails to load, every GPU entry point
+raises, so a run can never silently use another implementation.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
+ABI_VERSION = 1
+
+_lib = None
+
+
+class FlSide(ctypes.Structure):
+    """Mirror of ``fl_side`` (include/flashlog_hip.h)."""
+    _fields_ = [
+        ("edges", ctypes.c_int64),
+        ("groups", ctypes.c_int64),
+        ("col_ind", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+        ("row_group_ptr", ctypes.c_void_p),
+        ("group_rel", ctypes.c_void_p),
+        ("group_start", ctypes.c_void_p),
+        ("group_count", ctypes.c_void_p),
+        ("pull_ptr", ctypes.c_void_p),
+        ("pull_pos", ctypes.c_void_p),
+        ("pull_src", ctypes.c_void_p),
+        ("pull_rel", ctypes.c_void_p),
+        ("slot_of_pos", ctypes.c_void_p),
+        ("marks", ctypes.c_void_p),
+    ]
+
+
+_SIGS = {
+    "fl_last_error": (ctypes.c_char_p, []),
+    "fl_abi_version": (ctypes.c_int, []),
+    "fl_csr_build_side": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64] + [ctypes.c_void_p] * 11 +
+                          [ctypes.POINTER(ctypes.c_int64)]),
+    "fl_pull_index_build": (ctypes.c_int, [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 10),
+    "fl_apply_mask": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
+    "fl_mark_active": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                      ctypes.c_int64, ctypes.c_void_p]),
+    "fl_dense_topc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]),
+    "fl_dense_topc_backward": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 2),
+    "fl_dense_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
+    "fl_dense_sum_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                            ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int64,
+                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_size_t]),
+}
+
+
+def exported_symbols():
+    """Names the C-ABI header declares (the ctypes signature table)."""
+    return sorted(_SIGS)
+
+
+def lib():
+    """Load libflashlog_hip.so once; raise if it is missing or stale."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                "libflashlog_hip.so is not built (expected at %s); run "
+                "`python flashlog_amd/build.py` or __graft_entry__.build()" % LIB_PATH)
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        if handle.fl_abi_version() != ABI_VERSION:
+            raise RuntimeError("libflashlog_hip.so ABI version mismatch; rebuild it")
+        _lib = handle
+    return _lib
+
+
+def check(rc, what):
+    if rc != 0:
+        msg = lib().fl_last_error().decode(errors="replace")
+        if "nonnegative" in msg or "shape" in msg or "range" in msg:
+            raise ValueError("%s: %s" % (what, msg))
+        raise RuntimeError("%s failed (%d): %s" % (what, rc, msg))
+
+
+def stream_handle(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None and t.numel() > 0 else ctypes.c_void_p(0)

@@ -1,0 +1,132 @@
+/*
+ * flashlog_hip.h -- C-ABI of the MI355X (gfx950) FlashLog propagation library
+ * (libflashlog_hip.so).  Plain pointers and sizes only; every device pointer
+ * is a device (HBM) address, every stream is a hipStream_t passed as void*.
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to the qikunxun/FlashLog tree).
+ *
+ * Conventions
+ *   - Return value: FL_OK (0) or an FL_ERR_* code; fl_last_error() gives the
+ *     message of the last failure on the calling thread.
+ *   - No entry point allocates device memory.  Outputs and workspaces are
+ *     allocated by the caller (so allocation failures surface in the caller's
+ *     allocator, e.g. torch.cuda.OutOfMemoryError).  Workspace sizes come from
+ *     the matching *_workspace_bytes query.
+ *   - All device work is enqueued on the given stream; nothing synchronizes
+ *     the host unless stated.
+ */
+#ifndef FLASHLOG_HIP_H
+#define FLASHLOG_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FL_OK 0
+#define FL_ERR_ARG 1
+#define FL_ERR_HIP 2
+
+/* One side (ORI or INV) of the graph in device memory.  The first six
+ * fields are the reference's CSR tuple entries for that side
+ * (flashlog_kernel.py:697: col_ind, group metadata) plus the prepared
+ * CSR-ordered mask (flashlog_kernel.py:232-255).  The pull_* fields are this
+ * library's destination-major index of the same positions (built once per
+ * graph by fl_pull_index_build); marks is per-graph scratch of one byte per
+ * position, tagged with a per-call epoch. */
+typedef struct fl_side {
+    int64_t edges;                 /* M: CSR positions on this side        */
+    int64_t groups;                /* G: (source, relation) groups         */
+    const int32_t *col_ind;        /* [M] destination of each position     */
+    const float *mask;             /* [M] prepared mask, CSR order         */
+    const int32_t *row_group_ptr;  /* [E+1]                                */
+    const int16_t *group_rel;      /* [G]                                  */
+    const int32_t *group_start;    /* [G]                                  */
+    const int32_t *group_count;    /* [G]                                  */
+    const int32_t *pull_ptr;       /* [E+1] slots of each destination      */
+    const int32_t *pull_pos;       /* [M] CSR position of each slot        */
+    const int32_t *pull_src;       /* [M] source entity of each slot       */
+    const int16_t *pull_rel;       /* [M] relation of each slot            */
+    const int32_t *slot_of_pos;    /* [M] inverse of pull_pos              */
+    uint8_t *marks;                /* [M] scratch, epoch-tagged            */
+} fl_side;
+
+const char *fl_last_error(void);
+int fl_abi_version(void);
+
+/* ---- host-side graph preparation ------------------------------------- */
+
+/* Replaces csr.cpp:12-69 (build_side), called by build_csr_structure
+ * (flashlog_kernel.py:678-697).  Host arrays.  Positions are ordered by
+ * (source, relation, edge id); group arrays need capacity >= edges. */
+int fl_csr_build_side(int64_t edges, int64_t nodes, const int64_t *source,
+                      const int64_t *target, const int64_t *relation,
+                      int32_t *row_ptr, int32_t *columns, int16_t *edge_rel,
+                      int32_t *order, int32_t *group_ptr, int16_t *group_rel,
+                      int32_t *group_start, int32_t *group_count,
+                      int64_t *num_groups);
+
+/* No reference counterpart (the reference pushes with atomics): the
+ * destination-major pull index of one CSR side, host arrays.  Slots of a
+ * destination are in ascending CSR position, the order in which the
+ * reference's CPU path accumulates (flashlog.cpp:194-210). */
+int fl_pull_index_build(int64_t nodes, int64_t edges, int64_t groups,
+                        const int32_t *columns, const int32_t *row_group_ptr,
+                        const int16_t *group_rel, const int32_t *group_start,
+                        const int32_t *group_count, int32_t *pull_ptr,
+                        int32_t *pull_pos, int32_t *pull_src, int16_t *pull_rel,
+                        int32_t *slot_of_pos);
+
+/* ---- device entry points --------------------------------------------- */
+
+/* Replaces apply_mask_cuda (flashlog.cu:1291-1340):
+ * out[i] = mask[order[i]] * (weight ? sigmoid(weight[order[i]]) : 1). */
+int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool,
+                  const int32_t *order, const float *weight, float *out,
+                  int64_t nnz);
+
+/* Replaces compute_active_nodes_cuda's flag pass (flashlog.cu:1257-1284):
+ * flags[e] = 1 if any A[:, e] != 0 else 0. */
+int fl_mark_active(void *stream, const float *A, int64_t BL, int64_t E,
+                   int32_t *flags);
+
+/* Replaces _dense_topc_state (flashlog_kernel.py:814-842), the c1 entity
+ * budget: per row of A[BL, E], rows with more than c nonzeros keep their c
+ * largest nonzeros (ties at the cutoff go to the smaller entity id);
+ * out = A * keep.  row_state[BL*4] receives, per row, {over, cutoff key,
+ * last kept tied entity, nonzero count} for fl_dense_topc_backward. */
+int fl_dense_topc(void *stream, const float *A, float *out, int64_t BL,
+                  int64_t E, int64_t c, int32_t *row_state);
+
+/* Backward of the product A * keep: grad_A = grad * keep. */
+int fl_dense_topc_backward(void *stream, const float *grad, const float *A,
+                           const int32_t *row_state, float *grad_A, int64_t BL,
+                           int64_t E);
+
+/* Workspace for fl_dense_sum_forward / fl_dense_sum_backward. */
+size_t fl_dense_workspace_bytes(int64_t BL, int64_t E);
+
+/* Replaces flashlog_forward_cuda with agg_mode = sum (flashlog.cu:898-995),
+ * with the CPU path's bit-exact semantics (flashlog.cpp:151-211):
+ *   out_ind = A * w[:, n-1] (0 if wot_i);
+ *   out_ori[bl, d] = sum over kept ORI positions p (ascending) with
+ *       col[p] == d of (A[bl, src(p)] * w[bl, rel(p)]) * mask[p];
+ *   out_inv likewise with INV positions and w[bl, r_size + rel].
+ * topk_edges <= 0 or >= 2^60 disables c2 pruning (flashlog.cu:958).
+ * epoch (1..255) tags the marks of this call; the caller clears both sides'
+ * marks before reusing an epoch value. */
+int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv,
+                         const float *A, const float *w, int64_t BL, int64_t E,
+                         int64_t n, int64_t r_size, int wot_i,
+                         int64_t topk_edges, int epoch, float *out_ind,
+                         float *out_ori, float *out_inv, void *workspace,
+                         size_t workspace_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHLOG_HIP_H */

@@ -1,0 +1,475 @@
+/*
+ * flashlog_oracle.c -- CPU restatement of FlashLog's propagation arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (flashlog_amd/) links,
+ * loads or calls this file.  It is the checker that tests/, the smoke entry
+ * point and bench.py's cpu_baseline leg compare the HIP path against.
+ *
+ * Every function restates the reference's algorithm in plain C, in the same
+ * floating-point evaluation order, and cites the reference file:line it
+ * follows (paths relative to the qikunxun/FlashLog tree):
+ *
+ *   or_build_side            flashlog_kernel/source/csr.cpp:12-69
+ *   or_group_threshold       flashlog_kernel/source/flashlog.cpp:12-35
+ *   or_dense_forward         flashlog_kernel/source/flashlog.cpp:38-89,151-211
+ *   or_dense_backward        flashlog_kernel/source/flashlog.cpp:91-146,216-278
+ *   or_dense_topc            flashlog_kernel/flashlog_kernel.py:814-842
+ *   or_dense_max_forward     flashlog_kernel/source/flashlog.cu:104-121,523-637
+ *   or_filtered_ranks        flashlog_kernel/source/flashlog.cu:2754-2910
+ *
+ * Pinning (how each function is checked, see tests/test_oracle_*.py):
+ *   or_build_side, or_dense_forward, or_dense_backward: bit-compared against
+ *     the reference's own CPU sources compiled into oracle/_ref/ (Makefile.ref),
+ *     and against committed golden vectors produced from that build.
+ *   or_group_threshold: brute force (expand groups to edges, sort) on tiny inputs.
+ *   or_dense_topc: brute-force stable sort (value desc, entity asc) per row.
+ *   or_dense_max_forward: brute-force max over edges with explicit tie rule.
+ *   or_filtered_ranks: brute-force count over a dense score row.
+ *
+ * Compile with -O2 -ffp-contract=off (no FMA contraction: the reference's
+ * CPU build is ISO C++17 on x86-64 without -march, so it never fuses a*b+c).
+ */
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <math.h>
+
+/* ------------------------------------------------------------------------ */
+/* CSR side builder: csr.cpp:12-69.  Positions are ordered by (source,
+ * relation, original edge id); groups are maximal runs of equal
+ * (source, relation).  Group arrays must have capacity >= edges.          */
+int or_build_side(int64_t edges, int64_t nodes,
+                  const int64_t *source, const int64_t *target, const int64_t *relation,
+                  int32_t *row_ptr, int32_t *columns, int16_t *edge_rel, int32_t *order,
+                  int32_t *group_ptr, int16_t *group_rel, int32_t *group_start,
+                  int32_t *group_count, int64_t *num_groups)
+{
+    int64_t relations = 0;
+    for (int64_t i = 0; i < edges; ++i) {
+        if (source[i] < 0 || source[i] >= nodes || target[i] < 0 || target[i] >= nodes ||
+            relation[i] < 0 || relation[i] > 32767)
+            return -1;
+        if (relation[i] + 1 > relations) relations = relation[i] + 1;
+    }
+    /* stable bucket by relation, then stable bucket by source */
+    int64_t nb = relations > nodes ? relations : nodes;
+    int64_t *cur = (int64_t *)calloc((size_t)(nb + 1), sizeof(int64_t));
+    int32_t *by_rel = (int32_t *)malloc((size_t)(edges > 0 ? edges : 1) * sizeof(int32_t));
+    for (int64_t i = 0; i < edges; ++i) cur[relation[i]]++;
+    int64_t acc = 0;
+    for (int64_t r = 0; r < relations; ++r) { int64_t c = cur[r]; cur[r] = acc; acc += c; }
+    for (int64_t i = 0; i < edges; ++i) by_rel[cur[relation[i]]++] = (int32_t)i;
+    memset(cur, 0, (size_t)(nb + 1) * sizeof(int64_t));
+    for (int64_t i = 0; i < edges; ++i) cur[source[i]]++;
+    acc = 0;
+    for (int64_t v = 0; v < nodes; ++v) { int64_t c = cur[v]; row_ptr[v] = (int32_t)acc; cur[v] = acc; acc += c; }
+    row_ptr[nodes] = (int32_t)edges;
+    for (int64_t k = 0; k < edges; ++k) { int32_t i = by_rel[k]; order[cur[source[i]]++] = i; }
+    for (int64_t v = 0; v <= nodes; ++v) group_ptr[v] = 0;
+    int64_t g = -1;
+    for (int64_t j = 0; j < edges; ++j) {
+        int32_t i = order[j];
+        columns[j] = (int32_t)target[i];
+        edge_rel[j] = (int16_t)relation[i];
+        int fresh = (j == 0) || source[i] != source[order[j - 1]] || relation[i] != relation[order[j - 1]];
+        if (fresh) {
+            if (g >= 0) group_count[g] = (int32_t)(j - group_start[g]);
+            ++g;
+            group_start[g] = (int32_t)j;
+            group_rel[g] = (int16_t)relation[i];
+            group_ptr[source[i] + 1]++;
+        }
+    }
+    if (g >= 0) group_count[g] = (int32_t)(edges - group_start[g]);
+    for (int64_t v = 0; v < nodes; ++v) group_ptr[v + 1] += group_ptr[v];
+    *num_groups = g + 1;
+    free(cur);
+    free(by_rel);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* c2 threshold: flashlog.cpp:12-35.  Groups [begin,end) of one source row;
+ * weight of group g is weights[relations[g]].  Returns -1 when every
+ * eligible (w > 0) edge fits in the budget; otherwise the weight theta of
+ * the group holding the budget-th edge in weight-descending order, with
+ * *remaining = budget - #edges of weight > theta.                          */
+typedef struct { float w; int32_t c; } or_wc_f32;
+typedef struct { double w; int32_t c; } or_wc_f64;
+
+static int or_cmp_desc_f32(const void *a, const void *b)
+{
+    float x = ((const or_wc_f32 *)a)->w, y = ((const or_wc_f32 *)b)->w;
+    return (x < y) - (x > y);
+}
+static int or_cmp_desc_f64(const void *a, const void *b)
+{
+    double x = ((const or_wc_f64 *)a)->w, y = ((const or_wc_f64 *)b)->w;
+    return (x < y) - (x > y);
+}
+
+#define OR_DEFINE_THRESHOLD(T, SUF)                                                   \
+T or_group_threshold_##SUF(const T *weights, const int16_t *relations,               \
+                           const int32_t *sizes, int64_t begin, int64_t end,         \
+                           int64_t budget, int64_t *remaining)                       \
+{                                                                                     \
+    int64_t cnt = 0, total = 0;                                                       \
+    or_wc_##SUF *buf = (or_wc_##SUF *)malloc((size_t)((end - begin) > 0 ? (end - begin) : 1) * sizeof(or_wc_##SUF)); \
+    for (int64_t g = begin; g < end; ++g) {                                           \
+        T s = weights[relations[g]];                                                  \
+        if (s > (T)0) { buf[cnt].w = s; buf[cnt].c = sizes[g]; ++cnt; total += sizes[g]; } \
+    }                                                                                 \
+    *remaining = 0;                                                                   \
+    if (total <= budget) { free(buf); return (T)-1; }                                 \
+    qsort(buf, (size_t)cnt, sizeof(or_wc_##SUF), or_cmp_desc_##SUF);                  \
+    int64_t consumed = 0, higher = 0;                                                 \
+    T previous = (T)-1;                                                               \
+    for (int64_t k = 0; k < cnt; ++k) {                                               \
+        if (buf[k].w != previous) { higher = consumed; previous = buf[k].w; }         \
+        if (consumed + buf[k].c >= budget) {                                          \
+            *remaining = budget - higher; T th = buf[k].w; free(buf); return th;      \
+        }                                                                             \
+        consumed += buf[k].c;                                                         \
+    }                                                                                 \
+    free(buf);                                                                        \
+    return (T)-1;                                                                     \
+}
+OR_DEFINE_THRESHOLD(float, f32)
+OR_DEFINE_THRESHOLD(double, f64)
+
+/* Per-group take under the threshold: flashlog.cpp:61-77 (forward) and
+ * :117-133 (backward).  Groups of weight == theta consume a shared quota in
+ * group order; masked edges still consume it (mask is applied per edge).   */
+#define OR_TAKE(T)                                                                    \
+    int32_t take = w_val > (T)0 ? group_edge_count[g] : 0;                            \
+    if (take > 0 && threshold_weight >= 0) {                                          \
+        if (w_val < threshold_weight) take = 0;                                       \
+        else if (w_val == threshold_weight) {                                         \
+            int64_t left = keep_in_threshold - threshold_seen;                        \
+            take = left > 0 ? (int32_t)(left < group_edge_count[g] ? left : group_edge_count[g]) : 0; \
+            threshold_seen += take;                                                   \
+        }                                                                             \
+    }
+
+#define OR_DEFINE_DENSE(T, SUF)                                                       \
+static void or_forward_row_##SUF(int64_t src, int64_t bl, T a_val, const T *w,        \
+    const int32_t *row_group_ptr, const int16_t *group_rel,                           \
+    const int32_t *group_edge_start, const int32_t *group_edge_count,                 \
+    const int32_t *col_ind, const T *mask, T *out, int64_t topk_edges,                \
+    int64_t E, int64_t n, int64_t rel_offset)                                         \
+{                                                                                     \
+    int64_t g0 = row_group_ptr[src], g1 = row_group_ptr[src + 1];                     \
+    int64_t keep_in_threshold = 0;                                                    \
+    T threshold_weight = or_group_threshold_##SUF(w + bl * n + rel_offset, group_rel, \
+        group_edge_count, g0, g1, topk_edges, &keep_in_threshold);                    \
+    int64_t threshold_seen = 0;                                                       \
+    for (int64_t g = g0; g < g1; ++g) {                                               \
+        int64_t rel = group_rel[g];                                                   \
+        T w_val = w[bl * n + rel_offset + rel];                                       \
+        OR_TAKE(T)                                                                    \
+        if (take <= 0) continue;                                                      \
+        int64_t s = group_edge_start[g];                                              \
+        for (int64_t p = s; p < s + take; ++p) {                                      \
+            T m = mask[p];                                                            \
+            if (m == 0) continue;                                                     \
+            T prod = a_val * w_val;                                                   \
+            prod = prod * m;                                                          \
+            out[bl * E + col_ind[p]] += prod;                                         \
+        }                                                                             \
+    }                                                                                 \
+}                                                                                     \
+                                                                                      \
+static void or_backward_row_##SUF(int64_t src, int64_t bl, const T *grad_out,         \
+    const T *A, const T *w, const int32_t *row_group_ptr, const int16_t *group_rel,   \
+    const int32_t *group_edge_start, const int32_t *group_edge_count,                 \
+    const int32_t *col_ind, const T *mask, T *gA, T *gw, int64_t topk_edges,          \
+    int64_t E, int64_t n, int64_t rel_offset)                                         \
+{                                                                                     \
+    int64_t g0 = row_group_ptr[src], g1 = row_group_ptr[src + 1];                     \
+    int64_t keep_in_threshold = 0;                                                    \
+    T threshold_weight = or_group_threshold_##SUF(w + bl * n + rel_offset, group_rel, \
+        group_edge_count, g0, g1, topk_edges, &keep_in_threshold);                    \
+    T a_val = A[bl * E + src];                                                        \
+    int64_t threshold_seen = 0;                                                       \
+    for (int64_t g = g0; g < g1; ++g) {                                               \
+        int64_t rel = group_rel[g];                                                   \
+        T w_val = w[bl * n + rel_offset + rel];                                       \
+        OR_TAKE(T)                                                                    \
+        if (take <= 0) continue;                                                      \
+        int64_t s = group_edge_start[g];                                              \
+        for (int64_t p = s; p < s + take; ++p) {                                      \
+            T m = mask[p];                                                            \
+            if (m == 0) continue;                                                     \
+            T go = grad_out[bl * E + col_ind[p]];                                     \
+            if (go == 0) continue;                                                    \
+            T t1 = go * w_val; t1 = t1 * m;                                           \
+            gA[bl * E + src] += t1;                                                   \
+            T t2 = go * a_val; t2 = t2 * m;                                           \
+            gw[bl * n + rel_offset + rel] += t2;                                      \
+        }                                                                             \
+    }                                                                                 \
+}                                                                                     \
+                                                                                      \
+void or_dense_forward_##SUF(int64_t BL, int64_t E, int64_t n, const T *A, const T *w, \
+    const int64_t *active, int64_t num_active,                                        \
+    const int32_t *ori_col, const T *ori_mask, const int32_t *ori_gptr,               \
+    const int16_t *ori_grel, const int32_t *ori_gstart, const int32_t *ori_gcount,    \
+    const int32_t *inv_col, const T *inv_mask, const int32_t *inv_gptr,               \
+    const int16_t *inv_grel, const int32_t *inv_gstart, const int32_t *inv_gcount,    \
+    int64_t r_size, int wot_i, int64_t topk_edges, T *out_ind, T *out_ori, T *out_inv) \
+{                                                                                     \
+    for (int64_t i = 0; i < BL * E; ++i) { out_ori[i] = 0; out_inv[i] = 0; }          \
+    for (int64_t bl = 0; bl < BL; ++bl) {                                             \
+        T wid = w[bl * n + (n - 1)];                                                  \
+        for (int64_t e = 0; e < E; ++e)                                               \
+            out_ind[bl * E + e] = wot_i ? (T)0 : A[bl * E + e] * wid;                 \
+    }                                                                                 \
+    for (int64_t ai = 0; ai < num_active; ++ai) {                                     \
+        int64_t src = active[ai];                                                     \
+        for (int64_t bl = 0; bl < BL; ++bl) {                                         \
+            T a_val = A[bl * E + src];                                                \
+            if (a_val == 0) continue;                                                 \
+            or_forward_row_##SUF(src, bl, a_val, w, ori_gptr, ori_grel, ori_gstart,   \
+                ori_gcount, ori_col, ori_mask, out_ori, topk_edges, E, n, 0);         \
+            or_forward_row_##SUF(src, bl, a_val, w, inv_gptr, inv_grel, inv_gstart,   \
+                inv_gcount, inv_col, inv_mask, out_inv, topk_edges, E, n, r_size);    \
+        }                                                                             \
+    }                                                                                 \
+}                                                                                     \
+                                                                                      \
+void or_dense_backward_##SUF(int64_t BL, int64_t E, int64_t n,                        \
+    const T *grad_ind, const T *grad_ori, const T *grad_inv, const T *A, const T *w,  \
+    const int64_t *active, int64_t num_active,                                        \
+    const int32_t *ori_col, const T *ori_mask, const int32_t *ori_gptr,               \
+    const int16_t *ori_grel, const int32_t *ori_gstart, const int32_t *ori_gcount,    \
+    const int32_t *inv_col, const T *inv_mask, const int32_t *inv_gptr,               \
+    const int16_t *inv_grel, const int32_t *inv_gstart, const int32_t *inv_gcount,    \
+    int64_t r_size, int wot_i, int64_t topk_edges, T *gA, T *gw)                      \
+{                                                                                     \
+    for (int64_t i = 0; i < BL * E; ++i) gA[i] = 0;                                   \
+    for (int64_t i = 0; i < BL * n; ++i) gw[i] = 0;                                   \
+    if (!wot_i) {                                                                     \
+        for (int64_t bl = 0; bl < BL; ++bl) {                                         \
+            T wid = w[bl * n + (n - 1)];                                              \
+            T acc = 0;                                                                \
+            for (int64_t e = 0; e < E; ++e) {                                         \
+                T gi = grad_ind[bl * E + e];                                          \
+                gA[bl * E + e] += gi * wid;                                           \
+                acc += gi * A[bl * E + e];                                            \
+            }                                                                         \
+            gw[bl * n + (n - 1)] += acc;                                              \
+        }                                                                             \
+    }                                                                                 \
+    for (int64_t ai = 0; ai < num_active; ++ai) {                                     \
+        int64_t src = active[ai];                                                     \
+        for (int64_t bl = 0; bl < BL; ++bl) {                                         \
+            if (A[bl * E + src] == 0) continue;                                       \
+            or_backward_row_##SUF(src, bl, grad_ori, A, w, ori_gptr, ori_grel,        \
+                ori_gstart, ori_gcount, ori_col, ori_mask, gA, gw, topk_edges, E, n, 0); \
+            or_backward_row_##SUF(src, bl, grad_inv, A, w, inv_gptr, inv_grel,        \
+                inv_gstart, inv_gcount, inv_col, inv_mask, gA, gw, topk_edges, E, n, r_size); \
+        }                                                                             \
+    }                                                                                 \
+}
+OR_DEFINE_DENSE(float, f32)
+OR_DEFINE_DENSE(double, f64)
+
+/* ------------------------------------------------------------------------ */
+/* c1 entity budget on a dense state: flashlog_kernel.py:814-842.
+ * Per row: when #nonzero > c, keep the c largest nonzeros; at the cutoff
+ * value keep the earliest entities (cumsum rule, :835-840); the result is
+ * A * keep (so a dropped entry becomes A*0.0f).  Rows at or under the
+ * budget are untouched.  When no row is over budget the input is returned
+ * unchanged, which *changed == 0 reports.  Also returns per-row cutoff
+ * value and the last kept tied entity (E when every tie is kept; -1 for a
+ * row under budget) so the GPU's selection can be compared directly.     */
+typedef struct { float v; int32_t e; } or_ve;
+static int or_cmp_ve(const void *a, const void *b)
+{
+    const or_ve *x = (const or_ve *)a, *y = (const or_ve *)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return (x->e > y->e) - (x->e < y->e);
+}
+
+int or_dense_topc(int64_t BL, int64_t E, int64_t c, const float *A, float *out,
+                  float *cutoff, int32_t *last_tie, int *changed)
+{
+    *changed = 0;
+    memcpy(out, A, (size_t)(BL * E) * sizeof(float));
+    if (c < 0) return -1;
+    if (c >= E) { for (int64_t r = 0; r < BL; ++r) { cutoff[r] = 0.f; last_tie[r] = -1; } return 0; }
+    or_ve *buf = (or_ve *)malloc((size_t)(E > 0 ? E : 1) * sizeof(or_ve));
+    unsigned char *over = (unsigned char *)calloc((size_t)(BL > 0 ? BL : 1), 1);
+    unsigned char *keep = (unsigned char *)malloc((size_t)(E > 0 ? E : 1));
+    int any = 0;
+    for (int64_t r = 0; r < BL; ++r) {
+        int64_t nz = 0;
+        for (int64_t e = 0; e < E; ++e) if (A[r * E + e] != 0) ++nz;
+        over[r] = nz > c;
+        any |= over[r];
+        cutoff[r] = 0.f;
+        last_tie[r] = -1;
+    }
+    if (!any) { free(buf); free(over); free(keep); return 0; }
+    *changed = 1;
+    for (int64_t r = 0; r < BL; ++r) {
+        const float *row = A + r * E;
+        if (!over[r]) {
+            for (int64_t e = 0; e < E; ++e) out[r * E + e] = row[e] * 1.0f;
+            continue;
+        }
+        if (c == 0) {
+            for (int64_t e = 0; e < E; ++e) out[r * E + e] = row[e] * 0.0f;
+            continue;
+        }
+        int64_t k = 0;
+        for (int64_t e = 0; e < E; ++e) if (row[e] != 0) { buf[k].v = row[e]; buf[k].e = (int32_t)e; ++k; }
+        qsort(buf, (size_t)k, sizeof(or_ve), or_cmp_ve);
+        float cut = buf[c - 1].v;
+        int64_t above = 0, tied_total = 0;
+        for (int64_t e = 0; e < E; ++e) {
+            if (row[e] == 0) continue;
+            if (row[e] > cut) ++above; else if (row[e] == cut) ++tied_total;
+        }
+        int64_t remaining = c - above, seen = 0;
+        int32_t last = -1;
+        for (int64_t e = 0; e < E; ++e) {
+            int kp = 0;
+            if (row[e] != 0) {
+                if (row[e] > cut) kp = 1;
+                else if (row[e] == cut) { ++seen; if (seen <= remaining) { kp = 1; last = (int32_t)e; } }
+            }
+            keep[e] = (unsigned char)kp;
+        }
+        cutoff[r] = cut;
+        last_tie[r] = (remaining >= tied_total) ? (int32_t)E : last;
+        for (int64_t e = 0; e < E; ++e) out[r * E + e] = row[e] * (keep[e] ? 1.0f : 0.0f);
+    }
+    free(buf); free(over); free(keep);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Dense max aggregation forward: flashlog.cu:104-121 (packed (value, -p)
+ * CAS max: larger value wins, ties go to the smaller CSR position p) with
+ * the same source admission and c2 quota as the sum path (flashlog.cu:523-637).
+ * Untouched outputs are 0 with arg -1 (flashlog.cu:123-135: packed 0 means
+ * no contribution).  The comparison is on the raw float bits, as the
+ * reference packs __float_as_uint(value) in the high word.                  */
+static void or_max_row(int64_t src, int64_t bl, float a_val, const float *w,
+    const int32_t *gptr, const int16_t *grel, const int32_t *gstart, const int32_t *gcount,
+    const int32_t *col, const float *mask, uint64_t *packed, int64_t topk_edges,
+    int64_t E, int64_t n, int64_t off)
+{
+    int64_t g0 = gptr[src], g1 = gptr[src + 1];
+    int64_t keep_in_threshold = 0;
+    float threshold_weight = or_group_threshold_f32(w + bl * n + off, grel, gcount, g0, g1,
+                                                    topk_edges, &keep_in_threshold);
+    int64_t threshold_seen = 0;
+    for (int64_t g = g0; g < g1; ++g) {
+        int32_t *group_edge_count = (int32_t *)gcount;
+        float w_val = w[bl * n + off + grel[g]];
+        OR_TAKE(float)
+        if (take <= 0) continue;
+        float prod = a_val * w_val;
+        for (int64_t p = gstart[g]; p < gstart[g] + take; ++p) {
+            float m = mask[p];
+            if (m == 0) continue;
+            float v = prod * m;
+            uint32_t bits; memcpy(&bits, &v, 4);
+            uint64_t cand = ((uint64_t)bits << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)p);
+            uint64_t *slot = &packed[bl * E + col[p]];
+            if (cand > *slot) *slot = cand;
+        }
+    }
+}
+
+void or_dense_max_forward(int64_t BL, int64_t E, int64_t n, const float *A, const float *w,
+    const int64_t *active, int64_t num_active,
+    const int32_t *ori_col, const float *ori_mask, const int32_t *ori_gptr,
+    const int16_t *ori_grel, const int32_t *ori_gstart, const int32_t *ori_gcount,
+    const int32_t *inv_col, const float *inv_mask, const int32_t *inv_gptr,
+    const int16_t *inv_grel, const int32_t *inv_gstart, const int32_t *inv_gcount,
+    int64_t r_size, int wot_i, int64_t topk_edges,
+    float *out_ind, float *out_ori, float *out_inv, int64_t *ori_arg, int64_t *inv_arg)
+{
+    uint64_t *po = (uint64_t *)calloc((size_t)(BL * E > 0 ? BL * E : 1), 8);
+    uint64_t *pi = (uint64_t *)calloc((size_t)(BL * E > 0 ? BL * E : 1), 8);
+    for (int64_t bl = 0; bl < BL; ++bl) {
+        float wid = w[bl * n + (n - 1)];
+        for (int64_t e = 0; e < E; ++e) out_ind[bl * E + e] = wot_i ? 0.f : A[bl * E + e] * wid;
+    }
+    for (int64_t ai = 0; ai < num_active; ++ai) {
+        int64_t src = active[ai];
+        for (int64_t bl = 0; bl < BL; ++bl) {
+            float a = A[bl * E + src];
+            if (a == 0) continue;
+            or_max_row(src, bl, a, w, ori_gptr, ori_grel, ori_gstart, ori_gcount, ori_col,
+                       ori_mask, po, topk_edges, E, n, 0);
+            or_max_row(src, bl, a, w, inv_gptr, inv_grel, inv_gstart, inv_gcount, inv_col,
+                       inv_mask, pi, topk_edges, E, n, r_size);
+        }
+    }
+    for (int64_t i = 0; i < BL * E; ++i) {
+        uint32_t hb = (uint32_t)(po[i] >> 32); memcpy(&out_ori[i], &hb, 4);
+        ori_arg[i] = po[i] == 0 ? -1 : (int64_t)(int32_t)(0xFFFFFFFFu - (uint32_t)(po[i] & 0xFFFFFFFFu));
+        hb = (uint32_t)(pi[i] >> 32); memcpy(&out_inv[i], &hb, 4);
+        inv_arg[i] = pi[i] == 0 ? -1 : (int64_t)(int32_t)(0xFFFFFFFFu - (uint32_t)(pi[i] & 0xFFFFFFFFu));
+    }
+    free(po); free(pi);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Filtered, tie-aware rank of the target per query: flashlog.cu:2754-2910.
+ * Scores are a sparse [B, E] matrix given as (b, e, v) entries sorted by
+ * (b, e), at most one entry per coordinate; absent coordinates score 0.
+ * filter_keys holds b*E + e for the filtered answers (sorted ascending).
+ * truth = score of (b, target_b).  Over unfiltered explicit entries:
+ * greater = #(v > truth), eq_explicit = #(v == truth).  With use_eql:
+ *   eq = eq_explicit + (truth == 0 ? E - |filter_b| - explicit_unfiltered : 0) + 1
+ *   rank = greater + (eq + 1) / 2
+ * otherwise rank = greater + 1.  The target itself counts as filtered when
+ * its key is in filter_keys (the reference keeps it out of both counts).    */
+static int64_t or_lower_bound(const int64_t *a, int64_t n, int64_t key)
+{
+    int64_t lo = 0, hi = n;
+    while (lo < hi) { int64_t mid = lo + (hi - lo) / 2; if (a[mid] < key) lo = mid + 1; else hi = mid; }
+    return lo;
+}
+
+void or_filtered_ranks(int64_t nnz, const int64_t *idx_b, const int64_t *idx_e, const float *values,
+                       int64_t B, int64_t E, const int64_t *targets,
+                       int64_t nfilter, const int64_t *filter_keys, int use_eql, float *ranks)
+{
+    float *truth = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
+    float *greater = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
+    float *equal = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
+    float *explicit_unf = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
+    float *fcount = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
+    for (int64_t i = 0; i < nnz; ++i)
+        if (idx_e[i] == targets[idx_b[i]]) truth[idx_b[i]] = values[i];
+    for (int64_t k = 0; k < nfilter; ++k) {
+        int64_t b = filter_keys[k] / E;
+        if (b >= 0 && b < B) fcount[b] += 1.0f;
+    }
+    for (int64_t i = 0; i < nnz; ++i) {
+        int64_t b = idx_b[i], key = b * E + idx_e[i];
+        int64_t pos = or_lower_bound(filter_keys, nfilter, key);
+        if (pos < nfilter && filter_keys[pos] == key) continue;
+        explicit_unf[b] += 1.0f;
+        if (values[i] > truth[b]) greater[b] += 1.0f;
+        else if (values[i] == truth[b]) equal[b] += 1.0f;
+    }
+    for (int64_t b = 0; b < B; ++b) {
+        if (use_eql) {
+            float missing = (float)E - fcount[b] - explicit_unf[b];
+            float eq = equal[b] + (truth[b] == 0.0f ? missing : 0.0f);
+            eq += 1.0f;
+            ranks[b] = greater[b] + (eq + 1.0f) * 0.5f;
+        } else {
+            ranks[b] = greater[b] + 1.0f;
+        }
+    }
+    free(truth); free(greater); free(equal); free(explicit_unf); free(fcount);
+}

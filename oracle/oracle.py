@@ -1,0 +1,266 @@
+"""numpy/ctypes front end of the C oracle (oracle/flashlog_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Every function mirrors a reference function
+(citations in flashlog_oracle.c and below) in the reference's own float
+evaluation order, so its outputs are the bit-exact targets for the HIP path.
+
+Parity pinning of each function is listed in the C file's header; functions
+restated here in numpy (``dense_topc_brute``, ``group_threshold_brute``,
+``filtered_ranks_brute``) are the independent brute-force checks used to pin
+the C restatement, not restatements of the reference.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SRC = os.path.join(_HERE, "flashlog_oracle.c")
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+
+def build(force=False):
+    """Compile the C oracle with gcc (no FMA contraction, IEEE semantics)."""
+    if force or not os.path.exists(_LIB_PATH) or \
+            os.path.getmtime(_LIB_PATH) < os.path.getmtime(_SRC):
+        tmp = _LIB_PATH + ".tmp"
+        subprocess.check_call(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math",
+                               "-fPIC", "-shared", "-o", tmp, _SRC])
+        os.replace(tmp, _LIB_PATH)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# --------------------------------------------------------------------------
+# CSR build: csr.cpp:12-69 (via flashlog_kernel.py:678-697 for the 16-tuple)
+
+def build_side(source, target, relation, nodes):
+    source = _c(source, np.int64)
+    target = _c(target, np.int64)
+    relation = _c(relation, np.int64)
+    m = source.shape[0]
+    row_ptr = np.empty(nodes + 1, np.int32)
+    cols = np.empty(m, np.int32)
+    erel = np.empty(m, np.int16)
+    order = np.empty(m, np.int32)
+    gptr = np.empty(nodes + 1, np.int32)
+    grel = np.empty(max(m, 1), np.int16)
+    gstart = np.empty(max(m, 1), np.int32)
+    gcount = np.empty(max(m, 1), np.int32)
+    ng = ctypes.c_int64(0)
+    rc = lib().or_build_side(ctypes.c_int64(m), ctypes.c_int64(nodes), _p(source), _p(target),
+                             _p(relation), _p(row_ptr), _p(cols), _p(erel), _p(order), _p(gptr),
+                             _p(grel), _p(gstart), _p(gcount), ctypes.byref(ng))
+    if rc != 0:
+        raise ValueError("CSR entity or relation ID outside supported range")
+    g = ng.value
+    return row_ptr, cols, erel, order, gptr, grel[:g].copy(), gstart[:g].copy(), gcount[:g].copy()
+
+
+def build_csr_structure(h, t, r, nodes):
+    """The reference's 16-tuple (flashlog_kernel.py:678-697) as numpy arrays."""
+    ori = build_side(h, t, r, nodes)
+    inv = build_side(t, h, r, nodes)
+    return (*ori[:4], *inv[:4], *ori[4:], *inv[4:])
+
+
+# --------------------------------------------------------------------------
+# c2 threshold: flashlog.cpp:12-35
+
+def group_threshold(weights, relations, sizes, budget):
+    weights = _c(weights, np.float32)
+    relations = _c(relations, np.int16)
+    sizes = _c(sizes, np.int32)
+    rem = ctypes.c_int64(0)
+    f = lib().or_group_threshold_f32
+    f.restype = ctypes.c_float
+    th = f(_p(weights), _p(relations), _p(sizes), ctypes.c_int64(0),
+           ctypes.c_int64(relations.shape[0]), ctypes.c_int64(budget), ctypes.byref(rem))
+    return float(th), int(rem.value)
+
+
+def group_threshold_brute(weights, relations, sizes, budget):
+    """Independent check: expand every eligible group into its edges, sort by
+    weight descending, read the budget-th edge."""
+    ws = []
+    for g in range(len(relations)):
+        wv = np.float32(weights[relations[g]])
+        if wv > 0:
+            ws.extend([wv] * int(sizes[g]))
+    if len(ws) <= budget:
+        return -1.0, 0
+    ws = sorted(ws, reverse=True)
+    th = ws[budget - 1]
+    higher = sum(1 for x in ws if x > th)
+    return float(th), int(budget - higher)
+
+
+# --------------------------------------------------------------------------
+# Dense forward / backward: flashlog.cpp:151-211, :216-278
+
+def _csr_args(csr, masks):
+    (ori_rp, ori_col, ori_ri, ori_ord, inv_rp, inv_col, inv_ri, inv_ord,
+     ori_gp, ori_gr, ori_gs, ori_gc, inv_gp, inv_gr, inv_gs, inv_gc) = csr
+    ori_mask, inv_mask = masks
+    return [_c(ori_col, np.int32), ori_mask, _c(ori_gp, np.int32), _c(ori_gr, np.int16),
+            _c(ori_gs, np.int32), _c(ori_gc, np.int32),
+            _c(inv_col, np.int32), inv_mask, _c(inv_gp, np.int32), _c(inv_gr, np.int16),
+            _c(inv_gs, np.int32), _c(inv_gc, np.int32)]
+
+
+def active_nodes(A):
+    """Sorted entities with a nonzero in any row (flashlog_kernel.py:617-623)."""
+    A = np.asarray(A)
+    return np.nonzero((A != 0).any(axis=0))[0].astype(np.int64)
+
+
+def dense_forward(A, w, csr, masks, r_size, wot_i=False, topk_edges=1 << 60, active=None):
+    A = np.asarray(A)
+    dt = np.float64 if A.dtype == np.float64 else np.float32
+    suf = "f64" if dt == np.float64 else "f32"
+    A = _c(A, dt)
+    BL, E = A.shape
+    w = _c(w, dt).reshape(BL, -1)
+    n = w.shape[1]
+    if active is None:
+        active = active_nodes(A)
+    active = _c(active, np.int64)
+    masks = tuple(_c(m, dt) for m in masks)
+    args = _csr_args(csr, masks)
+    out = [np.empty((BL, E), dt) for _ in range(3)]
+    getattr(lib(), "or_dense_forward_" + suf)(
+        ctypes.c_int64(BL), ctypes.c_int64(E), ctypes.c_int64(n), _p(A), _p(w), _p(active),
+        ctypes.c_int64(active.shape[0]), *[_p(a) for a in args], ctypes.c_int64(r_size),
+        ctypes.c_int(int(bool(wot_i))), ctypes.c_int64(int(topk_edges)), *[_p(o) for o in out])
+    return tuple(out)
+
+
+def dense_backward(grad_ind, grad_ori, grad_inv, A, w, csr, masks, r_size, wot_i=False,
+                   topk_edges=1 << 60, active=None):
+    A = np.asarray(A)
+    dt = np.float64 if A.dtype == np.float64 else np.float32
+    suf = "f64" if dt == np.float64 else "f32"
+    A = _c(A, dt)
+    BL, E = A.shape
+    w = _c(w, dt).reshape(BL, -1)
+    n = w.shape[1]
+    if active is None:
+        active = active_nodes(A)
+    active = _c(active, np.int64)
+    grads = [_c(g, dt).reshape(BL, E) for g in (grad_ind, grad_ori, grad_inv)]
+    masks = tuple(_c(m, dt) for m in masks)
+    args = _csr_args(csr, masks)
+    gA = np.empty((BL, E), dt)
+    gw = np.empty((BL, n), dt)
+    getattr(lib(), "or_dense_backward_" + suf)(
+        ctypes.c_int64(BL), ctypes.c_int64(E), ctypes.c_int64(n), *[_p(g) for g in grads],
+        _p(A), _p(w), _p(active), ctypes.c_int64(active.shape[0]), *[_p(a) for a in args],
+        ctypes.c_int64(r_size), ctypes.c_int(int(bool(wot_i))), ctypes.c_int64(int(topk_edges)),
+        _p(gA), _p(gw))
+    return gA, gw
+
+
+def dense_max_forward(A, w, csr, masks, r_size, wot_i=False, topk_edges=1 << 60, active=None):
+    A = _c(A, np.float32)
+    BL, E = A.shape
+    w = _c(w, np.float32).reshape(BL, -1)
+    n = w.shape[1]
+    if active is None:
+        active = active_nodes(A)
+    active = _c(active, np.int64)
+    masks = tuple(_c(m, np.float32) for m in masks)
+    args = _csr_args(csr, masks)
+    out = [np.empty((BL, E), np.float32) for _ in range(3)]
+    args_out = [np.empty((BL, E), np.int64) for _ in range(2)]
+    lib().or_dense_max_forward(
+        ctypes.c_int64(BL), ctypes.c_int64(E), ctypes.c_int64(n), _p(A), _p(w), _p(active),
+        ctypes.c_int64(active.shape[0]), *[_p(a) for a in args], ctypes.c_int64(r_size),
+        ctypes.c_int(int(bool(wot_i))), ctypes.c_int64(int(topk_edges)),
+        *[_p(o) for o in out], *[_p(o) for o in args_out])
+    return (*out, *args_out)
+
+
+# --------------------------------------------------------------------------
+# c1 entity budget: flashlog_kernel.py:814-842
+
+def dense_topc(A, c):
+    """Returns (A_pruned, cutoff[BL], last_tie[BL], changed)."""
+    A = _c(A, np.float32)
+    BL, E = A.shape
+    out = np.empty_like(A)
+    cutoff = np.zeros(BL, np.float32)
+    last = np.zeros(BL, np.int32)
+    changed = ctypes.c_int(0)
+    rc = lib().or_dense_topc(ctypes.c_int64(BL), ctypes.c_int64(E), ctypes.c_int64(c), _p(A),
+                             _p(out), _p(cutoff), _p(last), ctypes.byref(changed))
+    if rc != 0:
+        raise ValueError("topk_nodes/c must be nonnegative")
+    return out, cutoff, last, bool(changed.value)
+
+
+def dense_topc_brute(A, c):
+    """Independent check of the c1 keep set: stable sort of the nonzeros of
+    each over-budget row by (value desc, entity asc), keep the first c."""
+    A = np.asarray(A, np.float32)
+    keep = np.ones(A.shape, bool)
+    for r in range(A.shape[0]):
+        nz = np.nonzero(A[r] != 0)[0]
+        if nz.size <= c:
+            continue
+        order = sorted(nz.tolist(), key=lambda e: (-float(A[r, e]), e))
+        keep[r] = False
+        keep[r, order[:c]] = True
+    return keep
+
+
+# --------------------------------------------------------------------------
+# Filtered ranks: flashlog.cu:2754-2910
+
+def filtered_ranks(idx_b, idx_e, values, targets, filter_keys, B, E, use_eql=False):
+    idx_b = _c(idx_b, np.int64)
+    idx_e = _c(idx_e, np.int64)
+    values = _c(values, np.float32)
+    targets = _c(targets, np.int64)
+    filter_keys = np.sort(_c(filter_keys, np.int64))
+    ranks = np.empty(B, np.float32)
+    lib().or_filtered_ranks(ctypes.c_int64(values.shape[0]), _p(idx_b), _p(idx_e), _p(values),
+                            ctypes.c_int64(B), ctypes.c_int64(E), _p(targets),
+                            ctypes.c_int64(filter_keys.shape[0]), _p(filter_keys),
+                            ctypes.c_int(int(bool(use_eql))), _p(ranks))
+    return ranks
+
+
+def filtered_ranks_brute(dense_scores, targets, filter_mask, use_eql=False):
+    """Independent check on a dense [B, E] score matrix: count unfiltered
+    entities scoring above / equal to the target (the target itself is not
+    counted unless it is unfiltered, in which case it is one of the ties)."""
+    S = np.asarray(dense_scores, np.float32)
+    B, E = S.shape
+    ranks = np.empty(B, np.float64)
+    for b in range(B):
+        t = S[b, targets[b]]
+        unf = ~filter_mask[b]
+        greater = int(np.sum(S[b][unf] > t))
+        eq = int(np.sum(S[b][unf] == t)) + 1
+        ranks[b] = greater + (eq + 1) / 2.0 if use_eql else greater + 1
+    return ranks
