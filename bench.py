@@ -1,0 +1,271 @@
+"""Benchmark of the FlashLog propagation hot path on one MI355X.
+
+A step is one DRUM evaluation pass over one batch: T = 3 hops of the dense
+sum propagation with the c1 entity budget and the c2 edge budget
+(dense_csr_sum_cuda, flashlog_kernel.py:1629-1663), each followed by the
+model's per-row normalization (src/model_DRUM_kernel.py:141-144), then the sum
+over channels (:149-152).  Workload: BASELINE.json configs[1] (C2: 41k
+entities, 11 base relations, 87k triples, Zipf(1.1) degrees, batch 32, N=3,
+c1=1000, c2=400), synthetic and seeded (flashlog_amd/synth.py).
+
+Prints one JSON line.  ``value`` = queries/sec (batch / step time) with all
+inputs resident in HBM.  ``roofline`` is for the dominant kernel (k_pull),
+timed with HIP events on its own stream inside the library; ``cpu_baseline``
+is the reference's CPU path (its flashlog.cpp built into oracle/_ref, serial
+as in the reference) on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="bound on the CPU baseline sample (0 disables it)")
+    ap.add_argument("--profile-steps", type=int, default=10)
+    return ap.parse_args()
+
+
+def c2_admitted(wv, cnt, K):
+    """Edges admitted per group for one (source, row, direction) under the c2
+    budget K (flashlog.cpp:12-89): groups with w > theta in full, ties at
+    theta by a shared quota in group order."""
+    import numpy as np
+    elig = wv > 0
+    take = np.where(elig, cnt, 0)
+    if K <= 0 or take.sum() <= K:
+        return take
+    order = np.argsort(-wv, kind="stable")
+    cum = np.cumsum(take[order])
+    k = int(np.searchsorted(cum, K))
+    theta = wv[order[k]]
+    left = K - int(take[wv > theta].sum())
+    out = np.where(wv > theta, cnt, 0)
+    for g in np.nonzero(wv == theta)[0]:
+        t = min(int(cnt[g]), max(left, 0))
+        out[g] = t
+        left -= t
+    return out
+
+
+def hop_pull_bytes(Ap, w, csr, R, K):
+    """Algorithmic HBM bytes of one k_pull launch: the two graph outputs
+    (8 B per state cell) plus, per direction and active source, its row
+    pointers (8 B), group records (10 B each) and the column and mask of
+    every edge admitted for at least one row (8 B each)."""
+    import numpy as np
+    BL, E = Ap.shape
+    nz = Ap != 0
+    act = np.nonzero(nz.any(0))[0]
+    total = 8 * BL * E
+    for (gptr, grel, gcount, off) in ((csr[8], csr[9], csr[11], 0), (csr[12], csr[13], csr[15], R)):
+        g0 = gptr[act].astype(np.int64)
+        g1 = gptr[act + 1].astype(np.int64)
+        total += 8 * act.size + 10 * int((g1 - g0).sum())
+        for s, a, b in zip(act, g0, g1):
+            if b == a:
+                continue
+            rows = np.nonzero(nz[:, s])[0]
+            rel = grel[a:b].astype(np.int64) + off
+            cnt = gcount[a:b].astype(np.int64)
+            W = w[rows][:, rel]
+            if K <= 0 or cnt.sum() <= K:
+                e_hat = int(cnt[(W > 0).any(0)].sum())
+            else:
+                take = np.stack([c2_admitted(W[i], cnt, K) for i in range(W.shape[0])])
+                e_hat = int(take.max(0).sum())
+            total += 8 * e_hat
+    return total
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(every (query, channel) row is independent; see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from flashlog_amd import _lib, synth
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+
+    cfg = synth.CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    h, r, t, E, R = synth.make_graph(args.config)
+    n = 2 * R + 1
+    B, L, T = cfg.batch, cfg.channels, cfg.hops
+    K = cfg.c2 // 2 if cfg.use_topk else 0
+    c1 = cfg.c1
+    M = h.shape[0]
+    th, tr, tt = (torch.from_numpy(a) for a in (h, r, t))
+    csr = fk.build_csr_structure(th.to(dev), tt.to(dev), tr.to(dev), E)
+    masks = fk.prepare_csr_masks(csr, torch.ones(M, dtype=torch.bool, device=dev))
+    rng = np.random.Generator(np.random.PCG64(1234 + args.config))
+    src, qrel, tgt = synth.make_queries(h, r, t, R, B, rng)
+    W = torch.from_numpy(synth.make_attention(B, L, n, T, rng)).to(dev)
+    x0 = torch.zeros(B, L, E, dtype=torch.float32, device=dev)
+    x0[torch.arange(B, device=dev), :, torch.from_numpy(src).to(dev)] = 1.0
+
+    def step(capture=None):
+        x = x0
+        for hop in range(T):
+            if capture is not None:
+                capture.append((fk._dense_topc_state(x, c1 if cfg.use_topk else None), W[hop]))
+            s_i, s_h, s_t = fk.dense_csr_sum_cuda(x, W[hop], csr, None, R, use_topk=cfg.use_topk,
+                                                  topk_nodes=c1, topk_edges=K, prepared_masks=masks)
+            s = s_i + s_h + s_t
+            x = s / s.sum(dim=-1, keepdim=True).clamp(1e-7)
+        return x.sum(dim=1)
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            out = step()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_step = e0.elapsed_time(e1) / args.steps
+        print("timed %d steps: %.3f ms/step (host wall %.3f ms/step)" % (args.steps, ms_step, 1e3 * wall / args.steps),
+              file=sys.stderr, flush=True)
+
+        # per-kernel HIP-event timing inside the library
+        kernels = ["k_topc_rows", "k_col_count", "k_block_scan", "k_col_fill", "k_c2", "k_pull_light", "k_pull_heavy", "k_heavy_offsets", "k_heavy_copy", "k_fold_heavy"]
+        _lib.prof_enable(True)
+        for _ in range(args.profile_steps):
+            step()
+        torch.cuda.synchronize()
+        prof = {k: _lib.prof_read(k) for k in kernels}
+        _lib.prof_enable(False)
+        per_launch = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in prof.items()}
+        print("per-launch ms: " + json.dumps({k: round(v, 5) for k, v in per_launch.items()}),
+              file=sys.stderr, flush=True)
+
+        # algorithmic bytes of k_pull per hop, from the hop inputs of one step
+        cap = []
+        step(capture=cap)
+        csr_np = [c.cpu().numpy() for c in csr]
+        hop_bytes = [hop_pull_bytes(a.reshape(B * L, E).cpu().numpy(), w.reshape(B * L, n).cpu().numpy(),
+                                    csr_np, R, K) for a, w in cap]
+    pull_ms = per_launch["k_pull_light"]
+    bytes_per_launch = float(np.mean(hop_bytes))
+    achieved = bytes_per_launch / (pull_ms * 1e-3) / 1e9 if pull_ms > 0 else 0.0
+
+    cpu = cpu_baseline(args, cfg, h, r, t, E, R, src, W.cpu().numpy()) if args.cpu_seconds > 0 else None
+
+    result = {
+        "metric": "queries/sec for L=3 propagation + % of HBM roofline; top-k select ms",
+        "value": B / (ms_step * 1e-3),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded %s graph, flashlog_amd/synth.py)" % cfg.name,
+        "config": {"workload": "%s DRUM dense eval: E=%d, R=%d, M=%d, B=%d, N=%d, T=%d, c1=%d, c2=%d"
+                   % (cfg.name, E, R, M, B, L, T, c1, cfg.c2),
+                   "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2},
+        "topk_select_ms": {"c1_per_hop": per_launch["k_topc_rows"], "c2_per_hop": per_launch["k_c2"]},
+        "kernel_ms_per_launch": per_launch,
+        "roofline": {"kernel": "k_pull", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(args, cfg, h, r, t, E, R, src, W):
+    """The reference's CPU dense path on the same inputs: c1 by torch top-k as
+    in flashlog_kernel.py:814-842, active nodes, then flashlog_forward_cpu from
+    the reference's flashlog.cpp (oracle/_ref; serial in the reference), then
+    the model's normalization.  Falls back to the C restatement if the
+    reference build is absent.  Runs whole steps until ~cpu_seconds."""
+    import numpy as np
+    import torch
+    torch.set_num_threads(1)
+    sys.path.insert(0, os.path.join(ROOT, "oracle", "_ref"))
+    kind = "reference"
+    try:
+        import flashlog_ref_cpp as ref
+    except ImportError:
+        ref = None
+        kind = "port"
+    from oracle import oracle as O
+    csr = O.build_csr_structure(h, t, r, E)
+    tc = [torch.from_numpy(np.ascontiguousarray(a)) for a in csr]
+    M = h.shape[0]
+    ones = torch.ones(M, dtype=torch.float32)
+    B, L, T = cfg.batch, cfg.channels, cfg.hops
+    n = 2 * R + 1
+    K = cfg.c2 // 2 if cfg.use_topk else (1 << 60)
+    Wt = torch.from_numpy(W)
+
+    def topc(A, c):
+        nonzero = A != 0
+        over = nonzero.sum(-1, keepdim=True) > c
+        if not bool(over.any()):
+            return A
+        scores = A.masked_fill(~nonzero, -float("inf"))
+        cutoff = scores.topk(c, dim=-1).values.min(-1, keepdim=True).values
+        above = nonzero & (A > cutoff)
+        tied = nonzero & (A == cutoff)
+        remaining = c - above.sum(-1, keepdim=True)
+        keep = ~over | above | (tied & (tied.cumsum(-1) <= remaining))
+        return A * keep
+
+    def step():
+        x = torch.zeros(B * L, E)
+        x[torch.arange(B * L), torch.from_numpy(np.repeat(src, L))] = 1.0
+        for hop in range(T):
+            A = topc(x, cfg.c1) if cfg.use_topk else x
+            w = Wt[hop].reshape(B * L, n).contiguous()
+            act = torch.nonzero(A.sum(0)).reshape(-1)
+            if ref is not None:
+                o = ref.flashlog_forward_cpu(A.contiguous(), w, act, tc[1], ones, tc[8], tc[9], tc[10], tc[11],
+                                             tc[5], ones, tc[12], tc[13], tc[14], tc[15], R, False, K)
+            else:
+                o = [torch.from_numpy(a) for a in
+                     O.dense_forward(A.numpy(), w.numpy(), csr, (ones.numpy(), ones.numpy()), R, topk_edges=K)]
+            s = o[0] + o[1] + o[2]
+            x = s / s.sum(-1, keepdim=True).clamp(1e-7)
+        return x.view(B, L, E).sum(1)
+
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        step()
+        steps += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": steps * B / el, "unit": "queries/s", "cores": 1, "kind": kind,
+            "sample": "%d full steps (%d queries x %d hops) in %.1f s, 1 thread" % (steps, B, T, el)}
+
+
+if __name__ == "__main__":
+    main()

@@ -12,7 +12,9 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 3
+FL_SEG = 32
+FL_SUP = 16
 
 _lib = None
 
@@ -34,6 +36,17 @@ class FlSide(ctypes.Structure):
         ("pull_rel", ctypes.c_void_p),
         ("slot_of_pos", ctypes.c_void_p),
         ("marks", ctypes.c_void_p),
+        ("nseg", ctypes.c_int64),
+        ("nheavy", ctypes.c_int64),
+        ("nsup", ctypes.c_int64),
+        ("seg_dst", ctypes.c_void_p),
+        ("seg_start", ctypes.c_void_p),
+        ("seg_h", ctypes.c_void_p),
+        ("heavy_dst", ctypes.c_void_p),
+        ("heavy_seg_ptr", ctypes.c_void_p),
+        ("heavy_sup_ptr", ctypes.c_void_p),
+        ("sup_h", ctypes.c_void_p),
+        ("sup_seg0", ctypes.c_void_p),
     ]
 
 
@@ -43,6 +56,8 @@ _SIGS = {
     "fl_csr_build_side": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64] + [ctypes.c_void_p] * 11 +
                           [ctypes.POINTER(ctypes.c_int64)]),
     "fl_pull_index_build": (ctypes.c_int, [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 10),
+    "fl_pull_segments": (ctypes.c_int, [ctypes.c_int64, ctypes.c_void_p] + [ctypes.POINTER(ctypes.c_int64)] * 3 +
+                         [ctypes.c_void_p] * 8),
     "fl_apply_mask": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
     "fl_mark_active": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
@@ -50,13 +65,29 @@ _SIGS = {
     "fl_dense_topc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                      ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]),
     "fl_dense_topc_backward": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 2),
-    "fl_dense_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
+    "fl_dense_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
+                                                   ctypes.c_int64, ctypes.c_int64]),
     "fl_dense_sum_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                             ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int64,
                                             ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_size_t]),
+    "fl_prof_enable": (ctypes.c_int, [ctypes.c_int]),
+    "fl_prof_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
+                                    ctypes.POINTER(ctypes.c_int64)]),
 }
+
+
+def prof_enable(on=True):
+    check(lib().fl_prof_enable(1 if on else 0), "prof_enable")
+
+
+def prof_read(kernel):
+    """(total_ms, launches) of `kernel` since prof_enable (waits on its events)."""
+    tot = ctypes.c_double(0.0)
+    cnt = ctypes.c_int64(0)
+    check(lib().fl_prof_read(kernel.encode(), ctypes.byref(tot), ctypes.byref(cnt)), "prof_read")
+    return tot.value, cnt.value
 
 
 def exported_symbols():

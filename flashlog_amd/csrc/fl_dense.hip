@@ -1,22 +1,30 @@
 // Dense-state propagation kernels for gfx950 (MI355X) and their C-ABI.
 //
 // One hop of the reference's dense sum path (flashlog.cu:898-995, with the
-// CPU path's accumulation order, flashlog.cpp:151-211) runs as five kernels:
+// CPU path's accumulation order, flashlog.cpp:151-211):
 //
-//   k_col_count  column walk of A[BL, E] (thread per entity, coalesced over
-//                entities): identity output, per-entity nonzero count and a
-//                bitmask of the nonzero rows, per-block totals.
-//   k_block_scan exclusive scan of the per-block totals (one workgroup).
-//   k_col_fill   the frontier: per active source, its nonzero (row, value)
-//                entries in row order (the transpose of A's sparsity).
-//   k_c2         per frontier entry and direction, the c2 edge budget as a
-//                (threshold, cut position) pair from a wave-level radix
-//                select over the source's relation groups; marks the pull
-//                slots of every position leaving an active source.
-//   k_pull       per tile of 64 destinations: walk the marked incoming slots
-//                in ascending CSR position and add (a*w)*m into LDS
-//                accumulators -- exactly the order in which the reference's
-//                CPU loop adds into out[bl, dst] -- then write the tile.
+//   k_col_count   column walk of A[BL, E] (thread per entity, coalesced over
+//                 entities): identity output, per-entity nonzero count and a
+//                 bitmask of the nonzero rows, per-block totals.
+//   k_block_scan  exclusive scan of the per-block totals (one workgroup).
+//   k_col_fill    the frontier (every nonzero (source, row) pair, grouped by
+//                 source) and the transposed state AT[source][row] of every
+//                 active source.
+//   k_c2          per frontier pair and direction, the c2 edge budget as a
+//                 (threshold, cut position) pair from a wave-level radix
+//                 select over the source's relation groups; marks the pull
+//                 slots of every position leaving an active source.
+//   k_pull_light  one thread per (destination, row): walk the destination's
+//                 marked incoming slots in ascending CSR position and add
+//                 (a*w)*m in a register -- the order in which the
+//                 reference's CPU loop adds into out[row, dst].  Tiles of
+//                 destinations are staged in LDS and written coalesced.
+//   k_pull_heavy  destinations with more than FL_SEG incoming slots are cut
+//                 into segments of FL_SEG slots; one thread per (segment,
+//                 row) records its kept products, in slot order, in a list.
+//   k_fold_heavy  one thread per (heavy destination, row) adds the lists of
+//                 its segments in segment order: the same sequence of
+//                 additions as a single walk.
 //
 // No atomics touch output values, so results are deterministic and equal to
 // the reference CPU bits.
@@ -256,7 +264,8 @@ __global__ __launch_bounds__(SCAN_NT) void k_block_scan(const int32_t *__restric
 __global__ __launch_bounds__(COL_NT) void k_col_fill(
     const float *__restrict__ A, int64_t BL, int64_t E, const int32_t *__restrict__ colcnt,
     const uint32_t *__restrict__ bitmask, const int32_t *__restrict__ blockoff,
-    int32_t *__restrict__ colptr, int32_t *__restrict__ fr_src, int4 *__restrict__ fr_ori) {
+    int32_t *__restrict__ colptr, int32_t *__restrict__ fr_src, int32_t *__restrict__ fr_bl,
+    float *__restrict__ AT) {
     __shared__ int lds_scan[COL_NT / FL_WAVE + 1];
     const int64_t e = (int64_t)blockIdx.x * COL_NT + threadIdx.x;
     const int cnt = (e < E) ? colcnt[e] : 0;
@@ -268,16 +277,20 @@ __global__ __launch_bounds__(COL_NT) void k_col_fill(
     if (e == E - 1) colptr[E] = slot + cnt;
     if (cnt == 0) return;
     const int64_t nw = (BL + 31) / 32;
+    float *at = AT + e * BL;
     for (int64_t wi = 0; wi < nw; ++wi) {
-        uint32_t bits = bitmask[wi * E + e];
-        while (bits) {
-            const int b = __ffs(bits) - 1;
-            bits &= bits - 1;
-            const int64_t bl = wi * 32 + b;
-            const float a = A[bl * E + e];
-            fr_src[slot] = (int32_t)e;
-            fr_ori[slot] = make_int4((int)bl, __float_as_int(a), 0, 0);
-            ++slot;
+        const uint32_t bits = bitmask[wi * E + e];
+        const int64_t b0 = wi * 32;
+        const int64_t b1 = (b0 + 32 < BL) ? b0 + 32 : BL;
+        for (int64_t bl = b0; bl < b1; ++bl) {
+            float a = 0.0f;
+            if (bits & (1u << (bl - b0))) {
+                a = A[bl * E + e];
+                fr_src[slot] = (int32_t)e;
+                fr_bl[slot] = (int32_t)bl;
+                ++slot;
+            }
+            at[bl] = a;
         }
     }
 }
@@ -372,12 +385,15 @@ __device__ __forceinline__ void row_positions(const fl_side &s, int64_t src, int
 
 constexpr int C2_NT = 256;
 
+// One wave per frontier pair (source, row): writes TH/CUT[dir][source][row]
+// (threshold 0 and cut 0 mean "every w > 0 edge") and, for the first pair of
+// each source, tags the pull slots of the source's positions with `epoch`.
 __global__ __launch_bounds__(C2_NT) void k_c2(fl_side ori, fl_side inv, const float *__restrict__ w,
-                                              int64_t n, int64_t r_size, int64_t K, int do_topk,
-                                              int64_t E, const int32_t *__restrict__ colptr,
+                                              int64_t BL, int64_t E, int64_t n, int64_t r_size, int64_t K,
+                                              int do_topk, const int32_t *__restrict__ colptr,
                                               const int32_t *__restrict__ fr_src,
-                                              int4 *__restrict__ fr_ori, int4 *__restrict__ fr_inv,
-                                              uint8_t epoch) {
+                                              const int32_t *__restrict__ fr_bl, float *__restrict__ TH,
+                                              int32_t *__restrict__ CUT, uint8_t epoch) {
     __shared__ int hist_all[C2_NT / FL_WAVE][256];
     const int lane = fl_lane();
     const int wid = threadIdx.x / FL_WAVE;
@@ -386,8 +402,7 @@ __global__ __launch_bounds__(C2_NT) void k_c2(fl_side ori, fl_side inv, const fl
     const int64_t total = colptr[E];
     for (int64_t j = (int64_t)blockIdx.x * (C2_NT / FL_WAVE) + wid; j < total; j += nwaves) {
         const int64_t src = fr_src[j];
-        const int4 f = fr_ori[j];
-        const int64_t bl = f.x;
+        const int64_t bl = fr_bl[j];
         for (int dir = 0; dir < 2; ++dir) {
             const fl_side &s = dir ? inv : ori;
             const int64_t off = dir ? r_size : 0;
@@ -403,8 +418,9 @@ __global__ __launch_bounds__(C2_NT) void k_c2(fl_side ori, fl_side inv, const fl
                 }
             }
             if (lane == 0) {
-                int4 r = make_int4(f.x, f.y, (int)thk, cut);
-                if (dir) fr_inv[j] = r; else fr_ori[j] = r;
+                const int64_t at = ((int64_t)dir * E + src) * BL + bl;
+                TH[at] = __uint_as_float(thk);
+                CUT[at] = cut;
             }
         }
         if (j == colptr[src]) {
@@ -418,84 +434,254 @@ __global__ __launch_bounds__(C2_NT) void k_c2(fl_side ori, fl_side inv, const fl
     }
 }
 
-// Pull: one workgroup per (64-destination tile, chunk of <= 128 rows).
-constexpr int PULL_NT = 256;
-constexpr int PULL_TILE = 64;
-
-__global__ __launch_bounds__(PULL_NT) void k_pull(fl_side ori, fl_side inv, const float *__restrict__ w,
-                                                  int64_t BL, int64_t E, int64_t n, int64_t r_size,
-                                                  int blc, const int32_t *__restrict__ colptr,
-                                                  const int4 *__restrict__ fr_ori,
-                                                  const int4 *__restrict__ fr_inv, uint8_t epoch,
-                                                  float *__restrict__ out_ori, float *__restrict__ out_inv) {
-    extern __shared__ float acc[];  // [2][blc][PULL_TILE]
-    const int lane = fl_lane();
-    const int wid = threadIdx.x / FL_WAVE;
-    const int64_t d0 = (int64_t)blockIdx.x * PULL_TILE;
-    const int64_t bl0 = (int64_t)blockIdx.y * blc;
-    const int64_t nbl = (bl0 + blc < BL) ? blc : BL - bl0;
-    for (int i = threadIdx.x; i < 2 * blc * PULL_TILE; i += PULL_NT) acc[i] = 0.0f;
-    __syncthreads();
-
-    for (int dl = wid; dl < PULL_TILE; dl += PULL_NT / FL_WAVE) {
-        const int64_t dst = d0 + dl;
-        if (dst >= E) break;
-        for (int dir = 0; dir < 2; ++dir) {
-            const fl_side &s = dir ? inv : ori;
-            const int4 *fr = dir ? fr_inv : fr_ori;
-            const int64_t off = dir ? r_size : 0;
-            float *accd = acc + (int64_t)dir * blc * PULL_TILE;
-            const int64_t s0 = s.pull_ptr[dst], s1 = s.pull_ptr[dst + 1];
-            for (int64_t base = s0; base < s1; base += FL_WAVE) {
-                const int64_t slot = base + lane;
-                int live = 0, pos = 0, rel = 0, j0 = 0, j1 = 0;
-                float m = 0.0f;
-                if (slot < s1 && s.marks[slot] == epoch) {
-                    pos = s.pull_pos[slot];
-                    const int src = s.pull_src[slot];
-                    rel = s.pull_rel[slot];
-                    m = s.mask[pos];
-                    if (m != 0.0f) {
-                        j0 = colptr[src];
-                        j1 = colptr[src + 1];
-                        live = j1 > j0;
-                    }
-                }
-                unsigned long long bal = __ballot(live);
-                while (bal) {
-                    const int i = __ffsll((long long)bal) - 1;
-                    bal &= bal - 1;
-                    const int ipos = __shfl(pos, i, FL_WAVE);
-                    const int irel = __shfl(rel, i, FL_WAVE);
-                    const float im = __shfl(m, i, FL_WAVE);
-                    const int ij0 = __shfl(j0, i, FL_WAVE);
-                    const int ij1 = __shfl(j1, i, FL_WAVE);
-                    for (int j = ij0 + lane; j < ij1; j += FL_WAVE) {
-                        const int4 f = fr[j];
-                        const int64_t bl = f.x;
-                        if (bl < bl0 || bl >= bl0 + nbl) continue;
-                        const float wv = w[bl * n + off + irel];
-                        const float th = __int_as_float(f.z);
-                        if (wv > th || (wv == th && ipos < f.w)) {
-                            const float prod = fl_mul(fl_mul(__int_as_float(f.y), wv), im);
-                            float *cell = accd + (bl - bl0) * PULL_TILE + dl;
-                            *cell = fl_add(*cell, prod);
-                        }
-                    }
-                }
+// Products of the kept edges into one destination for one row, over slots
+// [s0, s1) in order.  Light walks accumulate; heavy walks append to `list`.
+// Loads of four slots are issued together (slot data, mask, state) before
+// the in-order accumulation.
+template <bool LIST>
+__device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_t s1, int64_t bl,
+                                            int64_t BL, int64_t E, int64_t n, int64_t off, int dir,
+                                            const float *__restrict__ w, const float *__restrict__ AT,
+                                            const float *__restrict__ TH, const int32_t *__restrict__ CUT,
+                                            uint8_t epoch, float *__restrict__ list, int *count) {
+    float acc = 0.0f;
+    int k = 0;
+    const int64_t plane = (int64_t)dir * E * BL;
+    for (int64_t base = s0; base < s1; base += 4) {
+        int mk[4], pos[4], src[4], rel[4];
+        float m[4], a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t sl = base + u;
+            mk[u] = 0;
+            if (sl < s1) {
+                mk[u] = s.marks[sl] == epoch;
+                pos[u] = s.pull_pos[sl];
+                src[u] = s.pull_src[sl];
+                rel[u] = s.pull_rel[sl];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (mk[u]) {
+                m[u] = s.mask[pos[u]];
+                a[u] = AT[(int64_t)src[u] * BL + bl];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (!mk[u] || m[u] == 0.0f || a[u] == 0.0f) continue;
+            const int64_t at = plane + (int64_t)src[u] * BL + bl;
+            const float th = TH[at];
+            const int32_t cut = CUT[at];
+            const float wv = w[bl * n + off + rel[u]];
+            if (wv > th || (wv == th && pos[u] < cut)) {
+                const float prod = fl_mul(fl_mul(a[u], wv), m[u]);
+                if (LIST) list[k++] = prod;
+                else acc = fl_add(acc, prod);
             }
         }
     }
+    if (LIST) *count = k;
+    return acc;
+}
+
+constexpr int PULL_NT = 256;
+
+// One workgroup per tile of TD destinations; tiles are dealt to XCDs in
+// contiguous ranges (workgroup b runs on XCD b % 8), so each output line is
+// written from a single L2.
+__global__ __launch_bounds__(PULL_NT) void k_pull_light(
+    fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n,
+    int64_t r_size, int TD, int64_t ntiles, const float *__restrict__ AT, const float *__restrict__ TH,
+    const int32_t *__restrict__ CUT, uint8_t epoch, float *__restrict__ out_ori, float *__restrict__ out_inv) {
+    extern __shared__ float tile[];  // [2][BL][TD]
+    const int64_t per = gridDim.x / 8;
+    const int64_t tid = (int64_t)(blockIdx.x % 8) * per + blockIdx.x / 8;
+    if (tid >= ntiles) return;
+    const int64_t d0 = tid * TD;
+    const int64_t ntask = (int64_t)TD * BL;
+    for (int64_t q = threadIdx.x; q < ntask; q += PULL_NT) {
+        const int64_t dl = q / BL, bl = q - dl * BL;
+        const int64_t dst = d0 + dl;
+        float acc[2] = {0.0f, 0.0f};
+        if (dst < E) {
+#pragma unroll
+            for (int dir = 0; dir < 2; ++dir) {
+                const fl_side &s = dir ? inv : ori;
+                const int64_t s0 = s.pull_ptr[dst], s1 = s.pull_ptr[dst + 1];
+                if (s1 - s0 > FL_SEG) continue;  // heavy: written by k_fold_heavy
+                acc[dir] = walk_slots<false>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, AT, TH, CUT,
+                                             epoch, nullptr, nullptr);
+            }
+        }
+        tile[(0 * BL + bl) * TD + dl] = acc[0];
+        tile[(1 * BL + bl) * TD + dl] = acc[1];
+    }
     __syncthreads();
-    const int64_t ncol = (d0 + PULL_TILE <= E) ? PULL_TILE : E - d0;
-    for (int dir = 0; dir < 2; ++dir) {
-        float *out = dir ? out_inv : out_ori;
-        const float *accd = acc + (int64_t)dir * blc * PULL_TILE;
-        for (int64_t i = threadIdx.x; i < nbl * PULL_TILE; i += PULL_NT) {
-            const int64_t r = i / PULL_TILE, cidx = i % PULL_TILE;
-            if (cidx < ncol) out[(bl0 + r) * E + d0 + cidx] = accd[i];
+    for (int64_t i = threadIdx.x; i < ntask; i += PULL_NT) {
+        const int64_t bl = i / TD, dl = i - bl * TD;
+        const int64_t dst = d0 + dl;
+        if (dst < E) {
+            out_ori[bl * E + dst] = tile[(0 * BL + bl) * TD + dl];
+            out_inv[bl * E + dst] = tile[(1 * BL + bl) * TD + dl];
         }
     }
+}
+
+// Heavy destinations.  Segments of FL_SEG slots are grouped in supersegments
+// of FL_SUP segments.  One workgroup per (supersegment, block of 64 rows),
+// thread (segment, row): walk the segment, record its kept products in slot
+// order (list, cnt), and the offset of this segment's run within the
+// supersegment (local_off) and the supersegment's total per row (sup_tot).
+constexpr int HEAVY_BL = 64;
+constexpr int HEAVY_NT = FL_SUP * HEAVY_BL;  // 1024
+
+__global__ __launch_bounds__(HEAVY_NT) void k_pull_heavy(
+    fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n, int64_t r_size,
+    const float *__restrict__ AT, const float *__restrict__ TH, const int32_t *__restrict__ CUT, uint8_t epoch,
+    float *__restrict__ list_ori, float *__restrict__ list_inv, int32_t *__restrict__ cnt_ori,
+    int32_t *__restrict__ cnt_inv, int32_t *__restrict__ loff_ori, int32_t *__restrict__ loff_inv,
+    int32_t *__restrict__ stot_ori, int32_t *__restrict__ stot_inv) {
+    __shared__ int cnt_lds[FL_SUP][HEAVY_BL];
+    const int dir = blockIdx.x >= ori.nsup;
+    const int64_t sup = dir ? blockIdx.x - ori.nsup : blockIdx.x;
+    const fl_side &s = dir ? inv : ori;
+    const int sl = threadIdx.x / HEAVY_BL, bll = threadIdx.x % HEAVY_BL;
+    const int64_t bl = (int64_t)blockIdx.y * HEAVY_BL + bll;
+    const int64_t h = s.sup_h[sup];
+    const int64_t seg0 = s.sup_seg0[sup];
+    const int64_t segend = s.heavy_seg_ptr[h + 1];
+    const int64_t seg = seg0 + sl;
+    int k = 0;
+    if (seg < segend && bl < BL) {
+        const int64_t dst = s.heavy_dst[h];
+        const int64_t s0 = s.seg_start[seg];
+        const int64_t end = s.pull_ptr[dst + 1];
+        const int64_t s1 = (s0 + FL_SEG < end) ? s0 + FL_SEG : end;
+        float *list = (dir ? list_inv : list_ori) + (seg * BL + bl) * FL_SEG;
+        walk_slots<true>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, AT, TH, CUT, epoch, list, &k);
+        (dir ? cnt_inv : cnt_ori)[seg * BL + bl] = k;
+    }
+    cnt_lds[sl][bll] = k;
+    __syncthreads();
+    if (seg < segend && bl < BL) {
+        int run = 0;
+        for (int q = 0; q < sl; ++q) run += cnt_lds[q][bll];
+        (dir ? loff_inv : loff_ori)[seg * BL + bl] = run;
+        if (seg == segend - 1 || sl == FL_SUP - 1) (dir ? stot_inv : stot_ori)[sup * BL + bl] = run + k;
+    }
+}
+
+// One workgroup per heavy (destination, side): exclusive prefix over the
+// destination's supersegments of their per-row totals (sup_base), and the
+// per-row totals of the destination (tot).  P groups of BL threads scan
+// contiguous supersegment ranges.
+constexpr int HSCAN_NT = 1024;
+
+__global__ __launch_bounds__(HSCAN_NT) void k_heavy_offsets(fl_side ori, fl_side inv, int64_t BL,
+                                                           const int32_t *__restrict__ stot_ori,
+                                                           const int32_t *__restrict__ stot_inv,
+                                                           int32_t *__restrict__ sbase_ori,
+                                                           int32_t *__restrict__ sbase_inv,
+                                                           int32_t *__restrict__ tot_ori,
+                                                           int32_t *__restrict__ tot_inv) {
+    extern __shared__ int part[];  // [P][BL]
+    const int dir = blockIdx.x >= ori.nheavy;
+    const int64_t h = dir ? blockIdx.x - ori.nheavy : blockIdx.x;
+    const fl_side &s = dir ? inv : ori;
+    const int32_t *stot = dir ? stot_inv : stot_ori;
+    int32_t *sbase = dir ? sbase_inv : sbase_ori;
+    const int64_t u0 = s.heavy_sup_ptr[h], u1 = s.heavy_sup_ptr[h + 1];
+    const int P = (int)(HSCAN_NT / BL);
+    const int64_t per = (u1 - u0 + P - 1) / P;
+    const int t = threadIdx.x;
+    const int64_t bl = t % BL;
+    const int grp = t / (int)BL;
+    const bool active = grp < P;
+    int64_t a0 = 0, a1 = 0;
+    if (active) {
+        a0 = u0 + grp * per;
+        a1 = (a0 + per < u1) ? a0 + per : u1;
+        int local = 0;
+        for (int64_t u = a0; u < a1; ++u) local += stot[u * BL + bl];
+        part[grp * BL + bl] = local;
+    }
+    __syncthreads();
+    if (active) {
+        int run = 0;
+        for (int q = 0; q < grp; ++q) run += part[q * BL + bl];
+        for (int64_t u = a0; u < a1; ++u) { sbase[u * BL + bl] = run; run += stot[u * BL + bl]; }
+        if (grp == P - 1) (dir ? tot_inv : tot_ori)[h * BL + bl] = run;
+    }
+}
+
+// One thread per (heavy segment, row): copy the segment's list into the
+// row's contiguous run of the destination's region.
+__global__ __launch_bounds__(PULL_NT) void k_heavy_copy(
+    fl_side ori, fl_side inv, int64_t BL, const float *__restrict__ list_ori, const float *__restrict__ list_inv,
+    const int32_t *__restrict__ cnt_ori, const int32_t *__restrict__ cnt_inv, const int32_t *__restrict__ loff_ori,
+    const int32_t *__restrict__ loff_inv, const int32_t *__restrict__ sbase_ori,
+    const int32_t *__restrict__ sbase_inv, float *__restrict__ region_ori, float *__restrict__ region_inv) {
+    const int64_t q = (int64_t)blockIdx.x * PULL_NT + threadIdx.x;
+    const int64_t nq_ori = ori.nseg * BL;
+    if (q >= nq_ori + inv.nseg * BL) return;
+    const int dir = q >= nq_ori;
+    const int64_t qq = dir ? q - nq_ori : q;
+    const int64_t seg = qq / BL, bl = qq - seg * BL;
+    const fl_side &s = dir ? inv : ori;
+    const int64_t h = s.seg_h[seg];
+    const int64_t g0 = s.heavy_seg_ptr[h], g1 = s.heavy_seg_ptr[h + 1];
+    const int64_t sup = s.heavy_sup_ptr[h] + (seg - g0) / FL_SUP;
+    const int c = (dir ? cnt_inv : cnt_ori)[qq];
+    if (c == 0) return;
+    const int64_t off = (int64_t)(dir ? sbase_inv : sbase_ori)[sup * BL + bl] + (dir ? loff_inv : loff_ori)[qq];
+    const int64_t cap = (g1 - g0) * FL_SEG;
+    const float *src = (dir ? list_inv : list_ori) + qq * FL_SEG;
+    float *dstp = (dir ? region_inv : region_ori) + g0 * FL_SEG * BL + bl * cap + off;
+    for (int k = 0; k < c; ++k) dstp[k] = src[k];
+}
+
+// One workgroup per (heavy destination, side, block of FOLD_ROWS rows):
+// each row's run is staged through LDS in chunks and added in order by one
+// thread -- the additions of a single walk over all the slots.
+constexpr int FOLD_NT = 256;
+constexpr int FOLD_ROWS = 16;
+constexpr int FOLD_CHUNK = 1024;
+
+__global__ __launch_bounds__(FOLD_NT) void k_fold_heavy(
+    fl_side ori, fl_side inv, int64_t BL, int64_t E, const float *__restrict__ region_ori,
+    const float *__restrict__ region_inv, const int32_t *__restrict__ tot_ori, const int32_t *__restrict__ tot_inv,
+    float *__restrict__ out_ori, float *__restrict__ out_inv) {
+    __shared__ float stage[FOLD_ROWS][FOLD_CHUNK];
+    __shared__ int s_tot[FOLD_ROWS];
+    const int dir = blockIdx.x >= ori.nheavy;
+    const int64_t h = dir ? blockIdx.x - ori.nheavy : blockIdx.x;
+    const fl_side &s = dir ? inv : ori;
+    const float *region = dir ? region_inv : region_ori;
+    const int64_t g0 = s.heavy_seg_ptr[h], g1 = s.heavy_seg_ptr[h + 1];
+    const int64_t cap = (g1 - g0) * FL_SEG;
+    const int64_t rb = (int64_t)blockIdx.y * FOLD_ROWS;
+    const int t = threadIdx.x;
+    if (t < FOLD_ROWS) s_tot[t] = (rb + t < BL) ? (dir ? tot_inv : tot_ori)[h * BL + rb + t] : 0;
+    __syncthreads();
+    int maxtot = 0;
+    for (int r = 0; r < FOLD_ROWS; ++r) maxtot = s_tot[r] > maxtot ? s_tot[r] : maxtot;
+    float acc = 0.0f;
+    for (int64_t c0 = 0; c0 < maxtot; c0 += FOLD_CHUNK) {
+        for (int r = 0; r < FOLD_ROWS; ++r) {
+            const int64_t lim = (s_tot[r] - c0 < FOLD_CHUNK) ? s_tot[r] - c0 : FOLD_CHUNK;
+            const float *src = region + g0 * FL_SEG * BL + (rb + r) * cap + c0;
+            for (int64_t k = t; k < lim; k += FOLD_NT) stage[r][k] = src[k];
+        }
+        __syncthreads();
+        if (t < FOLD_ROWS && rb + t < BL) {
+            const int64_t lim = (s_tot[t] - c0 < FOLD_CHUNK) ? s_tot[t] - c0 : FOLD_CHUNK;
+            for (int64_t k = 0; k < lim; ++k) acc = fl_add(acc, stage[t][k]);
+        }
+        __syncthreads();
+    }
+    if (t < FOLD_ROWS && rb + t < BL) (dir ? out_inv : out_ori)[(rb + t) * E + s.heavy_dst[h]] = acc;
 }
 
 }  // namespace fl
@@ -508,15 +694,17 @@ using namespace fl;
 namespace {
 
 struct DenseWs {
-    int32_t *colcnt, *colptr, *blocksum, *blockoff, *fr_src;
+    int32_t *colcnt, *colptr, *blocksum, *blockoff, *fr_src, *fr_bl, *cut, *cnt_ori, *cnt_inv, *off_ori, *off_inv;
+    int32_t *stot_ori, *stot_inv, *sbase_ori, *sbase_inv, *tot_ori, *tot_inv;
     uint32_t *bitmask;
-    int4 *fr_ori, *fr_inv;
+    float *at, *th, *list_ori, *list_inv, *region_ori, *region_inv;
     size_t bytes;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-DenseWs dense_ws_layout(int64_t BL, int64_t E, char *base) {
+DenseWs dense_ws_layout(int64_t BL, int64_t E, const fl_side *ori, const fl_side *inv, char *base) {
+    const int64_t nseg_ori = ori->nseg, nseg_inv = inv->nseg;
     DenseWs ws{};
     const int64_t nblk = (E + COL_NT - 1) / COL_NT;
     const int64_t nw = (BL + 31) / 32;
@@ -529,8 +717,24 @@ DenseWs dense_ws_layout(int64_t BL, int64_t E, char *base) {
     ws.blockoff = (int32_t *)take(sizeof(int32_t) * (size_t)(nblk + 1));
     ws.bitmask = (uint32_t *)take(sizeof(uint32_t) * (size_t)(nw * E));
     ws.fr_src = (int32_t *)take(sizeof(int32_t) * (size_t)cap);
-    ws.fr_ori = (int4 *)take(sizeof(int4) * (size_t)cap);
-    ws.fr_inv = (int4 *)take(sizeof(int4) * (size_t)cap);
+    ws.fr_bl = (int32_t *)take(sizeof(int32_t) * (size_t)cap);
+    ws.at = (float *)take(sizeof(float) * (size_t)cap);
+    ws.th = (float *)take(sizeof(float) * (size_t)(2 * cap));
+    ws.cut = (int32_t *)take(sizeof(int32_t) * (size_t)(2 * cap));
+    ws.list_ori = (float *)take(sizeof(float) * (size_t)(nseg_ori * BL * FL_SEG));
+    ws.list_inv = (float *)take(sizeof(float) * (size_t)(nseg_inv * BL * FL_SEG));
+    ws.cnt_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(nseg_ori * BL));
+    ws.cnt_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(nseg_inv * BL));
+    ws.off_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(nseg_ori * BL));
+    ws.off_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(nseg_inv * BL));
+    ws.region_ori = (float *)take(sizeof(float) * (size_t)(nseg_ori * BL * FL_SEG));
+    ws.region_inv = (float *)take(sizeof(float) * (size_t)(nseg_inv * BL * FL_SEG));
+    ws.stot_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nsup * BL));
+    ws.stot_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(inv->nsup * BL));
+    ws.sbase_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nsup * BL));
+    ws.sbase_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(inv->nsup * BL));
+    ws.tot_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nheavy * BL));
+    ws.tot_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(inv->nheavy * BL));
     ws.bytes = off;
     return ws;
 }
@@ -542,6 +746,11 @@ int check_side(const fl_side *s, const char *name) {
                          !s->slot_of_pos || !s->marks))
         return fl_fail(FL_ERR_ARG, "%s side has a null array", name);
     if (!s->row_group_ptr || !s->pull_ptr) return fl_fail(FL_ERR_ARG, "%s side has null row pointers", name);
+    if (s->nseg < 0 || s->nheavy < 0 || s->nsup < 0 ||
+        (s->nseg > 0 && (!s->seg_dst || !s->seg_start || !s->seg_h)) ||
+        (s->nsup > 0 && (!s->sup_h || !s->sup_seg0)) ||
+        (s->nheavy > 0 && (!s->heavy_dst || !s->heavy_seg_ptr || !s->heavy_sup_ptr)))
+        return fl_fail(FL_ERR_ARG, "%s side has inconsistent heavy-destination segments", name);
     return FL_OK;
 }
 
@@ -549,7 +758,7 @@ int check_side(const fl_side *s, const char *name) {
 
 extern "C" {
 
-int fl_abi_version(void) { return 1; }
+int fl_abi_version(void) { return 3; }
 
 int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool, const int32_t *order,
                   const float *weight, float *out, int64_t nnz) {
@@ -560,10 +769,10 @@ int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool, const
     const int64_t nb = (nnz + nt - 1) / nt;
     hipStream_t st = (hipStream_t)stream;
     if (mask_is_bool)
-        hipLaunchKernelGGL(k_apply_mask<uint8_t>, dim3((unsigned)nb), dim3(nt), 0, st,
+        FL_LAUNCH("k_apply_mask", k_apply_mask<uint8_t>, dim3((unsigned)nb), dim3(nt), 0, st,
                            (const uint8_t *)mask_values, order, weight, out, nnz);
     else
-        hipLaunchKernelGGL(k_apply_mask<float>, dim3((unsigned)nb), dim3(nt), 0, st,
+        FL_LAUNCH("k_apply_mask", k_apply_mask<float>, dim3((unsigned)nb), dim3(nt), 0, st,
                            (const float *)mask_values, order, weight, out, nnz);
     return fl_check_launch("apply_mask");
 }
@@ -572,7 +781,7 @@ int fl_mark_active(void *stream, const float *A, int64_t BL, int64_t E, int32_t 
     if (BL < 0 || E < 0) return fl_fail(FL_ERR_ARG, "mark_active: negative size");
     if (E == 0) return FL_OK;
     const int nt = 256;
-    hipLaunchKernelGGL(k_mark_active, dim3((unsigned)((E + nt - 1) / nt)), dim3(nt), 0,
+    FL_LAUNCH("k_mark_active", k_mark_active, dim3((unsigned)((E + nt - 1) / nt)), dim3(nt), 0,
                        (hipStream_t)stream, A, flags, BL, E);
     return fl_check_launch("mark_active");
 }
@@ -582,7 +791,7 @@ int fl_dense_topc(void *stream, const float *A, float *out, int64_t BL, int64_t 
     if (c < 0) return fl_fail(FL_ERR_ARG, "topk_nodes/c must be nonnegative");
     if (BL < 0 || E < 0 || E > INT32_MAX - 1) return fl_fail(FL_ERR_ARG, "dense_topc: bad shape");
     if (BL == 0) return FL_OK;
-    hipLaunchKernelGGL(k_topc_rows, dim3((unsigned)BL), dim3(TOPC_NT), 0, (hipStream_t)stream,
+    FL_LAUNCH("k_topc_rows", k_topc_rows, dim3((unsigned)BL), dim3(TOPC_NT), 0, (hipStream_t)stream,
                        A, out, E, c, row_state);
     return fl_check_launch("dense_topc");
 }
@@ -591,14 +800,14 @@ int fl_dense_topc_backward(void *stream, const float *grad, const float *A,
                            const int32_t *row_state, float *grad_A, int64_t BL, int64_t E) {
     if (BL <= 0 || E <= 0) return FL_OK;
     const int nt = 256;
-    hipLaunchKernelGGL(k_topc_backward, dim3((unsigned)((E + nt - 1) / nt), (unsigned)BL), dim3(nt), 0,
+    FL_LAUNCH("k_topc_backward", k_topc_backward, dim3((unsigned)((E + nt - 1) / nt), (unsigned)BL), dim3(nt), 0,
                        (hipStream_t)stream, grad, A, row_state, grad_A, E);
     return fl_check_launch("dense_topc_backward");
 }
 
-size_t fl_dense_workspace_bytes(int64_t BL, int64_t E) {
-    if (BL <= 0 || E <= 0) return 256;
-    return dense_ws_layout(BL, E, nullptr).bytes;
+size_t fl_dense_workspace_bytes(const fl_side *ori, const fl_side *inv, int64_t BL, int64_t E) {
+    if (BL <= 0 || E <= 0 || !ori || !inv) return 256;
+    return dense_ws_layout(BL, E, ori, inv, nullptr).bytes;
 }
 
 int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv, const float *A,
@@ -615,25 +824,49 @@ int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv, c
                        (long long)n, (long long)r_size);
     if (epoch < 1 || epoch > 255) return fl_fail(FL_ERR_ARG, "dense_sum_forward: epoch out of range");
     if (BL == 0 || E == 0) return FL_OK;
-    DenseWs ws = dense_ws_layout(BL, E, (char *)workspace);
+    DenseWs ws = dense_ws_layout(BL, E, ori, inv, (char *)workspace);
     if (!workspace || workspace_bytes < ws.bytes)
         return fl_fail(FL_ERR_ARG, "dense_sum_forward: workspace of %zu bytes, need %zu", workspace_bytes, ws.bytes);
     hipStream_t st = (hipStream_t)stream;
     const int64_t nblk = (E + COL_NT - 1) / COL_NT;
-    hipLaunchKernelGGL(k_col_count, dim3((unsigned)nblk), dim3(COL_NT), 0, st, A, w, BL, E, n, wot_i,
-                       out_ind, ws.colcnt, ws.bitmask, ws.blocksum);
-    hipLaunchKernelGGL(k_block_scan, dim3(1), dim3(SCAN_NT), 0, st, ws.blocksum, ws.blockoff, nblk);
-    hipLaunchKernelGGL(k_col_fill, dim3((unsigned)nblk), dim3(COL_NT), 0, st, A, BL, E, ws.colcnt,
-                       ws.bitmask, ws.blockoff, ws.colptr, ws.fr_src, ws.fr_ori);
+    FL_LAUNCH("k_col_count", k_col_count, dim3((unsigned)nblk), dim3(COL_NT), 0, st, A, w, BL, E, n, wot_i,
+              out_ind, ws.colcnt, ws.bitmask, ws.blocksum);
+    FL_LAUNCH("k_block_scan", k_block_scan, dim3(1), dim3(SCAN_NT), 0, st, ws.blocksum, ws.blockoff, nblk);
+    FL_LAUNCH("k_col_fill", k_col_fill, dim3((unsigned)nblk), dim3(COL_NT), 0, st, A, BL, E, ws.colcnt,
+              ws.bitmask, ws.blockoff, ws.colptr, ws.fr_src, ws.fr_bl, ws.at);
     const int do_topk = (topk_edges > 0 && topk_edges < ((int64_t)1 << 60)) ? 1 : 0;
     const int64_t K = do_topk ? topk_edges : 0;
-    hipLaunchKernelGGL(k_c2, dim3(2048), dim3(C2_NT), 0, st, *ori, *inv, w, n, r_size, K, do_topk, E,
-                       ws.colptr, ws.fr_src, ws.fr_ori, ws.fr_inv, (uint8_t)epoch);
-    const int blc = (int)(BL < 128 ? BL : 128);
-    const size_t lds = sizeof(float) * 2 * (size_t)blc * PULL_TILE;
-    dim3 grid((unsigned)((E + PULL_TILE - 1) / PULL_TILE), (unsigned)((BL + blc - 1) / blc));
-    hipLaunchKernelGGL(k_pull, grid, dim3(PULL_NT), lds, st, *ori, *inv, w, BL, E, n, r_size, blc,
-                       ws.colptr, ws.fr_ori, ws.fr_inv, (uint8_t)epoch, out_ori, out_inv);
+    FL_LAUNCH("k_c2", k_c2, dim3(2048), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K, do_topk,
+              ws.colptr, ws.fr_src, ws.fr_bl, ws.th, ws.cut, (uint8_t)epoch);
+    // light destinations: TD destinations per workgroup, TD*BL ~ 512 tasks
+    int TD = (int)(512 / (BL > 0 ? BL : 1));
+    if (TD < 1) TD = 1;
+    if (TD > 64) TD = 64;
+    const int64_t ntiles = (E + TD - 1) / TD;
+    const int64_t nwg = ((ntiles + 7) / 8) * 8;
+    const size_t lds = sizeof(float) * 2 * (size_t)BL * (size_t)TD;
+    if (lds > 65536) return fl_fail(FL_ERR_ARG, "dense_sum_forward: BL=%lld exceeds the LDS tile", (long long)BL);
+    FL_LAUNCH("k_pull_light", k_pull_light, dim3((unsigned)nwg), dim3(PULL_NT), lds, st, *ori, *inv, w, BL, E, n,
+              r_size, TD, ntiles, ws.at, ws.th, ws.cut, (uint8_t)epoch, out_ori, out_inv);
+    const int64_t nq_seg = (ori->nseg + inv->nseg) * BL;
+    if (nq_seg > 0) {
+        if (BL > HSCAN_NT) return fl_fail(FL_ERR_ARG, "dense_sum_forward: BL=%lld above %d", (long long)BL, HSCAN_NT);
+        const unsigned nblc = (unsigned)((BL + HEAVY_BL - 1) / HEAVY_BL);
+        FL_LAUNCH("k_pull_heavy", k_pull_heavy, dim3((unsigned)(ori->nsup + inv->nsup), nblc), dim3(HEAVY_NT), 0, st,
+                  *ori, *inv, w, BL, E, n, r_size, ws.at, ws.th, ws.cut, (uint8_t)epoch, ws.list_ori, ws.list_inv,
+                  ws.cnt_ori, ws.cnt_inv, ws.off_ori, ws.off_inv, ws.stot_ori, ws.stot_inv);
+        const size_t slds = sizeof(int) * (size_t)((HSCAN_NT / BL) * BL);
+        FL_LAUNCH("k_heavy_offsets", k_heavy_offsets, dim3((unsigned)(ori->nheavy + inv->nheavy)), dim3(HSCAN_NT),
+                  slds, st, *ori, *inv, BL, ws.stot_ori, ws.stot_inv, ws.sbase_ori, ws.sbase_inv, ws.tot_ori,
+                  ws.tot_inv);
+        FL_LAUNCH("k_heavy_copy", k_heavy_copy, dim3((unsigned)((nq_seg + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0,
+                  st, *ori, *inv, BL, ws.list_ori, ws.list_inv, ws.cnt_ori, ws.cnt_inv, ws.off_ori, ws.off_inv,
+                  ws.sbase_ori, ws.sbase_inv, ws.region_ori, ws.region_inv);
+        FL_LAUNCH("k_fold_heavy", k_fold_heavy,
+                  dim3((unsigned)(ori->nheavy + inv->nheavy), (unsigned)((BL + FOLD_ROWS - 1) / FOLD_ROWS)),
+                  dim3(FOLD_NT), 0, st, *ori, *inv, BL, E, ws.region_ori, ws.region_inv, ws.tot_ori, ws.tot_inv,
+                  out_ori, out_inv);
+    }
     return fl_check_launch("dense_sum_forward");
 }
 

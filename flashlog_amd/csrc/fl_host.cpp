@@ -30,9 +30,64 @@ int fl_check_launch(const char *what) {
     return FL_OK;
 }
 
+struct ProfRec {
+    std::string name;
+    hipEvent_t start, stop;
+};
+static bool g_prof_on = false;
+static std::vector<ProfRec> g_prof;
+
+int prof_begin(const char *kernel, hipStream_t stream) {
+    if (!g_prof_on) return -1;
+    ProfRec r{kernel, nullptr, nullptr};
+    if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) return -1;
+    (void)hipEventRecord(r.start, stream);
+    g_prof.push_back(r);
+    return (int)g_prof.size() - 1;
+}
+
+void prof_end(int token, hipStream_t stream) {
+    if (token < 0 || token >= (int)g_prof.size()) return;
+    (void)hipEventRecord(g_prof[token].stop, stream);
+}
+
+static void prof_clear() {
+    for (auto &r : g_prof) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
+    g_prof.clear();
+}
+
 }  // namespace fl
 
 extern "C" {
+
+// Enables (1) or disables (0) per-kernel event timing; either call discards
+// earlier records.  Not thread-safe: for single-threaded benchmarking.
+int fl_prof_enable(int on) {
+    fl::prof_clear();
+    fl::g_prof_on = on != 0;
+    return FL_OK;
+}
+
+// Sum of event-timed durations (ms) and launch count of `kernel` since the
+// last fl_prof_enable; waits for the recorded events.
+int fl_prof_read(const char *kernel, double *total_ms, int64_t *launches) {
+    double tot = 0.0;
+    int64_t cnt = 0;
+    for (auto &r : fl::g_prof) {
+        if (r.name != kernel) continue;
+        if (hipEventSynchronize(r.stop) != hipSuccess) return fl::fl_fail(FL_ERR_HIP, "prof_read: event wait failed");
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, r.start, r.stop) != hipSuccess) return fl::fl_fail(FL_ERR_HIP, "prof_read: elapsed failed");
+        tot += ms;
+        ++cnt;
+    }
+    *total_ms = tot;
+    *launches = cnt;
+    return FL_OK;
+}
 
 const char *fl_last_error(void) { return fl::g_last_error.c_str(); }
 
@@ -121,6 +176,48 @@ int fl_pull_index_build(int64_t nodes, int64_t edges, int64_t groups, const int3
         pull_rel[slot] = rel[p];
         slot_of_pos[p] = (int32_t)slot;
     }
+    return FL_OK;
+}
+
+// Heavy destinations (more than FL_SEG slots), their FL_SEG-slot segments
+// and FL_SUP-segment supersegments, in destination order.
+int fl_pull_segments(int64_t nodes, const int32_t *pull_ptr, int64_t *nseg, int64_t *nheavy, int64_t *nsup,
+                     int32_t *seg_dst, int32_t *seg_start, int32_t *seg_h, int32_t *heavy_dst,
+                     int32_t *heavy_seg_ptr, int32_t *heavy_sup_ptr, int32_t *sup_h, int32_t *sup_seg0) {
+    if (nodes < 0 || !pull_ptr || !nseg || !nheavy || !nsup)
+        return fl::fl_fail(FL_ERR_ARG, "pull_segments: bad arguments");
+    const bool fill = seg_dst != nullptr;
+    int64_t ns = 0, nh = 0, nu = 0;
+    for (int64_t v = 0; v < nodes; ++v) {
+        const int64_t deg = (int64_t)pull_ptr[v + 1] - pull_ptr[v];
+        if (deg <= FL_SEG) continue;
+        const int64_t segs = (deg + FL_SEG - 1) / FL_SEG;
+        const int64_t sups = (segs + FL_SUP - 1) / FL_SUP;
+        if (fill) {
+            heavy_dst[nh] = (int32_t)v;
+            heavy_seg_ptr[nh] = (int32_t)ns;
+            heavy_sup_ptr[nh] = (int32_t)nu;
+            for (int64_t k = 0; k < segs; ++k) {
+                seg_dst[ns + k] = (int32_t)v;
+                seg_start[ns + k] = (int32_t)(pull_ptr[v] + k * FL_SEG);
+                seg_h[ns + k] = (int32_t)nh;
+            }
+            for (int64_t k = 0; k < sups; ++k) {
+                sup_h[nu + k] = (int32_t)nh;
+                sup_seg0[nu + k] = (int32_t)(ns + k * FL_SUP);
+            }
+        }
+        ns += segs;
+        nu += sups;
+        ++nh;
+    }
+    if (fill) {
+        heavy_seg_ptr[nh] = (int32_t)ns;
+        heavy_sup_ptr[nh] = (int32_t)nu;
+    }
+    *nseg = ns;
+    *nheavy = nh;
+    *nsup = nu;
     return FL_OK;
 }
 

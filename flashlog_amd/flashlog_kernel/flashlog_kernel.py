@@ -215,6 +215,17 @@ class _PullSide:
         check(_lib.lib().fl_pull_index_build(nodes, m, g, *[ptr(t) for t in host], ptr(pull_ptr),
                                              ptr(pull_pos), ptr(pull_src), ptr(pull_rel),
                                              ptr(slot_of_pos)), "pull_index_build")
+        counts = [ctypes.c_int64(0) for _ in range(3)]
+        check(_lib.lib().fl_pull_segments(nodes, ptr(pull_ptr), *[ctypes.byref(c) for c in counts],
+                                          *([None] * 8)), "pull_segments")
+        nseg, nheavy, nsup = (c.value for c in counts)
+        arrays = [torch.empty(k, dtype=torch.int32) for k in
+                  (nseg, nseg, nseg, nheavy, nheavy + 1, nheavy + 1, nsup, nsup)]
+        check(_lib.lib().fl_pull_segments(nodes, ptr(pull_ptr), *[ctypes.byref(c) for c in counts],
+                                          *[ptr(a) for a in arrays]), "pull_segments")
+        self.nseg, self.nheavy, self.nsup = nseg, nheavy, nsup
+        (self.seg_dst, self.seg_start, self.seg_h, self.heavy_dst, self.heavy_seg_ptr, self.heavy_sup_ptr,
+         self.sup_h, self.sup_seg0) = [a.to(device) for a in arrays]
         self.edges, self.groups, self.nodes = m, g, nodes
         self.max_rel = int(host[2].max()) if g else -1
         self.col_ind = col_ind.int().contiguous()
@@ -237,7 +248,10 @@ class _PullSide:
                       self.pull_ptr.data_ptr(), self.pull_pos.data_ptr() if self.edges else 0,
                       self.pull_src.data_ptr() if self.edges else 0,
                       self.pull_rel.data_ptr() if self.edges else 0,
-                      self.slot_of_pos.data_ptr() if self.edges else 0, self.marks.data_ptr())
+                      self.slot_of_pos.data_ptr() if self.edges else 0, self.marks.data_ptr(),
+                      self.nseg, self.nheavy, self.nsup, *[t.data_ptr() if t.numel() else 0 for t in (
+                          self.seg_dst, self.seg_start, self.seg_h, self.heavy_dst, self.heavy_seg_ptr,
+                          self.heavy_sup_ptr, self.sup_h, self.sup_seg0)])
 
 
 class _Graph:
@@ -439,11 +453,11 @@ def _dense_sum_forward(A_flat, w_flat, graph, ori_mask, inv_mask, r_size, wot_i,
     out_ind = torch.empty_like(A_flat)
     out_ori = torch.empty_like(A_flat)
     out_inv = torch.empty_like(A_flat)
-    ws_bytes = _lib.lib().fl_dense_workspace_bytes(BL, E)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A_flat.device)
-    epoch = graph.next_epoch()
     so = graph.ori.struct(ori_mask)
     si = graph.inv.struct(inv_mask)
+    ws_bytes = _lib.lib().fl_dense_workspace_bytes(ctypes.byref(so), ctypes.byref(si), BL, E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A_flat.device)
+    epoch = graph.next_epoch()
     check(_lib.lib().fl_dense_sum_forward(_stream(A_flat), ctypes.byref(so), ctypes.byref(si), ptr(A_flat),
                                           ptr(w_flat), BL, E, n, r_size, 1 if wot_i else 0, int(K), epoch,
                                           ptr(out_ind), ptr(out_ori), ptr(out_inv), ptr(ws), ws_bytes),

@@ -30,6 +30,12 @@ extern "C" {
 #define FL_ERR_ARG 1
 #define FL_ERR_HIP 2
 
+/* Destinations with more than FL_SEG incoming positions on a side are
+ * "heavy": their slots are processed in segments of FL_SEG. */
+#define FL_SEG 32
+/* Segments are grouped FL_SUP at a time into supersegments. */
+#define FL_SUP 16
+
 /* One side (ORI or INV) of the graph in device memory.  The first six
  * fields are the reference's CSR tuple entries for that side
  * (flashlog_kernel.py:697: col_ind, group metadata) plus the prepared
@@ -52,6 +58,17 @@ typedef struct fl_side {
     const int16_t *pull_rel;       /* [M] relation of each slot            */
     const int32_t *slot_of_pos;    /* [M] inverse of pull_pos              */
     uint8_t *marks;                /* [M] scratch, epoch-tagged            */
+    int64_t nseg;                  /* segments of heavy destinations       */
+    int64_t nheavy;                /* heavy destinations                   */
+    int64_t nsup;                  /* supersegments                        */
+    const int32_t *seg_dst;        /* [nseg] destination of each segment   */
+    const int32_t *seg_start;      /* [nseg] first slot of each segment    */
+    const int32_t *seg_h;          /* [nseg] heavy index of each segment   */
+    const int32_t *heavy_dst;      /* [nheavy] heavy destinations          */
+    const int32_t *heavy_seg_ptr;  /* [nheavy+1] segments of each          */
+    const int32_t *heavy_sup_ptr;  /* [nheavy+1] supersegments of each     */
+    const int32_t *sup_h;          /* [nsup] heavy index of each           */
+    const int32_t *sup_seg0;       /* [nsup] first segment of each         */
 } fl_side;
 
 const char *fl_last_error(void);
@@ -80,6 +97,15 @@ int fl_pull_index_build(int64_t nodes, int64_t edges, int64_t groups,
                         int32_t *pull_pos, int32_t *pull_src, int16_t *pull_rel,
                         int32_t *slot_of_pos);
 
+/* Heavy-destination segments of one side from its pull_ptr (host arrays):
+ * first call with null outputs to get the counts, then with arrays of those
+ * sizes (the *_ptr arrays have nheavy+1 entries). */
+int fl_pull_segments(int64_t nodes, const int32_t *pull_ptr, int64_t *nseg,
+                     int64_t *nheavy, int64_t *nsup, int32_t *seg_dst,
+                     int32_t *seg_start, int32_t *seg_h, int32_t *heavy_dst,
+                     int32_t *heavy_seg_ptr, int32_t *heavy_sup_ptr,
+                     int32_t *sup_h, int32_t *sup_seg0);
+
 /* ---- device entry points --------------------------------------------- */
 
 /* Replaces apply_mask_cuda (flashlog.cu:1291-1340):
@@ -106,8 +132,9 @@ int fl_dense_topc_backward(void *stream, const float *grad, const float *A,
                            const int32_t *row_state, float *grad_A, int64_t BL,
                            int64_t E);
 
-/* Workspace for fl_dense_sum_forward / fl_dense_sum_backward. */
-size_t fl_dense_workspace_bytes(int64_t BL, int64_t E);
+/* Workspace for fl_dense_sum_forward on this graph and state shape. */
+size_t fl_dense_workspace_bytes(const fl_side *ori, const fl_side *inv,
+                                int64_t BL, int64_t E);
 
 /* Replaces flashlog_forward_cuda with agg_mode = sum (flashlog.cu:898-995),
  * with the CPU path's bit-exact semantics (flashlog.cpp:151-211):
@@ -124,6 +151,17 @@ int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv,
                          int64_t topk_edges, int epoch, float *out_ind,
                          float *out_ori, float *out_inv, void *workspace,
                          size_t workspace_bytes);
+
+/* ---- measurement ------------------------------------------------------ */
+
+/* No reference counterpart (the reference's FLASHLOG_STAGE_TIMING,
+ * flashlog_kernel.py:145-165, times whole stages with host syncs): per-kernel
+ * HIP-event timing on the stream each kernel runs on.  fl_prof_enable(1)
+ * starts recording and discards earlier records; fl_prof_read waits for the
+ * recorded events of `kernel` and returns their summed duration (ms) and
+ * launch count.  Single-threaded use only. */
+int fl_prof_enable(int on);
+int fl_prof_read(const char *kernel, double *total_ms, int64_t *launches);
 
 #ifdef __cplusplus
 }
