@@ -150,7 +150,7 @@ def main():
               file=sys.stderr, flush=True)
 
         # per-kernel HIP-event timing inside the library
-        kernels = ["k_topc_rows", "k_col_count", "k_block_scan", "k_col_fill", "k_c2", "k_pull_light", "k_pull_heavy", "k_heavy_offsets", "k_heavy_copy", "k_fold_heavy"]
+        kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull_light", "k_pull_heavy", "k_heavy_offsets", "k_heavy_copy", "k_fold_heavy"]
         _lib.prof_enable(True)
         for _ in range(args.profile_steps):
             step()
@@ -189,7 +189,7 @@ def main():
         "config": {"workload": "%s DRUM dense eval: E=%d, R=%d, M=%d, B=%d, N=%d, T=%d, c1=%d, c2=%d"
                    % (cfg.name, E, R, M, B, L, T, c1, cfg.c2),
                    "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2},
-        "topk_select_ms": {"c1_per_hop": per_launch["k_topc_rows"], "c2_per_hop": per_launch["k_c2"]},
+        "topk_select_ms": {"c1_per_hop": per_launch["k_topc_rows"], "c2_per_hop": per_launch["k_c2_hard"]},
         "kernel_ms_per_launch": per_launch,
         "roofline": {"kernel": "k_pull", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,

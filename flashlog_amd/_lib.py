@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 FL_SEG = 32
 FL_SUP = 16
 
@@ -34,8 +34,6 @@ class FlSide(ctypes.Structure):
         ("pull_pos", ctypes.c_void_p),
         ("pull_src", ctypes.c_void_p),
         ("pull_rel", ctypes.c_void_p),
-        ("slot_of_pos", ctypes.c_void_p),
-        ("marks", ctypes.c_void_p),
         ("nseg", ctypes.c_int64),
         ("nheavy", ctypes.c_int64),
         ("nsup", ctypes.c_int64),
@@ -55,7 +53,7 @@ _SIGS = {
     "fl_abi_version": (ctypes.c_int, []),
     "fl_csr_build_side": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64] + [ctypes.c_void_p] * 11 +
                           [ctypes.POINTER(ctypes.c_int64)]),
-    "fl_pull_index_build": (ctypes.c_int, [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 10),
+    "fl_pull_index_build": (ctypes.c_int, [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 9),
     "fl_pull_segments": (ctypes.c_int, [ctypes.c_int64, ctypes.c_void_p] + [ctypes.POINTER(ctypes.c_int64)] * 3 +
                          [ctypes.c_void_p] * 8),
     "fl_apply_mask": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
@@ -70,7 +68,7 @@ _SIGS = {
     "fl_dense_sum_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                             ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int64,
-                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_size_t]),
     "fl_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "fl_prof_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),

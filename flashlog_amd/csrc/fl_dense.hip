@@ -3,28 +3,26 @@
 // One hop of the reference's dense sum path (flashlog.cu:898-995, with the
 // CPU path's accumulation order, flashlog.cpp:151-211):
 //
-//   k_col_count   column walk of A[BL, E] (thread per entity, coalesced over
-//                 entities): identity output, per-entity nonzero count and a
-//                 bitmask of the nonzero rows, per-block totals.
-//   k_block_scan  exclusive scan of the per-block totals (one workgroup).
-//   k_col_fill    the frontier (every nonzero (source, row) pair, grouped by
-//                 source) and the transposed state AT[source][row] of every
-//                 active source.
-//   k_c2          per frontier pair and direction, the c2 edge budget as a
-//                 (threshold, cut position) pair from a wave-level radix
-//                 select over the source's relation groups; marks the pull
-//                 slots of every position leaving an active source.
-//   k_pull_light  one thread per (destination, row): walk the destination's
-//                 marked incoming slots in ascending CSR position and add
-//                 (a*w)*m in a register -- the order in which the
-//                 reference's CPU loop adds into out[row, dst].  Tiles of
-//                 destinations are staged in LDS and written coalesced.
-//   k_pull_heavy  destinations with more than FL_SEG incoming slots are cut
-//                 into segments of FL_SEG slots; one thread per (segment,
-//                 row) records its kept products, in slot order, in a list.
-//   k_fold_heavy  one thread per (heavy destination, row) adds the lists of
-//                 its segments in segment order: the same sequence of
-//                 additions as a single walk.
+//   k_col_count      identity output and the row bitmask BM[word][source]
+//                    (thread per (source, 32-row word), coalesced over sources).
+//   k_frontier       per active source: the record PK[dir][source][row] =
+//                    {a, theta, cut} of each nonzero (source, row), and the
+//                    list of pairs whose source exceeds the c2 budget.
+//   k_c2_hard        one wave per listed pair: the c2 threshold and tie cut
+//                    from a wave-level radix select over the source's
+//                    relation groups.
+//   k_pull_light     one thread per (destination, row): walk the
+//                    destination's incoming slots in ascending CSR position
+//                    and add (a*w)*m in a register -- the order in which the
+//                    reference's CPU loop adds into out[row, dst].  Tiles of
+//                    destinations are staged in LDS and written coalesced.
+//   k_pull_heavy     destinations with more than FL_SEG incoming slots are cut
+//                    into segments of FL_SEG slots; thread per (segment, row)
+//                    records its kept products, in slot order, in a list.
+//   k_heavy_offsets  per heavy destination and row, where each segment's list
+//   k_heavy_copy     goes in one contiguous run per row, and the copy there.
+//   k_fold_heavy     the runs added in order, staged through LDS: the same
+//                    sequence of additions as a single walk.
 //
 // No atomics touch output values, so results are deterministic and equal to
 // the reference CPU bits.
@@ -89,6 +87,23 @@ __device__ __forceinline__ void topc_select(const int *hist, int need, int *lds_
     __syncthreads();
 }
 
+// Loads of TOPC_U elements per thread are issued together before their use.
+constexpr int TOPC_U = 8;
+
+#define TOPC_FOR_ROW(BODY)                                                        \
+    for (int64_t base_ = 0; base_ < E; base_ += (int64_t)TOPC_NT * TOPC_U) {      \
+        float v_[TOPC_U];                                                         \
+        _Pragma("unroll") for (int u_ = 0; u_ < TOPC_U; ++u_) {                   \
+            const int64_t e_ = base_ + (int64_t)u_ * TOPC_NT + t;                 \
+            v_[u_] = e_ < E ? a[e_] : 0.0f;                                       \
+        }                                                                         \
+        _Pragma("unroll") for (int u_ = 0; u_ < TOPC_U; ++u_) {                   \
+            const int64_t e = base_ + (int64_t)u_ * TOPC_NT + t;                  \
+            const float v = v_[u_];                                               \
+            if (e < E) { BODY }                                                   \
+        }                                                                         \
+    }
+
 __global__ __launch_bounds__(TOPC_NT) void k_topc_rows(const float *__restrict__ A,
                                                         float *__restrict__ out, int64_t E,
                                                         int64_t c, int32_t *__restrict__ row_state) {
@@ -103,10 +118,7 @@ __global__ __launch_bounds__(TOPC_NT) void k_topc_rows(const float *__restrict__
     for (int i = t; i < 2048; i += TOPC_NT) hist[i] = 0;
     __syncthreads();
     int nz_local = 0;
-    for (int64_t e = t; e < E; e += TOPC_NT) {
-        float v = a[e];
-        if (v != 0.0f) { ++nz_local; atomicAdd(&hist[fl_order_key(v) >> 21], 1); }
-    }
+    TOPC_FOR_ROW(if (v != 0.0f) { ++nz_local; atomicAdd(&hist[fl_order_key(v) >> 21], 1); })
     int nz;
     (void)fl_block_excl_scan<TOPC_NT>(nz_local, lds_scan, &nz);
     const bool over = (int64_t)nz > c;
@@ -120,11 +132,8 @@ __global__ __launch_bounds__(TOPC_NT) void k_topc_rows(const float *__restrict__
         // pass 2: bits [20:10]
         for (int i = t; i < 2048; i += TOPC_NT) hist[i] = 0;
         __syncthreads();
-        for (int64_t e = t; e < E; e += TOPC_NT) {
-            float v = a[e];
-            uint32_t k = fl_order_key(v);
-            if (v != 0.0f && (k >> 21) == (prefix >> 21)) atomicAdd(&hist[(k >> 10) & 2047], 1);
-        }
+        TOPC_FOR_ROW(const uint32_t k = fl_order_key(v);
+                     if (v != 0.0f && (k >> 21) == (prefix >> 21)) atomicAdd(&hist[(k >> 10) & 2047], 1);)
         __syncthreads();
         topc_select<2048>(hist, need, lds_scan, &sel_bin, &sel_need);
         prefix |= (uint32_t)sel_bin << 10;
@@ -132,11 +141,8 @@ __global__ __launch_bounds__(TOPC_NT) void k_topc_rows(const float *__restrict__
         // pass 3: bits [9:0]
         for (int i = t; i < 2048; i += TOPC_NT) hist[i] = 0;
         __syncthreads();
-        for (int64_t e = t; e < E; e += TOPC_NT) {
-            float v = a[e];
-            uint32_t k = fl_order_key(v);
-            if (v != 0.0f && (k >> 10) == (prefix >> 10)) atomicAdd(&hist[k & 1023], 1);
-        }
+        TOPC_FOR_ROW(const uint32_t k = fl_order_key(v);
+                     if (v != 0.0f && (k >> 10) == (prefix >> 10)) atomicAdd(&hist[k & 1023], 1);)
         __syncthreads();
         topc_select<1024>(hist, need, lds_scan, &sel_bin, &sel_need);
         prefix |= (uint32_t)sel_bin;
@@ -168,18 +174,15 @@ __global__ __launch_bounds__(TOPC_NT) void k_topc_rows(const float *__restrict__
         }
     }
     // apply: out = A * keep  (keep as 1.0f / 0.0f, like the reference's A * keep)
-    for (int64_t e = t; e < E; e += TOPC_NT) {
-        float v = a[e];
-        bool keep = true;
-        if (over) {
-            keep = false;
-            if (c > 0 && v != 0.0f) {
-                uint32_t k = fl_order_key(v);
-                keep = (k > cutkey) || (k == cutkey && e <= last);
-            }
-        }
-        o[e] = v * (keep ? 1.0f : 0.0f);
-    }
+    TOPC_FOR_ROW(bool keep = true;
+                 if (over) {
+                     keep = false;
+                     if (c > 0 && v != 0.0f) {
+                         const uint32_t k = fl_order_key(v);
+                         keep = (k > cutkey) || (k == cutkey && e <= last);
+                     }
+                 }
+                 o[e] = v * (keep ? 1.0f : 0.0f);)
     if (t == 0) {
         row_state[row * 4 + 0] = over ? 1 : 0;
         row_state[row * 4 + 1] = (int32_t)cutkey;
@@ -212,85 +215,104 @@ __global__ void k_topc_backward(const float *__restrict__ grad, const float *__r
 
 // ---------------------------------------------------------------------------
 // Dense sum forward
+//
+// Per-(source, row) record PK[dir][src][row] = {a, theta bits, cut, 0}: the
+// state value and the c2 admission rule of that source in that row and
+// direction (edge at position p of relation weight w is kept iff w > theta,
+// or w == theta and p < cut; theta = 0, cut = 0 admits every w > 0 edge).
+// Records are written only for nonzero (source, row) pairs; the row bitmask
+// BM[word][src] says which ones exist.
 
 constexpr int COL_NT = 256;
 
+// One thread per (source, 32-row word): identity output and the bitmask word.
+// Threads of a wave cover consecutive sources of the same rows (coalesced);
+// the 32 loads of a word are issued before use.
 __global__ __launch_bounds__(COL_NT) void k_col_count(
     const float *__restrict__ A, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n,
-    int wot_i, float *__restrict__ out_ind, int32_t *__restrict__ colcnt,
-    uint32_t *__restrict__ bitmask, int32_t *__restrict__ blocksum) {
-    __shared__ int lds_scan[COL_NT / FL_WAVE + 1];
-    const int64_t e = (int64_t)blockIdx.x * COL_NT + threadIdx.x;
-    int cnt = 0;
-    if (e < E) {
-        const int64_t nw = (BL + 31) / 32;
-        for (int64_t wi = 0; wi < nw; ++wi) {
-            const int64_t b0 = wi * 32;
-            const int64_t b1 = (b0 + 32 < BL) ? b0 + 32 : BL;
-            uint32_t bits = 0;
-#pragma unroll 8
-            for (int64_t bl = b0; bl < b1; ++bl) {
-                const float a = A[bl * E + e];
-                const float wid = w[bl * n + (n - 1)];
-                out_ind[bl * E + e] = wot_i ? 0.0f : fl_mul(a, wid);
-                if (a != 0.0f) bits |= 1u << (bl - b0);
-            }
-            bitmask[wi * E + e] = bits;
-            cnt += __popc(bits);
-        }
-        colcnt[e] = cnt;
-    }
-    int tot;
-    (void)fl_block_excl_scan<COL_NT>(cnt, lds_scan, &tot);
-    if (threadIdx.x == 0) blocksum[blockIdx.x] = tot;
-}
-
-constexpr int SCAN_NT = 1024;
-
-__global__ __launch_bounds__(SCAN_NT) void k_block_scan(const int32_t *__restrict__ in,
-                                                         int32_t *__restrict__ out, int64_t nblk) {
-    __shared__ int lds_scan[SCAN_NT / FL_WAVE + 1];
-    const int64_t per = (nblk + SCAN_NT - 1) / SCAN_NT;
-    const int64_t b0 = threadIdx.x * per;
-    const int64_t b1 = (b0 + per < nblk) ? b0 + per : nblk;
-    int local = 0;
-    for (int64_t i = b0; i < b1; ++i) local += in[i];
-    int tot;
-    int run = fl_block_excl_scan<SCAN_NT>(local, lds_scan, &tot);
-    for (int64_t i = b0; i < b1; ++i) { int v = in[i]; out[i] = run; run += v; }
-    if (threadIdx.x == 0) out[nblk] = tot;
-}
-
-__global__ __launch_bounds__(COL_NT) void k_col_fill(
-    const float *__restrict__ A, int64_t BL, int64_t E, const int32_t *__restrict__ colcnt,
-    const uint32_t *__restrict__ bitmask, const int32_t *__restrict__ blockoff,
-    int32_t *__restrict__ colptr, int32_t *__restrict__ fr_src, int32_t *__restrict__ fr_bl,
-    float *__restrict__ AT) {
-    __shared__ int lds_scan[COL_NT / FL_WAVE + 1];
-    const int64_t e = (int64_t)blockIdx.x * COL_NT + threadIdx.x;
-    const int cnt = (e < E) ? colcnt[e] : 0;
-    int tot;
-    const int ex = fl_block_excl_scan<COL_NT>(cnt, lds_scan, &tot);
-    if (e >= E) return;
-    int slot = blockoff[blockIdx.x] + ex;
-    colptr[e] = slot;
-    if (e == E - 1) colptr[E] = slot + cnt;
-    if (cnt == 0) return;
+    int wot_i, float *__restrict__ out_ind, uint32_t *__restrict__ BM, int32_t *__restrict__ hard_count) {
+    const int64_t q = (int64_t)blockIdx.x * COL_NT + threadIdx.x;
+    if (q == 0) *hard_count = 0;
     const int64_t nw = (BL + 31) / 32;
-    float *at = AT + e * BL;
+    if (q >= nw * E) return;
+    const int64_t wi = q / E, e = q - wi * E;
+    const int64_t b0 = wi * 32;
+    const int nb = (int)((b0 + 32 < BL) ? 32 : BL - b0);
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) v[k] = (k < nb) ? A[(b0 + k) * E + e] : 0.0f;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+        if (k < nb) {
+            const float wid = w[(b0 + k) * n + (n - 1)];
+            out_ind[(b0 + k) * E + e] = wot_i ? 0.0f : fl_mul(v[k], wid);
+            if (v[k] != 0.0f) bits |= 1u << k;
+        }
+    }
+    BM[wi * E + e] = bits;
+}
+
+__device__ __forceinline__ void row_positions(const fl_side &s, int64_t src, int64_t *p0, int64_t *p1) {
+    const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
+    if (g1 > g0) {
+        *p0 = s.group_start[g0];
+        *p1 = (int64_t)s.group_start[g1 - 1] + s.group_count[g1 - 1];
+    } else {
+        *p0 = 0; *p1 = 0;
+    }
+}
+
+// One thread per source: records of every nonzero (source, row).  Rows of a
+// source whose out-degree on a side exceeds the c2 budget go to the hard list
+// (entry = src * 4 + dirmask, row) for the wave-level selection.
+__global__ __launch_bounds__(COL_NT) void k_frontier(
+    fl_side ori, fl_side inv, const float *__restrict__ A, int64_t BL, int64_t E, int64_t K, int do_topk,
+    const uint32_t *__restrict__ BM, float4 *__restrict__ PK, int32_t *__restrict__ hard_count,
+    int2 *__restrict__ hard) {
+    const int64_t e = (int64_t)blockIdx.x * COL_NT + threadIdx.x;
+    if (e >= E) return;
+    const int64_t nw = (BL + 31) / 32;
+    int cnt = 0;
+    for (int64_t wi = 0; wi < nw; ++wi) cnt += __popc(BM[wi * E + e]);
+    if (cnt == 0) return;
+    int dirmask = 0;
+    if (do_topk) {
+        int64_t p0, p1;
+        row_positions(ori, e, &p0, &p1);
+        if (p1 - p0 > K) dirmask |= 1;
+        row_positions(inv, e, &p0, &p1);
+        if (p1 - p0 > K) dirmask |= 2;
+    }
+    int slot = 0;
+    if (dirmask) slot = atomicAdd(hard_count, cnt);
+    float4 *pk0 = PK + e * BL;
+    float4 *pk1 = PK + (E + e) * BL;
     for (int64_t wi = 0; wi < nw; ++wi) {
-        const uint32_t bits = bitmask[wi * E + e];
-        const int64_t b0 = wi * 32;
-        const int64_t b1 = (b0 + 32 < BL) ? b0 + 32 : BL;
-        for (int64_t bl = b0; bl < b1; ++bl) {
-            float a = 0.0f;
-            if (bits & (1u << (bl - b0))) {
-                a = A[bl * E + e];
-                fr_src[slot] = (int32_t)e;
-                fr_bl[slot] = (int32_t)bl;
-                ++slot;
+        uint32_t bits = BM[wi * E + e];
+        while (bits) {
+            int bb[8];
+            float av[8];
+            int m = 0;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (bits) {
+                    bb[u] = __ffs(bits) - 1;
+                    bits &= bits - 1;
+                    m = u + 1;
+                    av[u] = A[(wi * 32 + bb[u]) * E + e];
+                }
             }
-            at[bl] = a;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (u < m) {
+                    const int64_t bl = wi * 32 + bb[u];
+                    const float4 r = make_float4(av[u], 0.0f, __int_as_float(0), 0.0f);
+                    pk0[bl] = r;
+                    pk1[bl] = r;
+                    if (dirmask) hard[slot++] = make_int2((int)(e * 4 + dirmask), (int)bl);
+                }
+            }
         }
     }
 }
@@ -373,62 +395,33 @@ __device__ bool c2_select(const fl_side &s, int64_t g0, int64_t g1, const float 
     return true;
 }
 
-__device__ __forceinline__ void row_positions(const fl_side &s, int64_t src, int64_t *p0, int64_t *p1) {
-    const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-    if (g1 > g0) {
-        *p0 = s.group_start[g0];
-        *p1 = (int64_t)s.group_start[g1 - 1] + s.group_count[g1 - 1];
-    } else {
-        *p0 = 0; *p1 = 0;
-    }
-}
-
 constexpr int C2_NT = 256;
 
-// One wave per frontier pair (source, row): writes TH/CUT[dir][source][row]
-// (threshold 0 and cut 0 mean "every w > 0 edge") and, for the first pair of
-// each source, tags the pull slots of the source's positions with `epoch`.
-__global__ __launch_bounds__(C2_NT) void k_c2(fl_side ori, fl_side inv, const float *__restrict__ w,
-                                              int64_t BL, int64_t E, int64_t n, int64_t r_size, int64_t K,
-                                              int do_topk, const int32_t *__restrict__ colptr,
-                                              const int32_t *__restrict__ fr_src,
-                                              const int32_t *__restrict__ fr_bl, float *__restrict__ TH,
-                                              int32_t *__restrict__ CUT, uint8_t epoch) {
+// One wave per hard (source, row): the c2 selection for each flagged side.
+__global__ __launch_bounds__(C2_NT) void k_c2_hard(fl_side ori, fl_side inv, const float *__restrict__ w,
+                                                   int64_t BL, int64_t E, int64_t n, int64_t r_size, int64_t K,
+                                                   const int32_t *__restrict__ hard_count,
+                                                   const int2 *__restrict__ hard, float4 *__restrict__ PK) {
     __shared__ int hist_all[C2_NT / FL_WAVE][256];
     const int lane = fl_lane();
     const int wid = threadIdx.x / FL_WAVE;
     int *hist = hist_all[wid];
     const int64_t nwaves = (int64_t)gridDim.x * (C2_NT / FL_WAVE);
-    const int64_t total = colptr[E];
+    const int64_t total = *hard_count;
     for (int64_t j = (int64_t)blockIdx.x * (C2_NT / FL_WAVE) + wid; j < total; j += nwaves) {
-        const int64_t src = fr_src[j];
-        const int64_t bl = fr_bl[j];
+        const int2 hj = hard[j];
+        const int64_t src = hj.x >> 2;
+        const int dm = hj.x & 3;
+        const int64_t bl = hj.y;
         for (int dir = 0; dir < 2; ++dir) {
+            if (!(dm & (1 << dir))) continue;
             const fl_side &s = dir ? inv : ori;
-            const int64_t off = dir ? r_size : 0;
-            uint32_t thk = 0;
-            int32_t cut = 0;
-            if (do_topk) {
-                const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-                int64_t p0, p1;
-                row_positions(s, src, &p0, &p1);
-                if (p1 - p0 > K) {
-                    uint32_t k2; int32_t c2;
-                    if (c2_select(s, g0, g1, w + bl * n + off, K, hist, &k2, &c2)) { thk = k2; cut = c2; }
-                }
-            }
-            if (lane == 0) {
-                const int64_t at = ((int64_t)dir * E + src) * BL + bl;
-                TH[at] = __uint_as_float(thk);
-                CUT[at] = cut;
-            }
-        }
-        if (j == colptr[src]) {
-            for (int dir = 0; dir < 2; ++dir) {
-                const fl_side &s = dir ? inv : ori;
-                int64_t p0, p1;
-                row_positions(s, src, &p0, &p1);
-                for (int64_t p = p0 + lane; p < p1; p += FL_WAVE) s.marks[s.slot_of_pos[p]] = epoch;
+            const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
+            uint32_t k2; int32_t c2;
+            if (c2_select(s, g0, g1, w + bl * n + (dir ? r_size : 0), K, hist, &k2, &c2) && lane == 0) {
+                float4 *rec = PK + ((int64_t)dir * E + src) * BL + bl;
+                rec->y = __uint_as_float(k2);
+                rec->z = __int_as_float(c2);
             }
         }
     }
@@ -436,47 +429,50 @@ __global__ __launch_bounds__(C2_NT) void k_c2(fl_side ori, fl_side inv, const fl
 
 // Products of the kept edges into one destination for one row, over slots
 // [s0, s1) in order.  Light walks accumulate; heavy walks append to `list`.
-// Loads of four slots are issued together (slot data, mask, state) before
-// the in-order accumulation.
+// Per batch of WALK_U slots: one round of slot loads (position, source,
+// relation), then one round of (mask, bitmask word, record, weight) loads,
+// then the in-order accumulation.
+constexpr int WALK_U = 8;
+
 template <bool LIST>
 __device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_t s1, int64_t bl,
                                             int64_t BL, int64_t E, int64_t n, int64_t off, int dir,
-                                            const float *__restrict__ w, const float *__restrict__ AT,
-                                            const float *__restrict__ TH, const int32_t *__restrict__ CUT,
-                                            uint8_t epoch, float *__restrict__ list, int *count) {
+                                            const float *__restrict__ w, const uint32_t *__restrict__ BM,
+                                            const float4 *__restrict__ PK, float *__restrict__ list, int *count) {
     float acc = 0.0f;
     int k = 0;
-    const int64_t plane = (int64_t)dir * E * BL;
-    for (int64_t base = s0; base < s1; base += 4) {
-        int mk[4], pos[4], src[4], rel[4];
-        float m[4], a[4];
+    const uint32_t *bmw = BM + (bl >> 5) * E;
+    const uint32_t bit = 1u << (bl & 31);
+    const float4 *pk = PK + (int64_t)dir * E * BL + bl;
+    const float *wr = w + bl * n + off;
+    for (int64_t base = s0; base < s1; base += WALK_U) {
+        int pos[WALK_U], src[WALK_U], rel[WALK_U];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < WALK_U; ++u) {
             const int64_t sl = base + u;
-            mk[u] = 0;
-            if (sl < s1) {
-                mk[u] = s.marks[sl] == epoch;
-                pos[u] = s.pull_pos[sl];
-                src[u] = s.pull_src[sl];
-                rel[u] = s.pull_rel[sl];
-            }
+            if (sl < s1) { pos[u] = s.pull_pos[sl]; src[u] = s.pull_src[sl]; rel[u] = s.pull_rel[sl]; }
+            else { pos[u] = 0; src[u] = 0; rel[u] = 0; }
         }
+        float m[WALK_U], wv[WALK_U];
+        uint32_t bw[WALK_U];
+        float4 rc[WALK_U];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (mk[u]) {
+        for (int u = 0; u < WALK_U; ++u) {
+            if (base + u < s1) {
                 m[u] = s.mask[pos[u]];
-                a[u] = AT[(int64_t)src[u] * BL + bl];
+                bw[u] = bmw[src[u]];
+                rc[u] = pk[(int64_t)src[u] * BL];
+                wv[u] = wr[rel[u]];
+            } else {
+                bw[u] = 0;
             }
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            if (!mk[u] || m[u] == 0.0f || a[u] == 0.0f) continue;
-            const int64_t at = plane + (int64_t)src[u] * BL + bl;
-            const float th = TH[at];
-            const int32_t cut = CUT[at];
-            const float wv = w[bl * n + off + rel[u]];
-            if (wv > th || (wv == th && pos[u] < cut)) {
-                const float prod = fl_mul(fl_mul(a[u], wv), m[u]);
+        for (int u = 0; u < WALK_U; ++u) {
+            if (!(bw[u] & bit) || m[u] == 0.0f) continue;
+            const float th = rc[u].y;
+            if (wv[u] > th || (wv[u] == th && pos[u] < __float_as_int(rc[u].z))) {
+                const float prod = fl_mul(fl_mul(rc[u].x, wv[u]), m[u]);
                 if (LIST) list[k++] = prod;
                 else acc = fl_add(acc, prod);
             }
@@ -493,8 +489,8 @@ constexpr int PULL_NT = 256;
 // written from a single L2.
 __global__ __launch_bounds__(PULL_NT) void k_pull_light(
     fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n,
-    int64_t r_size, int TD, int64_t ntiles, const float *__restrict__ AT, const float *__restrict__ TH,
-    const int32_t *__restrict__ CUT, uint8_t epoch, float *__restrict__ out_ori, float *__restrict__ out_inv) {
+    int64_t r_size, int TD, int64_t ntiles, const uint32_t *__restrict__ BM, const float4 *__restrict__ PK,
+    float *__restrict__ out_ori, float *__restrict__ out_inv) {
     extern __shared__ float tile[];  // [2][BL][TD]
     const int64_t per = gridDim.x / 8;
     const int64_t tid = (int64_t)(blockIdx.x % 8) * per + blockIdx.x / 8;
@@ -511,8 +507,8 @@ __global__ __launch_bounds__(PULL_NT) void k_pull_light(
                 const fl_side &s = dir ? inv : ori;
                 const int64_t s0 = s.pull_ptr[dst], s1 = s.pull_ptr[dst + 1];
                 if (s1 - s0 > FL_SEG) continue;  // heavy: written by k_fold_heavy
-                acc[dir] = walk_slots<false>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, AT, TH, CUT,
-                                             epoch, nullptr, nullptr);
+                acc[dir] = walk_slots<false>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK,
+                                             nullptr, nullptr);
             }
         }
         tile[(0 * BL + bl) * TD + dl] = acc[0];
@@ -539,10 +535,10 @@ constexpr int HEAVY_NT = FL_SUP * HEAVY_BL;  // 1024
 
 __global__ __launch_bounds__(HEAVY_NT) void k_pull_heavy(
     fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n, int64_t r_size,
-    const float *__restrict__ AT, const float *__restrict__ TH, const int32_t *__restrict__ CUT, uint8_t epoch,
-    float *__restrict__ list_ori, float *__restrict__ list_inv, int32_t *__restrict__ cnt_ori,
-    int32_t *__restrict__ cnt_inv, int32_t *__restrict__ loff_ori, int32_t *__restrict__ loff_inv,
-    int32_t *__restrict__ stot_ori, int32_t *__restrict__ stot_inv) {
+    const uint32_t *__restrict__ BM, const float4 *__restrict__ PK, float *__restrict__ list_ori,
+    float *__restrict__ list_inv, int32_t *__restrict__ cnt_ori, int32_t *__restrict__ cnt_inv,
+    int32_t *__restrict__ loff_ori, int32_t *__restrict__ loff_inv, int32_t *__restrict__ stot_ori,
+    int32_t *__restrict__ stot_inv) {
     __shared__ int cnt_lds[FL_SUP][HEAVY_BL];
     const int dir = blockIdx.x >= ori.nsup;
     const int64_t sup = dir ? blockIdx.x - ori.nsup : blockIdx.x;
@@ -560,7 +556,7 @@ __global__ __launch_bounds__(HEAVY_NT) void k_pull_heavy(
         const int64_t end = s.pull_ptr[dst + 1];
         const int64_t s1 = (s0 + FL_SEG < end) ? s0 + FL_SEG : end;
         float *list = (dir ? list_inv : list_ori) + (seg * BL + bl) * FL_SEG;
-        walk_slots<true>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, AT, TH, CUT, epoch, list, &k);
+        walk_slots<true>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, list, &k);
         (dir ? cnt_inv : cnt_ori)[seg * BL + bl] = k;
     }
     cnt_lds[sl][bll] = k;
@@ -617,7 +613,8 @@ __global__ __launch_bounds__(HSCAN_NT) void k_heavy_offsets(fl_side ori, fl_side
 }
 
 // One thread per (heavy segment, row): copy the segment's list into the
-// row's contiguous run of the destination's region.
+// row's contiguous run of the destination's region (the whole 32-value list
+// is read at once; only its first cnt values are written).
 __global__ __launch_bounds__(PULL_NT) void k_heavy_copy(
     fl_side ori, fl_side inv, int64_t BL, const float *__restrict__ list_ori, const float *__restrict__ list_inv,
     const int32_t *__restrict__ cnt_ori, const int32_t *__restrict__ cnt_inv, const int32_t *__restrict__ loff_ori,
@@ -630,30 +627,39 @@ __global__ __launch_bounds__(PULL_NT) void k_heavy_copy(
     const int64_t qq = dir ? q - nq_ori : q;
     const int64_t seg = qq / BL, bl = qq - seg * BL;
     const fl_side &s = dir ? inv : ori;
+    const int c = (dir ? cnt_inv : cnt_ori)[qq];
+    if (c == 0) return;
     const int64_t h = s.seg_h[seg];
     const int64_t g0 = s.heavy_seg_ptr[h], g1 = s.heavy_seg_ptr[h + 1];
     const int64_t sup = s.heavy_sup_ptr[h] + (seg - g0) / FL_SUP;
-    const int c = (dir ? cnt_inv : cnt_ori)[qq];
-    if (c == 0) return;
     const int64_t off = (int64_t)(dir ? sbase_inv : sbase_ori)[sup * BL + bl] + (dir ? loff_inv : loff_ori)[qq];
     const int64_t cap = (g1 - g0) * FL_SEG;
-    const float *src = (dir ? list_inv : list_ori) + qq * FL_SEG;
+    const float4 *src = (const float4 *)((dir ? list_inv : list_ori) + qq * FL_SEG);
+    float v[FL_SEG];
+#pragma unroll
+    for (int k = 0; k < FL_SEG / 4; ++k) {
+        const float4 x = src[k];
+        v[4 * k] = x.x; v[4 * k + 1] = x.y; v[4 * k + 2] = x.z; v[4 * k + 3] = x.w;
+    }
     float *dstp = (dir ? region_inv : region_ori) + g0 * FL_SEG * BL + bl * cap + off;
-    for (int k = 0; k < c; ++k) dstp[k] = src[k];
+#pragma unroll
+    for (int k = 0; k < FL_SEG; ++k)
+        if (k < c) dstp[k] = v[k];
 }
 
 // One workgroup per (heavy destination, side, block of FOLD_ROWS rows):
-// each row's run is staged through LDS in chunks and added in order by one
-// thread -- the additions of a single walk over all the slots.
+// each row's run is staged through LDS in chunks (one float4 per thread per
+// row, all issued before the LDS stores) and added in order by one thread --
+// the additions of a single walk over all the slots.
 constexpr int FOLD_NT = 256;
 constexpr int FOLD_ROWS = 16;
-constexpr int FOLD_CHUNK = 1024;
+constexpr int FOLD_CHUNK = 4 * FOLD_NT;
 
 __global__ __launch_bounds__(FOLD_NT) void k_fold_heavy(
     fl_side ori, fl_side inv, int64_t BL, int64_t E, const float *__restrict__ region_ori,
     const float *__restrict__ region_inv, const int32_t *__restrict__ tot_ori, const int32_t *__restrict__ tot_inv,
     float *__restrict__ out_ori, float *__restrict__ out_inv) {
-    __shared__ float stage[FOLD_ROWS][FOLD_CHUNK];
+    __shared__ float4 stage[FOLD_ROWS][FOLD_NT];
     __shared__ int s_tot[FOLD_ROWS];
     const int dir = blockIdx.x >= ori.nheavy;
     const int64_t h = dir ? blockIdx.x - ori.nheavy : blockIdx.x;
@@ -669,15 +675,20 @@ __global__ __launch_bounds__(FOLD_NT) void k_fold_heavy(
     for (int r = 0; r < FOLD_ROWS; ++r) maxtot = s_tot[r] > maxtot ? s_tot[r] : maxtot;
     float acc = 0.0f;
     for (int64_t c0 = 0; c0 < maxtot; c0 += FOLD_CHUNK) {
+        float4 x[FOLD_ROWS];
+#pragma unroll
         for (int r = 0; r < FOLD_ROWS; ++r) {
-            const int64_t lim = (s_tot[r] - c0 < FOLD_CHUNK) ? s_tot[r] - c0 : FOLD_CHUNK;
-            const float *src = region + g0 * FL_SEG * BL + (rb + r) * cap + c0;
-            for (int64_t k = t; k < lim; k += FOLD_NT) stage[r][k] = src[k];
+            const int64_t k = c0 + 4 * t;  // cap is a multiple of FL_SEG: a float4 is all in or all out
+            x[r] = (k < s_tot[r]) ? *(const float4 *)(region + g0 * FL_SEG * BL + (rb + r) * cap + k)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+#pragma unroll
+        for (int r = 0; r < FOLD_ROWS; ++r) stage[r][t] = x[r];
         __syncthreads();
         if (t < FOLD_ROWS && rb + t < BL) {
             const int64_t lim = (s_tot[t] - c0 < FOLD_CHUNK) ? s_tot[t] - c0 : FOLD_CHUNK;
-            for (int64_t k = 0; k < lim; ++k) acc = fl_add(acc, stage[t][k]);
+            const float *row = (const float *)stage[t];
+            for (int64_t k = 0; k < lim; ++k) acc = fl_add(acc, row[k]);
         }
         __syncthreads();
     }
@@ -694,47 +705,41 @@ using namespace fl;
 namespace {
 
 struct DenseWs {
-    int32_t *colcnt, *colptr, *blocksum, *blockoff, *fr_src, *fr_bl, *cut, *cnt_ori, *cnt_inv, *off_ori, *off_inv;
-    int32_t *stot_ori, *stot_inv, *sbase_ori, *sbase_inv, *tot_ori, *tot_inv;
-    uint32_t *bitmask;
-    float *at, *th, *list_ori, *list_inv, *region_ori, *region_inv;
+    uint32_t *bm;
+    float4 *pk;
+    int2 *hard;
+    int32_t *hard_count, *cnt_ori, *cnt_inv, *loff_ori, *loff_inv, *stot_ori, *stot_inv, *sbase_ori, *sbase_inv,
+        *tot_ori, *tot_inv;
+    float *list_ori, *list_inv, *region_ori, *region_inv;
     size_t bytes;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 DenseWs dense_ws_layout(int64_t BL, int64_t E, const fl_side *ori, const fl_side *inv, char *base) {
-    const int64_t nseg_ori = ori->nseg, nseg_inv = inv->nseg;
     DenseWs ws{};
-    const int64_t nblk = (E + COL_NT - 1) / COL_NT;
     const int64_t nw = (BL + 31) / 32;
     const int64_t cap = BL * E;
     size_t off = 0;
     auto take = [&](size_t bytes) { char *p = base ? base + off : nullptr; off += align256(bytes); return p; };
-    ws.colcnt = (int32_t *)take(sizeof(int32_t) * (size_t)(E + 1));
-    ws.colptr = (int32_t *)take(sizeof(int32_t) * (size_t)(E + 1));
-    ws.blocksum = (int32_t *)take(sizeof(int32_t) * (size_t)(nblk + 1));
-    ws.blockoff = (int32_t *)take(sizeof(int32_t) * (size_t)(nblk + 1));
-    ws.bitmask = (uint32_t *)take(sizeof(uint32_t) * (size_t)(nw * E));
-    ws.fr_src = (int32_t *)take(sizeof(int32_t) * (size_t)cap);
-    ws.fr_bl = (int32_t *)take(sizeof(int32_t) * (size_t)cap);
-    ws.at = (float *)take(sizeof(float) * (size_t)cap);
-    ws.th = (float *)take(sizeof(float) * (size_t)(2 * cap));
-    ws.cut = (int32_t *)take(sizeof(int32_t) * (size_t)(2 * cap));
-    ws.list_ori = (float *)take(sizeof(float) * (size_t)(nseg_ori * BL * FL_SEG));
-    ws.list_inv = (float *)take(sizeof(float) * (size_t)(nseg_inv * BL * FL_SEG));
-    ws.cnt_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(nseg_ori * BL));
-    ws.cnt_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(nseg_inv * BL));
-    ws.off_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(nseg_ori * BL));
-    ws.off_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(nseg_inv * BL));
-    ws.region_ori = (float *)take(sizeof(float) * (size_t)(nseg_ori * BL * FL_SEG));
-    ws.region_inv = (float *)take(sizeof(float) * (size_t)(nseg_inv * BL * FL_SEG));
+    ws.bm = (uint32_t *)take(sizeof(uint32_t) * (size_t)(nw * E));
+    ws.pk = (float4 *)take(sizeof(float4) * (size_t)(2 * cap));
+    ws.hard = (int2 *)take(sizeof(int2) * (size_t)cap);
+    ws.hard_count = (int32_t *)take(sizeof(int32_t));
+    ws.cnt_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nseg * BL));
+    ws.cnt_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(inv->nseg * BL));
+    ws.loff_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nseg * BL));
+    ws.loff_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(inv->nseg * BL));
     ws.stot_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nsup * BL));
     ws.stot_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(inv->nsup * BL));
     ws.sbase_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nsup * BL));
     ws.sbase_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(inv->nsup * BL));
     ws.tot_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nheavy * BL));
     ws.tot_inv = (int32_t *)take(sizeof(int32_t) * (size_t)(inv->nheavy * BL));
+    ws.list_ori = (float *)take(sizeof(float) * (size_t)(ori->nseg * BL * FL_SEG));
+    ws.list_inv = (float *)take(sizeof(float) * (size_t)(inv->nseg * BL * FL_SEG));
+    ws.region_ori = (float *)take(sizeof(float) * (size_t)(ori->nseg * BL * FL_SEG));
+    ws.region_inv = (float *)take(sizeof(float) * (size_t)(inv->nseg * BL * FL_SEG));
     ws.bytes = off;
     return ws;
 }
@@ -742,8 +747,7 @@ DenseWs dense_ws_layout(int64_t BL, int64_t E, const fl_side *ori, const fl_side
 int check_side(const fl_side *s, const char *name) {
     if (!s) return fl_fail(FL_ERR_ARG, "%s side is null", name);
     if (s->edges > 0 && (!s->col_ind || !s->mask || !s->group_rel || !s->group_start ||
-                         !s->group_count || !s->pull_pos || !s->pull_src || !s->pull_rel ||
-                         !s->slot_of_pos || !s->marks))
+                         !s->group_count || !s->pull_pos || !s->pull_src || !s->pull_rel))
         return fl_fail(FL_ERR_ARG, "%s side has a null array", name);
     if (!s->row_group_ptr || !s->pull_ptr) return fl_fail(FL_ERR_ARG, "%s side has null row pointers", name);
     if (s->nseg < 0 || s->nheavy < 0 || s->nsup < 0 ||
@@ -758,7 +762,7 @@ int check_side(const fl_side *s, const char *name) {
 
 extern "C" {
 
-int fl_abi_version(void) { return 3; }
+int fl_abi_version(void) { return 4; }
 
 int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool, const int32_t *order,
                   const float *weight, float *out, int64_t nnz) {
@@ -812,55 +816,53 @@ size_t fl_dense_workspace_bytes(const fl_side *ori, const fl_side *inv, int64_t 
 
 int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv, const float *A,
                          const float *w, int64_t BL, int64_t E, int64_t n, int64_t r_size, int wot_i,
-                         int64_t topk_edges, int epoch, float *out_ind, float *out_ori,
-                         float *out_inv, void *workspace, size_t workspace_bytes) {
+                         int64_t topk_edges, float *out_ind, float *out_ori, float *out_inv,
+                         void *workspace, size_t workspace_bytes) {
     int rc;
     if ((rc = check_side(ori, "ori")) != FL_OK) return rc;
     if ((rc = check_side(inv, "inv")) != FL_OK) return rc;
     if (BL < 0 || E < 0 || n < 1) return fl_fail(FL_ERR_ARG, "dense_sum_forward: bad shape");
     if (BL * E >= (int64_t)INT32_MAX) return fl_fail(FL_ERR_ARG, "dense_sum_forward: BL*E must be < 2^31");
+    if (BL > HSCAN_NT) return fl_fail(FL_ERR_ARG, "dense_sum_forward: BL=%lld above %d", (long long)BL, HSCAN_NT);
     if (r_size < 0 || 2 * r_size + 1 > n + (wot_i ? 1 : 0))
         return fl_fail(FL_ERR_ARG, "dense_sum_forward: w width %lld too small for r_size %lld",
                        (long long)n, (long long)r_size);
-    if (epoch < 1 || epoch > 255) return fl_fail(FL_ERR_ARG, "dense_sum_forward: epoch out of range");
     if (BL == 0 || E == 0) return FL_OK;
     DenseWs ws = dense_ws_layout(BL, E, ori, inv, (char *)workspace);
     if (!workspace || workspace_bytes < ws.bytes)
         return fl_fail(FL_ERR_ARG, "dense_sum_forward: workspace of %zu bytes, need %zu", workspace_bytes, ws.bytes);
     hipStream_t st = (hipStream_t)stream;
-    const int64_t nblk = (E + COL_NT - 1) / COL_NT;
-    FL_LAUNCH("k_col_count", k_col_count, dim3((unsigned)nblk), dim3(COL_NT), 0, st, A, w, BL, E, n, wot_i,
-              out_ind, ws.colcnt, ws.bitmask, ws.blocksum);
-    FL_LAUNCH("k_block_scan", k_block_scan, dim3(1), dim3(SCAN_NT), 0, st, ws.blocksum, ws.blockoff, nblk);
-    FL_LAUNCH("k_col_fill", k_col_fill, dim3((unsigned)nblk), dim3(COL_NT), 0, st, A, BL, E, ws.colcnt,
-              ws.bitmask, ws.blockoff, ws.colptr, ws.fr_src, ws.fr_bl, ws.at);
+    const int64_t nw = (BL + 31) / 32;
     const int do_topk = (topk_edges > 0 && topk_edges < ((int64_t)1 << 60)) ? 1 : 0;
     const int64_t K = do_topk ? topk_edges : 0;
-    FL_LAUNCH("k_c2", k_c2, dim3(2048), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K, do_topk,
-              ws.colptr, ws.fr_src, ws.fr_bl, ws.th, ws.cut, (uint8_t)epoch);
+    FL_LAUNCH("k_col_count", k_col_count, dim3((unsigned)((nw * E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, A,
+              w, BL, E, n, wot_i, out_ind, ws.bm, ws.hard_count);
+    FL_LAUNCH("k_frontier", k_frontier, dim3((unsigned)((E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, *ori,
+              *inv, A, BL, E, K, do_topk, ws.bm, ws.pk, ws.hard_count, ws.hard);
+    if (do_topk)
+        FL_LAUNCH("k_c2_hard", k_c2_hard, dim3(1024), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K,
+                  ws.hard_count, ws.hard, ws.pk);
     // light destinations: TD destinations per workgroup, TD*BL ~ 512 tasks
-    int TD = (int)(512 / (BL > 0 ? BL : 1));
+    int TD = (int)(512 / BL);
     if (TD < 1) TD = 1;
     if (TD > 64) TD = 64;
     const int64_t ntiles = (E + TD - 1) / TD;
     const int64_t nwg = ((ntiles + 7) / 8) * 8;
     const size_t lds = sizeof(float) * 2 * (size_t)BL * (size_t)TD;
-    if (lds > 65536) return fl_fail(FL_ERR_ARG, "dense_sum_forward: BL=%lld exceeds the LDS tile", (long long)BL);
     FL_LAUNCH("k_pull_light", k_pull_light, dim3((unsigned)nwg), dim3(PULL_NT), lds, st, *ori, *inv, w, BL, E, n,
-              r_size, TD, ntiles, ws.at, ws.th, ws.cut, (uint8_t)epoch, out_ori, out_inv);
+              r_size, TD, ntiles, ws.bm, ws.pk, out_ori, out_inv);
     const int64_t nq_seg = (ori->nseg + inv->nseg) * BL;
     if (nq_seg > 0) {
-        if (BL > HSCAN_NT) return fl_fail(FL_ERR_ARG, "dense_sum_forward: BL=%lld above %d", (long long)BL, HSCAN_NT);
         const unsigned nblc = (unsigned)((BL + HEAVY_BL - 1) / HEAVY_BL);
         FL_LAUNCH("k_pull_heavy", k_pull_heavy, dim3((unsigned)(ori->nsup + inv->nsup), nblc), dim3(HEAVY_NT), 0, st,
-                  *ori, *inv, w, BL, E, n, r_size, ws.at, ws.th, ws.cut, (uint8_t)epoch, ws.list_ori, ws.list_inv,
-                  ws.cnt_ori, ws.cnt_inv, ws.off_ori, ws.off_inv, ws.stot_ori, ws.stot_inv);
+                  *ori, *inv, w, BL, E, n, r_size, ws.bm, ws.pk, ws.list_ori, ws.list_inv, ws.cnt_ori, ws.cnt_inv,
+                  ws.loff_ori, ws.loff_inv, ws.stot_ori, ws.stot_inv);
         const size_t slds = sizeof(int) * (size_t)((HSCAN_NT / BL) * BL);
         FL_LAUNCH("k_heavy_offsets", k_heavy_offsets, dim3((unsigned)(ori->nheavy + inv->nheavy)), dim3(HSCAN_NT),
                   slds, st, *ori, *inv, BL, ws.stot_ori, ws.stot_inv, ws.sbase_ori, ws.sbase_inv, ws.tot_ori,
                   ws.tot_inv);
         FL_LAUNCH("k_heavy_copy", k_heavy_copy, dim3((unsigned)((nq_seg + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0,
-                  st, *ori, *inv, BL, ws.list_ori, ws.list_inv, ws.cnt_ori, ws.cnt_inv, ws.off_ori, ws.off_inv,
+                  st, *ori, *inv, BL, ws.list_ori, ws.list_inv, ws.cnt_ori, ws.cnt_inv, ws.loff_ori, ws.loff_inv,
                   ws.sbase_ori, ws.sbase_inv, ws.region_ori, ws.region_inv);
         FL_LAUNCH("k_fold_heavy", k_fold_heavy,
                   dim3((unsigned)(ori->nheavy + inv->nheavy), (unsigned)((BL + FOLD_ROWS - 1) / FOLD_ROWS)),

@@ -146,8 +146,7 @@ int fl_csr_build_side(int64_t edges, int64_t nodes, const int64_t *source, const
 int fl_pull_index_build(int64_t nodes, int64_t edges, int64_t groups, const int32_t *columns,
                         const int32_t *row_group_ptr, const int16_t *group_rel,
                         const int32_t *group_start, const int32_t *group_count, int32_t *pull_ptr,
-                        int32_t *pull_pos, int32_t *pull_src, int16_t *pull_rel,
-                        int32_t *slot_of_pos) {
+                        int32_t *pull_pos, int32_t *pull_src, int16_t *pull_rel) {
     if (nodes < 0 || edges < 0 || groups < 0 || edges > INT32_MAX)
         return fl::fl_fail(FL_ERR_ARG, "pull_index_build: bad sizes");
     std::vector<int32_t> src(edges, -1);
@@ -174,7 +173,6 @@ int fl_pull_index_build(int64_t nodes, int64_t edges, int64_t groups, const int3
         pull_pos[slot] = (int32_t)p;
         pull_src[slot] = src[p];
         pull_rel[slot] = rel[p];
-        slot_of_pos[p] = (int32_t)slot;
     }
     return FL_OK;
 }

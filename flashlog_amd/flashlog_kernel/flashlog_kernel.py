@@ -211,10 +211,8 @@ class _PullSide:
         pull_pos = torch.empty(m, dtype=torch.int32)
         pull_src = torch.empty(m, dtype=torch.int32)
         pull_rel = torch.empty(m, dtype=torch.int16)
-        slot_of_pos = torch.empty(m, dtype=torch.int32)
         check(_lib.lib().fl_pull_index_build(nodes, m, g, *[ptr(t) for t in host], ptr(pull_ptr),
-                                             ptr(pull_pos), ptr(pull_src), ptr(pull_rel),
-                                             ptr(slot_of_pos)), "pull_index_build")
+                                             ptr(pull_pos), ptr(pull_src), ptr(pull_rel)), "pull_index_build")
         counts = [ctypes.c_int64(0) for _ in range(3)]
         check(_lib.lib().fl_pull_segments(nodes, ptr(pull_ptr), *[ctypes.byref(c) for c in counts],
                                           *([None] * 8)), "pull_segments")
@@ -237,8 +235,6 @@ class _PullSide:
         self.pull_pos = pull_pos.to(device)
         self.pull_src = pull_src.to(device)
         self.pull_rel = pull_rel.to(device)
-        self.slot_of_pos = slot_of_pos.to(device)
-        self.marks = torch.zeros(max(m, 1), dtype=torch.uint8, device=device)
 
     def struct(self, mask):
         return FlSide(self.edges, self.groups, self.col_ind.data_ptr(), mask.data_ptr() if mask.numel() else 0,
@@ -248,7 +244,6 @@ class _PullSide:
                       self.pull_ptr.data_ptr(), self.pull_pos.data_ptr() if self.edges else 0,
                       self.pull_src.data_ptr() if self.edges else 0,
                       self.pull_rel.data_ptr() if self.edges else 0,
-                      self.slot_of_pos.data_ptr() if self.edges else 0, self.marks.data_ptr(),
                       self.nseg, self.nheavy, self.nsup, *[t.data_ptr() if t.numel() else 0 for t in (
                           self.seg_dst, self.seg_start, self.seg_h, self.heavy_dst, self.heavy_seg_ptr,
                           self.heavy_sup_ptr, self.sup_h, self.sup_seg0)])
@@ -258,15 +253,6 @@ class _Graph:
     def __init__(self, ori_args, inv_args):
         self.ori = _PullSide(*ori_args)
         self.inv = _PullSide(*inv_args)
-        self.epoch = 0
-
-    def next_epoch(self):
-        self.epoch += 1
-        if self.epoch > 255:
-            self.ori.marks.zero_()
-            self.inv.marks.zero_()
-            self.epoch = 1
-        return self.epoch
 
 
 _GRAPHS = {}
@@ -457,9 +443,8 @@ def _dense_sum_forward(A_flat, w_flat, graph, ori_mask, inv_mask, r_size, wot_i,
     si = graph.inv.struct(inv_mask)
     ws_bytes = _lib.lib().fl_dense_workspace_bytes(ctypes.byref(so), ctypes.byref(si), BL, E)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A_flat.device)
-    epoch = graph.next_epoch()
     check(_lib.lib().fl_dense_sum_forward(_stream(A_flat), ctypes.byref(so), ctypes.byref(si), ptr(A_flat),
-                                          ptr(w_flat), BL, E, n, r_size, 1 if wot_i else 0, int(K), epoch,
+                                          ptr(w_flat), BL, E, n, r_size, 1 if wot_i else 0, int(K),
                                           ptr(out_ind), ptr(out_ori), ptr(out_inv), ptr(ws), ws_bytes),
           "dense_sum_forward")
     return out_ind, out_ori, out_inv

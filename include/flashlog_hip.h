@@ -36,13 +36,12 @@ extern "C" {
 /* Segments are grouped FL_SUP at a time into supersegments. */
 #define FL_SUP 16
 
-/* One side (ORI or INV) of the graph in device memory.  The first six
- * fields are the reference's CSR tuple entries for that side
- * (flashlog_kernel.py:697: col_ind, group metadata) plus the prepared
- * CSR-ordered mask (flashlog_kernel.py:232-255).  The pull_* fields are this
- * library's destination-major index of the same positions (built once per
- * graph by fl_pull_index_build); marks is per-graph scratch of one byte per
- * position, tagged with a per-call epoch. */
+/* One side (ORI or INV) of the graph in device memory.  col_ind and the
+ * group arrays are the reference's CSR tuple entries for that side
+ * (flashlog_kernel.py:697), mask the prepared CSR-ordered mask
+ * (flashlog_kernel.py:232-255).  The pull_* and heavy-destination fields are
+ * this library's destination-major index of the same positions, built once
+ * per graph by fl_pull_index_build and fl_pull_segments. */
 typedef struct fl_side {
     int64_t edges;                 /* M: CSR positions on this side        */
     int64_t groups;                /* G: (source, relation) groups         */
@@ -56,8 +55,6 @@ typedef struct fl_side {
     const int32_t *pull_pos;       /* [M] CSR position of each slot        */
     const int32_t *pull_src;       /* [M] source entity of each slot       */
     const int16_t *pull_rel;       /* [M] relation of each slot            */
-    const int32_t *slot_of_pos;    /* [M] inverse of pull_pos              */
-    uint8_t *marks;                /* [M] scratch, epoch-tagged            */
     int64_t nseg;                  /* segments of heavy destinations       */
     int64_t nheavy;                /* heavy destinations                   */
     int64_t nsup;                  /* supersegments                        */
@@ -94,8 +91,7 @@ int fl_pull_index_build(int64_t nodes, int64_t edges, int64_t groups,
                         const int32_t *columns, const int32_t *row_group_ptr,
                         const int16_t *group_rel, const int32_t *group_start,
                         const int32_t *group_count, int32_t *pull_ptr,
-                        int32_t *pull_pos, int32_t *pull_src, int16_t *pull_rel,
-                        int32_t *slot_of_pos);
+                        int32_t *pull_pos, int32_t *pull_src, int16_t *pull_rel);
 
 /* Heavy-destination segments of one side from its pull_ptr (host arrays):
  * first call with null outputs to get the counts, then with arrays of those
@@ -143,13 +139,12 @@ size_t fl_dense_workspace_bytes(const fl_side *ori, const fl_side *inv,
  *       col[p] == d of (A[bl, src(p)] * w[bl, rel(p)]) * mask[p];
  *   out_inv likewise with INV positions and w[bl, r_size + rel].
  * topk_edges <= 0 or >= 2^60 disables c2 pruning (flashlog.cu:958).
- * epoch (1..255) tags the marks of this call; the caller clears both sides'
- * marks before reusing an epoch value. */
+ * Requires BL <= 1024 and BL*E < 2^31. */
 int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv,
                          const float *A, const float *w, int64_t BL, int64_t E,
                          int64_t n, int64_t r_size, int wot_i,
-                         int64_t topk_edges, int epoch, float *out_ind,
-                         float *out_ori, float *out_inv, void *workspace,
+                         int64_t topk_edges, float *out_ind, float *out_ori,
+                         float *out_inv, void *workspace,
                          size_t workspace_bytes);
 
 /* ---- measurement ------------------------------------------------------ */

@@ -1,0 +1,60 @@
+"""Every public name of the reference operator module exists in the mirror
+with the same parameter list (tests/golden/api_surface.json, parsed from the
+reference's flashlog_kernel.py by tests/golden/make_golden.py)."""
+import inspect
+import json
+import os
+
+import pytest
+
+SURFACE = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "api_surface.json")))
+
+# Private helpers of the reference whose internals this mirror replaces.
+INTERNAL = {"_coalesce_sparse3d_reduce", "_coalesce_sparse3d_sum_raw", "_align_sparse_grad_to_output",
+            "_cached_raw_grad", "_max_sparse3d_winner_positions", "_coalesce_sparse3d_max_raw_parts",
+            "_align_sparse_grad_to_keys", "_gather_sparse3d_grad_at_entities", "_sparse3d_grad_values_at",
+            "_sparse_topc_entries", "_prune_sparse_sources", "_restore_pruned_gradient",
+            "_sparse_sum_selected_nodes", "_sample_group_quotas", "_sampled_sparse_cpu",
+            "load_flashlog_kernel", "_kernel_stage_timing_enabled", "_kernel_cuda_reduce_enabled",
+            "_kernel_sync", "_kernel_log"}
+
+PUBLIC = sorted(k for k in SURFACE if k.split(".")[0] not in INTERNAL)
+
+# Reference classes this build does not carry yet (their entry points exist
+# as functions that raise NotImplementedError).  strict: when one is added,
+# its xfail turns into a failure here until it is removed from this set.
+NOT_YET = {"FlashLogDenseMaxFunction", "FlashLogFunctionSparse3DAllEdgesSum", "FlashLogFunctionSparse3DCPUSum",
+           "FlashLogFunctionSparse3DCPUSumNorm", "FlashLogFunctionSparse3DTopKMax",
+           "FlashLogFunctionSparse3DTopKSum", "Sparse3DNormalizeFunction"}
+
+
+def _params(name):
+    return [pytest.param(n, marks=pytest.mark.xfail(strict=True, reason="not in this build yet"))
+            if n.split(".")[0] in NOT_YET else n for n in name]
+
+
+@pytest.mark.parametrize("name", _params(PUBLIC))
+def test_signature_matches_reference(name):
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+    obj = fk
+    for part in name.split("."):
+        if not hasattr(obj, part):
+            pytest.fail("missing %s" % name)
+        obj = getattr(obj, part)
+    params = list(inspect.signature(obj).parameters)
+    want = SURFACE[name]
+    if "." in name:  # autograd staticmethods: ctx first
+        assert params == want, (params, want)
+    else:
+        assert params == want, (params, want)
+
+
+def test_package_exports():
+    import flashlog_amd
+    pkg = flashlog_amd.install()
+    import flashlog_kernel
+    assert flashlog_kernel is pkg
+    for n in ("FlashLogFunction", "_compute_active_nodes", "build_csr_structure", "prepare_csr_masks",
+              "vectorized_operation_csr", "vectorized_operation_sparse3d_csr_sum",
+              "vectorized_operation_sparse3d_csr_sum_norm", "vectorized_operation_sparse3d_fixed_relation"):
+        assert hasattr(flashlog_kernel, n)
