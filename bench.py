@@ -9,7 +9,7 @@ entities, 11 base relations, 87k triples, Zipf(1.1) degrees, batch 32, N=3,
 c1=1000, c2=400), synthetic and seeded (flashlog_amd/synth.py).
 
 Prints one JSON line.  ``value`` = queries/sec (batch / step time) with all
-inputs resident in HBM.  ``roofline`` is for the dominant kernel (k_pull),
+inputs resident in HBM.  ``roofline`` is for the propagation kernel (k_pull),
 timed with HIP events on its own stream inside the library; ``cpu_baseline``
 is the reference's CPU path (its flashlog.cpp built into oracle/_ref, serial
 as in the reference) on a bounded sample of the same workload.
@@ -62,10 +62,12 @@ def c2_admitted(wv, cnt, K):
 
 
 def hop_pull_bytes(Ap, w, csr, R, K):
-    """Algorithmic HBM bytes of one k_pull launch: the two graph outputs
-    (8 B per state cell) plus, per direction and active source, its row
-    pointers (8 B), group records (10 B each) and the column and mask of
-    every edge admitted for at least one row (8 B each)."""
+    """Algorithmic HBM bytes of one k_pull launch (the propagation kernel):
+    the two graph outputs (8 B per state cell) plus, per direction and active
+    source, its row pointers (8 B), group records (10 B each) and the column
+    and mask of every edge admitted for at least one row (8 B each) -- the
+    graph term of SURVEY.md's dense-sum formula.  The identity output and the
+    read of A (8 B per cell) belong to k_col_count."""
     import numpy as np
     BL, E = Ap.shape
     nz = Ap != 0
@@ -150,7 +152,8 @@ def main():
               file=sys.stderr, flush=True)
 
         # per-kernel HIP-event timing inside the library
-        kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull_light", "k_pull_heavy", "k_heavy_offsets", "k_heavy_copy", "k_fold_heavy"]
+        kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull", "k_heavy_offsets",
+                   "k_heavy_copy", "k_fold_heavy"]
         _lib.prof_enable(True)
         for _ in range(args.profile_steps):
             step()
@@ -167,7 +170,7 @@ def main():
         csr_np = [c.cpu().numpy() for c in csr]
         hop_bytes = [hop_pull_bytes(a.reshape(B * L, E).cpu().numpy(), w.reshape(B * L, n).cpu().numpy(),
                                     csr_np, R, K) for a, w in cap]
-    pull_ms = per_launch["k_pull_light"]
+    pull_ms = per_launch["k_pull"]
     bytes_per_launch = float(np.mean(hop_bytes))
     achieved = bytes_per_launch / (pull_ms * 1e-3) / 1e9 if pull_ms > 0 else 0.0
 

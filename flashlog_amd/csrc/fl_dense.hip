@@ -11,14 +11,14 @@
 //   k_c2_hard        one wave per listed pair: the c2 threshold and tie cut
 //                    from a wave-level radix select over the source's
 //                    relation groups.
-//   k_pull_light     one thread per (destination, row): walk the
-//                    destination's incoming slots in ascending CSR position
-//                    and add (a*w)*m in a register -- the order in which the
-//                    reference's CPU loop adds into out[row, dst].  Tiles of
-//                    destinations are staged in LDS and written coalesced.
-//   k_pull_heavy     destinations with more than FL_SEG incoming slots are cut
-//                    into segments of FL_SEG slots; thread per (segment, row)
-//                    records its kept products, in slot order, in a list.
+//   k_pull           the propagation: one thread per (light destination,
+//                    row) walks the destination's incoming slots in ascending
+//                    CSR position and adds (a*w)*m in a register -- the order
+//                    in which the reference's CPU loop adds into out[row,
+//                    dst] -- with tiles of destinations staged in LDS and
+//                    written coalesced; destinations with more than FL_SEG
+//                    incoming slots are cut into FL_SEG-slot segments whose
+//                    kept products are listed, in slot order, per row.
 //   k_heavy_offsets  per heavy destination and row, where each segment's list
 //   k_heavy_copy     goes in one contiguous run per row, and the copy there.
 //   k_fold_heavy     the runs added in order, staged through LDS: the same
@@ -216,12 +216,12 @@ __global__ void k_topc_backward(const float *__restrict__ grad, const float *__r
 // ---------------------------------------------------------------------------
 // Dense sum forward
 //
-// Per-(source, row) record PK[dir][src][row] = {a, theta bits, cut, 0}: the
-// state value and the c2 admission rule of that source in that row and
-// direction (edge at position p of relation weight w is kept iff w > theta,
-// or w == theta and p < cut; theta = 0, cut = 0 admits every w > 0 edge).
-// Records are written only for nonzero (source, row) pairs; the row bitmask
-// BM[word][src] says which ones exist.
+// Per-(source, row) record PK[dir][src][row] = {a, theta}: the state value
+// and the c2 threshold of that source in that row and direction; the tie cut
+// CUT[dir][src][row] is written only where theta > 0.  An edge at position p
+// of relation weight w is kept iff w > theta, or w == theta > 0 and p < cut
+// (theta = 0 admits every w > 0 edge).  Records exist only for nonzero
+// (source, row) pairs; the row bitmask BM[word][src] says which.
 
 constexpr int COL_NT = 256;
 
@@ -268,7 +268,7 @@ __device__ __forceinline__ void row_positions(const fl_side &s, int64_t src, int
 // (entry = src * 4 + dirmask, row) for the wave-level selection.
 __global__ __launch_bounds__(COL_NT) void k_frontier(
     fl_side ori, fl_side inv, const float *__restrict__ A, int64_t BL, int64_t E, int64_t K, int do_topk,
-    const uint32_t *__restrict__ BM, float4 *__restrict__ PK, int32_t *__restrict__ hard_count,
+    const uint32_t *__restrict__ BM, float2 *__restrict__ PK, int32_t *__restrict__ hard_count,
     int2 *__restrict__ hard) {
     const int64_t e = (int64_t)blockIdx.x * COL_NT + threadIdx.x;
     if (e >= E) return;
@@ -286,8 +286,8 @@ __global__ __launch_bounds__(COL_NT) void k_frontier(
     }
     int slot = 0;
     if (dirmask) slot = atomicAdd(hard_count, cnt);
-    float4 *pk0 = PK + e * BL;
-    float4 *pk1 = PK + (E + e) * BL;
+    float2 *pk0 = PK + e * BL;
+    float2 *pk1 = PK + (E + e) * BL;
     for (int64_t wi = 0; wi < nw; ++wi) {
         uint32_t bits = BM[wi * E + e];
         while (bits) {
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(COL_NT) void k_frontier(
             for (int u = 0; u < 8; ++u) {
                 if (u < m) {
                     const int64_t bl = wi * 32 + bb[u];
-                    const float4 r = make_float4(av[u], 0.0f, __int_as_float(0), 0.0f);
+                    const float2 r = make_float2(av[u], 0.0f);
                     pk0[bl] = r;
                     pk1[bl] = r;
                     if (dirmask) hard[slot++] = make_int2((int)(e * 4 + dirmask), (int)bl);
@@ -401,7 +401,8 @@ constexpr int C2_NT = 256;
 __global__ __launch_bounds__(C2_NT) void k_c2_hard(fl_side ori, fl_side inv, const float *__restrict__ w,
                                                    int64_t BL, int64_t E, int64_t n, int64_t r_size, int64_t K,
                                                    const int32_t *__restrict__ hard_count,
-                                                   const int2 *__restrict__ hard, float4 *__restrict__ PK) {
+                                                   const int2 *__restrict__ hard, float2 *__restrict__ PK,
+                                                   int32_t *__restrict__ CUT) {
     __shared__ int hist_all[C2_NT / FL_WAVE][256];
     const int lane = fl_lane();
     const int wid = threadIdx.x / FL_WAVE;
@@ -419,9 +420,9 @@ __global__ __launch_bounds__(C2_NT) void k_c2_hard(fl_side ori, fl_side inv, con
             const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
             uint32_t k2; int32_t c2;
             if (c2_select(s, g0, g1, w + bl * n + (dir ? r_size : 0), K, hist, &k2, &c2) && lane == 0) {
-                float4 *rec = PK + ((int64_t)dir * E + src) * BL + bl;
-                rec->y = __uint_as_float(k2);
-                rec->z = __int_as_float(c2);
+                const int64_t at = ((int64_t)dir * E + src) * BL + bl;
+                PK[at].y = __uint_as_float(k2);
+                CUT[at] = c2;
             }
         }
     }
@@ -430,20 +431,21 @@ __global__ __launch_bounds__(C2_NT) void k_c2_hard(fl_side ori, fl_side inv, con
 // Products of the kept edges into one destination for one row, over slots
 // [s0, s1) in order.  Light walks accumulate; heavy walks append to `list`.
 // Per batch of WALK_U slots: one round of slot loads (position, source,
-// relation), then one round of (mask, bitmask word, record, weight) loads,
-// then the in-order accumulation.
+// relation); one round of (mask, bitmask word, weight, record {a, theta});
+// the tie cut only on an exact tie; then the in-order accumulation.
 constexpr int WALK_U = 8;
 
 template <bool LIST>
 __device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_t s1, int64_t bl,
                                             int64_t BL, int64_t E, int64_t n, int64_t off, int dir,
                                             const float *__restrict__ w, const uint32_t *__restrict__ BM,
-                                            const float4 *__restrict__ PK, float *__restrict__ list, int *count) {
+                                            const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
+                                            float *__restrict__ list, int *count) {
     float acc = 0.0f;
     int k = 0;
     const uint32_t *bmw = BM + (bl >> 5) * E;
     const uint32_t bit = 1u << (bl & 31);
-    const float4 *pk = PK + (int64_t)dir * E * BL + bl;
+    const int64_t plane = (int64_t)dir * E * BL + bl;
     const float *wr = w + bl * n + off;
     for (int64_t base = s0; base < s1; base += WALK_U) {
         int pos[WALK_U], src[WALK_U], rel[WALK_U];
@@ -455,23 +457,24 @@ __device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_
         }
         float m[WALK_U], wv[WALK_U];
         uint32_t bw[WALK_U];
-        float4 rc[WALK_U];
+        float2 rc[WALK_U];
 #pragma unroll
         for (int u = 0; u < WALK_U; ++u) {
+            bw[u] = 0;
             if (base + u < s1) {
                 m[u] = s.mask[pos[u]];
-                bw[u] = bmw[src[u]];
-                rc[u] = pk[(int64_t)src[u] * BL];
                 wv[u] = wr[rel[u]];
-            } else {
-                bw[u] = 0;
+                bw[u] = bmw[src[u]];
+                rc[u] = PK[plane + (int64_t)src[u] * BL];
             }
         }
 #pragma unroll
         for (int u = 0; u < WALK_U; ++u) {
-            if (!(bw[u] & bit) || m[u] == 0.0f) continue;
+            if (!(bw[u] & bit) || m[u] == 0.0f || !(wv[u] > 0.0f)) continue;
             const float th = rc[u].y;
-            if (wv[u] > th || (wv[u] == th && pos[u] < __float_as_int(rc[u].z))) {
+            bool kept = wv[u] > th;
+            if (!kept && wv[u] == th) kept = pos[u] < CUT[plane + (int64_t)src[u] * BL];
+            if (kept) {
                 const float prod = fl_mul(fl_mul(rc[u].x, wv[u]), m[u]);
                 if (LIST) list[k++] = prod;
                 else acc = fl_add(acc, prod);
@@ -483,89 +486,105 @@ __device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_
 }
 
 constexpr int PULL_NT = 256;
+constexpr int HEAVY_BL = 64;
+constexpr int HEAVY_TASKS = FL_SUP * HEAVY_BL;  // (segment, row) tasks of one heavy block
 
-// One workgroup per tile of TD destinations; tiles are dealt to XCDs in
-// contiguous ranges (workgroup b runs on XCD b % 8), so each output line is
-// written from a single L2.
-__global__ __launch_bounds__(PULL_NT) void k_pull_light(
-    fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n,
-    int64_t r_size, int TD, int64_t ntiles, const uint32_t *__restrict__ BM, const float4 *__restrict__ PK,
-    float *__restrict__ out_ori, float *__restrict__ out_inv) {
-    extern __shared__ float tile[];  // [2][BL][TD]
-    const int64_t per = gridDim.x / 8;
-    const int64_t tid = (int64_t)(blockIdx.x % 8) * per + blockIdx.x / 8;
-    if (tid >= ntiles) return;
-    const int64_t d0 = tid * TD;
-    const int64_t ntask = (int64_t)TD * BL;
-    for (int64_t q = threadIdx.x; q < ntask; q += PULL_NT) {
-        const int64_t dl = q / BL, bl = q - dl * BL;
-        const int64_t dst = d0 + dl;
-        float acc[2] = {0.0f, 0.0f};
-        if (dst < E) {
+// The propagation kernel.  Workgroups [nheavy_wg, +nlight) take tiles of TD light
+// destinations (in-degree <= FL_SEG): one thread per (destination, row)
+// walks the destination's slots in ascending CSR position and adds in a
+// register -- the reference CPU loop's order -- then the tile is written
+// from LDS, coalesced.  Light tiles are dealt to XCDs in contiguous ranges
+// (workgroup b runs on XCD b % 8), so each output line is written from one
+// L2.  Workgroups [0, nheavy_wg) -- the longer ones, dispatched first --
+// take (supersegment, block of 64 rows) of heavy
+// destinations: thread (segment, row) records its kept products in slot order
+// (list, cnt), the offset of its run inside the supersegment (loff) and the
+// supersegment's per-row total (stot); the fold finishes those rows.
+__global__ __launch_bounds__(PULL_NT) void k_pull(
+    fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n, int64_t r_size,
+    int TD, int64_t ntiles, int64_t nlight, int64_t nheavy_wg, const uint32_t *__restrict__ BM,
+    const float2 *__restrict__ PK,
+    const int32_t *__restrict__ CUT, float *__restrict__ out_ori, float *__restrict__ out_inv,
+    float *__restrict__ list_ori, float *__restrict__ list_inv, int32_t *__restrict__ cnt_ori,
+    int32_t *__restrict__ cnt_inv, int32_t *__restrict__ loff_ori, int32_t *__restrict__ loff_inv,
+    int32_t *__restrict__ stot_ori, int32_t *__restrict__ stot_inv) {
+    extern __shared__ float tile[];  // light: [2][BL][TD]
+    __shared__ int cnt_lds[FL_SUP][HEAVY_BL];
+    if ((int64_t)blockIdx.x >= nheavy_wg) {
+        const int64_t lb = (int64_t)blockIdx.x - nheavy_wg;  // nheavy_wg is a multiple of 8
+        const int64_t per = nlight / 8;
+        const int64_t tid = (lb % 8) * per + lb / 8;
+        if (tid >= ntiles) return;
+        const int64_t d0 = tid * TD;
+        const int64_t ntask = (int64_t)TD * BL;
+        for (int64_t q = threadIdx.x; q < ntask; q += PULL_NT) {
+            const int64_t dl = q / BL, bl = q - dl * BL;
+            const int64_t dst = d0 + dl;
+            float acc[2] = {0.0f, 0.0f};
+            if (dst < E) {
 #pragma unroll
-            for (int dir = 0; dir < 2; ++dir) {
-                const fl_side &s = dir ? inv : ori;
-                const int64_t s0 = s.pull_ptr[dst], s1 = s.pull_ptr[dst + 1];
-                if (s1 - s0 > FL_SEG) continue;  // heavy: written by k_fold_heavy
-                acc[dir] = walk_slots<false>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK,
-                                             nullptr, nullptr);
+                for (int dir = 0; dir < 2; ++dir) {
+                    const fl_side &s = dir ? inv : ori;
+                    const int64_t s0 = s.pull_ptr[dst], s1 = s.pull_ptr[dst + 1];
+                    if (s1 - s0 > FL_SEG) continue;  // heavy: written by k_fold_heavy
+                    acc[dir] = walk_slots<false>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT,
+                                                 nullptr, nullptr);
+                }
+            }
+            tile[(0 * BL + bl) * TD + dl] = acc[0];
+            tile[(1 * BL + bl) * TD + dl] = acc[1];
+        }
+        __syncthreads();
+        for (int64_t i = threadIdx.x; i < ntask; i += PULL_NT) {
+            const int64_t bl = i / TD, dl = i - bl * TD;
+            const int64_t dst = d0 + dl;
+            if (dst < E) {
+                out_ori[bl * E + dst] = tile[(0 * BL + bl) * TD + dl];
+                out_inv[bl * E + dst] = tile[(1 * BL + bl) * TD + dl];
             }
         }
-        tile[(0 * BL + bl) * TD + dl] = acc[0];
-        tile[(1 * BL + bl) * TD + dl] = acc[1];
+        return;
     }
-    __syncthreads();
-    for (int64_t i = threadIdx.x; i < ntask; i += PULL_NT) {
-        const int64_t bl = i / TD, dl = i - bl * TD;
-        const int64_t dst = d0 + dl;
-        if (dst < E) {
-            out_ori[bl * E + dst] = tile[(0 * BL + bl) * TD + dl];
-            out_inv[bl * E + dst] = tile[(1 * BL + bl) * TD + dl];
-        }
-    }
-}
-
-// Heavy destinations.  Segments of FL_SEG slots are grouped in supersegments
-// of FL_SUP segments.  One workgroup per (supersegment, block of 64 rows),
-// thread (segment, row): walk the segment, record its kept products in slot
-// order (list, cnt), and the offset of this segment's run within the
-// supersegment (local_off) and the supersegment's total per row (sup_tot).
-constexpr int HEAVY_BL = 64;
-constexpr int HEAVY_NT = FL_SUP * HEAVY_BL;  // 1024
-
-__global__ __launch_bounds__(HEAVY_NT) void k_pull_heavy(
-    fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n, int64_t r_size,
-    const uint32_t *__restrict__ BM, const float4 *__restrict__ PK, float *__restrict__ list_ori,
-    float *__restrict__ list_inv, int32_t *__restrict__ cnt_ori, int32_t *__restrict__ cnt_inv,
-    int32_t *__restrict__ loff_ori, int32_t *__restrict__ loff_inv, int32_t *__restrict__ stot_ori,
-    int32_t *__restrict__ stot_inv) {
-    __shared__ int cnt_lds[FL_SUP][HEAVY_BL];
-    const int dir = blockIdx.x >= ori.nsup;
-    const int64_t sup = dir ? blockIdx.x - ori.nsup : blockIdx.x;
+    // heavy block
+    const int64_t nblc = (BL + HEAVY_BL - 1) / HEAVY_BL;
+    const int64_t hb = blockIdx.x;
+    const int64_t supg = hb / nblc;
+    const int64_t blc = hb - supg * nblc;
+    if (supg >= ori.nsup + inv.nsup) return;  // padding of the heavy range
+    const int dir = supg >= ori.nsup;
+    const int64_t sup = dir ? supg - ori.nsup : supg;
     const fl_side &s = dir ? inv : ori;
-    const int sl = threadIdx.x / HEAVY_BL, bll = threadIdx.x % HEAVY_BL;
-    const int64_t bl = (int64_t)blockIdx.y * HEAVY_BL + bll;
     const int64_t h = s.sup_h[sup];
     const int64_t seg0 = s.sup_seg0[sup];
     const int64_t segend = s.heavy_seg_ptr[h + 1];
-    const int64_t seg = seg0 + sl;
-    int k = 0;
-    if (seg < segend && bl < BL) {
-        const int64_t dst = s.heavy_dst[h];
-        const int64_t s0 = s.seg_start[seg];
-        const int64_t end = s.pull_ptr[dst + 1];
-        const int64_t s1 = (s0 + FL_SEG < end) ? s0 + FL_SEG : end;
-        float *list = (dir ? list_inv : list_ori) + (seg * BL + bl) * FL_SEG;
-        walk_slots<true>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, list, &k);
-        (dir ? cnt_inv : cnt_ori)[seg * BL + bl] = k;
+    const int64_t dst = s.heavy_dst[h];
+    const int64_t end = s.pull_ptr[dst + 1];
+    for (int task = threadIdx.x; task < HEAVY_TASKS; task += PULL_NT) {
+        const int sl = task / HEAVY_BL, bll = task % HEAVY_BL;
+        const int64_t bl = blc * HEAVY_BL + bll;
+        const int64_t seg = seg0 + sl;
+        int k = 0;
+        if (seg < segend && bl < BL) {
+            const int64_t s0 = s.seg_start[seg];
+            const int64_t s1 = (s0 + FL_SEG < end) ? s0 + FL_SEG : end;
+            float *list = (dir ? list_inv : list_ori) + (seg * BL + bl) * FL_SEG;
+            walk_slots<true>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT, list, &k);
+            (dir ? cnt_inv : cnt_ori)[seg * BL + bl] = k;
+        }
+        cnt_lds[sl][bll] = k;
     }
-    cnt_lds[sl][bll] = k;
     __syncthreads();
-    if (seg < segend && bl < BL) {
-        int run = 0;
-        for (int q = 0; q < sl; ++q) run += cnt_lds[q][bll];
-        (dir ? loff_inv : loff_ori)[seg * BL + bl] = run;
-        if (seg == segend - 1 || sl == FL_SUP - 1) (dir ? stot_inv : stot_ori)[sup * BL + bl] = run + k;
+    for (int task = threadIdx.x; task < HEAVY_TASKS; task += PULL_NT) {
+        const int sl = task / HEAVY_BL, bll = task % HEAVY_BL;
+        const int64_t bl = blc * HEAVY_BL + bll;
+        const int64_t seg = seg0 + sl;
+        if (seg < segend && bl < BL) {
+            int run = 0;
+            for (int q = 0; q < sl; ++q) run += cnt_lds[q][bll];
+            (dir ? loff_inv : loff_ori)[seg * BL + bl] = run;
+            if (seg == segend - 1 || sl == FL_SUP - 1)
+                (dir ? stot_inv : stot_ori)[sup * BL + bl] = run + cnt_lds[sl][bll];
+        }
     }
 }
 
@@ -706,7 +725,8 @@ namespace {
 
 struct DenseWs {
     uint32_t *bm;
-    float4 *pk;
+    float2 *pk;
+    int32_t *cut;
     int2 *hard;
     int32_t *hard_count, *cnt_ori, *cnt_inv, *loff_ori, *loff_inv, *stot_ori, *stot_inv, *sbase_ori, *sbase_inv,
         *tot_ori, *tot_inv;
@@ -723,7 +743,8 @@ DenseWs dense_ws_layout(int64_t BL, int64_t E, const fl_side *ori, const fl_side
     size_t off = 0;
     auto take = [&](size_t bytes) { char *p = base ? base + off : nullptr; off += align256(bytes); return p; };
     ws.bm = (uint32_t *)take(sizeof(uint32_t) * (size_t)(nw * E));
-    ws.pk = (float4 *)take(sizeof(float4) * (size_t)(2 * cap));
+    ws.pk = (float2 *)take(sizeof(float2) * (size_t)(2 * cap));
+    ws.cut = (int32_t *)take(sizeof(int32_t) * (size_t)(2 * cap));
     ws.hard = (int2 *)take(sizeof(int2) * (size_t)cap);
     ws.hard_count = (int32_t *)take(sizeof(int32_t));
     ws.cnt_ori = (int32_t *)take(sizeof(int32_t) * (size_t)(ori->nseg * BL));
@@ -841,22 +862,22 @@ int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv, c
               *inv, A, BL, E, K, do_topk, ws.bm, ws.pk, ws.hard_count, ws.hard);
     if (do_topk)
         FL_LAUNCH("k_c2_hard", k_c2_hard, dim3(1024), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K,
-                  ws.hard_count, ws.hard, ws.pk);
+                  ws.hard_count, ws.hard, ws.pk, ws.cut);
     // light destinations: TD destinations per workgroup, TD*BL ~ 512 tasks
     int TD = (int)(512 / BL);
     if (TD < 1) TD = 1;
     if (TD > 64) TD = 64;
     const int64_t ntiles = (E + TD - 1) / TD;
-    const int64_t nwg = ((ntiles + 7) / 8) * 8;
+    const int64_t nlight = ((ntiles + 7) / 8) * 8;
+    const int64_t nblc = (BL + HEAVY_BL - 1) / HEAVY_BL;
+    const int64_t nheavy_wg = (((ori->nsup + inv->nsup) * nblc + 7) / 8) * 8;
     const size_t lds = sizeof(float) * 2 * (size_t)BL * (size_t)TD;
-    FL_LAUNCH("k_pull_light", k_pull_light, dim3((unsigned)nwg), dim3(PULL_NT), lds, st, *ori, *inv, w, BL, E, n,
-              r_size, TD, ntiles, ws.bm, ws.pk, out_ori, out_inv);
+    FL_LAUNCH("k_pull", k_pull, dim3((unsigned)(nlight + nheavy_wg)), dim3(PULL_NT), lds, st, *ori, *inv, w, BL,
+              E, n, r_size, TD, ntiles, nlight, nheavy_wg, ws.bm, ws.pk, ws.cut, out_ori, out_inv, ws.list_ori,
+              ws.list_inv,
+              ws.cnt_ori, ws.cnt_inv, ws.loff_ori, ws.loff_inv, ws.stot_ori, ws.stot_inv);
     const int64_t nq_seg = (ori->nseg + inv->nseg) * BL;
     if (nq_seg > 0) {
-        const unsigned nblc = (unsigned)((BL + HEAVY_BL - 1) / HEAVY_BL);
-        FL_LAUNCH("k_pull_heavy", k_pull_heavy, dim3((unsigned)(ori->nsup + inv->nsup), nblc), dim3(HEAVY_NT), 0, st,
-                  *ori, *inv, w, BL, E, n, r_size, ws.bm, ws.pk, ws.list_ori, ws.list_inv, ws.cnt_ori, ws.cnt_inv,
-                  ws.loff_ori, ws.loff_inv, ws.stot_ori, ws.stot_inv);
         const size_t slds = sizeof(int) * (size_t)((HSCAN_NT / BL) * BL);
         FL_LAUNCH("k_heavy_offsets", k_heavy_offsets, dim3((unsigned)(ori->nheavy + inv->nheavy)), dim3(HSCAN_NT),
                   slds, st, *ori, *inv, BL, ws.stot_ori, ws.stot_inv, ws.sbase_ori, ws.sbase_inv, ws.tot_ori,
