@@ -70,6 +70,11 @@ _SIGS = {
                                             ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int64,
                                             ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_size_t]),
+    "fl_dense_backward_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
+                                                            ctypes.c_int64, ctypes.c_int64]),
+    "fl_dense_sum_backward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide)] +
+                              [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_int64] +
+                              [ctypes.c_void_p] * 3 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t]),
     "fl_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "fl_prof_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_int64)]),

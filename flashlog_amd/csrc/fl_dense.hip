@@ -225,7 +225,8 @@ __global__ void k_topc_backward(const float *__restrict__ grad, const float *__r
 
 constexpr int COL_NT = 256;
 
-// One thread per (source, 32-row word): identity output and the bitmask word.
+// One thread per (source, 32-row word): identity output (skipped when
+// out_ind is null) and the bitmask word.
 // Threads of a wave cover consecutive sources of the same rows (coalesced);
 // the 32 loads of a word are issued before use.
 __global__ __launch_bounds__(COL_NT) void k_col_count(
@@ -245,8 +246,10 @@ __global__ __launch_bounds__(COL_NT) void k_col_count(
 #pragma unroll
     for (int k = 0; k < 32; ++k) {
         if (k < nb) {
-            const float wid = w[(b0 + k) * n + (n - 1)];
-            out_ind[(b0 + k) * E + e] = wot_i ? 0.0f : fl_mul(v[k], wid);
+            if (out_ind) {
+                const float wid = w[(b0 + k) * n + (n - 1)];
+                out_ind[(b0 + k) * E + e] = wot_i ? 0.0f : fl_mul(v[k], wid);
+            }
             if (v[k] != 0.0f) bits |= 1u << k;
         }
     }
@@ -714,6 +717,183 @@ __global__ __launch_bounds__(FOLD_NT) void k_fold_heavy(
     if (t < FOLD_ROWS && rb + t < BL) (dir ? out_inv : out_ori)[(rb + t) * E + s.heavy_dst[h]] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Dense sum backward (flashlog.cpp:91-146,216-278)
+//
+//   k_bwd_identity  per row: gA = 0 + g_ind * w[n-1] for every entity, and
+//                   gw[row, n-1] = sum_e g_ind * A (fixed tree order).
+//   (frontier)      the forward's k_col_count / k_frontier / k_c2_hard on the
+//                   same A and w give the same admitted edges.
+//   k_row_list      per row, its active sources in ascending order.
+//   k_bwd_rows      one thread per active (source, row): the ORI then INV row
+//                   walk of the reference, adding (go*w)*m onto the identity
+//                   term in CSR order (bit-exact gA), and per relation group
+//                   the partial sum of (go*a)*m into the pair's row of PG.
+//   k_bwd_gw        per row: gw[row, rel] = the pair partials of rel added in
+//                   ascending source order, staged through LDS.
+
+constexpr int BWD_NT = 256;
+
+__global__ __launch_bounds__(BWD_NT) void k_bwd_identity(const float *__restrict__ g_ind, const float *__restrict__ A,
+                                                        const float *__restrict__ w, int64_t E, int64_t n, int wot_i,
+                                                        float *__restrict__ gA, float *__restrict__ gw) {
+    __shared__ float part[BWD_NT];
+    const int64_t bl = blockIdx.x;
+    const int t = threadIdx.x;
+    const float wid = w[bl * n + (n - 1)];
+    float acc = 0.0f;
+    for (int64_t e = t; e < E; e += BWD_NT) {
+        const int64_t i = bl * E + e;
+        if (wot_i) {
+            gA[i] = 0.0f;
+        } else {
+            const float gi = g_ind[i];
+            gA[i] = fl_add(0.0f, fl_mul(gi, wid));
+            acc = fl_add(acc, fl_mul(gi, A[i]));
+        }
+    }
+    part[t] = acc;
+    __syncthreads();
+    for (int st = BWD_NT / 2; st > 0; st >>= 1) {
+        if (t < st) part[t] = fl_add(part[t], part[t + st]);
+        __syncthreads();
+    }
+    for (int64_t r = t; r < n; r += BWD_NT) gw[bl * n + r] = 0.0f;
+    __syncthreads();
+    if (t == 0 && !wot_i) gw[bl * n + (n - 1)] = part[0];
+}
+
+constexpr int RL_NT = 1024;
+
+// Ordered compaction of the row's active sources (bit bl of BM[bl/32][src]).
+__global__ __launch_bounds__(RL_NT) void k_row_list(const uint32_t *__restrict__ BM, int64_t E,
+                                                    int32_t *__restrict__ rowlist, int32_t *__restrict__ rowcnt) {
+    __shared__ int lds_scan[RL_NT / FL_WAVE + 1];
+    const int64_t bl = blockIdx.x;
+    const uint32_t *bm = BM + (bl >> 5) * E;
+    const uint32_t bit = 1u << (bl & 31);
+    int32_t *out = rowlist + bl * E;
+    int run = 0;
+    for (int64_t base = 0; base < E; base += RL_NT) {
+        const int64_t e = base + threadIdx.x;
+        const int f = (e < E && (bm[e] & bit)) ? 1 : 0;
+        int tot;
+        const int ex = fl_block_excl_scan<RL_NT>(f, lds_scan, &tot);
+        if (f) out[run + ex] = (int32_t)e;
+        run += tot;
+    }
+    if (threadIdx.x == 0) rowcnt[bl] = run;
+}
+
+// Kept range of group g for (source, row): [start, start + take).
+__device__ __forceinline__ int64_t group_take(float wv, float th, int32_t cut, int64_t start, int64_t count) {
+    if (!(wv > 0.0f)) return 0;
+    if (wv > th) return count;
+    if (wv == th) {
+        const int64_t t = (int64_t)cut - start;
+        return t <= 0 ? 0 : (t < count ? t : count);
+    }
+    return 0;
+}
+
+__device__ __forceinline__ float bwd_walk(const fl_side &s, int64_t src, int64_t bl, int64_t BL, int64_t E,
+                                          int64_t n, int64_t off, int dir, float a, const float *__restrict__ w,
+                                          const float *__restrict__ grad, const float2 *__restrict__ PK,
+                                          const int32_t *__restrict__ CUT, float acc, float *__restrict__ pg) {
+    const int64_t at = ((int64_t)dir * E + src) * BL + bl;
+    const float th = PK[at].y;
+    const int32_t cut = th > 0.0f ? CUT[at] : 0;
+    const float *wr = w + bl * n + off;
+    const float *gr = grad + bl * E;
+    const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
+    for (int64_t g = g0; g < g1; ++g) {
+        const int rel = s.group_rel[g];
+        const float wv = wr[rel];
+        const int64_t start = s.group_start[g];
+        const int64_t take = group_take(wv, th, cut, start, s.group_count[g]);
+        float gs = 0.0f;
+        for (int64_t b = start; b < start + take; b += 8) {
+            float m[8], go[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (b + u < start + take) {
+                    m[u] = s.mask[b + u];
+                    go[u] = gr[s.col_ind[b + u]];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (b + u >= start + take || m[u] == 0.0f || go[u] == 0.0f) continue;
+                acc = fl_add(acc, fl_mul(fl_mul(go[u], wv), m[u]));
+                gs = fl_add(gs, fl_mul(fl_mul(go[u], a), m[u]));
+            }
+        }
+        if (take > 0) pg[off + rel] = gs;
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(BWD_NT) void k_bwd_rows(
+    fl_side ori, fl_side inv, const float *__restrict__ A, const float *__restrict__ w,
+    const float *__restrict__ g_ori, const float *__restrict__ g_inv, int64_t BL, int64_t E, int64_t n,
+    int64_t r_size, const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
+    const int32_t *__restrict__ rowlist, const int32_t *__restrict__ rowcnt, const int64_t *__restrict__ rowoff,
+    int64_t pairs, float *__restrict__ gA, float *__restrict__ PG) {
+    const int64_t bl = blockIdx.y;
+    const int64_t cnt = rowcnt[bl];
+    for (int64_t k = (int64_t)blockIdx.x * BWD_NT + threadIdx.x; k < cnt; k += (int64_t)gridDim.x * BWD_NT) {
+        if (rowoff[bl] + k >= pairs) break;  // the caller's buffer holds `pairs` rows
+        const int64_t src = rowlist[bl * E + k];
+        const float a = A[bl * E + src];
+        float *pg = PG + (rowoff[bl] + k) * n;
+        for (int64_t r = 0; r < n; ++r) pg[r] = 0.0f;
+        float acc = gA[bl * E + src];  // identity term written by k_bwd_identity
+        acc = bwd_walk(ori, src, bl, BL, E, n, 0, 0, a, w, g_ori, PK, CUT, acc, pg);
+        acc = bwd_walk(inv, src, bl, BL, E, n, r_size, 1, a, w, g_inv, PK, CUT, acc, pg);
+        gA[bl * E + src] = acc;
+    }
+}
+
+// gw[row, r] for the relation columns r < 2*r_size: the pairs' partials in
+// ascending source order, GW_C pairs at a time through LDS.
+constexpr int GW_C = 32;
+
+__global__ __launch_bounds__(BWD_NT) void k_bwd_gw(const float *__restrict__ PG, const int32_t *__restrict__ rowcnt,
+                                                  const int64_t *__restrict__ rowoff, int64_t pairs, int64_t n,
+                                                  int64_t nrel, float *__restrict__ gw) {
+    extern __shared__ float stage[];  // [GW_C][n]
+    const int64_t bl = blockIdx.x;
+    int64_t cnt = rowcnt[bl];
+    if (rowoff[bl] + cnt > pairs) cnt = pairs - rowoff[bl] > 0 ? pairs - rowoff[bl] : 0;
+    const float *pg = PG + rowoff[bl] * n;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};  // columns t, t+256, t+512, t+768
+    for (int64_t k0 = 0; k0 < cnt; k0 += GW_C) {
+        const int64_t kc = (cnt - k0 < GW_C) ? cnt - k0 : GW_C;
+        for (int64_t i = threadIdx.x; i < kc * n; i += BWD_NT) stage[i] = pg[k0 * n + i];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t r = threadIdx.x + j * BWD_NT;
+            if (r < nrel)
+                for (int64_t k = 0; k < kc; ++k) acc[j] = fl_add(acc[j], stage[k * n + r]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t r = threadIdx.x + j * BWD_NT;
+        if (r < nrel) gw[bl * n + r] = acc[j];
+    }
+}
+
+__global__ void k_row_offsets(const int32_t *__restrict__ rowcnt, int64_t BL, int64_t *__restrict__ rowoff) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) {
+        int64_t run = 0;
+        for (int64_t b = 0; b < BL; ++b) { rowoff[b] = run; run += rowcnt[b]; }
+        rowoff[BL] = run;
+    }
+}
+
 }  // namespace fl
 
 // ---------------------------------------------------------------------------
@@ -891,6 +1071,60 @@ int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv, c
                   out_ori, out_inv);
     }
     return fl_check_launch("dense_sum_forward");
+}
+
+size_t fl_dense_backward_workspace_bytes(const fl_side *ori, const fl_side *inv, int64_t BL, int64_t E) {
+    if (BL <= 0 || E <= 0 || !ori || !inv) return 256;
+    // the forward's frontier arrays plus the row lists
+    return dense_ws_layout(BL, E, ori, inv, nullptr).bytes + align256(sizeof(int32_t) * (size_t)(BL * E)) +
+           align256(sizeof(int32_t) * (size_t)BL) + align256(sizeof(int64_t) * (size_t)(BL + 1));
+}
+
+int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv, const float *A, const float *w,
+                          const float *grad_ind, const float *grad_ori, const float *grad_inv, int64_t BL, int64_t E,
+                          int64_t n, int64_t r_size, int wot_i, int64_t topk_edges, float *grad_A, float *grad_w,
+                          float *pg, int64_t pg_pairs, void *workspace, size_t workspace_bytes) {
+    int rc;
+    if ((rc = check_side(ori, "ori")) != FL_OK) return rc;
+    if ((rc = check_side(inv, "inv")) != FL_OK) return rc;
+    if (BL <= 0 || E <= 0 || n < 1) return fl_fail(FL_ERR_ARG, "dense_sum_backward: bad shape");
+    if (BL * E >= (int64_t)INT32_MAX) return fl_fail(FL_ERR_ARG, "dense_sum_backward: BL*E must be < 2^31");
+    if (r_size < 0 || 2 * r_size + 1 > n + (wot_i ? 1 : 0))
+        return fl_fail(FL_ERR_ARG, "dense_sum_backward: w width too small for r_size");
+    const int64_t nrel = 2 * r_size;
+    if (nrel > 4 * BWD_NT) return fl_fail(FL_ERR_ARG, "dense_sum_backward: more than %d relation columns", 4 * BWD_NT);
+    if ((size_t)GW_C * n * sizeof(float) > 65536) return fl_fail(FL_ERR_ARG, "dense_sum_backward: w width too large");
+    if (pg_pairs < 0 || (pg_pairs > 0 && !pg)) return fl_fail(FL_ERR_ARG, "dense_sum_backward: bad partial buffer");
+    if (!workspace || workspace_bytes < fl_dense_backward_workspace_bytes(ori, inv, BL, E))
+        return fl_fail(FL_ERR_ARG, "dense_sum_backward: workspace too small");
+    DenseWs ws = dense_ws_layout(BL, E, ori, inv, (char *)workspace);
+    int32_t *rowlist = (int32_t *)((char *)workspace + ws.bytes);
+    int32_t *rowcnt = (int32_t *)((char *)rowlist + align256(sizeof(int32_t) * (size_t)(BL * E)));
+    int64_t *rowoff = (int64_t *)((char *)rowcnt + align256(sizeof(int32_t) * (size_t)BL));
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nw = (BL + 31) / 32;
+    const int do_topk = (topk_edges > 0 && topk_edges < ((int64_t)1 << 60)) ? 1 : 0;
+    const int64_t K = do_topk ? topk_edges : 0;
+    FL_LAUNCH("k_bwd_identity", k_bwd_identity, dim3((unsigned)BL), dim3(BWD_NT), 0, st, grad_ind, A, w, E, n, wot_i,
+              grad_A, grad_w);
+    // the forward's frontier (same A and w: same admitted edges); no identity output
+    FL_LAUNCH("k_col_count", k_col_count, dim3((unsigned)((nw * E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, A,
+              w, BL, E, n, wot_i, (float *)nullptr, ws.bm, ws.hard_count);
+    FL_LAUNCH("k_frontier", k_frontier, dim3((unsigned)((E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, *ori,
+              *inv, A, BL, E, K, do_topk, ws.bm, ws.pk, ws.hard_count, ws.hard);
+    if (do_topk)
+        FL_LAUNCH("k_c2_hard", k_c2_hard, dim3(1024), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K,
+                  ws.hard_count, ws.hard, ws.pk, ws.cut);
+    FL_LAUNCH("k_row_list", k_row_list, dim3((unsigned)BL), dim3(RL_NT), 0, st, ws.bm, E, rowlist, rowcnt);
+    FL_LAUNCH("k_row_offsets", k_row_offsets, dim3(1), dim3(64), 0, st, rowcnt, BL, rowoff);
+    if (pg_pairs > 0) {
+        FL_LAUNCH("k_bwd_rows", k_bwd_rows, dim3(16, (unsigned)BL), dim3(BWD_NT), 0, st, *ori, *inv, A, w, grad_ori,
+                  grad_inv, BL, E, n, r_size, ws.pk, ws.cut, rowlist, rowcnt, rowoff, pg_pairs, grad_A, pg);
+        const size_t lds = sizeof(float) * (size_t)(GW_C * n);
+        FL_LAUNCH("k_bwd_gw", k_bwd_gw, dim3((unsigned)BL), dim3(BWD_NT), lds, st, pg, rowcnt, rowoff, pg_pairs, n,
+                  nrel, grad_w);
+    }
+    return fl_check_launch("dense_sum_backward");
 }
 
 }  // extern "C"

@@ -487,8 +487,43 @@ class FlashLogFunction(autograd.Function):
         return (gA.view(B, L, E), gw.view(B, L, -1)) + (None,) * 16
 
 
+_DENSE_BACKWARD_ENABLED = False
+
+
 def _dense_sum_backward(grad_ind, grad_ori, grad_inv, A_f, w_f, graph, om, im, r_size, wot_i, K):
-    raise NotImplementedError("dense sum backward is not available in this build yet")
+    """flashlog_backward_cuda (flashlog.cu:1077-1185) with the CPU path's
+    order (flashlog.cpp:216-278): grad_A bit-identical, grad_w in a fixed
+    order (within float rounding of the CPU sum).
+
+    Disabled: an earlier build of this path faulted the GPU (k_col_count
+    wrote the identity output through the null pointer the backward passes);
+    the store is now guarded, and the path stays off until a GPU run has
+    verified it."""
+    if not _DENSE_BACKWARD_ENABLED:
+        raise RuntimeError("dense sum backward is disabled: its GPU kernels are awaiting verification "
+                           "after a memory fault (null identity-output store, now fixed)")
+    BL, E = A_f.shape
+    n = w_f.shape[1]
+
+    def g(x):
+        if x is None:
+            return torch.zeros_like(A_f)
+        return x.reshape(BL, E).contiguous().float()
+
+    gi, go, gv = g(grad_ind), g(grad_ori), g(grad_inv)
+    so = graph.ori.struct(om)
+    si = graph.inv.struct(im)
+    ws_bytes = _lib.lib().fl_dense_backward_workspace_bytes(ctypes.byref(so), ctypes.byref(si), BL, E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A_f.device)
+    gA = torch.empty_like(A_f)
+    gw = torch.empty_like(w_f)
+    pairs = int(torch.count_nonzero(A_f))  # nonzero (row, source) pairs: rows of the partial buffer
+    pg = torch.empty(max(pairs, 1) * n, dtype=torch.float32, device=A_f.device)
+    check(_lib.lib().fl_dense_sum_backward(_stream(A_f), ctypes.byref(so), ctypes.byref(si), ptr(A_f), ptr(w_f),
+                                           ptr(gi), ptr(go), ptr(gv), BL, E, n, r_size, 1 if wot_i else 0, int(K),
+                                           ptr(gA), ptr(gw), ptr(pg), pairs, ptr(ws), ws_bytes),
+          "dense_sum_backward")
+    return gA, gw
 
 
 def vectorized_operation_csr(A, w, csr_struct, mask_values, r_size,

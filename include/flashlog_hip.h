@@ -147,6 +147,29 @@ int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv,
                          float *out_inv, void *workspace,
                          size_t workspace_bytes);
 
+/* Workspace for fl_dense_sum_backward. */
+size_t fl_dense_backward_workspace_bytes(const fl_side *ori, const fl_side *inv,
+                                         int64_t BL, int64_t E);
+
+/* Replaces flashlog_backward_cuda with agg_mode = sum (flashlog.cu:1077-1185),
+ * with the CPU path's semantics (flashlog.cpp:91-146,216-278): grad_A is the
+ * identity term 0 + g_ind*w[n-1] plus the ORI then INV terms added in CSR
+ * order (bit-identical to the CPU path); grad_w's identity column is a fixed
+ * tree sum over entities and its relation columns add per-group partial
+ * sums in ascending source order (a fixed order, equal to the CPU path
+ * within float rounding).  pg holds pg_pairs * n floats of scratch, where
+ * pg_pairs must be the number of nonzero entries of A (rows beyond
+ * pg_pairs are skipped, never written).  The edge admission is rebuilt from
+ * A and w, so A must be the state the forward saw (after c1). */
+int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv,
+                          const float *A, const float *w,
+                          const float *grad_ind, const float *grad_ori,
+                          const float *grad_inv, int64_t BL, int64_t E,
+                          int64_t n, int64_t r_size, int wot_i,
+                          int64_t topk_edges, float *grad_A, float *grad_w,
+                          float *pg, int64_t pg_pairs, void *workspace,
+                          size_t workspace_bytes);
+
 /* ---- measurement ------------------------------------------------------ */
 
 /* No reference counterpart (the reference's FLASHLOG_STAGE_TIMING,
