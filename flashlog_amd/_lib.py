@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 6
 FL_SEG = 32
 FL_SUP = 16
 
@@ -45,6 +45,8 @@ class FlSide(ctypes.Structure):
         ("heavy_sup_ptr", ctypes.c_void_p),
         ("sup_h", ctypes.c_void_p),
         ("sup_seg0", ctypes.c_void_p),
+        ("pos_src", ctypes.c_void_p),
+        ("pos_rel", ctypes.c_void_p),
     ]
 
 
@@ -75,6 +77,17 @@ _SIGS = {
     "fl_dense_sum_backward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide)] +
                               [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_int64] +
                               [ctypes.c_void_p] * 3 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t]),
+    "fl_dense_max_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
+                                            ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                            ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int64] +
+                             [ctypes.c_void_p] * 6 + [ctypes.c_size_t]),
+    "fl_dense_max_backward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide)] +
+                              [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_int] +
+                              [ctypes.c_void_p] * 2),
+    "fl_filtered_ranks_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int]),
+    "fl_filtered_ranks": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int] + [ctypes.c_void_p] * 2 +
+                          [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                                  ctypes.c_size_t]),
     "fl_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "fl_prof_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_int64)]),

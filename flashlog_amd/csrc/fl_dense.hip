@@ -438,14 +438,12 @@ __global__ __launch_bounds__(C2_NT) void k_c2_hard(fl_side ori, fl_side inv, con
 // the tie cut only on an exact tie; then the in-order accumulation.
 constexpr int WALK_U = 8;
 
-template <bool LIST>
-__device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_t s1, int64_t bl,
-                                            int64_t BL, int64_t E, int64_t n, int64_t off, int dir,
-                                            const float *__restrict__ w, const uint32_t *__restrict__ BM,
-                                            const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
-                                            float *__restrict__ list, int *count) {
-    float acc = 0.0f;
-    int k = 0;
+// Calls emit(position, product) for every kept slot of [s0, s1) in order.
+template <typename Emit>
+__device__ __forceinline__ void walk_kept(const fl_side &s, int64_t s0, int64_t s1, int64_t bl, int64_t BL,
+                                          int64_t E, int64_t n, int64_t off, int dir, const float *__restrict__ w,
+                                          const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
+                                          const int32_t *__restrict__ CUT, Emit &&emit) {
     const uint32_t *bmw = BM + (bl >> 5) * E;
     const uint32_t bit = 1u << (bl & 31);
     const int64_t plane = (int64_t)dir * E * BL + bl;
@@ -477,15 +475,46 @@ __device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_
             const float th = rc[u].y;
             bool kept = wv[u] > th;
             if (!kept && wv[u] == th) kept = pos[u] < CUT[plane + (int64_t)src[u] * BL];
-            if (kept) {
-                const float prod = fl_mul(fl_mul(rc[u].x, wv[u]), m[u]);
-                if (LIST) list[k++] = prod;
-                else acc = fl_add(acc, prod);
-            }
+            if (kept) emit(pos[u], fl_mul(fl_mul(rc[u].x, wv[u]), m[u]));
         }
     }
+}
+
+// Sum: add the kept products in slot order (LIST: append them to `list`).
+template <bool LIST>
+__device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_t s1, int64_t bl,
+                                            int64_t BL, int64_t E, int64_t n, int64_t off, int dir,
+                                            const float *__restrict__ w, const uint32_t *__restrict__ BM,
+                                            const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
+                                            float *__restrict__ list, int *count) {
+    float acc = 0.0f;
+    int k = 0;
+    walk_kept(s, s0, s1, bl, BL, E, n, off, dir, w, BM, PK, CUT, [&](int, float prod) {
+        if (LIST) list[k++] = prod;
+        else acc = fl_add(acc, prod);
+    });
     if (LIST) *count = k;
     return acc;
+}
+
+// Max: the largest packed key (value bits << 32 | ~position) of the kept
+// products, 0 when none (flashlog.cu:104-121): larger value bits win, equal
+// bits go to the smaller position.
+__device__ __forceinline__ uint64_t max_key(float v, int pos) {
+    return ((uint64_t)__float_as_uint(v) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)pos);
+}
+
+__device__ __forceinline__ uint64_t walk_slots_max(const fl_side &s, int64_t s0, int64_t s1, int64_t bl,
+                                                   int64_t BL, int64_t E, int64_t n, int64_t off, int dir,
+                                                   const float *__restrict__ w, const uint32_t *__restrict__ BM,
+                                                   const float2 *__restrict__ PK,
+                                                   const int32_t *__restrict__ CUT) {
+    uint64_t best = 0;
+    walk_kept(s, s0, s1, bl, BL, E, n, off, dir, w, BM, PK, CUT, [&](int pos, float prod) {
+        const uint64_t k = max_key(prod, pos);
+        best = k > best ? k : best;
+    });
+    return best;
 }
 
 constexpr int PULL_NT = 256;
@@ -718,6 +747,141 @@ __global__ __launch_bounds__(FOLD_NT) void k_fold_heavy(
 }
 
 // ---------------------------------------------------------------------------
+// Dense max forward (flashlog.cu:523-637, 997-1072) and backward (:639-726,
+// 1187-1255).  The kept edges are the sum path's (same frontier and c2
+// selection); per (row, destination) the result is the largest packed key
+// over the kept products, which is order-free, so heavy destinations take
+// the maximum of their segments' maxima.
+
+__device__ __forceinline__ void max_unpack(uint64_t best, float *out, int64_t *arg) {
+    *out = __uint_as_float((uint32_t)(best >> 32));
+    *arg = best == 0 ? (int64_t)-1 : (int64_t)(int32_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
+}
+
+// Light tiles: thread per (destination, row), as k_pull's light part.
+__global__ __launch_bounds__(PULL_NT) void k_pull_max(
+    fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n, int64_t r_size, int TD,
+    int64_t ntiles, int64_t nlight, const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
+    const int32_t *__restrict__ CUT, float *__restrict__ out_ori, float *__restrict__ out_inv,
+    int64_t *__restrict__ arg_ori, int64_t *__restrict__ arg_inv) {
+    extern __shared__ uint64_t ktile[];  // [2][BL][TD]
+    const int64_t lb = blockIdx.x;
+    const int64_t per = nlight / 8;
+    const int64_t tid = (lb % 8) * per + lb / 8;
+    if (tid >= ntiles) return;
+    const int64_t d0 = tid * TD;
+    const int64_t ntask = (int64_t)TD * BL;
+    for (int64_t q = threadIdx.x; q < ntask; q += PULL_NT) {
+        const int64_t dl = q / BL, bl = q - dl * BL;
+        const int64_t dst = d0 + dl;
+        uint64_t best[2] = {0, 0};
+        if (dst < E) {
+#pragma unroll
+            for (int dir = 0; dir < 2; ++dir) {
+                const fl_side &s = dir ? inv : ori;
+                const int64_t s0 = s.pull_ptr[dst], s1 = s.pull_ptr[dst + 1];
+                if (s1 - s0 > FL_SEG) continue;  // heavy: written by k_heavy_max
+                best[dir] = walk_slots_max(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT);
+            }
+        }
+        ktile[(0 * BL + bl) * TD + dl] = best[0];
+        ktile[(1 * BL + bl) * TD + dl] = best[1];
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < ntask; i += PULL_NT) {
+        const int64_t bl = i / TD, dl = i - bl * TD;
+        const int64_t dst = d0 + dl;
+        if (dst < E) {
+            max_unpack(ktile[(0 * BL + bl) * TD + dl], &out_ori[bl * E + dst], &arg_ori[bl * E + dst]);
+            max_unpack(ktile[(1 * BL + bl) * TD + dl], &out_inv[bl * E + dst], &arg_inv[bl * E + dst]);
+        }
+    }
+}
+
+// Heavy destinations, step 1: thread per (segment, row), the segment's best key.
+__global__ __launch_bounds__(PULL_NT) void k_seg_max(fl_side ori, fl_side inv, const float *__restrict__ w,
+                                                     int64_t BL, int64_t E, int64_t n, int64_t r_size,
+                                                     const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
+                                                     const int32_t *__restrict__ CUT, uint64_t *__restrict__ sb_ori,
+                                                     uint64_t *__restrict__ sb_inv) {
+    const int64_t q = (int64_t)blockIdx.x * PULL_NT + threadIdx.x;
+    const int64_t nq_ori = ori.nseg * BL;
+    if (q >= nq_ori + inv.nseg * BL) return;
+    const int dir = q >= nq_ori;
+    const int64_t qq = dir ? q - nq_ori : q;
+    const int64_t seg = qq / BL, bl = qq - seg * BL;
+    const fl_side &s = dir ? inv : ori;
+    const int64_t s0 = s.seg_start[seg];
+    const int64_t end = s.pull_ptr[(int64_t)s.seg_dst[seg] + 1];
+    const int64_t s1 = (s0 + FL_SEG < end) ? s0 + FL_SEG : end;
+    (dir ? sb_inv : sb_ori)[qq] = walk_slots_max(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT);
+}
+
+// Heavy destinations, step 2: thread per (heavy destination, row).
+__global__ __launch_bounds__(PULL_NT) void k_heavy_max(fl_side ori, fl_side inv, int64_t BL, int64_t E,
+                                                       const uint64_t *__restrict__ sb_ori,
+                                                       const uint64_t *__restrict__ sb_inv,
+                                                       float *__restrict__ out_ori, float *__restrict__ out_inv,
+                                                       int64_t *__restrict__ arg_ori, int64_t *__restrict__ arg_inv) {
+    const int64_t q = (int64_t)blockIdx.x * PULL_NT + threadIdx.x;
+    const int64_t nq_ori = ori.nheavy * BL;
+    if (q >= nq_ori + inv.nheavy * BL) return;
+    const int dir = q >= nq_ori;
+    const int64_t qq = dir ? q - nq_ori : q;
+    const int64_t h = qq / BL, bl = qq - h * BL;
+    const fl_side &s = dir ? inv : ori;
+    const uint64_t *sb = dir ? sb_inv : sb_ori;
+    uint64_t best = 0;
+    for (int64_t g = s.heavy_seg_ptr[h]; g < s.heavy_seg_ptr[h + 1]; ++g) {
+        const uint64_t k = sb[g * BL + bl];
+        best = k > best ? k : best;
+    }
+    const int64_t at = bl * E + s.heavy_dst[h];
+    max_unpack(best, dir ? &out_inv[at] : &out_ori[at], dir ? &arg_inv[at] : &arg_ori[at]);
+}
+
+// Backward: thread per (row, destination); each side's winning position p
+// sends (go*w)*m to gA[row, src(p)] and (go*a)*m to the row's relation
+// column, as the reference's winner-only backward (flashlog.cu:699-710).
+// Relation columns are first reduced in LDS, then added to gw with one
+// atomic per workgroup and column.  Atomic order makes the last bits of
+// gA/gw run-dependent, as in the reference.
+constexpr int MB_NT = 256;
+
+__global__ __launch_bounds__(MB_NT) void k_max_bwd(fl_side ori, fl_side inv, const float *__restrict__ A,
+                                                   const float *__restrict__ w, const float *__restrict__ g_ori,
+                                                   const float *__restrict__ g_inv,
+                                                   const int64_t *__restrict__ arg_ori,
+                                                   const int64_t *__restrict__ arg_inv, int64_t BL, int64_t E,
+                                                   int64_t n, int64_t r_size, float *__restrict__ gA,
+                                                   float *__restrict__ gw) {
+    extern __shared__ float gwl[];  // [2 * r_size]
+    const int64_t nrel = 2 * r_size;
+    for (int64_t r = threadIdx.x; r < nrel; r += MB_NT) gwl[r] = 0.0f;
+    __syncthreads();
+    const int64_t bl = blockIdx.y;
+    const int64_t dst = (int64_t)blockIdx.x * MB_NT + threadIdx.x;
+    if (dst < E) {
+#pragma unroll
+        for (int dir = 0; dir < 2; ++dir) {
+            const fl_side &s = dir ? inv : ori;
+            const int64_t p = (dir ? arg_inv : arg_ori)[bl * E + dst];
+            if (p < 0 || p >= s.edges) continue;
+            const float go = (dir ? g_inv : g_ori)[bl * E + dst];
+            if (go == 0.0f) continue;
+            const int64_t src = s.pos_src[p];
+            const int64_t col = (dir ? r_size : 0) + s.pos_rel[p];
+            const float m = s.mask[p];
+            atomicAdd(&gA[bl * E + src], fl_mul(fl_mul(go, w[bl * n + col]), m));
+            atomicAdd(&gwl[col], fl_mul(fl_mul(go, A[bl * E + src]), m));
+        }
+    }
+    __syncthreads();
+    for (int64_t r = threadIdx.x; r < nrel; r += MB_NT)
+        if (gwl[r] != 0.0f) atomicAdd(&gw[bl * n + r], gwl[r]);
+}
+
+// ---------------------------------------------------------------------------
 // Dense sum backward (flashlog.cpp:91-146,216-278)
 //
 //   k_bwd_identity  per row: gA = 0 + g_ind * w[n-1] for every entity, and
@@ -736,7 +900,8 @@ constexpr int BWD_NT = 256;
 
 __global__ __launch_bounds__(BWD_NT) void k_bwd_identity(const float *__restrict__ g_ind, const float *__restrict__ A,
                                                         const float *__restrict__ w, int64_t E, int64_t n, int wot_i,
-                                                        float *__restrict__ gA, float *__restrict__ gw) {
+                                                        int add_zero, float *__restrict__ gA,
+                                                        float *__restrict__ gw) {
     __shared__ float part[BWD_NT];
     const int64_t bl = blockIdx.x;
     const int t = threadIdx.x;
@@ -748,7 +913,8 @@ __global__ __launch_bounds__(BWD_NT) void k_bwd_identity(const float *__restrict
             gA[i] = 0.0f;
         } else {
             const float gi = g_ind[i];
-            gA[i] = fl_add(0.0f, fl_mul(gi, wid));
+            const float t0 = fl_mul(gi, wid);
+            gA[i] = add_zero ? fl_add(0.0f, t0) : t0;
             acc = fl_add(acc, fl_mul(gi, A[i]));
         }
     }
@@ -963,7 +1129,7 @@ int check_side(const fl_side *s, const char *name) {
 
 extern "C" {
 
-int fl_abi_version(void) { return 4; }
+int fl_abi_version(void) { return 6; }
 
 int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool, const int32_t *order,
                   const float *weight, float *out, int64_t nnz) {
@@ -1106,7 +1272,7 @@ int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv, 
     const int do_topk = (topk_edges > 0 && topk_edges < ((int64_t)1 << 60)) ? 1 : 0;
     const int64_t K = do_topk ? topk_edges : 0;
     FL_LAUNCH("k_bwd_identity", k_bwd_identity, dim3((unsigned)BL), dim3(BWD_NT), 0, st, grad_ind, A, w, E, n, wot_i,
-              grad_A, grad_w);
+              1, grad_A, grad_w);
     // the forward's frontier (same A and w: same admitted edges); no identity output
     FL_LAUNCH("k_col_count", k_col_count, dim3((unsigned)((nw * E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, A,
               w, BL, E, n, wot_i, (float *)nullptr, ws.bm, ws.hard_count);
@@ -1125,6 +1291,78 @@ int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv, 
                   nrel, grad_w);
     }
     return fl_check_launch("dense_sum_backward");
+}
+
+int fl_dense_max_forward(void *stream, const fl_side *ori, const fl_side *inv, const float *A, const float *w,
+                         int64_t BL, int64_t E, int64_t n, int64_t r_size, int wot_i, int64_t topk_edges,
+                         float *out_ind, float *out_ori, float *out_inv, int64_t *arg_ori, int64_t *arg_inv,
+                         void *workspace, size_t workspace_bytes) {
+    int rc;
+    if ((rc = check_side(ori, "ori")) != FL_OK) return rc;
+    if ((rc = check_side(inv, "inv")) != FL_OK) return rc;
+    if (BL < 0 || E < 0 || n < 1) return fl_fail(FL_ERR_ARG, "dense_max_forward: bad shape");
+    if (BL * E >= (int64_t)INT32_MAX) return fl_fail(FL_ERR_ARG, "dense_max_forward: BL*E must be < 2^31");
+    if (BL > HSCAN_NT) return fl_fail(FL_ERR_ARG, "dense_max_forward: BL=%lld above %d", (long long)BL, HSCAN_NT);
+    if (r_size < 0 || 2 * r_size + 1 > n + (wot_i ? 1 : 0))
+        return fl_fail(FL_ERR_ARG, "dense_max_forward: w width %lld too small for r_size %lld", (long long)n,
+                       (long long)r_size);
+    if (BL == 0 || E == 0) return FL_OK;
+    DenseWs ws = dense_ws_layout(BL, E, ori, inv, (char *)workspace);
+    if (!workspace || workspace_bytes < ws.bytes)
+        return fl_fail(FL_ERR_ARG, "dense_max_forward: workspace of %zu bytes, need %zu", workspace_bytes, ws.bytes);
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nw = (BL + 31) / 32;
+    const int do_topk = (topk_edges > 0 && topk_edges < ((int64_t)1 << 60)) ? 1 : 0;
+    const int64_t K = do_topk ? topk_edges : 0;
+    FL_LAUNCH("k_col_count", k_col_count, dim3((unsigned)((nw * E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, A,
+              w, BL, E, n, wot_i, out_ind, ws.bm, ws.hard_count);
+    FL_LAUNCH("k_frontier", k_frontier, dim3((unsigned)((E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, *ori,
+              *inv, A, BL, E, K, do_topk, ws.bm, ws.pk, ws.hard_count, ws.hard);
+    if (do_topk)
+        FL_LAUNCH("k_c2_hard", k_c2_hard, dim3(1024), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K,
+                  ws.hard_count, ws.hard, ws.pk, ws.cut);
+    int TD = (int)(512 / BL);
+    if (TD < 1) TD = 1;
+    if (TD > 64) TD = 64;
+    const int64_t ntiles = (E + TD - 1) / TD;
+    const int64_t nlight = ((ntiles + 7) / 8) * 8;
+    const size_t lds = sizeof(uint64_t) * 2 * (size_t)BL * (size_t)TD;
+    FL_LAUNCH("k_pull_max", k_pull_max, dim3((unsigned)nlight), dim3(PULL_NT), lds, st, *ori, *inv, w, BL, E, n,
+              r_size, TD, ntiles, nlight, ws.bm, ws.pk, ws.cut, out_ori, out_inv, arg_ori, arg_inv);
+    // segment maxima reuse the heavy-list area (nseg*BL*FL_SEG floats >= nseg*BL keys)
+    uint64_t *sb_ori = (uint64_t *)ws.list_ori, *sb_inv = (uint64_t *)ws.list_inv;
+    const int64_t nq_seg = (ori->nseg + inv->nseg) * BL;
+    if (nq_seg > 0) {
+        FL_LAUNCH("k_seg_max", k_seg_max, dim3((unsigned)((nq_seg + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0, st,
+                  *ori, *inv, w, BL, E, n, r_size, ws.bm, ws.pk, ws.cut, sb_ori, sb_inv);
+        const int64_t nq_h = (ori->nheavy + inv->nheavy) * BL;
+        FL_LAUNCH("k_heavy_max", k_heavy_max, dim3((unsigned)((nq_h + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0,
+                  st, *ori, *inv, BL, E, sb_ori, sb_inv, out_ori, out_inv, arg_ori, arg_inv);
+    }
+    return fl_check_launch("dense_max_forward");
+}
+
+int fl_dense_max_backward(void *stream, const fl_side *ori, const fl_side *inv, const float *A, const float *w,
+                          const float *grad_ind, const float *grad_ori, const float *grad_inv,
+                          const int64_t *arg_ori, const int64_t *arg_inv, int64_t BL, int64_t E, int64_t n,
+                          int64_t r_size, int wot_i, float *grad_A, float *grad_w) {
+    if (!ori || !inv) return fl_fail(FL_ERR_ARG, "dense_max_backward: null side");
+    if (BL < 0 || E < 0 || n < 1) return fl_fail(FL_ERR_ARG, "dense_max_backward: bad shape");
+    if (r_size < 0 || 2 * r_size + 1 > n + (wot_i ? 1 : 0))
+        return fl_fail(FL_ERR_ARG, "dense_max_backward: w width too small for r_size");
+    if ((size_t)(2 * r_size) * sizeof(float) > 65536)
+        return fl_fail(FL_ERR_ARG, "dense_max_backward: more than 16384 relation columns");
+    for (const fl_side *s : {ori, inv})
+        if (s->edges > 0 && (!s->pos_src || !s->pos_rel || !s->mask))
+            return fl_fail(FL_ERR_ARG, "dense_max_backward: side without position arrays");
+    if (BL == 0 || E == 0) return FL_OK;
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_bwd_identity", k_bwd_identity, dim3((unsigned)BL), dim3(BWD_NT), 0, st, grad_ind, A, w, E, n, wot_i,
+              0, grad_A, grad_w);
+    const size_t lds = sizeof(float) * (size_t)(2 * r_size > 0 ? 2 * r_size : 1);
+    FL_LAUNCH("k_max_bwd", k_max_bwd, dim3((unsigned)((E + MB_NT - 1) / MB_NT), (unsigned)BL), dim3(MB_NT), lds, st,
+              *ori, *inv, A, w, grad_ori, grad_inv, arg_ori, arg_inv, BL, E, n, r_size, grad_A, grad_w);
+    return fl_check_launch("dense_max_backward");
 }
 
 }  // extern "C"

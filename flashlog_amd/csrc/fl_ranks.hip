@@ -1,0 +1,179 @@
+// Filtered tie-aware entity ranks over a sparse [B, E] score matrix
+// (flashlog.cu:2754-2910, wrapper flashlog_kernel.py:168-179).
+//
+// For query b with target t_b and truth score s = score(b, t_b) (0 when the
+// target has no explicit entry):
+//   greater  = unfiltered explicit entries scoring above s
+//   equal    = unfiltered explicit entries scoring exactly s
+//   explicit = unfiltered explicit entries
+//   filtered = filter keys of row b (keys are b*E + e, sorted ascending)
+//   use_eql:  eq = equal + (s == 0 ? E - filtered - explicit : 0) + 1
+//             rank = greater + (eq + 1) * 0.5
+//   else:     rank = greater + 1
+// Counts are kept as u32 and converted once (exact, as the reference's fp32
+// counters are, for counts below 2^24).  The per-row filter count is two
+// binary searches over the sorted keys instead of one atomic per key.
+// Entries whose query index lies outside [0, B) are ignored.
+#include "fl_common.h"
+#include "fl_abi.h"
+
+namespace fl {
+
+constexpr int RK_NT = 256;
+
+__device__ __forceinline__ int64_t rk_lower_bound(const int64_t *__restrict__ keys, int64_t n, int64_t key) {
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = lo + ((hi - lo) >> 1);
+        if (keys[mid] < key) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Per query: zero the truth score and counters; the filter count of the row.
+template <typename T>
+__global__ __launch_bounds__(RK_NT) void k_rank_init(const int64_t *__restrict__ filter_keys, int64_t n_filter,
+                                                     int64_t B, int64_t E, T *__restrict__ truth,
+                                                     uint32_t *__restrict__ cnt, uint32_t *__restrict__ fcount) {
+    const int64_t b = (int64_t)blockIdx.x * RK_NT + threadIdx.x;
+    if (b >= B) return;
+    truth[b] = (T)0;
+    cnt[b] = 0;
+    cnt[B + b] = 0;
+    cnt[2 * B + b] = 0;
+    const int64_t lo = rk_lower_bound(filter_keys, n_filter, b * E);
+    const int64_t hi = rk_lower_bound(filter_keys, n_filter, (b + 1) * E);
+    fcount[b] = (uint32_t)(hi - lo);
+}
+
+template <typename T>
+__global__ __launch_bounds__(RK_NT) void k_rank_truth(const int64_t *__restrict__ idx_b,
+                                                      const int64_t *__restrict__ idx_e, const T *__restrict__ values,
+                                                      const int64_t *__restrict__ targets, int64_t nnz, int64_t B,
+                                                      T *__restrict__ truth) {
+    const int64_t i = (int64_t)blockIdx.x * RK_NT + threadIdx.x;
+    if (i >= nnz) return;
+    const int64_t b = idx_b[i];
+    if (b < 0 || b >= B) return;
+    if (idx_e[i] == targets[b]) truth[b] = values[i];
+}
+
+// Per entry: skip filtered keys, then count explicit / greater / equal.
+// COO rows are usually contiguous, so a wave whose live lanes share one
+// query reduces its three counts and adds them with one atomic each.
+template <typename T>
+__global__ __launch_bounds__(RK_NT) void k_rank_count(const int64_t *__restrict__ idx_b,
+                                                      const int64_t *__restrict__ idx_e, const T *__restrict__ values,
+                                                      const T *__restrict__ truth,
+                                                      const int64_t *__restrict__ filter_keys, int64_t n_filter,
+                                                      int64_t nnz, int64_t B, int64_t E, uint32_t *__restrict__ cnt) {
+    const int64_t i = (int64_t)blockIdx.x * RK_NT + threadIdx.x;
+    int64_t b = -1;
+    int gt = 0, eq = 0, ex = 0;
+    if (i < nnz) {
+        b = idx_b[i];
+        if (b >= 0 && b < B) {
+            const int64_t key = b * E + idx_e[i];
+            const int64_t pos = rk_lower_bound(filter_keys, n_filter, key);
+            if (!(pos < n_filter && filter_keys[pos] == key)) {
+                const T v = values[i];
+                const T t = truth[b];
+                ex = 1;
+                if (v > t) gt = 1;
+                else if (v == t) eq = 1;
+            }
+        } else {
+            b = -1;
+        }
+    }
+    const int live = ex;
+    const unsigned long long lanes = __ballot(live);
+    if (!lanes) return;
+    const int first = __ffsll((long long)lanes) - 1;
+    const int64_t b0 = __shfl(b, first, FL_WAVE);
+    const bool uniform = __ballot(live && b != b0) == 0ull;
+    if (uniform) {
+        const int sg = fl_wave_sum_i32(gt), se = fl_wave_sum_i32(eq), sx = fl_wave_sum_i32(ex);
+        if (fl_lane() == first) {
+            if (sx) atomicAdd(&cnt[2 * B + b0], (uint32_t)sx);
+            if (sg) atomicAdd(&cnt[b0], (uint32_t)sg);
+            if (se) atomicAdd(&cnt[B + b0], (uint32_t)se);
+        }
+    } else if (live) {
+        atomicAdd(&cnt[2 * B + b], 1u);
+        if (gt) atomicAdd(&cnt[b], 1u);
+        if (eq) atomicAdd(&cnt[B + b], 1u);
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(RK_NT) void k_rank_final(const T *__restrict__ truth, const uint32_t *__restrict__ cnt,
+                                                      const uint32_t *__restrict__ fcount, int64_t B, int64_t E,
+                                                      int use_eql, float *__restrict__ ranks) {
+    const int64_t b = (int64_t)blockIdx.x * RK_NT + threadIdx.x;
+    if (b >= B) return;
+    const float greater = (float)cnt[b];
+    if (use_eql) {
+        const float equal = (float)cnt[B + b];
+        const float explicit_unf = (float)cnt[2 * B + b];
+        const float missing = __fsub_rn(__fsub_rn((float)E, (float)fcount[b]), explicit_unf);
+        float eq = fl_add(equal, truth[b] == (T)0 ? missing : 0.0f);
+        eq = fl_add(eq, 1.0f);
+        ranks[b] = fl_add(greater, fl_mul(fl_add(eq, 1.0f), 0.5f));
+    } else {
+        ranks[b] = fl_add(greater, 1.0f);
+    }
+}
+
+template <typename T>
+int launch_ranks(hipStream_t st, const int64_t *idx_b, const int64_t *idx_e, const T *values,
+                 const int64_t *targets, const int64_t *filter_keys, int64_t nnz, int64_t n_filter, int64_t B,
+                 int64_t E, int use_eql, float *ranks, char *ws) {
+    T *truth = (T *)ws;
+    uint32_t *cnt = (uint32_t *)(ws + ((sizeof(T) * (size_t)B + 255) & ~(size_t)255));
+    uint32_t *fcount = cnt + 3 * B;
+    const unsigned gb = (unsigned)((B + RK_NT - 1) / RK_NT);
+    FL_LAUNCH("k_rank_init", k_rank_init<T>, dim3(gb), dim3(RK_NT), 0, st, filter_keys, n_filter, B, E, truth, cnt,
+              fcount);
+    if (nnz > 0) {
+        const unsigned gn = (unsigned)((nnz + RK_NT - 1) / RK_NT);
+        FL_LAUNCH("k_rank_truth", k_rank_truth<T>, dim3(gn), dim3(RK_NT), 0, st, idx_b, idx_e, values, targets, nnz,
+                  B, truth);
+        FL_LAUNCH("k_rank_count", k_rank_count<T>, dim3(gn), dim3(RK_NT), 0, st, idx_b, idx_e, values, truth,
+                  filter_keys, n_filter, nnz, B, E, cnt);
+    }
+    FL_LAUNCH("k_rank_final", k_rank_final<T>, dim3(gb), dim3(RK_NT), 0, st, truth, cnt, fcount, B, E, use_eql,
+              ranks);
+    return fl_check_launch("filtered_ranks");
+}
+
+}  // namespace fl
+
+extern "C" {
+
+size_t fl_filtered_ranks_workspace_bytes(int64_t B, int values_f64) {
+    if (B <= 0) return 256;
+    const size_t tb = (values_f64 ? 8 : 4) * (size_t)B;
+    return ((tb + 255) & ~(size_t)255) + ((sizeof(uint32_t) * 4 * (size_t)B + 255) & ~(size_t)255);
+}
+
+int fl_filtered_ranks(void *stream, const int64_t *idx_b, const int64_t *idx_e, const void *values, int values_f64,
+                      const int64_t *targets, const int64_t *filter_keys, int64_t nnz, int64_t n_filter, int64_t B,
+                      int64_t E, int use_eql, float *ranks, void *workspace, size_t workspace_bytes) {
+    if (nnz < 0 || n_filter < 0 || B < 0 || E < 0) return fl::fl_fail(FL_ERR_ARG, "filtered_ranks: negative size");
+    if (B == 0) return FL_OK;
+    if (B > INT64_MAX / (E + 1)) return fl::fl_fail(FL_ERR_ARG, "filtered_ranks: B*E overflows int64");
+    if (!ranks || !targets || (nnz > 0 && (!idx_b || !idx_e || !values)) || (n_filter > 0 && !filter_keys))
+        return fl::fl_fail(FL_ERR_ARG, "filtered_ranks: null pointer");
+    if (!workspace || workspace_bytes < fl_filtered_ranks_workspace_bytes(B, values_f64))
+        return fl::fl_fail(FL_ERR_ARG, "filtered_ranks: workspace too small");
+    hipStream_t st = (hipStream_t)stream;
+    if (values_f64)
+        return fl::launch_ranks<double>(st, idx_b, idx_e, (const double *)values, targets, filter_keys, nnz,
+                                        n_filter, B, E, use_eql, ranks, (char *)workspace);
+    return fl::launch_ranks<float>(st, idx_b, idx_e, (const float *)values, targets, filter_keys, nnz, n_filter, B,
+                                   E, use_eql, ranks, (char *)workspace);
+}
+
+}  // extern "C"

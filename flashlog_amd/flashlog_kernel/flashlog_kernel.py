@@ -235,6 +235,13 @@ class _PullSide:
         self.pull_pos = pull_pos.to(device)
         self.pull_src = pull_src.to(device)
         self.pull_rel = pull_rel.to(device)
+        pos_src = torch.empty(m, dtype=torch.int32)
+        pos_rel = torch.empty(m, dtype=torch.int16)
+        pidx = pull_pos.long()
+        pos_src[pidx] = pull_src
+        pos_rel[pidx] = pull_rel
+        self.pos_src = pos_src.to(device)
+        self.pos_rel = pos_rel.to(device)
 
     def struct(self, mask):
         return FlSide(self.edges, self.groups, self.col_ind.data_ptr(), mask.data_ptr() if mask.numel() else 0,
@@ -246,7 +253,7 @@ class _PullSide:
                       self.pull_rel.data_ptr() if self.edges else 0,
                       self.nseg, self.nheavy, self.nsup, *[t.data_ptr() if t.numel() else 0 for t in (
                           self.seg_dst, self.seg_start, self.seg_h, self.heavy_dst, self.heavy_seg_ptr,
-                          self.heavy_sup_ptr, self.sup_h, self.sup_seg0)])
+                          self.heavy_sup_ptr, self.sup_h, self.sup_seg0, self.pos_src, self.pos_rel)])
 
 
 class _Graph:
@@ -420,10 +427,8 @@ def get_module():
     return _module
 
 
-def _dense_sum_forward(A_flat, w_flat, graph, ori_mask, inv_mask, r_size, wot_i, K):
+def _dense_check(A_flat, w_flat, graph, ori_mask, inv_mask, r_size):
     _require_cuda(A_flat, w_flat, ori_mask, inv_mask)
-    A_flat = A_flat.contiguous()
-    w_flat = w_flat.contiguous()
     if A_flat.dtype != torch.float32 or w_flat.dtype != torch.float32:
         raise TypeError("flashlog_amd dense propagation computes in float32")
     BL, E = A_flat.shape
@@ -436,6 +441,13 @@ def _dense_sum_forward(A_flat, w_flat, graph, ori_mask, inv_mask, r_size, wot_i,
         raise ValueError("mask length must equal the number of CSR positions")
     if max(graph.ori.max_rel, graph.inv.max_rel) >= r_size or 2 * r_size > n:
         raise ValueError("relation ids must be < r_size and w must hold 2*r_size (+1) columns")
+    return BL, E, n
+
+
+def _dense_sum_forward(A_flat, w_flat, graph, ori_mask, inv_mask, r_size, wot_i, K):
+    A_flat = A_flat.contiguous()
+    w_flat = w_flat.contiguous()
+    BL, E, n = _dense_check(A_flat, w_flat, graph, ori_mask, inv_mask, r_size)
     out_ind = torch.empty_like(A_flat)
     out_ori = torch.empty_like(A_flat)
     out_inv = torch.empty_like(A_flat)
@@ -448,6 +460,51 @@ def _dense_sum_forward(A_flat, w_flat, graph, ori_mask, inv_mask, r_size, wot_i,
                                           ptr(out_ind), ptr(out_ori), ptr(out_inv), ptr(ws), ws_bytes),
           "dense_sum_forward")
     return out_ind, out_ori, out_inv
+
+
+def _dense_max_forward(A_flat, w_flat, graph, ori_mask, inv_mask, r_size, wot_i, K):
+    """flashlog_forward_max_cuda (flashlog.cu:997-1072): values and int64
+    winning CSR positions (-1 where nothing arrives)."""
+    A_flat = A_flat.contiguous()
+    w_flat = w_flat.contiguous()
+    BL, E, n = _dense_check(A_flat, w_flat, graph, ori_mask, inv_mask, r_size)
+    out_ind = torch.empty_like(A_flat)
+    out_ori = torch.empty_like(A_flat)
+    out_inv = torch.empty_like(A_flat)
+    arg_ori = torch.empty((BL, E), dtype=torch.int64, device=A_flat.device)
+    arg_inv = torch.empty((BL, E), dtype=torch.int64, device=A_flat.device)
+    so = graph.ori.struct(ori_mask)
+    si = graph.inv.struct(inv_mask)
+    ws_bytes = _lib.lib().fl_dense_workspace_bytes(ctypes.byref(so), ctypes.byref(si), BL, E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A_flat.device)
+    check(_lib.lib().fl_dense_max_forward(_stream(A_flat), ctypes.byref(so), ctypes.byref(si), ptr(A_flat),
+                                          ptr(w_flat), BL, E, n, r_size, 1 if wot_i else 0, int(K),
+                                          ptr(out_ind), ptr(out_ori), ptr(out_inv), ptr(arg_ori), ptr(arg_inv),
+                                          ptr(ws), ws_bytes),
+          "dense_max_forward")
+    return out_ind, out_ori, out_inv, arg_ori, arg_inv
+
+
+def _dense_max_backward(grad_ind, grad_ori, grad_inv, arg_ori, arg_inv, A_f, w_f, graph, om, im, r_size, wot_i):
+    """flashlog_backward_max_cuda (flashlog.cu:1187-1255)."""
+    BL, E = A_f.shape
+    n = w_f.shape[1]
+
+    def g(x):
+        if x is None:
+            return torch.zeros_like(A_f)
+        return x.reshape(BL, E).contiguous().float()
+
+    gi, go, gv = g(grad_ind), g(grad_ori), g(grad_inv)
+    so = graph.ori.struct(om)
+    si = graph.inv.struct(im)
+    gA = torch.empty_like(A_f)
+    gw = torch.empty_like(w_f)
+    check(_lib.lib().fl_dense_max_backward(_stream(A_f), ctypes.byref(so), ctypes.byref(si), ptr(A_f), ptr(w_f),
+                                           ptr(gi), ptr(go), ptr(gv), ptr(arg_ori), ptr(arg_inv), BL, E, n,
+                                           r_size, 1 if wot_i else 0, ptr(gA), ptr(gw)),
+          "dense_max_backward")
+    return gA, gw
 
 
 # ---------------------------------------------------------------------------
@@ -631,7 +688,28 @@ def _not_yet(name):
 
 
 def sparse2d_filtered_ranks_cuda(idx_b, idx_e, values, targets, filter_keys, B, E, use_eql=False):
-    _not_yet("sparse2d_filtered_ranks_cuda")
+    """Filtered tie-aware ranks of each query's target over a COO [B, E] score
+    matrix (flashlog_kernel.py:168-179 -> flashlog.cu:2839-2910).  Returns
+    float32 ranks [B].  filter_keys (b*E + e) must be sorted ascending."""
+    tensors = (idx_b, idx_e, values, targets, filter_keys)
+    _require_cuda(*tensors)
+    if values.dtype not in (torch.float32, torch.float64):
+        raise RuntimeError("sparse2d_filtered_ranks_cuda: values must be float32 or float64")
+    idx_b = idx_b.long().contiguous()
+    idx_e = idx_e.long().contiguous()
+    values = values.contiguous()
+    targets = targets.long().contiguous()
+    filter_keys = filter_keys.long().contiguous()
+    B, E = int(B), int(E)
+    f64 = 1 if values.dtype == torch.float64 else 0
+    ranks = torch.empty(B, dtype=torch.float32, device=values.device)
+    ws_bytes = _lib.lib().fl_filtered_ranks_workspace_bytes(B, f64)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=values.device)
+    check(_lib.lib().fl_filtered_ranks(_stream(values), ptr(idx_b), ptr(idx_e), ptr(values), f64, ptr(targets),
+                                       ptr(filter_keys), values.shape[0], filter_keys.shape[0], B, E,
+                                       1 if use_eql else 0, ptr(ranks), ptr(ws), ws_bytes),
+          "sparse2d_filtered_ranks_cuda")
+    return ranks
 
 
 def vectorized_operation_sparse3d_fixed_relation(sp_state, operators, csr_struct, r_size):
@@ -642,9 +720,71 @@ def normalize_sparse3d(s, eps=1e-7):
     _not_yet("normalize_sparse3d")
 
 
+class FlashLogDenseMaxFunction(autograd.Function):
+    """GPU dense max hop (flashlog_kernel.py:992-1089): per destination the
+    largest kept (a*w)*m, ties to the smaller CSR position; the backward
+    routes the gradient to the winning edge only."""
+
+    @staticmethod
+    def forward(ctx, A, w, ori_row_ptr, ori_col_ind, ori_r_ind, ori_order,
+                inv_row_ptr, inv_col_ind, inv_r_ind, inv_order,
+                ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                mask_values, weight, r_size, wot_i,
+                use_topk, topk_nodes, topk_edges):
+        _require_cuda(A, w)
+        B, L, E = A.shape
+        BL = B * L
+        A_flat = A.reshape(BL, E).contiguous().float()
+        w_flat = w.reshape(BL, -1).contiguous().float()
+        prepared = _prepared_mask_pair(mask_values)
+        if prepared is not None:
+            ori_mask, inv_mask = prepared
+        else:
+            mask_f = (mask_values if mask_values.dtype == torch.bool else mask_values.float()).contiguous()
+            w_tensor = weight.to(device=A.device, dtype=torch.float).squeeze(-1) if weight is not None \
+                else torch.empty(0, device=A.device)
+            ori_mask = _HipModule.apply_mask_cuda(mask_f, ori_order, w_tensor)
+            inv_mask = _HipModule.apply_mask_cuda(mask_f, inv_order, w_tensor)
+        graph = _graph_for(ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                           ori_group_edge_count, inv_col_ind, inv_row_group_ptr, inv_group_rel,
+                           inv_group_edge_start, inv_group_edge_count)
+        K = int(topk_edges) if (use_topk and 0 < int(topk_edges) < (1 << 60)) else 0
+        out_ind, out_ori, out_inv, arg_ori, arg_inv = _dense_max_forward(
+            A_flat, w_flat, graph, ori_mask, inv_mask, int(r_size), bool(wot_i), K)
+        ctx.save_for_backward(A_flat, w_flat, ori_mask, inv_mask, arg_ori, arg_inv)
+        ctx.graph, ctx.r_size, ctx.wot_i, ctx.shape = graph, int(r_size), bool(wot_i), (B, L, E)
+        return out_ind.view(B, L, E), out_ori.view(B, L, E), out_inv.view(B, L, E)
+
+    @staticmethod
+    def backward(ctx, grad_ind, grad_ori, grad_inv):
+        A_f, w_f, om, im, arg_ori, arg_inv = ctx.saved_tensors
+        gA, gw = _dense_max_backward(grad_ind, grad_ori, grad_inv, arg_ori, arg_inv, A_f, w_f, ctx.graph, om, im,
+                                     ctx.r_size, ctx.wot_i)
+        B, L, E = ctx.shape
+        return (gA.view(B, L, E), gw.view(B, L, -1)) + (None,) * 23
+
+
 def dense_csr_max(A, w, csr_struct, mask_values, r_size, weight=None, wot_i=False,
                   use_topk=False, topk_nodes=100000, topk_edges=0, prepared_masks=None):
-    _not_yet("dense_csr_max")
+    """GPU dense max entry point (flashlog_kernel.py:1666-1688): c1 pruning,
+    then the max hop with c2 = topk_edges when use_topk."""
+    (ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
+     inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
+     ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+     inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count) = csr_struct
+    A = _dense_topc_state(A, topk_nodes if use_topk else None)
+    mask_input = prepared_masks if prepared_masks is not None else mask_values
+    weight_input = None if prepared_masks is not None else weight
+    return FlashLogDenseMaxFunction.apply(
+        A, w,
+        ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
+        inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
+        ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+        inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+        mask_input, weight_input,
+        r_size, wot_i,
+        use_topk, topk_nodes, topk_edges)
 
 
 def vectorized_operation_sparse3d_csr_sum(sp_state, w, csr_struct, mask_values, r_size, weight=None,

@@ -66,6 +66,8 @@ typedef struct fl_side {
     const int32_t *heavy_sup_ptr;  /* [nheavy+1] supersegments of each     */
     const int32_t *sup_h;          /* [nsup] heavy index of each           */
     const int32_t *sup_seg0;       /* [nsup] first segment of each         */
+    const int32_t *pos_src;        /* [M] source entity of each position   */
+    const int16_t *pos_rel;        /* [M] relation of each position        */
 } fl_side;
 
 const char *fl_last_error(void);
@@ -169,6 +171,57 @@ int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv,
                           int64_t topk_edges, float *grad_A, float *grad_w,
                           float *pg, int64_t pg_pairs, void *workspace,
                           size_t workspace_bytes);
+
+/* Replaces flashlog_forward_max_cuda (flashlog.cu:997-1072; kernels
+ * :523-637, packing :104-135), called by FlashLogDenseMaxFunction
+ * (flashlog_kernel.py:992-1055).  Same kept edges as fl_dense_sum_forward;
+ * out_ori[bl, d] is the product (A*w)*mask of the winning kept ORI position
+ * p, where the winner maximizes the 64-bit key (float bits of the product
+ * << 32 | 0xFFFFFFFF - p): larger value bits win, ties go to the smaller
+ * position.  arg_ori[bl, d] = p, or -1 (and 0.0) when no kept edge enters d.
+ * INV likewise.  out_ind = A * w[:, n-1] (0 if wot_i).  Uses the workspace
+ * size of fl_dense_workspace_bytes. */
+int fl_dense_max_forward(void *stream, const fl_side *ori, const fl_side *inv,
+                         const float *A, const float *w, int64_t BL, int64_t E,
+                         int64_t n, int64_t r_size, int wot_i,
+                         int64_t topk_edges, float *out_ind, float *out_ori,
+                         float *out_inv, int64_t *arg_ori, int64_t *arg_inv,
+                         void *workspace, size_t workspace_bytes);
+
+/* Replaces flashlog_backward_max_cuda (flashlog.cu:1187-1255; kernel
+ * :639-726): grad_A = g_ind * w[n-1] (0 if wot_i) plus, for every winning
+ * position p of (bl, d) with grad != 0, (grad*w[rel(p)])*mask[p] at
+ * src(p); grad_w[bl, n-1] = sum_e g_ind*A (fixed tree order) and
+ * grad_w[bl, off + rel(p)] += (grad*A[bl, src(p)])*mask[p].  The winner
+ * terms are added with atomics (run-dependent last bits, as the
+ * reference).  Needs the sides' pos_src / pos_rel arrays; no workspace. */
+int fl_dense_max_backward(void *stream, const fl_side *ori, const fl_side *inv,
+                          const float *A, const float *w,
+                          const float *grad_ind, const float *grad_ori,
+                          const float *grad_inv, const int64_t *arg_ori,
+                          const int64_t *arg_inv, int64_t BL, int64_t E,
+                          int64_t n, int64_t r_size, int wot_i, float *grad_A,
+                          float *grad_w);
+
+/* ---- evaluation --------------------------------------------------------- */
+
+/* Workspace for fl_filtered_ranks (values_f64: 1 for double scores). */
+size_t fl_filtered_ranks_workspace_bytes(int64_t B, int values_f64);
+
+/* Replaces sparse2d_filtered_ranks_cuda (flashlog.cu:2754-2910; wrapper
+ * flashlog_kernel.py:168-179).  Scores are a COO [B, E] matrix (idx_b,
+ * idx_e, values of float or double); filter_keys are b*E + e, sorted
+ * ascending.  truth[b] = the score of (b, targets[b]) or 0; over unfiltered
+ * explicit entries: greater / equal / explicit counts; ranks[b] =
+ * greater + (eq + 1) * 0.5 with eq = equal + (truth == 0 ? E - filtered -
+ * explicit : 0) + 1 when use_eql, else greater + 1 (fp32, exact for counts
+ * below 2^24).  Entries with idx_b outside [0, B) are ignored. */
+int fl_filtered_ranks(void *stream, const int64_t *idx_b, const int64_t *idx_e,
+                      const void *values, int values_f64,
+                      const int64_t *targets, const int64_t *filter_keys,
+                      int64_t nnz, int64_t n_filter, int64_t B, int64_t E,
+                      int use_eql, float *ranks, void *workspace,
+                      size_t workspace_bytes);
 
 /* ---- measurement ------------------------------------------------------ */
 

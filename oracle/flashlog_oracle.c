@@ -15,6 +15,7 @@
  *   or_dense_backward        flashlog_kernel/source/flashlog.cpp:91-146,216-278
  *   or_dense_topc            flashlog_kernel/flashlog_kernel.py:814-842
  *   or_dense_max_forward     flashlog_kernel/source/flashlog.cu:104-121,523-637
+ *   or_dense_max_backward    flashlog_kernel/source/flashlog.cu:639-726,1187-1255
  *   or_filtered_ranks        flashlog_kernel/source/flashlog.cu:2754-2910
  *
  * Pinning (how each function is checked, see tests/test_oracle_*.py):
@@ -24,6 +25,8 @@
  *   or_group_threshold: brute force (expand groups to edges, sort) on tiny inputs.
  *   or_dense_topc: brute-force stable sort (value desc, entity asc) per row.
  *   or_dense_max_forward: brute-force max over edges with explicit tie rule.
+ *   or_dense_max_backward: float64 brute force over the expanded edge list
+ *     (each winner edge's partial derivatives), and finite differences.
  *   or_filtered_ranks: brute-force count over a dense score row.
  *
  * Compile with -O2 -ffp-contract=off (no FMA contraction: the reference's
@@ -420,6 +423,75 @@ void or_dense_max_forward(int64_t BL, int64_t E, int64_t n, const float *A, cons
     free(po); free(pi);
 }
 
+/* Winner-only max backward: flashlog.cu:639-726 (kernel) and 1187-1255
+ * (host), in a sequential order: identity gA = g_ind * w[n-1] and gw[n-1] =
+ * sum over entities (ascending) of g_ind * A, then for active sources
+ * (ascending), rows, ORI then INV kept edges in CSR order: an edge p whose
+ * destination's arg is p adds (go*w)*m to gA[bl, src] and (go*a)*m to
+ * gw[bl, off + rel].  (The reference adds the winner terms with atomics.)  */
+static void or_max_bwd_row(int64_t src, int64_t bl, float a_val, const float *w,
+    const int32_t *gptr, const int16_t *grel, const int32_t *gstart, const int32_t *gcount,
+    const int32_t *col, const float *mask, const float *grad, const int64_t *arg,
+    float *gA, float *gw, int64_t topk_edges, int64_t E, int64_t n, int64_t off)
+{
+    int64_t g0 = gptr[src], g1 = gptr[src + 1];
+    int64_t keep_in_threshold = 0;
+    float threshold_weight = or_group_threshold_f32(w + bl * n + off, grel, gcount, g0, g1,
+                                                    topk_edges, &keep_in_threshold);
+    int64_t threshold_seen = 0;
+    for (int64_t g = g0; g < g1; ++g) {
+        int32_t *group_edge_count = (int32_t *)gcount;
+        float w_val = w[bl * n + off + grel[g]];
+        OR_TAKE(float)
+        if (take <= 0) continue;
+        for (int64_t p = gstart[g]; p < gstart[g] + take; ++p) {
+            float m = mask[p];
+            if (m == 0) continue;
+            int64_t dst = col[p];
+            if (arg[bl * E + dst] != p) continue;
+            float go = grad[bl * E + dst];
+            if (go == 0) continue;
+            gA[bl * E + src] += (go * w_val) * m;
+            gw[bl * n + off + grel[g]] += (go * a_val) * m;
+        }
+    }
+}
+
+void or_dense_max_backward(int64_t BL, int64_t E, int64_t n, const float *A, const float *w,
+    const float *grad_ind, const float *grad_ori, const float *grad_inv,
+    const int64_t *ori_arg, const int64_t *inv_arg,
+    const int64_t *active, int64_t num_active,
+    const int32_t *ori_col, const float *ori_mask, const int32_t *ori_gptr,
+    const int16_t *ori_grel, const int32_t *ori_gstart, const int32_t *ori_gcount,
+    const int32_t *inv_col, const float *inv_mask, const int32_t *inv_gptr,
+    const int16_t *inv_grel, const int32_t *inv_gstart, const int32_t *inv_gcount,
+    int64_t r_size, int wot_i, int64_t topk_edges, float *gA, float *gw)
+{
+    memset(gA, 0, sizeof(float) * (size_t)(BL * E));
+    memset(gw, 0, sizeof(float) * (size_t)(BL * n));
+    if (!wot_i) {
+        for (int64_t bl = 0; bl < BL; ++bl) {
+            float wid = w[bl * n + (n - 1)], acc = 0.0f;
+            for (int64_t e = 0; e < E; ++e) {
+                gA[bl * E + e] = grad_ind[bl * E + e] * wid;
+                acc += grad_ind[bl * E + e] * A[bl * E + e];
+            }
+            gw[bl * n + (n - 1)] = acc;
+        }
+    }
+    for (int64_t ai = 0; ai < num_active; ++ai) {
+        int64_t src = active[ai];
+        for (int64_t bl = 0; bl < BL; ++bl) {
+            float a = A[bl * E + src];
+            if (a == 0) continue;
+            or_max_bwd_row(src, bl, a, w, ori_gptr, ori_grel, ori_gstart, ori_gcount, ori_col, ori_mask,
+                           grad_ori, ori_arg, gA, gw, topk_edges, E, n, 0);
+            or_max_bwd_row(src, bl, a, w, inv_gptr, inv_grel, inv_gstart, inv_gcount, inv_col, inv_mask,
+                           grad_inv, inv_arg, gA, gw, topk_edges, E, n, r_size);
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* Filtered, tie-aware rank of the target per query: flashlog.cu:2754-2910.
  * Scores are a sparse [B, E] matrix given as (b, e, v) entries sorted by
@@ -438,38 +510,43 @@ static int64_t or_lower_bound(const int64_t *a, int64_t n, int64_t key)
     return lo;
 }
 
-void or_filtered_ranks(int64_t nnz, const int64_t *idx_b, const int64_t *idx_e, const float *values,
-                       int64_t B, int64_t E, const int64_t *targets,
-                       int64_t nfilter, const int64_t *filter_keys, int use_eql, float *ranks)
-{
-    float *truth = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
-    float *greater = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
-    float *equal = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
-    float *explicit_unf = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
-    float *fcount = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));
-    for (int64_t i = 0; i < nnz; ++i)
-        if (idx_e[i] == targets[idx_b[i]]) truth[idx_b[i]] = values[i];
-    for (int64_t k = 0; k < nfilter; ++k) {
-        int64_t b = filter_keys[k] / E;
-        if (b >= 0 && b < B) fcount[b] += 1.0f;
-    }
-    for (int64_t i = 0; i < nnz; ++i) {
-        int64_t b = idx_b[i], key = b * E + idx_e[i];
-        int64_t pos = or_lower_bound(filter_keys, nfilter, key);
-        if (pos < nfilter && filter_keys[pos] == key) continue;
-        explicit_unf[b] += 1.0f;
-        if (values[i] > truth[b]) greater[b] += 1.0f;
-        else if (values[i] == truth[b]) equal[b] += 1.0f;
-    }
-    for (int64_t b = 0; b < B; ++b) {
-        if (use_eql) {
-            float missing = (float)E - fcount[b] - explicit_unf[b];
-            float eq = equal[b] + (truth[b] == 0.0f ? missing : 0.0f);
-            eq += 1.0f;
-            ranks[b] = greater[b] + (eq + 1.0f) * 0.5f;
-        } else {
-            ranks[b] = greater[b] + 1.0f;
-        }
-    }
-    free(truth); free(greater); free(equal); free(explicit_unf); free(fcount);
+#define OR_DEFINE_FILTERED_RANKS(NAME, T)                                                    \
+void NAME(int64_t nnz, const int64_t *idx_b, const int64_t *idx_e, const T *values,             \
+          int64_t B, int64_t E, const int64_t *targets,                                          \
+          int64_t nfilter, const int64_t *filter_keys, int use_eql, float *ranks)                \
+{                                                                                                \
+    T *truth = (T *)calloc((size_t)(B > 0 ? B : 1), sizeof(T));                                  \
+    float *greater = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));                    \
+    float *equal = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));                      \
+    float *explicit_unf = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));               \
+    float *fcount = (float *)calloc((size_t)(B > 0 ? B : 1), sizeof(float));                     \
+    for (int64_t i = 0; i < nnz; ++i)                                                            \
+        if (idx_e[i] == targets[idx_b[i]]) truth[idx_b[i]] = values[i];                          \
+    for (int64_t k = 0; k < nfilter; ++k) {                                                      \
+        int64_t b = filter_keys[k] / E;                                                          \
+        if (b >= 0 && b < B) fcount[b] += 1.0f;                                                  \
+    }                                                                                            \
+    for (int64_t i = 0; i < nnz; ++i) {                                                          \
+        int64_t b = idx_b[i], key = b * E + idx_e[i];                                            \
+        int64_t pos = or_lower_bound(filter_keys, nfilter, key);                                 \
+        if (pos < nfilter && filter_keys[pos] == key) continue;                                  \
+        explicit_unf[b] += 1.0f;                                                                 \
+        if (values[i] > truth[b]) greater[b] += 1.0f;                                            \
+        else if (values[i] == truth[b]) equal[b] += 1.0f;                                        \
+    }                                                                                            \
+    for (int64_t b = 0; b < B; ++b) {                                                            \
+        if (use_eql) {                                                                           \
+            float missing = (float)E - fcount[b] - explicit_unf[b];                              \
+            float eq = equal[b] + (truth[b] == (T)0 ? missing : 0.0f);                           \
+            eq += 1.0f;                                                                          \
+            ranks[b] = greater[b] + (eq + 1.0f) * 0.5f;                                          \
+        } else {                                                                                 \
+            ranks[b] = greater[b] + 1.0f;                                                        \
+        }                                                                                        \
+    }                                                                                            \
+    free(truth); free(greater); free(equal); free(explicit_unf); free(fcount);                   \
 }
+
+/* flashlog.cu:2754-2910 for float and double scores (AT_DISPATCH_FLOATING_TYPES). */
+OR_DEFINE_FILTERED_RANKS(or_filtered_ranks, float)
+OR_DEFINE_FILTERED_RANKS(or_filtered_ranks_f64, double)

@@ -200,6 +200,28 @@ def dense_max_forward(A, w, csr, masks, r_size, wot_i=False, topk_edges=1 << 60,
     return (*out, *args_out)
 
 
+def dense_max_backward(grad_ind, grad_ori, grad_inv, arg_ori, arg_inv, A, w, csr, masks, r_size, wot_i=False,
+                       topk_edges=1 << 60, active=None):
+    A = _c(A, np.float32)
+    BL, E = A.shape
+    w = _c(w, np.float32).reshape(BL, -1)
+    n = w.shape[1]
+    if active is None:
+        active = active_nodes(A)
+    active = _c(active, np.int64)
+    masks = tuple(_c(m, np.float32) for m in masks)
+    args = _csr_args(csr, masks)
+    g = [_c(x, np.float32).reshape(BL, E) for x in (grad_ind, grad_ori, grad_inv)]
+    arg = [_c(x, np.int64).reshape(BL, E) for x in (arg_ori, arg_inv)]
+    gA = np.empty((BL, E), np.float32)
+    gw = np.empty((BL, n), np.float32)
+    lib().or_dense_max_backward(
+        ctypes.c_int64(BL), ctypes.c_int64(E), ctypes.c_int64(n), _p(A), _p(w), *[_p(x) for x in g],
+        *[_p(x) for x in arg], _p(active), ctypes.c_int64(active.shape[0]), *[_p(a) for a in args],
+        ctypes.c_int64(r_size), ctypes.c_int(int(bool(wot_i))), ctypes.c_int64(int(topk_edges)), _p(gA), _p(gw))
+    return gA, gw
+
+
 # --------------------------------------------------------------------------
 # c1 entity budget: flashlog_kernel.py:814-842
 
@@ -239,11 +261,13 @@ def dense_topc_brute(A, c):
 def filtered_ranks(idx_b, idx_e, values, targets, filter_keys, B, E, use_eql=False):
     idx_b = _c(idx_b, np.int64)
     idx_e = _c(idx_e, np.int64)
-    values = _c(values, np.float32)
+    f64 = np.asarray(values).dtype == np.float64
+    values = _c(values, np.float64 if f64 else np.float32)
     targets = _c(targets, np.int64)
     filter_keys = np.sort(_c(filter_keys, np.int64))
     ranks = np.empty(B, np.float32)
-    lib().or_filtered_ranks(ctypes.c_int64(values.shape[0]), _p(idx_b), _p(idx_e), _p(values),
+    fn = lib().or_filtered_ranks_f64 if f64 else lib().or_filtered_ranks
+    fn(ctypes.c_int64(values.shape[0]), _p(idx_b), _p(idx_e), _p(values),
                             ctypes.c_int64(B), ctypes.c_int64(E), _p(targets),
                             ctypes.c_int64(filter_keys.shape[0]), _p(filter_keys),
                             ctypes.c_int(int(bool(use_eql))), _p(ranks))
@@ -254,7 +278,9 @@ def filtered_ranks_brute(dense_scores, targets, filter_mask, use_eql=False):
     """Independent check on a dense [B, E] score matrix: count unfiltered
     entities scoring above / equal to the target (the target itself is not
     counted unless it is unfiltered, in which case it is one of the ties)."""
-    S = np.asarray(dense_scores, np.float32)
+    S = np.asarray(dense_scores)
+    if S.dtype != np.float64:
+        S = S.astype(np.float32)
     B, E = S.shape
     ranks = np.empty(B, np.float64)
     for b in range(B):

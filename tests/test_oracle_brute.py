@@ -140,15 +140,53 @@ def test_dense_max_forward_brute():
 
 
 @pytest.mark.parametrize("use_eql", [False, True])
-def test_filtered_ranks_brute(use_eql):
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("target_filtered", [True, False])
+def test_filtered_ranks_brute(use_eql, dtype, target_filtered):
     rng = np.random.default_rng(1)
     B, E = 6, 50
-    S = np.where(rng.random((B, E)) < 0.3, rng.integers(0, 4, (B, E)) / 4.0, 0.0).astype(np.float32)
+    S = np.where(rng.random((B, E)) < 0.3, rng.integers(0, 4, (B, E)) / 4.0, 0.0).astype(dtype)
     targets = rng.integers(0, E, B)
     filt = rng.random((B, E)) < 0.1
-    filt[np.arange(B), targets] = True
+    filt[np.arange(B), targets] = target_filtered
     b, e = np.nonzero(S)
     keys = np.nonzero(filt.reshape(-1))[0]
     got = O.filtered_ranks(b, e, S[b, e], targets, keys, B, E, use_eql)
     want = O.filtered_ranks_brute(S, targets, filt, use_eql)
     np.testing.assert_allclose(got, want)
+
+
+@pytest.mark.parametrize("K", [1 << 60, 2])
+@pytest.mark.parametrize("wot_i", [False, True])
+def test_dense_max_backward_brute(K, wot_i):
+    """Winner-only gradient, rebuilt in float64 from the per-position arrays
+    (row_ptr / r_ind), not from the group walk the oracle uses."""
+    rng = np.random.default_rng(4)
+    h, r, t, E, R, csr = small_graph(2, 0.01, seed=17)
+    n = 2 * R + 1
+    BL = 5
+    A = sparse_state(BL, E, 15, rng, ties=True)
+    w = attention(BL, n, rng)
+    _, masks = masks_for(csr, h.shape[0], rng)
+    oi, oo, ov, ao, av = O.dense_max_forward(A, w, csr, masks, R, wot_i=wot_i, topk_edges=K)
+    g = [rng.standard_normal((BL, E)).astype(np.float32) for _ in range(3)]
+    g[1][rng.random((BL, E)) < 0.3] = 0.0
+    gA, gw = O.dense_max_backward(*g, ao, av, A, w, csr, masks, R, wot_i=wot_i, topk_edges=K)
+    eA = np.zeros((BL, E))
+    ew = np.zeros((BL, n))
+    if not wot_i:
+        eA += g[0].astype(np.float64) * w[:, -1:].astype(np.float64)
+        ew[:, -1] = (g[0].astype(np.float64) * A).sum(1)
+    for side, (rp, ri, off, m, grad, arg) in enumerate([(csr[0], csr[2], 0, masks[0], g[1], ao),
+                                                       (csr[4], csr[6], R, masks[1], g[2], av)]):
+        for bl, d in zip(*np.nonzero(arg >= 0)):
+            p = arg[bl, d]
+            s = np.searchsorted(rp, p, side="right") - 1
+            go = float(grad[bl, d])
+            if go == 0.0:
+                continue
+            col = off + int(ri[p])
+            eA[bl, s] += go * float(w[bl, col]) * float(m[p])
+            ew[bl, col] += go * float(A[bl, s]) * float(m[p])
+    np.testing.assert_allclose(gA, eA, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(gw, ew, rtol=1e-5, atol=1e-5)
