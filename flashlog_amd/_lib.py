@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 FL_SEG = 32
 FL_SUP = 16
 
@@ -50,6 +50,19 @@ class FlSide(ctypes.Structure):
     ]
 
 
+class FlSparseHop(ctypes.Structure):
+    """Mirror of ``fl_sparse_hop`` (include/flashlog_hip.h)."""
+    _fields_ = [
+        ("sp_b", ctypes.c_void_p), ("sp_l", ctypes.c_void_p), ("sp_e", ctypes.c_void_p),
+        ("sp_v", ctypes.c_void_p), ("nnz", ctypes.c_int64), ("w", ctypes.c_void_p),
+        ("B", ctypes.c_int64), ("L", ctypes.c_int64), ("E", ctypes.c_int64), ("n", ctypes.c_int64),
+        ("r_size", ctypes.c_int64), ("wot_i", ctypes.c_int), ("mode", ctypes.c_int),
+        ("topk_edges", ctypes.c_int64), ("ws1", ctypes.c_void_p), ("ws1_bytes", ctypes.c_size_t),
+        ("ws2", ctypes.c_void_p), ("ws2_bytes", ctypes.c_size_t), ("items", ctypes.c_int64),
+        ("tiles", ctypes.c_int64),
+    ]
+
+
 _SIGS = {
     "fl_last_error": (ctypes.c_char_p, []),
     "fl_abi_version": (ctypes.c_int, []),
@@ -84,6 +97,22 @@ _SIGS = {
     "fl_dense_max_backward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide)] +
                               [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_int] +
                               [ctypes.c_void_p] * 2),
+    "fl_sparse_buckets": (ctypes.c_int64, [ctypes.c_int64]),
+    "fl_sparse_plan_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
+    "fl_sparse_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
+                                      ctypes.POINTER(FlSparseHop), ctypes.c_void_p]),
+    "fl_sparse_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int]),
+    "fl_sparse_expand": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
+                                        ctypes.POINTER(FlSparseHop), ctypes.c_void_p, ctypes.c_void_p]),
+    "fl_sparse_emit": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
+    "fl_sparse_backward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
+                                          ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
+    "fl_sparse_topc": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 + [ctypes.c_void_p] * 3),
+    "fl_sparse_rowptr_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "fl_sparse_normalize_forward": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3 +
+                                    [ctypes.c_float] + [ctypes.c_void_p] * 4),
+    "fl_sparse_normalize_backward": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_float,
+                                                                            ctypes.c_void_p]),
     "fl_filtered_ranks_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int]),
     "fl_filtered_ranks": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int] + [ctypes.c_void_p] * 2 +
                           [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,

@@ -24,6 +24,14 @@ __device__ __forceinline__ long long fl_wave_sum_i64(long long v) {
     return v;
 }
 
+// Butterfly sum of one float per lane (a fixed association, so the result
+// is the same on every run); every lane receives the total.
+__device__ __forceinline__ float fl_wave_sum_f32(float v) {
+#pragma unroll
+    for (int o = FL_WAVE / 2; o > 0; o >>= 1) v = fl_add(v, __shfl_xor(v, o, FL_WAVE));
+    return v;
+}
+
 // Inclusive prefix sum across the 64 lanes of a wave.
 __device__ __forceinline__ int fl_wave_incl_scan_i32(int v) {
     const int lane = fl_lane();

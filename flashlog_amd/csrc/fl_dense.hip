@@ -28,6 +28,8 @@
 // the reference CPU bits.
 #include "fl_common.h"
 #include "fl_abi.h"
+#include "fl_c2.h"
+#include "fl_topc.h"
 
 namespace fl {
 
@@ -63,46 +65,6 @@ __global__ void k_mark_active(const float *__restrict__ A, int32_t *__restrict__
 // c1 entity budget (flashlog_kernel.py:814-842): one 1024-thread workgroup per
 // row; exact radix select (11/11/10 bits) of the c-th largest nonzero, then an
 // ordered scan for the last kept tie.
-
-constexpr int TOPC_NT = 1024;
-
-template <int NBINS>
-__device__ __forceinline__ void topc_select(const int *hist, int need, int *lds_scan,
-                                            int *sel_bin, int *sel_need) {
-    constexpr int PER = NBINS / TOPC_NT;  // bins per thread (1 or 2)
-    const int t = threadIdx.x;
-    const int owner = TOPC_NT - 1 - t;    // reversed ownership: scan gives suffix sums
-    int v = 0;
-#pragma unroll
-    for (int k = 0; k < PER; ++k) v += hist[owner * PER + k];
-    int total;
-    int above = fl_block_excl_scan<TOPC_NT>(v, lds_scan, &total);
-#pragma unroll
-    for (int k = PER - 1; k >= 0; --k) {
-        int b = owner * PER + k;
-        int h = hist[b];
-        if (above < need && need <= above + h) { *sel_bin = b; *sel_need = need - above; }
-        above += h;
-    }
-    __syncthreads();
-}
-
-// Loads of TOPC_U elements per thread are issued together before their use.
-constexpr int TOPC_U = 8;
-
-#define TOPC_FOR_ROW(BODY)                                                        \
-    for (int64_t base_ = 0; base_ < E; base_ += (int64_t)TOPC_NT * TOPC_U) {      \
-        float v_[TOPC_U];                                                         \
-        _Pragma("unroll") for (int u_ = 0; u_ < TOPC_U; ++u_) {                   \
-            const int64_t e_ = base_ + (int64_t)u_ * TOPC_NT + t;                 \
-            v_[u_] = e_ < E ? a[e_] : 0.0f;                                       \
-        }                                                                         \
-        _Pragma("unroll") for (int u_ = 0; u_ < TOPC_U; ++u_) {                   \
-            const int64_t e = base_ + (int64_t)u_ * TOPC_NT + t;                  \
-            const float v = v_[u_];                                               \
-            if (e < E) { BODY }                                                   \
-        }                                                                         \
-    }
 
 __global__ __launch_bounds__(TOPC_NT) void k_topc_rows(const float *__restrict__ A,
                                                         float *__restrict__ out, int64_t E,
@@ -318,84 +280,6 @@ __global__ __launch_bounds__(COL_NT) void k_frontier(
             }
         }
     }
-}
-
-// Wave-level c2 threshold for one (source, row, direction): the weighted
-// order statistic of flashlog.cpp:12-35 by MSB-first radix select over the
-// float bits of the group weights (4 passes of 8 bits, group sizes as
-// multiplicities), then the tie-quota cut: ties are admitted in group order,
-// so the admitted tied edges are exactly the positions below `cut`.
-// Returns false when every eligible edge fits (no pruning).
-__device__ bool c2_select(const fl_side &s, int64_t g0, int64_t g1, const float *wrow,
-                          int64_t K, int *hist, uint32_t *th_key, int32_t *cut) {
-    const int lane = fl_lane();
-    long long tot = 0;
-    for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
-        float wv = wrow[s.group_rel[g]];
-        if (wv > 0.0f) tot += s.group_count[g];
-    }
-    tot = fl_wave_sum_i64(tot);
-    if (tot <= K) return false;
-    int need = (int)K;
-    uint32_t prefix = 0, pmask = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[lane * 4 + 0] = 0; hist[lane * 4 + 1] = 0;
-        hist[lane * 4 + 2] = 0; hist[lane * 4 + 3] = 0;
-        __builtin_amdgcn_wave_barrier();
-        for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
-            float wv = wrow[s.group_rel[g]];
-            uint32_t k = __float_as_uint(wv);
-            if (wv > 0.0f && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255], s.group_count[g]);
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const int owner = FL_WAVE - 1 - lane;
-        int h[4];
-        int v = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) { h[k] = hist[owner * 4 + k]; v += h[k]; }
-        int incl = fl_wave_incl_scan_i32(v);
-        int above = incl - v;
-        int found = 0, digit = 0, nneed = 0;
-#pragma unroll
-        for (int k = 3; k >= 0; --k) {
-            if (!found && above < need && need <= above + h[k]) { found = 1; digit = owner * 4 + k; nneed = need - above; }
-            above += h[k];
-        }
-        unsigned long long bal = __ballot(found);
-        int src_lane = __ffsll((long long)bal) - 1;
-        digit = __shfl(digit, src_lane, FL_WAVE);
-        nneed = __shfl(nneed, src_lane, FL_WAVE);
-        prefix |= (uint32_t)digit << shift;
-        pmask |= 0xFFu << shift;
-        need = nneed;
-        __builtin_amdgcn_wave_barrier();
-    }
-    // cut: first tied group whose cumulative tie count passes `need`
-    int run = 0;
-    int32_t c = 0x7FFFFFFF;
-    for (int64_t base = g0; base < g1; base += FL_WAVE) {
-        const int64_t g = base + lane;
-        int cnt = 0;
-        int st = 0;
-        if (g < g1) {
-            float wv = wrow[s.group_rel[g]];
-            if (wv > 0.0f && __float_as_uint(wv) == prefix) { cnt = s.group_count[g]; st = s.group_start[g]; }
-        }
-        int incl = fl_wave_incl_scan_i32(cnt);
-        int before = run + incl - cnt;
-        int hit = (cnt > 0) && (before + cnt > need);
-        unsigned long long bal = __ballot(hit);
-        if (bal) {
-            int hl = __ffsll((long long)bal) - 1;
-            c = __shfl(st + (need - before), hl, FL_WAVE);
-            break;
-        }
-        run += __shfl(incl, FL_WAVE - 1, FL_WAVE);
-    }
-    *th_key = prefix;
-    *cut = c;
-    return true;
 }
 
 constexpr int C2_NT = 256;
@@ -951,17 +835,6 @@ __global__ __launch_bounds__(RL_NT) void k_row_list(const uint32_t *__restrict__
     if (threadIdx.x == 0) rowcnt[bl] = run;
 }
 
-// Kept range of group g for (source, row): [start, start + take).
-__device__ __forceinline__ int64_t group_take(float wv, float th, int32_t cut, int64_t start, int64_t count) {
-    if (!(wv > 0.0f)) return 0;
-    if (wv > th) return count;
-    if (wv == th) {
-        const int64_t t = (int64_t)cut - start;
-        return t <= 0 ? 0 : (t < count ? t : count);
-    }
-    return 0;
-}
-
 __device__ __forceinline__ float bwd_walk(const fl_side &s, int64_t src, int64_t bl, int64_t BL, int64_t E,
                                           int64_t n, int64_t off, int dir, float a, const float *__restrict__ w,
                                           const float *__restrict__ grad, const float2 *__restrict__ PK,
@@ -1129,7 +1002,7 @@ int check_side(const fl_side *s, const char *name) {
 
 extern "C" {
 
-int fl_abi_version(void) { return 6; }
+int fl_abi_version(void) { return 7; }
 
 int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool, const int32_t *order,
                   const float *weight, float *out, int64_t nnz) {

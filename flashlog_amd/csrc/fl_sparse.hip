@@ -1,0 +1,948 @@
+// Sparse (COO) sum hop on gfx950.
+//
+// Replaces the expansion kernels of flashlog.cu (count/fill top-k
+// :1368-1559, all edges :1743-1829, identity :1831-1854) and the coalesce
+// of flashlog_kernel.py:258-357, with the addition order of the reference's
+// CPU path (flashlog.cpp:1388-1486): per (row, destination) the
+// contributions are added to 0 in input-entry order, and per entry ORI kept
+// edges (CSR position order), then INV kept edges, then the identity term.
+//
+// Pipeline (rows r = b*L + l; entries must be sorted by row):
+//   plan    k_sp_rowptr   entry range of every row, input validation
+//           k_sp_select   per (entry, side): c2 threshold and cut, item counts
+//           scan          item offsets of every entry (raw order)
+//           k_sp_rowinfo  item range and tile count of every row; scan
+//   expand  k_sp_fill     wave per entry: raw items (destination, value) in
+//                         order, and the per-(row, bucket, tile) histogram
+//           scan          bucket bases
+//           k_sp_partition workgroup per tile of a row: stable scatter of the
+//                         tile's items into destination buckets (block radix
+//                         rank over the bucket id)
+//           k_sp_accum    workgroup per (row, bucket): LDS accumulator of the
+//                         bucket's 8192 destinations; items are applied in
+//                         order, one item per destination per round, so every
+//                         destination sees its additions in raw order
+//           scan          output offsets
+//   emit    k_sp_emit     coalesced COO (b, l, e, v), ascending key
+//   backward k_sp_bwd     wave per entry: the same walk, gradients gathered
+//                         through the saved raw-item -> output map
+#include <limits.h>
+
+#include "fl_abi.h"
+#include "fl_c2.h"
+#include "fl_common.h"
+#include "fl_scan.h"
+#include "fl_topc.h"
+
+namespace fl {
+
+constexpr int SP_S = 13;               // destinations per bucket = 2^SP_S
+constexpr int SP_W = 1 << SP_S;
+constexpr int SP_NT = 256;
+constexpr int SP_IPT = 16;
+constexpr int SP_TILE = SP_NT * SP_IPT;  // items per partition tile
+constexpr int SP_HASH = 512;
+
+enum { SP_TOPK = 0, SP_ALL = 1 };
+
+// ---------------------------------------------------------------------------
+// plan
+
+// row_ptr[r] = first entry of row r (entries sorted by row); err[0] gets a
+// nonzero code for a malformed input (1: index out of range, 2: rows not
+// sorted).
+__global__ void k_sp_rowptr(const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
+                            const int64_t *__restrict__ se, int64_t nnz, int64_t B, int64_t L, int64_t E,
+                            int64_t *__restrict__ row_ptr, int64_t *__restrict__ err) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t R = B * L;
+    if (nnz == 0) {
+        for (int64_t r = i; r <= R; r += (int64_t)gridDim.x * blockDim.x) row_ptr[r] = 0;
+        return;
+    }
+    if (i >= nnz) return;
+    const int64_t b = sb[i], l = sl[i], e = se[i];
+    if (b < 0 || b >= B || l < 0 || l >= L || e < 0 || e >= E) {
+        atomicMax((unsigned long long *)err, 1ull);
+        return;
+    }
+    const int64_t r = b * L + l;
+    int64_t rp = -1;
+    if (i > 0) {
+        const int64_t pb = sb[i - 1], pl = sl[i - 1];
+        rp = (pb >= 0 && pb < B && pl >= 0 && pl < L) ? pb * L + pl : r;
+        if (rp > r) { atomicMax((unsigned long long *)err, 2ull); return; }
+    }
+    for (int64_t q = rp + 1; q <= r; ++q) row_ptr[q] = i;
+    if (i == nnz - 1)
+        for (int64_t q = r + 1; q <= R; ++q) row_ptr[q] = nnz;
+}
+
+// One wave per entry: per side the c2 threshold (bits of the threshold
+// weight, 0 = no pruning) and tie cut, and the number of raw items:
+// kept edges with a nonzero mask (top-k mode) or every edge (all-edges
+// mode), plus the identity item.
+constexpr int SEL_NT = 256;
+
+__global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
+                                                     const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
+                                                     int64_t nnz, const float *__restrict__ w, int64_t B, int64_t L,
+                                                     int64_t E, int64_t n, int64_t r_size, int wot_i, int mode, int64_t K,
+                                                     float *__restrict__ th, int32_t *__restrict__ cut,
+                                                     int32_t *__restrict__ cnt) {
+    __shared__ int hist_all[SEL_NT / FL_WAVE][256];
+    const int lane = fl_lane();
+    const int wid = threadIdx.x / FL_WAVE;
+    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + wid;
+    if (i >= nnz) return;
+    const int64_t src = se[i];
+    if (sb[i] < 0 || sb[i] >= B || sl[i] < 0 || sl[i] >= L || src < 0 || src >= E) {
+        if (lane == 0) { cnt[i] = 0; th[2 * i] = th[2 * i + 1] = 0.0f; cut[2 * i] = cut[2 * i + 1] = 0; }
+        return;  // reported by k_sp_rowptr; the plan is not used
+    }
+    const float *wrow = w + (sb[i] * L + sl[i]) * n;
+    int total = wot_i ? 0 : 1;
+    for (int dir = 0; dir < 2; ++dir) {
+        const fl_side &s = dir ? inv : ori;
+        const float *wr = wrow + (dir ? r_size : 0);
+        const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
+        float thv = 0.0f;
+        int32_t ct = 0;
+        long long c = 0;
+        if (mode == SP_ALL) {
+            for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) c += s.group_count[g];
+        } else {
+            uint32_t key;
+            int32_t cc;
+            if (K < 0) {
+                thv = __int_as_float(0x7f800000);  // budget <= 0: no edge is kept
+            } else if (K > 0 && c2_select(s, g0, g1, wr, K, hist_all[wid], &key, &cc)) {
+                thv = __uint_as_float(key);
+                ct = cc;
+            }
+            for (int64_t g = g0; g < g1; ++g) {
+                const int64_t start = s.group_start[g];
+                const int64_t take = group_take(wr[s.group_rel[g]], thv, ct, start, s.group_count[g]);
+                for (int64_t k = lane; k < take; k += FL_WAVE) c += s.mask[start + k] != 0.0f ? 1 : 0;
+            }
+        }
+        c = fl_wave_sum_i64(c);
+        total += (int)c;
+        if (lane == 0) {
+            th[2 * i + dir] = thv;
+            cut[2 * i + dir] = ct;
+        }
+    }
+    if (lane == 0) cnt[i] = total;
+}
+
+// Per row r (and r = R): first item and tile count.
+__global__ void k_sp_rowinfo(const int64_t *__restrict__ row_ptr, const int64_t *__restrict__ item_off, int64_t R,
+                             int64_t *__restrict__ row_item0, int32_t *__restrict__ ntiles) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r > R) return;
+    const int64_t a = item_off[row_ptr[r]];
+    row_item0[r] = a;
+    if (r < R) {
+        const int64_t b = item_off[row_ptr[r + 1]];
+        ntiles[r] = (int32_t)((b - a + SP_TILE - 1) / SP_TILE);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// expand
+
+struct SpRows {
+    const int64_t *row_item0;  // [R+1]
+    const int64_t *tile_base;  // [R+1]
+    int64_t NB;                // buckets per row
+};
+
+// One wave per entry: the entry's items in raw order at item_off[i].
+__global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
+                                                   const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
+                                                   const float *__restrict__ sv, int64_t nnz,
+                                                   const float *__restrict__ w, int64_t L, int64_t n,
+                                                   int64_t r_size, int wot_i, int mode,
+                                                   const float *__restrict__ th, const int32_t *__restrict__ cut,
+                                                   const int64_t *__restrict__ item_off, SpRows rows,
+                                                   int32_t *__restrict__ hist, int32_t *__restrict__ raw_dst,
+                                                   float *__restrict__ raw_val) {
+    const int lane = fl_lane();
+    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
+    if (i >= nnz) return;
+    const int64_t src = se[i];
+    const int64_t r = sb[i] * L + sl[i];
+    const float a = sv[i];
+    const float *wrow = w + r * n;
+    const int64_t rbase = rows.row_item0[r];
+    const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
+    int32_t *hrow = hist + rows.tile_base[r] * rows.NB;
+    const bool count = rows.NB > 1;
+    int64_t pos = item_off[i];
+    for (int dir = 0; dir < 2; ++dir) {
+        const fl_side &s = dir ? inv : ori;
+        const float *wr = wrow + (dir ? r_size : 0);
+        const float thv = th[2 * i + dir];
+        const int32_t ct = cut[2 * i + dir];
+        const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
+        for (int64_t g = g0; g < g1; ++g) {
+            const float wv = wr[s.group_rel[g]];
+            const int64_t start = s.group_start[g];
+            const int64_t cntg = s.group_count[g];
+            const int64_t take = mode == SP_ALL ? cntg : group_take(wv, thv, ct, start, cntg);
+            if (take <= 0) continue;
+            const float gp = fl_mul(a, wv);
+            for (int64_t k0 = 0; k0 < take; k0 += FL_WAVE) {
+                const int64_t k = k0 + lane;
+                int32_t d = 0;
+                float m = 0.0f;
+                bool keep = false;
+                if (k < take) {
+                    m = s.mask[start + k];
+                    d = s.col_ind[start + k];
+                    keep = mode == SP_ALL || m != 0.0f;
+                }
+                const unsigned long long bal = __ballot(keep);
+                if (keep) {
+                    const int64_t q = pos + __popcll(bal & ((1ull << lane) - 1ull));
+                    raw_dst[q] = d;
+                    raw_val[q] = fl_mul(gp, m);
+                    if (count) atomicAdd(&hrow[(int64_t)(d >> SP_S) * nt + (q - rbase) / SP_TILE], 1);
+                }
+                pos += __popcll(bal);
+            }
+        }
+    }
+    if (!wot_i && lane == 0) {
+        raw_dst[pos] = (int32_t)src;
+        raw_val[pos] = fl_mul(a, wrow[n - 1]);
+        if (count) atomicAdd(&hrow[(int64_t)(src >> SP_S) * nt + (pos - rbase) / SP_TILE], 1);
+    }
+}
+
+// Row of a tile: the r with tile_base[r] <= tile < tile_base[r+1].
+__device__ __forceinline__ int64_t sp_tile_row(const int64_t *tile_base, int64_t R, int64_t tile) {
+    int64_t lo = 0, hi = R;  // invariant: tile_base[lo] <= tile < tile_base[hi]
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (tile_base[mid] <= tile) lo = mid;
+        else hi = mid;
+    }
+    return lo;
+}
+
+// Stable block sort of SP_TILE packed keys (bucket << 12 | index) by the
+// bucket bits [12, 12 + nbits), 4 bits per pass.  kin/kout are LDS buffers
+// of SP_TILE keys; returns the buffer holding the result.
+__device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int nbits, uint16_t (*cnt)[SP_NT], int *scan_lds) {
+    const int t = threadIdx.x;
+    for (int shift = 12; shift < 12 + nbits; shift += 4) {
+        uint32_t key[SP_IPT];
+        uint16_t loc[SP_IPT];
+#pragma unroll
+        for (int d = 0; d < 16; ++d) cnt[d][t] = 0;
+#pragma unroll
+        for (int j = 0; j < SP_IPT; ++j) {
+            key[j] = kin[t * SP_IPT + j];
+            const int d = (key[j] >> shift) & 15;
+            loc[j] = cnt[d][t];
+            cnt[d][t] = (uint16_t)(loc[j] + 1);
+        }
+        __syncthreads();
+        // exclusive scan of the counters in digit-major order; thread t owns
+        // flat entries [16t, 16t + 16) = digit t/16, threads 16*(t%16) ...
+        uint16_t *flat = &cnt[0][0];
+        int part = 0;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) part += flat[t * 16 + q];
+        int tot;
+        int run = fl_block_excl_scan<SP_NT>(part, scan_lds, &tot);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int c = flat[t * 16 + q];
+            flat[t * 16 + q] = (uint16_t)run;
+            run += c;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SP_IPT; ++j) {
+            const int d = (key[j] >> shift) & 15;
+            kout[cnt[d][t] + loc[j]] = key[j];
+        }
+        __syncthreads();
+        uint32_t *x = kin; kin = kout; kout = x;
+    }
+    return kin;
+}
+
+// Workgroup per tile: stable scatter of the tile's items into the row's
+// destination buckets (bases from the scanned histogram).
+__global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, int nbits,
+                                                       const int64_t *__restrict__ base,
+                                                       const int32_t *__restrict__ raw_dst,
+                                                       const float *__restrict__ raw_val,
+                                                       int32_t *__restrict__ part_dst, float *__restrict__ part_val,
+                                                       int32_t *__restrict__ part_raw) {
+    __shared__ uint32_t kb[2][SP_TILE];
+    __shared__ uint16_t cnt[16][SP_NT];
+    __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
+    const int64_t tile = blockIdx.x;
+    const int64_t r = sp_tile_row(rows.tile_base, R, tile);
+    const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
+    const int64_t tl = tile - rows.tile_base[r];
+    const int64_t i0 = rows.row_item0[r] + tl * SP_TILE;
+    const int64_t i1e = rows.row_item0[r + 1];
+    const int c = (int)((i1e - i0) < SP_TILE ? (i1e - i0) : SP_TILE);
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < SP_IPT; ++j) {
+        const int idx = t * SP_IPT + j;
+        uint32_t key = 0xFFFFF000u | (uint32_t)idx;  // padding sorts last
+        if (idx < c) key = ((uint32_t)(raw_dst[i0 + idx] >> SP_S) << 12) | (uint32_t)idx;
+        kb[0][idx] = key;
+    }
+    __syncthreads();
+    const uint32_t *sorted = sp_block_sort(kb[0], kb[1], nbits, cnt, scan_lds);
+    const int64_t *bb = base + rows.tile_base[r] * rows.NB + tl;
+#pragma unroll 4
+    for (int j = 0; j < SP_IPT; ++j) {
+        const int p = j * SP_NT + t;  // striped: consecutive threads write consecutive slots
+        if (p >= c) continue;
+        const uint32_t key = sorted[p];
+        const uint32_t bk = key >> 12;
+        // first sorted position of this bucket (binary search in LDS)
+        int lo = 0, hi = p;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if ((sorted[mid] >> 12) < bk) lo = mid + 1;
+            else hi = mid;
+        }
+        const int idx = (int)(key & 4095u);
+        const int64_t q = bb[(int64_t)bk * nt] + (p - lo);
+        part_dst[q] = raw_dst[i0 + idx];
+        part_val[q] = raw_val[i0 + idx];
+        if (part_raw) part_raw[q] = (int32_t)(i0 + idx);
+    }
+}
+
+// Workgroup per (row, bucket): ordered accumulation in LDS, then the
+// bucket's outputs compacted in destination order into the first slots of
+// its item range; raw_local[raw position] = the item's output index within
+// the bucket (for the backward).
+__global__ __launch_bounds__(SP_NT) void k_sp_accum(SpRows rows, const int64_t *__restrict__ base,
+                                                   int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                                   const int32_t *__restrict__ raw_arr,
+                                                   int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count) {
+    __shared__ float acc[SP_W];
+    __shared__ uint32_t bits[SP_W / 32];
+    __shared__ int owner[SP_HASH];
+    __shared__ int wpre[SP_W / 32];
+    __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
+    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
+    const int t = threadIdx.x;
+    int64_t start, end;
+    if (rows.NB == 1) {
+        start = rows.row_item0[r];
+        end = rows.row_item0[r + 1];
+    } else {
+        const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
+        const int64_t *bb = base + rows.tile_base[r] * rows.NB + bk * nt;
+        start = bb[0];
+        end = bb[nt];
+    }
+    const int64_t n = end - start;
+    if (n == 0) {
+        if (t == 0) out_count[r * rows.NB + bk] = 0;
+        return;
+    }
+    for (int q = t; q < SP_W / 32; q += SP_NT) bits[q] = 0;
+    for (int q = t; q < SP_HASH; q += SP_NT) owner[q] = INT_MAX;
+    __syncthreads();
+    for (int64_t w0 = 0; w0 < n; w0 += SP_NT) {
+        const int64_t k = w0 + t;
+        bool pending = k < n;
+        int dl = 0;
+        float v = 0.0f;
+        if (pending) {
+            dl = dst_arr[start + k] & (SP_W - 1);
+            v = val_arr[start + k];
+        }
+        const int h = dl & (SP_HASH - 1);
+        // rounds: per hash slot the earliest pending item applies
+        while (true) {
+            if (pending) atomicMin(&owner[h], t);
+            __syncthreads();
+            const bool win = pending && owner[h] == t;
+            if (win) {
+                const uint32_t m = 1u << (dl & 31);
+                const uint32_t old = atomicOr(&bits[dl >> 5], m);
+                acc[dl] = (old & m) ? fl_add(acc[dl], v) : fl_add(0.0f, v);
+            }
+            __syncthreads();
+            if (win) {
+                owner[h] = INT_MAX;
+                pending = false;
+            }
+            if (!__syncthreads_or(pending)) break;
+        }
+    }
+    // output ranks: one bitmap word per thread
+    const uint32_t word = bits[t];
+    int total;
+    const int pre = fl_block_excl_scan<SP_NT>(__popc(word), scan_lds, &total);
+    wpre[t] = pre;
+    __syncthreads();
+    if (raw_local) {
+        for (int64_t k = t; k < n; k += SP_NT) {
+            const int dl = dst_arr[start + k] & (SP_W - 1);
+            raw_local[raw_arr ? raw_arr[start + k] : start + k] =
+                wpre[dl >> 5] + __popc(bits[dl >> 5] & ((1u << (dl & 31)) - 1u));
+        }
+        __syncthreads();
+    }
+    const int32_t dbase = (int32_t)(bk << SP_S);
+    uint32_t wd = word;
+    int64_t o = start + pre;
+    while (wd) {
+        const int bit = __ffs(wd) - 1;
+        wd &= wd - 1;
+        const int dl = t * 32 + bit;
+        dst_arr[o] = dbase + dl;
+        val_arr[o] = acc[dl];
+        ++o;
+    }
+    if (t == 0) out_count[r * rows.NB + bk] = total;
+}
+
+// Workgroup per (row, bucket): staged outputs -> COO at out_base.
+__global__ __launch_bounds__(SP_NT) void k_sp_emit(SpRows rows, int64_t L, const int64_t *__restrict__ base,
+                                                  const int32_t *__restrict__ dst_arr,
+                                                  const float *__restrict__ val_arr,
+                                                  const int64_t *__restrict__ out_base, int64_t *__restrict__ ob,
+                                                  int64_t *__restrict__ ol, int64_t *__restrict__ oe,
+                                                  float *__restrict__ ov) {
+    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
+    const int64_t slot = r * rows.NB + bk;
+    const int64_t o0 = out_base[slot];
+    const int64_t cnt = out_base[slot + 1] - o0;
+    if (cnt == 0) return;
+    int64_t start;
+    if (rows.NB == 1) {
+        start = rows.row_item0[r];
+    } else {
+        const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
+        start = base[rows.tile_base[r] * rows.NB + bk * nt];
+    }
+    const int64_t b = r / L, l = r - (r / L) * L;
+    for (int64_t k = threadIdx.x; k < cnt; k += SP_NT) {
+        ob[o0 + k] = b;
+        ol[o0 + k] = l;
+        oe[o0 + k] = dst_arr[start + k];
+        ov[o0 + k] = val_arr[start + k];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+
+// One wave per entry: the fill walk again; item k of the entry (raw
+// position item_off[i] + k) maps to output out_base[r*NB + dst/8192] +
+// raw_local[...].  grad_v[i] = sum over items of (g*m)*w, plus g*w[n-1] for
+// the identity item (flashlog.cu:1856-1959, order fixed per entry);
+// grad_w[r, col] += (g*m)*a by atomics, as the reference.
+__global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
+                                                  const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
+                                                  const float *__restrict__ sv, int64_t nnz,
+                                                  const float *__restrict__ w, int64_t L, int64_t n, int64_t r_size,
+                                                  int wot_i, int mode, const float *__restrict__ th,
+                                                  const int32_t *__restrict__ cut,
+                                                  const int64_t *__restrict__ item_off, int64_t NB,
+                                                  const int64_t *__restrict__ out_base,
+                                                  const int32_t *__restrict__ raw_local,
+                                                  const float *__restrict__ grad, float *__restrict__ grad_v,
+                                                  float *__restrict__ grad_w) {
+    const int lane = fl_lane();
+    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
+    if (i >= nnz) return;
+    const int64_t src = se[i];
+    const int64_t r = sb[i] * L + sl[i];
+    const float a = sv[i];
+    const float *wrow = w + r * n;
+    const int64_t *orow = out_base + r * NB;
+    float gsp = 0.0f;
+    int64_t pos = item_off[i];
+    for (int dir = 0; dir < 2; ++dir) {
+        const fl_side &s = dir ? inv : ori;
+        const int64_t off = dir ? r_size : 0;
+        const float thv = th[2 * i + dir];
+        const int32_t ct = cut[2 * i + dir];
+        const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
+        for (int64_t g = g0; g < g1; ++g) {
+            const int rel = s.group_rel[g];
+            const float wv = wrow[off + rel];
+            const int64_t start = s.group_start[g];
+            const int64_t cntg = s.group_count[g];
+            const int64_t take = mode == SP_ALL ? cntg : group_take(wv, thv, ct, start, cntg);
+            if (take <= 0) continue;
+            float gws = 0.0f;
+            for (int64_t k0 = 0; k0 < take; k0 += FL_WAVE) {
+                const int64_t k = k0 + lane;
+                int32_t d = 0;
+                float m = 0.0f;
+                bool keep = false;
+                if (k < take) {
+                    m = s.mask[start + k];
+                    d = s.col_ind[start + k];
+                    keep = mode == SP_ALL || m != 0.0f;
+                }
+                const unsigned long long bal = __ballot(keep);
+                if (keep) {
+                    const int64_t q = pos + __popcll(bal & ((1ull << lane) - 1ull));
+                    const float gv = grad[orow[d >> SP_S] + raw_local[q]];
+                    const float gm = fl_mul(gv, m);
+                    gsp = fl_add(gsp, fl_mul(gm, wv));
+                    gws = fl_add(gws, fl_mul(gm, a));
+                }
+                pos += __popcll(bal);
+            }
+            gws = fl_wave_sum_f32(gws);
+            if (lane == 0 && gws != 0.0f) atomicAdd(&grad_w[r * n + off + rel], gws);
+        }
+    }
+    gsp = fl_wave_sum_f32(gsp);
+    if (lane == 0) {
+        if (!wot_i) {
+            const float gv = grad[orow[src >> SP_S] + raw_local[pos]];
+            gsp = fl_add(gsp, fl_mul(gv, wrow[n - 1]));
+            atomicAdd(&grad_w[r * n + n - 1], fl_mul(gv, a));
+        }
+        grad_v[i] = gsp;
+    }
+}
+
+__global__ void k_fill_i32(int32_t *__restrict__ p, int64_t n, int32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void k_fill_i64(int64_t *__restrict__ p, int64_t n, int64_t v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void k_sp_plan_out(const int64_t *__restrict__ items, const int64_t *__restrict__ tiles, int64_t NB,
+                              int64_t *__restrict__ plan) {
+    plan[0] = *items;
+    plan[1] = *tiles;
+    plan[3] = NB;
+}
+
+__global__ void k_fill_f32(float *__restrict__ p, int64_t n, float v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// ---------------------------------------------------------------------------
+// c1 on a coalesced COO state (_sparse_topc_entries, flashlog_kernel.py:
+// 1092-1140): one 1024-thread workgroup per row; rows with more than c
+// nonzeros keep their c largest nonzeros (ties to the earlier entry, i.e. the
+// smaller entity), other rows keep every entry, explicit zeros included.
+__global__ __launch_bounds__(TOPC_NT) void k_sp_topc(const int64_t *__restrict__ row_ptr,
+                                                    const float *__restrict__ vals, int64_t c,
+                                                    int32_t *__restrict__ keep) {
+    __shared__ int hist[2048];
+    __shared__ int lds_scan[TOPC_NT / FL_WAVE + 1];
+    __shared__ int sel_bin, sel_need, s_last, s_done;
+    const int64_t row = blockIdx.x;
+    const int64_t start = row_ptr[row];
+    const int64_t E = row_ptr[row + 1] - start;
+    if (E == 0) return;
+    const float *a = vals + start;
+    int32_t *kp = keep + start;
+    const int t = threadIdx.x;
+    for (int i = t; i < 2048; i += TOPC_NT) hist[i] = 0;
+    __syncthreads();
+    int nz_local = 0;
+    TOPC_FOR_ROW(if (v != 0.0f) { ++nz_local; atomicAdd(&hist[fl_order_key(v) >> 21], 1); })
+    int nz;
+    (void)fl_block_excl_scan<TOPC_NT>(nz_local, lds_scan, &nz);
+    const bool over = (int64_t)nz > c;
+    uint32_t cutkey = 0;
+    int64_t last = -1;
+    if (over && c > 0) {
+        topc_select<2048>(hist, (int)c, lds_scan, &sel_bin, &sel_need);
+        uint32_t prefix = (uint32_t)sel_bin << 21;
+        int need = sel_need;
+        for (int i = t; i < 2048; i += TOPC_NT) hist[i] = 0;
+        __syncthreads();
+        TOPC_FOR_ROW(const uint32_t k = fl_order_key(v);
+                     if (v != 0.0f && (k >> 21) == (prefix >> 21)) atomicAdd(&hist[(k >> 10) & 2047], 1);)
+        __syncthreads();
+        topc_select<2048>(hist, need, lds_scan, &sel_bin, &sel_need);
+        prefix |= (uint32_t)sel_bin << 10;
+        need = sel_need;
+        for (int i = t; i < 2048; i += TOPC_NT) hist[i] = 0;
+        __syncthreads();
+        TOPC_FOR_ROW(const uint32_t k = fl_order_key(v);
+                     if (v != 0.0f && (k >> 10) == (prefix >> 10)) atomicAdd(&hist[k & 1023], 1);)
+        __syncthreads();
+        topc_select<1024>(hist, need, lds_scan, &sel_bin, &sel_need);
+        prefix |= (uint32_t)sel_bin;
+        need = sel_need;
+        const int tied_total = hist[sel_bin];
+        cutkey = prefix;
+        if (need >= tied_total) {
+            last = E;
+        } else {
+            if (t == 0) { s_last = -1; s_done = 0; }
+            __syncthreads();
+            int run = 0;
+            for (int64_t base = 0; base < E; base += TOPC_NT) {
+                const int64_t e = base + t;
+                int flag = 0;
+                if (e < E) {
+                    const float v = a[e];
+                    flag = (v != 0.0f && fl_order_key(v) == cutkey) ? 1 : 0;
+                }
+                int tot;
+                const int ex = fl_block_excl_scan<TOPC_NT>(flag, lds_scan, &tot);
+                if (flag && run + ex + 1 == need) { s_last = (int)e; s_done = 1; }
+                run += tot;
+                __syncthreads();
+                if (s_done) break;
+            }
+            last = s_last;
+        }
+    }
+    TOPC_FOR_ROW(int k = 1;
+                 if (over) {
+                     k = 0;
+                     if (c > 0 && v != 0.0f) {
+                         const uint32_t q = fl_order_key(v);
+                         k = (q > cutkey) || (q == cutkey && e <= last);
+                     }
+                 }
+                 kp[e] = k;)
+}
+
+// ---------------------------------------------------------------------------
+// normalize_sparse3d (flashlog.cu:2480-2691; flashlog_kernel.py:536-614):
+// per row the sum of its values (fixed order: 256 strided partial sums, then
+// a tree), out = v / max(d, eps); backward g/dc - sum(g*v)/dc^2 where d >= eps.
+
+constexpr int NM_NT = 256;
+
+__device__ __forceinline__ float block_tree_sum(float v, float *red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int st = NM_NT / 2; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) red[threadIdx.x] = fl_add(red[threadIdx.x], red[threadIdx.x + st]);
+        __syncthreads();
+    }
+    const float s = red[0];
+    __syncthreads();
+    return s;
+}
+
+__global__ __launch_bounds__(NM_NT) void k_norm_fwd(const int64_t *__restrict__ row_ptr,
+                                                   const float *__restrict__ v, float eps, float *__restrict__ out,
+                                                   float *__restrict__ denom) {
+    __shared__ float red[NM_NT];
+    const int64_t r = blockIdx.x;
+    const int64_t a = row_ptr[r], b = row_ptr[r + 1];
+    float s = 0.0f;
+    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) s = fl_add(s, v[k]);
+    const float d = block_tree_sum(s, red);
+    const float dc = d < eps ? eps : d;
+    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) out[k] = __fdiv_rn(v[k], dc);
+    if (threadIdx.x == 0) denom[r] = d;
+}
+
+__global__ __launch_bounds__(NM_NT) void k_norm_bwd(const int64_t *__restrict__ row_ptr,
+                                                   const float *__restrict__ g, const float *__restrict__ v,
+                                                   const float *__restrict__ denom, float eps,
+                                                   float *__restrict__ gv) {
+    __shared__ float red[NM_NT];
+    const int64_t r = blockIdx.x;
+    const int64_t a = row_ptr[r], b = row_ptr[r + 1];
+    const float d = denom[r];
+    const float dc = d < eps ? eps : d;
+    float s = 0.0f;
+    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) s = fl_add(s, fl_mul(g[k], v[k]));
+    const float sgx = block_tree_sum(s, red);
+    const bool active = d >= eps;
+    const float corr = __fdiv_rn(sgx, fl_mul(dc, dc));
+    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) {
+        const float x = __fdiv_rn(g[k], dc);
+        gv[k] = active ? __fsub_rn(x, corr) : x;
+    }
+}
+
+}  // namespace fl
+
+// ---------------------------------------------------------------------------
+// C-ABI
+
+using namespace fl;
+
+namespace {
+
+size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int64_t sp_buckets(int64_t E) { return E <= 0 ? 1 : (E + SP_W - 1) / SP_W; }
+
+int sp_bucket_bits(int64_t NB) {
+    int b = 0;
+    while (((int64_t)1 << b) < NB) ++b;
+    return b;
+}
+
+// plan workspace layout
+struct SpPlan {
+    float *th;
+    int32_t *cut, *cnt, *ntiles;
+    int64_t *item_off, *row_ptr, *row_item0, *tile_base, *tmp;
+    size_t bytes;
+};
+
+SpPlan sp_plan_layout(int64_t nnz, int64_t R, char *base) {
+    SpPlan p{};
+    size_t off = 0;
+    auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
+    p.th = (float *)take(sizeof(float) * 2 * (size_t)nnz);
+    p.cut = (int32_t *)take(sizeof(int32_t) * 2 * (size_t)nnz);
+    p.cnt = (int32_t *)take(sizeof(int32_t) * (size_t)nnz);
+    p.item_off = (int64_t *)take(sizeof(int64_t) * (size_t)(nnz + 1));
+    p.row_ptr = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
+    p.row_item0 = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
+    p.ntiles = (int32_t *)take(sizeof(int32_t) * (size_t)R);
+    p.tile_base = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
+    const int64_t mx = nnz > R ? nnz : R;
+    p.tmp = (int64_t *)take(scan_tmp_bytes(mx + 1));
+    p.bytes = off;
+    return p;
+}
+
+// expansion workspace layout
+struct SpExp {
+    int32_t *raw_dst, *part_dst, *part_raw, *hist, *out_count;
+    float *raw_val, *part_val;
+    int64_t *base, *tmp;
+    size_t bytes;
+};
+
+SpExp sp_exp_layout(int64_t T, int64_t tiles, int64_t R, int64_t NB, int backward, char *base) {
+    SpExp x{};
+    size_t off = 0;
+    auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
+    const int64_t T1 = T > 0 ? T : 1;
+    x.raw_dst = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
+    x.raw_val = (float *)take(sizeof(float) * (size_t)T1);
+    if (NB > 1) {
+        x.part_dst = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
+        x.part_val = (float *)take(sizeof(float) * (size_t)T1);
+        x.hist = (int32_t *)take(sizeof(int32_t) * (size_t)(tiles * NB > 0 ? tiles * NB : 1));
+        x.base = (int64_t *)take(sizeof(int64_t) * (size_t)(tiles * NB + 1));
+    }
+    x.out_count = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
+    int64_t mx = tiles * NB;
+    if (R * NB > mx) mx = R * NB;
+    x.tmp = (int64_t *)take(scan_tmp_bytes(mx + 1));
+    // last, so that every other offset is the same with and without it
+    if (NB > 1 && backward) x.part_raw = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
+    x.bytes = off;
+    return x;
+}
+
+int sp_check(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, const char *what) {
+    if (!ori || !inv || !h) return fl_fail(FL_ERR_ARG, "%s: null argument", what);
+    if (h->nnz < 0 || h->B < 0 || h->L < 0 || h->E < 0 || h->n < 1)
+        return fl_fail(FL_ERR_ARG, "%s: bad shape", what);
+    if (h->E >= INT32_MAX) return fl_fail(FL_ERR_ARG, "%s: E must be < 2^31", what);
+    if (h->r_size < 0 || 2 * h->r_size + 1 > h->n + (h->wot_i ? 1 : 0))
+        return fl_fail(FL_ERR_ARG, "%s: w width %lld too small for r_size %lld", what, (long long)h->n,
+                       (long long)h->r_size);
+    if (h->mode != SP_TOPK && h->mode != SP_ALL) return fl_fail(FL_ERR_ARG, "%s: unknown mode", what);
+    if (h->nnz > 0 && (!h->sp_b || !h->sp_l || !h->sp_e || !h->sp_v || !h->w))
+        return fl_fail(FL_ERR_ARG, "%s: null input", what);
+    for (const fl_side *s : {ori, inv})
+        if (s->edges > 0 && (!s->col_ind || !s->mask || !s->group_rel || !s->group_start || !s->group_count))
+            return fl_fail(FL_ERR_ARG, "%s: side without CSR arrays", what);
+    return FL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t fl_sparse_buckets(int64_t E) { return sp_buckets(E); }
+
+size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R) {
+    if (nnz < 0 || R < 0) return 0;
+    return sp_plan_layout(nnz, R, nullptr).bytes;
+}
+
+int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, int64_t *plan) {
+    int rc;
+    if ((rc = sp_check(ori, inv, h, "sparse_plan")) != FL_OK) return rc;
+    if (!plan || !h->ws1) return fl_fail(FL_ERR_ARG, "sparse_plan: null plan or workspace");
+    const int64_t R = h->B * h->L;
+    if (h->ws1_bytes < fl_sparse_plan_bytes(h->nnz, R)) return fl_fail(FL_ERR_ARG, "sparse_plan: workspace too small");
+    SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nnz = h->nnz;
+    // c2 budget: K > 0 selects, 0 keeps every eligible edge, < 0 keeps none
+    int64_t K = 0;
+    if (h->mode == SP_TOPK && h->topk_edges < ((int64_t)1 << 60)) K = h->topk_edges > 0 ? h->topk_edges : -1;
+    // plan[0] items, plan[1] tiles, plan[2] error, plan[3] buckets per row
+    FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, (int32_t *)plan, (int64_t)8, 0);
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr, R + 1,
+              (int64_t)0);
+    const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
+    FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, h->sp_b, h->sp_l,
+              h->sp_e, nnz, h->B, h->L, h->E, p.row_ptr, plan + 2);
+    if (nnz > 0)
+        FL_LAUNCH("k_sp_select", k_sp_select, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
+                  h->r_size, h->wot_i, h->mode, K, p.th, p.cut, p.cnt);
+    if ((rc = exclusive_scan(st, p.cnt, p.item_off, nnz, p.tmp)) != FL_OK) return rc;
+    FL_LAUNCH("k_sp_rowinfo", k_sp_rowinfo, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr,
+              p.item_off, R, p.row_item0, p.ntiles);
+    if ((rc = exclusive_scan(st, p.ntiles, p.tile_base, R, p.tmp)) != FL_OK) return rc;
+    FL_LAUNCH("k_sp_plan_out", k_sp_plan_out, dim3(1), dim3(1), 0, st, p.item_off + nnz, p.tile_base + R,
+              sp_buckets(h->E), plan);
+    return fl_check_launch("sparse_plan");
+}
+
+size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t R, int64_t E, int backward) {
+    if (items < 0 || tiles < 0 || R < 0) return 0;
+    return sp_exp_layout(items, tiles, R, sp_buckets(E), backward, nullptr).bytes;
+}
+
+int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h,
+                     int64_t *out_base, int32_t *raw_local) {
+    int rc;
+    if ((rc = sp_check(ori, inv, h, "sparse_expand")) != FL_OK) return rc;
+    const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
+    if (!h->ws1 || !h->ws2 || !out_base) return fl_fail(FL_ERR_ARG, "sparse_expand: null workspace or out_base");
+    if (h->items < 0 || h->tiles < 0) return fl_fail(FL_ERR_ARG, "sparse_expand: negative plan sizes");
+    if (h->ws2_bytes < fl_sparse_expand_bytes(h->items, h->tiles, R, h->E, raw_local != nullptr))
+        return fl_fail(FL_ERR_ARG, "sparse_expand: workspace too small");
+    SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
+    SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, raw_local != nullptr, (char *)h->ws2);
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nnz = h->nnz;
+    SpRows rows{p.row_item0, p.tile_base, NB};
+    if (NB > 1 && h->tiles * NB > 0)
+        FL_LAUNCH("k_fill_i32", k_fill_i32, dim3((unsigned)((h->tiles * NB + 255) / 256)), dim3(256), 0, st, x.hist,
+                  h->tiles * NB, 0);
+    if (nnz > 0)
+        FL_LAUNCH("k_sp_fill", k_sp_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n,
+                  h->r_size, h->wot_i, h->mode, p.th, p.cut, p.item_off, rows, x.hist, x.raw_dst, x.raw_val);
+    int32_t *dst_arr = x.raw_dst, *raw_arr = nullptr;
+    float *val_arr = x.raw_val;
+    if (NB > 1) {
+        if ((rc = exclusive_scan(st, x.hist, x.base, h->tiles * NB, x.tmp)) != FL_OK) return rc;
+        if (h->tiles > 0)
+            FL_LAUNCH("k_sp_partition", k_sp_partition, dim3((unsigned)h->tiles), dim3(SP_NT), 0, st, R, rows,
+                      sp_bucket_bits(NB), x.base, x.raw_dst, x.raw_val, x.part_dst, x.part_val,
+                      raw_local ? x.part_raw : (int32_t *)nullptr);
+        dst_arr = x.part_dst;
+        val_arr = x.part_val;
+        raw_arr = raw_local ? x.part_raw : nullptr;
+    }
+    if (R * NB > 0)
+        FL_LAUNCH("k_sp_accum", k_sp_accum, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
+                  val_arr, raw_arr, raw_local, x.out_count);
+    if ((rc = exclusive_scan(st, x.out_count, out_base, R * NB, x.tmp)) != FL_OK) return rc;
+    return fl_check_launch("sparse_expand");
+}
+
+int fl_sparse_emit(void *stream, const fl_sparse_hop *h, const int64_t *out_base, int64_t *out_b, int64_t *out_l,
+                   int64_t *out_e, float *out_v) {
+    if (!h || !out_base) return fl_fail(FL_ERR_ARG, "sparse_emit: null argument");
+    const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
+    if (R * NB == 0) return FL_OK;
+    SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
+    SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, 0, (char *)h->ws2);
+    SpRows rows{p.row_item0, p.tile_base, NB};
+    FL_LAUNCH("k_sp_emit", k_sp_emit, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, (hipStream_t)stream, rows, h->L,
+              x.base, NB > 1 ? x.part_dst : x.raw_dst, NB > 1 ? x.part_val : x.raw_val, out_base, out_b, out_l,
+              out_e, out_v);
+    return fl_check_launch("sparse_emit");
+}
+
+int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h,
+                       const int64_t *out_base, const int32_t *raw_local, const float *grad_out, float *grad_v,
+                       float *grad_w) {
+    int rc;
+    if ((rc = sp_check(ori, inv, h, "sparse_backward")) != FL_OK) return rc;
+    if (!h->ws1 || !out_base || !grad_v || !grad_w) return fl_fail(FL_ERR_ARG, "sparse_backward: null argument");
+    if (h->items > 0 && (!raw_local || !grad_out)) return fl_fail(FL_ERR_ARG, "sparse_backward: null raw map");
+    const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
+    SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
+    hipStream_t st = (hipStream_t)stream;
+    if (R * h->n > 0)
+        FL_LAUNCH("k_fill_f32", k_fill_f32, dim3((unsigned)((R * h->n + 255) / 256)), dim3(256), 0, st, grad_w,
+                  R * h->n, 0.0f);
+    if (h->nnz > 0)
+        FL_LAUNCH("k_sp_bwd", k_sp_bwd, dim3((unsigned)((h->nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, h->nnz, h->w, h->L, h->n,
+                  h->r_size, h->wot_i, h->mode, p.th, p.cut, p.item_off, NB, out_base, raw_local, grad_out, grad_v,
+                  grad_w);
+    return fl_check_launch("sparse_backward");
+}
+
+int fl_sparse_topc(void *stream, const int64_t *sp_b, const int64_t *sp_l, const float *v, int64_t nnz, int64_t B,
+                   int64_t L, int64_t c, int32_t *keep, int64_t *row_ptr, int64_t *err) {
+    if (c < 0) return fl_fail(FL_ERR_ARG, "topk_nodes/c must be nonnegative");
+    if (nnz < 0 || B < 0 || L < 0) return fl_fail(FL_ERR_ARG, "sparse_topc: negative size");
+    if (!row_ptr || !err || (nnz > 0 && (!sp_b || !sp_l || !v || !keep)))
+        return fl_fail(FL_ERR_ARG, "sparse_topc: null argument");
+    const int64_t R = B * L;
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, row_ptr, R + 1,
+              (int64_t)0);
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3(1), dim3(64), 0, st, err, (int64_t)1, (int64_t)0);
+    const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
+    FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, sp_b,
+              nnz, B, L, INT64_MAX, row_ptr, err);
+    if (R > 0 && nnz > 0)
+        FL_LAUNCH("k_sp_topc", k_sp_topc, dim3((unsigned)R), dim3(TOPC_NT), 0, st, row_ptr, v, c, keep);
+    return fl_check_launch("sparse_topc");
+}
+
+size_t fl_sparse_rowptr_bytes(int64_t R) { return al(sizeof(int64_t) * (size_t)(R + 1)) + al(sizeof(int64_t) * 2); }
+
+int fl_sparse_normalize_forward(void *stream, const int64_t *sp_b, const int64_t *sp_l, const float *v, int64_t nnz,
+                                int64_t B, int64_t L, float eps, float *out, float *denom, int64_t *row_ptr,
+                                int64_t *err) {
+    if (nnz < 0 || B < 0 || L < 0) return fl_fail(FL_ERR_ARG, "sparse_normalize: negative size");
+    if (!row_ptr || !err || (nnz > 0 && (!sp_b || !sp_l || !v || !out)) || (B * L > 0 && !denom))
+        return fl_fail(FL_ERR_ARG, "sparse_normalize: null argument");
+    const int64_t R = B * L;
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, row_ptr, R + 1,
+              (int64_t)0);
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3(1), dim3(64), 0, st, err, (int64_t)1, (int64_t)0);
+    // entity bounds are not needed here: E = INT64_MAX disables that check
+    const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
+    FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, sp_b,
+              nnz, B, L, INT64_MAX, row_ptr, err);
+    if (R > 0)
+        FL_LAUNCH("k_norm_fwd", k_norm_fwd, dim3((unsigned)R), dim3(NM_NT), 0, st, row_ptr, v, eps, out, denom);
+    return fl_check_launch("sparse_normalize");
+}
+
+int fl_sparse_normalize_backward(void *stream, const int64_t *row_ptr, const float *grad, const float *v,
+                                 const float *denom, int64_t R, float eps, float *grad_v) {
+    if (R < 0 || !row_ptr) return fl_fail(FL_ERR_ARG, "sparse_normalize_backward: bad arguments");
+    if (R > 0)
+        FL_LAUNCH("k_norm_bwd", k_norm_bwd, dim3((unsigned)R), dim3(NM_NT), 0, (hipStream_t)stream, row_ptr, grad,
+                  v, denom, eps, grad_v);
+    return fl_check_launch("sparse_normalize_backward");
+}
+
+}  // extern "C"

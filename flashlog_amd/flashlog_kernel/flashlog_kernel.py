@@ -21,7 +21,7 @@ import torch
 from torch import autograd
 
 from .. import _lib
-from .._lib import FlSide, check, ptr, stream_handle
+from .._lib import FlSide, FlSparseHop, check, ptr, stream_handle
 
 _FLASHLOG_CPU_THREADS_CONFIGURED = False
 
@@ -716,10 +716,6 @@ def vectorized_operation_sparse3d_fixed_relation(sp_state, operators, csr_struct
     _not_yet("vectorized_operation_sparse3d_fixed_relation")
 
 
-def normalize_sparse3d(s, eps=1e-7):
-    _not_yet("normalize_sparse3d")
-
-
 class FlashLogDenseMaxFunction(autograd.Function):
     """GPU dense max hop (flashlog_kernel.py:992-1089): per destination the
     largest kept (a*w)*m, ties to the smaller CSR position; the backward
@@ -787,18 +783,544 @@ def dense_csr_max(A, w, csr_struct, mask_values, r_size, weight=None, wot_i=Fals
         use_topk, topk_nodes, topk_edges)
 
 
-def vectorized_operation_sparse3d_csr_sum(sp_state, w, csr_struct, mask_values, r_size, weight=None,
-                                          wot_i=False, use_topk=False, topk_edges=0, prepared_masks=None,
-                                          topk_nodes=None, sampling=False):
-    _not_yet("vectorized_operation_sparse3d_csr_sum")
-
-
-def vectorized_operation_sparse3d_csr_sum_norm(sp_state, w, csr_struct, mask_values, r_size, weight=None,
-                                               wot_i=False, use_topk=False, topk_edges=0, prepared_masks=None,
-                                               eps=1e-7, topk_nodes=None, sampling=False):
-    _not_yet("vectorized_operation_sparse3d_csr_sum_norm")
-
-
 def sampled_sparse_propagation(state, w, csr_struct, mask_values, r_size, weight=None, wot_i=False,
                                topk_nodes=None, topk_edges=0, mode="sum"):
     _not_yet("sampled_sparse_propagation")
+
+
+# ---------------------------------------------------------------------------
+# Sparse (COO) propagation (flashlog_kernel.py:1092-1954): one hop expands
+# every entry of the state through its kept edges and coalesces per
+# (b, l, entity) in the CPU path's addition order (fl_sparse_* in
+# libflashlog_hip.so).
+
+_SPARSE_TOPK, _SPARSE_ALL = 0, 1
+
+
+class _SparseSides:
+    """FlSide views of the CSR arrays the sparse kernels read (no pull index)."""
+
+    def __init__(self, ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount,
+                 inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount):
+        self.keep = []
+        self.ori = self._side(ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount)
+        self.inv = self._side(inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount)
+
+    def _side(self, col, mask, gptr, grel, gstart, gcount):
+        _require_cuda(col, mask, gptr, grel, gstart, gcount)
+        col = col.int().contiguous()
+        mask = mask.float().contiguous()
+        gptr = gptr.int().contiguous()
+        grel = grel.short().contiguous()
+        gstart = gstart.int().contiguous()
+        gcount = gcount.int().contiguous()
+        if mask.numel() != col.numel():
+            raise ValueError("mask length must equal the number of CSR positions")
+        self.keep += [col, mask, gptr, grel, gstart, gcount]
+        side = FlSide()
+        side.edges, side.groups = col.numel(), grel.numel()
+        side.col_ind, side.mask = ptr(col).value, ptr(mask).value
+        side.row_group_ptr, side.group_rel = ptr(gptr).value, ptr(grel).value
+        side.group_start, side.group_count = ptr(gstart).value, ptr(gcount).value
+        side.max_rel = int(grel.max()) if grel.numel() else -1
+        return side
+
+
+class _SparseState:
+    """A forward hop's saved pieces for the backward."""
+
+
+def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mode, topk_edges,
+                    need_backward):
+    """Runs plan -> expand -> emit.  Returns (indices [3, nout], values, state)."""
+    _require_cuda(sp_b, sp_l, sp_e, sp_v, w)
+    dev = sp_v.device
+    B, L, E, r_size = int(B), int(L), int(E), int(r_size)
+    R = B * L
+    sp_b = sp_b.long().contiguous()
+    sp_l = sp_l.long().contiguous()
+    sp_e = sp_e.long().contiguous()
+    sp_v = sp_v.contiguous()
+    if sp_v.dtype != torch.float32:
+        raise TypeError("flashlog_amd sparse propagation computes in float32")
+    w_flat = w.reshape(R, -1).contiguous().float()
+    n = w_flat.shape[1]
+    if max(sides.ori.max_rel, sides.inv.max_rel) >= r_size or 2 * r_size > n:
+        raise ValueError("relation ids must be < r_size and w must hold 2*r_size (+1) columns")
+    nnz = sp_v.numel()
+    lib = _lib.lib()
+    st = _stream(sp_v)
+    perm = None
+    for attempt in range(2):
+        h = FlSparseHop()
+        h.sp_b, h.sp_l, h.sp_e, h.sp_v = (ptr(t).value for t in (sp_b, sp_l, sp_e, sp_v))
+        h.nnz, h.w = nnz, ptr(w_flat).value
+        h.B, h.L, h.E, h.n, h.r_size = B, L, E, n, r_size
+        h.wot_i, h.mode, h.topk_edges = 1 if wot_i else 0, int(mode), int(topk_edges)
+        ws1 = torch.empty(max(lib.fl_sparse_plan_bytes(nnz, R), 1), dtype=torch.uint8, device=dev)
+        h.ws1, h.ws1_bytes = ptr(ws1).value, ws1.numel()
+        plan = torch.empty(4, dtype=torch.int64, device=dev)
+        check(lib.fl_sparse_plan(st, ctypes.byref(sides.ori), ctypes.byref(sides.inv), ctypes.byref(h), ptr(plan)),
+              "sparse_plan")
+        items, tiles, err, nb = plan.tolist()
+        if err == 2 and attempt == 0:
+            # rows out of order: process them in row order, entries of a row in input order
+            perm = torch.argsort(sp_b * L + sp_l, stable=True)
+            sp_b, sp_l, sp_e, sp_v = sp_b[perm], sp_l[perm], sp_e[perm], sp_v[perm].contiguous()
+            continue
+        if err:
+            raise ValueError("sparse state index out of range for shape (%d, %d, %d)" % (B, L, E))
+        break
+    h.items, h.tiles = items, tiles
+    ws2_bytes = lib.fl_sparse_expand_bytes(items, tiles, R, E, 1 if need_backward else 0)
+    ws2 = torch.empty(max(ws2_bytes, 1), dtype=torch.uint8, device=dev)
+    h.ws2, h.ws2_bytes = ptr(ws2).value, ws2.numel()
+    out_base = torch.empty(R * nb + 1, dtype=torch.int64, device=dev)
+    raw_local = torch.empty(max(items, 1), dtype=torch.int32, device=dev) if need_backward else None
+    check(lib.fl_sparse_expand(st, ctypes.byref(sides.ori), ctypes.byref(sides.inv), ctypes.byref(h),
+                               ptr(out_base), ptr(raw_local) if need_backward else None), "sparse_expand")
+    nout = int(out_base[-1])
+    idx = torch.empty((3, nout), dtype=torch.int64, device=dev)
+    vals = torch.empty(nout, dtype=torch.float32, device=dev)
+    check(lib.fl_sparse_emit(st, ctypes.byref(h), ptr(out_base), ptr(idx[0]), ptr(idx[1]), ptr(idx[2]),
+                             ptr(vals)), "sparse_emit")
+    state = None
+    if need_backward:
+        state = _SparseState()
+        state.h, state.sides, state.perm = h, sides, perm
+        state.keep = (sp_b, sp_l, sp_e, sp_v, w_flat, ws1, out_base, raw_local)
+        state.out_base, state.raw_local, state.nout, state.n = out_base, raw_local, nout, n
+    del ws2
+    return idx, vals, state
+
+
+def _sparse_backward(state, grad_values):
+    """grad_values: gradient of every output entry.  Returns (grad_v, grad_w [R, n])."""
+    h = state.h
+    dev = grad_values.device
+    grad_values = grad_values.contiguous().float()
+    gv = torch.empty(max(h.nnz, 1), dtype=torch.float32, device=dev)
+    gw = torch.empty((h.B * h.L, state.n), dtype=torch.float32, device=dev)
+    check(_lib.lib().fl_sparse_backward(_stream(grad_values), ctypes.byref(state.sides.ori),
+                                        ctypes.byref(state.sides.inv), ctypes.byref(h), ptr(state.out_base),
+                                        ptr(state.raw_local), ptr(grad_values), ptr(gv), ptr(gw)),
+          "sparse_backward")
+    gv = gv[:h.nnz]
+    if state.perm is not None:
+        restored = torch.empty_like(gv)
+        restored[state.perm] = gv
+        gv = restored
+    return gv, gw
+
+
+def _align_sparse_grad_to_output(grad, out_indices, L, E):
+    """Gradient values at the output coordinates (flashlog_kernel.py:360-376)."""
+    if not grad.is_sparse:
+        return grad[tuple(out_indices)].contiguous()
+    grad = grad.coalesce()
+    if torch.equal(grad.indices(), out_indices):
+        return grad.values().contiguous()
+    keys = out_indices[0] * (L * E) + out_indices[1] * E + out_indices[2]
+    gidx = grad.indices()
+    gkeys = gidx[0] * (L * E) + gidx[1] * E + gidx[2]
+    values = torch.zeros(keys.numel(), device=grad.device, dtype=grad.dtype)
+    if gkeys.numel() and keys.numel():
+        pos = torch.searchsorted(gkeys, keys)
+        safe = pos.clamp(max=gkeys.numel() - 1)
+        valid = (pos < gkeys.numel()) & (gkeys[safe] == keys)
+        values[valid] = grad.values()[safe[valid]]
+    return values
+
+
+def _sparse_rows_scratch(R, device):
+    return (torch.empty(R + 1, dtype=torch.int64, device=device),
+            torch.empty(1, dtype=torch.int64, device=device))
+
+
+@torch.no_grad()
+def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, num_rules, sampling=False):
+    """Kept entries of the c1 budget per (item, rule) row of a coalesced state
+    (flashlog_kernel.py:1092-1140), or None when nothing is pruned."""
+    if topk_nodes is None:
+        return None
+    if topk_nodes < 0:
+        raise ValueError("topk_nodes/c must be nonnegative")
+    if sampling:
+        raise NotImplementedError("sampled (exponential race) entity selection is not in this build yet")
+    if sp_entity.numel() <= topk_nodes:
+        return None
+    _require_cuda(sp_batch, sp_level, sp_value)
+    L = int(num_rules)
+    B = int(sp_batch.max()) + 1 if sp_batch.numel() else 0
+    sp_batch = sp_batch.long().contiguous()
+    sp_level = sp_level.long().contiguous()
+    sp_value = sp_value.contiguous().float()
+    keep = torch.empty(sp_value.numel(), dtype=torch.int32, device=sp_value.device)
+    row_ptr, err = _sparse_rows_scratch(B * L, sp_value.device)
+    check(_lib.lib().fl_sparse_topc(_stream(sp_value), ptr(sp_batch), ptr(sp_level), ptr(sp_value),
+                                    sp_value.numel(), B, L, int(topk_nodes), ptr(keep), ptr(row_ptr), ptr(err)),
+          "sparse_topc")
+    if int(err) != 0:
+        raise ValueError("sparse c1 needs a state coalesced by (batch, rule, entity)")
+    if bool(keep.all()):
+        return None
+    return torch.nonzero(keep, as_tuple=True)[0]
+
+
+def _prune_sparse_sources(ctx, batch, level, entity, value, topk_nodes, num_rules, sampling=False):
+    """Select one common input for fact and identity propagation."""
+    entries = _sparse_topc_entries(batch, level, entity, value, topk_nodes, num_rules, sampling)
+    ctx.pruned_entries = entries
+    ctx.original_input_size = value.numel()
+    if entries is None:
+        return batch, level, entity, value
+    return batch[entries], level[entries], entity[entries], value[entries]
+
+
+def _restore_pruned_gradient(ctx, gradient):
+    if ctx.pruned_entries is None:
+        return gradient
+    restored = gradient.new_zeros(ctx.original_input_size)
+    restored[ctx.pruned_entries] = gradient
+    return restored
+
+
+def _coo(idx, vals, B, L, E):
+    return torch.sparse_coo_tensor(idx, vals, [B, L, E], is_coalesced=True)
+
+
+class FlashLogFunctionSparse3DAllEdgesSum(autograd.Function):
+    """Sparse sum hop over every edge, masked ones included as 0-valued
+    coordinates (flashlog_kernel.py:1351-1447)."""
+
+    @staticmethod
+    def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, w,
+                ori_col_ind, ori_mask,
+                ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                inv_col_ind, inv_mask,
+                inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                B, L, E, r_size, wot_i, cache_backward=True):
+        sides = _SparseSides(ori_col_ind, ori_mask, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                             ori_group_edge_count, inv_col_ind, inv_mask, inv_row_group_ptr, inv_group_rel,
+                             inv_group_edge_start, inv_group_edge_count)
+        need = bool(any(ctx.needs_input_grad))
+        idx, vals, state = _sparse_forward(sp_batch, sp_level, sp_entity, sp_value, w, sides, B, L, E, r_size,
+                                           wot_i, _SPARSE_ALL, 0, need)
+        ctx.state, ctx.out_indices, ctx.dims = state, idx, (int(B), int(L), int(E), tuple(w.shape))
+        return _coo(idx, vals, int(B), int(L), int(E))
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        B, L, E, wshape = ctx.dims
+        aligned = _align_sparse_grad_to_output(grad_out, ctx.out_indices, L, E)
+        gv, gw = _sparse_backward(ctx.state, aligned)
+        grads = (None, None, None, gv, gw.view(wshape)) + (None,) * 17
+        return (grads + (None,))[:len(ctx.needs_input_grad)]
+
+
+class FlashLogFunctionSparse3DTopKSum(autograd.Function):
+    """Sparse sum hop with the c1 entity budget and the c2 edge budget
+    (flashlog_kernel.py:1158-1348): hard-masked edges take part in the c2
+    selection but produce no coordinate."""
+
+    @staticmethod
+    def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, w,
+                ori_row_ptr, ori_col_ind, ori_r_ind, ori_order,
+                inv_row_ptr, inv_col_ind, inv_r_ind, inv_order,
+                ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                mask_values, weight, B, L, E, r_size, wot_i, topk_edges,
+                edge_weight_is_score=False, topk_nodes=None, cache_backward=True, sampling=False):
+        if sampling:
+            raise NotImplementedError("sampled quotas (training --use_topk) are not in this build yet")
+        if weight is not None and bool(getattr(weight, "requires_grad", False)):
+            raise NotImplementedError("trainable edge weights on the sparse top-k path are not in this build yet")
+        _require_cuda(sp_value, w)
+        if not bool(torch.isfinite(w).all()):
+            raise RuntimeError("FlashLog sparse top-k received non-finite attention weights")
+        sp_batch, sp_level, sp_entity, sp_value = _prune_sparse_sources(
+            ctx, sp_batch, sp_level, sp_entity, sp_value, topk_nodes, w.size(1), sampling)
+        mask_f = mask_values.contiguous().view(-1)
+        if weight is not None and edge_weight_is_score:
+            m = mask_f.float() * weight.to(device=mask_f.device, dtype=torch.float).view(-1)
+            ori_mask = m[ori_order.long()].contiguous()
+            inv_mask = m[inv_order.long()].contiguous()
+        else:
+            ori_mask = _apply_mask_order(mask_f, ori_order, weight)
+            inv_mask = _apply_mask_order(mask_f, inv_order, weight)
+        sides = _SparseSides(ori_col_ind, ori_mask, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                             ori_group_edge_count, inv_col_ind, inv_mask, inv_row_group_ptr, inv_group_rel,
+                             inv_group_edge_start, inv_group_edge_count)
+        K = int(topk_edges)
+        need = bool(any(ctx.needs_input_grad))
+        idx, vals, state = _sparse_forward(sp_batch, sp_level, sp_entity, sp_value, w, sides, B, L, E, r_size,
+                                           wot_i, _SPARSE_TOPK, K, need)
+        ctx.state, ctx.out_indices, ctx.dims = state, idx, (int(B), int(L), int(E), tuple(w.shape))
+        return _coo(idx, vals, int(B), int(L), int(E))
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        B, L, E, wshape = ctx.dims
+        aligned = _align_sparse_grad_to_output(grad_out, ctx.out_indices, L, E)
+        gv, gw = _sparse_backward(ctx.state, aligned)
+        gv = _restore_pruned_gradient(ctx, gv)
+        grads = (None, None, None, gv, gw.view(wshape)) + (None,) * 28
+        return grads[:len(ctx.needs_input_grad)]
+
+
+class _SparseCpuPath:
+    """The reference's CPU sparse classes, run on the GPU: inputs and outputs
+    stay CPU tensors, the hop is the same fl_sparse_* pipeline (mode 0 with
+    the given c2 budget, i.e. the CPU path's kept-edge semantics)."""
+
+    @staticmethod
+    def run(ctx, sp_batch, sp_level, sp_entity, sp_value, w, side_args, B, L, E, r_size, wot_i, topk_edges):
+        if not torch.cuda.is_available():
+            raise RuntimeError("flashlog_amd runs its sparse kernels on the GPU; no GPU is visible")
+        dev = torch.device("cuda")
+        g = [t.to(dev) for t in side_args]
+        sides = _SparseSides(*g)
+        K = int(topk_edges)
+        need = bool(any(ctx.needs_input_grad))
+        idx, vals, state = _sparse_forward(sp_batch.to(dev), sp_level.to(dev), sp_entity.to(dev),
+                                           sp_value.to(dev).float(), w.to(dev), sides, B, L, E, r_size, wot_i,
+                                           _SPARSE_TOPK, K, need)
+        ctx.state, ctx.out_indices, ctx.dims = state, idx, (int(B), int(L), int(E), tuple(w.shape))
+        return idx, vals
+
+
+class FlashLogFunctionSparse3DCPUSum(autograd.Function):
+    """flashlog_kernel.py:1691-1744 with CPU tensors in and out."""
+
+    @staticmethod
+    def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, w,
+                ori_col_ind, ori_mask,
+                ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                inv_col_ind, inv_mask,
+                inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                B, L, E, r_size, wot_i, topk_edges):
+        idx, vals = _SparseCpuPath.run(
+            ctx, sp_batch, sp_level, sp_entity, sp_value, w,
+            (ori_col_ind, ori_mask, ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+             inv_col_ind, inv_mask, inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count),
+            B, L, E, r_size, wot_i, topk_edges)
+        ctx.home = sp_value.device
+        return _coo(idx.to(ctx.home), vals.to(ctx.home, sp_value.dtype), int(B), int(L), int(E))
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        B, L, E, wshape = ctx.dims
+        dev = ctx.out_indices.device
+        aligned = _align_sparse_grad_to_output(grad_out.to(dev), ctx.out_indices, L, E)
+        gv, gw = _sparse_backward(ctx.state, aligned)
+        return (None, None, None, gv.to(ctx.home), gw.view(wshape).to(ctx.home)) + (None,) * 18
+
+
+class FlashLogFunctionSparse3DCPUSumNorm(autograd.Function):
+    """flashlog_kernel.py:1747-1811 with CPU tensors in and out: the sum hop,
+    then the per-row normalization."""
+
+    @staticmethod
+    def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, w,
+                ori_col_ind, ori_mask,
+                ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                inv_col_ind, inv_mask,
+                inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                B, L, E, r_size, wot_i, topk_edges, eps):
+        idx, vals = _SparseCpuPath.run(
+            ctx, sp_batch, sp_level, sp_entity, sp_value, w,
+            (ori_col_ind, ori_mask, ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+             inv_col_ind, inv_mask, inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count),
+            B, L, E, r_size, wot_i, topk_edges)
+        out, denom, row_ptr = _normalize_forward(idx[0], idx[1], vals, int(B), int(L), float(eps))
+        ctx.norm = (vals, denom, row_ptr, float(eps))
+        ctx.home = sp_value.device
+        return _coo(idx.to(ctx.home), out.to(ctx.home, sp_value.dtype), int(B), int(L), int(E))
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        B, L, E, wshape = ctx.dims
+        dev = ctx.out_indices.device
+        vals, denom, row_ptr, eps = ctx.norm
+        aligned = _align_sparse_grad_to_output(grad_out.to(dev), ctx.out_indices, L, E)
+        g_sum = _normalize_backward(row_ptr, aligned, vals, denom, eps)
+        gv, gw = _sparse_backward(ctx.state, g_sum)
+        return (None, None, None, gv.to(ctx.home), gw.view(wshape).to(ctx.home)) + (None,) * 19
+
+
+def _normalize_forward(sp_b, sp_l, values, B, L, eps):
+    _require_cuda(sp_b, sp_l, values)
+    values = values.contiguous().float()
+    R = B * L
+    out = torch.empty_like(values)
+    denom = torch.empty(max(R, 1), dtype=torch.float32, device=values.device)
+    row_ptr, err = _sparse_rows_scratch(R, values.device)
+    check(_lib.lib().fl_sparse_normalize_forward(_stream(values), ptr(sp_b.long().contiguous()),
+                                                 ptr(sp_l.long().contiguous()), ptr(values), values.numel(),
+                                                 B, L, ctypes.c_float(eps), ptr(out), ptr(denom), ptr(row_ptr),
+                                                 ptr(err)), "sparse_normalize")
+    if int(err) != 0:
+        raise ValueError("normalize_sparse3d needs a state coalesced by (batch, rule, entity)")
+    return out, denom[:R], row_ptr
+
+
+def _normalize_backward(row_ptr, grad, values, denom, eps):
+    grad = grad.contiguous().float()
+    gv = torch.empty_like(values)
+    check(_lib.lib().fl_sparse_normalize_backward(_stream(values), ptr(row_ptr), ptr(grad), ptr(values),
+                                                  ptr(denom), denom.numel(), ctypes.c_float(eps), ptr(gv)),
+          "sparse_normalize_backward")
+    return gv
+
+
+class Sparse3DNormalizeFunction(autograd.Function):
+    """Per (b, l) row: v / max(sum of the row, eps) (flashlog_kernel.py:536-606)."""
+
+    @staticmethod
+    def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, B, L, E, eps):
+        sp_batch = sp_batch.contiguous().long()
+        sp_level = sp_level.contiguous().long()
+        sp_entity = sp_entity.contiguous().long()
+        values = sp_value.contiguous()
+        out, denom, row_ptr = _normalize_forward(sp_batch, sp_level, values, int(B), int(L), float(eps))
+        ctx.save_for_backward(sp_batch, sp_level, sp_entity, values.float(), denom, row_ptr)
+        ctx.B, ctx.L, ctx.E, ctx.eps = int(B), int(L), int(E), float(eps)
+        idx = torch.stack([sp_batch, sp_level, sp_entity], dim=0)
+        return torch.sparse_coo_tensor(idx, out.to(sp_value.dtype), [int(B), int(L), int(E)], is_coalesced=True)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        sp_batch, sp_level, sp_entity, values, denom, row_ptr = ctx.saved_tensors
+        if getattr(grad_out, "is_sparse", False):
+            g = _align_sparse_grad_to_output(grad_out, torch.stack([sp_batch, sp_level, sp_entity]), ctx.L, ctx.E)
+        else:
+            g = grad_out[sp_batch, sp_level, sp_entity]
+        gv = _normalize_backward(row_ptr, g, values, denom, ctx.eps)
+        return None, None, None, gv, None, None, None, None
+
+
+def normalize_sparse3d(s, eps=1e-7):
+    s = s if s.is_coalesced() else s.coalesce()
+    idx = s.indices()
+    B, L, E = s.shape
+    return Sparse3DNormalizeFunction.apply(idx[0], idx[1], idx[2], s.values(), B, L, E, eps)
+
+
+def _sparse_sum_selected_nodes(sp_state, entries, w, csr_struct, mask_values,
+                               r_size, weight, wot_i, topk_edges, prepared_masks):
+    idx, val = sp_state.indices(), sp_state.values()
+    selected = torch.sparse_coo_tensor(idx[:, entries], val[entries], sp_state.shape, is_coalesced=True)
+    return vectorized_operation_sparse3d_csr_sum(
+        selected, w, csr_struct, mask_values, r_size, weight=weight,
+        wot_i=wot_i, use_topk=True, topk_edges=topk_edges, prepared_masks=prepared_masks)
+
+
+def vectorized_operation_sparse3d_csr_sum(sp_state, w, csr_struct, mask_values,
+                                          r_size, weight=None, wot_i=False,
+                                          use_topk=False, topk_edges=0,
+                                          prepared_masks=None, topk_nodes=None, sampling=False):
+    """Sparse sum dispatcher (flashlog_kernel.py:1814-1888)."""
+    if sampling and use_topk:
+        return sampled_sparse_propagation(sp_state, w, csr_struct, mask_values, r_size,
+                                          weight, wot_i, topk_nodes, topk_edges, "sum")
+    sp_state = sp_state.coalesce()
+    idx = sp_state.indices()
+    val = sp_state.values()
+    B, L, E = sp_state.shape
+    (ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
+     inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
+     ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+     inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count) = csr_struct
+    effective_topk = topk_edges if (use_topk and topk_edges > 0) else (1 << 60)
+    if sp_state.is_cuda:
+        can_use_all_edges = not (use_topk and (topk_edges > 0 or topk_nodes is not None))
+        can_use_all_edges = can_use_all_edges and not (
+            weight is not None and bool(getattr(weight, "requires_grad", False)))
+        if can_use_all_edges:
+            prepared = (_prepared_mask_pair(prepared_masks) if prepared_masks is not None
+                        else _prepared_mask_pair(mask_values))
+            if prepared is not None:
+                ori_mask, inv_mask = prepared
+            else:
+                ori_mask, inv_mask = prepare_csr_masks(csr_struct, mask_values, weight)
+            return FlashLogFunctionSparse3DAllEdgesSum.apply(
+                idx[0], idx[1], idx[2], val, w,
+                ori_col_ind, ori_mask,
+                ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                inv_col_ind, inv_mask,
+                inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                B, L, E, r_size, wot_i, torch.is_grad_enabled())
+        return FlashLogFunctionSparse3DTopKSum.apply(
+            idx[0], idx[1], idx[2], val, w,
+            ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
+            inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
+            ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+            inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+            mask_values, weight, B, L, E, r_size, wot_i, effective_topk,
+            False, topk_nodes if use_topk else None, torch.is_grad_enabled())
+    # CPU tensors: the reference's CPU path semantics, computed on the GPU
+    if use_topk and topk_nodes is not None:
+        dev = torch.device("cuda")
+        entries = _sparse_topc_entries(idx[0].to(dev), idx[1].to(dev), idx[2].to(dev), val.to(dev),
+                                       topk_nodes, L)
+        if entries is not None:
+            return _sparse_sum_selected_nodes(sp_state, entries.cpu(), w, csr_struct, mask_values, r_size,
+                                              weight, wot_i, topk_edges, prepared_masks)
+    prepared = _prepared_mask_pair(prepared_masks) if prepared_masks is not None else None
+    if prepared is not None:
+        ori_mask, inv_mask = prepared
+    else:
+        dev = torch.device("cuda")
+        ori_mask, inv_mask = prepare_csr_masks(tuple(t.to(dev) for t in csr_struct), mask_values.to(dev),
+                                               None if weight is None else weight.to(dev))
+    return FlashLogFunctionSparse3DCPUSum.apply(
+        idx[0], idx[1], idx[2], val, w,
+        ori_col_ind, ori_mask,
+        ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+        inv_col_ind, inv_mask,
+        inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+        B, L, E, r_size, wot_i, effective_topk)
+
+
+def vectorized_operation_sparse3d_csr_sum_norm(sp_state, w, csr_struct, mask_values,
+                                               r_size, weight=None, wot_i=False,
+                                               use_topk=False, topk_edges=0,
+                                               prepared_masks=None, eps=1e-7, topk_nodes=None, sampling=False):
+    """Sparse sum + per-row normalization dispatcher (flashlog_kernel.py:1901-1954)."""
+    if sampling and use_topk:
+        return normalize_sparse3d(sampled_sparse_propagation(sp_state, w, csr_struct, mask_values, r_size,
+                                                             weight, wot_i, topk_nodes, topk_edges, "sum"), eps=eps)
+    if sp_state.is_cuda:
+        return normalize_sparse3d(
+            vectorized_operation_sparse3d_csr_sum(
+                sp_state, w, csr_struct, mask_values, r_size, weight=weight, wot_i=wot_i,
+                use_topk=use_topk, topk_edges=topk_edges, prepared_masks=prepared_masks,
+                topk_nodes=topk_nodes),
+            eps=eps)
+    sp_state = sp_state.coalesce()
+    idx = sp_state.indices()
+    val = sp_state.values()
+    B, L, E = sp_state.shape
+    if use_topk and topk_nodes is not None:
+        dev = torch.device("cuda")
+        entries = _sparse_topc_entries(idx[0].to(dev), idx[1].to(dev), idx[2].to(dev), val.to(dev),
+                                       topk_nodes, L)
+        if entries is not None:
+            return normalize_sparse3d(_sparse_sum_selected_nodes(
+                sp_state, entries.cpu(), w, csr_struct, mask_values, r_size,
+                weight, wot_i, topk_edges, prepared_masks), eps=eps)
+    effective_topk = topk_edges if (use_topk and topk_edges > 0) else (1 << 60)
+    prepared = _prepared_mask_pair(prepared_masks) if prepared_masks is not None else None
+    if prepared is not None:
+        ori_mask, inv_mask = prepared
+    else:
+        dev = torch.device("cuda")
+        ori_mask, inv_mask = prepare_csr_masks(tuple(t.to(dev) for t in csr_struct), mask_values.to(dev),
+                                               None if weight is None else weight.to(dev))
+    return FlashLogFunctionSparse3DCPUSumNorm.apply(
+        idx[0], idx[1], idx[2], val, w,
+        csr_struct[1], ori_mask,
+        csr_struct[8], csr_struct[9], csr_struct[10], csr_struct[11],
+        csr_struct[5], inv_mask,
+        csr_struct[12], csr_struct[13], csr_struct[14], csr_struct[15],
+        B, L, E, r_size, wot_i, effective_topk, eps)

@@ -203,6 +203,110 @@ int fl_dense_max_backward(void *stream, const fl_side *ori, const fl_side *inv,
                           int64_t n, int64_t r_size, int wot_i, float *grad_A,
                           float *grad_w);
 
+/* ---- sparse (COO) hop ------------------------------------------------- */
+
+/* One sparse hop: the COO state (entries sorted by row r = b*L + l, as a
+ * coalesced state is), attention w [B*L, n], and the caller's workspaces.
+ * mode 0 = top-k sum (kept edges with a nonzero mask; FlashLogFunction-
+ * Sparse3DTopKSum, flashlog.cu:1368-1559), mode 1 = all edges
+ * (FlashLogFunctionSparse3DAllEdgesSum, flashlog.cu:1743-1829).  items /
+ * tiles come from fl_sparse_plan's plan[0] / plan[1]. */
+typedef struct fl_sparse_hop {
+    const int64_t *sp_b, *sp_l, *sp_e;  /* [nnz] */
+    const float *sp_v;                 /* [nnz] */
+    int64_t nnz;
+    const float *w;                    /* [B*L, n] */
+    int64_t B, L, E, n, r_size;
+    int wot_i;
+    int mode;
+    int64_t topk_edges;                /* c2 budget K (mode 0): K >= 2^60 keeps
+                                          every eligible edge, 0 < K selects,
+                                          K <= 0 keeps none (the reference's
+                                          min(eligible, K) count)            */
+    void *ws1;                         /* plan workspace */
+    size_t ws1_bytes;
+    void *ws2;                         /* expansion workspace */
+    size_t ws2_bytes;
+    int64_t items, tiles;
+} fl_sparse_hop;
+
+/* Destination buckets per row (8192 entities each). */
+int64_t fl_sparse_buckets(int64_t E);
+
+/* Plan workspace bytes for nnz entries and R = B*L rows. */
+size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R);
+
+/* Replaces the count kernels and the host .item() syncs of
+ * flashlog_forward_sparse3d_topk_cuda / _alledges_cuda (flashlog.cu:
+ * 1999-2241): per entry and side the c2 threshold (flashlog.cpp:12-35) and
+ * item counts; plan (device int64[4]) receives {items, tiles, error,
+ * buckets}.  error: 0 ok, 1 index out of range, 2 entries not sorted by row.
+ * The caller reads plan after the stream completes. */
+int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv,
+                   const fl_sparse_hop *h, int64_t *plan);
+
+/* Expansion workspace bytes (backward = 1 when raw_local will be kept). */
+size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t R,
+                              int64_t E, int backward);
+
+/* Replaces the fill kernels (flashlog.cu:1402-1559,1759-1854) and the
+ * coalesce (flashlog_kernel.py:258-357): raw items in the CPU path's order
+ * (flashlog.cpp:1388-1486), grouped per (row, destination) and added to 0 in
+ * that order.  out_base [B*L*buckets + 1] receives the output offsets of
+ * every (row, bucket) (out_base[last] = output count); raw_local (optional,
+ * [items]) the output index of every raw item within its bucket, for
+ * fl_sparse_backward. */
+int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv,
+                     const fl_sparse_hop *h, int64_t *out_base,
+                     int32_t *raw_local);
+
+/* Writes the coalesced output (ascending (b, l, e)); arrays hold
+ * out_base[last] entries. */
+int fl_sparse_emit(void *stream, const fl_sparse_hop *h,
+                   const int64_t *out_base, int64_t *out_b, int64_t *out_l,
+                   int64_t *out_e, float *out_v);
+
+/* Replaces flashlog_backward_sparse3d_cached_cuda (flashlog.cu:2243-2478,
+ * kernels :1856-1997): grad_v[i] = sum over entry i's items of (g*m)*w
+ * (+ g*w[n-1] for the identity item); grad_w [B*L, n] accumulates (g*m)*a
+ * (+ g*a at n-1).  grad_out holds the gradient of every output entry.
+ * Needs the plan workspace of the forward. */
+int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv,
+                       const fl_sparse_hop *h, const int64_t *out_base,
+                       const int32_t *raw_local, const float *grad_out,
+                       float *grad_v, float *grad_w);
+
+/* Replaces _sparse_topc_entries (flashlog_kernel.py:1092-1140), the c1
+ * budget on a COO state sorted by row: keep[i] = 1 for the entries to keep.
+ * Rows with more than c nonzeros keep their c largest nonzeros (ties to the
+ * earlier entry); other rows keep every entry.  row_ptr [B*L+1] and err [1]
+ * are caller scratch as for fl_sparse_normalize_forward. */
+int fl_sparse_topc(void *stream, const int64_t *sp_b, const int64_t *sp_l,
+                   const float *v, int64_t nnz, int64_t B, int64_t L,
+                   int64_t c, int32_t *keep, int64_t *row_ptr, int64_t *err);
+
+/* Bytes of the row pointer + error slots used by the normalize calls. */
+size_t fl_sparse_rowptr_bytes(int64_t R);
+
+/* Replaces sparse3d_normalize_forward_cuda (flashlog.cu:2480-2640):
+ * per row r = b*L + l, denom[r] = sum of its values (fixed tree order) and
+ * out = v / max(denom, eps).  Entries sorted by row; row_ptr [R+1] and
+ * err [1] are caller scratch (err != 0 after the call: unsorted or out of
+ * range input). */
+int fl_sparse_normalize_forward(void *stream, const int64_t *sp_b,
+                                const int64_t *sp_l, const float *v,
+                                int64_t nnz, int64_t B, int64_t L, float eps,
+                                float *out, float *denom, int64_t *row_ptr,
+                                int64_t *err);
+
+/* Replaces sparse3d_normalize_backward_cuda (flashlog.cu:2642-2691):
+ * grad_v = g/dc - sum_row(g*v)/dc^2 where denom >= eps (dc = max(denom,
+ * eps)), else g/dc. */
+int fl_sparse_normalize_backward(void *stream, const int64_t *row_ptr,
+                                 const float *grad, const float *v,
+                                 const float *denom, int64_t R, float eps,
+                                 float *grad_v);
+
 /* ---- evaluation --------------------------------------------------------- */
 
 /* Workspace for fl_filtered_ranks (values_f64: 1 for double scores). */

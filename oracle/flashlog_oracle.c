@@ -17,6 +17,10 @@
  *   or_dense_max_forward     flashlog_kernel/source/flashlog.cu:104-121,523-637
  *   or_dense_max_backward    flashlog_kernel/source/flashlog.cu:639-726,1187-1255
  *   or_filtered_ranks        flashlog_kernel/source/flashlog.cu:2754-2910
+ *   or_sparse_forward        flashlog_kernel/source/flashlog.cpp:1388-1486 (mode 0),
+ *                            flashlog.cu:1743-1854 coordinates (mode 1)
+ *   or_sparse_backward       flashlog_kernel/source/flashlog.cu:1856-1959
+ *   or_sparse_normalize      flashlog_kernel/flashlog_kernel.py:551-555
  *
  * Pinning (how each function is checked, see tests/test_oracle_*.py):
  *   or_build_side, or_dense_forward, or_dense_backward: bit-compared against
@@ -28,6 +32,11 @@
  *   or_dense_max_backward: float64 brute force over the expanded edge list
  *     (each winner edge's partial derivatives), and finite differences.
  *   or_filtered_ranks: brute-force count over a dense score row.
+ *   or_sparse_forward: bit-compared with the reference's flashlog_forward_sparse3d_sum_cpu
+ *     (oracle/_ref) in mode 0 and, where the modes coincide, in mode 1; float64
+ *     closed form over the expanded edge list.
+ *   or_sparse_backward: float64 adjoint of the closed form.
+ *   or_sparse_normalize: closed form.
  *
  * Compile with -O2 -ffp-contract=off (no FMA contraction: the reference's
  * CPU build is ISO C++17 on x86-64 without -march, so it never fuses a*b+c).
@@ -36,6 +45,13 @@
 #include <stdlib.h>
 #include <string.h>
 #include <math.h>
+
+static int64_t or_lower_bound(const int64_t *a, int64_t n, int64_t key)
+{
+    int64_t lo = 0, hi = n;
+    while (lo < hi) { int64_t mid = lo + (hi - lo) / 2; if (a[mid] < key) lo = mid + 1; else hi = mid; }
+    return lo;
+}
 
 /* ------------------------------------------------------------------------ */
 /* CSR side builder: csr.cpp:12-69.  Positions are ordered by (source,
@@ -493,6 +509,182 @@ void or_dense_max_backward(int64_t BL, int64_t E, int64_t n, const float *A, con
 }
 
 /* ------------------------------------------------------------------------ */
+/* Sparse (COO) sum hop.
+ * mode 0 (top-k): flashlog.cpp:1388-1486 (rowwise branch of the CPU sum and
+ *   sum+norm paths): rows in order; per row its entries in input order; per
+ *   entry ORI kept edges with a nonzero mask (CSR order), then INV, then the
+ *   identity term (unless wot_i); a destination's first contribution is
+ *   added to 0.  value = (v * w) * m; identity = v * w[n-1].
+ * mode 1 (all edges): flashlog.cu:1743-1854 coordinates (every edge of every
+ *   group, masked or not, any weight, plus identity) added in the same order.
+ * Output: keys row*E + e ascending with their values; returns the count, or
+ * -1 when cap is too small.                                                 */
+typedef struct {
+    const int32_t *col; const float *mask; const int32_t *gptr; const int16_t *grel;
+    const int32_t *gstart; const int32_t *gcount;
+} or_side_t;
+
+typedef void (*or_item_fn)(void *ctx, int64_t entry, int dir, int64_t p, int64_t dst, int rel, float m,
+                           float value);
+
+/* Walks the items of one entry in raw order; the identity item has dir 2. */
+static void or_sparse_walk(int mode, int64_t i, const int64_t *sb, const int64_t *sl, const int64_t *se,
+                           const float *sv, int64_t L, const float *w, int64_t n, const or_side_t *sides,
+                           int64_t r_size, int wot_i, int64_t topk_edges, or_item_fn fn, void *ctx)
+{
+    int64_t row = sb[i] * L + sl[i], src = se[i];
+    const float *w_bl = w + row * n;
+    for (int dir = 0; dir < 2; ++dir) {
+        const or_side_t *sd = &sides[dir];
+        int64_t off = dir ? r_size : 0;
+        int64_t g0 = sd->gptr[src], g1 = sd->gptr[src + 1];
+        if (g0 == g1) continue;
+        int64_t keep_in_threshold = 0;
+        float threshold_weight = -1.0f;
+        if (mode == 0)
+            threshold_weight = or_group_threshold_f32(w_bl + off, sd->grel, sd->gcount, g0, g1, topk_edges,
+                                                      &keep_in_threshold);
+        int64_t threshold_seen = 0;
+        for (int64_t g = g0; g < g1; ++g) {
+            int32_t *group_edge_count = (int32_t *)sd->gcount;
+            float w_val = w_bl[off + sd->grel[g]];
+            int32_t take;
+            if (mode == 0) {
+                OR_TAKE(float)
+                if (take <= 0) continue;
+                for (int64_t p = sd->gstart[g]; p < sd->gstart[g] + take; ++p) {
+                    float m = sd->mask[p];
+                    if (m == 0) continue;
+                    fn(ctx, i, dir, p, sd->col[p], sd->grel[g], m, sv[i] * w_val * m);
+                }
+            } else {
+                take = group_edge_count[g];
+                float gp = sv[i] * w_val;
+                for (int64_t p = sd->gstart[g]; p < sd->gstart[g] + take; ++p) {
+                    float m = sd->mask[p];
+                    fn(ctx, i, dir, p, sd->col[p], sd->grel[g], m, gp * m);
+                }
+            }
+        }
+    }
+    if (!wot_i) fn(ctx, i, 2, -1, src, -1, 1.0f, sv[i] * w_bl[n - 1]);
+}
+
+typedef struct { float *acc; int64_t *mark; int64_t *touched; int64_t ntouched; int64_t stamp; } or_acc_t;
+
+static void or_acc_item(void *ctx, int64_t entry, int dir, int64_t p, int64_t dst, int rel, float m, float value)
+{
+    or_acc_t *a = (or_acc_t *)ctx;
+    (void)entry; (void)dir; (void)p; (void)rel; (void)m;
+    if (a->mark[dst] != a->stamp) {
+        a->mark[dst] = a->stamp;
+        a->acc[dst] = 0.0f;
+        a->touched[a->ntouched++] = dst;
+    }
+    a->acc[dst] += value;
+}
+
+static int or_cmp_i64(const void *x, const void *y)
+{
+    int64_t a = *(const int64_t *)x, b = *(const int64_t *)y;
+    return a < b ? -1 : a > b;
+}
+
+int64_t or_sparse_forward(int mode, int64_t nnz, const int64_t *sb, const int64_t *sl, const int64_t *se,
+    const float *sv, int64_t B, int64_t L, int64_t E, const float *w, int64_t n,
+    const int32_t *ori_col, const float *ori_mask, const int32_t *ori_gptr, const int16_t *ori_grel,
+    const int32_t *ori_gstart, const int32_t *ori_gcount,
+    const int32_t *inv_col, const float *inv_mask, const int32_t *inv_gptr, const int16_t *inv_grel,
+    const int32_t *inv_gstart, const int32_t *inv_gcount,
+    int64_t r_size, int wot_i, int64_t topk_edges, int64_t cap, int64_t *out_key, float *out_v)
+{
+    or_side_t sides[2] = {{ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount},
+                          {inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount}};
+    or_acc_t a;
+    a.acc = (float *)calloc((size_t)(E > 0 ? E : 1), sizeof(float));
+    a.mark = (int64_t *)malloc((size_t)(E > 0 ? E : 1) * sizeof(int64_t));
+    a.touched = (int64_t *)malloc((size_t)(E > 0 ? E : 1) * sizeof(int64_t));
+    for (int64_t e = 0; e < E; ++e) a.mark[e] = -1;
+    int64_t total = 0;
+    for (int64_t row = 0; row < B * L; ++row) {
+        a.ntouched = 0;
+        a.stamp = row;
+        for (int64_t i = 0; i < nnz; ++i)
+            if (sb[i] * L + sl[i] == row)
+                or_sparse_walk(mode, i, sb, sl, se, sv, L, w, n, sides, r_size, wot_i, topk_edges, or_acc_item, &a);
+        qsort(a.touched, (size_t)a.ntouched, sizeof(int64_t), or_cmp_i64);
+        if (total + a.ntouched > cap) { total = -1; break; }
+        for (int64_t k = 0; k < a.ntouched; ++k) {
+            out_key[total + k] = row * E + a.touched[k];
+            out_v[total + k] = a.acc[a.touched[k]];
+        }
+        total += a.ntouched;
+    }
+    free(a.acc); free(a.mark); free(a.touched);
+    return total;
+}
+
+/* Backward of the sparse hop (flashlog.cu:1856-1959 semantics, sequential
+ * order): grad_v[i] = sum over entry i's items of (g*m)*w, then + g*w[n-1]
+ * for the identity item; grad_w[row, off+rel] += (g*m)*v and
+ * grad_w[row, n-1] += g*v.  g is grad_out at the item's output key.        */
+typedef struct {
+    const int64_t *out_key; int64_t nout; const float *grad; const float *w; const float *sv;
+    const int64_t *sb, *sl; int64_t L, E, n, r_size; float *grad_v; float *grad_w; float gsp;
+} or_bwd_t;
+
+static void or_bwd_item(void *ctx, int64_t entry, int dir, int64_t p, int64_t dst, int rel, float m, float value)
+{
+    or_bwd_t *c = (or_bwd_t *)ctx;
+    (void)p; (void)value;
+    int64_t row = c->sb[entry] * c->L + c->sl[entry];
+    int64_t key = row * c->E + dst;
+    int64_t pos = or_lower_bound(c->out_key, c->nout, key);
+    float gv = (pos < c->nout && c->out_key[pos] == key) ? c->grad[pos] : 0.0f;
+    if (dir == 2) {
+        c->gsp += gv * c->w[row * c->n + c->n - 1];
+        c->grad_w[row * c->n + c->n - 1] += gv * c->sv[entry];
+        return;
+    }
+    int64_t col = (dir ? c->r_size : 0) + rel;
+    c->gsp += gv * m * c->w[row * c->n + col];
+    c->grad_w[row * c->n + col] += gv * m * c->sv[entry];
+}
+
+void or_sparse_backward(int mode, int64_t nnz, const int64_t *sb, const int64_t *sl, const int64_t *se,
+    const float *sv, int64_t B, int64_t L, int64_t E, const float *w, int64_t n,
+    const int32_t *ori_col, const float *ori_mask, const int32_t *ori_gptr, const int16_t *ori_grel,
+    const int32_t *ori_gstart, const int32_t *ori_gcount,
+    const int32_t *inv_col, const float *inv_mask, const int32_t *inv_gptr, const int16_t *inv_grel,
+    const int32_t *inv_gstart, const int32_t *inv_gcount,
+    int64_t r_size, int wot_i, int64_t topk_edges, const int64_t *out_key, int64_t nout, const float *grad_out,
+    float *grad_v, float *grad_w)
+{
+    or_side_t sides[2] = {{ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount},
+                          {inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount}};
+    or_bwd_t c = {out_key, nout, grad_out, w, sv, sb, sl, L, E, n, r_size, grad_v, grad_w, 0.0f};
+    memset(grad_w, 0, sizeof(float) * (size_t)(B * L * n));
+    for (int64_t i = 0; i < nnz; ++i) {
+        c.gsp = 0.0f;
+        or_sparse_walk(mode, i, sb, sl, se, sv, L, w, n, sides, r_size, wot_i, topk_edges, or_bwd_item, &c);
+        grad_v[i] = c.gsp;
+    }
+}
+
+/* normalize_sparse3d on the CPU (flashlog_kernel.py:551-555): per row the
+ * sum of its values in entry order (index_add_), out = v / max(d, eps).     */
+void or_sparse_normalize(int64_t nnz, const int64_t *sb, const int64_t *sl, const float *v, int64_t B, int64_t L,
+                         float eps, float *out, float *denom)
+{
+    for (int64_t r = 0; r < B * L; ++r) denom[r] = 0.0f;
+    for (int64_t i = 0; i < nnz; ++i) denom[sb[i] * L + sl[i]] += v[i];
+    for (int64_t i = 0; i < nnz; ++i) {
+        float d = denom[sb[i] * L + sl[i]];
+        out[i] = v[i] / (d < eps ? eps : d);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Filtered, tie-aware rank of the target per query: flashlog.cu:2754-2910.
  * Scores are a sparse [B, E] matrix given as (b, e, v) entries sorted by
  * (b, e), at most one entry per coordinate; absent coordinates score 0.
@@ -503,12 +695,6 @@ void or_dense_max_backward(int64_t BL, int64_t E, int64_t n, const float *A, con
  *   rank = greater + (eq + 1) / 2
  * otherwise rank = greater + 1.  The target itself counts as filtered when
  * its key is in filter_keys (the reference keeps it out of both counts).    */
-static int64_t or_lower_bound(const int64_t *a, int64_t n, int64_t key)
-{
-    int64_t lo = 0, hi = n;
-    while (lo < hi) { int64_t mid = lo + (hi - lo) / 2; if (a[mid] < key) lo = mid + 1; else hi = mid; }
-    return lo;
-}
 
 #define OR_DEFINE_FILTERED_RANKS(NAME, T)                                                    \
 void NAME(int64_t nnz, const int64_t *idx_b, const int64_t *idx_e, const T *values,             \

@@ -290,3 +290,97 @@ def filtered_ranks_brute(dense_scores, targets, filter_mask, use_eql=False):
         eq = int(np.sum(S[b][unf] == t)) + 1
         ranks[b] = greater + (eq + 1) / 2.0 if use_eql else greater + 1
     return ranks
+
+
+# --------------------------------------------------------------------------
+# Sparse (COO) hop: flashlog.cpp:1388-1486 (mode 0, top-k / CPU order) and the
+# all-edges coordinates of flashlog.cu:1743-1854 (mode 1)
+
+SPARSE_TOPK, SPARSE_ALL = 0, 1
+
+
+def _sparse_args(b, l, e, v):
+    return (_c(b, np.int64), _c(l, np.int64), _c(e, np.int64), _c(v, np.float32))
+
+
+def _sparse_cap(e, csr, nnz):
+    gc = [np.asarray(csr[11]), np.asarray(csr[15])]
+    gp = [np.asarray(csr[8]), np.asarray(csr[12])]
+    e = np.asarray(e, np.int64)
+    cap = nnz
+    for side in range(2):
+        deg = np.zeros(gp[side].shape[0] - 1, np.int64)
+        csum = np.concatenate([[0], np.cumsum(gc[side].astype(np.int64))])
+        deg = csum[gp[side][1:]] - csum[gp[side][:-1]]
+        cap += int(deg[e].sum()) if e.size else 0
+    return max(cap, 1)
+
+
+def sparse_forward(mode, b, l, e, v, B, L, E, w, csr, masks, r_size, wot_i=False, topk_edges=1 << 60):
+    """Returns (keys, values): keys = (b*L + l)*E + e ascending."""
+    b, l, e, v = _sparse_args(b, l, e, v)
+    w = _c(w, np.float32).reshape(B * L, -1)
+    n = w.shape[1]
+    masks = tuple(_c(m, np.float32) for m in masks)
+    args = _csr_args(csr, masks)
+    cap = _sparse_cap(e, csr, v.shape[0])
+    keys = np.empty(cap, np.int64)
+    vals = np.empty(cap, np.float32)
+    fn = lib().or_sparse_forward
+    fn.restype = ctypes.c_int64
+    cnt = fn(ctypes.c_int(mode), ctypes.c_int64(v.shape[0]), _p(b), _p(l), _p(e), _p(v), ctypes.c_int64(B),
+             ctypes.c_int64(L), ctypes.c_int64(E), _p(w), ctypes.c_int64(n), *[_p(a) for a in args],
+             ctypes.c_int64(r_size), ctypes.c_int(int(bool(wot_i))), ctypes.c_int64(int(topk_edges)),
+             ctypes.c_int64(cap), _p(keys), _p(vals))
+    assert cnt >= 0
+    return keys[:cnt].copy(), vals[:cnt].copy()
+
+
+def sparse_backward(mode, b, l, e, v, B, L, E, w, csr, masks, r_size, out_keys, grad_out, wot_i=False,
+                    topk_edges=1 << 60):
+    b, l, e, v = _sparse_args(b, l, e, v)
+    w = _c(w, np.float32).reshape(B * L, -1)
+    n = w.shape[1]
+    masks = tuple(_c(m, np.float32) for m in masks)
+    args = _csr_args(csr, masks)
+    out_keys = _c(out_keys, np.int64)
+    grad_out = _c(grad_out, np.float32)
+    gv = np.empty(v.shape[0], np.float32)
+    gw = np.empty((B * L, n), np.float32)
+    lib().or_sparse_backward(ctypes.c_int(mode), ctypes.c_int64(v.shape[0]), _p(b), _p(l), _p(e), _p(v),
+                             ctypes.c_int64(B), ctypes.c_int64(L), ctypes.c_int64(E), _p(w), ctypes.c_int64(n),
+                             *[_p(a) for a in args], ctypes.c_int64(r_size), ctypes.c_int(int(bool(wot_i))),
+                             ctypes.c_int64(int(topk_edges)), _p(out_keys), ctypes.c_int64(out_keys.shape[0]),
+                             _p(grad_out), _p(gv), _p(gw))
+    return gv, gw
+
+
+def sparse_normalize(b, l, v, B, L, eps=1e-7):
+    b, l, _, v = _sparse_args(b, l, b, v)
+    out = np.empty(v.shape[0], np.float32)
+    denom = np.empty(B * L, np.float32)
+    lib().or_sparse_normalize(ctypes.c_int64(v.shape[0]), _p(b), _p(l), _p(v), ctypes.c_int64(B),
+                              ctypes.c_int64(L), ctypes.c_float(eps), _p(out), _p(denom))
+    return out, denom
+
+
+def sparse_topc(b, l, v, L, c):
+    """Kept entry indices of the c1 budget on a coalesced COO state
+    (flashlog_kernel.py:1092-1140): per (b, l) row with more than c nonzeros,
+    its c largest nonzeros (ties to the earlier entry); other rows keep all."""
+    b = np.asarray(b, np.int64)
+    l = np.asarray(l, np.int64)
+    v = np.asarray(v, np.float32)
+    row = b * L + l
+    keep = np.ones(v.shape[0], bool)
+    for r in np.unique(row):
+        idx = np.nonzero(row == r)[0]
+        nz = idx[v[idx] != 0]
+        if nz.size <= c:
+            continue
+        keep[idx] = False
+        if c == 0:
+            continue
+        order = nz[np.lexsort((np.arange(nz.size), -v[nz].astype(np.float64)))]
+        keep[order[:c]] = True
+    return np.nonzero(keep)[0]

@@ -44,3 +44,16 @@ def to_torch_csr(csr, device):
 def bits(x):
     x = np.ascontiguousarray(x)
     return x.view(np.int32) if x.dtype == np.float32 else x.view(np.int64)
+
+
+def sparse_coo_state(B, L, E, per_row, rng, ties=False):
+    """Coalesced COO state: rows (b, l) ascending, entities ascending."""
+    bs, ls, es, vs = [], [], [], []
+    for b in range(B):
+        for l in range(L):
+            k = int(rng.integers(0, per_row + 1))
+            e = np.sort(rng.choice(E, k, replace=False))
+            v = (rng.integers(1, 4, k) / 8.0 if ties else rng.random(k) + 1e-3).astype(np.float32)
+            bs.append(np.full(k, b)); ls.append(np.full(k, l)); es.append(e); vs.append(v)
+    return (np.concatenate(bs).astype(np.int64), np.concatenate(ls).astype(np.int64),
+            np.concatenate(es).astype(np.int64), np.concatenate(vs).astype(np.float32))

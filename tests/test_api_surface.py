@@ -23,9 +23,7 @@ PUBLIC = sorted(k for k in SURFACE if k.split(".")[0] not in INTERNAL)
 # Reference classes this build does not carry yet (their entry points exist
 # as functions that raise NotImplementedError).  strict: when one is added,
 # its xfail turns into a failure here until it is removed from this set.
-NOT_YET = {"FlashLogFunctionSparse3DAllEdgesSum", "FlashLogFunctionSparse3DCPUSum",
-           "FlashLogFunctionSparse3DCPUSumNorm", "FlashLogFunctionSparse3DTopKMax",
-           "FlashLogFunctionSparse3DTopKSum", "Sparse3DNormalizeFunction"}
+NOT_YET = {"FlashLogFunctionSparse3DTopKMax"}
 
 
 def _params(name):

@@ -1,0 +1,224 @@
+"""GPU parity of the sparse (COO) hop against the oracle: coordinates and
+fp32 values bit for bit (the CPU path's addition order), gradients within
+1e-5 relative, normalization within 1e-6 relative (tree vs. sequential
+row sums)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import attention, bits, masks_for, small_graph, sparse_coo_state, to_torch_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def _fk():
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+    return fk
+
+
+def _case(cfg, scale, B, L, per_row, seed, ties=False, drop=0.1, graph_seed=None):
+    rng = np.random.default_rng(seed)
+    h, r, t, E, R, csr = small_graph(cfg, scale, seed=graph_seed)
+    n = 2 * R + 1
+    b, l, e, v = sparse_coo_state(B, L, E, per_row, rng, ties=ties)
+    w = attention(B * L, n, rng).reshape(B, L, n)
+    if ties:
+        w[..., : n // 2] = w[..., :1]
+    mbool, masks = masks_for(csr, h.shape[0], rng, drop=drop)
+    return rng, E, R, n, csr, mbool, masks, (b, l, e, v), w
+
+
+def _keys(idx, L, E):
+    idx = idx.cpu().numpy()
+    return (idx[0] * L + idx[1]) * E + idx[2]
+
+
+def _dev(*arrs):
+    return [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in arrs]
+
+
+def _all_edges(state, w, csr, masks, B, L, E, R, wot_i=False, grad=False):
+    fk = _fk()
+    b, l, e, v = _dev(*state)
+    v.requires_grad_(grad)
+    wt = torch.from_numpy(w).cuda().requires_grad_(grad)
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    om, im = _dev(*masks)
+    out = fk.FlashLogFunctionSparse3DAllEdgesSum.apply(b, l, e, v, wt, tc[1], om, tc[8], tc[9], tc[10], tc[11],
+                                                       tc[5], im, tc[12], tc[13], tc[14], tc[15], B, L, E, R,
+                                                       wot_i)
+    return out, v, wt
+
+
+def _topk(state, w, csr, mbool, B, L, E, R, K, c1=None, wot_i=False, grad=False):
+    fk = _fk()
+    b, l, e, v = _dev(*state)
+    v.requires_grad_(grad)
+    wt = torch.from_numpy(w).cuda().requires_grad_(grad)
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    mk = torch.from_numpy(mbool).cuda()
+    out = fk.FlashLogFunctionSparse3DTopKSum.apply(b, l, e, v, wt, *tc[:4], *tc[4:8], *tc[8:16], mk, None,
+                                                   B, L, E, R, wot_i, K, False, c1, True)
+    return out, v, wt
+
+
+@pytest.mark.parametrize("cfg,scale,per_row", [(2, 0.05, 40), (2, 1.0, 300), (3, 0.05, 60)])
+@pytest.mark.parametrize("wot_i", [False, True])
+def test_sparse_all_edges_bitexact(cfg, scale, per_row, wot_i):
+    B, L = 4, 3
+    rng, E, R, n, csr, mbool, masks, state, w = _case(cfg, scale, B, L, per_row, 10 + cfg + wot_i)
+    keys, vals = O.sparse_forward(O.SPARSE_ALL, *state, B, L, E, w, csr, masks, R, wot_i)
+    out, _, _ = _all_edges(state, w, csr, masks, B, L, E, R, wot_i)
+    torch.cuda.synchronize()
+    assert out.is_coalesced()
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+
+
+@pytest.mark.parametrize("K", [2, 7, 200, 1 << 60])
+@pytest.mark.parametrize("ties", [False, True])
+def test_sparse_topk_bitexact(K, ties):
+    B, L = 4, 3
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 1.0, B, L, 250, 40 + K % 11 + ties, ties=ties)
+    keys, vals = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, K)
+    out, _, _ = _topk(state, w, csr, mbool, B, L, E, R, K)
+    torch.cuda.synchronize()
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+
+
+@pytest.mark.parametrize("c1", [0, 5, 40])
+def test_sparse_topk_with_c1(c1):
+    B, L = 3, 3
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 0.3, B, L, 80, 70 + c1, ties=True)
+    kept = O.sparse_topc(state[0], state[1], state[3], L, c1)
+    sel = tuple(a[kept] for a in state)
+    keys, vals = O.sparse_forward(O.SPARSE_TOPK, *sel, B, L, E, w, csr, masks, R, False, 3)
+    out, v, wt = _topk(state, w, csr, mbool, B, L, E, R, 3, c1=c1, grad=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+    # gradient reaches only the kept entries
+    g = torch.randn(out.values().shape, device="cuda")
+    (out.values() * g).sum().backward()
+    dropped = np.setdiff1d(np.arange(state[3].shape[0]), kept)
+    assert np.all(v.grad.cpu().numpy()[dropped] == 0)
+
+
+def test_sparse_unsorted_input_and_edges():
+    fk = _fk()
+    B, L = 3, 2
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 0.1, B, L, 30, 5)
+    keys, vals = O.sparse_forward(O.SPARSE_ALL, *state, B, L, E, w, csr, masks, R)
+    perm = rng.permutation(state[0].shape[0])
+    shuffled = tuple(a[perm] for a in state)
+    # the CPU path visits entries of a row in input order: compare with the oracle on the same order
+    rows = shuffled[0] * L + shuffled[1]
+    order = np.argsort(rows, kind="stable")
+    k2, v2 = O.sparse_forward(O.SPARSE_ALL, *(a[order] for a in shuffled), B, L, E, w, csr, masks, R)
+    out, _, _ = _all_edges(shuffled, w, csr, masks, B, L, E, R)
+    assert np.array_equal(_keys(out.indices().detach(), L, E), k2)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(v2))
+    assert np.array_equal(k2, keys)
+    # empty state
+    empty = (np.zeros(0, np.int64),) * 3 + (np.zeros(0, np.float32),)
+    out, _, _ = _all_edges(empty, w, csr, masks, B, L, E, R)
+    assert out._nnz() == 0
+    # top-k budget 0: only the identity terms
+    out, _, _ = _topk(state, w, csr, mbool, B, L, E, R, 0)
+    kk, vv = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, 0)
+    assert np.array_equal(_keys(out.indices().detach(), L, E), kk)
+    # out-of-range entity
+    bad = (state[0], state[1], state[2].copy(), state[3])
+    bad[2][0] = E
+    with pytest.raises(ValueError):
+        _all_edges(bad, w, csr, masks, B, L, E, R)
+
+
+@pytest.mark.parametrize("mode", ["all", "topk"])
+@pytest.mark.parametrize("wot_i", [False, True])
+def test_sparse_backward(mode, wot_i):
+    B, L = 4, 3
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 1.0, B, L, 120, 90 + wot_i + (mode == "all"))
+    if mode == "all":
+        out, v, wt = _all_edges(state, w, csr, masks, B, L, E, R, wot_i, grad=True)
+        m, K = O.SPARSE_ALL, 1 << 60
+    else:
+        out, v, wt = _topk(state, w, csr, mbool, B, L, E, R, 5, wot_i=wot_i, grad=True)
+        m, K = O.SPARSE_TOPK, 5
+    keys = _keys(out.indices().detach(), L, E)
+    g = rng.standard_normal(keys.shape[0]).astype(np.float32)
+    (out.values() * torch.from_numpy(g).cuda()).sum().backward()
+    gv_ref, gw_ref = O.sparse_backward(m, *state, B, L, E, w, csr, masks, R, keys, g, wot_i, K)
+    np.testing.assert_allclose(v.grad.cpu().numpy(), gv_ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(wt.grad.reshape(B * L, n).cpu().numpy(), gw_ref, rtol=1e-5, atol=1e-4)
+
+
+def test_normalize_sparse3d():
+    fk = _fk()
+    rng = np.random.default_rng(3)
+    B, L, E = 5, 3, 400
+    b, l, e, v = sparse_coo_state(B, L, E, 90, rng)
+    idx = torch.from_numpy(np.stack([b, l, e])).cuda()
+    vt = torch.from_numpy(v).cuda().requires_grad_(True)
+    s = torch.sparse_coo_tensor(idx, vt, (B, L, E), is_coalesced=True)
+    out = fk.normalize_sparse3d(s)
+    want, denom = O.sparse_normalize(b, l, v, B, L)
+    np.testing.assert_allclose(out.values().detach().cpu().numpy(), want, rtol=1e-6)
+    g = rng.standard_normal(v.shape[0]).astype(np.float32)
+    (out.values() * torch.from_numpy(g).cuda()).sum().backward()
+    row = b * L + l
+    d = denom[row].astype(np.float64)
+    sgx = np.zeros(B * L)
+    np.add.at(sgx, row, g.astype(np.float64) * v)
+    want_g = g / d - sgx[row] / (d * d)
+    np.testing.assert_allclose(vt.grad.cpu().numpy(), want_g, rtol=1e-5, atol=1e-6)
+
+
+def test_three_hop_topk_pipeline():
+    """Per hop: c1 + top-k hop + normalize, each hop checked bit for bit on
+    the GPU's own input (the normalization differs from the CPU's in order)."""
+    fk = _fk()
+    B, L = 4, 3
+    rng, E, R, n, csr, mbool, masks, _, _ = _case(2, 1.0, B, L, 1, 123)
+    heads = rng.integers(0, E, B)
+    b = np.repeat(np.arange(B), L).astype(np.int64)
+    l = np.tile(np.arange(L), B).astype(np.int64)
+    e = np.repeat(heads, L).astype(np.int64)
+    v = np.ones(B * L, np.float32)
+    idx = torch.from_numpy(np.stack([b, l, e])).cuda()
+    state = torch.sparse_coo_tensor(idx, torch.from_numpy(v).cuda(), (B, L, E)).coalesce()
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    mk = torch.from_numpy(mbool).cuda()
+    for hop in range(3):
+        w = attention(B * L, n, rng).reshape(B, L, n)
+        si = state.indices().cpu().numpy()
+        sv = state.values().cpu().numpy()
+        kept = O.sparse_topc(si[0], si[1], sv, L, 100)
+        keys, vals = O.sparse_forward(O.SPARSE_TOPK, si[0][kept], si[1][kept], si[2][kept], sv[kept], B, L, E, w,
+                                      csr, masks, R, False, 200)
+        s = fk.vectorized_operation_sparse3d_csr_sum(state, torch.from_numpy(w).cuda(), tc, mk, R, use_topk=True,
+                                                     topk_edges=200, topk_nodes=100)
+        assert np.array_equal(_keys(s.indices(), L, E), keys)
+        assert np.array_equal(bits(s.values().cpu().numpy()), bits(vals))
+        state = fk.normalize_sparse3d(s)
+
+
+def test_cpu_sum_classes():
+    fk = _fk()
+    B, L = 3, 2
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 0.1, B, L, 30, 17)
+    sp = torch.sparse_coo_tensor(torch.from_numpy(np.stack(state[:3])), torch.from_numpy(state[3]),
+                                 (B, L, E)).coalesce()
+    tcsr = tuple(torch.from_numpy(np.ascontiguousarray(a)) for a in csr)
+    out = fk.vectorized_operation_sparse3d_csr_sum(sp, torch.from_numpy(w), tcsr, torch.from_numpy(mbool), R,
+                                                   use_topk=True, topk_edges=4)
+    assert out.device.type == "cpu"
+    keys, vals = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, 4)
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().numpy()), bits(vals))
+    outn = fk.vectorized_operation_sparse3d_csr_sum_norm(sp, torch.from_numpy(w), tcsr, torch.from_numpy(mbool),
+                                                         R, use_topk=True, topk_edges=4)
+    nv, _ = O.sparse_normalize(keys // (L * E), (keys // E) % L, vals, B, L)
+    np.testing.assert_allclose(outn.values().numpy(), nv, rtol=1e-6)
