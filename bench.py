@@ -36,6 +36,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU baseline sample (0 disables it)")
     ap.add_argument("--profile-steps", type=int, default=10)
+    ap.add_argument("--sparse", action="store_true",
+                    help="the DRUM --sparse GPU path (default for --config 5)")
     return ap.parse_args()
 
 
@@ -105,6 +107,8 @@ def main():
     from flashlog_amd import _lib, synth
     from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
 
+    if args.sparse or args.config == 5:
+        return main_sparse(args)
     cfg = synth.CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -198,6 +202,159 @@ def main():
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None},
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+SPARSE_KERNELS = ["k_sp_topc", "k_sp_rowptr", "k_sp_select", "k_sp_rowinfo", "k_sp_fill", "k_sp_partition",
+                  "k_sp_accum", "k_sp_accum_hot", "k_sp_emit", "k_norm_fwd", "k_scan_tiles", "k_scan_totals", "k_scan_apply",
+                  "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask", "k_sp_hist"]
+
+
+def fill_bytes(sides_np, b, l, e, R, L, n, W, K):
+    """Algorithmic bytes of one k_sp_fill launch: per entry its record
+    (b, l, e, v: 28 B) and identity item (8 B), per side the source's
+    row-group pointers (8 B), its group records (10 B each) and, per kept
+    edge (all masks are nonzero here: min(eligible edges, K)), the column and
+    mask read (8 B) and the (destination, value) item written (8 B)."""
+    import numpy as np
+    total = 36 * b.shape[0]
+    rows = (b * L + l).astype(np.int64)
+    for (gptr, grel, gcount, off) in sides_np:
+        g0 = gptr[e].astype(np.int64)
+        g1 = gptr[e + 1].astype(np.int64)
+        ng = g1 - g0
+        total += 8 * b.shape[0] + 10 * int(ng.sum())
+        if ng.sum() == 0:
+            continue
+        ent = np.repeat(np.arange(b.shape[0]), ng)
+        starts = np.cumsum(ng) - ng
+        gidx = np.arange(int(ng.sum())) - np.repeat(starts, ng) + np.repeat(g0, ng)
+        wv = W[rows[ent], off + grel[gidx].astype(np.int64)]
+        elig = np.where(wv > 0, gcount[gidx].astype(np.int64), 0)
+        per_entry = np.bincount(ent, weights=elig, minlength=b.shape[0])
+        total += 16 * int(np.minimum(per_entry, K).sum())
+    return total
+
+
+def main_sparse(args):
+    """C5: DRUM --sparse evaluation on one GPU.  A
+    step is T = 3 hops of FlashLogFunctionSparse3DTopKSum (c1 = 1000 entities,
+    c2 = 400 edges) each followed by normalize_sparse3d, from one-hot query
+    states (src/model_DRUM_kernel_sp.py:124-205)."""
+    import numpy as np
+    import torch
+    from flashlog_amd import _lib, synth
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+
+    cfg = synth.CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t_gen = time.perf_counter()
+    h, r, t, E, R = synth.make_graph(args.config)
+    n = 2 * R + 1
+    B, L, T = cfg.batch, cfg.channels, cfg.hops
+    K = cfg.c2 // 2
+    c1 = cfg.c1
+    M = h.shape[0]
+    th, tr, tt = (torch.from_numpy(a) for a in (h, r, t))
+    csr = fk.build_csr_structure(th.to(dev), tt.to(dev), tr.to(dev), E)
+    mask_values = torch.ones(M, dtype=torch.bool, device=dev)
+    rng = np.random.Generator(np.random.PCG64(1234 + args.config))
+    src, qrel, tgt = synth.make_queries(h, r, t, R, B, rng)
+    W = torch.from_numpy(synth.make_attention(B, L, n, T, rng)).to(dev)
+    print("graph %s: E=%d M=%d (%.1f s to generate)" % (cfg.name, E, M, time.perf_counter() - t_gen),
+          file=sys.stderr, flush=True)
+    b0 = torch.arange(B, device=dev).repeat_interleave(L)
+    l0 = torch.arange(L, device=dev).repeat(B)
+    e0 = torch.from_numpy(src).to(dev).repeat_interleave(L)
+    v0 = torch.ones(B * L, device=dev)
+
+    def step(capture=None):
+        b, l, e, v = b0, l0, e0, v0
+        for hop in range(T):
+            s = fk.FlashLogFunctionSparse3DTopKSum.apply(
+                b, l, e, v, W[hop], *csr[:4], *csr[4:8], *csr[8:16], mask_values, None,
+                B, L, E, R, False, K, False, c1, False)
+            if capture is not None:
+                capture.append(s._nnz())
+            s = fk.normalize_sparse3d(s)
+            idx = s.indices()
+            b, l, e, v = idx[0], idx[1], idx[2], s.values()
+        return torch.sparse.sum(s, dim=1)
+
+    with torch.inference_mode():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        e_0 = torch.cuda.Event(enable_timing=True)
+        e_1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e_0.record()
+        for _ in range(args.steps):
+            step()
+        e_1.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms_step = e_0.elapsed_time(e_1) / args.steps
+        print("timed %d steps: %.3f ms/step (host wall %.3f ms/step)"
+              % (args.steps, ms_step, 1e3 * wall / args.steps), file=sys.stderr, flush=True)
+        _lib.prof_enable(True)
+        for _ in range(args.profile_steps):
+            step()
+        torch.cuda.synchronize()
+        prof = {k: _lib.prof_read(k) for k in SPARSE_KERNELS}
+        _lib.prof_enable(False)
+        per_launch = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in prof.items()}
+        per_step = {k: (v[0] / args.profile_steps) for k, v in prof.items()}
+        print("per-launch ms: " + json.dumps({k: round(v, 4) for k, v in per_launch.items()}),
+              file=sys.stderr, flush=True)
+        print("per-step ms: " + json.dumps({k: round(v, 4) for k, v in per_step.items()}),
+              file=sys.stderr, flush=True)
+        # hop inputs of one step (after c1), for the algorithmic bytes of k_sp_fill
+        hop_inputs = []
+        b, l, e, v = b0, l0, e0, v0
+        for hop in range(T):
+            keep = fk._sparse_topc_entries(b, l, e, v, c1, L)
+            bb, ll, ee = (x if keep is None else x[keep] for x in (b, l, e))
+            hop_inputs.append((bb.cpu().numpy(), ll.cpu().numpy(), ee.cpu().numpy()))
+            s = fk.FlashLogFunctionSparse3DTopKSum.apply(
+                b, l, e, v, W[hop], *csr[:4], *csr[4:8], *csr[8:16], mask_values, None,
+                B, L, E, R, False, K, False, c1, False)
+            s = fk.normalize_sparse3d(s)
+            idx = s.indices()
+            b, l, e, v = idx[0], idx[1], idx[2], s.values()
+    csr_np = [c.cpu().numpy() for c in csr]
+    sides_np = ((csr_np[8], csr_np[9], csr_np[11], 0), (csr_np[12], csr_np[13], csr_np[15], R))
+    Wn = W.cpu().numpy()
+    fb = [fill_bytes(sides_np, bb, ll, ee, B * L, L, n, Wn[hop].reshape(B * L, n), K)
+          for hop, (bb, ll, ee) in enumerate(hop_inputs)]
+    fill_ms = per_launch["k_sp_fill"]
+    bytes_per_launch = float(np.mean(fb))
+    achieved = bytes_per_launch / (fill_ms * 1e-3) / 1e9 if fill_ms > 0 else 0.0
+    result = {
+        "metric": "queries/sec for L=3 propagation + % of HBM roofline; top-k select ms",
+        "value": B / (ms_step * 1e-3),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded %s graph, flashlog_amd/synth.py)" % cfg.name,
+        "config": {"workload": "%s DRUM --sparse eval: E=%d, R=%d, M=%d, B=%d, N=%d, T=%d, c1=%d, c2=%d"
+                   % (cfg.name, E, R, M, B, L, T, c1, cfg.c2),
+                   "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2},
+        "topk_select_ms": {"c1_per_hop": per_launch["k_sp_topc"], "c2_per_hop": per_launch["k_sp_select"]},
+        "kernel_ms_per_launch": per_launch,
+        "kernel_ms_per_step": per_step,
+        "roofline": {"kernel": "k_sp_fill", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None},
+        "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)
 

@@ -41,7 +41,6 @@ constexpr int SP_W = 1 << SP_S;
 constexpr int SP_NT = 256;
 constexpr int SP_IPT = 16;
 constexpr int SP_TILE = SP_NT * SP_IPT;  // items per partition tile
-constexpr int SP_HASH = 512;
 
 enum { SP_TOPK = 0, SP_ALL = 1 };
 
@@ -78,10 +77,58 @@ __global__ void k_sp_rowptr(const int64_t *__restrict__ sb, const int64_t *__res
         for (int64_t q = r + 1; q <= R; ++q) row_ptr[q] = nnz;
 }
 
+// Kept items of one (entry, side) in raw order (group order, then CSR
+// position), 64 at a time.  Groups are read 64 at a time, lane g holding
+// one group; a wave prefix sum of their kept counts places every item, and
+// each lane finds the group of its item by a binary search over the lanes.
+// fn(valid, k, p, rel, wv) is called by every lane of the wave for each
+// chunk of 64 items (valid = the lane holds an item; k = the item's index
+// within the side).  Returns the side's item count.
+template <typename F>
+__device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, int64_t g1, const float *wr,
+                                                 float thv, int32_t ct, int mode, F &&fn) {
+    const int lane = fl_lane();
+    int64_t base = 0;
+    for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
+        const int64_t g = gb + lane;
+        int64_t take = 0, start = 0;
+        int rel = 0;
+        float wv = 0.0f;
+        if (g < g1) {
+            rel = s.group_rel[g];
+            wv = wr[rel];
+            start = s.group_start[g];
+            const int64_t cnt = s.group_count[g];
+            take = mode == SP_ALL ? cnt : group_take(wv, thv, ct, start, cnt);
+        }
+        const long long incl = fl_wave_incl_scan_i64(take);
+        const long long total = __shfl(incl, FL_WAVE - 1, FL_WAVE);
+        for (long long k0 = 0; k0 < total; k0 += FL_WAVE) {
+            const long long k = k0 + lane;
+            // smallest lane j with incl_j > k
+            int lo = 0, hi = FL_WAVE - 1;
+#pragma unroll
+            for (int it = 0; it < 6; ++it) {
+                const int mid = (lo + hi) >> 1;
+                const long long im = __shfl(incl, mid, FL_WAVE);
+                if (im > k) hi = mid;
+                else lo = mid + 1;
+            }
+            const int j = lo;
+            const long long ej = __shfl(incl, j, FL_WAVE) - __shfl(take, j, FL_WAVE);
+            const int64_t p = __shfl(start, j, FL_WAVE) + (k - ej);
+            fn(k < total, base + k, p, __shfl(rel, j, FL_WAVE), __shfl(wv, j, FL_WAVE));
+        }
+        base += total;
+    }
+    return base;
+}
+
 // One wave per entry: per side the c2 threshold (bits of the threshold
-// weight, 0 = no pruning) and tie cut, and the number of raw items:
-// kept edges with a nonzero mask (top-k mode) or every edge (all-edges
-// mode), plus the identity item.
+// weight, 0 = no pruning) and tie cut, and the number of raw items: kept
+// edges (top-k mode; a kept edge with a zero mask becomes a hole, raw
+// destination -1, skipped downstream) or every edge (all-edges mode), plus
+// the identity item.
 constexpr int SEL_NT = 256;
 
 __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
@@ -120,10 +167,10 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
                 thv = __uint_as_float(key);
                 ct = cc;
             }
-            for (int64_t g = g0; g < g1; ++g) {
+            // kept edges, masked ones included (they become holes in the raw list)
+            for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
                 const int64_t start = s.group_start[g];
-                const int64_t take = group_take(wr[s.group_rel[g]], thv, ct, start, s.group_count[g]);
-                for (int64_t k = lane; k < take; k += FL_WAVE) c += s.mask[start + k] != 0.0f ? 1 : 0;
+                c += group_take(wr[s.group_rel[g]], thv, ct, start, s.group_count[g]);
             }
         }
         c = fl_wave_sum_i64(c);
@@ -165,9 +212,8 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
                                                    const float *__restrict__ w, int64_t L, int64_t n,
                                                    int64_t r_size, int wot_i, int mode,
                                                    const float *__restrict__ th, const int32_t *__restrict__ cut,
-                                                   const int64_t *__restrict__ item_off, SpRows rows,
-                                                   int32_t *__restrict__ hist, int32_t *__restrict__ raw_dst,
-                                                   float *__restrict__ raw_val) {
+                                                   const int64_t *__restrict__ item_off,
+                                                   int32_t *__restrict__ raw_dst, float *__restrict__ raw_val) {
     const int lane = fl_lane();
     const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
     if (i >= nnz) return;
@@ -175,10 +221,6 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
     const int64_t r = sb[i] * L + sl[i];
     const float a = sv[i];
     const float *wrow = w + r * n;
-    const int64_t rbase = rows.row_item0[r];
-    const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
-    int32_t *hrow = hist + rows.tile_base[r] * rows.NB;
-    const bool count = rows.NB > 1;
     int64_t pos = item_off[i];
     for (int dir = 0; dir < 2; ++dir) {
         const fl_side &s = dir ? inv : ori;
@@ -186,38 +228,18 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
         const float thv = th[2 * i + dir];
         const int32_t ct = cut[2 * i + dir];
         const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-        for (int64_t g = g0; g < g1; ++g) {
-            const float wv = wr[s.group_rel[g]];
-            const int64_t start = s.group_start[g];
-            const int64_t cntg = s.group_count[g];
-            const int64_t take = mode == SP_ALL ? cntg : group_take(wv, thv, ct, start, cntg);
-            if (take <= 0) continue;
-            const float gp = fl_mul(a, wv);
-            for (int64_t k0 = 0; k0 < take; k0 += FL_WAVE) {
-                const int64_t k = k0 + lane;
-                int32_t d = 0;
-                float m = 0.0f;
-                bool keep = false;
-                if (k < take) {
-                    m = s.mask[start + k];
-                    d = s.col_ind[start + k];
-                    keep = mode == SP_ALL || m != 0.0f;
-                }
-                const unsigned long long bal = __ballot(keep);
-                if (keep) {
-                    const int64_t q = pos + __popcll(bal & ((1ull << lane) - 1ull));
-                    raw_dst[q] = d;
-                    raw_val[q] = fl_mul(gp, m);
-                    if (count) atomicAdd(&hrow[(int64_t)(d >> SP_S) * nt + (q - rbase) / SP_TILE], 1);
-                }
-                pos += __popcll(bal);
+        pos += sp_side_items(s, g0, g1, wr, thv, ct, mode, [&](bool valid, int64_t k, int64_t p, int, float wv) {
+            if (valid) {
+                const float m = s.mask[p];
+                const bool keep = mode == SP_ALL || m != 0.0f;
+                raw_dst[pos + k] = keep ? s.col_ind[p] : -1;
+                raw_val[pos + k] = fl_mul(fl_mul(a, wv), m);
             }
-        }
+        });
     }
     if (!wot_i && lane == 0) {
         raw_dst[pos] = (int32_t)src;
         raw_val[pos] = fl_mul(a, wrow[n - 1]);
-        if (count) atomicAdd(&hrow[(int64_t)(src >> SP_S) * nt + (pos - rbase) / SP_TILE], 1);
     }
 }
 
@@ -232,19 +254,45 @@ __device__ __forceinline__ int64_t sp_tile_row(const int64_t *tile_base, int64_t
     return lo;
 }
 
-// Stable block sort of SP_TILE packed keys (bucket << 12 | index) by the
-// bucket bits [12, 12 + nbits), 4 bits per pass.  kin/kout are LDS buffers
-// of SP_TILE keys; returns the buffer holding the result.
-__device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int nbits, uint16_t (*cnt)[SP_NT], int *scan_lds) {
+// Workgroup per tile of a row: the tile's destination-bucket histogram
+// (LDS atomics), written as hist[(row, bucket, tile)] for the scan.  Holes
+// (destination -1) are not counted.
+__global__ __launch_bounds__(SP_NT) void k_sp_hist(int64_t R, SpRows rows, const int32_t *__restrict__ raw_dst,
+                                                  int32_t *__restrict__ hist) {
+    extern __shared__ int hb[];  // [NB]
+    const int64_t tile = blockIdx.x;
+    const int64_t r = sp_tile_row(rows.tile_base, R, tile);
+    const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
+    const int64_t tl = tile - rows.tile_base[r];
+    const int64_t i0 = rows.row_item0[r] + tl * SP_TILE;
+    const int64_t i1e = rows.row_item0[r + 1];
+    const int c = (int)((i1e - i0) < SP_TILE ? (i1e - i0) : SP_TILE);
+    for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) hb[q] = 0;
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < c; idx += SP_NT) {
+        const int32_t d = raw_dst[i0 + idx];
+        if (d >= 0) atomicAdd(&hb[d >> SP_S], 1);
+    }
+    __syncthreads();
+    int32_t *hrow = hist + rows.tile_base[r] * rows.NB + tl;
+    for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) hrow[q * nt] = hb[q];
+}
+
+// Stable LSD block sort of SP_NT * IPT keys held in LDS (kin, blocked: thread
+// t owns kin[t*IPT .. t*IPT + IPT)) by bits [lo, lo + nbits), 4 bits per
+// pass; kout is the second LDS buffer.  Returns the buffer with the result.
+template <int IPT>
+__device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, int nbits, uint16_t (*cnt)[SP_NT],
+                                   int *scan_lds) {
     const int t = threadIdx.x;
-    for (int shift = 12; shift < 12 + nbits; shift += 4) {
-        uint32_t key[SP_IPT];
-        uint16_t loc[SP_IPT];
+    for (int shift = lo_bit; shift < lo_bit + nbits; shift += 4) {
+        uint32_t key[IPT];
+        uint16_t loc[IPT];
 #pragma unroll
         for (int d = 0; d < 16; ++d) cnt[d][t] = 0;
 #pragma unroll
-        for (int j = 0; j < SP_IPT; ++j) {
-            key[j] = kin[t * SP_IPT + j];
+        for (int j = 0; j < IPT; ++j) {
+            key[j] = kin[t * IPT + j];
             const int d = (key[j] >> shift) & 15;
             loc[j] = cnt[d][t];
             cnt[d][t] = (uint16_t)(loc[j] + 1);
@@ -266,7 +314,7 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int nbits, uin
         }
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < SP_IPT; ++j) {
+        for (int j = 0; j < IPT; ++j) {
             const int d = (key[j] >> shift) & 15;
             kout[cnt[d][t] + loc[j]] = key[j];
         }
@@ -298,12 +346,15 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
 #pragma unroll
     for (int j = 0; j < SP_IPT; ++j) {
         const int idx = t * SP_IPT + j;
-        uint32_t key = 0xFFFFF000u | (uint32_t)idx;  // padding sorts last
-        if (idx < c) key = ((uint32_t)(raw_dst[i0 + idx] >> SP_S) << 12) | (uint32_t)idx;
+        uint32_t key = 0xFFFFF000u | (uint32_t)idx;  // padding and holes sort last
+        if (idx < c) {
+            const int32_t d = raw_dst[i0 + idx];
+            if (d >= 0) key = ((uint32_t)(d >> SP_S) << 12) | (uint32_t)idx;
+        }
         kb[0][idx] = key;
     }
     __syncthreads();
-    const uint32_t *sorted = sp_block_sort(kb[0], kb[1], nbits, cnt, scan_lds);
+    const uint32_t *sorted = sp_block_sort<SP_IPT>(kb[0], kb[1], 12, nbits, cnt, scan_lds);
     const int64_t *bb = base + rows.tile_base[r] * rows.NB + tl;
 #pragma unroll 4
     for (int j = 0; j < SP_IPT; ++j) {
@@ -311,6 +362,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         if (p >= c) continue;
         const uint32_t key = sorted[p];
         const uint32_t bk = key >> 12;
+        if (bk == 0xFFFFFu) continue;  // hole
         // first sorted position of this bucket (binary search in LDS)
         int lo = 0, hi = p;
         while (lo < hi) {
@@ -326,68 +378,197 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
     }
 }
 
-// Workgroup per (row, bucket): ordered accumulation in LDS, then the
-// bucket's outputs compacted in destination order into the first slots of
-// its item range; raw_local[raw position] = the item's output index within
-// the bucket (for the backward).
+// Workgroup per (row, bucket): the bucket's items (raw order) grouped by
+// destination with each destination's values added to 0 in raw order; the
+// outputs are compacted in destination order into the first slots of the
+// bucket's item range, and raw_local[raw position] = the item's output index
+// within the bucket (for the backward).  Items are stably sorted by
+// destination in LDS (keys destination << 11 | index, LSD radix) and the
+// first thread of every run adds the run's values in order.
+//   k_sp_accum      buckets of at most SP_CHUNK items, one sort;
+//   k_sp_accum_hot  larger buckets: chunks of SP_CHUNK items in raw order,
+//                   each sorted and folded into a dense LDS accumulator of
+//                   the bucket's 8192 destinations that carries the partial
+//                   sums from chunk to chunk.
+constexpr int SP_CHUNK_IPT = 8;
+constexpr int SP_CHUNK = SP_NT * SP_CHUNK_IPT;
+
+__device__ __forceinline__ void sp_bucket_range(const SpRows &rows, const int64_t *base, int64_t r, int64_t bk,
+                                                int64_t *start, int64_t *end) {
+    if (rows.NB == 1) {
+        *start = rows.row_item0[r];
+        *end = rows.row_item0[r + 1];
+    } else {
+        const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
+        const int64_t *bb = base + rows.tile_base[r] * rows.NB + bk * nt;
+        *start = bb[0];
+        *end = bb[nt];
+    }
+}
+
+// Loads items [c0, c0 + SP_NT*IPT) of the bucket (blocked) as sort keys and
+// LDS values, sorts them, and returns the sorted keys.
+template <int IPT>
+__device__ __forceinline__ const uint32_t *sp_load_sort(const int32_t *__restrict__ dst_arr,
+                                                        const float *__restrict__ val_arr, int64_t start, int64_t c0,
+                                                        int64_t n, uint32_t (*kb)[SP_CHUNK], float *val,
+                                                        uint16_t (*cnt)[SP_NT], int *scan_lds) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int k = t * IPT + j;
+        uint32_t dl = SP_W;  // no item / hole: sorts last
+        if (c0 + k < n) {
+            const int32_t d = dst_arr[start + c0 + k];
+            if (d >= 0) {
+                dl = (uint32_t)d & (SP_W - 1);
+                val[k] = val_arr[start + c0 + k];
+            }
+        }
+        kb[0][k] = (dl << 11) | (uint32_t)k;
+    }
+    __syncthreads();
+    return sp_block_sort<IPT>(kb[0], kb[1], 11, 16, cnt, scan_lds);
+}
+
+// Values in sorted order: sv[p] = val[index of key p], for this thread's
+// blocked positions (sv is the sort's idle ping-pong buffer).
+template <int IPT>
+__device__ __forceinline__ float *sp_sorted_values(const uint32_t *key, uint32_t (*kb)[SP_CHUNK], const float *val) {
+    float *sv = reinterpret_cast<float *>(key == kb[0] ? kb[1] : kb[0]);
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int p = t * IPT + j;
+        sv[p] = val[key[p] & 2047u];
+    }
+    __syncthreads();
+    return sv;
+}
+
+// a + sv[p] + sv[p+1] + ... + sv[e-1], left to right; loads issued 8 ahead.
+__device__ __forceinline__ float sp_fold(float a, const float *sv, int p, int e) {
+    int q = p;
+    for (; q + 8 <= e; q += 8) {
+        float x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = sv[q + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a = fl_add(a, x[u]);
+    }
+    for (; q < e; ++q) a = fl_add(a, sv[q]);
+    return a;
+}
+
+__device__ __forceinline__ bool sp_is_head(const uint32_t *key, int p) {
+    const uint32_t d = key[p] >> 11;
+    return d < SP_W && (p == 0 || (key[p - 1] >> 11) != d);
+}
+
+__device__ __forceinline__ int sp_run_end(const uint32_t *key, int p, int size) {
+    const uint32_t d = key[p] >> 11;
+    int lo = p + 1, hi = size;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if ((key[mid] >> 11) <= d) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+template <int IPT>
+__device__ void sp_accum_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
+                             float *__restrict__ val_arr, const int32_t *__restrict__ raw_arr,
+                             int32_t *__restrict__ raw_local, int32_t *out_count, uint32_t (*kb)[SP_CHUNK],
+                             float *val, uint16_t (*cnt)[SP_NT], int *scan_lds) {
+    constexpr int SIZE = SP_NT * IPT;
+    const int t = threadIdx.x;
+    const uint32_t *key = sp_load_sort<IPT>(dst_arr, val_arr, start, 0, n, kb, val, cnt, scan_lds);
+    const float *sv = sp_sorted_values<IPT>(key, kb, val);
+    int heads = 0;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) heads += sp_is_head(key, t * IPT + j) ? 1 : 0;
+    int total;
+    int rank = fl_block_excl_scan<SP_NT>(heads, scan_lds, &total);
+    // all items were read before the first barrier: outputs may overwrite them
+    for (int j = 0; j < IPT; ++j) {
+        const int p = t * IPT + j;
+        if (!sp_is_head(key, p)) continue;
+        const int e = sp_run_end(key, p, SIZE);
+        const float a = sp_fold(0.0f, sv, p, e);
+        if (raw_local)
+            for (int q = p; q < e; ++q) {
+                const int idx = (int)(key[q] & 2047u);
+                raw_local[raw_arr ? raw_arr[start + idx] : start + idx] = rank;
+            }
+        dst_arr[start + rank] = dbase + (int32_t)(key[p] >> 11);
+        val_arr[start + rank] = a;
+        ++rank;
+    }
+    if (t == 0) *out_count = total;
+}
+
 __global__ __launch_bounds__(SP_NT) void k_sp_accum(SpRows rows, const int64_t *__restrict__ base,
                                                    int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
                                                    const int32_t *__restrict__ raw_arr,
                                                    int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count) {
+    __shared__ uint32_t kb[2][SP_CHUNK];
+    __shared__ float val[SP_CHUNK];
+    __shared__ uint16_t cnt[16][SP_NT];
+    __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
+    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
+    int64_t start, end;
+    sp_bucket_range(rows, base, r, bk, &start, &end);
+    const int64_t n = end - start;
+    if (n > SP_CHUNK) return;  // k_sp_accum_hot
+    int32_t *oc = &out_count[r * rows.NB + bk];
+    if (n == 0) {
+        if (threadIdx.x == 0) *oc = 0;
+        return;
+    }
+    const int32_t dbase = (int32_t)(bk << SP_S);
+    if (n <= SP_NT * 2)
+        sp_accum_one<2>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
+    else if (n <= SP_NT * 4)
+        sp_accum_one<4>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
+    else
+        sp_accum_one<8>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
+}
+
+__global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64_t *__restrict__ base,
+                                                       int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                                       const int32_t *__restrict__ raw_arr,
+                                                       int32_t *__restrict__ raw_local,
+                                                       int32_t *__restrict__ out_count) {
+    __shared__ uint32_t kb[2][SP_CHUNK];
+    __shared__ float val[SP_CHUNK];
+    __shared__ uint16_t cnt[16][SP_NT];
     __shared__ float acc[SP_W];
     __shared__ uint32_t bits[SP_W / 32];
-    __shared__ int owner[SP_HASH];
     __shared__ int wpre[SP_W / 32];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
     const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
-    const int t = threadIdx.x;
     int64_t start, end;
-    if (rows.NB == 1) {
-        start = rows.row_item0[r];
-        end = rows.row_item0[r + 1];
-    } else {
-        const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
-        const int64_t *bb = base + rows.tile_base[r] * rows.NB + bk * nt;
-        start = bb[0];
-        end = bb[nt];
-    }
+    sp_bucket_range(rows, base, r, bk, &start, &end);
     const int64_t n = end - start;
-    if (n == 0) {
-        if (t == 0) out_count[r * rows.NB + bk] = 0;
-        return;
-    }
+    if (n <= SP_CHUNK) return;  // k_sp_accum
+    const int t = threadIdx.x;
     for (int q = t; q < SP_W / 32; q += SP_NT) bits[q] = 0;
-    for (int q = t; q < SP_HASH; q += SP_NT) owner[q] = INT_MAX;
-    __syncthreads();
-    for (int64_t w0 = 0; w0 < n; w0 += SP_NT) {
-        const int64_t k = w0 + t;
-        bool pending = k < n;
-        int dl = 0;
-        float v = 0.0f;
-        if (pending) {
-            dl = dst_arr[start + k] & (SP_W - 1);
-            v = val_arr[start + k];
-        }
-        const int h = dl & (SP_HASH - 1);
-        // rounds: per hash slot the earliest pending item applies
-        while (true) {
-            if (pending) atomicMin(&owner[h], t);
-            __syncthreads();
-            const bool win = pending && owner[h] == t;
-            if (win) {
-                const uint32_t m = 1u << (dl & 31);
-                const uint32_t old = atomicOr(&bits[dl >> 5], m);
-                acc[dl] = (old & m) ? fl_add(acc[dl], v) : fl_add(0.0f, v);
-            }
-            __syncthreads();
-            if (win) {
-                owner[h] = INT_MAX;
-                pending = false;
-            }
-            if (!__syncthreads_or(pending)) break;
+    for (int64_t c0 = 0; c0 < n; c0 += SP_CHUNK) {
+        __syncthreads();  // previous chunk's folds done with kb / val
+        const uint32_t *key = sp_load_sort<SP_CHUNK_IPT>(dst_arr, val_arr, start, c0, n, kb, val, cnt, scan_lds);
+        const float *sv = sp_sorted_values<SP_CHUNK_IPT>(key, kb, val);
+        for (int j = 0; j < SP_CHUNK_IPT; ++j) {
+            const int p = t * SP_CHUNK_IPT + j;
+            if (!sp_is_head(key, p)) continue;
+            const int e = sp_run_end(key, p, SP_CHUNK);
+            const uint32_t d = key[p] >> 11;
+            const uint32_t m = 1u << (d & 31);
+            const uint32_t old = atomicOr(&bits[d >> 5], m);
+            acc[d] = sp_fold((old & m) ? acc[d] : 0.0f, sv, p, e);
         }
     }
-    // output ranks: one bitmap word per thread
+    __syncthreads();
     const uint32_t word = bits[t];
     int total;
     const int pre = fl_block_excl_scan<SP_NT>(__popc(word), scan_lds, &total);
@@ -395,7 +576,9 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum(SpRows rows, const int64_t *
     __syncthreads();
     if (raw_local) {
         for (int64_t k = t; k < n; k += SP_NT) {
-            const int dl = dst_arr[start + k] & (SP_W - 1);
+            const int32_t d = dst_arr[start + k];
+            if (d < 0) continue;  // hole
+            const int dl = d & (SP_W - 1);
             raw_local[raw_arr ? raw_arr[start + k] : start + k] =
                 wpre[dl >> 5] + __popc(bits[dl >> 5] & ((1u << (dl & 31)) - 1u));
         }
@@ -478,37 +661,33 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
         const float thv = th[2 * i + dir];
         const int32_t ct = cut[2 * i + dir];
         const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-        for (int64_t g = g0; g < g1; ++g) {
-            const int rel = s.group_rel[g];
-            const float wv = wrow[off + rel];
-            const int64_t start = s.group_start[g];
-            const int64_t cntg = s.group_count[g];
-            const int64_t take = mode == SP_ALL ? cntg : group_take(wv, thv, ct, start, cntg);
-            if (take <= 0) continue;
-            float gws = 0.0f;
-            for (int64_t k0 = 0; k0 < take; k0 += FL_WAVE) {
-                const int64_t k = k0 + lane;
-                int32_t d = 0;
-                float m = 0.0f;
-                bool keep = false;
-                if (k < take) {
-                    m = s.mask[start + k];
-                    d = s.col_ind[start + k];
-                    keep = mode == SP_ALL || m != 0.0f;
-                }
-                const unsigned long long bal = __ballot(keep);
-                if (keep) {
-                    const int64_t q = pos + __popcll(bal & ((1ull << lane) - 1ull));
-                    const float gv = grad[orow[d >> SP_S] + raw_local[q]];
+        pos += sp_side_items(s, g0, g1, wrow + off, thv, ct, mode, [&](bool valid, int64_t kk, int64_t p, int rel,
+                                                                        float wv) {
+            float gwv = 0.0f;
+            if (valid) {
+                const float m = s.mask[p];
+                if (mode == SP_ALL || m != 0.0f) {
+                    const int32_t d = s.col_ind[p];
+                    const float gv = grad[orow[d >> SP_S] + raw_local[pos + kk]];
                     const float gm = fl_mul(gv, m);
                     gsp = fl_add(gsp, fl_mul(gm, wv));
-                    gws = fl_add(gws, fl_mul(gm, a));
+                    gwv = fl_mul(gm, a);
                 }
-                pos += __popcll(bal);
             }
-            gws = fl_wave_sum_f32(gws);
-            if (lane == 0 && gws != 0.0f) atomicAdd(&grad_w[r * n + off + rel], gws);
-        }
+            // per-relation sums of this chunk: items of one group are on
+            // consecutive lanes (segmented scan keyed by the relation column)
+            const int seg = valid ? rel : -1;
+            float x = gwv;
+#pragma unroll
+            for (int o = 1; o < FL_WAVE; o <<= 1) {
+                const float y = __shfl_up(x, o, FL_WAVE);
+                const int sy = __shfl_up(seg, o, FL_WAVE);
+                if (lane >= o && sy == seg) x = fl_add(x, y);
+            }
+            const int snext = __shfl_down(seg, 1, FL_WAVE);
+            const bool tail = lane == FL_WAVE - 1 || snext != seg;
+            if (valid && tail && x != 0.0f) atomicAdd(&grad_w[r * n + off + rel], x);
+        });
     }
     gsp = fl_wave_sum_f32(gsp);
     if (lane == 0) {
@@ -759,7 +938,7 @@ int sp_check(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, con
     if (!ori || !inv || !h) return fl_fail(FL_ERR_ARG, "%s: null argument", what);
     if (h->nnz < 0 || h->B < 0 || h->L < 0 || h->E < 0 || h->n < 1)
         return fl_fail(FL_ERR_ARG, "%s: bad shape", what);
-    if (h->E >= INT32_MAX) return fl_fail(FL_ERR_ARG, "%s: E must be < 2^31", what);
+    if (h->E > ((int64_t)SP_W << 14)) return fl_fail(FL_ERR_ARG, "%s: E must be <= 2^27", what);
     if (h->r_size < 0 || 2 * h->r_size + 1 > h->n + (h->wot_i ? 1 : 0))
         return fl_fail(FL_ERR_ARG, "%s: w width %lld too small for r_size %lld", what, (long long)h->n,
                        (long long)h->r_size);
@@ -834,16 +1013,16 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     hipStream_t st = (hipStream_t)stream;
     const int64_t nnz = h->nnz;
     SpRows rows{p.row_item0, p.tile_base, NB};
-    if (NB > 1 && h->tiles * NB > 0)
-        FL_LAUNCH("k_fill_i32", k_fill_i32, dim3((unsigned)((h->tiles * NB + 255) / 256)), dim3(256), 0, st, x.hist,
-                  h->tiles * NB, 0);
     if (nnz > 0)
         FL_LAUNCH("k_sp_fill", k_sp_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n,
-                  h->r_size, h->wot_i, h->mode, p.th, p.cut, p.item_off, rows, x.hist, x.raw_dst, x.raw_val);
+                  h->r_size, h->wot_i, h->mode, p.th, p.cut, p.item_off, x.raw_dst, x.raw_val);
     int32_t *dst_arr = x.raw_dst, *raw_arr = nullptr;
     float *val_arr = x.raw_val;
     if (NB > 1) {
+        if (h->tiles > 0)
+            FL_LAUNCH("k_sp_hist", k_sp_hist, dim3((unsigned)h->tiles), dim3(SP_NT), sizeof(int) * (size_t)NB, st, R,
+                      rows, x.raw_dst, x.hist);
         if ((rc = exclusive_scan(st, x.hist, x.base, h->tiles * NB, x.tmp)) != FL_OK) return rc;
         if (h->tiles > 0)
             FL_LAUNCH("k_sp_partition", k_sp_partition, dim3((unsigned)h->tiles), dim3(SP_NT), 0, st, R, rows,
@@ -853,9 +1032,12 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         val_arr = x.part_val;
         raw_arr = raw_local ? x.part_raw : nullptr;
     }
-    if (R * NB > 0)
+    if (R * NB > 0) {
         FL_LAUNCH("k_sp_accum", k_sp_accum, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
                   val_arr, raw_arr, raw_local, x.out_count);
+        FL_LAUNCH("k_sp_accum_hot", k_sp_accum_hot, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base,
+                  dst_arr, val_arr, raw_arr, raw_local, x.out_count);
+    }
     if ((rc = exclusive_scan(st, x.out_count, out_base, R * NB, x.tmp)) != FL_OK) return rc;
     return fl_check_launch("sparse_expand");
 }

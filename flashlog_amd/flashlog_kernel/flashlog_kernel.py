@@ -989,6 +989,25 @@ def _coo(idx, vals, B, L, E):
     return torch.sparse_coo_tensor(idx, vals, [B, L, E], is_coalesced=True)
 
 
+_MASK_CACHE = {}
+
+
+def _cached_mask_order(mask_values, order):
+    """mask[order] as float, reused while the same (unmodified) mask and
+    order tensors are passed again (the top-k hop gets the raw per-edge mask
+    on every call; without edge weights its CSR-ordered form is fixed)."""
+    key = (mask_values.data_ptr(), mask_values._version, mask_values.numel(), order.data_ptr(), order._version,
+           order.numel())
+    hit = _MASK_CACHE.get(key)
+    if hit is not None and hit[0]() is mask_values and hit[1]() is order:
+        return hit[2]
+    for k in [k for k, v in _MASK_CACHE.items() if v[0]() is None or v[1]() is None]:
+        del _MASK_CACHE[k]
+    out = _apply_mask_order(mask_values.contiguous().view(-1), order, None)
+    _MASK_CACHE[key] = (weakref.ref(mask_values), weakref.ref(order), out)
+    return out
+
+
 class FlashLogFunctionSparse3DAllEdgesSum(autograd.Function):
     """Sparse sum hop over every edge, masked ones included as 0-valued
     coordinates (flashlog_kernel.py:1351-1447)."""
@@ -1045,6 +1064,9 @@ class FlashLogFunctionSparse3DTopKSum(autograd.Function):
             m = mask_f.float() * weight.to(device=mask_f.device, dtype=torch.float).view(-1)
             ori_mask = m[ori_order.long()].contiguous()
             inv_mask = m[inv_order.long()].contiguous()
+        elif weight is None:
+            ori_mask = _cached_mask_order(mask_values, ori_order)
+            inv_mask = _cached_mask_order(mask_values, inv_order)
         else:
             ori_mask = _apply_mask_order(mask_f, ori_order, weight)
             inv_mask = _apply_mask_order(mask_f, inv_order, weight)

@@ -230,7 +230,8 @@ typedef struct fl_sparse_hop {
     int64_t items, tiles;
 } fl_sparse_hop;
 
-/* Destination buckets per row (8192 entities each). */
+/* Destination buckets per row (8192 entities each).  The sparse hop
+ * supports E <= 2^27 entities. */
 int64_t fl_sparse_buckets(int64_t E);
 
 /* Plan workspace bytes for nnz entries and R = B*L rows. */

@@ -222,3 +222,37 @@ def test_cpu_sum_classes():
                                                          R, use_topk=True, topk_edges=4)
     nv, _ = O.sparse_normalize(keys // (L * E), (keys // E) % L, vals, B, L)
     np.testing.assert_allclose(outn.values().numpy(), nv, rtol=1e-6)
+
+
+@pytest.mark.parametrize("mode", ["all", "topk"])
+def test_sparse_hot_destination(mode):
+    """A destination receiving most edges: buckets far above one LDS chunk
+    (the chunked hot-bucket path), checked bit for bit, with gradients."""
+    from oracle import oracle as Oc
+    rng = np.random.default_rng(21)
+    E, R, M = 20000, 5, 60000
+    h = rng.integers(0, E, M)
+    t = np.where(rng.random(M) < 0.7, 12345, rng.integers(0, E, M))
+    r = rng.integers(0, R, M)
+    csr = Oc.build_csr_structure(h, t, r, E)
+    n = 2 * R + 1
+    B, L = 2, 2
+    b, l, e, v = sparse_coo_state(B, L, E, 1500, rng)
+    w = attention(B * L, n, rng).reshape(B, L, n)
+    mbool, masks = masks_for(csr, M, rng, drop=0.05)
+    state = (b, l, e, v)
+    if mode == "all":
+        keys, vals = O.sparse_forward(O.SPARSE_ALL, *state, B, L, E, w, csr, masks, R)
+        out, vt, wt = _all_edges(state, w, csr, masks, B, L, E, R, grad=True)
+        m, K = O.SPARSE_ALL, 1 << 60
+    else:
+        keys, vals = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, 6)
+        out, vt, wt = _topk(state, w, csr, mbool, B, L, E, R, 6, grad=True)
+        m, K = O.SPARSE_TOPK, 6
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+    g = rng.standard_normal(keys.shape[0]).astype(np.float32)
+    (out.values() * torch.from_numpy(g).cuda()).sum().backward()
+    gv_ref, gw_ref = O.sparse_backward(m, *state, B, L, E, w, csr, masks, R, keys, g, False, K)
+    np.testing.assert_allclose(vt.grad.cpu().numpy(), gv_ref, rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(wt.grad.reshape(B * L, n).cpu().numpy(), gw_ref, rtol=1e-4, atol=1e-3)
