@@ -38,7 +38,20 @@ def parse():
     ap.add_argument("--profile-steps", type=int, default=10)
     ap.add_argument("--sparse", action="store_true",
                     help="the DRUM --sparse GPU path (default for --config 5)")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="first run 3 plain device copies of this many MiB (a known-size reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
+
+
+def copy_calibration(mb):
+    import torch
+    x = torch.ones(mb * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print("copy calibration: 3 copies of %d MiB" % mb, file=sys.stderr, flush=True)
 
 
 def c2_admitted(wv, cnt, K):
@@ -107,6 +120,8 @@ def main():
     from flashlog_amd import _lib, synth
     from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
 
+    if args.copy_mb > 0:
+        copy_calibration(args.copy_mb)
     if args.sparse or args.config == 5:
         return main_sparse(args)
     cfg = synth.CONFIGS[args.config]
