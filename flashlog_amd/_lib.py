@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 FL_SEG = 32
 FL_SUP = 16
 
@@ -59,7 +59,7 @@ class FlSparseHop(ctypes.Structure):
         ("r_size", ctypes.c_int64), ("wot_i", ctypes.c_int), ("mode", ctypes.c_int),
         ("topk_edges", ctypes.c_int64), ("ws1", ctypes.c_void_p), ("ws1_bytes", ctypes.c_size_t),
         ("ws2", ctypes.c_void_p), ("ws2_bytes", ctypes.c_size_t), ("items", ctypes.c_int64),
-        ("tiles", ctypes.c_int64),
+        ("tiles", ctypes.c_int64), ("operators", ctypes.c_void_p),
     ]
 
 
@@ -113,6 +113,10 @@ _SIGS = {
                                     [ctypes.c_float] + [ctypes.c_void_p] * 4),
     "fl_sparse_normalize_backward": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_float,
                                                                             ctypes.c_void_p]),
+    "fl_rule_accumulate": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_void_p] +
+                           [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_void_p]),
+    "fl_rule_finalize": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 3 +
+                         [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
     "fl_filtered_ranks_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int]),
     "fl_filtered_ranks": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int] + [ctypes.c_void_p] * 2 +
                           [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,

@@ -1,0 +1,104 @@
+// Rule-bank scoring accumulators (rules/shared_inference.py:12-245, the
+// dense-accumulator branch :87-96,200-206,224-237).
+//
+// A chunk of rules has been grounded for every source b: a COO state
+// (b, rule l, entity e, v) with v the path count (or 0/1 with Boolean paths).
+// Per rank k the scores are
+//   sum:  S_k[b, e] += v * W[rule, k]
+//   max:  S_k[b, e]  = max(S_k[b, e], v * W[rule, k])      (W >= 0)
+// accumulated over chunks in a dense [K, B*E] buffer; then every (k, b) row
+// is normalized by its sum (clamped to 1e-30) and the ranks are summed (or
+// maxed with final_max) into one [B*E] score.
+#include "fl_abi.h"
+#include "fl_common.h"
+
+namespace fl {
+
+constexpr int RB_NT = 256;
+
+// Thread per state entry.  Sums use float atomics (run-dependent last bits,
+// as the reference's index_add_); maxima of nonnegative values use the
+// integer order of their bits, which is exact.
+__global__ __launch_bounds__(RB_NT) void k_rule_accum(const int64_t *__restrict__ sb,
+                                                     const int64_t *__restrict__ sl,
+                                                     const int64_t *__restrict__ se,
+                                                     const float *__restrict__ sv, int64_t nnz,
+                                                     const float *__restrict__ W, int64_t K, int64_t B, int64_t E,
+                                                     int is_max, float *__restrict__ dense) {
+    const int64_t i = (int64_t)blockIdx.x * RB_NT + threadIdx.x;
+    if (i >= nnz) return;
+    const int64_t key = sb[i] * E + se[i];
+    const float v = sv[i];
+    const float *wr = W + sl[i] * K;
+    for (int64_t k = 0; k < K; ++k) {
+        const float x = fl_mul(v, wr[k]);
+        float *slot = dense + k * B * E + key;
+        if (is_max) {
+            if (x > 0.0f) atomicMax((unsigned int *)slot, __float_as_uint(x));
+        } else if (x != 0.0f) {
+            atomicAdd(slot, x);
+        }
+    }
+}
+
+// Workgroup per (k, b): the row's sum in a fixed order.
+__global__ __launch_bounds__(RB_NT) void k_rule_rowsum(const float *__restrict__ dense, int64_t E,
+                                                      float *__restrict__ rowsum) {
+    __shared__ float red[RB_NT];
+    const float *row = dense + (int64_t)blockIdx.x * E;
+    float s = 0.0f;
+    for (int64_t e = threadIdx.x; e < E; e += RB_NT) s = fl_add(s, row[e]);
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int st = RB_NT / 2; st > 0; st >>= 1) {
+        if ((int)threadIdx.x < st) red[threadIdx.x] = fl_add(red[threadIdx.x], red[threadIdx.x + st]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) rowsum[blockIdx.x] = red[0];
+}
+
+// Thread per (b, e): the normalized ranks combined in rank order.
+__global__ __launch_bounds__(RB_NT) void k_rule_combine(const float *__restrict__ dense,
+                                                       const float *__restrict__ rowsum, int64_t K, int64_t B,
+                                                       int64_t E, int final_max, float *__restrict__ total) {
+    const int64_t q = (int64_t)blockIdx.x * RB_NT + threadIdx.x;
+    if (q >= B * E) return;
+    const int64_t b = q / E;
+    float t = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+        const float x = dense[k * B * E + q];
+        if (x == 0.0f) continue;
+        const float d = rowsum[k * B + b];
+        const float p = __fdiv_rn(x, d < 1e-30f ? 1e-30f : d);
+        t = final_max ? (p > t ? p : t) : fl_add(t, p);
+    }
+    total[q] = t;
+}
+
+}  // namespace fl
+
+extern "C" {
+
+int fl_rule_accumulate(void *stream, const int64_t *sb, const int64_t *sl, const int64_t *se, const float *sv,
+                       int64_t nnz, const float *W, int64_t K, int64_t B, int64_t E, int is_max, float *dense) {
+    if (nnz < 0 || K < 1 || B < 0 || E < 0) return fl::fl_fail(FL_ERR_ARG, "rule_accumulate: bad shape");
+    if (nnz == 0) return FL_OK;
+    if (!sb || !sl || !se || !sv || !W || !dense) return fl::fl_fail(FL_ERR_ARG, "rule_accumulate: null pointer");
+    FL_LAUNCH("k_rule_accum", fl::k_rule_accum, dim3((unsigned)((nnz + fl::RB_NT - 1) / fl::RB_NT)), dim3(fl::RB_NT),
+              0, (hipStream_t)stream, sb, sl, se, sv, nnz, W, K, B, E, is_max, dense);
+    return fl::fl_check_launch("rule_accumulate");
+}
+
+int fl_rule_finalize(void *stream, const float *dense, int64_t K, int64_t B, int64_t E, int final_max,
+                     float *rowsum, float *total) {
+    if (K < 1 || B < 0 || E < 0) return fl::fl_fail(FL_ERR_ARG, "rule_finalize: bad shape");
+    if (B * E == 0) return FL_OK;
+    if (!dense || !rowsum || !total) return fl::fl_fail(FL_ERR_ARG, "rule_finalize: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_rule_rowsum", fl::k_rule_rowsum, dim3((unsigned)(K * B)), dim3(fl::RB_NT), 0, st, dense, E, rowsum);
+    FL_LAUNCH("k_rule_combine", fl::k_rule_combine, dim3((unsigned)((B * E + fl::RB_NT - 1) / fl::RB_NT)),
+              dim3(fl::RB_NT), 0, st, dense, rowsum, K, B, E, final_max, total);
+    return fl::fl_check_launch("rule_finalize");
+}
+
+}  // extern "C"

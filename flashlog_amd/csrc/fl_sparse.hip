@@ -42,7 +42,7 @@ constexpr int SP_NT = 256;
 constexpr int SP_IPT = 16;
 constexpr int SP_TILE = SP_NT * SP_IPT;  // items per partition tile
 
-enum { SP_TOPK = 0, SP_ALL = 1 };
+enum { SP_TOPK = 0, SP_ALL = 1, SP_FIXED = 2 };
 
 // ---------------------------------------------------------------------------
 // plan
@@ -181,6 +181,79 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
         }
     }
     if (lane == 0) cnt[i] = total;
+}
+
+// Fixed-relation rule step (flashlog.cu:1561-1741): entry (b, l, e, v) with
+// operator op = operators[b*L + l] goes to every edge of its (e, op) group
+// with the value unchanged (op < R: ORI relation op; R <= op < 2R: INV
+// relation op - R; op == 2R: the identity, one item at e).  No masks and no
+// budgets.  k_fx_count: thread per entry, the group by binary search over
+// the source's group relations (stored in cut[2i], side in cut[2i+1]).
+__device__ __forceinline__ int64_t fx_find_group(const fl_side &s, int64_t src, int rel) {
+    int64_t lo = s.row_group_ptr[src], hi = s.row_group_ptr[src + 1];
+    const int64_t end = hi;
+    while (lo < hi) {
+        const int64_t mid = lo + ((hi - lo) >> 1);
+        if ((int)s.group_rel[mid] < rel) lo = mid + 1;
+        else hi = mid;
+    }
+    return (lo < end && (int)s.group_rel[lo] == rel) ? lo : -1;
+}
+
+__global__ void k_fx_count(fl_side ori, fl_side inv, const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
+                           const int64_t *__restrict__ se, const int64_t *__restrict__ ops, int64_t nnz, int64_t B,
+                           int64_t L, int64_t E, int64_t R, int32_t *__restrict__ cut, int32_t *__restrict__ cnt) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    const int64_t b = sb[i], l = sl[i], src = se[i];
+    int32_t c = 0, g = -1, side = 0;
+    if (b >= 0 && b < B && l >= 0 && l < L && src >= 0 && src < E) {
+        const int64_t op = ops[b * L + l];
+        if (op == 2 * R) {
+            c = 1;
+            side = 2;
+        } else if (op >= 0 && op < 2 * R) {
+            side = op >= R ? 1 : 0;
+            const fl_side &s = side ? inv : ori;
+            const int64_t gg = fx_find_group(s, src, (int)(side ? op - R : op));
+            if (gg >= 0) {
+                g = (int32_t)gg;
+                c = s.group_count[gg];
+            }
+        }
+    }
+    cut[2 * i] = g;
+    cut[2 * i + 1] = side;
+    cnt[i] = c;
+}
+
+// Wave per entry: the entry's items (group columns, or itself) at item_off[i].
+__global__ __launch_bounds__(SEL_NT) void k_fx_fill(fl_side ori, fl_side inv, const int64_t *__restrict__ se,
+                                                   const float *__restrict__ sv, int64_t nnz,
+                                                   const int32_t *__restrict__ cut,
+                                                   const int64_t *__restrict__ item_off,
+                                                   int32_t *__restrict__ raw_dst, float *__restrict__ raw_val) {
+    const int lane = fl_lane();
+    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
+    if (i >= nnz) return;
+    const int64_t pos = item_off[i];
+    const int64_t c = item_off[i + 1] - pos;
+    if (c == 0) return;
+    const float v = sv[i];
+    const int32_t side = cut[2 * i + 1];
+    if (side == 2) {
+        if (lane == 0) {
+            raw_dst[pos] = (int32_t)se[i];
+            raw_val[pos] = v;
+        }
+        return;
+    }
+    const fl_side &s = side ? inv : ori;
+    const int64_t start = s.group_start[cut[2 * i]];
+    for (int64_t k = lane; k < c; k += FL_WAVE) {
+        raw_dst[pos + k] = s.col_ind[start + k];
+        raw_val[pos + k] = v;
+    }
 }
 
 // Per row r (and r = R): first item and tile count.
@@ -939,14 +1012,18 @@ int sp_check(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, con
     if (h->nnz < 0 || h->B < 0 || h->L < 0 || h->E < 0 || h->n < 1)
         return fl_fail(FL_ERR_ARG, "%s: bad shape", what);
     if (h->E > ((int64_t)SP_W << 14)) return fl_fail(FL_ERR_ARG, "%s: E must be <= 2^27", what);
-    if (h->r_size < 0 || 2 * h->r_size + 1 > h->n + (h->wot_i ? 1 : 0))
+    if (h->mode != SP_TOPK && h->mode != SP_ALL && h->mode != SP_FIXED)
+        return fl_fail(FL_ERR_ARG, "%s: unknown mode", what);
+    if (h->mode != SP_FIXED && (h->r_size < 0 || 2 * h->r_size + 1 > h->n + (h->wot_i ? 1 : 0)))
         return fl_fail(FL_ERR_ARG, "%s: w width %lld too small for r_size %lld", what, (long long)h->n,
                        (long long)h->r_size);
-    if (h->mode != SP_TOPK && h->mode != SP_ALL) return fl_fail(FL_ERR_ARG, "%s: unknown mode", what);
-    if (h->nnz > 0 && (!h->sp_b || !h->sp_l || !h->sp_e || !h->sp_v || !h->w))
+    if (h->nnz > 0 && (!h->sp_b || !h->sp_l || !h->sp_e || !h->sp_v))
         return fl_fail(FL_ERR_ARG, "%s: null input", what);
+    if (h->nnz > 0 && h->mode != SP_FIXED && !h->w) return fl_fail(FL_ERR_ARG, "%s: null attention", what);
+    if (h->nnz > 0 && h->mode == SP_FIXED && !h->operators) return fl_fail(FL_ERR_ARG, "%s: null operators", what);
     for (const fl_side *s : {ori, inv})
-        if (s->edges > 0 && (!s->col_ind || !s->mask || !s->group_rel || !s->group_start || !s->group_count))
+        if (s->edges > 0 && (!s->col_ind || (!s->mask && h->mode != SP_FIXED) || !s->group_rel ||
+                             !s->group_start || !s->group_count))
             return fl_fail(FL_ERR_ARG, "%s: side without CSR arrays", what);
     return FL_OK;
 }
@@ -981,7 +1058,10 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
     FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, h->sp_b, h->sp_l,
               h->sp_e, nnz, h->B, h->L, h->E, p.row_ptr, plan + 2);
-    if (nnz > 0)
+    if (nnz > 0 && h->mode == SP_FIXED)
+        FL_LAUNCH("k_fx_count", k_fx_count, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, *ori, *inv,
+                  h->sp_b, h->sp_l, h->sp_e, h->operators, nnz, h->B, h->L, h->E, h->r_size, p.cut, p.cnt);
+    else if (nnz > 0)
         FL_LAUNCH("k_sp_select", k_sp_select, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
                   h->r_size, h->wot_i, h->mode, K, p.th, p.cut, p.cnt);
@@ -1013,7 +1093,10 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     hipStream_t st = (hipStream_t)stream;
     const int64_t nnz = h->nnz;
     SpRows rows{p.row_item0, p.tile_base, NB};
-    if (nnz > 0)
+    if (nnz > 0 && h->mode == SP_FIXED)
+        FL_LAUNCH("k_fx_fill", k_fx_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_e, h->sp_v, nnz, p.cut, p.item_off, x.raw_dst, x.raw_val);
+    else if (nnz > 0)
         FL_LAUNCH("k_sp_fill", k_sp_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n,
                   h->r_size, h->wot_i, h->mode, p.th, p.cut, p.item_off, x.raw_dst, x.raw_val);

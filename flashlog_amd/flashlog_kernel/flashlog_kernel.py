@@ -713,7 +713,24 @@ def sparse2d_filtered_ranks_cuda(idx_b, idx_e, values, targets, filter_keys, B, 
 
 
 def vectorized_operation_sparse3d_fixed_relation(sp_state, operators, csr_struct, r_size):
-    _not_yet("vectorized_operation_sparse3d_fixed_relation")
+    """Advance sparse rule levels through one fixed relation per level
+    (flashlog_kernel.py:182-210).  ``operators`` is shaped ``[B, L]`` with the
+    FlashLog operator ids: forward relations, inverse relations offset by
+    ``r_size`` and the identity at ``2 * r_size``.  Values are carried
+    unchanged and summed per endpoint (path counts)."""
+    if not sp_state.is_cuda:
+        raise ValueError("fixed-relation rule inference currently requires CUDA")
+    sp_state = sp_state.coalesce()
+    indices = sp_state.indices()
+    values = sp_state.values()
+    B, L, E = sp_state.shape
+    if tuple(operators.shape) != (B, L):
+        raise ValueError("operators must have shape [{}, {}], got {}".format(B, L, tuple(operators.shape)))
+    sides = _fixed_sides(csr_struct)
+    idx, vals, _ = _sparse_forward(indices[0], indices[1], indices[2], values.float(), None, sides, B, L, E,
+                                   int(r_size), False, _SPARSE_FIXED, 0, False,
+                                   operators=operators.to(device=values.device, dtype=torch.int64).contiguous())
+    return _coo(idx, vals.to(values.dtype), int(B), int(L), int(E))
 
 
 class FlashLogDenseMaxFunction(autograd.Function):
@@ -794,7 +811,7 @@ def sampled_sparse_propagation(state, w, csr_struct, mask_values, r_size, weight
 # (b, l, entity) in the CPU path's addition order (fl_sparse_* in
 # libflashlog_hip.so).
 
-_SPARSE_TOPK, _SPARSE_ALL = 0, 1
+_SPARSE_TOPK, _SPARSE_ALL, _SPARSE_FIXED = 0, 1, 2
 
 
 class _SparseSides:
@@ -807,19 +824,21 @@ class _SparseSides:
         self.inv = self._side(inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount)
 
     def _side(self, col, mask, gptr, grel, gstart, gcount):
-        _require_cuda(col, mask, gptr, grel, gstart, gcount)
+        _require_cuda(col, gptr, grel, gstart, gcount)
         col = col.int().contiguous()
-        mask = mask.float().contiguous()
         gptr = gptr.int().contiguous()
         grel = grel.short().contiguous()
         gstart = gstart.int().contiguous()
         gcount = gcount.int().contiguous()
-        if mask.numel() != col.numel():
-            raise ValueError("mask length must equal the number of CSR positions")
+        if mask is not None:
+            _require_cuda(mask)
+            mask = mask.float().contiguous()
+            if mask.numel() != col.numel():
+                raise ValueError("mask length must equal the number of CSR positions")
         self.keep += [col, mask, gptr, grel, gstart, gcount]
         side = FlSide()
         side.edges, side.groups = col.numel(), grel.numel()
-        side.col_ind, side.mask = ptr(col).value, ptr(mask).value
+        side.col_ind, side.mask = ptr(col).value, (ptr(mask).value if mask is not None else None)
         side.row_group_ptr, side.group_rel = ptr(gptr).value, ptr(grel).value
         side.group_start, side.group_count = ptr(gstart).value, ptr(gcount).value
         side.max_rel = int(grel.max()) if grel.numel() else -1
@@ -831,9 +850,9 @@ class _SparseState:
 
 
 def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mode, topk_edges,
-                    need_backward):
+                    need_backward, operators=None):
     """Runs plan -> expand -> emit.  Returns (indices [3, nout], values, state)."""
-    _require_cuda(sp_b, sp_l, sp_e, sp_v, w)
+    _require_cuda(sp_b, sp_l, sp_e, sp_v)
     dev = sp_v.device
     B, L, E, r_size = int(B), int(L), int(E), int(r_size)
     R = B * L
@@ -843,10 +862,15 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     sp_v = sp_v.contiguous()
     if sp_v.dtype != torch.float32:
         raise TypeError("flashlog_amd sparse propagation computes in float32")
-    w_flat = w.reshape(R, -1).contiguous().float()
-    n = w_flat.shape[1]
-    if max(sides.ori.max_rel, sides.inv.max_rel) >= r_size or 2 * r_size > n:
-        raise ValueError("relation ids must be < r_size and w must hold 2*r_size (+1) columns")
+    if mode == _SPARSE_FIXED:
+        w_flat = torch.zeros(1, dtype=torch.float32, device=dev)
+        n = 1
+    else:
+        _require_cuda(w)
+        w_flat = w.reshape(R, -1).contiguous().float()
+        n = w_flat.shape[1]
+        if max(sides.ori.max_rel, sides.inv.max_rel) >= r_size or 2 * r_size > n:
+            raise ValueError("relation ids must be < r_size and w must hold 2*r_size (+1) columns")
     nnz = sp_v.numel()
     lib = _lib.lib()
     st = _stream(sp_v)
@@ -857,6 +881,7 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         h.nnz, h.w = nnz, ptr(w_flat).value
         h.B, h.L, h.E, h.n, h.r_size = B, L, E, n, r_size
         h.wot_i, h.mode, h.topk_edges = 1 if wot_i else 0, int(mode), int(topk_edges)
+        h.operators = ptr(operators).value if operators is not None else None
         ws1 = torch.empty(max(lib.fl_sparse_plan_bytes(nnz, R), 1), dtype=torch.uint8, device=dev)
         h.ws1, h.ws1_bytes = ptr(ws1).value, ws1.numel()
         plan = torch.empty(4, dtype=torch.int64, device=dev)
@@ -866,6 +891,7 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         if err == 2 and attempt == 0:
             # rows out of order: process them in row order, entries of a row in input order
             perm = torch.argsort(sp_b * L + sp_l, stable=True)
+            # (operators are per row, unaffected by the entry order)
             sp_b, sp_l, sp_e, sp_v = sp_b[perm], sp_l[perm], sp_e[perm], sp_v[perm].contiguous()
             continue
         if err:
@@ -892,6 +918,24 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         state.out_base, state.raw_local, state.nout, state.n = out_base, raw_local, nout, n
     del ws2
     return idx, vals, state
+
+
+def _fixed_sides(csr_struct):
+    """Sides for the fixed-relation step (no masks): cached per CSR tuple."""
+    keyed = (csr_struct[1], csr_struct[8], csr_struct[10], csr_struct[5], csr_struct[12], csr_struct[14])
+    key = tuple((t.data_ptr(), t.numel(), t._version) for t in keyed)
+    hit = _FIXED_SIDES.get(key)
+    if hit is not None and all(r() is t for r, t in zip(hit[0], keyed)):
+        return hit[1]
+    for k in [k for k, v in _FIXED_SIDES.items() if any(r() is None for r in v[0])]:
+        del _FIXED_SIDES[k]
+    sides = _SparseSides(csr_struct[1], None, csr_struct[8], csr_struct[9], csr_struct[10], csr_struct[11],
+                         csr_struct[5], None, csr_struct[12], csr_struct[13], csr_struct[14], csr_struct[15])
+    _FIXED_SIDES[key] = (tuple(weakref.ref(t) for t in keyed), sides)
+    return sides
+
+
+_FIXED_SIDES = {}
 
 
 def _sparse_backward(state, grad_values):

@@ -209,8 +209,11 @@ int fl_dense_max_backward(void *stream, const fl_side *ori, const fl_side *inv,
  * coalesced state is), attention w [B*L, n], and the caller's workspaces.
  * mode 0 = top-k sum (kept edges with a nonzero mask; FlashLogFunction-
  * Sparse3DTopKSum, flashlog.cu:1368-1559), mode 1 = all edges
- * (FlashLogFunctionSparse3DAllEdgesSum, flashlog.cu:1743-1829).  items /
- * tiles come from fl_sparse_plan's plan[0] / plan[1]. */
+ * (FlashLogFunctionSparse3DAllEdgesSum, flashlog.cu:1743-1829), mode 2 =
+ * fixed-relation rule step (flashlog_forward_sparse3d_fixed_relation_cuda,
+ * flashlog.cu:1561-1741: row (b, l) follows operators[b*L + l], values
+ * unchanged, no masks; w, n and wot_i unused, r_size = base relations).
+ * items / tiles come from fl_sparse_plan's plan[0] / plan[1]. */
 typedef struct fl_sparse_hop {
     const int64_t *sp_b, *sp_l, *sp_e;  /* [nnz] */
     const float *sp_v;                 /* [nnz] */
@@ -228,6 +231,7 @@ typedef struct fl_sparse_hop {
     void *ws2;                         /* expansion workspace */
     size_t ws2_bytes;
     int64_t items, tiles;
+    const int64_t *operators;          /* mode 2: [B*L] operator per row     */
 } fl_sparse_hop;
 
 /* Destination buckets per row (8192 entities each).  The sparse hop
@@ -307,6 +311,24 @@ int fl_sparse_normalize_backward(void *stream, const int64_t *row_ptr,
                                  const float *grad, const float *v,
                                  const float *denom, int64_t R, float eps,
                                  float *grad_v);
+
+/* ---- rule-bank scoring ------------------------------------------------- */
+
+/* Replaces the dense accumulation of rules/shared_inference.py:200-206: the
+ * grounded COO state of a rule chunk (b, rule l, entity e, v) is added
+ * into dense [K, B*E] as v * W[l, k] (is_max = 0, float atomics) or maxed
+ * into it (is_max = 1; values >= 0, exact). */
+int fl_rule_accumulate(void *stream, const int64_t *sb, const int64_t *sl,
+                       const int64_t *se, const float *sv, int64_t nnz,
+                       const float *W, int64_t K, int64_t B, int64_t E,
+                       int is_max, float *dense);
+
+/* Replaces the finalization of rules/shared_inference.py:224-237: rowsum
+ * [K*B] = per (rank, source) row sums (fixed order); total [B*E] = over ranks
+ * in order, the sum (or max with final_max) of dense / max(rowsum, 1e-30)
+ * at the nonzero entries. */
+int fl_rule_finalize(void *stream, const float *dense, int64_t K, int64_t B,
+                     int64_t E, int final_max, float *rowsum, float *total);
 
 /* ---- evaluation --------------------------------------------------------- */
 

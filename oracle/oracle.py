@@ -384,3 +384,92 @@ def sparse_topc(b, l, v, L, c):
         order = nz[np.lexsort((np.arange(nz.size), -v[nz].astype(np.float64)))]
         keep[order[:c]] = True
     return np.nonzero(keep)[0]
+
+
+# --------------------------------------------------------------------------
+# Rule-bank scoring: rules/shared_inference.py:12-245 and the fixed-relation
+# step flashlog.cu:1561-1741 (float64, from the raw triples)
+
+def _op_matrix(h, r, t, E, R, op):
+    """Operator op as an E x E path-count matrix: op < R the relation,
+    R <= op < 2R its inverse, op == 2R the identity."""
+    import scipy.sparse as sp
+    if op == 2 * R:
+        return sp.identity(E, format="csr", dtype=np.float64)
+    rel = op if op < R else op - R
+    sel = np.asarray(r) == rel
+    src, dst = (np.asarray(h)[sel], np.asarray(t)[sel]) if op < R else (np.asarray(t)[sel], np.asarray(h)[sel])
+    return sp.csr_matrix((np.ones(src.shape[0]), (src, dst)), shape=(E, E))
+
+
+def fixed_relation_step(b, l, e, v, ops, h, r, t, E, R):
+    """{(b, l, e'): value}: every entry follows its row's operator through
+    every matching triple, values summed per endpoint."""
+    out = {}
+    h, r, t = (np.asarray(x) for x in (h, r, t))
+    for bi, li, ei, vi in zip(np.asarray(b), np.asarray(l), np.asarray(e), np.asarray(v, np.float64)):
+        op = int(ops[bi][li])
+        if op == 2 * R:
+            dsts = [ei]
+        elif 0 <= op < R:
+            dsts = t[(h == ei) & (r == op)]
+        elif R <= op < 2 * R:
+            dsts = h[(t == ei) & (r == op - R)]
+        else:
+            dsts = []
+        for d in dsts:
+            key = (int(bi), int(li), int(d))
+            out[key] = out.get(key, 0.0) + float(vi)
+    return out
+
+
+def rule_scores(h, r, t, E, R, sources, bodies, W, reduction="sum", boolean_paths=False, final_max=False):
+    """Dense [B, E] float64 scores: per rule the path-count vector
+    e_s^T M_op1 M_op2 ... (Boolean after every step when boolean_paths or
+    max), per rank the weighted sum (or max) over rules, each (rank, source)
+    row divided by max(its sum, 1e-30), ranks summed (or maxed)."""
+    boolean_paths = boolean_paths or reduction == "max"
+    W = np.asarray(W, np.float64)
+    mats = {}
+    B, K = len(sources), W.shape[1]
+    S = np.zeros((K, B, E))
+    for ri, body in enumerate(bodies):
+        for bi, s in enumerate(sources):
+            x = np.zeros(E)
+            x[s] = 1.0
+            for op in body:
+                if op not in mats:
+                    mats[op] = _op_matrix(h, r, t, E, R, op)
+                x = mats[op].T @ x
+                if boolean_paths:
+                    x = (x > 0).astype(np.float64)
+            for k in range(K):
+                if reduction == "max":
+                    S[k, bi] = np.maximum(S[k, bi], W[ri, k] * (x > 0))
+                else:
+                    S[k, bi] += W[ri, k] * x
+    total = np.zeros((B, E))
+    for k in range(K):
+        d = np.maximum(S[k].sum(1, keepdims=True), 1e-30)
+        part = S[k] / d
+        total = np.maximum(total, part) if final_max else total + part
+    return total
+
+
+def rule_paths_brute(h, r, t, R, source, body):
+    """Path counts by explicit enumeration of the edge sequences (tiny graphs)."""
+    h, r, t = (list(map(int, x)) for x in (h, r, t))
+    ends = {source: 1}
+    for op in body:
+        nxt = {}
+        for node, cnt in ends.items():
+            if op == 2 * R:
+                nxt[node] = nxt.get(node, 0) + cnt
+                continue
+            for hh, rr, tt in zip(h, r, t):
+                if op < R and rr == op and hh == node:
+                    nxt[tt] = nxt.get(tt, 0) + cnt
+                elif R <= op < 2 * R and rr == op - R and tt == node:
+                    nxt[hh] = nxt.get(hh, 0) + cnt
+        ends = nxt
+    return ends

@@ -84,7 +84,13 @@ def main():
     cases["specs"] = np.array([[s[0], s[1], s[2], s[3], s[4], s[5]] for s in specs], np.int64)
     np.savez_compressed(os.path.join(HERE, "dense_golden.npz"), **cases)
 
-    # API surface of the reference package (names + parameters only)
+    write_api_surface()
+    print("wrote", len(cases), "arrays")
+
+
+def write_api_surface():
+    """Signatures (names and parameter names only) of the reference's
+    operator module and rule-scoring entry points, parsed with ast."""
     src = open(os.path.join(REF, "flashlog_kernel", "flashlog_kernel.py")).read()
     tree = ast.parse(src)
     surface = {}
@@ -96,8 +102,18 @@ def main():
                 if isinstance(sub, ast.FunctionDef) and sub.name in ("forward", "backward"):
                     surface["%s.%s" % (node.name, sub.name)] = [a.arg for a in sub.args.args]
     json.dump(surface, open(os.path.join(HERE, "api_surface.json"), "w"), indent=1, sort_keys=True)
-    print("wrote", len(cases), "arrays and", len(surface), "signatures")
+    rules = {}
+    for mod in ("shared_inference", "max_inference"):
+        tree = ast.parse(open(os.path.join(REF, "rules", mod + ".py")).read())
+        for node in tree.body:
+            if isinstance(node, ast.FunctionDef) and node.name == "score":
+                rules["%s.score" % mod] = [a.arg for a in node.args.args]
+    json.dump(rules, open(os.path.join(HERE, "rules_surface.json"), "w"), indent=1, sort_keys=True)
+    print("wrote", len(surface) + len(rules), "signatures")
 
 
 if __name__ == "__main__":
-    main()
+    if "--api-only" in sys.argv:
+        write_api_surface()
+    else:
+        main()

@@ -56,3 +56,14 @@ def test_package_exports():
               "vectorized_operation_csr", "vectorized_operation_sparse3d_csr_sum",
               "vectorized_operation_sparse3d_csr_sum_norm", "vectorized_operation_sparse3d_fixed_relation"):
         assert hasattr(flashlog_kernel, n)
+
+
+RULES = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "rules_surface.json")))
+
+
+@pytest.mark.parametrize("name", sorted(RULES))
+def test_rules_signature_matches_reference(name):
+    import importlib
+    mod, fn = name.split(".")
+    obj = getattr(importlib.import_module("flashlog_amd.rules." + mod), fn)
+    assert list(inspect.signature(obj).parameters) == RULES[name]

@@ -1,0 +1,79 @@
+"""GPU parity of the fixed-relation rule step and of the rule-bank scores
+against the float64 oracle (tests/test_oracle_rules.py pins it)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import small_graph, to_torch_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def _fk():
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+    return fk
+
+
+def test_fixed_relation_step_exact():
+    fk = _fk()
+    rng = np.random.default_rng(4)
+    h, r, t, E, R, csr = small_graph(3, 0.02)
+    B, L = 3, 5
+    rows = []
+    for b in range(B):
+        for l in range(L):
+            for e in np.sort(rng.choice(E, 6, replace=False)):
+                rows.append((b, l, e, float(rng.integers(1, 4))))
+    b, l, e, v = (np.array(x) for x in zip(*rows))
+    ops = rng.integers(0, 2 * R + 1, (B, L))
+    ops[0, 0] = 2 * R       # identity
+    ops[1, 1] = 2 * R + 5   # no such operator: no output
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    st = torch.sparse_coo_tensor(torch.from_numpy(np.stack([b, l, e])).cuda(),
+                                 torch.from_numpy(v.astype(np.float32)).cuda(), (B, L, E)).coalesce()
+    out = fk.vectorized_operation_sparse3d_fixed_relation(st, torch.from_numpy(ops).cuda(), tc, R)
+    want = O.fixed_relation_step(b, l, e, v, ops, h, r, t, E, R)
+    idx = out.indices().cpu().numpy()
+    got = {(int(a), int(c), int(d)): float(x) for a, c, d, x in zip(*idx, out.values().cpu().numpy())}
+    assert got == want
+    assert out.is_coalesced()
+
+
+@pytest.mark.parametrize("reduction,boolean,final_max", [("sum", False, False), ("sum", True, False),
+                                                         ("max", True, False), ("max", True, True)])
+@pytest.mark.parametrize("chunk", [1, 7, 64])
+def test_rule_scores(reduction, boolean, final_max, chunk):
+    from flashlog_amd.rules import shared_inference
+    rng = np.random.default_rng(10 + chunk)
+    h, r, t, E, R, csr = small_graph(3, 0.02)
+    bodies = [list(map(int, rng.integers(0, 2 * R + 1, rng.integers(1, 4)))) for _ in range(40)]
+    bodies.append([])  # empty body: the source itself
+    W = rng.random((len(bodies), 3)).astype(np.float32)
+    rules = [{"body": bd, "rank_weights": list(map(float, w))} for bd, w in zip(bodies, W)]
+    sources = rng.integers(0, E, 5)
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    stats = {}
+    out = shared_inference.score(None, torch.from_numpy(sources).cuda(), rules, tc, R, E, chunk,
+                                 final_max=final_max, reduction=reduction, boolean_paths=boolean,
+                                 dense_budget_bytes=2 * 3 * E * 4, stats=stats)
+    want = O.rule_scores(h, r, t, E, R, list(sources), bodies, W.astype(np.float64), reduction, boolean,
+                         final_max)
+    got = out.to_dense().cpu().numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-7)
+    assert stats["chunks"] >= 1 and stats["rules_after"] <= stats["rules_before"]
+
+
+def test_rule_scores_edges():
+    from flashlog_amd.rules import max_inference, shared_inference
+    h, r, t, E, R, csr = small_graph(3, 0.02)
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    src = torch.tensor([1, 2], device="cuda")
+    assert shared_inference.score(None, src, [], tc, R, E, 4)._nnz() == 0
+    with pytest.raises(ValueError):
+        shared_inference.score(None, src, [{"body": [2 * R], "rank_weights": [-1.0]}], tc, R, E, 4)
+    with pytest.raises(ValueError):
+        shared_inference.score(None, src, [{"body": [0], "rank_weights": [1.0]}], tc, R, E, 4, reduction="mean")
+    rules = [{"body": [2 * R], "rank_weights": [0.5]}]
+    out = max_inference.score(None, src, rules, tc, R, E, 4)
+    assert out.to_dense()[0, 1].item() == 1.0 and out.to_dense()[1, 2].item() == 1.0
