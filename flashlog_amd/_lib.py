@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 FL_SEG = 32
 FL_SUP = 16
 
@@ -47,6 +47,7 @@ class FlSide(ctypes.Structure):
         ("sup_seg0", ctypes.c_void_p),
         ("pos_src", ctypes.c_void_p),
         ("pos_rel", ctypes.c_void_p),
+        ("order", ctypes.c_void_p),
     ]
 
 
@@ -59,7 +60,8 @@ class FlSparseHop(ctypes.Structure):
         ("r_size", ctypes.c_int64), ("wot_i", ctypes.c_int), ("mode", ctypes.c_int),
         ("topk_edges", ctypes.c_int64), ("ws1", ctypes.c_void_p), ("ws1_bytes", ctypes.c_size_t),
         ("ws2", ctypes.c_void_p), ("ws2_bytes", ctypes.c_size_t), ("items", ctypes.c_int64),
-        ("tiles", ctypes.c_int64), ("operators", ctypes.c_void_p),
+        ("tiles", ctypes.c_int64), ("operators", ctypes.c_void_p), ("aggregate", ctypes.c_int),
+        ("sampling_seed", ctypes.c_int64),
     ]
 
 
@@ -101,7 +103,7 @@ _SIGS = {
     "fl_sparse_plan_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
     "fl_sparse_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                       ctypes.POINTER(FlSparseHop), ctypes.c_void_p]),
-    "fl_sparse_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int]),
+    "fl_sparse_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int] * 2),
     "fl_sparse_expand": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                         ctypes.POINTER(FlSparseHop), ctypes.c_void_p, ctypes.c_void_p]),
     "fl_sparse_emit": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
@@ -109,6 +111,11 @@ _SIGS = {
                                           ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
     "fl_sparse_topc": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 + [ctypes.c_void_p] * 3),
     "fl_sparse_rowptr_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "fl_sparse_race_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 2),
+    "fl_sparse_race_plan": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 +
+                            [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "fl_sparse_race_select": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 4 +
+                              [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "fl_sparse_normalize_forward": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3 +
                                     [ctypes.c_float] + [ctypes.c_void_p] * 4),
     "fl_sparse_normalize_backward": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_float,

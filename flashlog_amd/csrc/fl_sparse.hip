@@ -1,11 +1,14 @@
-// Sparse (COO) sum hop on gfx950.
+// Sparse (COO) hop on gfx950, sum and max aggregation.
 //
 // Replaces the expansion kernels of flashlog.cu (count/fill top-k
 // :1368-1559, all edges :1743-1829, identity :1831-1854) and the coalesce
-// of flashlog_kernel.py:258-357, with the addition order of the reference's
-// CPU path (flashlog.cpp:1388-1486): per (row, destination) the
-// contributions are added to 0 in input-entry order, and per entry ORI kept
-// edges (CSR position order), then INV kept edges, then the identity term.
+// of flashlog_kernel.py:258-357 (sum) and :399-478 (max).  Sum keeps the
+// addition order of the reference's CPU path (flashlog.cpp:1388-1486): per
+// (row, destination) the contributions are added to 0 in input-entry order,
+// and per entry ORI kept edges (CSR position order), then INV kept edges,
+// then the identity term.  Max keeps, per (row, destination), the item with
+// the largest value; ties go to ORI before INV before the identity term,
+// then to the smaller original edge id, then to the earlier raw item.
 //
 // Pipeline (rows r = b*L + l; entries must be sorted by row):
 //   plan    k_sp_rowptr   entry range of every row, input validation
@@ -18,10 +21,10 @@
 //           k_sp_partition workgroup per tile of a row: stable scatter of the
 //                         tile's items into destination buckets (block radix
 //                         rank over the bucket id)
-//           k_sp_accum    workgroup per (row, bucket): LDS accumulator of the
-//                         bucket's 8192 destinations; items are applied in
-//                         order, one item per destination per round, so every
-//                         destination sees its additions in raw order
+//           k_sp_accum    workgroup per (row, bucket): the bucket's items
+//                         stably sorted by destination in LDS, each run added
+//                         in raw order (k_sp_accum_hot: large buckets, dense
+//                         LDS accumulator); max: k_sp_max / k_sp_max_hot
 //           scan          output offsets
 //   emit    k_sp_emit     coalesced COO (b, l, e, v), ascending key
 //   backward k_sp_bwd     wave per entry: the same walk, gradients gathered
@@ -39,10 +42,24 @@ namespace fl {
 constexpr int SP_S = 13;               // destinations per bucket = 2^SP_S
 constexpr int SP_W = 1 << SP_S;
 constexpr int SP_NT = 256;
+constexpr int NM_NT0 = 256;  // row-reduction workgroup size
 constexpr int SP_IPT = 16;
 constexpr int SP_TILE = SP_NT * SP_IPT;  // items per partition tile
 
 enum { SP_TOPK = 0, SP_ALL = 1, SP_FIXED = 2 };
+enum { SP_SUM = 0, SP_MAX = 1 };
+// raw item tie keys of the max (ascending = preferred on equal values)
+constexpr uint32_t SP_TIE_INV = 0x80000000u;  // | original edge id
+constexpr uint32_t SP_TIE_IDENTITY = 0xFFFFFFFFu;
+
+// SplitMix64 output function (Steele, Lea and Flood 2014; the public-domain
+// splitmix64.c of Vigna): one step from state z.
+__device__ __forceinline__ uint64_t fl_splitmix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
 
 // ---------------------------------------------------------------------------
 // plan
@@ -77,30 +94,130 @@ __global__ void k_sp_rowptr(const int64_t *__restrict__ sb, const int64_t *__res
         for (int64_t q = r + 1; q <= R; ++q) row_ptr[q] = nnz;
 }
 
+// Take rule of one (entry, side).  TAKE_ALL: every edge (all-edges mode);
+// TAKE_TH: the c2 threshold th and tie cut (group_take); TAKE_QUOTA: the
+// training quotas of flashlog.cu:1433-1528 (sampling seed >= 0, more eligible
+// edges than K): every eligible group (w > 0) first gets
+// min(count, floor(K*w/wsum)); the residual K - allocated is spread over the
+// groups' spare capacities by systematic rounding of the capacity prefix
+// with a SplitMix64 phase per (b, l, source, side).  Double arithmetic in
+// the reference's evaluation order (wsum added in group order).
+enum { TAKE_ALL = 0, TAKE_TH = 1, TAKE_QUOTA = 2 };
+
+struct SpTake {
+    int kind;
+    float th;
+    int32_t cut;
+    double wsum, phase;
+    long long target, residual, spare, left, cap_left, prefix;
+};
+
+__device__ __forceinline__ long long sp_quota_base(const SpTake &tk, float wv, long long cnt) {
+    return (long long)fmin((double)cnt, floor(__ddiv_rn(__dmul_rn((double)tk.target, (double)wv), tk.wsum)));
+}
+
+template <bool Q>
+__device__ SpTake sp_take(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int mode, float thv, int32_t ct,
+                          int64_t K, int64_t seed, int64_t b, int64_t l, int64_t src, int dir) {
+    SpTake tk{};
+    tk.th = thv;
+    tk.cut = ct;
+    if (mode == SP_ALL) { tk.kind = TAKE_ALL; return tk; }
+    if (!Q || !__builtin_isnan(thv)) { tk.kind = TAKE_TH; return tk; }
+    tk.kind = TAKE_QUOTA;
+    const int lane = fl_lane();
+    double ws = 0.0;
+    long long cap = 0;
+    for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
+        const int64_t g = gb + lane;
+        float wv = 0.0f;
+        if (g < g1) {
+            wv = wr[s.group_rel[g]];
+            if (wv > 0.0f) cap += s.group_count[g];
+        }
+        const int nl = (int)((g1 - gb) < FL_WAVE ? (g1 - gb) : FL_WAVE);
+        for (int j = 0; j < nl; ++j) {  // group order
+            const float wj = __shfl(wv, j, FL_WAVE);
+            if (wj > 0.0f) ws = __dadd_rn(ws, (double)wj);
+        }
+    }
+    cap = fl_wave_sum_i64(cap);
+    tk.wsum = ws;
+    tk.target = K < cap ? K : cap;
+    long long alloc = 0;
+    for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
+        const float wv = wr[s.group_rel[g]];
+        if (wv > 0.0f) alloc += sp_quota_base(tk, wv, s.group_count[g]);
+    }
+    alloc = fl_wave_sum_i64(alloc);
+    tk.residual = tk.target - alloc;
+    tk.spare = cap - alloc;
+    tk.left = tk.residual;
+    tk.cap_left = tk.spare;
+    tk.prefix = 0;
+    const uint64_t z = (uint64_t)seed ^ ((uint64_t)b * 0x9e3779b97f4a7c15ull) ^ ((uint64_t)l * 0xbf58476d1ce4e5b9ull) ^
+                       ((uint64_t)src * 0x94d049bb133111ebull) ^ (dir ? 0xd1b54a32d192ed03ull : 0x8cb92baa3f3d8dd7ull);
+    tk.phase = (double)(fl_splitmix64(z) >> 11) * 0x1.0p-53;
+    return tk;
+}
+
+// Quota takes of the window's groups (lane j: group gb + j; nl valid lanes):
+// the sequential carry of the reference, run uniformly by every lane.
+__device__ long long sp_quota_window(SpTake &tk, float wv, long long cnt, bool valid, int nl) {
+    const int lane = fl_lane();
+    const bool el = valid && wv > 0.0f && cnt > 0;
+    const long long base = el ? sp_quota_base(tk, wv, cnt) : 0;
+    const long long spare = cnt - base;
+    long long mine = 0;
+    for (int j = 0; j < nl; ++j) {
+        const int elj = __shfl((int)el, j, FL_WAVE);
+        const long long bj = __shfl(base, j, FL_WAVE);
+        const long long sj = __shfl(spare, j, FL_WAVE);
+        if (!elj) continue;
+        tk.prefix += sj;
+        tk.cap_left -= sj;
+        const long long cum =
+            tk.prefix == tk.spare
+                ? tk.residual
+                : (long long)floor(__dadd_rn(
+                      __ddiv_rn(__dmul_rn((double)tk.residual, (double)tk.prefix), (double)tk.spare), tk.phase));
+        long long extra = cum - (tk.residual - tk.left);
+        extra = extra < tk.left ? extra : tk.left;
+        extra = extra < sj ? extra : sj;
+        extra = extra > 0 ? extra : 0;
+        extra = extra > tk.left - tk.cap_left ? extra : tk.left - tk.cap_left;
+        tk.left -= extra;
+        if (lane == j) mine = bj + extra;
+    }
+    return mine;
+}
+
 // Kept items of one (entry, side) in raw order (group order, then CSR
 // position), 64 at a time.  Groups are read 64 at a time, lane g holding
 // one group; a wave prefix sum of their kept counts places every item, and
 // each lane finds the group of its item by a binary search over the lanes.
 // fn(valid, k, p, rel, wv) is called by every lane of the wave for each
 // chunk of 64 items (valid = the lane holds an item; k = the item's index
-// within the side).  Returns the side's item count.
-template <typename F>
+// within the side).  Returns the side's item count.  Q: quotas possible.
+template <bool Q, typename F>
 __device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, int64_t g1, const float *wr,
-                                                 float thv, int32_t ct, int mode, F &&fn) {
+                                                 SpTake &tk, F &&fn) {
     const int lane = fl_lane();
     int64_t base = 0;
     for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
         const int64_t g = gb + lane;
-        int64_t take = 0, start = 0;
+        int64_t take = 0, start = 0, cnt = 0;
         int rel = 0;
         float wv = 0.0f;
         if (g < g1) {
             rel = s.group_rel[g];
             wv = wr[rel];
             start = s.group_start[g];
-            const int64_t cnt = s.group_count[g];
-            take = mode == SP_ALL ? cnt : group_take(wv, thv, ct, start, cnt);
+            cnt = s.group_count[g];
+            take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? group_take(wv, tk.th, tk.cut, start, cnt) : 0);
         }
+        if (Q && tk.kind == TAKE_QUOTA)
+            take = sp_quota_window(tk, wv, cnt, g < g1, (int)((g1 - gb) < FL_WAVE ? (g1 - gb) : FL_WAVE));
         const long long incl = fl_wave_incl_scan_i64(take);
         const long long total = __shfl(incl, FL_WAVE - 1, FL_WAVE);
         for (long long k0 = 0; k0 < total; k0 += FL_WAVE) {
@@ -125,17 +242,18 @@ __device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, i
 }
 
 // One wave per entry: per side the c2 threshold (bits of the threshold
-// weight, 0 = no pruning) and tie cut, and the number of raw items: kept
-// edges (top-k mode; a kept edge with a zero mask becomes a hole, raw
-// destination -1, skipped downstream) or every edge (all-edges mode), plus
-// the identity item.
+// weight, 0 = no pruning, NaN = training quotas) and tie cut, and the number
+// of raw items: kept edges (top-k mode; for the sum a kept edge with a zero
+// mask becomes a hole, raw destination -1, skipped downstream) or every edge
+// (all-edges mode), plus the identity item.  With quotas the side keeps
+// exactly min(eligible, K) edges, as the threshold does.
 constexpr int SEL_NT = 256;
 
 __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                      const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
                                                      int64_t nnz, const float *__restrict__ w, int64_t B, int64_t L,
                                                      int64_t E, int64_t n, int64_t r_size, int wot_i, int mode, int64_t K,
-                                                     float *__restrict__ th, int32_t *__restrict__ cut,
+                                                     int64_t seed, float *__restrict__ th, int32_t *__restrict__ cut,
                                                      int32_t *__restrict__ cnt) {
     __shared__ int hist_all[SEL_NT / FL_WAVE][256];
     const int lane = fl_lane();
@@ -161,16 +279,27 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
         } else {
             uint32_t key;
             int32_t cc;
+            bool quota = false;
             if (K < 0) {
                 thv = __int_as_float(0x7f800000);  // budget <= 0: no edge is kept
+            } else if (K > 0 && seed >= 0) {
+                long long e = 0;
+                for (int64_t g = g0 + lane; g < g1; g += FL_WAVE)
+                    if (wr[s.group_rel[g]] > 0.0f) e += s.group_count[g];
+                quota = fl_wave_sum_i64(e) > K;
+                if (quota) thv = __int_as_float(0x7fc00000);
             } else if (K > 0 && c2_select(s, g0, g1, wr, K, hist_all[wid], &key, &cc)) {
                 thv = __uint_as_float(key);
                 ct = cc;
             }
-            // kept edges, masked ones included (they become holes in the raw list)
-            for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
-                const int64_t start = s.group_start[g];
-                c += group_take(wr[s.group_rel[g]], thv, ct, start, s.group_count[g]);
+            if (quota) {
+                c = lane == 0 ? K : 0;
+            } else {
+                // kept edges, masked ones included
+                for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
+                    const int64_t start = s.group_start[g];
+                    c += group_take(wr[s.group_rel[g]], thv, ct, start, s.group_count[g]);
+                }
             }
         }
         c = fl_wave_sum_i64(c);
@@ -278,15 +407,20 @@ struct SpRows {
     int64_t NB;                // buckets per row
 };
 
-// One wave per entry: the entry's items in raw order at item_off[i].
+// One wave per entry: the entry's items in raw order at item_off[i]; for
+// the max also their tie keys (original edge id, INV ones above ORI ones,
+// the identity item last).  Q: training quotas possible.
+template <bool Q>
 __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                    const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
                                                    const float *__restrict__ sv, int64_t nnz,
                                                    const float *__restrict__ w, int64_t L, int64_t n,
-                                                   int64_t r_size, int wot_i, int mode,
-                                                   const float *__restrict__ th, const int32_t *__restrict__ cut,
+                                                   int64_t r_size, int wot_i, int mode, int agg, int64_t K,
+                                                   int64_t seed, const float *__restrict__ th,
+                                                   const int32_t *__restrict__ cut,
                                                    const int64_t *__restrict__ item_off,
-                                                   int32_t *__restrict__ raw_dst, float *__restrict__ raw_val) {
+                                                   int32_t *__restrict__ raw_dst, float *__restrict__ raw_val,
+                                                   uint32_t *__restrict__ raw_tie) {
     const int lane = fl_lane();
     const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
     if (i >= nnz) return;
@@ -294,25 +428,28 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
     const int64_t r = sb[i] * L + sl[i];
     const float a = sv[i];
     const float *wrow = w + r * n;
+    const bool holes = mode == SP_TOPK && agg == SP_SUM;
     int64_t pos = item_off[i];
+    // the plan's item count bounds every write (the walk reproduces it)
+    const int64_t lim = item_off[i + 1] - (wot_i ? 0 : 1);
     for (int dir = 0; dir < 2; ++dir) {
         const fl_side &s = dir ? inv : ori;
         const float *wr = wrow + (dir ? r_size : 0);
-        const float thv = th[2 * i + dir];
-        const int32_t ct = cut[2 * i + dir];
         const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-        pos += sp_side_items(s, g0, g1, wr, thv, ct, mode, [&](bool valid, int64_t k, int64_t p, int, float wv) {
-            if (valid) {
+        SpTake tk = sp_take<Q>(s, g0, g1, wr, mode, th[2 * i + dir], cut[2 * i + dir], K, seed, sb[i], sl[i], src, dir);
+        pos += sp_side_items<Q>(s, g0, g1, wr, tk, [&](bool valid, int64_t k, int64_t p, int, float wv) {
+            if (valid && pos + k < lim) {
                 const float m = s.mask[p];
-                const bool keep = mode == SP_ALL || m != 0.0f;
-                raw_dst[pos + k] = keep ? s.col_ind[p] : -1;
+                raw_dst[pos + k] = (!holes || m != 0.0f) ? s.col_ind[p] : -1;
                 raw_val[pos + k] = fl_mul(fl_mul(a, wv), m);
+                if (raw_tie) raw_tie[pos + k] = (dir ? SP_TIE_INV : 0u) | (uint32_t)s.order[p];
             }
         });
     }
-    if (!wot_i && lane == 0) {
+    if (!wot_i && lane == 0 && pos == lim) {
         raw_dst[pos] = (int32_t)src;
         raw_val[pos] = fl_mul(a, wrow[n - 1]);
+        if (raw_tie) raw_tie[pos] = SP_TIE_IDENTITY;
     }
 }
 
@@ -404,7 +541,9 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
                                                        const int32_t *__restrict__ raw_dst,
                                                        const float *__restrict__ raw_val,
                                                        int32_t *__restrict__ part_dst, float *__restrict__ part_val,
-                                                       int32_t *__restrict__ part_raw) {
+                                                       int32_t *__restrict__ part_raw,
+                                                       const uint32_t *__restrict__ raw_tie,
+                                                       uint32_t *__restrict__ part_tie) {
     __shared__ uint32_t kb[2][SP_TILE];
     __shared__ uint16_t cnt[16][SP_NT];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
@@ -448,6 +587,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         part_dst[q] = raw_dst[i0 + idx];
         part_val[q] = raw_val[i0 + idx];
         if (part_raw) part_raw[q] = (int32_t)(i0 + idx);
+        if (part_tie) part_tie[q] = raw_tie[i0 + idx];
     }
 }
 
@@ -671,6 +811,165 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64
     if (t == 0) out_count[r * rows.NB + bk] = total;
 }
 
+// Max per (row, bucket) (flashlog_kernel.py:399-478): per destination the
+// winning item is the largest value (zeros of either sign equal), then the
+// smallest tie key (ORI < INV < identity, then the original edge id), then
+// the earliest raw item; outputs are compacted in destination order as for
+// the sum, with the winning value (+0 for a zero), and raw_local[raw] = the
+// output index of winners, -1 for the other items.
+//   k_sp_max      buckets of at most SP_CHUNK items: stable LDS sort by
+//                 destination, the first thread of every run scans it;
+//   k_sp_max_hot  larger buckets: dense LDS arrays over the bucket's 8192
+//                 destinations, a max of the value keys, then a min of
+//                 (tie key, position) among the items holding the max.
+__device__ __forceinline__ float sp_canon(float v) { return v == 0.0f ? 0.0f : v; }
+
+__device__ __forceinline__ float fl_order_key_inv(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+template <int IPT>
+__device__ void sp_max_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
+                           float *__restrict__ val_arr, const uint32_t *__restrict__ tie_arr,
+                           const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local, int32_t *out_count,
+                           uint32_t (*kb)[SP_CHUNK], float *val, uint32_t *tie, uint16_t (*cnt)[SP_NT],
+                           int *scan_lds) {
+    constexpr int SIZE = SP_NT * IPT;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int k = t * IPT + j;
+        if (k < n) tie[k] = tie_arr[start + k];
+    }
+    const uint32_t *key = sp_load_sort<IPT>(dst_arr, val_arr, start, 0, n, kb, val, cnt, scan_lds);
+    int heads = 0;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) heads += sp_is_head(key, t * IPT + j) ? 1 : 0;
+    int total;
+    int rank = fl_block_excl_scan<SP_NT>(heads, scan_lds, &total);
+    // all items were read before the first barrier: outputs may overwrite them
+    for (int j = 0; j < IPT; ++j) {
+        const int p = t * IPT + j;
+        if (!sp_is_head(key, p)) continue;
+        const int e = sp_run_end(key, p, SIZE);
+        int bi = (int)(key[p] & 2047u);
+        float bv = sp_canon(val[bi]);
+        uint32_t bt = tie[bi];
+        for (int q = p + 1; q < e; ++q) {
+            const int idx = (int)(key[q] & 2047u);
+            const float v = sp_canon(val[idx]);
+            const uint32_t tq = tie[idx];
+            if (v > bv || (v == bv && tq < bt)) { bi = idx; bv = v; bt = tq; }
+        }
+        if (raw_local)
+            for (int q = p; q < e; ++q) {
+                const int idx = (int)(key[q] & 2047u);
+                raw_local[raw_arr ? raw_arr[start + idx] : start + idx] = idx == bi ? rank : -1;
+            }
+        dst_arr[start + rank] = dbase + (int32_t)(key[p] >> 11);
+        val_arr[start + rank] = bv;
+        ++rank;
+    }
+    if (t == 0) *out_count = total;
+}
+
+__global__ __launch_bounds__(SP_NT) void k_sp_max(SpRows rows, const int64_t *__restrict__ base,
+                                                 int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                                 const uint32_t *__restrict__ tie_arr,
+                                                 const int32_t *__restrict__ raw_arr,
+                                                 int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count) {
+    __shared__ uint32_t kb[2][SP_CHUNK];
+    __shared__ float val[SP_CHUNK];
+    __shared__ uint32_t tie[SP_CHUNK];
+    __shared__ uint16_t cnt[16][SP_NT];
+    __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
+    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
+    int64_t start, end;
+    sp_bucket_range(rows, base, r, bk, &start, &end);
+    const int64_t n = end - start;
+    if (n > SP_CHUNK) return;  // k_sp_max_hot
+    int32_t *oc = &out_count[r * rows.NB + bk];
+    if (n == 0) {
+        if (threadIdx.x == 0) *oc = 0;
+        return;
+    }
+    const int32_t dbase = (int32_t)(bk << SP_S);
+    if (n <= SP_NT * 2)
+        sp_max_one<2>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
+    else if (n <= SP_NT * 4)
+        sp_max_one<4>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
+    else
+        sp_max_one<8>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
+}
+
+__global__ __launch_bounds__(SP_NT) void k_sp_max_hot(SpRows rows, const int64_t *__restrict__ base,
+                                                     int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                                     const uint32_t *__restrict__ tie_arr,
+                                                     const int32_t *__restrict__ raw_arr,
+                                                     int32_t *__restrict__ raw_local,
+                                                     int32_t *__restrict__ out_count) {
+    __shared__ uint32_t vbest[SP_W];
+    __shared__ unsigned long long tbest[SP_W];
+    __shared__ uint32_t bits[SP_W / 32];
+    __shared__ int wpre[SP_W / 32];
+    __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
+    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
+    int64_t start, end;
+    sp_bucket_range(rows, base, r, bk, &start, &end);
+    const int64_t n = end - start;
+    if (n <= SP_CHUNK) return;  // k_sp_max
+    const int t = threadIdx.x;
+    for (int q = t; q < SP_W; q += SP_NT) {
+        vbest[q] = 0u;  // below the key of every non-NaN value
+        tbest[q] = ~0ull;
+    }
+    for (int q = t; q < SP_W / 32; q += SP_NT) bits[q] = 0;
+    __syncthreads();
+    for (int64_t k = t; k < n; k += SP_NT) {
+        const int32_t d = dst_arr[start + k];
+        if (d < 0) continue;
+        const int dl = d & (SP_W - 1);
+        atomicMax(&vbest[dl], fl_order_key(sp_canon(val_arr[start + k])));
+        atomicOr(&bits[dl >> 5], 1u << (dl & 31));
+    }
+    __syncthreads();
+    for (int64_t k = t; k < n; k += SP_NT) {
+        const int32_t d = dst_arr[start + k];
+        if (d < 0) continue;
+        const int dl = d & (SP_W - 1);
+        if (fl_order_key(sp_canon(val_arr[start + k])) == vbest[dl])
+            atomicMin(&tbest[dl], ((unsigned long long)tie_arr[start + k] << 32) | (unsigned long long)k);
+    }
+    __syncthreads();
+    const uint32_t word = bits[t];
+    int total;
+    const int pre = fl_block_excl_scan<SP_NT>(__popc(word), scan_lds, &total);
+    wpre[t] = pre;
+    __syncthreads();
+    if (raw_local) {
+        for (int64_t k = t; k < n; k += SP_NT) {
+            const int32_t d = dst_arr[start + k];
+            if (d < 0) continue;
+            const int dl = d & (SP_W - 1);
+            const int o = wpre[dl >> 5] + __popc(bits[dl >> 5] & ((1u << (dl & 31)) - 1u));
+            raw_local[raw_arr ? raw_arr[start + k] : start + k] = (uint32_t)tbest[dl] == (uint32_t)k ? o : -1;
+        }
+        __syncthreads();
+    }
+    const int32_t dbase = (int32_t)(bk << SP_S);
+    uint32_t wd = word;
+    int64_t o = start + pre;
+    while (wd) {
+        const int bit = __ffs(wd) - 1;
+        wd &= wd - 1;
+        const int dl = t * 32 + bit;
+        dst_arr[o] = dbase + dl;
+        val_arr[o] = fl_order_key_inv(vbest[dl]);
+        ++o;
+    }
+    if (t == 0) out_count[r * rows.NB + bk] = total;
+}
+
 // Workgroup per (row, bucket): staged outputs -> COO at out_base.
 __global__ __launch_bounds__(SP_NT) void k_sp_emit(SpRows rows, int64_t L, const int64_t *__restrict__ base,
                                                   const int32_t *__restrict__ dst_arr,
@@ -706,13 +1005,15 @@ __global__ __launch_bounds__(SP_NT) void k_sp_emit(SpRows rows, int64_t L, const
 // position item_off[i] + k) maps to output out_base[r*NB + dst/8192] +
 // raw_local[...].  grad_v[i] = sum over items of (g*m)*w, plus g*w[n-1] for
 // the identity item (flashlog.cu:1856-1959, order fixed per entry);
-// grad_w[r, col] += (g*m)*a by atomics, as the reference.
+// grad_w[r, col] += (g*m)*a by atomics, as the reference.  Max: only the
+// winning items (raw_local >= 0) take part (flashlog.cu:2364-2410).
+template <bool Q>
 __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                   const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
                                                   const float *__restrict__ sv, int64_t nnz,
                                                   const float *__restrict__ w, int64_t L, int64_t n, int64_t r_size,
-                                                  int wot_i, int mode, const float *__restrict__ th,
-                                                  const int32_t *__restrict__ cut,
+                                                  int wot_i, int mode, int agg, int64_t K, int64_t seed,
+                                                  const float *__restrict__ th, const int32_t *__restrict__ cut,
                                                   const int64_t *__restrict__ item_off, int64_t NB,
                                                   const int64_t *__restrict__ out_base,
                                                   const int32_t *__restrict__ raw_local,
@@ -726,22 +1027,24 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
     const float a = sv[i];
     const float *wrow = w + r * n;
     const int64_t *orow = out_base + r * NB;
+    const bool holes = mode == SP_TOPK && agg == SP_SUM;
     float gsp = 0.0f;
     int64_t pos = item_off[i];
+    const int64_t lim = item_off[i + 1] - (wot_i ? 0 : 1);
     for (int dir = 0; dir < 2; ++dir) {
         const fl_side &s = dir ? inv : ori;
         const int64_t off = dir ? r_size : 0;
-        const float thv = th[2 * i + dir];
-        const int32_t ct = cut[2 * i + dir];
         const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-        pos += sp_side_items(s, g0, g1, wrow + off, thv, ct, mode, [&](bool valid, int64_t kk, int64_t p, int rel,
-                                                                        float wv) {
+        SpTake tk = sp_take<Q>(s, g0, g1, wrow + off, mode, th[2 * i + dir], cut[2 * i + dir], K, seed, sb[i],
+                               sl[i], src, dir);
+        pos += sp_side_items<Q>(s, g0, g1, wrow + off, tk, [&](bool valid, int64_t kk, int64_t p, int rel, float wv) {
             float gwv = 0.0f;
-            if (valid) {
+            if (valid && pos + kk < lim) {
                 const float m = s.mask[p];
-                if (mode == SP_ALL || m != 0.0f) {
+                const int32_t loc = (!holes || m != 0.0f) ? raw_local[pos + kk] : -1;
+                if (loc >= 0) {
                     const int32_t d = s.col_ind[p];
-                    const float gv = grad[orow[d >> SP_S] + raw_local[pos + kk]];
+                    const float gv = grad[orow[d >> SP_S] + loc];
                     const float gm = fl_mul(gv, m);
                     gsp = fl_add(gsp, fl_mul(gm, wv));
                     gwv = fl_mul(gm, a);
@@ -764,8 +1067,9 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
     }
     gsp = fl_wave_sum_f32(gsp);
     if (lane == 0) {
-        if (!wot_i) {
-            const float gv = grad[orow[src >> SP_S] + raw_local[pos]];
+        const int32_t loc = (wot_i || pos != lim) ? -1 : raw_local[pos];
+        if (loc >= 0) {
+            const float gv = grad[orow[src >> SP_S] + loc];
             gsp = fl_add(gsp, fl_mul(gv, wrow[n - 1]));
             atomicAdd(&grad_w[r * n + n - 1], fl_mul(gv, a));
         }
@@ -789,6 +1093,8 @@ __global__ void k_sp_plan_out(const int64_t *__restrict__ items, const int64_t *
     plan[1] = *tiles;
     plan[3] = NB;
 }
+
+__global__ void k_fill_from(const int64_t *__restrict__ src, int64_t *__restrict__ dst) { *dst = *src; }
 
 __global__ void k_fill_f32(float *__restrict__ p, int64_t n, float v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -876,6 +1182,131 @@ __global__ __launch_bounds__(TOPC_NT) void k_sp_topc(const int64_t *__restrict__
                      }
                  }
                  kp[e] = k;)
+}
+
+// ---------------------------------------------------------------------------
+// Sampled c1 (flashlog_kernel.py:1121-1132, sampling=True): in rows with
+// more than c nonzeros the candidates (nonzero entries, which must be finite
+// and positive) are ranked by the exponential race score
+// log(v) - log(noise), noise ~ Exp(1) one per candidate in entry order, and
+// the c best are kept (ties to the earlier entry); zero entries of those rows
+// are dropped and other rows keep every entry.
+//   k_race_rows   workgroup per row: over[r] = (nonzeros > c)
+//   k_race_flags  thread per entry: candidate flag, score validation
+//   (scan)        candidate offsets; the caller draws the noise
+//   k_race_keys   thread per entry: 64-bit order key of the score
+//   k_race_select 1024-thread workgroup per row: radix select (11/11/11/11/
+//                 10/10 bits) of the c-th largest key, ordered tie scan
+
+__device__ __forceinline__ unsigned long long fl_order_key64(double d) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(d);
+    return (u >> 63) ? ~u : (u | 0x8000000000000000ull);
+}
+
+__global__ __launch_bounds__(NM_NT0) void k_race_rows(const int64_t *__restrict__ row_ptr,
+                                                      const float *__restrict__ v, int64_t c,
+                                                      int32_t *__restrict__ over) {
+    __shared__ int red[NM_NT0 / FL_WAVE];
+    const int64_t r = blockIdx.x;
+    const int64_t a = row_ptr[r], b = row_ptr[r + 1];
+    int nz = 0;
+    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT0) nz += v[k] != 0.0f ? 1 : 0;
+    nz = fl_wave_sum_i32(nz);
+    if (fl_lane() == 0) red[threadIdx.x / FL_WAVE] = nz;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        long long t = 0;
+        for (int q = 0; q < NM_NT0 / FL_WAVE; ++q) t += red[q];
+        over[r] = t > c ? 1 : 0;
+    }
+}
+
+__global__ void k_race_flags(const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
+                             const float *__restrict__ v, int64_t nnz, int64_t L, const int32_t *__restrict__ over,
+                             int32_t *__restrict__ cand, int64_t *__restrict__ err) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    const float x = v[i];
+    const int f = (over[sb[i] * L + sl[i]] && x != 0.0f) ? 1 : 0;
+    cand[i] = f;
+    if (f && !(x > 0.0f && x <= 3.402823466e38f)) atomicMax((unsigned long long *)err, 3ull);
+}
+
+__global__ void k_race_keys(const float *__restrict__ v, int64_t nnz, const int32_t *__restrict__ cand,
+                            const int64_t *__restrict__ cand_off, const double *__restrict__ noise,
+                            unsigned long long *__restrict__ keys) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    keys[i] = cand[i] ? fl_order_key64(__dsub_rn(log((double)v[i]), log(noise[cand_off[i]]))) : 0ull;
+}
+
+__global__ __launch_bounds__(TOPC_NT) void k_race_select(const int64_t *__restrict__ row_ptr,
+                                                        const int32_t *__restrict__ over,
+                                                        const int32_t *__restrict__ cand,
+                                                        const unsigned long long *__restrict__ keys, int64_t c,
+                                                        int32_t *__restrict__ keep) {
+    __shared__ int hist[2048];
+    __shared__ int lds_scan[TOPC_NT / FL_WAVE + 1];
+    __shared__ int sel_bin, sel_need, s_last, s_done;
+    const int64_t row = blockIdx.x;
+    const int64_t a = row_ptr[row], n = row_ptr[row + 1] - a;
+    const int t = threadIdx.x;
+    if (n == 0) return;
+    if (!over[row]) {
+        for (int64_t k = t; k < n; k += TOPC_NT) keep[a + k] = 1;
+        return;
+    }
+    // radix select of the c-th largest candidate key, most significant first
+    const int shifts[6] = {53, 42, 31, 20, 10, 0};
+    const int widths[6] = {11, 11, 11, 11, 10, 10};
+    unsigned long long prefix = 0, pmask = 0;
+    int need = (int)c;
+    int tied_total = 0;
+    for (int ps = 0; ps < 6; ++ps) {
+        const int sh = shifts[ps], wd = widths[ps];
+        const int nb = 1 << wd;
+        for (int q = t; q < 2048; q += TOPC_NT) hist[q] = 0;
+        __syncthreads();
+        for (int64_t k = t; k < n; k += TOPC_NT) {
+            if (!cand[a + k]) continue;
+            const unsigned long long key = keys[a + k];
+            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> sh) & (nb - 1)], 1);
+        }
+        __syncthreads();
+        if (nb == 2048) topc_select<2048>(hist, need, lds_scan, &sel_bin, &sel_need);
+        else topc_select<1024>(hist, need, lds_scan, &sel_bin, &sel_need);
+        prefix |= (unsigned long long)sel_bin << sh;
+        pmask |= (unsigned long long)(nb - 1) << sh;
+        need = sel_need;
+        tied_total = hist[sel_bin];
+        __syncthreads();
+    }
+    const unsigned long long cutkey = prefix;
+    int64_t last = n;
+    if (need < tied_total) {
+        if (t == 0) { s_last = -1; s_done = 0; }
+        __syncthreads();
+        int run = 0;
+        for (int64_t base = 0; base < n; base += TOPC_NT) {
+            const int64_t k = base + t;
+            const int flag = (k < n && cand[a + k] && keys[a + k] == cutkey) ? 1 : 0;
+            int tot;
+            const int ex = fl_block_excl_scan<TOPC_NT>(flag, lds_scan, &tot);
+            if (flag && run + ex + 1 == need) { s_last = (int)k; s_done = 1; }
+            run += tot;
+            __syncthreads();
+            if (s_done) break;
+        }
+        last = s_last;
+    }
+    for (int64_t k = t; k < n; k += TOPC_NT) {
+        int kp = 0;
+        if (cand[a + k]) {
+            const unsigned long long key = keys[a + k];
+            kp = key > cutkey || (key == cutkey && k <= last);
+        }
+        keep[a + k] = kp;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -980,20 +1411,23 @@ SpPlan sp_plan_layout(int64_t nnz, int64_t R, char *base) {
 struct SpExp {
     int32_t *raw_dst, *part_dst, *part_raw, *hist, *out_count;
     float *raw_val, *part_val;
+    uint32_t *raw_tie, *part_tie;
     int64_t *base, *tmp;
     size_t bytes;
 };
 
-SpExp sp_exp_layout(int64_t T, int64_t tiles, int64_t R, int64_t NB, int backward, char *base) {
+SpExp sp_exp_layout(int64_t T, int64_t tiles, int64_t R, int64_t NB, int backward, int agg, char *base) {
     SpExp x{};
     size_t off = 0;
     auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
     const int64_t T1 = T > 0 ? T : 1;
     x.raw_dst = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
     x.raw_val = (float *)take(sizeof(float) * (size_t)T1);
+    if (agg == SP_MAX) x.raw_tie = (uint32_t *)take(sizeof(uint32_t) * (size_t)T1);
     if (NB > 1) {
         x.part_dst = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
         x.part_val = (float *)take(sizeof(float) * (size_t)T1);
+        if (agg == SP_MAX) x.part_tie = (uint32_t *)take(sizeof(uint32_t) * (size_t)T1);
         x.hist = (int32_t *)take(sizeof(int32_t) * (size_t)(tiles * NB > 0 ? tiles * NB : 1));
         x.base = (int64_t *)take(sizeof(int64_t) * (size_t)(tiles * NB + 1));
     }
@@ -1014,6 +1448,11 @@ int sp_check(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, con
     if (h->E > ((int64_t)SP_W << 14)) return fl_fail(FL_ERR_ARG, "%s: E must be <= 2^27", what);
     if (h->mode != SP_TOPK && h->mode != SP_ALL && h->mode != SP_FIXED)
         return fl_fail(FL_ERR_ARG, "%s: unknown mode", what);
+    if (h->aggregate != SP_SUM && h->aggregate != SP_MAX) return fl_fail(FL_ERR_ARG, "%s: unknown aggregate", what);
+    if (h->aggregate == SP_MAX && h->mode != SP_TOPK)
+        return fl_fail(FL_ERR_ARG, "%s: the max aggregate needs the top-k mode", what);
+    if (h->sampling_seed >= 0 && h->mode != SP_TOPK)
+        return fl_fail(FL_ERR_ARG, "%s: training quotas need the top-k mode", what);
     if (h->mode != SP_FIXED && (h->r_size < 0 || 2 * h->r_size + 1 > h->n + (h->wot_i ? 1 : 0)))
         return fl_fail(FL_ERR_ARG, "%s: w width %lld too small for r_size %lld", what, (long long)h->n,
                        (long long)h->r_size);
@@ -1025,6 +1464,9 @@ int sp_check(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, con
         if (s->edges > 0 && (!s->col_ind || (!s->mask && h->mode != SP_FIXED) || !s->group_rel ||
                              !s->group_start || !s->group_count))
             return fl_fail(FL_ERR_ARG, "%s: side without CSR arrays", what);
+    if (h->aggregate == SP_MAX)
+        for (const fl_side *s : {ori, inv})
+            if (s->edges > 0 && !s->order) return fl_fail(FL_ERR_ARG, "%s: max needs the sides' edge order", what);
     return FL_OK;
 }
 
@@ -1039,6 +1481,10 @@ size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R) {
     return sp_plan_layout(nnz, R, nullptr).bytes;
 }
 
+static int64_t sp_budget(const fl_sparse_hop *h);
+// Training quotas can apply (sampling seed, top-k mode, a positive budget).
+static bool sp_quotas(const fl_sparse_hop *h) { return h->sampling_seed >= 0 && sp_budget(h) > 0; }
+
 int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, int64_t *plan) {
     int rc;
     if ((rc = sp_check(ori, inv, h, "sparse_plan")) != FL_OK) return rc;
@@ -1048,9 +1494,7 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
     hipStream_t st = (hipStream_t)stream;
     const int64_t nnz = h->nnz;
-    // c2 budget: K > 0 selects, 0 keeps every eligible edge, < 0 keeps none
-    int64_t K = 0;
-    if (h->mode == SP_TOPK && h->topk_edges < ((int64_t)1 << 60)) K = h->topk_edges > 0 ? h->topk_edges : -1;
+    const int64_t K = sp_budget(h);
     // plan[0] items, plan[1] tiles, plan[2] error, plan[3] buckets per row
     FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, (int32_t *)plan, (int64_t)8, 0);
     FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr, R + 1,
@@ -1064,7 +1508,7 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     else if (nnz > 0)
         FL_LAUNCH("k_sp_select", k_sp_select, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
-                  h->r_size, h->wot_i, h->mode, K, p.th, p.cut, p.cnt);
+                  h->r_size, h->wot_i, h->mode, K, h->sampling_seed, p.th, p.cut, p.cnt);
     if ((rc = exclusive_scan(st, p.cnt, p.item_off, nnz, p.tmp)) != FL_OK) return rc;
     FL_LAUNCH("k_sp_rowinfo", k_sp_rowinfo, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr,
               p.item_off, R, p.row_item0, p.ntiles);
@@ -1074,9 +1518,16 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     return fl_check_launch("sparse_plan");
 }
 
-size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t R, int64_t E, int backward) {
+size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t R, int64_t E, int backward, int aggregate) {
     if (items < 0 || tiles < 0 || R < 0) return 0;
-    return sp_exp_layout(items, tiles, R, sp_buckets(E), backward, nullptr).bytes;
+    return sp_exp_layout(items, tiles, R, sp_buckets(E), backward, aggregate, nullptr).bytes;
+}
+
+// c2 budget of the plan and walk kernels: K > 0 selects, 0 keeps every
+// eligible edge, < 0 keeps none.
+static int64_t sp_budget(const fl_sparse_hop *h) {
+    if (h->mode != SP_TOPK || h->topk_edges >= ((int64_t)1 << 60)) return 0;
+    return h->topk_edges > 0 ? h->topk_edges : -1;
 }
 
 int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h,
@@ -1086,10 +1537,11 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
     if (!h->ws1 || !h->ws2 || !out_base) return fl_fail(FL_ERR_ARG, "sparse_expand: null workspace or out_base");
     if (h->items < 0 || h->tiles < 0) return fl_fail(FL_ERR_ARG, "sparse_expand: negative plan sizes");
-    if (h->ws2_bytes < fl_sparse_expand_bytes(h->items, h->tiles, R, h->E, raw_local != nullptr))
+    if (h->ws2_bytes < fl_sparse_expand_bytes(h->items, h->tiles, R, h->E, raw_local != nullptr, h->aggregate))
         return fl_fail(FL_ERR_ARG, "sparse_expand: workspace too small");
     SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
-    SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, raw_local != nullptr, (char *)h->ws2);
+    SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, raw_local != nullptr, h->aggregate, (char *)h->ws2);
+    const bool mx = h->aggregate == SP_MAX;
     hipStream_t st = (hipStream_t)stream;
     const int64_t nnz = h->nnz;
     SpRows rows{p.row_item0, p.tile_base, NB};
@@ -1097,11 +1549,13 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         FL_LAUNCH("k_fx_fill", k_fx_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_e, h->sp_v, nnz, p.cut, p.item_off, x.raw_dst, x.raw_val);
     else if (nnz > 0)
-        FL_LAUNCH("k_sp_fill", k_sp_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+        FL_LAUNCH("k_sp_fill", sp_quotas(h) ? k_sp_fill<true> : k_sp_fill<false>, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n,
-                  h->r_size, h->wot_i, h->mode, p.th, p.cut, p.item_off, x.raw_dst, x.raw_val);
+                  h->r_size, h->wot_i, h->mode, h->aggregate, sp_budget(h), h->sampling_seed, p.th, p.cut,
+                  p.item_off, x.raw_dst, x.raw_val, x.raw_tie);
     int32_t *dst_arr = x.raw_dst, *raw_arr = nullptr;
     float *val_arr = x.raw_val;
+    uint32_t *tie_arr = x.raw_tie;
     if (NB > 1) {
         if (h->tiles > 0)
             FL_LAUNCH("k_sp_hist", k_sp_hist, dim3((unsigned)h->tiles), dim3(SP_NT), sizeof(int) * (size_t)NB, st, R,
@@ -1110,12 +1564,18 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         if (h->tiles > 0)
             FL_LAUNCH("k_sp_partition", k_sp_partition, dim3((unsigned)h->tiles), dim3(SP_NT), 0, st, R, rows,
                       sp_bucket_bits(NB), x.base, x.raw_dst, x.raw_val, x.part_dst, x.part_val,
-                      raw_local ? x.part_raw : (int32_t *)nullptr);
+                      raw_local ? x.part_raw : (int32_t *)nullptr, x.raw_tie, x.part_tie);
         dst_arr = x.part_dst;
         val_arr = x.part_val;
+        tie_arr = x.part_tie;
         raw_arr = raw_local ? x.part_raw : nullptr;
     }
-    if (R * NB > 0) {
+    if (R * NB > 0 && mx) {
+        FL_LAUNCH("k_sp_max", k_sp_max, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
+                  val_arr, tie_arr, raw_arr, raw_local, x.out_count);
+        FL_LAUNCH("k_sp_max_hot", k_sp_max_hot, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base,
+                  dst_arr, val_arr, tie_arr, raw_arr, raw_local, x.out_count);
+    } else if (R * NB > 0) {
         FL_LAUNCH("k_sp_accum", k_sp_accum, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
                   val_arr, raw_arr, raw_local, x.out_count);
         FL_LAUNCH("k_sp_accum_hot", k_sp_accum_hot, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base,
@@ -1131,7 +1591,7 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h, const int64_t *out_base
     const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
     if (R * NB == 0) return FL_OK;
     SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
-    SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, 0, (char *)h->ws2);
+    SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, 0, h->aggregate, (char *)h->ws2);
     SpRows rows{p.row_item0, p.tile_base, NB};
     FL_LAUNCH("k_sp_emit", k_sp_emit, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, (hipStream_t)stream, rows, h->L,
               x.base, NB > 1 ? x.part_dst : x.raw_dst, NB > 1 ? x.part_val : x.raw_val, out_base, out_b, out_l,
@@ -1153,10 +1613,10 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
         FL_LAUNCH("k_fill_f32", k_fill_f32, dim3((unsigned)((R * h->n + 255) / 256)), dim3(256), 0, st, grad_w,
                   R * h->n, 0.0f);
     if (h->nnz > 0)
-        FL_LAUNCH("k_sp_bwd", k_sp_bwd, dim3((unsigned)((h->nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+        FL_LAUNCH("k_sp_bwd", sp_quotas(h) ? k_sp_bwd<true> : k_sp_bwd<false>, dim3((unsigned)((h->nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, h->nnz, h->w, h->L, h->n,
-                  h->r_size, h->wot_i, h->mode, p.th, p.cut, p.item_off, NB, out_base, raw_local, grad_out, grad_v,
-                  grad_w);
+                  h->r_size, h->wot_i, h->mode, h->aggregate, sp_budget(h), h->sampling_seed, p.th, p.cut,
+                  p.item_off, NB, out_base, raw_local, grad_out, grad_v, grad_w);
     return fl_check_launch("sparse_backward");
 }
 
@@ -1177,6 +1637,77 @@ int fl_sparse_topc(void *stream, const int64_t *sp_b, const int64_t *sp_l, const
     if (R > 0 && nnz > 0)
         FL_LAUNCH("k_sp_topc", k_sp_topc, dim3((unsigned)R), dim3(TOPC_NT), 0, st, row_ptr, v, c, keep);
     return fl_check_launch("sparse_topc");
+}
+
+// Sampled c1 workspace: row pointer, over flags, candidate flags and
+// offsets, order keys, scan scratch.
+struct SpRace {
+    int64_t *row_ptr, *cand_off, *tmp;
+    int32_t *over, *cand;
+    unsigned long long *keys;
+    size_t bytes;
+};
+
+static SpRace sp_race_layout(int64_t nnz, int64_t R, char *base) {
+    SpRace x{};
+    size_t off = 0;
+    auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
+    const int64_t n1 = nnz > 0 ? nnz : 1;
+    x.row_ptr = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
+    x.over = (int32_t *)take(sizeof(int32_t) * (size_t)(R > 0 ? R : 1));
+    x.cand = (int32_t *)take(sizeof(int32_t) * (size_t)n1);
+    x.cand_off = (int64_t *)take(sizeof(int64_t) * (size_t)(nnz + 1));
+    x.keys = (unsigned long long *)take(sizeof(unsigned long long) * (size_t)n1);
+    x.tmp = (int64_t *)take(scan_tmp_bytes(nnz + 1));
+    x.bytes = off;
+    return x;
+}
+
+size_t fl_sparse_race_bytes(int64_t nnz, int64_t R) {
+    if (nnz < 0 || R < 0) return 0;
+    return sp_race_layout(nnz, R, nullptr).bytes;
+}
+
+int fl_sparse_race_plan(void *stream, const int64_t *sp_b, const int64_t *sp_l, const float *v, int64_t nnz,
+                        int64_t B, int64_t L, int64_t c, void *ws, size_t ws_bytes, int64_t *info) {
+    if (c < 1) return fl_fail(FL_ERR_ARG, "sparse_race: c must be positive (c = 0 needs no ranking)");
+    if (nnz < 0 || B < 0 || L < 0) return fl_fail(FL_ERR_ARG, "sparse_race: negative size");
+    if (!ws || !info || (nnz > 0 && (!sp_b || !sp_l || !v))) return fl_fail(FL_ERR_ARG, "sparse_race: null argument");
+    const int64_t R = B * L;
+    if (ws_bytes < fl_sparse_race_bytes(nnz, R)) return fl_fail(FL_ERR_ARG, "sparse_race: workspace too small");
+    SpRace x = sp_race_layout(nnz, R, (char *)ws);
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3(1), dim3(64), 0, st, info, (int64_t)2, (int64_t)0);
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, x.row_ptr, R + 1,
+              (int64_t)0);
+    const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
+    FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, sp_b, nnz,
+              B, L, INT64_MAX, x.row_ptr, info + 1);
+    if (R > 0)
+        FL_LAUNCH("k_race_rows", k_race_rows, dim3((unsigned)R), dim3(NM_NT0), 0, st, x.row_ptr, v, c, x.over);
+    if (nnz > 0)
+        FL_LAUNCH("k_race_flags", k_race_flags, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, v,
+                  nnz, L, x.over, x.cand, info + 1);
+    int rc;
+    if ((rc = exclusive_scan(st, x.cand, x.cand_off, nnz, x.tmp)) != FL_OK) return rc;
+    FL_LAUNCH("k_fill_from", k_fill_from, dim3(1), dim3(1), 0, st, x.cand_off + nnz, info);
+    return fl_check_launch("sparse_race_plan");
+}
+
+int fl_sparse_race_select(void *stream, const float *v, int64_t nnz, int64_t B, int64_t L, int64_t c,
+                          const double *noise, void *ws, size_t ws_bytes, int32_t *keep) {
+    if (c < 1 || nnz < 0 || B < 0 || L < 0) return fl_fail(FL_ERR_ARG, "sparse_race_select: bad arguments");
+    const int64_t R = B * L;
+    if (!ws || ws_bytes < fl_sparse_race_bytes(nnz, R)) return fl_fail(FL_ERR_ARG, "sparse_race_select: workspace");
+    if (nnz == 0 || R == 0) return FL_OK;
+    if (!v || !noise || !keep) return fl_fail(FL_ERR_ARG, "sparse_race_select: null argument");
+    SpRace x = sp_race_layout(nnz, R, (char *)ws);
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_race_keys", k_race_keys, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, v, nnz, x.cand,
+              x.cand_off, noise, x.keys);
+    FL_LAUNCH("k_race_select", k_race_select, dim3((unsigned)R), dim3(TOPC_NT), 0, st, x.row_ptr, x.over, x.cand,
+              x.keys, c, keep);
+    return fl_check_launch("sparse_race_select");
 }
 
 size_t fl_sparse_rowptr_bytes(int64_t R) { return al(sizeof(int64_t) * (size_t)(R + 1)) + al(sizeof(int64_t) * 2); }

@@ -683,10 +683,6 @@ def dense_csr_sum_cuda(A, w, csr_struct, mask_values, r_size,
 # Entry points not yet carried by this build.  Signatures follow the
 # reference so callers fail with a clear message instead of a NameError.
 
-def _not_yet(name):
-    raise NotImplementedError("%s is not available in this flashlog_amd build yet" % name)
-
-
 def sparse2d_filtered_ranks_cuda(idx_b, idx_e, values, targets, filter_keys, B, E, use_eql=False):
     """Filtered tie-aware ranks of each query's target over a COO [B, E] score
     matrix (flashlog_kernel.py:168-179 -> flashlog.cu:2839-2910).  Returns
@@ -802,7 +798,30 @@ def dense_csr_max(A, w, csr_struct, mask_values, r_size, weight=None, wot_i=Fals
 
 def sampled_sparse_propagation(state, w, csr_struct, mask_values, r_size, weight=None, wot_i=False,
                                topk_nodes=None, topk_edges=0, mode="sum"):
-    _not_yet("sampled_sparse_propagation")
+    """Training-time hop (flashlog_kernel.py:1955-1969): the top-k sum or max
+    hop with sampling=True (exponential-race c1, quota c2), topk_edges <= 0
+    meaning no edge budget.  A CPU state runs the same GPU hop (inputs moved
+    to the GPU, output moved back), so its random selections follow the GPU
+    path's draws."""
+    state = state.coalesce()
+    on_cpu = not state.is_cuda
+    if on_cpu:
+        dev = torch.device("cuda", torch.cuda.current_device()) if torch.cuda.is_available() else None
+        if dev is None:
+            raise RuntimeError("flashlog_amd needs a ROCm GPU: sampled_sparse_propagation has no CPU path")
+        state = state.to(dev)
+        w = w.to(dev)
+        csr_struct = tuple(t.to(dev) for t in csr_struct)
+        mask_values = mask_values.to(dev)
+        weight = weight.to(dev) if weight is not None else None
+    idx, val = state.indices(), state.values()
+    B, L, E = state.shape
+    function = FlashLogFunctionSparse3DTopKMax if mode == "max" else FlashLogFunctionSparse3DTopKSum
+    out = function.apply(idx[0], idx[1], idx[2], val, w, *csr_struct,
+                         mask_values, weight, B, L, E, r_size, wot_i,
+                         topk_edges if topk_edges > 0 else (1 << 60),
+                         False, topk_nodes, torch.is_grad_enabled(), True)
+    return out.cpu() if on_cpu else out
 
 
 # ---------------------------------------------------------------------------
@@ -812,18 +831,19 @@ def sampled_sparse_propagation(state, w, csr_struct, mask_values, r_size, weight
 # libflashlog_hip.so).
 
 _SPARSE_TOPK, _SPARSE_ALL, _SPARSE_FIXED = 0, 1, 2
+_SPARSE_SUM, _SPARSE_MAX = 0, 1
 
 
 class _SparseSides:
     """FlSide views of the CSR arrays the sparse kernels read (no pull index)."""
 
     def __init__(self, ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount,
-                 inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount):
+                 inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, ori_order=None, inv_order=None):
         self.keep = []
-        self.ori = self._side(ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount)
-        self.inv = self._side(inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount)
+        self.ori = self._side(ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount, ori_order)
+        self.inv = self._side(inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, inv_order)
 
-    def _side(self, col, mask, gptr, grel, gstart, gcount):
+    def _side(self, col, mask, gptr, grel, gstart, gcount, order=None):
         _require_cuda(col, gptr, grel, gstart, gcount)
         col = col.int().contiguous()
         gptr = gptr.int().contiguous()
@@ -835,9 +855,15 @@ class _SparseSides:
             mask = mask.float().contiguous()
             if mask.numel() != col.numel():
                 raise ValueError("mask length must equal the number of CSR positions")
-        self.keep += [col, mask, gptr, grel, gstart, gcount]
+        if order is not None:
+            _require_cuda(order)
+            order = order.int().contiguous()
+            if order.numel() != col.numel():
+                raise ValueError("order length must equal the number of CSR positions")
+        self.keep += [col, mask, gptr, grel, gstart, gcount, order]
         side = FlSide()
         side.edges, side.groups = col.numel(), grel.numel()
+        side.order = ptr(order).value if order is not None else None
         side.col_ind, side.mask = ptr(col).value, (ptr(mask).value if mask is not None else None)
         side.row_group_ptr, side.group_rel = ptr(gptr).value, ptr(grel).value
         side.group_start, side.group_count = ptr(gstart).value, ptr(gcount).value
@@ -850,8 +876,10 @@ class _SparseState:
 
 
 def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mode, topk_edges,
-                    need_backward, operators=None):
-    """Runs plan -> expand -> emit.  Returns (indices [3, nout], values, state)."""
+                    need_backward, operators=None, aggregate=_SPARSE_SUM, seed=-1):
+    """Runs plan -> expand -> emit.  Returns (indices [3, nout], values, state).
+    aggregate: sum or max; seed >= 0: training quotas instead of the c2
+    threshold."""
     _require_cuda(sp_b, sp_l, sp_e, sp_v)
     dev = sp_v.device
     B, L, E, r_size = int(B), int(L), int(E), int(r_size)
@@ -882,6 +910,7 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         h.B, h.L, h.E, h.n, h.r_size = B, L, E, n, r_size
         h.wot_i, h.mode, h.topk_edges = 1 if wot_i else 0, int(mode), int(topk_edges)
         h.operators = ptr(operators).value if operators is not None else None
+        h.aggregate, h.sampling_seed = int(aggregate), int(seed)
         ws1 = torch.empty(max(lib.fl_sparse_plan_bytes(nnz, R), 1), dtype=torch.uint8, device=dev)
         h.ws1, h.ws1_bytes = ptr(ws1).value, ws1.numel()
         plan = torch.empty(4, dtype=torch.int64, device=dev)
@@ -898,7 +927,7 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
             raise ValueError("sparse state index out of range for shape (%d, %d, %d)" % (B, L, E))
         break
     h.items, h.tiles = items, tiles
-    ws2_bytes = lib.fl_sparse_expand_bytes(items, tiles, R, E, 1 if need_backward else 0)
+    ws2_bytes = lib.fl_sparse_expand_bytes(items, tiles, R, E, 1 if need_backward else 0, int(aggregate))
     ws2 = torch.empty(max(ws2_bytes, 1), dtype=torch.uint8, device=dev)
     h.ws2, h.ws2_bytes = ptr(ws2).value, ws2.numel()
     out_base = torch.empty(R * nb + 1, dtype=torch.int64, device=dev)
@@ -989,8 +1018,6 @@ def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, nu
         return None
     if topk_nodes < 0:
         raise ValueError("topk_nodes/c must be nonnegative")
-    if sampling:
-        raise NotImplementedError("sampled (exponential race) entity selection is not in this build yet")
     if sp_entity.numel() <= topk_nodes:
         return None
     _require_cuda(sp_batch, sp_level, sp_value)
@@ -1000,6 +1027,8 @@ def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, nu
     sp_level = sp_level.long().contiguous()
     sp_value = sp_value.contiguous().float()
     keep = torch.empty(sp_value.numel(), dtype=torch.int32, device=sp_value.device)
+    if sampling and topk_nodes > 0:
+        return _sparse_race_entries(sp_batch, sp_level, sp_value, B, L, int(topk_nodes), keep)
     row_ptr, err = _sparse_rows_scratch(B * L, sp_value.device)
     check(_lib.lib().fl_sparse_topc(_stream(sp_value), ptr(sp_batch), ptr(sp_level), ptr(sp_value),
                                     sp_value.numel(), B, L, int(topk_nodes), ptr(keep), ptr(row_ptr), ptr(err)),
@@ -1008,6 +1037,32 @@ def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, nu
         raise ValueError("sparse c1 needs a state coalesced by (batch, rule, entity)")
     if bool(keep.all()):
         return None
+    return torch.nonzero(keep, as_tuple=True)[0]
+
+
+def _sparse_race_entries(sp_batch, sp_level, sp_value, B, L, c, keep):
+    """Sampled c1 (flashlog_kernel.py:1121-1132): the exponential race over
+    the nonzero entries of over-limit rows.  The Exp(1) noise is drawn as the
+    reference draws it (one float64 per candidate, entry order, torch's
+    generator of the state's device)."""
+    lib = _lib.lib()
+    dev = sp_value.device
+    nnz = sp_value.numel()
+    ws = torch.empty(max(lib.fl_sparse_race_bytes(nnz, B * L), 1), dtype=torch.uint8, device=dev)
+    info = torch.empty(2, dtype=torch.int64, device=dev)
+    st = _stream(sp_value)
+    check(lib.fl_sparse_race_plan(st, ptr(sp_batch), ptr(sp_level), ptr(sp_value), nnz, B, L, c, ptr(ws),
+                                  ws.numel(), ptr(info)), "sparse_race_plan")
+    ncand, err = info.tolist()
+    if err in (1, 2):
+        raise ValueError("sparse c1 needs a state coalesced by (batch, rule, entity)")
+    if ncand == 0:
+        return None
+    if err == 3:
+        raise ValueError("Entity sampling requires finite nonnegative state scores")
+    noise = torch.empty(ncand, dtype=torch.float64, device=dev).exponential_()
+    check(lib.fl_sparse_race_select(st, ptr(sp_value), nnz, B, L, c, ptr(noise), ptr(ws), ws.numel(), ptr(keep)),
+          "sparse_race_select")
     return torch.nonzero(keep, as_tuple=True)[0]
 
 
@@ -1081,10 +1136,60 @@ class FlashLogFunctionSparse3DAllEdgesSum(autograd.Function):
         return (grads + (None,))[:len(ctx.needs_input_grad)]
 
 
+def _topk_hop_forward(ctx, aggregate, sp_batch, sp_level, sp_entity, sp_value, w, ori_col_ind, ori_order,
+                      inv_col_ind, inv_order, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                      ori_group_edge_count, inv_row_group_ptr, inv_group_rel, inv_group_edge_start,
+                      inv_group_edge_count, mask_values, weight, B, L, E, r_size, wot_i, topk_edges,
+                      edge_weight_is_score, topk_nodes, sampling):
+    """Forward of the top-k sum / max hops (flashlog_kernel.py:1158-1348,
+    1450-1626): c1 (sampled with the exponential race when training), then
+    the hop with the c2 threshold or, when sampling, the training quotas
+    seeded by one draw of torch's CPU generator, as the reference draws it."""
+    if weight is not None and bool(getattr(weight, "requires_grad", False)):
+        raise NotImplementedError("trainable edge weights on the sparse top-k path are not in this build yet")
+    _require_cuda(sp_value, w)
+    if not bool(torch.isfinite(w).all()):
+        raise RuntimeError("FlashLog sparse top-k received non-finite attention weights")
+    sp_batch, sp_level, sp_entity, sp_value = _prune_sparse_sources(
+        ctx, sp_batch, sp_level, sp_entity, sp_value, topk_nodes, w.size(1), sampling)
+    mask_f = mask_values.contiguous().view(-1)
+    if weight is not None and edge_weight_is_score:
+        m = mask_f.float() * weight.to(device=mask_f.device, dtype=torch.float).view(-1)
+        ori_mask = m[ori_order.long()].contiguous()
+        inv_mask = m[inv_order.long()].contiguous()
+    elif weight is None:
+        ori_mask = _cached_mask_order(mask_values, ori_order)
+        inv_mask = _cached_mask_order(mask_values, inv_order)
+    else:
+        ori_mask = _apply_mask_order(mask_f, ori_order, weight)
+        inv_mask = _apply_mask_order(mask_f, inv_order, weight)
+    max_hop = aggregate == _SPARSE_MAX
+    sides = _SparseSides(ori_col_ind, ori_mask, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                         ori_group_edge_count, inv_col_ind, inv_mask, inv_row_group_ptr, inv_group_rel,
+                         inv_group_edge_start, inv_group_edge_count,
+                         ori_order if max_hop else None, inv_order if max_hop else None)
+    seed = int(torch.randint(0, 2 ** 63 - 1, ()).item()) if sampling else -1
+    need = bool(any(ctx.needs_input_grad))
+    idx, vals, state = _sparse_forward(sp_batch, sp_level, sp_entity, sp_value, w, sides, B, L, E, r_size,
+                                       wot_i, _SPARSE_TOPK, int(topk_edges), need, aggregate=aggregate, seed=seed)
+    ctx.state, ctx.out_indices, ctx.dims = state, idx, (int(B), int(L), int(E), tuple(w.shape))
+    return _coo(idx, vals, int(B), int(L), int(E))
+
+
+def _topk_hop_backward(ctx, grad_out):
+    B, L, E, wshape = ctx.dims
+    aligned = _align_sparse_grad_to_output(grad_out, ctx.out_indices, L, E)
+    gv, gw = _sparse_backward(ctx.state, aligned)
+    gv = _restore_pruned_gradient(ctx, gv)
+    grads = (None, None, None, gv, gw.view(wshape)) + (None,) * 28
+    return grads[:len(ctx.needs_input_grad)]
+
+
 class FlashLogFunctionSparse3DTopKSum(autograd.Function):
     """Sparse sum hop with the c1 entity budget and the c2 edge budget
     (flashlog_kernel.py:1158-1348): hard-masked edges take part in the c2
-    selection but produce no coordinate."""
+    selection but produce no coordinate.  sampling=True: the training
+    selections (exponential-race c1, quota c2)."""
 
     @staticmethod
     def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, w,
@@ -1094,44 +1199,41 @@ class FlashLogFunctionSparse3DTopKSum(autograd.Function):
                 inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
                 mask_values, weight, B, L, E, r_size, wot_i, topk_edges,
                 edge_weight_is_score=False, topk_nodes=None, cache_backward=True, sampling=False):
-        if sampling:
-            raise NotImplementedError("sampled quotas (training --use_topk) are not in this build yet")
-        if weight is not None and bool(getattr(weight, "requires_grad", False)):
-            raise NotImplementedError("trainable edge weights on the sparse top-k path are not in this build yet")
-        _require_cuda(sp_value, w)
-        if not bool(torch.isfinite(w).all()):
-            raise RuntimeError("FlashLog sparse top-k received non-finite attention weights")
-        sp_batch, sp_level, sp_entity, sp_value = _prune_sparse_sources(
-            ctx, sp_batch, sp_level, sp_entity, sp_value, topk_nodes, w.size(1), sampling)
-        mask_f = mask_values.contiguous().view(-1)
-        if weight is not None and edge_weight_is_score:
-            m = mask_f.float() * weight.to(device=mask_f.device, dtype=torch.float).view(-1)
-            ori_mask = m[ori_order.long()].contiguous()
-            inv_mask = m[inv_order.long()].contiguous()
-        elif weight is None:
-            ori_mask = _cached_mask_order(mask_values, ori_order)
-            inv_mask = _cached_mask_order(mask_values, inv_order)
-        else:
-            ori_mask = _apply_mask_order(mask_f, ori_order, weight)
-            inv_mask = _apply_mask_order(mask_f, inv_order, weight)
-        sides = _SparseSides(ori_col_ind, ori_mask, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
-                             ori_group_edge_count, inv_col_ind, inv_mask, inv_row_group_ptr, inv_group_rel,
-                             inv_group_edge_start, inv_group_edge_count)
-        K = int(topk_edges)
-        need = bool(any(ctx.needs_input_grad))
-        idx, vals, state = _sparse_forward(sp_batch, sp_level, sp_entity, sp_value, w, sides, B, L, E, r_size,
-                                           wot_i, _SPARSE_TOPK, K, need)
-        ctx.state, ctx.out_indices, ctx.dims = state, idx, (int(B), int(L), int(E), tuple(w.shape))
-        return _coo(idx, vals, int(B), int(L), int(E))
+        return _topk_hop_forward(ctx, _SPARSE_SUM, sp_batch, sp_level, sp_entity, sp_value, w, ori_col_ind,
+                                 ori_order, inv_col_ind, inv_order, ori_row_group_ptr, ori_group_rel,
+                                 ori_group_edge_start, ori_group_edge_count, inv_row_group_ptr, inv_group_rel,
+                                 inv_group_edge_start, inv_group_edge_count, mask_values, weight, B, L, E, r_size,
+                                 wot_i, topk_edges, edge_weight_is_score, topk_nodes, sampling)
 
     @staticmethod
     def backward(ctx, grad_out):
-        B, L, E, wshape = ctx.dims
-        aligned = _align_sparse_grad_to_output(grad_out, ctx.out_indices, L, E)
-        gv, gw = _sparse_backward(ctx.state, aligned)
-        gv = _restore_pruned_gradient(ctx, gv)
-        grads = (None, None, None, gv, gw.view(wshape)) + (None,) * 28
-        return grads[:len(ctx.needs_input_grad)]
+        return _topk_hop_backward(ctx, grad_out)
+
+
+class FlashLogFunctionSparse3DTopKMax(autograd.Function):
+    """Sparse max hop (flashlog_kernel.py:1450-1626): per output the largest
+    item, ties to ORI before INV before the identity term, then the smaller
+    original edge id, then the earlier item; masked kept edges are 0-valued
+    items (their coordinates exist).  The backward routes each output's
+    gradient to its winner only."""
+
+    @staticmethod
+    def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, w,
+                ori_row_ptr, ori_col_ind, ori_r_ind, ori_order,
+                inv_row_ptr, inv_col_ind, inv_r_ind, inv_order,
+                ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                mask_values, weight, B, L, E, r_size, wot_i, topk_edges,
+                edge_weight_is_score=False, topk_nodes=None, cache_backward=True, sampling=False):
+        return _topk_hop_forward(ctx, _SPARSE_MAX, sp_batch, sp_level, sp_entity, sp_value, w, ori_col_ind,
+                                 ori_order, inv_col_ind, inv_order, ori_row_group_ptr, ori_group_rel,
+                                 ori_group_edge_start, ori_group_edge_count, inv_row_group_ptr, inv_group_rel,
+                                 inv_group_edge_start, inv_group_edge_count, mask_values, weight, B, L, E, r_size,
+                                 wot_i, topk_edges, edge_weight_is_score, topk_nodes, sampling)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        return _topk_hop_backward(ctx, grad_out)
 
 
 class _SparseCpuPath:

@@ -68,6 +68,8 @@ typedef struct fl_side {
     const int32_t *sup_seg0;       /* [nsup] first segment of each         */
     const int32_t *pos_src;        /* [M] source entity of each position   */
     const int16_t *pos_rel;        /* [M] relation of each position        */
+    const int32_t *order;          /* [M] original edge id of each position
+                                      (sparse max tie order; else unused)  */
 } fl_side;
 
 const char *fl_last_error(void);
@@ -232,6 +234,17 @@ typedef struct fl_sparse_hop {
     size_t ws2_bytes;
     int64_t items, tiles;
     const int64_t *operators;          /* mode 2: [B*L] operator per row     */
+    int aggregate;                     /* 0 sum (masked kept edges produce no
+                                          coordinate), 1 max (masked kept
+                                          edges are 0-valued items; ties go to
+                                          ORI < INV < identity, then the
+                                          smaller original edge id, then raw
+                                          order: flashlog_kernel.py:399-478) */
+    int64_t sampling_seed;             /* mode 0: < 0 the c2 threshold;
+                                          >= 0 the training quotas of
+                                          flashlog.cu:1433-1528 (weighted
+                                          floors + SplitMix64-phased
+                                          systematic residuals)             */
 } fl_sparse_hop;
 
 /* Destination buckets per row (8192 entities each).  The sparse hop
@@ -250,17 +263,19 @@ size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R);
 int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv,
                    const fl_sparse_hop *h, int64_t *plan);
 
-/* Expansion workspace bytes (backward = 1 when raw_local will be kept). */
+/* Expansion workspace bytes (backward = 1 when raw_local will be kept;
+ * aggregate as in fl_sparse_hop). */
 size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t R,
-                              int64_t E, int backward);
+                              int64_t E, int backward, int aggregate);
 
 /* Replaces the fill kernels (flashlog.cu:1402-1559,1759-1854) and the
- * coalesce (flashlog_kernel.py:258-357): raw items in the CPU path's order
- * (flashlog.cpp:1388-1486), grouped per (row, destination) and added to 0 in
- * that order.  out_base [B*L*buckets + 1] receives the output offsets of
- * every (row, bucket) (out_base[last] = output count); raw_local (optional,
- * [items]) the output index of every raw item within its bucket, for
- * fl_sparse_backward. */
+ * coalesce (flashlog_kernel.py:258-357 sum, :399-478 max): raw items in the
+ * CPU path's order (flashlog.cpp:1388-1486), grouped per (row, destination)
+ * and added to 0 in that order (sum) or reduced to the winning item (max).
+ * out_base [B*L*buckets + 1] receives the output offsets of every (row,
+ * bucket) (out_base[last] = output count); raw_local (optional, [items]) the
+ * output index of every raw item within its bucket (max: of the winning
+ * items; -1 for the others), for fl_sparse_backward. */
 int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv,
                      const fl_sparse_hop *h, int64_t *out_base,
                      int32_t *raw_local);
@@ -271,11 +286,12 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h,
                    const int64_t *out_base, int64_t *out_b, int64_t *out_l,
                    int64_t *out_e, float *out_v);
 
-/* Replaces flashlog_backward_sparse3d_cached_cuda (flashlog.cu:2243-2478,
- * kernels :1856-1997): grad_v[i] = sum over entry i's items of (g*m)*w
- * (+ g*w[n-1] for the identity item); grad_w [B*L, n] accumulates (g*m)*a
- * (+ g*a at n-1).  grad_out holds the gradient of every output entry.
- * Needs the plan workspace of the forward. */
+/* Replaces flashlog_backward_sparse3d_cached_cuda and, for max,
+ * flashlog_backward_sparse3d_max_cached_cuda (flashlog.cu:2243-2478,
+ * kernels :1856-1997): grad_v[i] = sum over entry i's items (max: its
+ * winning items) of (g*m)*w (+ g*w[n-1] for the identity item); grad_w
+ * [B*L, n] accumulates (g*m)*a (+ g*a at n-1).  grad_out holds the gradient
+ * of every output entry.  Needs the plan workspace of the forward. */
 int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv,
                        const fl_sparse_hop *h, const int64_t *out_base,
                        const int32_t *raw_local, const float *grad_out,
@@ -289,6 +305,27 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv,
 int fl_sparse_topc(void *stream, const int64_t *sp_b, const int64_t *sp_l,
                    const float *v, int64_t nnz, int64_t B, int64_t L,
                    int64_t c, int32_t *keep, int64_t *row_ptr, int64_t *err);
+
+/* Sampled c1 (_sparse_topc_entries with sampling=True, flashlog_kernel.py:
+ * 1092-1140): the exponential race.  Two phases around the caller's noise
+ * draw.  fl_sparse_race_plan (c >= 1; c = 0 is fl_sparse_topc): per row r =
+ * b*L + l of a COO state sorted by row, rows with more than c nonzeros make
+ * their nonzero entries candidates; info (device int64[2]) receives
+ * {candidates, error} (error 1 index out of range, 2 not sorted by row,
+ * 3 a candidate value not finite and positive).  The caller then draws one
+ * Exp(1) double per candidate (entry order) into noise and calls
+ * fl_sparse_race_select: in those rows keep[i] = 1 for the c candidates with
+ * the largest log(v) - log(noise) (ties to the earlier entry), 0 for the
+ * rest; other rows keep every entry.  ws is the same workspace in both
+ * calls. */
+size_t fl_sparse_race_bytes(int64_t nnz, int64_t R);
+int fl_sparse_race_plan(void *stream, const int64_t *sp_b, const int64_t *sp_l,
+                        const float *v, int64_t nnz, int64_t B, int64_t L,
+                        int64_t c, void *ws, size_t ws_bytes, int64_t *info);
+int fl_sparse_race_select(void *stream, const float *v, int64_t nnz,
+                          int64_t B, int64_t L, int64_t c,
+                          const double *noise, void *ws, size_t ws_bytes,
+                          int32_t *keep);
 
 /* Bytes of the row pointer + error slots used by the normalize calls. */
 size_t fl_sparse_rowptr_bytes(int64_t R);

@@ -20,6 +20,9 @@
  *   or_sparse_forward        flashlog_kernel/source/flashlog.cpp:1388-1486 (mode 0),
  *                            flashlog.cu:1743-1854 coordinates (mode 1)
  *   or_sparse_backward       flashlog_kernel/source/flashlog.cu:1856-1959
+ *   or_quota_takes           flashlog_kernel/source/flashlog.cu:1433-1528 (training quotas)
+ *   or_sparse_max_forward    flashlog_kernel/flashlog_kernel.py:399-478,1450-1626
+ *   or_sparse_max_backward   flashlog_kernel/source/flashlog.cu:1918-1997,2364-2410
  *   or_sparse_normalize      flashlog_kernel/flashlog_kernel.py:551-555
  *
  * Pinning (how each function is checked, see tests/test_oracle_*.py):
@@ -36,6 +39,13 @@
  *     (oracle/_ref) in mode 0 and, where the modes coincide, in mode 1; float64
  *     closed form over the expanded edge list.
  *   or_sparse_backward: float64 adjoint of the closed form.
+ *   or_quota_takes: the published SplitMix64 output sequence (seed 0); the
+ *     closed form of the reference's own CPU quota rule (flashlog_kernel.py:
+ *     1978-2003: floors + differences of the rounded capacity prefix) with
+ *     the same phase; budget and capacity invariants.
+ *   or_sparse_max_forward/backward: numpy brute force over the expanded item
+ *     list (lexicographic sort by value, source, edge id, item order), the
+ *     plain maximum where values are distinct, and constructed ties.
  *   or_sparse_normalize: closed form.
  *
  * Compile with -O2 -ffp-contract=off (no FMA contraction: the reference's
@@ -521,16 +531,83 @@ void or_dense_max_backward(int64_t BL, int64_t E, int64_t n, const float *A, con
  * -1 when cap is too small.                                                 */
 typedef struct {
     const int32_t *col; const float *mask; const int32_t *gptr; const int16_t *grel;
-    const int32_t *gstart; const int32_t *gcount;
+    const int32_t *gstart; const int32_t *gcount; const int32_t *order;
 } or_side_t;
 
-typedef void (*or_item_fn)(void *ctx, int64_t entry, int dir, int64_t p, int64_t dst, int rel, float m,
+/* SplitMix64 output function (Steele, Lea and Flood 2014; public-domain
+ * splitmix64.c): one step from state z. */
+uint64_t or_splitmix64(uint64_t z)
+{
+    z += 0x9e3779b97f4a7c15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+/* Training quotas of one (entry, side): flashlog.cu:1433-1528, sequentially
+ * in group order.  weights[k] / counts[k] are group k's attention weight and
+ * edge count; takes[k] receives its kept edge count.                        */
+void or_quota_takes(int64_t ngroups, const float *weights, const int32_t *counts, int64_t topk_edges,
+                    int64_t b, int64_t l, int64_t src, int is_inv, int64_t seed, int32_t *takes)
+{
+    int64_t capacity = 0;
+    double weight_sum = 0.0;
+    for (int64_t g = 0; g < ngroups; ++g) {
+        double weight = weights[g];
+        if (weight > 0 && counts[g] > 0) { capacity += counts[g]; weight_sum += weight; }
+    }
+    int64_t target = topk_edges < capacity ? topk_edges : capacity;
+    int64_t allocated = capacity;
+    if (target < capacity) {
+        allocated = 0;
+        for (int64_t g = 0; g < ngroups; ++g) {
+            double weight = weights[g];
+            int64_t count = counts[g];
+            if (weight > 0 && count > 0)
+                allocated += (int64_t)fmin((double)count, floor((double)target * weight / weight_sum));
+        }
+    }
+    int64_t residual = target - allocated, spare_total = capacity - allocated;
+    int64_t left = residual, capacity_left = spare_total, prefix = 0;
+    uint64_t z = (uint64_t)seed ^ ((uint64_t)b * 0x9e3779b97f4a7c15ULL) ^ ((uint64_t)l * 0xbf58476d1ce4e5b9ULL) ^
+                 ((uint64_t)src * 0x94d049bb133111ebULL) ^ (is_inv ? 0xd1b54a32d192ed03ULL : 0x8cb92baa3f3d8dd7ULL);
+    double phase = (double)(or_splitmix64(z) >> 11) * 0x1.0p-53;
+    for (int64_t g = 0; g < ngroups; ++g) {
+        float score = weights[g];
+        int32_t cnt = counts[g];
+        int32_t take = score > 0.0f ? cnt : 0;
+        if (take > 0 && spare_total > 0) {
+            int64_t base = (int64_t)fmin((double)cnt, floor((double)target * (double)score / weight_sum));
+            int64_t spare = (int64_t)cnt - base;
+            prefix += spare;
+            capacity_left -= spare;
+            int64_t cumulative = prefix == spare_total ? residual
+                : (int64_t)floor((double)residual * (double)prefix / (double)spare_total + phase);
+            int64_t extra = cumulative - (residual - left);
+            if (extra > left) extra = left;
+            if (extra > spare) extra = spare;
+            if (extra < 0) extra = 0;
+            if (extra < left - capacity_left) extra = left - capacity_left;
+            left -= extra;
+            take = (int32_t)(base + extra);
+        }
+        takes[g] = take;
+    }
+}
+
+/* Item callback: dir 0 ORI, 1 INV, 2 identity (p = edge = -1, rel = -1);
+ * edge = the original edge id (order[p]) when the side has an order array. */
+typedef void (*or_item_fn)(void *ctx, int64_t entry, int dir, int64_t p, int64_t edge, int64_t dst, int rel, float m,
                            float value);
 
-/* Walks the items of one entry in raw order; the identity item has dir 2. */
-static void or_sparse_walk(int mode, int64_t i, const int64_t *sb, const int64_t *sl, const int64_t *se,
-                           const float *sv, int64_t L, const float *w, int64_t n, const or_side_t *sides,
-                           int64_t r_size, int wot_i, int64_t topk_edges, or_item_fn fn, void *ctx)
+/* Walks the items of one entry in raw order.  mode 0 (top-k): kept edges by
+ * the c2 threshold (seed < 0) or the training quotas (seed >= 0); masked kept
+ * edges are skipped unless keep_masked (the max keeps them as 0-valued
+ * items).  mode 1: every edge of every group. */
+static void or_sparse_walk(int mode, int keep_masked, int64_t seed, int64_t i, const int64_t *sb, const int64_t *sl,
+                           const int64_t *se, const float *sv, int64_t L, const float *w, int64_t n,
+                           const or_side_t *sides, int64_t r_size, int wot_i, int64_t topk_edges, or_item_fn fn,
+                           void *ctx)
 {
     int64_t row = sb[i] * L + sl[i], src = se[i];
     const float *w_bl = w + row * n;
@@ -541,41 +618,57 @@ static void or_sparse_walk(int mode, int64_t i, const int64_t *sb, const int64_t
         if (g0 == g1) continue;
         int64_t keep_in_threshold = 0;
         float threshold_weight = -1.0f;
-        if (mode == 0)
+        int32_t *quota = NULL;
+        if (mode == 0 && seed >= 0 && topk_edges > 0) {
+            float *wg = (float *)malloc(sizeof(float) * (size_t)(g1 - g0));
+            quota = (int32_t *)malloc(sizeof(int32_t) * (size_t)(g1 - g0));
+            for (int64_t g = g0; g < g1; ++g) wg[g - g0] = w_bl[off + sd->grel[g]];
+            or_quota_takes(g1 - g0, wg, sd->gcount + g0, topk_edges, sb[i], sl[i], src, dir, seed, quota);
+            free(wg);
+        } else if (mode == 0) {
             threshold_weight = or_group_threshold_f32(w_bl + off, sd->grel, sd->gcount, g0, g1, topk_edges,
                                                       &keep_in_threshold);
+        }
         int64_t threshold_seen = 0;
         for (int64_t g = g0; g < g1; ++g) {
             int32_t *group_edge_count = (int32_t *)sd->gcount;
             float w_val = w_bl[off + sd->grel[g]];
-            int32_t take;
+            int32_t kept;
             if (mode == 0) {
-                OR_TAKE(float)
-                if (take <= 0) continue;
-                for (int64_t p = sd->gstart[g]; p < sd->gstart[g] + take; ++p) {
+                if (quota) {
+                    kept = quota[g - g0];
+                } else {
+                    OR_TAKE(float)
+                    kept = take;
+                }
+                if (kept <= 0) continue;
+                for (int64_t p = sd->gstart[g]; p < sd->gstart[g] + kept; ++p) {
                     float m = sd->mask[p];
-                    if (m == 0) continue;
-                    fn(ctx, i, dir, p, sd->col[p], sd->grel[g], m, sv[i] * w_val * m);
+                    if (m == 0 && !keep_masked) continue;
+                    fn(ctx, i, dir, p, sd->order ? sd->order[p] : -1, sd->col[p], sd->grel[g], m,
+                       sv[i] * w_val * m);
                 }
             } else {
-                take = group_edge_count[g];
+                kept = group_edge_count[g];
                 float gp = sv[i] * w_val;
-                for (int64_t p = sd->gstart[g]; p < sd->gstart[g] + take; ++p) {
+                for (int64_t p = sd->gstart[g]; p < sd->gstart[g] + kept; ++p) {
                     float m = sd->mask[p];
-                    fn(ctx, i, dir, p, sd->col[p], sd->grel[g], m, gp * m);
+                    fn(ctx, i, dir, p, sd->order ? sd->order[p] : -1, sd->col[p], sd->grel[g], m, gp * m);
                 }
             }
         }
+        free(quota);
     }
-    if (!wot_i) fn(ctx, i, 2, -1, src, -1, 1.0f, sv[i] * w_bl[n - 1]);
+    if (!wot_i) fn(ctx, i, 2, -1, -1, src, -1, 1.0f, sv[i] * w_bl[n - 1]);
 }
 
 typedef struct { float *acc; int64_t *mark; int64_t *touched; int64_t ntouched; int64_t stamp; } or_acc_t;
 
-static void or_acc_item(void *ctx, int64_t entry, int dir, int64_t p, int64_t dst, int rel, float m, float value)
+static void or_acc_item(void *ctx, int64_t entry, int dir, int64_t p, int64_t edge, int64_t dst, int rel, float m,
+                        float value)
 {
     or_acc_t *a = (or_acc_t *)ctx;
-    (void)entry; (void)dir; (void)p; (void)rel; (void)m;
+    (void)entry; (void)dir; (void)p; (void)edge; (void)rel; (void)m;
     if (a->mark[dst] != a->stamp) {
         a->mark[dst] = a->stamp;
         a->acc[dst] = 0.0f;
@@ -590,16 +683,20 @@ static int or_cmp_i64(const void *x, const void *y)
     return a < b ? -1 : a > b;
 }
 
+#define OR_SIDES                                                                                    \
+    or_side_t sides[2] = {{ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount, ori_order}, \
+                          {inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, inv_order}}
+
 int64_t or_sparse_forward(int mode, int64_t nnz, const int64_t *sb, const int64_t *sl, const int64_t *se,
     const float *sv, int64_t B, int64_t L, int64_t E, const float *w, int64_t n,
     const int32_t *ori_col, const float *ori_mask, const int32_t *ori_gptr, const int16_t *ori_grel,
     const int32_t *ori_gstart, const int32_t *ori_gcount,
     const int32_t *inv_col, const float *inv_mask, const int32_t *inv_gptr, const int16_t *inv_grel,
     const int32_t *inv_gstart, const int32_t *inv_gcount,
-    int64_t r_size, int wot_i, int64_t topk_edges, int64_t cap, int64_t *out_key, float *out_v)
+    int64_t r_size, int wot_i, int64_t topk_edges, int64_t seed, int64_t cap, int64_t *out_key, float *out_v)
 {
-    or_side_t sides[2] = {{ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount},
-                          {inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount}};
+    const int32_t *ori_order = NULL, *inv_order = NULL;
+    OR_SIDES;
     or_acc_t a;
     a.acc = (float *)calloc((size_t)(E > 0 ? E : 1), sizeof(float));
     a.mark = (int64_t *)malloc((size_t)(E > 0 ? E : 1) * sizeof(int64_t));
@@ -611,7 +708,8 @@ int64_t or_sparse_forward(int mode, int64_t nnz, const int64_t *sb, const int64_
         a.stamp = row;
         for (int64_t i = 0; i < nnz; ++i)
             if (sb[i] * L + sl[i] == row)
-                or_sparse_walk(mode, i, sb, sl, se, sv, L, w, n, sides, r_size, wot_i, topk_edges, or_acc_item, &a);
+                or_sparse_walk(mode, 0, seed, i, sb, sl, se, sv, L, w, n, sides, r_size, wot_i, topk_edges,
+                               or_acc_item, &a);
         qsort(a.touched, (size_t)a.ntouched, sizeof(int64_t), or_cmp_i64);
         if (total + a.ntouched > cap) { total = -1; break; }
         for (int64_t k = 0; k < a.ntouched; ++k) {
@@ -633,10 +731,11 @@ typedef struct {
     const int64_t *sb, *sl; int64_t L, E, n, r_size; float *grad_v; float *grad_w; float gsp;
 } or_bwd_t;
 
-static void or_bwd_item(void *ctx, int64_t entry, int dir, int64_t p, int64_t dst, int rel, float m, float value)
+static void or_bwd_item(void *ctx, int64_t entry, int dir, int64_t p, int64_t edge, int64_t dst, int rel, float m,
+                        float value)
 {
     or_bwd_t *c = (or_bwd_t *)ctx;
-    (void)p; (void)value;
+    (void)p; (void)edge; (void)value;
     int64_t row = c->sb[entry] * c->L + c->sl[entry];
     int64_t key = row * c->E + dst;
     int64_t pos = or_lower_bound(c->out_key, c->nout, key);
@@ -657,17 +756,127 @@ void or_sparse_backward(int mode, int64_t nnz, const int64_t *sb, const int64_t 
     const int32_t *ori_gstart, const int32_t *ori_gcount,
     const int32_t *inv_col, const float *inv_mask, const int32_t *inv_gptr, const int16_t *inv_grel,
     const int32_t *inv_gstart, const int32_t *inv_gcount,
-    int64_t r_size, int wot_i, int64_t topk_edges, const int64_t *out_key, int64_t nout, const float *grad_out,
-    float *grad_v, float *grad_w)
+    int64_t r_size, int wot_i, int64_t topk_edges, int64_t seed, const int64_t *out_key, int64_t nout,
+    const float *grad_out, float *grad_v, float *grad_w)
 {
-    or_side_t sides[2] = {{ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount},
-                          {inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount}};
+    const int32_t *ori_order = NULL, *inv_order = NULL;
+    OR_SIDES;
     or_bwd_t c = {out_key, nout, grad_out, w, sv, sb, sl, L, E, n, r_size, grad_v, grad_w, 0.0f};
     memset(grad_w, 0, sizeof(float) * (size_t)(B * L * n));
     for (int64_t i = 0; i < nnz; ++i) {
         c.gsp = 0.0f;
-        or_sparse_walk(mode, i, sb, sl, se, sv, L, w, n, sides, r_size, wot_i, topk_edges, or_bwd_item, &c);
+        or_sparse_walk(mode, 0, seed, i, sb, sl, se, sv, L, w, n, sides, r_size, wot_i, topk_edges, or_bwd_item, &c);
         grad_v[i] = c.gsp;
+    }
+}
+
+/* Sparse max hop: FlashLogFunctionSparse3DTopKMax (flashlog_kernel.py:
+ * 1450-1626) with the coalesce of :399-478.  Items as the top-k walk, masked
+ * kept edges included as (v*w)*0 items; per (row, destination) the winner is
+ * the largest value (== comparison, so zeros of either sign tie), then the
+ * smallest source (ORI 0, INV 1, identity 2), then the smallest original edge
+ * id (0 for the identity item), then the earliest item (raw order within a
+ * source).  Outputs: keys ascending, the winner's value (+0 for a zero), and
+ * the winner's entry, dir (0/1/2) and CSR position (-1 for the identity).  */
+typedef struct {
+    float *best; int32_t *src_rank; int64_t *edge; int64_t *entry; int32_t *dir; int64_t *pos;
+    int64_t *mark; int64_t *touched; int64_t ntouched; int64_t stamp;
+} or_max_t;
+
+static void or_max_item(void *ctx, int64_t entry, int dir, int64_t p, int64_t edge, int64_t dst, int rel, float m,
+                        float value)
+{
+    or_max_t *a = (or_max_t *)ctx;
+    (void)rel; (void)m;
+    int64_t tie_edge = dir == 2 ? 0 : edge;
+    if (a->mark[dst] != a->stamp) {
+        a->mark[dst] = a->stamp;
+        a->touched[a->ntouched++] = dst;
+    } else {
+        float b = a->best[dst];
+        int better = value > b || (value == b && (dir < a->src_rank[dst] ||
+                                                  (dir == a->src_rank[dst] && tie_edge < a->edge[dst])));
+        if (!better) return;
+    }
+    a->best[dst] = value;
+    a->src_rank[dst] = dir;
+    a->edge[dst] = tie_edge;
+    a->entry[dst] = entry;
+    a->dir[dst] = dir;
+    a->pos[dst] = p;
+}
+
+int64_t or_sparse_max_forward(int64_t nnz, const int64_t *sb, const int64_t *sl, const int64_t *se,
+    const float *sv, int64_t B, int64_t L, int64_t E, const float *w, int64_t n,
+    const int32_t *ori_col, const float *ori_mask, const int32_t *ori_gptr, const int16_t *ori_grel,
+    const int32_t *ori_gstart, const int32_t *ori_gcount,
+    const int32_t *inv_col, const float *inv_mask, const int32_t *inv_gptr, const int16_t *inv_grel,
+    const int32_t *inv_gstart, const int32_t *inv_gcount, const int32_t *ori_order, const int32_t *inv_order,
+    int64_t r_size, int wot_i, int64_t topk_edges, int64_t seed, int64_t cap, int64_t *out_key, float *out_v,
+    int64_t *win_entry, int32_t *win_dir, int64_t *win_pos)
+{
+    OR_SIDES;
+    size_t e1 = (size_t)(E > 0 ? E : 1);
+    or_max_t a;
+    a.best = (float *)calloc(e1, sizeof(float));
+    a.src_rank = (int32_t *)calloc(e1, sizeof(int32_t));
+    a.edge = (int64_t *)calloc(e1, sizeof(int64_t));
+    a.entry = (int64_t *)calloc(e1, sizeof(int64_t));
+    a.dir = (int32_t *)calloc(e1, sizeof(int32_t));
+    a.pos = (int64_t *)calloc(e1, sizeof(int64_t));
+    a.mark = (int64_t *)malloc(e1 * sizeof(int64_t));
+    a.touched = (int64_t *)malloc(e1 * sizeof(int64_t));
+    for (int64_t e = 0; e < E; ++e) a.mark[e] = -1;
+    int64_t total = 0;
+    for (int64_t row = 0; row < B * L; ++row) {
+        a.ntouched = 0;
+        a.stamp = row;
+        for (int64_t i = 0; i < nnz; ++i)
+            if (sb[i] * L + sl[i] == row)
+                or_sparse_walk(0, 1, seed, i, sb, sl, se, sv, L, w, n, sides, r_size, wot_i, topk_edges,
+                               or_max_item, &a);
+        qsort(a.touched, (size_t)a.ntouched, sizeof(int64_t), or_cmp_i64);
+        if (total + a.ntouched > cap) { total = -1; break; }
+        for (int64_t k = 0; k < a.ntouched; ++k) {
+            int64_t d = a.touched[k];
+            out_key[total + k] = row * E + d;
+            out_v[total + k] = a.best[d] == 0.0f ? 0.0f : a.best[d];
+            win_entry[total + k] = a.entry[d];
+            win_dir[total + k] = a.dir[d];
+            win_pos[total + k] = a.pos[d];
+        }
+        total += a.ntouched;
+    }
+    free(a.best); free(a.src_rank); free(a.edge); free(a.entry); free(a.dir); free(a.pos);
+    free(a.mark); free(a.touched);
+    return total;
+}
+
+/* Backward of the sparse max (flashlog.cu:2364-2410): the gradient of every
+ * output goes to its winner only: edge winner (entry i, side, position p):
+ * grad_v[i] += (g*m)*w[off+rel], grad_w[row, off+rel] += (g*m)*v; identity
+ * winner: grad_v[i] += g*w[n-1], grad_w[row, n-1] += g*v (outputs in order). */
+void or_sparse_max_backward(int64_t nnz, const int64_t *sb, const int64_t *sl, const float *sv, int64_t B,
+    int64_t L, const float *w, int64_t n, const float *ori_mask, const int16_t *ori_prel, const float *inv_mask,
+    const int16_t *inv_prel, int64_t r_size, int64_t nout, const float *grad_out, const int64_t *win_entry,
+    const int32_t *win_dir, const int64_t *win_pos, float *grad_v, float *grad_w)
+{
+    memset(grad_v, 0, sizeof(float) * (size_t)nnz);
+    memset(grad_w, 0, sizeof(float) * (size_t)(B * L * n));
+    for (int64_t o = 0; o < nout; ++o) {
+        int64_t i = win_entry[o];
+        int64_t row = sb[i] * L + sl[i];
+        float g = grad_out[o];
+        if (win_dir[o] == 2) {
+            grad_v[i] += g * w[row * n + n - 1];
+            grad_w[row * n + n - 1] += g * sv[i];
+            continue;
+        }
+        int64_t p = win_pos[o];
+        float m = win_dir[o] ? inv_mask[p] : ori_mask[p];
+        int64_t col = (win_dir[o] ? r_size + inv_prel[p] : ori_prel[p]);
+        grad_v[i] += g * m * w[row * n + col];
+        grad_w[row * n + col] += g * m * sv[i];
     }
 }
 

@@ -316,8 +316,9 @@ def _sparse_cap(e, csr, nnz):
     return max(cap, 1)
 
 
-def sparse_forward(mode, b, l, e, v, B, L, E, w, csr, masks, r_size, wot_i=False, topk_edges=1 << 60):
-    """Returns (keys, values): keys = (b*L + l)*E + e ascending."""
+def sparse_forward(mode, b, l, e, v, B, L, E, w, csr, masks, r_size, wot_i=False, topk_edges=1 << 60, seed=-1):
+    """Returns (keys, values): keys = (b*L + l)*E + e ascending.  seed >= 0:
+    the training quotas (flashlog.cu:1433-1528) instead of the threshold."""
     b, l, e, v = _sparse_args(b, l, e, v)
     w = _c(w, np.float32).reshape(B * L, -1)
     n = w.shape[1]
@@ -331,13 +332,13 @@ def sparse_forward(mode, b, l, e, v, B, L, E, w, csr, masks, r_size, wot_i=False
     cnt = fn(ctypes.c_int(mode), ctypes.c_int64(v.shape[0]), _p(b), _p(l), _p(e), _p(v), ctypes.c_int64(B),
              ctypes.c_int64(L), ctypes.c_int64(E), _p(w), ctypes.c_int64(n), *[_p(a) for a in args],
              ctypes.c_int64(r_size), ctypes.c_int(int(bool(wot_i))), ctypes.c_int64(int(topk_edges)),
-             ctypes.c_int64(cap), _p(keys), _p(vals))
+             ctypes.c_int64(int(seed)), ctypes.c_int64(cap), _p(keys), _p(vals))
     assert cnt >= 0
     return keys[:cnt].copy(), vals[:cnt].copy()
 
 
 def sparse_backward(mode, b, l, e, v, B, L, E, w, csr, masks, r_size, out_keys, grad_out, wot_i=False,
-                    topk_edges=1 << 60):
+                    topk_edges=1 << 60, seed=-1):
     b, l, e, v = _sparse_args(b, l, e, v)
     w = _c(w, np.float32).reshape(B * L, -1)
     n = w.shape[1]
@@ -350,9 +351,104 @@ def sparse_backward(mode, b, l, e, v, B, L, E, w, csr, masks, r_size, out_keys, 
     lib().or_sparse_backward(ctypes.c_int(mode), ctypes.c_int64(v.shape[0]), _p(b), _p(l), _p(e), _p(v),
                              ctypes.c_int64(B), ctypes.c_int64(L), ctypes.c_int64(E), _p(w), ctypes.c_int64(n),
                              *[_p(a) for a in args], ctypes.c_int64(r_size), ctypes.c_int(int(bool(wot_i))),
-                             ctypes.c_int64(int(topk_edges)), _p(out_keys), ctypes.c_int64(out_keys.shape[0]),
-                             _p(grad_out), _p(gv), _p(gw))
+                             ctypes.c_int64(int(topk_edges)), ctypes.c_int64(int(seed)), _p(out_keys),
+                             ctypes.c_int64(out_keys.shape[0]), _p(grad_out), _p(gv), _p(gw))
     return gv, gw
+
+
+def sparse_max_forward(b, l, e, v, B, L, E, w, csr, masks, r_size, wot_i=False, topk_edges=1 << 60, seed=-1):
+    """Sparse max hop (flashlog_kernel.py:399-478,1450-1626).  Returns
+    (keys, values, win_entry, win_dir, win_pos): the winner of every output
+    (entry index, 0 ORI / 1 INV / 2 identity, CSR position or -1)."""
+    b, l, e, v = _sparse_args(b, l, e, v)
+    w = _c(w, np.float32).reshape(B * L, -1)
+    n = w.shape[1]
+    masks = tuple(_c(m, np.float32) for m in masks)
+    args = _csr_args(csr, masks)
+    orders = [_c(csr[3], np.int32), _c(csr[7], np.int32)]
+    cap = _sparse_cap(e, csr, v.shape[0])
+    keys = np.empty(cap, np.int64)
+    vals = np.empty(cap, np.float32)
+    went = np.empty(cap, np.int64)
+    wdir = np.empty(cap, np.int32)
+    wpos = np.empty(cap, np.int64)
+    fn = lib().or_sparse_max_forward
+    fn.restype = ctypes.c_int64
+    cnt = fn(ctypes.c_int64(v.shape[0]), _p(b), _p(l), _p(e), _p(v), ctypes.c_int64(B), ctypes.c_int64(L),
+             ctypes.c_int64(E), _p(w), ctypes.c_int64(n), *[_p(a) for a in args], *[_p(a) for a in orders],
+             ctypes.c_int64(r_size), ctypes.c_int(int(bool(wot_i))), ctypes.c_int64(int(topk_edges)),
+             ctypes.c_int64(int(seed)), ctypes.c_int64(cap), _p(keys), _p(vals), _p(went), _p(wdir), _p(wpos))
+    assert cnt >= 0
+    return keys[:cnt].copy(), vals[:cnt].copy(), went[:cnt].copy(), wdir[:cnt].copy(), wpos[:cnt].copy()
+
+
+def sparse_max_backward(b, l, v, B, L, w, csr, masks, r_size, grad_out, win_entry, win_dir, win_pos):
+    """Gradient of the sparse max through the forward's winners
+    (flashlog.cu:2364-2410).  Returns (grad_v, grad_w [B*L, n])."""
+    b, l, _, v = _sparse_args(b, l, b, v)
+    w = _c(w, np.float32).reshape(B * L, -1)
+    n = w.shape[1]
+    om, im = (_c(m, np.float32) for m in masks)
+    orel = _c(np.asarray(csr[2]), np.int16)
+    irel = _c(np.asarray(csr[6]), np.int16)
+    grad_out = _c(grad_out, np.float32)
+    went, wdir, wpos = _c(win_entry, np.int64), _c(win_dir, np.int32), _c(win_pos, np.int64)
+    gv = np.empty(max(v.shape[0], 1), np.float32)
+    gw = np.empty((B * L, n), np.float32)
+    lib().or_sparse_max_backward(ctypes.c_int64(v.shape[0]), _p(b), _p(l), _p(v), ctypes.c_int64(B),
+                                 ctypes.c_int64(L), _p(w), ctypes.c_int64(n), _p(om), _p(orel), _p(im), _p(irel),
+                                 ctypes.c_int64(r_size), ctypes.c_int64(grad_out.shape[0]), _p(grad_out), _p(went),
+                                 _p(wdir), _p(wpos), _p(gv), _p(gw))
+    return gv[:v.shape[0]], gw
+
+
+def splitmix64(state):
+    """One SplitMix64 output from state (uint64)."""
+    fn = lib().or_splitmix64
+    fn.restype = ctypes.c_uint64
+    return int(fn(ctypes.c_uint64(state & 0xFFFFFFFFFFFFFFFF)))
+
+
+def quota_takes(weights, counts, topk_edges, b, l, src, is_inv, seed):
+    """Training quotas of one (entry, side) (flashlog.cu:1433-1528)."""
+    weights = _c(weights, np.float32)
+    counts = _c(counts, np.int32)
+    takes = np.empty(max(weights.shape[0], 1), np.int32)
+    lib().or_quota_takes(ctypes.c_int64(weights.shape[0]), _p(weights), _p(counts), ctypes.c_int64(int(topk_edges)),
+                         ctypes.c_int64(int(b)), ctypes.c_int64(int(l)), ctypes.c_int64(int(src)),
+                         ctypes.c_int(int(is_inv)), ctypes.c_int64(int(seed)), _p(takes))
+    return takes[:weights.shape[0]]
+
+
+def quota_phase(b, l, src, is_inv, seed):
+    """The SplitMix64 rounding phase in [0, 1) of one (b, l, source, side)."""
+    m = 0xFFFFFFFFFFFFFFFF
+    z = (int(seed) & m) ^ ((int(b) * 0x9e3779b97f4a7c15) & m) ^ ((int(l) * 0xbf58476d1ce4e5b9) & m) ^ \
+        ((int(src) * 0x94d049bb133111eb) & m) ^ (0xd1b54a32d192ed03 if is_inv else 0x8cb92baa3f3d8dd7)
+    return (splitmix64(z) >> 11) * 2.0 ** -53
+
+
+def quota_closed_form(weights, counts, topk_edges, phase):
+    """Independent check of quota_takes: the reference's own CPU quota rule
+    (flashlog_kernel.py:1978-2003: weighted floors, then differences of the
+    rounded residual-capacity prefix, the last one pinned to the residual)
+    with the same phase.  Agrees with the sequential rule except at
+    floating-point boundaries."""
+    w = np.asarray(weights, np.float32).astype(np.float64)
+    c = np.asarray(counts, np.int64) * (w > 0)
+    cap = int(c.sum())
+    target = min(cap, int(topk_edges))
+    if target == cap:
+        return c
+    wsum = 0.0
+    for x in w[c > 0]:
+        wsum += float(x)
+    base = np.where(c > 0, np.minimum(c, np.floor(target * w / wsum)), 0).astype(np.int64)
+    spare = c - base
+    residual = target - int(base.sum())
+    cumulative = np.floor(residual * np.cumsum(spare).astype(np.float64) / int(spare.sum()) + phase).astype(np.int64)
+    cumulative[-1] = residual
+    return base + np.diff(cumulative, prepend=0)
 
 
 def sparse_normalize(b, l, v, B, L, eps=1e-7):
@@ -382,6 +478,44 @@ def sparse_topc(b, l, v, L, c):
         if c == 0:
             continue
         order = nz[np.lexsort((np.arange(nz.size), -v[nz].astype(np.float64)))]
+        keep[order[:c]] = True
+    return np.nonzero(keep)[0]
+
+
+def sparse_topc_race_candidates(b, l, v, L, c):
+    """Entry indices of the sampled c1's candidates (nonzero entries of rows
+    with more than c nonzeros), in entry order: one noise draw each."""
+    row = np.asarray(b, np.int64) * L + np.asarray(l, np.int64)
+    v = np.asarray(v, np.float32)
+    cand = []
+    for r in np.unique(row):
+        idx = np.nonzero(row == r)[0]
+        nz = idx[v[idx] != 0]
+        if nz.size > c:
+            cand.append(nz)
+    return np.sort(np.concatenate(cand)) if cand else np.zeros(0, np.int64)
+
+
+def sparse_topc_race(b, l, v, L, c, noise):
+    """Sampled c1 (flashlog_kernel.py:1121-1132, sampling=True): in rows with
+    more than c nonzeros keep the c candidates with the largest
+    log(v) - log(noise) (float64; ties to the earlier entry), noise[k] for
+    the k-th candidate in entry order; other rows keep every entry."""
+    row = np.asarray(b, np.int64) * L + np.asarray(l, np.int64)
+    v = np.asarray(v, np.float32)
+    cand = sparse_topc_race_candidates(b, l, v, L, c)
+    noise = np.asarray(noise, np.float64)
+    assert noise.shape[0] == cand.shape[0]
+    keep = np.ones(v.shape[0], bool)
+    score = np.full(v.shape[0], -np.inf)
+    score[cand] = np.log(v[cand].astype(np.float64)) - np.log(noise)
+    is_cand = np.zeros(v.shape[0], bool)
+    is_cand[cand] = True
+    for r in np.unique(row[cand]):
+        idx = np.nonzero(row == r)[0]
+        keep[idx] = False
+        ci = idx[is_cand[idx]]
+        order = ci[np.lexsort((np.arange(ci.size), -score[ci]))]
         keep[order[:c]] = True
     return np.nonzero(keep)[0]
 

@@ -20,10 +20,9 @@ INTERNAL = {"_coalesce_sparse3d_reduce", "_coalesce_sparse3d_sum_raw", "_align_s
 
 PUBLIC = sorted(k for k in SURFACE if k.split(".")[0] not in INTERNAL)
 
-# Reference classes this build does not carry yet (their entry points exist
-# as functions that raise NotImplementedError).  strict: when one is added,
-# its xfail turns into a failure here until it is removed from this set.
-NOT_YET = {"FlashLogFunctionSparse3DTopKMax"}
+# Reference classes this build does not carry yet.  strict: when one is
+# added, its xfail turns into a failure here until it is removed from this set.
+NOT_YET = set()
 
 
 def _params(name):

@@ -1,0 +1,245 @@
+"""GPU parity of the sparse max hop (FlashLogFunctionSparse3DTopKMax) and of
+the training selections (quota c2, exponential-race c1,
+sampled_sparse_propagation) against the oracle: coordinates, values and
+winners bit for bit, gradients within 1e-5 relative."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import attention, bits, masks_for, small_graph, sparse_coo_state, to_torch_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def _fk():
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+    return fk
+
+
+def _case(cfg, scale, B, L, per_row, seed, ties=False, drop=0.1):
+    rng = np.random.default_rng(seed)
+    h, r, t, E, R, csr = small_graph(cfg, scale)
+    n = 2 * R + 1
+    b, l, e, v = sparse_coo_state(B, L, E, per_row, rng, ties=ties)
+    w = attention(B * L, n, rng).reshape(B, L, n)
+    if ties:
+        w[..., : n // 2] = w[..., :1]
+    mbool, masks = masks_for(csr, h.shape[0], rng, drop=drop)
+    return rng, E, R, n, csr, mbool, masks, (b, l, e, v), w
+
+
+def _keys(idx, L, E):
+    idx = idx.cpu().numpy()
+    return (idx[0] * L + idx[1]) * E + idx[2]
+
+
+def _dev(*arrs):
+    return [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in arrs]
+
+
+def _hop(cls, state, w, csr, mbool, B, L, E, R, K, c1=None, wot_i=False, grad=False, sampling=False):
+    b, l, e, v = _dev(*state)
+    v.requires_grad_(grad)
+    wt = torch.from_numpy(w).cuda().requires_grad_(grad)
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    mk = torch.from_numpy(mbool).cuda()
+    out = cls.apply(b, l, e, v, wt, *tc[:4], *tc[4:8], *tc[8:16], mk, None, B, L, E, R, wot_i, K, False, c1,
+                    True, sampling)
+    return out, v, wt
+
+
+def _max(*a, **k):
+    return _hop(_fk().FlashLogFunctionSparse3DTopKMax, *a, **k)
+
+
+def _sum(*a, **k):
+    return _hop(_fk().FlashLogFunctionSparse3DTopKSum, *a, **k)
+
+
+def _check_max(out, v, wt, state, w, csr, masks, B, L, E, R, n, K, wot_i, rng, seed=-1, grad=True):
+    keys, vals, went, wdir, wpos = O.sparse_max_forward(*state, B, L, E, w, csr, masks, R, wot_i, K, seed)
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+    if not grad:
+        return
+    g = rng.standard_normal(keys.shape[0]).astype(np.float32)
+    (out.values() * torch.from_numpy(g).cuda()).sum().backward()
+    gv, gw = O.sparse_max_backward(state[0], state[1], state[3], B, L, w, csr, masks, R, g, went, wdir, wpos)
+    np.testing.assert_allclose(v.grad.cpu().numpy(), gv, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(wt.grad.reshape(B * L, n).cpu().numpy(), gw, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("K", [2, 7, 200, 1 << 60])
+@pytest.mark.parametrize("ties", [False, True])
+@pytest.mark.parametrize("wot_i", [False, True])
+def test_sparse_max_bitexact(K, ties, wot_i):
+    B, L = 4, 3
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 1.0, B, L, 250, 140 + K % 13 + ties + 2 * wot_i,
+                                                      ties=ties, drop=0.2)
+    out, v, wt = _max(state, w, csr, mbool, B, L, E, R, K, wot_i=wot_i, grad=True)
+    _check_max(out, v, wt, state, w, csr, masks, B, L, E, R, n, K, wot_i, rng)
+
+
+@pytest.mark.parametrize("c1", [0, 5, 40])
+def test_sparse_max_with_c1(c1):
+    B, L = 3, 3
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 0.3, B, L, 80, 170 + c1, ties=True)
+    kept = O.sparse_topc(state[0], state[1], state[3], L, c1)
+    sel = tuple(a[kept] for a in state)
+    keys, vals, *_ = O.sparse_max_forward(*sel, B, L, E, w, csr, masks, R, False, 3)
+    out, v, wt = _max(state, w, csr, mbool, B, L, E, R, 3, c1=c1, grad=True)
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+    g = torch.randn(out.values().shape, device="cuda")
+    (out.values() * g).sum().backward()
+    dropped = np.setdiff1d(np.arange(state[3].shape[0]), kept)
+    assert np.all(v.grad.cpu().numpy()[dropped] == 0)
+
+
+def test_sparse_max_hot_destination():
+    """Most edges end at one destination: buckets far above one LDS chunk
+    (the dense-LDS max path), E above one bucket, ties from repeated values."""
+    rng = np.random.default_rng(31)
+    E, R, M = 20000, 5, 60000
+    h = rng.integers(0, E, M)
+    t = np.where(rng.random(M) < 0.7, 12345, rng.integers(0, E, M))
+    r = rng.integers(0, R, M)
+    csr = O.build_csr_structure(h, t, r, E)
+    n = 2 * R + 1
+    B, L = 2, 2
+    b, l, e, v = sparse_coo_state(B, L, E, 1500, rng, ties=True)
+    w = attention(B * L, n, rng).reshape(B, L, n)
+    w[..., :R] = w[..., :1]
+    mbool, masks = masks_for(csr, M, rng, drop=0.05)
+    state = (b, l, e, v)
+    for K in (6, 1 << 60):
+        out, vt, wt = _max(state, w, csr, mbool, B, L, E, R, K, grad=True)
+        _check_max(out, vt, wt, state, w, csr, masks, B, L, E, R, n, K, False, rng)
+
+
+def test_sparse_max_masked_edges_keep_coordinates():
+    B, L = 2, 2
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 0.2, B, L, 60, 7, drop=0.5)
+    out, _, _ = _max(state, w, csr, mbool, B, L, E, R, 1 << 60)
+    s_out, _, _ = _sum(state, w, csr, mbool, B, L, E, R, 1 << 60)
+    mk = set(_keys(out.indices(), L, E).tolist())
+    sk = set(_keys(s_out.indices(), L, E).tolist())
+    assert sk < mk
+    zero = out.values().detach().cpu().numpy() == 0
+    assert zero.sum() >= len(mk - sk)
+
+
+@pytest.mark.parametrize("agg", ["sum", "max"])
+@pytest.mark.parametrize("K", [1, 3, 40])
+@pytest.mark.parametrize("seed", [0, 987654321])
+def test_quota_hop_bitexact(agg, K, seed):
+    """The training quotas (fixed seed) through the internal hop, against the
+    oracle's sequential restatement; forward bits and gradients."""
+    fk = _fk()
+    B, L = 4, 3
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 1.0, B, L, 200, 300 + K + seed % 7, drop=0.2)
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    om, im = _dev(*masks)
+    mx = agg == "max"
+    sides = fk._SparseSides(tc[1], om, tc[8], tc[9], tc[10], tc[11], tc[5], im, tc[12], tc[13], tc[14], tc[15],
+                            tc[3] if mx else None, tc[7] if mx else None)
+    b, l, e, v = _dev(*state)
+    wt = torch.from_numpy(w).cuda()
+    idx, vals, st = fk._sparse_forward(b, l, e, v, wt, sides, B, L, E, R, False, fk._SPARSE_TOPK, K, True,
+                                       aggregate=fk._SPARSE_MAX if mx else fk._SPARSE_SUM, seed=seed)
+    keys = _keys(idx, L, E)
+    g = rng.standard_normal(keys.shape[0]).astype(np.float32)
+    gv, gw = fk._sparse_backward(st, torch.from_numpy(g).cuda())
+    if mx:
+        rk, rv, went, wdir, wpos = O.sparse_max_forward(*state, B, L, E, w, csr, masks, R, False, K, seed)
+        gv_ref, gw_ref = O.sparse_max_backward(state[0], state[1], state[3], B, L, w, csr, masks, R, g, went, wdir,
+                                               wpos)
+    else:
+        rk, rv = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, K, seed)
+        gv_ref, gw_ref = O.sparse_backward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, rk, g, False, K, seed)
+    assert np.array_equal(keys, rk)
+    assert np.array_equal(bits(vals.cpu().numpy()), bits(rv))
+    np.testing.assert_allclose(gv.cpu().numpy(), gv_ref, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(gw.cpu().numpy(), gw_ref, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("agg", ["sum", "max"])
+def test_sampling_seed_drawn_like_reference(agg):
+    """sampling=True draws the quota seed with one torch.randint on the CPU
+    generator (flashlog_kernel.py:1201,1487); same torch seed, same bits."""
+    B, L = 3, 2
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 1.0, B, L, 150, 77)
+    torch.manual_seed(1234)
+    out, _, _ = (_max if agg == "max" else _sum)(state, w, csr, mbool, B, L, E, R, 4, sampling=True)
+    torch.manual_seed(1234)
+    seed = int(torch.randint(0, 2 ** 63 - 1, ()).item())
+    if agg == "max":
+        keys, vals, *_ = O.sparse_max_forward(*state, B, L, E, w, csr, masks, R, False, 4, seed)
+    else:
+        keys, vals = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, 4, seed)
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+
+
+@pytest.mark.parametrize("c", [1, 6, 50])
+def test_race_c1_matches_oracle(c):
+    fk = _fk()
+    rng = np.random.default_rng(c)
+    B, L, E = 3, 2, 4000
+    b, l, e, v = sparse_coo_state(B, L, E, 300, rng)
+    v[rng.random(v.shape[0]) < 0.1] = 0.0  # explicit zeros: never candidates, dropped in over rows
+    cand = O.sparse_topc_race_candidates(b, l, v, L, c)
+    tb, tl, te, tv = _dev(b, l, e, v)
+    torch.manual_seed(99)
+    kept = fk._sparse_topc_entries(tb, tl, te, tv, c, L, sampling=True)
+    torch.manual_seed(99)
+    noise = torch.empty(cand.shape[0], dtype=torch.float64, device="cuda").exponential_()
+    ref = O.sparse_topc_race(b, l, v, L, c, noise.cpu().numpy())
+    assert kept is not None
+    np.testing.assert_array_equal(kept.cpu().numpy(), ref)
+    # validation: a negative candidate value is refused, as the reference does
+    v2 = v.copy()
+    v2[cand[0]] = -1.0
+    with pytest.raises(ValueError):
+        fk._sparse_topc_entries(tb, tl, te, torch.from_numpy(v2).cuda(), c, L, sampling=True)
+    # no row over the budget: nothing pruned, no noise drawn
+    assert fk._sparse_topc_entries(tb, tl, te, tv, 100000 if c > 1 else v.shape[0], L, sampling=True) is None
+
+
+@pytest.mark.parametrize("mode", ["sum", "max"])
+def test_sampled_sparse_propagation_two_hops(mode):
+    """Two training hops with c1 and c2 through the public entry point:
+    reproducible under torch's seed, budgets respected, gradients flow."""
+    fk = _fk()
+    rng = np.random.default_rng(5)
+    h, r, t, E, R, csr = small_graph(2, 1.0)
+    n = 2 * R + 1
+    B, L = 4, 3
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    mk = torch.from_numpy(masks_for(csr, h.shape[0], rng)[0]).cuda()
+    w0 = torch.from_numpy(attention(B * L, n, rng).reshape(B, L, n)).cuda()
+    src = torch.from_numpy(rng.integers(0, E, B)).cuda()
+
+    def run(seed):
+        torch.manual_seed(seed)
+        w = w0.clone().requires_grad_(True)
+        idx = torch.stack([torch.arange(B, device="cuda").repeat_interleave(L),
+                           torch.arange(L, device="cuda").repeat(B), src.repeat_interleave(L)])
+        s = torch.sparse_coo_tensor(idx, torch.ones(B * L, device="cuda"), (B, L, E)).coalesce()
+        for _ in range(2):
+            s = fk.sampled_sparse_propagation(s, w, tc, mk, R, None, False, 20, 5, mode)
+            s = fk.normalize_sparse3d(s)
+        loss = (s.values() ** 2).sum()
+        loss.backward()
+        return s.coalesce(), w.grad.clone()
+
+    s1, g1 = run(3)
+    s2, g2 = run(3)
+    assert torch.equal(s1.indices(), s2.indices()) and torch.equal(s1.values(), s2.values())
+    np.testing.assert_allclose(g1.cpu().numpy(), g2.cpu().numpy(), rtol=1e-5, atol=1e-6)
+    assert torch.isfinite(g1).all() and g1.abs().sum() > 0
+    # c1 = 20 bounds each row's entries before the second hop: at most
+    # 20 * (2 sides * 5 edges + identity) outputs per row
+    rows = s1.indices()[0] * L + s1.indices()[1]
+    assert int(torch.bincount(rows).max()) <= 20 * 11
