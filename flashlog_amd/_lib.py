@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 FL_SEG = 32
 FL_SUP = 16
 
@@ -48,6 +48,8 @@ class FlSide(ctypes.Structure):
         ("pos_src", ctypes.c_void_p),
         ("pos_rel", ctypes.c_void_p),
         ("order", ctypes.c_void_p),
+        ("dscore", ctypes.c_void_p),
+        ("grad_edge", ctypes.c_void_p),
     ]
 
 
@@ -75,6 +77,7 @@ _SIGS = {
                          [ctypes.c_void_p] * 8),
     "fl_apply_mask": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
                                      ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]),
+    "fl_edge_dscore": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64]),
     "fl_mark_active": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
                                       ctypes.c_int64, ctypes.c_void_p]),
     "fl_dense_topc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,

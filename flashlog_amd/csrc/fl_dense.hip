@@ -51,6 +51,16 @@ __global__ void k_apply_mask(const MT *__restrict__ mask, const int32_t *__restr
     out[i] = m;
 }
 
+// out[i] = 1 - sigmoid(weight[order[i]]): the edge-score derivative factor
+// of the sparse backward (flashlog_kernel.py:1306-1336), the sigmoid of
+// k_apply_mask.
+__global__ void k_edge_dscore(const float *__restrict__ weight, const int32_t *__restrict__ order,
+                              float *__restrict__ out, int64_t nnz) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    out[i] = 1.0f - 1.0f / (1.0f + expf(-weight[order[i]]));
+}
+
 __global__ void k_mark_active(const float *__restrict__ A, int32_t *__restrict__ flags,
                               int64_t BL, int64_t E) {
     int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1002,7 +1012,7 @@ int check_side(const fl_side *s, const char *name) {
 
 extern "C" {
 
-int fl_abi_version(void) { return 9; }
+int fl_abi_version(void) { return 10; }
 
 int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool, const int32_t *order,
                   const float *weight, float *out, int64_t nnz) {
@@ -1019,6 +1029,15 @@ int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool, const
         FL_LAUNCH("k_apply_mask", k_apply_mask<float>, dim3((unsigned)nb), dim3(nt), 0, st,
                            (const float *)mask_values, order, weight, out, nnz);
     return fl_check_launch("apply_mask");
+}
+
+int fl_edge_dscore(void *stream, const float *weight, const int32_t *order, float *out, int64_t nnz) {
+    if (nnz < 0) return fl_fail(FL_ERR_ARG, "edge_dscore: negative nnz");
+    if (nnz == 0) return FL_OK;
+    if (!weight || !order || !out) return fl_fail(FL_ERR_ARG, "edge_dscore: null pointer");
+    FL_LAUNCH("k_edge_dscore", k_edge_dscore, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+              weight, order, out, nnz);
+    return fl_check_launch("edge_dscore");
 }
 
 int fl_mark_active(void *stream, const float *A, int64_t BL, int64_t E, int32_t *flags) {

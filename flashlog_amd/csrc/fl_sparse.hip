@@ -1048,6 +1048,10 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
                     const float gm = fl_mul(gv, m);
                     gsp = fl_add(gsp, fl_mul(gm, wv));
                     gwv = fl_mul(gm, a);
+                    if (s.grad_edge) {
+                        const float ge = fl_mul(fl_mul(fl_mul(fl_mul(gv, a), wv), m), s.dscore[p]);
+                        if (ge != 0.0f) atomicAdd(&s.grad_edge[s.order[p]], ge);
+                    }
                 }
             }
             // per-relation sums of this chunk: items of one group are on
@@ -1467,6 +1471,9 @@ int sp_check(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, con
     if (h->aggregate == SP_MAX)
         for (const fl_side *s : {ori, inv})
             if (s->edges > 0 && !s->order) return fl_fail(FL_ERR_ARG, "%s: max needs the sides' edge order", what);
+    for (const fl_side *s : {ori, inv})
+        if (s->edges > 0 && s->grad_edge && (!s->order || !s->dscore))
+            return fl_fail(FL_ERR_ARG, "%s: edge-weight gradients need the order and dscore arrays", what);
     return FL_OK;
 }
 

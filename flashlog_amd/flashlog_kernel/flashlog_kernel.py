@@ -838,12 +838,19 @@ class _SparseSides:
     """FlSide views of the CSR arrays the sparse kernels read (no pull index)."""
 
     def __init__(self, ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount,
-                 inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, ori_order=None, inv_order=None):
+                 inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, ori_order=None, inv_order=None,
+                 ori_dscore=None, inv_dscore=None):
         self.keep = []
-        self.ori = self._side(ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount, ori_order)
-        self.inv = self._side(inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, inv_order)
+        self.ori = self._side(ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount, ori_order, ori_dscore)
+        self.inv = self._side(inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, inv_order, inv_dscore)
 
-    def _side(self, col, mask, gptr, grel, gstart, gcount, order=None):
+    def set_grad_edge(self, grad_edge):
+        """Points both sides' edge-weight gradient at grad_edge (or None)."""
+        p = ptr(grad_edge).value if grad_edge is not None else None
+        self.ori.grad_edge = p
+        self.inv.grad_edge = p
+
+    def _side(self, col, mask, gptr, grel, gstart, gcount, order=None, dscore=None):
         _require_cuda(col, gptr, grel, gstart, gcount)
         col = col.int().contiguous()
         gptr = gptr.int().contiguous()
@@ -860,10 +867,11 @@ class _SparseSides:
             order = order.int().contiguous()
             if order.numel() != col.numel():
                 raise ValueError("order length must equal the number of CSR positions")
-        self.keep += [col, mask, gptr, grel, gstart, gcount, order]
+        self.keep += [col, mask, gptr, grel, gstart, gcount, order, dscore]
         side = FlSide()
         side.edges, side.groups = col.numel(), grel.numel()
         side.order = ptr(order).value if order is not None else None
+        side.dscore = ptr(dscore).value if dscore is not None else None
         side.col_ind, side.mask = ptr(col).value, (ptr(mask).value if mask is not None else None)
         side.row_group_ptr, side.group_rel = ptr(gptr).value, ptr(grel).value
         side.group_start, side.group_count = ptr(gstart).value, ptr(gcount).value
@@ -967,17 +975,23 @@ def _fixed_sides(csr_struct):
 _FIXED_SIDES = {}
 
 
-def _sparse_backward(state, grad_values):
-    """grad_values: gradient of every output entry.  Returns (grad_v, grad_w [R, n])."""
+def _sparse_backward(state, grad_values, grad_edge=None):
+    """grad_values: gradient of every output entry.  Returns (grad_v, grad_w [R, n]);
+    grad_edge (zeroed, by original edge id) receives the edge-weight gradient
+    when the forward's sides carry the dscore factors."""
     h = state.h
     dev = grad_values.device
     grad_values = grad_values.contiguous().float()
     gv = torch.empty(max(h.nnz, 1), dtype=torch.float32, device=dev)
     gw = torch.empty((h.B * h.L, state.n), dtype=torch.float32, device=dev)
-    check(_lib.lib().fl_sparse_backward(_stream(grad_values), ctypes.byref(state.sides.ori),
-                                        ctypes.byref(state.sides.inv), ctypes.byref(h), ptr(state.out_base),
-                                        ptr(state.raw_local), ptr(grad_values), ptr(gv), ptr(gw)),
-          "sparse_backward")
+    state.sides.set_grad_edge(grad_edge)
+    try:
+        check(_lib.lib().fl_sparse_backward(_stream(grad_values), ctypes.byref(state.sides.ori),
+                                            ctypes.byref(state.sides.inv), ctypes.byref(h), ptr(state.out_base),
+                                            ptr(state.raw_local), ptr(grad_values), ptr(gv), ptr(gw)),
+              "sparse_backward")
+    finally:
+        state.sides.set_grad_edge(None)
     gv = gv[:h.nnz]
     if state.perm is not None:
         restored = torch.empty_like(gv)
@@ -1145,8 +1159,7 @@ def _topk_hop_forward(ctx, aggregate, sp_batch, sp_level, sp_entity, sp_value, w
     1450-1626): c1 (sampled with the exponential race when training), then
     the hop with the c2 threshold or, when sampling, the training quotas
     seeded by one draw of torch's CPU generator, as the reference draws it."""
-    if weight is not None and bool(getattr(weight, "requires_grad", False)):
-        raise NotImplementedError("trainable edge weights on the sparse top-k path are not in this build yet")
+    trainable = weight is not None and bool(getattr(weight, "requires_grad", False))
     _require_cuda(sp_value, w)
     if not bool(torch.isfinite(w).all()):
         raise RuntimeError("FlashLog sparse top-k received non-finite attention weights")
@@ -1164,24 +1177,42 @@ def _topk_hop_forward(ctx, aggregate, sp_batch, sp_level, sp_entity, sp_value, w
         ori_mask = _apply_mask_order(mask_f, ori_order, weight)
         inv_mask = _apply_mask_order(mask_f, inv_order, weight)
     max_hop = aggregate == _SPARSE_MAX
+    dscore = (None, None)
+    if trainable:
+        ew = weight.detach().to(device=mask_f.device, dtype=torch.float).contiguous().view(-1)
+        dscore = tuple(_edge_dscore(ew, order) for order in (ori_order, inv_order))
+    with_order = max_hop or trainable
     sides = _SparseSides(ori_col_ind, ori_mask, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
                          ori_group_edge_count, inv_col_ind, inv_mask, inv_row_group_ptr, inv_group_rel,
                          inv_group_edge_start, inv_group_edge_count,
-                         ori_order if max_hop else None, inv_order if max_hop else None)
+                         ori_order if with_order else None, inv_order if with_order else None, *dscore)
     seed = int(torch.randint(0, 2 ** 63 - 1, ()).item()) if sampling else -1
     need = bool(any(ctx.needs_input_grad))
     idx, vals, state = _sparse_forward(sp_batch, sp_level, sp_entity, sp_value, w, sides, B, L, E, r_size,
                                        wot_i, _SPARSE_TOPK, int(topk_edges), need, aggregate=aggregate, seed=seed)
     ctx.state, ctx.out_indices, ctx.dims = state, idx, (int(B), int(L), int(E), tuple(w.shape))
+    ctx.edge_weight = (tuple(weight.shape), weight.dtype, weight.device) if trainable else None
     return _coo(idx, vals, int(B), int(L), int(E))
+
+
+def _edge_dscore(ew, order):
+    order = order.to(device=ew.device, dtype=torch.int32).contiguous()
+    out = torch.empty(order.numel(), dtype=torch.float32, device=ew.device)
+    check(_lib.lib().fl_edge_dscore(_stream(ew), ptr(ew), ptr(order), ptr(out), order.numel()), "edge_dscore")
+    return out
 
 
 def _topk_hop_backward(ctx, grad_out):
     B, L, E, wshape = ctx.dims
     aligned = _align_sparse_grad_to_output(grad_out, ctx.out_indices, L, E)
-    gv, gw = _sparse_backward(ctx.state, aligned)
+    grad_edge = None
+    if ctx.edge_weight is not None:
+        shape, dtype, device = ctx.edge_weight
+        grad_edge = torch.zeros(int(np.prod(shape)), dtype=torch.float32, device=aligned.device)
+    gv, gw = _sparse_backward(ctx.state, aligned, grad_edge)
     gv = _restore_pruned_gradient(ctx, gv)
-    grads = (None, None, None, gv, gw.view(wshape)) + (None,) * 28
+    ge = grad_edge.view(shape).to(device=device, dtype=dtype) if grad_edge is not None else None
+    grads = (None, None, None, gv, gw.view(wshape)) + (None,) * 17 + (ge,) + (None,) * 10
     return grads[:len(ctx.needs_input_grad)]
 
 

@@ -69,7 +69,14 @@ typedef struct fl_side {
     const int32_t *pos_src;        /* [M] source entity of each position   */
     const int16_t *pos_rel;        /* [M] relation of each position        */
     const int32_t *order;          /* [M] original edge id of each position
-                                      (sparse max tie order; else unused)  */
+                                      (sparse max tie order, edge-weight
+                                      gradients; else unused)              */
+    const float *dscore;           /* [M] optional: 1 - sigmoid(edge weight)
+                                      of each position (trainable edge
+                                      weights, sparse backward)            */
+    float *grad_edge;              /* optional: [edges] gradient of the edge
+                                      weights by original edge id (both
+                                      sides may share it)                  */
 } fl_side;
 
 const char *fl_last_error(void);
@@ -113,6 +120,12 @@ int fl_pull_segments(int64_t nodes, const int32_t *pull_ptr, int64_t *nseg,
 int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool,
                   const int32_t *order, const float *weight, float *out,
                   int64_t nnz);
+
+/* out[i] = 1 - sigmoid(weight[order[i]]) for i < nnz: the per-position edge
+ * score derivative factor of the sparse backward with trainable edge
+ * weights (flashlog_kernel.py:1306-1336, score_function :221). */
+int fl_edge_dscore(void *stream, const float *weight, const int32_t *order,
+                   float *out, int64_t nnz);
 
 /* Replaces compute_active_nodes_cuda's flag pass (flashlog.cu:1257-1284):
  * flags[e] = 1 if any A[:, e] != 0 else 0. */
@@ -291,7 +304,10 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h,
  * kernels :1856-1997): grad_v[i] = sum over entry i's items (max: its
  * winning items) of (g*m)*w (+ g*w[n-1] for the identity item); grad_w
  * [B*L, n] accumulates (g*m)*a (+ g*a at n-1).  grad_out holds the gradient
- * of every output entry.  Needs the plan workspace of the forward. */
+ * of every output entry.  With a side's grad_edge set (trainable edge
+ * weights, flashlog_kernel.py:1306-1336), grad_edge[order[p]] also
+ * accumulates (((g*a)*w)*m)*dscore[p] for the side's items (the caller
+ * zeroes it).  Needs the plan workspace of the forward. */
 int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv,
                        const fl_sparse_hop *h, const int64_t *out_base,
                        const int32_t *raw_local, const float *grad_out,

@@ -243,3 +243,76 @@ def test_sampled_sparse_propagation_two_hops(mode):
     # 20 * (2 sides * 5 edges + identity) outputs per row
     rows = s1.indices()[0] * L + s1.indices()[1]
     assert int(torch.bincount(rows).max()) <= 20 * 11
+
+
+@pytest.mark.parametrize("agg", ["sum", "max"])
+def test_trainable_edge_weights(agg):
+    """Soft edge weights (use_soft): masks mask*sigmoid(ew) and the edge-weight
+    gradient of flashlog_kernel.py:1306-1336, against a float64 brute force
+    over the kept (sum) or winning (max) items, and a finite difference."""
+    from tests.test_oracle_sparse_max import _kept_items
+    B, L = 3, 2
+    K = 4
+    rng, E, R, n, csr, mbool, _, state, w = _case(2, 0.3, B, L, 60, 404 + (agg == "max"), drop=0.2)
+    M = mbool.shape[0]
+    ew = (rng.standard_normal(M) * 0.7).astype(np.float32)
+    sig = (1.0 / (1.0 + np.exp(-ew.astype(np.float64))))
+    masks = tuple((mbool[csr[o]] * sig[csr[o]]).astype(np.float32) for o in (3, 7))
+    cls = _fk().FlashLogFunctionSparse3DTopKMax if agg == "max" else _fk().FlashLogFunctionSparse3DTopKSum
+    b, l, e, v = _dev(*state)
+    wt = torch.from_numpy(w).cuda()
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    mk = torch.from_numpy(mbool).cuda()
+    weight = torch.from_numpy(ew.reshape(M, 1)).cuda().requires_grad_(True)
+
+    def fwd(wp):
+        return cls.apply(b, l, e, v, wt, *tc[:4], *tc[4:8], *tc[8:16], mk, wp, B, L, E, R, False, K, False, None,
+                         True, False)
+
+    out = fwd(weight)
+    keys = _keys(out.indices().detach(), L, E)
+    if agg == "max":
+        rk, rv, went, wdir, wpos = O.sparse_max_forward(*state, B, L, E, w, csr, masks, R, False, K)
+    else:
+        rk, rv = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, K)
+    assert np.array_equal(keys, rk)
+    np.testing.assert_allclose(out.values().detach().cpu().numpy(), rv, rtol=2e-6, atol=1e-7)
+    g = rng.standard_normal(keys.shape[0]).astype(np.float32)
+    (out.values() * torch.from_numpy(g).cuda()).sum().backward()
+    ge = weight.grad.view(-1).cpu().numpy().astype(np.float64)
+    ref = np.zeros(M)
+    pos = {int(k): o for o, k in enumerate(keys)}
+    wf = w.reshape(-1, n).astype(np.float64)
+    if agg == "max":
+        for o in range(keys.shape[0]):
+            if wdir[o] == 2:
+                continue
+            i, d, p = went[o], wdir[o], wpos[o]
+            edge = int(csr[3 if d == 0 else 7][p])
+            row = state[0][i] * L + state[1][i]
+            col = (R if d else 0) + int(csr[6 if d else 2][p])
+            m = float(masks[d][p])
+            ref[edge] += g[o] * float(state[3][i]) * wf[row, col] * m * (1 - sig[edge])
+    else:
+        for key, val, d, edge, i, _, p in _kept_items(*state, L, w, csr, masks, R, K, False):
+            if d == 2 or masks[d][p] == 0:
+                continue
+            row = state[0][i] * L + state[1][i]
+            col = (R if d else 0) + int(csr[6 if d else 2][p])
+            ref[edge] += g[pos[key]] * float(state[3][i]) * wf[row, col] * float(masks[d][p]) * (1 - sig[edge])
+    np.testing.assert_allclose(ge, ref, rtol=1e-4, atol=1e-6)
+    if agg == "max":
+        return  # winners may switch under a perturbation: no finite difference
+    # finite difference on the edges with the largest gradients
+    gt = torch.from_numpy(g).cuda()
+    for edge in np.argsort(-np.abs(ref))[:3]:
+        d = torch.zeros(M, 1, device="cuda")
+        d[edge] = 1e-2
+        with torch.no_grad():
+            fp = fwd(weight.detach() + d)
+            fm = fwd(weight.detach() - d)
+        lp = float((fp.values() * gt[:fp.values().numel()]).sum()) if fp._nnz() == keys.shape[0] else None
+        lm = float((fm.values() * gt[:fm.values().numel()]).sum()) if fm._nnz() == keys.shape[0] else None
+        if lp is None or lm is None:
+            continue
+        assert abs((lp - lm) / 2e-2 - ref[edge]) <= 2e-2 * abs(ref[edge]) + 1e-4
