@@ -17,6 +17,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _SRC = os.path.join(_HERE, "flashlog_oracle.c")
+_SRCS = [_SRC, os.path.join(_HERE, "grounding_oracle.c")]
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _lib = None
 
@@ -26,10 +27,10 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 def build(force=False):
     """Compile the C oracle with gcc (no FMA contraction, IEEE semantics)."""
     if force or not os.path.exists(_LIB_PATH) or \
-            os.path.getmtime(_LIB_PATH) < os.path.getmtime(_SRC):
+            os.path.getmtime(_LIB_PATH) < max(os.path.getmtime(f) for f in _SRCS):
         tmp = _LIB_PATH + ".tmp"
         subprocess.check_call(["gcc", "-O2", "-ffp-contract=off", "-fno-fast-math",
-                               "-fPIC", "-shared", "-o", tmp, _SRC])
+                               "-fPIC", "-shared", "-o", tmp] + _SRCS + ["-lm"])
         os.replace(tmp, _LIB_PATH)
     return _LIB_PATH
 
@@ -607,3 +608,125 @@ def rule_paths_brute(h, r, t, R, source, body):
                     nxt[hh] = nxt.get(hh, 0) + cnt
         ends = nxt
     return ends
+
+
+# --------------------------------------------------------------------------
+# Soft grounding (flashlog_kernel/soft_grounding_kernel/source/
+# soft_grounding.cpp): reservoir, walks (C, grounding_oracle.c), and the
+# count merge / cap / fold union (numpy, :454-614)
+
+def mt64_nth(seed, k):
+    """k-th output of std::mt19937_64 seeded with seed."""
+    fn = lib().or_mt64_nth
+    fn.restype = ctypes.c_uint64
+    return int(fn(ctypes.c_uint64(seed), ctypes.c_int64(k)))
+
+
+def reservoir(row_group_ptr, group_rel, relations, max_sources, seed):
+    """sample_relation_sources_reservoir (soft_grounding.cpp:1029-1124)."""
+    gp = _c(row_group_ptr, np.int32)
+    gr = _c(group_rel, np.int16)
+    rel = _c(relations, np.int64)
+    out = np.empty((rel.shape[0], max_sources), np.int32)
+    avail = np.empty(rel.shape[0], np.int64)
+    rc = lib().or_reservoir(ctypes.c_int64(gp.shape[0] - 1), _p(gp), _p(gr), ctypes.c_int64(rel.shape[0]), _p(rel),
+                            ctypes.c_int64(max_sources), ctypes.c_int64(seed), _p(out), _p(avail))
+    if rc != 0:
+        raise ValueError("relation ids must be unique and in [0, 32767]")
+    return out, avail
+
+
+def ground_walks(att, R, head, task_source, task_index, csr, walks, topk_edges, mask_query_head, seed,
+                 temperature=1.0):
+    """Walk records of every source task: (keys [tasks, walks] uint64,
+    positive [tasks, walks] uint8); att [3, ranks, 2R+1]."""
+    att = _c(att, np.float32)
+    steps, ranks, vocab = att.shape
+    assert steps == 3 and vocab == 2 * R + 1
+    ts = _c(task_source, np.int64)
+    ti = _c(task_index, np.int64)
+    arrs = [_c(csr[1], np.int32), _c(csr[5], np.int32), _c(csr[8], np.int32), _c(csr[9], np.int16),
+            _c(csr[10], np.int32), _c(csr[11], np.int32), _c(csr[12], np.int32), _c(csr[13], np.int16),
+            _c(csr[14], np.int32), _c(csr[15], np.int32)]
+    gp = [np.asarray(csr[8]), np.asarray(csr[12])]
+    max_groups = max(int(np.max(np.diff(g))) if g.shape[0] > 1 else 0 for g in gp) + 1
+    keys = np.empty((ts.shape[0], walks), np.uint64)
+    pos = np.empty((ts.shape[0], walks), np.uint8)
+    lib().or_ground_walks(_p(att), ctypes.c_int64(ranks), ctypes.c_int64(vocab), ctypes.c_int64(R),
+                          ctypes.c_int32(head), ctypes.c_int64(ts.shape[0]), _p(ts), _p(ti), *[_p(a) for a in arrs],
+                          ctypes.c_int64(walks), ctypes.c_int64(topk_edges), ctypes.c_int(int(bool(mask_query_head))),
+                          ctypes.c_int64(seed), ctypes.c_double(temperature), ctypes.c_int64(max_groups), _p(keys),
+                          _p(pos))
+    return keys, pos
+
+
+def _encode(length, body):
+    m = (1 << 20) - 1
+    return (length << 60) | ((body[0] & m) << 40) | ((body[1] & m) << 20) | (body[2] & m)
+
+
+def ground_aggregate(keys, pos, task_fold, nfolds, head, budgets):
+    """Per fold the body counts (walk hits, source hits, positive walk hits,
+    positive source hits; soft_grounding.cpp:427-449), capped per length by
+    (walk hits desc, key asc) (:454-531), then united over folds with totals
+    and per-fold minimums, the trivial body (head) dropped, ascending key
+    (:533-614).  Returns (rows int64 [n, 12], raw unique counts per fold)."""
+    capped, raw = [], []
+    for f in range(nfolds):
+        stats = {}
+        for t in np.nonzero(np.asarray(task_fold) == f)[0]:
+            local = {}
+            for k, p in zip(keys[t].tolist(), pos[t].tolist()):
+                if k == 0:
+                    continue
+                c = local.setdefault(k, [0, 0])
+                c[0] += 1
+                c[1] += p
+            for k, (wh, pw) in local.items():
+                s = stats.setdefault(k, [0, 0, 0, 0])
+                s[0] += wh
+                s[1] += 1
+                s[2] += pw
+                s[3] += 1 if pw > 0 else 0
+        raw.append(len(stats))
+        rows = []
+        for length in (1, 2, 3):
+            b = budgets[length - 1]
+            if b <= 0:
+                continue
+            cand = sorted(((k, v) for k, v in stats.items() if k >> 60 == length), key=lambda kv: (-kv[1][0], kv[0]))
+            rows += cand[:b]
+        capped.append(rows)
+    trivial = _encode(1, (head, 0, 0))
+    agg = {}
+    for rows in capped:
+        for k, v in rows:
+            if k == trivial:
+                continue
+            if k not in agg:
+                agg[k] = [list(v), list(v), 1]
+            else:
+                a = agg[k]
+                a[0] = [x + y for x, y in zip(a[0], v)]
+                a[1] = [min(x, y) for x, y in zip(a[1], v)]
+                a[2] += 1
+    out = np.zeros((len(agg), 12), np.int64)
+    m = (1 << 20) - 1
+    for i, k in enumerate(sorted(agg)):
+        tot, mn, seen = agg[k]
+        if seen != nfolds:
+            mn = [0, 0, 0, 0]
+        out[i, :4] = [k >> 60, (k >> 40) & m, (k >> 20) & m, k & m]
+        out[i, 4:8] = tot
+        out[i, 8:12] = mn
+    return out, raw
+
+
+def ground(att, R, head, folds, csr, walks, topk_edges, mask_query_head, seed, budgets, temperature=1.0):
+    """One head of ground_head_batch_source_folds_sampled_capped_counts:
+    folds = list of source arrays.  Returns (rows, raw counts per fold)."""
+    src = np.concatenate([np.asarray(f, np.int64) for f in folds]) if folds else np.zeros(0, np.int64)
+    idx = np.concatenate([np.arange(len(f), dtype=np.int64) for f in folds]) if folds else src
+    fold = np.concatenate([np.full(len(f), i, np.int64) for i, f in enumerate(folds)]) if folds else src
+    keys, pos = ground_walks(att, R, head, src, idx, csr, walks, topk_edges, mask_query_head, seed, temperature)
+    return ground_aggregate(keys, pos, fold, len(folds), head, budgets)
