@@ -15,6 +15,10 @@ def install():
     this package's mirror (drop-in replacement of the reference package)."""
     from . import flashlog_kernel as pkg
     from .flashlog_kernel import flashlog_kernel as mod
+    from .flashlog_kernel import soft_grounding_kernel as sg
+    from .flashlog_kernel.soft_grounding_kernel import soft_grounding_kernel as sgm
     sys.modules["flashlog_kernel"] = pkg
     sys.modules["flashlog_kernel.flashlog_kernel"] = mod
+    sys.modules["flashlog_kernel.soft_grounding_kernel"] = sg
+    sys.modules["flashlog_kernel.soft_grounding_kernel.soft_grounding_kernel"] = sgm
     return pkg

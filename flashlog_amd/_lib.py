@@ -67,6 +67,18 @@ class FlSparseHop(ctypes.Structure):
     ]
 
 
+class FlGroundGraph(ctypes.Structure):
+    """Mirror of ``fl_ground_graph`` (include/flashlog_hip.h)."""
+    _fields_ = [
+        ("ori_col", ctypes.c_void_p), ("inv_col", ctypes.c_void_p),
+        ("ori_ptr", ctypes.c_void_p), ("ori_start", ctypes.c_void_p), ("ori_count", ctypes.c_void_p),
+        ("ori_rel", ctypes.c_void_p),
+        ("inv_ptr", ctypes.c_void_p), ("inv_start", ctypes.c_void_p), ("inv_count", ctypes.c_void_p),
+        ("inv_rel", ctypes.c_void_p),
+        ("nodes", ctypes.c_int64), ("num_relations", ctypes.c_int64), ("max_groups", ctypes.c_int64),
+    ]
+
+
 _SIGS = {
     "fl_last_error": (ctypes.c_char_p, []),
     "fl_abi_version": (ctypes.c_int, []),
@@ -114,6 +126,21 @@ _SIGS = {
                                           ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
     "fl_sparse_topc": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 + [ctypes.c_void_p] * 3),
     "fl_sparse_rowptr_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "fl_reservoir_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4),
+    "fl_reservoir": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                                    ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                    ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]),
+    "fl_ground_walk_bytes": (ctypes.c_size_t, [ctypes.POINTER(FlGroundGraph), ctypes.c_int64]),
+    "fl_ground_walks": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlGroundGraph), ctypes.c_void_p,
+                                       ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_int64] + [ctypes.c_void_p] * 3 +
+                        [ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_double, ctypes.c_void_p,
+                         ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]),
+    "fl_ground_count_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3),
+    "fl_ground_count": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                       ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                       ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]),
     "fl_sparse_race_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 2),
     "fl_sparse_race_plan": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 +
                             [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),

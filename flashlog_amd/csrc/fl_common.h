@@ -81,3 +81,12 @@ __device__ __forceinline__ uint32_t fl_order_key(float v) {
     uint32_t u = __float_as_uint(v);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
+
+// SplitMix64 output function (Steele, Lea and Flood 2014; the public-domain
+// splitmix64.c of Vigna): one step from state z.
+__device__ __forceinline__ uint64_t fl_splitmix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}

@@ -414,6 +414,79 @@ int fl_filtered_ranks(void *stream, const int64_t *idx_b, const int64_t *idx_e,
 int fl_prof_enable(int on);
 int fl_prof_read(const char *kernel, double *total_ms, int64_t *launches);
 
+/* ---- soft grounding (flashlog_kernel/soft_grounding_kernel) ---------- */
+
+/* Replaces sample_relation_sources_reservoir (soft_grounding.cpp:1029-1124,
+ * soft_grounding_kernel.py:87-112): per requested relation (relations
+ * [nreq], unique, in [0, 32767]) a uniform reservoir of at most max_sources
+ * rows holding a group of that relation, in CSR group order with SplitMix64
+ * positions, then a SplitMix64 Fisher-Yates shuffle.  sampled
+ * [nreq, max_sources] (-1 padded), available [nreq] = groups per relation.
+ * All pointers are device memory. */
+size_t fl_reservoir_bytes(int64_t groups, int64_t rows, int64_t nreq,
+                          int64_t max_sources);
+int fl_reservoir(void *stream, const int32_t *row_group_ptr, int64_t rows,
+                 const int16_t *group_rel, int64_t groups,
+                 const int64_t *relations, int64_t nreq, int64_t max_sources,
+                 int64_t seed, void *ws, size_t ws_bytes, int32_t *sampled,
+                 int64_t *available);
+
+/* The CSR arrays the grounding walks read (the 16-tuple's entries 1, 5,
+ * 8-15, soft_grounding_kernel.py:79). */
+typedef struct fl_ground_graph {
+    const int32_t *ori_col, *inv_col;
+    const int32_t *ori_ptr, *ori_start, *ori_count;
+    const int16_t *ori_rel;
+    const int32_t *inv_ptr, *inv_start, *inv_count;
+    const int16_t *inv_rel;
+    int64_t nodes;          /* entities (ptr arrays hold nodes + 1)       */
+    int64_t num_relations;  /* R: operators 0..2R-1, identity 2R          */
+    int64_t max_groups;     /* most groups of one node on one side        */
+} fl_ground_graph;
+
+/* Replaces the walk part of ground_head_batch_source_folds_sampled_capped_
+ * counts (soft_grounding.cpp:112-449, 898-1027) for rule_steps = 3: for
+ * task t (head slot task_head[t], source task_source[t], position
+ * task_index[t] within its fold) walks attention-guided walks with the
+ * engine std::mt19937_64(splitmix64(seeds[h] ^ index << 32 ^ source)),
+ * option masses proposal(w) = w^(1/temperature), the c2 edge prefix
+ * topk_edges per side, the query head excluded from the source when
+ * mask_query_head.  Record t*walks + j receives the body key (length << 60 |
+ * three 20-bit operators; 0 when the walk stops or stays) and whether it
+ * ends at a positive target of (source, head).  att: [nheads, 3, ranks,
+ * 2R+1].  The draws are those of libstdc++ 11 (generate_canonical<double,
+ * 64>, uniform_int_distribution by Lemire's method). */
+size_t fl_ground_walk_bytes(const fl_ground_graph *g, int64_t ntasks);
+int fl_ground_walks(void *stream, const fl_ground_graph *g, const float *att,
+                    int64_t nheads, int64_t ranks, const int64_t *heads,
+                    const int64_t *seeds, int64_t ntasks,
+                    const int32_t *task_head, const int64_t *task_source,
+                    const int64_t *task_index, int64_t walks,
+                    int64_t topk_edges, int mask_query_head,
+                    double temperature, void *ws, size_t ws_bytes,
+                    uint64_t *keys, uint8_t *positive);
+
+/* Replaces merge_and_cap_source_stats and union_encoded_source_folds
+ * (soft_grounding.cpp:454-614): records of segment s = (head, fold) are
+ * tasks [seg_task_off[s], seg_task_off[s+1]) (segments head-major);
+ * seg_head [nsegments] head slot; heads [nheads] head operators;
+ * head_folds [nheads] folds per head; budgets (host int64[3]) per body
+ * length.  rows [row_cap, 12] receives per head (in head order) the united
+ * rows (length, 3 operators, totals of walk / source / positive walk /
+ * positive source hits, their minimums over folds or 0 when a fold lacks
+ * the body), ascending body key, trivial body (head) dropped; info (device
+ * int64[nsegments + nheads + 1]) the unique bodies per fold, then the row
+ * offsets of every head.  Synchronises the stream (sizes). */
+size_t fl_ground_count_bytes(int64_t nrecords, int64_t nsegments,
+                             int64_t nheads);
+int fl_ground_count(void *stream, const uint64_t *keys,
+                    const uint8_t *positive, int64_t walks,
+                    int64_t nsegments, const int64_t *seg_task_off,
+                    const int64_t *seg_head, int64_t nheads,
+                    const int64_t *heads, const int64_t *head_folds,
+                    const int64_t *budgets, void *ws, size_t ws_bytes,
+                    int64_t *rows, int64_t row_cap, int64_t *info);
+
 #ifdef __cplusplus
 }
 #endif

@@ -109,7 +109,14 @@ def write_api_surface():
             if isinstance(node, ast.FunctionDef) and node.name == "score":
                 rules["%s.score" % mod] = [a.arg for a in node.args.args]
     json.dump(rules, open(os.path.join(HERE, "rules_surface.json"), "w"), indent=1, sort_keys=True)
-    print("wrote", len(surface) + len(rules), "signatures")
+    grounding = {}
+    tree = ast.parse(open(os.path.join(REF, "flashlog_kernel", "soft_grounding_kernel",
+                                       "soft_grounding_kernel.py")).read())
+    for node in tree.body:
+        if isinstance(node, ast.FunctionDef) and not node.name.startswith("_"):
+            grounding[node.name] = [a.arg for a in node.args.args]
+    json.dump(grounding, open(os.path.join(HERE, "grounding_surface.json"), "w"), indent=1, sort_keys=True)
+    print("wrote", len(surface) + len(rules) + len(grounding), "signatures")
 
 
 if __name__ == "__main__":

@@ -66,3 +66,14 @@ def test_rules_signature_matches_reference(name):
     mod, fn = name.split(".")
     obj = getattr(importlib.import_module("flashlog_amd.rules." + mod), fn)
     assert list(inspect.signature(obj).parameters) == RULES[name]
+
+
+GROUNDING = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "grounding_surface.json")))
+
+
+@pytest.mark.parametrize("name", sorted(GROUNDING))
+def test_grounding_signature_matches_reference(name):
+    import flashlog_amd
+    flashlog_amd.install()
+    import flashlog_kernel.soft_grounding_kernel as sg
+    assert list(inspect.signature(getattr(sg, name)).parameters) == GROUNDING[name]
