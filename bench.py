@@ -222,8 +222,9 @@ def main():
 
 
 SPARSE_KERNELS = ["k_sp_topc", "k_sp_rowptr", "k_sp_select", "k_sp_rowinfo", "k_sp_fill", "k_sp_partition",
-                  "k_sp_accum", "k_sp_accum_hot", "k_sp_emit", "k_norm_fwd", "k_scan_tiles", "k_scan_totals", "k_scan_apply",
-                  "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask", "k_sp_hist"]
+                  "k_sp_accum_small", "k_sp_accum_mid", "k_sp_accum_hot", "k_sp_emit", "k_norm_fwd", "k_scan_tiles",
+                  "k_scan_totals", "k_scan_apply", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask",
+                  "k_sp_hist"]
 
 
 def fill_bytes(sides_np, b, l, e, R, L, n, W, K):
@@ -265,6 +266,8 @@ def main_sparse(args):
     cfg = synth.CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_mb > 0:
+        copy_calibration(args.copy_mb)
     t_gen = time.perf_counter()
     h, r, t, E, R = synth.make_graph(args.config)
     n = 2 * R + 1
@@ -321,7 +324,7 @@ def main_sparse(args):
         prof = {k: _lib.prof_read(k) for k in SPARSE_KERNELS}
         _lib.prof_enable(False)
         per_launch = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in prof.items()}
-        per_step = {k: (v[0] / args.profile_steps) for k, v in prof.items()}
+        per_step = {k: (v[0] / max(args.profile_steps, 1)) for k, v in prof.items()}
         print("per-launch ms: " + json.dumps({k: round(v, 4) for k, v in per_launch.items()}),
               file=sys.stderr, flush=True)
         print("per-step ms: " + json.dumps({k: round(v, 4) for k, v in per_step.items()}),

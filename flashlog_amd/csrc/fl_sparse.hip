@@ -21,10 +21,12 @@
 //           k_sp_partition workgroup per tile of a row: stable scatter of the
 //                         tile's items into destination buckets (block radix
 //                         rank over the bucket id)
-//           k_sp_accum    workgroup per (row, bucket): the bucket's items
-//                         stably sorted by destination in LDS, each run added
-//                         in raw order (k_sp_accum_hot: large buckets, dense
-//                         LDS accumulator); max: k_sp_max / k_sp_max_hot
+//           k_sp_accum_small  wave per (row, bucket) of at most 512 items:
+//                         the items stably sorted by destination in LDS, each
+//                         run added in raw order; larger buckets are listed
+//                         for k_sp_accum_mid (workgroup sort, persistent) and
+//                         k_sp_accum_hot (chunks into a dense LDS accumulator,
+//                         persistent); max: k_sp_max / k_sp_max_hot
 //           scan          output offsets
 //   emit    k_sp_emit     coalesced COO (b, l, e, v), ascending key
 //   backward k_sp_bwd     wave per entry: the same walk, gradients gathered
@@ -210,6 +212,7 @@ __device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, i
         }
         if (Q && tk.kind == TAKE_QUOTA)
             take = sp_quota_window(tk, wv, cnt, g < g1, (int)((g1 - gb) < FL_WAVE ? (g1 - gb) : FL_WAVE));
+        if (__ballot(take > 0) == 0) continue;  // nothing kept in this window (typical for hub sources)
         const long long incl = fl_wave_incl_scan_i64(take);
         const long long total = __shfl(incl, FL_WAVE - 1, FL_WAVE);
         for (long long k0 = 0; k0 < total; k0 += FL_WAVE) {
@@ -590,13 +593,15 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
 // within the bucket (for the backward).  Items are stably sorted by
 // destination in LDS (keys destination << 11 | index, LSD radix) and the
 // first thread of every run adds the run's values in order.
-//   k_sp_accum      buckets of at most SP_CHUNK items, one sort;
+//   sp_accum_one    buckets of at most SP_CHUNK items, one sort (the
+//                   workgroup path of k_sp_accum_mid);
 //   k_sp_accum_hot  larger buckets: chunks of SP_CHUNK items in raw order,
 //                   each sorted and folded into a dense LDS accumulator of
 //                   the bucket's 8192 destinations that carries the partial
 //                   sums from chunk to chunk.
 constexpr int SP_CHUNK_IPT = 8;
 constexpr int SP_CHUNK = SP_NT * SP_CHUNK_IPT;
+constexpr int SP_HOT_GRID = 1024;  // workgroups of the persistent hot-bucket kernels
 
 __device__ __forceinline__ void sp_bucket_range(const SpRows &rows, const int64_t *base, int64_t r, int64_t bk,
                                                 int64_t *start, int64_t *end) {
@@ -682,7 +687,7 @@ __device__ __forceinline__ int sp_run_end(const uint32_t *key, int p, int size) 
 }
 
 template <int IPT>
-__device__ void sp_accum_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
+__device__ __forceinline__ void sp_accum_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
                              float *__restrict__ val_arr, const int32_t *__restrict__ raw_arr,
                              int32_t *__restrict__ raw_local, int32_t *out_count, uint32_t (*kb)[SP_CHUNK],
                              float *val, uint16_t (*cnt)[SP_NT], int *scan_lds) {
@@ -713,38 +718,215 @@ __device__ void sp_accum_one(int64_t start, int64_t n, int32_t dbase, int32_t *_
     if (t == 0) *out_count = total;
 }
 
-__global__ __launch_bounds__(SP_NT) void k_sp_accum(SpRows rows, const int64_t *__restrict__ base,
-                                                   int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
-                                                   const int32_t *__restrict__ raw_arr,
-                                                   int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count) {
+// ---- Small buckets (at most SP_WB items): one wave per bucket with
+// wave-private LDS and no block barriers; four buckets per workgroup.
+constexpr int SP_WIPT = 8;
+constexpr int SP_WB = FL_WAVE * SP_WIPT;  // 512 items
+constexpr int SP_SMALL_WAVES = SP_NT / FL_WAVE;
+constexpr int SP_MID_GRID = 2048;  // workgroups of the persistent mid-size kernel
+
+// LDS ordering between the lanes of one wave (program order + fence).
+__device__ __forceinline__ void fl_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Stable LSD sort of 64 * IPT keys in LDS (blocked: lane t owns
+// kin[t*IPT .. t*IPT + IPT)) by bits [lo, lo + nbits), 4 bits per pass.
+template <int IPT>
+__device__ __forceinline__ uint32_t *sp_wave_sort(uint32_t *kin, uint32_t *kout, int lo_bit, int nbits, uint16_t (*cnt)[FL_WAVE]) {
+    const int t = fl_lane();
+    for (int shift = lo_bit; shift < lo_bit + nbits; shift += 4) {
+        uint32_t key[IPT];
+        uint16_t loc[IPT];
+#pragma unroll
+        for (int d = 0; d < 16; ++d) cnt[d][t] = 0;
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            key[j] = kin[t * IPT + j];
+            const int d = (key[j] >> shift) & 15;
+            loc[j] = cnt[d][t];
+            cnt[d][t] = (uint16_t)(loc[j] + 1);
+        }
+        fl_wave_sync();
+        // exclusive scan of the counters in digit-major order: lane t owns
+        // flat entries [16t, 16t + 16)
+        uint16_t *flat = &cnt[0][0];
+        int part = 0;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) part += flat[t * 16 + q];
+        int run = fl_wave_incl_scan_i32(part) - part;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int c = flat[t * 16 + q];
+            flat[t * 16 + q] = (uint16_t)run;
+            run += c;
+        }
+        fl_wave_sync();
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int d = (key[j] >> shift) & 15;
+            kout[cnt[d][t] + loc[j]] = key[j];
+        }
+        fl_wave_sync();
+        uint32_t *x = kin;
+        kin = kout;
+        kout = x;
+    }
+    return kin;
+}
+
+// The bucket's items sorted by destination (stable) and each run added to
+// 0 in raw order, outputs compacted in destination order in place, as
+// sp_accum_one does for a workgroup.
+template <int IPT>
+__device__ __forceinline__ void sp_wave_accum(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
+                              float *__restrict__ val_arr, const int32_t *__restrict__ raw_arr,
+                              int32_t *__restrict__ raw_local, int32_t *out_count, uint32_t (*kb)[SP_WB], float *val,
+                              uint16_t (*cnt)[FL_WAVE]) {
+    constexpr int SIZE = FL_WAVE * IPT;
+    const int t = fl_lane();
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int k = t * IPT + j;
+        uint32_t dl = SP_W;  // no item / hole: sorts last
+        if (k < n) {
+            const int32_t d = dst_arr[start + k];
+            if (d >= 0) {
+                dl = (uint32_t)d & (SP_W - 1);
+                val[k] = val_arr[start + k];
+            }
+        }
+        kb[0][k] = (dl << 11) | (uint32_t)k;
+    }
+    fl_wave_sync();
+    const uint32_t *key = sp_wave_sort<IPT>(kb[0], kb[1], 11, 16, cnt);
+    float *sv = reinterpret_cast<float *>(key == kb[0] ? kb[1] : kb[0]);
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int p = t * IPT + j;
+        sv[p] = val[key[p] & 2047u];
+    }
+    fl_wave_sync();
+    int heads = 0;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) heads += sp_is_head(key, t * IPT + j) ? 1 : 0;
+    const int incl = fl_wave_incl_scan_i32(heads);
+    const int total = __shfl(incl, FL_WAVE - 1, FL_WAVE);
+    int rank = incl - heads;
+    // every item was read before the sort: outputs may overwrite them
+    for (int j = 0; j < IPT; ++j) {
+        const int p = t * IPT + j;
+        if (!sp_is_head(key, p)) continue;
+        const int e = sp_run_end(key, p, SIZE);
+        const float a = sp_fold(0.0f, sv, p, e);
+        if (raw_local)
+            for (int q = p; q < e; ++q) {
+                const int idx = (int)(key[q] & 2047u);
+                raw_local[raw_arr ? raw_arr[start + idx] : start + idx] = rank;
+            }
+        dst_arr[start + rank] = dbase + (int32_t)(key[p] >> 11);
+        val_arr[start + rank] = a;
+        ++rank;
+    }
+    if (t == 0) *out_count = total;
+}
+
+// One wave per (row, bucket) slot: small buckets are accumulated here,
+// larger ones listed for the persistent kernels (lists[0] hot, lists[2]
+// mid-size; lists[1], lists[3] their claim counters).
+__global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int64_t *__restrict__ base,
+                                                         int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                                         const int32_t *__restrict__ raw_arr,
+                                                         int32_t *__restrict__ raw_local,
+                                                         int32_t *__restrict__ out_count, int64_t nslots,
+                                                         int32_t *__restrict__ hot_list,
+                                                         int32_t *__restrict__ mid_list,
+                                                         int32_t *__restrict__ lists) {
+    __shared__ uint32_t kb[SP_SMALL_WAVES][2][SP_WB];
+    __shared__ float val[SP_SMALL_WAVES][SP_WB];
+    __shared__ uint16_t cnt[SP_SMALL_WAVES][16][FL_WAVE];
+    const int w = threadIdx.x / FL_WAVE;
+    const int64_t slot = (int64_t)blockIdx.x * SP_SMALL_WAVES + w;
+    if (slot >= nslots) return;  // no block barrier follows
+    const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
+    int64_t start, end;
+    sp_bucket_range(rows, base, r, bk, &start, &end);
+    const int64_t n = end - start;
+    const int lane = fl_lane();
+    if (n > SP_CHUNK) {
+        if (lane == 0) hot_list[atomicAdd(&lists[0], 1)] = (int32_t)slot;
+        return;
+    }
+    if (n > SP_WB) {
+        if (lane == 0) mid_list[atomicAdd(&lists[2], 1)] = (int32_t)slot;
+        return;
+    }
+    int32_t *oc = &out_count[slot];
+    if (n == 0) {
+        if (lane == 0) *oc = 0;
+        return;
+    }
+    const int32_t dbase = (int32_t)(bk << SP_S);
+    if (n <= FL_WAVE)
+        sp_wave_accum<1>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+    else if (n <= 2 * FL_WAVE)
+        sp_wave_accum<2>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+    else if (n <= 4 * FL_WAVE)
+        sp_wave_accum<4>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+    else
+        sp_wave_accum<8>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+}
+
+// Persistent grid over the mid-size buckets (SP_WB < n <= SP_CHUNK).
+__global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64_t *__restrict__ base,
+                                                       int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                                       const int32_t *__restrict__ raw_arr,
+                                                       int32_t *__restrict__ raw_local,
+                                                       int32_t *__restrict__ out_count,
+                                                       const int32_t *__restrict__ mid_list,
+                                                       int32_t *__restrict__ lists) {
     __shared__ uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
     __shared__ uint16_t cnt[16][SP_NT];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
-    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
-    int64_t start, end;
-    sp_bucket_range(rows, base, r, bk, &start, &end);
-    const int64_t n = end - start;
-    if (n > SP_CHUNK) return;  // k_sp_accum_hot
-    int32_t *oc = &out_count[r * rows.NB + bk];
-    if (n == 0) {
-        if (threadIdx.x == 0) *oc = 0;
-        return;
+    __shared__ int claim;
+    const int nmid = lists[2];
+    for (;;) {
+        __syncthreads();  // the previous bucket is done with the LDS arrays
+        if (threadIdx.x == 0) claim = atomicAdd(&lists[3], 1);
+        __syncthreads();
+        const int mi = claim;
+        if (mi >= nmid) break;
+        const int64_t slot = mid_list[mi];
+        const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
+        int64_t start, end;
+        sp_bucket_range(rows, base, r, bk, &start, &end);
+        const int64_t n = end - start;
+        const int32_t dbase = (int32_t)(bk << SP_S);
+        int32_t *oc = &out_count[slot];
+        if (n <= SP_NT * 4)
+            sp_accum_one<4>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
+        else
+            sp_accum_one<8>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
     }
-    const int32_t dbase = (int32_t)(bk << SP_S);
-    if (n <= SP_NT * 2)
-        sp_accum_one<2>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
-    else if (n <= SP_NT * 4)
-        sp_accum_one<4>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
-    else
-        sp_accum_one<8>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
 }
 
+__device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__restrict__ base, int64_t r, int64_t bk,
+                                 int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                 const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local,
+                                 int32_t *__restrict__ out_count, uint32_t (*kb)[SP_CHUNK], float *val,
+                                 uint16_t (*cnt)[SP_NT], float *acc, uint32_t *bits, int *wpre, int *scan_lds);
+
+// Persistent grid over the list of hot buckets collected by k_sp_accum_small.
 __global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64_t *__restrict__ base,
                                                        int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
                                                        const int32_t *__restrict__ raw_arr,
                                                        int32_t *__restrict__ raw_local,
-                                                       int32_t *__restrict__ out_count) {
+                                                       int32_t *__restrict__ out_count,
+                                                       const int32_t *__restrict__ hot_list,
+                                                       int32_t *__restrict__ hot_count) {
     __shared__ uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
     __shared__ uint16_t cnt[16][SP_NT];
@@ -752,11 +934,29 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64
     __shared__ uint32_t bits[SP_W / 32];
     __shared__ int wpre[SP_W / 32];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
-    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
+    // hot_count[0]: listed buckets; hot_count[1]: next bucket to claim
+    __shared__ int claim;
+    const int nhot = hot_count[0];
+    for (;;) {
+        __syncthreads();  // the previous bucket is done with the LDS arrays
+        if (threadIdx.x == 0) claim = atomicAdd(&hot_count[1], 1);
+        __syncthreads();
+        const int hi = claim;
+        if (hi >= nhot) break;
+        const int64_t slot = hot_list[hi];
+        sp_accum_hot_one(rows, base, slot / rows.NB, slot % rows.NB, dst_arr, val_arr, raw_arr, raw_local,
+                         out_count, kb, val, cnt, acc, bits, wpre, scan_lds);
+    }
+}
+
+__device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__restrict__ base, int64_t r, int64_t bk,
+                                 int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                 const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local,
+                                 int32_t *__restrict__ out_count, uint32_t (*kb)[SP_CHUNK], float *val,
+                                 uint16_t (*cnt)[SP_NT], float *acc, uint32_t *bits, int *wpre, int *scan_lds) {
     int64_t start, end;
     sp_bucket_range(rows, base, r, bk, &start, &end);
     const int64_t n = end - start;
-    if (n <= SP_CHUNK) return;  // k_sp_accum
     const int t = threadIdx.x;
     for (int q = t; q < SP_W / 32; q += SP_NT) bits[q] = 0;
     for (int64_t c0 = 0; c0 < n; c0 += SP_CHUNK) {
@@ -821,7 +1021,7 @@ __device__ __forceinline__ float fl_order_key_inv(uint32_t k) {
 }
 
 template <int IPT>
-__device__ void sp_max_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
+__device__ __forceinline__ void sp_max_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
                            float *__restrict__ val_arr, const uint32_t *__restrict__ tie_arr,
                            const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local, int32_t *out_count,
                            uint32_t (*kb)[SP_CHUNK], float *val, uint32_t *tie, uint16_t (*cnt)[SP_NT],
@@ -869,7 +1069,8 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max(SpRows rows, const int64_t *__
                                                  int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
                                                  const uint32_t *__restrict__ tie_arr,
                                                  const int32_t *__restrict__ raw_arr,
-                                                 int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count) {
+                                                 int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count,
+                                                 int32_t *__restrict__ hot_list, int32_t *__restrict__ hot_count) {
     __shared__ uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
     __shared__ uint32_t tie[SP_CHUNK];
@@ -879,7 +1080,10 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max(SpRows rows, const int64_t *__
     int64_t start, end;
     sp_bucket_range(rows, base, r, bk, &start, &end);
     const int64_t n = end - start;
-    if (n > SP_CHUNK) return;  // k_sp_max_hot
+    if (n > SP_CHUNK) {  // for k_sp_max_hot
+        if (threadIdx.x == 0) hot_list[atomicAdd(hot_count, 1)] = (int32_t)blockIdx.x;
+        return;
+    }
     int32_t *oc = &out_count[r * rows.NB + bk];
     if (n == 0) {
         if (threadIdx.x == 0) *oc = 0;
@@ -894,22 +1098,49 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max(SpRows rows, const int64_t *__
         sp_max_one<8>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
 }
 
+__device__ __forceinline__ void sp_max_hot_one(SpRows rows, const int64_t *__restrict__ base, int64_t r, int64_t bk,
+                               int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                               const uint32_t *__restrict__ tie_arr, const int32_t *__restrict__ raw_arr,
+                               int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count, uint32_t *vbest,
+                               unsigned long long *tbest, uint32_t *bits, int *wpre, int *scan_lds);
+
+// Persistent grid over the list of hot buckets collected by k_sp_max.
 __global__ __launch_bounds__(SP_NT) void k_sp_max_hot(SpRows rows, const int64_t *__restrict__ base,
                                                      int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
                                                      const uint32_t *__restrict__ tie_arr,
                                                      const int32_t *__restrict__ raw_arr,
                                                      int32_t *__restrict__ raw_local,
-                                                     int32_t *__restrict__ out_count) {
+                                                     int32_t *__restrict__ out_count,
+                                                     const int32_t *__restrict__ hot_list,
+                                                     int32_t *__restrict__ hot_count) {
     __shared__ uint32_t vbest[SP_W];
     __shared__ unsigned long long tbest[SP_W];
     __shared__ uint32_t bits[SP_W / 32];
     __shared__ int wpre[SP_W / 32];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
-    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
+    // hot_count[0]: listed buckets; hot_count[1]: next bucket to claim
+    __shared__ int claim;
+    const int nhot = hot_count[0];
+    for (;;) {
+        __syncthreads();  // the previous bucket is done with the LDS arrays
+        if (threadIdx.x == 0) claim = atomicAdd(&hot_count[1], 1);
+        __syncthreads();
+        const int hi = claim;
+        if (hi >= nhot) break;
+        const int64_t slot = hot_list[hi];
+        sp_max_hot_one(rows, base, slot / rows.NB, slot % rows.NB, dst_arr, val_arr, tie_arr, raw_arr, raw_local,
+                       out_count, vbest, tbest, bits, wpre, scan_lds);
+    }
+}
+
+__device__ __forceinline__ void sp_max_hot_one(SpRows rows, const int64_t *__restrict__ base, int64_t r, int64_t bk,
+                               int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                               const uint32_t *__restrict__ tie_arr, const int32_t *__restrict__ raw_arr,
+                               int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count, uint32_t *vbest,
+                               unsigned long long *tbest, uint32_t *bits, int *wpre, int *scan_lds) {
     int64_t start, end;
     sp_bucket_range(rows, base, r, bk, &start, &end);
     const int64_t n = end - start;
-    if (n <= SP_CHUNK) return;  // k_sp_max
     const int t = threadIdx.x;
     for (int q = t; q < SP_W; q += SP_NT) {
         vbest[q] = 0u;  // below the key of every non-NaN value
@@ -1408,6 +1639,7 @@ struct SpExp {
     int32_t *raw_dst, *part_dst, *part_raw, *hist, *out_count;
     float *raw_val, *part_val;
     uint32_t *raw_tie, *part_tie;
+    int32_t *hot_list, *mid_list, *hot_count;
     int64_t *base, *tmp;
     size_t bytes;
 };
@@ -1431,6 +1663,9 @@ SpExp sp_exp_layout(int64_t T, int64_t tiles, int64_t R, int64_t NB, int backwar
     int64_t mx = tiles * NB;
     if (R * NB > mx) mx = R * NB;
     x.tmp = (int64_t *)take(scan_tmp_bytes(mx + 1));
+    x.hot_list = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
+    x.mid_list = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
+    x.hot_count = (int32_t *)take(4 * sizeof(int32_t));
     // last, so that every other offset is the same with and without it
     if (NB > 1 && backward) x.part_raw = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
     x.bytes = off;
@@ -1569,16 +1804,26 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         tie_arr = x.part_tie;
         raw_arr = raw_local ? x.part_raw : nullptr;
     }
+    // hot buckets (more than one LDS chunk) are listed by the first kernel
+    // and taken by a persistent grid of the second
+    const unsigned hot_grid = (unsigned)(R * NB < SP_HOT_GRID ? R * NB : SP_HOT_GRID);
+    if (R * NB > 0)
+        FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, x.hot_count, (int64_t)4, 0);
     if (R * NB > 0 && mx) {
         FL_LAUNCH("k_sp_max", k_sp_max, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
-                  val_arr, tie_arr, raw_arr, raw_local, x.out_count);
-        FL_LAUNCH("k_sp_max_hot", k_sp_max_hot, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base,
-                  dst_arr, val_arr, tie_arr, raw_arr, raw_local, x.out_count);
+                  val_arr, tie_arr, raw_arr, raw_local, x.out_count, x.hot_list, x.hot_count);
+        FL_LAUNCH("k_sp_max_hot", k_sp_max_hot, dim3(hot_grid), dim3(SP_NT), 0, st, rows, x.base, dst_arr, val_arr,
+                  tie_arr, raw_arr, raw_local, x.out_count, x.hot_list, x.hot_count);
     } else if (R * NB > 0) {
-        FL_LAUNCH("k_sp_accum", k_sp_accum, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
-                  val_arr, raw_arr, raw_local, x.out_count);
-        FL_LAUNCH("k_sp_accum_hot", k_sp_accum_hot, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base,
-                  dst_arr, val_arr, raw_arr, raw_local, x.out_count);
+        const int64_t nslot = R * NB;
+        FL_LAUNCH("k_sp_accum_small", k_sp_accum_small,
+                  dim3((unsigned)((nslot + SP_SMALL_WAVES - 1) / SP_SMALL_WAVES)), dim3(SP_NT), 0, st, rows, x.base,
+                  dst_arr, val_arr, raw_arr, raw_local, x.out_count, nslot, x.hot_list, x.mid_list, x.hot_count);
+        FL_LAUNCH("k_sp_accum_mid", k_sp_accum_mid, dim3((unsigned)(nslot < SP_MID_GRID ? nslot : SP_MID_GRID)),
+                  dim3(SP_NT), 0, st, rows, x.base, dst_arr, val_arr, raw_arr, raw_local, x.out_count, x.mid_list,
+                  x.hot_count);
+        FL_LAUNCH("k_sp_accum_hot", k_sp_accum_hot, dim3(hot_grid), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
+                  val_arr, raw_arr, raw_local, x.out_count, x.hot_list, x.hot_count);
     }
     if ((rc = exclusive_scan(st, x.out_count, out_base, R * NB, x.tmp)) != FL_OK) return rc;
     return fl_check_launch("sparse_expand");
