@@ -221,7 +221,7 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-SPARSE_KERNELS = ["k_sp_topc", "k_sp_rowptr", "k_sp_select", "k_sp_rowinfo", "k_sp_fill", "k_sp_partition",
+SPARSE_KERNELS = ["k_sp_topc", "k_sp_rowptr", "k_sp_relorder", "k_sp_select", "k_sp_rowinfo", "k_sp_fill", "k_sp_partition",
                   "k_sp_accum_small", "k_sp_accum_mid", "k_sp_accum_hot", "k_sp_emit", "k_norm_fwd", "k_scan_tiles",
                   "k_scan_totals", "k_scan_apply", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask",
                   "k_sp_hist"]

@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 FL_SEG = 32
 FL_SUP = 16
 
@@ -115,7 +115,7 @@ _SIGS = {
                               [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_int] +
                               [ctypes.c_void_p] * 2),
     "fl_sparse_buckets": (ctypes.c_int64, [ctypes.c_int64]),
-    "fl_sparse_plan_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
+    "fl_sparse_plan_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     "fl_sparse_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                       ctypes.POINTER(FlSparseHop), ctypes.c_void_p]),
     "fl_sparse_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int] * 2),

@@ -236,6 +236,107 @@ __device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, i
     return base;
 }
 
+// Admission order of c2 per (row, side): the relations with a positive
+// weight sorted by (weight desc, relation asc), ties in relation order =
+// group order (flashlog.cpp:12-89).  Workgroup per (row, side), bitonic sort
+// in LDS; sides of more than RO_MAX relations are not ordered (their
+// entries use c2_select).
+constexpr int RO_MAX = 4096;
+constexpr int RO_NT = 256;
+
+__global__ __launch_bounds__(RO_NT) void k_sp_relorder(const float *__restrict__ w, int64_t n, int64_t r_size,
+                                                      int16_t *__restrict__ order, int32_t *__restrict__ nelig) {
+    __shared__ unsigned long long key[RO_MAX];
+    const int64_t row = blockIdx.x >> 1;
+    const int side = blockIdx.x & 1;
+    const float *wr = w + row * n + (side ? r_size : 0);
+    const int t = threadIdx.x;
+    int P = 64;
+    while (P < r_size) P <<= 1;
+    for (int i = t; i < P; i += RO_NT) {
+        unsigned long long k = ~0ull;
+        if (i < r_size) {
+            const float wv = wr[i];
+            if (wv > 0.0f) k = ((unsigned long long)(~fl_order_key(wv)) << 32) | (unsigned)i;
+        }
+        key[i] = k;
+    }
+    __syncthreads();
+    for (int k = 2; k <= P; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = t; i < P; i += RO_NT) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const unsigned long long a = key[i], b = key[l];
+                    if (((i & k) == 0) ? (a > b) : (a < b)) {
+                        key[i] = b;
+                        key[l] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    int16_t *o = order + (row * 2 + side) * r_size;
+    for (int i = t; i < r_size; i += RO_NT) o[i] = key[i] != ~0ull ? (int16_t)(key[i] & 0xFFFFull) : (int16_t)-1;
+    if (t == 0) {
+        int lo = 0, hi = P;  // first ineligible slot
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (key[mid] != ~0ull) lo = mid + 1;
+            else hi = mid;
+        }
+        nelig[row * 2 + side] = lo < r_size ? lo : (int)r_size;
+    }
+}
+
+// c2 of one (entry, side) whose source has more than K edges, from the
+// row's admission order: the source's groups are found in that order (64
+// relations at a time, binary search over the source's group relations)
+// until the cumulative edge count reaches K.  The group holding the K-th
+// edge gives the threshold weight and the tie cut (its CSR start plus the
+// edges still admitted), the same (threshold, cut) as c2_select.  Returns
+// the kept items (lane partial sums).
+__device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int64_t K,
+                                      const int16_t *__restrict__ ord, int ne, float *thv_out, int32_t *ct_out) {
+    const int lane = fl_lane();
+    long long carry = 0;
+    for (int k0 = 0; k0 < ne; k0 += FL_WAVE) {
+        const int kk = k0 + lane;
+        const int rel = kk < ne ? (int)ord[kk] : -1;
+        int64_t g = -1;
+        long long cnt = 0;
+        if (rel >= 0) {
+            int64_t lo = g0, hi = g1;
+            while (lo < hi) {
+                const int64_t mid = lo + ((hi - lo) >> 1);
+                if ((int)s.group_rel[mid] < rel) lo = mid + 1;
+                else hi = mid;
+            }
+            if (lo < g1 && (int)s.group_rel[lo] == rel) {
+                g = lo;
+                cnt = s.group_count[lo];
+            }
+        }
+        const long long incl = fl_wave_incl_scan_i64(cnt);
+        const long long before = carry + incl - cnt;
+        const bool hit = cnt > 0 && before < K && before + cnt >= K;
+        const unsigned long long bal = __ballot(hit);
+        if (bal) {
+            const int hl = __ffsll((long long)bal) - 1;
+            const int relj = __shfl(rel, hl, FL_WAVE);
+            const long long bj = __shfl(before, hl, FL_WAVE);
+            const int gj = (int)__shfl((long long)g, hl, FL_WAVE);
+            *thv_out = wr[relj];
+            *ct_out = (int32_t)(s.group_start[gj] + (K - bj));
+            return lane == 0 ? K : 0;
+        }
+        carry += __shfl(incl, FL_WAVE - 1, FL_WAVE);
+    }
+    *thv_out = 0.0f;  // fewer than K eligible edges: every one is kept
+    *ct_out = 0;
+    return lane == 0 ? carry : 0;
+}
+
 // One wave per entry: per side the c2 threshold (bits of the threshold
 // weight, 0 = no pruning, NaN = training quotas) and tie cut, and the number
 // of raw items: kept edges (top-k mode; for the sum a kept edge with a zero
@@ -249,7 +350,8 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
                                                      int64_t nnz, const float *__restrict__ w, int64_t B, int64_t L,
                                                      int64_t E, int64_t n, int64_t r_size, int wot_i, int mode, int64_t K,
                                                      int64_t seed, float *__restrict__ th, int32_t *__restrict__ cut,
-                                                     int32_t *__restrict__ cnt) {
+                                                     int32_t *__restrict__ cnt, const int16_t *__restrict__ rel_order,
+                                                     const int32_t *__restrict__ rel_nelig) {
     __shared__ int hist_all[SEL_NT / FL_WAVE][256];
     const int lane = fl_lane();
     const int wid = threadIdx.x / FL_WAVE;
@@ -271,6 +373,17 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
         long long c = 0;
         if (mode == SP_ALL) {
             for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) c += s.group_count[g];
+        } else if (K > 0 && seed < 0 && rel_order && g1 - g0 > FL_WAVE) {
+            // more than one window of groups: every edge kept when the source
+            // has at most K, else the admission-order lookup
+            const int64_t deg = (int64_t)s.group_start[g1 - 1] + s.group_count[g1 - 1] - s.group_start[g0];
+            if (deg <= K) {
+                for (int64_t g = g0 + lane; g < g1; g += FL_WAVE)
+                    c += wr[s.group_rel[g]] > 0.0f ? s.group_count[g] : 0;
+            } else {
+                const int64_t ro = (sb[i] * L + sl[i]) * 2 + dir;
+                c = sp_select_lookup(s, g0, g1, wr, K, rel_order + ro * r_size, rel_nelig[ro], &thv, &ct);
+            }
         } else {
             uint32_t key;
             int32_t cc;
@@ -1613,10 +1726,12 @@ struct SpPlan {
     float *th;
     int32_t *cut, *cnt, *ntiles;
     int64_t *item_off, *row_ptr, *row_item0, *tile_base, *tmp;
+    int16_t *rel_order;   // [R][2][r_size] c2 admission order (r_size <= RO_MAX)
+    int32_t *rel_nelig;   // [R][2] relations with a positive weight
     size_t bytes;
 };
 
-SpPlan sp_plan_layout(int64_t nnz, int64_t R, char *base) {
+SpPlan sp_plan_layout(int64_t nnz, int64_t R, int64_t r_size, char *base) {
     SpPlan p{};
     size_t off = 0;
     auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
@@ -1630,6 +1745,10 @@ SpPlan sp_plan_layout(int64_t nnz, int64_t R, char *base) {
     p.tile_base = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
     const int64_t mx = nnz > R ? nnz : R;
     p.tmp = (int64_t *)take(scan_tmp_bytes(mx + 1));
+    if (r_size > 0 && r_size <= RO_MAX) {
+        p.rel_order = (int16_t *)take(sizeof(int16_t) * 2 * (size_t)R * (size_t)r_size);
+        p.rel_nelig = (int32_t *)take(sizeof(int32_t) * 2 * (size_t)(R > 0 ? R : 1));
+    }
     p.bytes = off;
     return p;
 }
@@ -1710,12 +1829,14 @@ extern "C" {
 
 int64_t fl_sparse_buckets(int64_t E) { return sp_buckets(E); }
 
-size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R) {
-    if (nnz < 0 || R < 0) return 0;
-    return sp_plan_layout(nnz, R, nullptr).bytes;
+size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R, int64_t r_size) {
+    if (nnz < 0 || R < 0 || r_size < 0) return 0;
+    return sp_plan_layout(nnz, R, r_size, nullptr).bytes;
 }
 
 static int64_t sp_budget(const fl_sparse_hop *h);
+// relations per side of the hop's attention (0 for the fixed-relation step)
+static int64_t sp_rsize(const fl_sparse_hop *h) { return h->mode == SP_FIXED ? 0 : h->r_size; }
 // Training quotas can apply (sampling seed, top-k mode, a positive budget).
 static bool sp_quotas(const fl_sparse_hop *h) { return h->sampling_seed >= 0 && sp_budget(h) > 0; }
 
@@ -1724,8 +1845,9 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     if ((rc = sp_check(ori, inv, h, "sparse_plan")) != FL_OK) return rc;
     if (!plan || !h->ws1) return fl_fail(FL_ERR_ARG, "sparse_plan: null plan or workspace");
     const int64_t R = h->B * h->L;
-    if (h->ws1_bytes < fl_sparse_plan_bytes(h->nnz, R)) return fl_fail(FL_ERR_ARG, "sparse_plan: workspace too small");
-    SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
+    if (h->ws1_bytes < fl_sparse_plan_bytes(h->nnz, R, sp_rsize(h)))
+        return fl_fail(FL_ERR_ARG, "sparse_plan: workspace too small");
+    SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     hipStream_t st = (hipStream_t)stream;
     const int64_t nnz = h->nnz;
     const int64_t K = sp_budget(h);
@@ -1739,10 +1861,16 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     if (nnz > 0 && h->mode == SP_FIXED)
         FL_LAUNCH("k_fx_count", k_fx_count, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, *ori, *inv,
                   h->sp_b, h->sp_l, h->sp_e, h->operators, nnz, h->B, h->L, h->E, h->r_size, p.cut, p.cnt);
-    else if (nnz > 0)
+    else if (nnz > 0) {
+        if (p.rel_order && h->mode == SP_TOPK && K > 0 && h->sampling_seed < 0 && R > 0)
+            FL_LAUNCH("k_sp_relorder", k_sp_relorder, dim3((unsigned)(2 * R)), dim3(RO_NT), 0, st, h->w, h->n,
+                      h->r_size, p.rel_order, p.rel_nelig);
+        const bool lookup = p.rel_order && h->mode == SP_TOPK && K > 0 && h->sampling_seed < 0;
         FL_LAUNCH("k_sp_select", k_sp_select, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
-                  h->r_size, h->wot_i, h->mode, K, h->sampling_seed, p.th, p.cut, p.cnt);
+                  h->r_size, h->wot_i, h->mode, K, h->sampling_seed, p.th, p.cut, p.cnt,
+                  lookup ? p.rel_order : (const int16_t *)nullptr, lookup ? p.rel_nelig : (const int32_t *)nullptr);
+    }
     if ((rc = exclusive_scan(st, p.cnt, p.item_off, nnz, p.tmp)) != FL_OK) return rc;
     FL_LAUNCH("k_sp_rowinfo", k_sp_rowinfo, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr,
               p.item_off, R, p.row_item0, p.ntiles);
@@ -1773,7 +1901,7 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     if (h->items < 0 || h->tiles < 0) return fl_fail(FL_ERR_ARG, "sparse_expand: negative plan sizes");
     if (h->ws2_bytes < fl_sparse_expand_bytes(h->items, h->tiles, R, h->E, raw_local != nullptr, h->aggregate))
         return fl_fail(FL_ERR_ARG, "sparse_expand: workspace too small");
-    SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
+    SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, raw_local != nullptr, h->aggregate, (char *)h->ws2);
     const bool mx = h->aggregate == SP_MAX;
     hipStream_t st = (hipStream_t)stream;
@@ -1834,7 +1962,7 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h, const int64_t *out_base
     if (!h || !out_base) return fl_fail(FL_ERR_ARG, "sparse_emit: null argument");
     const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
     if (R * NB == 0) return FL_OK;
-    SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
+    SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, 0, h->aggregate, (char *)h->ws2);
     SpRows rows{p.row_item0, p.tile_base, NB};
     FL_LAUNCH("k_sp_emit", k_sp_emit, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, (hipStream_t)stream, rows, h->L,
@@ -1851,7 +1979,7 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
     if (!h->ws1 || !out_base || !grad_v || !grad_w) return fl_fail(FL_ERR_ARG, "sparse_backward: null argument");
     if (h->items > 0 && (!raw_local || !grad_out)) return fl_fail(FL_ERR_ARG, "sparse_backward: null raw map");
     const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
-    SpPlan p = sp_plan_layout(h->nnz, R, (char *)h->ws1);
+    SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     hipStream_t st = (hipStream_t)stream;
     if (R * h->n > 0)
         FL_LAUNCH("k_fill_f32", k_fill_f32, dim3((unsigned)((R * h->n + 255) / 256)), dim3(256), 0, st, grad_w,

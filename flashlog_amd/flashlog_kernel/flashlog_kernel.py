@@ -919,7 +919,8 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         h.wot_i, h.mode, h.topk_edges = 1 if wot_i else 0, int(mode), int(topk_edges)
         h.operators = ptr(operators).value if operators is not None else None
         h.aggregate, h.sampling_seed = int(aggregate), int(seed)
-        ws1 = torch.empty(max(lib.fl_sparse_plan_bytes(nnz, R), 1), dtype=torch.uint8, device=dev)
+        ws1 = torch.empty(max(lib.fl_sparse_plan_bytes(nnz, R, 0 if mode == _SPARSE_FIXED else r_size), 1),
+                          dtype=torch.uint8, device=dev)
         h.ws1, h.ws1_bytes = ptr(ws1).value, ws1.numel()
         plan = torch.empty(4, dtype=torch.int64, device=dev)
         check(lib.fl_sparse_plan(st, ctypes.byref(sides.ori), ctypes.byref(sides.inv), ctypes.byref(h), ptr(plan)),

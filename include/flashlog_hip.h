@@ -264,8 +264,11 @@ typedef struct fl_sparse_hop {
  * supports E <= 2^27 entities. */
 int64_t fl_sparse_buckets(int64_t E);
 
-/* Plan workspace bytes for nnz entries and R = B*L rows. */
-size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R);
+/* Plan workspace bytes for nnz entries, R = B*L rows and r_size relations
+ * per side (0 for the fixed-relation step).  With 0 < r_size <= 4096 the
+ * plan holds each row's c2 admission order (relations by weight desc, id
+ * asc), which the top-k threshold of sources with many groups reads. */
+size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R, int64_t r_size);
 
 /* Replaces the count kernels and the host .item() syncs of
  * flashlog_forward_sparse3d_topk_cuda / _alledges_cuda (flashlog.cu:

@@ -316,3 +316,50 @@ def test_trainable_edge_weights(agg):
         if lp is None or lm is None:
             continue
         assert abs((lp - lm) / 2e-2 - ref[edge]) <= 2e-2 * abs(ref[edge]) + 1e-4
+
+
+def _many_groups_case(seed, ties):
+    """R = 150 relations; node 0 heads a group of every relation (1-4 edges
+    each), node 7 receives every relation: sources with far more than 64
+    groups per side, whose c2 threshold comes from the row's admission
+    order.  Every row holds both hubs plus random entities."""
+    rng = np.random.default_rng(seed)
+    E, R = 3000, 150
+    c0 = 1 + np.arange(R) % 4
+    c7 = 1 + np.arange(R) % 3
+    h = np.concatenate([np.zeros(c0.sum(), np.int64), rng.integers(0, E, c7.sum()), rng.integers(0, E, 20000)])
+    t = np.concatenate([rng.integers(0, E, c0.sum()), np.full(c7.sum(), 7, np.int64), rng.integers(0, E, 20000)])
+    r = np.concatenate([np.repeat(np.arange(R), c0), np.repeat(np.arange(R), c7), rng.integers(0, R, 20000)])
+    csr = O.build_csr_structure(h, t, r, E)
+    n = 2 * R + 1
+    B, L = 2, 3
+    b, l, e, v = sparse_coo_state(B, L, E, 60, rng)
+    keep = (e != 0) & (e != 7)
+    b, l, e, v = b[keep], l[keep], e[keep], v[keep]
+    bl = np.concatenate([b * L + l, np.repeat(np.arange(B * L), 2)])
+    e = np.concatenate([e, np.tile([0, 7], B * L)])
+    v = np.concatenate([v, rng.random(2 * B * L).astype(np.float32) + 0.5])
+    o = np.lexsort((e, bl))
+    state = ((bl // L)[o], (bl % L)[o], e[o], v[o].astype(np.float32))
+    w = attention(B * L, n, rng).reshape(B, L, n)
+    w[rng.random(w.shape) < 0.15] = 0.0
+    if ties:
+        w[..., 10:R] = w[..., 10:11]
+        w[..., R + 20:2 * R] = w[..., R + 20:R + 21]
+    mbool, masks = masks_for(csr, h.shape[0], rng, drop=0.1)
+    return rng, E, R, n, csr, mbool, masks, state, w, B, L
+
+
+@pytest.mark.parametrize("K", [1, 30, 149, 250, 400, 1 << 60])
+@pytest.mark.parametrize("ties", [False, True])
+@pytest.mark.parametrize("agg", ["sum", "max"])
+def test_topk_many_groups(K, ties, agg):
+    rng, E, R, n, csr, mbool, masks, state, w, B, L = _many_groups_case(90 + K % 97 + ties, ties)
+    if agg == "sum":
+        keys, vals = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, K)
+        out, _, _ = _sum(state, w, csr, mbool, B, L, E, R, K)
+        assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+        assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+    else:
+        out, v, wt = _max(state, w, csr, mbool, B, L, E, R, K, grad=True)
+        _check_max(out, v, wt, state, w, csr, masks, B, L, E, R, n, K, False, rng)
