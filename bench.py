@@ -343,6 +343,8 @@ def main_sparse(args):
             idx = s.indices()
             b, l, e, v = idx[0], idx[1], idx[2], s.values()
     csr_np = [c.cpu().numpy() for c in csr]
+    cpu = (cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, W.cpu(), T)
+           if args.cpu_seconds > 0 else None)
     sides_np = ((csr_np[8], csr_np[9], csr_np[11], 0), (csr_np[12], csr_np[13], csr_np[15], R))
     Wn = W.cpu().numpy()
     fb = [fill_bytes(sides_np, bb, ll, ee, B * L, L, n, Wn[hop].reshape(B * L, n), K)
@@ -372,9 +374,79 @@ def main_sparse(args):
         "roofline": {"kernel": "k_sp_fill", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, W, T):
+    """The reference's CPU --sparse evaluation on a sample of the batch: per
+    hop the c1 entity selection of flashlog_kernel.py:1093-1140 (torch ops,
+    restated here) and flashlog_forward_sparse3d_sum_norm_cpu from the
+    reference's flashlog.cpp (oracle/_ref; at::parallel_for over the
+    entries, flashlog_kernel.py:1902-1913 dispatch).  Query rows are
+    independent, so the sample is the first Bs queries of the same batch,
+    run as whole steps until ~cpu_seconds."""
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle", "_ref"))
+    try:
+        import flashlog_ref_cpp as ref
+    except ImportError:
+        print("cpu baseline skipped: oracle/_ref not built", file=sys.stderr, flush=True)
+        return None
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    tc = [torch.from_numpy(a) for a in csr_np]
+    om = torch.ones(tc[1].shape[0], dtype=torch.float32)
+    im = torch.ones(tc[5].shape[0], dtype=torch.float32)
+    n = 2 * R + 1
+    Bs = min(16, W.shape[1])
+    Wt = W[:, :Bs].contiguous()
+
+    def topc(b, l, e, v):
+        if e.numel() <= c1:
+            return None
+        groups, inv = torch.unique_consecutive(b * L + l, return_inverse=True)
+        nz = v != 0
+        cnt = torch.zeros(groups.numel(), dtype=torch.long).scatter_add_(0, inv, nz.long())
+        over = cnt > c1
+        if not bool(over.any()):
+            return None
+        keep = ~over[inv]
+        cand = torch.nonzero(over[inv] & nz, as_tuple=True)[0]
+        ranked = cand[torch.argsort(v[cand], descending=True, stable=True)]
+        ranked = ranked[torch.argsort(inv[ranked], stable=True)]
+        g = inv[ranked]
+        first = torch.searchsorted(g, g, right=False)
+        keep[ranked[(torch.arange(g.numel()) - first) < c1]] = True
+        return torch.nonzero(keep, as_tuple=True)[0]
+
+    def step():
+        b = torch.arange(Bs).repeat_interleave(L)
+        l = torch.arange(L).repeat(Bs)
+        e = torch.from_numpy(src[:Bs]).repeat_interleave(L)
+        v = torch.ones(Bs * L)
+        for hop in range(T):
+            keep = topc(b, l, e, v)
+            if keep is not None:
+                b, l, e, v = b[keep], l[keep], e[keep], v[keep]
+            o = ref.flashlog_forward_sparse3d_sum_norm_cpu(
+                b, l, e, v, Wt[hop].reshape(Bs, L, n), tc[1], om, tc[8], tc[9], tc[10], tc[11],
+                tc[5], im, tc[12], tc[13], tc[14], tc[15], Bs, L, E, R, False, K, 1e-7, False)
+            b, l, e, v = o[0], o[1], o[2], o[3]
+        return b.numel()
+
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        step()
+        steps += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": steps * Bs / el, "unit": "queries/s", "cores": threads, "kind": "reference",
+            "sample": "%d full steps of %d queries x %d hops (first %d queries of the batch) in %.1f s, "
+                      "%d threads" % (steps, Bs, T, Bs, el, threads)}
 
 
 def cpu_baseline(args, cfg, h, r, t, E, R, src, W):

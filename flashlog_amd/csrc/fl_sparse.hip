@@ -236,6 +236,13 @@ __device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, i
     return base;
 }
 
+// LDS ordering between the lanes of one wave (program order + fence).
+__device__ __forceinline__ void fl_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Admission order of c2 per (row, side): the relations with a positive
 // weight sorted by (weight desc, relation asc), ties in relation order =
 // group order (flashlog.cpp:12-89).  Workgroup per (row, side), bitonic sort
@@ -290,31 +297,45 @@ __global__ __launch_bounds__(RO_NT) void k_sp_relorder(const float *__restrict__
 }
 
 // c2 of one (entry, side) whose source has more than K edges, from the
-// row's admission order: the source's groups are found in that order (64
-// relations at a time, binary search over the source's group relations)
-// until the cumulative edge count reaches K.  The group holding the K-th
-// edge gives the threshold weight and the tie cut (its CSR start plus the
-// edges still admitted), the same (threshold, cut) as c2_select.  Returns
-// the kept items (lane partial sums).
+// row's admission order: the source's group counts are found in that order
+// (64 relations at a time) until the cumulative edge count reaches K.  The
+// group holding the K-th edge gives the threshold weight and the tie cut
+// (its CSR start plus the edges still admitted), the same (threshold, cut)
+// as c2_select.  cmap (wave-private LDS, r_size ints, all zero on entry and
+// on return) maps relation -> group count; without it each relation is
+// found by binary search over the source's group relations.  Returns the
+// kept items (lane partial sums).
+__device__ __forceinline__ int64_t sp_find_group(const fl_side &s, int64_t g0, int64_t g1, int rel) {
+    int64_t lo = g0, hi = g1;
+    while (lo < hi) {
+        const int64_t mid = lo + ((hi - lo) >> 1);
+        if ((int)s.group_rel[mid] < rel) lo = mid + 1;
+        else hi = mid;
+    }
+    return (lo < g1 && (int)s.group_rel[lo] == rel) ? lo : -1;
+}
+
 __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int64_t K,
-                                      const int16_t *__restrict__ ord, int ne, float *thv_out, int32_t *ct_out) {
+                                      const int16_t *__restrict__ ord, int ne, int *cmap, float *thv_out,
+                                      int32_t *ct_out) {
     const int lane = fl_lane();
+    if (cmap) {
+        for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) cmap[s.group_rel[g]] = s.group_count[g];
+        fl_wave_sync();
+    }
     long long carry = 0;
+    int hit_rel = -1;
+    long long hit_before = 0;
     for (int k0 = 0; k0 < ne; k0 += FL_WAVE) {
         const int kk = k0 + lane;
         const int rel = kk < ne ? (int)ord[kk] : -1;
-        int64_t g = -1;
         long long cnt = 0;
         if (rel >= 0) {
-            int64_t lo = g0, hi = g1;
-            while (lo < hi) {
-                const int64_t mid = lo + ((hi - lo) >> 1);
-                if ((int)s.group_rel[mid] < rel) lo = mid + 1;
-                else hi = mid;
-            }
-            if (lo < g1 && (int)s.group_rel[lo] == rel) {
-                g = lo;
-                cnt = s.group_count[lo];
+            if (cmap) {
+                cnt = cmap[rel];
+            } else {
+                const int64_t g = sp_find_group(s, g0, g1, rel);
+                cnt = g >= 0 ? s.group_count[g] : 0;
             }
         }
         const long long incl = fl_wave_incl_scan_i64(cnt);
@@ -323,14 +344,22 @@ __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, 
         const unsigned long long bal = __ballot(hit);
         if (bal) {
             const int hl = __ffsll((long long)bal) - 1;
-            const int relj = __shfl(rel, hl, FL_WAVE);
-            const long long bj = __shfl(before, hl, FL_WAVE);
-            const int gj = (int)__shfl((long long)g, hl, FL_WAVE);
-            *thv_out = wr[relj];
-            *ct_out = (int32_t)(s.group_start[gj] + (K - bj));
-            return lane == 0 ? K : 0;
+            hit_rel = __shfl(rel, hl, FL_WAVE);
+            hit_before = __shfl(before, hl, FL_WAVE);
+            break;
         }
         carry += __shfl(incl, FL_WAVE - 1, FL_WAVE);
+    }
+    if (cmap) {
+        fl_wave_sync();
+        for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) cmap[s.group_rel[g]] = 0;
+        fl_wave_sync();
+    }
+    if (hit_rel >= 0) {
+        const int64_t gj = sp_find_group(s, g0, g1, hit_rel);
+        *thv_out = wr[hit_rel];
+        *ct_out = (int32_t)(s.group_start[gj] + (K - hit_before));
+        return lane == 0 ? K : 0;
     }
     *thv_out = 0.0f;  // fewer than K eligible edges: every one is kept
     *ct_out = 0;
@@ -344,6 +373,7 @@ __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, 
 // (all-edges mode), plus the identity item.  With quotas the side keeps
 // exactly min(eligible, K) edges, as the threshold does.
 constexpr int SEL_NT = 256;
+constexpr int SEL_MAP_MAX = 2048;  // relations per side of the LDS count maps
 
 __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                      const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
@@ -351,11 +381,17 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
                                                      int64_t E, int64_t n, int64_t r_size, int wot_i, int mode, int64_t K,
                                                      int64_t seed, float *__restrict__ th, int32_t *__restrict__ cut,
                                                      int32_t *__restrict__ cnt, const int16_t *__restrict__ rel_order,
-                                                     const int32_t *__restrict__ rel_nelig) {
+                                                     const int32_t *__restrict__ rel_nelig, int use_map) {
     __shared__ int hist_all[SEL_NT / FL_WAVE][256];
+    extern __shared__ int cmap_all[];  // [SEL_NT / FL_WAVE][r_size] when the map is used
     const int lane = fl_lane();
     const int wid = threadIdx.x / FL_WAVE;
     const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + wid;
+    int *cmap = use_map ? cmap_all + wid * r_size : nullptr;
+    if (cmap) {
+        for (int64_t q = lane; q < r_size; q += FL_WAVE) cmap[q] = 0;
+        fl_wave_sync();
+    }
     if (i >= nnz) return;
     const int64_t src = se[i];
     if (sb[i] < 0 || sb[i] >= B || sl[i] < 0 || sl[i] >= L || src < 0 || src >= E) {
@@ -382,7 +418,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
                     c += wr[s.group_rel[g]] > 0.0f ? s.group_count[g] : 0;
             } else {
                 const int64_t ro = (sb[i] * L + sl[i]) * 2 + dir;
-                c = sp_select_lookup(s, g0, g1, wr, K, rel_order + ro * r_size, rel_nelig[ro], &thv, &ct);
+                c = sp_select_lookup(s, g0, g1, wr, K, rel_order + ro * r_size, rel_nelig[ro], cmap, &thv, &ct);
             }
         } else {
             uint32_t key;
@@ -838,12 +874,6 @@ constexpr int SP_WB = FL_WAVE * SP_WIPT;  // 512 items
 constexpr int SP_SMALL_WAVES = SP_NT / FL_WAVE;
 constexpr int SP_MID_GRID = 2048;  // workgroups of the persistent mid-size kernel
 
-// LDS ordering between the lanes of one wave (program order + fence).
-__device__ __forceinline__ void fl_wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 // Stable LSD sort of 64 * IPT keys in LDS (blocked: lane t owns
 // kin[t*IPT .. t*IPT + IPT)) by bits [lo, lo + nbits), 4 bits per pass.
@@ -1866,10 +1896,14 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
             FL_LAUNCH("k_sp_relorder", k_sp_relorder, dim3((unsigned)(2 * R)), dim3(RO_NT), 0, st, h->w, h->n,
                       h->r_size, p.rel_order, p.rel_nelig);
         const bool lookup = p.rel_order && h->mode == SP_TOPK && K > 0 && h->sampling_seed < 0;
+        // relation -> count maps in LDS for up to SEL_MAP_MAX relations
+        const int use_map = lookup && h->r_size <= SEL_MAP_MAX;
+        const size_t lds = use_map ? sizeof(int) * (SEL_NT / FL_WAVE) * (size_t)h->r_size : 0;
         FL_LAUNCH("k_sp_select", k_sp_select, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
-                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
+                  dim3(SEL_NT), lds, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
                   h->r_size, h->wot_i, h->mode, K, h->sampling_seed, p.th, p.cut, p.cnt,
-                  lookup ? p.rel_order : (const int16_t *)nullptr, lookup ? p.rel_nelig : (const int32_t *)nullptr);
+                  lookup ? p.rel_order : (const int16_t *)nullptr, lookup ? p.rel_nelig : (const int32_t *)nullptr,
+                  use_map);
     }
     if ((rc = exclusive_scan(st, p.cnt, p.item_off, nnz, p.tmp)) != FL_OK) return rc;
     FL_LAUNCH("k_sp_rowinfo", k_sp_rowinfo, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr,
