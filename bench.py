@@ -38,6 +38,9 @@ def parse():
     ap.add_argument("--profile-steps", type=int, default=10)
     ap.add_argument("--sparse", action="store_true",
                     help="the DRUM --sparse GPU path (default for --config 5)")
+    ap.add_argument("--mode", choices=["train", "eval"], default="train",
+                    help="--sparse step: a training step (sampled hops, loss, backward; the default, as "
+                         "configs[4] is quoted forward and backward) or an evaluation pass")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (a known-size reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -112,7 +115,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(every (query, channel) row is independent; see DESIGN.md for how it would shard)",
+              "(every (query, channel) row is independent, so batches would shard by query)",
               file=sys.stderr)
         sys.exit(2)
     import numpy as np
@@ -221,10 +224,11 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-SPARSE_KERNELS = ["k_sp_topc", "k_sp_rowptr", "k_sp_relorder", "k_sp_select", "k_sp_rowinfo", "k_sp_fill", "k_sp_partition",
-                  "k_sp_accum_small", "k_sp_accum_mid", "k_sp_accum_hot", "k_sp_emit", "k_norm_fwd", "k_scan_tiles",
-                  "k_scan_totals", "k_scan_apply", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask",
-                  "k_sp_hist"]
+SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_race_select", "k_fill_from",
+                  "k_sp_rowptr", "k_sp_relorder", "k_sp_select", "k_sp_rowinfo", "k_sp_fill", "k_sp_hist",
+                  "k_sp_partition", "k_sp_accum_small", "k_sp_accum_mid", "k_sp_accum_hot", "k_sp_emit",
+                  "k_norm_fwd", "k_norm_bwd", "k_sp_bwd", "k_fill_f32", "k_scan_tiles", "k_scan_totals",
+                  "k_scan_apply", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask"]
 
 
 def fill_bytes(sides_np, b, l, e, R, L, n, W, K):
@@ -254,10 +258,16 @@ def fill_bytes(sides_np, b, l, e, R, L, n, W, K):
 
 
 def main_sparse(args):
-    """C5: DRUM --sparse evaluation on one GPU.  A
-    step is T = 3 hops of FlashLogFunctionSparse3DTopKSum (c1 = 1000 entities,
-    c2 = 400 edges) each followed by normalize_sparse3d, from one-hot query
-    states (src/model_DRUM_kernel_sp.py:124-205)."""
+    """C5: DRUM --sparse on one GPU, T = 3 hops of
+    the sparse sum hop (c1 = 1000 entities, c2 = 400 edges), each followed by
+    normalize_sparse3d, from one-hot query states, then the sum over the
+    channels (src/model_DRUM_kernel_sp.py:124-205).
+      train (default): the training step of that model -- each hop is
+      sampled_sparse_propagation (exponential-race c1, quota c2), then the
+      model's log loss on the target entity (src/utils.py:37-47) and the
+      backward pass to the per-hop attention;
+      eval: FlashLogFunctionSparse3DTopKSum with the c1/c2 thresholds, no
+      gradients."""
     import numpy as np
     import torch
     from flashlog_amd import _lib, synth
@@ -266,8 +276,7 @@ def main_sparse(args):
     cfg = synth.CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.copy_mb > 0:
-        copy_calibration(args.copy_mb)
+    train = args.mode == "train"
     t_gen = time.perf_counter()
     h, r, t, E, R = synth.make_graph(args.config)
     n = 2 * R + 1
@@ -287,21 +296,45 @@ def main_sparse(args):
     l0 = torch.arange(L, device=dev).repeat(B)
     e0 = torch.from_numpy(src).to(dev).repeat_interleave(L)
     v0 = torch.ones(B * L, device=dev)
+    state0 = torch.sparse_coo_tensor(torch.stack([b0, l0, e0]), v0, [B, L, E]).coalesce()
+    tgt_key = torch.arange(B, device=dev) * E + torch.from_numpy(tgt).to(dev)
+    Wl = W.clone().requires_grad_(train)
+
+    def hop(s, w):
+        if train:
+            return fk.sampled_sparse_propagation(s, w, csr, mask_values, R, None, False, c1, K, "sum")
+        idx = s.indices()
+        return fk.FlashLogFunctionSparse3DTopKSum.apply(
+            idx[0], idx[1], idx[2], s.values(), w, *csr[:4], *csr[4:8], *csr[8:16], mask_values, None,
+            B, L, E, R, False, K, False, c1, False)
 
     def step(capture=None):
-        b, l, e, v = b0, l0, e0, v0
-        for hop in range(T):
-            s = fk.FlashLogFunctionSparse3DTopKSum.apply(
-                b, l, e, v, W[hop], *csr[:4], *csr[4:8], *csr[8:16], mask_values, None,
-                B, L, E, R, False, K, False, c1, False)
+        s = state0
+        for t_ in range(T):
             if capture is not None:
-                capture.append(s._nnz())
-            s = fk.normalize_sparse3d(s)
-            idx = s.indices()
-            b, l, e, v = idx[0], idx[1], idx[2], s.values()
-        return torch.sparse.sum(s, dim=1)
+                # the entries the hop keeps (the same c1 draws as the hop's own)
+                idx = s.indices()
+                rng_state = torch.cuda.get_rng_state()
+                keep = fk._sparse_topc_entries(idx[0], idx[1], idx[2], s.values(), c1, L, sampling=train)
+                torch.cuda.set_rng_state(rng_state)
+                capture.append(tuple((x if keep is None else x[keep]).cpu().numpy() for x in idx))
+            s = fk.normalize_sparse3d(hop(s, Wl[t_]))
+        idx = s.indices()
+        final = torch.sparse_coo_tensor(torch.stack([idx[0], idx[2]]), s.values(), [B, E]).coalesce()
+        if not train:
+            return final
+        # log loss on each query's target entity (src/utils.py:37-47, tau_2 = 1)
+        fi = final.indices()
+        keys = fi[0] * E + fi[1]
+        pos = torch.searchsorted(keys, tgt_key).clamp(max=max(keys.numel() - 1, 0))
+        logit = torch.where(keys[pos] == tgt_key, final.values()[pos], torch.zeros((), device=dev))
+        loss = -torch.log(torch.clamp(logit, min=1e-7)).mean()
+        Wl.grad = None
+        loss.backward()
+        return loss
 
-    with torch.inference_mode():
+    ctx = torch.enable_grad() if train else torch.inference_mode()
+    with ctx:
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
@@ -315,8 +348,8 @@ def main_sparse(args):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms_step = e_0.elapsed_time(e_1) / args.steps
-        print("timed %d steps: %.3f ms/step (host wall %.3f ms/step)"
-              % (args.steps, ms_step, 1e3 * wall / args.steps), file=sys.stderr, flush=True)
+        print("timed %d %s steps: %.3f ms/step (host wall %.3f ms/step)"
+              % (args.steps, args.mode, ms_step, 1e3 * wall / args.steps), file=sys.stderr, flush=True)
         _lib.prof_enable(True)
         for _ in range(args.profile_steps):
             step()
@@ -331,24 +364,15 @@ def main_sparse(args):
               file=sys.stderr, flush=True)
         # hop inputs of one step (after c1), for the algorithmic bytes of k_sp_fill
         hop_inputs = []
-        b, l, e, v = b0, l0, e0, v0
-        for hop in range(T):
-            keep = fk._sparse_topc_entries(b, l, e, v, c1, L)
-            bb, ll, ee = (x if keep is None else x[keep] for x in (b, l, e))
-            hop_inputs.append((bb.cpu().numpy(), ll.cpu().numpy(), ee.cpu().numpy()))
-            s = fk.FlashLogFunctionSparse3DTopKSum.apply(
-                b, l, e, v, W[hop], *csr[:4], *csr[4:8], *csr[8:16], mask_values, None,
-                B, L, E, R, False, K, False, c1, False)
-            s = fk.normalize_sparse3d(s)
-            idx = s.indices()
-            b, l, e, v = idx[0], idx[1], idx[2], s.values()
+        step(capture=hop_inputs)
+        torch.cuda.synchronize()
     csr_np = [c.cpu().numpy() for c in csr]
-    cpu = (cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, W.cpu(), T)
+    cpu = (cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W.cpu(), T, train)
            if args.cpu_seconds > 0 else None)
     sides_np = ((csr_np[8], csr_np[9], csr_np[11], 0), (csr_np[12], csr_np[13], csr_np[15], R))
     Wn = W.cpu().numpy()
-    fb = [fill_bytes(sides_np, bb, ll, ee, B * L, L, n, Wn[hop].reshape(B * L, n), K)
-          for hop, (bb, ll, ee) in enumerate(hop_inputs)]
+    fb = [fill_bytes(sides_np, bb, ll, ee, B * L, L, n, Wn[hop_].reshape(B * L, n), K)
+          for hop_, (bb, ll, ee) in enumerate(hop_inputs)]
     fill_ms = per_launch["k_sp_fill"]
     bytes_per_launch = float(np.mean(fb))
     achieved = bytes_per_launch / (fill_ms * 1e-3) / 1e9 if fill_ms > 0 else 0.0
@@ -364,11 +388,14 @@ def main_sparse(args):
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded %s graph, flashlog_amd/synth.py)" % cfg.name,
-        "config": {"workload": "%s DRUM --sparse eval: E=%d, R=%d, M=%d, B=%d, N=%d, T=%d, c1=%d, c2=%d"
-                   % (cfg.name, E, R, M, B, L, T, c1, cfg.c2),
-                   "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2},
-        "topk_select_ms": {"c1_per_hop": per_launch["k_sp_topc"], "c2_per_hop": per_launch["k_sp_select"]},
+        "data": "synthetic (seeded %s graph, flashlog_amd/synth.py; random attention in place of the "
+                "model's LSTM)" % cfg.name,
+        "config": {"workload": "%s DRUM --sparse %s step (%s): E=%d, R=%d, M=%d, B=%d, N=%d, T=%d, c1=%d, c2=%d"
+                   % (cfg.name, args.mode, "forward + backward" if train else "forward", E, R, M, B, L, T,
+                      c1, cfg.c2),
+                   "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2, "mode": args.mode},
+        "topk_select_ms": {"c1_per_hop": per_launch["k_race_select"] if train else per_launch["k_sp_topc"],
+                           "c2_per_hop": per_launch["k_sp_select"]},
         "kernel_ms_per_launch": per_launch,
         "kernel_ms_per_step": per_step,
         "roofline": {"kernel": "k_sp_fill", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
@@ -379,14 +406,19 @@ def main_sparse(args):
     print(json.dumps(result), flush=True)
 
 
-def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, W, T):
-    """The reference's CPU --sparse evaluation on a sample of the batch: per
-    hop the c1 entity selection of flashlog_kernel.py:1093-1140 (torch ops,
-    restated here) and flashlog_forward_sparse3d_sum_norm_cpu from the
-    reference's flashlog.cpp (oracle/_ref; at::parallel_for over the
-    entries, flashlog_kernel.py:1902-1913 dispatch).  Query rows are
-    independent, so the sample is the first Bs queries of the same batch,
-    run as whole steps until ~cpu_seconds."""
+def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W, T, train):
+    """The reference's CPU --sparse path on a sample of the batch: per hop the
+    c1 entity selection of flashlog_kernel.py:1093-1140 (torch ops, restated
+    here) and flashlog_forward_sparse3d_sum_norm_cpu from the reference's
+    flashlog.cpp (oracle/_ref; at::parallel_for over the entries,
+    flashlog_kernel.py:1902-1913 dispatch), then the sum over channels.
+    train: also the log-loss gradient on the target entities and
+    flashlog_backward_sparse3d_sum_norm_cpu back through the hops
+    (flashlog_kernel.py:1790-1811).  The reference's sampled selections on
+    the CPU are Python code (flashlog_kernel.py:1955-2100), so the CPU
+    training step uses the deterministic c1/c2 budgets.  Query rows are
+    independent: the sample is the first Bs queries of the same batch, run
+    as whole steps until ~cpu_seconds."""
     import torch
     sys.path.insert(0, os.path.join(ROOT, "oracle", "_ref"))
     try:
@@ -402,6 +434,7 @@ def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, W, T):
     n = 2 * R + 1
     Bs = min(16, W.shape[1])
     Wt = W[:, :Bs].contiguous()
+    tg = torch.from_numpy(tgt[:Bs]).long()
 
     def topc(b, l, e, v):
         if e.numel() <= c1:
@@ -426,15 +459,41 @@ def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, W, T):
         l = torch.arange(L).repeat(Bs)
         e = torch.from_numpy(src[:Bs]).repeat_interleave(L)
         v = torch.ones(Bs * L)
+        tape = []
         for hop in range(T):
             keep = topc(b, l, e, v)
             if keep is not None:
                 b, l, e, v = b[keep], l[keep], e[keep], v[keep]
+            w = Wt[hop].reshape(Bs, L, n)
             o = ref.flashlog_forward_sparse3d_sum_norm_cpu(
-                b, l, e, v, Wt[hop].reshape(Bs, L, n), tc[1], om, tc[8], tc[9], tc[10], tc[11],
-                tc[5], im, tc[12], tc[13], tc[14], tc[15], Bs, L, E, R, False, K, 1e-7, False)
+                b, l, e, v, w, tc[1], om, tc[8], tc[9], tc[10], tc[11],
+                tc[5], im, tc[12], tc[13], tc[14], tc[15], Bs, L, E, R, False, K, 1e-7, train)
+            tape.append((keep, b, l, e, v, w, o))
             b, l, e, v = o[0], o[1], o[2], o[3]
-        return b.numel()
+        # sum over the channels: per (query, entity)
+        key = b * E + e
+        fk_, inv = torch.unique(key, return_inverse=True)
+        final = torch.zeros(fk_.numel()).index_add_(0, inv, v)
+        if not train:
+            return
+        tk = torch.arange(Bs) * E + tg
+        pos = torch.searchsorted(fk_, tk).clamp(max=max(fk_.numel() - 1, 0))
+        hit = fk_[pos] == tk
+        logit = torch.where(hit, final[pos], torch.zeros(()))
+        dlogit = torch.where(hit & (logit > 1e-7), -1.0 / (Bs * logit), torch.zeros(()))
+        grad = torch.where(e == tg[b], dlogit[b], torch.zeros(()))  # d loss / d output values
+        for hop in reversed(range(T)):
+            keep, hb, hl, he, hv, w, o = tape[hop]
+            gsp, gw = ref.flashlog_backward_sparse3d_sum_norm_cpu(
+                o[0], o[1], o[2], grad.float(), o[4], o[5], o[6], hb, hl, he, hv, w,
+                *o[7:14], *o[14:21], o[21], Bs, L, E, R, False, 1e-7)
+            if hop > 0:
+                prev = tape[hop - 1][6]
+                grad = torch.zeros(prev[3].numel())
+                if keep is None:
+                    grad = gsp
+                else:
+                    grad[keep] = gsp
 
     t0 = time.perf_counter()
     steps = 0
@@ -444,9 +503,10 @@ def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, W, T):
         if time.perf_counter() - t0 >= args.cpu_seconds:
             break
     el = time.perf_counter() - t0
+    what = "forward + backward" if train else "forward"
     return {"value": steps * Bs / el, "unit": "queries/s", "cores": threads, "kind": "reference",
-            "sample": "%d full steps of %d queries x %d hops (first %d queries of the batch) in %.1f s, "
-                      "%d threads" % (steps, Bs, T, Bs, el, threads)}
+            "sample": "%d full %s steps of %d queries x %d hops (first %d queries of the batch; deterministic "
+                      "c1/c2 selections) in %.1f s, %d threads" % (steps, what, Bs, T, Bs, el, threads)}
 
 
 def cpu_baseline(args, cfg, h, r, t, E, R, src, W):

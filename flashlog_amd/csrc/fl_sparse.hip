@@ -91,11 +91,24 @@ __global__ void k_sp_rowptr(const int64_t *__restrict__ sb, const int64_t *__res
 // Take rule of one (entry, side).  TAKE_ALL: every edge (all-edges mode);
 // TAKE_TH: the c2 threshold th and tie cut (group_take); TAKE_QUOTA: the
 // training quotas of flashlog.cu:1433-1528 (sampling seed >= 0, more eligible
-// edges than K): every eligible group (w > 0) first gets
-// min(count, floor(K*w/wsum)); the residual K - allocated is spread over the
-// groups' spare capacities by systematic rounding of the capacity prefix
-// with a SplitMix64 phase per (b, l, source, side).  Double arithmetic in
-// the reference's evaluation order (wsum added in group order).
+// edges than K): every eligible group (w > 0, count > 0) first gets
+// base = min(count, floor(K*w/wsum)); the residual K - sum(base) is spread
+// over the groups' spare capacities by systematic rounding of the spare
+// prefix with a SplitMix64 phase per (b, l, source, side).
+//
+// The reference runs the residual loop sequentially with clamps on each
+// group's extra; with cum(p) = floor(residual * p / spare + phase) (residual
+// at p == spare) none of those clamps can bind (cum is monotone, below the
+// residual, grows by at most a group's spare and stays above
+// residual - spare + p, each with a margin of at least 1/spare, far above
+// the double rounding error for any budget and graph that fit in int32), so
+// a group's extra is exactly cum(p_g) - cum(p_{g-1}), p_g the inclusive
+// spare prefix in group order: one wave scan per 64 groups.
+//   The reference adds wsum sequentially in group order.  When every
+// partial sum is exact in double (all eligible weights are multiples of
+// 2^emin and the total stays below 2^(emin+53)) any order gives the same
+// bits, and the wave sums in parallel; otherwise the groups are added one by
+// one in order.
 enum { TAKE_ALL = 0, TAKE_TH = 1, TAKE_QUOTA = 2 };
 
 struct SpTake {
@@ -103,11 +116,24 @@ struct SpTake {
     float th;
     int32_t cut;
     double wsum, phase;
-    long long target, residual, spare, left, cap_left, prefix;
+    long long target, residual, spare, prefix, cum;
 };
 
 __device__ __forceinline__ long long sp_quota_base(const SpTake &tk, float wv, long long cnt) {
     return (long long)fmin((double)cnt, floor(__ddiv_rn(__dmul_rn((double)tk.target, (double)wv), tk.wsum)));
+}
+
+__device__ __forceinline__ long long sp_quota_cum(const SpTake &tk, long long p) {
+    return p == tk.spare ? tk.residual
+                         : (long long)floor(__dadd_rn(
+                               __ddiv_rn(__dmul_rn((double)tk.residual, (double)p), (double)tk.spare), tk.phase));
+}
+
+// exponent of the lowest set bit's place value of a positive finite float
+__device__ __forceinline__ int sp_lsb_exp(float w) {
+    const uint32_t u = __float_as_uint(w);
+    const int e = (int)((u >> 23) & 0xFF);
+    return (e == 0 ? 1 : e) - 150;
 }
 
 template <bool Q>
@@ -121,69 +147,78 @@ __device__ SpTake sp_take(const fl_side &s, int64_t g0, int64_t g1, const float 
     tk.kind = TAKE_QUOTA;
     const int lane = fl_lane();
     double ws = 0.0;
-    long long cap = 0;
-    for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
-        const int64_t g = gb + lane;
-        float wv = 0.0f;
-        if (g < g1) {
-            wv = wr[s.group_rel[g]];
-            if (wv > 0.0f) cap += s.group_count[g];
-        }
-        const int nl = (int)((g1 - gb) < FL_WAVE ? (g1 - gb) : FL_WAVE);
-        for (int j = 0; j < nl; ++j) {  // group order
-            const float wj = __shfl(wv, j, FL_WAVE);
-            if (wj > 0.0f) ws = __dadd_rn(ws, (double)wj);
+    long long cap = 0, nel = 0;
+    int emin = 1 << 20, emax = -(1 << 20);
+    for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
+        const float wv = wr[s.group_rel[g]];
+        const int32_t c = s.group_count[g];
+        if (wv > 0.0f && c > 0) {
+            cap += c;
+            ++nel;
+            ws = __dadd_rn(ws, (double)wv);
+            const int lo = sp_lsb_exp(wv), hi = (int)((__float_as_uint(wv) >> 23) & 0xFF) - 127;
+            emin = lo < emin ? lo : emin;
+            emax = hi > emax ? hi : emax;
         }
     }
     cap = fl_wave_sum_i64(cap);
+    nel = fl_wave_sum_i64(nel);
+#pragma unroll
+    for (int o = FL_WAVE / 2; o > 0; o >>= 1) {
+        ws = __dadd_rn(ws, __shfl_xor(ws, o, FL_WAVE));
+        const int a = __shfl_xor(emin, o, FL_WAVE), c = __shfl_xor(emax, o, FL_WAVE);
+        emin = a < emin ? a : emin;
+        emax = c > emax ? c : emax;
+    }
+    int lg = 0;
+    while ((1ll << lg) < nel) ++lg;
+    if (emax + 1 + lg - emin > 53) {
+        // partial sums may round: the reference's sequential order
+        ws = 0.0;
+        for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
+            const int64_t g = gb + lane;
+            float wv = 0.0f;
+            if (g < g1 && s.group_count[g] > 0) wv = wr[s.group_rel[g]];
+            const int nl = (int)((g1 - gb) < FL_WAVE ? (g1 - gb) : FL_WAVE);
+            for (int j = 0; j < nl; ++j) {  // group order
+                const float wj = __shfl(wv, j, FL_WAVE);
+                if (wj > 0.0f) ws = __dadd_rn(ws, (double)wj);
+            }
+        }
+    }
     tk.wsum = ws;
     tk.target = K < cap ? K : cap;
     long long alloc = 0;
     for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
         const float wv = wr[s.group_rel[g]];
-        if (wv > 0.0f) alloc += sp_quota_base(tk, wv, s.group_count[g]);
+        const int32_t c = s.group_count[g];
+        if (wv > 0.0f && c > 0) alloc += sp_quota_base(tk, wv, c);
     }
     alloc = fl_wave_sum_i64(alloc);
     tk.residual = tk.target - alloc;
     tk.spare = cap - alloc;
-    tk.left = tk.residual;
-    tk.cap_left = tk.spare;
     tk.prefix = 0;
+    tk.cum = 0;  // cum(0) = floor(phase) = 0
     const uint64_t z = (uint64_t)seed ^ ((uint64_t)b * 0x9e3779b97f4a7c15ull) ^ ((uint64_t)l * 0xbf58476d1ce4e5b9ull) ^
                        ((uint64_t)src * 0x94d049bb133111ebull) ^ (dir ? 0xd1b54a32d192ed03ull : 0x8cb92baa3f3d8dd7ull);
     tk.phase = (double)(fl_splitmix64(z) >> 11) * 0x1.0p-53;
     return tk;
 }
 
-// Quota takes of the window's groups (lane j: group gb + j; nl valid lanes):
-// the sequential carry of the reference, run uniformly by every lane.
-__device__ long long sp_quota_window(SpTake &tk, float wv, long long cnt, bool valid, int nl) {
+// Quota takes of the window's groups (lane j: one group, valid = it exists):
+// base + cum(p_g) - cum(p_{g-1}) for eligible groups, carried across windows.
+__device__ __forceinline__ long long sp_quota_window(SpTake &tk, float wv, long long cnt, bool valid) {
     const int lane = fl_lane();
     const bool el = valid && wv > 0.0f && cnt > 0;
     const long long base = el ? sp_quota_base(tk, wv, cnt) : 0;
-    const long long spare = cnt - base;
-    long long mine = 0;
-    for (int j = 0; j < nl; ++j) {
-        const int elj = __shfl((int)el, j, FL_WAVE);
-        const long long bj = __shfl(base, j, FL_WAVE);
-        const long long sj = __shfl(spare, j, FL_WAVE);
-        if (!elj) continue;
-        tk.prefix += sj;
-        tk.cap_left -= sj;
-        const long long cum =
-            tk.prefix == tk.spare
-                ? tk.residual
-                : (long long)floor(__dadd_rn(
-                      __ddiv_rn(__dmul_rn((double)tk.residual, (double)tk.prefix), (double)tk.spare), tk.phase));
-        long long extra = cum - (tk.residual - tk.left);
-        extra = extra < tk.left ? extra : tk.left;
-        extra = extra < sj ? extra : sj;
-        extra = extra > 0 ? extra : 0;
-        extra = extra > tk.left - tk.cap_left ? extra : tk.left - tk.cap_left;
-        tk.left -= extra;
-        if (lane == j) mine = bj + extra;
-    }
-    return mine;
+    const long long spare = el ? cnt - base : 0;
+    const long long incl = fl_wave_incl_scan_i64(spare);
+    const long long cum = sp_quota_cum(tk, tk.prefix + incl);
+    const long long prev = __shfl_up(cum, 1, FL_WAVE);
+    const long long extra = cum - (lane == 0 ? tk.cum : prev);
+    tk.prefix += __shfl(incl, FL_WAVE - 1, FL_WAVE);
+    tk.cum = __shfl(cum, FL_WAVE - 1, FL_WAVE);
+    return el ? base + extra : 0;
 }
 
 // Kept items of one (entry, side) in raw order (group order, then CSR
@@ -211,7 +246,7 @@ __device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, i
             take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? group_take(wv, tk.th, tk.cut, start, cnt) : 0);
         }
         if (Q && tk.kind == TAKE_QUOTA)
-            take = sp_quota_window(tk, wv, cnt, g < g1, (int)((g1 - gb) < FL_WAVE ? (g1 - gb) : FL_WAVE));
+            take = sp_quota_window(tk, wv, cnt, g < g1);
         if (__ballot(take > 0) == 0) continue;  // nothing kept in this window (typical for hub sources)
         const long long incl = fl_wave_incl_scan_i64(take);
         const long long total = __shfl(incl, FL_WAVE - 1, FL_WAVE);

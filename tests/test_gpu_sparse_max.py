@@ -133,12 +133,22 @@ def test_sparse_max_masked_edges_keep_coordinates():
 @pytest.mark.parametrize("agg", ["sum", "max"])
 @pytest.mark.parametrize("K", [1, 3, 40])
 @pytest.mark.parametrize("seed", [0, 987654321])
-def test_quota_hop_bitexact(agg, K, seed):
+@pytest.mark.parametrize("graph,weights", [("c2", "softmax"), ("c2", "wide"), ("many", "softmax"),
+                                           ("many", "wide")])
+def test_quota_hop_bitexact(agg, K, seed, graph, weights):
     """The training quotas (fixed seed) through the internal hop, against the
-    oracle's sequential restatement; forward bits and gradients."""
+    oracle's sequential restatement; forward bits and gradients.  "many":
+    sources with 150 groups per side (quota carries across group windows);
+    "wide": a fifth of the weights scaled by 2^-70, so the weight sums round
+    and the sequential sum order is taken."""
     fk = _fk()
-    B, L = 4, 3
-    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 1.0, B, L, 200, 300 + K + seed % 7, drop=0.2)
+    if graph == "c2":
+        B, L = 4, 3
+        rng, E, R, n, csr, mbool, masks, state, w = _case(2, 1.0, B, L, 200, 300 + K + seed % 7, drop=0.2)
+    else:
+        rng, E, R, n, csr, mbool, masks, state, w, B, L = _many_groups_case(400 + K + seed % 7, False)
+    if weights == "wide":
+        w = np.where(rng.random(w.shape) < 0.2, w * np.float32(2.0 ** -70), w).astype(np.float32)
     tc = to_torch_csr(csr, torch.device("cuda"))
     om, im = _dev(*masks)
     mx = agg == "max"

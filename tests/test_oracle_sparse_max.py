@@ -57,6 +57,29 @@ def test_quota_takes_closed_form_and_invariants(seed):
         assert np.all(takes >= base)
 
 
+@pytest.mark.parametrize("seed", range(60))
+def test_quota_takes_prefix_form_at_scale(seed):
+    # The GPU computes each group's extra as the difference of the rounded
+    # spare prefix (one scan), relying on none of the sequential rule's
+    # clamps binding.  Hub-sized sides, large budgets, zero and extreme
+    # weights: the sequential rule and the prefix form must agree exactly.
+    rng = np.random.default_rng(1000 + seed)
+    G = int(rng.integers(60, 2000))
+    w = rng.random(G).astype(np.float32)
+    w[rng.random(G) < 0.2] = 0.0
+    if seed % 3 == 1:
+        w = np.where(rng.random(G) < 0.3, w * np.float32(2.0 ** -70), w).astype(np.float32)
+    c = rng.integers(1, 5000 if seed % 2 else 8, G).astype(np.int32)
+    cap = int(c[w > 0].sum())
+    K = int(rng.integers(1, max(cap, 2)))
+    b, l, src, inv = (int(x) for x in rng.integers(0, 1 << 20, 4))
+    inv &= 1
+    takes = O.quota_takes(w, c, K, b, l, src, inv, seed * 104729 + 7)
+    phase = O.quota_phase(b, l, src, inv, seed * 104729 + 7)
+    np.testing.assert_array_equal(takes, O.quota_closed_form(w, c, K, phase))
+    assert int(takes.sum()) == min(K, cap)
+
+
 def test_quota_takes_systematic_rounding_distribution():
     # equal weights, 3 groups of 4 edges, budget 5: floors give 1 each, the
     # residual 2 lands on the groups by the phase; over many phases every
