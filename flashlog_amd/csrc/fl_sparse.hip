@@ -870,6 +870,24 @@ __device__ __forceinline__ int sp_run_end(const uint32_t *key, int p, int size) 
     return lo;
 }
 
+// raw_local of the items at sorted positions [p0, p0 + IPT): the output rank
+// of each one's run.  rank0 = the runs that start before p0, so a position
+// before this thread's first head belongs to run rank0 - 1.
+template <int IPT>
+__device__ __forceinline__ void sp_raw_ranks(const uint32_t *key, int p0, int rank0, int64_t start,
+                                             const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local) {
+    int r = rank0 - 1;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int p = p0 + j;
+        const uint32_t k = key[p];
+        if ((k >> 11) >= SP_W) continue;  // hole or padding (sorted last)
+        if (sp_is_head(key, p)) ++r;
+        const int idx = (int)(k & 2047u);
+        raw_local[raw_arr ? raw_arr[start + idx] : start + idx] = r;
+    }
+}
+
 template <int IPT>
 __device__ __forceinline__ void sp_accum_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
                              float *__restrict__ val_arr, const int32_t *__restrict__ raw_arr,
@@ -884,17 +902,13 @@ __device__ __forceinline__ void sp_accum_one(int64_t start, int64_t n, int32_t d
     for (int j = 0; j < IPT; ++j) heads += sp_is_head(key, t * IPT + j) ? 1 : 0;
     int total;
     int rank = fl_block_excl_scan<SP_NT>(heads, scan_lds, &total);
+    if (raw_local) sp_raw_ranks<IPT>(key, t * IPT, rank, start, raw_arr, raw_local);
     // all items were read before the first barrier: outputs may overwrite them
     for (int j = 0; j < IPT; ++j) {
         const int p = t * IPT + j;
         if (!sp_is_head(key, p)) continue;
         const int e = sp_run_end(key, p, SIZE);
         const float a = sp_fold(0.0f, sv, p, e);
-        if (raw_local)
-            for (int q = p; q < e; ++q) {
-                const int idx = (int)(key[q] & 2047u);
-                raw_local[raw_arr ? raw_arr[start + idx] : start + idx] = rank;
-            }
         dst_arr[start + rank] = dbase + (int32_t)(key[p] >> 11);
         val_arr[start + rank] = a;
         ++rank;
@@ -993,17 +1007,13 @@ __device__ __forceinline__ void sp_wave_accum(int64_t start, int64_t n, int32_t 
     const int incl = fl_wave_incl_scan_i32(heads);
     const int total = __shfl(incl, FL_WAVE - 1, FL_WAVE);
     int rank = incl - heads;
+    if (raw_local) sp_raw_ranks<IPT>(key, t * IPT, rank, start, raw_arr, raw_local);
     // every item was read before the sort: outputs may overwrite them
     for (int j = 0; j < IPT; ++j) {
         const int p = t * IPT + j;
         if (!sp_is_head(key, p)) continue;
         const int e = sp_run_end(key, p, SIZE);
         const float a = sp_fold(0.0f, sv, p, e);
-        if (raw_local)
-            for (int q = p; q < e; ++q) {
-                const int idx = (int)(key[q] & 2047u);
-                raw_local[raw_arr ? raw_arr[start + idx] : start + idx] = rank;
-            }
         dst_arr[start + rank] = dbase + (int32_t)(key[p] >> 11);
         val_arr[start + rank] = a;
         ++rank;
