@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 11
+ABI_VERSION = 12
 FL_SEG = 32
 FL_SUP = 16
 
@@ -63,7 +63,7 @@ class FlSparseHop(ctypes.Structure):
         ("topk_edges", ctypes.c_int64), ("ws1", ctypes.c_void_p), ("ws1_bytes", ctypes.c_size_t),
         ("ws2", ctypes.c_void_p), ("ws2_bytes", ctypes.c_size_t), ("items", ctypes.c_int64),
         ("tiles", ctypes.c_int64), ("operators", ctypes.c_void_p), ("aggregate", ctypes.c_int),
-        ("sampling_seed", ctypes.c_int64),
+        ("sampling_seed", ctypes.c_int64), ("raw_pos", ctypes.c_void_p), ("raw_col", ctypes.c_void_p),
     ]
 
 

@@ -76,6 +76,17 @@ __device__ __forceinline__ int fl_block_excl_scan(int v, int *lds, int *total) {
     return res;
 }
 
+// A wave-uniform value moved to scalar registers (the value of the first
+// active lane; every lane must hold the same value).
+__device__ __forceinline__ long long fl_uniform_i64(long long x) {
+    const int lo = __builtin_amdgcn_readfirstlane((int)(unsigned long long)x);
+    const int hi = __builtin_amdgcn_readfirstlane((int)((unsigned long long)x >> 32));
+    return (long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ double fl_uniform_f64(double x) {
+    return __longlong_as_double(fl_uniform_i64(__double_as_longlong(x)));
+}
+
 // Float key that orders like the value (ascending) for every non-NaN float.
 __device__ __forceinline__ uint32_t fl_order_key(float v) {
     uint32_t u = __float_as_uint(v);

@@ -186,7 +186,8 @@ __device__ SpTake sp_take(const fl_side &s, int64_t g0, int64_t g1, const float 
             }
         }
     }
-    tk.wsum = ws;
+    tk.wsum = fl_uniform_f64(ws);
+    cap = fl_uniform_i64(cap);
     tk.target = K < cap ? K : cap;
     long long alloc = 0;
     for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
@@ -194,7 +195,7 @@ __device__ SpTake sp_take(const fl_side &s, int64_t g0, int64_t g1, const float 
         const int32_t c = s.group_count[g];
         if (wv > 0.0f && c > 0) alloc += sp_quota_base(tk, wv, c);
     }
-    alloc = fl_wave_sum_i64(alloc);
+    alloc = fl_uniform_i64(fl_wave_sum_i64(alloc));
     tk.residual = tk.target - alloc;
     tk.spare = cap - alloc;
     tk.prefix = 0;
@@ -216,8 +217,8 @@ __device__ __forceinline__ long long sp_quota_window(SpTake &tk, float wv, long 
     const long long cum = sp_quota_cum(tk, tk.prefix + incl);
     const long long prev = __shfl_up(cum, 1, FL_WAVE);
     const long long extra = cum - (lane == 0 ? tk.cum : prev);
-    tk.prefix += __shfl(incl, FL_WAVE - 1, FL_WAVE);
-    tk.cum = __shfl(cum, FL_WAVE - 1, FL_WAVE);
+    tk.prefix += fl_uniform_i64(__shfl(incl, FL_WAVE - 1, FL_WAVE));
+    tk.cum = fl_uniform_i64(__shfl(cum, FL_WAVE - 1, FL_WAVE));
     return el ? base + extra : 0;
 }
 
@@ -589,7 +590,7 @@ struct SpRows {
 // One wave per entry: the entry's items in raw order at item_off[i]; for
 // the max also their tie keys (original edge id, INV ones above ORI ones,
 // the identity item last).  Q: training quotas possible.
-template <bool Q>
+template <bool Q, bool BWD>
 __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                    const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
                                                    const float *__restrict__ sv, int64_t nnz,
@@ -599,7 +600,8 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
                                                    const int32_t *__restrict__ cut,
                                                    const int64_t *__restrict__ item_off,
                                                    int32_t *__restrict__ raw_dst, float *__restrict__ raw_val,
-                                                   uint32_t *__restrict__ raw_tie) {
+                                                   uint32_t *__restrict__ raw_tie, int32_t *__restrict__ raw_pos,
+                                                   int16_t *__restrict__ raw_col) {
     const int lane = fl_lane();
     const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
     if (i >= nnz) return;
@@ -616,12 +618,16 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
         const float *wr = wrow + (dir ? r_size : 0);
         const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
         SpTake tk = sp_take<Q>(s, g0, g1, wr, mode, th[2 * i + dir], cut[2 * i + dir], K, seed, sb[i], sl[i], src, dir);
-        pos += sp_side_items<Q>(s, g0, g1, wr, tk, [&](bool valid, int64_t k, int64_t p, int, float wv) {
+        pos += sp_side_items<Q>(s, g0, g1, wr, tk, [&](bool valid, int64_t k, int64_t p, int rel, float wv) {
             if (valid && pos + k < lim) {
                 const float m = s.mask[p];
                 raw_dst[pos + k] = (!holes || m != 0.0f) ? s.col_ind[p] : -1;
                 raw_val[pos + k] = fl_mul(fl_mul(a, wv), m);
                 if (raw_tie) raw_tie[pos + k] = (dir ? SP_TIE_INV : 0u) | (uint32_t)s.order[p];
+                if (BWD) {
+                    raw_pos[pos + k] = (int32_t)p;
+                    raw_col[pos + k] = (int16_t)((dir ? r_size : 0) + rel);
+                }
             }
         });
     }
@@ -629,6 +635,10 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
         raw_dst[pos] = (int32_t)src;
         raw_val[pos] = fl_mul(a, wrow[n - 1]);
         if (raw_tie) raw_tie[pos] = SP_TIE_IDENTITY;
+        if (BWD) {
+            raw_pos[pos] = -1;
+            raw_col[pos] = (int16_t)(n - 1);
+        }
     }
 }
 
@@ -1412,22 +1422,23 @@ __global__ __launch_bounds__(SP_NT) void k_sp_emit(SpRows rows, int64_t L, const
 // ---------------------------------------------------------------------------
 // backward
 
-// One wave per entry: the fill walk again; item k of the entry (raw
-// position item_off[i] + k) maps to output out_base[r*NB + dst/8192] +
-// raw_local[...].  grad_v[i] = sum over items of (g*m)*w, plus g*w[n-1] for
-// the identity item (flashlog.cu:1856-1959, order fixed per entry);
-// grad_w[r, col] += (g*m)*a by atomics, as the reference.  Max: only the
-// winning items (raw_local >= 0) take part (flashlog.cu:2364-2410).
-template <bool Q>
+// Backward, wave per entry over the entry's raw items (raw order; the
+// forward recorded each one's CSR position and attention column):
+// grad_v[i] = sum over items of (g*m)*w, the identity item taken with m = 1
+// (flashlog.cu:1856-1959); grad_w[r, col] += (g*m)*a, summed per column
+// within each 64-item chunk (the items of a group are consecutive) and
+// added by atomics, as the reference adds its per-item terms.  Holes (sum:
+// masked kept edges) and, for max, the losing items (raw_local = -1) take
+// no part (flashlog.cu:2364-2410).
 __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                   const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
                                                   const float *__restrict__ sv, int64_t nnz,
                                                   const float *__restrict__ w, int64_t L, int64_t n, int64_t r_size,
-                                                  int wot_i, int mode, int agg, int64_t K, int64_t seed,
-                                                  const float *__restrict__ th, const int32_t *__restrict__ cut,
-                                                  const int64_t *__restrict__ item_off, int64_t NB,
+                                                  int holes, const int64_t *__restrict__ item_off, int64_t NB,
                                                   const int64_t *__restrict__ out_base,
                                                   const int32_t *__restrict__ raw_local,
+                                                  const int32_t *__restrict__ raw_pos,
+                                                  const int16_t *__restrict__ raw_col,
                                                   const float *__restrict__ grad, float *__restrict__ grad_v,
                                                   float *__restrict__ grad_w) {
     const int lane = fl_lane();
@@ -1438,58 +1449,46 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
     const float a = sv[i];
     const float *wrow = w + r * n;
     const int64_t *orow = out_base + r * NB;
-    const bool holes = mode == SP_TOPK && agg == SP_SUM;
+    const int64_t k0 = item_off[i], k1 = item_off[i + 1];
     float gsp = 0.0f;
-    int64_t pos = item_off[i];
-    const int64_t lim = item_off[i + 1] - (wot_i ? 0 : 1);
-    for (int dir = 0; dir < 2; ++dir) {
-        const fl_side &s = dir ? inv : ori;
-        const int64_t off = dir ? r_size : 0;
-        const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-        SpTake tk = sp_take<Q>(s, g0, g1, wrow + off, mode, th[2 * i + dir], cut[2 * i + dir], K, seed, sb[i],
-                               sl[i], src, dir);
-        pos += sp_side_items<Q>(s, g0, g1, wrow + off, tk, [&](bool valid, int64_t kk, int64_t p, int rel, float wv) {
-            float gwv = 0.0f;
-            if (valid && pos + kk < lim) {
-                const float m = s.mask[p];
-                const int32_t loc = (!holes || m != 0.0f) ? raw_local[pos + kk] : -1;
-                if (loc >= 0) {
-                    const int32_t d = s.col_ind[p];
-                    const float gv = grad[orow[d >> SP_S] + loc];
-                    const float gm = fl_mul(gv, m);
-                    gsp = fl_add(gsp, fl_mul(gm, wv));
-                    gwv = fl_mul(gm, a);
-                    if (s.grad_edge) {
-                        const float ge = fl_mul(fl_mul(fl_mul(fl_mul(gv, a), wv), m), s.dscore[p]);
-                        if (ge != 0.0f) atomicAdd(&s.grad_edge[s.order[p]], ge);
-                    }
+    for (int64_t kb = k0; kb < k1; kb += FL_WAVE) {
+        const int64_t k = kb + lane;
+        int col = -1;
+        float gwv = 0.0f;
+        if (k < k1) {
+            const int32_t p = raw_pos[k];
+            col = raw_col[k];
+            const bool iv = p >= 0 && col >= r_size;
+            const fl_side &s = iv ? inv : ori;
+            const float m = p >= 0 ? s.mask[p] : 1.0f;
+            const int32_t loc = (p < 0 || !holes || m != 0.0f) ? raw_local[k] : -1;
+            if (loc >= 0) {
+                const int32_t d = p >= 0 ? s.col_ind[p] : (int32_t)src;
+                const float gv = grad[orow[d >> SP_S] + loc];
+                const float wv = wrow[col];
+                const float gm = fl_mul(gv, m);
+                gsp = fl_add(gsp, fl_mul(gm, wv));
+                gwv = fl_mul(gm, a);
+                if (p >= 0 && s.grad_edge) {
+                    const float ge = fl_mul(fl_mul(fl_mul(fl_mul(gv, a), wv), m), s.dscore[p]);
+                    if (ge != 0.0f) atomicAdd(&s.grad_edge[s.order[p]], ge);
                 }
             }
-            // per-relation sums of this chunk: items of one group are on
-            // consecutive lanes (segmented scan keyed by the relation column)
-            const int seg = valid ? rel : -1;
-            float x = gwv;
+        }
+        // per-column sums of this chunk (segmented scan keyed by the column)
+        float x = gwv;
 #pragma unroll
-            for (int o = 1; o < FL_WAVE; o <<= 1) {
-                const float y = __shfl_up(x, o, FL_WAVE);
-                const int sy = __shfl_up(seg, o, FL_WAVE);
-                if (lane >= o && sy == seg) x = fl_add(x, y);
-            }
-            const int snext = __shfl_down(seg, 1, FL_WAVE);
-            const bool tail = lane == FL_WAVE - 1 || snext != seg;
-            if (valid && tail && x != 0.0f) atomicAdd(&grad_w[r * n + off + rel], x);
-        });
+        for (int o = 1; o < FL_WAVE; o <<= 1) {
+            const float y = __shfl_up(x, o, FL_WAVE);
+            const int sy = __shfl_up(col, o, FL_WAVE);
+            if (lane >= o && sy == col) x = fl_add(x, y);
+        }
+        const int snext = __shfl_down(col, 1, FL_WAVE);
+        const bool tail = lane == FL_WAVE - 1 || snext != col;
+        if (col >= 0 && tail && x != 0.0f) atomicAdd(&grad_w[r * n + col], x);
     }
     gsp = fl_wave_sum_f32(gsp);
-    if (lane == 0) {
-        const int32_t loc = (wot_i || pos != lim) ? -1 : raw_local[pos];
-        if (loc >= 0) {
-            const float gv = grad[orow[src >> SP_S] + loc];
-            gsp = fl_add(gsp, fl_mul(gv, wrow[n - 1]));
-            atomicAdd(&grad_w[r * n + n - 1], fl_mul(gv, a));
-        }
-        grad_v[i] = gsp;
-    }
+    if (lane == 0) grad_v[i] = gsp;
 }
 
 __global__ void k_fill_i32(int32_t *__restrict__ p, int64_t n, int32_t v) {
@@ -1980,6 +1979,11 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     if (h->items < 0 || h->tiles < 0) return fl_fail(FL_ERR_ARG, "sparse_expand: negative plan sizes");
     if (h->ws2_bytes < fl_sparse_expand_bytes(h->items, h->tiles, R, h->E, raw_local != nullptr, h->aggregate))
         return fl_fail(FL_ERR_ARG, "sparse_expand: workspace too small");
+    if (raw_local && h->mode != SP_FIXED && h->items > 0) {
+        if (!h->raw_pos || !h->raw_col)
+            return fl_fail(FL_ERR_ARG, "sparse_expand: raw_local needs raw_pos and raw_col");
+        if (h->n > 32767) return fl_fail(FL_ERR_ARG, "sparse_expand: backward columns need n <= 32767");
+    }
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, raw_local != nullptr, h->aggregate, (char *)h->ws2);
     const bool mx = h->aggregate == SP_MAX;
@@ -1990,10 +1994,14 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         FL_LAUNCH("k_fx_fill", k_fx_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_e, h->sp_v, nnz, p.cut, p.item_off, x.raw_dst, x.raw_val);
     else if (nnz > 0)
-        FL_LAUNCH("k_sp_fill", sp_quotas(h) ? k_sp_fill<true> : k_sp_fill<false>, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+        FL_LAUNCH("k_sp_fill",
+                  raw_local ? (sp_quotas(h) ? k_sp_fill<true, true> : k_sp_fill<false, true>)
+                            : (sp_quotas(h) ? k_sp_fill<true, false> : k_sp_fill<false, false>),
+                  dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n,
                   h->r_size, h->wot_i, h->mode, h->aggregate, sp_budget(h), h->sampling_seed, p.th, p.cut,
-                  p.item_off, x.raw_dst, x.raw_val, x.raw_tie);
+                  p.item_off, x.raw_dst, x.raw_val, x.raw_tie, raw_local ? h->raw_pos : (int32_t *)nullptr,
+                  raw_local ? h->raw_col : (int16_t *)nullptr);
     int32_t *dst_arr = x.raw_dst, *raw_arr = nullptr;
     float *val_arr = x.raw_val;
     uint32_t *tie_arr = x.raw_tie;
@@ -2056,7 +2064,9 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
     int rc;
     if ((rc = sp_check(ori, inv, h, "sparse_backward")) != FL_OK) return rc;
     if (!h->ws1 || !out_base || !grad_v || !grad_w) return fl_fail(FL_ERR_ARG, "sparse_backward: null argument");
-    if (h->items > 0 && (!raw_local || !grad_out)) return fl_fail(FL_ERR_ARG, "sparse_backward: null raw map");
+    if (h->items > 0 && (!raw_local || !grad_out || !h->raw_pos || !h->raw_col))
+        return fl_fail(FL_ERR_ARG, "sparse_backward: null raw map (raw_local, raw_pos, raw_col)");
+    if (h->mode == SP_FIXED) return fl_fail(FL_ERR_ARG, "sparse_backward: the fixed-relation step has no backward");
     const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     hipStream_t st = (hipStream_t)stream;
@@ -2064,10 +2074,10 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
         FL_LAUNCH("k_fill_f32", k_fill_f32, dim3((unsigned)((R * h->n + 255) / 256)), dim3(256), 0, st, grad_w,
                   R * h->n, 0.0f);
     if (h->nnz > 0)
-        FL_LAUNCH("k_sp_bwd", sp_quotas(h) ? k_sp_bwd<true> : k_sp_bwd<false>, dim3((unsigned)((h->nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+        FL_LAUNCH("k_sp_bwd", k_sp_bwd, dim3((unsigned)((h->nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, h->nnz, h->w, h->L, h->n,
-                  h->r_size, h->wot_i, h->mode, h->aggregate, sp_budget(h), h->sampling_seed, p.th, p.cut,
-                  p.item_off, NB, out_base, raw_local, grad_out, grad_v, grad_w);
+                  h->r_size, (h->mode == SP_TOPK && h->aggregate == SP_SUM) ? 1 : 0, p.item_off, NB, out_base,
+                  raw_local, h->raw_pos, h->raw_col, grad_out, grad_v, grad_w);
     return fl_check_launch("sparse_backward");
 }
 

@@ -941,6 +941,11 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     h.ws2, h.ws2_bytes = ptr(ws2).value, ws2.numel()
     out_base = torch.empty(R * nb + 1, dtype=torch.int64, device=dev)
     raw_local = torch.empty(max(items, 1), dtype=torch.int32, device=dev) if need_backward else None
+    raw_pos = raw_col = None
+    if need_backward:
+        raw_pos = torch.empty(max(items, 1), dtype=torch.int32, device=dev)
+        raw_col = torch.empty(max(items, 1), dtype=torch.int16, device=dev)
+        h.raw_pos, h.raw_col = ptr(raw_pos).value, ptr(raw_col).value
     check(lib.fl_sparse_expand(st, ctypes.byref(sides.ori), ctypes.byref(sides.inv), ctypes.byref(h),
                                ptr(out_base), ptr(raw_local) if need_backward else None), "sparse_expand")
     nout = int(out_base[-1])
@@ -952,7 +957,7 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     if need_backward:
         state = _SparseState()
         state.h, state.sides, state.perm = h, sides, perm
-        state.keep = (sp_b, sp_l, sp_e, sp_v, w_flat, ws1, out_base, raw_local)
+        state.keep = (sp_b, sp_l, sp_e, sp_v, w_flat, ws1, out_base, raw_local, raw_pos, raw_col)
         state.out_base, state.raw_local, state.nout, state.n = out_base, raw_local, nout, n
     del ws2
     return idx, vals, state

@@ -258,6 +258,16 @@ typedef struct fl_sparse_hop {
                                           flashlog.cu:1433-1528 (weighted
                                           floors + SplitMix64-phased
                                           systematic residuals)             */
+    int32_t *raw_pos;                  /* with raw_local (fl_sparse_expand):
+                                          [items] receives every raw item's
+                                          CSR position in its side (-1 for
+                                          the identity item)                */
+    int16_t *raw_col;                  /* with raw_local: [items] receives its
+                                          attention column (ORI relation,
+                                          r_size + INV relation, n - 1 for the
+                                          identity); needs n <= 32767.  The
+                                          backward reads both instead of
+                                          walking the groups again.          */
 } fl_sparse_hop;
 
 /* Destination buckets per row (8192 entities each).  The sparse hop
@@ -310,7 +320,8 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h,
  * of every output entry.  With a side's grad_edge set (trainable edge
  * weights, flashlog_kernel.py:1306-1336), grad_edge[order[p]] also
  * accumulates (((g*a)*w)*m)*dscore[p] for the side's items (the caller
- * zeroes it).  Needs the plan workspace of the forward. */
+ * zeroes it).  Needs the plan workspace of the forward and the raw_pos /
+ * raw_col arrays that its expand filled (h->raw_pos, h->raw_col). */
 int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv,
                        const fl_sparse_hop *h, const int64_t *out_base,
                        const int32_t *raw_local, const float *grad_out,
