@@ -1,18 +1,26 @@
 """Benchmark of the FlashLog propagation hot path on one MI355X.
 
-A step is one DRUM evaluation pass over one batch: T = 3 hops of the dense
-sum propagation with the c1 entity budget and the c2 edge budget
-(dense_csr_sum_cuda, flashlog_kernel.py:1629-1663), each followed by the
-model's per-row normalization (src/model_DRUM_kernel.py:141-144), then the sum
-over channels (:149-152).  Workload: BASELINE.json configs[1] (C2: 41k
-entities, 11 base relations, 87k triples, Zipf(1.1) degrees, batch 32, N=3,
-c1=1000, c2=400), synthetic and seeded (flashlog_amd/synth.py).
+Default workload: BASELINE.json configs[4] (C5), the largest configuration
+and the one the throughput target is stated on -- DRUM --sparse on one GPU,
+4.6M entities, 822 base relations, 20M triples (Zipf(1.0) relations,
+Zipf(1.3) degrees), batch 256, N=3 channels, T=3 hops, c1=1000, c2=400,
+forward and backward.  A step is one training step of that model
+(src/model_DRUM_kernel_sp.py:92-205): three hops of sampled_sparse_propagation
+(exponential-race c1, quota c2), each followed by normalize_sparse3d, the sum
+over the channels, the model's log loss on each query's target entity
+(src/utils.py:37-47) and the backward pass to the per-hop attention.  The
+attention is random (softmax of N(0,1) logits) in place of the model's LSTM;
+graph and queries are synthetic and seeded (flashlog_amd/synth.py).
+--mode eval: the evaluation pass (c1/c2 thresholds, no gradients).
+--config 2: configs[1] (C2), the dense DRUM hop (dense_csr_sum_cuda,
+flashlog_kernel.py:1629-1663) with c1=1000, c2=400 and the model's
+normalization.
 
 Prints one JSON line.  ``value`` = queries/sec (batch / step time) with all
-inputs resident in HBM.  ``roofline`` is for the propagation kernel (k_pull),
-timed with HIP events on its own stream inside the library; ``cpu_baseline``
-is the reference's CPU path (its flashlog.cpp built into oracle/_ref, serial
-as in the reference) on a bounded sample of the same workload.
+inputs resident in HBM.  ``roofline`` is for the propagation kernel (k_sp_fill
+for C5, k_pull for C2), timed with HIP events the library records around its
+launches on its own stream; ``cpu_baseline`` is the reference's CPU path (its
+flashlog.cpp built into oracle/_ref) on a bounded sample of the same workload.
 """
 import argparse
 import json
@@ -32,7 +40,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--config", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU baseline sample (0 disables it)")
     ap.add_argument("--profile-steps", type=int, default=10)

@@ -10,9 +10,13 @@ import sys
 __version__ = "0.1.0"
 
 
-def install():
-    """Alias ``flashlog_kernel`` and ``flashlog_kernel.flashlog_kernel`` to
-    this package's mirror (drop-in replacement of the reference package)."""
+def install(rules=False):
+    """Alias ``flashlog_kernel``, ``flashlog_kernel.flashlog_kernel`` and
+    ``flashlog_kernel.soft_grounding_kernel[.soft_grounding_kernel]`` to this
+    package's mirrors (drop-in replacement of the reference package).
+    rules=True also redirects ``rules.shared_inference`` and
+    ``rules.max_inference`` (their ``score`` entry points) to the GPU
+    rule-bank scoring, leaving the rest of a ``rules`` package alone."""
     from . import flashlog_kernel as pkg
     from .flashlog_kernel import flashlog_kernel as mod
     from .flashlog_kernel import soft_grounding_kernel as sg
@@ -21,4 +25,11 @@ def install():
     sys.modules["flashlog_kernel.flashlog_kernel"] = mod
     sys.modules["flashlog_kernel.soft_grounding_kernel"] = sg
     sys.modules["flashlog_kernel.soft_grounding_kernel.soft_grounding_kernel"] = sgm
+    if rules:
+        from .rules import max_inference as mi, shared_inference as si
+        sys.modules["rules.shared_inference"] = si
+        sys.modules["rules.max_inference"] = mi
+        parent = sys.modules.get("rules")
+        if parent is not None:
+            parent.shared_inference, parent.max_inference = si, mi
     return pkg

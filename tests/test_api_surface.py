@@ -77,3 +77,26 @@ def test_grounding_signature_matches_reference(name):
     flashlog_amd.install()
     import flashlog_kernel.soft_grounding_kernel as sg
     assert list(inspect.signature(getattr(sg, name)).parameters) == GROUNDING[name]
+
+
+def test_install_aliases_reference_module_names():
+    import importlib
+    import sys
+    import flashlog_amd
+    saved = {k: sys.modules.get(k) for k in ("rules", "rules.shared_inference", "rules.max_inference")}
+    try:
+        flashlog_amd.install(rules=True)
+        assert importlib.import_module("flashlog_kernel.flashlog_kernel").__name__ == \
+            "flashlog_amd.flashlog_kernel.flashlog_kernel"
+        sg = importlib.import_module("flashlog_kernel.soft_grounding_kernel.soft_grounding_kernel")
+        assert hasattr(sg, "ground_head_batch_source_folds_sampled_capped_counts")
+        from rules.max_inference import score as max_score
+        from rules.shared_inference import score as shared_score
+        assert shared_score.__module__ == "flashlog_amd.rules.shared_inference"
+        assert max_score.__module__ == "flashlog_amd.rules.max_inference"
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                sys.modules.pop(k, None)
+            else:
+                sys.modules[k] = v
