@@ -136,15 +136,14 @@ __device__ __forceinline__ int sp_lsb_exp(float w) {
     return (e == 0 ? 1 : e) - 150;
 }
 
-template <bool Q>
-__device__ SpTake sp_take(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int mode, float thv, int32_t ct,
-                          int64_t K, int64_t seed, int64_t b, int64_t l, int64_t src, int dir) {
-    SpTake tk{};
-    tk.th = thv;
-    tk.cut = ct;
-    if (mode == SP_ALL) { tk.kind = TAKE_ALL; return tk; }
-    if (!Q || !__builtin_isnan(thv)) { tk.kind = TAKE_TH; return tk; }
-    tk.kind = TAKE_QUOTA;
+// Quota parameters of one (entry, side), computed once by k_sp_select and
+// read by the fill: wsum, target = min(K, capacity), residual, spare.
+struct SpQuota {
+    double wsum;
+    long long cap, target, residual, spare;
+};
+
+__device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int64_t K) {
     const int lane = fl_lane();
     double ws = 0.0;
     long long cap = 0, nel = 0;
@@ -186,18 +185,38 @@ __device__ SpTake sp_take(const fl_side &s, int64_t g0, int64_t g1, const float 
             }
         }
     }
-    tk.wsum = fl_uniform_f64(ws);
-    cap = fl_uniform_i64(cap);
-    tk.target = K < cap ? K : cap;
+    SpQuota q;
+    q.wsum = ws;
+    q.cap = cap;
+    q.target = K < cap ? K : cap;
+    SpTake tk{};
+    tk.wsum = ws;
+    tk.target = q.target;
     long long alloc = 0;
     for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
         const float wv = wr[s.group_rel[g]];
         const int32_t c = s.group_count[g];
         if (wv > 0.0f && c > 0) alloc += sp_quota_base(tk, wv, c);
     }
-    alloc = fl_uniform_i64(fl_wave_sum_i64(alloc));
-    tk.residual = tk.target - alloc;
-    tk.spare = cap - alloc;
+    alloc = fl_wave_sum_i64(alloc);
+    q.residual = q.target - alloc;
+    q.spare = cap - alloc;
+    return q;
+}
+
+template <bool Q>
+__device__ __forceinline__ SpTake sp_take(int mode, float thv, int32_t ct, const SpQuota *qp, int64_t seed,
+                                          int64_t b, int64_t l, int64_t src, int dir) {
+    SpTake tk{};
+    tk.th = thv;
+    tk.cut = ct;
+    if (mode == SP_ALL) { tk.kind = TAKE_ALL; return tk; }
+    if (!Q || !__builtin_isnan(thv)) { tk.kind = TAKE_TH; return tk; }
+    tk.kind = TAKE_QUOTA;
+    tk.wsum = qp->wsum;
+    tk.target = qp->target;
+    tk.residual = qp->residual;
+    tk.spare = qp->spare;
     tk.prefix = 0;
     tk.cum = 0;  // cum(0) = floor(phase) = 0
     const uint64_t z = (uint64_t)seed ^ ((uint64_t)b * 0x9e3779b97f4a7c15ull) ^ ((uint64_t)l * 0xbf58476d1ce4e5b9ull) ^
@@ -411,13 +430,15 @@ __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, 
 constexpr int SEL_NT = 256;
 constexpr int SEL_MAP_MAX = 2048;  // relations per side of the LDS count maps
 
+template <bool QS>
 __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                      const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
                                                      int64_t nnz, const float *__restrict__ w, int64_t B, int64_t L,
                                                      int64_t E, int64_t n, int64_t r_size, int wot_i, int mode, int64_t K,
                                                      int64_t seed, float *__restrict__ th, int32_t *__restrict__ cut,
                                                      int32_t *__restrict__ cnt, const int16_t *__restrict__ rel_order,
-                                                     const int32_t *__restrict__ rel_nelig, int use_map) {
+                                                     const int32_t *__restrict__ rel_nelig, int use_map,
+                                                     SpQuota *__restrict__ qout) {
     __shared__ int hist_all[SEL_NT / FL_WAVE][256];
     extern __shared__ int cmap_all[];  // [SEL_NT / FL_WAVE][r_size] when the map is used
     const int lane = fl_lane();
@@ -462,12 +483,13 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
             bool quota = false;
             if (K < 0) {
                 thv = __int_as_float(0x7f800000);  // budget <= 0: no edge is kept
-            } else if (K > 0 && seed >= 0) {
-                long long e = 0;
-                for (int64_t g = g0 + lane; g < g1; g += FL_WAVE)
-                    if (wr[s.group_rel[g]] > 0.0f) e += s.group_count[g];
-                quota = fl_wave_sum_i64(e) > K;
-                if (quota) thv = __int_as_float(0x7fc00000);
+            } else if (QS && K > 0 && seed >= 0) {
+                const SpQuota q = sp_quota_setup(s, g0, g1, wr, K);
+                quota = q.cap > K;  // more eligible edges than the budget
+                if (quota) {
+                    thv = __int_as_float(0x7fc00000);
+                    if (lane == 0) qout[2 * i + dir] = q;
+                }
             } else if (K > 0 && c2_select(s, g0, g1, wr, K, hist_all[wid], &key, &cc)) {
                 thv = __uint_as_float(key);
                 ct = cc;
@@ -597,7 +619,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
                                                    const float *__restrict__ w, int64_t L, int64_t n,
                                                    int64_t r_size, int wot_i, int mode, int agg, int64_t K,
                                                    int64_t seed, const float *__restrict__ th,
-                                                   const int32_t *__restrict__ cut,
+                                                   const int32_t *__restrict__ cut, const SpQuota *__restrict__ quota,
                                                    const int64_t *__restrict__ item_off,
                                                    int32_t *__restrict__ raw_dst, float *__restrict__ raw_val,
                                                    uint32_t *__restrict__ raw_tie, int32_t *__restrict__ raw_pos,
@@ -617,7 +639,8 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
         const fl_side &s = dir ? inv : ori;
         const float *wr = wrow + (dir ? r_size : 0);
         const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-        SpTake tk = sp_take<Q>(s, g0, g1, wr, mode, th[2 * i + dir], cut[2 * i + dir], K, seed, sb[i], sl[i], src, dir);
+        SpTake tk = sp_take<Q>(mode, th[2 * i + dir], cut[2 * i + dir], quota + 2 * i + dir, seed, sb[i], sl[i], src,
+                               dir);
         pos += sp_side_items<Q>(s, g0, g1, wr, tk, [&](bool valid, int64_t k, int64_t p, int rel, float wv) {
             if (valid && pos + k < lim) {
                 const float m = s.mask[p];
@@ -1800,6 +1823,7 @@ struct SpPlan {
     float *th;
     int32_t *cut, *cnt, *ntiles;
     int64_t *item_off, *row_ptr, *row_item0, *tile_base, *tmp;
+    SpQuota *quota;       // [nnz][2] training quota parameters (quota sides only)
     int16_t *rel_order;   // [R][2][r_size] c2 admission order (r_size <= RO_MAX)
     int32_t *rel_nelig;   // [R][2] relations with a positive weight
     size_t bytes;
@@ -1819,6 +1843,7 @@ SpPlan sp_plan_layout(int64_t nnz, int64_t R, int64_t r_size, char *base) {
     p.tile_base = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
     const int64_t mx = nnz > R ? nnz : R;
     p.tmp = (int64_t *)take(scan_tmp_bytes(mx + 1));
+    p.quota = (SpQuota *)take(sizeof(SpQuota) * 2 * (size_t)(nnz > 0 ? nnz : 1));
     if (r_size > 0 && r_size <= RO_MAX) {
         p.rel_order = (int16_t *)take(sizeof(int16_t) * 2 * (size_t)R * (size_t)r_size);
         p.rel_nelig = (int32_t *)take(sizeof(int32_t) * 2 * (size_t)(R > 0 ? R : 1));
@@ -1943,11 +1968,11 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
         // relation -> count maps in LDS for up to SEL_MAP_MAX relations
         const int use_map = lookup && h->r_size <= SEL_MAP_MAX;
         const size_t lds = use_map ? sizeof(int) * (SEL_NT / FL_WAVE) * (size_t)h->r_size : 0;
-        FL_LAUNCH("k_sp_select", k_sp_select, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
+        FL_LAUNCH("k_sp_select", sp_quotas(h) ? k_sp_select<true> : k_sp_select<false>, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), lds, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
                   h->r_size, h->wot_i, h->mode, K, h->sampling_seed, p.th, p.cut, p.cnt,
                   lookup ? p.rel_order : (const int16_t *)nullptr, lookup ? p.rel_nelig : (const int32_t *)nullptr,
-                  use_map);
+                  use_map, p.quota);
     }
     if ((rc = exclusive_scan(st, p.cnt, p.item_off, nnz, p.tmp)) != FL_OK) return rc;
     FL_LAUNCH("k_sp_rowinfo", k_sp_rowinfo, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr,
@@ -2000,7 +2025,7 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
                   dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n,
                   h->r_size, h->wot_i, h->mode, h->aggregate, sp_budget(h), h->sampling_seed, p.th, p.cut,
-                  p.item_off, x.raw_dst, x.raw_val, x.raw_tie, raw_local ? h->raw_pos : (int32_t *)nullptr,
+                  p.quota, p.item_off, x.raw_dst, x.raw_val, x.raw_tie, raw_local ? h->raw_pos : (int32_t *)nullptr,
                   raw_local ? h->raw_col : (int16_t *)nullptr);
     int32_t *dst_arr = x.raw_dst, *raw_arr = nullptr;
     float *val_arr = x.raw_val;
