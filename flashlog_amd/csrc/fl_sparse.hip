@@ -873,15 +873,32 @@ __device__ __forceinline__ float *sp_sorted_values(const uint32_t *key, uint32_t
     return sv;
 }
 
-// a + sv[p] + sv[p+1] + ... + sv[e-1], left to right; loads issued 8 ahead.
+// a + sv[p] + sv[p+1] + ... + sv[e-1], left to right.  Long runs (hub
+// destinations) are a sequential chain of adds: their values are read 32 at
+// a time with 16-byte LDS loads (sv is 16-byte aligned) so the chain waits
+// on one LDS round trip per 32 adds.
 __device__ __forceinline__ float sp_fold(float a, const float *sv, int p, int e) {
     int q = p;
-    for (; q + 8 <= e; q += 8) {
-        float x[8];
+    while (q < e && (q & 3)) a = fl_add(a, sv[q++]);
+    const float4 *v4 = reinterpret_cast<const float4 *>(sv);
+    for (; q + 32 <= e; q += 32) {
+        float4 x[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = sv[q + u];
+        for (int u = 0; u < 8; ++u) x[u] = v4[(q >> 2) + u];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) a = fl_add(a, x[u]);
+        for (int u = 0; u < 8; ++u) {
+            a = fl_add(a, x[u].x);
+            a = fl_add(a, x[u].y);
+            a = fl_add(a, x[u].z);
+            a = fl_add(a, x[u].w);
+        }
+    }
+    for (; q + 4 <= e; q += 4) {
+        const float4 x = v4[q >> 2];
+        a = fl_add(a, x.x);
+        a = fl_add(a, x.y);
+        a = fl_add(a, x.z);
+        a = fl_add(a, x.w);
     }
     for (; q < e; ++q) a = fl_add(a, sv[q]);
     return a;
@@ -1065,7 +1082,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
                                                          int32_t *__restrict__ hot_list,
                                                          int32_t *__restrict__ mid_list,
                                                          int32_t *__restrict__ lists) {
-    __shared__ uint32_t kb[SP_SMALL_WAVES][2][SP_WB];
+    __shared__ __align__(16) uint32_t kb[SP_SMALL_WAVES][2][SP_WB];
     __shared__ float val[SP_SMALL_WAVES][SP_WB];
     __shared__ uint16_t cnt[SP_SMALL_WAVES][16][FL_WAVE];
     const int w = threadIdx.x / FL_WAVE;
@@ -1108,7 +1125,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64
                                                        int32_t *__restrict__ out_count,
                                                        const int32_t *__restrict__ mid_list,
                                                        int32_t *__restrict__ lists) {
-    __shared__ uint32_t kb[2][SP_CHUNK];
+    __shared__ __align__(16) uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
     __shared__ uint16_t cnt[16][SP_NT];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
@@ -1148,7 +1165,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64
                                                        int32_t *__restrict__ out_count,
                                                        const int32_t *__restrict__ hot_list,
                                                        int32_t *__restrict__ hot_count) {
-    __shared__ uint32_t kb[2][SP_CHUNK];
+    __shared__ __align__(16) uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
     __shared__ uint16_t cnt[16][SP_NT];
     __shared__ float acc[SP_W];
@@ -1292,7 +1309,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max(SpRows rows, const int64_t *__
                                                  const int32_t *__restrict__ raw_arr,
                                                  int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count,
                                                  int32_t *__restrict__ hot_list, int32_t *__restrict__ hot_count) {
-    __shared__ uint32_t kb[2][SP_CHUNK];
+    __shared__ __align__(16) uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
     __shared__ uint32_t tie[SP_CHUNK];
     __shared__ uint16_t cnt[16][SP_NT];
