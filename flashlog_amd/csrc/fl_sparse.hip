@@ -780,6 +780,20 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
     __syncthreads();
     const uint32_t *sorted = sp_block_sort<SP_IPT>(kb[0], kb[1], 12, nbits, cnt, scan_lds);
     const int64_t *bb = base + rows.tile_base[r] * rows.NB + tl;
+    // first sorted position of every bucket present, in the sort's idle
+    // buffer when the buckets fit (else a binary search per item)
+    uint32_t *first = sorted == kb[0] ? kb[1] : kb[0];
+    const bool table = rows.NB <= SP_TILE;
+    if (table) {
+#pragma unroll 4
+        for (int j = 0; j < SP_IPT; ++j) {
+            const int p = j * SP_NT + t;
+            if (p >= c) continue;
+            const uint32_t bk = sorted[p] >> 12;
+            if (bk != 0xFFFFFu && (p == 0 || (sorted[p - 1] >> 12) != bk)) first[bk] = (uint32_t)p;
+        }
+        __syncthreads();
+    }
 #pragma unroll 4
     for (int j = 0; j < SP_IPT; ++j) {
         const int p = j * SP_NT + t;  // striped: consecutive threads write consecutive slots
@@ -787,12 +801,17 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         const uint32_t key = sorted[p];
         const uint32_t bk = key >> 12;
         if (bk == 0xFFFFFu) continue;  // hole
-        // first sorted position of this bucket (binary search in LDS)
-        int lo = 0, hi = p;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if ((sorted[mid] >> 12) < bk) lo = mid + 1;
-            else hi = mid;
+        int lo;
+        if (table) {
+            lo = (int)first[bk];
+        } else {
+            lo = 0;
+            int hi = p;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if ((sorted[mid] >> 12) < bk) lo = mid + 1;
+                else hi = mid;
+            }
         }
         const int idx = (int)(key & 4095u);
         const int64_t q = bb[(int64_t)bk * nt] + (p - lo);
