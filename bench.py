@@ -87,7 +87,7 @@ def c2_admitted(wv, cnt, K):
     return out
 
 
-def hop_pull_bytes(Ap, w, csr, R, K):
+def hop_pull_bytes(Ap, w, csr, R, K, out_bytes=8):
     """Algorithmic HBM bytes of one k_pull launch (the propagation kernel):
     the two graph outputs (8 B per state cell) plus, per direction and active
     source, its row pointers (8 B), group records (10 B each) and the column
@@ -98,7 +98,7 @@ def hop_pull_bytes(Ap, w, csr, R, K):
     BL, E = Ap.shape
     nz = Ap != 0
     act = np.nonzero(nz.any(0))[0]
-    total = 8 * BL * E
+    total = out_bytes * BL * E
     for (gptr, grel, gcount, off) in ((csr[8], csr[9], csr[11], 0), (csr[12], csr[13], csr[15], R)):
         g0 = gptr[act].astype(np.int64)
         g1 = gptr[act + 1].astype(np.int64)
@@ -135,6 +135,8 @@ def main():
         copy_calibration(args.copy_mb)
     if args.sparse or args.config == 5:
         return main_sparse(args)
+    if args.config == 4:
+        return main_c4(args)
     cfg = synth.CONFIGS[args.config]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -230,6 +232,191 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+
+
+def main_c4(args):
+    """C4: mmDRUM on the dense GPU path, 123k
+    entities, 37 relations, 1.08M triples with Zipf(1.2) hubs, batch 32,
+    N = 3, T = 3, c1 = 1000, c2 = 400, forward and backward: per hop
+    dense_csr_max, the elementwise max of its three outputs and the row
+    normalization, then the max over channels (src/model_mmDRUM_kernel.py:
+    101-126), the model's log loss (src/utils.py:28-34) and the backward
+    pass to the attention.  Plus the evaluation's filtered ranking of 5,000
+    queries over all entities (src/main.py:468-512) by
+    dense_filtered_ranks_cuda, reported in "ranking"."""
+    import numpy as np
+    import torch
+    from flashlog_amd import _lib, synth
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+
+    cfg = synth.CONFIGS[4]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    h, r, t, E, R = synth.make_graph(4)
+    n = 2 * R + 1
+    B, L, T = cfg.batch, cfg.channels, cfg.hops
+    K, c1 = cfg.c2 // 2, cfg.c1
+    M = h.shape[0]
+    csr = fk.build_csr_structure(*(torch.from_numpy(a).to(dev) for a in (h, t, r)), E)
+    masks = fk.prepare_csr_masks(csr, torch.ones(M, dtype=torch.bool, device=dev))
+    rng = np.random.Generator(np.random.PCG64(1234 + 4))
+    src, qrel, tgt = synth.make_queries(h, r, t, R, B, rng)
+    W = torch.from_numpy(synth.make_attention(B, L, n, T, rng)).to(dev).requires_grad_(True)
+    x0 = torch.zeros(B, L, E, dtype=torch.float32, device=dev)
+    x0[torch.arange(B, device=dev), :, torch.from_numpy(src).to(dev)] = 1.0
+    tgt_t = torch.from_numpy(tgt).to(dev)
+
+    def step(capture=None):
+        x = x0
+        for hop in range(T):
+            if capture is not None:
+                capture.append((fk._dense_topc_state(x.detach(), c1), W[hop].detach()))
+            s_i, s_h, s_t = fk.dense_csr_max(x, W[hop], csr, None, R, use_topk=True, topk_nodes=c1,
+                                             topk_edges=K, prepared_masks=masks)
+            s = torch.max(torch.stack([s_i, s_h, s_t], dim=0), dim=0).values
+            x = s / s.sum(dim=-1, keepdim=True).clamp(1e-7)
+        p = x.max(dim=1)[0]
+        loss = -torch.log(torch.clamp(p[torch.arange(B, device=dev), tgt_t], min=1e-7)).mean()
+        W.grad = None
+        loss.backward()
+        return loss
+
+    kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull_max", "k_seg_max", "k_heavy_max",
+               "k_max_bwd", "k_bwd_identity"]
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    print("timed %d mmDRUM steps: %.3f ms/step" % (args.steps, ms_step), file=sys.stderr, flush=True)
+    _lib.prof_enable(True)
+    for _ in range(max(args.profile_steps, 1)):
+        step()
+    torch.cuda.synchronize()
+    prof = {k: _lib.prof_read(k) for k in kernels}
+    _lib.prof_enable(False)
+    per_launch = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in prof.items()}
+    print("per-launch ms: " + json.dumps({k: round(v, 5) for k, v in per_launch.items()}), file=sys.stderr,
+          flush=True)
+    cap = []
+    step(capture=cap)
+    csr_np = [c.cpu().numpy() for c in csr]
+    # the max gather: k_pull_max (light destinations) + k_seg_max / k_heavy_max (hub destinations);
+    # outputs 24 B per (row, destination): two fp32 values and two int64 winning positions
+    hop_bytes = [hop_pull_bytes(a.reshape(B * L, E).cpu().numpy(), w.reshape(B * L, n).cpu().numpy(), csr_np, R, K,
+                                out_bytes=24) for a, w in cap]
+    gather_ms = per_launch["k_pull_max"] + per_launch["k_seg_max"] + per_launch["k_heavy_max"]
+    bytes_per_hop = float(np.mean(hop_bytes))
+    achieved = bytes_per_hop / (gather_ms * 1e-3) / 1e9 if gather_ms > 0 else 0.0
+
+    # filtered ranking: 5,000 queries over all entities; filter = each query's known answers + target
+    QN = 5000
+    qrng = np.random.Generator(np.random.PCG64(4321))
+    scores = (qrng.integers(0, 1 << 12, (QN, E)) / float(1 << 12)).astype(np.float32)  # ties on purpose
+    qt = qrng.integers(0, E, QN)
+    nf = 20 * QN
+    fb, fe = qrng.integers(0, QN, nf), qrng.integers(0, E, nf)
+    st_d = torch.from_numpy(scores).to(dev)
+    qt_d = torch.from_numpy(qt).to(dev)
+    fidx = (torch.from_numpy(fb).to(dev), torch.from_numpy(fe).to(dev))
+    for _ in range(2):
+        fk.dense_filtered_ranks_cuda(st_d, qt_d, fidx, True)
+    torch.cuda.synchronize()
+    _lib.prof_enable(True)
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    r0.record()
+    for _ in range(10):
+        fk.dense_filtered_ranks_cuda(st_d, qt_d, fidx, True)
+    r1.record()
+    torch.cuda.synchronize()
+    rk = _lib.prof_read("k_dense_rank")
+    _lib.prof_enable(False)
+    rank_ms = r0.elapsed_time(r1) / 10
+    rank_kernel_ms = rk[0] / rk[1] if rk[1] else 0.0
+    rank_bytes = 4.0 * QN * E + 8.0 * QN + 16.0 * (nf + QN)
+    cpu_rank = None
+    if args.cpu_seconds > 0:
+        from oracle import oracle as O
+        Qs = 500
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            O.dense_filtered_ranks(scores[:Qs], qt[:Qs], fb[fb < Qs], fe[fb < Qs], True)
+            reps += 1
+            if time.perf_counter() - t0 >= min(args.cpu_seconds, 5.0):
+                break
+        el = time.perf_counter() - t0
+        cpu_rank = {"value": reps * Qs / el, "unit": "queries/s", "cores": 1, "kind": "port",
+                    "sample": "%d rankings of %d queries over %d entities (numpy restatement of src/main.py:468-512)"
+                              % (reps, Qs, E)}
+    cpu = cpu_baseline_c4(args, cap, csr_np, B, L, E, R, K) if args.cpu_seconds > 0 else None
+    result = {
+        "metric": "queries/sec for L=3 propagation + % of HBM roofline; top-k select ms",
+        "value": B / (ms_step * 1e-3),
+        "unit": "queries/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded C4 graph, flashlog_amd/synth.py; random attention in place of the model's LSTM)",
+        "config": {"workload": "C4 mmDRUM dense max step (forward + backward): E=%d, R=%d, M=%d, B=%d, N=%d, T=%d, "
+                               "c1=%d, c2=%d" % (E, R, M, B, L, T, c1, cfg.c2),
+                   "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2},
+        "topk_select_ms": {"c1_per_hop": per_launch["k_topc_rows"], "c2_per_hop": per_launch["k_c2_hard"]},
+        "kernel_ms_per_launch": per_launch,
+        "roofline": {"kernel": "k_pull_max+k_seg_max+k_heavy_max", "bound": "hbm", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "algorithmic_bytes_per_launch": bytes_per_hop, "traffic": None},
+        "cpu_baseline": cpu,
+        "ranking": {"queries": QN, "entities": E, "filter_entries": nf, "ms": rank_ms,
+                    "queries_per_s": QN / (rank_ms * 1e-3),
+                    "roofline": {"kernel": "k_dense_rank", "bound": "hbm",
+                                 "achieved": rank_bytes / (rank_kernel_ms * 1e-3) / 1e9 if rank_kernel_ms else 0.0,
+                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                 "frac": rank_bytes / (rank_kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+                                 if rank_kernel_ms else 0.0,
+                                 "algorithmic_bytes_per_launch": rank_bytes},
+                    "cpu_baseline": cpu_rank},
+    }
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_c4(args, cap, csr_np, B, L, E, R, K):
+    """mmDRUM's dense max has no CPU path in the reference (GPU only,
+    flashlog_kernel.py:1666-1688), so the CPU figure is the C restatement of
+    the op (oracle: or_dense_max_forward / or_dense_max_backward, one thread)
+    forward and backward on each hop's pruned input for the first Bs queries
+    (rows are independent); the model's elementwise ops are not included."""
+    import numpy as np
+    from oracle import oracle as O
+    n = 2 * R + 1
+    Bs = min(4, B)
+    ones = (np.ones(csr_np[1].shape[0], np.float32), np.ones(csr_np[5].shape[0], np.float32))
+    hops = [(a.reshape(B * L, E)[:Bs * L].cpu().numpy(), w.reshape(B * L, n)[:Bs * L].cpu().numpy())
+            for a, w in cap]
+    g = np.ones((Bs * L, E), np.float32)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for A, w in hops:
+            o = O.dense_max_forward(A, w, csr_np, ones, R, False, K)
+            O.dense_max_backward(g, g, g, o[3], o[4], A, w, csr_np, ones, R, False, K)
+        reps += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    el = time.perf_counter() - t0
+    return {"value": reps * Bs / el, "unit": "queries/s", "cores": 1, "kind": "port",
+            "sample": "%d x %d hops forward + backward of the dense max op for %d queries (oracle C restatement; "
+                      "the reference has no CPU max path) in %.1f s, 1 thread" % (reps, len(hops), Bs, el)}
 
 
 SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_race_select", "k_fill_from",

@@ -155,6 +155,8 @@ _SIGS = {
     "fl_rule_finalize": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 3 +
                          [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
     "fl_filtered_ranks_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int]),
+    "fl_dense_filtered_ranks": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3 + [ctypes.c_int,
+                                                                                            ctypes.c_void_p]),
     "fl_filtered_ranks": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int] + [ctypes.c_void_p] * 2 +
                           [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                                                   ctypes.c_size_t]),

@@ -177,3 +177,89 @@ int fl_filtered_ranks(void *stream, const int64_t *idx_b, const int64_t *idx_e, 
 }
 
 }  // extern "C"
+
+namespace fl {
+
+// Dense filtered ranks (src/main.py:468-512, the ranks of
+// calculate_hits_full_with_filter_indices): one workgroup per query row b
+// of a dense score matrix [B, E]; truth = state[b, target_b];
+//   greater = #{e : s > truth} - #{e in filter_b : s > truth}
+//   equal   = #{e : s == truth} - #{e in filter_b : s == truth}
+//   use_eql: rank = greater + ((equal + 1) + 1) / 2;  else greater + 1
+// with the reference's fp32 arithmetic on exact integer counts.  The row is
+// read once (coalesced, HBM-bound); filter_b is the row's range of the
+// sorted unique keys b*E + e.
+constexpr int DR_NT = 256;
+
+__global__ __launch_bounds__(DR_NT) void k_dense_rank(const float *__restrict__ state, int64_t E,
+                                                      const int64_t *__restrict__ targets,
+                                                      const int64_t *__restrict__ filter_keys, int64_t n_filter,
+                                                      int use_eql, float *__restrict__ ranks) {
+    __shared__ uint32_t red[4][DR_NT / FL_WAVE];
+    const int64_t b = blockIdx.x;
+    const int t = threadIdx.x;
+    const float *row = state + b * E;
+    const float truth = row[targets[b]];
+    uint32_t gt = 0, eq = 0;
+    for (int64_t e = t; e < E; e += DR_NT) {
+        const float x = row[e];
+        gt += x > truth;
+        eq += x == truth;
+    }
+    uint32_t fgt = 0, feq = 0;
+    if (n_filter > 0) {
+        const int64_t lo = rk_lower_bound(filter_keys, n_filter, b * E);
+        const int64_t hi = rk_lower_bound(filter_keys, n_filter, (b + 1) * E);
+        for (int64_t k = lo + t; k < hi; k += DR_NT) {
+            const float x = row[filter_keys[k] - b * E];
+            fgt += x > truth;
+            feq += x == truth;
+        }
+    }
+    gt = (uint32_t)fl_wave_sum_i32((int)gt);
+    eq = (uint32_t)fl_wave_sum_i32((int)eq);
+    fgt = (uint32_t)fl_wave_sum_i32((int)fgt);
+    feq = (uint32_t)fl_wave_sum_i32((int)feq);
+    const int w = t / FL_WAVE;
+    if (fl_lane() == 0) {
+        red[0][w] = gt;
+        red[1][w] = eq;
+        red[2][w] = fgt;
+        red[3][w] = feq;
+    }
+    __syncthreads();
+    if (t == 0) {
+        uint32_t a[4] = {0, 0, 0, 0};
+        for (int q = 0; q < 4; ++q)
+            for (int i = 0; i < DR_NT / FL_WAVE; ++i) a[q] += red[q][i];
+        // the reference's float counters: sum().float(), then scatter_add of 1.0f
+        float greater = (float)a[0];
+        if (n_filter > 0) greater = greater - (float)a[2];
+        if (use_eql) {
+            float equal = (float)a[1];
+            if (n_filter > 0) equal = equal - (float)a[3];
+            equal = equal + 1.0f;
+            ranks[b] = greater + (equal + 1.0f) / 2.0f;
+        } else {
+            ranks[b] = greater + 1.0f;
+        }
+    }
+}
+
+}  // namespace fl
+
+extern "C" {
+
+int fl_dense_filtered_ranks(void *stream, const float *state, const int64_t *targets, const int64_t *filter_keys,
+                            int64_t n_filter, int64_t B, int64_t E, int use_eql, float *ranks) {
+    if (B < 0 || E <= 0 || n_filter < 0) return fl::fl_fail(FL_ERR_ARG, "dense_filtered_ranks: bad sizes");
+    if (B == 0) return FL_OK;
+    if (B > INT64_MAX / E) return fl::fl_fail(FL_ERR_ARG, "dense_filtered_ranks: B*E overflows int64");
+    if (!state || !targets || !ranks || (n_filter > 0 && !filter_keys))
+        return fl::fl_fail(FL_ERR_ARG, "dense_filtered_ranks: null pointer");
+    FL_LAUNCH("k_dense_rank", fl::k_dense_rank, dim3((unsigned)B), dim3(fl::DR_NT), 0, (hipStream_t)stream, state, E,
+              targets, filter_keys, n_filter, use_eql, ranks);
+    return fl::fl_check_launch("dense_filtered_ranks");
+}
+
+}  // extern "C"

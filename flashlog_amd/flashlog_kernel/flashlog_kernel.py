@@ -708,6 +708,42 @@ def sparse2d_filtered_ranks_cuda(idx_b, idx_e, values, targets, filter_keys, B, 
     return ranks
 
 
+def dense_filtered_ranks_cuda(state, targets, filter_indices=None, use_eql=False):
+    """Filtered tie-aware ranks of each query's target over a dense [B, E]
+    score matrix: the rank computation of the evaluation driver's
+    calculate_hits_full_with_filter_indices (src/main.py:468-512), where it
+    is a chain of torch ops.  filter_indices: (batch, entity) index tensors
+    of the known answers, or None for no filtering; as in the reference, the
+    targets join the filter and duplicate keys count once.  Returns float32
+    ranks [B] (greater + 1, or greater + (equal + 1) / 2 with use_eql,
+    equal already counting the target once)."""
+    _require_cuda(state, targets)
+    if state.dim() != 2:
+        raise ValueError("dense_filtered_ranks_cuda: state must be [B, E]")
+    B, E = state.shape
+    state = state.float().contiguous()
+    targets = targets.long().contiguous()
+    if targets.numel() != B:
+        raise ValueError("dense_filtered_ranks_cuda: one target per query")
+    if B and (int(targets.min()) < 0 or int(targets.max()) >= E):
+        raise ValueError("dense_filtered_ranks_cuda: target out of range")
+    keys = None
+    if filter_indices is not None:
+        fb, fe = filter_indices
+        batch_idx = torch.arange(B, device=state.device, dtype=torch.long)
+        fb = torch.cat([fb.to(state.device).long(), batch_idx])
+        fe = torch.cat([fe.to(state.device).long(), targets])
+        if fb.numel() and (int(fb.min()) < 0 or int(fb.max()) >= B or int(fe.min()) < 0 or int(fe.max()) >= E):
+            raise ValueError("dense_filtered_ranks_cuda: filter index out of range")
+        keys = torch.unique(fb * E + fe)
+    ranks = torch.empty(B, dtype=torch.float32, device=state.device)
+    check(_lib.lib().fl_dense_filtered_ranks(_stream(state), ptr(state), ptr(targets),
+                                             ptr(keys) if keys is not None else None,
+                                             keys.numel() if keys is not None else 0, B, E,
+                                             1 if use_eql else 0, ptr(ranks)), "dense_filtered_ranks_cuda")
+    return ranks
+
+
 def vectorized_operation_sparse3d_fixed_relation(sp_state, operators, csr_struct, r_size):
     """Advance sparse rule levels through one fixed relation per level
     (flashlog_kernel.py:182-210).  ``operators`` is shaped ``[B, L]`` with the

@@ -399,6 +399,18 @@ int fl_rule_finalize(void *stream, const float *dense, int64_t K, int64_t B,
 
 /* ---- evaluation --------------------------------------------------------- */
 
+/* Replaces the rank computation of calculate_hits_full_with_filter_indices
+ * (src/main.py:468-512, torch ops in the reference): state [B, E] fp32
+ * dense scores, targets [B]; filter_keys (n_filter >= 0) the sorted unique
+ * keys b*E + e of the filter with every (b, targets[b]) included, or none
+ * (n_filter = 0: no filtering, as filter_indices=None).  ranks[b] =
+ * greater + 1, or with use_eql greater + ((equal + 1) + 1) / 2, where
+ * greater / equal count the unfiltered entities scoring above / exactly at
+ * state[b, targets[b]] (fp32, exact below 2^24). */
+int fl_dense_filtered_ranks(void *stream, const float *state, const int64_t *targets,
+                            const int64_t *filter_keys, int64_t n_filter, int64_t B,
+                            int64_t E, int use_eql, float *ranks);
+
 /* Workspace for fl_filtered_ranks (values_f64: 1 for double scores). */
 size_t fl_filtered_ranks_workspace_bytes(int64_t B, int values_f64);
 

@@ -730,3 +730,30 @@ def ground(att, R, head, folds, csr, walks, topk_edges, mask_query_head, seed, b
     fold = np.concatenate([np.full(len(f), i, np.int64) for i, f in enumerate(folds)]) if folds else src
     keys, pos = ground_walks(att, R, head, src, idx, csr, walks, topk_edges, mask_query_head, seed, temperature)
     return ground_aggregate(keys, pos, fold, len(folds), head, budgets)
+
+
+def dense_filtered_ranks(state, targets, filter_b=None, filter_e=None, use_eql=False):
+    """Ranks of calculate_hits_full_with_filter_indices (src/main.py:468-512)
+    in its float32 arithmetic: greater / equal over the row, minus the
+    filtered entities' (the filter with the targets appended, unique keys)."""
+    state = np.asarray(state, np.float32)
+    B, E = state.shape
+    targets = np.asarray(targets, np.int64)
+    truth = state[np.arange(B), targets]
+    greater = (state > truth[:, None]).sum(1).astype(np.float32)
+    equal = (state == truth[:, None]).sum(1).astype(np.float32)
+    if filter_b is not None:
+        keys = np.unique(np.concatenate([np.asarray(filter_b, np.int64) * E + np.asarray(filter_e, np.int64),
+                                         np.arange(B) * E + targets]))
+        fb, fe = keys // E, keys % E
+        fs = state[fb, fe]
+        fg = np.zeros(B, np.float32)
+        fq = np.zeros(B, np.float32)
+        np.add.at(fg, fb, (fs > truth[fb]).astype(np.float32))
+        np.add.at(fq, fb, (fs == truth[fb]).astype(np.float32))
+        greater = (greater - fg).astype(np.float32)
+        equal = (equal - fq).astype(np.float32)
+    if use_eql:
+        equal = (equal + np.float32(1)).astype(np.float32)
+        return (greater + (equal + np.float32(1)) / np.float32(2)).astype(np.float32)
+    return (greater + np.float32(1)).astype(np.float32)

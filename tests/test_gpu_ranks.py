@@ -111,3 +111,40 @@ def test_filtered_ranks_rejects_cpu_and_half():
     with pytest.raises(RuntimeError):
         fk.sparse2d_filtered_ranks_cuda(z.to(d), z.to(d), torch.zeros(1, dtype=torch.float16, device=d), z.to(d),
                                         z.to(d), 1, 4)
+
+
+@pytest.mark.parametrize("use_eql", [False, True])
+@pytest.mark.parametrize("filtered", [False, True])
+@pytest.mark.parametrize("E", [777, 5000])
+def test_dense_filtered_ranks_bitexact(use_eql, filtered, E):
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+    rng = np.random.default_rng(E + 2 * use_eql + filtered)
+    B = 64
+    state = (rng.integers(0, 9, (B, E)) / 8.0).astype(np.float32)  # heavy ties
+    state[3] = 0.0  # a row of zeros: everything ties with the target
+    targets = rng.integers(0, E, B)
+    fb = fe = None
+    fidx = None
+    if filtered:
+        n = 3000
+        fb = rng.integers(0, B, n)
+        fe = rng.integers(0, E, n)
+        fidx = (torch.from_numpy(fb).cuda(), torch.from_numpy(fe).cuda())
+    got = fk.dense_filtered_ranks_cuda(torch.from_numpy(state).cuda(), torch.from_numpy(targets).cuda(), fidx,
+                                       use_eql)
+    want = O.dense_filtered_ranks(state, targets, fb, fe, use_eql)
+    assert got.dtype == torch.float32
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
+def test_dense_filtered_ranks_checks():
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+    s = torch.zeros(2, 10, device="cuda")
+    with pytest.raises(ValueError):
+        fk.dense_filtered_ranks_cuda(s, torch.tensor([0, 10], device="cuda"))
+    with pytest.raises(ValueError):
+        fk.dense_filtered_ranks_cuda(s, torch.tensor([0, 1], device="cuda"),
+                                     (torch.tensor([2], device="cuda"), torch.tensor([0], device="cuda")))
+    out = fk.dense_filtered_ranks_cuda(torch.zeros(0, 10, device="cuda"), torch.zeros(0, dtype=torch.long,
+                                                                                      device="cuda"))
+    assert out.shape == (0,)
