@@ -281,8 +281,8 @@ def main_c4(args):
         loss.backward()
         return loss
 
-    kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull_max", "k_seg_max", "k_heavy_max",
-               "k_max_bwd", "k_bwd_identity"]
+    kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull_max", "k_seg_max", "k_sup_max",
+               "k_heavy_max", "k_max_bwd", "k_bwd_identity"]
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -306,11 +306,11 @@ def main_c4(args):
     cap = []
     step(capture=cap)
     csr_np = [c.cpu().numpy() for c in csr]
-    # the max gather: k_pull_max (light destinations) + k_seg_max / k_heavy_max (hub destinations);
+    # the max gather: k_pull_max (light destinations) + k_seg_max / k_sup_max / k_heavy_max (hubs);
     # outputs 24 B per (row, destination): two fp32 values and two int64 winning positions
     hop_bytes = [hop_pull_bytes(a.reshape(B * L, E).cpu().numpy(), w.reshape(B * L, n).cpu().numpy(), csr_np, R, K,
                                 out_bytes=24) for a, w in cap]
-    gather_ms = per_launch["k_pull_max"] + per_launch["k_seg_max"] + per_launch["k_heavy_max"]
+    gather_ms = per_launch["k_pull_max"] + per_launch["k_seg_max"] + per_launch["k_sup_max"] + per_launch["k_heavy_max"]
     bytes_per_hop = float(np.mean(hop_bytes))
     achieved = bytes_per_hop / (gather_ms * 1e-3) / 1e9 if gather_ms > 0 else 0.0
 
@@ -373,7 +373,7 @@ def main_c4(args):
                    "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2},
         "topk_select_ms": {"c1_per_hop": per_launch["k_topc_rows"], "c2_per_hop": per_launch["k_c2_hard"]},
         "kernel_ms_per_launch": per_launch,
-        "roofline": {"kernel": "k_pull_max+k_seg_max+k_heavy_max", "bound": "hbm", "achieved": achieved,
+        "roofline": {"kernel": "k_pull_max+k_seg_max+k_sup_max+k_heavy_max", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": bytes_per_hop, "traffic": None},
         "cpu_baseline": cpu,

@@ -711,7 +711,32 @@ __global__ __launch_bounds__(PULL_NT) void k_seg_max(fl_side ori, fl_side inv, c
     (dir ? sb_inv : sb_ori)[qq] = walk_slots_max(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT);
 }
 
-// Heavy destinations, step 2: thread per (heavy destination, row).
+// Heavy destinations, step 2: thread per (supersegment, row): the maximum of
+// its (at most FL_SUP) segments' maxima, stored in place of its first
+// segment's (every segment belongs to one supersegment).
+__global__ __launch_bounds__(PULL_NT) void k_sup_max(fl_side ori, fl_side inv, int64_t BL,
+                                                     uint64_t *__restrict__ sb_ori, uint64_t *__restrict__ sb_inv) {
+    const int64_t q = (int64_t)blockIdx.x * PULL_NT + threadIdx.x;
+    const int64_t nq_ori = ori.nsup * BL;
+    if (q >= nq_ori + inv.nsup * BL) return;
+    const int dir = q >= nq_ori;
+    const int64_t qq = dir ? q - nq_ori : q;
+    const int64_t sup = qq / BL, bl = qq - sup * BL;
+    const fl_side &s = dir ? inv : ori;
+    uint64_t *sb = dir ? sb_inv : sb_ori;
+    const int64_t seg0 = s.sup_seg0[sup];
+    const int64_t end = s.heavy_seg_ptr[(int64_t)s.sup_h[sup] + 1];
+    const int64_t seg1 = seg0 + FL_SUP < end ? seg0 + FL_SUP : end;
+    uint64_t best = 0;
+    for (int64_t g = seg0; g < seg1; ++g) {
+        const uint64_t k = sb[g * BL + bl];
+        best = k > best ? k : best;
+    }
+    sb[seg0 * BL + bl] = best;
+}
+
+// Heavy destinations, step 3: thread per (heavy destination, row): the
+// maximum over its supersegments (8 loads in flight).
 __global__ __launch_bounds__(PULL_NT) void k_heavy_max(fl_side ori, fl_side inv, int64_t BL, int64_t E,
                                                        const uint64_t *__restrict__ sb_ori,
                                                        const uint64_t *__restrict__ sb_inv,
@@ -725,11 +750,23 @@ __global__ __launch_bounds__(PULL_NT) void k_heavy_max(fl_side ori, fl_side inv,
     const int64_t h = qq / BL, bl = qq - h * BL;
     const fl_side &s = dir ? inv : ori;
     const uint64_t *sb = dir ? sb_inv : sb_ori;
-    uint64_t best = 0;
-    for (int64_t g = s.heavy_seg_ptr[h]; g < s.heavy_seg_ptr[h + 1]; ++g) {
-        const uint64_t k = sb[g * BL + bl];
-        best = k > best ? k : best;
+    const int64_t u0 = s.heavy_sup_ptr[h], u1 = s.heavy_sup_ptr[h + 1];
+    uint64_t b8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t u = u0;
+    for (; u + 8 <= u1; u += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint64_t k = sb[(int64_t)s.sup_seg0[u + j] * BL + bl];
+            b8[j] = k > b8[j] ? k : b8[j];
+        }
     }
+    for (; u < u1; ++u) {
+        const uint64_t k = sb[(int64_t)s.sup_seg0[u] * BL + bl];
+        b8[0] = k > b8[0] ? k : b8[0];
+    }
+    uint64_t best = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) best = b8[j] > best ? b8[j] : best;
     const int64_t at = bl * E + s.heavy_dst[h];
     max_unpack(best, dir ? &out_inv[at] : &out_ori[at], dir ? &arg_inv[at] : &arg_ori[at]);
 }
@@ -1227,6 +1264,10 @@ int fl_dense_max_forward(void *stream, const fl_side *ori, const fl_side *inv, c
     if (nq_seg > 0) {
         FL_LAUNCH("k_seg_max", k_seg_max, dim3((unsigned)((nq_seg + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0, st,
                   *ori, *inv, w, BL, E, n, r_size, ws.bm, ws.pk, ws.cut, sb_ori, sb_inv);
+        const int64_t nq_sup = (ori->nsup + inv->nsup) * BL;
+        if (nq_sup > 0)
+            FL_LAUNCH("k_sup_max", k_sup_max, dim3((unsigned)((nq_sup + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0,
+                      st, *ori, *inv, BL, sb_ori, sb_inv);
         const int64_t nq_h = (ori->nheavy + inv->nheavy) * BL;
         FL_LAUNCH("k_heavy_max", k_heavy_max, dim3((unsigned)((nq_h + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0,
                   st, *ori, *inv, BL, E, sb_ori, sb_inv, out_ori, out_inv, arg_ori, arg_inv);

@@ -201,7 +201,21 @@ __global__ __launch_bounds__(DR_NT) void k_dense_rank(const float *__restrict__ 
     const float *row = state + b * E;
     const float truth = row[targets[b]];
     uint32_t gt = 0, eq = 0;
-    for (int64_t e = t; e < E; e += DR_NT) {
+    // 16-byte loads over the aligned middle of the row, scalars at its ends
+    const int64_t pre = ((4 - ((b * E) & 3)) & 3) < E ? ((4 - ((b * E) & 3)) & 3) : E;
+    const int64_t nvec = (E - pre) >> 2;
+    if (t < pre) {
+        const float x = row[t];
+        gt += x > truth;
+        eq += x == truth;
+    }
+    const float4 *v4 = reinterpret_cast<const float4 *>(row + pre);
+    for (int64_t k = t; k < nvec; k += DR_NT) {
+        const float4 x = v4[k];
+        gt += (x.x > truth) + (x.y > truth) + (x.z > truth) + (x.w > truth);
+        eq += (x.x == truth) + (x.y == truth) + (x.z == truth) + (x.w == truth);
+    }
+    for (int64_t e = pre + 4 * nvec + t; e < E; e += DR_NT) {
         const float x = row[e];
         gt += x > truth;
         eq += x == truth;

@@ -108,3 +108,28 @@ def test_dense_max_backward(K, wot_i):
     gw = wt.grad.reshape(BL, n).cpu().numpy()
     np.testing.assert_allclose(gA, gA_ref, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(gw, gw_ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("K", [0, 5])
+def test_dense_max_hub_destination(K):
+    """A destination receiving 70% of 60k edges (~1300 segments, ~80
+    supersegments: the per-supersegment pre-reduction and the unrolled
+    heavy loop), values and winning positions bit for bit."""
+    rng = np.random.default_rng(77 + K)
+    E, R, M = 20000, 5, 60000
+    h = rng.integers(0, E, M)
+    t = np.where(rng.random(M) < 0.7, 12345, rng.integers(0, E, M))
+    r = rng.integers(0, R, M)
+    csr = O.build_csr_structure(h, t, r, E)
+    n = 2 * R + 1
+    B, L = 2, 3
+    BL = B * L
+    A = sparse_state(BL, E, 3000, rng, ties=True)
+    w = attention(BL, n, rng)
+    _, masks = masks_for(csr, M, rng, drop=0.1)
+    kk = K if K > 0 else (1 << 60)
+    oi, oo, ov, ao, av = O.dense_max_forward(A, w, csr, masks, R, topk_edges=kk)
+    _, _, outs = _run_forward(A, w, csr, masks, R, K, False, B, L)
+    for name, o, rr in zip(("ind", "ori", "inv"), outs, (oi, oo, ov)):
+        assert np.array_equal(bits(o.reshape(BL, E).detach().cpu().numpy()), bits(rr)), name
+    assert np.any(oo[:, 12345] != 0)
