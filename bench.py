@@ -46,6 +46,8 @@ def parse():
     ap.add_argument("--profile-steps", type=int, default=10)
     ap.add_argument("--sparse", action="store_true",
                     help="the DRUM --sparse GPU path (default for --config 5)")
+    ap.add_argument("--grounding", action="store_true",
+                    help="soft grounding (rule extraction's walk sampler) on the C3 graph")
     ap.add_argument("--mode", choices=["train", "eval"], default="train",
                     help="--sparse step: a training step (sampled hops, loss, backward; the default, as "
                          "configs[4] is quoted forward and backward) or an evaluation pass")
@@ -133,6 +135,8 @@ def main():
 
     if args.copy_mb > 0:
         copy_calibration(args.copy_mb)
+    if args.grounding:
+        return main_grounding(args)
     if args.sparse or args.config == 5:
         return main_sparse(args)
     if args.config == 4:
@@ -417,6 +421,116 @@ def cpu_baseline_c4(args, cap, csr_np, B, L, E, R, K):
     return {"value": reps * Bs / el, "unit": "queries/s", "cores": 1, "kind": "port",
             "sample": "%d x %d hops forward + backward of the dense max op for %d queries (oracle C restatement; "
                       "the reference has no CPU max path) in %.1f s, 1 thread" % (reps, len(hops), Bs, el)}
+
+
+def main_grounding(args):
+    """Soft grounding (ground_head_batch_source_folds_sampled_capped_counts,
+    soft_grounding.cpp:898-1027) with the reference extraction's defaults
+    (rules/extract.py:385-427): a batch of 16 head relations, one fold of up
+    to 512 sources per head from sample_relation_sources_reservoir, 4096
+    walks per source, top-k 200 edges (c2 = 400), temperature 1, length caps
+    [64, 4096, 16384], seeds seed ^ (head * 0x9E3779B1); on the C3 graph
+    (14.5k entities, 237 relations, 272k triples) with random attention.
+    value = walks per second over the whole call (walks, counting and the
+    candidate rows returned on the host, as the reference returns them)."""
+    import numpy as np
+    import torch
+    from flashlog_amd import _lib, synth
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+    from flashlog_amd.flashlog_kernel.soft_grounding_kernel import soft_grounding_kernel as sg
+
+    cfg = synth.CONFIGS[3]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    h, r, t, E, R = synth.make_graph(3)
+    V = 2 * R + 1
+    csr = fk.build_csr_structure(*(torch.from_numpy(a) for a in (h, t, r)), E)
+    csr = tuple(c.cpu() for c in csr)
+    rng = np.random.Generator(np.random.PCG64(1234 + 3))
+    NH, SPF, WALKS, TOPK, CAPS, SEED = 16, 512, 4096, 200, [64, 4096, 16384], 1234
+    heads = [int(x) for x in rng.choice(2 * R, NH, replace=False)]
+    rels = np.array(sorted(set(hd % R for hd in heads)), np.int64)
+    # sources of a head: the reservoir of rows holding a group of its relation (inverse heads use the INV side)
+    picked = {}
+    for side, (gptr, grel) in enumerate(((csr[8], csr[9]), (csr[12], csr[13]))):
+        out, _ = sg.sample_relation_sources_reservoir(gptr, grel, torch.from_numpy(rels), SPF, SEED)
+        for i, rel in enumerate(rels):
+            picked[(side, int(rel))] = [int(x) for x in out[i].tolist() if x >= 0]
+    folds = [[np.array(picked[(hd // R, hd % R)] or [0], np.int64)] for hd in heads]
+    logits = rng.standard_normal((NH, 3, 3, V)).astype(np.float32)
+    att = np.exp(logits - logits.max(-1, keepdims=True))
+    att = (att / att.sum(-1, keepdims=True)).astype(np.float32)
+    seeds = [SEED ^ (hd * 0x9E3779B1) for hd in heads]
+    walks_total = sum(len(f[0]) for f in folds) * WALKS
+    att_t = torch.from_numpy(att)
+
+    def call():
+        return sg.ground_head_batch_source_folds_sampled_capped_counts(att_t, heads, R, folds, csr, WALKS, TOPK, False,
+                                                                       seeds, 500000, 16, CAPS)
+
+    for _ in range(max(args.warmup, 1)):
+        call()
+    torch.cuda.synchronize()
+    reps = max(1, min(args.steps, 10))
+    _lib.prof_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        cands, raw, _ = call()
+    torch.cuda.synchronize()
+    el = (time.perf_counter() - t0) / reps
+    kn = ["k_gr_walk", "k_ct_flags", "k_ct_accum", "k_ct_capkey", "k_ct_keep", "k_ct_gather", "k_ct_emit"]
+    prof = {k: _lib.prof_read(k) for k in kn}
+    _lib.prof_enable(False)
+    per_call = {k: v[0] / reps for k, v in prof.items()}
+    print("grounding: %.1f ms per call, %d walks; kernel ms per call %s"
+          % (el * 1e3, walks_total, json.dumps({k: round(v, 3) for k, v in per_call.items()})),
+          file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_seconds > 0:
+        sys.path.insert(0, os.path.join(ROOT, "oracle", "_ref"))
+        try:
+            import flashlog_grounding_ref as ref
+        except ImportError:
+            ref = None
+        if ref is not None:
+            threads = min(16, os.cpu_count() or 1)
+            nh = 2  # bounded sample: the first heads of the batch
+            tens = [csr[i] for i in (1, 5, 8, 9, 10, 11, 12, 13, 14, 15)]
+            tf = [[torch.from_numpy(f[0])] for f in folds[:nh]]
+            t1 = time.perf_counter()
+            n = 0
+            while True:
+                ref.ground_head_batch_source_folds_sampled_capped_counts(
+                    att_t[:nh].contiguous(), heads[:nh], R, tf, *tens, WALKS, TOPK, False, seeds[:nh], 500000,
+                    threads, CAPS)
+                n += 1
+                if time.perf_counter() - t1 >= args.cpu_seconds:
+                    break
+            cel = time.perf_counter() - t1
+            cwalks = sum(len(f[0]) for f in folds[:nh]) * WALKS
+            cpu = {"value": n * cwalks / cel, "unit": "walks/s", "cores": threads, "kind": "reference",
+                   "sample": "%d calls of %d heads x %d walks (soft_grounding.cpp built in oracle/_ref, OpenMP) in "
+                             "%.1f s, %d threads" % (n, nh, cwalks, cel, threads)}
+    result = {
+        "metric": "soft grounding walks/sec (rule extraction sampler)",
+        "value": walks_total / el,
+        "unit": "walks/s",
+        "n_gpus": 1,
+        "steps": reps,
+        "warmup": max(args.warmup, 1),
+        "ms_per_step": el * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64/f64 (mt19937_64, double masses)",
+        "data": "synthetic (seeded C3 graph, flashlog_amd/synth.py; random attention)",
+        "config": {"workload": "soft grounding, C3 graph: %d heads x <=%d sources x %d walks, top-k %d, caps %s"
+                               % (NH, SPF, WALKS, TOPK, CAPS)},
+        "kernel_ms_per_call": per_call,
+        "roofline": None,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
 
 
 SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_race_select", "k_fill_from",

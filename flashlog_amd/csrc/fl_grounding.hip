@@ -106,7 +106,7 @@ __device__ __forceinline__ double gr_canonical(uint64_t *mt, int &idx) {
 
 // std::uniform_int_distribution over [0, range) with a 64-bit engine:
 // Lemire's nearly divisionless method with the 128-bit product.
-__device__ uint64_t gr_below(uint64_t *mt, int &idx, uint64_t range) {
+__device__ __forceinline__ uint64_t gr_below(uint64_t *mt, int &idx, uint64_t range) {
     uint64_t x = mt_next(mt, idx);
     uint64_t hi = __umul64hi(x, range), lo = x * range;
     if (lo < range) {
@@ -157,7 +157,7 @@ struct GrOpts {
     double mass;    // register mode; cumulative mass after gr_cumulate
 };
 
-__device__ GrOpts gr_side_reg(const GrSide &s, int32_t off, int64_t g0, int G, const float *w, int32_t excluded,
+__device__ __forceinline__ GrOpts gr_side_reg(const GrSide &s, int32_t off, int64_t g0, int G, const float *w, int32_t excluded,
                               int64_t topk, double temp) {
     const int lane = fl_lane();
     uint64_t key = ~0ull;
@@ -203,9 +203,101 @@ struct GrScratch {
     double *omass;
 };
 
+// Options of a side of up to 64*RR groups (RR keys per lane, element
+// i = r*64 + lane): the same bitonic network as the scratch sort, with
+// compare-exchanges inside a lane for strides >= 64 and across lanes
+// below; keys are distinct (the operator is in the low bits), so the order
+// is the same.  Options are written to the scratch lists at o; returns n.
+template <int RR>
+__device__ __forceinline__ int gr_side_regsort(const GrSide &s, int32_t off, int64_t g0, int64_t G, const float *w,
+                                               int32_t excluded, int64_t topk, double temp, const GrScratch &sc,
+                                               int o) {
+    const int lane = fl_lane();
+    uint64_t key[RR];
+    int32_t grp[RR];
+#pragma unroll
+    for (int r = 0; r < RR; ++r) {
+        const int64_t i = (int64_t)r * FL_WAVE + lane;
+        key[r] = ~0ull;
+        grp[r] = -1;
+        if (i < G) {
+            const int32_t g = (int32_t)(g0 + i);
+            const int32_t op = (int32_t)s.rel[g] + off;
+            const float wv = w[op];
+            if (op != excluded && wv > 0.0f && s.count[g] > 0) key[r] = gr_key(wv, op);
+            grp[r] = g;
+        }
+    }
+    constexpr int LOGP = RR == 2 ? 7 : RR == 4 ? 8 : 9;
+    static_assert((1 << LOGP) == RR * FL_WAVE, "RR is 2, 4 or 8");
+#pragma unroll
+    for (int lk = 1; lk <= LOGP; ++lk) {
+        const int k = 1 << lk;
+#pragma unroll
+        for (int lj = lk - 1; lj >= 0; --lj) {
+            const int j = 1 << lj;
+            if (j >= FL_WAVE) {
+                const int jr = j / FL_WAVE;
+#pragma unroll
+                for (int r = 0; r < RR; ++r) {
+                    const int pr = r ^ jr;
+                    if (pr > r) {
+                        const bool up = (((r * FL_WAVE + lane) & k) == 0);
+                        if (up ? (key[r] > key[pr]) : (key[r] < key[pr])) {
+                            const uint64_t tk = key[r];
+                            key[r] = key[pr];
+                            key[pr] = tk;
+                            const int32_t tg = grp[r];
+                            grp[r] = grp[pr];
+                            grp[pr] = tg;
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < RR; ++r) {
+                    const uint64_t ok = __shfl_xor(key[r], j, FL_WAVE);
+                    const int32_t og = __shfl_xor(grp[r], j, FL_WAVE);
+                    const bool up = (((r * FL_WAVE + lane) & k) == 0), lower = (lane & j) == 0;
+                    if ((lower == up) ? (ok < key[r]) : (ok > key[r])) {
+                        key[r] = ok;
+                        grp[r] = og;
+                    }
+                }
+            }
+        }
+    }
+    long long carry = 0;
+    int n = 0;
+#pragma unroll
+    for (int r = 0; r < RR; ++r) {
+        if (carry >= topk) break;
+        const bool el = key[r] != ~0ull;
+        const int32_t g = grp[r];
+        const long long cnt = el ? s.count[g] : 0;
+        const long long incl = fl_wave_incl_scan_i64(cnt);
+        long long take = topk - (carry + incl - cnt);
+        take = take < cnt ? take : cnt;
+        take = take > 0 ? take : 0;
+        if (take > 0) {
+            const int32_t op = (int32_t)(key[r] & 0xFFFFFFFFull);
+            sc.oop[o + n + lane] = op;
+            sc.ostart[o + n + lane] = s.start[g];
+            sc.otake[o + n + lane] = (int32_t)take;
+            sc.omass[o + n + lane] = __dmul_rn(gr_proposal(w[op], temp), (double)take);
+        }
+        n += __popcll(__ballot(take > 0));
+        carry += __shfl(incl, FL_WAVE - 1, FL_WAVE);
+        if (__ballot(el) != ~0ull) break;
+    }
+    __syncthreads();  // the option lists are visible to every lane
+    return n;
+}
+
 // Options of a large side written at o (options [o, o + n) of the scratch
 // lists).  Returns n.
-__device__ int gr_side_mem(const GrSide &s, int32_t off, int64_t g0, int64_t G, const float *w, int32_t excluded,
+__device__ __forceinline__ int gr_side_mem(const GrSide &s, int32_t off, int64_t g0, int64_t G, const float *w,
+                                           int32_t excluded,
                            int64_t topk, double temp, const GrScratch &sc, int o) {
     const int lane = fl_lane();
     int64_t P = 128;
@@ -267,36 +359,54 @@ __device__ int gr_side_mem(const GrSide &s, int32_t off, int64_t g0, int64_t G, 
     return n;
 }
 
+// A side of more than 64 groups: register sort up to 256 groups, else the
+// scratch (or LDS) sort.
+__device__ __forceinline__ int gr_side_large(const GrSide &s, int32_t off, int64_t g0, int64_t G, const float *w,
+                                             int32_t excluded, int64_t topk, double temp, const GrScratch &sc,
+                                             int o) {
+    if (G <= 2 * FL_WAVE) return gr_side_regsort<2>(s, off, g0, G, w, excluded, topk, temp, sc, o);
+    if (G <= 4 * FL_WAVE) return gr_side_regsort<4>(s, off, g0, G, w, excluded, topk, temp, sc, o);
+    return gr_side_mem(s, off, g0, G, w, excluded, topk, temp, sc, o);
+}
+
 // Cumulative masses in option order (one sequential sum, as the reference):
 // register options get their cumulative mass in .mass, scratch options in
 // omass.  Returns the running total.
-__device__ double gr_cumulate(GrOpts &o, const GrScratch &sc, int obase, double run) {
+__device__ __forceinline__ double gr_cumulate(GrOpts &o, const GrScratch &sc, int obase, double run, double *mb) {
+    // mb: wave-private LDS [64].  Lane j adds the broadcast masses 0..j in
+    // order, so its value is the sequential sum up to its option.
     const int lane = fl_lane();
     if (!o.mem) {
-        double cum = 0.0;
-        for (int j = 0; j < o.n; ++j) {
-            run = __dadd_rn(run, __shfl(o.mass, j, FL_WAVE));
-            if (lane == j) cum = run;
+        mb[lane] = lane < o.n ? o.mass : 0.0;
+        __syncthreads();
+        double acc = run;
+        for (int i = 0; i < o.n; ++i) {
+            const double m = mb[i];
+            if (i <= lane) acc = __dadd_rn(acc, m);
         }
-        o.mass = cum;
-        return run;
+        __syncthreads();
+        o.mass = lane < o.n ? acc : 0.0;
+        return o.n > 0 ? __shfl(acc, o.n - 1, FL_WAVE) : run;
     }
     for (int base = 0; base < o.n; base += FL_WAVE) {
         const int cnt = o.n - base < FL_WAVE ? o.n - base : FL_WAVE;
-        const double m = lane < cnt ? sc.omass[obase + base + lane] : 0.0;
-        double cum = 0.0;
-        for (int j = 0; j < cnt; ++j) {
-            run = __dadd_rn(run, __shfl(m, j, FL_WAVE));
-            if (lane == j) cum = run;
+        mb[lane] = lane < cnt ? sc.omass[obase + base + lane] : 0.0;
+        __syncthreads();
+        double acc = run;
+        for (int i = 0; i < cnt; ++i) {
+            const double m = mb[i];
+            if (i <= lane) acc = __dadd_rn(acc, m);
         }
-        if (lane < cnt) sc.omass[obase + base + lane] = cum;
+        __syncthreads();
+        if (lane < cnt) sc.omass[obase + base + lane] = acc;
+        run = __shfl(acc, cnt - 1, FL_WAVE);
     }
     __syncthreads();
     return run;
 }
 
 // First option of the side with draw < cumulative mass: its index, or -1.
-__device__ int gr_pick(const GrOpts &o, const GrScratch &sc, int obase, double draw) {
+__device__ __forceinline__ int gr_pick(const GrOpts &o, const GrScratch &sc, int obase, double draw) {
     const int lane = fl_lane();
     if (!o.mem) {
         const unsigned long long b = __ballot(lane < o.n && draw < o.mass);
@@ -325,9 +435,11 @@ __device__ __forceinline__ void gr_option(const GrOpts &o, const GrScratch &sc, 
 }
 
 constexpr int GR_NT = 64;
+constexpr int64_t GR_LDS_SORT_MAX = 4096;  // groups per side sorted in LDS (48 KB)
 
 // One wave per source task (grid-stride over tasks): the task's walks in
 // order with the task's engine; record j of task t = (body key, positive).
+template <bool LS>
 __global__ __launch_bounds__(GR_NT) void k_gr_walk(GrGraph gg, const float *__restrict__ att, int64_t ranks,
                                                   int64_t vocab, const int64_t *__restrict__ heads,
                                                   const int64_t *__restrict__ seeds, int64_t ntasks,
@@ -338,6 +450,8 @@ __global__ __launch_bounds__(GR_NT) void k_gr_walk(GrGraph gg, const float *__re
                                                   int64_t ocap, char *__restrict__ scratch, size_t stride,
                                                   uint64_t *__restrict__ out_key, uint8_t *__restrict__ out_pos) {
     __shared__ uint64_t mt[MT_N];
+    __shared__ double gr_mb[FL_WAVE];
+    extern __shared__ __align__(8) char gr_lds[];  // [pmax] keys + [pmax] groups when lds_sort
     const int lane = fl_lane();
     char *ws = scratch + (size_t)blockIdx.x * stride;
     GrScratch sc;
@@ -347,6 +461,10 @@ __global__ __launch_bounds__(GR_NT) void k_gr_walk(GrGraph gg, const float *__re
     sc.oop = sc.sgrp + pmax;
     sc.ostart = sc.oop + ocap;
     sc.otake = sc.ostart + ocap;
+    if (LS) {  // the large-side sort runs in LDS (the option lists stay in the scratch)
+        sc.skey = (uint64_t *)gr_lds;
+        sc.sgrp = (int32_t *)(sc.skey + pmax);
+    }
     const int32_t R = gg.R, identity = 2 * R;
     for (int64_t t = blockIdx.x; t < ntasks; t += gridDim.x) {
         const int32_t hslot = task_head[t];
@@ -388,19 +506,19 @@ __global__ __launch_bounds__(GR_NT) void k_gr_walk(GrGraph gg, const float *__re
                     fo = gr_side_reg(gg.fw, 0, fg0, (int)fG, w, excl, topk, temp);
                 } else {
                     fo.mem = 1;
-                    fo.n = gr_side_mem(gg.fw, 0, fg0, fG, w, excl, topk, temp, sc, 0);
+                    fo.n = gr_side_large(gg.fw, 0, fg0, fG, w, excl, topk, temp, sc, 0);
                 }
                 const int ibase = fo.mem ? fo.n : 0;
                 if (iG <= FL_WAVE) {
                     io = gr_side_reg(gg.inv, R, ig0, (int)iG, w, excl, topk, temp);
                 } else {
                     io.mem = 1;
-                    io.n = gr_side_mem(gg.inv, R, ig0, iG, w, excl, topk, temp, sc, ibase);
+                    io.n = gr_side_large(gg.inv, R, ig0, iG, w, excl, topk, temp, sc, ibase);
                 }
                 if (fo.mem || io.mem) __syncthreads();
                 const float wid = w[identity];
-                double total = gr_cumulate(fo, sc, 0, 0.0);
-                total = gr_cumulate(io, sc, ibase, total);
+                double total = gr_cumulate(fo, sc, 0, 0.0, gr_mb);
+                total = gr_cumulate(io, sc, ibase, total, gr_mb);
                 if (wid > 0.0f) total = __dadd_rn(total, gr_proposal(wid, temp));
                 if (!(total > 0.0)) {
                     viable = false;
@@ -872,9 +990,13 @@ int fl_ground_walks(void *stream, const fl_ground_graph *g, const float *att, in
         return fl_fail(FL_ERR_ARG, "ground_walks: null argument");
     const GrWalkLayout L = gr_walk_layout(g, ntasks);
     if (ws_bytes < L.bytes) return fl_fail(FL_ERR_ARG, "ground_walks: workspace too small");
-    FL_LAUNCH("k_gr_walk", k_gr_walk, dim3((unsigned)L.waves), dim3(GR_NT), 0, (hipStream_t)stream, gr_graph(g), att,
-              ranks, 2 * g->num_relations + 1, heads, seeds, ntasks, task_head, task_source, task_index, walks,
-              topk_edges, mask_query_head, temperature, L.pmax, L.ocap, (char *)ws, L.stride, keys, positive);
+    // sides of up to GR_LDS_SORT_MAX groups are sorted in LDS, larger ones in the scratch
+    const int lds_sort = L.pmax <= GR_LDS_SORT_MAX ? 1 : 0;
+    const size_t lds = lds_sort ? (sizeof(uint64_t) + sizeof(int32_t)) * (size_t)L.pmax : 0;
+    FL_LAUNCH("k_gr_walk", lds_sort ? k_gr_walk<true> : k_gr_walk<false>, dim3((unsigned)L.waves), dim3(GR_NT), lds,
+              (hipStream_t)stream, gr_graph(g), att, ranks, 2 * g->num_relations + 1, heads, seeds, ntasks, task_head,
+              task_source, task_index, walks, topk_edges, mask_query_head, temperature, L.pmax, L.ocap, (char *)ws,
+              L.stride, keys, positive);
     return fl_check_launch("ground_walks");
 }
 
