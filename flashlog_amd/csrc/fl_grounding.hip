@@ -723,13 +723,74 @@ __global__ void k_ct_emit(const uint64_t *__restrict__ ukey, const uint32_t *__r
     }
 }
 
-// raw unique rows per segment and output rows per head
-__global__ void k_ct_counts(const int32_t *__restrict__ rseg, int64_t nrun, const int32_t *__restrict__ uhead,
-                            const int32_t *__restrict__ uhead_flag, int64_t nu, int64_t *__restrict__ seg_raw,
-                            int64_t *__restrict__ head_rows) {
+// Histogram of a nondecreasing array of bins (entries with flag 0 skipped):
+// each wave takes CT_SPAN consecutive entries, counts them per distinct bin
+// with ballots and keeps a running (bin, count) pair, so an atomic is issued
+// only where the bin changes (instead of one per entry on a few addresses).
+constexpr int CT_SPAN = 16 * FL_WAVE;
+
+__global__ void k_ct_sorted_hist(const int32_t *__restrict__ bin, const int32_t *__restrict__ flag, int64_t n,
+                                 int64_t *__restrict__ count) {
+    const int lane = fl_lane();
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / FL_WAVE;
+    const int64_t base = wave * CT_SPAN;
+    if (base >= n) return;  // whole wave
+    int32_t cur = -1;
+    unsigned long long cnt = 0;
+    for (int r = 0; r < CT_SPAN / FL_WAVE; ++r) {
+        const int64_t i = base + (int64_t)r * FL_WAVE + lane;
+        const bool valid = i < n && (!flag || flag[i]);
+        const int32_t b = valid ? bin[i] : -1;
+        uint64_t left = __ballot(valid);
+        while (left) {
+            const int32_t k = __shfl(b, __ffsll((long long)left) - 1, FL_WAVE);
+            const uint64_t m = __ballot(valid && b == k);
+            left &= ~m;
+            if (k != cur) {
+                if (lane == 0 && cnt) atomicAdd((unsigned long long *)&count[cur], cnt);
+                cur = k;
+                cnt = 0;
+            }
+            cnt += (unsigned long long)__popcll(m);
+        }
+    }
+    if (lane == 0 && cnt) atomicAdd((unsigned long long *)&count[cur], cnt);
+}
+
+// OR of every body key (the widest relation field sets the packed width)
+__global__ void k_ct_or(const uint64_t *__restrict__ keys, int64_t n, unsigned long long *__restrict__ acc) {
+    uint64_t v = 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        v |= keys[i];
+#pragma unroll
+    for (int o = FL_WAVE / 2; o > 0; o >>= 1) v |= __shfl_xor(v, o, FL_WAVE);
+    if (fl_lane() == 0 && v) atomicOr(acc, (unsigned long long)v);
+}
+
+// Sort key of record i: (fold segment, len, body[0..2]) with rb bits per
+// relation field, ordered as (segment, body key), so one stable sort of the
+// whole batch is the per-segment stable sort by body key.
+__global__ void k_ct_pack(const uint64_t *__restrict__ keys, int64_t n, const int64_t *__restrict__ rec_off,
+                          int64_t nseg, int rb, uint64_t *__restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < nrun) atomicAdd((unsigned long long *)&seg_raw[rseg[i]], 1ull);
-    if (i < nu && uhead_flag[i]) atomicAdd((unsigned long long *)&head_rows[uhead[i]], 1ull);
+    if (i >= n) return;
+    int64_t lo = 0, hi = nseg;  // last s with rec_off[s] <= i
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (rec_off[mid] <= i) lo = mid;
+        else hi = mid;
+    }
+    const uint64_t k = keys[i], m = (1ull << 20) - 1;
+    const uint64_t body = ((k >> 60) << (3 * rb)) | (((k >> 40) & m) << (2 * rb)) | (((k >> 20) & m) << rb) | (k & m);
+    out[i] = ((uint64_t)lo << (2 + 3 * rb)) | body;
+}
+
+// back to body keys, in place
+__global__ void k_ct_unpack(uint64_t *__restrict__ keys, int64_t n, int rb) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t p = keys[i], m = (1ull << rb) - 1;
+    keys[i] = (((p >> (3 * rb)) & 3ull) << 60) | (((p >> (2 * rb)) & m) << 40) | (((p >> rb) & m) << 20) | (p & m);
 }
 
 // ---------------------------------------------------------------------------
@@ -1031,10 +1092,32 @@ int fl_ground_count(void *stream, const uint64_t *keys, const uint8_t *positive,
               walks, x.rec_off);
     FL_LAUNCH("k_iota_u32", k_iota_u32, dim3(nblk(n)), dim3(CT_NT), 0, st, x.rec_in, n);
     size_t sb = x.sort_bytes;
-    if ((rc = gr_rc(rocprim::segmented_radix_sort_pairs(x.sort_tmp, sb, keys, x.skey, x.rec_in, x.rec, (unsigned)n,
-                                                        (unsigned)nsegments, x.rec_off, x.rec_off + 1, 0, 63, st),
-                    "ground_count: record sort")) != FL_OK)
+    // width of the relation fields from the OR of all keys
+    unsigned long long kor = 0;
+    FL_LAUNCH("k_u64_fill", k_u64_fill, dim3(1), dim3(CT_NT), 0, st, x.rcnt, (int64_t)1, 0ull);
+    FL_LAUNCH("k_ct_or", k_ct_or, dim3((unsigned)std::min<int64_t>(nblk(n), 2048)), dim3(CT_NT), 0, st, keys, n,
+              x.rcnt);
+    if (hipMemcpyAsync(&kor, x.rcnt, sizeof(kor), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fl_fail(FL_ERR_HIP, "ground_count: reading the key width");
+    const uint64_t fields = ((kor >> 40) | (kor >> 20) | kor) & ((1ull << 20) - 1);
+    const int rb = fields ? 64 - __builtin_clzll(fields) : 1;
+    const int segbits = nsegments > 1 ? 64 - __builtin_clzll((unsigned long long)(nsegments - 1)) : 0;
+    const int tb = segbits + 2 + 3 * rb;
+    if (tb <= 64) {
+        FL_LAUNCH("k_ct_pack", k_ct_pack, dim3(nblk(n)), dim3(CT_NT), 0, st, keys, n, x.rec_off, nsegments, rb,
+                  x.rkey);
+        if ((rc = gr_rc(rocprim::radix_sort_pairs(x.sort_tmp, sb, x.rkey, x.skey, x.rec_in, x.rec, (unsigned)n, 0,
+                                                  (unsigned)tb, st),
+                        "ground_count: record sort")) != FL_OK)
+            return rc;
+        FL_LAUNCH("k_ct_unpack", k_ct_unpack, dim3(nblk(n)), dim3(CT_NT), 0, st, x.skey, n, rb);
+    } else if ((rc = gr_rc(rocprim::segmented_radix_sort_pairs(x.sort_tmp, sb, keys, x.skey, x.rec_in, x.rec,
+                                                               (unsigned)n, (unsigned)nsegments, x.rec_off,
+                                                               x.rec_off + 1, 0, 63, st),
+                           "ground_count: record sort")) != FL_OK) {
         return rc;
+    }
     FL_LAUNCH("k_ct_flags", k_ct_flags, dim3(nblk(n)), dim3(CT_NT), 0, st, x.skey, x.rec, n, x.rec_off, nsegments,
               walks, x.run_head, x.src_head);
     if ((rc = exclusive_scan(st, x.run_head, x.run_id, n, x.tmp)) != FL_OK) return rc;
@@ -1092,8 +1175,14 @@ int fl_ground_count(void *stream, const uint64_t *keys, const uint8_t *positive,
     }
     FL_LAUNCH("k_u64_fill", k_u64_fill, dim3(nblk(nheads + 1)), dim3(CT_NT), 0, st,
               (unsigned long long *)x.head_rows, nheads + 1, 0ull);
-    FL_LAUNCH("k_ct_counts", k_ct_counts, dim3(nblk(nrun > nu ? nrun : nu)), dim3(CT_NT), 0, st, x.rseg, nrun,
-              x.uhead, x.uflag, nu, info, x.head_rows);
+    const auto hist_blocks = [](int64_t m) { return dim3((unsigned)((m + CT_SPAN * (CT_NT / FL_WAVE) - 1) /
+                                                                    (CT_SPAN * (CT_NT / FL_WAVE)))); };
+    if (nrun > 0)
+        FL_LAUNCH("k_ct_sorted_hist", k_ct_sorted_hist, hist_blocks(nrun), dim3(CT_NT), 0, st, x.rseg,
+                  (const int32_t *)nullptr, nrun, info);
+    if (nu > 0)
+        FL_LAUNCH("k_ct_sorted_hist", k_ct_sorted_hist, hist_blocks(nu), dim3(CT_NT), 0, st, x.uhead, x.uflag, nu,
+                  x.head_rows);
     // row offsets per head: exclusive scan of the per-head row counts
     if ((rc = exclusive_scan(st, x.head_rows, info + nsegments, nheads, x.tmp)) != FL_OK) return rc;
     return fl_check_launch("ground_count");

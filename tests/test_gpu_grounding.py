@@ -95,6 +95,37 @@ def test_grounding_rows_match_oracle(mask):
     assert cands[3].shape == (0, 12)
 
 
+def test_grounding_rows_wide_keys():
+    """Relation ids near 2^15 (inverse operators need 16 bits) and 32769
+    folds: the (fold, body) sort key needs 16 + 2 + 3*16 > 64 bits, so the
+    counts take the per-fold segmented sort instead of the packed one."""
+    sg = _sg()
+    rng = np.random.default_rng(21)
+    E, R, n_edges = 300, 20000, 4000
+    h, t = rng.integers(0, E, n_edges), rng.integers(0, E, n_edges)
+    r = rng.integers(19000, R, n_edges)
+    csr = O.build_csr_structure(h, t, r, E)
+    att = _att(rng, 1, 1, 2 * R + 1, zero=0.0)
+    head = 19500
+    nfolds = 32769
+    folds = [[s] for s in rng.integers(0, E, nfolds)]
+    budgets = [4, 30, 100]
+    csr_t = tuple(torch.from_numpy(np.asarray(a)) for a in csr)
+    cands, raw, _ = sg.ground_head_batch_source_folds_sampled_capped_counts(
+        torch.from_numpy(att), [head], R, [[np.asarray(f) for f in folds]], csr_t, 1, 3, False, [5], 1000, 8,
+        budgets)
+    fold_src = [np.asarray(f, np.int64) for f in folds]
+    rows, rraw = O.ground(att[0], R, head, fold_src, csr, 1, 3, False, 5, budgets)
+    # the case is the wide one: 16-bit relation fields and 16 fold bits
+    src = np.concatenate(fold_src)
+    keys, _ = O.ground_walks(att[0], R, head, src, np.zeros(nfolds, np.int64), csr, 1, 3, False, 5)
+    kor = int(np.bitwise_or.reduce(keys.reshape(-1)))
+    fields = ((kor >> 40) | (kor >> 20) | kor) & ((1 << 20) - 1)
+    assert fields.bit_length() == 16 and (nfolds - 1).bit_length() + 2 + 3 * 16 > 64
+    np.testing.assert_array_equal(cands[0].numpy(), rows.reshape(-1, 12))
+    assert raw[0] == tuple(rraw)
+
+
 def test_grounding_api_checks():
     sg = _sg()
     h, r, t, E, R, csr = small_graph(2, 0.05)
