@@ -17,7 +17,7 @@ flashlog_kernel.py:1629-1663) with c1=1000, c2=400 and the model's
 normalization.
 
 Prints one JSON line.  ``value`` = queries/sec (batch / step time) with all
-inputs resident in HBM.  ``roofline`` is for the propagation kernel (k_sp_fill
+inputs resident in HBM.  ``roofline`` is for the propagation kernel (k_sp_items
 for C5, k_pull for C2), timed with HIP events the library records around its
 launches on its own stream; ``cpu_baseline`` is the reference's CPU path (its
 flashlog.cpp built into oracle/_ref) on a bounded sample of the same workload.
@@ -534,36 +534,20 @@ def main_grounding(args):
 
 
 SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_race_select", "k_fill_from",
-                  "k_sp_rowptr", "k_sp_relorder", "k_sp_select", "k_sp_rowinfo", "k_sp_fill", "k_sp_hist",
+                  "k_sp_rowptr", "k_sp_relorder", "k_sp_select", "k_sp_rowinfo", "k_sp_runs", "k_sp_items",
+                  "k_sp_hist",
                   "k_sp_partition", "k_sp_accum_small", "k_sp_accum_mid", "k_sp_accum_hot", "k_sp_emit",
                   "k_norm_fwd", "k_norm_bwd", "k_sp_bwd", "k_fill_f32", "k_scan_tiles", "k_scan_totals",
                   "k_scan_apply", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask"]
 
 
-def fill_bytes(sides_np, b, l, e, R, L, n, W, K):
-    """Algorithmic bytes of one k_sp_fill launch: per entry its record
-    (b, l, e, v: 28 B) and identity item (8 B), per side the source's
-    row-group pointers (8 B), its group records (10 B each) and, per kept
-    edge (all masks are nonzero here: min(eligible edges, K)), the column and
-    mask read (8 B) and the (destination, value) item written (8 B)."""
-    import numpy as np
-    total = 36 * b.shape[0]
-    rows = (b * L + l).astype(np.int64)
-    for (gptr, grel, gcount, off) in sides_np:
-        g0 = gptr[e].astype(np.int64)
-        g1 = gptr[e + 1].astype(np.int64)
-        ng = g1 - g0
-        total += 8 * b.shape[0] + 10 * int(ng.sum())
-        if ng.sum() == 0:
-            continue
-        ent = np.repeat(np.arange(b.shape[0]), ng)
-        starts = np.cumsum(ng) - ng
-        gidx = np.arange(int(ng.sum())) - np.repeat(starts, ng) + np.repeat(g0, ng)
-        wv = W[rows[ent], off + grel[gidx].astype(np.int64)]
-        elig = np.where(wv > 0, gcount[gidx].astype(np.int64), 0)
-        per_entry = np.bincount(ent, weights=elig, minlength=b.shape[0])
-        total += 16 * int(np.minimum(per_entry, K).sum())
-    return total
+def items_bytes(plan):
+    """Algorithmic bytes of one k_sp_items launch (the CSR gather of the kept
+    edges): per raw item the column and mask read and the (destination,
+    value) item written, 16 B, + 6 B of CSR position and attention column
+    with a backward.  The run and chunk tables the kernel also reads are not
+    counted (conservative)."""
+    return (16 + (6 if plan["backward"] else 0)) * plan["items"]
 
 
 def main_sparse(args):
@@ -617,16 +601,9 @@ def main_sparse(args):
             idx[0], idx[1], idx[2], s.values(), w, *csr[:4], *csr[4:8], *csr[8:16], mask_values, None,
             B, L, E, R, False, K, False, c1, False)
 
-    def step(capture=None):
+    def step():
         s = state0
         for t_ in range(T):
-            if capture is not None:
-                # the entries the hop keeps (the same c1 draws as the hop's own)
-                idx = s.indices()
-                rng_state = torch.cuda.get_rng_state()
-                keep = fk._sparse_topc_entries(idx[0], idx[1], idx[2], s.values(), c1, L, sampling=train)
-                torch.cuda.set_rng_state(rng_state)
-                capture.append(tuple((x if keep is None else x[keep]).cpu().numpy() for x in idx))
             s = fk.normalize_sparse3d(hop(s, Wl[t_]))
         idx = s.indices()
         final = torch.sparse_coo_tensor(torch.stack([idx[0], idx[2]]), s.values(), [B, E]).coalesce()
@@ -671,20 +648,19 @@ def main_sparse(args):
               file=sys.stderr, flush=True)
         print("per-step ms: " + json.dumps({k: round(v, 4) for k, v in per_step.items()}),
               file=sys.stderr, flush=True)
-        # hop inputs of one step (after c1), for the algorithmic bytes of k_sp_fill
-        hop_inputs = []
-        step(capture=hop_inputs)
+        # plan sizes of one step's hops, for the algorithmic bytes of k_sp_items
+        fk.plan_log = []
+        step()
         torch.cuda.synchronize()
+        plans = fk.plan_log
+        fk.plan_log = None
     csr_np = [c.cpu().numpy() for c in csr]
     cpu = (cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W.cpu(), T, train)
            if args.cpu_seconds > 0 else None)
-    sides_np = ((csr_np[8], csr_np[9], csr_np[11], 0), (csr_np[12], csr_np[13], csr_np[15], R))
-    Wn = W.cpu().numpy()
-    fb = [fill_bytes(sides_np, bb, ll, ee, B * L, L, n, Wn[hop_].reshape(B * L, n), K)
-          for hop_, (bb, ll, ee) in enumerate(hop_inputs)]
-    fill_ms = per_launch["k_sp_fill"]
+    fb = [items_bytes(p) for p in plans]
+    items_ms = per_launch["k_sp_items"]
     bytes_per_launch = float(np.mean(fb))
-    achieved = bytes_per_launch / (fill_ms * 1e-3) / 1e9 if fill_ms > 0 else 0.0
+    achieved = bytes_per_launch / (items_ms * 1e-3) / 1e9 if items_ms > 0 else 0.0
     result = {
         "metric": "queries/sec for L=3 propagation + % of HBM roofline; top-k select ms",
         "value": B / (ms_step * 1e-3),
@@ -707,9 +683,10 @@ def main_sparse(args):
                            "c2_per_hop": per_launch["k_sp_select"]},
         "kernel_ms_per_launch": per_launch,
         "kernel_ms_per_step": per_step,
-        "roofline": {"kernel": "k_sp_fill", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+        "roofline": {"kernel": "k_sp_items", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None},
+        "hop_plans": plans,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

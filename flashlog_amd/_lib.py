@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 12
+ABI_VERSION = 13
 FL_SEG = 32
 FL_SUP = 16
 
@@ -64,6 +64,7 @@ class FlSparseHop(ctypes.Structure):
         ("ws2", ctypes.c_void_p), ("ws2_bytes", ctypes.c_size_t), ("items", ctypes.c_int64),
         ("tiles", ctypes.c_int64), ("operators", ctypes.c_void_p), ("aggregate", ctypes.c_int),
         ("sampling_seed", ctypes.c_int64), ("raw_pos", ctypes.c_void_p), ("raw_col", ctypes.c_void_p),
+        ("chunks", ctypes.c_int64),
     ]
 
 
@@ -118,7 +119,7 @@ _SIGS = {
     "fl_sparse_plan_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     "fl_sparse_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                       ctypes.POINTER(FlSparseHop), ctypes.c_void_p]),
-    "fl_sparse_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4 + [ctypes.c_int] * 2),
+    "fl_sparse_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 5 + [ctypes.c_int] * 2),
     "fl_sparse_expand": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                         ctypes.POINTER(FlSparseHop), ctypes.c_void_p, ctypes.c_void_p]),
     "fl_sparse_emit": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),

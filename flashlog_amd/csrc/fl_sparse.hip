@@ -12,11 +12,14 @@
 //
 // Pipeline (rows r = b*L + l; entries must be sorted by row):
 //   plan    k_sp_rowptr   entry range of every row, input validation
-//           k_sp_select   per (entry, side): c2 threshold and cut, item counts
-//           scan          item offsets of every entry (raw order)
+//           k_sp_select   per (entry, side): c2 threshold and cut, item and
+//                         run counts (a run = the kept edges of one group)
+//           scan          item and run offsets of every entry (raw order)
 //           k_sp_rowinfo  item range and tile count of every row; scan
-//   expand  k_sp_fill     wave per entry: raw items (destination, value) in
-//                         order, and the per-(row, bucket, tile) histogram
+//   expand  k_sp_runs     wave per entry: one descriptor per run
+//           k_sp_items    wave per 64 raw items: destination and value of
+//                         each, from the runs that cover the chunk
+//           k_sp_hist     workgroup per tile: (row, bucket, tile) histogram
 //           scan          bucket bases
 //           k_sp_partition workgroup per tile of a row: stable scatter of the
 //                         tile's items into destination buckets (block radix
@@ -241,16 +244,16 @@ __device__ __forceinline__ long long sp_quota_window(SpTake &tk, float wv, long 
     return el ? base + extra : 0;
 }
 
-// Kept items of one (entry, side) in raw order (group order, then CSR
-// position), 64 at a time.  Groups are read 64 at a time, lane g holding
-// one group; a wave prefix sum of their kept counts places every item, and
-// each lane finds the group of its item by a binary search over the lanes.
-// fn(valid, k, p, rel, wv) is called by every lane of the wave for each
-// chunk of 64 items (valid = the lane holds an item; k = the item's index
-// within the side).  Returns the side's item count.  Q: quotas possible.
+// Kept runs of one (entry, side) in raw order (group order; a run = the
+// first take edges of a group, from CSR position start).  Groups are read
+// 64 at a time, lane j holding one group and its kept count (threshold,
+// every edge, or the quota window); fn(take, start, rel, wv, ex) is called
+// by every lane for each window that keeps an item, with ex = the lane's
+// first item index within the side (a wave prefix sum of the takes).
+// Returns the side's item count.  Q: quotas possible.
 template <bool Q, typename F>
-__device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, int64_t g1, const float *wr,
-                                                 SpTake &tk, F &&fn) {
+__device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, int64_t g1, const float *wr,
+                                                SpTake &tk, F &&fn) {
     const int lane = fl_lane();
     int64_t base = 0;
     for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
@@ -267,26 +270,10 @@ __device__ __forceinline__ int64_t sp_side_items(const fl_side &s, int64_t g0, i
         }
         if (Q && tk.kind == TAKE_QUOTA)
             take = sp_quota_window(tk, wv, cnt, g < g1);
-        if (__ballot(take > 0) == 0) continue;  // nothing kept in this window (typical for hub sources)
+        if (__ballot(take > 0) == 0) continue;
         const long long incl = fl_wave_incl_scan_i64(take);
-        const long long total = __shfl(incl, FL_WAVE - 1, FL_WAVE);
-        for (long long k0 = 0; k0 < total; k0 += FL_WAVE) {
-            const long long k = k0 + lane;
-            // smallest lane j with incl_j > k
-            int lo = 0, hi = FL_WAVE - 1;
-#pragma unroll
-            for (int it = 0; it < 6; ++it) {
-                const int mid = (lo + hi) >> 1;
-                const long long im = __shfl(incl, mid, FL_WAVE);
-                if (im > k) hi = mid;
-                else lo = mid + 1;
-            }
-            const int j = lo;
-            const long long ej = __shfl(incl, j, FL_WAVE) - __shfl(take, j, FL_WAVE);
-            const int64_t p = __shfl(start, j, FL_WAVE) + (k - ej);
-            fn(k < total, base + k, p, __shfl(rel, j, FL_WAVE), __shfl(wv, j, FL_WAVE));
-        }
-        base += total;
+        fn((long long)take, start, rel, wv, (long long)(base + incl - take));
+        base += __shfl(incl, FL_WAVE - 1, FL_WAVE);
     }
     return base;
 }
@@ -428,6 +415,7 @@ __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, 
 // (all-edges mode), plus the identity item.  With quotas the side keeps
 // exactly min(eligible, K) edges, as the threshold does.
 constexpr int SEL_NT = 256;
+constexpr int SP_ICHUNK = FL_WAVE;  // raw items per chunk of the item pass
 constexpr int SEL_MAP_MAX = 2048;  // relations per side of the LDS count maps
 
 template <bool QS>
@@ -438,7 +426,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
                                                      int64_t seed, float *__restrict__ th, int32_t *__restrict__ cut,
                                                      int32_t *__restrict__ cnt, const int16_t *__restrict__ rel_order,
                                                      const int32_t *__restrict__ rel_nelig, int use_map,
-                                                     SpQuota *__restrict__ qout) {
+                                                     SpQuota *__restrict__ qout, int32_t *__restrict__ nch) {
     __shared__ int hist_all[SEL_NT / FL_WAVE][256];
     extern __shared__ int cmap_all[];  // [SEL_NT / FL_WAVE][r_size] when the map is used
     const int lane = fl_lane();
@@ -452,7 +440,12 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
     if (i >= nnz) return;
     const int64_t src = se[i];
     if (sb[i] < 0 || sb[i] >= B || sl[i] < 0 || sl[i] >= L || src < 0 || src >= E) {
-        if (lane == 0) { cnt[i] = 0; th[2 * i] = th[2 * i + 1] = 0.0f; cut[2 * i] = cut[2 * i + 1] = 0; }
+        if (lane == 0) {
+            cnt[i] = 0;
+            nch[i] = 0;
+            th[2 * i] = th[2 * i + 1] = 0.0f;
+            cut[2 * i] = cut[2 * i + 1] = 0;
+        }
         return;  // reported by k_sp_rowptr; the plan is not used
     }
     const float *wrow = w + (sb[i] * L + sl[i]) * n;
@@ -511,7 +504,10 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
             cut[2 * i + dir] = ct;
         }
     }
-    if (lane == 0) cnt[i] = total;
+    if (lane == 0) {
+        cnt[i] = total;
+        nch[i] = (total + SP_ICHUNK - 1) / SP_ICHUNK;  // 64-item chunks of the entry's items
+    }
 }
 
 // Fixed-relation rule step (flashlog.cu:1561-1741): entry (b, l, e, v) with
@@ -609,21 +605,44 @@ struct SpRows {
     int64_t NB;                // buckets per row
 };
 
-// One wave per entry: the entry's items in raw order at item_off[i]; for
-// the max also their tie keys (original edge id, INV ones above ORI ones,
-// the identity item last).  Q: training quotas possible.
-template <bool Q, bool BWD>
-__global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
+// Raw items are written in two passes.  k_sp_runs (wave per entry) walks
+// the entry's groups as the plan did and writes one descriptor per kept
+// group (a run: the group's first take edges, at consecutive item slots)
+// plus one for the identity item, at run slot item_off[i] + (its index in
+// the entry) (an entry has at most as many runs as items): its first item
+// (within the entry), CSR position (the source for the identity), a * w of
+// its relation, and its attention column | side flags.  An entry's items
+// are cut into chunks of 64 (chunk_off from the plan); for each chunk the
+// walk records its first item, item count, the run holding that item and
+// the entry's run-slot limit.  k_sp_items (wave per chunk) then writes the
+// chunk's items from the at most 64 runs that touch it, all lanes loading
+// and storing consecutive slots.
+constexpr uint32_t SP_RUN_INV = 0x80000000u;  // run of the INV side
+constexpr uint32_t SP_RUN_ID = 0x40000000u;   // the identity item
+constexpr uint32_t SP_RUN_COL = 0x3FFFFFFFu;  // attention column
+
+struct SpRuns {
+    int32_t *first;    // [items] first item of the run within its entry
+    int32_t *p;        // [items] CSR position of the first item (identity: the source)
+    float *aw;         // [items] a * w[column]
+    uint32_t *meta;    // [items] column | SP_RUN_INV | SP_RUN_ID
+    int64_t *c_base;   // [chunks] first item slot of the chunk's entry
+    int64_t *c_run;    // [chunks] run slot holding the chunk's first item
+    int64_t *c_rlim;   // [chunks] end of the entry's run slots
+    int32_t *c_off;    // [chunks] first item of the chunk within the entry
+    int32_t *c_n;      // [chunks] items in the chunk
+};
+
+template <bool Q>
+__global__ __launch_bounds__(SEL_NT) void k_sp_runs(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                    const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
                                                    const float *__restrict__ sv, int64_t nnz,
                                                    const float *__restrict__ w, int64_t L, int64_t n,
-                                                   int64_t r_size, int wot_i, int mode, int agg, int64_t K,
-                                                   int64_t seed, const float *__restrict__ th,
-                                                   const int32_t *__restrict__ cut, const SpQuota *__restrict__ quota,
+                                                   int64_t r_size, int wot_i, int mode, int64_t seed,
+                                                   const float *__restrict__ th, const int32_t *__restrict__ cut,
+                                                   const SpQuota *__restrict__ quota,
                                                    const int64_t *__restrict__ item_off,
-                                                   int32_t *__restrict__ raw_dst, float *__restrict__ raw_val,
-                                                   uint32_t *__restrict__ raw_tie, int32_t *__restrict__ raw_pos,
-                                                   int16_t *__restrict__ raw_col) {
+                                                   const int64_t *__restrict__ chunk_off, SpRuns ru) {
     const int lane = fl_lane();
     const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
     if (i >= nnz) return;
@@ -631,36 +650,132 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_fill(fl_side ori, fl_side inv, co
     const int64_t r = sb[i] * L + sl[i];
     const float a = sv[i];
     const float *wrow = w + r * n;
-    const bool holes = mode == SP_TOPK && agg == SP_SUM;
-    int64_t pos = item_off[i];
+    const int64_t base = item_off[i];
+    const int64_t nitems = item_off[i + 1] - base;
+    const int64_t u0 = chunk_off[i];
     // the plan's item count bounds every write (the walk reproduces it)
-    const int64_t lim = item_off[i + 1] - (wot_i ? 0 : 1);
+    const int64_t lim = nitems - (wot_i ? 0 : 1);
+    int64_t pos = 0, rix = 0;  // within the entry
+    const uint64_t below = (1ull << lane) - 1;
     for (int dir = 0; dir < 2; ++dir) {
         const fl_side &s = dir ? inv : ori;
         const float *wr = wrow + (dir ? r_size : 0);
         const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
         SpTake tk = sp_take<Q>(mode, th[2 * i + dir], cut[2 * i + dir], quota + 2 * i + dir, seed, sb[i], sl[i], src,
                                dir);
-        pos += sp_side_items<Q>(s, g0, g1, wr, tk, [&](bool valid, int64_t k, int64_t p, int rel, float wv) {
-            if (valid && pos + k < lim) {
-                const float m = s.mask[p];
-                raw_dst[pos + k] = (!holes || m != 0.0f) ? s.col_ind[p] : -1;
-                raw_val[pos + k] = fl_mul(fl_mul(a, wv), m);
-                if (raw_tie) raw_tie[pos + k] = (dir ? SP_TIE_INV : 0u) | (uint32_t)s.order[p];
-                if (BWD) {
-                    raw_pos[pos + k] = (int32_t)p;
-                    raw_col[pos + k] = (int16_t)((dir ? r_size : 0) + rel);
-                }
+        const uint32_t side = dir ? SP_RUN_INV : 0u;
+        const uint32_t col0 = dir ? (uint32_t)r_size : 0u;
+        pos += sp_side_runs<Q>(s, g0, g1, wr, tk, [&](long long take, int64_t start, int rel, float wv, long long ex) {
+            const uint64_t m = __ballot(take > 0);
+            const int64_t ri = rix + __popcll(m & below);
+            const int64_t o = pos + ex;
+            if (take > 0 && o + take <= lim) {  // then ri < o + 1 <= nitems
+                ru.first[base + ri] = (int32_t)o;
+                ru.p[base + ri] = (int32_t)start;
+                ru.aw[base + ri] = fl_mul(a, wv);
+                ru.meta[base + ri] = side | (col0 + (uint32_t)rel);
+                for (int64_t q = (o + SP_ICHUNK - 1) / SP_ICHUNK; q * SP_ICHUNK < o + take; ++q)
+                    ru.c_run[u0 + q] = base + ri;
             }
+            rix += __popcll(m);
         });
     }
-    if (!wot_i && lane == 0 && pos == lim) {
-        raw_dst[pos] = (int32_t)src;
-        raw_val[pos] = fl_mul(a, wrow[n - 1]);
-        if (raw_tie) raw_tie[pos] = SP_TIE_IDENTITY;
+    if (!wot_i && lane == 0 && pos == lim && rix <= lim) {
+        ru.first[base + rix] = (int32_t)lim;
+        ru.p[base + rix] = (int32_t)src;
+        ru.aw[base + rix] = fl_mul(a, wrow[n - 1]);
+        ru.meta[base + rix] = SP_RUN_ID | (uint32_t)(n - 1);
+        if (lim % SP_ICHUNK == 0) ru.c_run[u0 + lim / SP_ICHUNK] = base + rix;
+    }
+    const int64_t nr = rix + (wot_i ? 0 : 1);
+    const int64_t nq = chunk_off[i + 1] - u0;
+    for (int64_t q = lane; q < nq; q += FL_WAVE) {
+        const int64_t c0 = q * SP_ICHUNK;
+        ru.c_base[u0 + q] = base;
+        ru.c_rlim[u0 + q] = base + (nr < nitems ? nr : nitems);
+        ru.c_off[u0 + q] = (int32_t)c0;
+        ru.c_n[u0 + q] = (int32_t)(nitems - c0 < SP_ICHUNK ? nitems - c0 : SP_ICHUNK);
+    }
+}
+
+// Wave per chunk (grid-stride): lane j loads run slot r0 + j (r0 holds the
+// chunk's first item); the runs starting inside the chunk mark their first
+// slot in LDS, and the owner of slot k is the number of marks at slots
+// 1..k (an entry's runs tile its items in order).  The items are the
+// reference's raw items: destination (-1 for a masked edge of the top-k
+// sum), value (a * w) * m, and for the max the tie key, for the backward
+// the CSR position and attention column.
+constexpr int SP_ITEMS_NT = 256;
+constexpr int64_t SP_ITEMS_GRID = 8192;  // workgroups of the grid-stride item pass
+
+template <bool MAXT, bool BWD>
+__global__ __launch_bounds__(SP_ITEMS_NT) void k_sp_items(fl_side ori, fl_side inv, int64_t nchunks, SpRuns ru,
+                                                         int holes, int32_t *__restrict__ raw_dst,
+                                                         float *__restrict__ raw_val, uint32_t *__restrict__ raw_tie,
+                                                         int32_t *__restrict__ raw_pos,
+                                                         int16_t *__restrict__ raw_col) {
+    __shared__ uint8_t mark_all[SP_ITEMS_NT / FL_WAVE][SP_ICHUNK];
+    const int lane = fl_lane();
+    uint8_t *mark = mark_all[threadIdx.x / FL_WAVE];
+    const int64_t waves = (int64_t)gridDim.x * (SP_ITEMS_NT / FL_WAVE);
+    const uint64_t upto = lane == FL_WAVE - 1 ? ~0ull : ((2ull << lane) - 1);
+    for (int64_t c = (int64_t)blockIdx.x * (SP_ITEMS_NT / FL_WAVE) + threadIdx.x / FL_WAVE; c < nchunks; c += waves) {
+        const int64_t base = fl_uniform_i64(ru.c_base[c]);
+        const int64_t r0 = fl_uniform_i64(ru.c_run[c]);
+        const int64_t rlim = fl_uniform_i64(ru.c_rlim[c]);
+        const int off = __builtin_amdgcn_readfirstlane(ru.c_off[c]);
+        const int cn = __builtin_amdgcn_readfirstlane(ru.c_n[c]);
+        const int64_t rj = r0 + lane;
+        int32_t d = SP_ICHUNK, rp = 0;
+        float aw = 0.0f;
+        uint32_t rm = 0;
+        if (rj >= base && rj < rlim) {
+            // first item of the run relative to the chunk's (both within the entry)
+            const int32_t f = ru.first[rj] - off;
+            d = f < SP_ICHUNK ? f : SP_ICHUNK;
+            rp = ru.p[rj];
+            aw = ru.aw[rj];
+            rm = ru.meta[rj];
+        }
+        mark[lane] = 0;
+        fl_wave_sync();
+        if (lane > 0 && d > 0 && d < SP_ICHUNK) mark[d] = 1;
+        fl_wave_sync();
+        const uint64_t starts = __ballot(mark[lane] != 0);
+        const int j = __popcll(starts & upto);
+        const int32_t dj = __shfl(d, j, FL_WAVE);
+        const int32_t pj = __shfl(rp, j, FL_WAVE) + (lane - dj);
+        const float awj = __shfl(aw, j, FL_WAVE);
+        const uint32_t mj = (uint32_t)__shfl((int)rm, j, FL_WAVE);
+        fl_wave_sync();  // marks read before the next chunk clears them
+        if (lane >= cn) continue;
+        const int64_t k = base + off + lane;
+        int32_t dst = -1, pos = -1;
+        float val = 0.0f;
+        uint32_t tie = SP_TIE_IDENTITY;
+        if (mj & SP_RUN_ID) {
+            dst = pj;
+            val = awj;
+        } else {
+            const bool inv_side = (mj & SP_RUN_INV) != 0;
+            const int64_t edges = inv_side ? inv.edges : ori.edges;
+            const float *mk = inv_side ? inv.mask : ori.mask;
+            const int32_t *ci = inv_side ? inv.col_ind : ori.col_ind;
+            if (pj >= 0 && pj < edges) {
+                const float m = mk[pj];
+                const int32_t e = ci[pj];
+                dst = (!holes || m != 0.0f) ? e : -1;
+                val = fl_mul(awj, m);
+                if (MAXT) tie = (inv_side ? SP_TIE_INV : 0u) | (uint32_t)(inv_side ? inv.order : ori.order)[pj];
+                pos = pj;
+            }
+        }
+        raw_dst[k] = dst;
+        raw_val[k] = val;
+        if (MAXT) raw_tie[k] = tie;
         if (BWD) {
-            raw_pos[pos] = -1;
-            raw_col[pos] = (int16_t)(n - 1);
+            raw_pos[k] = pos;
+            raw_col[k] = (int16_t)(mj & SP_RUN_COL);
         }
     }
 }
@@ -1561,10 +1676,11 @@ __global__ void k_fill_i64(int64_t *__restrict__ p, int64_t n, int64_t v) {
 }
 
 __global__ void k_sp_plan_out(const int64_t *__restrict__ items, const int64_t *__restrict__ tiles, int64_t NB,
-                              int64_t *__restrict__ plan) {
+                              const int64_t *__restrict__ chunks, int64_t *__restrict__ plan) {
     plan[0] = *items;
     plan[1] = *tiles;
     plan[3] = NB;
+    plan[4] = chunks ? *chunks : 0;
 }
 
 __global__ void k_fill_from(const int64_t *__restrict__ src, int64_t *__restrict__ dst) { *dst = *src; }
@@ -1857,8 +1973,8 @@ int sp_bucket_bits(int64_t NB) {
 // plan workspace layout
 struct SpPlan {
     float *th;
-    int32_t *cut, *cnt, *ntiles;
-    int64_t *item_off, *row_ptr, *row_item0, *tile_base, *tmp;
+    int32_t *cut, *cnt, *ntiles, *nch;
+    int64_t *item_off, *row_ptr, *row_item0, *tile_base, *tmp, *chunk_off;
     SpQuota *quota;       // [nnz][2] training quota parameters (quota sides only)
     int16_t *rel_order;   // [R][2][r_size] c2 admission order (r_size <= RO_MAX)
     int32_t *rel_nelig;   // [R][2] relations with a positive weight
@@ -1873,6 +1989,8 @@ SpPlan sp_plan_layout(int64_t nnz, int64_t R, int64_t r_size, char *base) {
     p.cut = (int32_t *)take(sizeof(int32_t) * 2 * (size_t)nnz);
     p.cnt = (int32_t *)take(sizeof(int32_t) * (size_t)nnz);
     p.item_off = (int64_t *)take(sizeof(int64_t) * (size_t)(nnz + 1));
+    p.nch = (int32_t *)take(sizeof(int32_t) * (size_t)nnz);
+    p.chunk_off = (int64_t *)take(sizeof(int64_t) * (size_t)(nnz + 1));
     p.row_ptr = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
     p.row_item0 = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
     p.ntiles = (int32_t *)take(sizeof(int32_t) * (size_t)R);
@@ -1895,14 +2013,27 @@ struct SpExp {
     uint32_t *raw_tie, *part_tie;
     int32_t *hot_list, *mid_list, *hot_count;
     int64_t *base, *tmp;
+    SpRuns runs;
     size_t bytes;
 };
 
-SpExp sp_exp_layout(int64_t T, int64_t tiles, int64_t R, int64_t NB, int backward, int agg, char *base) {
+SpExp sp_exp_layout(int64_t T, int64_t tiles, int64_t chunks, int64_t R, int64_t NB, int backward, int agg,
+                    char *base) {
     SpExp x{};
     size_t off = 0;
     auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
     const int64_t T1 = T > 0 ? T : 1;
+    const int64_t U1 = chunks > 0 ? chunks : 1;
+    // run table (at most one run per item) and chunk table
+    x.runs.first = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
+    x.runs.p = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
+    x.runs.aw = (float *)take(sizeof(float) * (size_t)T1);
+    x.runs.meta = (uint32_t *)take(sizeof(uint32_t) * (size_t)T1);
+    x.runs.c_base = (int64_t *)take(sizeof(int64_t) * (size_t)U1);
+    x.runs.c_run = (int64_t *)take(sizeof(int64_t) * (size_t)U1);
+    x.runs.c_rlim = (int64_t *)take(sizeof(int64_t) * (size_t)U1);
+    x.runs.c_off = (int32_t *)take(sizeof(int32_t) * (size_t)U1);
+    x.runs.c_n = (int32_t *)take(sizeof(int32_t) * (size_t)U1);
     x.raw_dst = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
     x.raw_val = (float *)take(sizeof(float) * (size_t)T1);
     if (agg == SP_MAX) x.raw_tie = (uint32_t *)take(sizeof(uint32_t) * (size_t)T1);
@@ -1986,8 +2117,8 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     hipStream_t st = (hipStream_t)stream;
     const int64_t nnz = h->nnz;
     const int64_t K = sp_budget(h);
-    // plan[0] items, plan[1] tiles, plan[2] error, plan[3] buckets per row
-    FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, (int32_t *)plan, (int64_t)8, 0);
+    // plan[0] items, plan[1] tiles, plan[2] error, plan[3] buckets per row, plan[4] item chunks
+    FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, (int32_t *)plan, (int64_t)10, 0);
     FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr, R + 1,
               (int64_t)0);
     const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
@@ -2008,20 +2139,23 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
                   dim3(SEL_NT), lds, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
                   h->r_size, h->wot_i, h->mode, K, h->sampling_seed, p.th, p.cut, p.cnt,
                   lookup ? p.rel_order : (const int16_t *)nullptr, lookup ? p.rel_nelig : (const int32_t *)nullptr,
-                  use_map, p.quota);
+                  use_map, p.quota, p.nch);
     }
     if ((rc = exclusive_scan(st, p.cnt, p.item_off, nnz, p.tmp)) != FL_OK) return rc;
+    const bool fixed = h->mode == SP_FIXED;
+    if (!fixed && (rc = exclusive_scan(st, p.nch, p.chunk_off, nnz, p.tmp)) != FL_OK) return rc;
     FL_LAUNCH("k_sp_rowinfo", k_sp_rowinfo, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr,
               p.item_off, R, p.row_item0, p.ntiles);
     if ((rc = exclusive_scan(st, p.ntiles, p.tile_base, R, p.tmp)) != FL_OK) return rc;
     FL_LAUNCH("k_sp_plan_out", k_sp_plan_out, dim3(1), dim3(1), 0, st, p.item_off + nnz, p.tile_base + R,
-              sp_buckets(h->E), plan);
+              sp_buckets(h->E), fixed ? (const int64_t *)nullptr : p.chunk_off + nnz, plan);
     return fl_check_launch("sparse_plan");
 }
 
-size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t R, int64_t E, int backward, int aggregate) {
-    if (items < 0 || tiles < 0 || R < 0) return 0;
-    return sp_exp_layout(items, tiles, R, sp_buckets(E), backward, aggregate, nullptr).bytes;
+size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t chunks, int64_t R, int64_t E, int backward,
+                              int aggregate) {
+    if (items < 0 || tiles < 0 || chunks < 0 || R < 0) return 0;
+    return sp_exp_layout(items, tiles, chunks, R, sp_buckets(E), backward, aggregate, nullptr).bytes;
 }
 
 // c2 budget of the plan and walk kernels: K > 0 selects, 0 keeps every
@@ -2037,8 +2171,12 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     if ((rc = sp_check(ori, inv, h, "sparse_expand")) != FL_OK) return rc;
     const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
     if (!h->ws1 || !h->ws2 || !out_base) return fl_fail(FL_ERR_ARG, "sparse_expand: null workspace or out_base");
-    if (h->items < 0 || h->tiles < 0) return fl_fail(FL_ERR_ARG, "sparse_expand: negative plan sizes");
-    if (h->ws2_bytes < fl_sparse_expand_bytes(h->items, h->tiles, R, h->E, raw_local != nullptr, h->aggregate))
+    if (h->items < 0 || h->tiles < 0 || h->chunks < 0)
+        return fl_fail(FL_ERR_ARG, "sparse_expand: negative plan sizes");
+    if (h->mode != SP_FIXED && h->chunks > h->items + h->nnz)
+        return fl_fail(FL_ERR_ARG, "sparse_expand: more item chunks than the plan allows");
+    if (h->ws2_bytes <
+        fl_sparse_expand_bytes(h->items, h->tiles, h->chunks, R, h->E, raw_local != nullptr, h->aggregate))
         return fl_fail(FL_ERR_ARG, "sparse_expand: workspace too small");
     if (raw_local && h->mode != SP_FIXED && h->items > 0) {
         if (!h->raw_pos || !h->raw_col)
@@ -2046,7 +2184,8 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         if (h->n > 32767) return fl_fail(FL_ERR_ARG, "sparse_expand: backward columns need n <= 32767");
     }
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
-    SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, raw_local != nullptr, h->aggregate, (char *)h->ws2);
+    SpExp x = sp_exp_layout(h->items, h->tiles, h->chunks, R, NB, raw_local != nullptr, h->aggregate,
+                            (char *)h->ws2);
     const bool mx = h->aggregate == SP_MAX;
     hipStream_t st = (hipStream_t)stream;
     const int64_t nnz = h->nnz;
@@ -2054,15 +2193,30 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     if (nnz > 0 && h->mode == SP_FIXED)
         FL_LAUNCH("k_fx_fill", k_fx_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_e, h->sp_v, nnz, p.cut, p.item_off, x.raw_dst, x.raw_val);
-    else if (nnz > 0)
-        FL_LAUNCH("k_sp_fill",
-                  raw_local ? (sp_quotas(h) ? k_sp_fill<true, true> : k_sp_fill<false, true>)
-                            : (sp_quotas(h) ? k_sp_fill<true, false> : k_sp_fill<false, false>),
-                  dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
-                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n,
-                  h->r_size, h->wot_i, h->mode, h->aggregate, sp_budget(h), h->sampling_seed, p.th, p.cut,
-                  p.quota, p.item_off, x.raw_dst, x.raw_val, x.raw_tie, raw_local ? h->raw_pos : (int32_t *)nullptr,
-                  raw_local ? h->raw_col : (int16_t *)nullptr);
+    else if (nnz > 0 && h->items > 0 && h->chunks > 0) {
+        FL_LAUNCH("k_sp_runs", sp_quotas(h) ? k_sp_runs<true> : k_sp_runs<false>,
+                  dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))), dim3(SEL_NT), 0, st, *ori,
+                  *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n, h->r_size, h->wot_i, h->mode,
+                  h->sampling_seed, p.th, p.cut, p.quota, p.item_off, p.chunk_off, x.runs);
+        const int64_t wpb = SP_ITEMS_NT / FL_WAVE;
+        const int64_t blocks = (h->chunks + wpb - 1) / wpb;
+        const unsigned grid = (unsigned)(blocks < SP_ITEMS_GRID ? blocks : SP_ITEMS_GRID);
+        const int holes = h->mode == SP_TOPK && h->aggregate == SP_SUM;
+        int32_t *rp = raw_local ? h->raw_pos : (int32_t *)nullptr;
+        int16_t *rc16 = raw_local ? h->raw_col : (int16_t *)nullptr;
+        if (mx && raw_local)
+            FL_LAUNCH("k_sp_items", (k_sp_items<true, true>), dim3(grid), dim3(SP_ITEMS_NT), 0, st, *ori, *inv,
+                      h->chunks, x.runs, holes, x.raw_dst, x.raw_val, x.raw_tie, rp, rc16);
+        else if (mx)
+            FL_LAUNCH("k_sp_items", (k_sp_items<true, false>), dim3(grid), dim3(SP_ITEMS_NT), 0, st, *ori, *inv,
+                      h->chunks, x.runs, holes, x.raw_dst, x.raw_val, x.raw_tie, rp, rc16);
+        else if (raw_local)
+            FL_LAUNCH("k_sp_items", (k_sp_items<false, true>), dim3(grid), dim3(SP_ITEMS_NT), 0, st, *ori, *inv,
+                      h->chunks, x.runs, holes, x.raw_dst, x.raw_val, x.raw_tie, rp, rc16);
+        else
+            FL_LAUNCH("k_sp_items", (k_sp_items<false, false>), dim3(grid), dim3(SP_ITEMS_NT), 0, st, *ori, *inv,
+                      h->chunks, x.runs, holes, x.raw_dst, x.raw_val, x.raw_tie, rp, rc16);
+    }
     int32_t *dst_arr = x.raw_dst, *raw_arr = nullptr;
     float *val_arr = x.raw_val;
     uint32_t *tie_arr = x.raw_tie;
@@ -2111,7 +2265,7 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h, const int64_t *out_base
     const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
     if (R * NB == 0) return FL_OK;
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
-    SpExp x = sp_exp_layout(h->items, h->tiles, R, NB, 0, h->aggregate, (char *)h->ws2);
+    SpExp x = sp_exp_layout(h->items, h->tiles, h->chunks, R, NB, 0, h->aggregate, (char *)h->ws2);
     SpRows rows{p.row_item0, p.tile_base, NB};
     FL_LAUNCH("k_sp_emit", k_sp_emit, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, (hipStream_t)stream, rows, h->L,
               x.base, NB > 1 ? x.part_dst : x.raw_dst, NB > 1 ? x.part_val : x.raw_val, out_base, out_b, out_l,

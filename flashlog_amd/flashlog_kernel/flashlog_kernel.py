@@ -915,6 +915,11 @@ class _SparseSides:
         return side
 
 
+# When a list, every sparse hop appends its plan's sizes to it as
+# {"nnz", "items", "chunks", "backward"} (for byte counts in measurements).
+plan_log = None
+
+
 class _SparseState:
     """A forward hop's saved pieces for the backward."""
 
@@ -958,10 +963,10 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         ws1 = torch.empty(max(lib.fl_sparse_plan_bytes(nnz, R, 0 if mode == _SPARSE_FIXED else r_size), 1),
                           dtype=torch.uint8, device=dev)
         h.ws1, h.ws1_bytes = ptr(ws1).value, ws1.numel()
-        plan = torch.empty(4, dtype=torch.int64, device=dev)
+        plan = torch.empty(5, dtype=torch.int64, device=dev)
         check(lib.fl_sparse_plan(st, ctypes.byref(sides.ori), ctypes.byref(sides.inv), ctypes.byref(h), ptr(plan)),
               "sparse_plan")
-        items, tiles, err, nb = plan.tolist()
+        items, tiles, err, nb, chunks = plan.tolist()
         if err == 2 and attempt == 0:
             # rows out of order: process them in row order, entries of a row in input order
             perm = torch.argsort(sp_b * L + sp_l, stable=True)
@@ -971,8 +976,10 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         if err:
             raise ValueError("sparse state index out of range for shape (%d, %d, %d)" % (B, L, E))
         break
-    h.items, h.tiles = items, tiles
-    ws2_bytes = lib.fl_sparse_expand_bytes(items, tiles, R, E, 1 if need_backward else 0, int(aggregate))
+    h.items, h.tiles, h.chunks = items, tiles, chunks
+    if plan_log is not None:
+        plan_log.append({"nnz": nnz, "items": items, "chunks": chunks, "backward": bool(need_backward)})
+    ws2_bytes = lib.fl_sparse_expand_bytes(items, tiles, chunks, R, E, 1 if need_backward else 0, int(aggregate))
     ws2 = torch.empty(max(ws2_bytes, 1), dtype=torch.uint8, device=dev)
     h.ws2, h.ws2_bytes = ptr(ws2).value, ws2.numel()
     out_base = torch.empty(R * nb + 1, dtype=torch.int64, device=dev)

@@ -228,7 +228,8 @@ int fl_dense_max_backward(void *stream, const fl_side *ori, const fl_side *inv,
  * fixed-relation rule step (flashlog_forward_sparse3d_fixed_relation_cuda,
  * flashlog.cu:1561-1741: row (b, l) follows operators[b*L + l], values
  * unchanged, no masks; w, n and wot_i unused, r_size = base relations).
- * items / tiles come from fl_sparse_plan's plan[0] / plan[1]. */
+ * items / tiles / chunks come from fl_sparse_plan's plan[0] / plan[1] /
+ * plan[4]. */
 typedef struct fl_sparse_hop {
     const int64_t *sp_b, *sp_l, *sp_e;  /* [nnz] */
     const float *sp_v;                 /* [nnz] */
@@ -268,6 +269,10 @@ typedef struct fl_sparse_hop {
                                           identity); needs n <= 32767.  The
                                           backward reads both instead of
                                           walking the groups again.          */
+    int64_t chunks;                    /* the plan's 64-item chunks (each
+                                          entry's items cut into chunks of
+                                          64), sizing the expansion's chunk
+                                          table                              */
 } fl_sparse_hop;
 
 /* Destination buckets per row (8192 entities each).  The sparse hop
@@ -283,16 +288,17 @@ size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R, int64_t r_size);
 /* Replaces the count kernels and the host .item() syncs of
  * flashlog_forward_sparse3d_topk_cuda / _alledges_cuda (flashlog.cu:
  * 1999-2241): per entry and side the c2 threshold (flashlog.cpp:12-35) and
- * item counts; plan (device int64[4]) receives {items, tiles, error,
- * buckets}.  error: 0 ok, 1 index out of range, 2 entries not sorted by row.
+ * item counts; plan (device int64[5]) receives {items, tiles, error,
+ * buckets, chunks} (chunks: the sum over entries of ceil(items / 64)).  error: 0 ok, 1 index out of range, 2 entries not sorted by row.
  * The caller reads plan after the stream completes. */
 int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv,
                    const fl_sparse_hop *h, int64_t *plan);
 
 /* Expansion workspace bytes (backward = 1 when raw_local will be kept;
  * aggregate as in fl_sparse_hop). */
-size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t R,
-                              int64_t E, int backward, int aggregate);
+size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t chunks,
+                              int64_t R, int64_t E, int backward,
+                              int aggregate);
 
 /* Replaces the fill kernels (flashlog.cu:1402-1559,1759-1854) and the
  * coalesce (flashlog_kernel.py:258-357 sum, :399-478 max): raw items in the
