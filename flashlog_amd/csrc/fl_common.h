@@ -32,25 +32,51 @@ __device__ __forceinline__ float fl_wave_sum_f32(float v) {
     return v;
 }
 
-// Inclusive prefix sum across the 64 lanes of a wave.
+// A lane's value moved by a DPP control (gfx9 encodings: row_shr:n =
+// 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143); lanes without a
+// source, or outside row_mask / bank_mask, receive 0.
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ int fl_dpp(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ long long fl_dpp64(long long v) {
+    const unsigned long long u = (unsigned long long)v;
+    const unsigned lo = (unsigned)fl_dpp<CTRL, ROW_MASK, BANK_MASK>((int)(unsigned)u);
+    const unsigned hi = (unsigned)fl_dpp<CTRL, ROW_MASK, BANK_MASK>((int)(unsigned)(u >> 32));
+    return (long long)(((unsigned long long)hi << 32) | lo);
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave with DPP moves: the
+// Hillis-Steele steps 1, 2, 4, 8 inside each row of 16 lanes, then row 0's
+// total into row 1 and row 2's into row 3 (row_bcast:15), then the total of
+// rows 0-1 into rows 2-3 (row_bcast:31).
 __device__ __forceinline__ int fl_wave_incl_scan_i32(int v) {
-    const int lane = fl_lane();
-#pragma unroll
-    for (int o = 1; o < FL_WAVE; o <<= 1) {
-        int t = __shfl_up(v, o, FL_WAVE);
-        if (lane >= o) v += t;
-    }
+    v += fl_dpp<0x111>(v);
+    v += fl_dpp<0x112>(v);
+    v += fl_dpp<0x114>(v);
+    v += fl_dpp<0x118>(v);
+    v += fl_dpp<0x142, 0xa>(v);
+    v += fl_dpp<0x143, 0xc>(v);
     return v;
 }
 
 __device__ __forceinline__ long long fl_wave_incl_scan_i64(long long v) {
-    const int lane = fl_lane();
-#pragma unroll
-    for (int o = 1; o < FL_WAVE; o <<= 1) {
-        long long t = __shfl_up(v, o, FL_WAVE);
-        if (lane >= o) v += t;
-    }
+    v += fl_dpp64<0x111>(v);
+    v += fl_dpp64<0x112>(v);
+    v += fl_dpp64<0x114>(v);
+    v += fl_dpp64<0x118>(v);
+    v += fl_dpp64<0x142, 0xa>(v);
+    v += fl_dpp64<0x143, 0xc>(v);
     return v;
+}
+
+// Lane l's 64-bit value, in scalar registers.
+__device__ __forceinline__ long long fl_readlane_i64(long long x, int l) {
+    const unsigned long long u = (unsigned long long)x;
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), l);
+    return (long long)(((unsigned long long)hi << 32) | lo);
 }
 
 // Block-wide exclusive scan of one int per thread (NT threads, NT % 64 == 0,

@@ -151,16 +151,32 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     double ws = 0.0;
     long long cap = 0, nel = 0;
     int emin = 1 << 20, emax = -(1 << 20);
-    for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
-        const float wv = wr[s.group_rel[g]];
-        const int32_t c = s.group_count[g];
-        if (wv > 0.0f && c > 0) {
-            cap += c;
-            ++nel;
-            ws = __dadd_rn(ws, (double)wv);
-            const int lo = sp_lsb_exp(wv), hi = (int)((__float_as_uint(wv) >> 23) & 0xFF) - 127;
-            emin = lo < emin ? lo : emin;
-            emax = hi > emax ? hi : emax;
+    // groups 4 windows at a time (the loads of a batch in flight together);
+    // each lane still visits its groups in order
+    for (int64_t gb = g0; gb < g1; gb += 4 * FL_WAVE) {
+        int rl[4];
+        int32_t cl[4];
+        float wl[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t g = gb + u * FL_WAVE + lane;
+            rl[u] = g < g1 ? s.group_rel[g] : 0;
+            cl[u] = g < g1 ? s.group_count[g] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wl[u] = gb + u * FL_WAVE + lane < g1 ? wr[rl[u]] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float wv = wl[u];
+            const int32_t c = cl[u];
+            if (wv > 0.0f && c > 0) {
+                cap += c;
+                ++nel;
+                ws = __dadd_rn(ws, (double)wv);
+                const int lo = sp_lsb_exp(wv), hi = (int)((__float_as_uint(wv) >> 23) & 0xFF) - 127;
+                emin = lo < emin ? lo : emin;
+                emax = hi > emax ? hi : emax;
+            }
         }
     }
     cap = fl_wave_sum_i64(cap);
@@ -196,10 +212,21 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     tk.wsum = ws;
     tk.target = q.target;
     long long alloc = 0;
-    for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
-        const float wv = wr[s.group_rel[g]];
-        const int32_t c = s.group_count[g];
-        if (wv > 0.0f && c > 0) alloc += sp_quota_base(tk, wv, c);
+    for (int64_t gb = g0; gb < g1; gb += 4 * FL_WAVE) {
+        int rl[4];
+        int32_t cl[4];
+        float wl[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t g = gb + u * FL_WAVE + lane;
+            rl[u] = g < g1 ? s.group_rel[g] : 0;
+            cl[u] = g < g1 ? s.group_count[g] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wl[u] = gb + u * FL_WAVE + lane < g1 ? wr[rl[u]] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (wl[u] > 0.0f && cl[u] > 0) alloc += sp_quota_base(tk, wl[u], cl[u]);
     }
     alloc = fl_wave_sum_i64(alloc);
     q.residual = q.target - alloc;
@@ -239,8 +266,8 @@ __device__ __forceinline__ long long sp_quota_window(SpTake &tk, float wv, long 
     const long long cum = sp_quota_cum(tk, tk.prefix + incl);
     const long long prev = __shfl_up(cum, 1, FL_WAVE);
     const long long extra = cum - (lane == 0 ? tk.cum : prev);
-    tk.prefix += fl_uniform_i64(__shfl(incl, FL_WAVE - 1, FL_WAVE));
-    tk.cum = fl_uniform_i64(__shfl(cum, FL_WAVE - 1, FL_WAVE));
+    tk.prefix += fl_readlane_i64(incl, FL_WAVE - 1);
+    tk.cum = fl_readlane_i64(cum, FL_WAVE - 1);
     return el ? base + extra : 0;
 }
 
@@ -273,7 +300,7 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
         if (__ballot(take > 0) == 0) continue;
         const long long incl = fl_wave_incl_scan_i64(take);
         fn((long long)take, start, rel, wv, (long long)(base + incl - take));
-        base += __shfl(incl, FL_WAVE - 1, FL_WAVE);
+        base += fl_readlane_i64(incl, FL_WAVE - 1);
     }
     return base;
 }
