@@ -12,16 +12,18 @@ __device__ __forceinline__ float fl_add(float a, float b) { return __fadd_rn(a, 
 
 __device__ __forceinline__ int fl_lane() { return threadIdx.x & (FL_WAVE - 1); }
 
+__device__ __forceinline__ int fl_wave_incl_scan_i32(int v);
+__device__ __forceinline__ long long fl_wave_incl_scan_i64(long long v);
+__device__ __forceinline__ long long fl_readlane_i64(long long x, int l);
+
+// Integer wave sums (any order gives the same total): the inclusive scan's
+// last lane, uniform in scalar registers.
 __device__ __forceinline__ int fl_wave_sum_i32(int v) {
-#pragma unroll
-    for (int o = FL_WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, FL_WAVE);
-    return v;
+    return __builtin_amdgcn_readlane(fl_wave_incl_scan_i32(v), FL_WAVE - 1);
 }
 
 __device__ __forceinline__ long long fl_wave_sum_i64(long long v) {
-#pragma unroll
-    for (int o = FL_WAVE / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, FL_WAVE);
-    return v;
+    return fl_readlane_i64(fl_wave_incl_scan_i64(v), FL_WAVE - 1);
 }
 
 // Butterfly sum of one float per lane (a fixed association, so the result
@@ -70,6 +72,9 @@ __device__ __forceinline__ long long fl_wave_incl_scan_i64(long long v) {
     v += fl_dpp64<0x143, 0xc>(v);
     return v;
 }
+
+// The previous lane's value (wave_shr:1); lane 0 receives 0.
+__device__ __forceinline__ long long fl_wave_shr1_i64(long long v) { return fl_dpp64<0x138>(v); }
 
 // Lane l's 64-bit value, in scalar registers.
 __device__ __forceinline__ long long fl_readlane_i64(long long x, int l) {

@@ -264,7 +264,7 @@ __device__ __forceinline__ long long sp_quota_window(SpTake &tk, float wv, long 
     const long long spare = el ? cnt - base : 0;
     const long long incl = fl_wave_incl_scan_i64(spare);
     const long long cum = sp_quota_cum(tk, tk.prefix + incl);
-    const long long prev = __shfl_up(cum, 1, FL_WAVE);
+    const long long prev = fl_wave_shr1_i64(cum);
     const long long extra = cum - (lane == 0 ? tk.cum : prev);
     tk.prefix += fl_readlane_i64(incl, FL_WAVE - 1);
     tk.cum = fl_readlane_i64(cum, FL_WAVE - 1);
