@@ -1623,21 +1623,72 @@ __global__ __launch_bounds__(SP_NT) void k_sp_emit(SpRows rows, int64_t L, const
 // ---------------------------------------------------------------------------
 // backward
 
+// After the accumulation: every raw item's output index, the index within
+// its (row, bucket) that the accumulation recorded plus the bucket's output
+// base (the losing items of the max stay -1).  With one bucket per row the
+// accumulation has compacted its outputs into raw_dst, so the destinations
+// are read only with several buckets (then holes of the sum become -1);
+// with one, holes keep an unspecified index and the backward skips them by
+// their mask.  Workgroup per tile of a row, as k_sp_hist.
+__global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows rows, const int32_t *__restrict__ raw_dst,
+                                                          const int64_t *__restrict__ out_base,
+                                                          int32_t *__restrict__ raw_local) {
+    const int64_t tile = blockIdx.x;
+    const int64_t r = sp_tile_row(rows.tile_base, R, tile);
+    const int64_t tl = tile - rows.tile_base[r];
+    const int64_t i0 = rows.row_item0[r] + tl * SP_TILE;
+    const int64_t i1e = rows.row_item0[r + 1];
+    const int c = (int)((i1e - i0) < SP_TILE ? (i1e - i0) : SP_TILE);
+    const int64_t *orow = out_base + r * rows.NB;
+    for (int idx = threadIdx.x; idx < c; idx += SP_NT) {
+        const int64_t k = i0 + idx;
+        const int32_t loc = raw_local[k];
+        if (rows.NB > 1) {
+            const int32_t d = raw_dst[k];
+            raw_local[k] = (loc >= 0 && d >= 0) ? (int32_t)(orow[d >> SP_S] + loc) : -1;
+        } else {
+            raw_local[k] = loc >= 0 ? (int32_t)(orow[0] + loc) : -1;
+        }
+    }
+}
+
+// Segmented inclusive sum of x over runs of equal key across the wave (runs
+// are contiguous), with DPP moves; lanes whose source is outside the wave
+// see key -1 + 1 = 0, which matches only the unused key -1 (x = 0 there).
+__device__ __forceinline__ float sp_dpp_add_if(float x, int key1, float y, int ky) {
+    return ky == key1 ? fl_add(x, y) : x;
+}
+template <int CTRL, int RM = 0xf>
+__device__ __forceinline__ float sp_seg_step(float x, int key1) {
+    const float y = __int_as_float(fl_dpp<CTRL, RM>(__float_as_int(x)));
+    const int ky = fl_dpp<CTRL, RM>(key1);
+    return sp_dpp_add_if(x, key1, y, ky);
+}
+__device__ __forceinline__ float sp_seg_scan(float x, int key) {
+    const int key1 = key + 1;
+    x = sp_seg_step<0x111>(x, key1);
+    x = sp_seg_step<0x112>(x, key1);
+    x = sp_seg_step<0x114>(x, key1);
+    x = sp_seg_step<0x118>(x, key1);
+    x = sp_seg_step<0x142, 0xa>(x, key1);
+    x = sp_seg_step<0x143, 0xc>(x, key1);
+    return x;
+}
+
 // Backward, wave per entry over the entry's raw items (raw order; the
-// forward recorded each one's CSR position and attention column):
-// grad_v[i] = sum over items of (g*m)*w, the identity item taken with m = 1
-// (flashlog.cu:1856-1959); grad_w[r, col] += (g*m)*a, summed per column
-// within each 64-item chunk (the items of a group are consecutive) and
-// added by atomics, as the reference adds its per-item terms.  Holes (sum:
-// masked kept edges) and, for max, the losing items (raw_local = -1) take
-// no part (flashlog.cu:2364-2410).
+// forward recorded each one's CSR position, attention column and output
+// index): grad_v[i] = sum over items of (g*m)*w, the identity item taken
+// with m = 1 (flashlog.cu:1856-1959); grad_w[r, col] += (g*m)*a, summed per
+// column within each 64-item chunk (the items of a group are consecutive)
+// and added by atomics, as the reference adds its per-item terms.  Holes
+// (sum: masked kept edges, m == 0) and, for max, the losing items (output
+// index -1) take no part (flashlog.cu:2364-2410).  The next chunk's records are
+// requested before the current chunk's gathers.
 __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
-                                                  const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
-                                                  const float *__restrict__ sv, int64_t nnz,
-                                                  const float *__restrict__ w, int64_t L, int64_t n, int64_t r_size,
-                                                  int holes, const int64_t *__restrict__ item_off, int64_t NB,
-                                                  const int64_t *__restrict__ out_base,
-                                                  const int32_t *__restrict__ raw_local,
+                                                  const int64_t *__restrict__ sl, const float *__restrict__ sv,
+                                                  int64_t nnz, const float *__restrict__ w, int64_t L, int64_t n,
+                                                  int64_t r_size, int holes, const int64_t *__restrict__ item_off,
+                                                  const int32_t *__restrict__ raw_out,
                                                   const int32_t *__restrict__ raw_pos,
                                                   const int16_t *__restrict__ raw_col,
                                                   const float *__restrict__ grad, float *__restrict__ grad_v,
@@ -1645,48 +1696,53 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
     const int lane = fl_lane();
     const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
     if (i >= nnz) return;
-    const int64_t src = se[i];
     const int64_t r = sb[i] * L + sl[i];
     const float a = sv[i];
     const float *wrow = w + r * n;
-    const int64_t *orow = out_base + r * NB;
     const int64_t k0 = item_off[i], k1 = item_off[i + 1];
+    const bool edge_grads = ori.grad_edge || inv.grad_edge;
     float gsp = 0.0f;
+    int32_t p = -1, loc = -1;
+    int col = -1;
+    if (k0 + lane < k1) {
+        p = raw_pos[k0 + lane];
+        col = raw_col[k0 + lane];
+        loc = raw_out[k0 + lane];
+    }
     for (int64_t kb = k0; kb < k1; kb += FL_WAVE) {
-        const int64_t k = kb + lane;
-        int col = -1;
+        const int64_t kn = kb + FL_WAVE + lane;
+        int32_t pn = -1, locn = -1;
+        int coln = -1;
+        if (kn < k1) {
+            pn = raw_pos[kn];
+            coln = raw_col[kn];
+            locn = raw_out[kn];
+        }
         float gwv = 0.0f;
-        if (k < k1) {
-            const int32_t p = raw_pos[k];
-            col = raw_col[k];
-            const bool iv = p >= 0 && col >= r_size;
-            const fl_side &s = iv ? inv : ori;
-            const float m = p >= 0 ? s.mask[p] : 1.0f;
-            const int32_t loc = (p < 0 || !holes || m != 0.0f) ? raw_local[k] : -1;
-            if (loc >= 0) {
-                const int32_t d = p >= 0 ? s.col_ind[p] : (int32_t)src;
-                const float gv = grad[orow[d >> SP_S] + loc];
-                const float wv = wrow[col];
-                const float gm = fl_mul(gv, m);
-                gsp = fl_add(gsp, fl_mul(gm, wv));
-                gwv = fl_mul(gm, a);
-                if (p >= 0 && s.grad_edge) {
+        const bool iv = p >= 0 && col >= r_size;
+        const float m = (loc >= 0 && p >= 0) ? (iv ? inv.mask : ori.mask)[p] : 1.0f;
+        if (loc >= 0 && !(holes && p >= 0 && m == 0.0f)) {
+            const float gv = grad[loc];
+            const float wv = wrow[col];
+            const float gm = fl_mul(gv, m);
+            gsp = fl_add(gsp, fl_mul(gm, wv));
+            gwv = fl_mul(gm, a);
+            if (edge_grads && p >= 0) {
+                const fl_side &s = iv ? inv : ori;
+                if (s.grad_edge) {
                     const float ge = fl_mul(fl_mul(fl_mul(fl_mul(gv, a), wv), m), s.dscore[p]);
                     if (ge != 0.0f) atomicAdd(&s.grad_edge[s.order[p]], ge);
                 }
             }
         }
         // per-column sums of this chunk (segmented scan keyed by the column)
-        float x = gwv;
-#pragma unroll
-        for (int o = 1; o < FL_WAVE; o <<= 1) {
-            const float y = __shfl_up(x, o, FL_WAVE);
-            const int sy = __shfl_up(col, o, FL_WAVE);
-            if (lane >= o && sy == col) x = fl_add(x, y);
-        }
-        const int snext = __shfl_down(col, 1, FL_WAVE);
-        const bool tail = lane == FL_WAVE - 1 || snext != col;
+        const float x = sp_seg_scan(gwv, col);
+        const int next1 = fl_dpp<0x130>(col + 1);  // wave_shl:1, lane 63 receives 0
+        const bool tail = next1 != col + 1;
         if (col >= 0 && tail && x != 0.0f) atomicAdd(&grad_w[r * n + col], x);
+        p = pn;
+        col = coln;
+        loc = locn;
     }
     gsp = fl_wave_sum_f32(gsp);
     if (lane == 0) grad_v[i] = gsp;
@@ -2209,6 +2265,7 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         if (!h->raw_pos || !h->raw_col)
             return fl_fail(FL_ERR_ARG, "sparse_expand: raw_local needs raw_pos and raw_col");
         if (h->n > 32767) return fl_fail(FL_ERR_ARG, "sparse_expand: backward columns need n <= 32767");
+        if (h->items > INT32_MAX) return fl_fail(FL_ERR_ARG, "sparse_expand: backward output indices need items < 2^31");
     }
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     SpExp x = sp_exp_layout(h->items, h->tiles, h->chunks, R, NB, raw_local != nullptr, h->aggregate,
@@ -2283,6 +2340,10 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
                   val_arr, raw_arr, raw_local, x.out_count, x.hot_list, x.hot_count);
     }
     if ((rc = exclusive_scan(st, x.out_count, out_base, R * NB, x.tmp)) != FL_OK) return rc;
+    // the backward's map: each raw item's output index
+    if (raw_local && h->tiles > 0)
+        FL_LAUNCH("k_sp_local_to_out", k_sp_local_to_out, dim3((unsigned)h->tiles), dim3(SP_NT), 0, st, R, rows,
+                  x.raw_dst, out_base, raw_local);
     return fl_check_launch("sparse_expand");
 }
 
@@ -2315,11 +2376,12 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
     if (R * h->n > 0)
         FL_LAUNCH("k_fill_f32", k_fill_f32, dim3((unsigned)((R * h->n + 255) / 256)), dim3(256), 0, st, grad_w,
                   R * h->n, 0.0f);
+    (void)NB;
     if (h->nnz > 0)
         FL_LAUNCH("k_sp_bwd", k_sp_bwd, dim3((unsigned)((h->nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
-                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, h->nnz, h->w, h->L, h->n,
-                  h->r_size, (h->mode == SP_TOPK && h->aggregate == SP_SUM) ? 1 : 0, p.item_off, NB, out_base,
-                  raw_local, h->raw_pos, h->raw_col, grad_out, grad_v, grad_w);
+                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_v, h->nnz, h->w, h->L, h->n, h->r_size,
+                  (h->mode == SP_TOPK && h->aggregate == SP_SUM) ? 1 : 0, p.item_off, raw_local, h->raw_pos,
+                  h->raw_col, grad_out, grad_v, grad_w);
     return fl_check_launch("sparse_backward");
 }
 

@@ -305,9 +305,10 @@ size_t fl_sparse_expand_bytes(int64_t items, int64_t tiles, int64_t chunks,
  * CPU path's order (flashlog.cpp:1388-1486), grouped per (row, destination)
  * and added to 0 in that order (sum) or reduced to the winning item (max).
  * out_base [B*L*buckets + 1] receives the output offsets of every (row,
- * bucket) (out_base[last] = output count); raw_local (optional, [items]) the
- * output index of every raw item within its bucket (max: of the winning
- * items; -1 for the others), for fl_sparse_backward. */
+ * bucket) (out_base[last] = output count); raw_local (optional, [items],
+ * needs items < 2^31) the output index of every raw item (-1 for the losing
+ * items of the max; unspecified for the holes of the sum, which the backward
+ * recognises by their mask), for fl_sparse_backward. */
 int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv,
                      const fl_sparse_hop *h, int64_t *out_base,
                      int32_t *raw_local);
