@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 13
+ABI_VERSION = 14
 FL_SEG = 32
 FL_SUP = 16
 
@@ -50,6 +50,7 @@ class FlSide(ctypes.Structure):
         ("order", ctypes.c_void_p),
         ("dscore", ctypes.c_void_p),
         ("grad_edge", ctypes.c_void_p),
+        ("mask_bits", ctypes.c_void_p),
     ]
 
 
@@ -119,6 +120,7 @@ _SIGS = {
     "fl_sparse_plan_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     "fl_sparse_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                       ctypes.POINTER(FlSparseHop), ctypes.c_void_p]),
+    "fl_mask_bits": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]),
     "fl_sparse_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 5 + [ctypes.c_int] * 2),
     "fl_sparse_expand": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                         ctypes.POINTER(FlSparseHop), ctypes.c_void_p, ctypes.c_void_p]),

@@ -632,6 +632,12 @@ struct SpRows {
     int64_t NB;                // buckets per row
 };
 
+// Mask of position p on a side: its bit when the side has a bitmap (every
+// mask value 0 or 1), else the mask value.
+__device__ __forceinline__ float sp_mask_at(const uint32_t *bits, const float *mask, int64_t p) {
+    return bits ? (((bits[p >> 5] >> (p & 31)) & 1u) ? 1.0f : 0.0f) : mask[p];
+}
+
 // Raw items are written in two passes.  k_sp_runs (wave per entry) walks
 // the entry's groups as the plan did and writes one descriptor per kept
 // group (a run: the group's first take edges, at consecutive item slots)
@@ -787,9 +793,10 @@ __global__ __launch_bounds__(SP_ITEMS_NT) void k_sp_items(fl_side ori, fl_side i
             const bool inv_side = (mj & SP_RUN_INV) != 0;
             const int64_t edges = inv_side ? inv.edges : ori.edges;
             const float *mk = inv_side ? inv.mask : ori.mask;
+            const uint32_t *mb = inv_side ? inv.mask_bits : ori.mask_bits;
             const int32_t *ci = inv_side ? inv.col_ind : ori.col_ind;
             if (pj >= 0 && pj < edges) {
-                const float m = mk[pj];
+                const float m = sp_mask_at(mb, mk, pj);
                 const int32_t e = ci[pj];
                 dst = (!holes || m != 0.0f) ? e : -1;
                 val = fl_mul(awj, m);
@@ -1720,7 +1727,8 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
         }
         float gwv = 0.0f;
         const bool iv = p >= 0 && col >= r_size;
-        const float m = (loc >= 0 && p >= 0) ? (iv ? inv.mask : ori.mask)[p] : 1.0f;
+        const float m =
+            (loc >= 0 && p >= 0) ? sp_mask_at(iv ? inv.mask_bits : ori.mask_bits, iv ? inv.mask : ori.mask, p) : 1.0f;
         if (loc >= 0 && !(holes && p >= 0 && m == 0.0f)) {
             const float gv = grad[loc];
             const float wv = wrow[col];
@@ -1746,6 +1754,17 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
     }
     gsp = fl_wave_sum_f32(gsp);
     if (lane == 0) grad_v[i] = gsp;
+}
+
+// Mask bitmap: thread per position, one ballot per 64 positions.
+__global__ void k_mask_bits(const float *__restrict__ mask, int64_t n, uint32_t *__restrict__ bits) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t b = __ballot(p < n && mask[p] != 0.0f);
+    const int lane = fl_lane();
+    const int64_t w0 = (p - lane) >> 5;  // first word of this wave's 64 positions
+    const int64_t nw = (n + 31) >> 5;
+    if (lane == 0 && w0 < nw) bits[w0] = (uint32_t)b;
+    if (lane == 32 && w0 + 1 < nw) bits[w0 + 1] = (uint32_t)(b >> 32);
 }
 
 __global__ void k_fill_i32(int32_t *__restrict__ p, int64_t n, int32_t v) {
@@ -2383,6 +2402,15 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
                   (h->mode == SP_TOPK && h->aggregate == SP_SUM) ? 1 : 0, p.item_off, raw_local, h->raw_pos,
                   h->raw_col, grad_out, grad_v, grad_w);
     return fl_check_launch("sparse_backward");
+}
+
+int fl_mask_bits(void *stream, const float *mask, int64_t n, uint32_t *bits) {
+    if (n < 0) return fl_fail(FL_ERR_ARG, "mask_bits: negative length");
+    if (n == 0) return FL_OK;
+    if (!mask || !bits) return fl_fail(FL_ERR_ARG, "mask_bits: null pointer");
+    FL_LAUNCH("k_mask_bits", k_mask_bits, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, mask,
+              n, bits);
+    return fl_check_launch("mask_bits");
 }
 
 int fl_sparse_topc(void *stream, const int64_t *sp_b, const int64_t *sp_l, const float *v, int64_t nnz, int64_t B,

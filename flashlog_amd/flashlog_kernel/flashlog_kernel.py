@@ -875,10 +875,12 @@ class _SparseSides:
 
     def __init__(self, ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount,
                  inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, ori_order=None, inv_order=None,
-                 ori_dscore=None, inv_dscore=None):
+                 ori_dscore=None, inv_dscore=None, ori_bits=None, inv_bits=None):
         self.keep = []
-        self.ori = self._side(ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount, ori_order, ori_dscore)
-        self.inv = self._side(inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, inv_order, inv_dscore)
+        self.ori = self._side(ori_col, ori_mask, ori_gptr, ori_grel, ori_gstart, ori_gcount, ori_order, ori_dscore,
+                              ori_bits)
+        self.inv = self._side(inv_col, inv_mask, inv_gptr, inv_grel, inv_gstart, inv_gcount, inv_order, inv_dscore,
+                              inv_bits)
 
     def set_grad_edge(self, grad_edge):
         """Points both sides' edge-weight gradient at grad_edge (or None)."""
@@ -886,7 +888,7 @@ class _SparseSides:
         self.ori.grad_edge = p
         self.inv.grad_edge = p
 
-    def _side(self, col, mask, gptr, grel, gstart, gcount, order=None, dscore=None):
+    def _side(self, col, mask, gptr, grel, gstart, gcount, order=None, dscore=None, bits=None):
         _require_cuda(col, gptr, grel, gstart, gcount)
         col = col.int().contiguous()
         gptr = gptr.int().contiguous()
@@ -903,8 +905,11 @@ class _SparseSides:
             order = order.int().contiguous()
             if order.numel() != col.numel():
                 raise ValueError("order length must equal the number of CSR positions")
-        self.keep += [col, mask, gptr, grel, gstart, gcount, order, dscore]
+        if bits is not None and (mask is None or bits.numel() < (col.numel() + 31) // 32):
+            raise ValueError("mask bits must cover every CSR position of a masked side")
+        self.keep += [col, mask, gptr, grel, gstart, gcount, order, dscore, bits]
         side = FlSide()
+        side.mask_bits = ptr(bits).value if bits is not None else None
         side.edges, side.groups = col.numel(), grel.numel()
         side.order = ptr(order).value if order is not None else None
         side.dscore = ptr(dscore).value if dscore is not None else None
@@ -1154,10 +1159,20 @@ def _coo(idx, vals, B, L, E):
 _MASK_CACHE = {}
 
 
+def _mask_bits(mask_f):
+    """One bit per CSR position (mask != 0), for masks of 0s and 1s."""
+    n = mask_f.numel()
+    bits = torch.empty(max((n + 31) // 32, 1), dtype=torch.int32, device=mask_f.device)
+    check(_lib.lib().fl_mask_bits(_stream(mask_f), ptr(mask_f), n, ptr(bits)), "mask_bits")
+    return bits
+
+
 def _cached_mask_order(mask_values, order):
-    """mask[order] as float, reused while the same (unmodified) mask and
-    order tensors are passed again (the top-k hop gets the raw per-edge mask
-    on every call; without edge weights its CSR-ordered form is fixed)."""
+    """(mask[order] as float, its bitmap when mask_values is bool -- every
+    value then 0 or 1 -- else None), reused while the same (unmodified) mask
+    and order tensors are passed again (the top-k hop gets the raw per-edge
+    mask on every call; without edge weights its CSR-ordered form is
+    fixed)."""
     key = (mask_values.data_ptr(), mask_values._version, mask_values.numel(), order.data_ptr(), order._version,
            order.numel())
     hit = _MASK_CACHE.get(key)
@@ -1166,8 +1181,9 @@ def _cached_mask_order(mask_values, order):
     for k in [k for k, v in _MASK_CACHE.items() if v[0]() is None or v[1]() is None]:
         del _MASK_CACHE[k]
     out = _apply_mask_order(mask_values.contiguous().view(-1), order, None)
-    _MASK_CACHE[key] = (weakref.ref(mask_values), weakref.ref(order), out)
-    return out
+    bits = _mask_bits(out) if mask_values.dtype == torch.bool else None
+    _MASK_CACHE[key] = (weakref.ref(mask_values), weakref.ref(order), (out, bits))
+    return out, bits
 
 
 class FlashLogFunctionSparse3DAllEdgesSum(autograd.Function):
@@ -1215,13 +1231,14 @@ def _topk_hop_forward(ctx, aggregate, sp_batch, sp_level, sp_entity, sp_value, w
     sp_batch, sp_level, sp_entity, sp_value = _prune_sparse_sources(
         ctx, sp_batch, sp_level, sp_entity, sp_value, topk_nodes, w.size(1), sampling)
     mask_f = mask_values.contiguous().view(-1)
+    ori_bits = inv_bits = None
     if weight is not None and edge_weight_is_score:
         m = mask_f.float() * weight.to(device=mask_f.device, dtype=torch.float).view(-1)
         ori_mask = m[ori_order.long()].contiguous()
         inv_mask = m[inv_order.long()].contiguous()
     elif weight is None:
-        ori_mask = _cached_mask_order(mask_values, ori_order)
-        inv_mask = _cached_mask_order(mask_values, inv_order)
+        ori_mask, ori_bits = _cached_mask_order(mask_values, ori_order)
+        inv_mask, inv_bits = _cached_mask_order(mask_values, inv_order)
     else:
         ori_mask = _apply_mask_order(mask_f, ori_order, weight)
         inv_mask = _apply_mask_order(mask_f, inv_order, weight)
@@ -1234,7 +1251,8 @@ def _topk_hop_forward(ctx, aggregate, sp_batch, sp_level, sp_entity, sp_value, w
     sides = _SparseSides(ori_col_ind, ori_mask, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
                          ori_group_edge_count, inv_col_ind, inv_mask, inv_row_group_ptr, inv_group_rel,
                          inv_group_edge_start, inv_group_edge_count,
-                         ori_order if with_order else None, inv_order if with_order else None, *dscore)
+                         ori_order if with_order else None, inv_order if with_order else None, *dscore,
+                         ori_bits=ori_bits, inv_bits=inv_bits)
     seed = int(torch.randint(0, 2 ** 63 - 1, ()).item()) if sampling else -1
     need = bool(any(ctx.needs_input_grad))
     idx, vals, state = _sparse_forward(sp_batch, sp_level, sp_entity, sp_value, w, sides, B, L, E, r_size,

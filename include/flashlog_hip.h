@@ -77,6 +77,11 @@ typedef struct fl_side {
     float *grad_edge;              /* optional: [edges] gradient of the edge
                                       weights by original edge id (both
                                       sides may share it)                  */
+    const uint32_t *mask_bits;     /* optional: [ceil(M/32)] bit p = mask[p]
+                                      != 0, set only when every mask value
+                                      is 0 or 1 (fl_mask_bits); the sparse
+                                      hop then tests bits instead of reading
+                                      mask                                  */
 } fl_side;
 
 const char *fl_last_error(void);
@@ -120,6 +125,13 @@ int fl_pull_segments(int64_t nodes, const int32_t *pull_ptr, int64_t *nseg,
 int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool,
                   const int32_t *order, const float *weight, float *out,
                   int64_t nnz);
+
+/* bits[w] bit j = (mask[32w + j] != 0) for the n positions of a CSR-ordered
+ * mask (bits: ceil(n/32) words): a side's mask_bits, for masks whose values
+ * are all 0 or 1 (a bool visibility mask without edge weights).  No
+ * counterpart in the reference: a compact copy of the mask the sparse
+ * kernels gather from. */
+int fl_mask_bits(void *stream, const float *mask, int64_t n, uint32_t *bits);
 
 /* out[i] = 1 - sigmoid(weight[order[i]]) for i < nnz: the per-position edge
  * score derivative factor of the sparse backward with trainable edge

@@ -373,3 +373,17 @@ def test_topk_many_groups(K, ties, agg):
     else:
         out, v, wt = _max(state, w, csr, mbool, B, L, E, R, K, grad=True)
         _check_max(out, v, wt, state, w, csr, masks, B, L, E, R, n, K, False, rng)
+
+
+@pytest.mark.parametrize("n", [1, 31, 64, 1000, 4097])
+def test_mask_bits_match_packbits(n):
+    """fl_mask_bits: bit j of word w = mask[32w + j] != 0 (little-endian bit
+    order within each 32-bit word), the tail of the last word zero."""
+    fk = _fk()
+    rng = np.random.default_rng(n)
+    mask = (rng.random(n) < 0.7).astype(np.float32)
+    got = fk._mask_bits(torch.from_numpy(mask).cuda()).cpu().numpy().view(np.uint32)
+    padded = np.zeros(((n + 31) // 32) * 32, np.uint8)
+    padded[:n] = mask != 0
+    want = np.packbits(padded, bitorder="little").view(np.uint32)
+    np.testing.assert_array_equal(got[: want.size], want)
