@@ -1691,19 +1691,67 @@ __device__ __forceinline__ float sp_seg_scan(float x, int key) {
 // (sum: masked kept edges, m == 0) and, for max, the losing items (output
 // index -1) take no part (flashlog.cu:2364-2410).  The next chunk's records are
 // requested before the current chunk's gathers.
+// Workgroup per BW_EPB consecutive entries (rows ascending): the per-column
+// sums of entries in the range's first or last row are added into LDS
+// copies of those two grad_w rows and flushed once per workgroup; entries of
+// rows strictly inside the range add to grad_w directly.
+constexpr int BW_EPB = 128;
+constexpr int64_t BW_LDS_MAX_N = 4096;  // columns of the LDS rows (2 * 4 * n bytes)
+
+__device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
+                                             const int64_t *__restrict__ sl, const float *__restrict__ sv,
+                                             const float *__restrict__ w, int64_t L, int64_t n, int64_t r_size,
+                                             int holes, const int64_t *__restrict__ item_off,
+                                             const int32_t *__restrict__ raw_out,
+                                             const int32_t *__restrict__ raw_pos,
+                                             const int16_t *__restrict__ raw_col, const float *__restrict__ grad,
+                                             float *__restrict__ grad_v, float *__restrict__ grad_w, int64_t i,
+                                             float *acc, int64_t rowa, int64_t rowb);
+
 __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                   const int64_t *__restrict__ sl, const float *__restrict__ sv,
                                                   int64_t nnz, const float *__restrict__ w, int64_t L, int64_t n,
-                                                  int64_t r_size, int holes, const int64_t *__restrict__ item_off,
+                                                  int64_t r_size, int holes, int use_lds,
+                                                  const int64_t *__restrict__ item_off,
                                                   const int32_t *__restrict__ raw_out,
                                                   const int32_t *__restrict__ raw_pos,
                                                   const int16_t *__restrict__ raw_col,
                                                   const float *__restrict__ grad, float *__restrict__ grad_v,
                                                   float *__restrict__ grad_w) {
+    extern __shared__ float bw_acc[];  // [2][n] when use_lds
+    const int64_t e0 = (int64_t)blockIdx.x * BW_EPB;
+    const int64_t e1 = e0 + BW_EPB < nnz ? e0 + BW_EPB : nnz;
+    const int64_t rowa = sb[e0] * L + sl[e0], rowb = sb[e1 - 1] * L + sl[e1 - 1];
+    if (use_lds) {
+        for (int64_t q = threadIdx.x; q < 2 * n; q += SEL_NT) bw_acc[q] = 0.0f;
+        __syncthreads();
+    }
+    for (int64_t i = e0 + threadIdx.x / FL_WAVE; i < e1; i += SEL_NT / FL_WAVE)
+        sp_bwd_entry(ori, inv, sb, sl, sv, w, L, n, r_size, holes, item_off, raw_out, raw_pos, raw_col, grad, grad_v,
+                     grad_w, i, use_lds ? bw_acc : nullptr, rowa, rowb);
+    if (use_lds) {
+        __syncthreads();
+        for (int64_t q = threadIdx.x; q < 2 * n; q += SEL_NT) {
+            const float x = bw_acc[q];
+            const int64_t row = q < n ? rowa : rowb;
+            if (x != 0.0f && (q < n || rowb != rowa)) atomicAdd(&grad_w[row * n + (q < n ? q : q - n)], x);
+        }
+    }
+}
+
+__device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
+                                             const int64_t *__restrict__ sl, const float *__restrict__ sv,
+                                             const float *__restrict__ w, int64_t L, int64_t n, int64_t r_size,
+                                             int holes, const int64_t *__restrict__ item_off,
+                                             const int32_t *__restrict__ raw_out,
+                                             const int32_t *__restrict__ raw_pos,
+                                             const int16_t *__restrict__ raw_col, const float *__restrict__ grad,
+                                             float *__restrict__ grad_v, float *__restrict__ grad_w, int64_t i,
+                                             float *acc, int64_t rowa, int64_t rowb) {
     const int lane = fl_lane();
-    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
-    if (i >= nnz) return;
     const int64_t r = sb[i] * L + sl[i];
+    // where this entry's per-column sums go: an LDS row or grad_w
+    float *gdst = acc ? (r == rowa ? acc : (r == rowb ? acc + n : nullptr)) : nullptr;
     const float a = sv[i];
     const float *wrow = w + r * n;
     const int64_t k0 = item_off[i], k1 = item_off[i + 1];
@@ -1747,7 +1795,10 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
         const float x = sp_seg_scan(gwv, col);
         const int next1 = fl_dpp<0x130>(col + 1);  // wave_shl:1, lane 63 receives 0
         const bool tail = next1 != col + 1;
-        if (col >= 0 && tail && x != 0.0f) atomicAdd(&grad_w[r * n + col], x);
+        if (col >= 0 && tail && x != 0.0f) {
+            if (gdst) atomicAdd(&gdst[col], x);
+            else atomicAdd(&grad_w[r * n + col], x);
+        }
         p = pn;
         col = coln;
         loc = locn;
@@ -2396,11 +2447,12 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
         FL_LAUNCH("k_fill_f32", k_fill_f32, dim3((unsigned)((R * h->n + 255) / 256)), dim3(256), 0, st, grad_w,
                   R * h->n, 0.0f);
     (void)NB;
+    const int use_lds = h->n <= BW_LDS_MAX_N;
     if (h->nnz > 0)
-        FL_LAUNCH("k_sp_bwd", k_sp_bwd, dim3((unsigned)((h->nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
-                  dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_v, h->nnz, h->w, h->L, h->n, h->r_size,
-                  (h->mode == SP_TOPK && h->aggregate == SP_SUM) ? 1 : 0, p.item_off, raw_local, h->raw_pos,
-                  h->raw_col, grad_out, grad_v, grad_w);
+        FL_LAUNCH("k_sp_bwd", k_sp_bwd, dim3((unsigned)((h->nnz + BW_EPB - 1) / BW_EPB)), dim3(SEL_NT),
+                  use_lds ? sizeof(float) * 2 * (size_t)h->n : 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_v, h->nnz,
+                  h->w, h->L, h->n, h->r_size, (h->mode == SP_TOPK && h->aggregate == SP_SUM) ? 1 : 0, use_lds,
+                  p.item_off, raw_local, h->raw_pos, h->raw_col, grad_out, grad_v, grad_w);
     return fl_check_launch("sparse_backward");
 }
 
