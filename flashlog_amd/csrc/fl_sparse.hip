@@ -283,24 +283,40 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
                                                 SpTake &tk, F &&fn) {
     const int lane = fl_lane();
     int64_t base = 0;
+    // the next window's group records are requested before this window's
+    // weights are gathered and its takes computed
+    int rel = 0;
+    int32_t start = 0, cnt = 0;
+    if (g0 + lane < g1) {
+        rel = s.group_rel[g0 + lane];
+        start = s.group_start[g0 + lane];
+        cnt = s.group_count[g0 + lane];
+    }
     for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
-        const int64_t g = gb + lane;
-        int64_t take = 0, start = 0, cnt = 0;
-        int rel = 0;
+        const int64_t g = gb + lane, gn = g + FL_WAVE;
+        int reln = 0;
+        int32_t startn = 0, cntn = 0;
+        if (gn < g1) {
+            reln = s.group_rel[gn];
+            startn = s.group_start[gn];
+            cntn = s.group_count[gn];
+        }
+        int64_t take = 0;
         float wv = 0.0f;
         if (g < g1) {
-            rel = s.group_rel[g];
             wv = wr[rel];
-            start = s.group_start[g];
-            cnt = s.group_count[g];
             take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? group_take(wv, tk.th, tk.cut, start, cnt) : 0);
         }
         if (Q && tk.kind == TAKE_QUOTA)
             take = sp_quota_window(tk, wv, cnt, g < g1);
-        if (__ballot(take > 0) == 0) continue;
-        const long long incl = fl_wave_incl_scan_i64(take);
-        fn((long long)take, start, rel, wv, (long long)(base + incl - take));
-        base += fl_readlane_i64(incl, FL_WAVE - 1);
+        if (__ballot(take > 0) != 0) {
+            const long long incl = fl_wave_incl_scan_i64(take);
+            fn((long long)take, (int64_t)start, rel, wv, (long long)(base + incl - take));
+            base += fl_readlane_i64(incl, FL_WAVE - 1);
+        }
+        rel = reln;
+        start = startn;
+        cnt = cntn;
     }
     return base;
 }
@@ -1695,7 +1711,7 @@ __device__ __forceinline__ float sp_seg_scan(float x, int key) {
 // sums of entries in the range's first or last row are added into LDS
 // copies of those two grad_w rows and flushed once per workgroup; entries of
 // rows strictly inside the range add to grad_w directly.
-constexpr int BW_EPB = 128;
+constexpr int BW_EPB = 64;
 constexpr int64_t BW_LDS_MAX_N = 4096;  // columns of the LDS rows (2 * 4 * n bytes)
 
 __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
