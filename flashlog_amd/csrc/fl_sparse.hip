@@ -1711,7 +1711,7 @@ __device__ __forceinline__ float sp_seg_scan(float x, int key) {
 // sums of entries in the range's first or last row are added into LDS
 // copies of those two grad_w rows and flushed once per workgroup; entries of
 // rows strictly inside the range add to grad_w directly.
-constexpr int BW_EPB = 64;
+constexpr int BW_EPB = 32;
 constexpr int64_t BW_LDS_MAX_N = 4096;  // columns of the LDS rows (2 * 4 * n bytes)
 
 __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
