@@ -14,7 +14,9 @@ graph and queries are synthetic and seeded (flashlog_amd/synth.py).
 --mode eval: the evaluation pass (c1/c2 thresholds, no gradients).
 --config 2: configs[1] (C2), the dense DRUM hop (dense_csr_sum_cuda,
 flashlog_kernel.py:1629-1663) with c1=1000, c2=400 and the model's
-normalization.
+normalization.  --config 4: configs[3] (C4), the mmDRUM dense max hop with
+its backward and the 5k-query filtered ranking.  --grounding: the soft
+grounding sampler on the C3 graph.  --rules: C3's rule-bank scoring.
 
 Prints one JSON line.  ``value`` = queries/sec (batch / step time) with all
 inputs resident in HBM.  ``roofline`` is for the propagation kernel (k_sp_items
@@ -48,6 +50,8 @@ def parse():
                     help="the DRUM --sparse GPU path (default for --config 5)")
     ap.add_argument("--grounding", action="store_true",
                     help="soft grounding (rule extraction's walk sampler) on the C3 graph")
+    ap.add_argument("--rules", action="store_true",
+                    help="rule-bank scoring (rules/shared_inference.score) on the C3 graph")
     ap.add_argument("--mode", choices=["train", "eval"], default="train",
                     help="--sparse step: a training step (sampled hops, loss, backward; the default, as "
                          "configs[4] is quoted forward and backward) or an evaluation pass")
@@ -137,6 +141,8 @@ def main():
         copy_calibration(args.copy_mb)
     if args.grounding:
         return main_grounding(args)
+    if args.rules:
+        return main_rules(args)
     if args.sparse or args.config == 5:
         return main_sparse(args)
     if args.config == 4:
@@ -529,6 +535,90 @@ def main_grounding(args):
         "kernel_ms_per_call": per_call,
         "roofline": None,
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+def main_rules(args):
+    """Rule-bank scoring (rules/shared_inference.py:12-245, called once per head
+    relation by rules/evaluate.py:521-527) on BASELINE configs[2] (C3: 14.5k
+    entities, 237 relations, 272k triples): 20k random rules with bodies of
+    1-3 directed relations and uniform(0, 1) weights for 3 ranks, spread over
+    the directed head relations; 5k (source, head) queries, each head's
+    sources scored against its rules (sum reduction, paths counted, chunks of
+    64 rules).  value = queries/s over the whole pass."""
+    import numpy as np
+    import torch
+    from flashlog_amd import _lib, synth
+    from flashlog_amd.flashlog_kernel import flashlog_kernel as fk
+    from flashlog_amd.rules import shared_inference
+    sys.path.insert(0, ROOT)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    h, r, t, E, R = synth.make_graph(3)
+    csr = fk.build_csr_structure(*(torch.from_numpy(a).to(dev) for a in (h, t, r)), E)
+    rng = np.random.Generator(np.random.PCG64(1234 + 33))
+    NR, NQ, RANKS, CHUNK = 20000, 5000, 3, 64
+    rule_head = rng.integers(0, 2 * R, NR)
+    bodies = [[int(x) for x in rng.integers(0, 2 * R, int(rng.integers(1, 4)))] for _ in range(NR)]
+    weights = rng.random((NR, RANKS)).astype(np.float32)
+    by_head = {}
+    for k in range(NR):
+        by_head.setdefault(int(rule_head[k]), []).append(k)
+    heads = np.array(sorted(by_head), np.int64)
+    q_head = rng.choice(heads, NQ)
+    q_src = h[rng.integers(0, h.shape[0], NQ)]
+    groups = []
+    for hd in np.unique(q_head):
+        ks = by_head[int(hd)]
+        rules = [{"body": bodies[k], "rank_weights": [float(x) for x in weights[k]]} for k in ks]
+        srcs = torch.from_numpy(q_src[q_head == hd].astype(np.int64)).to(dev)
+        groups.append((int(hd), srcs, rules, ks))
+
+    def run():
+        return [shared_inference.score(None, srcs, rules, csr, R, E, CHUNK) for _, srcs, rules, _ in groups]
+
+    for _ in range(max(args.warmup, 1)):
+        run()
+    torch.cuda.synchronize()
+    reps = max(1, min(args.steps, 5))
+    kn = ["k_fx_count", "k_fx_fill", "k_sp_hist", "k_sp_partition", "k_sp_accum_small", "k_sp_accum_mid",
+          "k_sp_accum_hot", "k_sp_emit", "k_rule_accum", "k_rule_rowsum", "k_rule_combine"]
+    _lib.prof_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    el = (time.perf_counter() - t0) / reps
+    prof = {k: _lib.prof_read(k) for k in kn}
+    _lib.prof_enable(False)
+    per_pass = {k: v[0] / reps for k, v in prof.items()}
+    print("rules: %.1f ms per pass of %d queries x %d rules (%d heads); kernel ms per pass %s"
+          % (el * 1e3, NQ, NR, len(groups), json.dumps({k: round(v, 3) for k, v in per_pass.items()})),
+          file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_seconds > 0:
+        from oracle import oracle as O
+        t1 = time.perf_counter()
+        nq = 0
+        for hd, srcs, rules, ks in groups:
+            O.rule_scores(h, r, t, E, R, [int(x) for x in srcs.cpu().tolist()], [bodies[k] for k in ks],
+                          weights[ks].astype(np.float64), "sum", False, False)
+            nq += srcs.numel()
+            if time.perf_counter() - t1 > args.cpu_seconds:
+                break
+        dt = time.perf_counter() - t1
+        cpu = {"value": nq / dt, "unit": "queries/s", "cores": 1, "kind": "port",
+               "sample": "%d queries of the first heads (the oracle's float64 path enumeration, numpy, "
+                         "1 thread; the reference's scorer is GPU-only Python) in %.1f s" % (nq, dt)}
+    result = {
+        "metric": "rule-bank scoring queries/sec (rules/shared_inference.score)",
+        "value": NQ / el, "unit": "queries/s", "n_gpus": 1, "steps": reps, "warmup": max(args.warmup, 1),
+        "ms_per_step": el * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded C3 graph, flashlog_amd/synth.py; random rules and queries)",
+        "config": {"workload": "C3 rule-bank scoring: %d rules (1-3 relations, %d ranks) over %d (source, head) "
+                               "queries, %d heads, chunks of %d rules" % (NR, RANKS, NQ, len(groups), CHUNK)},
+        "kernel_ms_per_pass": per_pass, "roofline": None, "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
 
