@@ -98,7 +98,7 @@ def hop_pull_bytes(Ap, w, csr, R, K, out_bytes=8):
     the two graph outputs (8 B per state cell) plus, per direction and active
     source, its row pointers (8 B), group records (10 B each) and the column
     and mask of every edge admitted for at least one row (8 B each) -- the
-    graph term of SURVEY.md's dense-sum formula.  The identity output and the
+    graph term of the dense hop's byte count.  The identity output and the
     read of A (8 B per cell) belong to k_col_count."""
     import numpy as np
     BL, E = Ap.shape
