@@ -1844,6 +1844,15 @@ __global__ void k_fill_i64(int64_t *__restrict__ p, int64_t n, int64_t v) {
     if (i < n) p[i] = v;
 }
 
+// plan[5] = 1 when an attention weight is not finite (any lane of a wave
+// that sees one sets it).
+__global__ void k_sp_finite(const float *__restrict__ w, int64_t count, unsigned long long *__restrict__ flag) {
+    bool bad = false;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+        bad |= !isfinite(w[i]);
+    if (__ballot(bad) != 0 && fl_lane() == 0) atomicOr(flag, 1ull);
+}
+
 __global__ void k_sp_plan_out(const int64_t *__restrict__ items, const int64_t *__restrict__ tiles, int64_t NB,
                               const int64_t *__restrict__ chunks, int64_t *__restrict__ plan) {
     plan[0] = *items;
@@ -2286,8 +2295,15 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     hipStream_t st = (hipStream_t)stream;
     const int64_t nnz = h->nnz;
     const int64_t K = sp_budget(h);
-    // plan[0] items, plan[1] tiles, plan[2] error, plan[3] buckets per row, plan[4] item chunks
-    FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, (int32_t *)plan, (int64_t)10, 0);
+    // plan[0] items, plan[1] tiles, plan[2] error, plan[3] buckets per row, plan[4] item chunks,
+    // plan[5] non-finite attention
+    FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, (int32_t *)plan, (int64_t)12, 0);
+    if (h->mode != SP_FIXED && h->w && R * h->n > 0) {
+        const int64_t cnt = R * h->n;
+        const int64_t blocks = (cnt + 255) / 256 < 1024 ? (cnt + 255) / 256 : 1024;
+        FL_LAUNCH("k_sp_finite", k_sp_finite, dim3((unsigned)blocks), dim3(256), 0, st, h->w, cnt,
+                  (unsigned long long *)(plan + 5));
+    }
     FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr, R + 1,
               (int64_t)0);
     const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);

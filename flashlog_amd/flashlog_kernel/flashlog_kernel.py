@@ -930,7 +930,7 @@ class _SparseState:
 
 
 def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mode, topk_edges,
-                    need_backward, operators=None, aggregate=_SPARSE_SUM, seed=-1):
+                    need_backward, operators=None, aggregate=_SPARSE_SUM, seed=-1, check_finite=False):
     """Runs plan -> expand -> emit.  Returns (indices [3, nout], values, state).
     aggregate: sum or max; seed >= 0: training quotas instead of the c2
     threshold."""
@@ -968,10 +968,14 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         ws1 = torch.empty(max(lib.fl_sparse_plan_bytes(nnz, R, 0 if mode == _SPARSE_FIXED else r_size), 1),
                           dtype=torch.uint8, device=dev)
         h.ws1, h.ws1_bytes = ptr(ws1).value, ws1.numel()
-        plan = torch.empty(5, dtype=torch.int64, device=dev)
+        plan = torch.empty(6, dtype=torch.int64, device=dev)
         check(lib.fl_sparse_plan(st, ctypes.byref(sides.ori), ctypes.byref(sides.inv), ctypes.byref(h), ptr(plan)),
               "sparse_plan")
-        items, tiles, err, nb, chunks = plan.tolist()
+        items, tiles, err, nb, chunks, nonfinite = plan.tolist()
+        if check_finite and nonfinite:
+            # flashlog.cu:2019-2021, checked by the plan after c1
+            raise RuntimeError("FlashLog sparse top-k received non-finite attention weights; "
+                               "aborting before edge count/fill to prevent uninitialized indices")
         if err == 2 and attempt == 0:
             # rows out of order: process them in row order, entries of a row in input order
             perm = torch.argsort(sp_b * L + sp_l, stable=True)
@@ -1079,9 +1083,10 @@ def _sparse_rows_scratch(R, device):
 
 
 @torch.no_grad()
-def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, num_rules, sampling=False):
+def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, num_rules, sampling=False, B=None):
     """Kept entries of the c1 budget per (item, rule) row of a coalesced state
-    (flashlog_kernel.py:1092-1140), or None when nothing is pruned."""
+    (flashlog_kernel.py:1092-1140), or None when nothing is pruned.  B: the
+    batch size when the caller knows it (else 1 + the largest batch index)."""
     if topk_nodes is None:
         return None
     if topk_nodes < 0:
@@ -1090,7 +1095,8 @@ def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, nu
         return None
     _require_cuda(sp_batch, sp_level, sp_value)
     L = int(num_rules)
-    B = int(sp_batch.max()) + 1 if sp_batch.numel() else 0
+    if B is None:
+        B = int(sp_batch.max()) + 1 if sp_batch.numel() else 0
     sp_batch = sp_batch.long().contiguous()
     sp_level = sp_level.long().contiguous()
     sp_value = sp_value.contiguous().float()
@@ -1134,9 +1140,9 @@ def _sparse_race_entries(sp_batch, sp_level, sp_value, B, L, c, keep):
     return torch.nonzero(keep, as_tuple=True)[0]
 
 
-def _prune_sparse_sources(ctx, batch, level, entity, value, topk_nodes, num_rules, sampling=False):
+def _prune_sparse_sources(ctx, batch, level, entity, value, topk_nodes, num_rules, sampling=False, B=None):
     """Select one common input for fact and identity propagation."""
-    entries = _sparse_topc_entries(batch, level, entity, value, topk_nodes, num_rules, sampling)
+    entries = _sparse_topc_entries(batch, level, entity, value, topk_nodes, num_rules, sampling, B)
     ctx.pruned_entries = entries
     ctx.original_input_size = value.numel()
     if entries is None:
@@ -1226,10 +1232,8 @@ def _topk_hop_forward(ctx, aggregate, sp_batch, sp_level, sp_entity, sp_value, w
     seeded by one draw of torch's CPU generator, as the reference draws it."""
     trainable = weight is not None and bool(getattr(weight, "requires_grad", False))
     _require_cuda(sp_value, w)
-    if not bool(torch.isfinite(w).all()):
-        raise RuntimeError("FlashLog sparse top-k received non-finite attention weights")
     sp_batch, sp_level, sp_entity, sp_value = _prune_sparse_sources(
-        ctx, sp_batch, sp_level, sp_entity, sp_value, topk_nodes, w.size(1), sampling)
+        ctx, sp_batch, sp_level, sp_entity, sp_value, topk_nodes, w.size(1), sampling, B=int(B))
     mask_f = mask_values.contiguous().view(-1)
     ori_bits = inv_bits = None
     if weight is not None and edge_weight_is_score:
@@ -1256,7 +1260,8 @@ def _topk_hop_forward(ctx, aggregate, sp_batch, sp_level, sp_entity, sp_value, w
     seed = int(torch.randint(0, 2 ** 63 - 1, ()).item()) if sampling else -1
     need = bool(any(ctx.needs_input_grad))
     idx, vals, state = _sparse_forward(sp_batch, sp_level, sp_entity, sp_value, w, sides, B, L, E, r_size,
-                                       wot_i, _SPARSE_TOPK, int(topk_edges), need, aggregate=aggregate, seed=seed)
+                                       wot_i, _SPARSE_TOPK, int(topk_edges), need, aggregate=aggregate, seed=seed,
+                                       check_finite=True)
     ctx.state, ctx.out_indices, ctx.dims = state, idx, (int(B), int(L), int(E), tuple(w.shape))
     ctx.edge_weight = (tuple(weight.shape), weight.dtype, weight.device) if trainable else None
     return _coo(idx, vals, int(B), int(L), int(E))

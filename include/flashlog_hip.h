@@ -300,8 +300,10 @@ size_t fl_sparse_plan_bytes(int64_t nnz, int64_t R, int64_t r_size);
 /* Replaces the count kernels and the host .item() syncs of
  * flashlog_forward_sparse3d_topk_cuda / _alledges_cuda (flashlog.cu:
  * 1999-2241): per entry and side the c2 threshold (flashlog.cpp:12-35) and
- * item counts; plan (device int64[5]) receives {items, tiles, error,
- * buckets, chunks} (chunks: the sum over entries of ceil(items / 64)).  error: 0 ok, 1 index out of range, 2 entries not sorted by row.
+ * item counts; plan (device int64[6]) receives {items, tiles, error,
+ * buckets, chunks, nonfinite} (chunks: the sum over entries of ceil(items
+ * / 64); nonfinite: 1 when an attention weight of w is not finite, the
+ * condition the top-k hops reject, flashlog.cu:2019-2021).  error: 0 ok, 1 index out of range, 2 entries not sorted by row.
  * The caller reads plan after the stream completes. */
 int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv,
                    const fl_sparse_hop *h, int64_t *plan);

@@ -387,3 +387,15 @@ def test_mask_bits_match_packbits(n):
     padded[:n] = mask != 0
     want = np.packbits(padded, bitorder="little").view(np.uint32)
     np.testing.assert_array_equal(got[: want.size], want)
+
+
+@pytest.mark.parametrize("agg", ["sum", "max"])
+def test_topk_hop_rejects_nonfinite_attention(agg):
+    """flashlog.cu:2019-2021: a non-finite attention weight is rejected (the
+    plan flags it; no item is expanded)."""
+    B, L = 2, 2
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 0.2, B, L, 50, 3)
+    w = w.copy()
+    w[1, 0, 3] = np.nan
+    with pytest.raises(RuntimeError, match="non-finite attention"):
+        (_sum if agg == "sum" else _max)(state, w, csr, mbool, B, L, E, R, 5)
