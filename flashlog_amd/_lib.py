@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 15
+ABI_VERSION = 16
 FL_SEG = 32
 FL_SUP = 16
 
@@ -65,7 +65,7 @@ class FlSparseHop(ctypes.Structure):
         ("ws2", ctypes.c_void_p), ("ws2_bytes", ctypes.c_size_t), ("items", ctypes.c_int64),
         ("tiles", ctypes.c_int64), ("operators", ctypes.c_void_p), ("aggregate", ctypes.c_int),
         ("sampling_seed", ctypes.c_int64), ("raw_pos", ctypes.c_void_p), ("raw_col", ctypes.c_void_p),
-        ("chunks", ctypes.c_int64),
+        ("chunks", ctypes.c_int64), ("entry_order", ctypes.c_void_p),
     ]
 
 

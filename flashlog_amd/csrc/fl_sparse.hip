@@ -469,18 +469,22 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
                                                      int64_t seed, float *__restrict__ th, int32_t *__restrict__ cut,
                                                      int32_t *__restrict__ cnt, const int16_t *__restrict__ rel_order,
                                                      const int32_t *__restrict__ rel_nelig, int use_map,
-                                                     SpQuota *__restrict__ qout, int32_t *__restrict__ nch) {
+                                                     SpQuota *__restrict__ qout, int32_t *__restrict__ nch,
+                                                     const int32_t *__restrict__ order) {
     __shared__ int hist_all[SEL_NT / FL_WAVE][256];
     extern __shared__ int cmap_all[];  // [SEL_NT / FL_WAVE][r_size] when the map is used
     const int lane = fl_lane();
     const int wid = threadIdx.x / FL_WAVE;
-    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + wid;
+    const int64_t wv_i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + wid;
+    // entries visited in the given order (by source entity: neighbouring
+    // waves read the same group records), results stored by entry
+    const int64_t i = (order && wv_i < nnz) ? (int64_t)order[wv_i] : wv_i;
     int *cmap = use_map ? cmap_all + wid * r_size : nullptr;
     if (cmap) {
         for (int64_t q = lane; q < r_size; q += FL_WAVE) cmap[q] = 0;
         fl_wave_sync();
     }
-    if (i >= nnz) return;
+    if (i < 0 || i >= nnz) return;  // (an order outside [0, nnz) is reported by the plan)
     const int64_t src = se[i];
     if (sb[i] < 0 || sb[i] >= B || sl[i] < 0 || sl[i] >= L || src < 0 || src >= E) {
         if (lane == 0) {
@@ -691,17 +695,21 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_runs(fl_side ori, fl_side inv, co
                                                    const float *__restrict__ th, const int32_t *__restrict__ cut,
                                                    const SpQuota *__restrict__ quota,
                                                    const int64_t *__restrict__ item_off,
-                                                   const int64_t *__restrict__ chunk_off, SpRuns ru) {
+                                                   const int64_t *__restrict__ chunk_off,
+                                                   const int32_t *__restrict__ order, SpRuns ru) {
     const int lane = fl_lane();
-    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
-    if (i >= nnz) return;
+    const int64_t wv_i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
+    if (wv_i >= nnz) return;
+    // entry visited in the plan's order; its chunks follow that order
+    const int64_t i = order ? (int64_t)order[wv_i] : wv_i;
+    if (i < 0 || i >= nnz) return;
     const int64_t src = se[i];
     const int64_t r = sb[i] * L + sl[i];
     const float a = sv[i];
     const float *wrow = w + r * n;
     const int64_t base = item_off[i];
     const int64_t nitems = item_off[i + 1] - base;
-    const int64_t u0 = chunk_off[i];
+    const int64_t u0 = chunk_off[wv_i];
     // the plan's item count bounds every write (the walk reproduces it)
     const int64_t lim = nitems - (wot_i ? 0 : 1);
     int64_t pos = 0, rix = 0;  // within the entry
@@ -737,7 +745,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_runs(fl_side ori, fl_side inv, co
         if (lim % SP_ICHUNK == 0) ru.c_run[u0 + lim / SP_ICHUNK] = base + rix;
     }
     const int64_t nr = rix + (wot_i ? 0 : 1);
-    const int64_t nq = chunk_off[i + 1] - u0;
+    const int64_t nq = chunk_off[wv_i + 1] - u0;
     for (int64_t q = lane; q < nq; q += FL_WAVE) {
         const int64_t c0 = q * SP_ICHUNK;
         ru.c_base[u0 + q] = base;
@@ -1834,6 +1842,31 @@ __global__ void k_mask_bits(const float *__restrict__ mask, int64_t n, uint32_t 
     if (lane == 32 && w0 + 1 < nw) bits[w0 + 1] = (uint32_t)(b >> 32);
 }
 
+// Entry order validation: every entry visited exactly once (else error 1).
+__global__ void k_sp_order_count(const int32_t *__restrict__ order, int64_t nnz, int32_t *__restrict__ seen,
+                                 int64_t *__restrict__ err) {
+    const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (w >= nnz) return;
+    const int32_t o = order[w];
+    if (o < 0 || o >= nnz) atomicMax((unsigned long long *)err, 1ull);
+    else atomicAdd(&seen[o], 1);
+}
+
+__global__ void k_sp_order_check(const int32_t *__restrict__ seen, int64_t nnz, int64_t *__restrict__ err) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < nnz && seen[i] != 1) atomicMax((unsigned long long *)err, 1ull);
+}
+
+// Chunk counts in visiting order.
+__global__ void k_sp_gather_nch(const int32_t *__restrict__ nch, const int32_t *__restrict__ order, int64_t nnz,
+                                int32_t *__restrict__ out) {
+    const int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (w < nnz) {
+        const int32_t o = order[w];
+        out[w] = (o >= 0 && o < nnz) ? nch[o] : 0;
+    }
+}
+
 __global__ void k_fill_i32(int32_t *__restrict__ p, int64_t n, int32_t v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -2151,7 +2184,7 @@ int sp_bucket_bits(int64_t NB) {
 // plan workspace layout
 struct SpPlan {
     float *th;
-    int32_t *cut, *cnt, *ntiles, *nch;
+    int32_t *cut, *cnt, *ntiles, *nch, *nch_ord;
     int64_t *item_off, *row_ptr, *row_item0, *tile_base, *tmp, *chunk_off;
     SpQuota *quota;       // [nnz][2] training quota parameters (quota sides only)
     int16_t *rel_order;   // [R][2][r_size] c2 admission order (r_size <= RO_MAX)
@@ -2168,6 +2201,7 @@ SpPlan sp_plan_layout(int64_t nnz, int64_t R, int64_t r_size, char *base) {
     p.cnt = (int32_t *)take(sizeof(int32_t) * (size_t)nnz);
     p.item_off = (int64_t *)take(sizeof(int64_t) * (size_t)(nnz + 1));
     p.nch = (int32_t *)take(sizeof(int32_t) * (size_t)nnz);
+    p.nch_ord = (int32_t *)take(sizeof(int32_t) * (size_t)nnz);
     p.chunk_off = (int64_t *)take(sizeof(int64_t) * (size_t)(nnz + 1));
     p.row_ptr = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
     p.row_item0 = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
@@ -2309,6 +2343,14 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
     const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
     FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, h->sp_b, h->sp_l,
               h->sp_e, nnz, h->B, h->L, h->E, p.row_ptr, plan + 2);
+    if (h->entry_order && nnz > 0 && h->mode != SP_FIXED) {
+        // the order must visit every entry once (nch_ord is the count scratch here)
+        FL_LAUNCH("k_fill_i32", k_fill_i32, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, p.nch_ord, nnz, 0);
+        FL_LAUNCH("k_sp_order_count", k_sp_order_count, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st,
+                  h->entry_order, nnz, p.nch_ord, plan + 2);
+        FL_LAUNCH("k_sp_order_check", k_sp_order_check, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st,
+                  p.nch_ord, nnz, plan + 2);
+    }
     if (nnz > 0 && h->mode == SP_FIXED)
         FL_LAUNCH("k_fx_count", k_fx_count, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, *ori, *inv,
                   h->sp_b, h->sp_l, h->sp_e, h->operators, nnz, h->B, h->L, h->E, h->r_size, p.cut, p.cnt);
@@ -2324,11 +2366,17 @@ int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const f
                   dim3(SEL_NT), lds, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e, nnz, h->w, h->B, h->L, h->E, h->n,
                   h->r_size, h->wot_i, h->mode, K, h->sampling_seed, p.th, p.cut, p.cnt,
                   lookup ? p.rel_order : (const int16_t *)nullptr, lookup ? p.rel_nelig : (const int32_t *)nullptr,
-                  use_map, p.quota, p.nch);
+                  use_map, p.quota, p.nch, h->entry_order);
     }
     if ((rc = exclusive_scan(st, p.cnt, p.item_off, nnz, p.tmp)) != FL_OK) return rc;
     const bool fixed = h->mode == SP_FIXED;
-    if (!fixed && (rc = exclusive_scan(st, p.nch, p.chunk_off, nnz, p.tmp)) != FL_OK) return rc;
+    if (!fixed && h->entry_order && nnz > 0) {
+        FL_LAUNCH("k_sp_gather_nch", k_sp_gather_nch, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, p.nch,
+                  h->entry_order, nnz, p.nch_ord);
+        if ((rc = exclusive_scan(st, p.nch_ord, p.chunk_off, nnz, p.tmp)) != FL_OK) return rc;
+    } else if (!fixed && (rc = exclusive_scan(st, p.nch, p.chunk_off, nnz, p.tmp)) != FL_OK) {
+        return rc;
+    }
     FL_LAUNCH("k_sp_rowinfo", k_sp_rowinfo, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, p.row_ptr,
               p.item_off, R, p.row_item0, p.ntiles);
     if ((rc = exclusive_scan(st, p.ntiles, p.tile_base, R, p.tmp)) != FL_OK) return rc;
@@ -2383,7 +2431,7 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         FL_LAUNCH("k_sp_runs", sp_quotas(h) ? k_sp_runs<true> : k_sp_runs<false>,
                   dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))), dim3(SEL_NT), 0, st, *ori,
                   *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n, h->r_size, h->wot_i, h->mode,
-                  h->sampling_seed, p.th, p.cut, p.quota, p.item_off, p.chunk_off, x.runs);
+                  h->sampling_seed, p.th, p.cut, p.quota, p.item_off, p.chunk_off, h->entry_order, x.runs);
         const int64_t wpb = SP_ITEMS_NT / FL_WAVE;
         const int64_t blocks = (h->chunks + wpb - 1) / wpb;
         const unsigned grid = (unsigned)(blocks < SP_ITEMS_GRID ? blocks : SP_ITEMS_GRID);

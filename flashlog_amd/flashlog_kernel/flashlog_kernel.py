@@ -920,6 +920,9 @@ class _SparseSides:
         return side
 
 
+# Hops with at least this many entries visit them by source entity.
+_ENTRY_ORDER_MIN = 4096
+
 # When a list, every sparse hop appends its plan's sizes to it as
 # {"nnz", "items", "chunks", "backward"} (for byte counts in measurements).
 plan_log = None
@@ -957,8 +960,13 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     lib = _lib.lib()
     st = _stream(sp_v)
     perm = None
+    order = None
     for attempt in range(2):
+        if mode != _SPARSE_FIXED and nnz >= _ENTRY_ORDER_MIN:
+            # visit entries by source entity (a source's rows then share cached group records)
+            order = torch.argsort(sp_e).to(torch.int32)
         h = FlSparseHop()
+        h.entry_order = ptr(order).value if order is not None else None
         h.sp_b, h.sp_l, h.sp_e, h.sp_v = (ptr(t).value for t in (sp_b, sp_l, sp_e, sp_v))
         h.nnz, h.w = nnz, ptr(w_flat).value
         h.B, h.L, h.E, h.n, h.r_size = B, L, E, n, r_size
@@ -1009,7 +1017,7 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     if need_backward:
         state = _SparseState()
         state.h, state.sides, state.perm = h, sides, perm
-        state.keep = (sp_b, sp_l, sp_e, sp_v, w_flat, ws1, out_base, raw_local, raw_pos, raw_col)
+        state.keep = (sp_b, sp_l, sp_e, sp_v, w_flat, ws1, out_base, raw_local, raw_pos, raw_col, order)
         state.out_base, state.raw_local, state.nout, state.n = out_base, raw_local, nout, n
     del ws2
     return idx, vals, state

@@ -285,6 +285,15 @@ typedef struct fl_sparse_hop {
                                           entry's items cut into chunks of
                                           64), sizing the expansion's chunk
                                           table                              */
+    const int32_t *entry_order;        /* optional: [nnz] a permutation of
+                                          the entries (e.g. by source
+                                          entity) in which the plan and the
+                                          expansion visit them, so that
+                                          entries of one source run close
+                                          together; results do not depend on
+                                          it.  The same array for plan and
+                                          expand; a non-permutation is
+                                          error 1                            */
 } fl_sparse_hop;
 
 /* Destination buckets per row (8192 entities each).  The sparse hop
