@@ -1050,6 +1050,41 @@ __device__ __forceinline__ const uint32_t *sp_load_sort(const int32_t *__restric
     return sp_block_sort<IPT>(kb[0], kb[1], 11, 16, cnt, scan_lds);
 }
 
+// The chunk's items [c0, c0 + SP_NT*IPT) of a bucket in registers (blocked:
+// thread t holds items t*IPT ..), destination -2 past the end; and those
+// registers turned into sort keys and LDS values as sp_load_sort does.
+template <int IPT>
+__device__ __forceinline__ void sp_chunk_regs(const int32_t *__restrict__ dst_arr, const float *__restrict__ val_arr,
+                                              int64_t start, int64_t c0, int64_t n, int32_t *pd, float *pv) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int64_t k = c0 + t * IPT + j;
+        pd[j] = -2;
+        pv[j] = 0.0f;
+        if (k < n) {
+            pd[j] = dst_arr[start + k];
+            pv[j] = val_arr[start + k];
+        }
+    }
+}
+
+template <int IPT>
+__device__ __forceinline__ void sp_regs_to_lds(const int32_t *pd, const float *pv, uint32_t (*kb)[SP_CHUNK],
+                                               float *val) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int k = t * IPT + j;
+        uint32_t dl = SP_W;  // no item / hole: sorts last
+        if (pd[j] >= 0) {
+            dl = (uint32_t)pd[j] & (SP_W - 1);
+            val[k] = pv[j];
+        }
+        kb[0][k] = (dl << 11) | (uint32_t)k;
+    }
+}
+
 // Values in sorted order: sv[p] = val[index of key p], for this thread's
 // blocked positions (sv is the sort's idle ping-pong buffer).
 template <int IPT>
@@ -1389,9 +1424,16 @@ __device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__r
     const int64_t n = end - start;
     const int t = threadIdx.x;
     for (int q = t; q < SP_W / 32; q += SP_NT) bits[q] = 0;
+    // the next chunk's items are requested while this chunk is sorted and folded
+    int32_t pd[SP_CHUNK_IPT];
+    float pv[SP_CHUNK_IPT];
+    sp_chunk_regs<SP_CHUNK_IPT>(dst_arr, val_arr, start, 0, n, pd, pv);
     for (int64_t c0 = 0; c0 < n; c0 += SP_CHUNK) {
         __syncthreads();  // previous chunk's folds done with kb / val
-        const uint32_t *key = sp_load_sort<SP_CHUNK_IPT>(dst_arr, val_arr, start, c0, n, kb, val, cnt, scan_lds);
+        sp_regs_to_lds<SP_CHUNK_IPT>(pd, pv, kb, val);
+        if (c0 + SP_CHUNK < n) sp_chunk_regs<SP_CHUNK_IPT>(dst_arr, val_arr, start, c0 + SP_CHUNK, n, pd, pv);
+        __syncthreads();
+        const uint32_t *key = sp_block_sort<SP_CHUNK_IPT>(kb[0], kb[1], 11, 16, cnt, scan_lds);
         const float *sv = sp_sorted_values<SP_CHUNK_IPT>(key, kb, val);
         for (int j = 0; j < SP_CHUNK_IPT; ++j) {
             const int p = t * SP_CHUNK_IPT + j;
