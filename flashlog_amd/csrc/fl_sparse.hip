@@ -929,7 +929,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
                                                        int32_t *__restrict__ part_raw,
                                                        const uint32_t *__restrict__ raw_tie,
                                                        uint32_t *__restrict__ part_tie) {
-    __shared__ uint32_t kb[2][SP_TILE];
+    __shared__ __align__(16) uint32_t kb[2][SP_TILE];
     __shared__ uint16_t cnt[16][SP_NT];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
     const int64_t tile = blockIdx.x;
@@ -953,17 +953,18 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
     __syncthreads();
     const uint32_t *sorted = sp_block_sort<SP_IPT>(kb[0], kb[1], 12, nbits, cnt, scan_lds);
     const int64_t *bb = base + rows.tile_base[r] * rows.NB + tl;
-    // first sorted position of every bucket present, in the sort's idle
-    // buffer when the buckets fit (else a binary search per item)
-    uint32_t *first = sorted == kb[0] ? kb[1] : kb[0];
-    const bool table = rows.NB <= SP_TILE;
+    // per bucket present: its output base minus its first sorted position
+    // (one base load per bucket and tile), in the sort's idle buffer when the
+    // buckets fit (else a binary search per item)
+    int64_t *boff = reinterpret_cast<int64_t *>(sorted == kb[0] ? kb[1] : kb[0]);
+    const bool table = rows.NB <= SP_TILE / 2;
     if (table) {
 #pragma unroll 4
         for (int j = 0; j < SP_IPT; ++j) {
             const int p = j * SP_NT + t;
             if (p >= c) continue;
             const uint32_t bk = sorted[p] >> 12;
-            if (bk != 0xFFFFFu && (p == 0 || (sorted[p - 1] >> 12) != bk)) first[bk] = (uint32_t)p;
+            if (bk != 0xFFFFFu && (p == 0 || (sorted[p - 1] >> 12) != bk)) boff[bk] = bb[(int64_t)bk * nt] - p;
         }
         __syncthreads();
     }
@@ -974,20 +975,19 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         const uint32_t key = sorted[p];
         const uint32_t bk = key >> 12;
         if (bk == 0xFFFFFu) continue;  // hole
-        int lo;
+        int64_t q;
         if (table) {
-            lo = (int)first[bk];
+            q = boff[bk] + p;
         } else {
-            lo = 0;
-            int hi = p;
+            int lo = 0, hi = p;
             while (lo < hi) {
                 const int mid = (lo + hi) >> 1;
                 if ((sorted[mid] >> 12) < bk) lo = mid + 1;
                 else hi = mid;
             }
+            q = bb[(int64_t)bk * nt] + (p - lo);
         }
         const int idx = (int)(key & 4095u);
-        const int64_t q = bb[(int64_t)bk * nt] + (p - lo);
         part_dst[q] = raw_dst[i0 + idx];
         part_val[q] = raw_val[i0 + idx];
         if (part_raw) part_raw[q] = (int32_t)(i0 + idx);
@@ -1452,6 +1452,7 @@ __device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__r
     wpre[t] = pre;
     __syncthreads();
     if (raw_local) {
+#pragma unroll 4
         for (int64_t k = t; k < n; k += SP_NT) {
             const int32_t d = dst_arr[start + k];
             if (d < 0) continue;  // hole
@@ -1642,6 +1643,7 @@ __device__ __forceinline__ void sp_max_hot_one(SpRows rows, const int64_t *__res
     wpre[t] = pre;
     __syncthreads();
     if (raw_local) {
+#pragma unroll 4
         for (int64_t k = t; k < n; k += SP_NT) {
             const int32_t d = dst_arr[start + k];
             if (d < 0) continue;
