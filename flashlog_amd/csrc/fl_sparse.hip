@@ -1705,6 +1705,8 @@ __global__ __launch_bounds__(SP_NT) void k_sp_emit(SpRows rows, int64_t L, const
 // are read only with several buckets (then holes of the sum become -1);
 // with one, holes keep an unspecified index and the backward skips them by
 // their mask.  Workgroup per tile of a row, as k_sp_hist.
+constexpr int SP_LTO_NB = 2048;  // buckets per row kept in LDS by k_sp_local_to_out
+
 __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows rows, const int32_t *__restrict__ raw_dst,
                                                           const int64_t *__restrict__ out_base,
                                                           int32_t *__restrict__ raw_local) {
@@ -1715,12 +1717,20 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
     const int64_t i1e = rows.row_item0[r + 1];
     const int c = (int)((i1e - i0) < SP_TILE ? (i1e - i0) : SP_TILE);
     const int64_t *orow = out_base + r * rows.NB;
+    // the row's bucket bases in LDS when they fit (one load each per tile)
+    __shared__ int64_t obase[SP_LTO_NB];
+    const bool lds = rows.NB <= SP_LTO_NB;
+    if (lds) {
+        for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) obase[q] = orow[q];
+        __syncthreads();
+    }
+#pragma unroll 4
     for (int idx = threadIdx.x; idx < c; idx += SP_NT) {
         const int64_t k = i0 + idx;
         const int32_t loc = raw_local[k];
         if (rows.NB > 1) {
             const int32_t d = raw_dst[k];
-            raw_local[k] = (loc >= 0 && d >= 0) ? (int32_t)(orow[d >> SP_S] + loc) : -1;
+            raw_local[k] = (loc >= 0 && d >= 0) ? (int32_t)((lds ? obase[d >> SP_S] : orow[d >> SP_S]) + loc) : -1;
         } else {
             raw_local[k] = loc >= 0 ? (int32_t)(orow[0] + loc) : -1;
         }
