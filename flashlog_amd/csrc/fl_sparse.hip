@@ -1667,15 +1667,20 @@ __device__ __forceinline__ void sp_max_hot_one(SpRows rows, const int64_t *__res
     if (t == 0) out_count[r * rows.NB + bk] = total;
 }
 
-// Workgroup per (row, bucket): staged outputs -> COO at out_base.
-__global__ __launch_bounds__(SP_NT) void k_sp_emit(SpRows rows, int64_t L, const int64_t *__restrict__ base,
+// Wave per (row, bucket), four per workgroup: staged outputs -> COO at
+// out_base.
+constexpr int SP_EMIT_WAVES = 4;
+
+__global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows, int64_t L, int64_t nslot,
+                                                  const int64_t *__restrict__ base,
                                                   const int32_t *__restrict__ dst_arr,
                                                   const float *__restrict__ val_arr,
                                                   const int64_t *__restrict__ out_base, int64_t *__restrict__ ob,
                                                   int64_t *__restrict__ ol, int64_t *__restrict__ oe,
                                                   float *__restrict__ ov) {
-    const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
-    const int64_t slot = r * rows.NB + bk;
+    const int64_t slot = (int64_t)blockIdx.x * SP_EMIT_WAVES + threadIdx.x / FL_WAVE;
+    if (slot >= nslot) return;
+    const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
     const int64_t o0 = out_base[slot];
     const int64_t cnt = out_base[slot + 1] - o0;
     if (cnt == 0) return;
@@ -1687,7 +1692,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_emit(SpRows rows, int64_t L, const
         start = base[rows.tile_base[r] * rows.NB + bk * nt];
     }
     const int64_t b = r / L, l = r - (r / L) * L;
-    for (int64_t k = threadIdx.x; k < cnt; k += SP_NT) {
+    for (int64_t k = fl_lane(); k < cnt; k += FL_WAVE) {
         ob[o0 + k] = b;
         ol[o0 + k] = l;
         oe[o0 + k] = dst_arr[start + k];
@@ -2559,9 +2564,10 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h, const int64_t *out_base
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     SpExp x = sp_exp_layout(h->items, h->tiles, h->chunks, R, NB, 0, h->aggregate, (char *)h->ws2);
     SpRows rows{p.row_item0, p.tile_base, NB};
-    FL_LAUNCH("k_sp_emit", k_sp_emit, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, (hipStream_t)stream, rows, h->L,
-              x.base, NB > 1 ? x.part_dst : x.raw_dst, NB > 1 ? x.part_val : x.raw_val, out_base, out_b, out_l,
-              out_e, out_v);
+    FL_LAUNCH("k_sp_emit", k_sp_emit, dim3((unsigned)((R * NB + SP_EMIT_WAVES - 1) / SP_EMIT_WAVES)),
+              dim3(SP_EMIT_WAVES * FL_WAVE), 0, (hipStream_t)stream, rows, h->L, R * NB, x.base,
+              NB > 1 ? x.part_dst : x.raw_dst, NB > 1 ? x.part_val : x.raw_val, out_base, out_b, out_l, out_e,
+              out_v);
     return fl_check_launch("sparse_emit");
 }
 
