@@ -923,6 +923,12 @@ class _SparseSides:
 # Hops with at least this many entries visit them by source entity.
 _ENTRY_ORDER_MIN = 4096
 
+def _entry_order(sp_e):
+    """Entries by source entity: a source's rows then share cached group
+    records in the plan and the run writer."""
+    return torch.argsort(sp_e).to(torch.int32)
+
+
 # When a list, every sparse hop appends its plan's sizes to it as
 # {"nnz", "items", "chunks", "backward"} (for byte counts in measurements).
 plan_log = None
@@ -963,8 +969,7 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     order = None
     for attempt in range(2):
         if mode != _SPARSE_FIXED and nnz >= _ENTRY_ORDER_MIN:
-            # visit entries by source entity (a source's rows then share cached group records)
-            order = torch.argsort(sp_e).to(torch.int32)
+            order = _entry_order(sp_e)
         h = FlSparseHop()
         h.entry_order = ptr(order).value if order is not None else None
         h.sp_b, h.sp_l, h.sp_e, h.sp_v = (ptr(t).value for t in (sp_b, sp_l, sp_e, sp_v))

@@ -399,3 +399,29 @@ def test_topk_hop_rejects_nonfinite_attention(agg):
     w[1, 0, 3] = np.nan
     with pytest.raises(RuntimeError, match="non-finite attention"):
         (_sum if agg == "sum" else _max)(state, w, csr, mbool, B, L, E, R, 5)
+
+
+def test_entry_order_must_be_a_permutation(monkeypatch):
+    """The plan checks the entry visiting order: an order that visits one
+    entry twice (and another never) is reported before any item is expanded."""
+    fk = _fk()
+    B, L = 4, 3
+    rng, E, R, n, csr, mbool, masks, state, w = _case(2, 1.0, B, L, 1500, 11)
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    om, im = _dev(*masks)
+    sides = fk._SparseSides(tc[1], om, tc[8], tc[9], tc[10], tc[11], tc[5], im, tc[12], tc[13], tc[14], tc[15])
+    b, l, e, v = _dev(*state)
+    assert v.numel() >= fk._ENTRY_ORDER_MIN
+    wt = torch.from_numpy(w).cuda()
+    good = fk._sparse_forward(b, l, e, v, wt, sides, B, L, E, R, False, fk._SPARSE_TOPK, 5, False)
+    rk, rv = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, 5)
+    assert np.array_equal(_keys(good[0], L, E), rk)
+
+    def bad(sp_e):
+        order = torch.argsort(sp_e).to(torch.int32)
+        order[1] = order[0]
+        return order
+
+    monkeypatch.setattr(fk, "_entry_order", bad)
+    with pytest.raises(ValueError):
+        fk._sparse_forward(b, l, e, v, wt, sides, B, L, E, R, False, fk._SPARSE_TOPK, 5, False)
