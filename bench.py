@@ -484,7 +484,7 @@ def main_grounding(args):
         cands, raw, _ = call()
     torch.cuda.synchronize()
     el = (time.perf_counter() - t0) / reps
-    kn = ["k_gr_walk", "k_ct_flags", "k_ct_accum", "k_ct_capkey", "k_ct_keep", "k_ct_gather", "k_ct_emit"]
+    kn = ["k_gr_hubs", "k_gr_walk", "k_ct_flags", "k_ct_accum", "k_ct_capkey", "k_ct_keep", "k_ct_gather", "k_ct_emit"]
     prof = {k: _lib.prof_read(k) for k in kn}
     _lib.prof_enable(False)
     per_call = {k: v[0] / reps for k, v in prof.items()}

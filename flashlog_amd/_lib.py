@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 16
+ABI_VERSION = 17
 FL_SEG = 32
 FL_SUP = 16
 
@@ -78,6 +78,8 @@ class FlGroundGraph(ctypes.Structure):
         ("inv_ptr", ctypes.c_void_p), ("inv_start", ctypes.c_void_p), ("inv_count", ctypes.c_void_p),
         ("inv_rel", ctypes.c_void_p),
         ("nodes", ctypes.c_int64), ("num_relations", ctypes.c_int64), ("max_groups", ctypes.c_int64),
+        ("nhub", ctypes.c_int64), ("hub_options", ctypes.c_int64), ("hub_id", ctypes.c_void_p),
+        ("hub_node", ctypes.c_void_p), ("hub_off", ctypes.c_void_p),
     ]
 
 
@@ -133,7 +135,7 @@ _SIGS = {
     "fl_reservoir": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
                                     ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]),
-    "fl_ground_walk_bytes": (ctypes.c_size_t, [ctypes.POINTER(FlGroundGraph), ctypes.c_int64]),
+    "fl_ground_walk_bytes": (ctypes.c_size_t, [ctypes.POINTER(FlGroundGraph)] + [ctypes.c_int64] * 3),
     "fl_ground_walks": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlGroundGraph), ctypes.c_void_p,
                                        ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_int64] + [ctypes.c_void_p] * 3 +

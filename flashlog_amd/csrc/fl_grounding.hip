@@ -203,6 +203,23 @@ struct GrScratch {
     double *omass;
 };
 
+// Hub cache: per (head slot, step, rank) combination c and hub h, the
+// node's option lists (fw options, then inv options) with cumulative masses
+// at c * nopt + hub_off[h], and the header {fw count, inv count, total}.
+struct GrHubHdr {
+    int32_t nf, ni;
+    double total;
+};
+
+struct GrHubPool {
+    GrHubHdr *hdr;                // [combos][nhub]
+    int32_t *op, *start, *take;   // [combos][nopt]
+    double *cum;                  // [combos][nopt]
+    const int32_t *hub_id, *hub_node;
+    const int64_t *hub_off;
+    int64_t nhub, nopt;
+};
+
 // Options of a side of up to 64*RR groups (RR keys per lane, element
 // i = r*64 + lane): the same bitonic network as the scratch sort, with
 // compare-exchanges inside a lane for strides >= 64 and across lanes
@@ -437,6 +454,78 @@ __device__ __forceinline__ void gr_option(const GrOpts &o, const GrScratch &sc, 
 constexpr int GR_NT = 64;
 constexpr int64_t GR_LDS_SORT_MAX = 4096;  // groups per side sorted in LDS (48 KB)
 
+// Hub cache fill, wave per (combination, hub) (grid-stride): the hub's
+// options ranked and their masses accumulated exactly as a walk step does
+// (no excluded operator), written to the pool; the sort scratch of large
+// sides is the block's walk scratch.
+__global__ __launch_bounds__(GR_NT) void k_gr_hubs(GrGraph gg, GrHubPool hp, const float *__restrict__ att,
+                                                  int64_t ranks, int64_t vocab, int64_t ncombo, int64_t topk,
+                                                  double temp, int64_t pmax, int64_t ocap, char *__restrict__ scratch,
+                                                  size_t stride) {
+    __shared__ double gr_mb[FL_WAVE];
+    const int lane = fl_lane();
+    char *ws = scratch + (size_t)blockIdx.x * stride;
+    const int32_t R = gg.R;
+    for (int64_t u = blockIdx.x; u < ncombo * hp.nhub; u += gridDim.x) {
+        const int64_t combo = u / hp.nhub, hid = u - combo * hp.nhub;
+        const int32_t node = hp.hub_node[hid];
+        const int64_t hslot = combo / (3 * ranks), step = (combo / ranks) % 3, rank = combo % ranks;
+        const float *w = att + hslot * 3 * ranks * vocab + (step * ranks + rank) * vocab;
+        const int64_t ob = combo * hp.nopt + hp.hub_off[hid];
+        GrScratch sc;
+        sc.skey = (uint64_t *)ws;
+        sc.sgrp = (int32_t *)(sc.skey + pmax);
+        sc.oop = hp.op + ob;
+        sc.ostart = hp.start + ob;
+        sc.otake = hp.take + ob;
+        sc.omass = hp.cum + ob;
+        (void)ocap;
+        const int64_t fg0 = gg.fw.ptr[node], fG = gg.fw.ptr[node + 1] - fg0;
+        const int64_t ig0 = gg.inv.ptr[node], iG = gg.inv.ptr[node + 1] - ig0;
+        GrOpts fo, io;
+        if (fG <= FL_WAVE) {
+            fo = gr_side_reg(gg.fw, 0, fg0, (int)fG, w, -1, topk, temp);
+            if (lane < fo.n) {
+                sc.oop[lane] = fo.op;
+                sc.ostart[lane] = fo.start;
+                sc.otake[lane] = fo.take;
+                sc.omass[lane] = fo.mass;
+            }
+            fo.mem = 1;
+        } else {
+            fo.mem = 1;
+            fo.n = gr_side_large(gg.fw, 0, fg0, fG, w, -1, topk, temp, sc, 0);
+        }
+        const int ibase = fo.n;
+        if (iG <= FL_WAVE) {
+            io = gr_side_reg(gg.inv, R, ig0, (int)iG, w, -1, topk, temp);
+            if (lane < io.n) {
+                sc.oop[ibase + lane] = io.op;
+                sc.ostart[ibase + lane] = io.start;
+                sc.otake[ibase + lane] = io.take;
+                sc.omass[ibase + lane] = io.mass;
+            }
+            io.mem = 1;
+        } else {
+            io.mem = 1;
+            io.n = gr_side_large(gg.inv, R, ig0, iG, w, -1, topk, temp, sc, ibase);
+        }
+        __syncthreads();  // the lists are visible to every lane
+        double total = gr_cumulate(fo, sc, 0, 0.0, gr_mb);
+        total = gr_cumulate(io, sc, ibase, total, gr_mb);
+        const float wid = w[2 * R];
+        if (wid > 0.0f) total = __dadd_rn(total, gr_proposal(wid, temp));
+        if (lane == 0) {
+            GrHubHdr hd;
+            hd.nf = fo.n;
+            hd.ni = io.n;
+            hd.total = total;
+            hp.hdr[combo * hp.nhub + hid] = hd;
+        }
+        __syncthreads();  // scratch reused by the next hub
+    }
+}
+
 // One wave per source task (grid-stride over tasks): the task's walks in
 // order with the task's engine; record j of task t = (body key, positive).
 template <bool LS>
@@ -448,7 +537,8 @@ __global__ __launch_bounds__(GR_NT) void k_gr_walk(GrGraph gg, const float *__re
                                                   const int64_t *__restrict__ task_index, int64_t walks,
                                                   int64_t topk, int mask_head, double temp, int64_t pmax,
                                                   int64_t ocap, char *__restrict__ scratch, size_t stride,
-                                                  uint64_t *__restrict__ out_key, uint8_t *__restrict__ out_pos) {
+                                                  GrHubPool hp, uint64_t *__restrict__ out_key,
+                                                  uint8_t *__restrict__ out_pos) {
     __shared__ uint64_t mt[MT_N];
     __shared__ double gr_mb[FL_WAVE];
     extern __shared__ __align__(8) char gr_lds[];  // [pmax] keys + [pmax] groups when lds_sort
@@ -499,43 +589,64 @@ __global__ __launch_bounds__(GR_NT) void k_gr_walk(GrGraph gg, const float *__re
             for (int step = 0; step < 3; ++step) {
                 const int32_t excl = (mask_head && node == source) ? head : -1;
                 const float *w = hatt + (step * ranks + rank) * vocab;
-                const int64_t fg0 = gg.fw.ptr[node], fG = gg.fw.ptr[node + 1] - fg0;
-                const int64_t ig0 = gg.inv.ptr[node], iG = gg.inv.ptr[node + 1] - ig0;
-                GrOpts fo, io;
-                if (fG <= FL_WAVE) {
-                    fo = gr_side_reg(gg.fw, 0, fg0, (int)fG, w, excl, topk, temp);
-                } else {
-                    fo.mem = 1;
-                    fo.n = gr_side_large(gg.fw, 0, fg0, fG, w, excl, topk, temp, sc, 0);
-                }
-                const int ibase = fo.mem ? fo.n : 0;
-                if (iG <= FL_WAVE) {
-                    io = gr_side_reg(gg.inv, R, ig0, (int)iG, w, excl, topk, temp);
-                } else {
-                    io.mem = 1;
-                    io.n = gr_side_large(gg.inv, R, ig0, iG, w, excl, topk, temp, sc, ibase);
-                }
-                if (fo.mem || io.mem) __syncthreads();
+                const int32_t hid = (hp.nhub > 0 && excl < 0) ? hp.hub_id[node] : -1;
                 const float wid = w[identity];
-                double total = gr_cumulate(fo, sc, 0, 0.0, gr_mb);
-                total = gr_cumulate(io, sc, ibase, total, gr_mb);
-                if (wid > 0.0f) total = __dadd_rn(total, gr_proposal(wid, temp));
+                GrOpts fo, io;
+                GrScratch scs = sc;
+                int ibase;
+                double total;
+                if (hid >= 0) {
+                    // a hub: the options this (head, step, rank) gives it, ranked once per call
+                    const int64_t combo = ((int64_t)hslot * 3 + step) * ranks + rank;
+                    const GrHubHdr hd = hp.hdr[combo * hp.nhub + hid];
+                    const int64_t ob = combo * hp.nopt + hp.hub_off[hid];
+                    scs.oop = hp.op + ob;
+                    scs.ostart = hp.start + ob;
+                    scs.otake = hp.take + ob;
+                    scs.omass = hp.cum + ob;
+                    fo.n = hd.nf;
+                    fo.mem = 1;
+                    io.n = hd.ni;
+                    io.mem = 1;
+                    ibase = hd.nf;
+                    total = hd.total;
+                } else {
+                    const int64_t fg0 = gg.fw.ptr[node], fG = gg.fw.ptr[node + 1] - fg0;
+                    const int64_t ig0 = gg.inv.ptr[node], iG = gg.inv.ptr[node + 1] - ig0;
+                    if (fG <= FL_WAVE) {
+                        fo = gr_side_reg(gg.fw, 0, fg0, (int)fG, w, excl, topk, temp);
+                    } else {
+                        fo.mem = 1;
+                        fo.n = gr_side_large(gg.fw, 0, fg0, fG, w, excl, topk, temp, sc, 0);
+                    }
+                    ibase = fo.mem ? fo.n : 0;
+                    if (iG <= FL_WAVE) {
+                        io = gr_side_reg(gg.inv, R, ig0, (int)iG, w, excl, topk, temp);
+                    } else {
+                        io.mem = 1;
+                        io.n = gr_side_large(gg.inv, R, ig0, iG, w, excl, topk, temp, sc, ibase);
+                    }
+                    if (fo.mem || io.mem) __syncthreads();
+                    total = gr_cumulate(fo, sc, 0, 0.0, gr_mb);
+                    total = gr_cumulate(io, sc, ibase, total, gr_mb);
+                    if (wid > 0.0f) total = __dadd_rn(total, gr_proposal(wid, temp));
+                }
                 if (!(total > 0.0)) {
                     viable = false;
                     break;
                 }
                 const double draw = __dmul_rn(gr_canonical(mt, idx), total);
                 int32_t op = identity, start = 0, take = 1;
-                int k = gr_pick(fo, sc, 0, draw);
+                int k = gr_pick(fo, scs, 0, draw);
                 if (k >= 0) {
-                    gr_option(fo, sc, 0, k, &op, &start, &take);
+                    gr_option(fo, scs, 0, k, &op, &start, &take);
                 } else {
-                    k = gr_pick(io, sc, ibase, draw);
-                    if (k >= 0) gr_option(io, sc, ibase, k, &op, &start, &take);
+                    k = gr_pick(io, scs, ibase, draw);
+                    if (k >= 0) gr_option(io, scs, ibase, k, &op, &start, &take);
                     else if (!(wid > 0.0f)) {
                         // none below the draw: the last option
-                        if (io.n > 0) gr_option(io, sc, ibase, io.n - 1, &op, &start, &take);
-                        else gr_option(fo, sc, 0, fo.n - 1, &op, &start, &take);
+                        if (io.n > 0) gr_option(io, scs, ibase, io.n - 1, &op, &start, &take);
+                        else gr_option(fo, scs, 0, fo.n - 1, &op, &start, &take);
                     }
                 }
                 if (op != identity) {
@@ -922,11 +1033,12 @@ GrGraph gr_graph(const fl_ground_graph *g) {
 }
 
 struct GrWalkLayout {
-    int64_t pmax, ocap, waves;
+    int64_t pmax, ocap, waves, ncombo;
     size_t stride, bytes;
+    size_t hub_hdr, hub_cum, hub_op, hub_start, hub_take;  // byte offsets of the hub cache (ncombo > 0)
 };
 
-GrWalkLayout gr_walk_layout(const fl_ground_graph *g, int64_t ntasks) {
+GrWalkLayout gr_walk_layout(const fl_ground_graph *g, int64_t ntasks, int64_t nheads, int64_t ranks) {
     GrWalkLayout L{};
     L.pmax = 128;
     while (L.pmax < g->max_groups) L.pmax <<= 1;
@@ -935,6 +1047,20 @@ GrWalkLayout gr_walk_layout(const fl_ground_graph *g, int64_t ntasks) {
     L.stride = gal(sizeof(uint64_t) * (size_t)L.pmax + sizeof(double) * (size_t)L.ocap +
                    sizeof(int32_t) * (size_t)L.pmax + 3 * sizeof(int32_t) * (size_t)L.ocap);
     L.bytes = L.stride * (size_t)(L.waves > 0 ? L.waves : 1);
+    if (g->nhub > 0 && g->hub_options > 0 && nheads > 0 && ranks > 0) {
+        L.ncombo = nheads * 3 * ranks;
+        const size_t slots = (size_t)L.ncombo * (size_t)g->hub_options;
+        L.hub_hdr = L.bytes;
+        L.bytes += gal(sizeof(GrHubHdr) * (size_t)L.ncombo * (size_t)g->nhub);
+        L.hub_cum = L.bytes;
+        L.bytes += gal(sizeof(double) * slots);
+        L.hub_op = L.bytes;
+        L.bytes += gal(sizeof(int32_t) * slots);
+        L.hub_start = L.bytes;
+        L.bytes += gal(sizeof(int32_t) * slots);
+        L.hub_take = L.bytes;
+        L.bytes += gal(sizeof(int32_t) * slots);
+    }
     return L;
 }
 
@@ -1032,9 +1158,9 @@ __global__ void k_copy_i64(const int64_t *__restrict__ src, int64_t *__restrict_
 
 extern "C" {
 
-size_t fl_ground_walk_bytes(const fl_ground_graph *g, int64_t ntasks) {
-    if (!g || ntasks < 0) return 0;
-    return gr_walk_layout(g, ntasks).bytes;
+size_t fl_ground_walk_bytes(const fl_ground_graph *g, int64_t ntasks, int64_t nheads, int64_t ranks) {
+    if (!g || ntasks < 0 || nheads < 0 || ranks < 0) return 0;
+    return gr_walk_layout(g, ntasks, nheads, ranks).bytes;
 }
 
 int fl_ground_walks(void *stream, const fl_ground_graph *g, const float *att, int64_t nheads, int64_t ranks,
@@ -1049,15 +1175,35 @@ int fl_ground_walks(void *stream, const fl_ground_graph *g, const float *att, in
     if (ntasks == 0) return FL_OK;
     if (!att || !heads || !seeds || !task_head || !task_source || !task_index || !keys || !positive || !ws)
         return fl_fail(FL_ERR_ARG, "ground_walks: null argument");
-    const GrWalkLayout L = gr_walk_layout(g, ntasks);
+    if (g->nhub > 0 && (!g->hub_id || !g->hub_node || !g->hub_off))
+        return fl_fail(FL_ERR_ARG, "ground_walks: hub cache without its arrays");
+    const GrWalkLayout L = gr_walk_layout(g, ntasks, nheads, ranks);
     if (ws_bytes < L.bytes) return fl_fail(FL_ERR_ARG, "ground_walks: workspace too small");
+    GrHubPool hp{};
+    char *wsb = (char *)ws;
+    if (L.ncombo > 0) {
+        hp.hdr = (GrHubHdr *)(wsb + L.hub_hdr);
+        hp.cum = (double *)(wsb + L.hub_cum);
+        hp.op = (int32_t *)(wsb + L.hub_op);
+        hp.start = (int32_t *)(wsb + L.hub_start);
+        hp.take = (int32_t *)(wsb + L.hub_take);
+        hp.hub_id = g->hub_id;
+        hp.hub_node = g->hub_node;
+        hp.hub_off = g->hub_off;
+        hp.nhub = g->nhub;
+        hp.nopt = g->hub_options;
+        const int64_t units = L.ncombo * g->nhub;
+        FL_LAUNCH("k_gr_hubs", k_gr_hubs, dim3((unsigned)(units < L.waves ? units : L.waves)), dim3(GR_NT), 0,
+                  (hipStream_t)stream, gr_graph(g), hp, att, ranks, 2 * g->num_relations + 1, L.ncombo, topk_edges,
+                  temperature, L.pmax, L.ocap, wsb, L.stride);
+    }
     // sides of up to GR_LDS_SORT_MAX groups are sorted in LDS, larger ones in the scratch
     const int lds_sort = L.pmax <= GR_LDS_SORT_MAX ? 1 : 0;
     const size_t lds = lds_sort ? (sizeof(uint64_t) + sizeof(int32_t)) * (size_t)L.pmax : 0;
     FL_LAUNCH("k_gr_walk", lds_sort ? k_gr_walk<true> : k_gr_walk<false>, dim3((unsigned)L.waves), dim3(GR_NT), lds,
               (hipStream_t)stream, gr_graph(g), att, ranks, 2 * g->num_relations + 1, heads, seeds, ntasks, task_head,
-              task_source, task_index, walks, topk_edges, mask_query_head, temperature, L.pmax, L.ocap, (char *)ws,
-              L.stride, keys, positive);
+              task_source, task_index, walks, topk_edges, mask_query_head, temperature, L.pmax, L.ocap, wsb,
+              L.stride, hp, keys, positive);
     return fl_check_launch("ground_walks");
 }
 

@@ -17,6 +17,8 @@ from ... import _lib
 from ..._lib import FlGroundGraph, check, ptr
 
 RULE_STEPS = 3  # the reference's default build (FLASHLOG_RULE_STEPS)
+HUB_MIN_GROUPS = 64  # sides with more groups make a node a hub of the walk's option cache
+HUB_CACHE_MAX_BYTES = 2 << 30  # the cache is skipped above this size
 
 
 def _device():
@@ -52,6 +54,23 @@ def _graph(csr, dev, num_relations):
     g.num_relations = int(num_relations)
     widths = [int((p[1:] - p[:-1]).max()) if p.numel() > 1 else 0 for p in (t[8], t[12])]
     g.max_groups = max(widths + [1])
+    # hub cache: nodes with more than 64 groups on a side (their options are
+    # ranked once per call for every head, step and rank)
+    fw = (t[8][1:] - t[8][:-1]).long()
+    iv = (t[12][1:] - t[12][:-1]).long()
+    hub = (fw > HUB_MIN_GROUPS) | (iv > HUB_MIN_GROUPS)
+    hub_node = torch.nonzero(hub).view(-1)
+    nhub = hub_node.numel()
+    g.nhub, g.hub_options = 0, 0
+    if nhub:
+        hub_id = torch.full((g.nodes,), -1, dtype=torch.int32, device=dev)
+        hub_id[hub_node] = torch.arange(nhub, dtype=torch.int32, device=dev)
+        cap = (fw + iv)[hub_node]
+        hub_off = torch.zeros(nhub + 1, dtype=torch.int64, device=dev)
+        hub_off[1:] = torch.cumsum(cap, 0)
+        t["hub_id"], t["hub_node"], t["hub_off"] = hub_id, hub_node.to(torch.int32).contiguous(), hub_off
+        g.nhub, g.hub_options = nhub, int(hub_off[-1])
+        g.hub_id, g.hub_node, g.hub_off = ptr(hub_id).value, ptr(t["hub_node"]).value, ptr(hub_off).value
     return g, t
 
 
@@ -67,7 +86,11 @@ def _walks(g, attentions, heads_d, seeds, task_head, task_source, task_index, wa
     ti = task_index.to(device=dev, dtype=torch.int64).contiguous()
     keys = torch.empty(max(ntasks * walks, 1), dtype=torch.int64, device=dev)
     positive = torch.empty(max(ntasks * walks, 1), dtype=torch.uint8, device=dev)
-    ws = torch.empty(max(lib.fl_ground_walk_bytes(ctypes.byref(g), ntasks), 1), dtype=torch.uint8, device=dev)
+    nheads, ranks = attentions.shape[0], attentions.shape[2]
+    if g.nhub and 3 * nheads * ranks * (20 * g.hub_options + 16 * g.nhub) > HUB_CACHE_MAX_BYTES:
+        g.nhub = 0  # too large a cache: every step ranks its options
+    ws = torch.empty(max(lib.fl_ground_walk_bytes(ctypes.byref(g), ntasks, nheads, ranks), 1), dtype=torch.uint8,
+                     device=dev)
     check(lib.fl_ground_walks(_stream(dev), ctypes.byref(g), ptr(att), att.shape[0], att.shape[2], ptr(heads_d),
                               ptr(seeds_d), ntasks, ptr(th), ptr(ts), ptr(ti), walks, int(topk_edges),
                               1 if mask else 0, temperature, ptr(ws), ws.numel(), ptr(keys), ptr(positive)),

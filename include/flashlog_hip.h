@@ -498,6 +498,15 @@ typedef struct fl_ground_graph {
     int64_t nodes;          /* entities (ptr arrays hold nodes + 1)       */
     int64_t num_relations;  /* R: operators 0..2R-1, identity 2R          */
     int64_t max_groups;     /* most groups of one node on one side        */
+    /* optional hub cache (nhub = 0 disables it): nodes with more than 64
+       groups on a side get their transition options precomputed once per
+       call for every (head, step, rank) instead of ranked at every visit */
+    int64_t nhub;           /* hub nodes                                  */
+    int64_t hub_options;    /* hub_off[nhub]                              */
+    const int32_t *hub_id;  /* [nodes] hub index of a node, -1 for others */
+    const int32_t *hub_node;/* [nhub] node of each hub                    */
+    const int64_t *hub_off; /* [nhub+1] option slots of each hub (its
+                               groups on both sides)                      */
 } fl_ground_graph;
 
 /* Replaces the walk part of ground_head_batch_source_folds_sampled_capped_
@@ -512,7 +521,8 @@ typedef struct fl_ground_graph {
  * ends at a positive target of (source, head).  att: [nheads, 3, ranks,
  * 2R+1].  The draws are those of libstdc++ 11 (generate_canonical<double,
  * 64>, uniform_int_distribution by Lemire's method). */
-size_t fl_ground_walk_bytes(const fl_ground_graph *g, int64_t ntasks);
+size_t fl_ground_walk_bytes(const fl_ground_graph *g, int64_t ntasks,
+                            int64_t nheads, int64_t ranks);
 int fl_ground_walks(void *stream, const fl_ground_graph *g, const float *att,
                     int64_t nheads, int64_t ranks, const int64_t *heads,
                     const int64_t *seeds, int64_t ntasks,
