@@ -209,6 +209,7 @@ struct GrScratch {
 struct GrHubHdr {
     int32_t nf, ni;
     double total;
+    int64_t off;  // first option slot in the pool
 };
 
 struct GrHubPool {
@@ -429,7 +430,20 @@ __device__ __forceinline__ int gr_pick(const GrOpts &o, const GrScratch &sc, int
         const unsigned long long b = __ballot(lane < o.n && draw < o.mass);
         return b ? __ffsll((long long)b) - 1 : -1;
     }
-    for (int base = 0; base < o.n; base += FL_WAVE) {
+    // the first four windows of 64 options requested together
+    double m[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = u * FL_WAVE + lane;
+        m[u] = i < o.n ? sc.omass[obase + i] : 0.0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = u * FL_WAVE + lane;
+        const unsigned long long b = __ballot(i < o.n && draw < m[u]);
+        if (b) return u * FL_WAVE + __ffsll((long long)b) - 1;
+    }
+    for (int base = 4 * FL_WAVE; base < o.n; base += FL_WAVE) {
         const int i = base + lane;
         const unsigned long long b = __ballot(i < o.n && draw < sc.omass[obase + i]);
         if (b) return base + __ffsll((long long)b) - 1;
@@ -520,6 +534,7 @@ __global__ __launch_bounds__(GR_NT) void k_gr_hubs(GrGraph gg, GrHubPool hp, con
             hd.nf = fo.n;
             hd.ni = io.n;
             hd.total = total;
+            hd.off = ob;
             hp.hdr[combo * hp.nhub + hid] = hd;
         }
         __syncthreads();  // scratch reused by the next hub
@@ -599,7 +614,7 @@ __global__ __launch_bounds__(GR_NT) void k_gr_walk(GrGraph gg, const float *__re
                     // a hub: the options this (head, step, rank) gives it, ranked once per call
                     const int64_t combo = ((int64_t)hslot * 3 + step) * ranks + rank;
                     const GrHubHdr hd = hp.hdr[combo * hp.nhub + hid];
-                    const int64_t ob = combo * hp.nopt + hp.hub_off[hid];
+                    const int64_t ob = hd.off;
                     scs.oop = hp.op + ob;
                     scs.ostart = hp.start + ob;
                     scs.otake = hp.take + ob;

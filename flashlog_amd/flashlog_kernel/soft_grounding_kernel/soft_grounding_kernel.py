@@ -17,7 +17,7 @@ from ... import _lib
 from ..._lib import FlGroundGraph, check, ptr
 
 RULE_STEPS = 3  # the reference's default build (FLASHLOG_RULE_STEPS)
-HUB_MIN_GROUPS = 64  # sides with more groups make a node a hub of the walk's option cache
+HUB_MIN_GROUPS = 8  # sides with more groups make a node a hub of the walk's option cache
 HUB_CACHE_MAX_BYTES = 2 << 30  # the cache is skipped above this size
 
 
