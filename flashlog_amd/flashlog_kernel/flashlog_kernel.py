@@ -1071,10 +1071,21 @@ def _sparse_backward(state, grad_values, grad_edge=None):
     return gv, gw
 
 
+def _same_index_rows(gi, rows):
+    """True when the rows of gi are the very tensors in rows (same storage),
+    so the values already follow those coordinates (no device round trip)."""
+    if gi.dim() != 2 or gi.shape[0] != len(rows) or gi.device != rows[0].device:
+        return False
+    return all(gi[k].numel() == r.numel() and gi[k].data_ptr() == r.data_ptr() and gi[k].stride() == r.stride()
+               for k, r in enumerate(rows))
+
+
 def _align_sparse_grad_to_output(grad, out_indices, L, E):
     """Gradient values at the output coordinates (flashlog_kernel.py:360-376)."""
     if not grad.is_sparse:
         return grad[tuple(out_indices)].contiguous()
+    if _same_index_rows(grad._indices(), [out_indices[k] for k in range(out_indices.shape[0])]):
+        return grad._values().contiguous()
     grad = grad.coalesce()
     if torch.equal(grad.indices(), out_indices):
         return grad.values().contiguous()
@@ -1476,7 +1487,11 @@ class Sparse3DNormalizeFunction(autograd.Function):
     def backward(ctx, grad_out):
         sp_batch, sp_level, sp_entity, values, denom, row_ptr = ctx.saved_tensors
         if getattr(grad_out, "is_sparse", False):
-            g = _align_sparse_grad_to_output(grad_out, torch.stack([sp_batch, sp_level, sp_entity]), ctx.L, ctx.E)
+            if _same_index_rows(grad_out._indices(), [sp_batch, sp_level, sp_entity]):
+                g = grad_out._values().contiguous()
+            else:
+                g = _align_sparse_grad_to_output(grad_out, torch.stack([sp_batch, sp_level, sp_entity]), ctx.L,
+                                                 ctx.E)
         else:
             g = grad_out[sp_batch, sp_level, sp_entity]
         gv = _normalize_backward(row_ptr, g, values, denom, ctx.eps)
