@@ -829,16 +829,24 @@ __global__ __launch_bounds__(MB_NT) void k_max_bwd(fl_side ori, fl_side inv, con
 
 constexpr int BWD_NT = 256;
 
+// Block (row, slice): gA for the slice's entities, and the slice's sum of
+// g_ind * A (tree order) -- with one slice written to gw[row, n-1] (the rest
+// of the row zeroed), else stored in gw[row, slice] for k_bwd_identity_fin,
+// which adds the slices in order.
+constexpr int BWD_SLICES_MAX = 32;
+
 __global__ __launch_bounds__(BWD_NT) void k_bwd_identity(const float *__restrict__ g_ind, const float *__restrict__ A,
                                                         const float *__restrict__ w, int64_t E, int64_t n, int wot_i,
-                                                        int add_zero, float *__restrict__ gA,
+                                                        int add_zero, int nsl, float *__restrict__ gA,
                                                         float *__restrict__ gw) {
     __shared__ float part[BWD_NT];
     const int64_t bl = blockIdx.x;
+    const int64_t span = (E + nsl - 1) / nsl;
+    const int64_t e0 = (int64_t)blockIdx.y * span, e1 = e0 + span < E ? e0 + span : E;
     const int t = threadIdx.x;
     const float wid = w[bl * n + (n - 1)];
     float acc = 0.0f;
-    for (int64_t e = t; e < E; e += BWD_NT) {
+    for (int64_t e = e0 + t; e < e1; e += BWD_NT) {
         const int64_t i = bl * E + e;
         if (wot_i) {
             gA[i] = 0.0f;
@@ -855,9 +863,44 @@ __global__ __launch_bounds__(BWD_NT) void k_bwd_identity(const float *__restrict
         if (t < st) part[t] = fl_add(part[t], part[t + st]);
         __syncthreads();
     }
+    if (nsl > 1) {
+        if (t == 0) gw[bl * n + blockIdx.y] = wot_i ? 0.0f : part[0];
+        return;
+    }
     for (int64_t r = t; r < n; r += BWD_NT) gw[bl * n + r] = 0.0f;
     __syncthreads();
     if (t == 0 && !wot_i) gw[bl * n + (n - 1)] = part[0];
+}
+
+__global__ __launch_bounds__(BWD_NT) void k_bwd_identity_fin(int64_t n, int nsl, int wot_i,
+                                                            float *__restrict__ gw) {
+    __shared__ float total;
+    const int64_t bl = blockIdx.x;
+    const int t = threadIdx.x;
+    if (t == 0) {
+        float sum = 0.0f;
+        for (int c = 0; c < nsl; ++c) sum = fl_add(sum, gw[bl * n + c]);
+        total = sum;
+    }
+    __syncthreads();
+    for (int64_t r = t; r < n; r += BWD_NT) gw[bl * n + r] = 0.0f;
+    __syncthreads();
+    if (t == 0 && !wot_i) gw[bl * n + (n - 1)] = total;
+}
+
+// The identity term of a dense backward: gA (every entity) and gw[:, n-1],
+// rows split into slices so that the launch fills the chip.
+static void bwd_identity(hipStream_t st, const float *g_ind, const float *A, const float *w, int64_t BL, int64_t E,
+                         int64_t n, int wot_i, int add_zero, float *gA, float *gw) {
+    int64_t nsl = (E + 4 * BWD_NT - 1) / (4 * BWD_NT);
+    if (nsl > BWD_SLICES_MAX) nsl = BWD_SLICES_MAX;
+    if (nsl > n - 1) nsl = n - 1;  // the partials live in gw[row, 0 .. n-2]
+    if (nsl < 1) nsl = 1;
+    FL_LAUNCH("k_bwd_identity", k_bwd_identity, dim3((unsigned)BL, (unsigned)nsl), dim3(BWD_NT), 0, st, g_ind,
+                   A, w, E, n, wot_i, add_zero, (int)nsl, gA, gw);
+    if (nsl > 1)
+        FL_LAUNCH("k_bwd_identity_fin", k_bwd_identity_fin, dim3((unsigned)BL), dim3(BWD_NT), 0, st, n,
+                       (int)nsl, wot_i, gw);
 }
 
 constexpr int RL_NT = 1024;
@@ -1200,8 +1243,7 @@ int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv, 
     const int64_t nw = (BL + 31) / 32;
     const int do_topk = (topk_edges > 0 && topk_edges < ((int64_t)1 << 60)) ? 1 : 0;
     const int64_t K = do_topk ? topk_edges : 0;
-    FL_LAUNCH("k_bwd_identity", k_bwd_identity, dim3((unsigned)BL), dim3(BWD_NT), 0, st, grad_ind, A, w, E, n, wot_i,
-              1, grad_A, grad_w);
+    bwd_identity(st, grad_ind, A, w, BL, E, n, wot_i, 1, grad_A, grad_w);
     // the forward's frontier (same A and w: same admitted edges); no identity output
     FL_LAUNCH("k_col_count", k_col_count, dim3((unsigned)((nw * E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, A,
               w, BL, E, n, wot_i, (float *)nullptr, ws.bm, ws.hard_count);
@@ -1290,8 +1332,7 @@ int fl_dense_max_backward(void *stream, const fl_side *ori, const fl_side *inv, 
             return fl_fail(FL_ERR_ARG, "dense_max_backward: side without position arrays");
     if (BL == 0 || E == 0) return FL_OK;
     hipStream_t st = (hipStream_t)stream;
-    FL_LAUNCH("k_bwd_identity", k_bwd_identity, dim3((unsigned)BL), dim3(BWD_NT), 0, st, grad_ind, A, w, E, n, wot_i,
-              0, grad_A, grad_w);
+    bwd_identity(st, grad_ind, A, w, BL, E, n, wot_i, 0, grad_A, grad_w);
     const size_t lds = sizeof(float) * (size_t)(2 * r_size > 0 ? 2 * r_size : 1);
     FL_LAUNCH("k_max_bwd", k_max_bwd, dim3((unsigned)((E + MB_NT - 1) / MB_NT), (unsigned)BL), dim3(MB_NT), lds, st,
               *ori, *inv, A, w, grad_ori, grad_inv, arg_ori, arg_inv, BL, E, n, r_size, grad_A, grad_w);
