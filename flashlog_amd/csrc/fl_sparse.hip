@@ -12,11 +12,12 @@
 //
 // Pipeline (rows r = b*L + l; entries must be sorted by row):
 //   plan    k_sp_rowptr   entry range of every row, input validation
-//           k_sp_select   per (entry, side): c2 threshold and cut, item and
-//                         run counts (a run = the kept edges of one group)
-//           scan          item and run offsets of every entry (raw order)
+//           k_sp_select   per (entry, side): c2 threshold and cut (training:
+//                         quota parameters), item counts and 64-item chunks
+//           scan          item and chunk offsets of every entry (raw order)
 //           k_sp_rowinfo  item range and tile count of every row; scan
-//   expand  k_sp_runs     wave per entry: one descriptor per run
+//   expand  k_sp_runs     wave per entry: one descriptor per run (the kept
+//                         edges of one group) and the entry's chunk records
 //           k_sp_items    wave per 64 raw items: destination and value of
 //                         each, from the runs that cover the chunk
 //           k_sp_hist     workgroup per tile: (row, bucket, tile) histogram
@@ -31,9 +32,13 @@
 //                         k_sp_accum_hot (chunks into a dense LDS accumulator,
 //                         persistent); max: k_sp_max / k_sp_max_hot
 //           scan          output offsets
+//           k_sp_local_to_out  (with a backward) every raw item's output index
 //   emit    k_sp_emit     coalesced COO (b, l, e, v), ascending key
-//   backward k_sp_bwd     wave per entry: the same walk, gradients gathered
-//                         through the saved raw-item -> output map
+//   backward k_sp_bwd     wave per entry over its raw items (CSR position,
+//                         column and output index saved by the forward)
+// The plan and the run writer may visit entries in a given order (by source
+// entity: a source's rows then share cached group records); a Boolean
+// visibility mask may be read as a bitmap (k_mask_bits).
 #include <limits.h>
 
 #include "fl_abi.h"
