@@ -628,7 +628,8 @@ SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_
                   "k_sp_hist",
                   "k_sp_partition", "k_sp_accum_small", "k_sp_accum_mid", "k_sp_accum_hot", "k_sp_emit", "k_sp_local_to_out",
                   "k_norm_fwd", "k_norm_bwd", "k_sp_bwd", "k_fill_f32", "k_scan_tiles", "k_scan_totals",
-                  "k_scan_apply", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask"]
+                  "k_scan_apply", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask",
+                  "k_cs_rank", "k_cs_emit"]
 
 
 def items_bytes(plan):
@@ -695,8 +696,7 @@ def main_sparse(args):
         s = state0
         for t_ in range(T):
             s = fk.normalize_sparse3d(hop(s, Wl[t_]))
-        idx = s.indices()
-        final = torch.sparse_coo_tensor(torch.stack([idx[0], idx[2]]), s.values(), [B, E]).coalesce()
+        final = fk.sum_sp_3d(s)  # src/model_DRUM_kernel_sp.py:204 (sum_sp_3d, :22-28)
         if not train:
             return final
         # log loss on each query's target entity (src/utils.py:37-47, tau_2 = 1)

@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 17
+ABI_VERSION = 18
 FL_SEG = 32
 FL_SUP = 16
 
@@ -131,6 +131,11 @@ _SIGS = {
                                           ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
     "fl_sparse_topc": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 + [ctypes.c_void_p] * 3),
     "fl_sparse_rowptr_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "fl_sparse_channel_sum_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3),
+    "fl_sparse_channel_sum_plan": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 +
+                                   [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "fl_sparse_channel_sum_emit": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3 +
+                                   [ctypes.c_void_p, ctypes.c_int64] + [ctypes.c_void_p] * 4),
     "fl_reservoir_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4),
     "fl_reservoir": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,

@@ -2367,6 +2367,88 @@ int sp_check(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, con
 
 }  // namespace
 
+// ---- channel sum of a coalesced [B, L, E] state (the models' sum_sp_3d) ----
+// Within one query b the L channel rows are each sorted by entity, so the
+// (b, e) order of the re-indexed entries is a merge of L sorted lists: an
+// entry's merged position is its index in its own row plus, in every other
+// row of b, the entries before it (entity < e, or <= e in an earlier channel,
+// so ties keep channel order as a stable sort does).  An entry is a head when
+// no earlier channel holds its entity; heads are scanned into output slots and
+// each head adds its run of the merged order from 0 in that order.
+__device__ __forceinline__ int64_t cs_lower_bound(const int64_t *__restrict__ se, int64_t lo, int64_t hi, int64_t e) {
+    while (lo < hi) {
+        const int64_t mid = lo + ((hi - lo) >> 1);
+        if (se[mid] < e) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+__global__ void k_cs_rank(const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
+                          const int64_t *__restrict__ se, int64_t nnz, int64_t L, int64_t R,
+                          const int64_t *__restrict__ row_ptr, int32_t *__restrict__ perm,
+                          int32_t *__restrict__ head, int64_t *__restrict__ err) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    const int64_t b = sb[i], l = sl[i], e = se[i];
+    if (b < 0 || l < 0 || l >= L || b * L + l >= R) return;  // flagged by k_sp_rowptr
+    const int64_t r = b * L + l;
+    const int64_t rs = row_ptr[r];
+    if (i > rs && se[i - 1] >= e) {  // entities not strictly increasing within the row
+        atomicMax((unsigned long long *)err, 3ull);
+        return;
+    }
+    int64_t pos = i - rs;
+    int h = 1;
+    for (int64_t q = 0; q < L; ++q) {
+        if (q == l) continue;
+        const int64_t a = row_ptr[b * L + q], z = row_ptr[b * L + q + 1];
+        const int64_t lb = cs_lower_bound(se, a, z, e);
+        if (q < l && lb < z && se[lb] == e) {
+            ++pos;
+            h = 0;
+        }
+        pos += lb - a;
+    }
+    const int64_t m = row_ptr[b * L] + pos;
+    if (m < row_ptr[b * L] || m >= row_ptr[b * L + L]) {
+        atomicMax((unsigned long long *)err, 4ull);
+        return;
+    }
+    perm[m] = (int32_t)i;
+    head[m] = h;
+}
+
+__global__ void k_cs_plan_out(const int64_t *__restrict__ hoff, int64_t nnz, const int64_t *__restrict__ err,
+                              int64_t *__restrict__ plan) {
+    if (threadIdx.x == 0) {
+        plan[0] = hoff[nnz];
+        plan[1] = err[0];
+    }
+}
+
+__global__ void k_cs_emit(const int64_t *__restrict__ sb, const int64_t *__restrict__ se,
+                          const float *__restrict__ v, int64_t nnz, const int32_t *__restrict__ perm,
+                          const int32_t *__restrict__ head, const int64_t *__restrict__ hoff, int64_t nout,
+                          int64_t *__restrict__ out_b, int64_t *__restrict__ out_e, float *__restrict__ out_v,
+                          int32_t *__restrict__ slot) {
+    const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= nnz || !head[m]) return;
+    const int64_t o = hoff[m];
+    const int32_t i = perm[m];
+    if (o < 0 || o >= nout || i < 0 || i >= nnz) return;
+    float acc = 0.0f;
+    for (int64_t k = m; k < nnz && (k == m || !head[k]); ++k) {
+        const int32_t j = perm[k];
+        if (j < 0 || j >= nnz) break;
+        acc = acc + v[j];
+        slot[j] = (int32_t)o;
+    }
+    out_b[o] = sb[i];
+    out_e[o] = se[i];
+    out_v[o] = acc;
+}
+
 extern "C" {
 
 int64_t fl_sparse_buckets(int64_t E) { return sp_buckets(E); }
@@ -2729,6 +2811,75 @@ int fl_sparse_normalize_backward(void *stream, const int64_t *row_ptr, const flo
         FL_LAUNCH("k_norm_bwd", k_norm_bwd, dim3((unsigned)R), dim3(NM_NT), 0, (hipStream_t)stream, row_ptr, grad,
                   v, denom, eps, grad_v);
     return fl_check_launch("sparse_normalize_backward");
+}
+
+struct CsLayout {
+    int64_t *row_ptr, *err, *hoff, *tmp;
+    int32_t *perm, *head;
+    size_t bytes;
+};
+
+static CsLayout cs_layout(int64_t nnz, int64_t R, char *base) {
+    CsLayout x{};
+    size_t off = 0;
+    auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
+    const int64_t n1 = nnz > 0 ? nnz : 1;
+    x.row_ptr = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
+    x.err = (int64_t *)take(sizeof(int64_t) * 2);
+    x.hoff = (int64_t *)take(sizeof(int64_t) * (size_t)(n1 + 1));
+    x.tmp = (int64_t *)take(scan_tmp_bytes(n1 + 1));
+    x.perm = (int32_t *)take(sizeof(int32_t) * (size_t)n1);
+    x.head = (int32_t *)take(sizeof(int32_t) * (size_t)n1);
+    x.bytes = off;
+    return x;
+}
+
+size_t fl_sparse_channel_sum_bytes(int64_t nnz, int64_t B, int64_t L) {
+    if (nnz < 0 || B < 0 || L < 0) return 0;
+    return cs_layout(nnz, B * L, nullptr).bytes;
+}
+
+int fl_sparse_channel_sum_plan(void *stream, const int64_t *sp_b, const int64_t *sp_l, const int64_t *sp_e,
+                               int64_t nnz, int64_t B, int64_t L, int64_t E, void *ws, size_t ws_bytes,
+                               int64_t *plan) {
+    if (nnz < 0 || B < 0 || L < 0 || E < 0) return fl_fail(FL_ERR_ARG, "sparse_channel_sum: negative size");
+    if (nnz > INT32_MAX) return fl_fail(FL_ERR_ARG, "sparse_channel_sum: more than 2^31 - 1 entries");
+    if (!ws || !plan || (nnz > 0 && (!sp_b || !sp_l || !sp_e)))
+        return fl_fail(FL_ERR_ARG, "sparse_channel_sum: null argument");
+    const int64_t R = B * L;
+    if (ws_bytes < fl_sparse_channel_sum_bytes(nnz, B, L))
+        return fl_fail(FL_ERR_ARG, "sparse_channel_sum: workspace too small");
+    CsLayout x = cs_layout(nnz, R, (char *)ws);
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, x.row_ptr, R + 1,
+              (int64_t)0);
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3(1), dim3(64), 0, st, x.err, (int64_t)2, (int64_t)0);
+    const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
+    FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, sp_e,
+              nnz, B, L, E, x.row_ptr, x.err);
+    if (nnz > 0) {
+        FL_LAUNCH("k_fill_i32", k_fill_i32, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, x.head, nnz, 0);
+        FL_LAUNCH("k_cs_rank", k_cs_rank, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, sp_e,
+                  nnz, L, R, x.row_ptr, x.perm, x.head, x.err);
+    }
+    int rc = exclusive_scan(st, x.head, x.hoff, nnz, x.tmp);
+    if (rc != FL_OK) return rc;
+    FL_LAUNCH("k_cs_plan_out", k_cs_plan_out, dim3(1), dim3(64), 0, st, x.hoff, nnz, x.err, plan);
+    return fl_check_launch("sparse_channel_sum_plan");
+}
+
+int fl_sparse_channel_sum_emit(void *stream, const int64_t *sp_b, const int64_t *sp_e, const float *v, int64_t nnz,
+                               int64_t B, int64_t L, void *ws, int64_t nout, int64_t *out_b, int64_t *out_e,
+                               float *out_v, int32_t *slot) {
+    if (nnz < 0 || B < 0 || L < 0 || nout < 0 || nout > nnz)
+        return fl_fail(FL_ERR_ARG, "sparse_channel_sum_emit: bad sizes");
+    if (!ws || (nnz > 0 && (!sp_b || !sp_e || !v || !slot)) || (nout > 0 && (!out_b || !out_e || !out_v)))
+        return fl_fail(FL_ERR_ARG, "sparse_channel_sum_emit: null argument");
+    CsLayout x = cs_layout(nnz, B * L, (char *)ws);
+    if (nnz > 0)
+        FL_LAUNCH("k_cs_emit", k_cs_emit, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                  sp_b, sp_e, v, nnz, x.perm, x.head, x.hoff, nout, out_b, out_e, out_v, slot);
+    return fl_check_launch("sparse_channel_sum_emit");
 }
 
 }  // extern "C"

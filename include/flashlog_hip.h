@@ -409,6 +409,29 @@ int fl_sparse_normalize_backward(void *stream, const int64_t *row_ptr,
                                  const float *denom, int64_t R, float eps,
                                  float *grad_v);
 
+/* Replaces the models' channel sum sum_sp_3d (src/model_DRUM_kernel_sp.py:
+ * 22-28, also the sum of src/model_smDRUM_kernel_sp.py and
+ * src/model_NeuralLP_kernel_sp.py): of a coalesced [B, L, E] state (entries
+ * sorted by (b, l), entities strictly increasing within a row), the [B, E]
+ * state out[b, e] = sum over l of v[b, l, e], added from 0 in channel order
+ * (torch's coalesce of the (b, e) re-index sorts stably, so duplicates add
+ * in l order).  fl_sparse_channel_sum_plan ranks the entries into the
+ * caller's workspace (fl_sparse_channel_sum_bytes) and writes plan[2] =
+ * {outputs, error} on the device (error != 0: entries out of range or not
+ * coalesced); after the host has read it, fl_sparse_channel_sum_emit (same
+ * workspace) writes out_b, out_e, out_v [outputs], in (b, e) order, and
+ * slot[nnz], the output slot of every entry (for the backward). */
+size_t fl_sparse_channel_sum_bytes(int64_t nnz, int64_t B, int64_t L);
+int fl_sparse_channel_sum_plan(void *stream, const int64_t *sp_b,
+                               const int64_t *sp_l, const int64_t *sp_e,
+                               int64_t nnz, int64_t B, int64_t L, int64_t E,
+                               void *ws, size_t ws_bytes, int64_t *plan);
+int fl_sparse_channel_sum_emit(void *stream, const int64_t *sp_b,
+                               const int64_t *sp_e, const float *v,
+                               int64_t nnz, int64_t B, int64_t L, void *ws,
+                               int64_t nout, int64_t *out_b, int64_t *out_e,
+                               float *out_v, int32_t *slot);
+
 /* ---- rule-bank scoring ------------------------------------------------- */
 
 /* Replaces the dense accumulation of rules/shared_inference.py:200-206: the

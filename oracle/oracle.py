@@ -461,6 +461,34 @@ def sparse_normalize(b, l, v, B, L, eps=1e-7):
     return out, denom
 
 
+def sum_sp_3d(b, l, e, v, B, L, E):
+    """Channel sum of a coalesced [B, L, E] state (src/model_DRUM_kernel_sp.py:
+    22-28): torch's coalesce of the (b, e) re-index, whose stable sort keeps
+    each key's entries in channel order, adds them from 0 in that order.
+    Returns (out_b, out_e, out_v, slot), slot[i] the output of entry i.
+    Pinned in tests/test_oracle_sparse.py by brute-force sums and torch's CPU
+    coalesce on dyadic values (exact in any order) and by a case whose
+    rounding depends on the channel order."""
+    b, l, e = (np.asarray(x, np.int64) for x in (b, l, e))
+    v = np.asarray(v, np.float32)
+    n = v.shape[0]
+    key = b * E + e
+    order = np.argsort(key, kind="stable")
+    ks, vs = key[order], v[order]
+    head = np.ones(n, bool)
+    head[1:] = ks[1:] != ks[:-1]
+    gid = np.cumsum(head) - 1
+    start = np.flatnonzero(head)
+    out = np.zeros(start.shape[0], np.float32)
+    rank = np.arange(n) - start[gid] if n else np.zeros(0, np.int64)
+    for k in range(int(rank.max()) + 1 if n else 0):
+        sel = rank == k
+        out[gid[sel]] = out[gid[sel]] + vs[sel]
+    slot = np.empty(n, np.int64)
+    slot[order] = gid
+    return ks[start] // E, ks[start] % E, out, slot
+
+
 def sparse_topc(b, l, v, L, c):
     """Kept entry indices of the c1 budget on a coalesced COO state
     (flashlog_kernel.py:1092-1140): per (b, l) row with more than c nonzeros,

@@ -162,3 +162,40 @@ def test_sparse_normalize_closed_form():
     np.add.at(d, row, v.astype(np.float64))
     np.testing.assert_allclose(denom, d, rtol=1e-6)
     np.testing.assert_allclose(out, v / np.maximum(d[row], 1e-7), rtol=1e-6)
+
+
+def _coalesced_state(rng, B, L, E, n):
+    keys = np.unique(rng.choice(B * L * E, size=n, replace=False))
+    return keys // (L * E), (keys // E) % L, keys % E
+
+
+def test_sum_sp_3d_matches_brute_force_and_torch():
+    import torch
+    rng = np.random.default_rng(7)
+    B, L, E = 6, 3, 50
+    b, l, e = _coalesced_state(rng, B, L, E, 400)
+    v = (rng.integers(1, 256, b.shape[0]) / 64.0).astype(np.float32)  # dyadic: sums exact in any order
+    ob, oe, ov, slot = O.sum_sp_3d(b, l, e, v, B, L, E)
+    acc = {}
+    for bb, ee, vv in zip(b.tolist(), e.tolist(), v.tolist()):
+        acc[(bb, ee)] = acc.get((bb, ee), 0.0) + vv
+    ks = sorted(acc)
+    assert [(int(x), int(y)) for x, y in zip(ob, oe)] == ks
+    assert np.array_equal(ov, np.array([acc[k] for k in ks], np.float32))
+    t = torch.sparse_coo_tensor(torch.from_numpy(np.stack([b, e])), torch.from_numpy(v), [B, E]).coalesce()
+    assert np.array_equal(t.indices().numpy(), np.stack([ob, oe]))
+    assert np.array_equal(t.values().numpy().view(np.int32), ov.view(np.int32))
+    assert np.array_equal(ob[slot], b) and np.array_equal(oe[slot], e)
+
+
+def test_sum_sp_3d_adds_in_channel_order():
+    # 1e8 + 1 rounds back to 1e8 in float32, so the result depends on the order
+    b = np.zeros(3, np.int64)
+    l = np.arange(3, dtype=np.int64)
+    e = np.full(3, 4, np.int64)
+    _, _, ov, _ = O.sum_sp_3d(b, l, e, np.array([1e8, 1.0, -1e8], np.float32), 1, 3, 9)
+    assert ov.tolist() == [0.0]
+    _, _, ov, _ = O.sum_sp_3d(b, l, e, np.array([1e8, -1e8, 1.0], np.float32), 1, 3, 9)
+    assert ov.tolist() == [1.0]
+    _, _, ov, slot = O.sum_sp_3d(np.zeros(0), np.zeros(0), np.zeros(0), np.zeros(0, np.float32), 2, 3, 9)
+    assert ov.shape == (0,) and slot.shape == (0,)
