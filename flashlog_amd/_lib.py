@@ -135,7 +135,7 @@ _SIGS = {
     "fl_sparse_channel_sum_plan": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 +
                                    [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "fl_sparse_channel_sum_emit": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3 +
-                                   [ctypes.c_void_p, ctypes.c_int64] + [ctypes.c_void_p] * 4),
+                                   [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64] + [ctypes.c_void_p] * 4),
     "fl_reservoir_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 4),
     "fl_reservoir": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
                                     ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,

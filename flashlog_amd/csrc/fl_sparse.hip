@@ -2427,6 +2427,9 @@ __global__ void k_cs_plan_out(const int64_t *__restrict__ hoff, int64_t nnz, con
     }
 }
 
+// op 0: the sum from 0 in channel order; op 1: the maximum (first of equal
+// values kept, NaN propagated, as torch's amax).
+template <int OP>
 __global__ void k_cs_emit(const int64_t *__restrict__ sb, const int64_t *__restrict__ se,
                           const float *__restrict__ v, int64_t nnz, const int32_t *__restrict__ perm,
                           const int32_t *__restrict__ head, const int64_t *__restrict__ hoff, int64_t nout,
@@ -2441,7 +2444,9 @@ __global__ void k_cs_emit(const int64_t *__restrict__ sb, const int64_t *__restr
     for (int64_t k = m; k < nnz && (k == m || !head[k]); ++k) {
         const int32_t j = perm[k];
         if (j < 0 || j >= nnz) break;
-        acc = acc + v[j];
+        const float x = v[j];
+        if (OP == 0) acc = acc + x;
+        else acc = (k == m || x > acc || x != x) ? x : acc;
         slot[j] = (int32_t)o;
     }
     out_b[o] = sb[i];
@@ -2869,16 +2874,17 @@ int fl_sparse_channel_sum_plan(void *stream, const int64_t *sp_b, const int64_t 
 }
 
 int fl_sparse_channel_sum_emit(void *stream, const int64_t *sp_b, const int64_t *sp_e, const float *v, int64_t nnz,
-                               int64_t B, int64_t L, void *ws, int64_t nout, int64_t *out_b, int64_t *out_e,
-                               float *out_v, int32_t *slot) {
+                               int64_t B, int64_t L, int op, void *ws, int64_t nout, int64_t *out_b,
+                               int64_t *out_e, float *out_v, int32_t *slot) {
+    if (op != 0 && op != 1) return fl_fail(FL_ERR_ARG, "sparse_channel_sum_emit: op must be 0 (sum) or 1 (max)");
     if (nnz < 0 || B < 0 || L < 0 || nout < 0 || nout > nnz)
         return fl_fail(FL_ERR_ARG, "sparse_channel_sum_emit: bad sizes");
     if (!ws || (nnz > 0 && (!sp_b || !sp_e || !v || !slot)) || (nout > 0 && (!out_b || !out_e || !out_v)))
         return fl_fail(FL_ERR_ARG, "sparse_channel_sum_emit: null argument");
     CsLayout x = cs_layout(nnz, B * L, (char *)ws);
     if (nnz > 0)
-        FL_LAUNCH("k_cs_emit", k_cs_emit, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                  sp_b, sp_e, v, nnz, x.perm, x.head, x.hoff, nout, out_b, out_e, out_v, slot);
+        FL_LAUNCH("k_cs_emit", op ? k_cs_emit<1> : k_cs_emit<0>, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0,
+                  (hipStream_t)stream, sp_b, sp_e, v, nnz, x.perm, x.head, x.hoff, nout, out_b, out_e, out_v, slot);
     return fl_check_launch("sparse_channel_sum_emit");
 }
 

@@ -1505,6 +1505,30 @@ def normalize_sparse3d(s, eps=1e-7):
     return Sparse3DNormalizeFunction.apply(idx[0], idx[1], idx[2], s.values(), B, L, E, eps)
 
 
+def _channel_reduce(sp_batch, sp_level, sp_entity, sp_value, B, L, E, op):
+    _require_cuda(sp_batch, sp_level, sp_entity, sp_value)
+    dev = sp_value.device
+    sb, sl, se = (x.long().contiguous() for x in (sp_batch, sp_level, sp_entity))
+    v = sp_value.detach().contiguous().float()
+    nnz = v.numel()
+    lib = _lib.lib()
+    st = _stream(v)
+    ws = torch.empty(max(int(lib.fl_sparse_channel_sum_bytes(nnz, B, L)), 1), dtype=torch.uint8, device=dev)
+    plan = torch.empty(2, dtype=torch.int64, device=dev)
+    check(lib.fl_sparse_channel_sum_plan(st, ptr(sb), ptr(sl), ptr(se), nnz, B, L, E, ptr(ws), ws.numel(),
+                                         ptr(plan)), "sparse_channel_sum_plan")
+    nout, err = (int(x) for x in plan.cpu())
+    if err != 0:
+        raise ValueError("the channel reduction needs a state coalesced by (batch, rule, entity) within its shape")
+    idx = torch.empty((2, nout), dtype=torch.int64, device=dev)
+    out = torch.empty(nout, dtype=torch.float32, device=dev)
+    slot = torch.empty(nnz, dtype=torch.int32, device=dev)
+    check(lib.fl_sparse_channel_sum_emit(st, ptr(sb), ptr(se), ptr(v), nnz, B, L, op, ptr(ws), nout,
+                                         ptr(idx[0]), ptr(idx[1]), ptr(out), ptr(slot)),
+          "sparse_channel_sum_emit")
+    return idx, out, slot.long(), v
+
+
 class Sparse3DChannelSumFunction(autograd.Function):
     """Values of the channel sum of a coalesced [B, L, E] state: per (b, e)
     the entries of every channel added from 0 in channel order, as torch's
@@ -1513,26 +1537,7 @@ class Sparse3DChannelSumFunction(autograd.Function):
 
     @staticmethod
     def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, B, L, E):
-        _require_cuda(sp_batch, sp_level, sp_entity, sp_value)
-        dev = sp_value.device
-        sb, sl, se = (x.long().contiguous() for x in (sp_batch, sp_level, sp_entity))
-        v = sp_value.detach().contiguous().float()
-        nnz = v.numel()
-        lib = _lib.lib()
-        st = _stream(v)
-        ws = torch.empty(max(int(lib.fl_sparse_channel_sum_bytes(nnz, B, L)), 1), dtype=torch.uint8, device=dev)
-        plan = torch.empty(2, dtype=torch.int64, device=dev)
-        check(lib.fl_sparse_channel_sum_plan(st, ptr(sb), ptr(sl), ptr(se), nnz, B, L, E, ptr(ws), ws.numel(),
-                                             ptr(plan)), "sparse_channel_sum_plan")
-        nout, err = (int(x) for x in plan.cpu())
-        if err != 0:
-            raise ValueError("sum_sp_3d needs a state coalesced by (batch, rule, entity) within its shape")
-        idx = torch.empty((2, nout), dtype=torch.int64, device=dev)
-        out = torch.empty(nout, dtype=torch.float32, device=dev)
-        slot = torch.empty(nnz, dtype=torch.int32, device=dev)
-        check(lib.fl_sparse_channel_sum_emit(st, ptr(sb), ptr(se), ptr(v), nnz, B, L, ptr(ws), nout,
-                                             ptr(idx[0]), ptr(idx[1]), ptr(out), ptr(slot)),
-              "sparse_channel_sum_emit")
+        idx, out, slot, _ = _channel_reduce(sp_batch, sp_level, sp_entity, sp_value, B, L, E, 0)
         ctx.slot = slot
         ctx.mark_non_differentiable(idx)
         return idx, out
@@ -1541,18 +1546,54 @@ class Sparse3DChannelSumFunction(autograd.Function):
     def backward(ctx, grad_idx, grad_out):
         if grad_out is None:
             return (None,) * 7
-        g = grad_out.contiguous().float()
-        return None, None, None, g[ctx.slot.long()], None, None, None
+        return None, None, None, grad_out.contiguous().float()[ctx.slot], None, None, None
+
+
+class Sparse3DChannelMaxFunction(autograd.Function):
+    """Values of the channel maximum of a coalesced [B, L, E] state
+    (src/model_mmDRUM_kernel_sp.py:17-32, scatter_reduce amax with
+    include_self=False).  Backward as torch's for amax: an output's gradient
+    is divided evenly among the entries equal to it and, where the maximum
+    is 0, the zero the reference reduces into (torch counts that initial
+    value among the ties)."""
+
+    @staticmethod
+    def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, B, L, E):
+        idx, out, slot, v = _channel_reduce(sp_batch, sp_level, sp_entity, sp_value, B, L, E, 1)
+        ctx.save_for_backward(v, out, slot)
+        ctx.mark_non_differentiable(idx)
+        return idx, out
+
+    @staticmethod
+    def backward(ctx, grad_idx, grad_out):
+        if grad_out is None:
+            return (None,) * 7
+        v, out, slot = ctx.saved_tensors
+        value = out[slot]
+        is_max = (v == value).to(v.dtype)
+        count = (out == 0).to(out.dtype).scatter_add_(0, slot, is_max)
+        share = grad_out.contiguous().float() / count
+        return None, None, None, is_max * share[slot], None, None, None
+
+
+def _channel_state(s, fn):
+    s = s if s.is_coalesced() else s.coalesce()
+    B, L, E = s.shape
+    idx = s.indices()
+    out_idx, out_val = fn.apply(idx[0], idx[1], idx[2], s.values(), B, L, E)
+    return torch.sparse_coo_tensor(out_idx, out_val, [B, E], is_coalesced=True)
 
 
 def sum_sp_3d(s):
     """[B, L, E] -> [B, E]: the sum over channels (src/model_DRUM_kernel_sp.py:
     22-28), a coalesced COO tensor whose values carry the gradient."""
-    s = s if s.is_coalesced() else s.coalesce()
-    B, L, E = s.shape
-    idx = s.indices()
-    out_idx, out_val = Sparse3DChannelSumFunction.apply(idx[0], idx[1], idx[2], s.values(), B, L, E)
-    return torch.sparse_coo_tensor(out_idx, out_val, [B, E], is_coalesced=True)
+    return _channel_state(s, Sparse3DChannelSumFunction)
+
+
+def max_sp_3d(s):
+    """[B, L, E] -> [B, E]: the maximum over channels
+    (src/model_mmDRUM_kernel_sp.py:17-32), a coalesced COO tensor."""
+    return _channel_state(s, Sparse3DChannelMaxFunction)
 
 
 def _sparse_sum_selected_nodes(sp_state, entries, w, csr_struct, mask_values,

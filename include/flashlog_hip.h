@@ -420,7 +420,10 @@ int fl_sparse_normalize_backward(void *stream, const int64_t *row_ptr,
  * {outputs, error} on the device (error != 0: entries out of range or not
  * coalesced); after the host has read it, fl_sparse_channel_sum_emit (same
  * workspace) writes out_b, out_e, out_v [outputs], in (b, e) order, and
- * slot[nnz], the output slot of every entry (for the backward). */
+ * slot[nnz], the output slot of every entry (for the backward).  op 1
+ * instead takes the maximum over the channels (max_sp_3d,
+ * src/model_mmDRUM_kernel_sp.py:17-32: scatter_reduce amax, NaN propagated;
+ * of equal values the first channel's is kept); op 0 is the sum. */
 size_t fl_sparse_channel_sum_bytes(int64_t nnz, int64_t B, int64_t L);
 int fl_sparse_channel_sum_plan(void *stream, const int64_t *sp_b,
                                const int64_t *sp_l, const int64_t *sp_e,
@@ -428,9 +431,9 @@ int fl_sparse_channel_sum_plan(void *stream, const int64_t *sp_b,
                                void *ws, size_t ws_bytes, int64_t *plan);
 int fl_sparse_channel_sum_emit(void *stream, const int64_t *sp_b,
                                const int64_t *sp_e, const float *v,
-                               int64_t nnz, int64_t B, int64_t L, void *ws,
-                               int64_t nout, int64_t *out_b, int64_t *out_e,
-                               float *out_v, int32_t *slot);
+                               int64_t nnz, int64_t B, int64_t L, int op,
+                               void *ws, int64_t nout, int64_t *out_b,
+                               int64_t *out_e, float *out_v, int32_t *slot);
 
 /* ---- rule-bank scoring ------------------------------------------------- */
 

@@ -75,3 +75,38 @@ def test_channel_sum_empty_and_errors():
     bad = torch.sparse_coo_tensor(idx, torch.ones(3, device=dev), [1, 3, 10], is_coalesced=True)
     with pytest.raises(ValueError):
         fk.sum_sp_3d(bad)
+
+
+def _reference_max_sp_3d(s):
+    # the reference's steps (src/model_mmDRUM_kernel_sp.py:17-32) in torch
+    s = s.coalesce()
+    idx, val = s.indices(), s.values()
+    B, _, E = s.shape
+    flat_key = idx[0] * E + idx[2]
+    order = torch.argsort(flat_key)
+    flat_key, val = flat_key[order], val[order]
+    uniq, inv = torch.unique_consecutive(flat_key, return_inverse=True)
+    out_val = torch.zeros(uniq.shape[0], device=val.device, dtype=val.dtype)
+    out_val = out_val.scatter_reduce(0, inv, val, reduce="amax", include_self=False)
+    return torch.sparse_coo_tensor(torch.stack([uniq // E, uniq % E]), out_val, [B, E]).coalesce()
+
+
+@pytest.mark.parametrize("B,L,E,n,seed", [(4, 3, 60, 300, 10), (16, 3, 5000, 20000, 11), (8, 5, 200, 6000, 12),
+                                          (256, 3, 4_600_000, 2_000_000, 13)])
+def test_channel_max_matches_reference_steps(B, L, E, n, seed):
+    fk = _fk()
+    dev = torch.device("cuda:0")
+    b, l, e, _ = _state(seed, B, L, E, n)
+    rng = np.random.default_rng(seed)
+    v = (rng.integers(0, 6, b.shape[0]) / 8.0).astype(np.float32)  # ties and exact zeros
+    tb, tl, te = (torch.from_numpy(x).to(dev) for x in (b, l, e))
+    vt = torch.from_numpy(v).to(dev).requires_grad_(True)
+    vr = vt.detach().clone().requires_grad_(True)
+    got = fk.max_sp_3d(torch.sparse_coo_tensor(torch.stack([tb, tl, te]), vt, [B, L, E], is_coalesced=True))
+    ref = _reference_max_sp_3d(torch.sparse_coo_tensor(torch.stack([tb, tl, te]), vr, [B, L, E]))
+    assert torch.equal(got.indices(), ref.indices())
+    assert torch.equal(got.values().detach().view(torch.int32), ref.values().detach().view(torch.int32))
+    g = torch.randn(ref.values().shape[0], device=dev)
+    (got.values() * g).sum().backward()
+    (ref.values() * g).sum().backward()
+    assert torch.equal(vt.grad.view(torch.int32), vr.grad.view(torch.int32))
