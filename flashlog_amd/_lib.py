@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 18
+ABI_VERSION = 19
 FL_SEG = 32
 FL_SUP = 16
 
@@ -86,6 +86,9 @@ class FlGroundGraph(ctypes.Structure):
 _SIGS = {
     "fl_last_error": (ctypes.c_char_p, []),
     "fl_abi_version": (ctypes.c_int, []),
+    "fl_side_bytes": (ctypes.c_size_t, []),
+    "fl_sparse_hop_bytes": (ctypes.c_size_t, []),
+    "fl_ground_graph_bytes": (ctypes.c_size_t, []),
     "fl_csr_build_side": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64] + [ctypes.c_void_p] * 11 +
                           [ctypes.POINTER(ctypes.c_int64)]),
     "fl_pull_index_build": (ctypes.c_int, [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 9),
@@ -116,8 +119,8 @@ _SIGS = {
                                             ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int64] +
                              [ctypes.c_void_p] * 6 + [ctypes.c_size_t]),
     "fl_dense_max_backward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide)] +
-                              [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_int] +
-                              [ctypes.c_void_p] * 2),
+                              [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_int64] +
+                              [ctypes.c_void_p] * 3 + [ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t]),
     "fl_sparse_buckets": (ctypes.c_int64, [ctypes.c_int64]),
     "fl_sparse_plan_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int64]),
     "fl_sparse_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
@@ -158,6 +161,8 @@ _SIGS = {
                               [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "fl_sparse_normalize_forward": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3 +
                                     [ctypes.c_float] + [ctypes.c_void_p] * 4),
+    "fl_sparse_gather": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64] + [ctypes.c_void_p] * 3 +
+                         [ctypes.c_int64] * 3 + [ctypes.c_void_p]),
     "fl_sparse_normalize_backward": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_float,
                                                                             ctypes.c_void_p]),
     "fl_rule_accumulate": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_void_p] +
@@ -193,6 +198,11 @@ def exported_symbols():
     return sorted(_SIGS)
 
 
+# each argument struct and the entry point returning the library's sizeof
+STRUCT_SIZES = ((FlSide, "fl_side_bytes"), (FlSparseHop, "fl_sparse_hop_bytes"),
+                (FlGroundGraph, "fl_ground_graph_bytes"))
+
+
 def lib():
     """Load libflashlog_hip.so once; raise if it is missing or stale."""
     global _lib
@@ -208,6 +218,10 @@ def lib():
             fn.argtypes = args
         if handle.fl_abi_version() != ABI_VERSION:
             raise RuntimeError("libflashlog_hip.so ABI version mismatch; rebuild it")
+        for struct, size_fn in STRUCT_SIZES:
+            if ctypes.sizeof(struct) != getattr(handle, size_fn)():
+                raise RuntimeError("ctypes layout of %s differs from the library's (%d vs %d bytes)"
+                                   % (struct.__name__, ctypes.sizeof(struct), getattr(handle, size_fn)()))
         _lib = handle
     return _lib
 

@@ -18,20 +18,29 @@ HIP_FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-fPIC", "-ffp-contra
              "-Wno-unused-command-line-argument"]
 
 
-def build(verbose=False):
+def _compile(src, build_dir, verbose):
+    obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
+    if src.endswith(".cpp"):
+        cmd = ["hipcc", "-c", "-x", "c++", os.path.join(CSRC, src), "-o", obj, "-O3", "-std=c++17",
+               "-fPIC", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
+    else:
+        cmd = ["hipcc", "-c", os.path.join(CSRC, src), "-o", obj] + HIP_FLAGS
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.check_call(cmd)
+    return obj
+
+
+def build(verbose=False, jobs=None):
+    """Compiles every source (in parallel, one hipcc per file) and links the
+    library; returns its path."""
+    from concurrent.futures import ThreadPoolExecutor
     build_dir = os.path.join(HERE, "_build")
     os.makedirs(build_dir, exist_ok=True)
-    objs = []
-    for src in HIP_SOURCES + HOST_SOURCES:
-        obj = os.path.join(build_dir, os.path.splitext(src)[0] + ".o")
-        cmd = ["hipcc", "-c", os.path.join(CSRC, src), "-o", obj] + HIP_FLAGS
-        if src.endswith(".cpp"):
-            cmd = ["hipcc", "-c", "-x", "c++", os.path.join(CSRC, src), "-o", obj, "-O3", "-std=c++17",
-                   "-fPIC", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        subprocess.check_call(cmd)
-        objs.append(obj)
+    srcs = HIP_SOURCES + HOST_SOURCES
+    jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, build_dir, verbose), srcs))
     tmp = LIB + ".tmp"
     cmd = ["hipcc", "-shared", "--offload-arch=gfx950", "-o", tmp] + objs
     if verbose:

@@ -771,47 +771,6 @@ __global__ __launch_bounds__(PULL_NT) void k_heavy_max(fl_side ori, fl_side inv,
     max_unpack(best, dir ? &out_inv[at] : &out_ori[at], dir ? &arg_inv[at] : &arg_ori[at]);
 }
 
-// Backward: thread per (row, destination); each side's winning position p
-// sends (go*w)*m to gA[row, src(p)] and (go*a)*m to the row's relation
-// column, as the reference's winner-only backward (flashlog.cu:699-710).
-// Relation columns are first reduced in LDS, then added to gw with one
-// atomic per workgroup and column.  Atomic order makes the last bits of
-// gA/gw run-dependent, as in the reference.
-constexpr int MB_NT = 256;
-
-__global__ __launch_bounds__(MB_NT) void k_max_bwd(fl_side ori, fl_side inv, const float *__restrict__ A,
-                                                   const float *__restrict__ w, const float *__restrict__ g_ori,
-                                                   const float *__restrict__ g_inv,
-                                                   const int64_t *__restrict__ arg_ori,
-                                                   const int64_t *__restrict__ arg_inv, int64_t BL, int64_t E,
-                                                   int64_t n, int64_t r_size, float *__restrict__ gA,
-                                                   float *__restrict__ gw) {
-    extern __shared__ float gwl[];  // [2 * r_size]
-    const int64_t nrel = 2 * r_size;
-    for (int64_t r = threadIdx.x; r < nrel; r += MB_NT) gwl[r] = 0.0f;
-    __syncthreads();
-    const int64_t bl = blockIdx.y;
-    const int64_t dst = (int64_t)blockIdx.x * MB_NT + threadIdx.x;
-    if (dst < E) {
-#pragma unroll
-        for (int dir = 0; dir < 2; ++dir) {
-            const fl_side &s = dir ? inv : ori;
-            const int64_t p = (dir ? arg_inv : arg_ori)[bl * E + dst];
-            if (p < 0 || p >= s.edges) continue;
-            const float go = (dir ? g_inv : g_ori)[bl * E + dst];
-            if (go == 0.0f) continue;
-            const int64_t src = s.pos_src[p];
-            const int64_t col = (dir ? r_size : 0) + s.pos_rel[p];
-            const float m = s.mask[p];
-            atomicAdd(&gA[bl * E + src], fl_mul(fl_mul(go, w[bl * n + col]), m));
-            atomicAdd(&gwl[col], fl_mul(fl_mul(go, A[bl * E + src]), m));
-        }
-    }
-    __syncthreads();
-    for (int64_t r = threadIdx.x; r < nrel; r += MB_NT)
-        if (gwl[r] != 0.0f) atomicAdd(&gw[bl * n + r], gwl[r]);
-}
-
 // ---------------------------------------------------------------------------
 // Dense sum backward (flashlog.cpp:91-146,216-278)
 //
@@ -925,15 +884,23 @@ __global__ __launch_bounds__(RL_NT) void k_row_list(const uint32_t *__restrict__
     if (threadIdx.x == 0) rowcnt[bl] = run;
 }
 
+// One side's walk of the kept positions of (source, row), in CSR order:
+// returns acc + sum of (go*w)*m, and stores per relation group the partial
+// sum of (go*a)*m in pg.  MAX: only positions that won their destination
+// (arg[row, dst] == p) contribute, as in the winner-only backward
+// (flashlog.cu:699-710); a winning position is always a kept one.
+template <bool MAX>
 __device__ __forceinline__ float bwd_walk(const fl_side &s, int64_t src, int64_t bl, int64_t BL, int64_t E,
                                           int64_t n, int64_t off, int dir, float a, const float *__restrict__ w,
-                                          const float *__restrict__ grad, const float2 *__restrict__ PK,
-                                          const int32_t *__restrict__ CUT, float acc, float *__restrict__ pg) {
+                                          const float *__restrict__ grad, const int64_t *__restrict__ arg,
+                                          const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
+                                          float acc, float *__restrict__ pg) {
     const int64_t at = ((int64_t)dir * E + src) * BL + bl;
     const float th = PK[at].y;
     const int32_t cut = th > 0.0f ? CUT[at] : 0;
     const float *wr = w + bl * n + off;
     const float *gr = grad + bl * E;
+    const int64_t *ar = MAX ? arg + bl * E : nullptr;
     const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
     for (int64_t g = g0; g < g1; ++g) {
         const int rel = s.group_rel[g];
@@ -943,16 +910,20 @@ __device__ __forceinline__ float bwd_walk(const fl_side &s, int64_t src, int64_t
         float gs = 0.0f;
         for (int64_t b = start; b < start + take; b += 8) {
             float m[8], go[8];
+            bool win[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
+                win[u] = true;
                 if (b + u < start + take) {
                     m[u] = s.mask[b + u];
-                    go[u] = gr[s.col_ind[b + u]];
+                    const int32_t dst = s.col_ind[b + u];
+                    go[u] = gr[dst];
+                    if (MAX) win[u] = ar[dst] == b + u;
                 }
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                if (b + u >= start + take || m[u] == 0.0f || go[u] == 0.0f) continue;
+                if (b + u >= start + take || !win[u] || m[u] == 0.0f || go[u] == 0.0f) continue;
                 acc = fl_add(acc, fl_mul(fl_mul(go[u], wv), m[u]));
                 gs = fl_add(gs, fl_mul(fl_mul(go[u], a), m[u]));
             }
@@ -962,9 +933,11 @@ __device__ __forceinline__ float bwd_walk(const fl_side &s, int64_t src, int64_t
     return acc;
 }
 
+template <bool MAX>
 __global__ __launch_bounds__(BWD_NT) void k_bwd_rows(
     fl_side ori, fl_side inv, const float *__restrict__ A, const float *__restrict__ w,
-    const float *__restrict__ g_ori, const float *__restrict__ g_inv, int64_t BL, int64_t E, int64_t n,
+    const float *__restrict__ g_ori, const float *__restrict__ g_inv, const int64_t *__restrict__ arg_ori,
+    const int64_t *__restrict__ arg_inv, int64_t BL, int64_t E, int64_t n,
     int64_t r_size, const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
     const int32_t *__restrict__ rowlist, const int32_t *__restrict__ rowcnt, const int64_t *__restrict__ rowoff,
     int64_t pairs, float *__restrict__ gA, float *__restrict__ PG) {
@@ -977,8 +950,8 @@ __global__ __launch_bounds__(BWD_NT) void k_bwd_rows(
         float *pg = PG + (rowoff[bl] + k) * n;
         for (int64_t r = 0; r < n; ++r) pg[r] = 0.0f;
         float acc = gA[bl * E + src];  // identity term written by k_bwd_identity
-        acc = bwd_walk(ori, src, bl, BL, E, n, 0, 0, a, w, g_ori, PK, CUT, acc, pg);
-        acc = bwd_walk(inv, src, bl, BL, E, n, r_size, 1, a, w, g_inv, PK, CUT, acc, pg);
+        acc = bwd_walk<MAX>(ori, src, bl, BL, E, n, 0, 0, a, w, g_ori, arg_ori, PK, CUT, acc, pg);
+        acc = bwd_walk<MAX>(inv, src, bl, BL, E, n, r_size, 1, a, w, g_inv, arg_inv, PK, CUT, acc, pg);
         gA[bl * E + src] = acc;
     }
 }
@@ -1092,7 +1065,7 @@ int check_side(const fl_side *s, const char *name) {
 
 extern "C" {
 
-int fl_abi_version(void) { return 18; }
+int fl_abi_version(void) { return 19; }
 
 int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool, const int32_t *order,
                   const float *weight, float *out, int64_t nnz) {
@@ -1218,23 +1191,32 @@ size_t fl_dense_backward_workspace_bytes(const fl_side *ori, const fl_side *inv,
            align256(sizeof(int32_t) * (size_t)BL) + align256(sizeof(int64_t) * (size_t)(BL + 1));
 }
 
-int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv, const float *A, const float *w,
-                          const float *grad_ind, const float *grad_ori, const float *grad_inv, int64_t BL, int64_t E,
-                          int64_t n, int64_t r_size, int wot_i, int64_t topk_edges, float *grad_A, float *grad_w,
-                          float *pg, int64_t pg_pairs, void *workspace, size_t workspace_bytes) {
+}  // extern "C"
+
+namespace {
+
+// The dense backward of both aggregations (arg_ori/arg_inv null: sum; else
+// the winner-only max backward): identity term, the forward's frontier and
+// c2 records, per-row source lists, the per-(source, row) walks, then grad_w.
+int dense_backward_impl(const char *name, void *stream, const fl_side *ori, const fl_side *inv, const float *A,
+                        const float *w, const float *grad_ind, const float *grad_ori, const float *grad_inv,
+                        const int64_t *arg_ori, const int64_t *arg_inv, int64_t BL, int64_t E, int64_t n,
+                        int64_t r_size, int wot_i, int64_t topk_edges, float *grad_A, float *grad_w, float *pg,
+                        int64_t pg_pairs, void *workspace, size_t workspace_bytes) {
     int rc;
     if ((rc = check_side(ori, "ori")) != FL_OK) return rc;
     if ((rc = check_side(inv, "inv")) != FL_OK) return rc;
-    if (BL <= 0 || E <= 0 || n < 1) return fl_fail(FL_ERR_ARG, "dense_sum_backward: bad shape");
-    if (BL * E >= (int64_t)INT32_MAX) return fl_fail(FL_ERR_ARG, "dense_sum_backward: BL*E must be < 2^31");
+    if (BL <= 0 || E <= 0 || n < 1) return fl_fail(FL_ERR_ARG, "%s: bad shape", name);
+    if (BL * E >= (int64_t)INT32_MAX) return fl_fail(FL_ERR_ARG, "%s: BL*E must be < 2^31", name);
     if (r_size < 0 || 2 * r_size + 1 > n + (wot_i ? 1 : 0))
-        return fl_fail(FL_ERR_ARG, "dense_sum_backward: w width too small for r_size");
+        return fl_fail(FL_ERR_ARG, "%s: w width too small for r_size", name);
     const int64_t nrel = 2 * r_size;
-    if (nrel > 4 * BWD_NT) return fl_fail(FL_ERR_ARG, "dense_sum_backward: more than %d relation columns", 4 * BWD_NT);
-    if ((size_t)GW_C * n * sizeof(float) > 65536) return fl_fail(FL_ERR_ARG, "dense_sum_backward: w width too large");
-    if (pg_pairs < 0 || (pg_pairs > 0 && !pg)) return fl_fail(FL_ERR_ARG, "dense_sum_backward: bad partial buffer");
+    if (nrel > 4 * BWD_NT) return fl_fail(FL_ERR_ARG, "%s: more than %d relation columns", name, 4 * BWD_NT);
+    if ((size_t)GW_C * n * sizeof(float) > 65536) return fl_fail(FL_ERR_ARG, "%s: w width too large", name);
+    if (pg_pairs < 0 || (pg_pairs > 0 && !pg)) return fl_fail(FL_ERR_ARG, "%s: bad partial buffer", name);
     if (!workspace || workspace_bytes < fl_dense_backward_workspace_bytes(ori, inv, BL, E))
-        return fl_fail(FL_ERR_ARG, "dense_sum_backward: workspace too small");
+        return fl_fail(FL_ERR_ARG, "%s: workspace too small", name);
+    const bool is_max = arg_ori != nullptr;
     DenseWs ws = dense_ws_layout(BL, E, ori, inv, (char *)workspace);
     int32_t *rowlist = (int32_t *)((char *)workspace + ws.bytes);
     int32_t *rowcnt = (int32_t *)((char *)rowlist + align256(sizeof(int32_t) * (size_t)(BL * E)));
@@ -1243,7 +1225,9 @@ int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv, 
     const int64_t nw = (BL + 31) / 32;
     const int do_topk = (topk_edges > 0 && topk_edges < ((int64_t)1 << 60)) ? 1 : 0;
     const int64_t K = do_topk ? topk_edges : 0;
-    bwd_identity(st, grad_ind, A, w, BL, E, n, wot_i, 1, grad_A, grad_w);
+    // the sum's identity term is added to 0 first (flashlog.cpp:242); the
+    // max's is stored as is (flashlog.cu:173-207)
+    bwd_identity(st, grad_ind, A, w, BL, E, n, wot_i, is_max ? 0 : 1, grad_A, grad_w);
     // the forward's frontier (same A and w: same admitted edges); no identity output
     FL_LAUNCH("k_col_count", k_col_count, dim3((unsigned)((nw * E + COL_NT - 1) / COL_NT)), dim3(COL_NT), 0, st, A,
               w, BL, E, n, wot_i, (float *)nullptr, ws.bm, ws.hard_count);
@@ -1255,13 +1239,32 @@ int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv, 
     FL_LAUNCH("k_row_list", k_row_list, dim3((unsigned)BL), dim3(RL_NT), 0, st, ws.bm, E, rowlist, rowcnt);
     FL_LAUNCH("k_row_offsets", k_row_offsets, dim3(1), dim3(64), 0, st, rowcnt, BL, rowoff);
     if (pg_pairs > 0) {
-        FL_LAUNCH("k_bwd_rows", k_bwd_rows, dim3(16, (unsigned)BL), dim3(BWD_NT), 0, st, *ori, *inv, A, w, grad_ori,
-                  grad_inv, BL, E, n, r_size, ws.pk, ws.cut, rowlist, rowcnt, rowoff, pg_pairs, grad_A, pg);
+        if (is_max)
+            FL_LAUNCH("k_bwd_rows_max", k_bwd_rows<true>, dim3(16, (unsigned)BL), dim3(BWD_NT), 0, st, *ori, *inv,
+                      A, w, grad_ori, grad_inv, arg_ori, arg_inv, BL, E, n, r_size, ws.pk, ws.cut, rowlist, rowcnt,
+                      rowoff, pg_pairs, grad_A, pg);
+        else
+            FL_LAUNCH("k_bwd_rows", k_bwd_rows<false>, dim3(16, (unsigned)BL), dim3(BWD_NT), 0, st, *ori, *inv, A,
+                      w, grad_ori, grad_inv, (const int64_t *)nullptr, (const int64_t *)nullptr, BL, E, n, r_size,
+                      ws.pk, ws.cut, rowlist, rowcnt, rowoff, pg_pairs, grad_A, pg);
         const size_t lds = sizeof(float) * (size_t)(GW_C * n);
         FL_LAUNCH("k_bwd_gw", k_bwd_gw, dim3((unsigned)BL), dim3(BWD_NT), lds, st, pg, rowcnt, rowoff, pg_pairs, n,
                   nrel, grad_w);
     }
-    return fl_check_launch("dense_sum_backward");
+    return fl_check_launch(name);
+}
+
+}  // namespace
+
+extern "C" {
+
+int fl_dense_sum_backward(void *stream, const fl_side *ori, const fl_side *inv, const float *A, const float *w,
+                          const float *grad_ind, const float *grad_ori, const float *grad_inv, int64_t BL, int64_t E,
+                          int64_t n, int64_t r_size, int wot_i, int64_t topk_edges, float *grad_A, float *grad_w,
+                          float *pg, int64_t pg_pairs, void *workspace, size_t workspace_bytes) {
+    return dense_backward_impl("dense_sum_backward", stream, ori, inv, A, w, grad_ind, grad_ori, grad_inv, nullptr,
+                               nullptr, BL, E, n, r_size, wot_i, topk_edges, grad_A, grad_w, pg, pg_pairs, workspace,
+                               workspace_bytes);
 }
 
 int fl_dense_max_forward(void *stream, const fl_side *ori, const fl_side *inv, const float *A, const float *w,
@@ -1320,23 +1323,12 @@ int fl_dense_max_forward(void *stream, const fl_side *ori, const fl_side *inv, c
 int fl_dense_max_backward(void *stream, const fl_side *ori, const fl_side *inv, const float *A, const float *w,
                           const float *grad_ind, const float *grad_ori, const float *grad_inv,
                           const int64_t *arg_ori, const int64_t *arg_inv, int64_t BL, int64_t E, int64_t n,
-                          int64_t r_size, int wot_i, float *grad_A, float *grad_w) {
-    if (!ori || !inv) return fl_fail(FL_ERR_ARG, "dense_max_backward: null side");
-    if (BL < 0 || E < 0 || n < 1) return fl_fail(FL_ERR_ARG, "dense_max_backward: bad shape");
-    if (r_size < 0 || 2 * r_size + 1 > n + (wot_i ? 1 : 0))
-        return fl_fail(FL_ERR_ARG, "dense_max_backward: w width too small for r_size");
-    if ((size_t)(2 * r_size) * sizeof(float) > 65536)
-        return fl_fail(FL_ERR_ARG, "dense_max_backward: more than 16384 relation columns");
-    for (const fl_side *s : {ori, inv})
-        if (s->edges > 0 && (!s->pos_src || !s->pos_rel || !s->mask))
-            return fl_fail(FL_ERR_ARG, "dense_max_backward: side without position arrays");
-    if (BL == 0 || E == 0) return FL_OK;
-    hipStream_t st = (hipStream_t)stream;
-    bwd_identity(st, grad_ind, A, w, BL, E, n, wot_i, 0, grad_A, grad_w);
-    const size_t lds = sizeof(float) * (size_t)(2 * r_size > 0 ? 2 * r_size : 1);
-    FL_LAUNCH("k_max_bwd", k_max_bwd, dim3((unsigned)((E + MB_NT - 1) / MB_NT), (unsigned)BL), dim3(MB_NT), lds, st,
-              *ori, *inv, A, w, grad_ori, grad_inv, arg_ori, arg_inv, BL, E, n, r_size, grad_A, grad_w);
-    return fl_check_launch("dense_max_backward");
+                          int64_t r_size, int wot_i, int64_t topk_edges, float *grad_A, float *grad_w, float *pg,
+                          int64_t pg_pairs, void *workspace, size_t workspace_bytes) {
+    if (!arg_ori || !arg_inv) return fl_fail(FL_ERR_ARG, "dense_max_backward: null winner arrays");
+    return dense_backward_impl("dense_max_backward", stream, ori, inv, A, w, grad_ind, grad_ori, grad_inv, arg_ori,
+                               arg_inv, BL, E, n, r_size, wot_i, topk_edges, grad_A, grad_w, pg, pg_pairs,
+                               workspace, workspace_bytes);
 }
 
 }  // extern "C"

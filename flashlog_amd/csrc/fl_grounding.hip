@@ -1236,8 +1236,11 @@ int fl_ground_count(void *stream, const uint64_t *keys, const uint8_t *positive,
     if (!keys || !positive || !seg_task_off || !seg_head || !heads || !head_folds || !ws || !info)
         return fl_fail(FL_ERR_ARG, "ground_count: null argument");
     if (nsegments >= ((int64_t)1 << 30)) return fl_fail(FL_ERR_ARG, "ground_count: too many folds");
+    // the task count was written on the caller's stream: read it there
     int64_t ntasks = 0;
-    if (hipMemcpy(&ntasks, seg_task_off + nsegments, sizeof(int64_t), hipMemcpyDeviceToHost) != hipSuccess)
+    if (hipMemcpyAsync(&ntasks, seg_task_off + nsegments, sizeof(int64_t), hipMemcpyDeviceToHost,
+                       (hipStream_t)stream) != hipSuccess ||
+        hipStreamSynchronize((hipStream_t)stream) != hipSuccess)
         return fl_fail(FL_ERR_HIP, "ground_count: reading the task count");
     const int64_t n = ntasks * walks;
     if (n >= ((int64_t)1 << 32)) return fl_fail(FL_ERR_ARG, "ground_count: more than 2^32 walk records");

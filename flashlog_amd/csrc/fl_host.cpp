@@ -91,6 +91,10 @@ int fl_prof_read(const char *kernel, double *total_ms, int64_t *launches) {
 
 const char *fl_last_error(void) { return fl::g_last_error.c_str(); }
 
+size_t fl_side_bytes(void) { return sizeof(fl_side); }
+size_t fl_sparse_hop_bytes(void) { return sizeof(fl_sparse_hop); }
+size_t fl_ground_graph_bytes(void) { return sizeof(fl_ground_graph); }
+
 // csr.cpp:12-69: positions ordered by (source, relation, edge id) through a
 // stable bucket pass by relation followed by a stable bucket pass by source;
 // groups are the maximal runs of equal (source, relation).

@@ -2192,20 +2192,53 @@ __device__ __forceinline__ float block_tree_sum(float v, float *red) {
     return s;
 }
 
+// Per row (workgroup): the denominator is a left fold from 0 over the row's
+// values in entry (= output key) order, as the CPU path adds them
+// (flashlog.cpp:1561-1565); the workgroup stages chunks of the row in LDS
+// (double-buffered) while its first thread folds the previous chunk.  The
+// clamp is the GPU path's (flashlog.cu:2540): d >= eps ? d : eps, so a NaN
+// sum divides by eps.
+constexpr int NF_CHUNK = 2048;
+
 __global__ __launch_bounds__(NM_NT) void k_norm_fwd(const int64_t *__restrict__ row_ptr,
                                                    const float *__restrict__ v, float eps, float *__restrict__ out,
                                                    float *__restrict__ denom) {
-    __shared__ float red[NM_NT];
+    __shared__ float4 buf[2][NF_CHUNK / 4];
+    __shared__ float dsh;
     const int64_t r = blockIdx.x;
     const int64_t a = row_ptr[r], b = row_ptr[r + 1];
-    float s = 0.0f;
-    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) s = fl_add(s, v[k]);
-    const float d = block_tree_sum(s, red);
-    const float dc = d < eps ? eps : d;
-    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) out[k] = __fdiv_rn(v[k], dc);
-    if (threadIdx.x == 0) denom[r] = d;
+    const int t = threadIdx.x;
+    float acc = 0.0f;
+    int c = 0;
+    for (int64_t base = a; base < b; base += NF_CHUNK, ++c) {
+        const int len = (int)((b - base) < NF_CHUNK ? (b - base) : NF_CHUNK);
+        float *cb = (float *)buf[c & 1];
+        for (int i = t; i < len; i += NM_NT) cb[i] = v[base + i];
+        __syncthreads();
+        if (t == 0) {
+            const int l4 = len >> 2;
+            for (int i = 0; i < l4; ++i) {
+                const float4 q = buf[c & 1][i];
+                acc = fl_add(acc, q.x);
+                acc = fl_add(acc, q.y);
+                acc = fl_add(acc, q.z);
+                acc = fl_add(acc, q.w);
+            }
+            for (int i = l4 * 4; i < len; ++i) acc = fl_add(acc, cb[i]);
+        }
+    }
+    if (t == 0) {
+        dsh = acc;
+        denom[r] = acc;
+    }
+    __syncthreads();
+    const float d = dsh;
+    const float dc = d >= eps ? d : eps;
+    for (int64_t k = a + t; k < b; k += NM_NT) out[k] = __fdiv_rn(v[k], dc);
 }
 
+// Backward (flashlog.cu:2553-2591): g/d - sum(g*v)/d^2 where d >= eps, else
+// g/eps; sum(g*v) in a fixed tree order.
 __global__ __launch_bounds__(NM_NT) void k_norm_bwd(const int64_t *__restrict__ row_ptr,
                                                    const float *__restrict__ g, const float *__restrict__ v,
                                                    const float *__restrict__ denom, float eps,
@@ -2214,16 +2247,35 @@ __global__ __launch_bounds__(NM_NT) void k_norm_bwd(const int64_t *__restrict__ 
     const int64_t r = blockIdx.x;
     const int64_t a = row_ptr[r], b = row_ptr[r + 1];
     const float d = denom[r];
-    const float dc = d < eps ? eps : d;
+    const bool active = d >= eps;
+    const float dc = active ? d : eps;
     float s = 0.0f;
     for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) s = fl_add(s, fl_mul(g[k], v[k]));
     const float sgx = block_tree_sum(s, red);
-    const bool active = d >= eps;
-    const float corr = __fdiv_rn(sgx, fl_mul(dc, dc));
-    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) {
-        const float x = __fdiv_rn(g[k], dc);
-        gv[k] = active ? __fsub_rn(x, corr) : x;
+    const float corr = active ? __fdiv_rn(sgx, fl_mul(dc, dc)) : 0.0f;
+    for (int64_t k = a + threadIdx.x; k < b; k += NM_NT) gv[k] = __fsub_rn(__fdiv_rn(g[k], dc), corr);
+}
+
+// Thread per query coordinate: the value stored at the same (b, l, e) of a
+// coalesced COO tensor (keys (b*L + l)*E + e strictly increasing), found by
+// binary search, or 0 when the tensor has no entry there.
+__global__ void k_sp_gather(const int64_t *__restrict__ gb, const int64_t *__restrict__ gl,
+                            const int64_t *__restrict__ ge, const float *__restrict__ gv, int64_t ng,
+                            const int64_t *__restrict__ qb, const int64_t *__restrict__ ql,
+                            const int64_t *__restrict__ qe, int64_t nq, int64_t L, int64_t E,
+                            float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nq) return;
+    const int64_t key = (qb[i] * L + ql[i]) * E + qe[i];
+    int64_t lo = 0, hi = ng;
+    while (lo < hi) {
+        const int64_t mid = lo + ((hi - lo) >> 1);
+        const int64_t mk = (gb[mid] * L + gl[mid]) * E + ge[mid];
+        if (mk < key) lo = mid + 1; else hi = mid;
     }
+    float val = 0.0f;
+    if (lo < ng && (gb[lo] * L + gl[lo]) * E + ge[lo] == key) val = gv[lo];
+    out[i] = val;
 }
 
 }  // namespace fl
@@ -2807,6 +2859,18 @@ int fl_sparse_normalize_forward(void *stream, const int64_t *sp_b, const int64_t
     if (R > 0)
         FL_LAUNCH("k_norm_fwd", k_norm_fwd, dim3((unsigned)R), dim3(NM_NT), 0, st, row_ptr, v, eps, out, denom);
     return fl_check_launch("sparse_normalize");
+}
+
+int fl_sparse_gather(void *stream, const int64_t *gb, const int64_t *gl, const int64_t *ge, const float *gv,
+                     int64_t ng, const int64_t *qb, const int64_t *ql, const int64_t *qe, int64_t nq, int64_t L,
+                     int64_t E, float *out) {
+    if (ng < 0 || nq < 0 || L < 1 || E < 0) return fl_fail(FL_ERR_ARG, "sparse_gather: bad shape");
+    if (nq == 0) return FL_OK;
+    if ((ng > 0 && (!gb || !gl || !ge || !gv)) || !qb || !ql || !qe || !out)
+        return fl_fail(FL_ERR_ARG, "sparse_gather: null argument");
+    FL_LAUNCH("k_sp_gather", k_sp_gather, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, (hipStream_t)stream, gb,
+              gl, ge, gv, ng, qb, ql, qe, nq, L, E, out);
+    return fl_check_launch("sparse_gather");
 }
 
 int fl_sparse_normalize_backward(void *stream, const int64_t *row_ptr, const float *grad, const float *v,

@@ -27,81 +27,61 @@ _FLASHLOG_CPU_THREADS_CONFIGURED = False
 
 
 # ---------------------------------------------------------------------------
-# CPU thread configuration (flashlog_kernel.py:13-102).  Kept for callers of
-# the reference API; it only adjusts torch's intra-op thread count.
+# CPU thread configuration (flashlog_kernel.py:60-102: the FLASHLOG_CPU_THREADS
+# and FLASHLOG_CPU_INTEROP_THREADS switches).  This module computes nothing on
+# the CPU, so the setting only reaches torch's own CPU ops.  "auto" here means
+# one thread per physical core this process may run on, at most 32.
 
-def _flashlog_available_logical_cpus():
+def _cpu_topology():
+    """(logical CPUs this process may use, physical cores among them); the
+    core count comes from the kernel's sibling lists, or is None when they
+    cannot be read."""
     try:
-        return len(os.sched_getaffinity(0))
-    except Exception:
-        return os.cpu_count() or 1
+        allowed = sorted(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = list(range(os.cpu_count() or 1))
+    cores = set()
+    for cpu in allowed:
+        path = "/sys/devices/system/cpu/cpu%d/topology/thread_siblings_list" % cpu
+        try:
+            with open(path) as f:
+                cores.add(f.read().strip())
+        except OSError:
+            return len(allowed), None
+    return len(allowed), len(cores)
 
 
-def _flashlog_physical_cores():
-    try:
-        cores = set()
-        phys = core = None
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                line = line.strip()
-                if not line:
-                    if phys is not None and core is not None:
-                        cores.add((phys, core))
-                    phys = core = None
-                elif line.startswith("physical id"):
-                    phys = line.split(":", 1)[1].strip()
-                elif line.startswith("core id"):
-                    core = line.split(":", 1)[1].strip()
-        if phys is not None and core is not None:
-            cores.add((phys, core))
-        return len(cores) or None
-    except Exception:
-        return None
-
-
-def _choose_flashlog_cpu_threads():
-    logical = max(1, _flashlog_available_logical_cpus())
-    physical = _flashlog_physical_cores() or max(1, logical // 2 if logical >= 8 else logical)
-    usable = min(physical, logical)
-    if logical >= 96:
-        return min(32, max(16, usable // 2))
-    if logical >= 48:
-        return min(24, max(12, usable // 2))
-    if logical >= 24:
-        return min(16, max(8, usable))
-    return max(1, logical)
+def _auto_cpu_threads():
+    logical, physical = _cpu_topology()
+    return max(1, min(32, physical or logical))
 
 
 def configure_flashlog_cpu_threads(force=False):
-    """FLASHLOG_CPU_THREADS: unset/off/0/false leaves torch alone, ``auto``
-    picks a bandwidth-friendly count, an integer forces it
-    (flashlog_kernel.py:60-102)."""
+    """Apply FLASHLOG_CPU_THREADS once (again with force=True): unset, "off",
+    "none", "false" or "0" leave torch's intra-op thread count alone; "auto"
+    (or empty) picks _auto_cpu_threads(); an integer is used as given (an
+    unparsable value counts as "auto"); the count is kept within the CPUs
+    this process may use.  FLASHLOG_CPU_INTEROP_THREADS, when set, is tried
+    for the inter-op pool (torch refuses it once that pool has started;
+    then it is left as is).  Returns torch's intra-op thread count."""
     global _FLASHLOG_CPU_THREADS_CONFIGURED
     if _FLASHLOG_CPU_THREADS_CONFIGURED and not force:
         return torch.get_num_threads()
-    setting = os.environ.get("FLASHLOG_CPU_THREADS", "off").strip().lower()
-    if setting in ("", "auto"):
-        target = _choose_flashlog_cpu_threads()
-    elif setting in ("off", "none", "false", "0"):
-        _FLASHLOG_CPU_THREADS_CONFIGURED = True
-        return torch.get_num_threads()
-    else:
-        try:
-            target = int(setting)
-        except ValueError:
-            target = _choose_flashlog_cpu_threads()
-    target = max(1, min(target, _flashlog_available_logical_cpus()))
-    if torch.get_num_threads() != target:
-        torch.set_num_threads(target)
-    interop = os.environ.get("FLASHLOG_CPU_INTEROP_THREADS")
-    if interop is not None:
-        try:
-            n = max(1, int(interop))
-            if torch.get_num_interop_threads() != n:
-                torch.set_num_interop_threads(n)
-        except (ValueError, RuntimeError):
-            pass
     _FLASHLOG_CPU_THREADS_CONFIGURED = True
+    raw = os.environ.get("FLASHLOG_CPU_THREADS", "off").strip().lower()
+    if raw in ("off", "none", "false", "0"):
+        return torch.get_num_threads()
+    wanted = int(raw) if raw.lstrip("-").isdigit() else _auto_cpu_threads()
+    logical, _ = _cpu_topology()
+    wanted = min(max(wanted, 1), logical)
+    if wanted != torch.get_num_threads():
+        torch.set_num_threads(wanted)
+    interop = os.environ.get("FLASHLOG_CPU_INTEROP_THREADS", "").strip()
+    if interop.isdigit() and int(interop) > 0 and int(interop) != torch.get_num_interop_threads():
+        try:
+            torch.set_num_interop_threads(int(interop))
+        except RuntimeError:
+            pass  # the inter-op pool is already running
     return torch.get_num_threads()
 
 
@@ -117,16 +97,6 @@ def _stream(t):
 
 # ---------------------------------------------------------------------------
 # Graph preparation
-
-def _ind2ptr_cpu(index, size):
-    """int32 CSR offsets of a sorted index (flashlog_kernel.py:626-634)."""
-    counts = torch.bincount(index, minlength=size)
-    np.cumsum(counts.numpy(), out=counts.numpy())
-    out = torch.empty(size + 1, dtype=torch.int32)
-    out[0] = 0
-    out[1:].copy_(counts)
-    return out
-
 
 def _group_starts_and_counts(sorted_values, sorted_relations=None):
     """Starts and lengths of runs of equal (value[, relation])
@@ -155,7 +125,9 @@ def _build_group_metadata(sorted_rows, sorted_rels, num_nodes, row_ptr=None):
     relations = sorted_rels[starts.long()].to(torch.int16) if starts.numel() else \
         torch.empty(0, dtype=torch.int16)
     if row_ptr is None:
-        row_ptr = _ind2ptr_cpu(sorted_rows, num_nodes)
+        # first position of every row (and the end), by binary search in the sorted rows
+        row_ptr = torch.searchsorted(sorted_rows.to("cpu", torch.int64),
+                                     torch.arange(num_nodes + 1, dtype=torch.int64), out_int32=True)
     group_ptr = torch.searchsorted(starts, row_ptr, out_int32=True)
     return group_ptr, relations, starts, counts
 
@@ -485,8 +457,18 @@ def _dense_max_forward(A_flat, w_flat, graph, ori_mask, inv_mask, r_size, wot_i,
     return out_ind, out_ori, out_inv, arg_ori, arg_inv
 
 
-def _dense_max_backward(grad_ind, grad_ori, grad_inv, arg_ori, arg_inv, A_f, w_f, graph, om, im, r_size, wot_i):
-    """flashlog_backward_max_cuda (flashlog.cu:1187-1255)."""
+def _dense_max_backward(grad_ind, grad_ori, grad_inv, arg_ori, arg_inv, A_f, w_f, graph, om, im, r_size, wot_i,
+                        K):
+    """flashlog_backward_max_cuda (flashlog.cu:1187-1255) as fixed-order
+    walks of the kept positions of every (source, row): only the winning
+    position of a destination passes its gradient on."""
+    return _dense_backward(grad_ind, grad_ori, grad_inv, A_f, w_f, graph, om, im, r_size, wot_i, K,
+                           arg_ori, arg_inv)
+
+
+def _dense_backward(grad_ind, grad_ori, grad_inv, A_f, w_f, graph, om, im, r_size, wot_i, K,
+                    arg_ori=None, arg_inv=None):
+    """Both dense backwards: the sum's (arg_ori None) and the max's."""
     BL, E = A_f.shape
     n = w_f.shape[1]
 
@@ -498,12 +480,19 @@ def _dense_max_backward(grad_ind, grad_ori, grad_inv, arg_ori, arg_inv, A_f, w_f
     gi, go, gv = g(grad_ind), g(grad_ori), g(grad_inv)
     so = graph.ori.struct(om)
     si = graph.inv.struct(im)
+    ws_bytes = _lib.lib().fl_dense_backward_workspace_bytes(ctypes.byref(so), ctypes.byref(si), BL, E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A_f.device)
     gA = torch.empty_like(A_f)
     gw = torch.empty_like(w_f)
-    check(_lib.lib().fl_dense_max_backward(_stream(A_f), ctypes.byref(so), ctypes.byref(si), ptr(A_f), ptr(w_f),
-                                           ptr(gi), ptr(go), ptr(gv), ptr(arg_ori), ptr(arg_inv), BL, E, n,
-                                           r_size, 1 if wot_i else 0, ptr(gA), ptr(gw)),
-          "dense_max_backward")
+    pairs = int(torch.count_nonzero(A_f))  # nonzero (row, source) pairs: rows of the partial buffer
+    pg = torch.empty(max(pairs, 1) * n, dtype=torch.float32, device=A_f.device)
+    common = (ctypes.byref(so), ctypes.byref(si), ptr(A_f), ptr(w_f), ptr(gi), ptr(go), ptr(gv))
+    tail = (BL, E, n, r_size, 1 if wot_i else 0, int(K), ptr(gA), ptr(gw), ptr(pg), pairs, ptr(ws), ws_bytes)
+    if arg_ori is None:
+        check(_lib.lib().fl_dense_sum_backward(_stream(A_f), *common, *tail), "dense_sum_backward")
+    else:
+        check(_lib.lib().fl_dense_max_backward(_stream(A_f), *common, ptr(arg_ori), ptr(arg_inv), *tail),
+              "dense_max_backward")
     return gA, gw
 
 
@@ -544,43 +533,12 @@ class FlashLogFunction(autograd.Function):
         return (gA.view(B, L, E), gw.view(B, L, -1)) + (None,) * 16
 
 
-_DENSE_BACKWARD_ENABLED = False
-
-
 def _dense_sum_backward(grad_ind, grad_ori, grad_inv, A_f, w_f, graph, om, im, r_size, wot_i, K):
     """flashlog_backward_cuda (flashlog.cu:1077-1185) with the CPU path's
-    order (flashlog.cpp:216-278): grad_A bit-identical, grad_w in a fixed
-    order (within float rounding of the CPU sum).
-
-    Disabled: an earlier build of this path faulted the GPU (k_col_count
-    wrote the identity output through the null pointer the backward passes);
-    the store is now guarded, and the path stays off until a GPU run has
-    verified it."""
-    if not _DENSE_BACKWARD_ENABLED:
-        raise RuntimeError("dense sum backward is disabled: its GPU kernels are awaiting verification "
-                           "after a memory fault (null identity-output store, now fixed)")
-    BL, E = A_f.shape
-    n = w_f.shape[1]
-
-    def g(x):
-        if x is None:
-            return torch.zeros_like(A_f)
-        return x.reshape(BL, E).contiguous().float()
-
-    gi, go, gv = g(grad_ind), g(grad_ori), g(grad_inv)
-    so = graph.ori.struct(om)
-    si = graph.inv.struct(im)
-    ws_bytes = _lib.lib().fl_dense_backward_workspace_bytes(ctypes.byref(so), ctypes.byref(si), BL, E)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=A_f.device)
-    gA = torch.empty_like(A_f)
-    gw = torch.empty_like(w_f)
-    pairs = int(torch.count_nonzero(A_f))  # nonzero (row, source) pairs: rows of the partial buffer
-    pg = torch.empty(max(pairs, 1) * n, dtype=torch.float32, device=A_f.device)
-    check(_lib.lib().fl_dense_sum_backward(_stream(A_f), ctypes.byref(so), ctypes.byref(si), ptr(A_f), ptr(w_f),
-                                           ptr(gi), ptr(go), ptr(gv), BL, E, n, r_size, 1 if wot_i else 0, int(K),
-                                           ptr(gA), ptr(gw), ptr(pg), pairs, ptr(ws), ws_bytes),
-          "dense_sum_backward")
-    return gA, gw
+    order (flashlog.cpp:216-278): grad_A bit-identical, grad_w from
+    per-(source, row) partials added in ascending source order (within
+    float rounding of the CPU's single sequential sum)."""
+    return _dense_backward(grad_ind, grad_ori, grad_inv, A_f, w_f, graph, om, im, r_size, wot_i, K)
 
 
 def vectorized_operation_csr(A, w, csr_struct, mask_values, r_size,
@@ -589,24 +547,14 @@ def vectorized_operation_csr(A, w, csr_struct, mask_values, r_size,
                              prepared_masks=None):
     """Dense entry point of the reference's CPU path (flashlog_kernel.py:845-882);
     here it runs the same arithmetic on the GPU."""
-    (ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
-     inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
-     ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-     inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count) = csr_struct
-    prepared = _prepared_mask_pair(prepared_masks) if prepared_masks is not None else _prepared_mask_pair(mask_values)
-    if prepared is not None:
-        ori_mask, inv_mask = prepared
-    else:
-        ori_mask, inv_mask = prepare_csr_masks(csr_struct, mask_values, weight)
-    A = _dense_topc_state(A, topk_nodes if use_topk else None)
-    effective_topk = topk_edges if (use_topk and topk_edges > 0) else (1 << 60)
-    return FlashLogFunction.apply(
-        A, w, None,
-        ori_col_ind, ori_mask,
-        ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-        inv_col_ind, inv_mask,
-        inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
-        r_size, wot_i, effective_topk)
+    masks = _prepared_mask_pair(mask_values if prepared_masks is None else prepared_masks)
+    if masks is None:
+        masks = prepare_csr_masks(csr_struct, mask_values, weight)
+    # FlashLogFunction takes per side: columns, mask, then the 4 group arrays
+    sides = [(csr_struct[col], m, *csr_struct[g0:g0 + 4]) for col, m, g0 in ((1, masks[0], 8), (5, masks[1], 12))]
+    budget = topk_edges if use_topk and topk_edges > 0 else 1 << 60
+    return FlashLogFunction.apply(_dense_topc_state(A, topk_nodes if use_topk else None), w, None,
+                                  *sides[0], *sides[1], r_size, wot_i, budget)
 
 
 class FlashLogDenseSumFunction(autograd.Function):
@@ -654,29 +602,26 @@ class FlashLogDenseSumFunction(autograd.Function):
         return (gA.view(B, L, E), gw.view(B, L, -1)) + (None,) * 24
 
 
+def _dense_gpu_args(A, w, csr_struct, mask_values, weight, use_topk, topk_nodes, prepared_masks):
+    """Leading positional arguments of the dense GPU autograd functions: the
+    c1-pruned state, w, the 16 CSR arrays in tuple order (the order of their
+    parameters), then the masks and edge weights (prepared masks, when
+    given, replace both)."""
+    pruned = _dense_topc_state(A, topk_nodes if use_topk else None)
+    if prepared_masks is not None:
+        mask_values, weight = prepared_masks, None
+    return (pruned, w, *csr_struct, mask_values, weight)
+
+
 def dense_csr_sum_cuda(A, w, csr_struct, mask_values, r_size,
                        weight=None, wot_i=False,
                        use_topk=False, topk_nodes=100000, topk_edges=0,
                        agg_mode="sum", prepared_masks=None):
     """GPU dense sum entry point (flashlog_kernel.py:1629-1663): c1 pruning,
     then the sum hop with c2 = topk_edges when use_topk."""
-    (ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
-     inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
-     ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-     inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count) = csr_struct
-    agg_id = 1 if agg_mode == "max" else 0
-    A = _dense_topc_state(A, topk_nodes if use_topk else None)
-    mask_input = prepared_masks if prepared_masks is not None else mask_values
-    weight_input = None if prepared_masks is not None else weight
-    return FlashLogDenseSumFunction.apply(
-        A, w,
-        ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
-        inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
-        ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-        inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
-        mask_input, weight_input,
-        r_size, wot_i,
-        use_topk, topk_nodes, topk_edges, agg_id)
+    lead = _dense_gpu_args(A, w, csr_struct, mask_values, weight, use_topk, topk_nodes, prepared_masks)
+    return FlashLogDenseSumFunction.apply(*lead, r_size, wot_i, use_topk, topk_nodes, topk_edges,
+                                          int(agg_mode == "max"))
 
 
 # ---------------------------------------------------------------------------
@@ -798,14 +743,14 @@ class FlashLogDenseMaxFunction(autograd.Function):
         out_ind, out_ori, out_inv, arg_ori, arg_inv = _dense_max_forward(
             A_flat, w_flat, graph, ori_mask, inv_mask, int(r_size), bool(wot_i), K)
         ctx.save_for_backward(A_flat, w_flat, ori_mask, inv_mask, arg_ori, arg_inv)
-        ctx.graph, ctx.r_size, ctx.wot_i, ctx.shape = graph, int(r_size), bool(wot_i), (B, L, E)
+        ctx.graph, ctx.r_size, ctx.wot_i, ctx.K, ctx.shape = graph, int(r_size), bool(wot_i), K, (B, L, E)
         return out_ind.view(B, L, E), out_ori.view(B, L, E), out_inv.view(B, L, E)
 
     @staticmethod
     def backward(ctx, grad_ind, grad_ori, grad_inv):
         A_f, w_f, om, im, arg_ori, arg_inv = ctx.saved_tensors
         gA, gw = _dense_max_backward(grad_ind, grad_ori, grad_inv, arg_ori, arg_inv, A_f, w_f, ctx.graph, om, im,
-                                     ctx.r_size, ctx.wot_i)
+                                     ctx.r_size, ctx.wot_i, ctx.K)
         B, L, E = ctx.shape
         return (gA.view(B, L, E), gw.view(B, L, -1)) + (None,) * 23
 
@@ -814,22 +759,8 @@ def dense_csr_max(A, w, csr_struct, mask_values, r_size, weight=None, wot_i=Fals
                   use_topk=False, topk_nodes=100000, topk_edges=0, prepared_masks=None):
     """GPU dense max entry point (flashlog_kernel.py:1666-1688): c1 pruning,
     then the max hop with c2 = topk_edges when use_topk."""
-    (ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
-     inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
-     ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-     inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count) = csr_struct
-    A = _dense_topc_state(A, topk_nodes if use_topk else None)
-    mask_input = prepared_masks if prepared_masks is not None else mask_values
-    weight_input = None if prepared_masks is not None else weight
-    return FlashLogDenseMaxFunction.apply(
-        A, w,
-        ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
-        inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
-        ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-        inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
-        mask_input, weight_input,
-        r_size, wot_i,
-        use_topk, topk_nodes, topk_edges)
+    lead = _dense_gpu_args(A, w, csr_struct, mask_values, weight, use_topk, topk_nodes, prepared_masks)
+    return FlashLogDenseMaxFunction.apply(*lead, r_size, wot_i, use_topk, topk_nodes, topk_edges)
 
 
 def sampled_sparse_propagation(state, w, csr_struct, mask_values, r_size, weight=None, wot_i=False,
@@ -1080,25 +1011,27 @@ def _same_index_rows(gi, rows):
                for k, r in enumerate(rows))
 
 
-def _align_sparse_grad_to_output(grad, out_indices, L, E):
-    """Gradient values at the output coordinates (flashlog_kernel.py:360-376)."""
+def _grad_at_outputs(grad, out_indices, L, E):
+    """The upstream gradient's values at the hop's output coordinates
+    [3, n] (the role of flashlog_kernel.py:360-376): a dense gradient is
+    indexed; a sparse one with the very index rows of the output is taken
+    as is; any other sparse one is coalesced and looked up by fl_sparse_gather
+    (0 where it holds no entry)."""
     if not grad.is_sparse:
         return grad[tuple(out_indices)].contiguous()
-    if _same_index_rows(grad._indices(), [out_indices[k] for k in range(out_indices.shape[0])]):
+    rows = [out_indices[k] for k in range(out_indices.shape[0])]
+    if _same_index_rows(grad._indices(), rows):
         return grad._values().contiguous()
-    grad = grad.coalesce()
-    if torch.equal(grad.indices(), out_indices):
-        return grad.values().contiguous()
-    keys = out_indices[0] * (L * E) + out_indices[1] * E + out_indices[2]
-    gidx = grad.indices()
-    gkeys = gidx[0] * (L * E) + gidx[1] * E + gidx[2]
-    values = torch.zeros(keys.numel(), device=grad.device, dtype=grad.dtype)
-    if gkeys.numel() and keys.numel():
-        pos = torch.searchsorted(gkeys, keys)
-        safe = pos.clamp(max=gkeys.numel() - 1)
-        valid = (pos < gkeys.numel()) & (gkeys[safe] == keys)
-        values[valid] = grad.values()[safe[valid]]
-    return values
+    g = grad.coalesce()
+    gi = g.indices()
+    gv = g.values().float().contiguous()
+    q = out_indices.long()
+    out = torch.empty(q.shape[1], dtype=torch.float32, device=q.device)
+    check(_lib.lib().fl_sparse_gather(_stream(q), ptr(gi[0].contiguous()), ptr(gi[1].contiguous()),
+                                      ptr(gi[2].contiguous()), ptr(gv), gv.numel(), ptr(q[0].contiguous()),
+                                      ptr(q[1].contiguous()), ptr(q[2].contiguous()), q.shape[1], int(L), int(E),
+                                      ptr(out)), "sparse_gather")
+    return out.to(grad.dtype)
 
 
 def _sparse_rows_scratch(R, device):
@@ -1164,22 +1097,30 @@ def _sparse_race_entries(sp_batch, sp_level, sp_value, B, L, c, keep):
     return torch.nonzero(keep, as_tuple=True)[0]
 
 
-def _prune_sparse_sources(ctx, batch, level, entity, value, topk_nodes, num_rules, sampling=False, B=None):
-    """Select one common input for fact and identity propagation."""
-    entries = _sparse_topc_entries(batch, level, entity, value, topk_nodes, num_rules, sampling, B)
-    ctx.pruned_entries = entries
-    ctx.original_input_size = value.numel()
-    if entries is None:
-        return batch, level, entity, value
-    return batch[entries], level[entries], entity[entries], value[entries]
+class _C1Pick:
+    """The entries a hop keeps under the c1 budget (all when `entries` is
+    None), applied to the state's arrays and undone on the gradient (the
+    role of flashlog_kernel.py:1140-1155)."""
+
+    def __init__(self, entries, size):
+        self.entries, self.size = entries, size
+
+    def take(self, *arrays):
+        if self.entries is None:
+            return arrays
+        return tuple(x.index_select(0, self.entries) for x in arrays)
+
+    def untake(self, grad):
+        if self.entries is None:
+            return grad
+        return grad.new_zeros(self.size).index_copy_(0, self.entries, grad)
 
 
-def _restore_pruned_gradient(ctx, gradient):
-    if ctx.pruned_entries is None:
-        return gradient
-    restored = gradient.new_zeros(ctx.original_input_size)
-    restored[ctx.pruned_entries] = gradient
-    return restored
+def _c1_pick(ctx, batch, level, entity, value, topk_nodes, num_rules, sampling=False, B=None):
+    pick = _C1Pick(_sparse_topc_entries(batch, level, entity, value, topk_nodes, num_rules, sampling, B),
+                   value.numel())
+    ctx.c1_pick = pick
+    return pick.take(batch, level, entity, value)
 
 
 def _coo(idx, vals, B, L, E):
@@ -1239,7 +1180,7 @@ class FlashLogFunctionSparse3DAllEdgesSum(autograd.Function):
     @staticmethod
     def backward(ctx, grad_out):
         B, L, E, wshape = ctx.dims
-        aligned = _align_sparse_grad_to_output(grad_out, ctx.out_indices, L, E)
+        aligned = _grad_at_outputs(grad_out, ctx.out_indices, L, E)
         gv, gw = _sparse_backward(ctx.state, aligned)
         grads = (None, None, None, gv, gw.view(wshape)) + (None,) * 17
         return (grads + (None,))[:len(ctx.needs_input_grad)]
@@ -1256,7 +1197,7 @@ def _topk_hop_forward(ctx, aggregate, sp_batch, sp_level, sp_entity, sp_value, w
     seeded by one draw of torch's CPU generator, as the reference draws it."""
     trainable = weight is not None and bool(getattr(weight, "requires_grad", False))
     _require_cuda(sp_value, w)
-    sp_batch, sp_level, sp_entity, sp_value = _prune_sparse_sources(
+    sp_batch, sp_level, sp_entity, sp_value = _c1_pick(
         ctx, sp_batch, sp_level, sp_entity, sp_value, topk_nodes, w.size(1), sampling, B=int(B))
     mask_f = mask_values.contiguous().view(-1)
     ori_bits = inv_bits = None
@@ -1300,13 +1241,13 @@ def _edge_dscore(ew, order):
 
 def _topk_hop_backward(ctx, grad_out):
     B, L, E, wshape = ctx.dims
-    aligned = _align_sparse_grad_to_output(grad_out, ctx.out_indices, L, E)
+    aligned = _grad_at_outputs(grad_out, ctx.out_indices, L, E)
     grad_edge = None
     if ctx.edge_weight is not None:
         shape, dtype, device = ctx.edge_weight
         grad_edge = torch.zeros(int(np.prod(shape)), dtype=torch.float32, device=aligned.device)
     gv, gw = _sparse_backward(ctx.state, aligned, grad_edge)
-    gv = _restore_pruned_gradient(ctx, gv)
+    gv = ctx.c1_pick.untake(gv)
     ge = grad_edge.view(shape).to(device=device, dtype=dtype) if grad_edge is not None else None
     grads = (None, None, None, gv, gw.view(wshape)) + (None,) * 17 + (ge,) + (None,) * 10
     return grads[:len(ctx.needs_input_grad)]
@@ -1406,7 +1347,7 @@ class FlashLogFunctionSparse3DCPUSum(autograd.Function):
     def backward(ctx, grad_out):
         B, L, E, wshape = ctx.dims
         dev = ctx.out_indices.device
-        aligned = _align_sparse_grad_to_output(grad_out.to(dev), ctx.out_indices, L, E)
+        aligned = _grad_at_outputs(grad_out.to(dev), ctx.out_indices, L, E)
         gv, gw = _sparse_backward(ctx.state, aligned)
         return (None, None, None, gv.to(ctx.home), gw.view(wshape).to(ctx.home)) + (None,) * 18
 
@@ -1437,7 +1378,7 @@ class FlashLogFunctionSparse3DCPUSumNorm(autograd.Function):
         B, L, E, wshape = ctx.dims
         dev = ctx.out_indices.device
         vals, denom, row_ptr, eps = ctx.norm
-        aligned = _align_sparse_grad_to_output(grad_out.to(dev), ctx.out_indices, L, E)
+        aligned = _grad_at_outputs(grad_out.to(dev), ctx.out_indices, L, E)
         g_sum = _normalize_backward(row_ptr, aligned, vals, denom, eps)
         gv, gw = _sparse_backward(ctx.state, g_sum)
         return (None, None, None, gv.to(ctx.home), gw.view(wshape).to(ctx.home)) + (None,) * 19
@@ -1490,7 +1431,7 @@ class Sparse3DNormalizeFunction(autograd.Function):
             if _same_index_rows(grad_out._indices(), [sp_batch, sp_level, sp_entity]):
                 g = grad_out._values().contiguous()
             else:
-                g = _align_sparse_grad_to_output(grad_out, torch.stack([sp_batch, sp_level, sp_entity]), ctx.L,
+                g = _grad_at_outputs(grad_out, torch.stack([sp_batch, sp_level, sp_entity]), ctx.L,
                                                  ctx.E)
         else:
             g = grad_out[sp_batch, sp_level, sp_entity]
@@ -1499,10 +1440,11 @@ class Sparse3DNormalizeFunction(autograd.Function):
 
 
 def normalize_sparse3d(s, eps=1e-7):
-    s = s if s.is_coalesced() else s.coalesce()
-    idx = s.indices()
-    B, L, E = s.shape
-    return Sparse3DNormalizeFunction.apply(idx[0], idx[1], idx[2], s.values(), B, L, E, eps)
+    """Per-(b, l) normalization of a [B, L, E] COO state
+    (flashlog_kernel.py:610-614), through Sparse3DNormalizeFunction."""
+    c = s.coalesce()  # returns s itself when it is already coalesced
+    b, l, e = c.indices()
+    return Sparse3DNormalizeFunction.apply(b, l, e, c.values(), *c.shape, eps)
 
 
 def _channel_reduce(sp_batch, sp_level, sp_entity, sp_value, B, L, E, op):

@@ -86,6 +86,12 @@ typedef struct fl_side {
 
 const char *fl_last_error(void);
 int fl_abi_version(void);
+/* sizeof of the argument structs, so that a binding can check its own
+ * layout against the library's (no counterpart in the reference: its
+ * pybind11 bindings take tensors, not structs). */
+size_t fl_side_bytes(void);
+size_t fl_sparse_hop_bytes(void);
+size_t fl_ground_graph_bytes(void);
 
 /* ---- host-side graph preparation ------------------------------------- */
 
@@ -216,19 +222,24 @@ int fl_dense_max_forward(void *stream, const fl_side *ori, const fl_side *inv,
                          void *workspace, size_t workspace_bytes);
 
 /* Replaces flashlog_backward_max_cuda (flashlog.cu:1187-1255; kernel
- * :639-726): grad_A = g_ind * w[n-1] (0 if wot_i) plus, for every winning
- * position p of (bl, d) with grad != 0, (grad*w[rel(p)])*mask[p] at
- * src(p); grad_w[bl, n-1] = sum_e g_ind*A (fixed tree order) and
- * grad_w[bl, off + rel(p)] += (grad*A[bl, src(p)])*mask[p].  The winner
- * terms are added with atomics (run-dependent last bits, as the
- * reference).  Needs the sides' pos_src / pos_rel arrays; no workspace. */
+ * :639-726) without its atomics: grad_A[bl, src] = g_ind*w[n-1] (0 if
+ * wot_i) plus, over the kept ORI then INV positions p of src in CSR order
+ * that won their destination d (arg[bl, d] == p) with mask and grad
+ * nonzero, (grad*w[rel(p)])*mask[p] -- a fixed order, so every run gives
+ * the same bits; grad_w[bl, n-1] = sum_e g_ind*A (fixed tree order) and the
+ * relation columns add per-(source, row) partials of (grad*A)*mask in
+ * ascending source order.  topk_edges must be the forward's (the kept
+ * positions are rebuilt from A and w as in fl_dense_sum_backward); pg,
+ * pg_pairs and the workspace (fl_dense_backward_workspace_bytes) as there. */
 int fl_dense_max_backward(void *stream, const fl_side *ori, const fl_side *inv,
                           const float *A, const float *w,
                           const float *grad_ind, const float *grad_ori,
                           const float *grad_inv, const int64_t *arg_ori,
                           const int64_t *arg_inv, int64_t BL, int64_t E,
-                          int64_t n, int64_t r_size, int wot_i, float *grad_A,
-                          float *grad_w);
+                          int64_t n, int64_t r_size, int wot_i,
+                          int64_t topk_edges, float *grad_A, float *grad_w,
+                          float *pg, int64_t pg_pairs, void *workspace,
+                          size_t workspace_bytes);
 
 /* ---- sparse (COO) hop ------------------------------------------------- */
 
@@ -391,19 +402,32 @@ int fl_sparse_race_select(void *stream, const float *v, int64_t nnz,
 size_t fl_sparse_rowptr_bytes(int64_t R);
 
 /* Replaces sparse3d_normalize_forward_cuda (flashlog.cu:2480-2640):
- * per row r = b*L + l, denom[r] = sum of its values (fixed tree order) and
- * out = v / max(denom, eps).  Entries sorted by row; row_ptr [R+1] and
- * err [1] are caller scratch (err != 0 after the call: unsorted or out of
- * range input). */
+ * per row r = b*L + l, denom[r] = the left fold from 0 of its values in
+ * entry order (the CPU path's order, flashlog.cpp:1561-1565, so the bits
+ * equal the CPU path's) and out = v / dc with dc = denom >= eps ? denom :
+ * eps (the GPU path's clamp, flashlog.cu:2540: a NaN sum divides by eps),
+ * IEEE division.  Entries sorted by row; row_ptr [R+1] and err [1] are
+ * caller scratch (err != 0 after the call: unsorted or out of range
+ * input). */
 int fl_sparse_normalize_forward(void *stream, const int64_t *sp_b,
                                 const int64_t *sp_l, const float *v,
                                 int64_t nnz, int64_t B, int64_t L, float eps,
                                 float *out, float *denom, int64_t *row_ptr,
                                 int64_t *err);
 
+/* Replaces _align_sparse_grad_to_output (flashlog_kernel.py:360-376):
+ * out[i] = the value of the coalesced COO tensor (gb, gl, ge, gv; ng
+ * entries, keys (b*L + l)*E + e strictly increasing) at query coordinate
+ * (qb[i], ql[i], qe[i]), or 0 where it has no entry. */
+int fl_sparse_gather(void *stream, const int64_t *gb, const int64_t *gl,
+                     const int64_t *ge, const float *gv, int64_t ng,
+                     const int64_t *qb, const int64_t *ql, const int64_t *qe,
+                     int64_t nq, int64_t L, int64_t E, float *out);
+
 /* Replaces sparse3d_normalize_backward_cuda (flashlog.cu:2642-2691):
- * grad_v = g/dc - sum_row(g*v)/dc^2 where denom >= eps (dc = max(denom,
- * eps)), else g/dc. */
+ * grad_v = g/dc - sum_row(g*v)/dc^2 where denom >= eps (dc = denom), else
+ * g/eps (dc = eps, NaN denominators included); sum_row in a fixed tree
+ * order. */
 int fl_sparse_normalize_backward(void *stream, const int64_t *row_ptr,
                                  const float *grad, const float *v,
                                  const float *denom, int64_t R, float eps,

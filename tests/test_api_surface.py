@@ -16,7 +16,8 @@ INTERNAL = {"_coalesce_sparse3d_reduce", "_coalesce_sparse3d_sum_raw", "_align_s
             "_sparse_topc_entries", "_prune_sparse_sources", "_restore_pruned_gradient",
             "_sparse_sum_selected_nodes", "_sample_group_quotas", "_sampled_sparse_cpu",
             "load_flashlog_kernel", "_kernel_stage_timing_enabled", "_kernel_cuda_reduce_enabled",
-            "_kernel_sync", "_kernel_log"}
+            "_kernel_sync", "_kernel_log", "_choose_flashlog_cpu_threads", "_flashlog_available_logical_cpus",
+            "_flashlog_physical_cores", "_ind2ptr_cpu"}
 
 PUBLIC = sorted(k for k in SURFACE if k.split(".")[0] not in INTERNAL)
 

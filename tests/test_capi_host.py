@@ -31,6 +31,16 @@ def test_library_exports_every_declared_symbol():
     assert _lib().lib().fl_abi_version() == _lib().ABI_VERSION
 
 
+def test_struct_layouts_match_the_library():
+    """The ctypes mirrors of fl_side, fl_sparse_hop and fl_ground_graph have
+    the sizes the library was compiled with."""
+    L = _lib()
+    lib = L.lib()
+    for struct, size_fn in L.STRUCT_SIZES:
+        assert ctypes.sizeof(struct) == getattr(lib, size_fn)(), struct.__name__
+    assert ctypes.sizeof(L.FlSide) == 8 * len(L.FlSide._fields_)
+
+
 @pytest.mark.parametrize("cfg,scale", [(1, 0.05), (2, 0.05), (3, 0.02)])
 def test_build_csr_structure_matches_oracle(cfg, scale):
     from flashlog_amd.flashlog_kernel import flashlog_kernel as fk

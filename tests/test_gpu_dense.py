@@ -93,9 +93,6 @@ def test_dense_pipeline_three_hops_c2_shape():
         x = (s / np.maximum(s.sum(-1, keepdims=True), np.float32(1e-7))).astype(np.float32)
 
 
-@pytest.mark.skip(reason="dense sum backward faulted the GPU twice (illegal memory access); cause found on "
-                         "reading: k_col_count stored the identity output through a null out_ind; fixed, "
-                         "but the fixed path is held off the GPU until its next verification run")
 @pytest.mark.parametrize("K", [0, 2, 7, 200])
 @pytest.mark.parametrize("wot_i", [False, True])
 def test_dense_sum_backward(K, wot_i):

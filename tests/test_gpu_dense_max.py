@@ -1,7 +1,8 @@
 """GPU parity of the dense max hop (dense_csr_max / FlashLogDenseMaxFunction)
 against the oracle: values and winning positions bit for bit; the
-winner-only gradients within 1e-5 relative (the winner terms are added with
-atomics, as in the reference)."""
+winner-only grad_A bit for bit (fixed per-(source, row) walks in CSR
+order) and grad_w within 1e-5 relative (per-pair partials in source
+order)."""
 import numpy as np
 import pytest
 import torch
@@ -106,8 +107,8 @@ def test_dense_max_backward(K, wot_i):
     torch.cuda.synchronize()
     gA = At.grad.reshape(BL, E).cpu().numpy()
     gw = wt.grad.reshape(BL, n).cpu().numpy()
-    np.testing.assert_allclose(gA, gA_ref, rtol=1e-5, atol=1e-6)
-    np.testing.assert_allclose(gw, gw_ref, rtol=1e-5, atol=1e-5)
+    assert np.array_equal(bits(gA), bits(gA_ref)), float(np.abs(gA - gA_ref).max())
+    np.testing.assert_allclose(gw, gw_ref, rtol=1e-5, atol=1e-6 * float(np.abs(gw_ref).max()))
 
 
 @pytest.mark.parametrize("K", [0, 5])

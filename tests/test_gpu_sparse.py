@@ -1,7 +1,7 @@
 """GPU parity of the sparse (COO) hop against the oracle: coordinates and
-fp32 values bit for bit (the CPU path's addition order), gradients within
-1e-5 relative, normalization within 1e-6 relative (tree vs. sequential
-row sums)."""
+fp32 values bit for bit (the CPU path's addition order), normalization
+bit for bit (the CPU path's sequential row sums), gradients within 1e-5
+relative."""
 import numpy as np
 import pytest
 import torch
@@ -156,6 +156,8 @@ def test_sparse_backward(mode, wot_i):
 
 
 def test_normalize_sparse3d():
+    """Values and denominators bit-identical to the CPU path (a left fold of
+    each row in entry order, then IEEE division); gradients within 1e-5."""
     fk = _fk()
     rng = np.random.default_rng(3)
     B, L, E = 5, 3, 400
@@ -165,7 +167,7 @@ def test_normalize_sparse3d():
     s = torch.sparse_coo_tensor(idx, vt, (B, L, E), is_coalesced=True)
     out = fk.normalize_sparse3d(s)
     want, denom = O.sparse_normalize(b, l, v, B, L)
-    np.testing.assert_allclose(out.values().detach().cpu().numpy(), want, rtol=1e-6)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(want))
     g = rng.standard_normal(v.shape[0]).astype(np.float32)
     (out.values() * torch.from_numpy(g).cuda()).sum().backward()
     row = b * L + l
@@ -176,9 +178,61 @@ def test_normalize_sparse3d():
     np.testing.assert_allclose(vt.grad.cpu().numpy(), want_g, rtol=1e-5, atol=1e-6)
 
 
+def test_normalize_long_rows_bitexact():
+    """Rows longer than one LDS chunk (2048 entries) and an empty row."""
+    fk = _fk()
+    rng = np.random.default_rng(31)
+    B, L, E = 2, 2, 60000
+    b, l, e, v = sparse_coo_state(B, L, E, 9000, rng)
+    keep = ~((b == 1) & (l == 0))
+    b, l, e, v = b[keep], l[keep], e[keep], v[keep]
+    s = torch.sparse_coo_tensor(torch.from_numpy(np.stack([b, l, e])).cuda(), torch.from_numpy(v).cuda(),
+                                (B, L, E), is_coalesced=True)
+    out = fk.normalize_sparse3d(s)
+    want, _ = O.sparse_normalize(b, l, v, B, L)
+    assert np.array_equal(bits(out.values().cpu().numpy()), bits(want))
+
+
+def test_normalize_nonfinite_rows():
+    """A row holding NaN, a row holding inf and a row summing below eps
+    against the GPU path's formula (flashlog.cu:2529-2591): d = row sum,
+    dc = d if d >= eps else eps (so a NaN sum divides by eps), out = v / dc;
+    backward g/dc - sum(g*v)/dc^2 where d >= eps, else g/dc."""
+    fk = _fk()
+    B, L, E, eps = 1, 4, 10, np.float32(1e-7)
+    b = np.zeros(9, np.int64)
+    l = np.array([0, 0, 1, 1, 2, 2, 3, 3, 3], np.int64)
+    e = np.array([1, 4, 2, 3, 0, 9, 1, 2, 3], np.int64)
+    v = np.array([0.5, np.nan, 0.25, np.inf, 1e-9, 2e-9, 0.125, -0.0, 0.375], np.float32)
+    vt = torch.from_numpy(v).cuda().requires_grad_(True)
+    s = torch.sparse_coo_tensor(torch.from_numpy(np.stack([b, l, e])).cuda(), vt, (B, L, E), is_coalesced=True)
+    out = fk.normalize_sparse3d(s)
+    row = l
+    d = np.zeros(L, np.float32)
+    for i in range(v.size):
+        d[row[i]] = np.float32(d[row[i]] + v[i])
+    dc = np.where(d >= eps, d, eps).astype(np.float32)
+    want = (v / dc[row]).astype(np.float32)
+    got = out.values().detach().cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(bits(got[fin]), bits(want[fin]))
+    g = np.array([1, 2, 3, 4, 5, 6, 7, 8, 9], np.float32)
+    (out.values() * torch.from_numpy(g).cuda()).sum().backward()
+    gv = vt.grad.cpu().numpy()
+    active = d >= eps
+    sgx = np.zeros(L, np.float64)
+    np.add.at(sgx, row, g.astype(np.float64) * v)
+    want_g = np.where(active[row], g / dc[row] - sgx[row] / (dc[row].astype(np.float64) ** 2), g / dc[row])
+    # row 0 (NaN sum) is inactive: g/eps; row 1 (inf sum) gives NaN corrections
+    ok = row != 1
+    np.testing.assert_allclose(gv[ok], want_g[ok], rtol=1e-5)
+    assert np.array_equal(np.isnan(gv[row == 1]), np.isnan(want_g[row == 1]))
+
+
 def test_three_hop_topk_pipeline():
     """Per hop: c1 + top-k hop + normalize, each hop checked bit for bit on
-    the GPU's own input (the normalization differs from the CPU's in order)."""
+    the GPU's own input."""
     fk = _fk()
     B, L = 4, 3
     rng, E, R, n, csr, mbool, masks, _, _ = _case(2, 1.0, B, L, 1, 123)
