@@ -14,6 +14,8 @@
 // counters are, for counts below 2^24).  The per-row filter count is two
 // binary searches over the sorted keys instead of one atomic per key.
 // Entries whose query index lies outside [0, B) are ignored.
+#include <mutex>
+
 #include "fl_common.h"
 #include "fl_abi.h"
 
@@ -174,6 +176,70 @@ int fl_filtered_ranks(void *stream, const int64_t *idx_b, const int64_t *idx_e, 
                                         n_filter, B, E, use_eql, ranks, (char *)workspace);
     return fl::launch_ranks<float>(st, idx_b, idx_e, (const float *)values, targets, filter_keys, nnz, n_filter, B,
                                    E, use_eql, ranks, (char *)workspace);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of fl_filtered_ranks: its scratch (truth scores and
+// counters, at most FL_RANKS_NOALLOC_MAX_B queries) lives in a file-scope
+// device array.  Each GPU holds its own copy; the host looks up that copy's
+// address once per device (hipGetSymbolAddress, with the device current) and
+// passes that address to the kernels -- the array's name in host code is not
+// a device address.
+
+namespace fl {
+namespace {
+
+constexpr size_t NOALLOC_BYTES =
+    ((sizeof(double) * (size_t)FL_RANKS_NOALLOC_MAX_B + 255) & ~(size_t)255) +
+    ((sizeof(uint32_t) * 4 * (size_t)FL_RANKS_NOALLOC_MAX_B + 255) & ~(size_t)255);
+
+__device__ __align__(256) unsigned char scratch[NOALLOC_BYTES];
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[NOALLOC_MAX_DEVICES];
+
+// This device's copy of `scratch` (looked up on the first call per device).
+int scratch_for_current_device(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+        return fl_fail(FL_ERR_HIP, "filtered_ranks_noalloc: no current device");
+    if (dev >= NOALLOC_MAX_DEVICES)
+        return fl_fail(FL_ERR_ARG, "filtered_ranks_noalloc: device %d beyond %d", dev, NOALLOC_MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (rc != hipSuccess || !p)
+            return fl_fail(FL_ERR_HIP, "filtered_ranks_noalloc: hipGetSymbolAddress failed: %s",
+                           hipGetErrorString(rc));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FL_OK;
+}
+
+}  // namespace
+}  // namespace fl
+
+extern "C" {
+
+int fl_filtered_ranks_noalloc(void *stream, const int64_t *idx_b, const int64_t *idx_e, const void *values,
+                              int values_f64, const int64_t *targets, const int64_t *filter_keys, int64_t nnz,
+                              int64_t n_filter, int64_t B, int64_t E, int use_eql, float *ranks) {
+    if (nnz < 0 || n_filter < 0 || B < 0 || E < 0)
+        return fl::fl_fail(FL_ERR_ARG, "filtered_ranks_noalloc: negative size");
+    if (B > FL_RANKS_NOALLOC_MAX_B)
+        return fl::fl_fail(FL_ERR_ARG, "filtered_ranks_noalloc: %lld queries, at most %d without a workspace",
+                           (long long)B, FL_RANKS_NOALLOC_MAX_B);
+    if (B == 0) return FL_OK;
+    void *ws = nullptr;
+    const int rc = fl::scratch_for_current_device(&ws);
+    if (rc != FL_OK) return rc;
+    return fl_filtered_ranks(stream, idx_b, idx_e, values, values_f64, targets, filter_keys, nnz, n_filter, B, E,
+                             use_eql, ranks, ws, fl::NOALLOC_BYTES);
 }
 
 }  // extern "C"

@@ -509,6 +509,23 @@ int fl_filtered_ranks(void *stream, const int64_t *idx_b, const int64_t *idx_e,
                       int use_eql, float *ranks, void *workspace,
                       size_t workspace_bytes);
 
+/* No counterpart in the reference.  fl_filtered_ranks without a workspace
+ * argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): its
+ * scratch is a file-scope device array of fixed size (about 1.5 MiB, held by
+ * every GPU the library runs on until the process ends), so at most
+ * FL_RANKS_NOALLOC_MAX_B queries per call (larger B is refused with
+ * FL_ERR_ARG).  It calls no allocator.  Every call on one GPU shares that
+ * GPU's array (each call clears what it uses, with kernels), so calls that
+ * overlap on one GPU -- on different streams or threads -- race. */
+#define FL_RANKS_NOALLOC_MAX_B 65536
+int fl_filtered_ranks_noalloc(void *stream, const int64_t *idx_b,
+                              const int64_t *idx_e, const void *values,
+                              int values_f64, const int64_t *targets,
+                              const int64_t *filter_keys, int64_t nnz,
+                              int64_t n_filter, int64_t B, int64_t E,
+                              int use_eql, float *ranks);
+
 /* ---- measurement ------------------------------------------------------ */
 
 /* No reference counterpart (the reference's FLASHLOG_STAGE_TIMING,
