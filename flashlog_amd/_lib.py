@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 19
+ABI_VERSION = 20
 FL_SEG = 32
 FL_SUP = 16
 
@@ -130,8 +130,10 @@ _SIGS = {
     "fl_sparse_expand": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                         ctypes.POINTER(FlSparseHop), ctypes.c_void_p, ctypes.c_void_p]),
     "fl_sparse_emit": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
+    "fl_sparse_backward_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3),
     "fl_sparse_backward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
-                                          ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
+                                          ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 6 +
+                           [ctypes.c_size_t]),
     "fl_sparse_topc": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 4 + [ctypes.c_void_p] * 3),
     "fl_sparse_rowptr_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
     "fl_sparse_channel_sum_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3),
@@ -165,8 +167,11 @@ _SIGS = {
                          [ctypes.c_int64] * 3 + [ctypes.c_void_p]),
     "fl_sparse_normalize_backward": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_float,
                                                                             ctypes.c_void_p]),
+    "fl_sparse_channel_weighted_add": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4 +
+                                       [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]),
+    "fl_rule_accumulate_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3),
     "fl_rule_accumulate": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64, ctypes.c_void_p] +
-                           [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_void_p]),
+                           [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]),
     "fl_rule_finalize": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 3 +
                          [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]),
     "fl_filtered_ranks_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int]),

@@ -4,7 +4,7 @@
 // A chunk of rules has been grounded for every source b: a COO state
 // (b, rule l, entity e, v) with v the path count (or 0/1 with Boolean paths).
 // Per rank k the scores are
-//   sum:  S_k[b, e] += v * W[rule, k]
+//   sum:  S_k[b, e] += sum over the chunk's rules, in rule order, of v * W[rule, k]
 //   max:  S_k[b, e]  = max(S_k[b, e], v * W[rule, k])      (W >= 0)
 // accumulated over chunks in a dense [K, B*E] buffer; then every (k, b) row
 // is normalized by its sum (clamped to 1e-30) and the ranks are summed (or
@@ -16,15 +16,16 @@ namespace fl {
 
 constexpr int RB_NT = 256;
 
-// Thread per state entry.  Sums use float atomics (run-dependent last bits,
-// as the reference's index_add_); maxima of nonnegative values use the
-// integer order of their bits, which is exact.
-__global__ __launch_bounds__(RB_NT) void k_rule_accum(const int64_t *__restrict__ sb,
-                                                     const int64_t *__restrict__ sl,
-                                                     const int64_t *__restrict__ se,
-                                                     const float *__restrict__ sv, int64_t nnz,
-                                                     const float *__restrict__ W, int64_t K, int64_t B, int64_t E,
-                                                     int is_max, float *__restrict__ dense) {
+// Maxima: thread per state entry; the maximum of nonnegative values is
+// exact in any order (the integer order of their bits), so atomics give the
+// same bits on every run.  (Sums go through fl_sparse_channel_weighted_add,
+// one writer per accumulator slot.)
+__global__ __launch_bounds__(RB_NT) void k_rule_accum_max(const int64_t *__restrict__ sb,
+                                                         const int64_t *__restrict__ sl,
+                                                         const int64_t *__restrict__ se,
+                                                         const float *__restrict__ sv, int64_t nnz,
+                                                         const float *__restrict__ W, int64_t K, int64_t B,
+                                                         int64_t E, float *__restrict__ dense) {
     const int64_t i = (int64_t)blockIdx.x * RB_NT + threadIdx.x;
     if (i >= nnz) return;
     const int64_t key = sb[i] * E + se[i];
@@ -32,12 +33,7 @@ __global__ __launch_bounds__(RB_NT) void k_rule_accum(const int64_t *__restrict_
     const float *wr = W + sl[i] * K;
     for (int64_t k = 0; k < K; ++k) {
         const float x = fl_mul(v, wr[k]);
-        float *slot = dense + k * B * E + key;
-        if (is_max) {
-            if (x > 0.0f) atomicMax((unsigned int *)slot, __float_as_uint(x));
-        } else if (x != 0.0f) {
-            atomicAdd(slot, x);
-        }
+        if (x > 0.0f) atomicMax((unsigned int *)(dense + k * B * E + key), __float_as_uint(x));
     }
 }
 
@@ -79,14 +75,31 @@ __global__ __launch_bounds__(RB_NT) void k_rule_combine(const float *__restrict_
 
 extern "C" {
 
+size_t fl_rule_accumulate_bytes(int64_t nnz, int64_t B, int64_t L) {
+    if (nnz < 0 || B < 0 || L < 0) return 0;
+    return ((fl_sparse_channel_sum_bytes(nnz, B, L) + 255) & ~(size_t)255) + 256;
+}
+
 int fl_rule_accumulate(void *stream, const int64_t *sb, const int64_t *sl, const int64_t *se, const float *sv,
-                       int64_t nnz, const float *W, int64_t K, int64_t B, int64_t E, int is_max, float *dense) {
-    if (nnz < 0 || K < 1 || B < 0 || E < 0) return fl::fl_fail(FL_ERR_ARG, "rule_accumulate: bad shape");
+                       int64_t nnz, const float *W, int64_t K, int64_t B, int64_t L, int64_t E, int is_max,
+                       float *dense, void *ws, size_t ws_bytes) {
+    if (nnz < 0 || K < 1 || B < 0 || L < 0 || E < 0) return fl::fl_fail(FL_ERR_ARG, "rule_accumulate: bad shape");
     if (nnz == 0) return FL_OK;
     if (!sb || !sl || !se || !sv || !W || !dense) return fl::fl_fail(FL_ERR_ARG, "rule_accumulate: null pointer");
-    FL_LAUNCH("k_rule_accum", fl::k_rule_accum, dim3((unsigned)((nnz + fl::RB_NT - 1) / fl::RB_NT)), dim3(fl::RB_NT),
-              0, (hipStream_t)stream, sb, sl, se, sv, nnz, W, K, B, E, is_max, dense);
-    return fl::fl_check_launch("rule_accumulate");
+    hipStream_t st = (hipStream_t)stream;
+    if (is_max) {
+        FL_LAUNCH("k_rule_accum_max", fl::k_rule_accum_max, dim3((unsigned)((nnz + fl::RB_NT - 1) / fl::RB_NT)),
+                  dim3(fl::RB_NT), 0, st, sb, sl, se, sv, nnz, W, K, B, E, dense);
+        return fl::fl_check_launch("rule_accumulate");
+    }
+    if (!ws || ws_bytes < fl_rule_accumulate_bytes(nnz, B, L))
+        return fl::fl_fail(FL_ERR_ARG, "rule_accumulate: workspace too small");
+    // rank the entries of every (b, e) in rule order, then one writer per slot
+    const size_t cs = (fl_sparse_channel_sum_bytes(nnz, B, L) + 255) & ~(size_t)255;
+    int64_t *plan = (int64_t *)((char *)ws + cs);
+    int rc = fl_sparse_channel_sum_plan(stream, sb, sl, se, nnz, B, L, E, ws, cs, plan);
+    if (rc != FL_OK) return rc;
+    return fl_sparse_channel_weighted_add(stream, sb, sl, se, sv, nnz, B, L, E, W, K, ws, dense);
 }
 
 int fl_rule_finalize(void *stream, const float *dense, int64_t K, int64_t B, int64_t E, int final_max,

@@ -1773,18 +1773,24 @@ __device__ __forceinline__ float sp_seg_scan(float x, int key) {
 // Backward, wave per entry over the entry's raw items (raw order; the
 // forward recorded each one's CSR position, attention column and output
 // index): grad_v[i] = sum over items of (g*m)*w, the identity item taken
-// with m = 1 (flashlog.cu:1856-1959); grad_w[r, col] += (g*m)*a, summed per
-// column within each 64-item chunk (the items of a group are consecutive)
-// and added by atomics, as the reference adds its per-item terms.  Holes
-// (sum: masked kept edges, m == 0) and, for max, the losing items (output
-// index -1) take no part (flashlog.cu:2364-2410).  The next chunk's records are
-// requested before the current chunk's gathers.
-// Workgroup per BW_EPB consecutive entries (rows ascending): the per-column
-// sums of entries in the range's first or last row are added into LDS
-// copies of those two grad_w rows and flushed once per workgroup; entries of
-// rows strictly inside the range add to grad_w directly.
-constexpr int BW_EPB = 32;
-constexpr int64_t BW_LDS_MAX_N = 4096;  // columns of the LDS rows (2 * 4 * n bytes)
+// with m = 1 (flashlog.cu:1856-1959); grad_w[r, col] = sum of (g*m)*a over
+// the row's items of that column (flashlog.cu:1910-1914,1957-1958, where
+// atomics add them).  Holes (sum: masked kept edges, m == 0) and, for max,
+// the losing items (output index -1) take no part (flashlog.cu:2364-2410).
+// The next chunk's records are requested before the current chunk's
+// gathers.
+//
+// grad_w without atomics, in a fixed order.  Within an entry every column
+// belongs to one run of consecutive items (one relation group, or the
+// identity item).  A workgroup takes BW_CH consecutive entries of one row;
+// wave w of it takes entries w, w+4, ... of those and adds, in that order,
+// each run's per-chunk segmented sums into a row of n floats of its own
+// (LDS, or global memory when n > BW_LDS_MAX_N); the workgroup writes the
+// sum ((row0 + row1) + row2) + row3 to its partial row, and k_sp_gw_fin adds
+// a row's partial rows in chunk order.
+constexpr int BW_CH = 128;
+constexpr int BW_WAVES = SEL_NT / FL_WAVE;
+constexpr int64_t BW_LDS_MAX_N = 4096;  // columns of the LDS rows (4 * 4 * n bytes)
 
 __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                              const int64_t *__restrict__ sl, const float *__restrict__ sv,
@@ -1793,38 +1799,64 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
                                              const int32_t *__restrict__ raw_out,
                                              const int32_t *__restrict__ raw_pos,
                                              const int16_t *__restrict__ raw_col, const float *__restrict__ grad,
-                                             float *__restrict__ grad_v, float *__restrict__ grad_w, int64_t i,
-                                             float *acc, int64_t rowa, int64_t rowb);
+                                             float *__restrict__ grad_v, int64_t i, float *gdst);
 
+// Thread per row: its number of BW_CH-entry chunks.
+__global__ void k_sp_bw_chunks(const int64_t *__restrict__ row_ptr, int64_t R, int64_t *__restrict__ nchunk) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= R) return;
+    nchunk[r] = (row_ptr[r + 1] - row_ptr[r] + BW_CH - 1) / BW_CH;
+}
+
+template <bool USE_LDS>
 __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                   const int64_t *__restrict__ sl, const float *__restrict__ sv,
-                                                  int64_t nnz, const float *__restrict__ w, int64_t L, int64_t n,
-                                                  int64_t r_size, int holes, int use_lds,
-                                                  const int64_t *__restrict__ item_off,
+                                                  const int64_t *__restrict__ row_ptr,
+                                                  const int64_t *__restrict__ chunk_ptr, int64_t R,
+                                                  const float *__restrict__ w, int64_t L, int64_t n, int64_t r_size,
+                                                  int holes, const int64_t *__restrict__ item_off,
                                                   const int32_t *__restrict__ raw_out,
                                                   const int32_t *__restrict__ raw_pos,
                                                   const int16_t *__restrict__ raw_col,
                                                   const float *__restrict__ grad, float *__restrict__ grad_v,
-                                                  float *__restrict__ grad_w) {
-    extern __shared__ float bw_acc[];  // [2][n] when use_lds
-    const int64_t e0 = (int64_t)blockIdx.x * BW_EPB;
-    const int64_t e1 = e0 + BW_EPB < nnz ? e0 + BW_EPB : nnz;
-    const int64_t rowa = sb[e0] * L + sl[e0], rowb = sb[e1 - 1] * L + sl[e1 - 1];
-    if (use_lds) {
-        for (int64_t q = threadIdx.x; q < 2 * n; q += SEL_NT) bw_acc[q] = 0.0f;
-        __syncthreads();
+                                                  float *__restrict__ wave_rows, float *__restrict__ part) {
+    extern __shared__ float bw_rows[];  // [BW_WAVES][n] when USE_LDS
+    const int64_t blk = blockIdx.x;
+    if (blk >= chunk_ptr[R]) return;  // the grid is an upper bound of the chunk count
+    // the block's row: chunk_ptr[r] <= blk < chunk_ptr[r + 1]
+    int64_t lo = 0, hi = R;
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (chunk_ptr[mid] <= blk) lo = mid; else hi = mid;
     }
-    for (int64_t i = e0 + threadIdx.x / FL_WAVE; i < e1; i += SEL_NT / FL_WAVE)
+    const int64_t r = lo;
+    const int64_t e0 = row_ptr[r] + (blk - chunk_ptr[r]) * BW_CH;
+    const int64_t e1 = e0 + BW_CH < row_ptr[r + 1] ? e0 + BW_CH : row_ptr[r + 1];
+    const int wid = threadIdx.x / FL_WAVE;
+    float *rows = USE_LDS ? bw_rows : wave_rows + blk * BW_WAVES * n;
+    for (int64_t q = threadIdx.x; q < BW_WAVES * n; q += SEL_NT) rows[q] = 0.0f;
+    __syncthreads();
+    for (int64_t i = e0 + wid; i < e1; i += BW_WAVES)
         sp_bwd_entry(ori, inv, sb, sl, sv, w, L, n, r_size, holes, item_off, raw_out, raw_pos, raw_col, grad, grad_v,
-                     grad_w, i, use_lds ? bw_acc : nullptr, rowa, rowb);
-    if (use_lds) {
-        __syncthreads();
-        for (int64_t q = threadIdx.x; q < 2 * n; q += SEL_NT) {
-            const float x = bw_acc[q];
-            const int64_t row = q < n ? rowa : rowb;
-            if (x != 0.0f && (q < n || rowb != rowa)) atomicAdd(&grad_w[row * n + (q < n ? q : q - n)], x);
-        }
+                     i, rows + wid * n);
+    __syncthreads();
+    for (int64_t c = threadIdx.x; c < n; c += SEL_NT) {
+        float x = rows[c];
+#pragma unroll
+        for (int k = 1; k < BW_WAVES; ++k) x = fl_add(x, rows[k * n + c]);
+        part[blk * n + c] = x;
     }
+}
+
+// grad_w[r, c] = the row's partial rows added in chunk order.
+__global__ void k_sp_gw_fin(const int64_t *__restrict__ chunk_ptr, const float *__restrict__ part, int64_t n,
+                            float *__restrict__ grad_w) {
+    const int64_t r = blockIdx.y;
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= n) return;
+    float x = 0.0f;
+    for (int64_t b = chunk_ptr[r]; b < chunk_ptr[r + 1]; ++b) x = fl_add(x, part[b * n + c]);
+    grad_w[r * n + c] = x;
 }
 
 __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
@@ -1834,12 +1866,9 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
                                              const int32_t *__restrict__ raw_out,
                                              const int32_t *__restrict__ raw_pos,
                                              const int16_t *__restrict__ raw_col, const float *__restrict__ grad,
-                                             float *__restrict__ grad_v, float *__restrict__ grad_w, int64_t i,
-                                             float *acc, int64_t rowa, int64_t rowb) {
+                                             float *__restrict__ grad_v, int64_t i, float *gdst) {
     const int lane = fl_lane();
     const int64_t r = sb[i] * L + sl[i];
-    // where this entry's per-column sums go: an LDS row or grad_w
-    float *gdst = acc ? (r == rowa ? acc : (r == rowb ? acc + n : nullptr)) : nullptr;
     const float a = sv[i];
     const float *wrow = w + r * n;
     const int64_t k0 = item_off[i], k1 = item_off[i + 1];
@@ -1874,19 +1903,20 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
             if (edge_grads && p >= 0) {
                 const fl_side &s = iv ? inv : ori;
                 if (s.grad_edge) {
+                    // trainable edge weights only: added with atomics, as the
+                    // reference's index_add_ does (run-dependent last bits)
                     const float ge = fl_mul(fl_mul(fl_mul(fl_mul(gv, a), wv), m), s.dscore[p]);
                     if (ge != 0.0f) atomicAdd(&s.grad_edge[s.order[p]], ge);
                 }
             }
         }
-        // per-column sums of this chunk (segmented scan keyed by the column)
+        // per-column sums of this chunk (segmented scan keyed by the column);
+        // the tail lane of each segment adds it to the wave's row -- each
+        // column has one tail per chunk, and the chunks go in order
         const float x = sp_seg_scan(gwv, col);
         const int next1 = fl_dpp<0x130>(col + 1);  // wave_shl:1, lane 63 receives 0
         const bool tail = next1 != col + 1;
-        if (col >= 0 && tail && x != 0.0f) {
-            if (gdst) atomicAdd(&gdst[col], x);
-            else atomicAdd(&grad_w[r * n + col], x);
-        }
+        if (col >= 0 && tail) gdst[col] = fl_add(gdst[col], x);
         p = pn;
         col = coln;
         loc = locn;
@@ -2506,6 +2536,33 @@ __global__ void k_cs_emit(const int64_t *__restrict__ sb, const int64_t *__restr
     out_v[o] = acc;
 }
 
+// Weighted channel sums into a dense accumulator (rule-bank scoring): for
+// the run of entries sharing (b, e), in channel order, and every rank k,
+// acc = sum from 0 of v * W[l, k]; then dense[k, b*E + e] += acc.  One thread
+// per run: each accumulator slot has one writer per call, so the dense sums
+// are added in a fixed order (calls in order, channels in order).
+__global__ void k_cs_weighted_add(const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
+                                  const int64_t *__restrict__ se, const float *__restrict__ v, int64_t nnz,
+                                  const int32_t *__restrict__ perm, const int32_t *__restrict__ head,
+                                  const float *__restrict__ W, int64_t K, int64_t B, int64_t E,
+                                  float *__restrict__ dense) {
+    const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (m >= nnz || !head[m]) return;
+    const int32_t i = perm[m];
+    if (i < 0 || i >= nnz) return;
+    const int64_t key = sb[i] * E + se[i];
+    for (int64_t k = 0; k < K; ++k) {
+        float acc = 0.0f;
+        for (int64_t q = m; q < nnz && (q == m || !head[q]); ++q) {
+            const int32_t j = perm[q];
+            if (j < 0 || j >= nnz) break;
+            acc = fl_add(acc, fl_mul(v[j], W[sl[j] * K + k]));
+        }
+        float *slot = dense + k * B * E + key;
+        *slot = fl_add(*slot, acc);
+    }
+}
+
 extern "C" {
 
 int64_t fl_sparse_buckets(int64_t E) { return sp_buckets(E); }
@@ -2715,28 +2772,75 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h, const int64_t *out_base
     return fl_check_launch("sparse_emit");
 }
 
+}  // extern "C"
+
+namespace {
+
+// fl_sparse_backward's workspace: chunk counts / pointers, scan scratch, the
+// partial rows and (n > BW_LDS_MAX_N) the waves' rows.
+struct SpBwd {
+    int64_t *chunk_ptr, *tmp;
+    float *part, *wave_rows;
+    int64_t blocks;
+    size_t bytes;
+};
+
+SpBwd sp_bwd_layout(int64_t nnz, int64_t R, int64_t n, char *base) {
+    SpBwd x{};
+    size_t off = 0;
+    auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
+    x.blocks = (nnz + BW_CH - 1) / BW_CH + R;  // at least the number of chunks
+    x.chunk_ptr = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
+    x.tmp = (int64_t *)take(scan_tmp_bytes(R + 1));
+    x.part = (float *)take(sizeof(float) * (size_t)(x.blocks * n));
+    x.wave_rows = n > BW_LDS_MAX_N ? (float *)take(sizeof(float) * (size_t)(x.blocks * BW_WAVES * n)) : nullptr;
+    x.bytes = off;
+    return x;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fl_sparse_backward_bytes(int64_t nnz, int64_t R, int64_t n) {
+    if (nnz < 0 || R < 0 || n < 1) return 0;
+    return sp_bwd_layout(nnz, R, n, nullptr).bytes;
+}
+
 int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h,
                        const int64_t *out_base, const int32_t *raw_local, const float *grad_out, float *grad_v,
-                       float *grad_w) {
+                       float *grad_w, void *workspace, size_t workspace_bytes) {
     int rc;
     if ((rc = sp_check(ori, inv, h, "sparse_backward")) != FL_OK) return rc;
     if (!h->ws1 || !out_base || !grad_v || !grad_w) return fl_fail(FL_ERR_ARG, "sparse_backward: null argument");
     if (h->items > 0 && (!raw_local || !grad_out || !h->raw_pos || !h->raw_col))
         return fl_fail(FL_ERR_ARG, "sparse_backward: null raw map (raw_local, raw_pos, raw_col)");
     if (h->mode == SP_FIXED) return fl_fail(FL_ERR_ARG, "sparse_backward: the fixed-relation step has no backward");
-    const int64_t R = h->B * h->L, NB = sp_buckets(h->E);
+    const int64_t R = h->B * h->L;
+    if (!workspace || workspace_bytes < fl_sparse_backward_bytes(h->nnz, R, h->n))
+        return fl_fail(FL_ERR_ARG, "sparse_backward: workspace too small");
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
+    SpBwd x = sp_bwd_layout(h->nnz, R, h->n, (char *)workspace);
     hipStream_t st = (hipStream_t)stream;
     if (R * h->n > 0)
         FL_LAUNCH("k_fill_f32", k_fill_f32, dim3((unsigned)((R * h->n + 255) / 256)), dim3(256), 0, st, grad_w,
                   R * h->n, 0.0f);
-    (void)NB;
-    const int use_lds = h->n <= BW_LDS_MAX_N;
-    if (h->nnz > 0)
-        FL_LAUNCH("k_sp_bwd", k_sp_bwd, dim3((unsigned)((h->nnz + BW_EPB - 1) / BW_EPB)), dim3(SEL_NT),
-                  use_lds ? sizeof(float) * 2 * (size_t)h->n : 0, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_v, h->nnz,
-                  h->w, h->L, h->n, h->r_size, (h->mode == SP_TOPK && h->aggregate == SP_SUM) ? 1 : 0, use_lds,
-                  p.item_off, raw_local, h->raw_pos, h->raw_col, grad_out, grad_v, grad_w);
+    if (h->nnz == 0 || R == 0) return fl_check_launch("sparse_backward");
+    FL_LAUNCH("k_sp_bw_chunks", k_sp_bw_chunks, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, p.row_ptr, R,
+              x.chunk_ptr);
+    if ((rc = exclusive_scan(st, x.chunk_ptr, x.chunk_ptr, R, x.tmp)) != FL_OK) return rc;
+    const int holes = (h->mode == SP_TOPK && h->aggregate == SP_SUM) ? 1 : 0;
+    if (h->n <= BW_LDS_MAX_N)
+        FL_LAUNCH("k_sp_bwd", k_sp_bwd<true>, dim3((unsigned)x.blocks), dim3(SEL_NT),
+                  sizeof(float) * BW_WAVES * (size_t)h->n, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_v, p.row_ptr,
+                  x.chunk_ptr, R, h->w, h->L, h->n, h->r_size, holes, p.item_off, raw_local, h->raw_pos, h->raw_col,
+                  grad_out, grad_v, x.wave_rows, x.part);
+    else
+        FL_LAUNCH("k_sp_bwd", k_sp_bwd<false>, dim3((unsigned)x.blocks), dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b,
+                  h->sp_l, h->sp_v, p.row_ptr, x.chunk_ptr, R, h->w, h->L, h->n, h->r_size, holes, p.item_off,
+                  raw_local, h->raw_pos, h->raw_col, grad_out, grad_v, x.wave_rows, x.part);
+    FL_LAUNCH("k_sp_gw_fin", k_sp_gw_fin, dim3((unsigned)((h->n + 255) / 256), (unsigned)R), dim3(256), 0, st,
+              x.chunk_ptr, x.part, h->n, grad_w);
     return fl_check_launch("sparse_backward");
 }
 
@@ -2935,6 +3039,20 @@ int fl_sparse_channel_sum_plan(void *stream, const int64_t *sp_b, const int64_t 
     if (rc != FL_OK) return rc;
     FL_LAUNCH("k_cs_plan_out", k_cs_plan_out, dim3(1), dim3(64), 0, st, x.hoff, nnz, x.err, plan);
     return fl_check_launch("sparse_channel_sum_plan");
+}
+
+int fl_sparse_channel_weighted_add(void *stream, const int64_t *sp_b, const int64_t *sp_l, const int64_t *sp_e,
+                                   const float *v, int64_t nnz, int64_t B, int64_t L, int64_t E, const float *W,
+                                   int64_t K, void *ws, float *dense) {
+    if (nnz < 0 || B < 0 || L < 0 || E < 0 || K < 1)
+        return fl_fail(FL_ERR_ARG, "sparse_channel_weighted_add: bad sizes");
+    if (nnz == 0) return FL_OK;
+    if (!ws || !sp_b || !sp_l || !sp_e || !v || !W || !dense)
+        return fl_fail(FL_ERR_ARG, "sparse_channel_weighted_add: null argument");
+    CsLayout x = cs_layout(nnz, B * L, (char *)ws);
+    FL_LAUNCH("k_cs_weighted_add", k_cs_weighted_add, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0,
+              (hipStream_t)stream, sp_b, sp_l, sp_e, v, nnz, x.perm, x.head, W, K, B, E, dense);
+    return fl_check_launch("sparse_channel_weighted_add");
 }
 
 int fl_sparse_channel_sum_emit(void *stream, const int64_t *sp_b, const int64_t *sp_e, const float *v, int64_t nnz,

@@ -986,11 +986,14 @@ def _sparse_backward(state, grad_values, grad_edge=None):
     grad_values = grad_values.contiguous().float()
     gv = torch.empty(max(h.nnz, 1), dtype=torch.float32, device=dev)
     gw = torch.empty((h.B * h.L, state.n), dtype=torch.float32, device=dev)
+    lib = _lib.lib()
+    ws_bytes = lib.fl_sparse_backward_bytes(h.nnz, h.B * h.L, state.n)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     state.sides.set_grad_edge(grad_edge)
     try:
-        check(_lib.lib().fl_sparse_backward(_stream(grad_values), ctypes.byref(state.sides.ori),
-                                            ctypes.byref(state.sides.inv), ctypes.byref(h), ptr(state.out_base),
-                                            ptr(state.raw_local), ptr(grad_values), ptr(gv), ptr(gw)),
+        check(lib.fl_sparse_backward(_stream(grad_values), ctypes.byref(state.sides.ori),
+                                     ctypes.byref(state.sides.inv), ctypes.byref(h), ptr(state.out_base),
+                                     ptr(state.raw_local), ptr(grad_values), ptr(gv), ptr(gw), ptr(ws), ws_bytes),
               "sparse_backward")
     finally:
         state.sides.set_grad_edge(None)

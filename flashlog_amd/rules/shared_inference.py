@@ -129,9 +129,11 @@ def score(ev, sources, rules, csr, relations, entities, chunk_size,
                 ix = state.indices()
                 vals = state.values().float().contiguous()
                 w = weights[off:off + C].contiguous()
+                ws_bytes = lib.fl_rule_accumulate_bytes(vals.numel(), nb, C)
+                ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
                 check(lib.fl_rule_accumulate(st, ptr(ix[0].contiguous()), ptr(ix[1].contiguous()),
                                              ptr(ix[2].contiguous()), ptr(vals), vals.numel(), ptr(w), ranks, nb,
-                                             E, is_max, ptr(dense)), "rule_accumulate")
+                                             C, E, is_max, ptr(dense), ptr(ws), ws_bytes), "rule_accumulate")
             stats["chunks"] += 1
         rowsum = torch.empty(ranks * nb, dtype=torch.float32, device=device)
         total = torch.empty(nb * E, dtype=torch.float32, device=device)

@@ -353,20 +353,30 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h,
                    const int64_t *out_base, int64_t *out_b, int64_t *out_l,
                    int64_t *out_e, float *out_v);
 
+/* Workspace bytes of fl_sparse_backward (nnz entries, R = B*L rows, n
+ * attention columns). */
+size_t fl_sparse_backward_bytes(int64_t nnz, int64_t R, int64_t n);
+
 /* Replaces flashlog_backward_sparse3d_cached_cuda and, for max,
  * flashlog_backward_sparse3d_max_cached_cuda (flashlog.cu:2243-2478,
- * kernels :1856-1997): grad_v[i] = sum over entry i's items (max: its
- * winning items) of (g*m)*w (+ g*w[n-1] for the identity item); grad_w
- * [B*L, n] accumulates (g*m)*a (+ g*a at n-1).  grad_out holds the gradient
- * of every output entry.  With a side's grad_edge set (trainable edge
- * weights, flashlog_kernel.py:1306-1336), grad_edge[order[p]] also
- * accumulates (((g*a)*w)*m)*dscore[p] for the side's items (the caller
- * zeroes it).  Needs the plan workspace of the forward and the raw_pos /
- * raw_col arrays that its expand filled (h->raw_pos, h->raw_col). */
+ * kernels :1856-1997) without their atomics: grad_v[i] = sum over entry
+ * i's items (max: its winning items) of (g*m)*w (+ g*w[n-1] for the
+ * identity item), added by one wave in a fixed order; grad_w [B*L, n] =
+ * per row the sum of (g*m)*a (+ g*a at n-1) over its items, in a fixed
+ * order (per entry and column the run of the column, entries in fixed
+ * chunks, chunks in order), so every run gives the same bits.  grad_out
+ * holds the gradient of every output entry.  With a side's grad_edge set
+ * (trainable edge weights, flashlog_kernel.py:1306-1336),
+ * grad_edge[order[p]] also accumulates (((g*a)*w)*m)*dscore[p] for the
+ * side's items, with atomics (the caller zeroes it).  Needs the plan
+ * workspace of the forward, the raw_pos / raw_col arrays that its expand
+ * filled (h->raw_pos, h->raw_col) and a workspace of
+ * fl_sparse_backward_bytes. */
 int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv,
                        const fl_sparse_hop *h, const int64_t *out_base,
                        const int32_t *raw_local, const float *grad_out,
-                       float *grad_v, float *grad_w);
+                       float *grad_v, float *grad_w, void *workspace,
+                       size_t workspace_bytes);
 
 /* Replaces _sparse_topc_entries (flashlog_kernel.py:1092-1140), the c1
  * budget on a COO state sorted by row: keep[i] = 1 for the entries to keep.
@@ -461,14 +471,35 @@ int fl_sparse_channel_sum_emit(void *stream, const int64_t *sp_b,
 
 /* ---- rule-bank scoring ------------------------------------------------- */
 
-/* Replaces the dense accumulation of rules/shared_inference.py:200-206: the
- * grounded COO state of a rule chunk (b, rule l, entity e, v) is added
- * into dense [K, B*E] as v * W[l, k] (is_max = 0, float atomics) or maxed
- * into it (is_max = 1; values >= 0, exact). */
+/* Adds weighted channel sums of a coalesced [B, L, E] state into a dense
+ * accumulator: for every (b, e) and rank k, dense[k, b*E + e] += the sum
+ * from 0, in channel order, of v[b, l, e] * W[l, k].  Uses the workspace
+ * that fl_sparse_channel_sum_plan filled (the host need not read its plan
+ * first); one writer per accumulator slot, so no atomics. */
+int fl_sparse_channel_weighted_add(void *stream, const int64_t *sp_b,
+                                   const int64_t *sp_l, const int64_t *sp_e,
+                                   const float *v, int64_t nnz, int64_t B,
+                                   int64_t L, int64_t E, const float *W,
+                                   int64_t K, void *ws, float *dense);
+
+/* ---- rule-bank scoring ------------------------------------------------- */
+
+/* Workspace bytes of fl_rule_accumulate (sum) for a chunk state of nnz
+ * entries, B sources and L rules. */
+size_t fl_rule_accumulate_bytes(int64_t nnz, int64_t B, int64_t L);
+
+/* Replaces the dense accumulation of rules/shared_inference.py:200-206
+ * (index_add_ / scatter_reduce_ amax): the grounded, coalesced COO state of
+ * a chunk of L rules (b, rule l, entity e, v) is added into dense [K, B*E]
+ * as, per (b, e), the sum over the chunk's rules in rule order of
+ * v * W[l, k] (is_max = 0; one writer per slot, so the bits are the same on
+ * every run), or maxed into it (is_max = 1; values >= 0: exact in any order,
+ * no workspace needed). */
 int fl_rule_accumulate(void *stream, const int64_t *sb, const int64_t *sl,
                        const int64_t *se, const float *sv, int64_t nnz,
-                       const float *W, int64_t K, int64_t B, int64_t E,
-                       int is_max, float *dense);
+                       const float *W, int64_t K, int64_t B, int64_t L,
+                       int64_t E, int is_max, float *dense, void *ws,
+                       size_t ws_bytes);
 
 /* Replaces the finalization of rules/shared_inference.py:224-237: rowsum
  * [K*B] = per (rank, source) row sums (fixed order); total [B*E] = over ranks

@@ -38,7 +38,10 @@
  *   or_sparse_forward: bit-compared with the reference's flashlog_forward_sparse3d_sum_cpu
  *     (oracle/_ref) in mode 0 and, where the modes coincide, in mode 1; float64
  *     closed form over the expanded edge list.
- *   or_sparse_backward: float64 adjoint of the closed form.
+ *   or_sparse_backward: element by element against the reference's
+ *     flashlog_backward_sparse3d_sum_cpu (oracle/_ref, one thread): bit for bit
+ *     with 0/1 masks, within 1e-6 with fractional ones; float64 adjoint of the
+ *     closed form.
  *   or_quota_takes: the published SplitMix64 output sequence (seed 0); the
  *     closed form of the reference's own CPU quota rule (flashlog_kernel.py:
  *     1978-2003: floors + differences of the rounded capacity prefix) with

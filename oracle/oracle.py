@@ -587,34 +587,38 @@ def fixed_relation_step(b, l, e, v, ops, h, r, t, E, R):
 
 
 def rule_scores(h, r, t, E, R, sources, bodies, W, reduction="sum", boolean_paths=False, final_max=False):
-    """Dense [B, E] float64 scores: per rule the path-count vector
-    e_s^T M_op1 M_op2 ... (Boolean after every step when boolean_paths or
-    max), per rank the weighted sum (or max) over rules, each (rank, source)
-    row divided by max(its sum, 1e-30), ranks summed (or maxed)."""
+    """Dense [B, E] float64 scores: per rule the path-count vectors
+    e_s^T M_op1 M_op2 ... of every source at once (sparse [E, B] columns;
+    Boolean after every step when boolean_paths or max), per rank the
+    weighted sum (or max) over rules, each (rank, source) row divided by
+    max(its sum, 1e-30), ranks summed (or maxed)."""
+    import scipy.sparse as sp
     boolean_paths = boolean_paths or reduction == "max"
     W = np.asarray(W, np.float64)
     mats = {}
     B, K = len(sources), W.shape[1]
-    S = np.zeros((K, B, E))
+    start = sp.csc_matrix((np.ones(B), (np.asarray(sources, np.int64), np.arange(B))), shape=(E, B))
+    S = np.zeros((K, E, B))
     for ri, body in enumerate(bodies):
-        for bi, s in enumerate(sources):
-            x = np.zeros(E)
-            x[s] = 1.0
-            for op in body:
-                if op not in mats:
-                    mats[op] = _op_matrix(h, r, t, E, R, op)
-                x = mats[op].T @ x
-                if boolean_paths:
-                    x = (x > 0).astype(np.float64)
-            for k in range(K):
-                if reduction == "max":
-                    S[k, bi] = np.maximum(S[k, bi], W[ri, k] * (x > 0))
-                else:
-                    S[k, bi] += W[ri, k] * x
+        x = start
+        for op in body:
+            if op not in mats:
+                mats[op] = _op_matrix(h, r, t, E, R, op).T.tocsr()
+            x = (mats[op] @ x).tocsc()
+            if boolean_paths:
+                x.data = (x.data > 0).astype(np.float64)
+                x.eliminate_zeros()
+        x = x.tocoo()
+        for k in range(K):
+            if reduction == "max":
+                np.maximum.at(S[k], (x.row, x.col), W[ri, k] * (x.data > 0))
+            else:
+                np.add.at(S[k], (x.row, x.col), W[ri, k] * x.data)
     total = np.zeros((B, E))
     for k in range(K):
-        d = np.maximum(S[k].sum(1, keepdims=True), 1e-30)
-        part = S[k] / d
+        Sk = S[k].T
+        d = np.maximum(Sk.sum(1, keepdims=True), 1e-30)
+        part = Sk / d
         total = np.maximum(total, part) if final_max else total + part
     return total
 

@@ -57,3 +57,13 @@ def sparse_coo_state(B, L, E, per_row, rng, ties=False):
             bs.append(np.full(k, b)); ls.append(np.full(k, l)); es.append(e); vs.append(v)
     return (np.concatenate(bs).astype(np.int64), np.concatenate(ls).astype(np.int64),
             np.concatenate(es).astype(np.int64), np.concatenate(vs).astype(np.float32))
+
+
+def assert_grad_close(got, ref, rtol=1e-5):
+    """Gradient parity: within rtol relative, with the absolute slack scaled
+    to the gradient's own magnitude (rtol/10 of its largest entry), so sums
+    that cancel are compared against the size of their terms' totals."""
+    got = np.asarray(got)
+    ref = np.asarray(ref)
+    scale = float(np.abs(ref).max()) if ref.size else 0.0
+    np.testing.assert_allclose(got, ref, rtol=rtol, atol=0.1 * rtol * max(scale, 1e-30))

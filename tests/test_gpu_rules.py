@@ -77,3 +77,34 @@ def test_rule_scores_edges():
     rules = [{"body": [2 * R], "rank_weights": [0.5]}]
     out = max_inference.score(None, src, rules, tc, R, E, 4)
     assert out.to_dense()[0, 1].item() == 1.0 and out.to_dense()[1, 2].item() == 1.0
+
+
+@pytest.mark.parametrize("reduction,boolean,final_max", [("sum", False, False), ("sum", True, False),
+                                                         ("max", True, False), ("max", True, True)])
+def test_rule_bank_c3_full_graph(reduction, boolean, final_max):
+    """1000 random rules (bodies of 1-3 operators, uniform rank weights) for
+    100 query sources on the full C3 graph (14.5k entities, 237 relations,
+    272k triples), chunk 16 as the reference's evaluation uses
+    (rules/evaluate.py:890), against the float64 oracle; a second call gives
+    the same bits (no atomics in the sums)."""
+    from flashlog_amd import synth
+    from flashlog_amd.rules import shared_inference
+    h, r, t, E, R = synth.make_graph(3)
+    csr = O.build_csr_structure(h, t, r, E)
+    rng = np.random.default_rng(2024)
+    bodies = [list(map(int, rng.integers(0, 2 * R, rng.integers(1, 4)))) for _ in range(1000)]
+    W = rng.random((len(bodies), 3)).astype(np.float32)
+    rules = [{"body": bd, "rank_weights": list(map(float, w))} for bd, w in zip(bodies, W)]
+    # sources drawn from the triples' heads, so most rules ground to something
+    sources = h[rng.integers(0, h.shape[0], 100)]
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    outs = []
+    for _ in range(2):
+        out = shared_inference.score(None, torch.from_numpy(sources).cuda(), rules, tc, R, E, 16,
+                                     final_max=final_max, reduction=reduction, boolean_paths=boolean)
+        outs.append(out.coalesce())
+    assert torch.equal(outs[0].indices(), outs[1].indices()) and torch.equal(outs[0].values(), outs[1].values())
+    want = O.rule_scores(h, r, t, E, R, list(sources), bodies, W.astype(np.float64), reduction, boolean, final_max)
+    got = outs[0].to_dense().cpu().numpy()
+    assert (want > 0).sum() > 10000
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-9)

@@ -84,6 +84,49 @@ def test_sparse_oracle_matches_reference_build(cfg, scale, K, wot_i):
     assert np.array_equal(nv.view(np.int32), rn[3].numpy().view(np.int32))
 
 
+@pytest.mark.parametrize("cfg,scale", [(1, 0.03), (2, 0.03), (3, 0.01)])
+@pytest.mark.parametrize("K", [1 << 60, 2, 200])
+@pytest.mark.parametrize("wot_i", [False, True])
+@pytest.mark.parametrize("soft", [False, True])
+def test_sparse_backward_matches_reference_build(cfg, scale, K, wot_i, soft):
+    """or_sparse_backward element by element against the reference's
+    flashlog_backward_sparse3d_sum_cpu (oracle/_ref) on one thread, fed the
+    raw metadata of its own forward: with 0/1 masks bit for bit (per entry
+    the ORI items, the INV items, then the identity term, in raw order; per
+    (row, column) the items in raw order); with fractional masks within
+    1e-6 of the largest gradient (the GPU path's (g*m)*w against the CPU
+    path's (g*w)*m)."""
+    import torch
+    ref = _ref()
+    torch.set_num_threads(1)
+    rng = np.random.default_rng(cfg * 11 + (K % 5) + 3 * wot_i + 7 * soft)
+    h, r, t, E, R, csr = small_graph(cfg, scale)
+    B, L = 3, 2
+    n = 2 * R + 1
+    b, l, e, v = sparse_coo_state(B, L, E, 25, rng, ties=K == 2)
+    w = attention(B * L, n, rng).reshape(B, L, n)
+    _, masks = masks_for(csr, h.shape[0], rng)
+    if soft:
+        masks = tuple((m * rng.uniform(0.25, 1.0, m.shape[0])).astype(np.float32) for m in masks)
+    T = lambda x: torch.from_numpy(np.ascontiguousarray(x))
+    args = (T(csr[1]), T(masks[0]), T(csr[8]), T(csr[9]), T(csr[10]), T(csr[11]), T(csr[5]), T(masks[1]),
+            T(csr[12]), T(csr[13]), T(csr[14]), T(csr[15]))
+    ro = ref.flashlog_forward_sparse3d_sum_cpu(T(b), T(l), T(e), T(v), T(w), *args, B, L, E, R, wot_i, K)
+    keys, vals = O.sparse_forward(O.SPARSE_TOPK, b, l, e, v, B, L, E, w, csr, masks, R, wot_i, K)
+    g = rng.standard_normal(keys.shape[0]).astype(np.float32)
+    g[rng.random(g.shape[0]) < 0.2] = 0.0
+    rgv, rgw = ref.flashlog_backward_sparse3d_sum_cpu(ro[0], ro[1], ro[2], T(g), T(b), T(l), T(e), T(v), T(w),
+                                                      *ro[4:16], B, L, E, R, wot_i)
+    gv, gw = O.sparse_backward(O.SPARSE_TOPK, b, l, e, v, B, L, E, w, csr, masks, R, keys, g, wot_i, K)
+    rgv, rgw = rgv.numpy(), rgw.numpy().reshape(B * L, n)
+    if soft:  # differently rounded terms: compare against the size of the sums
+        np.testing.assert_allclose(gv, rgv, rtol=1e-6, atol=1e-6 * float(np.abs(rgv).max()))
+        np.testing.assert_allclose(gw, rgw, rtol=1e-6, atol=1e-6 * float(np.abs(rgw).max()))
+    else:
+        assert np.array_equal(gv.view(np.int32), rgv.view(np.int32))
+        assert np.array_equal(gw.view(np.int32), rgw.view(np.int32))
+
+
 @pytest.mark.parametrize("mode", [O.SPARSE_TOPK, O.SPARSE_ALL])
 @pytest.mark.parametrize("K", [1 << 60, 3])
 def test_sparse_oracle_closed_form(mode, K):
