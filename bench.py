@@ -71,6 +71,24 @@ def copy_calibration(mb):
     print("copy calibration: 3 copies of %d MiB" % mb, file=sys.stderr, flush=True)
 
 
+def host_cpu():
+    """CPU model and core counts of the host the baseline runs on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"cpu_model": model, "nproc": os.cpu_count() or 1, "usable_cpus": usable}
+
+
 def c2_admitted(wv, cnt, K):
     """Edges admitted per group for one (source, row, direction) under the c2
     budget K (flashlog.cpp:12-89): groups with w > theta in full, ties at
@@ -361,7 +379,7 @@ def main_c4(args):
             if time.perf_counter() - t0 >= min(args.cpu_seconds, 5.0):
                 break
         el = time.perf_counter() - t0
-        cpu_rank = {"value": reps * Qs / el, "unit": "queries/s", "cores": 1, "kind": "port",
+        cpu_rank = {**host_cpu(), "value": reps * Qs / el, "unit": "queries/s", "cores": 1, "kind": "port",
                     "sample": "%d rankings of %d queries over %d entities (numpy restatement of src/main.py:468-512)"
                               % (reps, Qs, E)}
     cpu = cpu_baseline_c4(args, cap, csr_np, B, L, E, R, K) if args.cpu_seconds > 0 else None
@@ -424,7 +442,7 @@ def cpu_baseline_c4(args, cap, csr_np, B, L, E, R, K):
         if time.perf_counter() - t0 >= args.cpu_seconds:
             break
     el = time.perf_counter() - t0
-    return {"value": reps * Bs / el, "unit": "queries/s", "cores": 1, "kind": "port",
+    return {**host_cpu(), "value": reps * Bs / el, "unit": "queries/s", "cores": 1, "kind": "port",
             "sample": "%d x %d hops forward + backward of the dense max op for %d queries (oracle C restatement; "
                       "the reference has no CPU max path) in %.1f s, 1 thread" % (reps, len(hops), Bs, el)}
 
@@ -514,7 +532,7 @@ def main_grounding(args):
                     break
             cel = time.perf_counter() - t1
             cwalks = sum(len(f[0]) for f in folds[:nh]) * WALKS
-            cpu = {"value": n * cwalks / cel, "unit": "walks/s", "cores": threads, "kind": "reference",
+            cpu = {**host_cpu(), "value": n * cwalks / cel, "unit": "walks/s", "cores": threads, "kind": "reference",
                    "sample": "%d calls of %d heads x %d walks (soft_grounding.cpp built in oracle/_ref, OpenMP) in "
                              "%.1f s, %d threads" % (n, nh, cwalks, cel, threads)}
     result = {
@@ -608,7 +626,7 @@ def main_rules(args):
             if time.perf_counter() - t1 > args.cpu_seconds:
                 break
         dt = time.perf_counter() - t1
-        cpu = {"value": nq / dt, "unit": "queries/s", "cores": 1, "kind": "port",
+        cpu = {**host_cpu(), "value": nq / dt, "unit": "queries/s", "cores": 1, "kind": "port",
                "sample": "%d queries of the first heads (the oracle's float64 path enumeration, numpy, "
                          "1 thread; the reference's scorer is GPU-only Python) in %.1f s" % (nq, dt)}
     result = {
@@ -692,19 +710,35 @@ def main_sparse(args):
             idx[0], idx[1], idx[2], s.values(), w, *csr[:4], *csr[4:8], *csr[8:16], mask_values, None,
             B, L, E, R, False, K, False, c1, False)
 
+    def model_sum_sp_3d(s):
+        # the model file's own channel sum (src/model_DRUM_kernel_sp.py:22-28): torch's coalesce
+        s = s.coalesce()
+        idx = s.indices()
+        return torch.sparse_coo_tensor(torch.stack([idx[0], idx[2]], dim=0), s.values(),
+                                       [s.shape[0], s.shape[2]]).coalesce()
+
+    def log_loss_common_sp(p_score, label):
+        # src/utils.py:37-47 (tau_2 = 1): the target's score through a sparse one-hot product
+        i = torch.stack([torch.arange(label.shape[0], device=dev), label])
+        one_hot = torch.sparse_coo_tensor(i, torch.ones(label.shape[0], device=dev), [label.shape[0], E])
+        logits = torch.sparse.sum(p_score * one_hot, dim=-1).to_dense()
+        return -torch.mean(torch.log(torch.maximum(logits, torch.ones_like(logits) * 1e-7)), dim=-1)
+
+    tgt_t = torch.from_numpy(tgt).to(dev)
+    native_sum = [False]
+
     def step():
+        # src/model_DRUM_kernel_sp.py:132-205 per hop: the hop, normalize_sparse3d, dropout (training)
         s = state0
         for t_ in range(T):
             s = fk.normalize_sparse3d(hop(s, Wl[t_]))
-        final = fk.sum_sp_3d(s)  # src/model_DRUM_kernel_sp.py:204 (sum_sp_3d, :22-28)
+            if train:
+                s = torch.sparse_coo_tensor(s.indices(), torch.nn.functional.dropout(s.values(), 0.1, True),
+                                            s.shape, is_coalesced=True)
+        final = fk.sum_sp_3d(s) if native_sum[0] else model_sum_sp_3d(s)
         if not train:
             return final
-        # log loss on each query's target entity (src/utils.py:37-47, tau_2 = 1)
-        fi = final.indices()
-        keys = fi[0] * E + fi[1]
-        pos = torch.searchsorted(keys, tgt_key).clamp(max=max(keys.numel() - 1, 0))
-        logit = torch.where(keys[pos] == tgt_key, final.values()[pos], torch.zeros((), device=dev))
-        loss = -torch.log(torch.clamp(logit, min=1e-7)).mean()
+        loss = log_loss_common_sp(final, tgt_t)
         Wl.grad = None
         loss.backward()
         return loss
@@ -726,6 +760,20 @@ def main_sparse(args):
         ms_step = e_0.elapsed_time(e_1) / args.steps
         print("timed %d %s steps: %.3f ms/step (host wall %.3f ms/step)"
               % (args.steps, args.mode, ms_step, 1e3 * wall / args.steps), file=sys.stderr, flush=True)
+        # the same steps with this library's channel sum (flashlog_kernel.sum_sp_3d) in place of
+        # the model file's torch coalesce: what a model that imports it would run
+        native_sum[0] = True
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        e_0.record()
+        for _ in range(args.steps):
+            step()
+        e_1.record()
+        torch.cuda.synchronize()
+        ms_step_native = e_0.elapsed_time(e_1) / args.steps
+        native_sum[0] = False
+        print("with flashlog_kernel.sum_sp_3d: %.3f ms/step" % ms_step_native, file=sys.stderr, flush=True)
         _lib.prof_enable(True)
         for _ in range(args.profile_steps):
             step()
@@ -769,6 +817,8 @@ def main_sparse(args):
                    % (cfg.name, args.mode, "forward + backward" if train else "forward", E, R, M, B, L, T,
                       c1, cfg.c2),
                    "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2, "mode": args.mode},
+        "channel_sum": "the model file's torch sum_sp_3d (src/model_DRUM_kernel_sp.py:22-28)",
+        "ms_per_step_native_channel_sum": ms_step_native,
         "topk_select_ms": {"c1_per_hop": per_launch["k_race_select"] if train else per_launch["k_sp_topc"],
                            "c2_per_hop": per_launch["k_sp_select"]},
         "kernel_ms_per_launch": per_launch,
@@ -880,7 +930,7 @@ def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W, T, train):
             break
     el = time.perf_counter() - t0
     what = "forward + backward" if train else "forward"
-    return {"value": steps * Bs / el, "unit": "queries/s", "cores": threads, "kind": "reference",
+    return {**host_cpu(), "value": steps * Bs / el, "unit": "queries/s", "cores": threads, "kind": "reference",
             "sample": "%d full %s steps of %d queries x %d hops (first %d queries of the batch; deterministic "
                       "c1/c2 selections) in %.1f s, %d threads" % (steps, what, Bs, T, Bs, el, threads)}
 
@@ -949,7 +999,7 @@ def cpu_baseline(args, cfg, h, r, t, E, R, src, W):
         if time.perf_counter() - t0 >= args.cpu_seconds:
             break
     el = time.perf_counter() - t0
-    return {"value": steps * B / el, "unit": "queries/s", "cores": 1, "kind": kind,
+    return {**host_cpu(), "value": steps * B / el, "unit": "queries/s", "cores": 1, "kind": kind,
             "sample": "%d full steps (%d queries x %d hops) in %.1f s, 1 thread" % (steps, B, T, el)}
 
 
