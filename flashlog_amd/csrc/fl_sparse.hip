@@ -2297,6 +2297,11 @@ __global__ void k_sp_gather(const int64_t *__restrict__ gb, const int64_t *__res
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nq) return;
     const int64_t key = (qb[i] * L + ql[i]) * E + qe[i];
+    // the usual case: the same coordinates in the same order
+    if (i < ng && (gb[i] * L + gl[i]) * E + ge[i] == key) {
+        out[i] = gv[i];
+        return;
+    }
     int64_t lo = 0, hi = ng;
     while (lo < hi) {
         const int64_t mid = lo + ((hi - lo) >> 1);

@@ -1422,22 +1422,16 @@ class Sparse3DNormalizeFunction(autograd.Function):
         sp_entity = sp_entity.contiguous().long()
         values = sp_value.contiguous()
         out, denom, row_ptr = _normalize_forward(sp_batch, sp_level, values, int(B), int(L), float(eps))
-        ctx.save_for_backward(sp_batch, sp_level, sp_entity, values.float(), denom, row_ptr)
-        ctx.B, ctx.L, ctx.E, ctx.eps = int(B), int(L), int(E), float(eps)
         idx = torch.stack([sp_batch, sp_level, sp_entity], dim=0)
+        ctx.save_for_backward(idx, values.float(), denom, row_ptr)
+        ctx.B, ctx.L, ctx.E, ctx.eps = int(B), int(L), int(E), float(eps)
         return torch.sparse_coo_tensor(idx, out.to(sp_value.dtype), [int(B), int(L), int(E)], is_coalesced=True)
 
     @staticmethod
     def backward(ctx, grad_out):
-        sp_batch, sp_level, sp_entity, values, denom, row_ptr = ctx.saved_tensors
-        if getattr(grad_out, "is_sparse", False):
-            if _same_index_rows(grad_out._indices(), [sp_batch, sp_level, sp_entity]):
-                g = grad_out._values().contiguous()
-            else:
-                g = _grad_at_outputs(grad_out, torch.stack([sp_batch, sp_level, sp_entity]), ctx.L,
-                                                 ctx.E)
-        else:
-            g = grad_out[sp_batch, sp_level, sp_entity]
+        idx, values, denom, row_ptr = ctx.saved_tensors
+        # the output's own index tensor: a gradient built on it needs no lookup
+        g = _grad_at_outputs(grad_out, idx, ctx.L, ctx.E)
         gv = _normalize_backward(row_ptr, g, values, denom, ctx.eps)
         return None, None, None, gv, None, None, None, None
 
