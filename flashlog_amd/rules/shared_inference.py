@@ -1,7 +1,7 @@
 """Shared grounding for SUM and MAX rule inference (rules/shared_inference.py:
 12-245): every rule body (at most a few operators) is grounded from every
-source with the fixed-relation step of flashlog_kernel, and the grounded
-endpoints are scored per rank.
+source with the fixed-relation step, and the grounded endpoints are scored
+per rank.
 
 For sources s_b, rules r with operator bodies and rank weights W[r, k] >= 0:
   reduction='sum':  S_k[b, e] = sum_r W[r, k] * C_r(b, e)
@@ -13,16 +13,23 @@ its sum (clamped to 1e-30) and the ranks are summed (or maxed with
 final_max) into one score per (b, e); the result is a coalesced sparse
 [B, entities] tensor of the positive scores.
 
-Execution: chunks of ``chunk_size`` rules are grounded for a block of sources
-at once (one fixed-relation launch sequence per body step); the grounded
-states are added into a dense [ranks, sources x entities] accumulator by
-fl_rule_accumulate and finalized by fl_rule_finalize.  Sources are taken in
-blocks sized so that the accumulator fits ``dense_budget_bytes``.  The
-reference's prefix cache, source splits and sparse accumulators change only
-the order of floating-point additions, not what is computed.
+Execution: the grounding calls go through ``ev`` (the evaluate module: the
+reference's, or this package's flashlog_amd.rules.evaluate when ``ev`` is
+None): ev.initial_rule_state and ev.vectorized_operation_sparse3d_fixed_relation,
+with ev.advance_single_rule_state_memory_bounded after an out-of-memory
+step of one source and one rule.  A chunk whose grounding runs out of
+memory is retried with half as many rules (stats["oom_retries"]), down to
+one rule.  Grounded chunks are added into a dense [ranks, sources x
+entities] accumulator by fl_rule_accumulate (sums: per (source, entity) the
+chunk's rules in rule order, chunks in order; maxima: exact) and finalized
+by fl_rule_finalize.  Sources are taken in blocks sized so that the
+accumulator fits ``dense_budget_bytes``; as in the reference, a batch whose
+first hop would expand a frontier beyond ``source_frontier_budget_bytes`` is
+scored one source at a time.  The reference's prefix cache, source splits
+and sparse accumulators change only how the exact integer path counts are
+produced or the order of floating-point additions of the normalizers, not
+the values of the channel sums.
 """
-import ctypes  # noqa: F401  (ctypes types are used through _lib)
-
 import torch
 
 from .. import _lib
@@ -35,21 +42,51 @@ def _empty(shape, device):
                                    torch.empty(0, device=device), shape, is_coalesced=True)
 
 
-def _available_first_ops(sources, csr, relations):
-    """Operators that leave at least one source through an edge (plus the
-    identity): rules starting elsewhere ground to nothing
-    (shared_inference.py:34-47)."""
+def _first_degrees(sources, csr, relations):
+    """[(operator, group size)] of every first-hop group of the sources
+    (forward groups as their relation, inverse ones offset by relations)."""
     positions = torch.stack((sources, sources + 1), dim=1).reshape(-1)
     bounds = torch.stack((csr[8][positions], csr[12][positions])).cpu().tolist()
-    available = {2 * relations}
-    for direction, (ri, ci) in enumerate(((9, 11), (13, 15))):
+    degrees = []
+    for side, (ri, ci) in enumerate(((9, 11), (13, 15))):
         for i in range(sources.numel()):
-            start, end = bounds[direction][2 * i:2 * i + 2]
-            if end > start:
-                rels = (csr[ri][start:end].long() + direction * relations).tolist()
-                cnts = csr[ci][start:end].tolist()
-                available.update(rel for rel, c in zip(rels, cnts) if c > 0)
-    return available
+            lo, hi = bounds[side][2 * i:2 * i + 2]
+            if hi > lo:
+                ops = (csr[ri][lo:hi].long() + side * relations).tolist()
+                degrees.extend(zip(ops, csr[ci][lo:hi].tolist()))
+    return degrees
+
+
+def _default_ev():
+    from . import evaluate
+    return evaluate
+
+
+def _accumulate_chunk(state, W, dense, is_max, nb, E):
+    """dense [ranks, nb*E] += (max=) the chunk state's weighted rule sums."""
+    if state._nnz() == 0:
+        return
+    ix = state.indices()
+    vals = state.values().float().contiguous()
+    C = state.shape[1]
+    lib = _lib.lib()
+    ws_bytes = lib.fl_rule_accumulate_bytes(vals.numel(), nb, C)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=vals.device)
+    check(lib.fl_rule_accumulate(fk._stream(vals), ptr(ix[0].contiguous()), ptr(ix[1].contiguous()),
+                                 ptr(ix[2].contiguous()), ptr(vals), vals.numel(), ptr(W.contiguous()), W.shape[1],
+                                 nb, C, E, 1 if is_max else 0, ptr(dense), ptr(ws), ws_bytes),
+          "rule_accumulate")
+
+
+def _finalize(dense, nb, E, final_max):
+    """(flat keys, scores) of the block: rows normalized, ranks combined."""
+    ranks = dense.shape[0]
+    rowsum = torch.empty(ranks * nb, dtype=torch.float32, device=dense.device)
+    total = torch.empty(nb * E, dtype=torch.float32, device=dense.device)
+    check(_lib.lib().fl_rule_finalize(fk._stream(dense), ptr(dense), ranks, nb, E, 1 if final_max else 0,
+                                      ptr(rowsum), ptr(total)), "rule_finalize")
+    keys = total.nonzero().flatten()
+    return keys, total[keys]
 
 
 @torch.inference_mode()
@@ -57,30 +94,53 @@ def score(ev, sources, rules, csr, relations, entities, chunk_size,
           final_max=False, reduction="sum", boolean_paths=False, dense_budget_bytes=None,
           prefix_budget_bytes=512 * 1024**2, stats=None,
           source_frontier_budget_bytes=64 * 1024**2):
-    """Signature of rules/shared_inference.py:12-15.  ``ev`` (the reference's
-    evaluate module) is accepted for compatibility; grounding and reduction
-    run on this build's kernels."""
+    """Signature of rules/shared_inference.py:12-15."""
     if reduction not in ("sum", "max"):
         raise ValueError("Unknown reduction")
     boolean_paths = boolean_paths or reduction == "max"
     if chunk_size < 1:
         raise ValueError("chunk_size must be positive")
+    ev = ev if ev is not None else _default_ev()
     stats = {} if stats is None else stats
     for name in ("ground_calls", "prefix_hits", "chunks", "oom_retries"):
         stats.setdefault(name, 0)
     sources = sources.reshape(-1).long()
     device = sources.device
     batch = sources.numel()
-    shape = (batch, int(entities))
+    E = int(entities)
+    shape = (batch, E)
     if not rules:
         return _empty(shape, device)
+    all_rules = rules
     stats["rules_before"] = len(rules)
+    degrees = _first_degrees(sources, csr, relations) if len(csr) >= 16 and batch > 0 else []
     if len(csr) >= 16 and batch > 0:
-        available = _available_first_ops(sources, csr, relations)
+        available = {op for op, cnt in degrees if cnt > 0} | {2 * relations}
         rules = [r for r in rules if not r["body"] or r["body"][0] in available]
     stats["rules_after"] = len(rules)
     if not rules or batch == 0:
         return _empty(shape, device)
+    # the first hop's frontier per rule chunk (28 B per COO entry)
+    first_ops = {}
+    for r in rules:
+        if r["body"]:
+            first_ops[r["body"][0]] = first_ops.get(r["body"][0], 0) + 1
+    max_first = max((cnt for op, cnt in degrees if op in first_ops), default=0)
+    stats["first_frontier_bytes"] = max((cnt * min(chunk_size, first_ops.get(op, 0)) * 28 for op, cnt in degrees),
+                                        default=0)
+    if batch > 1 and max_first * 28 > source_frontier_budget_bytes:
+        stats["source_splits"] = stats.get("source_splits", 0) + 1
+        rows_out, cols_out, vals_out = [], [], []
+        for b in range(batch):
+            part = score(ev, sources[b:b + 1], all_rules, csr, relations, entities, chunk_size,
+                         final_max=final_max, reduction=reduction, boolean_paths=boolean_paths,
+                         dense_budget_bytes=dense_budget_bytes, prefix_budget_bytes=prefix_budget_bytes,
+                         stats=stats, source_frontier_budget_bytes=source_frontier_budget_bytes).coalesce()
+            rows_out.append(part.indices()[0] + b)
+            cols_out.append(part.indices()[1])
+            vals_out.append(part.values())
+        return torch.sparse_coo_tensor(torch.stack((torch.cat(rows_out), torch.cat(cols_out))), torch.cat(vals_out),
+                                       shape, is_coalesced=True)
     widths = {len(r["rank_weights"]) for r in rules}
     if len(widths) != 1 or next(iter(widths)) < 1:
         raise ValueError("nonempty rank_weights must have matching widths")
@@ -89,59 +149,69 @@ def score(ev, sources, rules, csr, relations, entities, chunk_size,
     if not bool(torch.isfinite(weights).all()) or bool((weights < 0).any()):
         raise ValueError("MAX rule weights must be finite and nonnegative")
     identity = 2 * relations
+    steps = max(len(r["body"]) for r in rules)
+    operators = torch.tensor([tuple(r["body"]) + (identity,) * (steps - len(r["body"])) for r in rules],
+                             dtype=torch.long, device=device).reshape(len(rules), max(steps, 1))
     lengths = [len(r["body"]) for r in rules]
-    max_steps = max(lengths)
-    operators = torch.tensor([list(r["body"]) + [identity] * (max_steps - len(r["body"])) for r in rules],
-                             dtype=torch.long, device=device).reshape(len(rules), max(max_steps, 1))
-    E = int(entities)
     if dense_budget_bytes is None:
         free = torch.cuda.mem_get_info(device)[0] if device.type == "cuda" else 256 * 1024**2
         dense_budget_bytes = max(free // 3, ranks * E * 4)
     block = max(1, min(batch, int(dense_budget_bytes) // max(1, ranks * E * 4)))
     stats["dense_accumulation"] = True
-    lib = _lib.lib()
-    st = fk._stream(sources)
-    is_max = 1 if reduction == "max" else 0
-    rows_out, cols_out, vals_out = [], [], []
+    stats["prefix_enabled"] = False
+    is_max = reduction == "max"
+
+    def advance(state, ops, nb):
+        stats["ground_calls"] += 1
+        try:
+            out = ev.vectorized_operation_sparse3d_fixed_relation(state, ops, csr, relations)
+        except torch.cuda.OutOfMemoryError:
+            if nb != 1 or state.shape[1] != 1:
+                raise
+            torch.cuda.empty_cache()
+            out = ev.advance_single_rule_state_memory_bounded(state, ops, csr, relations)
+        out = out.coalesce()
+        if boolean_paths:
+            # several paths are one piece of Boolean evidence, not a multiplicity
+            out = torch.sparse_coo_tensor(out.indices(), (out.values() > 0).to(out.dtype), out.shape,
+                                          is_coalesced=True)
+        return out
+
+    def ground(src, lo, hi):
+        nb = src.numel()
+        state = ev.initial_rule_state(src, hi - lo, E)
+        ops = operators[lo:hi]
+        for step in range(max(lengths[lo:hi])):
+            if state._nnz() == 0:
+                break
+            state = advance(state, ops[:, step].unsqueeze(0).expand(nb, -1), nb)
+        return state
+
+    keys_out, vals_out = [], []
     for s0 in range(0, batch, block):
         src = sources[s0:s0 + block]
         nb = src.numel()
         dense = torch.zeros((ranks, nb * E), dtype=torch.float32, device=device)
-        for off in range(0, len(rules), chunk_size):
-            C = min(chunk_size, len(rules) - off)
-            b = torch.arange(nb, device=device).repeat_interleave(C)
-            l = torch.arange(C, device=device).repeat(nb)
-            e = src.repeat_interleave(C)
-            state = torch.sparse_coo_tensor(torch.stack((b, l, e)), torch.ones(nb * C, device=device),
-                                            (nb, C, E), is_coalesced=True)
-            steps = max(lengths[off:off + C])
-            ops = operators[off:off + C]
-            for step in range(steps):
-                if state._nnz() == 0:
-                    break
-                stats["ground_calls"] += 1
-                state = fk.vectorized_operation_sparse3d_fixed_relation(
-                    state, ops[:, step].unsqueeze(0).expand(nb, -1), csr, relations)
-                if boolean_paths:
-                    state = torch.sparse_coo_tensor(state.indices(), (state.values() > 0).float(), state.shape,
-                                                    is_coalesced=True)
-            if state._nnz():
-                ix = state.indices()
-                vals = state.values().float().contiguous()
-                w = weights[off:off + C].contiguous()
-                ws_bytes = lib.fl_rule_accumulate_bytes(vals.numel(), nb, C)
-                ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
-                check(lib.fl_rule_accumulate(st, ptr(ix[0].contiguous()), ptr(ix[1].contiguous()),
-                                             ptr(ix[2].contiguous()), ptr(vals), vals.numel(), ptr(w), ranks, nb,
-                                             C, E, is_max, ptr(dense), ptr(ws), ws_bytes), "rule_accumulate")
+        off, size = 0, chunk_size
+        while off < len(rules):
+            hi = min(off + size, len(rules))
+            try:
+                state = ground(src, off, hi)
+            except torch.cuda.OutOfMemoryError:
+                state = None
+                torch.cuda.empty_cache()
+                stats["oom_retries"] += 1
+                if size == 1:
+                    raise torch.cuda.OutOfMemoryError("MAX grounding needs a smaller query batch")
+                size = max(1, size // 2)
+                continue
+            _accumulate_chunk(state, weights[off:hi], dense, is_max, nb, E)
+            off = hi
             stats["chunks"] += 1
-        rowsum = torch.empty(ranks * nb, dtype=torch.float32, device=device)
-        total = torch.empty(nb * E, dtype=torch.float32, device=device)
-        check(lib.fl_rule_finalize(st, ptr(dense), ranks, nb, E, 1 if final_max else 0, ptr(rowsum), ptr(total)),
-              "rule_finalize")
-        keys = total.nonzero().flatten()
-        rows_out.append(keys // E + s0)
-        cols_out.append(keys % E)
-        vals_out.append(total[keys])
-    indices = torch.stack((torch.cat(rows_out), torch.cat(cols_out)))
-    return torch.sparse_coo_tensor(indices, torch.cat(vals_out), shape, is_coalesced=True)
+        keys, vals = _finalize(dense, nb, E, final_max)
+        keys_out.append(keys + s0 * E)
+        vals_out.append(vals)
+        del dense
+    keys = torch.cat(keys_out)
+    return torch.sparse_coo_tensor(torch.stack((keys // E, keys % E)), torch.cat(vals_out), shape,
+                                   is_coalesced=True)

@@ -586,20 +586,16 @@ def fixed_relation_step(b, l, e, v, ops, h, r, t, E, R):
     return out
 
 
-def rule_scores(h, r, t, E, R, sources, bodies, W, reduction="sum", boolean_paths=False, final_max=False):
-    """Dense [B, E] float64 scores: per rule the path-count vectors
-    e_s^T M_op1 M_op2 ... of every source at once (sparse [E, B] columns;
-    Boolean after every step when boolean_paths or max), per rank the
-    weighted sum (or max) over rules, each (rank, source) row divided by
-    max(its sum, 1e-30), ranks summed (or maxed)."""
+def rule_path_counts(h, r, t, E, R, sources, bodies, boolean_paths=False):
+    """Per rule body, the path counts of every source as a sparse [E, B]
+    float64 matrix (column b: e_{s_b}^T M_op1 M_op2 ...; Boolean after every
+    step when boolean_paths)."""
     import scipy.sparse as sp
-    boolean_paths = boolean_paths or reduction == "max"
-    W = np.asarray(W, np.float64)
     mats = {}
-    B, K = len(sources), W.shape[1]
+    B = len(sources)
     start = sp.csc_matrix((np.ones(B), (np.asarray(sources, np.int64), np.arange(B))), shape=(E, B))
-    S = np.zeros((K, E, B))
-    for ri, body in enumerate(bodies):
+    out = []
+    for body in bodies:
         x = start
         for op in body:
             if op not in mats:
@@ -608,7 +604,20 @@ def rule_scores(h, r, t, E, R, sources, bodies, W, reduction="sum", boolean_path
             if boolean_paths:
                 x.data = (x.data > 0).astype(np.float64)
                 x.eliminate_zeros()
-        x = x.tocoo()
+        out.append(x.tocoo())
+    return out
+
+
+def rule_scores(h, r, t, E, R, sources, bodies, W, reduction="sum", boolean_paths=False, final_max=False):
+    """Dense [B, E] float64 scores: per rule the path-count vectors of every
+    source (rule_path_counts; Boolean when boolean_paths or max), per rank the
+    weighted sum (or max) over rules, each (rank, source) row divided by
+    max(its sum, 1e-30), ranks summed (or maxed)."""
+    boolean_paths = boolean_paths or reduction == "max"
+    W = np.asarray(W, np.float64)
+    B, K = len(sources), W.shape[1]
+    S = np.zeros((K, E, B))
+    for ri, x in enumerate(rule_path_counts(h, r, t, E, R, sources, bodies, boolean_paths)):
         for k in range(K):
             if reduction == "max":
                 np.maximum.at(S[k], (x.row, x.col), W[ri, k] * (x.data > 0))
@@ -621,6 +630,46 @@ def rule_scores(h, r, t, E, R, sources, bodies, W, reduction="sum", boolean_path
         part = Sk / d
         total = np.maximum(total, part) if final_max else total + part
     return total
+
+
+def rule_batch_scores(h, r, t, E, R, sources, rules, aggregation):
+    """The DRUM scorer's aggregations (rules/evaluate.py:554-734) as dense
+    [B, E] float64 arrays plus the Boolean set of reached (source, entity)
+    pairs: weighted_path_count / weighted_boolean (sum_r w_r C_r or
+    [C_r > 0]), max_confidence (max_r w_r over C_r > 0), rank_normalized /
+    rank_boolean_normalized (per rank the positive terms rw_r[k] C_r, rows
+    normalized, ranks summed), routed_normalized (the same over the routed
+    groups with w_r)."""
+    boolean = aggregation in ("weighted_boolean", "rank_boolean_normalized", "max_confidence")
+    B = len(sources)
+    counts = rule_path_counts(h, r, t, E, R, sources, [list(x["body"]) for x in rules], boolean)
+    reached = np.zeros((B, E), bool)
+    for x in counts:
+        reached[x.col, x.row] = True
+    if aggregation in ("weighted_path_count", "weighted_boolean", "max_confidence"):
+        S = np.full((B, E), -np.inf) if aggregation == "max_confidence" else np.zeros((B, E))
+        for rule, x in zip(rules, counts):
+            w = float(rule["weight"])
+            if aggregation == "max_confidence":
+                np.maximum.at(S, (x.col, x.row), w * (x.data > 0))
+            else:
+                np.add.at(S, (x.col, x.row), w * x.data)
+        return np.where(reached, S, 0.0), reached
+    if aggregation == "routed_normalized":
+        G = 1 + max(x["group_id"] for x in rules)
+        chan = np.zeros((len(rules), G))
+        for i, rule in enumerate(rules):
+            chan[i, rule["group_id"]] = max(float(rule["weight"]), 0.0)
+    else:
+        chan = np.maximum(np.asarray([x["rank_weights"] for x in rules], np.float64), 0.0)
+    S = np.zeros((chan.shape[1], B, E))
+    for i, x in enumerate(counts):
+        for k in range(chan.shape[1]):
+            np.add.at(S[k], (x.col, x.row), chan[i, k] * x.data)
+    total = np.zeros((B, E))
+    for k in range(chan.shape[1]):
+        total += S[k] / np.maximum(S[k].sum(1, keepdims=True), 1e-30)
+    return total, total > 0
 
 
 def rule_paths_brute(h, r, t, R, source, body):

@@ -62,3 +62,53 @@ def test_score_modes_direct_loop():
                 per_rank.append(row / max(row.sum(), 1e-30))
             want[bi] = np.max(per_rank, 0) if fmax else np.sum(per_rank, 0)
         np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-15)
+
+
+def test_rule_batch_scores_direct_loop():
+    """The DRUM scorer's aggregations against explicit path enumeration."""
+    rng, E, R, h, r, t = _tiny(3)
+    rules = []
+    for i in range(9):
+        body = tuple(int(x) for x in rng.integers(0, 2 * R + 1, rng.integers(1, 4)))
+        rules.append({"body": body, "weight": float(rng.choice([0.0, 0.25, 0.5, 1.5])),
+                      "rank_weights": tuple(float(x) for x in rng.choice([0.0, 0.3, 0.7], 3)),
+                      "group_id": int(rng.integers(0, 3))})
+    sources = [1, 5, 7]
+    for agg in ("weighted_path_count", "weighted_boolean", "max_confidence", "rank_normalized",
+                "rank_boolean_normalized", "routed_normalized"):
+        got, reached = O.rule_batch_scores(h, r, t, E, R, sources, rules, agg)
+        boolean = agg in ("weighted_boolean", "rank_boolean_normalized", "max_confidence")
+        want = np.zeros((len(sources), E))
+        want_reached = np.zeros((len(sources), E), bool)
+        for bi, s in enumerate(sources):
+            paths = [O.rule_paths_brute(h, r, t, R, s, list(rule["body"])) for rule in rules]
+            for c in paths:
+                for node, cnt in c.items():
+                    if cnt > 0:
+                        want_reached[bi, node] = True
+            if agg in ("weighted_path_count", "weighted_boolean", "max_confidence"):
+                best = {}
+                for rule, c in zip(rules, paths):
+                    for node, cnt in c.items():
+                        if cnt <= 0:
+                            continue
+                        val = rule["weight"] * (1.0 if boolean else cnt)
+                        best[node] = max(best.get(node, -np.inf), val) if agg == "max_confidence" \
+                            else best.get(node, 0.0) + val
+                for node, val in best.items():
+                    want[bi, node] = val
+            else:
+                for k in range(3):  # 3 ranks, or the 3 routed groups
+                    row = np.zeros(E)
+                    for rule, c in zip(rules, paths):
+                        if agg == "routed_normalized":
+                            wk = max(rule["weight"], 0.0) if rule["group_id"] == k else 0.0
+                        else:
+                            wk = max(rule["rank_weights"][k], 0.0)
+                        for node, cnt in c.items():
+                            if cnt > 0:
+                                row[node] += wk * (1.0 if boolean else cnt)
+                    want[bi] += row / max(row.sum(), 1e-30)
+        np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-15, err_msg=agg)
+        if agg in ("weighted_path_count", "weighted_boolean", "max_confidence"):
+            assert np.array_equal(reached, want_reached), agg
