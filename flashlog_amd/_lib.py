@@ -91,6 +91,9 @@ _SIGS = {
     "fl_ground_graph_bytes": (ctypes.c_size_t, []),
     "fl_csr_build_side": (ctypes.c_int, [ctypes.c_int64, ctypes.c_int64] + [ctypes.c_void_p] * 11 +
                           [ctypes.POINTER(ctypes.c_int64)]),
+    "fl_csr_build_side_gpu_bytes": (ctypes.c_size_t, [ctypes.c_int64, ctypes.c_int64]),
+    "fl_csr_build_side_gpu": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64] + [ctypes.c_void_p] * 13 +
+                              [ctypes.c_size_t]),
     "fl_pull_index_build": (ctypes.c_int, [ctypes.c_int64] * 3 + [ctypes.c_void_p] * 9),
     "fl_pull_segments": (ctypes.c_int, [ctypes.c_int64, ctypes.c_void_p] + [ctypes.POINTER(ctypes.c_int64)] * 3 +
                          [ctypes.c_void_p] * 8),

@@ -132,12 +132,50 @@ def _build_group_metadata(sorted_rows, sorted_rels, num_nodes, row_ptr=None):
     return group_ptr, relations, starts, counts
 
 
+def _build_csr_structure_gpu(row, col, rel, nodes):
+    if not (row.dim() == col.dim() == rel.dim() == 1) or not (row.numel() == col.numel() == rel.numel()):
+        raise ValueError("CSR requires equal 1D arrays and int32-sized graph")
+    dev = row.device
+    row, col, rel = (x.to(torch.int64).contiguous() for x in (row, col, rel))
+    m = row.numel()
+    lib = _lib.lib()
+    ws_bytes = lib.fl_csr_build_side_gpu_bytes(m, nodes)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    st = _stream(row)
+    info = torch.empty(2, dtype=torch.int64, device=dev)
+
+    def side(source, target):
+        row_ptr = torch.empty(nodes + 1, dtype=torch.int32, device=dev)
+        cols = torch.empty(m, dtype=torch.int32, device=dev)
+        erel = torch.empty(m, dtype=torch.int16, device=dev)
+        order = torch.empty(m, dtype=torch.int32, device=dev)
+        gptr = torch.empty(nodes + 1, dtype=torch.int32, device=dev)
+        grel = torch.empty(max(m, 1), dtype=torch.int16, device=dev)
+        gstart = torch.empty(max(m, 1), dtype=torch.int32, device=dev)
+        gcount = torch.empty(max(m, 1), dtype=torch.int32, device=dev)
+        check(lib.fl_csr_build_side_gpu(st, m, nodes, ptr(source), ptr(target), ptr(rel), ptr(row_ptr), ptr(cols),
+                                        ptr(erel), ptr(order), ptr(gptr), ptr(grel), ptr(gstart), ptr(gcount),
+                                        ptr(info), ptr(ws), ws_bytes), "csr_build_side_gpu")
+        g, err = info.tolist()
+        if err:
+            raise ValueError("CSR entity or relation ID outside supported range")
+        return (row_ptr, cols, erel, order, gptr, grel[:g].clone(), gstart[:g].clone(), gcount[:g].clone())
+
+    ori = side(row, col)
+    inv = side(col, row)
+    return (*ori[:4], *inv[:4], *ori[4:], *inv[4:])
+
+
 def build_csr_structure(row_indices, col_indices, r_indices, num_nodes):
     """The reference's 16-tuple (flashlog_kernel.py:678-697; csr.cpp:12-69):
     (ori_row_ptr, ori_col_ind, ori_r_ind, order_ori, inv_..., ori_row_group_ptr,
-    ori_group_rel, ori_group_edge_start, ori_group_edge_count, inv_...),
-    built by the library's host CSR builder and moved to the input's device."""
+    ori_group_rel, ori_group_edge_start, ori_group_edge_count, inv_...).
+    Inputs on a GPU are built there (fl_csr_build_side_gpu, one radix sort
+    per side); CPU inputs by the library's host builder.  Both give the
+    reference's arrays bit for bit, on the input's device."""
     device = row_indices.device
+    if device.type == "cuda":
+        return _build_csr_structure_gpu(row_indices, col_indices, r_indices, int(num_nodes))
     row, col, rel = [x.detach().to(device="cpu", dtype=torch.int64).contiguous()
                      for x in (row_indices, col_indices, r_indices)]
     if not (row.dim() == col.dim() == rel.dim() == 1) or not (row.numel() == col.numel() == rel.numel()):

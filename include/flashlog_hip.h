@@ -95,6 +95,23 @@ size_t fl_ground_graph_bytes(void);
 
 /* ---- host-side graph preparation ------------------------------------- */
 
+/* Replaces csr.cpp:12-69 (build_side) on the GPU: the same arrays as
+ * fl_csr_build_side (positions ordered by (source, relation, edge id),
+ * groups the runs of equal (source, relation)) from device arrays, by one
+ * stable radix sort of (source << 15 | relation) carrying the edge ids.
+ * Group arrays need capacity >= edges; info (device int64[2]) receives
+ * {number of groups, error} (error 1: an entity outside [0, nodes) or a
+ * relation outside [0, 32767]); workspace of fl_csr_build_side_gpu_bytes. */
+size_t fl_csr_build_side_gpu_bytes(int64_t edges, int64_t nodes);
+int fl_csr_build_side_gpu(void *stream, int64_t edges, int64_t nodes,
+                          const int64_t *source, const int64_t *target,
+                          const int64_t *relation, int32_t *row_ptr,
+                          int32_t *columns, int16_t *edge_rel, int32_t *order,
+                          int32_t *group_ptr, int16_t *group_rel,
+                          int32_t *group_start, int32_t *group_count,
+                          int64_t *info, void *workspace,
+                          size_t workspace_bytes);
+
 /* Replaces csr.cpp:12-69 (build_side), called by build_csr_structure
  * (flashlog_kernel.py:678-697).  Host arrays.  Positions are ordered by
  * (source, relation, edge id); group arrays need capacity >= edges. */
