@@ -14,8 +14,9 @@ def install(rules=False):
     """Alias ``flashlog_kernel``, ``flashlog_kernel.flashlog_kernel`` and
     ``flashlog_kernel.soft_grounding_kernel[.soft_grounding_kernel]`` to this
     package's mirrors (drop-in replacement of the reference package).
-    rules=True also redirects ``rules.shared_inference`` and
-    ``rules.max_inference`` (their ``score`` entry points) to the GPU
+    rules=True also redirects ``rules.shared_inference``,
+    ``rules.max_inference`` (their ``score`` entry points) and
+    ``rules.evaluate`` (the rule-evaluation primitives and scorer) to the GPU
     rule-bank scoring, leaving the rest of a ``rules`` package alone."""
     from . import flashlog_kernel as pkg
     from .flashlog_kernel import flashlog_kernel as mod
@@ -26,10 +27,11 @@ def install(rules=False):
     sys.modules["flashlog_kernel.soft_grounding_kernel"] = sg
     sys.modules["flashlog_kernel.soft_grounding_kernel.soft_grounding_kernel"] = sgm
     if rules:
-        from .rules import max_inference as mi, shared_inference as si
+        from .rules import evaluate as evm, max_inference as mi, shared_inference as si
         sys.modules["rules.shared_inference"] = si
         sys.modules["rules.max_inference"] = mi
+        sys.modules["rules.evaluate"] = evm
         parent = sys.modules.get("rules")
         if parent is not None:
-            parent.shared_inference, parent.max_inference = si, mi
+            parent.shared_inference, parent.max_inference, parent.evaluate = si, mi, evm
     return pkg

@@ -185,6 +185,14 @@ _SIGS = {
                                                   ctypes.c_size_t]),
     "fl_filtered_ranks_noalloc": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int] + [ctypes.c_void_p] * 2 +
                                   [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_void_p]),
+    "fl_filter_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
+    "fl_filter_expand_count": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p,
+                                                                     ctypes.c_int64, ctypes.c_int64,
+                                                                     ctypes.c_void_p, ctypes.c_void_p,
+                                                                     ctypes.c_size_t]),
+    "fl_filter_expand_fill": (ctypes.c_int, [ctypes.c_void_p] * 3 + [ctypes.c_int64, ctypes.c_void_p,
+                                                                    ctypes.c_void_p, ctypes.c_int64] +
+                              [ctypes.c_void_p] * 3),
     "fl_prof_enable": (ctypes.c_int, [ctypes.c_int]),
     "fl_prof_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_int64)]),

@@ -18,6 +18,7 @@
 
 #include "fl_common.h"
 #include "fl_abi.h"
+#include "fl_scan.h"
 
 namespace fl {
 
@@ -340,6 +341,102 @@ int fl_dense_filtered_ranks(void *stream, const float *state, const int64_t *tar
     FL_LAUNCH("k_dense_rank", fl::k_dense_rank, dim3((unsigned)B), dim3(fl::DR_NT), 0, (hipStream_t)stream, state, E,
               targets, filter_keys, n_filter, use_eql, ranks);
     return fl::fl_check_launch("dense_filtered_ranks");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Known-answer expansion of the filtered evaluation (src/main.py:212-276,
+// _expand_filter_side / _filter_indices_from_lookup).  The reference keys
+// the (source, relation) groups of one side as source * R + relation and
+// looks every query key up by binary search; here the key is split back into
+// (key floor-div R, key mod R) and the relation is searched among that
+// source's groups (ascending relation), which finds the same group for every
+// key.  The group's columns in CSR order are the query's known answers.
+// Outputs (query position, entity) pairs, queries in the given order.
+
+namespace fl {
+
+__global__ void k_flt_count(const int32_t *__restrict__ gptr, const int16_t *__restrict__ grel,
+                            const int32_t *__restrict__ gcount, int64_t nodes, const int64_t *__restrict__ keys,
+                            int64_t R, int64_t Q, int32_t *__restrict__ cnt, int64_t *__restrict__ gsel) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= Q) return;
+    const int64_t k = keys[q];
+    int64_t s = k / R, r = k % R;
+    if (r < 0) { r += R; s -= 1; }  // floor division
+    int64_t g = -1;
+    if (s >= 0 && s < nodes) {
+        int64_t lo = gptr[s], hi = gptr[s + 1];
+        while (lo < hi) {
+            const int64_t mid = lo + ((hi - lo) >> 1);
+            if (grel[mid] < r) lo = mid + 1; else hi = mid;
+        }
+        if (lo < gptr[s + 1] && grel[lo] == r) g = lo;
+    }
+    gsel[q] = g;
+    cnt[q] = g >= 0 ? gcount[g] : 0;
+}
+
+// Thread per output pair: its query by binary search over the offsets.
+__global__ void k_flt_fill(const int32_t *__restrict__ gstart, const int32_t *__restrict__ col,
+                           const int64_t *__restrict__ gsel, const int64_t *__restrict__ off, int64_t Q,
+                           const int64_t *__restrict__ qpos, int64_t total, int64_t *__restrict__ out_b,
+                           int64_t *__restrict__ out_e) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    int64_t lo = 0, hi = Q;  // last q with off[q] <= i
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (off[mid] <= i) lo = mid; else hi = mid;
+    }
+    const int64_t g = gsel[lo];
+    out_b[i] = qpos[lo];
+    out_e[i] = col[(int64_t)gstart[g] + (i - off[lo])];
+}
+
+size_t flt_al(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace fl
+
+extern "C" {
+
+size_t fl_filter_expand_bytes(int64_t Q) {
+    if (Q < 0) return 0;
+    const size_t q1 = (size_t)(Q > 0 ? Q : 1);
+    return fl::flt_al(sizeof(int32_t) * q1) + fl::flt_al(sizeof(int64_t) * q1) + fl::flt_al(fl::scan_tmp_bytes(Q + 1));
+}
+
+int fl_filter_expand_count(void *stream, const int32_t *gptr, const int16_t *grel, const int32_t *gcount,
+                           int64_t nodes, const int64_t *keys, int64_t R, int64_t Q, int64_t *off, void *ws,
+                           size_t ws_bytes) {
+    if (Q < 0 || nodes < 0 || R < 1) return fl::fl_fail(FL_ERR_ARG, "filter_expand: bad size");
+    if (!off || !ws || ws_bytes < fl_filter_expand_bytes(Q) || (Q > 0 && (!gptr || !grel || !gcount || !keys)))
+        return fl::fl_fail(FL_ERR_ARG, "filter_expand: null argument or workspace too small");
+    const size_t q1 = (size_t)(Q > 0 ? Q : 1);
+    int32_t *cnt = (int32_t *)ws;
+    int64_t *gsel = (int64_t *)((char *)ws + fl::flt_al(sizeof(int32_t) * q1));
+    int64_t *tmp = (int64_t *)((char *)gsel + fl::flt_al(sizeof(int64_t) * q1));
+    hipStream_t st = (hipStream_t)stream;
+    if (Q > 0)
+        FL_LAUNCH("k_flt_count", fl::k_flt_count, dim3((unsigned)((Q + 255) / 256)), dim3(256), 0, st, gptr, grel,
+                  gcount, nodes, keys, R, Q, cnt, gsel);
+    const int rc = fl::exclusive_scan(st, cnt, off, Q, tmp);
+    if (rc != FL_OK) return rc;
+    return fl::fl_check_launch("filter_expand_count");
+}
+
+int fl_filter_expand_fill(void *stream, const int32_t *gstart, const int32_t *col, int64_t Q, const int64_t *off,
+                          const int64_t *qpos, int64_t total, const void *ws, int64_t *out_b, int64_t *out_e) {
+    if (Q < 0 || total < 0) return fl::fl_fail(FL_ERR_ARG, "filter_expand: negative size");
+    if (total == 0) return FL_OK;
+    if (Q == 0 || !gstart || !col || !off || !qpos || !ws || !out_b || !out_e)
+        return fl::fl_fail(FL_ERR_ARG, "filter_expand: null argument");
+    const size_t q1 = (size_t)Q;
+    const int64_t *gsel = (const int64_t *)((const char *)ws + fl::flt_al(sizeof(int32_t) * q1));
+    FL_LAUNCH("k_flt_fill", fl::k_flt_fill, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+              (hipStream_t)stream, gstart, col, gsel, off, Q, qpos, total, out_b, out_e);
+    return fl::fl_check_launch("filter_expand_fill");
 }
 
 }  // extern "C"

@@ -132,19 +132,23 @@ def _build_group_metadata(sorted_rows, sorted_rels, num_nodes, row_ptr=None):
     return group_ptr, relations, starts, counts
 
 
-def _build_csr_structure_gpu(row, col, rel, nodes):
+def _gpu_csr_sides(row, col, rel, nodes, sides=((0, 1), (1, 0))):
+    """CSR sides built on the GPU: for each (s, t) in ``sides`` the side whose
+    sources are (row, col)[s] and targets (row, col)[t], as (row_ptr, columns,
+    edge_rel, order, group_ptr, group_rel, group_start, group_count)."""
     if not (row.dim() == col.dim() == rel.dim() == 1) or not (row.numel() == col.numel() == rel.numel()):
         raise ValueError("CSR requires equal 1D arrays and int32-sized graph")
     dev = row.device
     row, col, rel = (x.to(torch.int64).contiguous() for x in (row, col, rel))
+    ends = (row, col)
     m = row.numel()
     lib = _lib.lib()
     ws_bytes = lib.fl_csr_build_side_gpu_bytes(m, nodes)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     st = _stream(row)
     info = torch.empty(2, dtype=torch.int64, device=dev)
-
-    def side(source, target):
+    out = []
+    for s, t in sides:
         row_ptr = torch.empty(nodes + 1, dtype=torch.int32, device=dev)
         cols = torch.empty(m, dtype=torch.int32, device=dev)
         erel = torch.empty(m, dtype=torch.int16, device=dev)
@@ -153,16 +157,18 @@ def _build_csr_structure_gpu(row, col, rel, nodes):
         grel = torch.empty(max(m, 1), dtype=torch.int16, device=dev)
         gstart = torch.empty(max(m, 1), dtype=torch.int32, device=dev)
         gcount = torch.empty(max(m, 1), dtype=torch.int32, device=dev)
-        check(lib.fl_csr_build_side_gpu(st, m, nodes, ptr(source), ptr(target), ptr(rel), ptr(row_ptr), ptr(cols),
+        check(lib.fl_csr_build_side_gpu(st, m, nodes, ptr(ends[s]), ptr(ends[t]), ptr(rel), ptr(row_ptr), ptr(cols),
                                         ptr(erel), ptr(order), ptr(gptr), ptr(grel), ptr(gstart), ptr(gcount),
                                         ptr(info), ptr(ws), ws_bytes), "csr_build_side_gpu")
         g, err = info.tolist()
         if err:
             raise ValueError("CSR entity or relation ID outside supported range")
-        return (row_ptr, cols, erel, order, gptr, grel[:g].clone(), gstart[:g].clone(), gcount[:g].clone())
+        out.append((row_ptr, cols, erel, order, gptr, grel[:g].clone(), gstart[:g].clone(), gcount[:g].clone()))
+    return out
 
-    ori = side(row, col)
-    inv = side(col, row)
+
+def _build_csr_structure_gpu(row, col, rel, nodes):
+    ori, inv = _gpu_csr_sides(row, col, rel, nodes)
     return (*ori[:4], *inv[:4], *ori[4:], *inv[4:])
 
 
@@ -663,8 +669,7 @@ def dense_csr_sum_cuda(A, w, csr_struct, mask_values, r_size,
 
 
 # ---------------------------------------------------------------------------
-# Entry points not yet carried by this build.  Signatures follow the
-# reference so callers fail with a clear message instead of a NameError.
+# Filtered ranks of the evaluation (flashlog_kernel.py:168-179, src/main.py:468-512).
 
 def sparse2d_filtered_ranks_cuda(idx_b, idx_e, values, targets, filter_keys, B, E, use_eql=False):
     """Filtered tie-aware ranks of each query's target over a COO [B, E] score

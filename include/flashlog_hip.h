@@ -539,6 +539,26 @@ int fl_dense_filtered_ranks(void *stream, const float *state, const int64_t *tar
                             const int64_t *filter_keys, int64_t n_filter, int64_t B,
                             int64_t E, int use_eql, float *ranks);
 
+/* Replaces the known-answer expansion of the filtered evaluation
+ * (src/main.py:212-276, _expand_filter_side): per query q with key
+ * keys[q] = source * R + relation, the columns (in CSR order) of that
+ * (source, relation) group of one CSR side (its group pointers, relations,
+ * starts, counts and columns), as (qpos[q], entity) pairs, queries in the
+ * given order; a key with no group gives none.
+ * fl_filter_expand_count writes off [Q+1] (exclusive offsets; off[Q] = the
+ * number of pairs) using the workspace (fl_filter_expand_bytes); after the
+ * host has read off[Q], fl_filter_expand_fill (same workspace) writes the
+ * pairs. */
+size_t fl_filter_expand_bytes(int64_t Q);
+int fl_filter_expand_count(void *stream, const int32_t *gptr, const int16_t *grel,
+                           const int32_t *gcount, int64_t nodes, const int64_t *keys,
+                           int64_t R, int64_t Q, int64_t *off, void *ws,
+                           size_t ws_bytes);
+int fl_filter_expand_fill(void *stream, const int32_t *gstart, const int32_t *col,
+                          int64_t Q, const int64_t *off, const int64_t *qpos,
+                          int64_t total, const void *ws, int64_t *out_b,
+                          int64_t *out_e);
+
 /* Workspace for fl_filtered_ranks (values_f64: 1 for double scores). */
 size_t fl_filtered_ranks_workspace_bytes(int64_t B, int values_f64);
 

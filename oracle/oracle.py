@@ -838,3 +838,106 @@ def dense_filtered_ranks(state, targets, filter_b=None, filter_e=None, use_eql=F
         equal = (equal + np.float32(1)).astype(np.float32)
         return (greater + (equal + np.float32(1)) / np.float32(2)).astype(np.float32)
     return (greater + np.float32(1)).astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# Known-answer ("filter") indices of the evaluation (src/main.py:147-317)
+
+def filter_edge_lookup(source, relation, target, R):
+    """_build_filter_edge_lookup (src/main.py:147-161): (group keys ascending,
+    starts, counts, columns) with key = source * R + relation; equal keys
+    keep edge order (a stable sort; the reference's argsort leaves that
+    order open)."""
+    keys = np.asarray(source, np.int64) * R + np.asarray(relation, np.int64)
+    order = np.argsort(keys, kind="stable")
+    sk = keys[order]
+    cols = np.asarray(target, np.int64)[order]
+    if sk.size == 0:
+        e = np.zeros(0, np.int64)
+        return e, e, e, cols
+    starts = np.flatnonzero(np.r_[True, sk[1:] != sk[:-1]])
+    counts = np.diff(np.r_[starts, sk.size])
+    return sk[starts], starts, counts, cols
+
+
+def filter_side_lookup(row_group_ptr, group_rel, group_start, group_count, col_ind, R):
+    """_build_filter_side_lookup (src/main.py:181-200): a CSR side's groups
+    keyed by source * R + relation (the source of group g is the row whose
+    group range holds g)."""
+    gp = np.asarray(row_group_ptr, np.int64)
+    G = np.asarray(group_rel).size
+    if G == 0:
+        e = np.zeros(0, np.int64)
+        return e, e, e, np.asarray(col_ind, np.int64)
+    src = np.searchsorted(gp, np.arange(G), side="right") - 1
+    return (src * R + np.asarray(group_rel, np.int64), np.asarray(group_start, np.int64),
+            np.asarray(group_count, np.int64), np.asarray(col_ind, np.int64))
+
+
+def expand_filter_side(batch_pos, query_key, lookup):
+    """_expand_filter_side (src/main.py:227-267): every known answer of each
+    query key, queries in order, a group's columns in order."""
+    gk, starts, counts, cols = lookup
+    qk = np.asarray(query_key, np.int64)
+    bp = np.asarray(batch_pos, np.int64)
+    if qk.size == 0 or gk.size == 0:
+        e = np.zeros(0, np.int64)
+        return e, e
+    pos = np.searchsorted(gk, qk)
+    safe = np.minimum(pos, gk.size - 1)
+    ok = (pos < gk.size) & (gk[safe] == qk)
+    st, ct, b = starts[safe[ok]], counts[safe[ok]], bp[ok]
+    out_b = np.repeat(b, ct)
+    local = np.arange(out_b.size) - np.repeat(np.cumsum(ct) - ct, ct)
+    return out_b, cols[np.repeat(st, ct) + local]
+
+
+def filter_indices(input_x, input_r, R, lookup):
+    """_filter_indices_from_lookup (src/main.py:291-317): forward queries
+    (r < R) on the forward lookup, then inverse queries (key with r - R) on
+    the inverse lookup."""
+    x = np.asarray(input_x, np.int64).reshape(-1)
+    r = np.asarray(input_r, np.int64).reshape(-1)
+    pos = np.arange(x.size)
+    fwd = r < R
+    ob, oe = expand_filter_side(pos[fwd], x[fwd] * R + r[fwd], lookup[0])
+    ib, ie = expand_filter_side(pos[~fwd], x[~fwd] * R + (r[~fwd] - R), lookup[1])
+    return np.concatenate([ob, ib]), np.concatenate([oe, ie])
+
+
+def filter_indices_brute(h, r, t, R, input_x, input_r):
+    """Independent check: per query in batch order, a scan of every triple
+    (forward: tails of (x, r); inverse: heads of tail x under r - R); the
+    forward queries' pairs first, then the inverse queries'."""
+    h, r, t = (np.asarray(a, np.int64) for a in (h, r, t))
+    fwd_pairs, inv_pairs = [], []
+    for j, (x, q) in enumerate(zip(np.asarray(input_x).tolist(), np.asarray(input_r).tolist())):
+        if q < R:
+            fwd_pairs += [(j, int(t[i])) for i in range(h.size) if h[i] == x and r[i] == q]
+        else:
+            inv_pairs += [(j, int(h[i])) for i in range(h.size) if t[i] == x and r[i] == q - R]
+    pairs = fwd_pairs + inv_pairs
+    return (np.array([p[0] for p in pairs], np.int64), np.array([p[1] for p in pairs], np.int64))
+
+
+def raw_sparse_ranks(b, e, v, B, E, targets):
+    """Ranks of calculate_raw_hits_sparse (src/main.py:365-388) over a
+    coalesced [B, E] COO state: #entries >= the target's score, plus the
+    implicit zeros when that score is <= 0, in the values' dtype."""
+    b = np.asarray(b, np.int64)
+    e = np.asarray(e, np.int64)
+    v = np.asarray(v)
+    dt = v.dtype
+    truth = np.zeros(B, dt)
+    keys = b * E + e
+    tk = np.arange(B) * E + np.asarray(targets, np.int64)
+    pos = np.searchsorted(keys, tk)
+    safe = np.minimum(pos, max(keys.size - 1, 0))
+    ok = (pos < keys.size) & (keys[safe] == tk) if keys.size else np.zeros(B, bool)
+    truth[ok] = v[safe[ok]]
+    explicit = np.zeros(B, dt)
+    ge = np.zeros(B, dt)
+    np.add.at(explicit, b, np.ones_like(v))
+    np.add.at(ge, b, (v >= truth[b]).astype(dt))
+    missing = (dt.type(E) - explicit).astype(dt)
+    return (ge + np.where(truth <= 0, missing, np.zeros_like(missing))).astype(dt)

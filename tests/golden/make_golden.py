@@ -108,7 +108,25 @@ def write_api_surface():
         for node in tree.body:
             if isinstance(node, ast.FunctionDef) and node.name == "score":
                 rules["%s.score" % mod] = [a.arg for a in node.args.args]
+    # rule evaluation primitives and scorer (rules/evaluate.py), less its CLI and file readers
+    tree = ast.parse(open(os.path.join(REF, "rules", "evaluate.py")).read())
+    for node in tree.body:
+        if isinstance(node, ast.FunctionDef) and node.name not in ("main", "parse_args", "load_triples",
+                                                                     "dictionary_size"):
+            rules["evaluate.%s" % node.name] = [a.arg for a in node.args.args]
     json.dump(rules, open(os.path.join(HERE, "rules_surface.json"), "w"), indent=1, sort_keys=True)
+    # evaluation consumers of the driver (src/main.py:117-512)
+    evaluation = {}
+    names = ("create_eval_filter_csr", "_build_filter_edge_lookup", "_filter_csr_cache_key",
+             "_build_filter_side_lookup", "_get_filter_csr_lookup", "_expand_filter_side",
+             "build_filter_indices_csr", "_filter_indices_from_lookup", "build_filter_indices_graph",
+             "_sparse_truth_scores", "calculate_raw_hits_sparse", "calculate_hits_full_sparse",
+             "calculate_hits_full_with_filter_indices")
+    tree = ast.parse(open(os.path.join(REF, "src", "main.py")).read())
+    for node in tree.body:
+        if isinstance(node, ast.FunctionDef) and node.name in names:
+            evaluation[node.name] = [a.arg for a in node.args.args]
+    json.dump(evaluation, open(os.path.join(HERE, "evaluation_surface.json"), "w"), indent=1, sort_keys=True)
     grounding = {}
     tree = ast.parse(open(os.path.join(REF, "flashlog_kernel", "soft_grounding_kernel",
                                        "soft_grounding_kernel.py")).read())
@@ -116,7 +134,7 @@ def write_api_surface():
         if isinstance(node, ast.FunctionDef) and not node.name.startswith("_"):
             grounding[node.name] = [a.arg for a in node.args.args]
     json.dump(grounding, open(os.path.join(HERE, "grounding_surface.json"), "w"), indent=1, sort_keys=True)
-    print("wrote", len(surface) + len(rules) + len(grounding), "signatures")
+    print("wrote", len(surface) + len(rules) + len(evaluation) + len(grounding), "signatures")
 
 
 if __name__ == "__main__":

@@ -69,6 +69,15 @@ def test_rules_signature_matches_reference(name):
     assert list(inspect.signature(obj).parameters) == RULES[name]
 
 
+EVALUATION = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "evaluation_surface.json")))
+
+
+@pytest.mark.parametrize("name", sorted(EVALUATION))
+def test_evaluation_signature_matches_reference(name):
+    from flashlog_amd import evaluation
+    assert list(inspect.signature(getattr(evaluation, name)).parameters) == EVALUATION[name]
+
+
 GROUNDING = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "grounding_surface.json")))
 
 
@@ -84,7 +93,8 @@ def test_install_aliases_reference_module_names():
     import importlib
     import sys
     import flashlog_amd
-    saved = {k: sys.modules.get(k) for k in ("rules", "rules.shared_inference", "rules.max_inference")}
+    saved = {k: sys.modules.get(k) for k in ("rules", "rules.shared_inference", "rules.max_inference",
+                                             "rules.evaluate")}
     try:
         flashlog_amd.install(rules=True)
         assert importlib.import_module("flashlog_kernel.flashlog_kernel").__name__ == \
@@ -95,6 +105,8 @@ def test_install_aliases_reference_module_names():
         from rules.shared_inference import score as shared_score
         assert shared_score.__module__ == "flashlog_amd.rules.shared_inference"
         assert max_score.__module__ == "flashlog_amd.rules.max_inference"
+        from rules.evaluate import score_rule_batch
+        assert score_rule_batch.__module__ == "flashlog_amd.rules.evaluate"
     finally:
         for k, v in saved.items():
             if v is None:
