@@ -17,7 +17,8 @@ def install(rules=False):
     rules=True also redirects ``rules.shared_inference``,
     ``rules.max_inference`` (their ``score`` entry points) and
     ``rules.evaluate`` (the rule-evaluation primitives and scorer) to the GPU
-    rule-bank scoring, leaving the rest of a ``rules`` package alone."""
+    rule-bank scoring and ``rules.indexed_bank`` to this package's indexed
+    rule bank, leaving the rest of a ``rules`` package alone."""
     from . import flashlog_kernel as pkg
     from .flashlog_kernel import flashlog_kernel as mod
     from .flashlog_kernel import soft_grounding_kernel as sg
@@ -27,11 +28,13 @@ def install(rules=False):
     sys.modules["flashlog_kernel.soft_grounding_kernel"] = sg
     sys.modules["flashlog_kernel.soft_grounding_kernel.soft_grounding_kernel"] = sgm
     if rules:
-        from .rules import evaluate as evm, max_inference as mi, shared_inference as si
+        from .rules import evaluate as evm, indexed_bank as ib, max_inference as mi, shared_inference as si
+        sys.modules["rules.indexed_bank"] = ib
         sys.modules["rules.shared_inference"] = si
         sys.modules["rules.max_inference"] = mi
         sys.modules["rules.evaluate"] = evm
         parent = sys.modules.get("rules")
         if parent is not None:
             parent.shared_inference, parent.max_inference, parent.evaluate = si, mi, evm
+            parent.indexed_bank = ib
     return pkg

@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 20
+ABI_VERSION = 21
 FL_SEG = 32
 FL_SUP = 16
 
@@ -185,6 +185,11 @@ _SIGS = {
                                                   ctypes.c_size_t]),
     "fl_filtered_ranks_noalloc": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int] + [ctypes.c_void_p] * 2 +
                                   [ctypes.c_int64] * 4 + [ctypes.c_int, ctypes.c_void_p]),
+    "fl_rule_rank_weights": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int] + [ctypes.c_int64] * 4 +
+                             [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+                              ctypes.c_int] + [ctypes.c_void_p] * 4),
+    "fl_row_pairwise_sums": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                            ctypes.c_void_p]),
     "fl_filter_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64]),
     "fl_filter_expand_count": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_void_p,
                                                                      ctypes.c_int64, ctypes.c_int64,

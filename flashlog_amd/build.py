@@ -8,7 +8,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libflashlog_hip.so")
 HIP_SOURCES = ["fl_dense.hip", "fl_ranks.hip", "fl_scan.hip", "fl_sparse.hip", "fl_rules.hip", "fl_grounding.hip",
-               "fl_csr.hip"]
+               "fl_csr.hip", "fl_extract.hip"]
 HOST_SOURCES = ["fl_host.cpp"]
 
 # -ffp-contract=off: the bit-exact paths must not fuse a*b+c.

@@ -559,6 +559,27 @@ int fl_filter_expand_fill(void *stream, const int32_t *gstart, const int32_t *co
                           int64_t total, const void *ws, int64_t *out_b,
                           int64_t *out_e);
 
+/* Replaces the attention rank weights of extracted rule candidates
+ * (rules/extract.py:65-135, _three_step_weights / collapsed_rule_weights)
+ * and the row statistics of select_and_annotate_array (:148-201).
+ * attention: [H, T, L, n] float (att_f64 = 0) or double; rows: int64
+ * [N, W] = [length, op_1..op_T, ...] with trials at column W-8 and
+ * positives at W-6; row_head: int64 [N] head of each row in [0, H) (NULL:
+ * head 0).  mode 0: the 3-step closed form; 1: the dynamic program with
+ * sums; 2: with maxima.  Writes rank_weights double [N, L]; rank_sums
+ * (double [N], numpy's pairwise row sums; may be NULL) and precision
+ * (double [N], positives / trials or 0; may be NULL).  *err (device int64)
+ * is 1 when an operator lies outside [-n, n) (numpy's indexing) and 2 when
+ * a row head lies outside [0, H); the weights of such rows are 0. */
+int fl_rule_rank_weights(void *stream, const void *attention, int att_f64, int64_t H,
+                         int64_t T, int64_t L, int64_t n, const int64_t *rows, int64_t N,
+                         int64_t W, const int64_t *row_head, int64_t identity, int mode,
+                         double *rank_weights, double *rank_sums, double *precision,
+                         int64_t *err);
+/* Row sums of a double [N, L] matrix (L <= 128) in numpy's pairwise order
+ * (x.sum(axis=1) of fallback_rule_scores, rules/extract.py:141-145). */
+int fl_row_pairwise_sums(void *stream, const double *x, int64_t N, int64_t L, double *out);
+
 /* Workspace for fl_filtered_ranks (values_f64: 1 for double scores). */
 size_t fl_filtered_ranks_workspace_bytes(int64_t B, int values_f64);
 

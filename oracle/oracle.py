@@ -941,3 +941,118 @@ def raw_sparse_ranks(b, e, v, B, E, targets):
     np.add.at(ge, b, (v >= truth[b]).astype(dt))
     missing = (dt.type(E) - explicit).astype(dt)
     return (ge + np.where(truth <= 0, missing, np.zeros_like(missing))).astype(dt)
+
+
+# --------------------------------------------------------------------------
+# Extraction post-processing (rules/extract.py:65-201)
+
+def rank_weights_closed_form(attention, rows, identity):
+    """_three_step_weights (rules/extract.py:65-105): per body length 1..3
+    the sum over identity placements, each term's products left to right,
+    terms added left to right, in float64."""
+    a = np.asarray(attention)
+    rows = np.asarray(rows, np.int64)
+    out = np.zeros((rows.shape[0], a.shape[1]))
+    idw = a[:, :, identity].astype(np.float64)
+    v = lambda s, ops: a[s, :, ops].astype(np.float64)  # noqa: E731  [k, L]
+    i = np.flatnonzero(rows[:, 0] == 1)
+    if i.size:
+        o = rows[i, 1]
+        out[i] = v(0, o) * idw[1] * idw[2] + idw[0] * v(1, o) * idw[2] + idw[0] * idw[1] * v(2, o)
+    i = np.flatnonzero(rows[:, 0] == 2)
+    if i.size:
+        f, s = rows[i, 1], rows[i, 2]
+        out[i] = v(0, f) * v(1, s) * idw[2] + v(0, f) * idw[1] * v(2, s) + idw[0] * v(1, f) * v(2, s)
+    i = np.flatnonzero(rows[:, 0] == 3)
+    if i.size:
+        out[i] = v(0, rows[i, 1]) * v(1, rows[i, 2]) * v(2, rows[i, 3])
+    return out
+
+
+def rank_weights_dp(attention, rows, identity, maximum=False):
+    """collapsed_rule_weights (rules/extract.py:108-129): dp over (step,
+    operators placed), float64, sums or numpy maxima."""
+    a = np.asarray(attention, np.float64)
+    T, L, _ = a.shape
+    rows = np.asarray(rows, np.int64)
+    out = np.zeros((rows.shape[0], L))
+    for length in range(1, T + 1):
+        i = np.flatnonzero(rows[:, 0] == length)
+        if not i.size:
+            continue
+        ops = rows[i, 1:1 + length]
+        dp = np.zeros((i.size, length + 1, L))
+        dp[:, 0] = 1.0
+        for s in range(T):
+            nx = dp * a[s, :, identity]
+            for p in range(1, min(length, s + 1) + 1):
+                c = dp[:, p - 1] * a[s, :, ops[:, p - 1]]
+                nx[:, p] = np.maximum(nx[:, p], c) if maximum else nx[:, p] + c
+            dp = nx
+        out[i] = dp[:, length]
+    return out
+
+
+def rank_weights_brute(attention, rows, identity, maximum=False):
+    """Independent check: enumerate the step sets that hold the body's
+    operators (in order; the identity elsewhere), each product formed in
+    step order from 1.0; sum (in float64, no fixed order) or max."""
+    import itertools
+    a = np.asarray(attention, np.float64)
+    T, L, _ = a.shape
+    rows = np.asarray(rows, np.int64)
+    out = np.zeros((rows.shape[0], L))
+    for r, row in enumerate(rows):
+        length = int(row[0])
+        if not 1 <= length <= T:
+            continue
+        for c in range(L):
+            terms = []
+            for places in itertools.combinations(range(T), length):
+                prod, k = 1.0, 0
+                for s in range(T):
+                    if k < length and places[k] == s:
+                        prod *= a[s, c, row[1 + k]]
+                        k += 1
+                    else:
+                        prod *= a[s, c, identity]
+                terms.append(prod)
+            out[r, c] = max(terms) if maximum else float(np.sum(terms))
+    return out
+
+
+def select_and_annotate(candidates, attention, identity, minimum_positive_walks, fallback="sum"):
+    """select_and_annotate_array (rules/extract.py:148-201): selection,
+    fallback, precision and the lexicographic order, in numpy."""
+    cand = np.asarray(candidates, np.int64)
+    a = np.asarray(attention)
+    T = a.shape[0]
+    weights = (lambda rows: rank_weights_closed_form(a, rows, identity)) if T == 3 else \
+        (lambda rows: rank_weights_dp(a, rows, identity))
+    idx = np.flatnonzero(cand[:, -6] >= minimum_positive_walks)
+    used = False
+    allw = None
+    if idx.size == 0 and cand.shape[0]:
+        used = True
+        allw = weights(cand)
+        tot = allw.max(axis=1) if fallback == "max" else allw.sum(axis=1)
+        idx = np.asarray([max(range(cand.shape[0]),
+                              key=lambda j: (float(tot[j]), tuple(cand[j, 1:1 + cand[j, 0]])))])
+    sel = cand[idx]
+    rw = weights(sel) if allw is None else allw[idx]
+    trials = sel[:, -8].astype(np.float64)
+    pos = sel[:, -6].astype(np.float64)
+    prec = np.divide(pos, trials, out=np.zeros_like(pos), where=trials != 0)
+    cols = [np.where(sel[:, 0] >= p, sel[:, p], -1) for p in range(1, T + 1)]
+    order = np.lexsort(tuple(reversed(cols)) + (-rw.sum(axis=1), -sel[:, -5]))
+    return sel[order], prec[order], rw[order], used
+
+
+def select_order_brute(selected, rank_weights, T):
+    """Independent check of the output order: Python's stable sort by
+    (-positive source hits, -weight sum, body padded with -1)."""
+    keys = []
+    for j, row in enumerate(selected):
+        body = [int(row[p]) if row[0] >= p else -1 for p in range(1, T + 1)]
+        keys.append((-int(row[-5]), -float(np.sum(rank_weights[j])), tuple(body)))
+    return sorted(range(len(keys)), key=lambda j: keys[j])

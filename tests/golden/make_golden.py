@@ -114,6 +114,21 @@ def write_api_surface():
         if isinstance(node, ast.FunctionDef) and node.name not in ("main", "parse_args", "load_triples",
                                                                      "dictionary_size"):
             rules["evaluate.%s" % node.name] = [a.arg for a in node.args.args]
+    # extraction post-processing, the rule-serving CSR and the indexed rule bank
+    wanted = {"extract": ("_three_step_weights", "collapsed_rule_weights", "attention_rank_weights",
+                          "fallback_rule_scores", "select_and_annotate_array", "output_lines", "output_rule_lines"),
+              "prepare": ("read_heads", "directed_heads_from_train_relations", "build_rule_csr_structure",
+                          "load_train_columns"),
+              "indexed_bank": ("IndexedRuleBank", "IndexedHeadRules")}
+    for mod, names in wanted.items():
+        tree = ast.parse(open(os.path.join(REF, "rules", mod + ".py")).read())
+        for node in tree.body:
+            if isinstance(node, ast.FunctionDef) and node.name in names:
+                rules["%s.%s" % (mod, node.name)] = [a.arg for a in node.args.args]
+            elif isinstance(node, ast.ClassDef) and node.name in names:
+                for sub in node.body:
+                    if isinstance(sub, ast.FunctionDef) and sub.name == "__init__":
+                        rules["%s.%s" % (mod, node.name)] = [a.arg for a in sub.args.args][1:]
     json.dump(rules, open(os.path.join(HERE, "rules_surface.json"), "w"), indent=1, sort_keys=True)
     # evaluation consumers of the driver (src/main.py:117-512)
     evaluation = {}

@@ -94,7 +94,7 @@ def test_install_aliases_reference_module_names():
     import sys
     import flashlog_amd
     saved = {k: sys.modules.get(k) for k in ("rules", "rules.shared_inference", "rules.max_inference",
-                                             "rules.evaluate")}
+                                             "rules.evaluate", "rules.indexed_bank")}
     try:
         flashlog_amd.install(rules=True)
         assert importlib.import_module("flashlog_kernel.flashlog_kernel").__name__ == \
@@ -107,6 +107,8 @@ def test_install_aliases_reference_module_names():
         assert max_score.__module__ == "flashlog_amd.rules.max_inference"
         from rules.evaluate import score_rule_batch
         assert score_rule_batch.__module__ == "flashlog_amd.rules.evaluate"
+        from rules.indexed_bank import IndexedRuleBank
+        assert IndexedRuleBank.__module__ == "flashlog_amd.rules.indexed_bank"
     finally:
         for k, v in saved.items():
             if v is None:

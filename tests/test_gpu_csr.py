@@ -52,3 +52,13 @@ def test_gpu_csr_edge_cases():
     bad = [torch.tensor(x, device="cuda") for x in ([0, 1], [1, 2], [0, 40000])]
     with pytest.raises(ValueError):
         fk.build_csr_structure(*bad, 5)  # relation above 32767
+
+
+def test_gpu_rule_csr_matches_host():
+    from flashlog_amd.rules import prepare as P
+    h, r, t, E, R = synth.make_graph(3)
+    args = [torch.from_numpy(a) for a in (h, t, r)]
+    host = P.build_rule_csr_structure(*args, E)
+    gpu = P.build_rule_csr_structure(*(a.cuda() for a in args), E)
+    for a, b in zip(gpu, host):
+        assert a.is_cuda and torch.equal(a.cpu(), b)
