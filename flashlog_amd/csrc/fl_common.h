@@ -12,6 +12,16 @@ __device__ __forceinline__ float fl_add(float a, float b) { return __fadd_rn(a, 
 
 __device__ __forceinline__ int fl_lane() { return threadIdx.x & (FL_WAVE - 1); }
 
+// Workgroups of a launch go to the 8 XCDs round robin (workgroup g on XCD
+// g % 8).  This maps workgroup g of a grid of G to an index such that every
+// XCD takes one contiguous range of indices (work items that share cache
+// lines at their edges then meet in one L2); a bijection on [0, G).
+#define FL_XCDS 8
+__device__ __forceinline__ int64_t fl_xcd_contig(int64_t g, int64_t G) {
+    const int64_t q = G / FL_XCDS, rem = G % FL_XCDS, x = g % FL_XCDS, k = g / FL_XCDS;
+    return x * q + (x < rem ? x : rem) + k;
+}
+
 __device__ __forceinline__ int fl_wave_incl_scan_i32(int v);
 __device__ __forceinline__ long long fl_wave_incl_scan_i64(long long v);
 __device__ __forceinline__ long long fl_readlane_i64(long long x, int l);

@@ -860,7 +860,7 @@ __device__ __forceinline__ int64_t sp_tile_row(const int64_t *tile_base, int64_t
 __global__ __launch_bounds__(SP_NT) void k_sp_hist(int64_t R, SpRows rows, const int32_t *__restrict__ raw_dst,
                                                   int32_t *__restrict__ hist) {
     extern __shared__ int hb[];  // [NB]
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = fl_xcd_contig(blockIdx.x, gridDim.x);
     const int64_t r = sp_tile_row(rows.tile_base, R, tile);
     const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
     const int64_t tl = tile - rows.tile_base[r];
@@ -878,66 +878,105 @@ __global__ __launch_bounds__(SP_NT) void k_sp_hist(int64_t R, SpRows rows, const
     for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) hrow[q * nt] = hb[q];
 }
 
-// Stable LSD block sort of SP_NT * IPT keys held in LDS (kin, blocked: thread
-// t owns kin[t*IPT .. t*IPT + IPT)) by bits [lo, lo + nbits), 4 bits per
-// pass; kout is the second LDS buffer.  Returns the buffer with the result.
+// Stable LSD block sort of SP_NT * IPT keys held in LDS (kin, in positions
+// 0 .. SP_NT*IPT-1) by bits [lo, lo + nbits), SP_RB bits per pass; kout is
+// the second LDS buffer.  Returns the buffer with the result.
+//   A pass reads the keys striped (round j, thread t: position j*SP_NT + t,
+// so the current order is round-major, then wave, then lane) and ranks each
+// key among the equal digits of its wave and round with SP_RB ballots (the
+// lanes whose digit bits all agree, counted below the lane).  The lowest
+// such lane writes the group's size into the count table at
+// (digit, round, wave); an exclusive scan of the table in that order gives
+// every (digit, round, wave) its first output position, and each key goes
+// to that position plus its rank.  Equal digits keep their current order:
+// the sort is stable.  The table (two buffers: one is cleared while the
+// other is scanned) pads one entry per digit to spread the LDS banks.
+constexpr int SP_RB = 5;                     // radix bits per pass
+constexpr int SP_ND = 1 << SP_RB;            // digits
+constexpr int SP_NWV = SP_NT / FL_WAVE;      // waves per workgroup
+constexpr int SP_SORT_IPT_MAX = 16;
+constexpr int SP_SORT_TAB = 2 * SP_ND * (SP_SORT_IPT_MAX * SP_NWV + 1);  // uint16 entries
+
+__device__ __forceinline__ uint32_t sp_lanes_below(unsigned long long m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 template <int IPT>
-__device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, int nbits, uint16_t (*cnt)[SP_NT],
+__device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, int nbits, uint16_t *cnt,
                                    int *scan_lds) {
+    static_assert(IPT % 2 == 0 && IPT <= SP_SORT_IPT_MAX, "sort table sized for even IPT <= 16");
+    constexpr int SPAN = IPT * SP_NWV;                // entries of one digit
+    constexpr int TAB = SP_ND * (SPAN + 1);           // one buffer, padded
+    constexpr int PER = SP_ND * SPAN / SP_NT;         // scanned entries per thread
     const int t = threadIdx.x;
-    for (int shift = lo_bit; shift < lo_bit + nbits; shift += 4) {
+    const int lane = fl_lane();
+    const int w = t / FL_WAVE;
+    uint16_t *tab = cnt, *nxt = cnt + TAB;
+    for (int q = t; q < TAB; q += SP_NT) tab[q] = 0;
+    __syncthreads();
+    for (int shift = lo_bit; shift < lo_bit + nbits; shift += SP_RB) {
         uint32_t key[IPT];
-        uint16_t loc[IPT];
-#pragma unroll
-        for (int d = 0; d < 16; ++d) cnt[d][t] = 0;
+        uint16_t dg[IPT], rk[IPT];
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            key[j] = kin[t * IPT + j];
-            const int d = (key[j] >> shift) & 15;
-            loc[j] = cnt[d][t];
-            cnt[d][t] = (uint16_t)(loc[j] + 1);
+            key[j] = kin[j * SP_NT + t];
+            const int d = (int)((key[j] >> shift) & (SP_ND - 1));
+            unsigned long long m = ~0ull;
+#pragma unroll
+            for (int b = 0; b < SP_RB; ++b) {
+                const unsigned long long bal = __ballot((d >> b) & 1);
+                m &= ((d >> b) & 1) ? bal : ~bal;
+            }
+            const uint32_t below = sp_lanes_below(m);
+            dg[j] = (uint16_t)d;
+            rk[j] = (uint16_t)below;
+            if (below == 0) tab[d * (SPAN + 1) + j * SP_NWV + w] = (uint16_t)__popcll(m);
         }
         __syncthreads();
-        // exclusive scan of the counters in digit-major order; thread t owns
-        // flat entries [16t, 16t + 16) = digit t/16, threads 16*(t%16) ...
-        uint16_t *flat = &cnt[0][0];
-        int part = 0;
+        // exclusive scan in (digit, round, wave) order; the other buffer is cleared
+        int v[PER];
+        int sum = 0;
 #pragma unroll
-        for (int q = 0; q < 16; ++q) part += flat[t * 16 + q];
+        for (int q = 0; q < PER; ++q) {
+            const int f = t * PER + q;
+            v[q] = tab[f + f / SPAN];
+            sum += v[q];
+        }
         int tot;
-        int run = fl_block_excl_scan<SP_NT>(part, scan_lds, &tot);
+        int run = fl_block_excl_scan<SP_NT>(sum, scan_lds, &tot);
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int c = flat[t * 16 + q];
-            flat[t * 16 + q] = (uint16_t)run;
-            run += c;
+        for (int q = 0; q < PER; ++q) {
+            const int f = t * PER + q;
+            tab[f + f / SPAN] = (uint16_t)run;
+            run += v[q];
         }
+        for (int q = t; q < TAB; q += SP_NT) nxt[q] = 0;
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < IPT; ++j) {
-            const int d = (key[j] >> shift) & 15;
-            kout[cnt[d][t] + loc[j]] = key[j];
-        }
+        for (int j = 0; j < IPT; ++j) kout[tab[dg[j] * (SPAN + 1) + j * SP_NWV + w] + rk[j]] = key[j];
         __syncthreads();
         uint32_t *x = kin; kin = kout; kout = x;
+        uint16_t *y = tab; tab = nxt; nxt = y;
     }
     return kin;
 }
 
 // Workgroup per tile: stable scatter of the tile's items into the row's
-// destination buckets (bases from the scanned histogram).
+// destination buckets (bases from the scanned histogram).  With part_inv
+// (a backward), every item's partition position is recorded at its raw
+// position (written within the tile's range, not scattered over the row).
 __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, int nbits,
                                                        const int64_t *__restrict__ base,
                                                        const int32_t *__restrict__ raw_dst,
                                                        const float *__restrict__ raw_val,
                                                        int32_t *__restrict__ part_dst, float *__restrict__ part_val,
-                                                       int32_t *__restrict__ part_raw,
+                                                       int32_t *__restrict__ part_inv,
                                                        const uint32_t *__restrict__ raw_tie,
                                                        uint32_t *__restrict__ part_tie) {
     __shared__ __align__(16) uint32_t kb[2][SP_TILE];
-    __shared__ uint16_t cnt[16][SP_NT];
+    __shared__ uint16_t cnt[SP_SORT_TAB];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = fl_xcd_contig(blockIdx.x, gridDim.x);
     const int64_t r = sp_tile_row(rows.tile_base, R, tile);
     const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
     const int64_t tl = tile - rows.tile_base[r];
@@ -995,7 +1034,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         const int idx = (int)(key & 4095u);
         part_dst[q] = raw_dst[i0 + idx];
         part_val[q] = raw_val[i0 + idx];
-        if (part_raw) part_raw[q] = (int32_t)(i0 + idx);
+        if (part_inv) part_inv[i0 + idx] = (int32_t)q;
         if (part_tie) part_tie[q] = raw_tie[i0 + idx];
     }
 }
@@ -1003,8 +1042,8 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
 // Workgroup per (row, bucket): the bucket's items (raw order) grouped by
 // destination with each destination's values added to 0 in raw order; the
 // outputs are compacted in destination order into the first slots of the
-// bucket's item range, and raw_local[raw position] = the item's output index
-// within the bucket (for the backward).  Items are stably sorted by
+// bucket's item range, and raw_local[the item's position in the bucket's
+// items] = its output index within the bucket (for the backward).  Items are stably sorted by
 // destination in LDS (keys destination << 11 | index, LSD radix) and the
 // first thread of every run adds the run's values in order.
 //   sp_accum_one    buckets of at most SP_CHUNK items, one sort (the
@@ -1036,7 +1075,7 @@ template <int IPT>
 __device__ __forceinline__ const uint32_t *sp_load_sort(const int32_t *__restrict__ dst_arr,
                                                         const float *__restrict__ val_arr, int64_t start, int64_t c0,
                                                         int64_t n, uint32_t (*kb)[SP_CHUNK], float *val,
-                                                        uint16_t (*cnt)[SP_NT], int *scan_lds) {
+                                                        uint16_t *cnt, int *scan_lds) {
     const int t = threadIdx.x;
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
@@ -1052,7 +1091,7 @@ __device__ __forceinline__ const uint32_t *sp_load_sort(const int32_t *__restric
         kb[0][k] = (dl << 11) | (uint32_t)k;
     }
     __syncthreads();
-    return sp_block_sort<IPT>(kb[0], kb[1], 11, 16, cnt, scan_lds);
+    return sp_block_sort<IPT>(kb[0], kb[1], 11, 14, cnt, scan_lds);
 }
 
 // The chunk's items [c0, c0 + SP_NT*IPT) of a bucket in registers (blocked:
@@ -1142,8 +1181,17 @@ __device__ __forceinline__ bool sp_is_head(const uint32_t *key, int p) {
 }
 
 __device__ __forceinline__ int sp_run_end(const uint32_t *key, int p, int size) {
+    // the run holds positions [p, lo); probes at p + 1, 2, 4, .. find a key
+    // above the run (or the end), then a binary search between
     const uint32_t d = key[p] >> 11;
-    int lo = p + 1, hi = size;
+    int lo = p + 1, hi, step = 1;
+    for (;;) {
+        hi = p + step;
+        if (hi >= size) { hi = size; break; }
+        if ((key[hi] >> 11) > d) break;
+        lo = hi + 1;
+        step <<= 1;
+    }
     while (lo < hi) {
         const int mid = (lo + hi) >> 1;
         if ((key[mid] >> 11) <= d) lo = mid + 1;
@@ -1157,7 +1205,7 @@ __device__ __forceinline__ int sp_run_end(const uint32_t *key, int p, int size) 
 // before this thread's first head belongs to run rank0 - 1.
 template <int IPT>
 __device__ __forceinline__ void sp_raw_ranks(const uint32_t *key, int p0, int rank0, int64_t start,
-                                             const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local) {
+                                             int32_t *__restrict__ raw_local) {
     int r = rank0 - 1;
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
@@ -1166,15 +1214,14 @@ __device__ __forceinline__ void sp_raw_ranks(const uint32_t *key, int p0, int ra
         if ((k >> 11) >= SP_W) continue;  // hole or padding (sorted last)
         if (sp_is_head(key, p)) ++r;
         const int idx = (int)(k & 2047u);
-        raw_local[raw_arr ? raw_arr[start + idx] : start + idx] = r;
+        raw_local[start + idx] = r;
     }
 }
 
 template <int IPT>
 __device__ __forceinline__ void sp_accum_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
-                             float *__restrict__ val_arr, const int32_t *__restrict__ raw_arr,
-                             int32_t *__restrict__ raw_local, int32_t *out_count, uint32_t (*kb)[SP_CHUNK],
-                             float *val, uint16_t (*cnt)[SP_NT], int *scan_lds) {
+                             float *__restrict__ val_arr, int32_t *__restrict__ raw_local, int32_t *out_count, uint32_t (*kb)[SP_CHUNK],
+                             float *val, uint16_t *cnt, int *scan_lds) {
     constexpr int SIZE = SP_NT * IPT;
     const int t = threadIdx.x;
     const uint32_t *key = sp_load_sort<IPT>(dst_arr, val_arr, start, 0, n, kb, val, cnt, scan_lds);
@@ -1184,7 +1231,7 @@ __device__ __forceinline__ void sp_accum_one(int64_t start, int64_t n, int32_t d
     for (int j = 0; j < IPT; ++j) heads += sp_is_head(key, t * IPT + j) ? 1 : 0;
     int total;
     int rank = fl_block_excl_scan<SP_NT>(heads, scan_lds, &total);
-    if (raw_local) sp_raw_ranks<IPT>(key, t * IPT, rank, start, raw_arr, raw_local);
+    if (raw_local) sp_raw_ranks<IPT>(key, t * IPT, rank, start, raw_local);
     // all items were read before the first barrier: outputs may overwrite them
     for (int j = 0; j < IPT; ++j) {
         const int p = t * IPT + j;
@@ -1256,8 +1303,7 @@ __device__ __forceinline__ uint32_t *sp_wave_sort(uint32_t *kin, uint32_t *kout,
 // sp_accum_one does for a workgroup.
 template <int IPT>
 __device__ __forceinline__ void sp_wave_accum(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
-                              float *__restrict__ val_arr, const int32_t *__restrict__ raw_arr,
-                              int32_t *__restrict__ raw_local, int32_t *out_count, uint32_t (*kb)[SP_WB], float *val,
+                              float *__restrict__ val_arr, int32_t *__restrict__ raw_local, int32_t *out_count, uint32_t (*kb)[SP_WB], float *val,
                               uint16_t (*cnt)[FL_WAVE]) {
     constexpr int SIZE = FL_WAVE * IPT;
     const int t = fl_lane();
@@ -1289,7 +1335,7 @@ __device__ __forceinline__ void sp_wave_accum(int64_t start, int64_t n, int32_t 
     const int incl = fl_wave_incl_scan_i32(heads);
     const int total = __shfl(incl, FL_WAVE - 1, FL_WAVE);
     int rank = incl - heads;
-    if (raw_local) sp_raw_ranks<IPT>(key, t * IPT, rank, start, raw_arr, raw_local);
+    if (raw_local) sp_raw_ranks<IPT>(key, t * IPT, rank, start, raw_local);
     // every item was read before the sort: outputs may overwrite them
     for (int j = 0; j < IPT; ++j) {
         const int p = t * IPT + j;
@@ -1308,7 +1354,6 @@ __device__ __forceinline__ void sp_wave_accum(int64_t start, int64_t n, int32_t 
 // mid-size; lists[1], lists[3] their claim counters).
 __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int64_t *__restrict__ base,
                                                          int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
-                                                         const int32_t *__restrict__ raw_arr,
                                                          int32_t *__restrict__ raw_local,
                                                          int32_t *__restrict__ out_count, int64_t nslots,
                                                          int32_t *__restrict__ hot_list,
@@ -1318,7 +1363,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
     __shared__ float val[SP_SMALL_WAVES][SP_WB];
     __shared__ uint16_t cnt[SP_SMALL_WAVES][16][FL_WAVE];
     const int w = threadIdx.x / FL_WAVE;
-    const int64_t slot = (int64_t)blockIdx.x * SP_SMALL_WAVES + w;
+    const int64_t slot = fl_xcd_contig(blockIdx.x, gridDim.x) * SP_SMALL_WAVES + w;
     if (slot >= nslots) return;  // no block barrier follows
     const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
     int64_t start, end;
@@ -1340,32 +1385,33 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
     }
     const int32_t dbase = (int32_t)(bk << SP_S);
     if (n <= FL_WAVE)
-        sp_wave_accum<1>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+        sp_wave_accum<1>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
     else if (n <= 2 * FL_WAVE)
-        sp_wave_accum<2>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+        sp_wave_accum<2>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
     else if (n <= 4 * FL_WAVE)
-        sp_wave_accum<4>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+        sp_wave_accum<4>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
     else
-        sp_wave_accum<8>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+        sp_wave_accum<8>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
 }
 
 // Persistent grid over the mid-size buckets (SP_WB < n <= SP_CHUNK).
+// Persistent grid over a list of mid-size buckets (SP_WB < n <= SP_CHUNK);
+// ctr[0] = listed buckets, ctr[1] = next one to claim.
 __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64_t *__restrict__ base,
                                                        int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
-                                                       const int32_t *__restrict__ raw_arr,
                                                        int32_t *__restrict__ raw_local,
                                                        int32_t *__restrict__ out_count,
                                                        const int32_t *__restrict__ mid_list,
-                                                       int32_t *__restrict__ lists) {
+                                                       int32_t *__restrict__ ctr) {
     __shared__ __align__(16) uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
-    __shared__ uint16_t cnt[16][SP_NT];
+    __shared__ uint16_t cnt[SP_SORT_TAB];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
     __shared__ int claim;
-    const int nmid = lists[2];
+    const int nmid = ctr[0];
     for (;;) {
         __syncthreads();  // the previous bucket is done with the LDS arrays
-        if (threadIdx.x == 0) claim = atomicAdd(&lists[3], 1);
+        if (threadIdx.x == 0) claim = atomicAdd(&ctr[1], 1);
         __syncthreads();
         const int mi = claim;
         if (mi >= nmid) break;
@@ -1377,34 +1423,214 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64
         const int32_t dbase = (int32_t)(bk << SP_S);
         int32_t *oc = &out_count[slot];
         if (n <= SP_NT * 4)
-            sp_accum_one<4>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
+            sp_accum_one<4>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb, val, cnt, scan_lds);
         else
-            sp_accum_one<8>(start, n, dbase, dst_arr, val_arr, raw_arr, raw_local, oc, kb, val, cnt, scan_lds);
+            sp_accum_one<8>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb, val, cnt, scan_lds);
+    }
+}
+
+// ---- Buckets with few distinct destinations (at most SP_FEW): mid-size and
+// hot buckets are taken here first (persistent grid, hot list then mid
+// list).  One pass over the bucket marks its destinations; with more than
+// SP_FEW the bucket goes to a fallback list (k_sp_accum_mid / k_sp_accum_hot).
+// Otherwise destination j (in destination order) is slot j, the bucket's
+// output j, and thread j owns its sum in a register.  Chunks of SP_CHUNK
+// items in raw order: each item's slot is ranked among the equal slots of its
+// wave and round with ballots (as sp_block_sort does, one 6-bit pass), the
+// values are scattered slot-major into LDS in raw order within each slot, and
+// thread j adds its slot's run to its sum, in order.  raw_local (partition
+// order) gets each item's slot, written in place.
+constexpr int SP_FEW = 64;
+constexpr int SP_FEW_RB = 6;
+constexpr int SP_FEW_IPT = SP_CHUNK / SP_NT;               // 8
+constexpr int SP_FEW_SPAN = SP_FEW_IPT * SP_NWV;           // (round, wave) entries of one slot
+constexpr int SP_FEW_TAB = SP_FEW * (SP_FEW_SPAN + 1);     // one count table, padded per slot
+constexpr int SP_FEW_PER = SP_FEW * SP_FEW_SPAN / SP_NT;   // scanned entries per thread
+static_assert(SP_FEW == (1 << SP_FEW_RB) && SP_FEW <= SP_NT, "one slot per thread");
+
+__device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
+                                           float *__restrict__ val_arr, int32_t *__restrict__ raw_local,
+                                           int32_t *out_count, int total, const uint32_t *bits, const int *wpre,
+                                           const int32_t *slot_dl, uint16_t (*tab)[SP_FEW_TAB], float *sv,
+                                           int *scan_lds) {
+    const int t = threadIdx.x;
+    const int lane = fl_lane();
+    const int w = t / FL_WAVE;
+    for (int q = t; q < SP_FEW_TAB; q += SP_NT) tab[0][q] = 0;
+    float acc = 0.0f;  // thread t < total: the sum of slot t
+    int32_t pd[SP_FEW_IPT];
+    float pv[SP_FEW_IPT];
+#pragma unroll
+    for (int j = 0; j < SP_FEW_IPT; ++j) {  // striped: round j, thread t holds item j*SP_NT + t
+        const int64_t k = (int64_t)j * SP_NT + t;
+        pd[j] = k < n ? dst_arr[start + k] : 0;
+        pv[j] = k < n ? val_arr[start + k] : 0.0f;
+    }
+    __syncthreads();  // table cleared
+    int cur = 0;
+    for (int64_t c0 = 0; c0 < n; c0 += SP_CHUNK) {
+        uint8_t sl[SP_FEW_IPT], rk[SP_FEW_IPT];
+        float vv[SP_FEW_IPT];
+#pragma unroll
+        for (int j = 0; j < SP_FEW_IPT; ++j) {
+            const int64_t k = c0 + (int64_t)j * SP_NT + t;
+            const bool valid = k < n;
+            int sj = 0;
+            if (valid) {
+                const int dl = pd[j] & (SP_W - 1);
+                sj = wpre[dl >> 5] + __popc(bits[dl >> 5] & ((1u << (dl & 31)) - 1u));
+            }
+            unsigned long long m = __ballot(valid);
+#pragma unroll
+            for (int b = 0; b < SP_FEW_RB; ++b) {
+                const unsigned long long bal = __ballot((sj >> b) & 1);
+                m &= ((sj >> b) & 1) ? bal : ~bal;
+            }
+            const uint32_t below = sp_lanes_below(m);
+            if (valid && below == 0) tab[cur][sj * (SP_FEW_SPAN + 1) + j * SP_NWV + w] = (uint16_t)__popcll(m);
+            if (valid && raw_local) raw_local[start + k] = sj;
+            sl[j] = (uint8_t)sj;
+            rk[j] = (uint8_t)below;
+            vv[j] = pv[j];
+        }
+        // the next chunk's items are requested while this one is scanned and added
+        if (c0 + SP_CHUNK < n) {
+#pragma unroll
+            for (int j = 0; j < SP_FEW_IPT; ++j) {
+                const int64_t k = c0 + SP_CHUNK + (int64_t)j * SP_NT + t;
+                pd[j] = k < n ? dst_arr[start + k] : 0;
+                pv[j] = k < n ? val_arr[start + k] : 0.0f;
+            }
+        }
+        __syncthreads();  // counts written; every thread is past its previous sum
+        // exclusive scan in (slot, round, wave) order; the other table is cleared
+        int v[SP_FEW_PER];
+        int sum = 0;
+#pragma unroll
+        for (int q = 0; q < SP_FEW_PER; ++q) {
+            const int f = t * SP_FEW_PER + q;
+            v[q] = tab[cur][f + f / SP_FEW_SPAN];
+            sum += v[q];
+        }
+        int tot;
+        int run = fl_block_excl_scan<SP_NT>(sum, scan_lds, &tot);
+#pragma unroll
+        for (int q = 0; q < SP_FEW_PER; ++q) {
+            const int f = t * SP_FEW_PER + q;
+            tab[cur][f + f / SP_FEW_SPAN] = (uint16_t)run;
+            run += v[q];
+        }
+        for (int q = t; q < SP_FEW_TAB; q += SP_NT) tab[cur ^ 1][q] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < SP_FEW_IPT; ++j) {
+            if (c0 + (int64_t)j * SP_NT + t < n)
+                sv[tab[cur][sl[j] * (SP_FEW_SPAN + 1) + j * SP_NWV + w] + rk[j]] = vv[j];
+        }
+        __syncthreads();
+        if (t < total) {
+            const int lo = tab[cur][t * (SP_FEW_SPAN + 1)];
+            const int hi = t + 1 < SP_FEW ? tab[cur][(t + 1) * (SP_FEW_SPAN + 1)] : tot;
+            acc = sp_fold(acc, sv, lo, hi);
+        }
+        cur ^= 1;
+    }
+    __syncthreads();  // every item was read: outputs may overwrite them
+    if (t < total) {
+        dst_arr[start + t] = dbase + slot_dl[t];
+        val_arr[start + t] = acc;
+    }
+    if (t == 0) *out_count = total;
+}
+
+// lists: hot_list (ctr[0] listed, ctr[1] claim), then mid_list (ctr[2],
+// ctr[3]); fallbacks to hot_fb (ctr[4]) and mid_fb (ctr[6]).
+__global__ __launch_bounds__(SP_NT) void k_sp_accum_few(SpRows rows, const int64_t *__restrict__ base,
+                                                       int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
+                                                       int32_t *__restrict__ raw_local,
+                                                       int32_t *__restrict__ out_count,
+                                                       const int32_t *__restrict__ hot_list,
+                                                       const int32_t *__restrict__ mid_list,
+                                                       int32_t *__restrict__ hot_fb, int32_t *__restrict__ mid_fb,
+                                                       int32_t *__restrict__ ctr) {
+    __shared__ uint32_t bits[SP_W / 32];
+    __shared__ int wpre[SP_W / 32];
+    __shared__ int32_t slot_dl[SP_FEW];
+    __shared__ __align__(16) float sv[SP_CHUNK];
+    __shared__ uint16_t tab[2][SP_FEW_TAB];
+    __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
+    __shared__ int claim;
+    static_assert(SP_W / 32 == SP_NT, "one bitmap word per thread");
+    const int t = threadIdx.x;
+    const int nhot = ctr[0], nmid = ctr[2];
+    for (;;) {
+        __syncthreads();  // the previous bucket is done with the LDS arrays
+        if (t == 0) {
+            int c = atomicAdd(&ctr[1], 1);
+            if (c >= nhot) c = nhot + atomicAdd(&ctr[3], 1);
+            claim = c;
+        }
+        __syncthreads();
+        const int ci = claim;
+        if (ci >= nhot + nmid) break;
+        const bool hot = ci < nhot;
+        const int64_t slot = hot ? hot_list[ci] : mid_list[ci - nhot];
+        const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
+        int64_t start, end;
+        sp_bucket_range(rows, base, r, bk, &start, &end);
+        const int64_t n = end - start;
+        bits[t] = 0;
+        __syncthreads();
+#pragma unroll 8
+        for (int64_t k = t; k < n; k += SP_NT) {
+            const int dl = dst_arr[start + k] & (SP_W - 1);
+            atomicOr(&bits[dl >> 5], 1u << (dl & 31));
+        }
+        __syncthreads();
+        const uint32_t word = bits[t];
+        int total;
+        const int pre = fl_block_excl_scan<SP_NT>(__popc(word), scan_lds, &total);
+        if (total > SP_FEW) {
+            if (t == 0) {
+                if (hot) hot_fb[atomicAdd(&ctr[4], 1)] = (int32_t)slot;
+                else mid_fb[atomicAdd(&ctr[6], 1)] = (int32_t)slot;
+            }
+            continue;
+        }
+        wpre[t] = pre;
+        uint32_t wd = word;
+        for (int q = pre; wd; ++q) {
+            const int bit = __ffs(wd) - 1;
+            wd &= wd - 1;
+            slot_dl[q] = t * 32 + bit;
+        }
+        __syncthreads();
+        sp_few_one(start, n, (int32_t)(bk << SP_S), dst_arr, val_arr, raw_local, &out_count[slot], total, bits, wpre,
+                   slot_dl, tab, sv, scan_lds);
     }
 }
 
 __device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__restrict__ base, int64_t r, int64_t bk,
                                  int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
-                                 const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local,
+                                 int32_t *__restrict__ raw_local,
                                  int32_t *__restrict__ out_count, uint32_t (*kb)[SP_CHUNK], float *val,
-                                 uint16_t (*cnt)[SP_NT], float *acc, uint32_t *bits, int *wpre, int *scan_lds);
+                                 uint16_t *cnt, float *acc, uint32_t *bits, int *wpre, int *scan_lds);
 
-// Persistent grid over the list of hot buckets collected by k_sp_accum_small.
+// Persistent grid over a list of hot buckets (hot_count[0] listed,
+// hot_count[1] next to claim).
 __global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64_t *__restrict__ base,
                                                        int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
-                                                       const int32_t *__restrict__ raw_arr,
                                                        int32_t *__restrict__ raw_local,
                                                        int32_t *__restrict__ out_count,
                                                        const int32_t *__restrict__ hot_list,
                                                        int32_t *__restrict__ hot_count) {
     __shared__ __align__(16) uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
-    __shared__ uint16_t cnt[16][SP_NT];
+    __shared__ uint16_t cnt[SP_SORT_TAB];
     __shared__ float acc[SP_W];
     __shared__ uint32_t bits[SP_W / 32];
     __shared__ int wpre[SP_W / 32];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
-    // hot_count[0]: listed buckets; hot_count[1]: next bucket to claim
     __shared__ int claim;
     const int nhot = hot_count[0];
     for (;;) {
@@ -1414,16 +1640,16 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64
         const int hi = claim;
         if (hi >= nhot) break;
         const int64_t slot = hot_list[hi];
-        sp_accum_hot_one(rows, base, slot / rows.NB, slot % rows.NB, dst_arr, val_arr, raw_arr, raw_local,
+        sp_accum_hot_one(rows, base, slot / rows.NB, slot % rows.NB, dst_arr, val_arr, raw_local,
                          out_count, kb, val, cnt, acc, bits, wpre, scan_lds);
     }
 }
 
 __device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__restrict__ base, int64_t r, int64_t bk,
                                  int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
-                                 const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local,
+                                 int32_t *__restrict__ raw_local,
                                  int32_t *__restrict__ out_count, uint32_t (*kb)[SP_CHUNK], float *val,
-                                 uint16_t (*cnt)[SP_NT], float *acc, uint32_t *bits, int *wpre, int *scan_lds) {
+                                 uint16_t *cnt, float *acc, uint32_t *bits, int *wpre, int *scan_lds) {
     int64_t start, end;
     sp_bucket_range(rows, base, r, bk, &start, &end);
     const int64_t n = end - start;
@@ -1438,7 +1664,7 @@ __device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__r
         sp_regs_to_lds<SP_CHUNK_IPT>(pd, pv, kb, val);
         if (c0 + SP_CHUNK < n) sp_chunk_regs<SP_CHUNK_IPT>(dst_arr, val_arr, start, c0 + SP_CHUNK, n, pd, pv);
         __syncthreads();
-        const uint32_t *key = sp_block_sort<SP_CHUNK_IPT>(kb[0], kb[1], 11, 16, cnt, scan_lds);
+        const uint32_t *key = sp_block_sort<SP_CHUNK_IPT>(kb[0], kb[1], 11, 14, cnt, scan_lds);
         const float *sv = sp_sorted_values<SP_CHUNK_IPT>(key, kb, val);
         for (int j = 0; j < SP_CHUNK_IPT; ++j) {
             const int p = t * SP_CHUNK_IPT + j;
@@ -1462,7 +1688,7 @@ __device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__r
             const int32_t d = dst_arr[start + k];
             if (d < 0) continue;  // hole
             const int dl = d & (SP_W - 1);
-            raw_local[raw_arr ? raw_arr[start + k] : start + k] =
+            raw_local[start + k] =
                 wpre[dl >> 5] + __popc(bits[dl >> 5] & ((1u << (dl & 31)) - 1u));
         }
         __syncthreads();
@@ -1485,8 +1711,8 @@ __device__ __forceinline__ void sp_accum_hot_one(SpRows rows, const int64_t *__r
 // winning item is the largest value (zeros of either sign equal), then the
 // smallest tie key (ORI < INV < identity, then the original edge id), then
 // the earliest raw item; outputs are compacted in destination order as for
-// the sum, with the winning value (+0 for a zero), and raw_local[raw] = the
-// output index of winners, -1 for the other items.
+// the sum, with the winning value (+0 for a zero), and raw_local[the item's
+// position] = the output index of winners, -1 for the other items.
 //   k_sp_max      buckets of at most SP_CHUNK items: stable LDS sort by
 //                 destination, the first thread of every run scans it;
 //   k_sp_max_hot  larger buckets: dense LDS arrays over the bucket's 8192
@@ -1501,8 +1727,8 @@ __device__ __forceinline__ float fl_order_key_inv(uint32_t k) {
 template <int IPT>
 __device__ __forceinline__ void sp_max_one(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
                            float *__restrict__ val_arr, const uint32_t *__restrict__ tie_arr,
-                           const int32_t *__restrict__ raw_arr, int32_t *__restrict__ raw_local, int32_t *out_count,
-                           uint32_t (*kb)[SP_CHUNK], float *val, uint32_t *tie, uint16_t (*cnt)[SP_NT],
+                           int32_t *__restrict__ raw_local, int32_t *out_count,
+                           uint32_t (*kb)[SP_CHUNK], float *val, uint32_t *tie, uint16_t *cnt,
                            int *scan_lds) {
     constexpr int SIZE = SP_NT * IPT;
     const int t = threadIdx.x;
@@ -1534,7 +1760,7 @@ __device__ __forceinline__ void sp_max_one(int64_t start, int64_t n, int32_t dba
         if (raw_local)
             for (int q = p; q < e; ++q) {
                 const int idx = (int)(key[q] & 2047u);
-                raw_local[raw_arr ? raw_arr[start + idx] : start + idx] = idx == bi ? rank : -1;
+                raw_local[start + idx] = idx == bi ? rank : -1;
             }
         dst_arr[start + rank] = dbase + (int32_t)(key[p] >> 11);
         val_arr[start + rank] = bv;
@@ -1546,13 +1772,12 @@ __device__ __forceinline__ void sp_max_one(int64_t start, int64_t n, int32_t dba
 __global__ __launch_bounds__(SP_NT) void k_sp_max(SpRows rows, const int64_t *__restrict__ base,
                                                  int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
                                                  const uint32_t *__restrict__ tie_arr,
-                                                 const int32_t *__restrict__ raw_arr,
                                                  int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count,
                                                  int32_t *__restrict__ hot_list, int32_t *__restrict__ hot_count) {
     __shared__ __align__(16) uint32_t kb[2][SP_CHUNK];
     __shared__ float val[SP_CHUNK];
     __shared__ uint32_t tie[SP_CHUNK];
-    __shared__ uint16_t cnt[16][SP_NT];
+    __shared__ uint16_t cnt[SP_SORT_TAB];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
     const int64_t r = blockIdx.x / rows.NB, bk = blockIdx.x - (blockIdx.x / rows.NB) * rows.NB;
     int64_t start, end;
@@ -1569,24 +1794,22 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max(SpRows rows, const int64_t *__
     }
     const int32_t dbase = (int32_t)(bk << SP_S);
     if (n <= SP_NT * 2)
-        sp_max_one<2>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
+        sp_max_one<2>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
     else if (n <= SP_NT * 4)
-        sp_max_one<4>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
+        sp_max_one<4>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
     else
-        sp_max_one<8>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
+        sp_max_one<8>(start, n, dbase, dst_arr, val_arr, tie_arr, raw_local, oc, kb, val, tie, cnt, scan_lds);
 }
 
 __device__ __forceinline__ void sp_max_hot_one(SpRows rows, const int64_t *__restrict__ base, int64_t r, int64_t bk,
                                int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
-                               const uint32_t *__restrict__ tie_arr, const int32_t *__restrict__ raw_arr,
-                               int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count, uint32_t *vbest,
+                               const uint32_t *__restrict__ tie_arr, int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count, uint32_t *vbest,
                                unsigned long long *tbest, uint32_t *bits, int *wpre, int *scan_lds);
 
 // Persistent grid over the list of hot buckets collected by k_sp_max.
 __global__ __launch_bounds__(SP_NT) void k_sp_max_hot(SpRows rows, const int64_t *__restrict__ base,
                                                      int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
                                                      const uint32_t *__restrict__ tie_arr,
-                                                     const int32_t *__restrict__ raw_arr,
                                                      int32_t *__restrict__ raw_local,
                                                      int32_t *__restrict__ out_count,
                                                      const int32_t *__restrict__ hot_list,
@@ -1596,7 +1819,6 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max_hot(SpRows rows, const int64_t
     __shared__ uint32_t bits[SP_W / 32];
     __shared__ int wpre[SP_W / 32];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
-    // hot_count[0]: listed buckets; hot_count[1]: next bucket to claim
     __shared__ int claim;
     const int nhot = hot_count[0];
     for (;;) {
@@ -1606,15 +1828,14 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max_hot(SpRows rows, const int64_t
         const int hi = claim;
         if (hi >= nhot) break;
         const int64_t slot = hot_list[hi];
-        sp_max_hot_one(rows, base, slot / rows.NB, slot % rows.NB, dst_arr, val_arr, tie_arr, raw_arr, raw_local,
+        sp_max_hot_one(rows, base, slot / rows.NB, slot % rows.NB, dst_arr, val_arr, tie_arr, raw_local,
                        out_count, vbest, tbest, bits, wpre, scan_lds);
     }
 }
 
 __device__ __forceinline__ void sp_max_hot_one(SpRows rows, const int64_t *__restrict__ base, int64_t r, int64_t bk,
                                int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
-                               const uint32_t *__restrict__ tie_arr, const int32_t *__restrict__ raw_arr,
-                               int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count, uint32_t *vbest,
+                               const uint32_t *__restrict__ tie_arr, int32_t *__restrict__ raw_local, int32_t *__restrict__ out_count, uint32_t *vbest,
                                unsigned long long *tbest, uint32_t *bits, int *wpre, int *scan_lds) {
     int64_t start, end;
     sp_bucket_range(rows, base, r, bk, &start, &end);
@@ -1654,7 +1875,7 @@ __device__ __forceinline__ void sp_max_hot_one(SpRows rows, const int64_t *__res
             if (d < 0) continue;
             const int dl = d & (SP_W - 1);
             const int o = wpre[dl >> 5] + __popc(bits[dl >> 5] & ((1u << (dl & 31)) - 1u));
-            raw_local[raw_arr ? raw_arr[start + k] : start + k] = (uint32_t)tbest[dl] == (uint32_t)k ? o : -1;
+            raw_local[start + k] = (uint32_t)tbest[dl] == (uint32_t)k ? o : -1;
         }
         __syncthreads();
     }
@@ -1683,7 +1904,7 @@ __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows
                                                   const int64_t *__restrict__ out_base, int64_t *__restrict__ ob,
                                                   int64_t *__restrict__ ol, int64_t *__restrict__ oe,
                                                   float *__restrict__ ov) {
-    const int64_t slot = (int64_t)blockIdx.x * SP_EMIT_WAVES + threadIdx.x / FL_WAVE;
+    const int64_t slot = fl_xcd_contig(blockIdx.x, gridDim.x) * SP_EMIT_WAVES + threadIdx.x / FL_WAVE;
     if (slot >= nslot) return;
     const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
     const int64_t o0 = out_base[slot];
@@ -1715,12 +1936,15 @@ __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows
 // are read only with several buckets (then holes of the sum become -1);
 // with one, holes keep an unspecified index and the backward skips them by
 // their mask.  Workgroup per tile of a row, as k_sp_hist.
+
 constexpr int SP_LTO_NB = 2048;  // buckets per row kept in LDS by k_sp_local_to_out
 
 __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows rows, const int32_t *__restrict__ raw_dst,
                                                           const int64_t *__restrict__ out_base,
+                                                          const int32_t *__restrict__ part_inv,
+                                                          const int32_t *__restrict__ part_local,
                                                           int32_t *__restrict__ raw_local) {
-    const int64_t tile = blockIdx.x;
+    const int64_t tile = fl_xcd_contig(blockIdx.x, gridDim.x);
     const int64_t r = sp_tile_row(rows.tile_base, R, tile);
     const int64_t tl = tile - rows.tile_base[r];
     const int64_t i0 = rows.row_item0[r] + tl * SP_TILE;
@@ -1737,11 +1961,18 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
 #pragma unroll 4
     for (int idx = threadIdx.x; idx < c; idx += SP_NT) {
         const int64_t k = i0 + idx;
-        const int32_t loc = raw_local[k];
-        if (rows.NB > 1) {
+        if (part_inv) {
+            // partitioned: the local index sits at the item's partition position
+            // (holes were not partitioned)
             const int32_t d = raw_dst[k];
-            raw_local[k] = (loc >= 0 && d >= 0) ? (int32_t)((lds ? obase[d >> SP_S] : orow[d >> SP_S]) + loc) : -1;
+            int32_t o = -1;
+            if (d >= 0) {
+                const int32_t loc = part_local[part_inv[k]];
+                if (loc >= 0) o = (int32_t)((lds ? obase[d >> SP_S] : orow[d >> SP_S]) + loc);
+            }
+            raw_local[k] = o;
         } else {
+            const int32_t loc = raw_local[k];
             raw_local[k] = loc >= 0 ? (int32_t)(orow[0] + loc) : -1;
         }
     }
@@ -2371,10 +2602,10 @@ SpPlan sp_plan_layout(int64_t nnz, int64_t R, int64_t r_size, char *base) {
 
 // expansion workspace layout
 struct SpExp {
-    int32_t *raw_dst, *part_dst, *part_raw, *hist, *out_count;
+    int32_t *raw_dst, *part_dst, *part_inv, *hist, *out_count;
     float *raw_val, *part_val;
     uint32_t *raw_tie, *part_tie;
-    int32_t *hot_list, *mid_list, *hot_count;
+    int32_t *hot_list, *mid_list, *hot_fb, *mid_fb, *hot_count;
     int64_t *base, *tmp;
     SpRuns runs;
     size_t bytes;
@@ -2413,9 +2644,11 @@ SpExp sp_exp_layout(int64_t T, int64_t tiles, int64_t chunks, int64_t R, int64_t
     x.tmp = (int64_t *)take(scan_tmp_bytes(mx + 1));
     x.hot_list = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
     x.mid_list = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
-    x.hot_count = (int32_t *)take(4 * sizeof(int32_t));
+    x.hot_fb = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
+    x.mid_fb = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
+    x.hot_count = (int32_t *)take(8 * sizeof(int32_t));
     // last, so that every other offset is the same with and without it
-    if (NB > 1 && backward) x.part_raw = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
+    if (NB > 1 && backward) x.part_inv = (int32_t *)take(sizeof(int32_t) * (size_t)T1);
     x.bytes = off;
     return x;
 }
@@ -2716,7 +2949,7 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
             FL_LAUNCH("k_sp_items", (k_sp_items<false, false>), dim3(grid), dim3(SP_ITEMS_NT), 0, st, *ori, *inv,
                       h->chunks, x.runs, holes, x.raw_dst, x.raw_val, x.raw_tie, rp, rc16);
     }
-    int32_t *dst_arr = x.raw_dst, *raw_arr = nullptr;
+    int32_t *dst_arr = x.raw_dst;
     float *val_arr = x.raw_val;
     uint32_t *tie_arr = x.raw_tie;
     if (NB > 1) {
@@ -2726,39 +2959,48 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         if ((rc = exclusive_scan(st, x.hist, x.base, h->tiles * NB, x.tmp)) != FL_OK) return rc;
         if (h->tiles > 0)
             FL_LAUNCH("k_sp_partition", k_sp_partition, dim3((unsigned)h->tiles), dim3(SP_NT), 0, st, R, rows,
-                      sp_bucket_bits(NB), x.base, x.raw_dst, x.raw_val, x.part_dst, x.part_val,
-                      raw_local ? x.part_raw : (int32_t *)nullptr, x.raw_tie, x.part_tie);
+                      sp_bucket_bits(NB + 1), x.base, x.raw_dst, x.raw_val, x.part_dst, x.part_val,
+                      raw_local ? x.part_inv : (int32_t *)nullptr, x.raw_tie, x.part_tie);
         dst_arr = x.part_dst;
         val_arr = x.part_val;
         tie_arr = x.part_tie;
-        raw_arr = raw_local ? x.part_raw : nullptr;
     }
+    // with a backward the accumulation kernels write each item's output index
+    // within its bucket at the item's position: the raw map itself when the
+    // items were not partitioned, else a partition-order array in the raw
+    // value array (dead after the partition), mapped back by k_sp_local_to_out
+    int32_t *acc_local = raw_local && NB > 1 ? reinterpret_cast<int32_t *>(x.raw_val) : raw_local;
     // hot buckets (more than one LDS chunk) are listed by the first kernel
     // and taken by a persistent grid of the second
     const unsigned hot_grid = (unsigned)(R * NB < SP_HOT_GRID ? R * NB : SP_HOT_GRID);
     if (R * NB > 0)
-        FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, x.hot_count, (int64_t)4, 0);
+        FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, x.hot_count, (int64_t)8, 0);
     if (R * NB > 0 && mx) {
         FL_LAUNCH("k_sp_max", k_sp_max, dim3((unsigned)(R * NB)), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
-                  val_arr, tie_arr, raw_arr, raw_local, x.out_count, x.hot_list, x.hot_count);
+                  val_arr, tie_arr, acc_local, x.out_count, x.hot_list, x.hot_count);
         FL_LAUNCH("k_sp_max_hot", k_sp_max_hot, dim3(hot_grid), dim3(SP_NT), 0, st, rows, x.base, dst_arr, val_arr,
-                  tie_arr, raw_arr, raw_local, x.out_count, x.hot_list, x.hot_count);
+                  tie_arr, acc_local, x.out_count, x.hot_list, x.hot_count);
     } else if (R * NB > 0) {
         const int64_t nslot = R * NB;
         FL_LAUNCH("k_sp_accum_small", k_sp_accum_small,
                   dim3((unsigned)((nslot + SP_SMALL_WAVES - 1) / SP_SMALL_WAVES)), dim3(SP_NT), 0, st, rows, x.base,
-                  dst_arr, val_arr, raw_arr, raw_local, x.out_count, nslot, x.hot_list, x.mid_list, x.hot_count);
+                  dst_arr, val_arr, acc_local, x.out_count, nslot, x.hot_list, x.mid_list, x.hot_count);
+        // buckets of more than SP_WB items: few destinations here, the rest
+        // on the fallback lists
+        FL_LAUNCH("k_sp_accum_few", k_sp_accum_few, dim3((unsigned)(nslot < SP_MID_GRID ? nslot : SP_MID_GRID)),
+                  dim3(SP_NT), 0, st, rows, x.base, dst_arr, val_arr, acc_local, x.out_count, x.hot_list,
+                  x.mid_list, x.hot_fb, x.mid_fb, x.hot_count);
         FL_LAUNCH("k_sp_accum_mid", k_sp_accum_mid, dim3((unsigned)(nslot < SP_MID_GRID ? nslot : SP_MID_GRID)),
-                  dim3(SP_NT), 0, st, rows, x.base, dst_arr, val_arr, raw_arr, raw_local, x.out_count, x.mid_list,
-                  x.hot_count);
+                  dim3(SP_NT), 0, st, rows, x.base, dst_arr, val_arr, acc_local, x.out_count, x.mid_fb,
+                  x.hot_count + 6);
         FL_LAUNCH("k_sp_accum_hot", k_sp_accum_hot, dim3(hot_grid), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
-                  val_arr, raw_arr, raw_local, x.out_count, x.hot_list, x.hot_count);
+                  val_arr, acc_local, x.out_count, x.hot_fb, x.hot_count + 4);
     }
     if ((rc = exclusive_scan(st, x.out_count, out_base, R * NB, x.tmp)) != FL_OK) return rc;
     // the backward's map: each raw item's output index
     if (raw_local && h->tiles > 0)
         FL_LAUNCH("k_sp_local_to_out", k_sp_local_to_out, dim3((unsigned)h->tiles), dim3(SP_NT), 0, st, R, rows,
-                  x.raw_dst, out_base, raw_local);
+                  x.raw_dst, out_base, NB > 1 ? x.part_inv : (const int32_t *)nullptr, acc_local, raw_local);
     return fl_check_launch("sparse_expand");
 }
 
