@@ -58,7 +58,78 @@ def parse():
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="first run 3 plain device copies of this many MiB (a known-size reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--counter-steps", type=int, default=0,
+                    help="--sparse: run exactly this many steps and stop (a rocprofv3 counter pass; "
+                         "no timing, no CPU baseline)")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "STEPS", "OUT"),
+                    help="write the per-step HBM traffic summary of two rocprofv3 counter passes "
+                         "(FETCH_SIZE, then WRITE_SIZE, each over --copy-mb 256 --counter-steps STEPS)")
     return ap.parse_args()
+
+
+def _pmc_per_kernel(path, counter):
+    """{kernel: (dispatches, [values])} of one counter in a rocprofv3
+    counter_collection.csv (a dispatch's value summed over its rows)."""
+    import collections
+    import csv
+    per = collections.defaultdict(dict)
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            if (row.get("Counter_Name") or row.get("Counter-Name")) != counter:
+                continue
+            name = (row.get("Kernel_Name") or row.get("Kernel-Name") or "").replace("(anonymous namespace)::", "")
+            name = name.split("(")[0]
+            name = name.replace("void ", "").split("<")[0].split("::")[-1]
+            disp = row.get("Dispatch_Id") or row.get("Dispatch-Id")
+            per[name][disp] = per[name].get(disp, 0.0) + float(row.get("Counter_Value") or 0.0)
+    return {k: list(v.values()) for k, v in per.items()}
+
+
+def pmc_summary(fetch_csv, write_csv, steps, out_path):
+    """Per kernel: HBM MB per step = (FETCH_SIZE, WRITE_SIZE in KiB per
+    dispatch, each scaled by the ratio of the bytes a plain 256 MiB device
+    copy moves to what the counter reads for it) summed over the kernel's
+    dispatches / steps.  Kernels dispatched fewer times than there are steps
+    (once per run) are listed apart."""
+    fe = _pmc_per_kernel(fetch_csv, "FETCH_SIZE")
+    wr = _pmc_per_kernel(write_csv, "WRITE_SIZE")
+    copy = [k for k in fe if "copyBuffer" in k]
+    cf = max(max(fe[k]) for k in copy)
+    cw = max(max(wr[k]) for k in copy if k in wr)
+    ff, fw = 262144.0 / cf, 262144.0 / cw
+    rows = []
+    for k in fe:
+        if "copyBuffer" in k or not k.startswith("k_"):
+            continue
+        mb = (sum(fe[k]) * ff + sum(wr.get(k, [])) * fw) * 1024 / 1e6
+        rows.append((mb / steps, k, len(fe[k])))
+    rows.sort(reverse=True)
+    lines = ["# HBM traffic per step of this library's kernels, C5 sparse training step",
+             "",
+             "Two rocprofv3 counter passes over `--counter-steps %d` (from the repo root, on one MI355X):" % steps,
+             "",
+             "    cd /tmp && rocprofv3 --pmc FETCH_SIZE --output-format csv -d /tmp/p_fetch -o run -- "
+             "python3 <repo>/bench.py --copy-mb 256 --counter-steps %d" % steps,
+             "    cd /tmp && rocprofv3 --pmc WRITE_SIZE --output-format csv -d /tmp/p_write -o run -- "
+             "python3 <repo>/bench.py --copy-mb 256 --counter-steps %d" % steps,
+             "    python3 <repo>/bench.py --pmc-summary <fetch counter_collection.csv> "
+             "<write counter_collection.csv> %d <this file>" % steps,
+             "",
+             "Copy calibration: a 256 MiB device copy reads FETCH_SIZE %.1f KiB and WRITE_SIZE %.1f KiB; "
+             "scale factors to bytes %.3f (fetch) and %.3f (write)." % (cf, cw, ff, fw),
+             "",
+             "Per-step kernels (name, MB per step, dispatches in the run):", ""]
+    once = []
+    for mb, k, d in rows:
+        if d < steps:
+            once.append((mb * steps, k, d))
+            continue
+        lines.append("%s %.1f" % (k, mb))  # "<kernel> <MB per step>" lines are read by bench.py
+    lines += ["", "Once-per-run kernels (MB in the run, dispatches):", ""]
+    lines += ["    %s: %.1f MB, %d" % (k, mb, d) for mb, k, d in once]
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("wrote", out_path)
 
 
 def copy_calibration(mb):
@@ -145,6 +216,9 @@ def hop_pull_bytes(Ap, w, csr, R, K, out_bytes=8):
 
 def main():
     args = parse()
+    if args.pmc_summary:
+        fetch_csv, write_csv, steps, out = args.pmc_summary
+        return pmc_summary(fetch_csv, write_csv, int(steps), out)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(every (query, channel) row is independent, so batches would shard by query)",
@@ -650,13 +724,74 @@ SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_
                   "k_cs_rank", "k_cs_emit"]
 
 
-def items_bytes(plan):
-    """Algorithmic bytes of one k_sp_items launch (the CSR gather of the kept
-    edges): per raw item the column and mask read and the (destination,
-    value) item written, 16 B, + 6 B of CSR position and attention column
-    with a backward.  The run and chunk tables the kernel also reads are not
-    counted (conservative)."""
-    return (16 + (6 if plan["backward"] else 0)) * plan["items"]
+# The sparse hop's own kernels (forward and backward), without the c1 entity
+# selection, the normalizer and the channel sums that surround it in a step.
+HOP_EXCLUDE = ("k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_race_select", "k_fill_from",
+               "k_norm_fwd", "k_norm_bwd", "k_cs_rank", "k_cs_emit")
+HOP_KERNELS = [k for k in SPARSE_KERNELS if k not in HOP_EXCLUDE]
+
+
+def sparse_hop_bytes(plan):
+    """Algorithmic bytes of one sparse sum hop, forward and (with a backward)
+    backward, by the sparse formulas of the measurement plan:
+      forward  28 nnz_in + 4 BL n + sum over sides and entries (8 + 10 g(src)
+               + 9 kept) + 28 nnz_out
+      backward 28 nnz_in + 4 nnz_out + 8 BL n + sum (8 + 10 g + 13 kept)
+               + 4 nnz_in
+    with nnz_in the entries after c1, g the source's groups on a side and
+    kept its kept edges (the raw items less the identity items)."""
+    nnz, rows, n, nout, groups = plan["nnz"], plan["rows"], plan["n"], plan["nout"], plan["groups"]
+    kept = plan["items"] - (0 if plan["wot_i"] else nnz)
+    fwd = 28 * nnz + 4 * rows * n + 16 * nnz + 10 * groups + 9 * kept + 28 * nout
+    if not plan["backward"]:
+        return fwd
+    bwd = 28 * nnz + 4 * nout + 8 * rows * n + 16 * nnz + 10 * groups + 13 * kept + 4 * nnz
+    return fwd + bwd
+
+
+def item_kernel_bytes(plans):
+    """Algorithmic bytes per step of the kernels whose work is linear in the
+    raw items, summed over the step's hops (per raw item: k_sp_items reads
+    the column and mask and writes the destination and value, 16 B, + 6 B of
+    CSR position and attention column with a backward; k_sp_hist reads the
+    destination, 4 B; k_sp_partition reads destination and value and writes
+    them in bucket order, 16 B, + 4 B of the item's bucket position with a
+    backward; k_sp_local_to_out reads the destination, that position and
+    the bucket-order output index and writes the raw-order one, 16 B;
+    k_sp_bwd reads CSR position, column and output index and the output's
+    gradient, 14 B)."""
+    out = {"k_sp_items": 0, "k_sp_hist": 0, "k_sp_partition": 0, "k_sp_local_to_out": 0, "k_sp_bwd": 0}
+    for p in plans:
+        it, bw = p["items"], p["backward"]
+        out["k_sp_items"] += (16 + (6 if bw else 0)) * it
+        out["k_sp_hist"] += 4 * it
+        out["k_sp_partition"] += (16 + (4 if bw else 0)) * it
+        if bw:
+            out["k_sp_local_to_out"] += 16 * it
+            out["k_sp_bwd"] += 14 * it
+    return out
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sparse_hop_c5_train_traffic_per_step.txt")
+
+
+def measured_traffic(kernels):
+    """HBM bytes per step of the given kernels from the committed counter
+    summary (lines "<kernel> <MB per step>"), or None when it is absent or
+    lacks one of them."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    mb = {}
+    for line in open(TRAFFIC_FILE):
+        parts = line.split()
+        if len(parts) == 2 and parts[0].startswith("k_"):
+            try:
+                mb[parts[0]] = float(parts[1])
+            except ValueError:
+                pass
+    if not mb:
+        return None
+    return sum(mb.get(k, 0.0) for k in kernels) * 1e6
 
 
 def main_sparse(args):
@@ -744,6 +879,13 @@ def main_sparse(args):
         return loss
 
     ctx = torch.enable_grad() if train else torch.inference_mode()
+    if args.counter_steps > 0:
+        with ctx:
+            for _ in range(args.counter_steps):
+                step()
+            torch.cuda.synchronize()
+        print("counter run: %d %s steps" % (args.counter_steps, args.mode), file=sys.stderr, flush=True)
+        return
     with ctx:
         for _ in range(args.warmup):
             step()
@@ -795,10 +937,19 @@ def main_sparse(args):
     csr_np = [c.cpu().numpy() for c in csr]
     cpu = (cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W.cpu(), T, train)
            if args.cpu_seconds > 0 else None)
-    fb = [items_bytes(p) for p in plans]
-    items_ms = per_launch["k_sp_items"]
-    bytes_per_launch = float(np.mean(fb))
-    achieved = bytes_per_launch / (items_ms * 1e-3) / 1e9 if items_ms > 0 else 0.0
+    # roofline of the whole hop: the hop formula's bytes of the step's hops over
+    # the live time of the hop's kernels (HIP events around each launch)
+    step_bytes = float(sum(sparse_hop_bytes(p) for p in plans))
+    hop_ms = sum(per_step[k] for k in HOP_KERNELS)
+    achieved = step_bytes / (hop_ms * 1e-3) / 1e9 if hop_ms > 0 else 0.0
+    traffic = measured_traffic(HOP_KERNELS)
+    kernel_rooflines = {}
+    for k, b in item_kernel_bytes(plans).items():
+        if per_step.get(k, 0.0) > 0 and b > 0:
+            a = b / (per_step[k] * 1e-3) / 1e9
+            kernel_rooflines[k] = {"achieved": a, "frac": a / HBM_PEAK_GBS, "algorithmic_bytes_per_step": b,
+                                   "ms_per_step": per_step[k], "traffic": measured_traffic([k])}
+    dominant = max(per_step, key=lambda k: per_step[k])
     result = {
         "metric": "queries/sec for L=3 propagation + % of HBM roofline; top-k select ms",
         "value": B / (ms_step * 1e-3),
@@ -823,9 +974,13 @@ def main_sparse(args):
                            "c2_per_hop": per_launch["k_sp_select"]},
         "kernel_ms_per_launch": per_launch,
         "kernel_ms_per_step": per_step,
-        "roofline": {"kernel": "k_sp_items", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None},
+        "roofline": {"kernel": "sparse hop (its forward and backward kernels, per step)", "bound": "hbm",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "algorithmic_bytes_per_launch": step_bytes, "ms_per_launch": hop_ms,
+                     "traffic": traffic,
+                     "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if traffic is not None else None},
+        "dominant_kernel": {"name": dominant, "ms_per_step": per_step[dominant]},
+        "kernel_rooflines": kernel_rooflines,
         "hop_plans": plans,
         "cpu_baseline": cpu,
     }

@@ -903,8 +903,10 @@ def _entry_order(sp_e):
     return torch.argsort(sp_e).to(torch.int32)
 
 
-# When a list, every sparse hop appends its plan's sizes to it as
-# {"nnz", "items", "chunks", "backward"} (for byte counts in measurements).
+# When a list, every sparse hop appends its sizes to it as {"nnz" (entries
+# after c1), "items" (raw items), "chunks", "backward", "nout" (output
+# entries), "groups" (the entries' sources' groups over both sides), "rows"
+# (B*L), "n" (attention width), "wot_i"} (for byte counts in measurements).
 plan_log = None
 
 
@@ -973,8 +975,6 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
             raise ValueError("sparse state index out of range for shape (%d, %d, %d)" % (B, L, E))
         break
     h.items, h.tiles, h.chunks = items, tiles, chunks
-    if plan_log is not None:
-        plan_log.append({"nnz": nnz, "items": items, "chunks": chunks, "backward": bool(need_backward)})
     ws2_bytes = lib.fl_sparse_expand_bytes(items, tiles, chunks, R, E, 1 if need_backward else 0, int(aggregate))
     ws2 = torch.empty(max(ws2_bytes, 1), dtype=torch.uint8, device=dev)
     h.ws2, h.ws2_bytes = ptr(ws2).value, ws2.numel()
@@ -988,6 +988,12 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     check(lib.fl_sparse_expand(st, ctypes.byref(sides.ori), ctypes.byref(sides.inv), ctypes.byref(h),
                                ptr(out_base), ptr(raw_local) if need_backward else None), "sparse_expand")
     nout = int(out_base[-1])
+    if plan_log is not None:
+        # sizes for byte counts: the groups the entries' sources hold on both sides
+        go, gi = sides.keep[2].long(), sides.keep[11].long()
+        groups = int((go[sp_e + 1] - go[sp_e] + gi[sp_e + 1] - gi[sp_e]).sum()) if nnz else 0
+        plan_log.append({"nnz": nnz, "items": items, "chunks": chunks, "backward": bool(need_backward),
+                         "nout": nout, "groups": groups, "rows": R, "n": n, "wot_i": bool(wot_i)})
     idx = torch.empty((3, nout), dtype=torch.int64, device=dev)
     vals = torch.empty(nout, dtype=torch.float32, device=dev)
     check(lib.fl_sparse_emit(st, ctypes.byref(h), ptr(out_base), ptr(idx[0]), ptr(idx[1]), ptr(idx[2]),
