@@ -162,14 +162,22 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
         int rl[4];
         int32_t cl[4];
         float wl[4];
+        // loads at clamped indices (every one issued, none behind a branch);
+        // groups past the side's end are zeroed
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int64_t g = gb + u * FL_WAVE + lane;
-            rl[u] = g < g1 ? s.group_rel[g] : 0;
-            cl[u] = g < g1 ? s.group_count[g] : 0;
+            const int64_t gc = g < g1 ? g : g1 - 1;
+            rl[u] = s.group_rel[gc];
+            cl[u] = s.group_count[gc];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) wl[u] = gb + u * FL_WAVE + lane < g1 ? wr[rl[u]] : 0.0f;
+        for (int u = 0; u < 4; ++u) {
+            const bool in = gb + u * FL_WAVE + lane < g1;
+            const float wraw = wr[rl[u]];
+            wl[u] = in ? wraw : 0.0f;
+            cl[u] = in ? cl[u] : 0;
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const float wv = wl[u];
@@ -221,14 +229,22 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
         int rl[4];
         int32_t cl[4];
         float wl[4];
+        // loads at clamped indices (every one issued, none behind a branch);
+        // groups past the side's end are zeroed
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int64_t g = gb + u * FL_WAVE + lane;
-            rl[u] = g < g1 ? s.group_rel[g] : 0;
-            cl[u] = g < g1 ? s.group_count[g] : 0;
+            const int64_t gc = g < g1 ? g : g1 - 1;
+            rl[u] = s.group_rel[gc];
+            cl[u] = s.group_count[gc];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) wl[u] = gb + u * FL_WAVE + lane < g1 ? wr[rl[u]] : 0.0f;
+        for (int u = 0; u < 4; ++u) {
+            const bool in = gb + u * FL_WAVE + lane < g1;
+            const float wraw = wr[rl[u]];
+            wl[u] = in ? wraw : 0.0f;
+            cl[u] = in ? cl[u] : 0;
+        }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             if (wl[u] > 0.0f && cl[u] > 0) alloc += sp_quota_base(tk, wl[u], cl[u]);
@@ -289,31 +305,34 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
     const int lane = fl_lane();
     int64_t base = 0;
     // the next window's group records are requested before this window's
-    // weights are gathered and its takes computed
+    // weights are gathered and its takes computed; records at clamped
+    // indices (loads issued unconditionally), groups past the end zeroed
+    const int64_t glast = g1 - 1;
     int rel = 0;
     int32_t start = 0, cnt = 0;
-    if (g0 + lane < g1) {
-        rel = s.group_rel[g0 + lane];
-        start = s.group_start[g0 + lane];
-        cnt = s.group_count[g0 + lane];
+    if (g1 > g0) {
+        const int64_t gc = g0 + lane < g1 ? g0 + lane : glast;
+        rel = s.group_rel[gc];
+        start = s.group_start[gc];
+        cnt = s.group_count[gc];
     }
     for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
         const int64_t g = gb + lane, gn = g + FL_WAVE;
         int reln = 0;
         int32_t startn = 0, cntn = 0;
-        if (gn < g1) {
-            reln = s.group_rel[gn];
-            startn = s.group_start[gn];
-            cntn = s.group_count[gn];
+        if (gb + FL_WAVE < g1) {
+            const int64_t gc = gn < g1 ? gn : glast;
+            reln = s.group_rel[gc];
+            startn = s.group_start[gc];
+            cntn = s.group_count[gc];
         }
-        int64_t take = 0;
-        float wv = 0.0f;
-        if (g < g1) {
-            wv = wr[rel];
-            take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? group_take(wv, tk.th, tk.cut, start, cnt) : 0);
-        }
+        const bool in = g < g1;
+        const float wraw = wr[rel];
+        const float wv = in ? wraw : 0.0f;
+        if (!in) cnt = 0;
+        int64_t take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? group_take(wv, tk.th, tk.cut, start, cnt) : 0);
         if (Q && tk.kind == TAKE_QUOTA)
-            take = sp_quota_window(tk, wv, cnt, g < g1);
+            take = sp_quota_window(tk, wv, cnt, in);
         if (__ballot(take > 0) != 0) {
             const long long incl = fl_wave_incl_scan_i64(take);
             fn((long long)take, (int64_t)start, rel, wv, (long long)(base + incl - take));
@@ -526,6 +545,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
             uint32_t key;
             int32_t cc;
             bool quota = false;
+            long long eligible = -1;
             if (K < 0) {
                 thv = __int_as_float(0x7f800000);  // budget <= 0: no edge is kept
             } else if (QS && K > 0 && seed >= 0) {
@@ -535,12 +555,15 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
                     thv = __int_as_float(0x7fc00000);
                     if (lane == 0) qout[2 * i + dir] = q;
                 }
+                eligible = q.cap;  // without quotas every eligible edge is kept
             } else if (K > 0 && c2_select(s, g0, g1, wr, K, hist_all[wid], &key, &cc)) {
                 thv = __uint_as_float(key);
                 ct = cc;
             }
             if (quota) {
                 c = lane == 0 ? K : 0;
+            } else if (eligible >= 0) {
+                c = lane == 0 ? eligible : 0;
             } else {
                 // kept edges, masked ones included
                 for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
