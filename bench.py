@@ -717,6 +717,7 @@ def main_rules(args):
 
 SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_race_select", "k_fill_from",
                   "k_sp_rowptr", "k_sp_relorder", "k_sp_select", "k_sp_rowinfo", "k_sp_runs", "k_sp_items",
+                  "k_sp_expand_fused",
                   "k_sp_hist",
                   "k_sp_partition", "k_sp_accum_small", "k_sp_accum_few", "k_sp_accum_mid", "k_sp_accum_hot", "k_sp_emit", "k_sp_local_to_out",
                   "k_norm_fwd", "k_norm_bwd", "k_sp_bwd", "k_fill_f32", "k_scan_tiles", "k_scan_totals",

@@ -866,6 +866,148 @@ __global__ __launch_bounds__(SP_ITEMS_NT) void k_sp_items(fl_side ori, fl_side i
     }
 }
 
+// Fused run writer and item pass for budgeted (top-k) hops, whose entries
+// have at most 2K+1 items: wave per entry, the entry's runs (as k_sp_runs
+// writes them) kept in the wave's LDS instead of a global run table, then
+// the entry's items written 64 at a time as k_sp_items writes a chunk (the
+// runs starting inside the round marked in LDS, the owner of slot k the
+// number of marks at 1..k).  rcap: runs per wave the dynamic LDS holds.
+constexpr int64_t SP_FUSE_KMAX = 256;  // budgets whose runs fit the fused kernel's LDS
+
+struct SpLdsRuns {
+    int32_t *first, *p;
+    float *aw;
+    uint32_t *meta;
+};
+
+template <bool Q, bool MAXT, bool BWD>
+__global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
+    fl_side ori, fl_side inv, const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
+    const int64_t *__restrict__ se, const float *__restrict__ sv, int64_t nnz, const float *__restrict__ w, int64_t L,
+    int64_t n, int64_t r_size, int wot_i, int mode, int64_t seed, const float *__restrict__ th,
+    const int32_t *__restrict__ cut, const SpQuota *__restrict__ quota, const int64_t *__restrict__ item_off,
+    const int32_t *__restrict__ order, int rcap, int holes, int32_t *__restrict__ raw_dst, float *__restrict__ raw_val,
+    uint32_t *__restrict__ raw_tie, int32_t *__restrict__ raw_pos, int16_t *__restrict__ raw_col) {
+    extern __shared__ __align__(16) unsigned char fused_lds[];
+    __shared__ uint8_t mark_all[SEL_NT / FL_WAVE][SP_ICHUNK];
+    const int lane = fl_lane();
+    const int wid = threadIdx.x / FL_WAVE;
+    uint8_t *mark = mark_all[wid];
+    SpLdsRuns ru;
+    {
+        unsigned char *b = fused_lds + (size_t)wid * rcap * 16;
+        ru.first = reinterpret_cast<int32_t *>(b);
+        ru.p = reinterpret_cast<int32_t *>(b + (size_t)rcap * 4);
+        ru.aw = reinterpret_cast<float *>(b + (size_t)rcap * 8);
+        ru.meta = reinterpret_cast<uint32_t *>(b + (size_t)rcap * 12);
+    }
+    const int64_t wv_i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + wid;
+    if (wv_i >= nnz) return;  // no block barrier follows
+    const int64_t i = order ? (int64_t)order[wv_i] : wv_i;
+    if (i < 0 || i >= nnz) return;
+    const int64_t src = se[i];
+    const int64_t r = sb[i] * L + sl[i];
+    const float a = sv[i];
+    const float *wrow = w + r * n;
+    const int64_t base = item_off[i];
+    const int64_t nitems = item_off[i + 1] - base;
+    // the plan's item count bounds every run (the walk reproduces it)
+    const int64_t lim = nitems - (wot_i ? 0 : 1);
+    int64_t pos = 0, rix = 0;  // within the entry
+    const uint64_t below = (1ull << lane) - 1;
+    for (int dir = 0; dir < 2; ++dir) {
+        const fl_side &s = dir ? inv : ori;
+        const float *wr = wrow + (dir ? r_size : 0);
+        const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
+        SpTake tk = sp_take<Q>(mode, th[2 * i + dir], cut[2 * i + dir], quota + 2 * i + dir, seed, sb[i], sl[i], src,
+                               dir);
+        const uint32_t side = dir ? SP_RUN_INV : 0u;
+        const uint32_t col0 = dir ? (uint32_t)r_size : 0u;
+        pos += sp_side_runs<Q>(s, g0, g1, wr, tk, [&](long long take, int64_t start, int rel, float wv, long long ex) {
+            const uint64_t m = __ballot(take > 0);
+            const int64_t ri = rix + __popcll(m & below);
+            const int64_t o = pos + ex;
+            if (take > 0 && o + take <= lim && ri < rcap) {
+                ru.first[ri] = (int32_t)o;
+                ru.p[ri] = (int32_t)start;
+                ru.aw[ri] = fl_mul(a, wv);
+                ru.meta[ri] = side | (col0 + (uint32_t)rel);
+            }
+            rix += __popcll(m);
+        });
+    }
+    if (!wot_i && lane == 0 && pos == lim && rix < rcap) {
+        ru.first[rix] = (int32_t)lim;
+        ru.p[rix] = (int32_t)src;
+        ru.aw[rix] = fl_mul(a, wrow[n - 1]);
+        ru.meta[rix] = SP_RUN_ID | (uint32_t)(n - 1);
+    }
+    int64_t nr = rix + (wot_i ? 0 : 1);
+    if (nr > rcap) nr = rcap;
+    fl_wave_sync();
+    const uint64_t upto = lane == FL_WAVE - 1 ? ~0ull : ((2ull << lane) - 1);
+    int64_t r0 = 0;  // the run holding the round's first item
+    for (int64_t q0 = 0; q0 < nitems; q0 += SP_ICHUNK) {
+        const int64_t rj = r0 + lane;
+        int32_t d = SP_ICHUNK, rp = 0;
+        float aw = 0.0f;
+        uint32_t rm = 0;
+        if (rj < nr) {
+            const int64_t f = (int64_t)ru.first[rj] - q0;
+            d = f < SP_ICHUNK ? (int32_t)f : SP_ICHUNK;
+            rp = ru.p[rj];
+            aw = ru.aw[rj];
+            rm = ru.meta[rj];
+        }
+        mark[lane] = 0;
+        fl_wave_sync();
+        if (lane > 0 && d > 0 && d < SP_ICHUNK) mark[d] = 1;
+        fl_wave_sync();
+        const uint64_t starts = __ballot(mark[lane] != 0);
+        const int j = __popcll(starts & upto);
+        const int32_t dj = __shfl(d, j, FL_WAVE);
+        const int32_t pj = __shfl(rp, j, FL_WAVE) + (lane - dj);
+        const float awj = __shfl(aw, j, FL_WAVE);
+        const uint32_t mj = (uint32_t)__shfl((int)rm, j, FL_WAVE);
+        // the next round's first item: in the last run that started here, or
+        // in the run starting right at it
+        r0 += __popcll(starts);
+        if (r0 + 1 < nr && (int64_t)ru.first[r0 + 1] <= q0 + SP_ICHUNK) ++r0;
+        fl_wave_sync();  // marks read before the next round clears them
+        const int64_t it = q0 + lane;
+        if (it >= nitems) continue;
+        const int64_t k = base + it;
+        int32_t dst = -1, pp = -1;
+        float val = 0.0f;
+        uint32_t tie = SP_TIE_IDENTITY;
+        if (mj & SP_RUN_ID) {
+            dst = pj;
+            val = awj;
+        } else {
+            const bool inv_side = (mj & SP_RUN_INV) != 0;
+            const int64_t edges = inv_side ? inv.edges : ori.edges;
+            const float *mk = inv_side ? inv.mask : ori.mask;
+            const uint32_t *mb = inv_side ? inv.mask_bits : ori.mask_bits;
+            const int32_t *ci = inv_side ? inv.col_ind : ori.col_ind;
+            if (pj >= 0 && pj < edges) {
+                const float m = sp_mask_at(mb, mk, pj);
+                const int32_t e = ci[pj];
+                dst = (!holes || m != 0.0f) ? e : -1;
+                val = fl_mul(awj, m);
+                if (MAXT) tie = (inv_side ? SP_TIE_INV : 0u) | (uint32_t)(inv_side ? inv.order : ori.order)[pj];
+                pp = pj;
+            }
+        }
+        raw_dst[k] = dst;
+        raw_val[k] = val;
+        if (MAXT) raw_tie[k] = tie;
+        if (BWD) {
+            raw_pos[k] = pp;
+            raw_col[k] = (int16_t)(mj & SP_RUN_COL);
+        }
+    }
+}
+
 // Row of a tile: the r with tile_base[r] <= tile < tile_base[r+1].
 __device__ __forceinline__ int64_t sp_tile_row(const int64_t *tile_base, int64_t R, int64_t tile) {
     int64_t lo = 0, hi = R;  // invariant: tile_base[lo] <= tile < tile_base[hi]
@@ -2948,7 +3090,22 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     if (nnz > 0 && h->mode == SP_FIXED)
         FL_LAUNCH("k_fx_fill", k_fx_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_e, h->sp_v, nnz, p.cut, p.item_off, x.raw_dst, x.raw_val);
-    else if (nnz > 0 && h->items > 0 && h->chunks > 0) {
+    else if (nnz > 0 && h->items > 0 && sp_budget(h) > 0 && sp_budget(h) <= SP_FUSE_KMAX) {
+        // budgeted hop: at most 2K+1 items (and runs) per entry, kept in LDS
+        const int holes = h->mode == SP_TOPK && h->aggregate == SP_SUM;
+        const int rcap = (int)(2 * sp_budget(h) + 2);
+        const size_t lds = (size_t)(SEL_NT / FL_WAVE) * (size_t)rcap * 16;
+        const dim3 grid((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE)));
+        int32_t *rp = raw_local ? h->raw_pos : (int32_t *)nullptr;
+        int16_t *rc16 = raw_local ? h->raw_col : (int16_t *)nullptr;
+        auto kern = sp_quotas(h) ? (mx ? (raw_local ? k_sp_expand_fused<true, true, true> : k_sp_expand_fused<true, true, false>)
+                                       : (raw_local ? k_sp_expand_fused<true, false, true> : k_sp_expand_fused<true, false, false>))
+                                 : (mx ? (raw_local ? k_sp_expand_fused<false, true, true> : k_sp_expand_fused<false, true, false>)
+                                       : (raw_local ? k_sp_expand_fused<false, false, true> : k_sp_expand_fused<false, false, false>));
+        FL_LAUNCH("k_sp_expand_fused", kern, grid, dim3(SEL_NT), lds, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_e,
+                  h->sp_v, nnz, h->w, h->L, h->n, h->r_size, h->wot_i, h->mode, h->sampling_seed, p.th, p.cut,
+                  p.quota, p.item_off, h->entry_order, rcap, holes, x.raw_dst, x.raw_val, x.raw_tie, rp, rc16);
+    } else if (nnz > 0 && h->items > 0 && h->chunks > 0) {
         FL_LAUNCH("k_sp_runs", sp_quotas(h) ? k_sp_runs<true> : k_sp_runs<false>,
                   dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))), dim3(SEL_NT), 0, st, *ori,
                   *inv, h->sp_b, h->sp_l, h->sp_e, h->sp_v, nnz, h->w, h->L, h->n, h->r_size, h->wot_i, h->mode,
