@@ -860,7 +860,7 @@ __global__ __launch_bounds__(SP_ITEMS_NT) void k_sp_items(fl_side ori, fl_side i
         raw_val[k] = val;
         if (MAXT) raw_tie[k] = tie;
         if (BWD) {
-            raw_pos[k] = pos;
+            if (raw_pos) raw_pos[k] = pos;
             raw_col[k] = (int16_t)(mj & SP_RUN_COL);
         }
     }
@@ -1002,7 +1002,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
         raw_val[k] = val;
         if (MAXT) raw_tie[k] = tie;
         if (BWD) {
-            raw_pos[k] = pp;
+            if (raw_pos) raw_pos[k] = pp;
             raw_col[k] = (int16_t)(mj & SP_RUN_COL);
         }
     }
@@ -2272,8 +2272,10 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
     float gsp = 0.0f;
     int32_t p = -1, loc = -1;
     int col = -1;
+    // without positions every kept item has mask 1 (the holes, the masked
+    // items, carry output index -1) and there are no edge factors
     if (k0 + lane < k1) {
-        p = raw_pos[k0 + lane];
+        p = raw_pos ? raw_pos[k0 + lane] : -1;
         col = raw_col[k0 + lane];
         loc = raw_out[k0 + lane];
     }
@@ -2282,7 +2284,7 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
         int32_t pn = -1, locn = -1;
         int coln = -1;
         if (kn < k1) {
-            pn = raw_pos[kn];
+            pn = raw_pos ? raw_pos[kn] : -1;
             coln = raw_col[kn];
             locn = raw_out[kn];
         }
@@ -2980,6 +2982,14 @@ static int64_t sp_budget(const fl_sparse_hop *h);
 static int64_t sp_rsize(const fl_sparse_hop *h) { return h->mode == SP_FIXED ? 0 : h->r_size; }
 // Training quotas can apply (sampling seed, top-k mode, a positive budget).
 static bool sp_quotas(const fl_sparse_hop *h) { return h->sampling_seed >= 0 && sp_budget(h) > 0; }
+// The backward reads an item's CSR position only for its mask value and edge
+// factor.  It does without them for the top-k sum over several buckets per
+// row (masked items are holes with output index -1, kept items have mask 1
+// when every mask is a bitmap) with no edge factors.
+static bool sp_pos_optional(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h) {
+    const auto side_ok = [](const fl_side *s) { return (!s->mask || s->mask_bits) && !s->dscore; };
+    return h->mode == SP_TOPK && h->aggregate == SP_SUM && sp_buckets(h->E) > 1 && side_ok(ori) && side_ok(inv);
+}
 
 int fl_sparse_plan(void *stream, const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, int64_t *plan) {
     int rc;
@@ -3075,7 +3085,7 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         fl_sparse_expand_bytes(h->items, h->tiles, h->chunks, R, h->E, raw_local != nullptr, h->aggregate))
         return fl_fail(FL_ERR_ARG, "sparse_expand: workspace too small");
     if (raw_local && h->mode != SP_FIXED && h->items > 0) {
-        if (!h->raw_pos || !h->raw_col)
+        if (!h->raw_col || (!h->raw_pos && !sp_pos_optional(ori, inv, h)))
             return fl_fail(FL_ERR_ARG, "sparse_expand: raw_local needs raw_pos and raw_col");
         if (h->n > 32767) return fl_fail(FL_ERR_ARG, "sparse_expand: backward columns need n <= 32767");
         if (h->items > INT32_MAX) return fl_fail(FL_ERR_ARG, "sparse_expand: backward output indices need items < 2^31");
@@ -3240,8 +3250,10 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
     int rc;
     if ((rc = sp_check(ori, inv, h, "sparse_backward")) != FL_OK) return rc;
     if (!h->ws1 || !out_base || !grad_v || !grad_w) return fl_fail(FL_ERR_ARG, "sparse_backward: null argument");
-    if (h->items > 0 && (!raw_local || !grad_out || !h->raw_pos || !h->raw_col))
+    if (h->items > 0 && (!raw_local || !grad_out || !h->raw_col || (!h->raw_pos && !sp_pos_optional(ori, inv, h))))
         return fl_fail(FL_ERR_ARG, "sparse_backward: null raw map (raw_local, raw_pos, raw_col)");
+    if (h->items > 0 && !h->raw_pos && (ori->grad_edge || inv->grad_edge))
+        return fl_fail(FL_ERR_ARG, "sparse_backward: edge-weight gradients need raw_pos");
     if (h->mode == SP_FIXED) return fl_fail(FL_ERR_ARG, "sparse_backward: the fixed-relation step has no backward");
     const int64_t R = h->B * h->L;
     if (!workspace || workspace_bytes < fl_sparse_backward_bytes(h->nnz, R, h->n))

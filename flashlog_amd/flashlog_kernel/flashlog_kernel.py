@@ -862,6 +862,15 @@ class _SparseSides:
         self.ori.grad_edge = p
         self.inv.grad_edge = p
 
+    def positions_optional(self, mode, aggregate, buckets):
+        """True when the backward reads no item's CSR position: the top-k
+        sum over several destination buckets (masked items are dropped and
+        carry no output index), every mask a bitmap (kept items have mask 1)
+        and no edge-weight factors."""
+        def ok(s):
+            return (not s.mask or s.mask_bits) and not s.dscore
+        return mode == _SPARSE_TOPK and aggregate == _SPARSE_SUM and buckets > 1 and ok(self.ori) and ok(self.inv)
+
     def _side(self, col, mask, gptr, grel, gstart, gcount, order=None, dscore=None, bits=None):
         _require_cuda(col, gptr, grel, gstart, gcount)
         col = col.int().contiguous()
@@ -982,9 +991,11 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     raw_local = torch.empty(max(items, 1), dtype=torch.int32, device=dev) if need_backward else None
     raw_pos = raw_col = None
     if need_backward:
-        raw_pos = torch.empty(max(items, 1), dtype=torch.int32, device=dev)
+        if not sides.positions_optional(mode, aggregate, nb):
+            raw_pos = torch.empty(max(items, 1), dtype=torch.int32, device=dev)
         raw_col = torch.empty(max(items, 1), dtype=torch.int16, device=dev)
-        h.raw_pos, h.raw_col = ptr(raw_pos).value, ptr(raw_col).value
+        h.raw_pos = ptr(raw_pos).value if raw_pos is not None else None
+        h.raw_col = ptr(raw_col).value
     check(lib.fl_sparse_expand(st, ctypes.byref(sides.ori), ctypes.byref(sides.inv), ctypes.byref(h),
                                ptr(out_base), ptr(raw_local) if need_backward else None), "sparse_expand")
     nout = int(out_base[-1])

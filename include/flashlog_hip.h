@@ -302,7 +302,13 @@ typedef struct fl_sparse_hop {
     int32_t *raw_pos;                  /* with raw_local (fl_sparse_expand):
                                           [items] receives every raw item's
                                           CSR position in its side (-1 for
-                                          the identity item)                */
+                                          the identity item).  May be null
+                                          when the backward reads no mask
+                                          value or edge factor: the top-k
+                                          sum (masked items are dropped)
+                                          with E > 8192, each side's mask
+                                          absent or given as mask_bits, and
+                                          no side carrying dscore.          */
     int16_t *raw_col;                  /* with raw_local: [items] receives its
                                           attention column (ORI relation,
                                           r_size + INV relation, n - 1 for the

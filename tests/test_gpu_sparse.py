@@ -339,3 +339,44 @@ def test_sparse_backward_is_deterministic(mode):
         (out.values() * g).sum().backward()
         grads.append((vt.grad.clone(), wt.grad.clone()))
     assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+
+
+def test_backward_without_positions_matches(monkeypatch):
+    """The top-k sum over several destination buckets with bitmap masks keeps
+    no item CSR positions for its backward; its gradients are the same bits
+    as those of the backward that reads them."""
+    from oracle import oracle as Oc
+    fk = _fk()
+    rng = np.random.default_rng(23)
+    E, R, M = 30000, 4, 80000
+    h = rng.integers(0, E, M)
+    t = np.where(rng.random(M) < 0.3, 777, rng.integers(0, E, M))
+    r = rng.integers(0, R, M)
+    csr = Oc.build_csr_structure(h, t, r, E)
+    n = 2 * R + 1
+    B, L = 3, 2
+    state = sparse_coo_state(B, L, E, 900, rng)
+    w = attention(B * L, n, rng).reshape(B, L, n)
+    mbool, masks = masks_for(csr, M, rng, drop=0.2)
+    seen = []
+    orig = fk._SparseSides.positions_optional
+
+    def spy(self, *a):
+        seen.append(orig(self, *a))
+        return seen[-1]
+
+    grads = []
+    for force in (False, True):
+        monkeypatch.setattr(fk._SparseSides, "positions_optional",
+                            spy if not force else (lambda self, *a: False))
+        out, vt, wt = _topk(state, w, csr, mbool, B, L, E, R, 5, grad=True)
+        g = torch.from_numpy(np.random.default_rng(4).standard_normal(out._nnz()).astype(np.float32)).cuda()
+        (out.values() * g).sum().backward()
+        grads.append((vt.grad.clone(), wt.grad.clone()))
+    assert seen == [True]
+    assert torch.equal(grads[0][0], grads[1][0]) and torch.equal(grads[0][1], grads[1][1])
+    keys = _keys(out.indices().detach(), L, E)
+    gv_ref, gw_ref = O.sparse_backward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, keys,
+                                       g.cpu().numpy(), False, 5)
+    assert_grad_close(grads[0][0].cpu().numpy(), gv_ref)
+    assert_grad_close(grads[0][1].reshape(B * L, n).cpu().numpy(), gw_ref)
