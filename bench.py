@@ -64,7 +64,70 @@ def parse():
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "STEPS", "OUT"),
                     help="write the per-step HBM traffic summary of two rocprofv3 counter passes "
                          "(FETCH_SIZE, then WRITE_SIZE, each over --copy-mb 256 --counter-steps STEPS)")
+    ap.add_argument("--counter-table", nargs="+", metavar="ARG",
+                    help="OUT CSV [CSV ...]: write the per-dispatch means of every counter in these "
+                         "rocprofv3 counter_collection.csv files (one per pass over --counter-steps) for "
+                         "the sparse hop kernels, as a markdown table")
     return ap.parse_args()
+
+
+def _pmc_counters(path):
+    """Names of the counters in a rocprofv3 counter_collection.csv."""
+    import csv
+    with open(path) as f:
+        return sorted({row.get("Counter_Name") or row.get("Counter-Name") for row in csv.DictReader(f)})
+
+
+def counter_table(out_path, csvs):
+    """Per sparse hop kernel: dispatches and the mean over its dispatches
+    of every counter of the passes (a dispatch's value summed over its
+    rows), with two derived columns where their counters were collected:
+    LDS bank-conflict cycles per LDS-active cycle and VALU instructions per
+    wave."""
+    cols = {}
+    for path in csvs:
+        for c in _pmc_counters(path):
+            cols[c] = _pmc_per_kernel(path, c)
+    names = [k for k in SPARSE_KERNELS if any(k in per for per in cols.values())]
+    counters = sorted(cols)
+    head = ["kernel", "dispatches"] + counters
+    derived = []
+    for active in ("SQ_LDS_IDX_ACTIVE", "SQ_ACTIVE_INST_LDS"):
+        if "SQ_LDS_BANK_CONFLICT" in cols and active in cols:
+            derived.append(("LDS conflict / %s" % active, "SQ_LDS_BANK_CONFLICT", active))
+            break
+    if "SQ_INSTS_VALU" in cols and "SQ_WAVES" in cols:
+        derived.append(("VALU insts / wave", "SQ_INSTS_VALU", "SQ_WAVES"))
+    head += [d[0] for d in derived]
+    lines = ["# Counters per dispatch of the sparse hop kernels, C5 sparse training step", "",
+             "One rocprofv3 pass per counter set over `--counter-steps` (from the repo root, on one MI355X), "
+             "then this table:", ""]
+    for i, path in enumerate(csvs):
+        lines.append("    cd /tmp && rocprofv3 --pmc %s --output-format csv -d /tmp/p_%d -o run -- "
+                     "python3 <repo>/bench.py --counter-steps 3" % (" ".join(_pmc_counters(path)), i))
+    lines += ["    python3 <repo>/bench.py --counter-table <this file> "
+              + " ".join("<pass %d counter_collection.csv>" % i for i in range(len(csvs))), "",
+              "Means over each kernel's dispatches (all hops of the run); a dispatch's value is summed "
+              "over the counter's instances.", ""]
+    lines += ["| " + " | ".join(head) + " |", "|" + "---|" * len(head)]
+
+    def mean(c, k):
+        v = cols[c].get(k)
+        return sum(v) / len(v) if v else None
+
+    for k in names:
+        disp = max(len(cols[c].get(k, [])) for c in counters)
+        row = [k, str(disp)]
+        for c in counters:
+            m = mean(c, k)
+            row.append("-" if m is None else ("%.4g" % m))
+        for _, a, b in derived:
+            x, y = mean(a, k), mean(b, k)
+            row.append("%.3f" % (x / y) if x is not None and y else "-")
+        lines.append("| " + " | ".join(row) + " |")
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("wrote", out_path)
 
 
 def _pmc_per_kernel(path, counter):
@@ -219,6 +282,10 @@ def main():
     if args.pmc_summary:
         fetch_csv, write_csv, steps, out = args.pmc_summary
         return pmc_summary(fetch_csv, write_csv, int(steps), out)
+    if args.counter_table:
+        if len(args.counter_table) < 2:
+            sys.exit("--counter-table needs OUT and at least one CSV")
+        return counter_table(args.counter_table[0], args.counter_table[1:])
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(every (query, channel) row is independent, so batches would shard by query)",

@@ -128,6 +128,10 @@ __device__ __forceinline__ double fl_uniform_f64(double x) {
     return __longlong_as_double(fl_uniform_i64(__double_as_longlong(x)));
 }
 
+// The wave's index within its workgroup, in a scalar register (so that
+// per-wave indices, and loads at them, stay scalar).
+__device__ __forceinline__ int fl_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / FL_WAVE)); }
+
 // Float key that orders like the value (ascending) for every non-NaN float.
 __device__ __forceinline__ uint32_t fl_order_key(float v) {
     uint32_t u = __float_as_uint(v);

@@ -282,13 +282,15 @@ __device__ __forceinline__ long long sp_quota_window(SpTake &tk, float wv, long 
     const int lane = fl_lane();
     const bool el = valid && wv > 0.0f && cnt > 0;
     const long long base = el ? sp_quota_base(tk, wv, cnt) : 0;
-    const long long spare = el ? cnt - base : 0;
-    const long long incl = fl_wave_incl_scan_i64(spare);
-    const long long cum = sp_quota_cum(tk, tk.prefix + incl);
-    const long long prev = fl_wave_shr1_i64(cum);
-    const long long extra = cum - (lane == 0 ? tk.cum : prev);
-    tk.prefix += fl_readlane_i64(incl, FL_WAVE - 1);
-    tk.cum = fl_readlane_i64(cum, FL_WAVE - 1);
+    // 32-bit lanes: a window's spares add up to at most the source's edges on
+    // the side (CSR positions are int32) and cum stays within the residual
+    const int32_t spare = el ? (int32_t)(cnt - base) : 0;
+    const int32_t incl = fl_wave_incl_scan_i32(spare);
+    const int32_t cum = (int32_t)sp_quota_cum(tk, tk.prefix + incl);
+    const int32_t prev = fl_dpp<0x138>(cum);  // wave_shr:1
+    const long long extra = (long long)cum - (lane == 0 ? tk.cum : (long long)prev);
+    tk.prefix += __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
+    tk.cum = __builtin_amdgcn_readlane(cum, FL_WAVE - 1);
     return el ? base + extra : 0;
 }
 
@@ -334,9 +336,10 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
         if (Q && tk.kind == TAKE_QUOTA)
             take = sp_quota_window(tk, wv, cnt, in);
         if (__ballot(take > 0) != 0) {
-            const long long incl = fl_wave_incl_scan_i64(take);
+            // a window's takes add up to at most the source's edges (int32)
+            const int32_t incl = fl_wave_incl_scan_i32((int32_t)take);
             fn((long long)take, (int64_t)start, rel, wv, (long long)(base + incl - take));
-            base += fl_readlane_i64(incl, FL_WAVE - 1);
+            base += __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
         }
         rel = reln;
         start = startn;
@@ -498,7 +501,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, 
     __shared__ int hist_all[SEL_NT / FL_WAVE][256];
     extern __shared__ int cmap_all[];  // [SEL_NT / FL_WAVE][r_size] when the map is used
     const int lane = fl_lane();
-    const int wid = threadIdx.x / FL_WAVE;
+    const int wid = fl_wave_id();
     const int64_t wv_i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + wid;
     // entries visited in the given order (by source entity: neighbouring
     // waves read the same group records), results stored by entry
@@ -636,7 +639,7 @@ __global__ __launch_bounds__(SEL_NT) void k_fx_fill(fl_side ori, fl_side inv, co
                                                    const int64_t *__restrict__ item_off,
                                                    int32_t *__restrict__ raw_dst, float *__restrict__ raw_val) {
     const int lane = fl_lane();
-    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
+    const int64_t i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + fl_wave_id();
     if (i >= nnz) return;
     const int64_t pos = item_off[i];
     const int64_t c = item_off[i + 1] - pos;
@@ -726,7 +729,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_runs(fl_side ori, fl_side inv, co
                                                    const int64_t *__restrict__ chunk_off,
                                                    const int32_t *__restrict__ order, SpRuns ru) {
     const int lane = fl_lane();
-    const int64_t wv_i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + threadIdx.x / FL_WAVE;
+    const int64_t wv_i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + fl_wave_id();
     if (wv_i >= nnz) return;
     // entry visited in the plan's order; its chunks follow that order
     const int64_t i = order ? (int64_t)order[wv_i] : wv_i;
@@ -801,10 +804,10 @@ __global__ __launch_bounds__(SP_ITEMS_NT) void k_sp_items(fl_side ori, fl_side i
                                                          int16_t *__restrict__ raw_col) {
     __shared__ uint8_t mark_all[SP_ITEMS_NT / FL_WAVE][SP_ICHUNK];
     const int lane = fl_lane();
-    uint8_t *mark = mark_all[threadIdx.x / FL_WAVE];
+    uint8_t *mark = mark_all[fl_wave_id()];
     const int64_t waves = (int64_t)gridDim.x * (SP_ITEMS_NT / FL_WAVE);
     const uint64_t upto = lane == FL_WAVE - 1 ? ~0ull : ((2ull << lane) - 1);
-    for (int64_t c = (int64_t)blockIdx.x * (SP_ITEMS_NT / FL_WAVE) + threadIdx.x / FL_WAVE; c < nchunks; c += waves) {
+    for (int64_t c = (int64_t)blockIdx.x * (SP_ITEMS_NT / FL_WAVE) + fl_wave_id(); c < nchunks; c += waves) {
         const int64_t base = fl_uniform_i64(ru.c_base[c]);
         const int64_t r0 = fl_uniform_i64(ru.c_run[c]);
         const int64_t rlim = fl_uniform_i64(ru.c_rlim[c]);
@@ -891,7 +894,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
     extern __shared__ __align__(16) unsigned char fused_lds[];
     __shared__ uint8_t mark_all[SEL_NT / FL_WAVE][SP_ICHUNK];
     const int lane = fl_lane();
-    const int wid = threadIdx.x / FL_WAVE;
+    const int wid = fl_wave_id();
     uint8_t *mark = mark_all[wid];
     SpLdsRuns ru;
     {
@@ -1075,7 +1078,7 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
     constexpr int PER = SP_ND * SPAN / SP_NT;         // scanned entries per thread
     const int t = threadIdx.x;
     const int lane = fl_lane();
-    const int w = t / FL_WAVE;
+    const int w = fl_wave_id();
     uint16_t *tab = cnt, *nxt = cnt + TAB;
     for (int q = t; q < TAB; q += SP_NT) tab[q] = 0;
     __syncthreads();
@@ -1527,7 +1530,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
     __shared__ __align__(16) uint32_t kb[SP_SMALL_WAVES][2][SP_WB];
     __shared__ float val[SP_SMALL_WAVES][SP_WB];
     __shared__ uint16_t cnt[SP_SMALL_WAVES][16][FL_WAVE];
-    const int w = threadIdx.x / FL_WAVE;
+    const int w = fl_wave_id();
     const int64_t slot = fl_xcd_contig(blockIdx.x, gridDim.x) * SP_SMALL_WAVES + w;
     if (slot >= nslots) return;  // no block barrier follows
     const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
@@ -1620,7 +1623,7 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
                                            int *scan_lds) {
     const int t = threadIdx.x;
     const int lane = fl_lane();
-    const int w = t / FL_WAVE;
+    const int w = fl_wave_id();
     for (int q = t; q < SP_FEW_TAB; q += SP_NT) tab[0][q] = 0;
     float acc = 0.0f;  // thread t < total: the sum of slot t
     int32_t pd[SP_FEW_IPT];
@@ -2069,7 +2072,7 @@ __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows
                                                   const int64_t *__restrict__ out_base, int64_t *__restrict__ ob,
                                                   int64_t *__restrict__ ol, int64_t *__restrict__ oe,
                                                   float *__restrict__ ov) {
-    const int64_t slot = fl_xcd_contig(blockIdx.x, gridDim.x) * SP_EMIT_WAVES + threadIdx.x / FL_WAVE;
+    const int64_t slot = fl_xcd_contig(blockIdx.x, gridDim.x) * SP_EMIT_WAVES + fl_wave_id();
     if (slot >= nslot) return;
     const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
     const int64_t o0 = out_base[slot];
@@ -2228,7 +2231,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
     const int64_t r = lo;
     const int64_t e0 = row_ptr[r] + (blk - chunk_ptr[r]) * BW_CH;
     const int64_t e1 = e0 + BW_CH < row_ptr[r + 1] ? e0 + BW_CH : row_ptr[r + 1];
-    const int wid = threadIdx.x / FL_WAVE;
+    const int wid = fl_wave_id();
     float *rows = USE_LDS ? bw_rows : wave_rows + blk * BW_WAVES * n;
     for (int64_t q = threadIdx.x; q < BW_WAVES * n; q += SEL_NT) rows[q] = 0.0f;
     __syncthreads();
