@@ -164,8 +164,9 @@ def pmc_summary(fetch_csv, write_csv, steps, out_path):
     for k in fe:
         if "copyBuffer" in k or not k.startswith("k_"):
             continue
-        mb = (sum(fe[k]) * ff + sum(wr.get(k, [])) * fw) * 1024 / 1e6
-        rows.append((mb / steps, k, len(fe[k])))
+        f_mb = sum(fe[k]) * ff * 1024 / 1e6
+        w_mb = sum(wr.get(k, [])) * fw * 1024 / 1e6
+        rows.append(((f_mb + w_mb) / steps, k, len(fe[k]), f_mb / steps, w_mb / steps))
     rows.sort(reverse=True)
     lines = ["# HBM traffic per step of this library's kernels, C5 sparse training step",
              "",
@@ -181,13 +182,14 @@ def pmc_summary(fetch_csv, write_csv, steps, out_path):
              "Copy calibration: a 256 MiB device copy reads FETCH_SIZE %.1f KiB and WRITE_SIZE %.1f KiB; "
              "scale factors to bytes %.3f (fetch) and %.3f (write)." % (cf, cw, ff, fw),
              "",
-             "Per-step kernels (name, MB per step, dispatches in the run):", ""]
+             "Per-step kernels (name, MB per step, then its fetched and written MB):", ""]
     once = []
-    for mb, k, d in rows:
+    for mb, k, d, f_mb, w_mb in rows:
         if d < steps:
             once.append((mb * steps, k, d))
             continue
-        lines.append("%s %.1f" % (k, mb))  # "<kernel> <MB per step>" lines are read by bench.py
+        # "<kernel> <MB per step> ..." lines are read by bench.py
+        lines.append("%s %.1f (fetch %.1f, write %.1f)" % (k, mb, f_mb, w_mb))
     lines += ["", "Once-per-run kernels (MB in the run, dispatches):", ""]
     lines += ["    %s: %.1f MB, %d" % (k, mb, d) for mb, k, d in once]
     with open(out_path, "w") as f:
@@ -845,14 +847,14 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sparse_hop_c5_train_traffic_per_s
 
 def measured_traffic(kernels):
     """HBM bytes per step of the given kernels from the committed counter
-    summary (lines "<kernel> <MB per step>"), or None when it is absent or
-    lacks one of them."""
+    summary (lines "<kernel> <MB per step> ..."), or None when it is absent
+    or lacks one of them."""
     if not os.path.exists(TRAFFIC_FILE):
         return None
     mb = {}
     for line in open(TRAFFIC_FILE):
         parts = line.split()
-        if len(parts) == 2 and parts[0].startswith("k_"):
+        if len(parts) >= 2 and parts[0].startswith("k_"):
             try:
                 mb[parts[0]] = float(parts[1])
             except ValueError:

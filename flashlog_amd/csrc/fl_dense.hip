@@ -302,7 +302,7 @@ __global__ __launch_bounds__(C2_NT) void k_c2_hard(fl_side ori, fl_side inv, con
                                                    int32_t *__restrict__ CUT) {
     __shared__ int hist_all[C2_NT / FL_WAVE][256];
     const int lane = fl_lane();
-    const int wid = threadIdx.x / FL_WAVE;
+    const int wid = fl_wave_id();
     int *hist = hist_all[wid];
     const int64_t nwaves = (int64_t)gridDim.x * (C2_NT / FL_WAVE);
     const int64_t total = *hard_count;

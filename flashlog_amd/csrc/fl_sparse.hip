@@ -1607,7 +1607,8 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64
 // wave and round with ballots (as sp_block_sort does, one 6-bit pass), the
 // values are scattered slot-major into LDS in raw order within each slot, and
 // thread j adds its slot's run to its sum, in order.  raw_local (partition
-// order) gets each item's slot, written in place.
+// order) gets each item's slot, written in place.  Holes (destination -1:
+// with one bucket per row the bucket is the row's raw items) are skipped.
 constexpr int SP_FEW = 64;
 constexpr int SP_FEW_RB = 6;
 constexpr int SP_FEW_IPT = SP_CHUNK / SP_NT;               // 8
@@ -1639,10 +1640,12 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
     for (int64_t c0 = 0; c0 < n; c0 += SP_CHUNK) {
         uint8_t sl[SP_FEW_IPT], rk[SP_FEW_IPT];
         float vv[SP_FEW_IPT];
+        uint32_t okm = 0;  // bit j: item j exists and is no hole
 #pragma unroll
         for (int j = 0; j < SP_FEW_IPT; ++j) {
             const int64_t k = c0 + (int64_t)j * SP_NT + t;
-            const bool valid = k < n;
+            const bool valid = k < n && pd[j] >= 0;
+            okm |= valid ? 1u << j : 0u;
             int sj = 0;
             if (valid) {
                 const int dl = pd[j] & (SP_W - 1);
@@ -1692,8 +1695,7 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < SP_FEW_IPT; ++j) {
-            if (c0 + (int64_t)j * SP_NT + t < n)
-                sv[tab[cur][sl[j] * (SP_FEW_SPAN + 1) + j * SP_NWV + w] + rk[j]] = vv[j];
+            if (okm & (1u << j)) sv[tab[cur][sl[j] * (SP_FEW_SPAN + 1) + j * SP_NWV + w] + rk[j]] = vv[j];
         }
         __syncthreads();
         if (t < total) {
@@ -1749,10 +1751,22 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_few(SpRows rows, const int64
         const int64_t n = end - start;
         bits[t] = 0;
         __syncthreads();
-#pragma unroll 8
-        for (int64_t k = t; k < n; k += SP_NT) {
-            const int dl = dst_arr[start + k] & (SP_W - 1);
-            atomicOr(&bits[dl >> 5], 1u << (dl & 31));
+        // 8 loads in flight per thread, then the marks; a bit already set
+        // (the common case: few destinations) is read, not written again
+        for (int64_t k0 = t; k0 < n; k0 += 8 * SP_NT) {
+            int32_t dv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t k = k0 + (int64_t)u * SP_NT;
+                dv[u] = k < n ? dst_arr[start + k] : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (dv[u] < 0) continue;
+                const int dl = dv[u] & (SP_W - 1);
+                const uint32_t b = 1u << (dl & 31);
+                if (!(bits[dl >> 5] & b)) atomicOr(&bits[dl >> 5], b);
+            }
         }
         __syncthreads();
         const uint32_t word = bits[t];
@@ -2220,8 +2234,11 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
                                                   const float *__restrict__ grad, float *__restrict__ grad_v,
                                                   float *__restrict__ wave_rows, float *__restrict__ part) {
     extern __shared__ float bw_rows[];  // [BW_WAVES][n] when USE_LDS
-    const int64_t blk = blockIdx.x;
-    if (blk >= chunk_ptr[R]) return;  // the grid is an upper bound of the chunk count
+    const int64_t nblk = chunk_ptr[R];
+    if ((int64_t)blockIdx.x >= nblk) return;  // the grid is an upper bound of the chunk count
+    // chunks in contiguous ranges per XCD: the gradient rows a range reads
+    // stay in that XCD's L2
+    const int64_t blk = fl_xcd_contig(blockIdx.x, nblk);
     // the block's row: chunk_ptr[r] <= blk < chunk_ptr[r + 1]
     int64_t lo = 0, hi = R;
     while (hi - lo > 1) {

@@ -380,3 +380,43 @@ def test_backward_without_positions_matches(monkeypatch):
                                        g.cpu().numpy(), False, 5)
     assert_grad_close(grads[0][0].cpu().numpy(), gv_ref)
     assert_grad_close(grads[0][1].reshape(B * L, n).cpu().numpy(), gw_ref)
+
+
+@pytest.mark.parametrize("E", [5000, 30000])
+def test_few_destinations_with_holes(E):
+    """Rows whose items (well above one wave's 512) go to a handful of
+    destinations, with a quarter of the kept edges masked (holes of the
+    top-k sum): the few-destination accumulation, with one bucket per row
+    (holes among the row's raw items) and with several."""
+    from oracle import oracle as Oc
+    rng = np.random.default_rng(31)
+    R = 40
+    srcs = np.arange(6)
+    tgts = np.array([7, 11, 12, 300, 2047, E - 1])
+    h = np.repeat(srcs, R * tgts.size)
+    t = np.tile(np.repeat(tgts, R), srcs.size)
+    r = np.tile(np.arange(R), srcs.size * tgts.size)
+    extra = 3000
+    h = np.concatenate([h, rng.integers(0, E, extra)])
+    t = np.concatenate([t, rng.integers(0, E, extra)])
+    r = np.concatenate([r, rng.integers(0, R, extra)])
+    csr = Oc.build_csr_structure(h, t, r, E)
+    n = 2 * R + 1
+    B, L = 2, 2
+    b = np.repeat(np.arange(B), L * srcs.size)
+    l = np.tile(np.repeat(np.arange(L), srcs.size), B)
+    e = np.tile(srcs, B * L)
+    v = (rng.random(b.size) + 0.1).astype(np.float32)
+    state = (b.astype(np.int64), l.astype(np.int64), e.astype(np.int64), v)
+    w = attention(B * L, n, rng).reshape(B, L, n)
+    mbool, masks = masks_for(csr, h.shape[0], rng, drop=0.25)
+    K = 1 << 20
+    keys, vals = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, K)
+    out, vt, wt = _topk(state, w, csr, mbool, B, L, E, R, K, grad=True)
+    assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
+    assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(vals))
+    g = rng.standard_normal(keys.shape[0]).astype(np.float32)
+    (out.values() * torch.from_numpy(g).cuda()).sum().backward()
+    gv_ref, gw_ref = O.sparse_backward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, keys, g, False, K)
+    assert_grad_close(vt.grad.cpu().numpy(), gv_ref)
+    assert_grad_close(wt.grad.reshape(B * L, n).cpu().numpy(), gw_ref)
