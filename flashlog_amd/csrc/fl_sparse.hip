@@ -1517,6 +1517,120 @@ __device__ __forceinline__ void sp_wave_accum(int64_t start, int64_t n, int32_t 
     if (t == 0) *out_count = total;
 }
 
+// A bucket of at most 64 * IPT items with at most SP_WFEW distinct
+// destinations, by one wave without a sort: the destinations are marked in
+// a bitmap, destination j (in destination order) is slot j and the bucket's
+// output j; each item's slot is ranked among the equal slots of its round
+// (64 items in raw order) with SP_WFEW_RB ballots, the values are scattered
+// slot-major in raw order within each slot, and lane j adds slot j's run to
+// 0 in order.  Holes are skipped.  Returns false, having written nothing,
+// when the bucket has more destinations.  LDS: bits (SP_W / 32 words), wpre
+// (their prefix counts), tab ((SP_WFEW) x (IPT + 1) counts), dl (slot
+// destinations), sv (64 * IPT values, 16-byte aligned).
+constexpr int SP_WFEW = 64;
+constexpr int SP_WFEW_RB = 6;
+template <int IPT>
+__device__ __forceinline__ bool sp_wave_few(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
+                                            float *__restrict__ val_arr, int32_t *__restrict__ raw_local,
+                                            int32_t *out_count, uint32_t *bits, uint16_t *wpre, uint16_t *tab,
+                                            int16_t *dl_of, float *sv) {
+    constexpr int WPL = SP_W / 32 / FL_WAVE;  // bitmap words per lane
+    const int lane = fl_lane();
+    int32_t d[IPT];
+    float v[IPT];
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {  // striped: round j, lane t holds item j*64 + t
+        const int64_t k = (int64_t)j * FL_WAVE + lane;
+        d[j] = k < n ? dst_arr[start + k] : -1;
+        v[j] = k < n ? val_arr[start + k] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < WPL; ++q) bits[lane * WPL + q] = 0;
+    fl_wave_sync();
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        if (d[j] < 0) continue;
+        const int x = d[j] & (SP_W - 1);
+        const uint32_t b = 1u << (x & 31);
+        if (!(bits[x >> 5] & b)) atomicOr(&bits[x >> 5], b);
+    }
+    fl_wave_sync();
+    uint32_t wd[WPL];
+    int c = 0;
+#pragma unroll
+    for (int q = 0; q < WPL; ++q) {
+        wd[q] = bits[lane * WPL + q];
+        c += __popc(wd[q]);
+    }
+    const int incl = fl_wave_incl_scan_i32(c);
+    const int total = __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
+    if (total > SP_WFEW) return false;
+    int pre = incl - c;
+#pragma unroll
+    for (int q = 0; q < WPL; ++q) {
+        wpre[lane * WPL + q] = (uint16_t)pre;
+        uint32_t m = wd[q];
+        for (int o = pre; m; ++o) {
+            dl_of[o] = (int16_t)((lane * WPL + q) * 32 + __ffs(m) - 1);
+            m &= m - 1;
+        }
+        pre += __popc(wd[q]);
+    }
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) tab[lane * (IPT + 1) + j] = 0;
+    fl_wave_sync();
+    uint8_t sl[IPT], rk[IPT];
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const bool valid = d[j] >= 0;
+        int sj = 0;
+        if (valid) {
+            const int x = d[j] & (SP_W - 1);
+            sj = wpre[x >> 5] + __popc(bits[x >> 5] & ((1u << (x & 31)) - 1u));
+        }
+        unsigned long long m = __ballot(valid);
+#pragma unroll
+        for (int b = 0; b < SP_WFEW_RB; ++b) {
+            const unsigned long long bal = __ballot((sj >> b) & 1);
+            m &= ((sj >> b) & 1) ? bal : ~bal;
+        }
+        const uint32_t below = sp_lanes_below(m);
+        if (valid && below == 0) tab[sj * (IPT + 1) + j] = (uint16_t)__popcll(m);
+        if (valid && raw_local) raw_local[start + (int64_t)j * FL_WAVE + lane] = sj;
+        sl[j] = (uint8_t)sj;
+        rk[j] = (uint8_t)below;
+    }
+    fl_wave_sync();
+    // lane s: slot s's rounds in order; the slots' runs are consecutive
+    int cs = 0;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) cs += tab[lane * (IPT + 1) + j];
+    const int sincl = fl_wave_incl_scan_i32(cs);
+    const int lo = sincl - cs;
+    {
+        int run = lo;
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int x = tab[lane * (IPT + 1) + j];
+            tab[lane * (IPT + 1) + j] = (uint16_t)run;
+            run += x;
+        }
+    }
+    fl_wave_sync();
+#pragma unroll
+    for (int j = 0; j < IPT; ++j)
+        if (d[j] >= 0) sv[tab[sl[j] * (IPT + 1) + j] + rk[j]] = v[j];
+    fl_wave_sync();
+    // every item was read before: outputs may overwrite them
+    if (lane < total) {
+        const float a = sp_fold(0.0f, sv, lo, lo + cs);
+        dst_arr[start + lane] = dbase + dl_of[lane];
+        val_arr[start + lane] = a;
+    }
+    if (lane == 0) *out_count = total;
+    return true;
+}
+
 // One wave per (row, bucket) slot: small buckets are accumulated here,
 // larger ones listed for the persistent kernels (lists[0] hot, lists[2]
 // mid-size; lists[1], lists[3] their claim counters).
@@ -1528,8 +1642,10 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
                                                          int32_t *__restrict__ mid_list,
                                                          int32_t *__restrict__ lists) {
     __shared__ __align__(16) uint32_t kb[SP_SMALL_WAVES][2][SP_WB];
-    __shared__ float val[SP_SMALL_WAVES][SP_WB];
+    __shared__ __align__(16) float val[SP_SMALL_WAVES][SP_WB];
     __shared__ uint16_t cnt[SP_SMALL_WAVES][16][FL_WAVE];
+    static_assert(SP_W / 32 * 4 + SP_W / 32 * 2 + SP_WFEW * 2 <= SP_WB * 4, "few-path bitmap in the first key buffer");
+    static_assert(SP_WFEW * (SP_WIPT + 1) * 2 <= SP_WB * 4, "few-path counts in the second key buffer");
     const int w = fl_wave_id();
     const int64_t slot = fl_xcd_contig(blockIdx.x, gridDim.x) * SP_SMALL_WAVES + w;
     if (slot >= nslots) return;  // no block barrier follows
@@ -1552,6 +1668,23 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
         return;
     }
     const int32_t dbase = (int32_t)(bk << SP_S);
+    // buckets of few destinations without a sort (the key buffers and the
+    // value array hold the few path's arrays), else the sort
+    uint32_t *fbits = kb[w][0];
+    uint16_t *fwpre = reinterpret_cast<uint16_t *>(kb[w][0] + SP_W / 32);
+    int16_t *fdl = reinterpret_cast<int16_t *>(kb[w][0] + SP_W / 32 + SP_W / 64);
+    uint16_t *ftab = reinterpret_cast<uint16_t *>(kb[w][1]);
+    bool done;
+    if (n <= FL_WAVE)
+        done = sp_wave_few<1>(start, n, dbase, dst_arr, val_arr, raw_local, oc, fbits, fwpre, ftab, fdl, val[w]);
+    else if (n <= 2 * FL_WAVE)
+        done = sp_wave_few<2>(start, n, dbase, dst_arr, val_arr, raw_local, oc, fbits, fwpre, ftab, fdl, val[w]);
+    else if (n <= 4 * FL_WAVE)
+        done = sp_wave_few<4>(start, n, dbase, dst_arr, val_arr, raw_local, oc, fbits, fwpre, ftab, fdl, val[w]);
+    else
+        done = sp_wave_few<8>(start, n, dbase, dst_arr, val_arr, raw_local, oc, fbits, fwpre, ftab, fdl, val[w]);
+    if (done) return;
+    fl_wave_sync();  // the few path's reads of its arrays are done
     if (n <= FL_WAVE)
         sp_wave_accum<1>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
     else if (n <= 2 * FL_WAVE)
