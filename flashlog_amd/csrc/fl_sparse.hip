@@ -306,30 +306,40 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
                                                 SpTake &tk, F &&fn) {
     const int lane = fl_lane();
     int64_t base = 0;
-    // the next window's group records are requested before this window's
-    // weights are gathered and its takes computed; records at clamped
-    // indices (loads issued unconditionally), groups past the end zeroed
+    // software pipeline over the windows: the records two windows ahead and
+    // the weights one window ahead are requested before this window's takes
+    // are computed; records at clamped indices (loads issued
+    // unconditionally), groups past the end zeroed
     const int64_t glast = g1 - 1;
-    int rel = 0;
-    int32_t start = 0, cnt = 0;
+    int rel = 0, rel1 = 0;
+    int32_t start = 0, cnt = 0, start1 = 0, cnt1 = 0;
+    float wraw = 0.0f;
     if (g1 > g0) {
         const int64_t gc = g0 + lane < g1 ? g0 + lane : glast;
         rel = s.group_rel[gc];
         start = s.group_start[gc];
         cnt = s.group_count[gc];
+        if (g0 + FL_WAVE < g1) {
+            const int64_t gc1 = g0 + FL_WAVE + lane < g1 ? g0 + FL_WAVE + lane : glast;
+            rel1 = s.group_rel[gc1];
+            start1 = s.group_start[gc1];
+            cnt1 = s.group_count[gc1];
+        }
+        wraw = wr[rel];
     }
     for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
-        const int64_t g = gb + lane, gn = g + FL_WAVE;
-        int reln = 0;
-        int32_t startn = 0, cntn = 0;
-        if (gb + FL_WAVE < g1) {
+        const int64_t g = gb + lane;
+        int rel2 = 0;
+        int32_t start2 = 0, cnt2 = 0;
+        if (gb + 2 * FL_WAVE < g1) {
+            const int64_t gn = g + 2 * FL_WAVE;
             const int64_t gc = gn < g1 ? gn : glast;
-            reln = s.group_rel[gc];
-            startn = s.group_start[gc];
-            cntn = s.group_count[gc];
+            rel2 = s.group_rel[gc];
+            start2 = s.group_start[gc];
+            cnt2 = s.group_count[gc];
         }
+        const float wraw1 = gb + FL_WAVE < g1 ? wr[rel1] : 0.0f;
         const bool in = g < g1;
-        const float wraw = wr[rel];
         const float wv = in ? wraw : 0.0f;
         if (!in) cnt = 0;
         int64_t take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? group_take(wv, tk.th, tk.cut, start, cnt) : 0);
@@ -341,9 +351,13 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
             fn((long long)take, (int64_t)start, rel, wv, (long long)(base + incl - take));
             base += __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
         }
-        rel = reln;
-        start = startn;
-        cnt = cntn;
+        rel = rel1;
+        start = start1;
+        cnt = cnt1;
+        wraw = wraw1;
+        rel1 = rel2;
+        start1 = start2;
+        cnt1 = cnt2;
     }
     return base;
 }
