@@ -899,8 +899,27 @@ class _SparseSides:
         side.col_ind, side.mask = ptr(col).value, (ptr(mask).value if mask is not None else None)
         side.row_group_ptr, side.group_rel = ptr(gptr).value, ptr(grel).value
         side.group_start, side.group_count = ptr(gstart).value, ptr(gcount).value
-        side.max_rel = int(grel.max()) if grel.numel() else -1
+        side.max_rel = _max_relation(grel)
         return side
+
+
+# Largest relation id of a group-relation array, kept per tensor object and
+# version (the CSR arrays of a graph serve every hop; a read of the maximum
+# costs a reduction and a device synchronization).
+_MAX_REL = {}
+
+
+def _max_relation(grel):
+    if grel.numel() == 0:
+        return -1
+    hit = _MAX_REL.get(id(grel))
+    if hit is not None and hit[0]() is grel and hit[1] == grel._version:
+        return hit[2]
+    for k in [k for k, v in _MAX_REL.items() if v[0]() is None]:
+        del _MAX_REL[k]
+    m = int(grel.max())
+    _MAX_REL[id(grel)] = (weakref.ref(grel), grel._version, m)
+    return m
 
 
 # Hops with at least this many entries visit them by source entity.
@@ -908,8 +927,9 @@ _ENTRY_ORDER_MIN = 4096
 
 def _entry_order(sp_e):
     """Entries by source entity: a source's rows then share cached group
-    records in the plan and the run writer."""
-    return torch.argsort(sp_e).to(torch.int32)
+    records in the plan and the run writer (any order among a source's
+    entries; int32 keys for a radix sort)."""
+    return torch.sort(sp_e.to(torch.int32))[1].to(torch.int32)
 
 
 # When a list, every sparse hop appends its sizes to it as {"nnz" (entries
