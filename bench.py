@@ -64,11 +64,36 @@ def parse():
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "STEPS", "OUT"),
                     help="write the per-step HBM traffic summary of two rocprofv3 counter passes "
                          "(FETCH_SIZE, then WRITE_SIZE, each over --copy-mb 256 --counter-steps STEPS)")
+    ap.add_argument("--stats-table", nargs=4, metavar=("OUT", "STATS_CSV", "TITLE", "RUN_COMMAND"),
+                    help="write the kernel-time table of a rocprofv3 --kernel-trace --stats run "
+                         "(its kernel_stats.csv) as markdown, naming the run's command")
     ap.add_argument("--counter-table", nargs="+", metavar="ARG",
                     help="OUT CSV [CSV ...]: write the per-dispatch means of every counter in these "
                          "rocprofv3 counter_collection.csv files (one per pass over --counter-steps) for "
                          "the sparse hop kernels, as a markdown table")
     return ap.parse_args()
+
+
+def stats_table(out_path, stats_csv, title, run_command, top=30):
+    """The rocprofv3 kernel statistics (per kernel: calls, average, min and
+    max duration, share of GPU time) as a markdown table."""
+    import csv
+    rows = list(csv.DictReader(open(stats_csv)))
+    rows.sort(key=lambda r: -float(r["Percentage"]))
+    lines = ["# %s" % title, "", "Commands (from the repo root, on one MI355X):", "", "```",
+             "cd /tmp && rocprofv3 --kernel-trace --stats --output-format csv -d /tmp/prof -o run -- " + run_command,
+             "python3 <repo>/bench.py --stats-table <this file> <the run's kernel_stats.csv> <title> <run command>",
+             "```", "",
+             "Names: fl:: are this library's kernels, at:: and rocprim:: torch's.", "",
+             "| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|"]
+    for r in rows[:top]:
+        name = r["Name"].replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")[:72]
+        lines.append("| %s | %s | %.1f | %.1f | %.1f | %.2f |" % (
+            name, r["Calls"], float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3,
+            float(r["Percentage"])))
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("wrote", out_path)
 
 
 def _pmc_counters(path):
@@ -284,6 +309,9 @@ def main():
     if args.pmc_summary:
         fetch_csv, write_csv, steps, out = args.pmc_summary
         return pmc_summary(fetch_csv, write_csv, int(steps), out)
+    if args.stats_table:
+        out, csv_path, title, run_command = args.stats_table
+        return stats_table(out, csv_path, title, run_command)
     if args.counter_table:
         if len(args.counter_table) < 2:
             sys.exit("--counter-table needs OUT and at least one CSV")
