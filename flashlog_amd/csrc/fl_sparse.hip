@@ -153,12 +153,16 @@ struct SpQuota {
 
 __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int64_t K) {
     const int lane = fl_lane();
+    // 32-bit offsets from the side's first group (a wave-uniform base)
+    const int32_t ng = (int32_t)(g1 - g0);
+    const int16_t *__restrict__ grel = s.group_rel + g0;
+    const int32_t *__restrict__ gcnt = s.group_count + g0;
     double ws = 0.0;
     long long cap = 0, nel = 0;
     int emin = 1 << 20, emax = -(1 << 20);
     // groups 4 windows at a time (the loads of a batch in flight together);
     // each lane still visits its groups in order
-    for (int64_t gb = g0; gb < g1; gb += 4 * FL_WAVE) {
+    for (int32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
         int rl[4];
         int32_t cl[4];
         float wl[4];
@@ -166,14 +170,14 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
         // groups past the side's end are zeroed
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int64_t g = gb + u * FL_WAVE + lane;
-            const int64_t gc = g < g1 ? g : g1 - 1;
-            rl[u] = s.group_rel[gc];
-            cl[u] = s.group_count[gc];
+            const int32_t g = gb + u * FL_WAVE + lane;
+            const int32_t gc = g < ng ? g : ng - 1;
+            rl[u] = grel[gc];
+            cl[u] = gcnt[gc];
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const bool in = gb + u * FL_WAVE + lane < g1;
+            const bool in = gb + u * FL_WAVE + lane < ng;
             const float wraw = wr[rl[u]];
             wl[u] = in ? wraw : 0.0f;
             cl[u] = in ? cl[u] : 0;
@@ -206,11 +210,11 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     if (emax + 1 + lg - emin > 53) {
         // partial sums may round: the reference's sequential order
         ws = 0.0;
-        for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
-            const int64_t g = gb + lane;
+        for (int32_t gb = 0; gb < ng; gb += FL_WAVE) {
+            const int32_t g = gb + lane;
             float wv = 0.0f;
-            if (g < g1 && s.group_count[g] > 0) wv = wr[s.group_rel[g]];
-            const int nl = (int)((g1 - gb) < FL_WAVE ? (g1 - gb) : FL_WAVE);
+            if (g < ng && gcnt[g] > 0) wv = wr[grel[g]];
+            const int nl = (ng - gb) < FL_WAVE ? (ng - gb) : FL_WAVE;
             for (int j = 0; j < nl; ++j) {  // group order
                 const float wj = __shfl(wv, j, FL_WAVE);
                 if (wj > 0.0f) ws = __dadd_rn(ws, (double)wj);
@@ -225,7 +229,7 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     tk.wsum = ws;
     tk.target = q.target;
     long long alloc = 0;
-    for (int64_t gb = g0; gb < g1; gb += 4 * FL_WAVE) {
+    for (int32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
         int rl[4];
         int32_t cl[4];
         float wl[4];
@@ -233,14 +237,14 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
         // groups past the side's end are zeroed
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int64_t g = gb + u * FL_WAVE + lane;
-            const int64_t gc = g < g1 ? g : g1 - 1;
-            rl[u] = s.group_rel[gc];
-            cl[u] = s.group_count[gc];
+            const int32_t g = gb + u * FL_WAVE + lane;
+            const int32_t gc = g < ng ? g : ng - 1;
+            rl[u] = grel[gc];
+            cl[u] = gcnt[gc];
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const bool in = gb + u * FL_WAVE + lane < g1;
+            const bool in = gb + u * FL_WAVE + lane < ng;
             const float wraw = wr[rl[u]];
             wl[u] = in ? wraw : 0.0f;
             cl[u] = in ? cl[u] : 0;
@@ -309,45 +313,50 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
     // software pipeline over the windows: the records two windows ahead and
     // the weights one window ahead are requested before this window's takes
     // are computed; records at clamped indices (loads issued
-    // unconditionally), groups past the end zeroed
-    const int64_t glast = g1 - 1;
+    // unconditionally), groups past the end zeroed.  32-bit offsets from the
+    // side's first group (a wave-uniform base).
+    const int32_t ng = (int32_t)(g1 - g0);
+    const int16_t *__restrict__ grel = s.group_rel + g0;
+    const int32_t *__restrict__ gsta = s.group_start + g0;
+    const int32_t *__restrict__ gcnt = s.group_count + g0;
+    const int32_t glast = ng - 1;
     int rel = 0, rel1 = 0;
     int32_t start = 0, cnt = 0, start1 = 0, cnt1 = 0;
     float wraw = 0.0f;
-    if (g1 > g0) {
-        const int64_t gc = g0 + lane < g1 ? g0 + lane : glast;
-        rel = s.group_rel[gc];
-        start = s.group_start[gc];
-        cnt = s.group_count[gc];
-        if (g0 + FL_WAVE < g1) {
-            const int64_t gc1 = g0 + FL_WAVE + lane < g1 ? g0 + FL_WAVE + lane : glast;
-            rel1 = s.group_rel[gc1];
-            start1 = s.group_start[gc1];
-            cnt1 = s.group_count[gc1];
+    if (ng > 0) {
+        const int32_t gc = lane < ng ? lane : glast;
+        rel = grel[gc];
+        start = gsta[gc];
+        cnt = gcnt[gc];
+        if (FL_WAVE < ng) {
+            const int32_t gc1 = FL_WAVE + lane < ng ? FL_WAVE + lane : glast;
+            rel1 = grel[gc1];
+            start1 = gsta[gc1];
+            cnt1 = gcnt[gc1];
         }
         wraw = wr[rel];
     }
-    for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
-        const int64_t g = gb + lane;
+    for (int32_t gb = 0; gb < ng; gb += FL_WAVE) {
+        const int32_t g = gb + lane;
         int rel2 = 0;
         int32_t start2 = 0, cnt2 = 0;
-        if (gb + 2 * FL_WAVE < g1) {
-            const int64_t gn = g + 2 * FL_WAVE;
-            const int64_t gc = gn < g1 ? gn : glast;
-            rel2 = s.group_rel[gc];
-            start2 = s.group_start[gc];
-            cnt2 = s.group_count[gc];
+        if (gb + 2 * FL_WAVE < ng) {
+            const int32_t gn = g + 2 * FL_WAVE;
+            const int32_t gc = gn < ng ? gn : glast;
+            rel2 = grel[gc];
+            start2 = gsta[gc];
+            cnt2 = gcnt[gc];
         }
-        const float wraw1 = gb + FL_WAVE < g1 ? wr[rel1] : 0.0f;
-        const bool in = g < g1;
+        const float wraw1 = gb + FL_WAVE < ng ? wr[rel1] : 0.0f;
+        const bool in = g < ng;
         const float wv = in ? wraw : 0.0f;
         if (!in) cnt = 0;
-        int64_t take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? group_take(wv, tk.th, tk.cut, start, cnt) : 0);
+        int32_t take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? (int32_t)group_take(wv, tk.th, tk.cut, start, cnt) : 0);
         if (Q && tk.kind == TAKE_QUOTA)
-            take = sp_quota_window(tk, wv, cnt, in);
+            take = (int32_t)sp_quota_window(tk, wv, cnt, in);
         if (__ballot(take > 0) != 0) {
             // a window's takes add up to at most the source's edges (int32)
-            const int32_t incl = fl_wave_incl_scan_i32((int32_t)take);
+            const int32_t incl = fl_wave_incl_scan_i32(take);
             fn((long long)take, (int64_t)start, rel, wv, (long long)(base + incl - take));
             base += __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
         }
@@ -891,10 +900,10 @@ __global__ __launch_bounds__(SP_ITEMS_NT) void k_sp_items(fl_side ori, fl_side i
 // number of marks at 1..k).  rcap: runs per wave the dynamic LDS holds.
 constexpr int64_t SP_FUSE_KMAX = 256;  // budgets whose runs fit the fused kernel's LDS
 
+// A run in LDS: first item, CSR position, a*w (bits), column and side --
+// one 16-byte record (one LDS store and one load per run).
 struct SpLdsRuns {
-    int32_t *first, *p;
-    float *aw;
-    uint32_t *meta;
+    int4 *rec;
 };
 
 template <bool Q, bool MAXT, bool BWD>
@@ -912,11 +921,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
     uint8_t *mark = mark_all[wid];
     SpLdsRuns ru;
     {
-        unsigned char *b = fused_lds + (size_t)wid * rcap * 16;
-        ru.first = reinterpret_cast<int32_t *>(b);
-        ru.p = reinterpret_cast<int32_t *>(b + (size_t)rcap * 4);
-        ru.aw = reinterpret_cast<float *>(b + (size_t)rcap * 8);
-        ru.meta = reinterpret_cast<uint32_t *>(b + (size_t)rcap * 12);
+        ru.rec = reinterpret_cast<int4 *>(fused_lds + (size_t)wid * rcap * 16);
     }
     const int64_t wv_i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + wid;
     if (wv_i >= nnz) return;  // no block barrier follows
@@ -945,19 +950,15 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
             const int64_t ri = rix + __popcll(m & below);
             const int64_t o = pos + ex;
             if (take > 0 && o + take <= lim && ri < rcap) {
-                ru.first[ri] = (int32_t)o;
-                ru.p[ri] = (int32_t)start;
-                ru.aw[ri] = fl_mul(a, wv);
-                ru.meta[ri] = side | (col0 + (uint32_t)rel);
+                ru.rec[ri] = make_int4((int32_t)o, (int32_t)start, __float_as_int(fl_mul(a, wv)),
+                                       (int)(side | (col0 + (uint32_t)rel)));
             }
             rix += __popcll(m);
         });
     }
     if (!wot_i && lane == 0 && pos == lim && rix < rcap) {
-        ru.first[rix] = (int32_t)lim;
-        ru.p[rix] = (int32_t)src;
-        ru.aw[rix] = fl_mul(a, wrow[n - 1]);
-        ru.meta[rix] = SP_RUN_ID | (uint32_t)(n - 1);
+        ru.rec[rix] = make_int4((int32_t)lim, (int32_t)src, __float_as_int(fl_mul(a, wrow[n - 1])),
+                                (int)(SP_RUN_ID | (uint32_t)(n - 1)));
     }
     int64_t nr = rix + (wot_i ? 0 : 1);
     if (nr > rcap) nr = rcap;
@@ -970,11 +971,12 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
         float aw = 0.0f;
         uint32_t rm = 0;
         if (rj < nr) {
-            const int64_t f = (int64_t)ru.first[rj] - q0;
+            const int4 x = ru.rec[rj];
+            const int64_t f = (int64_t)x.x - q0;
             d = f < SP_ICHUNK ? (int32_t)f : SP_ICHUNK;
-            rp = ru.p[rj];
-            aw = ru.aw[rj];
-            rm = ru.meta[rj];
+            rp = x.y;
+            aw = __int_as_float(x.z);
+            rm = (uint32_t)x.w;
         }
         mark[lane] = 0;
         fl_wave_sync();
@@ -989,7 +991,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
         // the next round's first item: in the last run that started here, or
         // in the run starting right at it
         r0 += __popcll(starts);
-        if (r0 + 1 < nr && (int64_t)ru.first[r0 + 1] <= q0 + SP_ICHUNK) ++r0;
+        if (r0 + 1 < nr && (int64_t)ru.rec[r0 + 1].x <= q0 + SP_ICHUNK) ++r0;
         fl_wave_sync();  // marks read before the next round clears them
         const int64_t it = q0 + lane;
         if (it >= nitems) continue;
