@@ -128,6 +128,14 @@ __device__ __forceinline__ double fl_uniform_f64(double x) {
     return __longlong_as_double(fl_uniform_i64(__double_as_longlong(x)));
 }
 
+// base[idx] with the byte offset computed in 32 bits (a scalar base plus a
+// 32-bit vector offset is one load with no 64-bit address arithmetic); the
+// caller guarantees idx * sizeof(T) < 2^32.
+template <typename T>
+__device__ __forceinline__ T fl_ld32(const T *base, uint32_t idx) {
+    return *reinterpret_cast<const T *>(reinterpret_cast<const char *>(base) + (uint32_t)(idx * (uint32_t)sizeof(T)));
+}
+
 // The wave's index within its workgroup, in a scalar register (so that
 // per-wave indices, and loads at them, stay scalar).
 __device__ __forceinline__ int fl_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / FL_WAVE)); }

@@ -119,21 +119,24 @@ __global__ void k_sp_rowptr(const int64_t *__restrict__ sb, const int64_t *__res
 // one in order.
 enum { TAKE_ALL = 0, TAKE_TH = 1, TAKE_QUOTA = 2 };
 
+// Counts in 32 bits: a side's capacity, and with it the target, residual,
+// spare and prefixes, is at most the source's edges on that side (CSR
+// positions are int32); the double arithmetic is the reference's.
 struct SpTake {
     int kind;
     float th;
     int32_t cut;
     double wsum, phase;
-    long long target, residual, spare, prefix, cum;
+    int32_t target, residual, spare, prefix, cum;
 };
 
-__device__ __forceinline__ long long sp_quota_base(const SpTake &tk, float wv, long long cnt) {
-    return (long long)fmin((double)cnt, floor(__ddiv_rn(__dmul_rn((double)tk.target, (double)wv), tk.wsum)));
+__device__ __forceinline__ int32_t sp_quota_base(const SpTake &tk, float wv, int32_t cnt) {
+    return (int32_t)fmin((double)cnt, floor(__ddiv_rn(__dmul_rn((double)tk.target, (double)wv), tk.wsum)));
 }
 
-__device__ __forceinline__ long long sp_quota_cum(const SpTake &tk, long long p) {
+__device__ __forceinline__ int32_t sp_quota_cum(const SpTake &tk, int32_t p) {
     return p == tk.spare ? tk.residual
-                         : (long long)floor(__dadd_rn(
+                         : (int32_t)floor(__dadd_rn(
                                __ddiv_rn(__dmul_rn((double)tk.residual, (double)p), (double)tk.spare), tk.phase));
 }
 
@@ -154,7 +157,7 @@ struct SpQuota {
 __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int64_t K) {
     const int lane = fl_lane();
     // 32-bit offsets from the side's first group (a wave-uniform base)
-    const int32_t ng = (int32_t)(g1 - g0);
+    const uint32_t ng = (uint32_t)(g1 - g0);  // at most 32767: one group per relation
     const int16_t *__restrict__ grel = s.group_rel + g0;
     const int32_t *__restrict__ gcnt = s.group_count + g0;
     double ws = 0.0;
@@ -162,7 +165,7 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     int emin = 1 << 20, emax = -(1 << 20);
     // groups 4 windows at a time (the loads of a batch in flight together);
     // each lane still visits its groups in order
-    for (int32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
+    for (uint32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
         int rl[4];
         int32_t cl[4];
         float wl[4];
@@ -170,15 +173,15 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
         // groups past the side's end are zeroed
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int32_t g = gb + u * FL_WAVE + lane;
-            const int32_t gc = g < ng ? g : ng - 1;
-            rl[u] = grel[gc];
-            cl[u] = gcnt[gc];
+            const uint32_t g = gb + u * FL_WAVE + (uint32_t)lane;
+            const uint32_t gc = g < ng ? g : ng - 1;
+            rl[u] = fl_ld32(grel, gc);
+            cl[u] = fl_ld32(gcnt, gc);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const bool in = gb + u * FL_WAVE + lane < ng;
-            const float wraw = wr[rl[u]];
+            const bool in = gb + u * FL_WAVE + (uint32_t)lane < ng;
+            const float wraw = fl_ld32(wr, (uint32_t)rl[u]);
             wl[u] = in ? wraw : 0.0f;
             cl[u] = in ? cl[u] : 0;
         }
@@ -210,11 +213,11 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     if (emax + 1 + lg - emin > 53) {
         // partial sums may round: the reference's sequential order
         ws = 0.0;
-        for (int32_t gb = 0; gb < ng; gb += FL_WAVE) {
-            const int32_t g = gb + lane;
+        for (uint32_t gb = 0; gb < ng; gb += FL_WAVE) {
+            const uint32_t g = gb + (uint32_t)lane;
             float wv = 0.0f;
-            if (g < ng && gcnt[g] > 0) wv = wr[grel[g]];
-            const int nl = (ng - gb) < FL_WAVE ? (ng - gb) : FL_WAVE;
+            if (g < ng && fl_ld32(gcnt, g) > 0) wv = fl_ld32(wr, (uint32_t)fl_ld32(grel, g));
+            const int nl = (int)((ng - gb) < FL_WAVE ? (ng - gb) : FL_WAVE);
             for (int j = 0; j < nl; ++j) {  // group order
                 const float wj = __shfl(wv, j, FL_WAVE);
                 if (wj > 0.0f) ws = __dadd_rn(ws, (double)wj);
@@ -227,9 +230,9 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     q.target = K < cap ? K : cap;
     SpTake tk{};
     tk.wsum = ws;
-    tk.target = q.target;
+    tk.target = (int32_t)q.target;
     long long alloc = 0;
-    for (int32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
+    for (uint32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
         int rl[4];
         int32_t cl[4];
         float wl[4];
@@ -237,15 +240,15 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
         // groups past the side's end are zeroed
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int32_t g = gb + u * FL_WAVE + lane;
-            const int32_t gc = g < ng ? g : ng - 1;
-            rl[u] = grel[gc];
-            cl[u] = gcnt[gc];
+            const uint32_t g = gb + u * FL_WAVE + (uint32_t)lane;
+            const uint32_t gc = g < ng ? g : ng - 1;
+            rl[u] = fl_ld32(grel, gc);
+            cl[u] = fl_ld32(gcnt, gc);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const bool in = gb + u * FL_WAVE + lane < ng;
-            const float wraw = wr[rl[u]];
+            const bool in = gb + u * FL_WAVE + (uint32_t)lane < ng;
+            const float wraw = fl_ld32(wr, (uint32_t)rl[u]);
             wl[u] = in ? wraw : 0.0f;
             cl[u] = in ? cl[u] : 0;
         }
@@ -269,9 +272,9 @@ __device__ __forceinline__ SpTake sp_take(int mode, float thv, int32_t ct, const
     if (!Q || !__builtin_isnan(thv)) { tk.kind = TAKE_TH; return tk; }
     tk.kind = TAKE_QUOTA;
     tk.wsum = qp->wsum;
-    tk.target = qp->target;
-    tk.residual = qp->residual;
-    tk.spare = qp->spare;
+    tk.target = (int32_t)qp->target;
+    tk.residual = (int32_t)qp->residual;
+    tk.spare = (int32_t)qp->spare;
     tk.prefix = 0;
     tk.cum = 0;  // cum(0) = floor(phase) = 0
     const uint64_t z = (uint64_t)seed ^ ((uint64_t)b * 0x9e3779b97f4a7c15ull) ^ ((uint64_t)l * 0xbf58476d1ce4e5b9ull) ^
@@ -282,17 +285,17 @@ __device__ __forceinline__ SpTake sp_take(int mode, float thv, int32_t ct, const
 
 // Quota takes of the window's groups (lane j: one group, valid = it exists):
 // base + cum(p_g) - cum(p_{g-1}) for eligible groups, carried across windows.
-__device__ __forceinline__ long long sp_quota_window(SpTake &tk, float wv, long long cnt, bool valid) {
+__device__ __forceinline__ int32_t sp_quota_window(SpTake &tk, float wv, int32_t cnt, bool valid) {
     const int lane = fl_lane();
     const bool el = valid && wv > 0.0f && cnt > 0;
-    const long long base = el ? sp_quota_base(tk, wv, cnt) : 0;
-    // 32-bit lanes: a window's spares add up to at most the source's edges on
-    // the side (CSR positions are int32) and cum stays within the residual
-    const int32_t spare = el ? (int32_t)(cnt - base) : 0;
+    const int32_t base = el ? sp_quota_base(tk, wv, cnt) : 0;
+    // a window's spares add up to at most the source's edges on the side
+    // and cum stays within the residual
+    const int32_t spare = el ? cnt - base : 0;
     const int32_t incl = fl_wave_incl_scan_i32(spare);
-    const int32_t cum = (int32_t)sp_quota_cum(tk, tk.prefix + incl);
+    const int32_t cum = sp_quota_cum(tk, tk.prefix + incl);
     const int32_t prev = fl_dpp<0x138>(cum);  // wave_shr:1
-    const long long extra = (long long)cum - (lane == 0 ? tk.cum : (long long)prev);
+    const int32_t extra = cum - (lane == 0 ? tk.cum : prev);
     tk.prefix += __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
     tk.cum = __builtin_amdgcn_readlane(cum, FL_WAVE - 1);
     return el ? base + extra : 0;
@@ -314,40 +317,42 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
     // the weights one window ahead are requested before this window's takes
     // are computed; records at clamped indices (loads issued
     // unconditionally), groups past the end zeroed.  32-bit offsets from the
-    // side's first group (a wave-uniform base).
-    const int32_t ng = (int32_t)(g1 - g0);
+    // side's first group (a wave-uniform base; a side has at most 32767
+    // groups, one per relation).
+    const uint32_t ng = (uint32_t)(g1 - g0);
     const int16_t *__restrict__ grel = s.group_rel + g0;
     const int32_t *__restrict__ gsta = s.group_start + g0;
     const int32_t *__restrict__ gcnt = s.group_count + g0;
-    const int32_t glast = ng - 1;
+    const uint32_t glast = ng - 1;
+    const uint32_t ul = (uint32_t)lane;
     int rel = 0, rel1 = 0;
     int32_t start = 0, cnt = 0, start1 = 0, cnt1 = 0;
     float wraw = 0.0f;
     if (ng > 0) {
-        const int32_t gc = lane < ng ? lane : glast;
-        rel = grel[gc];
-        start = gsta[gc];
-        cnt = gcnt[gc];
+        const uint32_t gc = ul < ng ? ul : glast;
+        rel = fl_ld32(grel, gc);
+        start = fl_ld32(gsta, gc);
+        cnt = fl_ld32(gcnt, gc);
         if (FL_WAVE < ng) {
-            const int32_t gc1 = FL_WAVE + lane < ng ? FL_WAVE + lane : glast;
-            rel1 = grel[gc1];
-            start1 = gsta[gc1];
-            cnt1 = gcnt[gc1];
+            const uint32_t gc1 = FL_WAVE + ul < ng ? FL_WAVE + ul : glast;
+            rel1 = fl_ld32(grel, gc1);
+            start1 = fl_ld32(gsta, gc1);
+            cnt1 = fl_ld32(gcnt, gc1);
         }
-        wraw = wr[rel];
+        wraw = fl_ld32(wr, (uint32_t)rel);
     }
-    for (int32_t gb = 0; gb < ng; gb += FL_WAVE) {
-        const int32_t g = gb + lane;
+    for (uint32_t gb = 0; gb < ng; gb += FL_WAVE) {
+        const uint32_t g = gb + ul;
         int rel2 = 0;
         int32_t start2 = 0, cnt2 = 0;
         if (gb + 2 * FL_WAVE < ng) {
-            const int32_t gn = g + 2 * FL_WAVE;
-            const int32_t gc = gn < ng ? gn : glast;
-            rel2 = grel[gc];
-            start2 = gsta[gc];
-            cnt2 = gcnt[gc];
+            const uint32_t gn = g + 2 * FL_WAVE;
+            const uint32_t gc = gn < ng ? gn : glast;
+            rel2 = fl_ld32(grel, gc);
+            start2 = fl_ld32(gsta, gc);
+            cnt2 = fl_ld32(gcnt, gc);
         }
-        const float wraw1 = gb + FL_WAVE < ng ? wr[rel1] : 0.0f;
+        const float wraw1 = gb + FL_WAVE < ng ? fl_ld32(wr, (uint32_t)rel1) : 0.0f;
         const bool in = g < ng;
         const float wv = in ? wraw : 0.0f;
         if (!in) cnt = 0;
@@ -934,8 +939,9 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
     const int64_t base = item_off[i];
     const int64_t nitems = item_off[i + 1] - base;
     // the plan's item count bounds every run (the walk reproduces it)
-    const int64_t lim = nitems - (wot_i ? 0 : 1);
-    int64_t pos = 0, rix = 0;  // within the entry
+    // per-entry counts in 32 bits (at most 2K+1 items)
+    const int32_t lim = (int32_t)nitems - (wot_i ? 0 : 1);
+    int32_t pos = 0, rix = 0;  // within the entry
     const uint64_t below = (1ull << lane) - 1;
     for (int dir = 0; dir < 2; ++dir) {
         const fl_side &s = dir ? inv : ori;
@@ -945,11 +951,12 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
                                dir);
         const uint32_t side = dir ? SP_RUN_INV : 0u;
         const uint32_t col0 = dir ? (uint32_t)r_size : 0u;
-        pos += sp_side_runs<Q>(s, g0, g1, wr, tk, [&](long long take, int64_t start, int rel, float wv, long long ex) {
+        pos += (int32_t)sp_side_runs<Q>(s, g0, g1, wr, tk, [&](long long take, int64_t start, int rel, float wv,
+                                                               long long ex) {
             const uint64_t m = __ballot(take > 0);
-            const int64_t ri = rix + __popcll(m & below);
-            const int64_t o = pos + ex;
-            if (take > 0 && o + take <= lim && ri < rcap) {
+            const int32_t ri = rix + __popcll(m & below);
+            const int32_t o = pos + (int32_t)ex;
+            if (take > 0 && o + (int32_t)take <= lim && ri < rcap) {
                 ru.rec[ri] = make_int4((int32_t)o, (int32_t)start, __float_as_int(fl_mul(a, wv)),
                                        (int)(side | (col0 + (uint32_t)rel)));
             }
@@ -960,20 +967,20 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
         ru.rec[rix] = make_int4((int32_t)lim, (int32_t)src, __float_as_int(fl_mul(a, wrow[n - 1])),
                                 (int)(SP_RUN_ID | (uint32_t)(n - 1)));
     }
-    int64_t nr = rix + (wot_i ? 0 : 1);
+    int32_t nr = rix + (wot_i ? 0 : 1);
     if (nr > rcap) nr = rcap;
     fl_wave_sync();
     const uint64_t upto = lane == FL_WAVE - 1 ? ~0ull : ((2ull << lane) - 1);
-    int64_t r0 = 0;  // the run holding the round's first item
-    for (int64_t q0 = 0; q0 < nitems; q0 += SP_ICHUNK) {
-        const int64_t rj = r0 + lane;
+    int32_t r0 = 0;  // the run holding the round's first item
+    for (int32_t q0 = 0; q0 < (int32_t)nitems; q0 += SP_ICHUNK) {
+        const int32_t rj = r0 + lane;
         int32_t d = SP_ICHUNK, rp = 0;
         float aw = 0.0f;
         uint32_t rm = 0;
         if (rj < nr) {
             const int4 x = ru.rec[rj];
-            const int64_t f = (int64_t)x.x - q0;
-            d = f < SP_ICHUNK ? (int32_t)f : SP_ICHUNK;
+            const int32_t f = x.x - q0;
+            d = f < SP_ICHUNK ? f : SP_ICHUNK;
             rp = x.y;
             aw = __int_as_float(x.z);
             rm = (uint32_t)x.w;
@@ -991,10 +998,10 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
         // the next round's first item: in the last run that started here, or
         // in the run starting right at it
         r0 += __popcll(starts);
-        if (r0 + 1 < nr && (int64_t)ru.rec[r0 + 1].x <= q0 + SP_ICHUNK) ++r0;
+        if (r0 + 1 < nr && ru.rec[r0 + 1].x <= q0 + SP_ICHUNK) ++r0;
         fl_wave_sync();  // marks read before the next round clears them
-        const int64_t it = q0 + lane;
-        if (it >= nitems) continue;
+        const int32_t it = q0 + lane;
+        if (it >= (int32_t)nitems) continue;
         const int64_t k = base + it;
         int32_t dst = -1, pp = -1;
         float val = 0.0f;
@@ -1004,11 +1011,11 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
             val = awj;
         } else {
             const bool inv_side = (mj & SP_RUN_INV) != 0;
-            const int64_t edges = inv_side ? inv.edges : ori.edges;
+            const uint32_t edges = (uint32_t)(inv_side ? inv.edges : ori.edges);
             const float *mk = inv_side ? inv.mask : ori.mask;
             const uint32_t *mb = inv_side ? inv.mask_bits : ori.mask_bits;
             const int32_t *ci = inv_side ? inv.col_ind : ori.col_ind;
-            if (pj >= 0 && pj < edges) {
+            if ((uint32_t)pj < edges) {
                 const float m = sp_mask_at(mb, mk, pj);
                 const int32_t e = ci[pj];
                 dst = (!holes || m != 0.0f) ? e : -1;

@@ -899,27 +899,27 @@ class _SparseSides:
         side.col_ind, side.mask = ptr(col).value, (ptr(mask).value if mask is not None else None)
         side.row_group_ptr, side.group_rel = ptr(gptr).value, ptr(grel).value
         side.group_start, side.group_count = ptr(gstart).value, ptr(gcount).value
-        side.max_rel = _max_relation(grel)
+        side.min_rel, side.max_rel = _relation_range(grel)
         return side
 
 
-# Largest relation id of a group-relation array, kept per tensor object and
-# version (the CSR arrays of a graph serve every hop; a read of the maximum
-# costs a reduction and a device synchronization).
-_MAX_REL = {}
+# Smallest and largest relation id of a group-relation array, kept per
+# tensor object and version (the CSR arrays of a graph serve every hop; a
+# read of the range costs reductions and a device synchronization).
+_REL_RANGE = {}
 
 
-def _max_relation(grel):
+def _relation_range(grel):
     if grel.numel() == 0:
-        return -1
-    hit = _MAX_REL.get(id(grel))
+        return 0, -1
+    hit = _REL_RANGE.get(id(grel))
     if hit is not None and hit[0]() is grel and hit[1] == grel._version:
         return hit[2]
-    for k in [k for k, v in _MAX_REL.items() if v[0]() is None]:
-        del _MAX_REL[k]
-    m = int(grel.max())
-    _MAX_REL[id(grel)] = (weakref.ref(grel), grel._version, m)
-    return m
+    for k in [k for k, v in _REL_RANGE.items() if v[0]() is None]:
+        del _REL_RANGE[k]
+    lo, hi = (int(x) for x in torch.stack([grel.min(), grel.max()]).tolist())
+    _REL_RANGE[id(grel)] = (weakref.ref(grel), grel._version, (lo, hi))
+    return lo, hi
 
 
 # Hops with at least this many entries visit them by source entity.
@@ -965,8 +965,9 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
         _require_cuda(w)
         w_flat = w.reshape(R, -1).contiguous().float()
         n = w_flat.shape[1]
-        if max(sides.ori.max_rel, sides.inv.max_rel) >= r_size or 2 * r_size > n:
-            raise ValueError("relation ids must be < r_size and w must hold 2*r_size (+1) columns")
+        if (max(sides.ori.max_rel, sides.inv.max_rel) >= r_size or min(sides.ori.min_rel, sides.inv.min_rel) < 0
+                or 2 * r_size > n):
+            raise ValueError("relation ids must be in [0, r_size) and w must hold 2*r_size (+1) columns")
     nnz = sp_v.numel()
     lib = _lib.lib()
     st = _stream(sp_v)
