@@ -127,17 +127,31 @@ struct SpTake {
     float th;
     int32_t cut;
     double wsum, phase;
+    double wsum_r, spare_r;  // RN(1 / wsum), RN(1 / spare)
     int32_t target, residual, spare, prefix, cum;
 };
 
+// x / y rounded to nearest, from yr = RN(1 / y) computed once per divisor
+// (Markstein's theorem: q0 = RN(x * yr) is within an ulp of x / y, the
+// remainder x - q0 * y is exact with an FMA, and RN(q0 + r * yr) is the
+// correctly rounded quotient; the operands here stay far from overflow and
+// underflow).  Three instructions instead of a full division per group.
+__device__ __forceinline__ double sp_div_r(double x, double y, double yr) {
+    const double q0 = __dmul_rn(x, yr);
+    const double r = __fma_rn(-q0, y, x);
+    return __fma_rn(r, yr, q0);
+}
+
 __device__ __forceinline__ int32_t sp_quota_base(const SpTake &tk, float wv, int32_t cnt) {
-    return (int32_t)fmin((double)cnt, floor(__ddiv_rn(__dmul_rn((double)tk.target, (double)wv), tk.wsum)));
+    return (int32_t)fmin((double)cnt,
+                         floor(sp_div_r(__dmul_rn((double)tk.target, (double)wv), tk.wsum, tk.wsum_r)));
 }
 
 __device__ __forceinline__ int32_t sp_quota_cum(const SpTake &tk, int32_t p) {
     return p == tk.spare ? tk.residual
                          : (int32_t)floor(__dadd_rn(
-                               __ddiv_rn(__dmul_rn((double)tk.residual, (double)p), (double)tk.spare), tk.phase));
+                               sp_div_r(__dmul_rn((double)tk.residual, (double)p), (double)tk.spare, tk.spare_r),
+                               tk.phase));
 }
 
 // exponent of the lowest set bit's place value of a positive finite float
@@ -229,7 +243,8 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     q.cap = cap;
     q.target = K < cap ? K : cap;
     SpTake tk{};
-    tk.wsum = ws;
+    tk.wsum = fl_uniform_f64(ws);
+    tk.wsum_r = __ddiv_rn(1.0, tk.wsum);
     tk.target = (int32_t)q.target;
     long long alloc = 0;
     for (uint32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
@@ -272,9 +287,11 @@ __device__ __forceinline__ SpTake sp_take(int mode, float thv, int32_t ct, const
     if (!Q || !__builtin_isnan(thv)) { tk.kind = TAKE_TH; return tk; }
     tk.kind = TAKE_QUOTA;
     tk.wsum = qp->wsum;
+    tk.wsum_r = __ddiv_rn(1.0, tk.wsum);
     tk.target = (int32_t)qp->target;
     tk.residual = (int32_t)qp->residual;
     tk.spare = (int32_t)qp->spare;
+    tk.spare_r = __ddiv_rn(1.0, (double)tk.spare);
     tk.prefix = 0;
     tk.cum = 0;  // cum(0) = floor(phase) = 0
     const uint64_t z = (uint64_t)seed ^ ((uint64_t)b * 0x9e3779b97f4a7c15ull) ^ ((uint64_t)l * 0xbf58476d1ce4e5b9ull) ^
