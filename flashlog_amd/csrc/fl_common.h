@@ -136,6 +136,12 @@ __device__ __forceinline__ T fl_ld32(const T *base, uint32_t idx) {
     return *reinterpret_cast<const T *>(reinterpret_cast<const char *>(base) + (uint32_t)(idx * (uint32_t)sizeof(T)));
 }
 
+// base[idx] = v with the byte offset computed in 32 bits (as fl_ld32).
+template <typename T>
+__device__ __forceinline__ void fl_st32(T *base, uint32_t idx, T v) {
+    *reinterpret_cast<T *>(reinterpret_cast<char *>(base) + (uint32_t)(idx * (uint32_t)sizeof(T))) = v;
+}
+
 // The wave's index within its workgroup, in a scalar register (so that
 // per-wave indices, and loads at them, stay scalar).
 __device__ __forceinline__ int fl_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / FL_WAVE)); }

@@ -1019,7 +1019,6 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
         fl_wave_sync();  // marks read before the next round clears them
         const int32_t it = q0 + lane;
         if (it >= (int32_t)nitems) continue;
-        const int64_t k = base + it;
         int32_t dst = -1, pp = -1;
         float val = 0.0f;
         uint32_t tie = SP_TIE_IDENTITY;
@@ -1041,12 +1040,13 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
                 pp = pj;
             }
         }
-        raw_dst[k] = dst;
-        raw_val[k] = val;
-        if (MAXT) raw_tie[k] = tie;
+        // the entry's items from wave-uniform bases, 32-bit offsets
+        fl_st32(raw_dst + base, (uint32_t)it, dst);
+        fl_st32(raw_val + base, (uint32_t)it, val);
+        if (MAXT) fl_st32(raw_tie + base, (uint32_t)it, tie);
         if (BWD) {
-            if (raw_pos) raw_pos[k] = pp;
-            raw_col[k] = (int16_t)(mj & SP_RUN_COL);
+            if (raw_pos) fl_st32(raw_pos + base, (uint32_t)it, pp);
+            fl_st32(raw_col + base, (uint32_t)it, (int16_t)(mj & SP_RUN_COL));
         }
     }
 }
