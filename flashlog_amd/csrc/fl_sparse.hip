@@ -1077,8 +1077,9 @@ __global__ __launch_bounds__(SP_NT) void k_sp_hist(int64_t R, SpRows rows, const
     const int c = (int)((i1e - i0) < SP_TILE ? (i1e - i0) : SP_TILE);
     for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) hb[q] = 0;
     __syncthreads();
-    for (int idx = threadIdx.x; idx < c; idx += SP_NT) {
-        const int32_t d = raw_dst[i0 + idx];
+    const int32_t *__restrict__ tdst = raw_dst + i0;
+    for (uint32_t idx = threadIdx.x; idx < (uint32_t)c; idx += SP_NT) {
+        const int32_t d = fl_ld32(tdst, idx);
         if (d >= 0) atomicAdd(&hb[d >> SP_S], 1);
     }
     __syncthreads();
@@ -1197,7 +1198,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         const int idx = t * SP_IPT + j;
         uint32_t key = 0xFFFFF000u | (uint32_t)idx;  // padding and holes sort last
         if (idx < c) {
-            const int32_t d = raw_dst[i0 + idx];
+            const int32_t d = fl_ld32(raw_dst + i0, (uint32_t)idx);
             if (d >= 0) key = ((uint32_t)(d >> SP_S) << 12) | (uint32_t)idx;
         }
         kb[0][idx] = key;
@@ -1239,11 +1240,11 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
             }
             q = bb[(int64_t)bk * nt] + (p - lo);
         }
-        const int idx = (int)(key & 4095u);
-        part_dst[q] = raw_dst[i0 + idx];
-        part_val[q] = raw_val[i0 + idx];
-        if (part_inv) part_inv[i0 + idx] = (int32_t)q;
-        if (part_tie) part_tie[q] = raw_tie[i0 + idx];
+        const uint32_t idx = key & 4095u;
+        part_dst[q] = fl_ld32(raw_dst + i0, idx);
+        part_val[q] = fl_ld32(raw_val + i0, idx);
+        if (part_inv) fl_st32(part_inv + i0, idx, (int32_t)q);
+        if (part_tie) part_tie[q] = fl_ld32(raw_tie + i0, idx);
     }
 }
 
@@ -2273,11 +2274,18 @@ __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows
         start = base[rows.tile_base[r] * rows.NB + bk * nt];
     }
     const int64_t b = r / L, l = r - (r / L) * L;
-    for (int64_t k = fl_lane(); k < cnt; k += FL_WAVE) {
-        ob[o0 + k] = b;
-        ol[o0 + k] = l;
-        oe[o0 + k] = dst_arr[start + k];
-        ov[o0 + k] = val_arr[start + k];
+    // a bucket's outputs (at most 8192) from wave-uniform bases, 32-bit offsets
+    int64_t *__restrict__ pb = ob + o0;
+    int64_t *__restrict__ pl = ol + o0;
+    int64_t *__restrict__ pe = oe + o0;
+    float *__restrict__ pv = ov + o0;
+    const int32_t *__restrict__ sd = dst_arr + start;
+    const float *__restrict__ svl = val_arr + start;
+    for (uint32_t k = fl_lane(); k < (uint32_t)cnt; k += FL_WAVE) {
+        fl_st32(pb, k, b);
+        fl_st32(pl, k, l);
+        fl_st32(pe, k, (int64_t)fl_ld32(sd, k));
+        fl_st32(pv, k, fl_ld32(svl, k));
     }
 }
 
@@ -2313,22 +2321,25 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
         for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) obase[q] = orow[q];
         __syncthreads();
     }
+    // the tile's items from wave-uniform bases, 32-bit offsets
+    const int32_t *__restrict__ tdst = raw_dst + i0;
+    int32_t *__restrict__ tloc = raw_local + i0;
+    const int32_t *__restrict__ tinv = part_inv ? part_inv + i0 : nullptr;
 #pragma unroll 4
-    for (int idx = threadIdx.x; idx < c; idx += SP_NT) {
-        const int64_t k = i0 + idx;
-        if (part_inv) {
+    for (uint32_t idx = threadIdx.x; idx < (uint32_t)c; idx += SP_NT) {
+        if (tinv) {
             // partitioned: the local index sits at the item's partition position
             // (holes were not partitioned)
-            const int32_t d = raw_dst[k];
+            const int32_t d = fl_ld32(tdst, idx);
             int32_t o = -1;
             if (d >= 0) {
-                const int32_t loc = part_local[part_inv[k]];
+                const int32_t loc = part_local[fl_ld32(tinv, idx)];
                 if (loc >= 0) o = (int32_t)((lds ? obase[d >> SP_S] : orow[d >> SP_S]) + loc);
             }
-            raw_local[k] = o;
+            fl_st32(tloc, idx, o);
         } else {
-            const int32_t loc = raw_local[k];
-            raw_local[k] = loc >= 0 ? (int32_t)(orow[0] + loc) : -1;
+            const int32_t loc = fl_ld32(tloc, idx);
+            fl_st32(tloc, idx, loc >= 0 ? (int32_t)(orow[0] + loc) : -1);
         }
     }
 }
