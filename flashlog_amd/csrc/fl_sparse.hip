@@ -1776,7 +1776,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64
 // list).  One pass over the bucket marks its destinations; with more than
 // SP_FEW the bucket goes to a fallback list (k_sp_accum_mid / k_sp_accum_hot).
 // Otherwise destination j (in destination order) is slot j, the bucket's
-// output j, and thread j owns its sum in a register.  Chunks of SP_CHUNK
+// output j, and thread j owns its sum in a register.  Chunks of SP_FEW_CHUNK
 // items in raw order: each item's slot is ranked among the equal slots of its
 // wave and round with ballots (as sp_block_sort does, one 6-bit pass), the
 // values are scattered slot-major into LDS in raw order within each slot, and
@@ -1785,7 +1785,8 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64
 // with one bucket per row the bucket is the row's raw items) are skipped.
 constexpr int SP_FEW = 64;
 constexpr int SP_FEW_RB = 6;
-constexpr int SP_FEW_IPT = SP_CHUNK / SP_NT;               // 8
+constexpr int SP_FEW_CHUNK = 1024;  // items per ranked chunk
+constexpr int SP_FEW_IPT = SP_FEW_CHUNK / SP_NT;
 constexpr int SP_FEW_SPAN = SP_FEW_IPT * SP_NWV;           // (round, wave) entries of one slot
 constexpr int SP_FEW_TAB = SP_FEW * (SP_FEW_SPAN + 1);     // one count table, padded per slot
 constexpr int SP_FEW_PER = SP_FEW * SP_FEW_SPAN / SP_NT;   // scanned entries per thread
@@ -1811,7 +1812,7 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
     }
     __syncthreads();  // table cleared
     int cur = 0;
-    for (int64_t c0 = 0; c0 < n; c0 += SP_CHUNK) {
+    for (int64_t c0 = 0; c0 < n; c0 += SP_FEW_CHUNK) {
         uint8_t sl[SP_FEW_IPT], rk[SP_FEW_IPT];
         float vv[SP_FEW_IPT];
         uint32_t okm = 0;  // bit j: item j exists and is no hole
@@ -1839,10 +1840,10 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
             vv[j] = pv[j];
         }
         // the next chunk's items are requested while this one is scanned and added
-        if (c0 + SP_CHUNK < n) {
+        if (c0 + SP_FEW_CHUNK < n) {
 #pragma unroll
             for (int j = 0; j < SP_FEW_IPT; ++j) {
-                const int64_t k = c0 + SP_CHUNK + (int64_t)j * SP_NT + t;
+                const int64_t k = c0 + SP_FEW_CHUNK + (int64_t)j * SP_NT + t;
                 pd[j] = k < n ? dst_arr[start + k] : 0;
                 pv[j] = k < n ? val_arr[start + k] : 0.0f;
             }
@@ -1900,7 +1901,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_few(SpRows rows, const int64
     __shared__ uint32_t bits[SP_W / 32];
     __shared__ int wpre[SP_W / 32];
     __shared__ int32_t slot_dl[SP_FEW];
-    __shared__ __align__(16) float sv[SP_CHUNK];
+    __shared__ __align__(16) float sv[SP_FEW_CHUNK];
     __shared__ uint16_t tab[2][SP_FEW_TAB];
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
     __shared__ int claim;
