@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 21
+ABI_VERSION = 22
 FL_SEG = 32
 FL_SUP = 16
 
@@ -164,6 +164,11 @@ _SIGS = {
                             [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "fl_sparse_race_select": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 4 +
                               [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "fl_sparse_race_select_compact": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64] * 4 +
+                                      [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t] + [ctypes.c_void_p] * 6),
+    "fl_sparse_entry_order_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 2),
+    "fl_sparse_entry_order": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                             ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "fl_sparse_normalize_forward": (ctypes.c_int, [ctypes.c_void_p] * 4 + [ctypes.c_int64] * 3 +
                                     [ctypes.c_float] + [ctypes.c_void_p] * 4),
     "fl_sparse_gather": (ctypes.c_int, [ctypes.c_void_p] * 5 + [ctypes.c_int64] + [ctypes.c_void_p] * 3 +

@@ -2554,6 +2554,27 @@ __global__ void k_sp_order_check(const int32_t *__restrict__ seen, int64_t nnz, 
     if (i < nnz && seen[i] != 1) atomicMax((unsigned long long *)err, 1ull);
 }
 
+// Entry visiting order by source entity (a counting sort; entries of one
+// entity in any order): rank[i] = the entry's slot among its entity's
+// entries, then order[start of entity + rank] = i.  Entity ids outside
+// [0, E) share the last bin (the plan reports them).
+__global__ void k_sp_ord_count(const int64_t *__restrict__ se, int64_t nnz, int64_t E, int32_t *__restrict__ cnt,
+                               int32_t *__restrict__ rank) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    const int64_t e = se[i];
+    rank[i] = atomicAdd(&cnt[(e >= 0 && e < E) ? e : E], 1);
+}
+
+__global__ void k_sp_ord_place(const int64_t *__restrict__ se, int64_t nnz, int64_t E,
+                               const int64_t *__restrict__ start, const int32_t *__restrict__ rank,
+                               int32_t *__restrict__ order) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nnz) return;
+    const int64_t e = se[i];
+    order[start[(e >= 0 && e < E) ? e : E] + rank[i]] = (int32_t)i;
+}
+
 // Chunk counts in visiting order.
 __global__ void k_sp_gather_nch(const int32_t *__restrict__ nch, const int32_t *__restrict__ order, int64_t nnz,
                                 int32_t *__restrict__ out) {
@@ -2702,7 +2723,7 @@ __device__ __forceinline__ unsigned long long fl_order_key64(double d) {
 
 __global__ __launch_bounds__(NM_NT0) void k_race_rows(const int64_t *__restrict__ row_ptr,
                                                       const float *__restrict__ v, int64_t c,
-                                                      int32_t *__restrict__ over) {
+                                                      int32_t *__restrict__ over, int64_t *__restrict__ kept) {
     __shared__ int red[NM_NT0 / FL_WAVE];
     const int64_t r = blockIdx.x;
     const int64_t a = row_ptr[r], b = row_ptr[r + 1];
@@ -2715,6 +2736,7 @@ __global__ __launch_bounds__(NM_NT0) void k_race_rows(const int64_t *__restrict_
         long long t = 0;
         for (int q = 0; q < NM_NT0 / FL_WAVE; ++q) t += red[q];
         over[r] = t > c ? 1 : 0;
+        kept[r] = t > c ? c : b - a;  // an over-limit row keeps exactly c of its nonzeros
     }
 }
 
@@ -2737,11 +2759,30 @@ __global__ void k_race_keys(const float *__restrict__ v, int64_t nnz, const int3
     keys[i] = cand[i] ? fl_order_key64(__dsub_rn(log((double)v[i]), log(noise[cand_off[i]]))) : 0ull;
 }
 
+// With a compaction (entries non-null): the kept entries of row r also go,
+// in entry order, to positions kept_off[r] .. of entries (their indices) and
+// of ob, ol, oe, ov (their coordinates and values).
+struct SpCompact {
+    const int64_t *sb, *sl, *se;
+    const float *v;
+    const int64_t *kept_off;
+    int64_t *entries, *ob, *ol, *oe;
+    float *ov;
+};
+
+__device__ __forceinline__ void sp_compact_put(const SpCompact &cp, int64_t i, int64_t q) {
+    cp.entries[q] = i;
+    cp.ob[q] = cp.sb[i];
+    cp.ol[q] = cp.sl[i];
+    cp.oe[q] = cp.se[i];
+    cp.ov[q] = cp.v[i];
+}
+
 __global__ __launch_bounds__(TOPC_NT) void k_race_select(const int64_t *__restrict__ row_ptr,
                                                         const int32_t *__restrict__ over,
                                                         const int32_t *__restrict__ cand,
                                                         const unsigned long long *__restrict__ keys, int64_t c,
-                                                        int32_t *__restrict__ keep) {
+                                                        int32_t *__restrict__ keep, SpCompact cp) {
     __shared__ int hist[2048];
     __shared__ int lds_scan[TOPC_NT / FL_WAVE + 1];
     __shared__ int sel_bin, sel_need, s_last, s_done;
@@ -2750,7 +2791,11 @@ __global__ __launch_bounds__(TOPC_NT) void k_race_select(const int64_t *__restri
     const int t = threadIdx.x;
     if (n == 0) return;
     if (!over[row]) {
-        for (int64_t k = t; k < n; k += TOPC_NT) keep[a + k] = 1;
+        const int64_t q0 = cp.entries ? cp.kept_off[row] : 0;
+        for (int64_t k = t; k < n; k += TOPC_NT) {
+            keep[a + k] = 1;
+            if (cp.entries) sp_compact_put(cp, a + k, q0 + k);
+        }
         return;
     }
     // radix select of the c-th largest candidate key, most significant first
@@ -2796,13 +2841,23 @@ __global__ __launch_bounds__(TOPC_NT) void k_race_select(const int64_t *__restri
         }
         last = s_last;
     }
-    for (int64_t k = t; k < n; k += TOPC_NT) {
+    const int64_t q0 = cp.entries ? cp.kept_off[row] : 0;
+    int64_t run = 0;
+    for (int64_t base = 0; base < n; base += TOPC_NT) {
+        const int64_t k = base + t;
         int kp = 0;
-        if (cand[a + k]) {
+        if (k < n && cand[a + k]) {
             const unsigned long long key = keys[a + k];
             kp = key > cutkey || (key == cutkey && k <= last);
         }
-        keep[a + k] = kp;
+        if (k < n) keep[a + k] = kp;
+        if (cp.entries) {
+            // the row keeps exactly c entries: ranks beyond c are never written
+            int tot;
+            const int ex = fl_block_excl_scan<TOPC_NT>(kp, lds_scan, &tot);
+            if (kp && run + ex < c) sp_compact_put(cp, a + k, q0 + run + ex);
+            run += tot;
+        }
     }
 }
 
@@ -3519,7 +3574,7 @@ int fl_sparse_topc(void *stream, const int64_t *sp_b, const int64_t *sp_l, const
 // Sampled c1 workspace: row pointer, over flags, candidate flags and
 // offsets, order keys, scan scratch.
 struct SpRace {
-    int64_t *row_ptr, *cand_off, *tmp;
+    int64_t *row_ptr, *cand_off, *tmp, *kept, *kept_off;
     int32_t *over, *cand;
     unsigned long long *keys;
     size_t bytes;
@@ -3532,10 +3587,12 @@ static SpRace sp_race_layout(int64_t nnz, int64_t R, char *base) {
     const int64_t n1 = nnz > 0 ? nnz : 1;
     x.row_ptr = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
     x.over = (int32_t *)take(sizeof(int32_t) * (size_t)(R > 0 ? R : 1));
+    x.kept = (int64_t *)take(sizeof(int64_t) * (size_t)(R > 0 ? R : 1));
+    x.kept_off = (int64_t *)take(sizeof(int64_t) * (size_t)(R + 1));
     x.cand = (int32_t *)take(sizeof(int32_t) * (size_t)n1);
     x.cand_off = (int64_t *)take(sizeof(int64_t) * (size_t)(nnz + 1));
     x.keys = (unsigned long long *)take(sizeof(unsigned long long) * (size_t)n1);
-    x.tmp = (int64_t *)take(scan_tmp_bytes(nnz + 1));
+    x.tmp = (int64_t *)take(scan_tmp_bytes((nnz > R ? nnz : R) + 1));
     x.bytes = off;
     return x;
 }
@@ -3554,20 +3611,25 @@ int fl_sparse_race_plan(void *stream, const int64_t *sp_b, const int64_t *sp_l, 
     if (ws_bytes < fl_sparse_race_bytes(nnz, R)) return fl_fail(FL_ERR_ARG, "sparse_race: workspace too small");
     SpRace x = sp_race_layout(nnz, R, (char *)ws);
     hipStream_t st = (hipStream_t)stream;
-    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3(1), dim3(64), 0, st, info, (int64_t)2, (int64_t)0);
+    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3(1), dim3(64), 0, st, info, (int64_t)3, (int64_t)0);
     FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, x.row_ptr, R + 1,
               (int64_t)0);
     const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
     FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, sp_b, nnz,
               B, L, INT64_MAX, x.row_ptr, info + 1);
     if (R > 0)
-        FL_LAUNCH("k_race_rows", k_race_rows, dim3((unsigned)R), dim3(NM_NT0), 0, st, x.row_ptr, v, c, x.over);
+        FL_LAUNCH("k_race_rows", k_race_rows, dim3((unsigned)R), dim3(NM_NT0), 0, st, x.row_ptr, v, c, x.over,
+                  x.kept);
     if (nnz > 0)
         FL_LAUNCH("k_race_flags", k_race_flags, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, v,
                   nnz, L, x.over, x.cand, info + 1);
     int rc;
     if ((rc = exclusive_scan(st, x.cand, x.cand_off, nnz, x.tmp)) != FL_OK) return rc;
     FL_LAUNCH("k_fill_from", k_fill_from, dim3(1), dim3(1), 0, st, x.cand_off + nnz, info);
+    if (R > 0) {
+        if ((rc = exclusive_scan(st, x.kept, x.kept_off, R, x.tmp)) != FL_OK) return rc;
+        FL_LAUNCH("k_fill_from", k_fill_from, dim3(1), dim3(1), 0, st, x.kept_off + R, info + 2);
+    }
     return fl_check_launch("sparse_race_plan");
 }
 
@@ -3583,8 +3645,66 @@ int fl_sparse_race_select(void *stream, const float *v, int64_t nnz, int64_t B, 
     FL_LAUNCH("k_race_keys", k_race_keys, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, v, nnz, x.cand,
               x.cand_off, noise, x.keys);
     FL_LAUNCH("k_race_select", k_race_select, dim3((unsigned)R), dim3(TOPC_NT), 0, st, x.row_ptr, x.over, x.cand,
-              x.keys, c, keep);
+              x.keys, c, keep, SpCompact{});
     return fl_check_launch("sparse_race_select");
+}
+
+int fl_sparse_race_select_compact(void *stream, const int64_t *sp_b, const int64_t *sp_l, const int64_t *sp_e,
+                                  const float *v, int64_t nnz, int64_t B, int64_t L, int64_t c, const double *noise,
+                                  void *ws, size_t ws_bytes, int32_t *keep, int64_t *entries, int64_t *out_b,
+                                  int64_t *out_l, int64_t *out_e, float *out_v) {
+    if (c < 1 || nnz < 0 || B < 0 || L < 0) return fl_fail(FL_ERR_ARG, "sparse_race_select: bad arguments");
+    const int64_t R = B * L;
+    if (!ws || ws_bytes < fl_sparse_race_bytes(nnz, R)) return fl_fail(FL_ERR_ARG, "sparse_race_select: workspace");
+    if (nnz == 0 || R == 0) return FL_OK;
+    if (!sp_b || !sp_l || !sp_e || !v || !noise || !keep || !entries || !out_b || !out_l || !out_e || !out_v)
+        return fl_fail(FL_ERR_ARG, "sparse_race_select: null argument");
+    SpRace x = sp_race_layout(nnz, R, (char *)ws);
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_race_keys", k_race_keys, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, v, nnz, x.cand,
+              x.cand_off, noise, x.keys);
+    const SpCompact cp{sp_b, sp_l, sp_e, v, x.kept_off, entries, out_b, out_l, out_e, out_v};
+    FL_LAUNCH("k_race_select", k_race_select, dim3((unsigned)R), dim3(TOPC_NT), 0, st, x.row_ptr, x.over, x.cand,
+              x.keys, c, keep, cp);
+    return fl_check_launch("sparse_race_select");
+}
+
+static size_t sp_order_layout(int64_t nnz, int64_t E, char *base, int32_t **cnt, int32_t **rank, int64_t **start,
+                              int64_t **tmp) {
+    size_t off = 0;
+    auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
+    *cnt = (int32_t *)take(sizeof(int32_t) * (size_t)(E + 1));
+    *rank = (int32_t *)take(sizeof(int32_t) * (size_t)(nnz > 0 ? nnz : 1));
+    *start = (int64_t *)take(sizeof(int64_t) * (size_t)(E + 2));
+    *tmp = (int64_t *)take(scan_tmp_bytes(E + 2));
+    return off;
+}
+
+size_t fl_sparse_entry_order_bytes(int64_t nnz, int64_t E) {
+    if (nnz < 0 || E < 0) return 0;
+    int32_t *a, *b;
+    int64_t *c, *d;
+    return sp_order_layout(nnz, E, nullptr, &a, &b, &c, &d);
+}
+
+int fl_sparse_entry_order(void *stream, const int64_t *sp_e, int64_t nnz, int64_t E, void *ws, size_t ws_bytes,
+                          int32_t *order) {
+    if (nnz < 0 || E < 0 || nnz > INT32_MAX) return fl_fail(FL_ERR_ARG, "sparse_entry_order: bad size");
+    if (nnz == 0) return FL_OK;
+    if (!sp_e || !ws || !order) return fl_fail(FL_ERR_ARG, "sparse_entry_order: null argument");
+    if (ws_bytes < fl_sparse_entry_order_bytes(nnz, E)) return fl_fail(FL_ERR_ARG, "sparse_entry_order: workspace");
+    int32_t *cnt, *rank;
+    int64_t *start, *tmp;
+    sp_order_layout(nnz, E, (char *)ws, &cnt, &rank, &start, &tmp);
+    hipStream_t st = (hipStream_t)stream;
+    FL_LAUNCH("k_fill_i32", k_fill_i32, dim3((unsigned)((E + 1 + 255) / 256)), dim3(256), 0, st, cnt, E + 1, 0);
+    FL_LAUNCH("k_sp_ord_count", k_sp_ord_count, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, sp_e, nnz, E,
+              cnt, rank);
+    int rc;
+    if ((rc = exclusive_scan(st, cnt, start, E + 1, tmp)) != FL_OK) return rc;
+    FL_LAUNCH("k_sp_ord_place", k_sp_ord_place, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, sp_e, nnz, E,
+              start, rank, order);
+    return fl_check_launch("sparse_entry_order");
 }
 
 size_t fl_sparse_rowptr_bytes(int64_t R) { return al(sizeof(int64_t) * (size_t)(R + 1)) + al(sizeof(int64_t) * 2); }

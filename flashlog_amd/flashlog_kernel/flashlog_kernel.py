@@ -925,11 +925,18 @@ def _relation_range(grel):
 # Hops with at least this many entries visit them by source entity.
 _ENTRY_ORDER_MIN = 4096
 
-def _entry_order(sp_e):
+def _entry_order(sp_e, E):
     """Entries by source entity: a source's rows then share cached group
     records in the plan and the run writer (any order among a source's
-    entries; int32 keys for a radix sort)."""
-    return torch.sort(sp_e.to(torch.int32))[1].to(torch.int32)
+    entries: fl_sparse_entry_order's counting sort)."""
+    nnz = sp_e.numel()
+    lib = _lib.lib()
+    ws = torch.empty(max(int(lib.fl_sparse_entry_order_bytes(nnz, int(E))), 1), dtype=torch.uint8,
+                     device=sp_e.device)
+    order = torch.empty(max(nnz, 1), dtype=torch.int32, device=sp_e.device)
+    check(lib.fl_sparse_entry_order(_stream(sp_e), ptr(sp_e), nnz, int(E), ptr(ws), ws.numel(), ptr(order)),
+          "sparse_entry_order")
+    return order[:nnz]
 
 
 # When a list, every sparse hop appends its sizes to it as {"nnz" (entries
@@ -975,7 +982,7 @@ def _sparse_forward(sp_b, sp_l, sp_e, sp_v, w, sides, B, L, E, r_size, wot_i, mo
     order = None
     for attempt in range(2):
         if mode != _SPARSE_FIXED and nnz >= _ENTRY_ORDER_MIN:
-            order = _entry_order(sp_e)
+            order = _entry_order(sp_e, E)
         h = FlSparseHop()
         h.entry_order = ptr(order).value if order is not None else None
         h.sp_b, h.sp_l, h.sp_e, h.sp_v = (ptr(t).value for t in (sp_b, sp_l, sp_e, sp_v))
@@ -1128,6 +1135,14 @@ def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, nu
     """Kept entries of the c1 budget per (item, rule) row of a coalesced state
     (flashlog_kernel.py:1092-1140), or None when nothing is pruned.  B: the
     batch size when the caller knows it (else 1 + the largest batch index)."""
+    picked = _sparse_topc_select(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, num_rules, sampling, B)
+    return None if picked is None else picked[0]
+
+
+def _sparse_topc_select(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, num_rules, sampling=False, B=None):
+    """(kept entries, their (b, l, e, v) or None) of the c1 budget, or None
+    when nothing is pruned.  The sampled race compacts the kept entries in
+    its select kernel, with their count known from its plan."""
     if topk_nodes is None:
         return None
     if topk_nodes < 0:
@@ -1143,7 +1158,8 @@ def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, nu
     sp_value = sp_value.contiguous().float()
     keep = torch.empty(sp_value.numel(), dtype=torch.int32, device=sp_value.device)
     if sampling and topk_nodes > 0:
-        return _sparse_race_entries(sp_batch, sp_level, sp_value, B, L, int(topk_nodes), keep)
+        return _sparse_race_entries(sp_batch, sp_level, sp_entity.long().contiguous(), sp_value, B, L,
+                                    int(topk_nodes), keep)
     row_ptr, err = _sparse_rows_scratch(B * L, sp_value.device)
     check(_lib.lib().fl_sparse_topc(_stream(sp_value), ptr(sp_batch), ptr(sp_level), ptr(sp_value),
                                     sp_value.numel(), B, L, int(topk_nodes), ptr(keep), ptr(row_ptr), ptr(err)),
@@ -1152,23 +1168,25 @@ def _sparse_topc_entries(sp_batch, sp_level, sp_entity, sp_value, topk_nodes, nu
         raise ValueError("sparse c1 needs a state coalesced by (batch, rule, entity)")
     if bool(keep.all()):
         return None
-    return torch.nonzero(keep, as_tuple=True)[0]
+    return torch.nonzero(keep, as_tuple=True)[0], None
 
 
-def _sparse_race_entries(sp_batch, sp_level, sp_value, B, L, c, keep):
+def _sparse_race_entries(sp_batch, sp_level, sp_entity, sp_value, B, L, c, keep):
     """Sampled c1 (flashlog_kernel.py:1121-1132): the exponential race over
     the nonzero entries of over-limit rows.  The Exp(1) noise is drawn as the
     reference draws it (one float64 per candidate, entry order, torch's
-    generator of the state's device)."""
+    generator of the state's device).  Returns (kept entries, their
+    (b, l, e, v)), both written by the select; the kept count comes with the
+    candidate count."""
     lib = _lib.lib()
     dev = sp_value.device
     nnz = sp_value.numel()
     ws = torch.empty(max(lib.fl_sparse_race_bytes(nnz, B * L), 1), dtype=torch.uint8, device=dev)
-    info = torch.empty(2, dtype=torch.int64, device=dev)
+    info = torch.empty(3, dtype=torch.int64, device=dev)
     st = _stream(sp_value)
     check(lib.fl_sparse_race_plan(st, ptr(sp_batch), ptr(sp_level), ptr(sp_value), nnz, B, L, c, ptr(ws),
                                   ws.numel(), ptr(info)), "sparse_race_plan")
-    ncand, err = info.tolist()
+    ncand, err, kept = info.tolist()
     if err in (1, 2):
         raise ValueError("sparse c1 needs a state coalesced by (batch, rule, entity)")
     if ncand == 0:
@@ -1176,9 +1194,14 @@ def _sparse_race_entries(sp_batch, sp_level, sp_value, B, L, c, keep):
     if err == 3:
         raise ValueError("Entity sampling requires finite nonnegative state scores")
     noise = torch.empty(ncand, dtype=torch.float64, device=dev).exponential_()
-    check(lib.fl_sparse_race_select(st, ptr(sp_value), nnz, B, L, c, ptr(noise), ptr(ws), ws.numel(), ptr(keep)),
+    entries = torch.empty(kept, dtype=torch.int64, device=dev)
+    out = torch.empty((3, kept), dtype=torch.int64, device=dev)
+    out_v = torch.empty(kept, dtype=torch.float32, device=dev)
+    check(lib.fl_sparse_race_select_compact(st, ptr(sp_batch), ptr(sp_level), ptr(sp_entity), ptr(sp_value), nnz,
+                                            B, L, c, ptr(noise), ptr(ws), ws.numel(), ptr(keep), ptr(entries),
+                                            ptr(out[0]), ptr(out[1]), ptr(out[2]), ptr(out_v)),
           "sparse_race_select")
-    return torch.nonzero(keep, as_tuple=True)[0]
+    return entries, (out[0], out[1], out[2], out_v)
 
 
 class _C1Pick:
@@ -1186,12 +1209,16 @@ class _C1Pick:
     None), applied to the state's arrays and undone on the gradient (the
     role of flashlog_kernel.py:1140-1155)."""
 
-    def __init__(self, entries, size):
-        self.entries, self.size = entries, size
+    def __init__(self, picked, size):
+        self.entries, self.taken = picked if picked is not None else (None, None)
+        self.size = size
 
     def take(self, *arrays):
         if self.entries is None:
             return arrays
+        if self.taken is not None:
+            # the selection wrote the kept (b, l, e, v) itself
+            return tuple(t.to(x.dtype) for t, x in zip(self.taken, arrays))
         return tuple(x.index_select(0, self.entries) for x in arrays)
 
     def untake(self, grad):
@@ -1201,7 +1228,7 @@ class _C1Pick:
 
 
 def _c1_pick(ctx, batch, level, entity, value, topk_nodes, num_rules, sampling=False, B=None):
-    pick = _C1Pick(_sparse_topc_entries(batch, level, entity, value, topk_nodes, num_rules, sampling, B),
+    pick = _C1Pick(_sparse_topc_select(batch, level, entity, value, topk_nodes, num_rules, sampling, B),
                    value.numel())
     ctx.c1_pick = pick
     return pick.take(batch, level, entity, value)
@@ -1469,6 +1496,10 @@ class FlashLogFunctionSparse3DCPUSumNorm(autograd.Function):
 
 
 def _normalize_forward(sp_b, sp_l, values, B, L, eps):
+    """As the reference's GPU path (flashlog.cu:2594-2649) the entry order
+    is not checked on the host (no device read): the state comes from
+    coalesce(), and rows out of order give unspecified values without any
+    access out of bounds."""
     _require_cuda(sp_b, sp_l, values)
     values = values.contiguous().float()
     R = B * L
@@ -1479,8 +1510,6 @@ def _normalize_forward(sp_b, sp_l, values, B, L, eps):
                                                  ptr(sp_l.long().contiguous()), ptr(values), values.numel(),
                                                  B, L, ctypes.c_float(eps), ptr(out), ptr(denom), ptr(row_ptr),
                                                  ptr(err)), "sparse_normalize")
-    if int(err) != 0:
-        raise ValueError("normalize_sparse3d needs a state coalesced by (batch, rule, entity)")
     return out, denom[:R], row_ptr
 
 
@@ -1493,6 +1522,19 @@ def _normalize_backward(row_ptr, grad, values, denom, eps):
     return gv
 
 
+def _stacked_rows(*rows):
+    """torch.stack(rows): a view when the rows already are the consecutive
+    rows of one contiguous [k, n] tensor (a state's own index tensor), else
+    a copy."""
+    r0 = rows[0]
+    n = r0.numel()
+    if all(r.dim() == 1 and r.dtype == r0.dtype and r.device == r0.device and r.stride(0) == 1 and r.numel() == n
+           and r.untyped_storage().data_ptr() == r0.untyped_storage().data_ptr()
+           and r.storage_offset() == r0.storage_offset() + k * n for k, r in enumerate(rows)):
+        return r0.as_strided((len(rows), n), (n, 1), r0.storage_offset())
+    return torch.stack(rows, dim=0)
+
+
 class Sparse3DNormalizeFunction(autograd.Function):
     """Per (b, l) row: v / max(sum of the row, eps) (flashlog_kernel.py:536-606)."""
 
@@ -1503,7 +1545,7 @@ class Sparse3DNormalizeFunction(autograd.Function):
         sp_entity = sp_entity.contiguous().long()
         values = sp_value.contiguous()
         out, denom, row_ptr = _normalize_forward(sp_batch, sp_level, values, int(B), int(L), float(eps))
-        idx = torch.stack([sp_batch, sp_level, sp_entity], dim=0)
+        idx = _stacked_rows(sp_batch, sp_level, sp_entity)
         ctx.save_for_backward(idx, values.float(), denom, row_ptr)
         ctx.B, ctx.L, ctx.E, ctx.eps = int(B), int(L), int(E), float(eps)
         return torch.sparse_coo_tensor(idx, out.to(sp_value.dtype), [int(B), int(L), int(E)], is_coalesced=True)

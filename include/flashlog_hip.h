@@ -414,14 +414,20 @@ int fl_sparse_topc(void *stream, const int64_t *sp_b, const int64_t *sp_l,
  * 1092-1140): the exponential race.  Two phases around the caller's noise
  * draw.  fl_sparse_race_plan (c >= 1; c = 0 is fl_sparse_topc): per row r =
  * b*L + l of a COO state sorted by row, rows with more than c nonzeros make
- * their nonzero entries candidates; info (device int64[2]) receives
- * {candidates, error} (error 1 index out of range, 2 not sorted by row,
- * 3 a candidate value not finite and positive).  The caller then draws one
- * Exp(1) double per candidate (entry order) into noise and calls
- * fl_sparse_race_select: in those rows keep[i] = 1 for the c candidates with
- * the largest log(v) - log(noise) (ties to the earlier entry), 0 for the
- * rest; other rows keep every entry.  ws is the same workspace in both
- * calls. */
+ * their nonzero entries candidates; info (device int64[3]) receives
+ * {candidates, error, kept} (error 1 index out of range, 2 not sorted by
+ * row, 3 a candidate value not finite and positive; kept = the entries the
+ * select will keep: c per over-limit row, every entry of the others).  The
+ * caller then draws one Exp(1) double per candidate (entry order) into noise
+ * and calls fl_sparse_race_select: in those rows keep[i] = 1 for the c
+ * candidates with the largest log(v) - log(noise) (ties to the earlier
+ * entry), 0 for the rest; other rows keep every entry.  ws is the same
+ * workspace in both calls.  fl_sparse_race_select_compact does the same and
+ * also writes the kept entries in entry order (the reference's
+ * torch.nonzero(keep) and the gathers of _prune_sparse_sources,
+ * flashlog_kernel.py:1137-1147): entries [kept] their indices, out_b, out_l,
+ * out_e, out_v [kept] their coordinates and values (kept from info[2], so
+ * the caller sizes them without another read of the device). */
 size_t fl_sparse_race_bytes(int64_t nnz, int64_t R);
 int fl_sparse_race_plan(void *stream, const int64_t *sp_b, const int64_t *sp_l,
                         const float *v, int64_t nnz, int64_t B, int64_t L,
@@ -430,6 +436,26 @@ int fl_sparse_race_select(void *stream, const float *v, int64_t nnz,
                           int64_t B, int64_t L, int64_t c,
                           const double *noise, void *ws, size_t ws_bytes,
                           int32_t *keep);
+int fl_sparse_race_select_compact(void *stream, const int64_t *sp_b,
+                                  const int64_t *sp_l, const int64_t *sp_e,
+                                  const float *v, int64_t nnz, int64_t B,
+                                  int64_t L, int64_t c, const double *noise,
+                                  void *ws, size_t ws_bytes, int32_t *keep,
+                                  int64_t *entries, int64_t *out_b,
+                                  int64_t *out_l, int64_t *out_e,
+                                  float *out_v);
+
+/* The entry visiting order a sparse hop may take (fl_sparse_hop.entry_order).
+ * No counterpart in the reference: a locality order for this library's plan
+ * and run writer (the entries of one source entity read the same group
+ * records); the hop's results do not depend on it.  order [nnz] (int32)
+ * lists the entries grouped by ascending entity id sp_e (a counting sort;
+ * the entries of one entity in any order).  nnz < 2^31; ws of
+ * fl_sparse_entry_order_bytes(nnz, E). */
+size_t fl_sparse_entry_order_bytes(int64_t nnz, int64_t E);
+int fl_sparse_entry_order(void *stream, const int64_t *sp_e, int64_t nnz,
+                          int64_t E, void *ws, size_t ws_bytes,
+                          int32_t *order);
 
 /* Bytes of the row pointer + error slots used by the normalize calls. */
 size_t fl_sparse_rowptr_bytes(int64_t R);

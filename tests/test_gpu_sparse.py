@@ -168,6 +168,12 @@ def test_normalize_sparse3d():
     out = fk.normalize_sparse3d(s)
     want, denom = O.sparse_normalize(b, l, v, B, L)
     assert np.array_equal(bits(out.values().detach().cpu().numpy()), bits(want))
+    # the output takes the input's index tensor as it is (no copy)
+    assert out._indices().data_ptr() == idx.data_ptr() and torch.equal(out._indices(), idx)
+    # separate index rows are stacked
+    rows = [idx[k].clone() for k in range(3)]
+    o2 = fk.Sparse3DNormalizeFunction.apply(*rows, vt.detach(), B, L, E, 1e-7)
+    assert torch.equal(o2._indices(), idx) and o2._indices().data_ptr() != idx.data_ptr()
     g = rng.standard_normal(v.shape[0]).astype(np.float32)
     (out.values() * torch.from_numpy(g).cuda()).sum().backward()
     row = b * L + l

@@ -208,6 +208,12 @@ def test_race_c1_matches_oracle(c):
     ref = O.sparse_topc_race(b, l, v, L, c, noise.cpu().numpy())
     assert kept is not None
     np.testing.assert_array_equal(kept.cpu().numpy(), ref)
+    # the select's own compaction: the kept coordinates and values in entry order
+    torch.manual_seed(99)
+    ent, taken = fk._sparse_topc_select(tb, tl, te, tv, c, L, sampling=True)
+    np.testing.assert_array_equal(ent.cpu().numpy(), ref)
+    for got, full in zip(taken, (b, l, e, v)):
+        np.testing.assert_array_equal(got.cpu().numpy(), full[ref])
     # validation: a negative candidate value is refused, as the reference does
     v2 = v.copy()
     v2[cand[0]] = -1.0
@@ -215,6 +221,18 @@ def test_race_c1_matches_oracle(c):
         fk._sparse_topc_entries(tb, tl, te, torch.from_numpy(v2).cuda(), c, L, sampling=True)
     # no row over the budget: nothing pruned, no noise drawn
     assert fk._sparse_topc_entries(tb, tl, te, tv, 100000 if c > 1 else v.shape[0], L, sampling=True) is None
+
+
+@pytest.mark.parametrize("nnz,E", [(1, 5), (5000, 7), (20000, 300000), (70000, 1000)])
+def test_entry_order_groups_entities(nnz, E):
+    """fl_sparse_entry_order: a permutation of the entries with ascending
+    entity ids (entries of one entity in any order)."""
+    fk = _fk()
+    rng = np.random.default_rng(nnz)
+    e = torch.from_numpy(rng.integers(0, E, nnz)).cuda()
+    order = fk._entry_order(e, E).long().cpu().numpy()
+    assert np.array_equal(np.sort(order), np.arange(nnz))
+    assert np.all(np.diff(e.cpu().numpy()[order]) >= 0)
 
 
 @pytest.mark.parametrize("mode", ["sum", "max"])
@@ -417,7 +435,7 @@ def test_entry_order_must_be_a_permutation(monkeypatch):
     rk, rv = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, 5)
     assert np.array_equal(_keys(good[0], L, E), rk)
 
-    def bad(sp_e):
+    def bad(sp_e, E):
         order = torch.argsort(sp_e).to(torch.int32)
         order[1] = order[0]
         return order
