@@ -1221,6 +1221,35 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         }
         __syncthreads();
     }
+    if (table && part_inv) {
+        // the keys move to registers and the key buffer takes the inverse map
+        // (raw index -> partition position), stored to part_inv coalesced
+        // instead of one scattered store per item
+        uint32_t key[SP_IPT];
+#pragma unroll
+        for (int j = 0; j < SP_IPT; ++j) key[j] = sorted[j * SP_NT + t];
+        __syncthreads();
+        int32_t *inv_lds = reinterpret_cast<int32_t *>(const_cast<uint32_t *>(sorted));
+#pragma unroll 4
+        for (int j = 0; j < SP_IPT; ++j) {
+            const int p = j * SP_NT + t;
+            if (p >= c) continue;
+            const uint32_t bk = key[j] >> 12;
+            const uint32_t idx = key[j] & 4095u;
+            if (bk == 0xFFFFFu) {  // hole: no partition position
+                inv_lds[idx] = -1;
+                continue;
+            }
+            const int64_t q = boff[bk] + p;
+            part_dst[q] = fl_ld32(raw_dst + i0, idx);
+            part_val[q] = fl_ld32(raw_val + i0, idx);
+            inv_lds[idx] = (int32_t)q;
+            if (part_tie) part_tie[q] = fl_ld32(raw_tie + i0, idx);
+        }
+        __syncthreads();
+        for (uint32_t idx = (uint32_t)t; idx < (uint32_t)c; idx += SP_NT) fl_st32(part_inv + i0, idx, inv_lds[idx]);
+        return;
+    }
 #pragma unroll 4
     for (int j = 0; j < SP_IPT; ++j) {
         const int p = j * SP_NT + t;  // striped: consecutive threads write consecutive slots
