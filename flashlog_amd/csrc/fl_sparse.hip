@@ -1110,25 +1110,26 @@ __device__ __forceinline__ uint32_t sp_lanes_below(unsigned long long m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-template <int IPT>
+template <int IPT, int NT = SP_NT>
 __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, int nbits, uint16_t *cnt,
                                    int *scan_lds) {
-    static_assert(IPT % 2 == 0 && IPT <= SP_SORT_IPT_MAX, "sort table sized for even IPT <= 16");
-    constexpr int SPAN = IPT * SP_NWV;                // entries of one digit
+    constexpr int NWV = NT / FL_WAVE;
+    static_assert(IPT % 2 == 0 && IPT * NWV <= SP_SORT_IPT_MAX * SP_NWV, "sort table sized for 64 (round, wave)s");
+    constexpr int SPAN = IPT * NWV;                   // entries of one digit
     constexpr int TAB = SP_ND * (SPAN + 1);           // one buffer, padded
-    constexpr int PER = SP_ND * SPAN / SP_NT;         // scanned entries per thread
+    constexpr int PER = SP_ND * SPAN / NT;            // scanned entries per thread
     const int t = threadIdx.x;
     const int lane = fl_lane();
     const int w = fl_wave_id();
     uint16_t *tab = cnt, *nxt = cnt + TAB;
-    for (int q = t; q < TAB; q += SP_NT) tab[q] = 0;
+    for (int q = t; q < TAB; q += NT) tab[q] = 0;
     __syncthreads();
     for (int shift = lo_bit; shift < lo_bit + nbits; shift += SP_RB) {
         uint32_t key[IPT];
         uint16_t dg[IPT], rk[IPT];
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            key[j] = kin[j * SP_NT + t];
+            key[j] = kin[j * NT + t];
             const int d = (int)((key[j] >> shift) & (SP_ND - 1));
             unsigned long long m = ~0ull;
 #pragma unroll
@@ -1139,7 +1140,7 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
             const uint32_t below = sp_lanes_below(m);
             dg[j] = (uint16_t)d;
             rk[j] = (uint16_t)below;
-            if (below == 0) tab[d * (SPAN + 1) + j * SP_NWV + w] = (uint16_t)__popcll(m);
+            if (below == 0) tab[d * (SPAN + 1) + j * NWV + w] = (uint16_t)__popcll(m);
         }
         __syncthreads();
         // exclusive scan in (digit, round, wave) order; the other buffer is cleared
@@ -1152,17 +1153,17 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
             sum += v[q];
         }
         int tot;
-        int run = fl_block_excl_scan<SP_NT>(sum, scan_lds, &tot);
+        int run = fl_block_excl_scan<NT>(sum, scan_lds, &tot);
 #pragma unroll
         for (int q = 0; q < PER; ++q) {
             const int f = t * PER + q;
             tab[f + f / SPAN] = (uint16_t)run;
             run += v[q];
         }
-        for (int q = t; q < TAB; q += SP_NT) nxt[q] = 0;
+        for (int q = t; q < TAB; q += NT) nxt[q] = 0;
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < IPT; ++j) kout[tab[dg[j] * (SPAN + 1) + j * SP_NWV + w] + rk[j]] = key[j];
+        for (int j = 0; j < IPT; ++j) kout[tab[dg[j] * (SPAN + 1) + j * NWV + w] + rk[j]] = key[j];
         __syncthreads();
         uint32_t *x = kin; kin = kout; kout = x;
         uint16_t *y = tab; tab = nxt; nxt = y;
@@ -1174,7 +1175,12 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
 // destination buckets (bases from the scanned histogram).  With part_inv
 // (a backward), every item's partition position is recorded at its raw
 // position (written within the tile's range, not scattered over the row).
-__global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, int nbits,
+// the partition's workgroup: one 4096-item tile over 512 threads (8 items
+// each: twice the waves per CU of 256 threads at the same LDS)
+constexpr int SP_PT_NT = 512;
+constexpr int SP_PT_IPT = SP_TILE / SP_PT_NT;
+
+__global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows rows, int nbits,
                                                        const int64_t *__restrict__ base,
                                                        const int32_t *__restrict__ raw_dst,
                                                        const float *__restrict__ raw_val,
@@ -1184,7 +1190,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
                                                        uint32_t *__restrict__ part_tie) {
     __shared__ __align__(16) uint32_t kb[2][SP_TILE];
     __shared__ uint16_t cnt[SP_SORT_TAB];
-    __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
+    __shared__ int scan_lds[SP_PT_NT / FL_WAVE + 1];
     const int64_t tile = fl_xcd_contig(blockIdx.x, gridDim.x);
     const int64_t r = sp_tile_row(rows.tile_base, R, tile);
     const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
@@ -1194,8 +1200,8 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
     const int c = (int)((i1e - i0) < SP_TILE ? (i1e - i0) : SP_TILE);
     const int t = threadIdx.x;
 #pragma unroll
-    for (int j = 0; j < SP_IPT; ++j) {
-        const int idx = t * SP_IPT + j;
+    for (int j = 0; j < SP_PT_IPT; ++j) {
+        const int idx = t * SP_PT_IPT + j;
         uint32_t key = 0xFFFFF000u | (uint32_t)idx;  // padding and holes sort last
         if (idx < c) {
             const int32_t d = fl_ld32(raw_dst + i0, (uint32_t)idx);
@@ -1204,7 +1210,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         kb[0][idx] = key;
     }
     __syncthreads();
-    const uint32_t *sorted = sp_block_sort<SP_IPT>(kb[0], kb[1], 12, nbits, cnt, scan_lds);
+    const uint32_t *sorted = sp_block_sort<SP_PT_IPT, SP_PT_NT>(kb[0], kb[1], 12, nbits, cnt, scan_lds);
     const int64_t *bb = base + rows.tile_base[r] * rows.NB + tl;
     // per bucket present: its output base minus its first sorted position
     // (one base load per bucket and tile), in the sort's idle buffer when the
@@ -1213,8 +1219,8 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
     const bool table = rows.NB <= SP_TILE / 2;
     if (table) {
 #pragma unroll 4
-        for (int j = 0; j < SP_IPT; ++j) {
-            const int p = j * SP_NT + t;
+        for (int j = 0; j < SP_PT_IPT; ++j) {
+            const int p = j * SP_PT_NT + t;
             if (p >= c) continue;
             const uint32_t bk = sorted[p] >> 12;
             if (bk != 0xFFFFFu && (p == 0 || (sorted[p - 1] >> 12) != bk)) boff[bk] = bb[(int64_t)bk * nt] - p;
@@ -1225,14 +1231,14 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
         // the keys move to registers and the key buffer takes the inverse map
         // (raw index -> partition position), stored to part_inv coalesced
         // instead of one scattered store per item
-        uint32_t key[SP_IPT];
+        uint32_t key[SP_PT_IPT];
 #pragma unroll
-        for (int j = 0; j < SP_IPT; ++j) key[j] = sorted[j * SP_NT + t];
+        for (int j = 0; j < SP_PT_IPT; ++j) key[j] = sorted[j * SP_PT_NT + t];
         __syncthreads();
         int32_t *inv_lds = reinterpret_cast<int32_t *>(const_cast<uint32_t *>(sorted));
 #pragma unroll 4
-        for (int j = 0; j < SP_IPT; ++j) {
-            const int p = j * SP_NT + t;
+        for (int j = 0; j < SP_PT_IPT; ++j) {
+            const int p = j * SP_PT_NT + t;
             if (p >= c) continue;
             const uint32_t bk = key[j] >> 12;
             const uint32_t idx = key[j] & 4095u;
@@ -1247,12 +1253,12 @@ __global__ __launch_bounds__(SP_NT) void k_sp_partition(int64_t R, SpRows rows, 
             if (part_tie) part_tie[q] = fl_ld32(raw_tie + i0, idx);
         }
         __syncthreads();
-        for (uint32_t idx = (uint32_t)t; idx < (uint32_t)c; idx += SP_NT) fl_st32(part_inv + i0, idx, inv_lds[idx]);
+        for (uint32_t idx = (uint32_t)t; idx < (uint32_t)c; idx += SP_PT_NT) fl_st32(part_inv + i0, idx, inv_lds[idx]);
         return;
     }
 #pragma unroll 4
-    for (int j = 0; j < SP_IPT; ++j) {
-        const int p = j * SP_NT + t;  // striped: consecutive threads write consecutive slots
+    for (int j = 0; j < SP_PT_IPT; ++j) {
+        const int p = j * SP_PT_NT + t;  // striped: consecutive threads write consecutive slots
         if (p >= c) continue;
         const uint32_t key = sorted[p];
         const uint32_t bk = key >> 12;
@@ -3437,7 +3443,7 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
                       rows, x.raw_dst, x.hist);
         if ((rc = exclusive_scan(st, x.hist, x.base, h->tiles * NB, x.tmp)) != FL_OK) return rc;
         if (h->tiles > 0)
-            FL_LAUNCH("k_sp_partition", k_sp_partition, dim3((unsigned)h->tiles), dim3(SP_NT), 0, st, R, rows,
+            FL_LAUNCH("k_sp_partition", k_sp_partition, dim3((unsigned)h->tiles), dim3(SP_PT_NT), 0, st, R, rows,
                       sp_bucket_bits(NB + 1), x.base, x.raw_dst, x.raw_val, x.part_dst, x.part_val,
                       raw_local ? x.part_inv : (int32_t *)nullptr, x.raw_tie, x.part_tie);
         dst_arr = x.part_dst;
