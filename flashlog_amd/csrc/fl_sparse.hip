@@ -1790,7 +1790,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64
         __syncthreads();  // the previous bucket is done with the LDS arrays
         if (threadIdx.x == 0) claim = atomicAdd(&ctr[1], 1);
         __syncthreads();
-        const int mi = claim;
+        const int mi = __builtin_amdgcn_readfirstlane(claim);  // uniform: scalar registers
         if (mi >= nmid) break;
         const int64_t slot = mid_list[mi];
         const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
@@ -1837,24 +1837,29 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
     const int w = fl_wave_id();
     for (int q = t; q < SP_FEW_TAB; q += SP_NT) tab[0][q] = 0;
     float acc = 0.0f;  // thread t < total: the sum of slot t
+    // the bucket's items from wave-uniform bases, 32-bit offsets (a bucket
+    // holds fewer than 2^31 items)
+    const int32_t *__restrict__ bd = dst_arr + start;
+    const float *__restrict__ bv = val_arr + start;
+    const uint32_t un = (uint32_t)n;
     int32_t pd[SP_FEW_IPT];
     float pv[SP_FEW_IPT];
 #pragma unroll
     for (int j = 0; j < SP_FEW_IPT; ++j) {  // striped: round j, thread t holds item j*SP_NT + t
-        const int64_t k = (int64_t)j * SP_NT + t;
-        pd[j] = k < n ? dst_arr[start + k] : 0;
-        pv[j] = k < n ? val_arr[start + k] : 0.0f;
+        const uint32_t k = (uint32_t)(j * SP_NT + t);
+        pd[j] = k < un ? fl_ld32(bd, k) : 0;
+        pv[j] = k < un ? fl_ld32(bv, k) : 0.0f;
     }
     __syncthreads();  // table cleared
     int cur = 0;
-    for (int64_t c0 = 0; c0 < n; c0 += SP_FEW_CHUNK) {
+    for (uint32_t c0 = 0; c0 < un; c0 += SP_FEW_CHUNK) {
         uint8_t sl[SP_FEW_IPT], rk[SP_FEW_IPT];
         float vv[SP_FEW_IPT];
         uint32_t okm = 0;  // bit j: item j exists and is no hole
 #pragma unroll
         for (int j = 0; j < SP_FEW_IPT; ++j) {
-            const int64_t k = c0 + (int64_t)j * SP_NT + t;
-            const bool valid = k < n && pd[j] >= 0;
+            const uint32_t k = c0 + (uint32_t)(j * SP_NT + t);
+            const bool valid = k < un && pd[j] >= 0;
             okm |= valid ? 1u << j : 0u;
             int sj = 0;
             if (valid) {
@@ -1869,18 +1874,18 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
             }
             const uint32_t below = sp_lanes_below(m);
             if (valid && below == 0) tab[cur][sj * (SP_FEW_SPAN + 1) + j * SP_NWV + w] = (uint16_t)__popcll(m);
-            if (valid && raw_local) raw_local[start + k] = sj;
+            if (valid && raw_local) fl_st32(raw_local + start, k, (int32_t)sj);
             sl[j] = (uint8_t)sj;
             rk[j] = (uint8_t)below;
             vv[j] = pv[j];
         }
         // the next chunk's items are requested while this one is scanned and added
-        if (c0 + SP_FEW_CHUNK < n) {
+        if (c0 + SP_FEW_CHUNK < un) {
 #pragma unroll
             for (int j = 0; j < SP_FEW_IPT; ++j) {
-                const int64_t k = c0 + SP_FEW_CHUNK + (int64_t)j * SP_NT + t;
-                pd[j] = k < n ? dst_arr[start + k] : 0;
-                pv[j] = k < n ? val_arr[start + k] : 0.0f;
+                const uint32_t k = c0 + SP_FEW_CHUNK + (uint32_t)(j * SP_NT + t);
+                pd[j] = k < un ? fl_ld32(bd, k) : 0;
+                pv[j] = k < un ? fl_ld32(bv, k) : 0.0f;
             }
         }
         __syncthreads();  // counts written; every thread is past its previous sum
@@ -1925,7 +1930,7 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
 
 // lists: hot_list (ctr[0] listed, ctr[1] claim), then mid_list (ctr[2],
 // ctr[3]); fallbacks to hot_fb (ctr[4]) and mid_fb (ctr[6]).
-__global__ __launch_bounds__(SP_NT) void k_sp_accum_few(SpRows rows, const int64_t *__restrict__ base,
+__global__ __launch_bounds__(SP_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_sp_accum_few(SpRows rows, const int64_t *__restrict__ base,
                                                        int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
                                                        int32_t *__restrict__ raw_local,
                                                        int32_t *__restrict__ out_count,
@@ -1951,7 +1956,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_few(SpRows rows, const int64
             claim = c;
         }
         __syncthreads();
-        const int ci = claim;
+        const int ci = __builtin_amdgcn_readfirstlane(claim);  // uniform: scalar registers
         if (ci >= nhot + nmid) break;
         const bool hot = ci < nhot;
         const int64_t slot = hot ? hot_list[ci] : mid_list[ci - nhot];
@@ -1963,12 +1968,13 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_few(SpRows rows, const int64
         __syncthreads();
         // 8 loads in flight per thread, then the marks; a bit already set
         // (the common case: few destinations) is read, not written again
-        for (int64_t k0 = t; k0 < n; k0 += 8 * SP_NT) {
+        const int32_t *__restrict__ bd = dst_arr + start;
+        for (uint32_t k0 = (uint32_t)t; k0 < (uint32_t)n; k0 += 8 * SP_NT) {
             int32_t dv[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int64_t k = k0 + (int64_t)u * SP_NT;
-                dv[u] = k < n ? dst_arr[start + k] : -1;
+                const uint32_t k = k0 + (uint32_t)(u * SP_NT);
+                dv[u] = k < (uint32_t)n ? fl_ld32(bd, k) : -1;
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
@@ -2029,7 +2035,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64
         __syncthreads();  // the previous bucket is done with the LDS arrays
         if (threadIdx.x == 0) claim = atomicAdd(&hot_count[1], 1);
         __syncthreads();
-        const int hi = claim;
+        const int hi = __builtin_amdgcn_readfirstlane(claim);  // uniform: scalar registers
         if (hi >= nhot) break;
         const int64_t slot = hot_list[hi];
         sp_accum_hot_one(rows, base, slot / rows.NB, slot % rows.NB, dst_arr, val_arr, raw_local,
@@ -2217,7 +2223,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max_hot(SpRows rows, const int64_t
         __syncthreads();  // the previous bucket is done with the LDS arrays
         if (threadIdx.x == 0) claim = atomicAdd(&hot_count[1], 1);
         __syncthreads();
-        const int hi = claim;
+        const int hi = __builtin_amdgcn_readfirstlane(claim);  // uniform: scalar registers
         if (hi >= nhot) break;
         const int64_t slot = hot_list[hi];
         sp_max_hot_one(rows, base, slot / rows.NB, slot % rows.NB, dst_arr, val_arr, tie_arr, raw_local,
