@@ -534,7 +534,7 @@ constexpr int SP_ICHUNK = FL_WAVE;  // raw items per chunk of the item pass
 constexpr int SEL_MAP_MAX = 2048;  // relations per side of the LDS count maps
 
 template <bool QS>
-__global__ __launch_bounds__(SEL_NT) void k_sp_select(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
+__global__ __launch_bounds__(SEL_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_sp_select(fl_side ori, fl_side inv, const int64_t *__restrict__ sb,
                                                      const int64_t *__restrict__ sl, const int64_t *__restrict__ se,
                                                      int64_t nnz, const float *__restrict__ w, int64_t B, int64_t L,
                                                      int64_t E, int64_t n, int64_t r_size, int wot_i, int mode, int64_t K,
@@ -922,14 +922,26 @@ __global__ __launch_bounds__(SP_ITEMS_NT) void k_sp_items(fl_side ori, fl_side i
 // number of marks at 1..k).  rcap: runs per wave the dynamic LDS holds.
 constexpr int64_t SP_FUSE_KMAX = 256;  // budgets whose runs fit the fused kernel's LDS
 
-// A run in LDS: first item, CSR position, a*w (bits), column and side --
-// one 16-byte record (one LDS store and one load per run).
+// A run in LDS, one 8-byte record (one LDS store and one load per run):
+// x = first item << 20 | side and identity flags (bits 19, 18) | column,
+// y = CSR position.  The item pass takes a*w as a * w[column], the product
+// the walk formed (the same float load and multiply).
 struct SpLdsRuns {
-    int4 *rec;
+    int2 *rec;
 };
+constexpr int SP_LR_FIRST = 20;
+constexpr uint32_t SP_LR_INV = 1u << 19, SP_LR_ID = 1u << 18, SP_LR_COL = (1u << 18) - 1;
+__device__ __forceinline__ int32_t sp_lr_pack(int32_t first, uint32_t meta) {
+    const uint32_t fl = ((meta & SP_RUN_INV) ? SP_LR_INV : 0u) | ((meta & SP_RUN_ID) ? SP_LR_ID : 0u);
+    return (int32_t)(((uint32_t)first << SP_LR_FIRST) | fl | (meta & SP_LR_COL));
+}
+__device__ __forceinline__ uint32_t sp_lr_meta(int32_t x) {
+    const uint32_t u = (uint32_t)x;
+    return ((u & SP_LR_INV) ? SP_RUN_INV : 0u) | ((u & SP_LR_ID) ? SP_RUN_ID : 0u) | (u & SP_LR_COL);
+}
 
 template <bool Q, bool MAXT, bool BWD>
-__global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
+__global__ __launch_bounds__(SEL_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_sp_expand_fused(
     fl_side ori, fl_side inv, const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
     const int64_t *__restrict__ se, const float *__restrict__ sv, int64_t nnz, const float *__restrict__ w, int64_t L,
     int64_t n, int64_t r_size, int wot_i, int mode, int64_t seed, const float *__restrict__ th,
@@ -943,7 +955,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
     uint8_t *mark = mark_all[wid];
     SpLdsRuns ru;
     {
-        ru.rec = reinterpret_cast<int4 *>(fused_lds + (size_t)wid * rcap * 16);
+        ru.rec = reinterpret_cast<int2 *>(fused_lds + (size_t)wid * rcap * 8);
     }
     const int64_t wv_i = (int64_t)blockIdx.x * (SEL_NT / FL_WAVE) + wid;
     if (wv_i >= nnz) return;  // no block barrier follows
@@ -973,17 +985,13 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
             const uint64_t m = __ballot(take > 0);
             const int32_t ri = rix + __popcll(m & below);
             const int32_t o = pos + (int32_t)ex;
-            if (take > 0 && o + (int32_t)take <= lim && ri < rcap) {
-                ru.rec[ri] = make_int4((int32_t)o, (int32_t)start, __float_as_int(fl_mul(a, wv)),
-                                       (int)(side | (col0 + (uint32_t)rel)));
-            }
+            if (take > 0 && o + (int32_t)take <= lim && ri < rcap)
+                ru.rec[ri] = make_int2(sp_lr_pack(o, side | (col0 + (uint32_t)rel)), (int32_t)start);
             rix += __popcll(m);
         });
     }
-    if (!wot_i && lane == 0 && pos == lim && rix < rcap) {
-        ru.rec[rix] = make_int4((int32_t)lim, (int32_t)src, __float_as_int(fl_mul(a, wrow[n - 1])),
-                                (int)(SP_RUN_ID | (uint32_t)(n - 1)));
-    }
+    if (!wot_i && lane == 0 && pos == lim && rix < rcap)
+        ru.rec[rix] = make_int2(sp_lr_pack(lim, SP_RUN_ID | (uint32_t)(n - 1)), (int32_t)src);
     int32_t nr = rix + (wot_i ? 0 : 1);
     if (nr > rcap) nr = rcap;
     fl_wave_sync();
@@ -992,15 +1000,13 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
     for (int32_t q0 = 0; q0 < (int32_t)nitems; q0 += SP_ICHUNK) {
         const int32_t rj = r0 + lane;
         int32_t d = SP_ICHUNK, rp = 0;
-        float aw = 0.0f;
         uint32_t rm = 0;
         if (rj < nr) {
-            const int4 x = ru.rec[rj];
-            const int32_t f = x.x - q0;
+            const int2 x = ru.rec[rj];
+            const int32_t f = (int32_t)((uint32_t)x.x >> SP_LR_FIRST) - q0;
             d = f < SP_ICHUNK ? f : SP_ICHUNK;
             rp = x.y;
-            aw = __int_as_float(x.z);
-            rm = (uint32_t)x.w;
+            rm = sp_lr_meta(x.x);
         }
         mark[lane] = 0;
         fl_wave_sync();
@@ -1010,15 +1016,15 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_expand_fused(
         const int j = __popcll(starts & upto);
         const int32_t dj = __shfl(d, j, FL_WAVE);
         const int32_t pj = __shfl(rp, j, FL_WAVE) + (lane - dj);
-        const float awj = __shfl(aw, j, FL_WAVE);
         const uint32_t mj = (uint32_t)__shfl((int)rm, j, FL_WAVE);
         // the next round's first item: in the last run that started here, or
         // in the run starting right at it
         r0 += __popcll(starts);
-        if (r0 + 1 < nr && ru.rec[r0 + 1].x <= q0 + SP_ICHUNK) ++r0;
+        if (r0 + 1 < nr && (int32_t)((uint32_t)ru.rec[r0 + 1].x >> SP_LR_FIRST) <= q0 + SP_ICHUNK) ++r0;
         fl_wave_sync();  // marks read before the next round clears them
         const int32_t it = q0 + lane;
         if (it >= (int32_t)nitems) continue;
+        const float awj = fl_mul(a, fl_ld32(wrow, mj & SP_RUN_COL));
         int32_t dst = -1, pp = -1;
         float val = 0.0f;
         uint32_t tie = SP_TIE_IDENTITY;
@@ -3401,11 +3407,12 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     if (nnz > 0 && h->mode == SP_FIXED)
         FL_LAUNCH("k_fx_fill", k_fx_fill, dim3((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE))),
                   dim3(SEL_NT), 0, st, *ori, *inv, h->sp_e, h->sp_v, nnz, p.cut, p.item_off, x.raw_dst, x.raw_val);
-    else if (nnz > 0 && h->items > 0 && sp_budget(h) > 0 && sp_budget(h) <= SP_FUSE_KMAX) {
+    else if (nnz > 0 && h->items > 0 && sp_budget(h) > 0 && sp_budget(h) <= SP_FUSE_KMAX &&
+             h->n <= (int64_t)SP_LR_COL + 1) {
         // budgeted hop: at most 2K+1 items (and runs) per entry, kept in LDS
         const int holes = h->mode == SP_TOPK && h->aggregate == SP_SUM;
         const int rcap = (int)(2 * sp_budget(h) + 2);
-        const size_t lds = (size_t)(SEL_NT / FL_WAVE) * (size_t)rcap * 16;
+        const size_t lds = (size_t)(SEL_NT / FL_WAVE) * (size_t)rcap * 8;
         const dim3 grid((unsigned)((nnz + SEL_NT / FL_WAVE - 1) / (SEL_NT / FL_WAVE)));
         int32_t *rp = raw_local ? h->raw_pos : (int32_t *)nullptr;
         int16_t *rc16 = raw_local ? h->raw_col : (int16_t *)nullptr;
