@@ -2373,6 +2373,26 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
     const int32_t *__restrict__ tdst = raw_dst + i0;
     int32_t *__restrict__ tloc = raw_local + i0;
     const int32_t *__restrict__ tinv = part_inv ? part_inv + i0 : nullptr;
+    if (tinv && lds && c == SP_TILE) {
+        // a full tile: every position and destination first, then every
+        // gather, then every store (16 independent chains per thread)
+        constexpr int Q = SP_TILE / SP_NT;
+        int32_t dd[Q], qq[Q];
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t idx = (uint32_t)(j * SP_NT) + threadIdx.x;
+            dd[j] = fl_ld32(tdst, idx);
+            qq[j] = fl_ld32(tinv, idx);
+        }
+#pragma unroll
+        for (int j = 0; j < Q; ++j) qq[j] = dd[j] >= 0 ? part_local[qq[j]] : -1;
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t idx = (uint32_t)(j * SP_NT) + threadIdx.x;
+            fl_st32(tloc, idx, qq[j] >= 0 ? (int32_t)(obase[dd[j] >> SP_S] + qq[j]) : -1);
+        }
+        return;
+    }
 #pragma unroll 4
     for (uint32_t idx = threadIdx.x; idx < (uint32_t)c; idx += SP_NT) {
         if (tinv) {
