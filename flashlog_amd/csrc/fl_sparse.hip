@@ -1084,9 +1084,20 @@ __global__ __launch_bounds__(SP_NT) void k_sp_hist(int64_t R, SpRows rows, const
     for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) hb[q] = 0;
     __syncthreads();
     const int32_t *__restrict__ tdst = raw_dst + i0;
-    for (uint32_t idx = threadIdx.x; idx < (uint32_t)c; idx += SP_NT) {
-        const int32_t d = fl_ld32(tdst, idx);
-        if (d >= 0) atomicAdd(&hb[d >> SP_S], 1);
+    if (c == SP_TILE) {
+        // a full tile: every load in flight before the LDS atomics
+        constexpr int Q = SP_TILE / SP_NT;
+        int32_t dd[Q];
+#pragma unroll
+        for (int j = 0; j < Q; ++j) dd[j] = fl_ld32(tdst, (uint32_t)(j * SP_NT) + threadIdx.x);
+#pragma unroll
+        for (int j = 0; j < Q; ++j)
+            if (dd[j] >= 0) atomicAdd(&hb[dd[j] >> SP_S], 1);
+    } else {
+        for (uint32_t idx = threadIdx.x; idx < (uint32_t)c; idx += SP_NT) {
+            const int32_t d = fl_ld32(tdst, idx);
+            if (d >= 0) atomicAdd(&hb[d >> SP_S], 1);
+        }
     }
     __syncthreads();
     int32_t *hrow = hist + rows.tile_base[r] * rows.NB + tl;
