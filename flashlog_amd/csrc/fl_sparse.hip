@@ -1253,7 +1253,17 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
         for (int j = 0; j < SP_PT_IPT; ++j) key[j] = sorted[j * SP_PT_NT + t];
         __syncthreads();
         int32_t *inv_lds = reinterpret_cast<int32_t *>(const_cast<uint32_t *>(sorted));
-#pragma unroll 4
+        // every item's destination and value requested before the stores
+        int32_t dv[SP_PT_IPT];
+        float vv[SP_PT_IPT];
+#pragma unroll
+        for (int j = 0; j < SP_PT_IPT; ++j) {
+            const uint32_t idx = key[j] & 4095u;
+            const bool ok = j * SP_PT_NT + t < c && (key[j] >> 12) != 0xFFFFFu;
+            dv[j] = ok ? fl_ld32(raw_dst + i0, idx) : 0;
+            vv[j] = ok ? fl_ld32(raw_val + i0, idx) : 0.0f;
+        }
+#pragma unroll
         for (int j = 0; j < SP_PT_IPT; ++j) {
             const int p = j * SP_PT_NT + t;
             if (p >= c) continue;
@@ -1264,8 +1274,8 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
                 continue;
             }
             const int64_t q = boff[bk] + p;
-            part_dst[q] = fl_ld32(raw_dst + i0, idx);
-            part_val[q] = fl_ld32(raw_val + i0, idx);
+            part_dst[q] = dv[j];
+            part_val[q] = vv[j];
             inv_lds[idx] = (int32_t)q;
             if (part_tie) part_tie[q] = fl_ld32(raw_tie + i0, idx);
         }
