@@ -25,10 +25,11 @@
 //           k_sp_partition workgroup per tile of a row: stable scatter of the
 //                         tile's items into destination buckets (block radix
 //                         rank over the bucket id)
-//           k_sp_accum_small  wave per (row, bucket) of at most 512 items:
-//                         the items stably sorted by destination in LDS, each
-//                         run added in raw order; larger buckets are listed
-//                         for k_sp_accum_mid (workgroup sort, persistent) and
+//           k_sp_accum_small  wave per (row, bucket) of at most 512 items
+//                         and 64 destinations: each destination's values added
+//                         in raw order; other buckets are listed for
+//                         k_sp_accum_few (at most 64 destinations), then
+//                         k_sp_accum_mid (workgroup sort, persistent) and
 //                         k_sp_accum_hot (chunks into a dense LDS accumulator,
 //                         persistent); max: k_sp_max / k_sp_max_hot
 //           scan          output offsets
@@ -1517,108 +1518,13 @@ __device__ __forceinline__ void sp_accum_one(int64_t start, int64_t n, int32_t d
 }
 
 // ---- Small buckets (at most SP_WB items): one wave per bucket with
-// wave-private LDS and no block barriers; four buckets per workgroup.
+// wave-private LDS and no block barriers; four buckets per workgroup.  A
+// small bucket of more than SP_WFEW destinations goes to the workgroup sort
+// of k_sp_accum_mid.
 constexpr int SP_WIPT = 8;
 constexpr int SP_WB = FL_WAVE * SP_WIPT;  // 512 items
 constexpr int SP_SMALL_WAVES = SP_NT / FL_WAVE;
 constexpr int SP_MID_GRID = 2048;  // workgroups of the persistent mid-size kernel
-
-
-// Stable LSD sort of 64 * IPT keys in LDS (blocked: lane t owns
-// kin[t*IPT .. t*IPT + IPT)) by bits [lo, lo + nbits), 4 bits per pass.
-template <int IPT>
-__device__ __forceinline__ uint32_t *sp_wave_sort(uint32_t *kin, uint32_t *kout, int lo_bit, int nbits, uint16_t (*cnt)[FL_WAVE]) {
-    const int t = fl_lane();
-    for (int shift = lo_bit; shift < lo_bit + nbits; shift += 4) {
-        uint32_t key[IPT];
-        uint16_t loc[IPT];
-#pragma unroll
-        for (int d = 0; d < 16; ++d) cnt[d][t] = 0;
-#pragma unroll
-        for (int j = 0; j < IPT; ++j) {
-            key[j] = kin[t * IPT + j];
-            const int d = (key[j] >> shift) & 15;
-            loc[j] = cnt[d][t];
-            cnt[d][t] = (uint16_t)(loc[j] + 1);
-        }
-        fl_wave_sync();
-        // exclusive scan of the counters in digit-major order: lane t owns
-        // flat entries [16t, 16t + 16)
-        uint16_t *flat = &cnt[0][0];
-        int part = 0;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) part += flat[t * 16 + q];
-        int run = fl_wave_incl_scan_i32(part) - part;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int c = flat[t * 16 + q];
-            flat[t * 16 + q] = (uint16_t)run;
-            run += c;
-        }
-        fl_wave_sync();
-#pragma unroll
-        for (int j = 0; j < IPT; ++j) {
-            const int d = (key[j] >> shift) & 15;
-            kout[cnt[d][t] + loc[j]] = key[j];
-        }
-        fl_wave_sync();
-        uint32_t *x = kin;
-        kin = kout;
-        kout = x;
-    }
-    return kin;
-}
-
-// The bucket's items sorted by destination (stable) and each run added to
-// 0 in raw order, outputs compacted in destination order in place, as
-// sp_accum_one does for a workgroup.
-template <int IPT>
-__device__ __forceinline__ void sp_wave_accum(int64_t start, int64_t n, int32_t dbase, int32_t *__restrict__ dst_arr,
-                              float *__restrict__ val_arr, int32_t *__restrict__ raw_local, int32_t *out_count, uint32_t (*kb)[SP_WB], float *val,
-                              uint16_t (*cnt)[FL_WAVE]) {
-    constexpr int SIZE = FL_WAVE * IPT;
-    const int t = fl_lane();
-#pragma unroll
-    for (int j = 0; j < IPT; ++j) {
-        const int k = t * IPT + j;
-        uint32_t dl = SP_W;  // no item / hole: sorts last
-        if (k < n) {
-            const int32_t d = dst_arr[start + k];
-            if (d >= 0) {
-                dl = (uint32_t)d & (SP_W - 1);
-                val[k] = val_arr[start + k];
-            }
-        }
-        kb[0][k] = (dl << 11) | (uint32_t)k;
-    }
-    fl_wave_sync();
-    const uint32_t *key = sp_wave_sort<IPT>(kb[0], kb[1], 11, 16, cnt);
-    float *sv = reinterpret_cast<float *>(key == kb[0] ? kb[1] : kb[0]);
-#pragma unroll
-    for (int j = 0; j < IPT; ++j) {
-        const int p = t * IPT + j;
-        sv[p] = val[key[p] & 2047u];
-    }
-    fl_wave_sync();
-    int heads = 0;
-#pragma unroll
-    for (int j = 0; j < IPT; ++j) heads += sp_is_head(key, t * IPT + j) ? 1 : 0;
-    const int incl = fl_wave_incl_scan_i32(heads);
-    const int total = __shfl(incl, FL_WAVE - 1, FL_WAVE);
-    int rank = incl - heads;
-    if (raw_local) sp_raw_ranks<IPT>(key, t * IPT, rank, start, raw_local);
-    // every item was read before the sort: outputs may overwrite them
-    for (int j = 0; j < IPT; ++j) {
-        const int p = t * IPT + j;
-        if (!sp_is_head(key, p)) continue;
-        const int e = sp_run_end(key, p, SIZE);
-        const float a = sp_fold(0.0f, sv, p, e);
-        dst_arr[start + rank] = dbase + (int32_t)(key[p] >> 11);
-        val_arr[start + rank] = a;
-        ++rank;
-    }
-    if (t == 0) *out_count = total;
-}
 
 // A bucket of at most 64 * IPT items with at most SP_WFEW distinct
 // destinations, by one wave without a sort: the destinations are marked in
@@ -1743,12 +1649,15 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
                                                          int32_t *__restrict__ out_count, int64_t nslots,
                                                          int32_t *__restrict__ hot_list,
                                                          int32_t *__restrict__ mid_list,
+                                                         int32_t *__restrict__ mid_fb,
                                                          int32_t *__restrict__ lists) {
-    __shared__ __align__(16) uint32_t kb[SP_SMALL_WAVES][2][SP_WB];
+    // per wave: the destination bitmap, its word prefixes, the slots'
+    // destinations, the count table and the values in slot order (4.8 KB:
+    // eight workgroups per CU)
+    constexpr int FB_WORDS = SP_W / 32, FP_WORDS = SP_W / 64, FD_WORDS = SP_WFEW / 2,
+                  FT_WORDS = (SP_WFEW * (SP_WIPT + 1) + 1) / 2;
+    __shared__ __align__(16) uint32_t fw[SP_SMALL_WAVES][FB_WORDS + FP_WORDS + FD_WORDS + FT_WORDS];
     __shared__ __align__(16) float val[SP_SMALL_WAVES][SP_WB];
-    __shared__ uint16_t cnt[SP_SMALL_WAVES][16][FL_WAVE];
-    static_assert(SP_W / 32 * 4 + SP_W / 32 * 2 + SP_WFEW * 2 <= SP_WB * 4, "few-path bitmap in the first key buffer");
-    static_assert(SP_WFEW * (SP_WIPT + 1) * 2 <= SP_WB * 4, "few-path counts in the second key buffer");
     const int w = fl_wave_id();
     const int64_t slot = fl_xcd_contig(blockIdx.x, gridDim.x) * SP_SMALL_WAVES + w;
     if (slot >= nslots) return;  // no block barrier follows
@@ -1771,12 +1680,12 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
         return;
     }
     const int32_t dbase = (int32_t)(bk << SP_S);
-    // buckets of few destinations without a sort (the key buffers and the
-    // value array hold the few path's arrays), else the sort
-    uint32_t *fbits = kb[w][0];
-    uint16_t *fwpre = reinterpret_cast<uint16_t *>(kb[w][0] + SP_W / 32);
-    int16_t *fdl = reinterpret_cast<int16_t *>(kb[w][0] + SP_W / 32 + SP_W / 64);
-    uint16_t *ftab = reinterpret_cast<uint16_t *>(kb[w][1]);
+    // buckets of few destinations without a sort; the others go to the
+    // workgroup sort of k_sp_accum_mid
+    uint32_t *fbits = fw[w];
+    uint16_t *fwpre = reinterpret_cast<uint16_t *>(fw[w] + FB_WORDS);
+    int16_t *fdl = reinterpret_cast<int16_t *>(fw[w] + FB_WORDS + FP_WORDS);
+    uint16_t *ftab = reinterpret_cast<uint16_t *>(fw[w] + FB_WORDS + FP_WORDS + FD_WORDS);
     bool done;
     if (n <= FL_WAVE)
         done = sp_wave_few<1>(start, n, dbase, dst_arr, val_arr, raw_local, oc, fbits, fwpre, ftab, fdl, val[w]);
@@ -1786,21 +1695,12 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_small(SpRows rows, const int
         done = sp_wave_few<4>(start, n, dbase, dst_arr, val_arr, raw_local, oc, fbits, fwpre, ftab, fdl, val[w]);
     else
         done = sp_wave_few<8>(start, n, dbase, dst_arr, val_arr, raw_local, oc, fbits, fwpre, ftab, fdl, val[w]);
-    if (done) return;
-    fl_wave_sync();  // the few path's reads of its arrays are done
-    if (n <= FL_WAVE)
-        sp_wave_accum<1>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
-    else if (n <= 2 * FL_WAVE)
-        sp_wave_accum<2>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
-    else if (n <= 4 * FL_WAVE)
-        sp_wave_accum<4>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
-    else
-        sp_wave_accum<8>(start, n, dbase, dst_arr, val_arr, raw_local, oc, kb[w], val[w], cnt[w]);
+    if (!done && lane == 0) mid_fb[atomicAdd(&lists[6], 1)] = (int32_t)slot;
 }
 
-// Persistent grid over the mid-size buckets (SP_WB < n <= SP_CHUNK).
-// Persistent grid over a list of mid-size buckets (SP_WB < n <= SP_CHUNK);
-// ctr[0] = listed buckets, ctr[1] = next one to claim.
+// Persistent grid over a list of buckets of at most SP_CHUNK items and more
+// destinations than the few-destination paths take; ctr[0] = listed
+// buckets, ctr[1] = next one to claim.
 __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64_t *__restrict__ base,
                                                        int32_t *__restrict__ dst_arr, float *__restrict__ val_arr,
                                                        int32_t *__restrict__ raw_local,
@@ -3523,7 +3423,7 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         const int64_t nslot = R * NB;
         FL_LAUNCH("k_sp_accum_small", k_sp_accum_small,
                   dim3((unsigned)((nslot + SP_SMALL_WAVES - 1) / SP_SMALL_WAVES)), dim3(SP_NT), 0, st, rows, x.base,
-                  dst_arr, val_arr, acc_local, x.out_count, nslot, x.hot_list, x.mid_list, x.hot_count);
+                  dst_arr, val_arr, acc_local, x.out_count, nslot, x.hot_list, x.mid_list, x.mid_fb, x.hot_count);
         // buckets of more than SP_WB items: few destinations here, the rest
         // on the fallback lists
         FL_LAUNCH("k_sp_accum_few", k_sp_accum_few, dim3((unsigned)(nslot < SP_MID_GRID ? nslot : SP_MID_GRID)),
