@@ -1128,7 +1128,7 @@ __device__ __forceinline__ uint32_t sp_lanes_below(unsigned long long m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
-template <int IPT, int NT = SP_NT>
+template <int IPT, int NT = SP_NT, bool TWO_TABLES = true>
 __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, int nbits, uint16_t *cnt,
                                    int *scan_lds) {
     constexpr int NWV = NT / FL_WAVE;
@@ -1139,10 +1139,15 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
     const int t = threadIdx.x;
     const int lane = fl_lane();
     const int w = fl_wave_id();
-    uint16_t *tab = cnt, *nxt = cnt + TAB;
+    uint16_t *tab = cnt, *nxt = TWO_TABLES ? cnt + TAB : cnt;
     for (int q = t; q < TAB; q += NT) tab[q] = 0;
     __syncthreads();
     for (int shift = lo_bit; shift < lo_bit + nbits; shift += SP_RB) {
+        if (!TWO_TABLES && shift != lo_bit) {
+            // one table: cleared after the previous pass's scatter
+            for (int q = t; q < TAB; q += NT) tab[q] = 0;
+            __syncthreads();
+        }
         uint32_t key[IPT];
         uint16_t dg[IPT], rk[IPT];
 #pragma unroll
@@ -1178,7 +1183,8 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
             tab[f + f / SPAN] = (uint16_t)run;
             run += v[q];
         }
-        for (int q = t; q < TAB; q += NT) nxt[q] = 0;
+        if (TWO_TABLES)
+            for (int q = t; q < TAB; q += NT) nxt[q] = 0;
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < IPT; ++j) kout[tab[dg[j] * (SPAN + 1) + j * NWV + w] + rk[j]] = key[j];
@@ -1207,7 +1213,7 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
                                                        const uint32_t *__restrict__ raw_tie,
                                                        uint32_t *__restrict__ part_tie) {
     __shared__ __align__(16) uint32_t kb[2][SP_TILE];
-    __shared__ uint16_t cnt[SP_SORT_TAB];
+    __shared__ uint16_t cnt[SP_SORT_TAB / 2];  // one count table: four workgroups per CU
     __shared__ int scan_lds[SP_PT_NT / FL_WAVE + 1];
     const int64_t tile = fl_xcd_contig(blockIdx.x, gridDim.x);
     const int64_t r = sp_tile_row(rows.tile_base, R, tile);
@@ -1228,7 +1234,7 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
         kb[0][idx] = key;
     }
     __syncthreads();
-    const uint32_t *sorted = sp_block_sort<SP_PT_IPT, SP_PT_NT>(kb[0], kb[1], 12, nbits, cnt, scan_lds);
+    const uint32_t *sorted = sp_block_sort<SP_PT_IPT, SP_PT_NT, false>(kb[0], kb[1], 12, nbits, cnt, scan_lds);
     const int64_t *bb = base + rows.tile_base[r] * rows.NB + tl;
     // per bucket present: its output base minus its first sorted position
     // (one base load per bucket and tile), in the sort's idle buffer when the
