@@ -89,6 +89,37 @@ __global__ __launch_bounds__(SC_NT) void k_scan_apply(const T *in, int64_t n, co
     if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) out[n] = tile_sum[gridDim.x];
 }
 
+// One workgroup for at most one tile (n <= SC_TILE): every element read
+// before any is written (out may alias in), one launch instead of three.
+template <typename T>
+__global__ __launch_bounds__(SC_NT) void k_scan_one(const T *in, int64_t n, int64_t *out) {
+    __shared__ long long wsum[SC_NT / FL_WAVE];
+    long long v[SC_IPT];
+    long long s = 0;
+#pragma unroll
+    for (int j = 0; j < SC_IPT; ++j) {
+        const int64_t i = (int64_t)threadIdx.x * SC_IPT + j;
+        v[j] = i < n ? (long long)in[i] : 0;
+        s += v[j];
+    }
+    const long long incl = fl_wave_incl_scan_i64(s);
+    if (fl_lane() == FL_WAVE - 1) wsum[threadIdx.x / FL_WAVE] = incl;
+    __syncthreads();
+    long long run = 0, tot = 0;
+    for (int k = 0; k < SC_NT / FL_WAVE; ++k) {
+        if (k < (int)(threadIdx.x / FL_WAVE)) run += wsum[k];
+        tot += wsum[k];
+    }
+    run += incl - s;
+#pragma unroll
+    for (int j = 0; j < SC_IPT; ++j) {
+        const int64_t i = (int64_t)threadIdx.x * SC_IPT + j;
+        if (i < n) out[i] = run;
+        run += v[j];
+    }
+    if (threadIdx.x == 0) out[n] = tot;
+}
+
 size_t scan_tmp_bytes(int64_t n) {
     const int64_t nt = (n + SC_TILE - 1) / SC_TILE;
     return sizeof(int64_t) * (size_t)(nt + 1);
@@ -98,6 +129,10 @@ template <typename T>
 static int scan_impl(hipStream_t st, const T *in, int64_t *out, int64_t n, int64_t *tmp) {
     if (n <= 0) {
         hipLaunchKernelGGL(k_scan_totals, dim3(1), dim3(SC_NT), 0, st, out, (int64_t)0);
+        return fl_check_launch("exclusive_scan");
+    }
+    if (n <= SC_TILE) {
+        FL_LAUNCH("k_scan_one", k_scan_one<T>, dim3(1), dim3(SC_NT), 0, st, in, n, out);
         return fl_check_launch("exclusive_scan");
     }
     const int64_t nt = (n + SC_TILE - 1) / SC_TILE;
