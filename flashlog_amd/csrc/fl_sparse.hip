@@ -2548,16 +2548,21 @@ __global__ void k_sp_order_check(const int32_t *__restrict__ seen, int64_t nnz, 
     if (i < nnz && seen[i] != 1) atomicMax((unsigned long long *)err, 1ull);
 }
 
-// Entry visiting order by source entity (a counting sort; entries of one
-// entity in any order): rank[i] = the entry's slot among its entity's
-// entries, then order[start of entity + rank] = i.  Entity ids outside
-// [0, E) share the last bin (the plan reports them).
+// Entry visiting order by source entity, in blocks of SP_ORD_BLK entity ids
+// (a counting sort over the blocks; the entries of one block in any order):
+// rank[i] = the entry's slot among its block's entries, then
+// order[start of block + rank] = i.  Entity ids outside [0, E) share the
+// last bin (the plan reports them).
+constexpr int SP_ORD_SHIFT = 6;  // 64 entity ids per block
+__device__ __forceinline__ int64_t sp_ord_bin(int64_t e, int64_t E) {
+    return (e >= 0 && e < E) ? (e >> SP_ORD_SHIFT) : (E >> SP_ORD_SHIFT) + 1;
+}
+
 __global__ void k_sp_ord_count(const int64_t *__restrict__ se, int64_t nnz, int64_t E, int32_t *__restrict__ cnt,
                                int32_t *__restrict__ rank) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nnz) return;
-    const int64_t e = se[i];
-    rank[i] = atomicAdd(&cnt[(e >= 0 && e < E) ? e : E], 1);
+    rank[i] = atomicAdd(&cnt[sp_ord_bin(se[i], E)], 1);
 }
 
 __global__ void k_sp_ord_place(const int64_t *__restrict__ se, int64_t nnz, int64_t E,
@@ -2565,8 +2570,7 @@ __global__ void k_sp_ord_place(const int64_t *__restrict__ se, int64_t nnz, int6
                                int32_t *__restrict__ order) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nnz) return;
-    const int64_t e = se[i];
-    order[start[(e >= 0 && e < E) ? e : E] + rank[i]] = (int32_t)i;
+    order[start[sp_ord_bin(se[i], E)] + rank[i]] = (int32_t)i;
 }
 
 // Chunk counts in visiting order.
@@ -3664,14 +3668,19 @@ int fl_sparse_race_select_compact(void *stream, const int64_t *sp_b, const int64
     return fl_check_launch("sparse_race_select");
 }
 
+// the count bins of the entry order: (E >> SP_ORD_SHIFT) + 1 blocks and one
+// for out-of-range ids
+static int64_t sp_ord_bins(int64_t E) { return (E >> SP_ORD_SHIFT) + 2; }
+
 static size_t sp_order_layout(int64_t nnz, int64_t E, char *base, int32_t **cnt, int32_t **rank, int64_t **start,
                               int64_t **tmp) {
     size_t off = 0;
     auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
-    *cnt = (int32_t *)take(sizeof(int32_t) * (size_t)(E + 1));
+    const int64_t nb = sp_ord_bins(E);
+    *cnt = (int32_t *)take(sizeof(int32_t) * (size_t)nb);
     *rank = (int32_t *)take(sizeof(int32_t) * (size_t)(nnz > 0 ? nnz : 1));
-    *start = (int64_t *)take(sizeof(int64_t) * (size_t)(E + 2));
-    *tmp = (int64_t *)take(scan_tmp_bytes(E + 2));
+    *start = (int64_t *)take(sizeof(int64_t) * (size_t)(nb + 1));
+    *tmp = (int64_t *)take(scan_tmp_bytes(nb + 1));
     return off;
 }
 
@@ -3692,11 +3701,12 @@ int fl_sparse_entry_order(void *stream, const int64_t *sp_e, int64_t nnz, int64_
     int64_t *start, *tmp;
     sp_order_layout(nnz, E, (char *)ws, &cnt, &rank, &start, &tmp);
     hipStream_t st = (hipStream_t)stream;
-    FL_LAUNCH("k_fill_i32", k_fill_i32, dim3((unsigned)((E + 1 + 255) / 256)), dim3(256), 0, st, cnt, E + 1, 0);
+    const int64_t nb = sp_ord_bins(E);
+    FL_LAUNCH("k_fill_i32", k_fill_i32, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, cnt, nb, 0);
     FL_LAUNCH("k_sp_ord_count", k_sp_ord_count, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, sp_e, nnz, E,
               cnt, rank);
     int rc;
-    if ((rc = exclusive_scan(st, cnt, start, E + 1, tmp)) != FL_OK) return rc;
+    if ((rc = exclusive_scan(st, cnt, start, nb, tmp)) != FL_OK) return rc;
     FL_LAUNCH("k_sp_ord_place", k_sp_ord_place, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, sp_e, nnz, E,
               start, rank, order);
     return fl_check_launch("sparse_entry_order");

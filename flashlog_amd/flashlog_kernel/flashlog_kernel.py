@@ -927,8 +927,8 @@ _ENTRY_ORDER_MIN = 4096
 
 def _entry_order(sp_e, E):
     """Entries by source entity: a source's rows then share cached group
-    records in the plan and the run writer (any order among a source's
-    entries: fl_sparse_entry_order's counting sort)."""
+    records in the plan and the run writer (fl_sparse_entry_order's counting
+    sort over blocks of 64 entity ids; any order within a block)."""
     nnz = sp_e.numel()
     lib = _lib.lib()
     ws = torch.empty(max(int(lib.fl_sparse_entry_order_bytes(nnz, int(E))), 1), dtype=torch.uint8,

@@ -449,9 +449,9 @@ int fl_sparse_race_select_compact(void *stream, const int64_t *sp_b,
  * No counterpart in the reference: a locality order for this library's plan
  * and run writer (the entries of one source entity read the same group
  * records); the hop's results do not depend on it.  order [nnz] (int32)
- * lists the entries grouped by ascending entity id sp_e (a counting sort;
- * the entries of one entity in any order).  nnz < 2^31; ws of
- * fl_sparse_entry_order_bytes(nnz, E). */
+ * lists the entries grouped by ascending blocks of 64 entity ids (sp_e >> 6;
+ * a counting sort over the blocks, the entries of one block in any order).
+ * nnz < 2^31; ws of fl_sparse_entry_order_bytes(nnz, E). */
 size_t fl_sparse_entry_order_bytes(int64_t nnz, int64_t E);
 int fl_sparse_entry_order(void *stream, const int64_t *sp_e, int64_t nnz,
                           int64_t E, void *ws, size_t ws_bytes,
