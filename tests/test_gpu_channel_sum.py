@@ -110,3 +110,31 @@ def test_channel_max_matches_reference_steps(B, L, E, n, seed):
     (got.values() * g).sum().backward()
     (ref.values() * g).sum().backward()
     assert torch.equal(vt.grad.view(torch.int32), vr.grad.view(torch.int32))
+
+
+@pytest.mark.parametrize("seed", [21, 22])
+def test_channel_max_special_values(seed):
+    """NaN and +-inf inside (b, e) groups: value bits and the amax gradient
+    split as the reference's scatter_reduce steps give them.  (A group
+    holding both -0.0 and +0.0 has no fixed reference: torch's atomic amax
+    keeps whichever zero it stores first, so such ties are left out.)"""
+    fk = _fk()
+    dev = torch.device("cuda:0")
+    B, L, E, n = 4, 3, 40, 240
+    b, l, e, _ = _state(seed, B, L, E, n)
+    rng = np.random.default_rng(seed)
+    v = (rng.integers(-3, 4, b.shape[0]) / 4.0).astype(np.float32)
+    specials = np.array([np.nan, np.inf, -np.inf], dtype=np.float32)
+    pick = rng.choice(b.shape[0], size=min(40, b.shape[0]), replace=False)
+    v[pick] = specials[rng.integers(0, specials.shape[0], pick.shape[0])]
+    tb, tl, te = (torch.from_numpy(x).to(dev) for x in (b, l, e))
+    vt = torch.from_numpy(v).to(dev).requires_grad_(True)
+    vr = vt.detach().clone().requires_grad_(True)
+    got = fk.max_sp_3d(torch.sparse_coo_tensor(torch.stack([tb, tl, te]), vt, [B, L, E], is_coalesced=True))
+    ref = _reference_max_sp_3d(torch.sparse_coo_tensor(torch.stack([tb, tl, te]), vr, [B, L, E]))
+    assert torch.equal(got.indices(), ref.indices())
+    assert torch.equal(got.values().detach().view(torch.int32), ref.values().detach().view(torch.int32))
+    g = torch.randn(ref.values().shape[0], device=dev)
+    (got.values() * g).sum().backward()
+    (ref.values() * g).sum().backward()
+    assert torch.equal(vt.grad.view(torch.int32), vr.grad.view(torch.int32))
