@@ -2227,6 +2227,7 @@ __device__ __forceinline__ void sp_max_hot_one(SpRows rows, const int64_t *__res
 // Wave per (row, bucket), four per workgroup: staged outputs -> COO at
 // out_base.
 constexpr int SP_EMIT_WAVES = 4;
+constexpr int SP_EMIT_SLOTS = 4 * SP_EMIT_WAVES;  // slots per workgroup of k_sp_emit
 
 __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows, int64_t L, int64_t nslot,
                                                   const int64_t *__restrict__ base,
@@ -2235,12 +2236,16 @@ __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows
                                                   const int64_t *__restrict__ out_base, int64_t *__restrict__ ob,
                                                   int64_t *__restrict__ ol, int64_t *__restrict__ oe,
                                                   float *__restrict__ ov) {
-    const int64_t slot = fl_xcd_contig(blockIdx.x, gridDim.x) * SP_EMIT_WAVES + fl_wave_id();
+    // a workgroup takes SP_EMIT_SLOTS consecutive slots, its waves every
+    // SP_EMIT_WAVES-th of them (most slots of an early hop are empty or small)
+    const int64_t g = fl_xcd_contig(blockIdx.x, gridDim.x);
+    for (int s_ = 0; s_ < SP_EMIT_SLOTS / SP_EMIT_WAVES; ++s_) {
+    const int64_t slot = g * SP_EMIT_SLOTS + (int64_t)s_ * SP_EMIT_WAVES + fl_wave_id();
     if (slot >= nslot) return;
     const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
     const int64_t o0 = out_base[slot];
     const int64_t cnt = out_base[slot + 1] - o0;
-    if (cnt == 0) return;
+    if (cnt == 0) continue;
     int64_t start;
     if (rows.NB == 1) {
         start = rows.row_item0[r];
@@ -2261,6 +2266,7 @@ __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows
         fl_st32(pl, k, l);
         fl_st32(pe, k, (int64_t)fl_ld32(sd, k));
         fl_st32(pv, k, fl_ld32(svl, k));
+    }
     }
 }
 
@@ -3461,7 +3467,7 @@ int fl_sparse_emit(void *stream, const fl_sparse_hop *h, const int64_t *out_base
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     SpExp x = sp_exp_layout(h->items, h->tiles, h->chunks, R, NB, 0, h->aggregate, (char *)h->ws2);
     SpRows rows{p.row_item0, p.tile_base, NB};
-    FL_LAUNCH("k_sp_emit", k_sp_emit, dim3((unsigned)((R * NB + SP_EMIT_WAVES - 1) / SP_EMIT_WAVES)),
+    FL_LAUNCH("k_sp_emit", k_sp_emit, dim3((unsigned)((R * NB + SP_EMIT_SLOTS - 1) / SP_EMIT_SLOTS)),
               dim3(SP_EMIT_WAVES * FL_WAVE), 0, (hipStream_t)stream, rows, h->L, R * NB, x.base,
               NB > 1 ? x.part_dst : x.raw_dst, NB > 1 ? x.part_val : x.raw_val, out_base, out_b, out_l, out_e,
               out_v);
