@@ -1070,14 +1070,13 @@ __device__ __forceinline__ int64_t sp_tile_row(const int64_t *tile_base, int64_t
 }
 
 // Workgroup per tile of a row: the tile's destination-bucket histogram
-// (LDS atomics), written as hist[(row, bucket, tile)] for the scan.  Holes
-// (destination -1) are not counted.
+// (LDS atomics), written as hist[tile * NB + bucket] (coalesced) for
+// k_sp_vscan.  Holes (destination -1) are not counted.
 __global__ __launch_bounds__(SP_NT) void k_sp_hist(int64_t R, SpRows rows, const int32_t *__restrict__ raw_dst,
                                                   int32_t *__restrict__ hist) {
     extern __shared__ int hb[];  // [NB]
     const int64_t tile = fl_xcd_contig(blockIdx.x, gridDim.x);
     const int64_t r = sp_tile_row(rows.tile_base, R, tile);
-    const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
     const int64_t tl = tile - rows.tile_base[r];
     const int64_t i0 = rows.row_item0[r] + tl * SP_TILE;
     const int64_t i1e = rows.row_item0[r + 1];
@@ -1101,8 +1100,26 @@ __global__ __launch_bounds__(SP_NT) void k_sp_hist(int64_t R, SpRows rows, const
         }
     }
     __syncthreads();
-    int32_t *hrow = hist + rows.tile_base[r] * rows.NB + tl;
-    for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) hrow[q * nt] = hb[q];
+    int32_t *hrow = hist + tile * rows.NB;
+    for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) hrow[q] = hb[q];
+}
+
+// Thread per (row, bucket): the bucket's count in each of the row's tiles
+// replaced by the exclusive prefix over the row's earlier tiles (in place),
+// the bucket's total to tot[row * NB + bucket] (then scanned into the
+// buckets' first positions).  Neighbouring threads read neighbouring
+// buckets of one tile: every access is coalesced.
+__global__ void k_sp_vscan(int64_t R, SpRows rows, int32_t *__restrict__ hist, int32_t *__restrict__ tot) {
+    const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= R * rows.NB) return;
+    const int64_t r = s / rows.NB, bk = s - r * rows.NB;
+    int32_t run = 0;
+    for (int64_t t = rows.tile_base[r]; t < rows.tile_base[r + 1]; ++t) {
+        const int32_t c = hist[t * rows.NB + bk];
+        hist[t * rows.NB + bk] = run;
+        run += c;
+    }
+    tot[s] = run;
 }
 
 // Stable LSD block sort of SP_NT * IPT keys held in LDS (kin, in positions
@@ -1206,6 +1223,7 @@ constexpr int SP_PT_IPT = SP_TILE / SP_PT_NT;
 
 __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows rows, int nbits,
                                                        const int64_t *__restrict__ base,
+                                                       const int32_t *__restrict__ colpre,
                                                        const int32_t *__restrict__ raw_dst,
                                                        const float *__restrict__ raw_val,
                                                        int32_t *__restrict__ part_dst, float *__restrict__ part_val,
@@ -1217,7 +1235,6 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
     __shared__ int scan_lds[SP_PT_NT / FL_WAVE + 1];
     const int64_t tile = fl_xcd_contig(blockIdx.x, gridDim.x);
     const int64_t r = sp_tile_row(rows.tile_base, R, tile);
-    const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
     const int64_t tl = tile - rows.tile_base[r];
     const int64_t i0 = rows.row_item0[r] + tl * SP_TILE;
     const int64_t i1e = rows.row_item0[r + 1];
@@ -1235,7 +1252,10 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
     }
     __syncthreads();
     const uint32_t *sorted = sp_block_sort<SP_PT_IPT, SP_PT_NT, false>(kb[0], kb[1], 12, nbits, cnt, scan_lds);
-    const int64_t *bb = base + rows.tile_base[r] * rows.NB + tl;
+    // bucket bk's first position in this tile: the bucket's first position
+    // in the row plus the row's earlier tiles' items of the bucket
+    const int64_t *bb = base + r * rows.NB;
+    const int32_t *cp = colpre + tile * rows.NB;
     // per bucket present: its output base minus its first sorted position
     // (one base load per bucket and tile), in the sort's idle buffer when the
     // buckets fit (else a binary search per item)
@@ -1247,7 +1267,7 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
             const int p = j * SP_PT_NT + t;
             if (p >= c) continue;
             const uint32_t bk = sorted[p] >> 12;
-            if (bk != 0xFFFFFu && (p == 0 || (sorted[p - 1] >> 12) != bk)) boff[bk] = bb[(int64_t)bk * nt] - p;
+            if (bk != 0xFFFFFu && (p == 0 || (sorted[p - 1] >> 12) != bk)) boff[bk] = bb[bk] + cp[bk] - p;
         }
         __syncthreads();
     }
@@ -1307,7 +1327,7 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
                 if ((sorted[mid] >> 12) < bk) lo = mid + 1;
                 else hi = mid;
             }
-            q = bb[(int64_t)bk * nt] + (p - lo);
+            q = bb[bk] + cp[bk] + (p - lo);
         }
         const uint32_t idx = key & 4095u;
         part_dst[q] = fl_ld32(raw_dst + i0, idx);
@@ -1340,10 +1360,8 @@ __device__ __forceinline__ void sp_bucket_range(const SpRows &rows, const int64_
         *start = rows.row_item0[r];
         *end = rows.row_item0[r + 1];
     } else {
-        const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
-        const int64_t *bb = base + rows.tile_base[r] * rows.NB + bk * nt;
-        *start = bb[0];
-        *end = bb[nt];
+        *start = base[r * rows.NB + bk];
+        *end = base[r * rows.NB + bk + 1];
     }
 }
 
@@ -2250,8 +2268,7 @@ __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows
     if (rows.NB == 1) {
         start = rows.row_item0[r];
     } else {
-        const int64_t nt = rows.tile_base[r + 1] - rows.tile_base[r];
-        start = base[rows.tile_base[r] * rows.NB + bk * nt];
+        start = base[slot];
     }
     const int64_t b = r / L, l = r - (r / L) * L;
     // a bucket's outputs (at most 8192) from wave-uniform bases, 32-bit offsets
@@ -3033,7 +3050,7 @@ SpPlan sp_plan_layout(int64_t nnz, int64_t R, int64_t r_size, char *base) {
 
 // expansion workspace layout
 struct SpExp {
-    int32_t *raw_dst, *part_dst, *part_inv, *hist, *out_count;
+    int32_t *raw_dst, *part_dst, *part_inv, *hist, *tot, *out_count;
     float *raw_val, *part_val;
     uint32_t *raw_tie, *part_tie;
     int32_t *hot_list, *mid_list, *hot_fb, *mid_fb, *hot_count;
@@ -3067,7 +3084,8 @@ SpExp sp_exp_layout(int64_t T, int64_t tiles, int64_t chunks, int64_t R, int64_t
         x.part_val = (float *)take(sizeof(float) * (size_t)T1);
         if (agg == SP_MAX) x.part_tie = (uint32_t *)take(sizeof(uint32_t) * (size_t)T1);
         x.hist = (int32_t *)take(sizeof(int32_t) * (size_t)(tiles * NB > 0 ? tiles * NB : 1));
-        x.base = (int64_t *)take(sizeof(int64_t) * (size_t)(tiles * NB + 1));
+        x.tot = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
+        x.base = (int64_t *)take(sizeof(int64_t) * (size_t)(R * NB + 1));
     }
     x.out_count = (int32_t *)take(sizeof(int32_t) * (size_t)(R * NB > 0 ? R * NB : 1));
     int64_t mx = tiles * NB;
@@ -3411,10 +3429,13 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         if (h->tiles > 0)
             FL_LAUNCH("k_sp_hist", k_sp_hist, dim3((unsigned)h->tiles), dim3(SP_NT), sizeof(int) * (size_t)NB, st, R,
                       rows, x.raw_dst, x.hist);
-        if ((rc = exclusive_scan(st, x.hist, x.base, h->tiles * NB, x.tmp)) != FL_OK) return rc;
+        if (R * NB > 0)
+            FL_LAUNCH("k_sp_vscan", k_sp_vscan, dim3((unsigned)((R * NB + 255) / 256)), dim3(256), 0, st, R, rows,
+                      x.hist, x.tot);
+        if ((rc = exclusive_scan(st, x.tot, x.base, R * NB, x.tmp)) != FL_OK) return rc;
         if (h->tiles > 0)
             FL_LAUNCH("k_sp_partition", k_sp_partition, dim3((unsigned)h->tiles), dim3(SP_PT_NT), 0, st, R, rows,
-                      sp_bucket_bits(NB + 1), x.base, x.raw_dst, x.raw_val, x.part_dst, x.part_val,
+                      sp_bucket_bits(NB + 1), x.base, x.hist, x.raw_dst, x.raw_val, x.part_dst, x.part_val,
                       raw_local ? x.part_inv : (int32_t *)nullptr, x.raw_tie, x.part_tie);
         dst_arr = x.part_dst;
         val_arr = x.part_val;
