@@ -20,8 +20,9 @@
 //                         edges of one group) and the entry's chunk records
 //           k_sp_items    wave per 64 raw items: destination and value of
 //                         each, from the runs that cover the chunk
-//           k_sp_hist     workgroup per tile: (row, bucket, tile) histogram
-//           scan          bucket bases
+//           k_sp_hist     workgroup per tile: the tile's bucket histogram
+//           k_sp_vscan    per (row, bucket): prefixes over the row's tiles
+//           scan          the buckets' first positions
 //           k_sp_partition workgroup per tile of a row: stable scatter of the
 //                         tile's items into destination buckets (block radix
 //                         rank over the bucket id)
