@@ -819,7 +819,7 @@ SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_
                   "k_sp_partition", "k_sp_accum_small", "k_sp_accum_few", "k_sp_accum_mid", "k_sp_accum_hot", "k_sp_emit", "k_sp_local_to_out",
                   "k_norm_fwd", "k_norm_bwd", "k_sp_bwd", "k_fill_f32", "k_scan_tiles", "k_scan_totals",
                   "k_scan_apply", "k_scan_one", "k_sp_vscan", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask",
-                  "k_sp_ord_count", "k_sp_ord_place", "k_sp_order_count", "k_sp_order_check", "k_sp_gather_nch",
+                  "k_sp_ord_count", "k_sp_ord_place", "k_sp_rowptr_search", "k_sp_order_count", "k_sp_order_check", "k_sp_gather_nch",
                   "k_sp_finite", "k_sp_bw_chunks", "k_sp_gw_fin",
                   "k_cs_rank", "k_cs_emit"]
 

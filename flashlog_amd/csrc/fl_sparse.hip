@@ -2902,6 +2902,23 @@ __device__ __forceinline__ float block_tree_sum(float v, float *red) {
     return s;
 }
 
+// row_ptr[r] for r in [0, R] by binary search over the row keys b*L + l of
+// entries sorted by row (the first entry of row r or later), without
+// checking the order: every value stays in [0, nnz], so kernels bounded by
+// it stay in range on any input.
+__global__ void k_sp_rowptr_search(const int64_t *__restrict__ sb, const int64_t *__restrict__ sl, int64_t nnz,
+                                   int64_t L, int64_t R, int64_t *__restrict__ row_ptr) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r > R) return;
+    int64_t lo = 0, hi = nnz;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (sb[mid] * L + sl[mid] < r) lo = mid + 1;
+        else hi = mid;
+    }
+    row_ptr[r] = lo;
+}
+
 // Per row (workgroup): the denominator is a left fold from 0 over the row's
 // values in entry (= output key) order, as the CPU path adds them
 // (flashlog.cpp:1561-1565); the workgroup stages chunks of the row in LDS
@@ -3750,13 +3767,11 @@ int fl_sparse_normalize_forward(void *stream, const int64_t *sp_b, const int64_t
         return fl_fail(FL_ERR_ARG, "sparse_normalize: null argument");
     const int64_t R = B * L;
     hipStream_t st = (hipStream_t)stream;
-    FL_LAUNCH("k_fill_i64", k_fill_i64, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st, row_ptr, R + 1,
-              (int64_t)0);
+    // the reference's GPU path checks no order either (flashlog.cu:2594-2649):
+    // row starts by binary search, err cleared
     FL_LAUNCH("k_fill_i64", k_fill_i64, dim3(1), dim3(64), 0, st, err, (int64_t)1, (int64_t)0);
-    // entity bounds are not needed here: E = INT64_MAX disables that check
-    const int64_t g1 = (nnz > R + 1 ? nnz : R + 1);
-    FL_LAUNCH("k_sp_rowptr", k_sp_rowptr, dim3((unsigned)((g1 + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, sp_b,
-              nnz, B, L, INT64_MAX, row_ptr, err);
+    FL_LAUNCH("k_sp_rowptr_search", k_sp_rowptr_search, dim3((unsigned)((R + 1 + 255) / 256)), dim3(256), 0, st,
+              sp_b, sp_l, nnz, L, R, row_ptr);
     if (R > 0)
         FL_LAUNCH("k_norm_fwd", k_norm_fwd, dim3((unsigned)R), dim3(NM_NT), 0, st, row_ptr, v, eps, out, denom);
     return fl_check_launch("sparse_normalize");

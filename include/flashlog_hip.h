@@ -465,9 +465,10 @@ size_t fl_sparse_rowptr_bytes(int64_t R);
  * entry order (the CPU path's order, flashlog.cpp:1561-1565, so the bits
  * equal the CPU path's) and out = v / dc with dc = denom >= eps ? denom :
  * eps (the GPU path's clamp, flashlog.cu:2540: a NaN sum divides by eps),
- * IEEE division.  Entries sorted by row; row_ptr [R+1] and err [1] are
- * caller scratch (err != 0 after the call: unsorted or out of range
- * input). */
+ * IEEE division.  Entries sorted by row (not checked, as the reference's
+ * GPU path does not: rows found by binary search; other input gives
+ * unspecified values and no access out of range); row_ptr [R+1] and err [1]
+ * are caller scratch (err is cleared). */
 int fl_sparse_normalize_forward(void *stream, const int64_t *sp_b,
                                 const int64_t *sp_l, const float *v,
                                 int64_t nnz, int64_t B, int64_t L, float eps,
