@@ -2942,17 +2942,7 @@ __global__ __launch_bounds__(NM_NT) void k_norm_fwd(const int64_t *__restrict__ 
         float *cb = (float *)buf[c & 1];
         for (int i = t; i < len; i += NM_NT) cb[i] = v[base + i];
         __syncthreads();
-        if (t == 0) {
-            const int l4 = len >> 2;
-            for (int i = 0; i < l4; ++i) {
-                const float4 q = buf[c & 1][i];
-                acc = fl_add(acc, q.x);
-                acc = fl_add(acc, q.y);
-                acc = fl_add(acc, q.z);
-                acc = fl_add(acc, q.w);
-            }
-            for (int i = l4 * 4; i < len; ++i) acc = fl_add(acc, cb[i]);
-        }
+        if (t == 0) acc = sp_fold(acc, cb, 0, len);  // 32 values per LDS round trip
     }
     if (t == 0) {
         dsh = acc;
