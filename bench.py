@@ -851,7 +851,14 @@ def sparse_hop_bytes(plan):
 
 def item_kernel_bytes(plans):
     """Algorithmic bytes per step of the kernels whose work is linear in the
-    raw items, summed over the step's hops (per raw item: k_sp_items reads
+    entries' group records and raw items, summed over the step's hops
+    (k_sp_select reads each entry's coordinates, 24 B, and per side its
+    group range, 8 B, and every group record once, 10 B, and writes the
+    entry's counts, thresholds and cuts, 24 B; k_sp_expand_fused reads each
+    entry's coordinates, value and item range, 36 B, per side the group
+    range and the threshold and cut, 16 B, every group record, 10 B, and per
+    kept item its CSR column, 4 B, and writes every raw item's destination
+    and value, 8 B, + 2 B of attention column with a backward; per raw item: k_sp_items reads
     the column and mask and writes the destination and value, 16 B, + 6 B of
     CSR position and attention column with a backward; k_sp_hist reads the
     destination, 4 B; k_sp_partition reads destination and value and writes
@@ -860,9 +867,13 @@ def item_kernel_bytes(plans):
     the bucket-order output index and writes the raw-order one, 16 B;
     k_sp_bwd reads CSR position, column and output index and the output's
     gradient, 14 B)."""
-    out = {"k_sp_items": 0, "k_sp_hist": 0, "k_sp_partition": 0, "k_sp_local_to_out": 0, "k_sp_bwd": 0}
+    out = {"k_sp_select": 0, "k_sp_expand_fused": 0, "k_sp_items": 0, "k_sp_hist": 0, "k_sp_partition": 0,
+           "k_sp_local_to_out": 0, "k_sp_bwd": 0}
     for p in plans:
         it, bw = p["items"], p["backward"]
+        kept = it - (0 if p["wot_i"] else p["nnz"])
+        out["k_sp_select"] += (24 + 2 * 8 + 24) * p["nnz"] + 10 * p["groups"]
+        out["k_sp_expand_fused"] += (36 + 2 * 16) * p["nnz"] + 10 * p["groups"] + 4 * kept + (8 + (2 if bw else 0)) * it
         out["k_sp_items"] += (16 + (6 if bw else 0)) * it
         out["k_sp_hist"] += 4 * it
         out["k_sp_partition"] += (16 + (4 if bw else 0)) * it
