@@ -25,9 +25,10 @@ __global__ __launch_bounds__(RB_NT) void k_rule_accum_max(const int64_t *__restr
                                                          const int64_t *__restrict__ se,
                                                          const float *__restrict__ sv, int64_t nnz,
                                                          const float *__restrict__ W, int64_t K, int64_t B,
-                                                         int64_t E, float *__restrict__ dense) {
+                                                         int64_t L, int64_t E, float *__restrict__ dense) {
     const int64_t i = (int64_t)blockIdx.x * RB_NT + threadIdx.x;
     if (i >= nnz) return;
+    if (sb[i] < 0 || sb[i] >= B || se[i] < 0 || se[i] >= E || sl[i] < 0 || sl[i] >= L) return;  // outside the shape
     const int64_t key = sb[i] * E + se[i];
     const float v = sv[i];
     const float *wr = W + sl[i] * K;
@@ -89,7 +90,7 @@ int fl_rule_accumulate(void *stream, const int64_t *sb, const int64_t *sl, const
     hipStream_t st = (hipStream_t)stream;
     if (is_max) {
         FL_LAUNCH("k_rule_accum_max", fl::k_rule_accum_max, dim3((unsigned)((nnz + fl::RB_NT - 1) / fl::RB_NT)),
-                  dim3(fl::RB_NT), 0, st, sb, sl, se, sv, nnz, W, K, B, E, dense);
+                  dim3(fl::RB_NT), 0, st, sb, sl, se, sv, nnz, W, K, B, L, E, dense);
         return fl::fl_check_launch("rule_accumulate");
     }
     if (!ws || ws_bytes < fl_rule_accumulate_bytes(nnz, B, L))

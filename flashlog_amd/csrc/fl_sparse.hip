@@ -2916,7 +2916,12 @@ __global__ void k_sp_rowptr_search(const int64_t *__restrict__ sb, const int64_t
         if (sb[mid] * L + sl[mid] < r) lo = mid + 1;
         else hi = mid;
     }
-    row_ptr[r] = lo;
+    // The first row starts at entry 0 and the last ends at nnz whatever the
+    // keys hold: the search result is monotone in r even over unsorted keys,
+    // so every entry then lies in exactly one row's range and every output
+    // is written (keys outside [0, R) or out of order give unspecified
+    // values, never unwritten ones).
+    row_ptr[r] = r == 0 ? 0 : (r == R ? nnz : lo);
 }
 
 // Per row (workgroup): the denominator is a left fold from 0 over the row's
@@ -3162,13 +3167,17 @@ __device__ __forceinline__ int64_t cs_lower_bound(const int64_t *__restrict__ se
 }
 
 __global__ void k_cs_rank(const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
-                          const int64_t *__restrict__ se, int64_t nnz, int64_t L, int64_t R,
+                          const int64_t *__restrict__ se, int64_t nnz, int64_t L, int64_t R, int64_t E,
                           const int64_t *__restrict__ row_ptr, int32_t *__restrict__ perm,
                           int32_t *__restrict__ head, int64_t *__restrict__ err) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nnz) return;
     const int64_t b = sb[i], l = sl[i], e = se[i];
     if (b < 0 || l < 0 || l >= L || b * L + l >= R) return;  // flagged by k_sp_rowptr
+    if (e < 0 || e >= E) {  // flagged by k_sp_rowptr as well; never placed
+        atomicMax((unsigned long long *)err, 1ull);
+        return;
+    }
     const int64_t r = b * L + l;
     const int64_t rs = row_ptr[r];
     if (i > rs && se[i - 1] >= e) {  // entities not strictly increasing within the row
@@ -3235,14 +3244,16 @@ __global__ void k_cs_emit(const int64_t *__restrict__ sb, const int64_t *__restr
 // the run of entries sharing (b, e), in channel order, and every rank k,
 // acc = sum from 0 of v * W[l, k]; then dense[k, b*E + e] += acc.  One thread
 // per run: each accumulator slot has one writer per call, so the dense sums
-// are added in a fixed order (calls in order, channels in order).
+// are added in a fixed order (calls in order, channels in order).  A state
+// the plan flagged (not coalesced, or an index outside [B, L, E]) adds
+// nothing: the plan's error word is read here, on the device.
 __global__ void k_cs_weighted_add(const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
                                   const int64_t *__restrict__ se, const float *__restrict__ v, int64_t nnz,
                                   const int32_t *__restrict__ perm, const int32_t *__restrict__ head,
                                   const float *__restrict__ W, int64_t K, int64_t B, int64_t E,
-                                  float *__restrict__ dense) {
+                                  const int64_t *__restrict__ err, float *__restrict__ dense) {
     const int64_t m = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (m >= nnz || !head[m]) return;
+    if (m >= nnz || *err != 0 || !head[m]) return;
     const int32_t i = perm[m];
     if (i < 0 || i >= nnz) return;
     const int64_t key = sb[i] * E + se[i];
@@ -3835,7 +3846,7 @@ int fl_sparse_channel_sum_plan(void *stream, const int64_t *sp_b, const int64_t 
     if (nnz > 0) {
         FL_LAUNCH("k_fill_i32", k_fill_i32, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, x.head, nnz, 0);
         FL_LAUNCH("k_cs_rank", k_cs_rank, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, sp_b, sp_l, sp_e,
-                  nnz, L, R, x.row_ptr, x.perm, x.head, x.err);
+                  nnz, L, R, E, x.row_ptr, x.perm, x.head, x.err);
     }
     int rc = exclusive_scan(st, x.head, x.hoff, nnz, x.tmp);
     if (rc != FL_OK) return rc;
@@ -3853,7 +3864,7 @@ int fl_sparse_channel_weighted_add(void *stream, const int64_t *sp_b, const int6
         return fl_fail(FL_ERR_ARG, "sparse_channel_weighted_add: null argument");
     CsLayout x = cs_layout(nnz, B * L, (char *)ws);
     FL_LAUNCH("k_cs_weighted_add", k_cs_weighted_add, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0,
-              (hipStream_t)stream, sp_b, sp_l, sp_e, v, nnz, x.perm, x.head, W, K, B, E, dense);
+              (hipStream_t)stream, sp_b, sp_l, sp_e, v, nnz, x.perm, x.head, W, K, B, E, x.err, dense);
     return fl_check_launch("sparse_channel_weighted_add");
 }
 

@@ -8,9 +8,13 @@ internals are this library's: the dense hop is a destination-major pull with
 a per-source frontier (no atomics on outputs, bit-identical to the
 reference's CPU accumulation order).
 
-This module has no CPU compute path: CPU tensors raise, and a missing or
-stale HIP library raises.  (The reference's CPU kernels are the oracle this
-library is tested against, not part of it.)
+This module has no CPU compute path.  The reference's CPU routes
+(vectorized_operation_csr / FlashLogFunction, the CPU sparse classes and
+their dispatch, prepare_csr_masks and _compute_active_nodes on CPU tensors)
+take CPU tensors and return CPU tensors, but the arithmetic runs in this
+library's GPU kernels; with no GPU visible they raise, and a missing or stale
+HIP library raises.  (The reference's CPU kernels are the oracle this library
+is tested against, not part of it.)
 """
 import ctypes
 import os
@@ -89,6 +93,33 @@ def _require_cuda(*tensors):
     for t in tensors:
         if torch.is_tensor(t) and not t.is_cuda:
             raise RuntimeError("flashlog_amd runs on the GPU only; got a CPU tensor")
+
+
+def _work_device():
+    """The GPU that computes for CPU inputs (the reference's CPU routes run
+    this library's kernels there; inputs go over, results come back)."""
+    if not torch.cuda.is_available():
+        raise RuntimeError("flashlog_amd computes on a ROCm GPU; none is visible for these CPU tensors")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+# Device copies of CPU graph arrays (CSR tuples are built once per graph and
+# passed on every call): kept while the CPU tensor lives unmodified.
+_RESIDENT = {}
+
+
+def _resident(t, dev):
+    if not torch.is_tensor(t) or t.device == dev:
+        return t
+    key = (id(t), t._version, str(dev))
+    hit = _RESIDENT.get(key)
+    if hit is not None and hit[0]() is t:
+        return hit[1]
+    for k in [k for k, v in _RESIDENT.items() if v[0]() is None]:
+        del _RESIDENT[k]
+    copy = t.to(dev)
+    _RESIDENT[key] = (weakref.ref(t), copy)
+    return copy
 
 
 def _stream(t):
@@ -312,9 +343,42 @@ def _prepared_mask_pair(mask_values):
     return None
 
 
+class _HostMaskOrder(autograd.Function):
+    """mask[order] * sigmoid(weight[order]) for CPU inputs, computed by the
+    GPU kernel and returned on the CPU.  As the reference's CPU expression
+    (flashlog_kernel.py:250-254, torch ops) it is differentiable in the edge
+    weight: d/dweight[order[i]] = g[i] * mask * s * (1 - s), one position
+    per edge and side (order is a permutation), so the scatter has no
+    collisions."""
+
+    @staticmethod
+    def forward(ctx, mask_f, order, weight):
+        dev = _work_device()
+        m, o = mask_f.to(dev), _resident(order, dev).to(torch.int32).contiguous()
+        wt = weight.detach().to(device=dev, dtype=torch.float).squeeze(-1).contiguous() if weight is not None \
+            else torch.empty(0, device=dev)
+        out = _HipModule.apply_mask_cuda(m, o, wt)
+        ctx.keep = (m, o, wt, weight is not None)
+        ctx.weight_meta = (weight.shape, weight.dtype) if weight is not None else None
+        return out.to(mask_f.device)
+
+    @staticmethod
+    def backward(ctx, grad):
+        m, o, wt, has_w = ctx.keep
+        if not has_w or not ctx.needs_input_grad[2]:
+            return None, None, None
+        pos = o.long()
+        s = torch.sigmoid(wt[pos])
+        g = grad.to(m.device).float() * m[pos].float() * s * (1.0 - s)
+        gw = torch.zeros(wt.numel(), dtype=torch.float32, device=m.device).index_put_((pos,), g)
+        shape, dtype = ctx.weight_meta
+        return None, None, gw.view(shape).to(device=grad.device, dtype=dtype)
+
+
 def _apply_mask_order(mask_values, order, weight=None):
     mask_f = (mask_values if mask_values.dtype == torch.bool else mask_values.float()).contiguous().view(-1)
-    _require_cuda(mask_f)
+    if not mask_f.is_cuda:
+        return _HostMaskOrder.apply(mask_f, order, weight)
     return _HipModule.apply_mask_cuda(
         mask_f, order.to(device=mask_f.device, dtype=torch.int32).contiguous(),
         torch.empty(0, device=mask_f.device) if weight is None else
@@ -329,10 +393,13 @@ def prepare_csr_masks(csr_struct, mask_values, weight=None):
 
 def _compute_active_nodes(A):
     """Sorted unique entities with a nonzero in any row of A [B, L, E]
-    (flashlog_kernel.py:617-623)."""
-    _require_cuda(A)
-    flat = A.reshape(-1, A.shape[-1]).contiguous().float()
-    return _HipModule.compute_active_nodes_cuda(flat)
+    (flashlog_kernel.py:617-623), on the input's device.  The reference
+    takes the nonzeros of A.sum(1); the two differ only where a (b, e)'s
+    channel values cancel to exactly 0, which no propagation state (sums of
+    nonnegative products) produces."""
+    dev = A.device if A.is_cuda else _work_device()
+    flat = A.detach().reshape(-1, A.shape[-1]).to(dev).contiguous().float()
+    return _HipModule.compute_active_nodes_cuda(flat).to(A.device)
 
 
 # ---------------------------------------------------------------------------
@@ -379,7 +446,8 @@ def _dense_topc_state(A, topk_nodes):
         raise ValueError("topk_nodes/c must be nonnegative")
     if topk_nodes >= A.shape[-1]:
         return A
-    _require_cuda(A)
+    if not A.is_cuda:  # the CPU route: selected on the GPU, returned to the CPU (differentiably)
+        return _DenseTopC.apply(A.to(_work_device()), int(topk_nodes)).to(A.device)
     return _DenseTopC.apply(A, int(topk_nodes))
 
 
@@ -545,7 +613,11 @@ def _dense_backward(grad_ind, grad_ori, grad_inv, A_f, w_f, graph, om, im, r_siz
 
 class FlashLogFunction(autograd.Function):
     """Dense propagation with precomputed active nodes and CSR-ordered masks
-    (flashlog_kernel.py:700-811)."""
+    (flashlog_kernel.py:700-811).  GPU tensors run in place; CPU tensors (the
+    reference's flashlog_forward_cpu / flashlog_backward_cpu route) run the
+    same kernels on the GPU, with the graph arrays' device copies kept per
+    CSR tensor, and get CPU outputs and gradients back.  ``active_nodes`` is
+    accepted for the signature: the kernels derive the frontier from A."""
 
     @staticmethod
     def forward(ctx, A, w, active_nodes,
@@ -554,27 +626,30 @@ class FlashLogFunction(autograd.Function):
                 inv_col_ind, inv_mask,
                 inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
                 r_size, wot_i, topk_edges):
-        _require_cuda(A, w)
+        home = A.device
+        dev = home if A.is_cuda else _work_device()
         B, L, E = A.shape
-        graph = _graph_for(ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
-                           ori_group_edge_count, inv_col_ind, inv_row_group_ptr, inv_group_rel,
-                           inv_group_edge_start, inv_group_edge_count)
-        A_f = A.reshape(B * L, E).contiguous().float()
-        w_f = w.reshape(B * L, -1).contiguous().float()
-        om, im = ori_mask.float().contiguous(), inv_mask.float().contiguous()
+        graph = _graph_for(*(_resident(t, dev) for t in (
+            ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+            inv_col_ind, inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count)))
+        A_f = A.reshape(B * L, E).to(dev).contiguous().float()
+        w_f = w.reshape(B * L, -1).to(dev).contiguous().float()
+        om, im = (m.to(dev).float().contiguous() for m in (ori_mask, inv_mask))
         K = int(topk_edges) if 0 < int(topk_edges) < (1 << 60) else 0
-        out_ind, out_ori, out_inv = _dense_sum_forward(A_f, w_f, graph, om, im, int(r_size), bool(wot_i), K)
+        outs = _dense_sum_forward(A_f, w_f, graph, om, im, int(r_size), bool(wot_i), K)
         ctx.save_for_backward(A_f, w_f, om, im)
         ctx.graph, ctx.r_size, ctx.wot_i, ctx.K, ctx.shape = graph, int(r_size), bool(wot_i), K, (B, L, E)
-        return out_ind.view(B, L, E), out_ori.view(B, L, E), out_inv.view(B, L, E)
+        ctx.home = home
+        return tuple(o.view(B, L, E).to(home) for o in outs)
 
     @staticmethod
     def backward(ctx, grad_ind, grad_ori, grad_inv):
         A_f, w_f, om, im = ctx.saved_tensors
-        gA, gw = _dense_sum_backward(grad_ind, grad_ori, grad_inv, A_f, w_f, ctx.graph, om, im,
-                                     ctx.r_size, ctx.wot_i, ctx.K)
+        dev = A_f.device
+        grads = [g.to(dev) if g is not None else None for g in (grad_ind, grad_ori, grad_inv)]
+        gA, gw = _dense_sum_backward(*grads, A_f, w_f, ctx.graph, om, im, ctx.r_size, ctx.wot_i, ctx.K)
         B, L, E = ctx.shape
-        return (gA.view(B, L, E), gw.view(B, L, -1)) + (None,) * 16
+        return (gA.view(B, L, E).to(ctx.home), gw.view(B, L, -1).to(ctx.home)) + (None,) * 16
 
 
 def _dense_sum_backward(grad_ind, grad_ori, grad_inv, A_f, w_f, graph, om, im, r_size, wot_i, K):
@@ -589,8 +664,12 @@ def vectorized_operation_csr(A, w, csr_struct, mask_values, r_size,
                              weight=None, wot_i=False,
                              use_topk=False, topk_nodes=100000, topk_edges=0,
                              prepared_masks=None):
-    """Dense entry point of the reference's CPU path (flashlog_kernel.py:845-882);
-    here it runs the same arithmetic on the GPU."""
+    """Dense entry point of the reference's CPU route (flashlog_kernel.py:
+    845-882), used by the dense models when CUDA is off
+    (src/model_DRUM_kernel.py:133-140, src/model_NeuralLP_kernel.py:127-132):
+    masks, c1, then FlashLogFunction with topk_edges or, without a budget,
+    1 << 60.  CPU tensors in, CPU tensors out; the arithmetic runs on the GPU
+    in the CPU path's order (bit-equal to flashlog.cpp:151-278)."""
     masks = _prepared_mask_pair(mask_values if prepared_masks is None else prepared_masks)
     if masks is None:
         masks = prepare_csr_masks(csr_struct, mask_values, weight)
@@ -1536,7 +1615,10 @@ def _stacked_rows(*rows):
 
 
 class Sparse3DNormalizeFunction(autograd.Function):
-    """Per (b, l) row: v / max(sum of the row, eps) (flashlog_kernel.py:536-606)."""
+    """Per (b, l) row: v / max(sum of the row, eps) (flashlog_kernel.py:536-606).
+    The entries must be sorted by row with b*L + l in [0, B*L) (a coalesced
+    state); as in the reference's GPU path this is not checked, and other
+    input gives unspecified (but written) values."""
 
     @staticmethod
     def forward(ctx, sp_batch, sp_level, sp_entity, sp_value, B, L, E, eps):
@@ -1658,121 +1740,127 @@ def max_sp_3d(s):
     return _channel_state(s, Sparse3DChannelMaxFunction)
 
 
-def _sparse_sum_selected_nodes(sp_state, entries, w, csr_struct, mask_values,
-                               r_size, weight, wot_i, topk_edges, prepared_masks):
-    idx, val = sp_state.indices(), sp_state.values()
-    selected = torch.sparse_coo_tensor(idx[:, entries], val[entries], sp_state.shape, is_coalesced=True)
-    return vectorized_operation_sparse3d_csr_sum(
-        selected, w, csr_struct, mask_values, r_size, weight=weight,
-        wot_i=wot_i, use_topk=True, topk_edges=topk_edges, prepared_masks=prepared_masks)
+# ---------------------------------------------------------------------------
+# Sparse dispatch (the two entry points of flashlog_kernel.py:1814-1954).
+# One routine serves both: it decides a route from where the state lives and
+# what the call budgets, and builds the chosen class's positional arguments
+# from slices of the CSR tuple.  Routes:
+#   "sampled" -- training selections (sampling with use_topk);
+#   "all"     -- GPU state, no budget and no trainable edge weight: every edge;
+#   "topk"    -- GPU state with a c1/c2 budget or a trainable edge weight;
+#   "host"    -- CPU state: the CPU classes (computed on the GPU, CPU tensors
+#                out), after c1 when a node budget is given.
+
+# Per side, the CSR tuple slots of (columns, group pointer, group relations,
+# group starts, group counts).
+_SIDE_SLOTS = ((1, 8, 9, 10, 11), (5, 12, 13, 14, 15))
+
+
+def _side_parameters(csr_struct, masks):
+    """(columns, mask, 4 group arrays) of ORI then INV: the side parameters
+    of the all-edges and CPU hop classes."""
+    params = []
+    for (col, *groups), mask in zip(_SIDE_SLOTS, masks):
+        params.append(csr_struct[col])
+        params.append(mask)
+        params.extend(csr_struct[g] for g in groups)
+    return params
+
+
+def _ordered_masks(csr_struct, mask_values, weight, prepared_masks, accept_raw_pair):
+    """CSR-ordered masks: the prepared pair when one is given (or, where the
+    reference accepts it, a pair passed as the raw mask), else prepared here."""
+    candidates = [prepared_masks] if prepared_masks is not None else []
+    if accept_raw_pair and prepared_masks is None:
+        candidates.append(mask_values)
+    for c in candidates:
+        pair = _prepared_mask_pair(c)
+        if pair is not None:
+            return pair
+    return prepare_csr_masks(csr_struct, mask_values, weight)
+
+
+def _sparse_route(state, use_topk, topk_edges, topk_nodes, weight, sampling):
+    if sampling and use_topk:
+        return "sampled"
+    if not state.is_cuda:
+        return "host"
+    budgeted = use_topk and (topk_edges > 0 or topk_nodes is not None)
+    trained = weight is not None and bool(getattr(weight, "requires_grad", False))
+    return "topk" if (budgeted or trained) else "all"
+
+
+def _normalized(out, eps):
+    return out if eps is None else normalize_sparse3d(out, eps=eps)
+
+
+def _host_c1_subset(state, topk_nodes):
+    """The CPU state restricted to its c1 entries (selected on the GPU), or
+    None when the budget prunes nothing."""
+    idx, val = state.indices(), state.values()
+    if not torch.cuda.is_available():
+        raise RuntimeError("flashlog_amd runs its sparse kernels on the GPU; no GPU is visible")
+    dev = torch.device("cuda")
+    kept = _sparse_topc_entries(*(x.to(dev) for x in (idx[0], idx[1], idx[2], val)), topk_nodes, state.shape[1])
+    if kept is None:
+        return None
+    kept = kept.cpu()
+    return torch.sparse_coo_tensor(idx.index_select(1, kept), val.index_select(0, kept), state.shape,
+                                   is_coalesced=True)
+
+
+def _sparse_hop(sp_state, w, csr_struct, mask_values, r_size, weight, wot_i, use_topk, topk_edges,
+                prepared_masks, topk_nodes, sampling, eps):
+    """The sum hop (eps None) or the sum followed by the per-row
+    normalization with eps, on the route _sparse_route picks."""
+    route = _sparse_route(sp_state, use_topk, topk_edges, topk_nodes, weight, sampling)
+    if route == "sampled":
+        out = sampled_sparse_propagation(sp_state, w, csr_struct, mask_values, r_size, weight, wot_i, topk_nodes,
+                                         topk_edges, "sum")
+        return _normalized(out, eps)
+    state = sp_state.coalesce()
+    B, L, E = state.shape
+    coords = (*state.indices(), state.values(), w)
+    budget = topk_edges if (use_topk and topk_edges > 0) else (1 << 60)
+    grad_on = torch.is_grad_enabled()
+    if route == "topk":
+        out = FlashLogFunctionSparse3DTopKSum.apply(
+            *coords, *csr_struct[:16], mask_values, weight, B, L, E, r_size, wot_i, budget, False,
+            topk_nodes if use_topk else None, grad_on)
+        return _normalized(out, eps)
+    if route == "all":
+        masks = _ordered_masks(csr_struct, mask_values, weight, prepared_masks, True)
+        out = FlashLogFunctionSparse3DAllEdgesSum.apply(*coords, *_side_parameters(csr_struct, masks),
+                                                        B, L, E, r_size, wot_i, grad_on)
+        return _normalized(out, eps)
+    # route "host": c1 first; a pruned state takes the (unfused) sum, then the normalization
+    if use_topk and topk_nodes is not None:
+        subset = _host_c1_subset(state, topk_nodes)
+        if subset is not None:
+            out = _sparse_hop(subset, w, csr_struct, mask_values, r_size, weight, wot_i, True, topk_edges,
+                              prepared_masks, None, False, None)
+            return _normalized(out, eps)
+    masks = _ordered_masks(csr_struct, mask_values, weight, prepared_masks, False)
+    sides = _side_parameters(csr_struct, masks)
+    if eps is None:
+        return FlashLogFunctionSparse3DCPUSum.apply(*coords, *sides, B, L, E, r_size, wot_i, budget)
+    return FlashLogFunctionSparse3DCPUSumNorm.apply(*coords, *sides, B, L, E, r_size, wot_i, budget, eps)
 
 
 def vectorized_operation_sparse3d_csr_sum(sp_state, w, csr_struct, mask_values,
                                           r_size, weight=None, wot_i=False,
                                           use_topk=False, topk_edges=0,
                                           prepared_masks=None, topk_nodes=None, sampling=False):
-    """Sparse sum dispatcher (flashlog_kernel.py:1814-1888)."""
-    if sampling and use_topk:
-        return sampled_sparse_propagation(sp_state, w, csr_struct, mask_values, r_size,
-                                          weight, wot_i, topk_nodes, topk_edges, "sum")
-    sp_state = sp_state.coalesce()
-    idx = sp_state.indices()
-    val = sp_state.values()
-    B, L, E = sp_state.shape
-    (ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
-     inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
-     ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-     inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count) = csr_struct
-    effective_topk = topk_edges if (use_topk and topk_edges > 0) else (1 << 60)
-    if sp_state.is_cuda:
-        can_use_all_edges = not (use_topk and (topk_edges > 0 or topk_nodes is not None))
-        can_use_all_edges = can_use_all_edges and not (
-            weight is not None and bool(getattr(weight, "requires_grad", False)))
-        if can_use_all_edges:
-            prepared = (_prepared_mask_pair(prepared_masks) if prepared_masks is not None
-                        else _prepared_mask_pair(mask_values))
-            if prepared is not None:
-                ori_mask, inv_mask = prepared
-            else:
-                ori_mask, inv_mask = prepare_csr_masks(csr_struct, mask_values, weight)
-            return FlashLogFunctionSparse3DAllEdgesSum.apply(
-                idx[0], idx[1], idx[2], val, w,
-                ori_col_ind, ori_mask,
-                ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-                inv_col_ind, inv_mask,
-                inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
-                B, L, E, r_size, wot_i, torch.is_grad_enabled())
-        return FlashLogFunctionSparse3DTopKSum.apply(
-            idx[0], idx[1], idx[2], val, w,
-            ori_row_ptr, ori_col_ind, ori_r_ind, order_ori,
-            inv_row_ptr, inv_col_ind, inv_r_ind, order_inv,
-            ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-            inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
-            mask_values, weight, B, L, E, r_size, wot_i, effective_topk,
-            False, topk_nodes if use_topk else None, torch.is_grad_enabled())
-    # CPU tensors: the reference's CPU path semantics, computed on the GPU
-    if use_topk and topk_nodes is not None:
-        dev = torch.device("cuda")
-        entries = _sparse_topc_entries(idx[0].to(dev), idx[1].to(dev), idx[2].to(dev), val.to(dev),
-                                       topk_nodes, L)
-        if entries is not None:
-            return _sparse_sum_selected_nodes(sp_state, entries.cpu(), w, csr_struct, mask_values, r_size,
-                                              weight, wot_i, topk_edges, prepared_masks)
-    prepared = _prepared_mask_pair(prepared_masks) if prepared_masks is not None else None
-    if prepared is not None:
-        ori_mask, inv_mask = prepared
-    else:
-        dev = torch.device("cuda")
-        ori_mask, inv_mask = prepare_csr_masks(tuple(t.to(dev) for t in csr_struct), mask_values.to(dev),
-                                               None if weight is None else weight.to(dev))
-    return FlashLogFunctionSparse3DCPUSum.apply(
-        idx[0], idx[1], idx[2], val, w,
-        ori_col_ind, ori_mask,
-        ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
-        inv_col_ind, inv_mask,
-        inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
-        B, L, E, r_size, wot_i, effective_topk)
+    """Sparse sum entry point (flashlog_kernel.py:1814-1888)."""
+    return _sparse_hop(sp_state, w, csr_struct, mask_values, r_size, weight, wot_i, use_topk, topk_edges,
+                       prepared_masks, topk_nodes, sampling, None)
 
 
 def vectorized_operation_sparse3d_csr_sum_norm(sp_state, w, csr_struct, mask_values,
                                                r_size, weight=None, wot_i=False,
                                                use_topk=False, topk_edges=0,
                                                prepared_masks=None, eps=1e-7, topk_nodes=None, sampling=False):
-    """Sparse sum + per-row normalization dispatcher (flashlog_kernel.py:1901-1954)."""
-    if sampling and use_topk:
-        return normalize_sparse3d(sampled_sparse_propagation(sp_state, w, csr_struct, mask_values, r_size,
-                                                             weight, wot_i, topk_nodes, topk_edges, "sum"), eps=eps)
-    if sp_state.is_cuda:
-        return normalize_sparse3d(
-            vectorized_operation_sparse3d_csr_sum(
-                sp_state, w, csr_struct, mask_values, r_size, weight=weight, wot_i=wot_i,
-                use_topk=use_topk, topk_edges=topk_edges, prepared_masks=prepared_masks,
-                topk_nodes=topk_nodes),
-            eps=eps)
-    sp_state = sp_state.coalesce()
-    idx = sp_state.indices()
-    val = sp_state.values()
-    B, L, E = sp_state.shape
-    if use_topk and topk_nodes is not None:
-        dev = torch.device("cuda")
-        entries = _sparse_topc_entries(idx[0].to(dev), idx[1].to(dev), idx[2].to(dev), val.to(dev),
-                                       topk_nodes, L)
-        if entries is not None:
-            return normalize_sparse3d(_sparse_sum_selected_nodes(
-                sp_state, entries.cpu(), w, csr_struct, mask_values, r_size,
-                weight, wot_i, topk_edges, prepared_masks), eps=eps)
-    effective_topk = topk_edges if (use_topk and topk_edges > 0) else (1 << 60)
-    prepared = _prepared_mask_pair(prepared_masks) if prepared_masks is not None else None
-    if prepared is not None:
-        ori_mask, inv_mask = prepared
-    else:
-        dev = torch.device("cuda")
-        ori_mask, inv_mask = prepare_csr_masks(tuple(t.to(dev) for t in csr_struct), mask_values.to(dev),
-                                               None if weight is None else weight.to(dev))
-    return FlashLogFunctionSparse3DCPUSumNorm.apply(
-        idx[0], idx[1], idx[2], val, w,
-        csr_struct[1], ori_mask,
-        csr_struct[8], csr_struct[9], csr_struct[10], csr_struct[11],
-        csr_struct[5], inv_mask,
-        csr_struct[12], csr_struct[13], csr_struct[14], csr_struct[15],
-        B, L, E, r_size, wot_i, effective_topk, eps)
+    """Sparse sum + per-row normalization entry point
+    (flashlog_kernel.py:1901-1954)."""
+    return _sparse_hop(sp_state, w, csr_struct, mask_values, r_size, weight, wot_i, use_topk, topk_edges,
+                       prepared_masks, topk_nodes, sampling, eps)

@@ -32,6 +32,7 @@ import io
 import json
 import mmap
 import os
+import tempfile
 import time
 from pathlib import Path
 
@@ -122,38 +123,66 @@ def _head_runs(data, first):
     return out, line_no, None
 
 
+# Columns a routed-rule TSV must name; the weight column's name is the bank's
+# weight_field.  Checked in this order, so the first missing one is reported.
+def _required_columns(weight_field):
+    return ("head_id", "body_ids", weight_field, "group_id")
+
+
+def _load_sidecar(cache_path, source, signature):
+    """The sidecar's record when it is a version-1 index of ``source`` with
+    the file's current signature; None when it is absent, unreadable or
+    stale."""
+    try:
+        record = json.loads(cache_path.read_text())
+    except (OSError, ValueError):
+        return None
+    if not isinstance(record, dict):
+        return None
+    fresh = (record.get("version") == 1, record.get("signature") == signature, record.get("source") == source)
+    return record if all(fresh) else None
+
+
+def _store_sidecar(cache_path, record):
+    """Writes the record so that readers see the old sidecar or the whole
+    new one: a uniquely named file beside it, then one rename over it."""
+    cache_path.parent.mkdir(parents=True, exist_ok=True)
+    fd, staged = tempfile.mkstemp(dir=str(cache_path.parent), prefix=cache_path.name + ".", suffix=".tmp")
+    try:
+        with os.fdopen(fd, "w") as out:
+            json.dump(record, out)
+        os.replace(staged, cache_path)
+    except BaseException:
+        if os.path.exists(staged):
+            os.unlink(staged)
+        raise
+
+
 class IndexedRuleBank:
     """Byte-range index of a routed-rule TSV, read from or written to the
-    JSON sidecar ``cache_path`` (rules/indexed_bank.py:21-88)."""
+    JSON sidecar ``cache_path`` (rules/indexed_bank.py:21-88).  Public
+    attributes as the reference's: path, weight_field, signature, columns,
+    heads, index_reused, index_seconds, materialization_seconds,
+    loaded_heads."""
 
     def __init__(self, path, cache_path, weight_field="weight"):
-        started = time.perf_counter()
+        clock = time.perf_counter()
         self.path = Path(path).resolve()
         self.weight_field = weight_field
+        self.signature = _signature(self.path)
         self.materialization_seconds = 0.0
         self.loaded_heads = 0
-        self.signature = _signature(self.path)
         cache_path = Path(cache_path)
-        cached = None
-        if cache_path.exists():
-            try:
-                cached = json.loads(cache_path.read_text())
-            except (ValueError, OSError):
-                cached = None
-        self.index_reused = bool(cached and cached.get("version") == 1 and cached.get("signature") == self.signature
-                                 and cached.get("source") == str(self.path))
-        if not self.index_reused:
-            cached = self._index()
-            cache_path.parent.mkdir(parents=True, exist_ok=True)
-            tmp = cache_path.with_name(cache_path.name + ".%d.tmp" % os.getpid())
-            tmp.write_text(json.dumps(cached))
-            os.replace(tmp, cache_path)
-        self.columns = cached["columns"]
-        for name in ("head_id", "body_ids", weight_field, "group_id"):
-            if name not in self.columns:
-                raise ValueError("Missing routed-rule column: %s" % name)
-        self.heads = cached["heads"]
-        self.index_seconds = time.perf_counter() - started
+        record = _load_sidecar(cache_path, str(self.path), self.signature)
+        self.index_reused = record is not None
+        if record is None:
+            record = self._index()
+            _store_sidecar(cache_path, record)
+        absent = [name for name in _required_columns(weight_field) if name not in record["columns"]]
+        if absent:
+            raise ValueError("Missing routed-rule column: %s" % absent[0])
+        self.columns, self.heads = record["columns"], record["heads"]
+        self.index_seconds = time.perf_counter() - clock
 
     def _index(self):
         with self.path.open("rb") as f:
@@ -193,43 +222,59 @@ class IndexedHeadRules:
     def __len__(self):
         return sum(b[3] for b in self.blocks)
 
-    def compact(self):
-        """One rule per distinct body (first row's id), weight 1, its
-        rank_weights the weight of every group 0..max group of the head."""
-        if self._compact is not None:
-            return self._compact
-        started = time.perf_counter()
-        bank = self.bank
-        if _signature(bank.path) != bank.signature:
-            raise RuntimeError("Rule file changed after indexing")
-        col = {name: i for i, name in enumerate(bank.columns)}
-        ih, ib, iw, ig = col["head_id"], col["body_ids"], col[bank.weight_field], col["group_id"]
-        merged = {}  # body -> [first rule id, {group: weight}]
-        width = 0
-        with bank.path.open("rb") as f:
+    def _rows(self):
+        """(row id, fields) of every row of the head's runs in file order;
+        each run must hold the number of rows its index entry records."""
+        with self.bank.path.open("rb") as f:
             for start, end, first_id, count in self.blocks:
                 f.seek(start)
-                text = f.read(end - start).decode()
-                seen = 0
-                for offset, row in enumerate(csv.reader(io.StringIO(text), delimiter="\t")):
-                    if int(row[ih]) != self.head:
-                        raise ValueError("Rule index relation mismatch")
-                    body = tuple(int(x) for x in row[ib].split())
-                    group = int(row[ig])
-                    if group < 0:
-                        raise ValueError("Negative rule group")
-                    weight = float(row[iw])
-                    width = max(width, group + 1)
-                    slot = merged.setdefault(body, [first_id + offset, {}])
-                    if slot[1].get(group, 0.0) != 0.0:
-                        raise ValueError("duplicate Horn rule/group instance")
-                    slot[1][group] = weight
-                    seen += 1
-                if seen != count:
+                parsed = 0
+                for fields in csv.reader(io.StringIO(f.read(end - start).decode()), delimiter="\t"):
+                    yield first_id + parsed, fields
+                    parsed += 1
+                if parsed != count:
                     raise ValueError("Rule index row-count mismatch")
-        self._compact = [dict(rule_id=rid, head=self.head, body=body, weight=1.0, group_id=None,
-                              rank_weights=tuple(w.get(g, 0.0) for g in range(width)))
-                         for body, (rid, w) in merged.items()]
-        bank.materialization_seconds += time.perf_counter() - started
-        bank.loaded_heads += 1
+
+    def _materialize(self):
+        """One rule per distinct body, in order of first appearance: the id
+        of its first row, weight 1, and rank_weights holding its weight in
+        every group 0 .. (largest group of the head).  A second row of a
+        (body, group) whose first weight is nonzero is an error."""
+        bank = self.bank
+        pos = {name: i for i, name in enumerate(bank.columns)}
+        head_col, body_col = pos["head_id"], pos["body_ids"]
+        weight_col, group_col = pos[bank.weight_field], pos["group_id"]
+        body_slot = {}        # body -> its rule's index
+        first_row = []        # rule index -> id of the body's first row
+        cell = {}             # (rule index, group) -> weight
+        groups = 0
+        for row_id, fields in self._rows():
+            if int(fields[head_col]) != self.head:
+                raise ValueError("Rule index relation mismatch")
+            body = tuple(int(x) for x in fields[body_col].split())
+            group = int(fields[group_col])
+            if group < 0:
+                raise ValueError("Negative rule group")
+            weight = float(fields[weight_col])
+            k = body_slot.get(body)
+            if k is None:
+                k = body_slot[body] = len(first_row)
+                first_row.append(row_id)
+            if cell.get((k, group), 0.0) != 0.0:
+                raise ValueError("duplicate Horn rule/group instance")
+            cell[(k, group)] = weight
+            groups = max(groups, group + 1)
+        return [dict(rule_id=first_row[k], head=self.head, body=body, weight=1.0, group_id=None,
+                     rank_weights=tuple(cell.get((k, g), 0.0) for g in range(groups)))
+                for body, k in body_slot.items()]
+
+    def compact(self):
+        """The head's compacted rules (computed once per object)."""
+        if self._compact is None:
+            clock = time.perf_counter()
+            if _signature(self.bank.path) != self.bank.signature:
+                raise RuntimeError("Rule file changed after indexing")
+            self._compact = self._materialize()
+            self.bank.materialization_seconds += time.perf_counter() - clock
+            self.bank.loaded_heads += 1
         return self._compact

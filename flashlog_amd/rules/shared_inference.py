@@ -30,6 +30,8 @@ and sparse accumulators change only how the exact integer path counts are
 produced or the order of floating-point additions of the normalizers, not
 the values of the channel sums.
 """
+import types
+
 import torch
 
 from .. import _lib
@@ -60,6 +62,18 @@ def _first_degrees(sources, csr, relations):
 def _default_ev():
     from . import evaluate
     return evaluate
+
+
+def _grounding_hooks(ev):
+    """The ``ev`` whose grounding hooks score() calls: this package's
+    evaluation module for None or for any module other than it (a caller
+    passing the reference's own rules.evaluate module, without install(),
+    still grounds on this build's kernels); an object that is not a module
+    (a caller's own hook set) is used as given."""
+    own = _default_ev()
+    if ev is None or (isinstance(ev, types.ModuleType) and ev is not own):
+        return own
+    return ev
 
 
 def _accumulate_chunk(state, W, dense, is_max, nb, E):
@@ -100,7 +114,7 @@ def score(ev, sources, rules, csr, relations, entities, chunk_size,
     boolean_paths = boolean_paths or reduction == "max"
     if chunk_size < 1:
         raise ValueError("chunk_size must be positive")
-    ev = ev if ev is not None else _default_ev()
+    ev = _grounding_hooks(ev)
     stats = {} if stats is None else stats
     for name in ("ground_calls", "prefix_hits", "chunks", "oom_retries"):
         stats.setdefault(name, 0)

@@ -465,10 +465,12 @@ size_t fl_sparse_rowptr_bytes(int64_t R);
  * entry order (the CPU path's order, flashlog.cpp:1561-1565, so the bits
  * equal the CPU path's) and out = v / dc with dc = denom >= eps ? denom :
  * eps (the GPU path's clamp, flashlog.cu:2540: a NaN sum divides by eps),
- * IEEE division.  Entries sorted by row (not checked, as the reference's
- * GPU path does not: rows found by binary search; other input gives
- * unspecified values and no access out of range); row_ptr [R+1] and err [1]
- * are caller scratch (err is cleared). */
+ * IEEE division.  Precondition: entries sorted by row with every row key in
+ * [0, R) (not checked, as the reference's GPU path does not: rows found by
+ * binary search).  Other input gives unspecified values, but every entry of
+ * out is written (row 0 starts at entry 0 and row R-1 ends at nnz) and
+ * nothing is accessed out of range; row_ptr [R+1] and err [1] are caller
+ * scratch (err is cleared). */
 int fl_sparse_normalize_forward(void *stream, const int64_t *sp_b,
                                 const int64_t *sp_l, const float *v,
                                 int64_t nnz, int64_t B, int64_t L, float eps,
@@ -525,7 +527,8 @@ int fl_sparse_channel_sum_emit(void *stream, const int64_t *sp_b,
  * accumulator: for every (b, e) and rank k, dense[k, b*E + e] += the sum
  * from 0, in channel order, of v[b, l, e] * W[l, k].  Uses the workspace
  * that fl_sparse_channel_sum_plan filled (the host need not read its plan
- * first); one writer per accumulator slot, so no atomics. */
+ * first: a state the plan flagged adds nothing, the kernel reads the error
+ * word itself); one writer per accumulator slot, so no atomics. */
 int fl_sparse_channel_weighted_add(void *stream, const int64_t *sp_b,
                                    const int64_t *sp_l, const int64_t *sp_e,
                                    const float *v, int64_t nnz, int64_t B,
@@ -544,7 +547,11 @@ size_t fl_rule_accumulate_bytes(int64_t nnz, int64_t B, int64_t L);
  * as, per (b, e), the sum over the chunk's rules in rule order of
  * v * W[l, k] (is_max = 0; one writer per slot, so the bits are the same on
  * every run), or maxed into it (is_max = 1; values >= 0: exact in any order,
- * no workspace needed). */
+ * no workspace needed).  Malformed states write nothing out of bounds: with
+ * is_max = 0 a state that is not coalesced or holds an index outside
+ * [B, L, E] adds nothing (the plan's error word, read on the device); with
+ * is_max = 1 such entries are skipped.  No error is returned for them (that
+ * would need a host read of device data). */
 int fl_rule_accumulate(void *stream, const int64_t *sb, const int64_t *sl,
                        const int64_t *se, const float *sv, int64_t nnz,
                        const float *W, int64_t K, int64_t B, int64_t L,

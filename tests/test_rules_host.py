@@ -164,3 +164,30 @@ def test_load_rules_and_compact_csr_cache(tmp_path):
         assert torch.equal(a, b) if i in ev_mod.CSR_RULE_FIELDS else a.numel() == 0
     with pytest.raises(ValueError, match="entity count"):
         ev_mod.build_compact_rule_csr(None, E + 1, torch.device("cpu"), str(cache))
+
+
+def test_foreign_evaluation_module_grounds_on_this_build():
+    """score()'s ev: a module other than this package's evaluation module
+    (e.g. the reference's rules.evaluate passed without install()) is
+    replaced by this package's; None likewise; a caller's own hook object
+    (not a module) is used as given."""
+    foreign = types.ModuleType("rules.evaluate")
+    foreign.vectorized_operation_sparse3d_fixed_relation = lambda *a: pytest.fail("foreign grounding called")
+    assert si._grounding_hooks(foreign) is ev_mod
+    assert si._grounding_hooks(None) is ev_mod
+    assert si._grounding_hooks(ev_mod) is ev_mod
+    own = types.SimpleNamespace()
+    assert si._grounding_hooks(own) is own
+
+
+def test_foreign_module_score_uses_this_builds_hooks(monkeypatch, recorder):
+    """Through score(): the grounding calls reach this package's hooks, not
+    the foreign module's."""
+    calls = []
+    monkeypatch.setattr(ev_mod, "vectorized_operation_sparse3d_fixed_relation",
+                        lambda state, ops, csr, rel: calls.append(state.shape) or state)
+    foreign = types.ModuleType("rules.evaluate")
+    foreign.initial_rule_state = lambda *a: pytest.fail("foreign initial state called")
+    foreign.vectorized_operation_sparse3d_fixed_relation = lambda *a: pytest.fail("foreign grounding called")
+    si.score(foreign, torch.tensor([1, 4]), _rules(4), _csr(), R, E, 4)
+    assert calls and recorder == [4]
