@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 22
+ABI_VERSION = 23
 FL_SEG = 32
 FL_SUP = 16
 
@@ -134,6 +134,7 @@ _SIGS = {
                                         ctypes.POINTER(FlSparseHop), ctypes.c_void_p, ctypes.c_void_p]),
     "fl_sparse_emit": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 5),
     "fl_sparse_backward_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3),
+    "fl_sparse_backward_edge_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 3),
     "fl_sparse_backward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                           ctypes.POINTER(FlSparseHop)] + [ctypes.c_void_p] * 6 +
                            [ctypes.c_size_t]),

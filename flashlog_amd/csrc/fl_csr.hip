@@ -139,6 +139,19 @@ CsrWs csr_ws(int64_t M, int64_t nodes, char *base) {
 }
 
 }  // namespace
+
+int radix_sort_u32_f32(hipStream_t st, void *tmp, size_t *tmp_bytes, const uint32_t *keys_in, uint32_t *keys_out,
+                       const float *vals_in, float *vals_out, int64_t n, int bits) {
+    if (n < 0 || n > UINT32_MAX || bits < 1 || bits > 32 || !tmp_bytes)
+        return fl_fail(FL_ERR_ARG, "radix_sort_u32_f32: bad arguments");
+    size_t sb = *tmp_bytes;
+    const hipError_t e = rocprim::radix_sort_pairs(tmp, sb, keys_in, keys_out, vals_in, vals_out, (unsigned)n, 0,
+                                                   (unsigned)bits, st);
+    if (!tmp) *tmp_bytes = sb;
+    if (e != hipSuccess) return fl_fail(FL_ERR_HIP, "radix sort: %s", hipGetErrorString(e));
+    return FL_OK;
+}
+
 }  // namespace fl
 
 using namespace fl;

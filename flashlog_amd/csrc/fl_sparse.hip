@@ -2415,7 +2415,8 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
                                              const int32_t *__restrict__ raw_out,
                                              const int32_t *__restrict__ raw_pos,
                                              const int16_t *__restrict__ raw_col, const float *__restrict__ grad,
-                                             float *__restrict__ grad_v, int64_t i, float *gdst);
+                                             float *__restrict__ grad_v, int64_t i, float *gdst,
+                                             uint32_t *__restrict__ ekey, float *__restrict__ eval);
 
 // Thread per row: its number of BW_CH-entry chunks.
 __global__ void k_sp_bw_chunks(const int64_t *__restrict__ row_ptr, int64_t R, int64_t *__restrict__ nchunk) {
@@ -2435,7 +2436,8 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
                                                   const int32_t *__restrict__ raw_pos,
                                                   const int16_t *__restrict__ raw_col,
                                                   const float *__restrict__ grad, float *__restrict__ grad_v,
-                                                  float *__restrict__ wave_rows, float *__restrict__ part) {
+                                                  float *__restrict__ wave_rows, float *__restrict__ part,
+                                                  uint32_t *__restrict__ ekey, float *__restrict__ eval) {
     extern __shared__ float bw_rows[];  // [BW_WAVES][n] when USE_LDS
     const int64_t nblk = chunk_ptr[R];
     if ((int64_t)blockIdx.x >= nblk) return;  // the grid is an upper bound of the chunk count
@@ -2457,7 +2459,7 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
     __syncthreads();
     for (int64_t i = e0 + wid; i < e1; i += BW_WAVES)
         sp_bwd_entry(ori, inv, sb, sl, sv, w, L, n, r_size, holes, item_off, raw_out, raw_pos, raw_col, grad, grad_v,
-                     i, rows + wid * n);
+                     i, rows + wid * n, ekey, eval);
     __syncthreads();
     for (int64_t c = threadIdx.x; c < n; c += SEL_NT) {
         float x = rows[c];
@@ -2465,6 +2467,27 @@ __global__ __launch_bounds__(SEL_NT) void k_sp_bwd(fl_side ori, fl_side inv, con
         for (int k = 1; k < BW_WAVES; ++k) x = fl_add(x, rows[k * n + c]);
         part[blk * n + c] = x;
     }
+}
+
+// Edge-weight gradients: the items' terms sorted stably by key (side offset +
+// CSR position), so each position's terms form a run in raw item order.  A
+// thread per run head of one side folds its run from 0 and adds the sum to
+// the position's edge: the ORI side's launch first, then the INV side's (an
+// edge id has one position per side, so within a launch every edge has one
+// writer).  grad_edge[e] = (g + ORI fold) + INV fold, the same bits each run.
+constexpr uint32_t SP_EDGE_NONE = 0xFFFFFFFFu;
+
+__global__ void k_sp_edge_fold(const uint32_t *__restrict__ key, const float *__restrict__ val, int64_t items,
+                               uint32_t lo, uint32_t hi, const int32_t *__restrict__ order,
+                               float *__restrict__ grad_edge) {
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= items) return;
+    const uint32_t k = key[j];
+    if (k < lo || k >= hi || (j > 0 && key[j - 1] == k)) return;
+    float x = 0.0f;
+    for (int64_t q = j; q < items && key[q] == k; ++q) x = fl_add(x, val[q]);
+    float *dst = grad_edge + order[k - lo];
+    *dst = fl_add(*dst, x);
 }
 
 // grad_w[r, c] = the row's partial rows added in chunk order.
@@ -2485,7 +2508,8 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
                                              const int32_t *__restrict__ raw_out,
                                              const int32_t *__restrict__ raw_pos,
                                              const int16_t *__restrict__ raw_col, const float *__restrict__ grad,
-                                             float *__restrict__ grad_v, int64_t i, float *gdst) {
+                                             float *__restrict__ grad_v, int64_t i, float *gdst,
+                                             uint32_t *__restrict__ ekey, float *__restrict__ eval) {
     const int lane = fl_lane();
     const int64_t r = sb[i] * L + sl[i];
     const float a = sv[i];
@@ -2515,6 +2539,8 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
         const bool iv = p >= 0 && col >= r_size;
         const float m =
             (loc >= 0 && p >= 0) ? sp_mask_at(iv ? inv.mask_bits : ori.mask_bits, iv ? inv.mask : ori.mask, p) : 1.0f;
+        uint32_t key = SP_EDGE_NONE;
+        float ge = 0.0f;
         if (loc >= 0 && !(holes && p >= 0 && m == 0.0f)) {
             const float gv = grad[loc];
             const float wv = wrow[col];
@@ -2524,12 +2550,17 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
             if (edge_grads && p >= 0) {
                 const fl_side &s = iv ? inv : ori;
                 if (s.grad_edge) {
-                    // trainable edge weights only: added with atomics, as the
-                    // reference's index_add_ does (run-dependent last bits)
-                    const float ge = fl_mul(fl_mul(fl_mul(fl_mul(gv, a), wv), m), s.dscore[p]);
-                    if (ge != 0.0f) atomicAdd(&s.grad_edge[s.order[p]], ge);
+                    // trainable edge weights: the item's term, keyed by its
+                    // side and CSR position, is folded per position in raw
+                    // order after a stable sort (no atomics)
+                    ge = fl_mul(fl_mul(fl_mul(fl_mul(gv, a), wv), m), s.dscore[p]);
+                    key = (uint32_t)(iv ? ori.edges + p : p);
                 }
             }
+        }
+        if (ekey && kb + lane < k1) {
+            ekey[kb + lane] = key;
+            eval[kb + lane] = ge;
         }
         // per-column sums of this chunk (segmented scan keyed by the column);
         // the tail lane of each segment adds it to the wave's row -- each
@@ -3549,6 +3580,47 @@ size_t fl_sparse_backward_bytes(int64_t nnz, int64_t R, int64_t n) {
     return sp_bwd_layout(nnz, R, n, nullptr).bytes;
 }
 
+// The edge-gradient scratch after fl_sparse_backward's own workspace: the
+// items' keys and terms, their sorted copies and the sort's scratch.
+struct SpEdge {
+    uint32_t *key, *skey;
+    float *val, *sval;
+    void *sort_tmp;
+    size_t sort_bytes, bytes;
+    int bits;
+};
+
+static int sp_key_bits(int64_t keys) {
+    int b = 1;
+    while (b < 32 && ((int64_t)1 << b) <= keys) ++b;
+    return b;
+}
+
+static SpEdge sp_edge_layout(int64_t items, int64_t ori_edges, int64_t inv_edges, char *base) {
+    SpEdge x{};
+    size_t off = 0;
+    auto take = [&](size_t b) { char *q = base ? base + off : nullptr; off += al(b); return q; };
+    const int64_t n1 = items > 0 ? items : 1;
+    x.key = (uint32_t *)take(sizeof(uint32_t) * (size_t)n1);
+    x.skey = (uint32_t *)take(sizeof(uint32_t) * (size_t)n1);
+    x.val = (float *)take(sizeof(float) * (size_t)n1);
+    x.sval = (float *)take(sizeof(float) * (size_t)n1);
+    // keys below N = ori_edges + inv_edges < 2^bits: the no-edge key (all
+    // ones) has low bits 2^bits - 1 > N - 1, so it sorts last on these bits
+    x.bits = sp_key_bits(ori_edges + inv_edges);
+    size_t sb = 0;
+    if (radix_sort_u32_f32(nullptr, nullptr, &sb, nullptr, nullptr, nullptr, nullptr, n1, x.bits) != FL_OK) sb = 0;
+    x.sort_bytes = sb;
+    x.sort_tmp = take(sb);
+    x.bytes = off;
+    return x;
+}
+
+size_t fl_sparse_backward_edge_bytes(int64_t items, int64_t ori_edges, int64_t inv_edges) {
+    if (items < 0 || ori_edges < 0 || inv_edges < 0) return 0;
+    return sp_edge_layout(items, ori_edges, inv_edges, nullptr).bytes;
+}
+
 int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h,
                        const int64_t *out_base, const int32_t *raw_local, const float *grad_out, float *grad_v,
                        float *grad_w, void *workspace, size_t workspace_bytes) {
@@ -3561,10 +3633,16 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
         return fl_fail(FL_ERR_ARG, "sparse_backward: edge-weight gradients need raw_pos");
     if (h->mode == SP_FIXED) return fl_fail(FL_ERR_ARG, "sparse_backward: the fixed-relation step has no backward");
     const int64_t R = h->B * h->L;
-    if (!workspace || workspace_bytes < fl_sparse_backward_bytes(h->nnz, R, h->n))
+    const bool edge_grads = (ori->grad_edge || inv->grad_edge) && h->items > 0;
+    if (edge_grads && ori->edges + inv->edges >= (int64_t)SP_EDGE_NONE)
+        return fl_fail(FL_ERR_ARG, "sparse_backward: edge-weight gradients need fewer than 2^32 - 1 positions");
+    const size_t own = fl_sparse_backward_bytes(h->nnz, R, h->n);
+    const size_t extra = edge_grads ? fl_sparse_backward_edge_bytes(h->items, ori->edges, inv->edges) : 0;
+    if (!workspace || workspace_bytes < own + extra)
         return fl_fail(FL_ERR_ARG, "sparse_backward: workspace too small");
     SpPlan p = sp_plan_layout(h->nnz, R, sp_rsize(h), (char *)h->ws1);
     SpBwd x = sp_bwd_layout(h->nnz, R, h->n, (char *)workspace);
+    SpEdge eg = sp_edge_layout(h->items, ori->edges, inv->edges, edge_grads ? (char *)workspace + own : nullptr);
     hipStream_t st = (hipStream_t)stream;
     if (R * h->n > 0)
         FL_LAUNCH("k_fill_f32", k_fill_f32, dim3((unsigned)((R * h->n + 255) / 256)), dim3(256), 0, st, grad_w,
@@ -3578,13 +3656,27 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
         FL_LAUNCH("k_sp_bwd", k_sp_bwd<true>, dim3((unsigned)x.blocks), dim3(SEL_NT),
                   sizeof(float) * BW_WAVES * (size_t)h->n, st, *ori, *inv, h->sp_b, h->sp_l, h->sp_v, p.row_ptr,
                   x.chunk_ptr, R, h->w, h->L, h->n, h->r_size, holes, p.item_off, raw_local, h->raw_pos, h->raw_col,
-                  grad_out, grad_v, x.wave_rows, x.part);
+                  grad_out, grad_v, x.wave_rows, x.part, eg.key, eg.val);
     else
         FL_LAUNCH("k_sp_bwd", k_sp_bwd<false>, dim3((unsigned)x.blocks), dim3(SEL_NT), 0, st, *ori, *inv, h->sp_b,
                   h->sp_l, h->sp_v, p.row_ptr, x.chunk_ptr, R, h->w, h->L, h->n, h->r_size, holes, p.item_off,
-                  raw_local, h->raw_pos, h->raw_col, grad_out, grad_v, x.wave_rows, x.part);
+                  raw_local, h->raw_pos, h->raw_col, grad_out, grad_v, x.wave_rows, x.part, eg.key, eg.val);
     FL_LAUNCH("k_sp_gw_fin", k_sp_gw_fin, dim3((unsigned)((h->n + 255) / 256), (unsigned)R), dim3(256), 0, st,
               x.chunk_ptr, x.part, h->n, grad_w);
+    if (edge_grads) {
+        size_t sb = eg.sort_bytes;
+        if ((rc = radix_sort_u32_f32(st, eg.sort_tmp, &sb, eg.key, eg.skey, eg.val, eg.sval, h->items, eg.bits)) !=
+            FL_OK)
+            return rc;
+        const unsigned g = (unsigned)((h->items + 255) / 256);
+        const uint32_t split = (uint32_t)ori->edges, end = (uint32_t)(ori->edges + inv->edges);
+        if (ori->grad_edge)
+            FL_LAUNCH("k_sp_edge_fold", k_sp_edge_fold, dim3(g), dim3(256), 0, st, eg.skey, eg.sval, h->items,
+                      (uint32_t)0, split, ori->order, ori->grad_edge);
+        if (inv->grad_edge)
+            FL_LAUNCH("k_sp_edge_fold", k_sp_edge_fold, dim3(g), dim3(256), 0, st, eg.skey, eg.sval, h->items, split,
+                      end, inv->order, inv->grad_edge);
+    }
     return fl_check_launch("sparse_backward");
 }
 

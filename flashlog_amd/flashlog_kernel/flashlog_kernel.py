@@ -31,43 +31,76 @@ _FLASHLOG_CPU_THREADS_CONFIGURED = False
 
 
 # ---------------------------------------------------------------------------
-# CPU thread configuration (flashlog_kernel.py:60-102: the FLASHLOG_CPU_THREADS
+# CPU thread configuration (flashlog_kernel.py:13-102: the FLASHLOG_CPU_THREADS
 # and FLASHLOG_CPU_INTEROP_THREADS switches).  This module computes nothing on
-# the CPU, so the setting only reaches torch's own CPU ops.  "auto" here means
-# one thread per physical core this process may run on, at most 32.
+# the CPU, so the setting only reaches torch's own CPU ops; the rule for
+# "auto" is the reference's, so a process configures torch the same way.
 
-def _cpu_topology():
-    """(logical CPUs this process may use, physical cores among them); the
-    core count comes from the kernel's sibling lists, or is None when they
-    cannot be read."""
+def _logical_cpus():
+    """CPUs this process may run on."""
     try:
-        allowed = sorted(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except (AttributeError, OSError):
-        allowed = list(range(os.cpu_count() or 1))
-    cores = set()
-    for cpu in allowed:
-        path = "/sys/devices/system/cpu/cpu%d/topology/thread_siblings_list" % cpu
+        return os.cpu_count() or 1
+
+
+def _machine_cores():
+    """Physical cores of the machine: distinct (package, core) pairs over
+    every online CPU, from the kernel's topology files (the count of
+    distinct (physical id, core id) pairs the reference reads from
+    /proc/cpuinfo), or None when they cannot be read."""
+    root = "/sys/devices/system/cpu"
+    try:
+        names = [d for d in os.listdir(root) if d.startswith("cpu") and d[3:].isdigit()]
+    except OSError:
+        return None
+    pairs = set()
+    for d in names:
+        topo = os.path.join(root, d, "topology")
         try:
-            with open(path) as f:
-                cores.add(f.read().strip())
+            with open(os.path.join(topo, "physical_package_id")) as f:
+                pkg = f.read().strip()
+            with open(os.path.join(topo, "core_id")) as f:
+                core = f.read().strip()
         except OSError:
-            return len(allowed), None
-    return len(allowed), len(cores)
+            continue  # offline CPUs have no topology
+        pairs.add((pkg, core))
+    return len(pairs) or None
 
 
-def _auto_cpu_threads():
-    logical, physical = _cpu_topology()
-    return max(1, min(32, physical or logical))
+_PROBE = object()
+
+
+def _auto_cpu_threads(logical=None, physical=_PROBE):
+    """The "auto" thread count (flashlog_kernel.py:45-57): the whole usable
+    count on small machines, then capped tiers chosen by the logical CPU
+    count -- 24+ CPUs: the physical cores within [8, 16]; 48+: half of them
+    within [12, 24]; 96+: half within [16, 32].  Without a core count the
+    physical cores are taken as half the logical CPUs (8 or more) or all of
+    them.  ``logical`` and ``physical`` default to this machine's (a
+    physical of None stands for an unreadable core count)."""
+    logical = max(1, _logical_cpus() if logical is None else logical)
+    if physical is _PROBE:
+        physical = _machine_cores()
+    if physical is None:
+        physical = max(1, logical // 2 if logical >= 8 else logical)
+    usable = min(physical, logical)
+    for floor_cpus, lo, hi, halve in ((96, 16, 32, True), (48, 12, 24, True), (24, 8, 16, False)):
+        if logical >= floor_cpus:
+            want = usable // 2 if halve else usable
+            return min(hi, max(lo, want))
+    return logical
 
 
 def configure_flashlog_cpu_threads(force=False):
-    """Apply FLASHLOG_CPU_THREADS once (again with force=True): unset, "off",
-    "none", "false" or "0" leave torch's intra-op thread count alone; "auto"
-    (or empty) picks _auto_cpu_threads(); an integer is used as given (an
-    unparsable value counts as "auto"); the count is kept within the CPUs
-    this process may use.  FLASHLOG_CPU_INTEROP_THREADS, when set, is tried
-    for the inter-op pool (torch refuses it once that pool has started;
-    then it is left as is).  Returns torch's intra-op thread count."""
+    """Apply FLASHLOG_CPU_THREADS to torch's intra-op pool, once (again with
+    force=True): unset, "off", "none", "false" or "0" leave it alone; "" or
+    "auto" take _auto_cpu_threads(); an integer is used as given and an
+    unparsable value counts as "auto"; the count is kept within [1, CPUs
+    this process may use].  FLASHLOG_CPU_INTEROP_THREADS, when set, is tried
+    for the inter-op pool (at least 1; an unparsable value, or a pool that
+    has already started, leaves it as is).  Returns torch's intra-op thread
+    count."""
     global _FLASHLOG_CPU_THREADS_CONFIGURED
     if _FLASHLOG_CPU_THREADS_CONFIGURED and not force:
         return torch.get_num_threads()
@@ -75,17 +108,21 @@ def configure_flashlog_cpu_threads(force=False):
     raw = os.environ.get("FLASHLOG_CPU_THREADS", "off").strip().lower()
     if raw in ("off", "none", "false", "0"):
         return torch.get_num_threads()
-    wanted = int(raw) if raw.lstrip("-").isdigit() else _auto_cpu_threads()
-    logical, _ = _cpu_topology()
-    wanted = min(max(wanted, 1), logical)
+    try:
+        wanted = _auto_cpu_threads() if raw in ("", "auto") else int(raw)
+    except ValueError:
+        wanted = _auto_cpu_threads()
+    wanted = min(max(wanted, 1), _logical_cpus())
     if wanted != torch.get_num_threads():
         torch.set_num_threads(wanted)
-    interop = os.environ.get("FLASHLOG_CPU_INTEROP_THREADS", "").strip()
-    if interop.isdigit() and int(interop) > 0 and int(interop) != torch.get_num_interop_threads():
+    interop = os.environ.get("FLASHLOG_CPU_INTEROP_THREADS")
+    if interop is not None:
         try:
-            torch.set_num_interop_threads(int(interop))
-        except RuntimeError:
-            pass  # the inter-op pool is already running
+            pool = max(1, int(interop))
+            if pool != torch.get_num_interop_threads():
+                torch.set_num_interop_threads(pool)
+        except (ValueError, RuntimeError):
+            pass  # unparsable, or the inter-op pool is already running
     return torch.get_num_threads()
 
 
@@ -497,9 +534,157 @@ class _HipModule:
         graph = _graph_for(ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
                            ori_group_edge_count, inv_col_ind, inv_row_group_ptr, inv_group_rel,
                            inv_group_edge_start, inv_group_edge_count)
-        K = int(topk_edges) if use_topk else 0
         return _dense_sum_forward(A, w, graph, ori_mask.float().contiguous(), inv_mask.float().contiguous(),
+                                  int(r_size), bool(wot_i), _edge_budget(use_topk, topk_edges))
+
+    @staticmethod
+    def flashlog_forward_max_cuda(A, w, active_nodes,
+                                  ori_row_ptr, ori_col_ind, ori_r_ind, ori_mask,
+                                  inv_row_ptr, inv_col_ind, inv_r_ind, inv_mask,
+                                  ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                                  inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                                  r_size, wot_i, use_topk, topk_edges):
+        """flashlog.cu:997-1072: (out_ind, out_ori, out_inv, ori_arg, inv_arg),
+        the args int64 winning CSR positions (-1 where nothing arrives)."""
+        graph = _graph_for(ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                           ori_group_edge_count, inv_col_ind, inv_row_group_ptr, inv_group_rel,
+                           inv_group_edge_start, inv_group_edge_count)
+        return _dense_max_forward(A.float(), w.float(), graph, ori_mask.float().contiguous(),
+                                  inv_mask.float().contiguous(), int(r_size), bool(wot_i),
+                                  _edge_budget(use_topk, topk_edges))
+
+    @staticmethod
+    def flashlog_backward_cuda(grad_ind, grad_ori, grad_inv, out_ori, out_inv, A, w, active_nodes,
+                               ori_row_ptr, ori_col_ind, ori_r_ind, ori_mask,
+                               inv_row_ptr, inv_col_ind, inv_r_ind, inv_mask,
+                               ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                               inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                               r_size, wot_i, use_topk, topk_edges, agg_mode):
+        """flashlog.cu:1077-1185 (agg_mode 0): (grad_A [BL, E], grad_w [BL, n]).
+        out_ori / out_inv served the reference's legacy max tolerance only."""
+        if int(agg_mode) != 0:
+            raise NotImplementedError("agg_mode=max on the sum entry point: use flashlog_backward_max_cuda")
+        graph = _graph_for(ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                           ori_group_edge_count, inv_col_ind, inv_row_group_ptr, inv_group_rel,
+                           inv_group_edge_start, inv_group_edge_count)
+        return _dense_sum_backward(grad_ind, grad_ori, grad_inv, A.contiguous().float(), w.contiguous().float(),
+                                   graph, ori_mask.float().contiguous(), inv_mask.float().contiguous(), int(r_size),
+                                   bool(wot_i), _edge_budget(use_topk, topk_edges))
+
+    @staticmethod
+    def flashlog_backward_max_cuda(grad_ind, grad_ori, grad_inv, ori_arg, inv_arg, A, w, active_nodes,
+                                   ori_row_ptr, ori_col_ind, ori_r_ind, ori_mask,
+                                   inv_row_ptr, inv_col_ind, inv_r_ind, inv_mask,
+                                   ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                                   inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                                   r_size, wot_i, use_topk, topk_edges):
+        """flashlog.cu:1187-1255: the gradient reaches only each destination's
+        winning position."""
+        graph = _graph_for(ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                           ori_group_edge_count, inv_col_ind, inv_row_group_ptr, inv_group_rel,
+                           inv_group_edge_start, inv_group_edge_count)
+        return _dense_max_backward(grad_ind, grad_ori, grad_inv, ori_arg.long().contiguous(),
+                                   inv_arg.long().contiguous(), A.contiguous().float(), w.contiguous().float(), graph,
+                                   ori_mask.float().contiguous(), inv_mask.float().contiguous(), int(r_size),
+                                   bool(wot_i), _edge_budget(use_topk, topk_edges))
+
+    @staticmethod
+    def flashlog_forward_cpu(A, w, active_nodes,
+                             ori_col_ind, ori_mask,
+                             ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                             inv_col_ind, inv_mask,
+                             inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                             r_size, wot_i, topk_edges):
+        """flashlog.cpp:284-337 for CPU tensors [BL, E]: computed by the GPU
+        kernels (the same order and bits), returned on the CPU."""
+        dev = _work_device()
+        BL, E = A.shape
+        graph = _graph_for(*(_resident(t, dev) for t in (
+            ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+            inv_col_ind, inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count)))
+        K = int(topk_edges) if 0 < int(topk_edges) < (1 << 60) else 0
+        outs = _dense_sum_forward(A.to(dev).contiguous().float(), w.to(dev).contiguous().float(), graph,
+                                  ori_mask.to(dev).float().contiguous(), inv_mask.to(dev).float().contiguous(),
                                   int(r_size), bool(wot_i), K)
+        return tuple(o.to(A.device) for o in outs)
+
+    @staticmethod
+    def flashlog_backward_cpu(grad_ind, grad_ori, grad_inv, A, w, active_nodes,
+                              ori_col_ind, ori_mask,
+                              ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+                              inv_col_ind, inv_mask,
+                              inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count,
+                              r_size, wot_i, topk_edges):
+        """flashlog.cpp:339-393 for CPU tensors: (grad_A, grad_w) on the CPU,
+        grad_A bit-equal to the CPU path's, grad_w its terms in a fixed
+        association."""
+        dev = _work_device()
+        graph = _graph_for(*(_resident(t, dev) for t in (
+            ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start, ori_group_edge_count,
+            inv_col_ind, inv_row_group_ptr, inv_group_rel, inv_group_edge_start, inv_group_edge_count)))
+        K = int(topk_edges) if 0 < int(topk_edges) < (1 << 60) else 0
+        grads = [g.to(dev) if g is not None else None for g in (grad_ind, grad_ori, grad_inv)]
+        gA, gw = _dense_sum_backward(*grads, A.to(dev).contiguous().float(), w.to(dev).contiguous().float(), graph,
+                                     ori_mask.to(dev).float().contiguous(), inv_mask.to(dev).float().contiguous(),
+                                     int(r_size), bool(wot_i), K)
+        return gA.to(A.device), gw.to(A.device)
+
+    @staticmethod
+    def sparse3d_normalize_forward_cuda(sp_batch, sp_level, values, B, L, eps):
+        """flashlog.cu:2593-2649: (out_values, denom [B, L], row_start [B*L],
+        row_end [B*L]) of a state sorted by row."""
+        out, denom, row_ptr = _normalize_forward(sp_batch, sp_level, values, int(B), int(L), float(eps))
+        R = int(B) * int(L)
+        return out.to(values.dtype), denom.view(int(B), int(L)), row_ptr[:R].clone(), row_ptr[1:R + 1].clone()
+
+    @staticmethod
+    def sparse3d_normalize_backward_cuda(grad_out_values, values, denom, row_start, row_end, eps):
+        """flashlog.cu:2651-2691.  Rows are [row_start, row_end) of a state
+        sorted by row; an empty row may hold any equal pair (the reference
+        marks it (0, 0)): the row pointer is rebuilt from the nonempty rows."""
+        _require_cuda(grad_out_values, values, denom, row_start, row_end)
+        nnz = values.numel()
+        starts = row_start.long()
+        nonempty = row_end.long() > starts
+        nxt = torch.where(nonempty, starts, torch.full_like(starts, nnz))
+        nxt = torch.flip(torch.cummin(torch.flip(nxt, (0,)), 0).values, (0,))
+        row_ptr = torch.cat([nxt, nxt.new_full((1,), nnz)]).contiguous()
+        return _normalize_backward(row_ptr, grad_out_values, values.contiguous().float(),
+                                   denom.contiguous().view(-1).float(), float(eps)).to(values.dtype)
+
+    @staticmethod
+    def flashlog_forward_sparse3d_fixed_relation_cuda(sp_batch, sp_level, sp_entity, sp_value, operators,
+                                                      ori_col_ind, ori_row_group_ptr, ori_group_rel,
+                                                      ori_group_edge_start, ori_group_edge_count,
+                                                      inv_col_ind, inv_row_group_ptr, inv_group_rel,
+                                                      inv_group_edge_start, inv_group_edge_count,
+                                                      B, L, E, r_size):
+        """flashlog.cu:1677-1741: the (b, l, e, v) of one fixed-relation step,
+        here already coalesced (path counts are exact integers, so the
+        caller's coalesce of them gives the same state)."""
+        csr = [None] * 16
+        for slot, t in zip((1, 8, 9, 10, 11, 5, 12, 13, 14, 15),
+                           (ori_col_ind, ori_row_group_ptr, ori_group_rel, ori_group_edge_start,
+                            ori_group_edge_count, inv_col_ind, inv_row_group_ptr, inv_group_rel,
+                            inv_group_edge_start, inv_group_edge_count)):
+            csr[slot] = t
+        st = torch.sparse_coo_tensor(torch.stack([sp_batch.long(), sp_level.long(), sp_entity.long()]),
+                                     sp_value.float(), (int(B), int(L), int(E)))
+        out = vectorized_operation_sparse3d_fixed_relation(st, operators, tuple(csr), int(r_size))
+        b, l, e = out.indices()
+        return b, l, e, out.values()
+
+    @staticmethod
+    def sparse2d_filtered_ranks_cuda(idx_b, idx_e, values, targets, filter_keys, B, E, use_eql):
+        """flashlog.cu:2839-2910."""
+        return sparse2d_filtered_ranks_cuda(idx_b, idx_e, values, targets, filter_keys, B, E, use_eql)
+
+
+def _edge_budget(use_topk, topk_edges):
+    """The c2 budget the dense kernels take (0: none), as the reference's host
+    wrappers decide it (flashlog.cu:958,1142: use_topk and 0 < K < 2^60)."""
+    K = int(topk_edges)
+    return K if use_topk and 0 < K < (1 << 60) else 0
 
 
 _module = _HipModule()
@@ -1155,6 +1340,8 @@ def _sparse_backward(state, grad_values, grad_edge=None):
     gw = torch.empty((h.B * h.L, state.n), dtype=torch.float32, device=dev)
     lib = _lib.lib()
     ws_bytes = lib.fl_sparse_backward_bytes(h.nnz, h.B * h.L, state.n)
+    if grad_edge is not None:  # the edge terms' sort and fold scratch
+        ws_bytes += lib.fl_sparse_backward_edge_bytes(h.items, state.sides.ori.edges, state.sides.inv.edges)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     state.sides.set_grad_edge(grad_edge)
     try:

@@ -390,16 +390,26 @@ size_t fl_sparse_backward_bytes(int64_t nnz, int64_t R, int64_t n);
  * chunks, chunks in order), so every run gives the same bits.  grad_out
  * holds the gradient of every output entry.  With a side's grad_edge set
  * (trainable edge weights, flashlog_kernel.py:1306-1336),
- * grad_edge[order[p]] also accumulates (((g*a)*w)*m)*dscore[p] for the
- * side's items, with atomics (the caller zeroes it).  Needs the plan
- * workspace of the forward, the raw_pos / raw_col arrays that its expand
- * filled (h->raw_pos, h->raw_col) and a workspace of
- * fl_sparse_backward_bytes. */
+ * grad_edge[order[p]] also receives (((g*a)*w)*m)*dscore[p] of the side's
+ * items without atomics (the reference adds them with index_add_): per
+ * position the terms are folded from 0 in raw item order, then added to
+ * the edge's value, the ORI side before the INV side (the caller zeroes
+ * grad_edge; the same bits on every run).  Needs the plan workspace of the
+ * forward, the raw_pos / raw_col arrays that its expand filled
+ * (h->raw_pos, h->raw_col) and a workspace of fl_sparse_backward_bytes,
+ * plus fl_sparse_backward_edge_bytes when a side has grad_edge. */
 int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv,
                        const fl_sparse_hop *h, const int64_t *out_base,
                        const int32_t *raw_local, const float *grad_out,
                        float *grad_v, float *grad_w, void *workspace,
                        size_t workspace_bytes);
+
+/* Extra workspace bytes fl_sparse_backward needs, after its own, when a
+ * side carries grad_edge: per raw item a key and a term, their sorted
+ * copies and the radix sort's scratch (no counterpart in the reference,
+ * whose edge gradient is an atomic index_add_). */
+size_t fl_sparse_backward_edge_bytes(int64_t items, int64_t ori_edges,
+                                     int64_t inv_edges);
 
 /* Replaces _sparse_topc_entries (flashlog_kernel.py:1092-1140), the c1
  * budget on a COO state sorted by row: keep[i] = 1 for the entries to keep.

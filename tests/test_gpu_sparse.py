@@ -266,22 +266,50 @@ def test_three_hop_topk_pipeline():
 
 
 def test_cpu_sum_classes():
+    """The CPU classes (FlashLogFunctionSparse3DCPUSum / CPUSumNorm) through
+    their dispatchers: CPU tensors in and out, forward bit for bit, and the
+    backward (grad_v, grad_w on the CPU) against the oracle's backward --
+    for the fused normalization after the closed-form normalize backward --
+    within 1e-5."""
     fk = _fk()
     B, L = 3, 2
     rng, E, R, n, csr, mbool, masks, state, w = _case(2, 0.1, B, L, 30, 17)
-    sp = torch.sparse_coo_tensor(torch.from_numpy(np.stack(state[:3])), torch.from_numpy(state[3]),
-                                 (B, L, E)).coalesce()
     tcsr = tuple(torch.from_numpy(np.ascontiguousarray(a)) for a in csr)
-    out = fk.vectorized_operation_sparse3d_csr_sum(sp, torch.from_numpy(w), tcsr, torch.from_numpy(mbool), R,
+
+    def leaves():
+        v_t = torch.from_numpy(state[3].copy()).requires_grad_(True)
+        w_t = torch.from_numpy(w.copy()).requires_grad_(True)
+        sp = torch.sparse_coo_tensor(torch.from_numpy(np.stack(state[:3])), v_t, (B, L, E)).coalesce()
+        return v_t, w_t, sp
+
+    v_t, w_t, sp = leaves()
+    out = fk.vectorized_operation_sparse3d_csr_sum(sp, w_t, tcsr, torch.from_numpy(mbool), R,
                                                    use_topk=True, topk_edges=4)
     assert out.device.type == "cpu"
     keys, vals = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, 4)
     assert np.array_equal(_keys(out.indices().detach(), L, E), keys)
-    assert np.array_equal(bits(out.values().numpy()), bits(vals))
-    outn = fk.vectorized_operation_sparse3d_csr_sum_norm(sp, torch.from_numpy(w), tcsr, torch.from_numpy(mbool),
+    assert np.array_equal(bits(out.values().detach().numpy()), bits(vals))
+    g = rng.standard_normal(keys.shape[0]).astype(np.float32)
+    (out.values() * torch.from_numpy(g)).sum().backward()
+    rgv, rgw = O.sparse_backward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, keys, g, False, 4)
+    assert v_t.grad.device.type == "cpu" and w_t.grad.device.type == "cpu"
+    assert_grad_close(v_t.grad.numpy(), rgv)
+    assert_grad_close(w_t.grad.numpy().reshape(B * L, n), rgw)
+
+    v_t, w_t, sp = leaves()
+    outn = fk.vectorized_operation_sparse3d_csr_sum_norm(sp, w_t, tcsr, torch.from_numpy(mbool),
                                                          R, use_topk=True, topk_edges=4)
-    nv, _ = O.sparse_normalize(keys // (L * E), (keys // E) % L, vals, B, L)
-    assert np.array_equal(bits(outn.values().numpy()), bits(nv))
+    row = keys // E
+    nv, denom = O.sparse_normalize(row // L, row % L, vals, B, L)
+    assert np.array_equal(bits(outn.values().detach().numpy()), bits(nv))
+    (outn.values() * torch.from_numpy(g)).sum().backward()
+    d = np.maximum(denom.astype(np.float64), 1e-7)[row]
+    sgv = np.zeros(B * L)
+    np.add.at(sgv, row, g.astype(np.float64) * vals)
+    g_sum = (g / d - sgv[row] / d ** 2).astype(np.float32)
+    rgv, rgw = O.sparse_backward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, keys, g_sum, False, 4)
+    assert_grad_close(v_t.grad.numpy(), rgv)
+    assert_grad_close(w_t.grad.numpy().reshape(B * L, n), rgw)
 
 
 @pytest.mark.parametrize("mode", ["all", "topk"])
