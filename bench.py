@@ -821,7 +821,7 @@ SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_
                   "k_scan_apply", "k_scan_one", "k_sp_vscan", "k_fill_i32", "k_fill_i64", "k_sp_plan_out", "k_apply_mask",
                   "k_sp_ord_count", "k_sp_ord_place", "k_sp_rowptr_search", "k_sp_order_count", "k_sp_order_check", "k_sp_gather_nch",
                   "k_sp_finite", "k_sp_bw_chunks", "k_sp_gw_fin",
-                  "k_cs_rank", "k_cs_emit"]
+                  "k_cs_rank", "k_cs_emit", "k_pack_bool_bits", "k_order_bits"]
 
 
 # The sparse hop's own kernels (forward and backward), without the c1 entity
@@ -936,25 +936,35 @@ def main_sparse(args):
     csr = fk.build_csr_structure(th.to(dev), tt.to(dev), tr.to(dev), E)
     mask_values = torch.ones(M, dtype=torch.bool, device=dev)
     rng = np.random.Generator(np.random.PCG64(1234 + args.config))
-    src, qrel, tgt = synth.make_queries(h, r, t, R, B, rng)
+    src, qrel, tgt, qidx = synth.make_queries(h, r, t, R, B, rng, return_index=True)
     W = torch.from_numpy(synth.make_attention(B, L, n, T, rng)).to(dev)
     print("graph %s: E=%d M=%d (%.1f s to generate)" % (cfg.name, E, M, time.perf_counter() - t_gen),
           file=sys.stderr, flush=True)
-    b0 = torch.arange(B, device=dev).repeat_interleave(L)
-    l0 = torch.arange(L, device=dev).repeat(B)
-    e0 = torch.from_numpy(src).to(dev).repeat_interleave(L)
-    v0 = torch.ones(B * L, device=dev)
-    state0 = torch.sparse_coo_tensor(torch.stack([b0, l0, e0]), v0, [B, L, E]).coalesce()
-    tgt_key = torch.arange(B, device=dev) * E + torch.from_numpy(tgt).to(dev)
-    Wl = W.clone().requires_grad_(train)
+    # the reference's own training batch: --batch_size 256 propagates each
+    # triple forward and inverse (src/dataloader.py:114-122), 2B queries
+    src2, _, tgt2 = synth.training_queries(h, r, t, R, qidx)
+    W2 = torch.from_numpy(synth.make_attention(2 * B, L, n, T, np.random.Generator(np.random.PCG64(4321 + args.config)))).to(dev)
+
+    def workload(q_src, q_tgt, Wq):
+        nb = q_src.shape[0]
+        b0 = torch.arange(nb, device=dev).repeat_interleave(L)
+        l0 = torch.arange(L, device=dev).repeat(nb)
+        e0 = torch.from_numpy(q_src).to(dev).repeat_interleave(L)
+        v0 = torch.ones(nb * L, device=dev)
+        state0 = torch.sparse_coo_tensor(torch.stack([b0, l0, e0]), v0, [nb, L, E]).coalesce()
+        return nb, state0, Wq.clone().requires_grad_(train), torch.from_numpy(q_tgt).to(dev)
+
+    work = [workload(src, tgt, W)]
+    batch_edges = torch.from_numpy(qidx).to(dev)
 
     def hop(s, w):
         if train:
             return fk.sampled_sparse_propagation(s, w, csr, mask_values, R, None, False, c1, K, "sum")
         idx = s.indices()
+        nb = s.shape[0]
         return fk.FlashLogFunctionSparse3DTopKSum.apply(
             idx[0], idx[1], idx[2], s.values(), w, *csr[:4], *csr[4:8], *csr[8:16], mask_values, None,
-            B, L, E, R, False, K, False, c1, False)
+            nb, L, E, R, False, K, False, c1, False)
 
     def model_sum_sp_3d(s):
         # the model file's own channel sum (src/model_DRUM_kernel_sp.py:22-28): torch's coalesce
@@ -970,11 +980,15 @@ def main_sparse(args):
         logits = torch.sparse.sum(p_score * one_hot, dim=-1).to_dense()
         return -torch.mean(torch.log(torch.maximum(logits, torch.ones_like(logits) * 1e-7)), dim=-1)
 
-    tgt_t = torch.from_numpy(tgt).to(dev)
     native_sum = [False]
 
     def step():
-        # src/model_DRUM_kernel_sp.py:132-205 per hop: the hop, normalize_sparse3d, dropout (training)
+        # src/main.py:887-890: the batch's triples are hidden from the graph
+        # for the step (the mask is updated in place), restored after it (:927-930);
+        # src/model_DRUM_kernel_sp.py:132-205 per hop: the hop, normalize_sparse3d, dropout
+        _, state0, Wl, tgt_t = work[0]
+        if train:
+            mask_values[batch_edges] = False
         s = state0
         for t_ in range(T):
             s = fk.normalize_sparse3d(hop(s, Wl[t_]))
@@ -987,6 +1001,7 @@ def main_sparse(args):
         loss = log_loss_common_sp(final, tgt_t)
         Wl.grad = None
         loss.backward()
+        mask_values[batch_edges] = True
         return loss
 
     ctx = torch.enable_grad() if train else torch.inference_mode()
@@ -1027,6 +1042,27 @@ def main_sparse(args):
         ms_step_native = e_0.elapsed_time(e_1) / args.steps
         native_sum[0] = False
         print("with flashlog_kernel.sum_sp_3d: %.3f ms/step" % ms_step_native, file=sys.stderr, flush=True)
+        # the reference's training batch for --batch_size 256: 2B queries (each
+        # triple forward and inverse), the same step otherwise
+        ref_batch = None
+        if train:
+            work.insert(0, workload(src2, tgt2, W2))
+            for _ in range(2):
+                step()
+            torch.cuda.synchronize()
+            e_0.record()
+            for _ in range(args.steps):
+                step()
+            e_1.record()
+            torch.cuda.synchronize()
+            ms_step_2b = e_0.elapsed_time(e_1) / args.steps
+            work.pop(0)
+            ref_batch = {"queries_per_step": 2 * B, "ms_per_step": ms_step_2b,
+                         "value": 2 * B / (ms_step_2b * 1e-3), "unit": "queries/s",
+                         "what": "the same training step on the %d queries the reference propagates for "
+                                 "--batch_size %d (each batch triple forward and inverse, "
+                                 "src/dataloader.py:114-122)" % (2 * B, B)}
+            print("reference batch (%d queries): %.3f ms/step" % (2 * B, ms_step_2b), file=sys.stderr, flush=True)
         _lib.prof_enable(True)
         for _ in range(args.profile_steps):
             step()
@@ -1081,6 +1117,10 @@ def main_sparse(args):
                    "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2, "mode": args.mode},
         "channel_sum": "the model file's torch sum_sp_3d (src/model_DRUM_kernel_sp.py:22-28)",
         "ms_per_step_native_channel_sum": ms_step_native,
+        "mask": ("the batch's %d triples hidden in the edge mask in place before each step and restored after "
+                 "it (src/main.py:887-890,927-930), so each step rebuilds the CSR-ordered mask bitmaps" % B
+                 if train else "all edges visible"),
+        "reference_batch": ref_batch,
         "topk_select_ms": {"c1_per_hop": per_launch["k_race_select"] if train else per_launch["k_sp_topc"],
                            "c2_per_hop": per_launch["k_sp_select"]},
         "kernel_ms_per_launch": per_launch,
@@ -1119,14 +1159,10 @@ def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W, T, train):
         print("cpu baseline skipped: oracle/_ref not built", file=sys.stderr, flush=True)
         return None
     threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
     tc = [torch.from_numpy(a) for a in csr_np]
     om = torch.ones(tc[1].shape[0], dtype=torch.float32)
     im = torch.ones(tc[5].shape[0], dtype=torch.float32)
     n = 2 * R + 1
-    Bs = min(16, W.shape[1])
-    Wt = W[:, :Bs].contiguous()
-    tg = torch.from_numpy(tgt[:Bs]).long()
 
     def topc(b, l, e, v):
         if e.numel() <= c1:
@@ -1146,7 +1182,9 @@ def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W, T, train):
         keep[ranked[(torch.arange(g.numel()) - first) < c1]] = True
         return torch.nonzero(keep, as_tuple=True)[0]
 
-    def step():
+    def step(Bs):
+        Wt = W[:, :Bs].contiguous()
+        tg = torch.from_numpy(tgt[:Bs]).long()
         b = torch.arange(Bs).repeat_interleave(L)
         l = torch.arange(L).repeat(Bs)
         e = torch.from_numpy(src[:Bs]).repeat_interleave(L)
@@ -1187,18 +1225,31 @@ def cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W, T, train):
                 else:
                     grad[keep] = gsp
 
-    t0 = time.perf_counter()
-    steps = 0
-    while True:
-        step()
-        steps += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    el = time.perf_counter() - t0
+    def timed(nthreads, Bs, seconds):
+        torch.set_num_threads(nthreads)
+        t0 = time.perf_counter()
+        steps = 0
+        while True:
+            step(Bs)
+            steps += 1
+            if time.perf_counter() - t0 >= seconds:
+                break
+        return steps, time.perf_counter() - t0
+
     what = "forward + backward" if train else "forward"
+    Bs = min(16, W.shape[1])
+    steps, el = timed(threads, Bs, args.cpu_seconds)
+    # the reference's sum_norm CPU path at one thread (its at::parallel_for
+    # over the rows, flashlog.cpp:1454, serial), on a smaller sample
+    Bs1 = min(4, W.shape[1])
+    steps1, el1 = timed(1, Bs1, args.cpu_seconds / 2)
+    torch.set_num_threads(threads)
     return {**host_cpu(), "value": steps * Bs / el, "unit": "queries/s", "cores": threads, "kind": "reference",
             "sample": "%d full %s steps of %d queries x %d hops (first %d queries of the batch; deterministic "
-                      "c1/c2 selections) in %.1f s, %d threads" % (steps, what, Bs, T, Bs, el, threads)}
+                      "c1/c2 selections) in %.1f s, %d threads" % (steps, what, Bs, T, Bs, el, threads),
+            "one_thread": {"value": steps1 * Bs1 / el1, "unit": "queries/s", "cores": 1,
+                           "sample": "%d full %s steps of %d queries x %d hops in %.1f s, 1 thread"
+                                     % (steps1, what, Bs1, T, el1)}}
 
 
 def cpu_baseline(args, cfg, h, r, t, E, R, src, W):

@@ -12,7 +12,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libflashlog_hip.so")
-ABI_VERSION = 23
+ABI_VERSION = 24
 FL_SEG = 32
 FL_SUP = 16
 
@@ -129,6 +129,8 @@ _SIGS = {
     "fl_sparse_plan": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                       ctypes.POINTER(FlSparseHop), ctypes.c_void_p]),
     "fl_mask_bits": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]),
+    "fl_mask_order_bits": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                          ctypes.c_void_p, ctypes.c_void_p]),
     "fl_sparse_expand_bytes": (ctypes.c_size_t, [ctypes.c_int64] * 5 + [ctypes.c_int] * 2),
     "fl_sparse_expand": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(FlSide), ctypes.POINTER(FlSide),
                                         ctypes.POINTER(FlSparseHop), ctypes.c_void_p, ctypes.c_void_p]),

@@ -2588,6 +2588,38 @@ __global__ void k_mask_bits(const float *__restrict__ mask, int64_t n, uint32_t 
     if (lane == 32 && w0 + 1 < nw) bits[w0 + 1] = (uint32_t)(b >> 32);
 }
 
+// A Boolean visibility mask straight to a side's bitmap, without the float
+// gather of fl_apply_mask: the mask (by original edge id, one byte each) is
+// packed into bits by edge id (coalesced, one ballot per 64 edges), then each
+// CSR position reads its edge's bit through order (a 4-byte gather from a
+// bitmap of M/8 bytes, which stays in L2) and the bits are packed again by
+// position.  An order value outside [0, n) reads as 0.
+__global__ void k_pack_bool_bits(const uint8_t *__restrict__ mask, int64_t n, uint32_t *__restrict__ bits) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t b = __ballot(e < n && mask[e] != 0);
+    const int lane = fl_lane();
+    const int64_t w0 = (e - lane) >> 5;
+    const int64_t nw = (n + 31) >> 5;
+    if (lane == 0 && w0 < nw) bits[w0] = (uint32_t)b;
+    if (lane == 32 && w0 + 1 < nw) bits[w0 + 1] = (uint32_t)(b >> 32);
+}
+
+__global__ void k_order_bits(const uint32_t *__restrict__ edge_bits, const int32_t *__restrict__ order, int64_t n,
+                             uint32_t *__restrict__ bits) {
+    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    bool on = false;
+    if (p < n) {
+        const int32_t e = order[p];
+        on = e >= 0 && e < n && ((edge_bits[e >> 5] >> (e & 31)) & 1u);
+    }
+    const uint64_t b = __ballot(on);
+    const int lane = fl_lane();
+    const int64_t w0 = (p - lane) >> 5;
+    const int64_t nw = (n + 31) >> 5;
+    if (lane == 0 && w0 < nw) bits[w0] = (uint32_t)b;
+    if (lane == 32 && w0 + 1 < nw) bits[w0 + 1] = (uint32_t)(b >> 32);
+}
+
 // Entry order validation: every entry visited exactly once (else error 1).
 __global__ void k_sp_order_count(const int32_t *__restrict__ order, int64_t nnz, int32_t *__restrict__ seen,
                                  int64_t *__restrict__ err) {
@@ -3166,7 +3198,7 @@ int sp_check(const fl_side *ori, const fl_side *inv, const fl_sparse_hop *h, con
     if (h->nnz > 0 && h->mode != SP_FIXED && !h->w) return fl_fail(FL_ERR_ARG, "%s: null attention", what);
     if (h->nnz > 0 && h->mode == SP_FIXED && !h->operators) return fl_fail(FL_ERR_ARG, "%s: null operators", what);
     for (const fl_side *s : {ori, inv})
-        if (s->edges > 0 && (!s->col_ind || (!s->mask && h->mode != SP_FIXED) || !s->group_rel ||
+        if (s->edges > 0 && (!s->col_ind || (!s->mask && !s->mask_bits && h->mode != SP_FIXED) || !s->group_rel ||
                              !s->group_start || !s->group_count))
             return fl_fail(FL_ERR_ARG, "%s: side without CSR arrays", what);
     if (h->aggregate == SP_MAX)
@@ -3678,6 +3710,18 @@ int fl_sparse_backward(void *stream, const fl_side *ori, const fl_side *inv, con
                       end, inv->order, inv->grad_edge);
     }
     return fl_check_launch("sparse_backward");
+}
+
+int fl_mask_order_bits(void *stream, const uint8_t *mask, const int32_t *order, int64_t n, uint32_t *edge_bits,
+                       uint32_t *bits) {
+    if (n < 0 || n > INT32_MAX) return fl_fail(FL_ERR_ARG, "mask_order_bits: bad length");
+    if (n == 0) return FL_OK;
+    if (!mask || !order || !edge_bits || !bits) return fl_fail(FL_ERR_ARG, "mask_order_bits: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned g = (unsigned)((n + 255) / 256);
+    FL_LAUNCH("k_pack_bool_bits", k_pack_bool_bits, dim3(g), dim3(256), 0, st, mask, n, edge_bits);
+    FL_LAUNCH("k_order_bits", k_order_bits, dim3(g), dim3(256), 0, st, edge_bits, order, n, bits);
+    return fl_check_launch("mask_order_bits");
 }
 
 int fl_mask_bits(void *stream, const float *mask, int64_t n, uint32_t *bits) {

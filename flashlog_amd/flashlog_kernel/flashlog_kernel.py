@@ -1152,7 +1152,7 @@ class _SparseSides:
             order = order.int().contiguous()
             if order.numel() != col.numel():
                 raise ValueError("order length must equal the number of CSR positions")
-        if bits is not None and (mask is None or bits.numel() < (col.numel() + 31) // 32):
+        if bits is not None and bits.numel() < (col.numel() + 31) // 32:
             raise ValueError("mask bits must cover every CSR position of a masked side")
         self.keep += [col, mask, gptr, grel, gstart, gcount, order, dscore, bits]
         side = FlSide()
@@ -1515,12 +1515,26 @@ def _mask_bits(mask_f):
     return bits
 
 
+def _mask_order_bits(mask_values, order):
+    """The side's bitmap (bit p = mask[order[p]]) straight from a Boolean
+    mask by edge id (fl_mask_order_bits: no float mask is gathered)."""
+    n = order.numel()
+    words = max((n + 31) // 32, 1)
+    edge_bits = torch.empty(words, dtype=torch.int32, device=mask_values.device)
+    bits = torch.empty(words, dtype=torch.int32, device=mask_values.device)
+    check(_lib.lib().fl_mask_order_bits(_stream(mask_values), ptr(mask_values), ptr(order), n, ptr(edge_bits),
+                                        ptr(bits)), "mask_order_bits")
+    return bits
+
+
 def _cached_mask_order(mask_values, order):
-    """(mask[order] as float, its bitmap when mask_values is bool -- every
-    value then 0 or 1 -- else None), reused while the same (unmodified) mask
-    and order tensors are passed again (the top-k hop gets the raw per-edge
-    mask on every call; without edge weights its CSR-ordered form is
-    fixed)."""
+    """(mask[order] as float, or None; its bitmap, or None) for a side of the
+    top-k hop without edge weights: a Boolean mask gives only the bitmap
+    (every value 0 or 1, read as bits by the kernels), another mask only the
+    float gather.  Reused while the same (unmodified) mask and order tensors
+    are passed again (the hop gets the raw per-edge mask on every call; a
+    training step that hides its batch's triples in place changes the
+    mask's version, so the first hop of the step rebuilds it)."""
     key = (mask_values.data_ptr(), mask_values._version, mask_values.numel(), order.data_ptr(), order._version,
            order.numel())
     hit = _MASK_CACHE.get(key)
@@ -1528,10 +1542,16 @@ def _cached_mask_order(mask_values, order):
         return hit[2]
     for k in [k for k, v in _MASK_CACHE.items() if v[0]() is None or v[1]() is None]:
         del _MASK_CACHE[k]
-    out = _apply_mask_order(mask_values.contiguous().view(-1), order, None)
-    bits = _mask_bits(out) if mask_values.dtype == torch.bool else None
-    _MASK_CACHE[key] = (weakref.ref(mask_values), weakref.ref(order), (out, bits))
-    return out, bits
+    flat = mask_values.contiguous().view(-1)
+    _require_cuda(flat, order)
+    if flat.dtype == torch.bool:
+        if order.numel() != flat.numel():
+            raise ValueError("mask length must equal the number of CSR positions")
+        out = (None, _mask_order_bits(flat, order.to(torch.int32).contiguous()))
+    else:
+        out = (_apply_mask_order(flat, order, None), None)
+    _MASK_CACHE[key] = (weakref.ref(mask_values), weakref.ref(order), out)
+    return out
 
 
 class FlashLogFunctionSparse3DAllEdgesSum(autograd.Function):

@@ -67,14 +67,27 @@ def make_graph(cfg_id, scale=1.0, seed=None):
     return h.astype(np.int64), r.astype(np.int64), t.astype(np.int64), E, R
 
 
-def make_queries(h, r, t, R, B, rng):
+def make_queries(h, r, t, R, B, rng, return_index=False):
     """B queries drawn from the triples; each is forward (h, r) or inverse
-    (t, r + R) with probability 1/2 (the eval batches of src/main.py:717-720)."""
+    (t, r + R) with probability 1/2 (the eval batches of src/main.py:717-720).
+    return_index: also the triples' indices (the edge ids a training step
+    hides, src/main.py:887-890); the draws are the same either way."""
     idx = rng.integers(0, h.shape[0], size=B)
     inv = rng.random(B) < 0.5
     src = np.where(inv, t[idx], h[idx])
     rel = np.where(inv, r[idx] + R, r[idx])
     tgt = np.where(inv, h[idx], t[idx])
+    out = (src.astype(np.int64), rel.astype(np.int64), tgt.astype(np.int64))
+    return out + (idx.astype(np.int64),) if return_index else out
+
+
+def training_queries(h, r, t, R, idx):
+    """The queries a training batch of triples idx propagates without
+    wot_inv (src/dataloader.py:114-122): each triple forward (h, r -> t),
+    then inverse (t, r + R -> h), interleaved."""
+    src = np.stack([h[idx], t[idx]], 1).reshape(-1)
+    rel = np.stack([r[idx], r[idx] + R], 1).reshape(-1)
+    tgt = np.stack([t[idx], h[idx]], 1).reshape(-1)
     return src.astype(np.int64), rel.astype(np.int64), tgt.astype(np.int64)
 
 

@@ -79,9 +79,10 @@ typedef struct fl_side {
                                       sides may share it)                  */
     const uint32_t *mask_bits;     /* optional: [ceil(M/32)] bit p = mask[p]
                                       != 0, set only when every mask value
-                                      is 0 or 1 (fl_mask_bits); the sparse
-                                      hop then tests bits instead of reading
-                                      mask                                  */
+                                      is 0 or 1 (fl_mask_bits, or
+                                      fl_mask_order_bits from a bool mask);
+                                      the sparse hop then tests bits and
+                                      never reads mask, which may be null  */
 } fl_side;
 
 const char *fl_last_error(void);
@@ -155,6 +156,16 @@ int fl_apply_mask(void *stream, const void *mask_values, int mask_is_bool,
  * counterpart in the reference: a compact copy of the mask the sparse
  * kernels gather from. */
 int fl_mask_bits(void *stream, const float *mask, int64_t n, uint32_t *bits);
+
+/* A side's mask_bits straight from the Boolean visibility mask by original
+ * edge id (bool [n], one byte each) and the side's order (CSR position ->
+ * edge id): bits[w] bit j = mask[order[32w + j]], for the n positions.
+ * edge_bits is caller scratch of ceil(n/32) words (the mask packed by edge
+ * id).  Replaces apply_mask_cuda (flashlog.cu:1291-1340) followed by
+ * fl_mask_bits for a bool mask without edge weights, without the float
+ * gather (a bit gather from an M/8-byte table instead). */
+int fl_mask_order_bits(void *stream, const uint8_t *mask, const int32_t *order, int64_t n,
+                       uint32_t *edge_bits, uint32_t *bits);
 
 /* out[i] = 1 - sigmoid(weight[order[i]]) for i < nnz: the per-position edge
  * score derivative factor of the sparse backward with trainable edge

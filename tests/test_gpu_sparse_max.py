@@ -418,6 +418,49 @@ def test_mask_bits_match_packbits(n):
     np.testing.assert_array_equal(got[: want.size], want)
 
 
+@pytest.mark.parametrize("n", [1, 31, 64, 1000, 4097, 100003])
+def test_mask_order_bits_match_packbits(n):
+    """fl_mask_order_bits: bit p of the side's bitmap = mask[order[p]] for a
+    Boolean mask by edge id and a permutation order (a CSR side's), packed as
+    numpy's little-endian packbits; the tail of the last word zero."""
+    fk = _fk()
+    rng = np.random.default_rng(n + 1)
+    mask = rng.random(n) < 0.6
+    order = rng.permutation(n).astype(np.int32)
+    got = fk._mask_order_bits(torch.from_numpy(mask).cuda(), torch.from_numpy(order).cuda()).cpu().numpy()
+    padded = np.zeros(((n + 31) // 32) * 32, np.uint8)
+    padded[:n] = mask[order]
+    want = np.packbits(padded, bitorder="little").view(np.uint32)
+    np.testing.assert_array_equal(got.view(np.uint32)[: want.size], want)
+
+
+def test_mask_updated_in_place_between_hops():
+    """A training step hides its batch's triples in the mask in place and
+    restores them afterwards (src/main.py:887-890,927-930): the top-k hop
+    sees each version of the mask (its cached bitmap is rebuilt), checked
+    bit for bit against the oracle with that version's masks."""
+    B, L, K = 3, 2, 4
+    rng, E, R, n, csr, mbool, _, state, w = _case(2, 0.3, B, L, 60, 515, drop=0.0)
+    fk = _fk()
+    b, l, e, v = _dev(*state)
+    wt = torch.from_numpy(w).cuda()
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    mk = torch.from_numpy(mbool).cuda()
+    hidden = torch.from_numpy(rng.choice(mbool.shape[0], 500, replace=False)).cuda()
+    for step in range(3):
+        if step == 1:
+            mk[hidden] = False
+        if step == 2:
+            mk[hidden] = True
+        out = fk.FlashLogFunctionSparse3DTopKSum.apply(b, l, e, v, wt, *tc[:4], *tc[4:8], *tc[8:16], mk, None,
+                                                       B, L, E, R, False, K, False, None, False, False)
+        mnow = mk.cpu().numpy()
+        masks = tuple(mnow[csr[o]].astype(np.float32) for o in (3, 7))
+        keys, vals = O.sparse_forward(O.SPARSE_TOPK, *state, B, L, E, w, csr, masks, R, False, K)
+        assert np.array_equal(_keys(out.indices(), L, E), keys), step
+        assert np.array_equal(bits(out.values().cpu().numpy()), bits(vals)), step
+
+
 @pytest.mark.parametrize("agg", ["sum", "max"])
 def test_topk_hop_rejects_nonfinite_attention(agg):
     """flashlog.cu:2019-2021: a non-finite attention weight is rejected (the
