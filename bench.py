@@ -771,19 +771,27 @@ def main_rules(args):
         run()
     torch.cuda.synchronize()
     reps = max(1, min(args.steps, 5))
-    kn = ["k_fx_count", "k_fx_fill", "k_sp_hist", "k_sp_partition", "k_sp_accum_small", "k_sp_accum_mid",
-          "k_sp_accum_hot", "k_sp_emit", "k_rule_accum", "k_rule_rowsum", "k_rule_combine"]
-    _lib.prof_enable(True)
     t0 = time.perf_counter()
     for _ in range(reps):
         run()
     torch.cuda.synchronize()
     el = (time.perf_counter() - t0) / reps
-    prof = {k: _lib.prof_read(k) for k in kn}
+    # kernel times (HIP events around each launch) and the steps' sizes, one more pass
+    _lib.prof_enable(True)
+    fk.plan_log = []
+    run()
+    torch.cuda.synchronize()
+    plans = fk.plan_log
+    fk.plan_log = None
+    prof = {k: _lib.prof_read(k) for k in RULE_STEP_KERNELS + RULE_ACC_KERNELS}
     _lib.prof_enable(False)
-    per_pass = {k: v[0] / reps for k, v in prof.items()}
-    print("rules: %.1f ms per pass of %d queries x %d rules (%d heads); kernel ms per pass %s"
-          % (el * 1e3, NQ, NR, len(groups), json.dumps({k: round(v, 3) for k, v in per_pass.items()})),
+    per_pass = {k: v[0] for k, v in prof.items()}
+    step_ms = sum(per_pass[k] for k in RULE_STEP_KERNELS)
+    step_bytes = float(sum(rule_step_bytes(p) for p in plans))
+    achieved = step_bytes / (step_ms * 1e-3) / 1e9 if step_ms > 0 else 0.0
+    dominant = max(per_pass, key=lambda k: per_pass[k])
+    print("rules: %.1f ms per pass of %d queries x %d rules (%d heads), %d grounding steps; kernel ms per pass %s"
+          % (el * 1e3, NQ, NR, len(groups), len(plans), json.dumps({k: round(v, 3) for k, v in per_pass.items()})),
           file=sys.stderr, flush=True)
     cpu = None
     if args.cpu_seconds > 0:
@@ -807,9 +815,38 @@ def main_rules(args):
         "dtype": "f32", "data": "synthetic (seeded C3 graph, flashlog_amd/synth.py; random rules and queries)",
         "config": {"workload": "C3 rule-bank scoring: %d rules (1-3 relations, %d ranks) over %d (source, head) "
                                "queries, %d heads, chunks of %d rules" % (NR, RANKS, NQ, len(groups), CHUNK)},
-        "kernel_ms_per_pass": per_pass, "roofline": None, "cpu_baseline": cpu,
+        "kernel_ms_per_pass": per_pass,
+        "kernel_ms_total": sum(per_pass.values()),
+        "roofline": {"kernel": "fixed-relation rule steps (their kernels, per pass)", "bound": "hbm",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "algorithmic_bytes_per_launch": step_bytes, "ms_per_launch": step_ms, "traffic": None,
+                     "steps_per_pass": len(plans)},
+        "dominant_kernel": {"name": dominant, "ms_per_pass": per_pass[dominant]},
+        "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
+
+
+# The fixed-relation rule step's kernels (the sparse pipeline's mode 2) and the
+# rule bank's accumulation kernels.
+RULE_STEP_KERNELS = ["k_fx_count", "k_fx_fill", "k_sp_rowptr", "k_sp_rowinfo", "k_sp_hist", "k_sp_vscan",
+                     "k_sp_partition", "k_sp_accum_small", "k_sp_accum_few", "k_sp_accum_mid", "k_sp_accum_hot",
+                     "k_sp_emit", "k_scan_tiles", "k_scan_totals", "k_scan_apply", "k_scan_one", "k_fill_i32",
+                     "k_fill_i64", "k_sp_plan_out"]
+RULE_ACC_KERNELS = ["k_cs_rank", "k_cs_weighted_add", "k_rule_accum_max", "k_rule_rowsum", "k_rule_combine"]
+
+
+def rule_step_bytes(plan):
+    """Algorithmic bytes of one fixed-relation rule step by the measurement
+    plan's formula: 28 nnz_in (entries) + 8 per row (its operator) + per
+    entry 8 B of row group pointers, 2 ceil(log2 g) B of group relations
+    searched and 8 B of group start and count + 4 B per item (its column) +
+    28 nnz_out; g is taken as the entries' mean groups per side."""
+    import math
+    nnz, items, nout, rows = plan["nnz"], plan["items"], plan["nout"], plan["rows"]
+    g = plan["groups"] / max(2 * nnz, 1)
+    lg = math.ceil(math.log2(g)) if g > 1 else 0
+    return 28 * nnz + 8 * rows + nnz * (16 + 2 * lg) + 4 * items + 28 * nout
 
 
 SPARSE_KERNELS = ["k_sp_topc", "k_race_flags", "k_race_keys", "k_race_rows", "k_race_select", "k_fill_from",

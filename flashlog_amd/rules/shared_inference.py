@@ -31,7 +31,9 @@ produced or the order of floating-point additions of the normalizers, not
 the values of the channel sums.
 """
 import types
+import weakref
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -44,19 +46,45 @@ def _empty(shape, device):
                                    torch.empty(0, device=device), shape, is_coalesced=True)
 
 
+# Host copies of a CSR tuple's group arrays (row group pointers, group
+# relations and counts of both sides), kept while the tensors live
+# unmodified: the first-hop degrees of every call read them on the host
+# instead of slicing device tensors source by source.
+_HOST_GROUPS = {}
+
+
+def _host_groups(csr):
+    keyed = tuple(csr[i] for i in (8, 9, 11, 12, 13, 15))
+    key = tuple((id(t), t._version) for t in keyed)
+    hit = _HOST_GROUPS.get(key)
+    if hit is not None and all(r() is t for r, t in zip(hit[0], keyed)):
+        return hit[1]
+    for k in [k for k, v in _HOST_GROUPS.items() if any(r() is None for r in v[0])]:
+        del _HOST_GROUPS[k]
+    arrays = tuple(t.detach().cpu().numpy().astype(np.int64) for t in keyed)
+    _HOST_GROUPS[key] = (tuple(weakref.ref(t) for t in keyed), arrays)
+    return arrays
+
+
 def _first_degrees(sources, csr, relations):
-    """[(operator, group size)] of every first-hop group of the sources
-    (forward groups as their relation, inverse ones offset by relations)."""
-    positions = torch.stack((sources, sources + 1), dim=1).reshape(-1)
-    bounds = torch.stack((csr[8][positions], csr[12][positions])).cpu().tolist()
-    degrees = []
-    for side, (ri, ci) in enumerate(((9, 11), (13, 15))):
-        for i in range(sources.numel()):
-            lo, hi = bounds[side][2 * i:2 * i + 2]
-            if hi > lo:
-                ops = (csr[ri][lo:hi].long() + side * relations).tolist()
-                degrees.extend(zip(ops, csr[ci][lo:hi].tolist()))
-    return degrees
+    """(operators, group sizes) of every first-hop group of the sources, as
+    int64 arrays: forward groups as their relation, inverse ones offset by
+    relations (rules/shared_inference.py:34-47; one read of the sources)."""
+    gp_o, rel_o, cnt_o, gp_i, rel_i, cnt_i = _host_groups(csr)
+    src = sources.detach().cpu().numpy().astype(np.int64)
+    ops, cnts = [], []
+    for side, (gp, rel, cnt) in enumerate(((gp_o, rel_o, cnt_o), (gp_i, rel_i, cnt_i))):
+        lo, hi = gp[src], gp[src + 1]
+        n = hi - lo
+        if n.sum() == 0:
+            continue
+        # every group index of every source, sources in order
+        idx = np.repeat(lo - np.concatenate(([0], np.cumsum(n)[:-1])), n) + np.arange(int(n.sum()))
+        ops.append(rel[idx] + side * relations)
+        cnts.append(cnt[idx])
+    if not ops:
+        return np.zeros(0, np.int64), np.zeros(0, np.int64)
+    return np.concatenate(ops), np.concatenate(cnts)
 
 
 def _default_ev():
@@ -127,10 +155,12 @@ def score(ev, sources, rules, csr, relations, entities, chunk_size,
         return _empty(shape, device)
     all_rules = rules
     stats["rules_before"] = len(rules)
-    degrees = _first_degrees(sources, csr, relations) if len(csr) >= 16 and batch > 0 else []
     if len(csr) >= 16 and batch > 0:
-        available = {op for op, cnt in degrees if cnt > 0} | {2 * relations}
+        deg_ops, deg_cnt = _first_degrees(sources, csr, relations)
+        available = set(np.unique(deg_ops[deg_cnt > 0]).tolist()) | {2 * relations}
         rules = [r for r in rules if not r["body"] or r["body"][0] in available]
+    else:
+        deg_ops, deg_cnt = np.zeros(0, np.int64), np.zeros(0, np.int64)
     stats["rules_after"] = len(rules)
     if not rules or batch == 0:
         return _empty(shape, device)
@@ -139,9 +169,14 @@ def score(ev, sources, rules, csr, relations, entities, chunk_size,
     for r in rules:
         if r["body"]:
             first_ops[r["body"][0]] = first_ops.get(r["body"][0], 0) + 1
-    max_first = max((cnt for op, cnt in degrees if op in first_ops), default=0)
-    stats["first_frontier_bytes"] = max((cnt * min(chunk_size, first_ops.get(op, 0)) * 28 for op, cnt in degrees),
-                                        default=0)
+    # per first-hop group: the rules starting with its operator (0 for none)
+    table = np.zeros(2 * relations + 2, np.int64)
+    for op, k in first_ops.items():
+        if 0 <= op < table.size:
+            table[op] = k
+    uses = table[np.clip(deg_ops, 0, table.size - 1)] if deg_ops.size else deg_ops
+    max_first = int(deg_cnt[uses > 0].max()) if (uses > 0).any() else 0
+    stats["first_frontier_bytes"] = int((deg_cnt * np.minimum(chunk_size, uses) * 28).max()) if deg_ops.size else 0
     if batch > 1 and max_first * 28 > source_frontier_budget_bytes:
         stats["source_splits"] = stats.get("source_splits", 0) + 1
         rows_out, cols_out, vals_out = [], [], []
@@ -159,9 +194,10 @@ def score(ev, sources, rules, csr, relations, entities, chunk_size,
     if len(widths) != 1 or next(iter(widths)) < 1:
         raise ValueError("nonempty rank_weights must have matching widths")
     ranks = next(iter(widths))
-    weights = torch.tensor([r["rank_weights"] for r in rules], dtype=torch.float32, device=device)
-    if not bool(torch.isfinite(weights).all()) or bool((weights < 0).any()):
+    host_w = np.asarray([r["rank_weights"] for r in rules], dtype=np.float32)
+    if not np.isfinite(host_w).all() or (host_w < 0).any():
         raise ValueError("MAX rule weights must be finite and nonnegative")
+    weights = torch.from_numpy(host_w).to(device)
     identity = 2 * relations
     steps = max(len(r["body"]) for r in rules)
     operators = torch.tensor([tuple(r["body"]) + (identity,) * (steps - len(r["body"])) for r in rules],

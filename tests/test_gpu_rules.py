@@ -108,3 +108,31 @@ def test_rule_bank_c3_full_graph(reduction, boolean, final_max):
     got = outs[0].to_dense().cpu().numpy()
     assert (want > 0).sum() > 10000
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-9)
+
+
+@pytest.mark.parametrize("reduction,final_max,sample", [("sum", False, None), ("max", True, 60)])
+def test_rule_bank_c3_scale(reduction, final_max, sample):
+    """C3's rule-bank scale: 5000 random rules (bodies of 1-3 operators, 3
+    uniform rank weights) for 500 query sources on the full C3 graph, chunk
+    16 (rules/evaluate.py:890), one call of shared_inference.score.  The sum
+    is checked on every source against the float64 oracle; the Boolean max
+    with final_max on a sample of 60 sources (each source's scores depend
+    only on its own paths, so the oracle runs on the sample)."""
+    from flashlog_amd import synth
+    from flashlog_amd.rules import shared_inference
+    h, r, t, E, R = synth.make_graph(3)
+    csr = O.build_csr_structure(h, t, r, E)
+    rng = np.random.default_rng(77)
+    bodies = [list(map(int, rng.integers(0, 2 * R, rng.integers(1, 4)))) for _ in range(5000)]
+    W = rng.random((len(bodies), 3)).astype(np.float32)
+    rules = [{"body": bd, "rank_weights": list(map(float, w))} for bd, w in zip(bodies, W)]
+    sources = h[rng.integers(0, h.shape[0], 500)]
+    tc = to_torch_csr(csr, torch.device("cuda"))
+    out = shared_inference.score(None, torch.from_numpy(sources).cuda(), rules, tc, R, E, 16,
+                                 final_max=final_max, reduction=reduction).coalesce()
+    got = out.to_dense().cpu().numpy()
+    rows = np.arange(len(sources)) if sample is None else np.sort(rng.choice(len(sources), sample, replace=False))
+    want = O.rule_scores(h, r, t, E, R, list(sources[rows]), bodies, W.astype(np.float64), reduction, False,
+                         final_max)
+    assert (want > 0).sum() > 100000
+    np.testing.assert_allclose(got[rows], want, rtol=1e-5, atol=1e-9)
