@@ -833,7 +833,8 @@ RULE_STEP_KERNELS = ["k_fx_count", "k_fx_fill", "k_sp_rowptr", "k_sp_rowinfo", "
                      "k_sp_partition", "k_sp_accum_small", "k_sp_accum_few", "k_sp_accum_mid", "k_sp_accum_hot",
                      "k_sp_emit", "k_scan_tiles", "k_scan_totals", "k_scan_apply", "k_scan_one", "k_fill_i32",
                      "k_fill_i64", "k_sp_plan_out"]
-RULE_ACC_KERNELS = ["k_cs_rank", "k_cs_weighted_add", "k_rule_accum_max", "k_rule_rowsum", "k_rule_combine"]
+RULE_ACC_KERNELS = ["k_ra_rows", "k_ra_sum", "k_cs_rank", "k_cs_weighted_add", "k_rule_accum_max", "k_rule_rowsum",
+                    "k_rule_combine"]
 
 
 def rule_step_bytes(plan):

@@ -38,6 +38,79 @@ __global__ __launch_bounds__(RB_NT) void k_rule_accum_max(const int64_t *__restr
     }
 }
 
+// Sums through LDS (entities of a source fit a workgroup's LDS): row
+// pointers of the coalesced chunk state first (thread per entry; err 1: an
+// index outside [B, L, E], 2: rows out of order, 3: entities not strictly
+// increasing within a row), then a workgroup per (source b, rank k) holds
+// acc[e] for every entity in LDS and walks the chunk's rules in order: rule
+// l's entries (distinct entities: no two lanes add into one slot) add
+// v * W[l, k] to acc, a barrier between rules.  Per entity the terms are
+// thus added from 0 in rule order, then the chunk's sum is added to the
+// dense accumulator: the order of k_cs_weighted_add, without the merge.
+constexpr int RA_NT = 256;
+
+__global__ void k_ra_zero(unsigned long long *err) {
+    if (threadIdx.x == 0) *err = 0;
+}
+constexpr int64_t RA_LDS_MAX_E = 16384;  // 64 KB of LDS per workgroup
+
+__global__ __launch_bounds__(RA_NT) void k_ra_rows(const int64_t *__restrict__ sb, const int64_t *__restrict__ sl,
+                                                  const int64_t *__restrict__ se, int64_t nnz, int64_t B, int64_t L,
+                                                  int64_t E, int64_t *__restrict__ row_ptr,
+                                                  unsigned long long *__restrict__ err) {
+    const int64_t i = (int64_t)blockIdx.x * RA_NT + threadIdx.x;
+    if (i >= nnz) return;
+    const int64_t b = sb[i], l = sl[i], e = se[i];
+    if (b < 0 || b >= B || l < 0 || l >= L || e < 0 || e >= E) {
+        atomicMax(err, 1ull);
+        return;
+    }
+    const int64_t r = b * L + l;
+    int64_t rp = -1;
+    if (i > 0) {
+        const int64_t pb = sb[i - 1], pl = sl[i - 1];
+        rp = (pb >= 0 && pb < B && pl >= 0 && pl < L) ? pb * L + pl : r;
+        if (rp > r) {
+            atomicMax(err, 2ull);
+            return;
+        }
+        if (rp == r && se[i - 1] >= e) {
+            atomicMax(err, 3ull);
+            return;
+        }
+    }
+    for (int64_t q = rp + 1; q <= r; ++q) row_ptr[q] = i;
+    if (i == nnz - 1)
+        for (int64_t q = r + 1; q <= B * L; ++q) row_ptr[q] = nnz;
+}
+
+__global__ __launch_bounds__(RA_NT) void k_ra_sum(const int64_t *__restrict__ se, const float *__restrict__ sv,
+                                                 const int64_t *__restrict__ row_ptr,
+                                                 const unsigned long long *__restrict__ err,
+                                                 const float *__restrict__ W, int64_t K, int64_t B, int64_t L,
+                                                 int64_t E, float *__restrict__ dense) {
+    extern __shared__ float acc[];  // [E]
+    if (*err != 0) return;          // a malformed state adds nothing
+    const int64_t b = blockIdx.x, k = blockIdx.y;
+    const int t = threadIdx.x;
+    for (int64_t e = t; e < E; e += RA_NT) acc[e] = 0.0f;
+    __syncthreads();
+    for (int64_t l = 0; l < L; ++l) {
+        const int64_t a = row_ptr[b * L + l], z = row_ptr[b * L + l + 1];
+        const float wk = W[l * K + k];
+        for (int64_t i = a + t; i < z; i += RA_NT) {
+            const int64_t e = se[i];
+            acc[e] = fl_add(acc[e], fl_mul(sv[i], wk));
+        }
+        __syncthreads();
+    }
+    float *drow = dense + k * B * E + b * E;
+    for (int64_t e = t; e < E; e += RA_NT) {
+        const float x = acc[e];
+        if (x != 0.0f) drow[e] = fl_add(drow[e], x);
+    }
+}
+
 // Workgroup per (k, b): the row's sum in a fixed order.
 __global__ __launch_bounds__(RB_NT) void k_rule_rowsum(const float *__restrict__ dense, int64_t E,
                                                       float *__restrict__ rowsum) {
@@ -78,7 +151,9 @@ extern "C" {
 
 size_t fl_rule_accumulate_bytes(int64_t nnz, int64_t B, int64_t L) {
     if (nnz < 0 || B < 0 || L < 0) return 0;
-    return ((fl_sparse_channel_sum_bytes(nnz, B, L) + 255) & ~(size_t)255) + 256;
+    const size_t merge = ((fl_sparse_channel_sum_bytes(nnz, B, L) + 255) & ~(size_t)255) + 256;
+    const size_t lds = ((sizeof(int64_t) * (size_t)(B * L + 1) + 255) & ~(size_t)255) + 256;
+    return merge > lds ? merge : lds;
 }
 
 int fl_rule_accumulate(void *stream, const int64_t *sb, const int64_t *sl, const int64_t *se, const float *sv,
@@ -95,6 +170,18 @@ int fl_rule_accumulate(void *stream, const int64_t *sb, const int64_t *sl, const
     }
     if (!ws || ws_bytes < fl_rule_accumulate_bytes(nnz, B, L))
         return fl::fl_fail(FL_ERR_ARG, "rule_accumulate: workspace too small");
+    if (E <= fl::RA_LDS_MAX_E && B * K <= 0x7fffffff && K <= 65535) {
+        // rules in order through an LDS accumulator per (source, rank)
+        int64_t *row_ptr = (int64_t *)ws;
+        unsigned long long *err =
+            (unsigned long long *)((char *)ws + ((sizeof(int64_t) * (size_t)(B * L + 1) + 255) & ~(size_t)255));
+        FL_LAUNCH("k_fill_u64", fl::k_ra_zero, dim3(1), dim3(64), 0, st, err);
+        FL_LAUNCH("k_ra_rows", fl::k_ra_rows, dim3((unsigned)((nnz + fl::RA_NT - 1) / fl::RA_NT)), dim3(fl::RA_NT), 0,
+                  st, sb, sl, se, nnz, B, L, E, row_ptr, err);
+        FL_LAUNCH("k_ra_sum", fl::k_ra_sum, dim3((unsigned)B, (unsigned)K), dim3(fl::RA_NT),
+                  sizeof(float) * (size_t)E, st, se, sv, row_ptr, err, W, K, B, L, E, dense);
+        return fl::fl_check_launch("rule_accumulate");
+    }
     // rank the entries of every (b, e) in rule order, then one writer per slot
     const size_t cs = (fl_sparse_channel_sum_bytes(nnz, B, L) + 255) & ~(size_t)255;
     int64_t *plan = (int64_t *)((char *)ws + cs);

@@ -1738,6 +1738,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_mid(SpRows rows, const int64
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
     __shared__ int claim;
     const int nmid = ctr[0];
+    if ((int)blockIdx.x >= nmid) return;  // no bucket left for this workgroup (see k_sp_accum_few)
     for (;;) {
         __syncthreads();  // the previous bucket is done with the LDS arrays
         if (threadIdx.x == 0) claim = atomicAdd(&ctr[1], 1);
@@ -1900,6 +1901,10 @@ __global__ __launch_bounds__(SP_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) v
     static_assert(SP_W / 32 == SP_NT, "one bitmap word per thread");
     const int t = threadIdx.x;
     const int nhot = ctr[0], nmid = ctr[2];
+    // workgroups past the listed buckets take none: the others claim every
+    // one (a participant stops only after a claim past the lists); the whole
+    // workgroup leaves at once, before any barrier
+    if ((int)blockIdx.x >= nhot + nmid) return;
     for (;;) {
         __syncthreads();  // the previous bucket is done with the LDS arrays
         if (t == 0) {
@@ -1983,6 +1988,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_accum_hot(SpRows rows, const int64
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
     __shared__ int claim;
     const int nhot = hot_count[0];
+    if ((int)blockIdx.x >= nhot) return;  // no bucket left for this workgroup (see k_sp_accum_few)
     for (;;) {
         __syncthreads();  // the previous bucket is done with the LDS arrays
         if (threadIdx.x == 0) claim = atomicAdd(&hot_count[1], 1);
@@ -2171,6 +2177,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_max_hot(SpRows rows, const int64_t
     __shared__ int scan_lds[SP_NT / FL_WAVE + 1];
     __shared__ int claim;
     const int nhot = hot_count[0];
+    if ((int)blockIdx.x >= nhot) return;  // no bucket left for this workgroup (see k_sp_accum_few)
     for (;;) {
         __syncthreads();  // the previous bucket is done with the LDS arrays
         if (threadIdx.x == 0) claim = atomicAdd(&hot_count[1], 1);

@@ -37,9 +37,12 @@ def _accumulate(b, l, e, v, W, B, L, E, is_max):
     return buf.cpu().numpy(), K * B * E
 
 
+@pytest.mark.parametrize("E", [10, 20000])
 @pytest.mark.parametrize("is_max", [0, 1])
-def test_rule_accumulate_well_formed(is_max):
-    B, L, E = 2, 3, 10
+def test_rule_accumulate_well_formed(is_max, E):
+    """Both sum paths: entities in LDS (E <= 16384) and the merge over the
+    channels (larger E)."""
+    B, L = 2, 3
     b, l, e = [0, 0, 1, 1], [0, 2, 1, 2], [3, 3, 9, 9]
     v = [1.0, 2.0, 3.0, 1.0]
     W = np.array([[0.5, 1.0], [0.25, 2.0], [1.0, 0.125]], np.float32)
@@ -62,19 +65,22 @@ def test_rule_accumulate_well_formed(is_max):
     assert (got[n:] == 0.5).all()
 
 
+@pytest.mark.parametrize("E", [8, 20000])
 @pytest.mark.parametrize("is_max", [0, 1])
-@pytest.mark.parametrize("case", ["entity_high", "entity_negative", "batch_high", "unsorted"])
-def test_rule_accumulate_malformed_writes_nothing_out_of_shape(case, is_max):
-    B, L, E = 2, 2, 8
+@pytest.mark.parametrize("case", ["entity_high", "entity_negative", "batch_high", "unsorted", "duplicate"])
+def test_rule_accumulate_malformed_writes_nothing_out_of_shape(case, is_max, E):
+    B, L = 2, 2
     b, l, e, v = [0, 0, 1], [0, 1, 1], [1, 2, 7], [1.0, 1.0, 1.0]
     if case == "entity_high":
-        e = [1, 2, 8]
+        e = [1, 2, E]
     elif case == "entity_negative":
         e = [-1, 2, 7]
     elif case == "batch_high":
         b = [0, 0, 2]
-    else:
+    elif case == "unsorted":
         b, l, e = [0, 0, 0], [1, 1, 0], [5, 2, 1]
+    else:  # an entity twice in one row (not coalesced)
+        b, l, e = [0, 0, 1], [1, 1, 1], [2, 2, 7]
     W = np.ones((L, 1), np.float32)
     got, n = _accumulate(b, l, e, v, W, B, L, E, is_max)
     assert (got[n:] == 0.5).all()
