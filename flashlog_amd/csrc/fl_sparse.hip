@@ -1219,10 +1219,21 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
 // position (written within the tile's range, not scattered over the row).
 // the partition's workgroup: one 4096-item tile over 512 threads (8 items
 // each: twice the waves per CU of 256 threads at the same LDS)
+// The inverse map of a row (raw index -> partition position) is encoded as
+// bucket << pos_bits | position within the row's partitioned items when the
+// row has fewer than 2^pos_bits items (pos_bits = 31 - the bucket bits, so
+// the value stays nonnegative; holes are -1) and the row's buckets fit the
+// partition's LDS table; else it holds the global partition position.  Both
+// the partition and the output map decide it per row from the same sizes.
+__device__ __forceinline__ bool sp_inv_encoded(const SpRows &rows, int64_t r, int pos_bits) {
+    return pos_bits > 0 && rows.NB <= SP_TILE / 2 &&
+           rows.row_item0[r + 1] - rows.row_item0[r] < ((int64_t)1 << pos_bits);
+}
+
 constexpr int SP_PT_NT = 512;
 constexpr int SP_PT_IPT = SP_TILE / SP_PT_NT;
 
-__global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows rows, int nbits,
+__global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows rows, int nbits, int pos_bits,
                                                        const int64_t *__restrict__ base,
                                                        const int32_t *__restrict__ colpre,
                                                        const int32_t *__restrict__ raw_dst,
@@ -1281,6 +1292,11 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
         for (int j = 0; j < SP_PT_IPT; ++j) key[j] = sorted[j * SP_PT_NT + t];
         __syncthreads();
         int32_t *inv_lds = reinterpret_cast<int32_t *>(const_cast<uint32_t *>(sorted));
+        // rows of fewer than 2^pos_bits items store bucket << pos_bits | the
+        // position within the row's partitioned items, so that the output
+        // map needs no destination (sp_inv_encoded)
+        const bool enc = sp_inv_encoded(rows, r, pos_bits);
+        const int64_t rowpos0 = bb[0];
         // every item's destination and value requested before the stores
         int32_t dv[SP_PT_IPT];
         float vv[SP_PT_IPT];
@@ -1304,7 +1320,7 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
             const int64_t q = boff[bk] + p;
             part_dst[q] = dv[j];
             part_val[q] = vv[j];
-            inv_lds[idx] = (int32_t)q;
+            inv_lds[idx] = enc ? (int32_t)((bk << pos_bits) | (uint32_t)(q - rowpos0)) : (int32_t)q;
             if (part_tie) part_tie[q] = fl_ld32(raw_tie + i0, idx);
         }
         __syncthreads();
@@ -2310,6 +2326,7 @@ constexpr int SP_LTO_NB = 2048;  // buckets per row kept in LDS by k_sp_local_to
 
 __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows rows, const int32_t *__restrict__ raw_dst,
                                                           const int64_t *__restrict__ out_base,
+                                                          const int64_t *__restrict__ base, int pos_bits,
                                                           const int32_t *__restrict__ part_inv,
                                                           const int32_t *__restrict__ part_local,
                                                           int32_t *__restrict__ raw_local) {
@@ -2331,6 +2348,29 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
     const int32_t *__restrict__ tdst = raw_dst + i0;
     int32_t *__restrict__ tloc = raw_local + i0;
     const int32_t *__restrict__ tinv = part_inv ? part_inv + i0 : nullptr;
+    if (tinv && lds && sp_inv_encoded(rows, r, pos_bits)) {
+        // the map carries each item's bucket: no destination is read; every
+        // entry of the map first, then every gather, then every store
+        constexpr int Q = SP_TILE / SP_NT;
+        const int32_t *__restrict__ rloc = part_local + base[r * rows.NB];
+        const uint32_t pmask = (1u << pos_bits) - 1u;
+        int32_t qq[Q];
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t idx = (uint32_t)(j * SP_NT) + threadIdx.x;
+            qq[j] = idx < (uint32_t)c ? fl_ld32(tinv, idx) : -1;
+        }
+        int32_t ll[Q];
+#pragma unroll
+        for (int j = 0; j < Q; ++j) ll[j] = qq[j] >= 0 ? fl_ld32(rloc, (uint32_t)qq[j] & pmask) : -1;
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t idx = (uint32_t)(j * SP_NT) + threadIdx.x;
+            if (idx < (uint32_t)c)
+                fl_st32(tloc, idx, ll[j] >= 0 ? (int32_t)(obase[(uint32_t)qq[j] >> pos_bits] + ll[j]) : -1);
+        }
+        return;
+    }
     if (tinv && lds && c == SP_TILE) {
         // a full tile: every position and destination first, then every
         // gather, then every store (16 independent chains per thread)
@@ -3524,7 +3564,8 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
         if ((rc = exclusive_scan(st, x.tot, x.base, R * NB, x.tmp)) != FL_OK) return rc;
         if (h->tiles > 0)
             FL_LAUNCH("k_sp_partition", k_sp_partition, dim3((unsigned)h->tiles), dim3(SP_PT_NT), 0, st, R, rows,
-                      sp_bucket_bits(NB + 1), x.base, x.hist, x.raw_dst, x.raw_val, x.part_dst, x.part_val,
+                      sp_bucket_bits(NB + 1), 31 - sp_bucket_bits(NB), x.base, x.hist, x.raw_dst, x.raw_val,
+                      x.part_dst, x.part_val,
                       raw_local ? x.part_inv : (int32_t *)nullptr, x.raw_tie, x.part_tie);
         dst_arr = x.part_dst;
         val_arr = x.part_val;
@@ -3565,7 +3606,8 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     // the backward's map: each raw item's output index
     if (raw_local && h->tiles > 0)
         FL_LAUNCH("k_sp_local_to_out", k_sp_local_to_out, dim3((unsigned)h->tiles), dim3(SP_NT), 0, st, R, rows,
-                  x.raw_dst, out_base, NB > 1 ? x.part_inv : (const int32_t *)nullptr, acc_local, raw_local);
+                  x.raw_dst, out_base, x.base, 31 - sp_bucket_bits(NB),
+                  NB > 1 ? x.part_inv : (const int32_t *)nullptr, acc_local, raw_local);
     return fl_check_launch("sparse_expand");
 }
 
