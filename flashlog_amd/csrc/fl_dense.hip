@@ -353,13 +353,19 @@ __device__ __forceinline__ void walk_kept(const fl_side &s, int64_t s0, int64_t 
         float m[WALK_U], wv[WALK_U];
         uint32_t bw[WALK_U];
         float2 rc[WALK_U];
+        // the sources' row bits first: a slot's mask, weight and record are
+        // read only where its source is active in this row (a small share of
+        // the in-edges under the c1 budget)
+#pragma unroll
+        for (int u = 0; u < WALK_U; ++u) bw[u] = base + u < s1 ? bmw[src[u]] : 0u;
 #pragma unroll
         for (int u = 0; u < WALK_U; ++u) {
-            bw[u] = 0;
-            if (base + u < s1) {
+            m[u] = 0.0f;
+            wv[u] = 0.0f;
+            rc[u] = make_float2(0.0f, 0.0f);
+            if (bw[u] & bit) {
                 m[u] = s.mask[pos[u]];
                 wv[u] = wr[rel[u]];
-                bw[u] = bmw[src[u]];
                 rc[u] = PK[plane + (int64_t)src[u] * BL];
             }
         }
