@@ -481,7 +481,7 @@ def main_c4(args):
         return loss
 
     kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull_max", "k_seg_max", "k_sup_max",
-               "k_heavy_max", "k_max_bwd", "k_bwd_identity"]
+               "k_heavy_max", "k_bwd_pairs_max", "k_bwd_identity", "k_row_list"]
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()

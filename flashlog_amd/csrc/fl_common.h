@@ -146,6 +146,13 @@ __device__ __forceinline__ void fl_st32(T *base, uint32_t idx, T v) {
 // per-wave indices, and loads at them, stay scalar).
 __device__ __forceinline__ int fl_wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / FL_WAVE)); }
 
+// LDS ordering between the lanes of one wave (program order + fence).
+__device__ __forceinline__ void fl_wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Float key that orders like the value (ascending) for every non-NaN float.
 __device__ __forceinline__ uint32_t fl_order_key(float v) {
     uint32_t u = __float_as_uint(v);

@@ -785,7 +785,7 @@ __global__ __launch_bounds__(PULL_NT) void k_heavy_max(fl_side ori, fl_side inv,
 //   (frontier)      the forward's k_col_count / k_frontier / k_c2_hard on the
 //                   same A and w give the same admitted edges.
 //   k_row_list      per row, its active sources in ascending order.
-//   k_bwd_rows      one thread per active (source, row): the ORI then INV row
+//   k_bwd_pairs     one wave per active (source, row): the ORI then INV row
 //                   walk of the reference, adding (go*w)*m onto the identity
 //                   term in CSR order (bit-exact gA), and per relation group
 //                   the partial sum of (go*a)*m into the pair's row of PG.
@@ -890,17 +890,25 @@ __global__ __launch_bounds__(RL_NT) void k_row_list(const uint32_t *__restrict__
     if (threadIdx.x == 0) rowcnt[bl] = run;
 }
 
-// One side's walk of the kept positions of (source, row), in CSR order:
-// returns acc + sum of (go*w)*m, and stores per relation group the partial
-// sum of (go*a)*m in pg.  MAX: only positions that won their destination
-// (arg[row, dst] == p) contribute, as in the winner-only backward
-// (flashlog.cu:699-710); a winning position is always a kept one.
+// One side of an active (source, row) pair, by one wave: the kept positions
+// in CSR order (groups in order, each group's first `take` edges), 64 at a
+// time.  Lane j of a window holds group j; item k of the window belongs to
+// the first group whose inclusive take prefix exceeds k.  Each item's terms
+// (go*w)*m and (go*a)*m are formed in parallel; the contributing items are
+// then added one after another in position order -- the first term onto
+// acc, the second onto its group's partial, held by the group's lane -- so
+// the additions are those of a sequential walk.  MAX: only positions that
+// won their destination (arg[row, dst] == p) contribute, as in the
+// winner-only backward (flashlog.cu:699-710); a winning position is always a
+// kept one.  Group partials go to the pair's row of relation columns in LDS
+// (pgl, written where take > 0).
 template <bool MAX>
-__device__ __forceinline__ float bwd_walk(const fl_side &s, int64_t src, int64_t bl, int64_t BL, int64_t E,
+__device__ __forceinline__ float bwd_side(const fl_side &s, int64_t src, int64_t bl, int64_t BL, int64_t E,
                                           int64_t n, int64_t off, int dir, float a, const float *__restrict__ w,
                                           const float *__restrict__ grad, const int64_t *__restrict__ arg,
                                           const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
-                                          float acc, float *__restrict__ pg) {
+                                          float acc, float *pgl) {
+    const int lane = fl_lane();
     const int64_t at = ((int64_t)dir * E + src) * BL + bl;
     const float th = PK[at].y;
     const int32_t cut = th > 0.0f ? CUT[at] : 0;
@@ -908,58 +916,96 @@ __device__ __forceinline__ float bwd_walk(const fl_side &s, int64_t src, int64_t
     const float *gr = grad + bl * E;
     const int64_t *ar = MAX ? arg + bl * E : nullptr;
     const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
-    for (int64_t g = g0; g < g1; ++g) {
-        const int rel = s.group_rel[g];
-        const float wv = wr[rel];
-        const int64_t start = s.group_start[g];
-        const int64_t take = group_take(wv, th, cut, start, s.group_count[g]);
+    for (int64_t gb = g0; gb < g1; gb += FL_WAVE) {
+        const int64_t g = gb + lane;
+        int rel = 0;
+        int32_t start = 0, take = 0;
+        float wv = 0.0f;
+        if (g < g1) {
+            rel = s.group_rel[g];
+            wv = wr[rel];
+            start = s.group_start[g];
+            take = (int32_t)group_take(wv, th, cut, start, s.group_count[g]);
+        }
+        // a source's kept edges on a side fit int32 (CSR positions are int32)
+        const int32_t incl = fl_wave_incl_scan_i32(take);
+        const int32_t total = __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
+        const int32_t first = start - (incl - take);  // item k of group j sits at first_j + k
         float gs = 0.0f;
-        for (int64_t b = start; b < start + take; b += 8) {
-            float m[8], go[8];
-            bool win[8];
+        for (int32_t q0 = 0; q0 < total; q0 += FL_WAVE) {
+            const int32_t k = q0 + lane;
+            int j = 0;  // lanes whose inclusive prefix is <= k
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                win[u] = true;
-                if (b + u < start + take) {
-                    m[u] = s.mask[b + u];
-                    const int32_t dst = s.col_ind[b + u];
-                    go[u] = gr[dst];
-                    if (MAX) win[u] = ar[dst] == b + u;
+            for (int step = FL_WAVE / 2; step > 0; step >>= 1)
+                if (__shfl(incl, j + step - 1, FL_WAVE) <= k) j += step;
+            const bool valid = k < total;
+            const int32_t p = __shfl(first, j, FL_WAVE) + k;
+            const float wj = __shfl(wv, j, FL_WAVE);
+            float m = 0.0f, go = 0.0f;
+            bool win = false;
+            if (valid) {
+                m = s.mask[p];
+                const int32_t dst = s.col_ind[p];
+                if (m != 0.0f) {
+                    go = gr[dst];
+                    win = MAX ? ar[dst] == (int64_t)p : true;
                 }
             }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (b + u >= start + take || !win[u] || m[u] == 0.0f || go[u] == 0.0f) continue;
-                acc = fl_add(acc, fl_mul(fl_mul(go[u], wv), m[u]));
-                gs = fl_add(gs, fl_mul(fl_mul(go[u], a), m[u]));
+            const bool contrib = valid && win && m != 0.0f && go != 0.0f;
+            const float t1 = fl_mul(fl_mul(go, wj), m);
+            const float t2 = fl_mul(fl_mul(go, a), m);
+            for (uint64_t bal = __ballot(contrib); bal; bal &= bal - 1) {
+                const int i = __ffsll((long long)bal) - 1;
+                acc = fl_add(acc, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t1), i)));
+                const int gi = __builtin_amdgcn_readlane(j, i);
+                const float t2i = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t2), i));
+                if (lane == gi) gs = fl_add(gs, t2i);
             }
         }
-        if (take > 0) pg[off + rel] = gs;
+        if (take > 0) pgl[off + rel] = gs;
     }
     return acc;
 }
 
+// One wave per active (source, row) pair, pairs in row-major order (the
+// row's sources ascending, from k_row_list): gA[row, src] = the identity
+// term written by k_bwd_identity plus the ORI then INV walks, and the pair's
+// row of PG (relation partials, 0 where no edge of the relation is kept).
+constexpr int BWDP_WAVES = BWD_NT / FL_WAVE;
+
 template <bool MAX>
-__global__ __launch_bounds__(BWD_NT) void k_bwd_rows(
+__global__ __launch_bounds__(BWD_NT) void k_bwd_pairs(
     fl_side ori, fl_side inv, const float *__restrict__ A, const float *__restrict__ w,
     const float *__restrict__ g_ori, const float *__restrict__ g_inv, const int64_t *__restrict__ arg_ori,
     const int64_t *__restrict__ arg_inv, int64_t BL, int64_t E, int64_t n,
     int64_t r_size, const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
     const int32_t *__restrict__ rowlist, const int32_t *__restrict__ rowcnt, const int64_t *__restrict__ rowoff,
     int64_t pairs, float *__restrict__ gA, float *__restrict__ PG) {
-    const int64_t bl = blockIdx.y;
-    const int64_t cnt = rowcnt[bl];
-    for (int64_t k = (int64_t)blockIdx.x * BWD_NT + threadIdx.x; k < cnt; k += (int64_t)gridDim.x * BWD_NT) {
-        if (rowoff[bl] + k >= pairs) break;  // the caller's buffer holds `pairs` rows
-        const int64_t src = rowlist[bl * E + k];
-        const float a = A[bl * E + src];
-        float *pg = PG + (rowoff[bl] + k) * n;
-        for (int64_t r = 0; r < n; ++r) pg[r] = 0.0f;
-        float acc = gA[bl * E + src];  // identity term written by k_bwd_identity
-        acc = bwd_walk<MAX>(ori, src, bl, BL, E, n, 0, 0, a, w, g_ori, arg_ori, PK, CUT, acc, pg);
-        acc = bwd_walk<MAX>(inv, src, bl, BL, E, n, r_size, 1, a, w, g_inv, arg_inv, PK, CUT, acc, pg);
-        gA[bl * E + src] = acc;
+    extern __shared__ float pg_lds[];  // [BWDP_WAVES][n]
+    const int lane = fl_lane();
+    const int wid = fl_wave_id();
+    const int64_t q = (int64_t)blockIdx.x * BWDP_WAVES + wid;
+    if (q >= pairs || q >= rowoff[BL]) return;  // no block barrier follows
+    int64_t lo = 0, hi = BL;  // the row: rowoff[lo] <= q < rowoff[lo + 1]
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (rowoff[mid] <= q) lo = mid;
+        else hi = mid;
     }
+    const int64_t bl = lo, k = q - rowoff[bl];
+    if (k >= rowcnt[bl]) return;
+    const int64_t src = rowlist[bl * E + k];
+    const float a = A[bl * E + src];
+    float *pgl = pg_lds + (int64_t)wid * n;
+    for (int64_t r = lane; r < n; r += FL_WAVE) pgl[r] = 0.0f;
+    fl_wave_sync();
+    float acc = gA[bl * E + src];  // identity term written by k_bwd_identity
+    acc = bwd_side<MAX>(ori, src, bl, BL, E, n, 0, 0, a, w, g_ori, arg_ori, PK, CUT, acc, pgl);
+    acc = bwd_side<MAX>(inv, src, bl, BL, E, n, r_size, 1, a, w, g_inv, arg_inv, PK, CUT, acc, pgl);
+    fl_wave_sync();
+    float *pg = PG + q * n;
+    for (int64_t r = lane; r < n; r += FL_WAVE) pg[r] = pgl[r];
+    if (lane == 0) gA[bl * E + src] = acc;
 }
 
 // gw[row, r] for the relation columns r < 2*r_size: the pairs' partials in
@@ -1245,13 +1291,17 @@ int dense_backward_impl(const char *name, void *stream, const fl_side *ori, cons
     FL_LAUNCH("k_row_list", k_row_list, dim3((unsigned)BL), dim3(RL_NT), 0, st, ws.bm, E, rowlist, rowcnt);
     FL_LAUNCH("k_row_offsets", k_row_offsets, dim3(1), dim3(64), 0, st, rowcnt, BL, rowoff);
     if (pg_pairs > 0) {
+        // a wave per pair: the host's pair count bounds the grid (pairs past
+        // the row lists' total leave at once)
+        const unsigned nb = (unsigned)((pg_pairs + BWDP_WAVES - 1) / BWDP_WAVES);
+        const size_t plds = sizeof(float) * (size_t)(BWDP_WAVES * n);
         if (is_max)
-            FL_LAUNCH("k_bwd_rows_max", k_bwd_rows<true>, dim3(16, (unsigned)BL), dim3(BWD_NT), 0, st, *ori, *inv,
-                      A, w, grad_ori, grad_inv, arg_ori, arg_inv, BL, E, n, r_size, ws.pk, ws.cut, rowlist, rowcnt,
+            FL_LAUNCH("k_bwd_pairs_max", k_bwd_pairs<true>, dim3(nb), dim3(BWD_NT), plds, st, *ori, *inv, A, w,
+                      grad_ori, grad_inv, arg_ori, arg_inv, BL, E, n, r_size, ws.pk, ws.cut, rowlist, rowcnt,
                       rowoff, pg_pairs, grad_A, pg);
         else
-            FL_LAUNCH("k_bwd_rows", k_bwd_rows<false>, dim3(16, (unsigned)BL), dim3(BWD_NT), 0, st, *ori, *inv, A,
-                      w, grad_ori, grad_inv, (const int64_t *)nullptr, (const int64_t *)nullptr, BL, E, n, r_size,
+            FL_LAUNCH("k_bwd_pairs", k_bwd_pairs<false>, dim3(nb), dim3(BWD_NT), plds, st, *ori, *inv, A, w,
+                      grad_ori, grad_inv, (const int64_t *)nullptr, (const int64_t *)nullptr, BL, E, n, r_size,
                       ws.pk, ws.cut, rowlist, rowcnt, rowoff, pg_pairs, grad_A, pg);
         const size_t lds = sizeof(float) * (size_t)(GW_C * n);
         FL_LAUNCH("k_bwd_gw", k_bwd_gw, dim3((unsigned)BL), dim3(BWD_NT), lds, st, pg, rowcnt, rowoff, pg_pairs, n,

@@ -395,13 +395,6 @@ __device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, in
     return base;
 }
 
-// LDS ordering between the lanes of one wave (program order + fence).
-__device__ __forceinline__ void fl_wave_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // Admission order of c2 per (row, side): the relations with a positive
 // weight sorted by (weight desc, relation asc), ties in relation order =
 // group order (flashlog.cpp:12-89).  Workgroup per (row, side), bitonic sort

@@ -12,7 +12,7 @@ compared bit for bit with the CPU oracle of flashlog.cpp:216-278.
 
 The sequence is k_bwd_identity (+ k_bwd_identity_fin) -> k_col_count with a
 null out_ind -> k_frontier -> k_c2_hard -> k_row_list -> k_row_offsets ->
-k_bwd_rows -> k_bwd_gw, on the inputs of tests/test_gpu_dense.py's
+k_bwd_pairs -> k_bwd_gw, on the inputs of tests/test_gpu_dense.py's
 test_dense_sum_backward.  An earlier k_col_count stored the identity output
 without testing out_ind; the replay of that form stores through the null
 pointer, which is what faulted, and the guarded form touches nothing out of
@@ -304,51 +304,88 @@ def group_take(wv, th, cut, start, count):
     return 0
 
 
-def bwd_walk(s, src, bl, BL, E, n, off, d, a, w, grad, PKt, CUT, acc, PG, pgbase):
+def bwd_side(s, src, bl, BL, E, n, off, d, a, w, grad, PKt, CUT, acc, pgl):
+    """One side of a pair, lane by lane as the wave computes it: windows of
+    64 groups, the inclusive take prefix, each item's group by the binary
+    search over the lanes' prefixes, then the ordered additions."""
     at = (d * E + src) * BL + bl
     th = PKt[at]
     cut = int(CUT[at]) if th > 0 else 0
     g0, g1 = int(s.row_group_ptr[src]), int(s.row_group_ptr[src + 1])
-    for g in range(g0, g1):
-        rel = int(s.group_rel[g])
-        wv = w[bl * n + off + rel]
-        start = int(s.group_start[g])
-        take = group_take(wv, th, cut, start, int(s.group_count[g]))
-        gs = F32(0)
-        for b in range(start, start + take, 8):
-            m, go = [None] * 8, [None] * 8
-            for u in range(8):
-                if b + u < start + take:
-                    m[u] = s.mask[b + u]
-                    go[u] = grad[bl * E + int(s.col_ind[b + u])]
-            for u in range(8):
-                if b + u >= start + take or m[u] == 0 or go[u] == 0:
+    for gb in range(g0, g1, WAVE):
+        rel, start, take, wv = [0] * WAVE, [0] * WAVE, [0] * WAVE, [F32(0)] * WAVE
+        for lane in range(WAVE):
+            g = gb + lane
+            if g < g1:
+                rel[lane] = int(s.group_rel[g])
+                wv[lane] = w[bl * n + off + rel[lane]]
+                start[lane] = int(s.group_start[g])
+                take[lane] = group_take(wv[lane], th, cut, start[lane], int(s.group_count[g]))
+        incl = [int(x) for x in np.cumsum(take)]
+        total = incl[WAVE - 1]
+        first = [start[j] - (incl[j] - take[j]) for j in range(WAVE)]
+        gs = [F32(0)] * WAVE
+        for q0 in range(0, total, WAVE):
+            t1, t2, grp, contrib = [None] * WAVE, [None] * WAVE, [0] * WAVE, [False] * WAVE
+            for lane in range(WAVE):
+                k = q0 + lane
+                j = 0
+                step = WAVE // 2
+                while step > 0:
+                    if incl[j + step - 1] <= k:
+                        j += step
+                    step //= 2
+                if k >= total:
                     continue
-                acc = F32(acc + F32(F32(go[u] * wv) * m[u]))
-                gs = F32(gs + F32(F32(go[u] * a) * m[u]))
-        if take > 0:
-            PG[pgbase + off + rel] = gs
+                assert 0 <= j < WAVE and incl[j] - take[j] <= k < incl[j]
+                p = first[j] + k
+                m = s.mask[p]
+                dst = int(s.col_ind[p])
+                go = grad[bl * E + dst] if m != 0 else F32(0)
+                grp[lane] = j
+                contrib[lane] = m != 0 and go != 0
+                t1[lane] = F32(F32(go * wv[j]) * m)
+                t2[lane] = F32(F32(go * a) * m)
+            for lane in range(WAVE):
+                if contrib[lane]:
+                    acc = F32(acc + t1[lane])
+                    gs[grp[lane]] = F32(gs[grp[lane]] + t2[lane])
+        for lane in range(WAVE):
+            if take[lane] > 0:
+                pgl[off + rel[lane]] = gs[lane]
     return acc
 
 
-def k_bwd_rows(ori, inv, A, w, g_ori, g_inv, BL, E, n, r_size, PKt, CUT, rowlist, rowcnt, rowoff, pairs,
-               gA, PG):
-    for bl in range(BL):
-        cnt = int(rowcnt[bl])
-        # thread (x, t) of row bl's 16 workgroups takes k = x*256 + t, then k += 16*256:
-        # together they visit k = 0, 1, ..., cnt-1 once each
-        for k in range(cnt):
-            if int(rowoff[bl]) + k >= pairs:
-                break
-            src = int(rowlist[bl * E + k])
-            a = A[bl * E + src]
-            pgbase = (int(rowoff[bl]) + k) * n
-            for r in range(n):
-                PG[pgbase + r] = 0.0
-            acc = gA[bl * E + src]
-            acc = bwd_walk(ori, src, bl, BL, E, n, 0, 0, a, w, g_ori, PKt, CUT, acc, PG, pgbase)
-            acc = bwd_walk(inv, src, bl, BL, E, n, r_size, 1, a, w, g_inv, PKt, CUT, acc, PG, pgbase)
-            gA[bl * E + src] = acc
+BWDP_WAVES = BWD_NT // WAVE
+
+
+def k_bwd_pairs(ori, inv, A, w, g_ori, g_inv, BL, E, n, r_size, PKt, CUT, rowlist, rowcnt, rowoff, pairs,
+                gA, PG):
+    nb = (pairs + BWDP_WAVES - 1) // BWDP_WAVES
+    for q in range(nb * BWDP_WAVES):  # wave q of the grid
+        if q >= pairs or q >= int(rowoff[BL]):
+            continue
+        lo, hi = 0, BL
+        while hi - lo > 1:
+            mid = (lo + hi) >> 1
+            if int(rowoff[mid]) <= q:
+                lo = mid
+            else:
+                hi = mid
+        bl, k = lo, q - int(rowoff[lo])
+        if k >= int(rowcnt[bl]):
+            continue
+        src = int(rowlist[bl * E + k])
+        a = A[bl * E + src]
+        pgl = Buf("pair relation row (LDS)", n, F32)
+        for r in range(n):
+            pgl[r] = F32(0)
+        acc = gA[bl * E + src]
+        acc = bwd_side(ori, src, bl, BL, E, n, 0, 0, a, w, g_ori, PKt, CUT, acc, pgl)
+        acc = bwd_side(inv, src, bl, BL, E, n, r_size, 1, a, w, g_inv, PKt, CUT, acc, pgl)
+        for r in range(n):
+            PG[q * n + r] = pgl[r]
+        gA[bl * E + src] = acc
 
 
 def k_bwd_gw(PG, rowcnt, rowoff, pairs, n, nrel, gw, BL):
@@ -407,7 +444,7 @@ def replay(A, w, g, csr, masks, R, wot_i, K, guard_out_ind=True):
     k_row_list(BM, BL, E, rowlist, rowcnt)
     k_row_offsets(rowcnt, BL, rowoff)
     if pairs > 0:
-        k_bwd_rows(ori, inv, Ab, wb, go, gv, BL, E, n, R, PKt, CUT, rowlist, rowcnt, rowoff, pairs, gA, PG)
+        k_bwd_pairs(ori, inv, Ab, wb, go, gv, BL, E, n, R, PKt, CUT, rowlist, rowcnt, rowoff, pairs, gA, PG)
         k_bwd_gw(PG, rowcnt, rowoff, pairs, n, 2 * R, gw, BL)
     return gA.a.reshape(BL, E), gw.a.reshape(BL, n), gA.init.all() and gw.init.all()
 
