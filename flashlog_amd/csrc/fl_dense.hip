@@ -404,19 +404,6 @@ __device__ __forceinline__ uint64_t max_key(float v, int pos) {
     return ((uint64_t)__float_as_uint(v) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)pos);
 }
 
-__device__ __forceinline__ uint64_t walk_slots_max(const fl_side &s, int64_t s0, int64_t s1, int64_t bl,
-                                                   int64_t BL, int64_t E, int64_t n, int64_t off, int dir,
-                                                   const float *__restrict__ w, const uint32_t *__restrict__ BM,
-                                                   const float2 *__restrict__ PK,
-                                                   const int32_t *__restrict__ CUT) {
-    uint64_t best = 0;
-    walk_kept(s, s0, s1, bl, BL, E, n, off, dir, w, BM, PK, CUT, [&](int pos, float prod) {
-        const uint64_t k = max_key(prod, pos);
-        best = k > best ? k : best;
-    });
-    return best;
-}
-
 constexpr int PULL_NT = 256;
 constexpr int HEAVY_BL = 64;
 constexpr int HEAVY_TASKS = FL_SUP * HEAVY_BL;  // (segment, row) tasks of one heavy block
@@ -658,63 +645,177 @@ __device__ __forceinline__ void max_unpack(uint64_t best, float *out, int64_t *a
     *arg = best == 0 ? (int64_t)-1 : (int64_t)(int32_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
 }
 
-// Light tiles: thread per (destination, row), as k_pull's light part.
-__global__ __launch_bounds__(PULL_NT) void k_pull_max(
-    fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n, int64_t r_size, int TD,
-    int64_t ntiles, int64_t nlight, const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
-    const int32_t *__restrict__ CUT, float *__restrict__ out_ori, float *__restrict__ out_inv,
-    int64_t *__restrict__ arg_ori, int64_t *__restrict__ arg_inv) {
-    extern __shared__ uint64_t ktile[];  // [2][BL][TD]
-    const int64_t lb = blockIdx.x;
-    const int64_t per = nlight / 8;
-    const int64_t tid = (lb % 8) * per + lb / 8;
-    if (tid >= ntiles) return;
-    const int64_t d0 = tid * TD;
-    const int64_t ntask = (int64_t)TD * BL;
-    for (int64_t q = threadIdx.x; q < ntask; q += PULL_NT) {
-        const int64_t dl = q / BL, bl = q - dl * BL;
-        const int64_t dst = d0 + dl;
-        uint64_t best[2] = {0, 0};
-        if (dst < E) {
+// The kept products of nslot slots of one side, reduced into LDS cells:
+// slot_of(k, &sl, &c) names the k-th slot and its cell row (its destination
+// within the tile, or its segment within the chunk).  Task (slot, 32-row
+// word): the slot's source and row word, its position and mask, then one
+// key per row of the word where the source is active, folded into cell[row]
+// with a 64-bit LDS max (the max is order-free, so every order gives the
+// same cells).
+template <typename SlotOf>
+__device__ __forceinline__ void max_slots(const fl_side &s, int64_t nslot, int dir, int64_t BL, int64_t E,
+                                          int64_t n, int64_t off, const float *__restrict__ w,
+                                          const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
+                                          const int32_t *__restrict__ CUT, uint64_t *cells, SlotOf &&slot_of) {
+    const int64_t nw = (BL + 31) / 32;
+    const int64_t plane = (int64_t)dir * E * BL;
+    const int64_t ntask = nslot * nw;
+    for (int64_t t = threadIdx.x; t < ntask; t += PULL_NT) {
+        const int64_t k = t / nw, wi = t - k * nw;
+        int32_t sl;
+        int c;
+        slot_of(k, &sl, &c);
+        const int32_t src = s.pull_src[sl];
+        uint32_t bits = BM[wi * E + src];
+        if (!bits) continue;
+        const int32_t pos = s.pull_pos[sl];
+        const float m = s.mask[pos];
+        if (m == 0.0f) continue;
+        const int rel = s.pull_rel[sl];
+        uint64_t *crow = cells + (int64_t)c * BL;
+        const float *wc = w + off + rel;
+        const int64_t at0 = plane + (int64_t)src * BL;
+        // the word's active rows 8 at a time: their weights and records
+        // requested together, then the tests
+        while (bits) {
+            int64_t bl[8];
+            float wv[8];
+            float2 rc[8];
 #pragma unroll
-            for (int dir = 0; dir < 2; ++dir) {
-                const fl_side &s = dir ? inv : ori;
-                const int64_t s0 = s.pull_ptr[dst], s1 = s.pull_ptr[dst + 1];
-                if (s1 - s0 > FL_SEG) continue;  // heavy: written by k_heavy_max
-                best[dir] = walk_slots_max(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT);
+            for (int j = 0; j < 8; ++j) {
+                bl[j] = -1;
+                wv[j] = 0.0f;
+                rc[j] = make_float2(0.0f, 0.0f);
+                if (bits) {
+                    bl[j] = wi * 32 + __ffs(bits) - 1;
+                    bits &= bits - 1;
+                    wv[j] = wc[bl[j] * n];
+                    rc[j] = PK[at0 + bl[j]];
+                }
             }
-        }
-        ktile[(0 * BL + bl) * TD + dl] = best[0];
-        ktile[(1 * BL + bl) * TD + dl] = best[1];
-    }
-    __syncthreads();
-    for (int64_t i = threadIdx.x; i < ntask; i += PULL_NT) {
-        const int64_t bl = i / TD, dl = i - bl * TD;
-        const int64_t dst = d0 + dl;
-        if (dst < E) {
-            max_unpack(ktile[(0 * BL + bl) * TD + dl], &out_ori[bl * E + dst], &arg_ori[bl * E + dst]);
-            max_unpack(ktile[(1 * BL + bl) * TD + dl], &out_inv[bl * E + dst], &arg_inv[bl * E + dst]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (bl[j] < 0 || !(wv[j] > 0.0f)) continue;
+                bool kept = wv[j] > rc[j].y;
+                if (!kept && wv[j] == rc[j].y) kept = pos < CUT[at0 + bl[j]];
+                if (kept)
+                    atomicMax((unsigned long long *)&crow[bl[j]],
+                              (unsigned long long)max_key(fl_mul(fl_mul(rc[j].x, wv[j]), m), pos));
+            }
         }
     }
 }
 
-// Heavy destinations, step 1: thread per (segment, row), the segment's best key.
+// Light tiles of the max: workgroup per tile of td <= MAX_TD destinations (dealt
+// to XCDs in contiguous ranges), the kept products of the tile's light
+// slots (destinations of in-degree <= FL_SEG; the slots of each listed
+// through an LDS prefix of their counts) reduced per (destination, row) in
+// LDS (max_slots), then the tile written coalesced.  Heavy destinations get
+// 0 / -1 here and their values from k_heavy_max.
+constexpr int MAX_TD = 16;
+
+__global__ __launch_bounds__(PULL_NT) void k_pull_max(
+    fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n, int64_t r_size,
+    int td, int64_t ntiles, const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
+    const int32_t *__restrict__ CUT, float *__restrict__ out_ori, float *__restrict__ out_inv,
+    int64_t *__restrict__ arg_ori, int64_t *__restrict__ arg_inv) {
+    extern __shared__ uint64_t ktile[];  // [2][td][BL]
+    __shared__ int32_t first[2][MAX_TD], pre[2][MAX_TD + 1];
+    const int64_t tid = fl_xcd_contig(blockIdx.x, gridDim.x);
+    if (tid >= ntiles) return;
+    const int64_t d0 = tid * td;
+    const int nd = (int)(E - d0 < td ? E - d0 : td);
+    for (int64_t i = threadIdx.x; i < 2 * td * BL; i += PULL_NT) ktile[i] = 0;
+    if (threadIdx.x < 2 * FL_WAVE) {
+        // wave 0: ORI, wave 1: INV; lane j < nd: destination j's light slots
+        const int dir = threadIdx.x / FL_WAVE, j = fl_lane();
+        const fl_side &s = dir ? inv : ori;
+        int32_t c = 0;
+        if (j < nd) {
+            const int64_t p0 = s.pull_ptr[d0 + j], p1 = s.pull_ptr[d0 + j + 1];
+            first[dir][j] = (int32_t)p0;
+            c = p1 - p0 <= FL_SEG ? (int32_t)(p1 - p0) : 0;
+        }
+        const int32_t incl = fl_wave_incl_scan_i32(c);
+        if (j < nd) pre[dir][j + 1] = incl;
+        if (j == 0) pre[dir][0] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int dir = 0; dir < 2; ++dir) {
+        const fl_side &s = dir ? inv : ori;
+        const int32_t *pp = pre[dir], *fs = first[dir];
+        max_slots(s, pp[nd], dir, BL, E, n, dir ? r_size : 0, w, BM, PK, CUT, ktile + dir * td * BL,
+                  [&](int64_t k, int32_t *sl, int *c) {
+                      int lo = 0, hi = nd;  // the destination: pp[lo] <= k < pp[lo + 1]
+                      while (hi - lo > 1) {
+                          const int mid = (lo + hi) >> 1;
+                          if (pp[mid] <= k) lo = mid;
+                          else hi = mid;
+                      }
+                      *sl = fs[lo] + (int32_t)(k - pp[lo]);
+                      *c = lo;
+                  });
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < (int64_t)td * BL; i += PULL_NT) {
+        const int64_t bl = i / td, dl = i - bl * td;
+        if (dl < nd) {
+            const int64_t at = bl * E + d0 + dl;
+            max_unpack(ktile[dl * BL + bl], &out_ori[at], &arg_ori[at]);
+            max_unpack(ktile[(td + dl) * BL + bl], &out_inv[at], &arg_inv[at]);
+        }
+    }
+}
+
+// Heavy destinations, step 1: workgroup per chunk of SEGS_PER_WG segments
+// of one side, each segment's best key per row (max_slots over the
+// segments' slots -- segment j holds [seg_start, seg_start + FL_SEG) clipped
+// to its destination's end -- cell = segment within the chunk), stored to
+// sb[segment][row].
+constexpr int SEGS_PER_WG = 8;
+
 __global__ __launch_bounds__(PULL_NT) void k_seg_max(fl_side ori, fl_side inv, const float *__restrict__ w,
                                                      int64_t BL, int64_t E, int64_t n, int64_t r_size,
                                                      const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
                                                      const int32_t *__restrict__ CUT, uint64_t *__restrict__ sb_ori,
                                                      uint64_t *__restrict__ sb_inv) {
-    const int64_t q = (int64_t)blockIdx.x * PULL_NT + threadIdx.x;
-    const int64_t nq_ori = ori.nseg * BL;
-    if (q >= nq_ori + inv.nseg * BL) return;
-    const int dir = q >= nq_ori;
-    const int64_t qq = dir ? q - nq_ori : q;
-    const int64_t seg = qq / BL, bl = qq - seg * BL;
+    extern __shared__ uint64_t cells[];  // [SEGS_PER_WG][BL]
+    __shared__ int32_t first[SEGS_PER_WG], pre[SEGS_PER_WG + 1];
+    const int64_t nwg_ori = (ori.nseg + SEGS_PER_WG - 1) / SEGS_PER_WG;
+    const int dir = (int64_t)blockIdx.x >= nwg_ori;
     const fl_side &s = dir ? inv : ori;
-    const int64_t s0 = s.seg_start[seg];
-    const int64_t end = s.pull_ptr[(int64_t)s.seg_dst[seg] + 1];
-    const int64_t s1 = (s0 + FL_SEG < end) ? s0 + FL_SEG : end;
-    (dir ? sb_inv : sb_ori)[qq] = walk_slots_max(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT);
+    const int64_t seg0 = ((int64_t)blockIdx.x - (dir ? nwg_ori : 0)) * SEGS_PER_WG;
+    if (seg0 >= s.nseg) return;
+    const int ns = (int)(s.nseg - seg0 < SEGS_PER_WG ? s.nseg - seg0 : SEGS_PER_WG);
+    for (int64_t i = threadIdx.x; i < (int64_t)SEGS_PER_WG * BL; i += PULL_NT) cells[i] = 0;
+    if (threadIdx.x < FL_WAVE) {
+        const int j = fl_lane();
+        int32_t c = 0;
+        if (j < ns) {
+            const int64_t a = s.seg_start[seg0 + j];
+            const int64_t end = s.pull_ptr[(int64_t)s.seg_dst[seg0 + j] + 1];
+            first[j] = (int32_t)a;
+            c = (int32_t)(a + FL_SEG < end ? FL_SEG : end - a);
+        }
+        const int32_t incl = fl_wave_incl_scan_i32(c);
+        if (j < ns) pre[j + 1] = incl;
+        if (j == 0) pre[0] = 0;
+    }
+    __syncthreads();
+    max_slots(s, pre[ns], dir, BL, E, n, dir ? r_size : 0, w, BM, PK, CUT, cells, [&](int64_t k, int32_t *sl, int *c) {
+        int lo = 0, hi = ns;  // the segment: pre[lo] <= k < pre[lo + 1]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (pre[mid] <= k) lo = mid;
+            else hi = mid;
+        }
+        *sl = first[lo] + (int32_t)(k - pre[lo]);
+        *c = lo;
+    });
+    __syncthreads();
+    uint64_t *sb = (dir ? sb_inv : sb_ori) + seg0 * BL;
+    for (int64_t i = threadIdx.x; i < (int64_t)ns * BL; i += PULL_NT) sb[i] = cells[i];
 }
 
 // Heavy destinations, step 2: thread per (supersegment, row): the maximum of
@@ -1351,20 +1452,21 @@ int fl_dense_max_forward(void *stream, const fl_side *ori, const fl_side *inv, c
     if (do_topk)
         FL_LAUNCH("k_c2_hard", k_c2_hard, dim3(1024), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K,
                   ws.hard_count, ws.hard, ws.pk, ws.cut);
-    int TD = (int)(512 / BL);
-    if (TD < 1) TD = 1;
-    if (TD > 64) TD = 64;
-    const int64_t ntiles = (E + TD - 1) / TD;
-    const int64_t nlight = ((ntiles + 7) / 8) * 8;
-    const size_t lds = sizeof(uint64_t) * 2 * (size_t)BL * (size_t)TD;
-    FL_LAUNCH("k_pull_max", k_pull_max, dim3((unsigned)nlight), dim3(PULL_NT), lds, st, *ori, *inv, w, BL, E, n,
-              r_size, TD, ntiles, nlight, ws.bm, ws.pk, ws.cut, out_ori, out_inv, arg_ori, arg_inv);
+    // key cells of a tile: 2 * td * BL, at most 64 KiB of LDS (BL <= 1024)
+    int td = (int)(4096 / BL);
+    if (td < 1) td = 1;
+    if (td > MAX_TD) td = MAX_TD;
+    const int64_t ntiles = (E + td - 1) / td;
+    const size_t lds = sizeof(uint64_t) * 2 * (size_t)BL * (size_t)td;
+    FL_LAUNCH("k_pull_max", k_pull_max, dim3((unsigned)ntiles), dim3(PULL_NT), lds, st, *ori, *inv, w, BL, E, n,
+              r_size, td, ntiles, ws.bm, ws.pk, ws.cut, out_ori, out_inv, arg_ori, arg_inv);
     // segment maxima reuse the heavy-list area (nseg*BL*FL_SEG floats >= nseg*BL keys)
     uint64_t *sb_ori = (uint64_t *)ws.list_ori, *sb_inv = (uint64_t *)ws.list_inv;
     const int64_t nq_seg = (ori->nseg + inv->nseg) * BL;
     if (nq_seg > 0) {
-        FL_LAUNCH("k_seg_max", k_seg_max, dim3((unsigned)((nq_seg + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0, st,
-                  *ori, *inv, w, BL, E, n, r_size, ws.bm, ws.pk, ws.cut, sb_ori, sb_inv);
+        const int64_t nwg = (ori->nseg + SEGS_PER_WG - 1) / SEGS_PER_WG + (inv->nseg + SEGS_PER_WG - 1) / SEGS_PER_WG;
+        FL_LAUNCH("k_seg_max", k_seg_max, dim3((unsigned)nwg), dim3(PULL_NT), sizeof(uint64_t) * SEGS_PER_WG * BL,
+                  st, *ori, *inv, w, BL, E, n, r_size, ws.bm, ws.pk, ws.cut, sb_ori, sb_inv);
         const int64_t nq_sup = (ori->nsup + inv->nsup) * BL;
         if (nq_sup > 0)
             FL_LAUNCH("k_sup_max", k_sup_max, dim3((unsigned)((nq_sup + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0,
