@@ -12,11 +12,11 @@
 //                    from a wave-level radix select over the source's
 //                    relation groups.
 //   k_pull           the propagation: one thread per (light destination,
-//                    row) walks the destination's incoming slots in ascending
-//                    CSR position and adds (a*w)*m in a register -- the order
-//                    in which the reference's CPU loop adds into out[row,
-//                    dst] -- with tiles of destinations staged in LDS and
-//                    written coalesced; destinations with more than FL_SEG
+//                    row) walks the destination's incoming slots (staged in
+//                    LDS) in ascending CSR position and adds (a*w)*m in a
+//                    register -- the order in which the reference's CPU loop
+//                    adds into out[row, dst] -- with tiles of destinations
+//                    written coalesced from LDS; destinations with more than FL_SEG
 //                    incoming slots are cut into FL_SEG-slot segments whose
 //                    kept products are listed, in slot order, per row.
 //   k_heavy_offsets  per heavy destination and row, where each segment's list
@@ -325,77 +325,8 @@ __global__ __launch_bounds__(C2_NT) void k_c2_hard(fl_side ori, fl_side inv, con
     }
 }
 
-// Products of the kept edges into one destination for one row, over slots
-// [s0, s1) in order.  Light walks accumulate; heavy walks append to `list`.
-// Per batch of WALK_U slots: one round of slot loads (position, source,
-// relation); one round of (mask, bitmask word, weight, record {a, theta});
-// the tie cut only on an exact tie; then the in-order accumulation.
+// Slots whose weight and record loads are requested together in a walk.
 constexpr int WALK_U = 8;
-
-// Calls emit(position, product) for every kept slot of [s0, s1) in order.
-template <typename Emit>
-__device__ __forceinline__ void walk_kept(const fl_side &s, int64_t s0, int64_t s1, int64_t bl, int64_t BL,
-                                          int64_t E, int64_t n, int64_t off, int dir, const float *__restrict__ w,
-                                          const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
-                                          const int32_t *__restrict__ CUT, Emit &&emit) {
-    const uint32_t *bmw = BM + (bl >> 5) * E;
-    const uint32_t bit = 1u << (bl & 31);
-    const int64_t plane = (int64_t)dir * E * BL + bl;
-    const float *wr = w + bl * n + off;
-    for (int64_t base = s0; base < s1; base += WALK_U) {
-        int pos[WALK_U], src[WALK_U], rel[WALK_U];
-#pragma unroll
-        for (int u = 0; u < WALK_U; ++u) {
-            const int64_t sl = base + u;
-            if (sl < s1) { pos[u] = s.pull_pos[sl]; src[u] = s.pull_src[sl]; rel[u] = s.pull_rel[sl]; }
-            else { pos[u] = 0; src[u] = 0; rel[u] = 0; }
-        }
-        float m[WALK_U], wv[WALK_U];
-        uint32_t bw[WALK_U];
-        float2 rc[WALK_U];
-        // the sources' row bits first: a slot's mask, weight and record are
-        // read only where its source is active in this row (a small share of
-        // the in-edges under the c1 budget)
-#pragma unroll
-        for (int u = 0; u < WALK_U; ++u) bw[u] = base + u < s1 ? bmw[src[u]] : 0u;
-#pragma unroll
-        for (int u = 0; u < WALK_U; ++u) {
-            m[u] = 0.0f;
-            wv[u] = 0.0f;
-            rc[u] = make_float2(0.0f, 0.0f);
-            if (bw[u] & bit) {
-                m[u] = s.mask[pos[u]];
-                wv[u] = wr[rel[u]];
-                rc[u] = PK[plane + (int64_t)src[u] * BL];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < WALK_U; ++u) {
-            if (!(bw[u] & bit) || m[u] == 0.0f || !(wv[u] > 0.0f)) continue;
-            const float th = rc[u].y;
-            bool kept = wv[u] > th;
-            if (!kept && wv[u] == th) kept = pos[u] < CUT[plane + (int64_t)src[u] * BL];
-            if (kept) emit(pos[u], fl_mul(fl_mul(rc[u].x, wv[u]), m[u]));
-        }
-    }
-}
-
-// Sum: add the kept products in slot order (LIST: append them to `list`).
-template <bool LIST>
-__device__ __forceinline__ float walk_slots(const fl_side &s, int64_t s0, int64_t s1, int64_t bl,
-                                            int64_t BL, int64_t E, int64_t n, int64_t off, int dir,
-                                            const float *__restrict__ w, const uint32_t *__restrict__ BM,
-                                            const float2 *__restrict__ PK, const int32_t *__restrict__ CUT,
-                                            float *__restrict__ list, int *count) {
-    float acc = 0.0f;
-    int k = 0;
-    walk_kept(s, s0, s1, bl, BL, E, n, off, dir, w, BM, PK, CUT, [&](int, float prod) {
-        if (LIST) list[k++] = prod;
-        else acc = fl_add(acc, prod);
-    });
-    if (LIST) *count = k;
-    return acc;
-}
 
 // Max: the largest packed key (value bits << 32 | ~position) of the kept
 // products, 0 when none (flashlog.cu:104-121): larger value bits win, equal
@@ -405,14 +336,22 @@ __device__ __forceinline__ uint64_t max_key(float v, int pos) {
 }
 
 constexpr int PULL_NT = 256;
+constexpr int MAX_TD = 16;  // destinations per light tile, at most
 constexpr int HEAVY_BL = 64;
+
+// Dynamic LDS of a light k_pull tile: the output tile (2 x BL x TD floats)
+// and the staged slots of both sides.
+inline size_t pull_lds_bytes(int64_t BL, int TD) {
+    const int64_t nw = (BL + 31) / 32;
+    return sizeof(float) * 2 * (size_t)BL * (size_t)TD + (size_t)2 * TD * FL_SEG * (16 + 4 * (size_t)nw);
+}
 constexpr int HEAVY_TASKS = FL_SUP * HEAVY_BL;  // (segment, row) tasks of one heavy block
 
-// The propagation kernel.  Workgroups [nheavy_wg, +nlight) take tiles of TD light
-// destinations (in-degree <= FL_SEG): one thread per (destination, row)
-// walks the destination's slots in ascending CSR position and adds in a
-// register -- the reference CPU loop's order -- then the tile is written
-// from LDS, coalesced.  Light tiles are dealt to XCDs in contiguous ranges
+// The propagation kernel.  Workgroups [nheavy_wg, +nlight) take tiles of TD
+// destinations: the light ones' slots (in-degree <= FL_SEG) are staged in
+// LDS, one thread per (destination, row) walks the destination's slots in
+// ascending CSR position and adds in a register -- the reference CPU loop's
+// order -- then the tile is written from LDS, coalesced.  Light tiles are dealt to XCDs in contiguous ranges
 // (workgroup b runs on XCD b % 8), so each output line is written from one
 // L2.  Workgroups [0, nheavy_wg) -- the longer ones, dispatched first --
 // take (supersegment, block of 64 rows) of heavy
@@ -427,39 +366,110 @@ __global__ __launch_bounds__(PULL_NT) void k_pull(
     float *__restrict__ list_ori, float *__restrict__ list_inv, int32_t *__restrict__ cnt_ori,
     int32_t *__restrict__ cnt_inv, int32_t *__restrict__ loff_ori, int32_t *__restrict__ loff_inv,
     int32_t *__restrict__ stot_ori, int32_t *__restrict__ stot_inv) {
-    extern __shared__ float tile[];  // light: [2][BL][TD]
+    extern __shared__ __align__(16) unsigned char pull_lds[];
     __shared__ int cnt_lds[FL_SUP][HEAVY_BL];
+    __shared__ int32_t lfirst[2][MAX_TD], lpre[2][MAX_TD + 1];
     if ((int64_t)blockIdx.x >= nheavy_wg) {
+        // light tile: the tile's light slots (destinations of in-degree <=
+        // FL_SEG, listed through an LDS prefix of their counts) staged in
+        // LDS -- source, position, relation, mask and the source's row words
+        // -- then thread per (destination, row) walks its destination's
+        // slots from LDS in CSR position order, reading a slot's weight and
+        // record only where the source is active in the row
         const int64_t lb = (int64_t)blockIdx.x - nheavy_wg;  // nheavy_wg is a multiple of 8
         const int64_t per = nlight / 8;
         const int64_t tid = (lb % 8) * per + lb / 8;
         if (tid >= ntiles) return;
         const int64_t d0 = tid * TD;
-        const int64_t ntask = (int64_t)TD * BL;
-        for (int64_t q = threadIdx.x; q < ntask; q += PULL_NT) {
-            const int64_t dl = q / BL, bl = q - dl * BL;
-            const int64_t dst = d0 + dl;
-            float acc[2] = {0.0f, 0.0f};
-            if (dst < E) {
-#pragma unroll
-                for (int dir = 0; dir < 2; ++dir) {
-                    const fl_side &s = dir ? inv : ori;
-                    const int64_t s0 = s.pull_ptr[dst], s1 = s.pull_ptr[dst + 1];
-                    if (s1 - s0 > FL_SEG) continue;  // heavy: written by k_fold_heavy
-                    acc[dir] = walk_slots<false>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT,
-                                                 nullptr, nullptr);
-                }
+        const int nd = (int)(E - d0 < TD ? E - d0 : TD);
+        const int64_t nw = (BL + 31) / 32;
+        const int S = TD * FL_SEG;  // light slots of a side in one tile, at most
+        float *tile = reinterpret_cast<float *>(pull_lds);  // [2][BL][TD]
+        int32_t *st_src = reinterpret_cast<int32_t *>(tile + 2 * BL * TD);  // [2][S]
+        int32_t *st_pos = st_src + 2 * S;
+        int32_t *st_rel = st_pos + 2 * S;
+        float *st_m = reinterpret_cast<float *>(st_rel + 2 * S);
+        uint32_t *st_w = reinterpret_cast<uint32_t *>(st_m + 2 * S);  // [2][S][nw]
+        if (threadIdx.x < 2 * FL_WAVE) {
+            const int dir = threadIdx.x / FL_WAVE, j = fl_lane();
+            const fl_side &s = dir ? inv : ori;
+            int32_t c = 0;
+            if (j < nd) {
+                const int64_t p0 = s.pull_ptr[d0 + j], p1 = s.pull_ptr[d0 + j + 1];
+                lfirst[dir][j] = (int32_t)p0;
+                c = p1 - p0 <= FL_SEG ? (int32_t)(p1 - p0) : 0;
             }
-            tile[(0 * BL + bl) * TD + dl] = acc[0];
-            tile[(1 * BL + bl) * TD + dl] = acc[1];
+            const int32_t incl = fl_wave_incl_scan_i32(c);
+            if (j < nd) lpre[dir][j + 1] = incl;
+            if (j == 0) lpre[dir][0] = 0;
         }
         __syncthreads();
-        for (int64_t i = threadIdx.x; i < ntask; i += PULL_NT) {
+#pragma unroll
+        for (int dir = 0; dir < 2; ++dir) {
+            const fl_side &s = dir ? inv : ori;
+            const int32_t *pp = lpre[dir], *fs = lfirst[dir];
+            for (int k = threadIdx.x; k < pp[nd]; k += PULL_NT) {
+                int lo = 0, hi = nd;  // the destination: pp[lo] <= k < pp[lo + 1]
+                while (hi - lo > 1) {
+                    const int mid = (lo + hi) >> 1;
+                    if (pp[mid] <= k) lo = mid;
+                    else hi = mid;
+                }
+                const int64_t sl = fs[lo] + (k - pp[lo]);
+                const int32_t src = s.pull_src[sl], pos = s.pull_pos[sl];
+                const int at = dir * S + k;
+                st_src[at] = src;
+                st_pos[at] = pos;
+                st_rel[at] = s.pull_rel[sl];
+                st_m[at] = s.mask[pos];
+                for (int64_t wi = 0; wi < nw; ++wi) st_w[(int64_t)at * nw + wi] = BM[wi * E + src];
+            }
+        }
+        __syncthreads();
+        const int64_t ntask = (int64_t)nd * BL;
+        for (int64_t q = threadIdx.x; q < ntask; q += PULL_NT) {
+            const int64_t dl = q / BL, bl = q - dl * BL;
+            const int64_t wi = bl >> 5;
+            const uint32_t bit = 1u << (bl & 31);
+#pragma unroll
+            for (int dir = 0; dir < 2; ++dir) {
+                const int k0 = lpre[dir][dl], k1 = lpre[dir][dl + 1];
+                const float *wr = w + bl * n + (dir ? r_size : 0);
+                const int64_t plane = (int64_t)dir * E * BL + bl;
+                float acc = 0.0f;
+                for (int kb = k0; kb < k1; kb += WALK_U) {
+                    bool act[WALK_U];
+                    float wv[WALK_U];
+                    float2 rc[WALK_U];
+#pragma unroll
+                    for (int u = 0; u < WALK_U; ++u) {
+                        const int at = dir * S + kb + u;
+                        act[u] = kb + u < k1 && (st_w[(int64_t)at * nw + wi] & bit) && st_m[at] != 0.0f;
+                        wv[u] = 0.0f;
+                        rc[u] = make_float2(0.0f, 0.0f);
+                        if (act[u]) {
+                            wv[u] = wr[st_rel[at]];
+                            rc[u] = PK[plane + (int64_t)st_src[at] * BL];
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < WALK_U; ++u) {
+                        if (!act[u] || !(wv[u] > 0.0f)) continue;
+                        const int at = dir * S + kb + u;
+                        bool kept = wv[u] > rc[u].y;
+                        if (!kept && wv[u] == rc[u].y) kept = st_pos[at] < CUT[plane + (int64_t)st_src[at] * BL];
+                        if (kept) acc = fl_add(acc, fl_mul(fl_mul(rc[u].x, wv[u]), st_m[at]));
+                    }
+                }
+                tile[(dir * BL + bl) * TD + dl] = acc;
+            }
+        }
+        __syncthreads();
+        for (int64_t i = threadIdx.x; i < (int64_t)TD * BL; i += PULL_NT) {
             const int64_t bl = i / TD, dl = i - bl * TD;
-            const int64_t dst = d0 + dl;
-            if (dst < E) {
-                out_ori[bl * E + dst] = tile[(0 * BL + bl) * TD + dl];
-                out_inv[bl * E + dst] = tile[(1 * BL + bl) * TD + dl];
+            if (dl < nd) {
+                out_ori[bl * E + d0 + dl] = tile[(0 * BL + bl) * TD + dl];
+                out_inv[bl * E + d0 + dl] = tile[(1 * BL + bl) * TD + dl];
             }
         }
         return;
@@ -478,16 +488,70 @@ __global__ __launch_bounds__(PULL_NT) void k_pull(
     const int64_t segend = s.heavy_seg_ptr[h + 1];
     const int64_t dst = s.heavy_dst[h];
     const int64_t end = s.pull_ptr[dst + 1];
+    // the supersegment's slots (its segments tile [first, last) in order),
+    // staged in LDS with the row words of this block's 64 rows
+    const int64_t first = s.seg_start[seg0];
+    const int64_t last = first + (int64_t)FL_SUP * FL_SEG < end ? first + (int64_t)FL_SUP * FL_SEG : end;
+    const int nst = (int)(last - first);
+    const int64_t nw = (BL + 31) / 32;
+    const int64_t wi0 = blc * (HEAVY_BL / 32);
+    int32_t *st_src = reinterpret_cast<int32_t *>(pull_lds);  // [FL_SUP * FL_SEG]
+    int32_t *st_pos = st_src + FL_SUP * FL_SEG;
+    int32_t *st_rel = st_pos + FL_SUP * FL_SEG;
+    float *st_m = reinterpret_cast<float *>(st_rel + FL_SUP * FL_SEG);
+    uint32_t *st_w = reinterpret_cast<uint32_t *>(st_m + FL_SUP * FL_SEG);  // [slot][HEAVY_BL / 32]
+    for (int k = threadIdx.x; k < nst; k += PULL_NT) {
+        const int64_t sl = first + k;
+        const int32_t src = s.pull_src[sl], pos = s.pull_pos[sl];
+        st_src[k] = src;
+        st_pos[k] = pos;
+        st_rel[k] = s.pull_rel[sl];
+        st_m[k] = s.mask[pos];
+#pragma unroll
+        for (int j = 0; j < HEAVY_BL / 32; ++j)
+            st_w[k * (HEAVY_BL / 32) + j] = wi0 + j < nw ? BM[(wi0 + j) * E + src] : 0u;
+    }
+    __syncthreads();
+    const int64_t off = dir ? r_size : 0;
     for (int task = threadIdx.x; task < HEAVY_TASKS; task += PULL_NT) {
         const int sl = task / HEAVY_BL, bll = task % HEAVY_BL;
         const int64_t bl = blc * HEAVY_BL + bll;
         const int64_t seg = seg0 + sl;
         int k = 0;
         if (seg < segend && bl < BL) {
-            const int64_t s0 = s.seg_start[seg];
-            const int64_t s1 = (s0 + FL_SEG < end) ? s0 + FL_SEG : end;
+            // the segment's slots [k0, k1) of the staged range, in order;
+            // a slot's weight and record are read only where its source is
+            // active in the row
+            const int k0 = sl * FL_SEG, k1 = k0 + FL_SEG < nst ? k0 + FL_SEG : nst;
             float *list = (dir ? list_inv : list_ori) + (seg * BL + bl) * FL_SEG;
-            walk_slots<true>(s, s0, s1, bl, BL, E, n, dir ? r_size : 0, dir, w, BM, PK, CUT, list, &k);
+            const int wj = bll >> 5;
+            const uint32_t bit = 1u << (bll & 31);
+            const float *wr = w + bl * n + off;
+            const int64_t plane = (int64_t)dir * E * BL + bl;
+            for (int kb = k0; kb < k1; kb += WALK_U) {
+                bool act[WALK_U];
+                float wv[WALK_U];
+                float2 rc[WALK_U];
+#pragma unroll
+                for (int u = 0; u < WALK_U; ++u) {
+                    const int q = kb + u;
+                    act[u] = q < k1 && (st_w[q * (HEAVY_BL / 32) + wj] & bit) && st_m[q] != 0.0f;
+                    wv[u] = 0.0f;
+                    rc[u] = make_float2(0.0f, 0.0f);
+                    if (act[u]) {
+                        wv[u] = wr[st_rel[q]];
+                        rc[u] = PK[plane + (int64_t)st_src[q] * BL];
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < WALK_U; ++u) {
+                    if (!act[u] || !(wv[u] > 0.0f)) continue;
+                    const int q = kb + u;
+                    bool kept = wv[u] > rc[u].y;
+                    if (!kept && wv[u] == rc[u].y) kept = st_pos[q] < CUT[plane + (int64_t)st_src[q] * BL];
+                    if (kept) list[k++] = fl_mul(fl_mul(rc[u].x, wv[u]), st_m[q]);
+                }
+            }
             (dir ? cnt_inv : cnt_ori)[seg * BL + bl] = k;
         }
         cnt_lds[sl][bll] = k;
@@ -712,8 +776,6 @@ __device__ __forceinline__ void max_slots(const fl_side &s, int64_t nslot, int d
 // through an LDS prefix of their counts) reduced per (destination, row) in
 // LDS (max_slots), then the tile written coalesced.  Heavy destinations get
 // 0 / -1 here and their values from k_heavy_max.
-constexpr int MAX_TD = 16;
-
 __global__ __launch_bounds__(PULL_NT) void k_pull_max(
     fl_side ori, fl_side inv, const float *__restrict__ w, int64_t BL, int64_t E, int64_t n, int64_t r_size,
     int td, int64_t ntiles, const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
@@ -1307,15 +1369,20 @@ int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv, c
     if (do_topk)
         FL_LAUNCH("k_c2_hard", k_c2_hard, dim3(1024), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K,
                   ws.hard_count, ws.hard, ws.pk, ws.cut);
-    // light destinations: TD destinations per workgroup, TD*BL ~ 512 tasks
-    int TD = (int)(512 / BL);
-    if (TD < 1) TD = 1;
-    if (TD > 64) TD = 64;
+    // light destinations: TD <= MAX_TD destinations per workgroup, with the
+    // output tile and the staged slots (two sides of TD*FL_SEG slots, 16
+    // bytes and nw row words each) in at most 64 KiB of LDS
+    int TD = MAX_TD;
+    while (TD > 1 && pull_lds_bytes(BL, TD) > 65536) --TD;
     const int64_t ntiles = (E + TD - 1) / TD;
     const int64_t nlight = ((ntiles + 7) / 8) * 8;
     const int64_t nblc = (BL + HEAVY_BL - 1) / HEAVY_BL;
     const int64_t nheavy_wg = (((ori->nsup + inv->nsup) * nblc + 7) / 8) * 8;
-    const size_t lds = sizeof(float) * 2 * (size_t)BL * (size_t)TD;
+    // the heavy blocks stage FL_SUP * FL_SEG slots (16 bytes and two row
+    // words each) in the same area
+    size_t lds = pull_lds_bytes(BL, TD);
+    const size_t heavy_lds = (size_t)FL_SUP * FL_SEG * (16 + 4 * (HEAVY_BL / 32));
+    if (lds < heavy_lds) lds = heavy_lds;
     FL_LAUNCH("k_pull", k_pull, dim3((unsigned)(nlight + nheavy_wg)), dim3(PULL_NT), lds, st, *ori, *inv, w, BL,
               E, n, r_size, TD, ntiles, nlight, nheavy_wg, ws.bm, ws.pk, ws.cut, out_ori, out_inv, ws.list_ori,
               ws.list_inv,
