@@ -232,6 +232,32 @@ def copy_calibration(mb):
     print("copy calibration: 3 copies of %d MiB" % mb, file=sys.stderr, flush=True)
 
 
+FLUSH_MIB = 512
+
+
+def cache_flusher(mib=FLUSH_MIB):
+    """A callable that writes a `mib` MiB device buffer.  Run before each hop
+    of a timed pass it evicts the L2s and the 256 MB Infinity Cache: the
+    cold-cache condition of the roofline measurement (the hop then reads its
+    graph and state from HBM)."""
+    import torch
+    buf = torch.empty(mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+    return lambda: buf.fill_(0.0)
+
+
+def profile_pass(lib, kernels, steps, run):
+    """Per-launch ms of `kernels` over `steps` calls of run() (HIP events
+    around each launch inside the library)."""
+    import torch
+    lib.prof_enable(True)
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    prof = {k: lib.prof_read(k) for k in kernels}
+    lib.prof_enable(False)
+    return {k: (v[0] / v[1] if v[1] else 0.0) for k, v in prof.items()}
+
+
 def host_cpu():
     """CPU model and core counts of the host the baseline runs on."""
     model = "unknown"
@@ -354,9 +380,11 @@ def main():
     x0 = torch.zeros(B, L, E, dtype=torch.float32, device=dev)
     x0[torch.arange(B, device=dev), :, torch.from_numpy(src).to(dev)] = 1.0
 
-    def step(capture=None):
+    def step(capture=None, flush=None):
         x = x0
         for hop in range(T):
+            if flush is not None:
+                flush()
             if capture is not None:
                 capture.append((fk._dense_topc_state(x, c1 if cfg.use_topk else None), W[hop]))
             s_i, s_h, s_t = fk.dense_csr_sum_cuda(x, W[hop], csr, None, R, use_topk=cfg.use_topk,
@@ -385,14 +413,12 @@ def main():
         # per-kernel HIP-event timing inside the library
         kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull", "k_heavy_offsets",
                    "k_heavy_copy", "k_fold_heavy"]
-        _lib.prof_enable(True)
-        for _ in range(args.profile_steps):
-            step()
-        torch.cuda.synchronize()
-        prof = {k: _lib.prof_read(k) for k in kernels}
-        _lib.prof_enable(False)
-        per_launch = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in prof.items()}
+        per_launch = profile_pass(_lib, kernels, args.profile_steps, step)
         print("per-launch ms: " + json.dumps({k: round(v, 5) for k, v in per_launch.items()}),
+              file=sys.stderr, flush=True)
+        flush = cache_flusher()
+        cold = profile_pass(_lib, kernels, args.profile_steps, lambda: step(flush=flush))
+        print("per-launch ms, cold cache: " + json.dumps({k: round(v, 5) for k, v in cold.items()}),
               file=sys.stderr, flush=True)
 
         # algorithmic bytes of k_pull per hop, from the hop inputs of one step
@@ -401,9 +427,11 @@ def main():
         csr_np = [c.cpu().numpy() for c in csr]
         hop_bytes = [hop_pull_bytes(a.reshape(B * L, E).cpu().numpy(), w.reshape(B * L, n).cpu().numpy(),
                                     csr_np, R, K) for a, w in cap]
-    pull_ms = per_launch["k_pull"]
     bytes_per_launch = float(np.mean(hop_bytes))
+    pull_ms = cold["k_pull"]
     achieved = bytes_per_launch / (pull_ms * 1e-3) / 1e9 if pull_ms > 0 else 0.0
+    warm_ms = per_launch["k_pull"]
+    warm = bytes_per_launch / (warm_ms * 1e-3) / 1e9 if warm_ms > 0 else 0.0
 
     cpu = cpu_baseline(args, cfg, h, r, t, E, R, src, W.cpu().numpy()) if args.cpu_seconds > 0 else None
 
@@ -425,9 +453,12 @@ def main():
                    "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2},
         "topk_select_ms": {"c1_per_hop": per_launch["k_topc_rows"], "c2_per_hop": per_launch["k_c2_hard"]},
         "kernel_ms_per_launch": per_launch,
+        "kernel_ms_per_launch_cold": cold,
         "roofline": {"kernel": "k_pull", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None},
+                     "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None, "ms": pull_ms,
+                     "cache": "cold: %d MiB written before each hop" % FLUSH_MIB,
+                     "warm": {"achieved": warm, "frac": warm / HBM_PEAK_GBS, "ms": warm_ms}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
@@ -465,9 +496,11 @@ def main_c4(args):
     x0[torch.arange(B, device=dev), :, torch.from_numpy(src).to(dev)] = 1.0
     tgt_t = torch.from_numpy(tgt).to(dev)
 
-    def step(capture=None):
+    def step(capture=None, flush=None):
         x = x0
         for hop in range(T):
+            if flush is not None:
+                flush()
             if capture is not None:
                 capture.append((fk._dense_topc_state(x.detach(), c1), W[hop].detach()))
             s_i, s_h, s_t = fk.dense_csr_max(x, W[hop], csr, None, R, use_topk=True, topk_nodes=c1,
@@ -493,14 +526,12 @@ def main_c4(args):
     torch.cuda.synchronize()
     ms_step = e0.elapsed_time(e1) / args.steps
     print("timed %d mmDRUM steps: %.3f ms/step" % (args.steps, ms_step), file=sys.stderr, flush=True)
-    _lib.prof_enable(True)
-    for _ in range(max(args.profile_steps, 1)):
-        step()
-    torch.cuda.synchronize()
-    prof = {k: _lib.prof_read(k) for k in kernels}
-    _lib.prof_enable(False)
-    per_launch = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in prof.items()}
+    per_launch = profile_pass(_lib, kernels, max(args.profile_steps, 1), step)
     print("per-launch ms: " + json.dumps({k: round(v, 5) for k, v in per_launch.items()}), file=sys.stderr,
+          flush=True)
+    flush = cache_flusher()
+    cold = profile_pass(_lib, kernels, max(args.profile_steps, 1), lambda: step(flush=flush))
+    print("per-launch ms, cold cache: " + json.dumps({k: round(v, 5) for k, v in cold.items()}), file=sys.stderr,
           flush=True)
     cap = []
     step(capture=cap)
@@ -509,9 +540,12 @@ def main_c4(args):
     # outputs 24 B per (row, destination): two fp32 values and two int64 winning positions
     hop_bytes = [hop_pull_bytes(a.reshape(B * L, E).cpu().numpy(), w.reshape(B * L, n).cpu().numpy(), csr_np, R, K,
                                 out_bytes=24) for a, w in cap]
-    gather_ms = per_launch["k_pull_max"] + per_launch["k_seg_max"] + per_launch["k_sup_max"] + per_launch["k_heavy_max"]
+    gather = ("k_pull_max", "k_seg_max", "k_sup_max", "k_heavy_max")
+    gather_ms = sum(cold[k] for k in gather)
+    warm_ms = sum(per_launch[k] for k in gather)
     bytes_per_hop = float(np.mean(hop_bytes))
     achieved = bytes_per_hop / (gather_ms * 1e-3) / 1e9 if gather_ms > 0 else 0.0
+    warm = bytes_per_hop / (warm_ms * 1e-3) / 1e9 if warm_ms > 0 else 0.0
 
     # filtered ranking: 5,000 queries over all entities; filter = each query's known answers + target
     QN = 5000
@@ -572,9 +606,12 @@ def main_c4(args):
                    "batch": B, "channels": L, "hops": T, "c1": c1, "c2": cfg.c2},
         "topk_select_ms": {"c1_per_hop": per_launch["k_topc_rows"], "c2_per_hop": per_launch["k_c2_hard"]},
         "kernel_ms_per_launch": per_launch,
+        "kernel_ms_per_launch_cold": cold,
         "roofline": {"kernel": "k_pull_max+k_seg_max+k_sup_max+k_heavy_max", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "algorithmic_bytes_per_launch": bytes_per_hop, "traffic": None},
+                     "algorithmic_bytes_per_launch": bytes_per_hop, "traffic": None, "ms": gather_ms,
+                     "cache": "cold: %d MiB written before each hop" % FLUSH_MIB,
+                     "warm": {"achieved": warm, "frac": warm / HBM_PEAK_GBS, "ms": warm_ms}},
         "cpu_baseline": cpu,
         "ranking": {"queries": QN, "entities": E, "filter_entries": nf, "ms": rank_ms,
                     "queries_per_s": QN / (rank_ms * 1e-3),
@@ -1020,7 +1057,7 @@ def main_sparse(args):
 
     native_sum = [False]
 
-    def step():
+    def step(flush=None):
         # src/main.py:887-890: the batch's triples are hidden from the graph
         # for the step (the mask is updated in place), restored after it (:927-930);
         # src/model_DRUM_kernel_sp.py:132-205 per hop: the hop, normalize_sparse3d, dropout
@@ -1029,6 +1066,8 @@ def main_sparse(args):
             mask_values[batch_edges] = False
         s = state0
         for t_ in range(T):
+            if flush is not None:
+                flush()
             s = fk.normalize_sparse3d(hop(s, Wl[t_]))
             if train:
                 s = torch.sparse_coo_tensor(s.indices(), torch.nn.functional.dropout(s.values(), 0.1, True),
@@ -1109,6 +1148,16 @@ def main_sparse(args):
         _lib.prof_enable(False)
         per_launch = {k: (v[0] / v[1] if v[1] else 0.0) for k, v in prof.items()}
         per_step = {k: (v[0] / max(args.profile_steps, 1)) for k, v in prof.items()}
+        # the same steps with the caches flushed before each hop
+        flush = cache_flusher()
+        _lib.prof_enable(True)
+        for _ in range(args.profile_steps):
+            step(flush=flush)
+        torch.cuda.synchronize()
+        prof_cold = {k: _lib.prof_read(k) for k in SPARSE_KERNELS}
+        _lib.prof_enable(False)
+        del flush
+        cold_step = {k: (v[0] / max(args.profile_steps, 1)) for k, v in prof_cold.items()}
         print("per-launch ms: " + json.dumps({k: round(v, 4) for k, v in per_launch.items()}),
               file=sys.stderr, flush=True)
         print("per-step ms: " + json.dumps({k: round(v, 4) for k, v in per_step.items()}),
@@ -1125,15 +1174,19 @@ def main_sparse(args):
     # roofline of the whole hop: the hop formula's bytes of the step's hops over
     # the live time of the hop's kernels (HIP events around each launch)
     step_bytes = float(sum(sparse_hop_bytes(p) for p in plans))
-    hop_ms = sum(per_step[k] for k in HOP_KERNELS)
+    hop_ms = sum(cold_step[k] for k in HOP_KERNELS)
     achieved = step_bytes / (hop_ms * 1e-3) / 1e9 if hop_ms > 0 else 0.0
+    warm_ms = sum(per_step[k] for k in HOP_KERNELS)
+    warm = step_bytes / (warm_ms * 1e-3) / 1e9 if warm_ms > 0 else 0.0
     traffic = measured_traffic(HOP_KERNELS)
     kernel_rooflines = {}
     for k, b in item_kernel_bytes(plans).items():
-        if per_step.get(k, 0.0) > 0 and b > 0:
-            a = b / (per_step[k] * 1e-3) / 1e9
+        if cold_step.get(k, 0.0) > 0 and per_step.get(k, 0.0) > 0 and b > 0:
+            a = b / (cold_step[k] * 1e-3) / 1e9
+            aw = b / (per_step[k] * 1e-3) / 1e9
             kernel_rooflines[k] = {"achieved": a, "frac": a / HBM_PEAK_GBS, "algorithmic_bytes_per_step": b,
-                                   "ms_per_step": per_step[k], "traffic": measured_traffic([k])}
+                                   "ms_per_step": cold_step[k], "traffic": measured_traffic([k]),
+                                   "warm": {"achieved": aw, "frac": aw / HBM_PEAK_GBS, "ms_per_step": per_step[k]}}
     dominant = max(per_step, key=lambda k: per_step[k])
     result = {
         "metric": "queries/sec for L=3 propagation + % of HBM roofline; top-k select ms",
@@ -1163,9 +1216,12 @@ def main_sparse(args):
                            "c2_per_hop": per_launch["k_sp_select"]},
         "kernel_ms_per_launch": per_launch,
         "kernel_ms_per_step": per_step,
+        "kernel_ms_per_step_cold": cold_step,
         "roofline": {"kernel": "sparse hop (its forward and backward kernels, per step)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "algorithmic_bytes_per_launch": step_bytes, "ms_per_launch": hop_ms,
+                     "cache": "cold: %d MiB written before each hop" % FLUSH_MIB,
+                     "warm": {"achieved": warm, "frac": warm / HBM_PEAK_GBS, "ms_per_launch": warm_ms},
                      "traffic": traffic,
                      "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT) if traffic is not None else None},
         "dominant_kernel": {"name": dominant, "ms_per_step": per_step[dominant]},
