@@ -244,6 +244,12 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     q.wsum = ws;
     q.cap = cap;
     q.target = K < cap ? K : cap;
+    if (cap <= K) {
+        // every eligible edge is kept: no quotas, no residual to spread
+        q.residual = 0;
+        q.spare = 0;
+        return q;
+    }
     SpTake tk{};
     tk.wsum = fl_uniform_f64(ws);
     tk.wsum_r = __ddiv_rn(1.0, tk.wsum);
