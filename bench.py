@@ -59,14 +59,17 @@ def parse():
                     help="first run 3 plain device copies of this many MiB (a known-size reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--counter-steps", type=int, default=0,
-                    help="--sparse: run exactly this many steps and stop (a rocprofv3 counter pass; "
-                         "no timing, no CPU baseline)")
+                    help="run exactly this many steps of the configuration's step and stop (a rocprofv3 "
+                         "counter pass; no timing, no CPU baseline)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "STEPS", "OUT"),
                     help="write the per-step HBM traffic summary of two rocprofv3 counter passes "
-                         "(FETCH_SIZE, then WRITE_SIZE, each over --copy-mb 256 --counter-steps STEPS)")
-    ap.add_argument("--stats-table", nargs=4, metavar=("OUT", "STATS_CSV", "TITLE", "RUN_COMMAND"),
-                    help="write the kernel-time table of a rocprofv3 --kernel-trace --stats run "
-                         "(its kernel_stats.csv) as markdown, naming the run's command")
+                         "(FETCH_SIZE, then WRITE_SIZE, each over --copy-mb 256 --counter-steps STEPS); "
+                         "with --config, of that configuration's runs")
+    ap.add_argument("--stats-table", nargs="+", metavar="ARG",
+                    help="OUT STATS_CSV TITLE RUN_COMMAND [TRACE_CSV FIRST_STEPS]: write the kernel-time table "
+                         "of a rocprofv3 --kernel-trace --stats run (its kernel_stats.csv) as markdown, naming "
+                         "the run's command; with its kernel_trace.csv, also each per-hop kernel's mean over "
+                         "the run's first FIRST_STEPS steps")
     ap.add_argument("--counter-table", nargs="+", metavar="ARG",
                     help="OUT CSV [CSV ...]: write the per-dispatch means of every counter in these "
                          "rocprofv3 counter_collection.csv files (one per pass over --counter-steps) for "
@@ -74,15 +77,30 @@ def parse():
     return ap.parse_args()
 
 
-def stats_table(out_path, stats_csv, title, run_command, top=30):
+def stats_table(out_path, stats_csv, title, run_command, top=30, trace_csv=None, first_steps=0, per_step=3):
     """The rocprofv3 kernel statistics (per kernel: calls, average, min and
-    max duration, share of GPU time) as a markdown table."""
+    max duration, share of GPU time) as a markdown table.  With a kernel
+    trace and first_steps: for the kernels launched per_step times a step,
+    also the mean duration over their first first_steps * per_step launches
+    (the default workload's steps, which the C5 bench runs before its
+    reference-batch steps) -- the figure the bench's own per-launch timing
+    is comparable with."""
     import csv
     rows = list(csv.DictReader(open(stats_csv)))
     rows.sort(key=lambda r: -float(r["Percentage"]))
+    first = {}
+    if trace_csv and first_steps > 0:
+        launches = {}
+        for r in sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"])):
+            launches.setdefault(r["Kernel_Name"], []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        n = first_steps * per_step
+        for name, d in launches.items():
+            if len(d) >= n and len(d) % per_step == 0:
+                first[name] = sum(d[:n]) / n / 1e3
     lines = ["# %s" % title, "", "Commands (from the repo root, on one MI355X):", "", "```",
              "cd /tmp && rocprofv3 --kernel-trace --stats --output-format csv -d /tmp/prof -o run -- " + run_command,
-             "python3 <repo>/bench.py --stats-table <this file> <the run's kernel_stats.csv> <title> <run command>",
+             "python3 <repo>/bench.py --stats-table <this file> <the run's kernel_stats.csv> <title> <run command>"
+             + (" <the run's kernel_trace.csv> %d" % first_steps if first else ""),
              "```", "",
              "Names: fl:: are this library's kernels, at:: and rocprim:: torch's.", "",
              "| kernel | calls | avg us | min us | max us | % of GPU time |", "|---|---|---|---|---|---|"]
@@ -91,6 +109,14 @@ def stats_table(out_path, stats_csv, title, run_command, top=30):
         lines.append("| %s | %s | %.1f | %.1f | %.1f | %.2f |" % (
             name, r["Calls"], float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3,
             float(r["Percentage"])))
+    if first:
+        lines += ["", "The default batch's steps alone (the first %d steps of the run, %d launches per step of "
+                  "each kernel below; the reference batch's %s-query steps follow them): mean us per launch, "
+                  "from the run's kernel trace." % (first_steps, per_step, "512"), "",
+                  "| kernel | mean us per launch, default batch |", "|---|---|"]
+        for name, us in sorted(first.items(), key=lambda x: -x[1])[:20]:
+            short = name.replace("(anonymous namespace)::", "").split("(")[0].replace("void ", "")[:72]
+            lines.append("| %s | %.1f |" % (short, us))
     with open(out_path, "w") as f:
         f.write("\n".join(lines) + "\n")
     print("wrote", out_path)
@@ -173,7 +199,12 @@ def _pmc_per_kernel(path, counter):
     return {k: list(v.values()) for k, v in per.items()}
 
 
-def pmc_summary(fetch_csv, write_csv, steps, out_path):
+PMC_WORKLOADS = {5: ("C5 sparse training step", ""),
+                 2: ("C2 dense sum step (evaluation)", "--config 2 "),
+                 4: ("C4 dense max step (forward + backward)", "--config 4 ")}
+
+
+def pmc_summary(fetch_csv, write_csv, steps, out_path, config=5):
     """Per kernel: HBM MB per step = (FETCH_SIZE, WRITE_SIZE in KiB per
     dispatch, each scaled by the ratio of the bytes a plain 256 MiB device
     copy moves to what the counter reads for it) summed over the kernel's
@@ -193,16 +224,17 @@ def pmc_summary(fetch_csv, write_csv, steps, out_path):
         w_mb = sum(wr.get(k, [])) * fw * 1024 / 1e6
         rows.append(((f_mb + w_mb) / steps, k, len(fe[k]), f_mb / steps, w_mb / steps))
     rows.sort(reverse=True)
-    lines = ["# HBM traffic per step of this library's kernels, C5 sparse training step",
+    title, run = PMC_WORKLOADS[config]
+    lines = ["# HBM traffic per step of this library's kernels, %s" % title,
              "",
              "Two rocprofv3 counter passes over `--counter-steps %d` (from the repo root, on one MI355X):" % steps,
              "",
              "    cd /tmp && rocprofv3 --pmc FETCH_SIZE --output-format csv -d /tmp/p_fetch -o run -- "
-             "python3 <repo>/bench.py --copy-mb 256 --counter-steps %d" % steps,
+             "python3 <repo>/bench.py %s--copy-mb 256 --counter-steps %d" % (run, steps),
              "    cd /tmp && rocprofv3 --pmc WRITE_SIZE --output-format csv -d /tmp/p_write -o run -- "
-             "python3 <repo>/bench.py --copy-mb 256 --counter-steps %d" % steps,
-             "    python3 <repo>/bench.py --pmc-summary <fetch counter_collection.csv> "
-             "<write counter_collection.csv> %d <this file>" % steps,
+             "python3 <repo>/bench.py %s--copy-mb 256 --counter-steps %d" % (run, steps),
+             "    python3 <repo>/bench.py %s--pmc-summary <fetch counter_collection.csv> "
+             "<write counter_collection.csv> %d <this file>" % (run, steps),
              "",
              "Copy calibration: a 256 MiB device copy reads FETCH_SIZE %.1f KiB and WRITE_SIZE %.1f KiB; "
              "scale factors to bytes %.3f (fetch) and %.3f (write)." % (cf, cw, ff, fw),
@@ -334,10 +366,13 @@ def main():
     args = parse()
     if args.pmc_summary:
         fetch_csv, write_csv, steps, out = args.pmc_summary
-        return pmc_summary(fetch_csv, write_csv, int(steps), out)
+        return pmc_summary(fetch_csv, write_csv, int(steps), out, args.config)
     if args.stats_table:
-        out, csv_path, title, run_command = args.stats_table
-        return stats_table(out, csv_path, title, run_command)
+        if len(args.stats_table) not in (4, 6):
+            sys.exit("--stats-table takes OUT STATS_CSV TITLE RUN_COMMAND [TRACE_CSV FIRST_STEPS]")
+        out, csv_path, title, run_command = args.stats_table[:4]
+        trace, first_steps = (args.stats_table[4], int(args.stats_table[5])) if len(args.stats_table) == 6 else (None, 0)
+        return stats_table(out, csv_path, title, run_command, trace_csv=trace, first_steps=first_steps)
     if args.counter_table:
         if len(args.counter_table) < 2:
             sys.exit("--counter-table needs OUT and at least one CSV")
@@ -394,6 +429,12 @@ def main():
         return x.sum(dim=1)
 
     with torch.inference_mode():
+        if args.counter_steps > 0:
+            for _ in range(args.counter_steps):
+                step()
+            torch.cuda.synchronize()
+            print("counter run: %d steps" % args.counter_steps, file=sys.stderr, flush=True)
+            return
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
@@ -428,6 +469,8 @@ def main():
         hop_bytes = [hop_pull_bytes(a.reshape(B * L, E).cpu().numpy(), w.reshape(B * L, n).cpu().numpy(),
                                     csr_np, R, K) for a, w in cap]
     bytes_per_launch = float(np.mean(hop_bytes))
+    traffic = measured_traffic(["k_pull"], DENSE_TRAFFIC_FILES[2])
+    traffic = traffic / T if traffic is not None else None  # per launch: T launches per step
     pull_ms = cold["k_pull"]
     achieved = bytes_per_launch / (pull_ms * 1e-3) / 1e9 if pull_ms > 0 else 0.0
     warm_ms = per_launch["k_pull"]
@@ -456,7 +499,8 @@ def main():
         "kernel_ms_per_launch_cold": cold,
         "roofline": {"kernel": "k_pull", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": None, "ms": pull_ms,
+                     "algorithmic_bytes_per_launch": bytes_per_launch, "traffic": traffic, "ms": pull_ms,
+                     "traffic_source": os.path.relpath(DENSE_TRAFFIC_FILES[2], ROOT) if traffic is not None else None,
                      "cache": "cold: %d MiB written before each hop" % FLUSH_MIB,
                      "warm": {"achieved": warm, "frac": warm / HBM_PEAK_GBS, "ms": warm_ms}},
         "cpu_baseline": cpu,
@@ -514,7 +558,13 @@ def main_c4(args):
         return loss
 
     kernels = ["k_topc_rows", "k_col_count", "k_frontier", "k_c2_hard", "k_pull_max", "k_seg_max", "k_sup_max",
-               "k_heavy_max", "k_bwd_pairs_max", "k_bwd_identity", "k_row_list"]
+               "k_heavy_max", "k_bwd_pairs_max", "k_bwd_identity", "k_row_count", "k_row_fill"]
+    if args.counter_steps > 0:
+        for _ in range(args.counter_steps):
+            step()
+        torch.cuda.synchronize()
+        print("counter run: %d mmDRUM steps" % args.counter_steps, file=sys.stderr, flush=True)
+        return
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -544,6 +594,8 @@ def main_c4(args):
     gather_ms = sum(cold[k] for k in gather)
     warm_ms = sum(per_launch[k] for k in gather)
     bytes_per_hop = float(np.mean(hop_bytes))
+    traffic = measured_traffic(list(gather), DENSE_TRAFFIC_FILES[4])
+    traffic = traffic / T if traffic is not None else None  # per hop: T hops per step
     achieved = bytes_per_hop / (gather_ms * 1e-3) / 1e9 if gather_ms > 0 else 0.0
     warm = bytes_per_hop / (warm_ms * 1e-3) / 1e9 if warm_ms > 0 else 0.0
 
@@ -609,7 +661,8 @@ def main_c4(args):
         "kernel_ms_per_launch_cold": cold,
         "roofline": {"kernel": "k_pull_max+k_seg_max+k_sup_max+k_heavy_max", "bound": "hbm", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "algorithmic_bytes_per_launch": bytes_per_hop, "traffic": None, "ms": gather_ms,
+                     "algorithmic_bytes_per_launch": bytes_per_hop, "traffic": traffic, "ms": gather_ms,
+                     "traffic_source": os.path.relpath(DENSE_TRAFFIC_FILES[4], ROOT) if traffic is not None else None,
                      "cache": "cold: %d MiB written before each hop" % FLUSH_MIB,
                      "warm": {"achieved": warm, "frac": warm / HBM_PEAK_GBS, "ms": warm_ms}},
         "cpu_baseline": cpu,
@@ -938,8 +991,9 @@ def item_kernel_bytes(plans):
     CSR position and attention column with a backward; k_sp_hist reads the
     destination, 4 B; k_sp_partition reads destination and value and writes
     them in bucket order, 16 B, + 4 B of the item's bucket position with a
-    backward; k_sp_local_to_out reads the destination, that position and
-    the bucket-order output index and writes the raw-order one, 16 B;
+    backward; k_sp_local_to_out reads that position (which carries the
+    item's bucket) and the bucket-order output index and writes the
+    raw-order one, 12 B;
     k_sp_bwd reads CSR position, column and output index and the output's
     gradient, 14 B)."""
     out = {"k_sp_select": 0, "k_sp_expand_fused": 0, "k_sp_items": 0, "k_sp_hist": 0, "k_sp_partition": 0,
@@ -953,22 +1007,25 @@ def item_kernel_bytes(plans):
         out["k_sp_hist"] += 4 * it
         out["k_sp_partition"] += (16 + (4 if bw else 0)) * it
         if bw:
-            out["k_sp_local_to_out"] += 16 * it
+            out["k_sp_local_to_out"] += 12 * it
             out["k_sp_bwd"] += 14 * it
     return out
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sparse_hop_c5_train_traffic_per_step.txt")
+DENSE_TRAFFIC_FILES = {2: os.path.join(ROOT, "profiles", "dense_hop_c2_traffic_per_step.txt"),
+                       4: os.path.join(ROOT, "profiles", "dense_max_c4_traffic_per_step.txt")}
 
 
-def measured_traffic(kernels):
-    """HBM bytes per step of the given kernels from the committed counter
-    summary (lines "<kernel> <MB per step> ..."), or None when it is absent
-    or lacks one of them."""
-    if not os.path.exists(TRAFFIC_FILE):
+def measured_traffic(kernels, path=None):
+    """HBM bytes per step of the given kernels from a committed counter
+    summary (lines "<kernel> <MB per step> ..."; by default the C5 one), or
+    None when it is absent."""
+    path = path or TRAFFIC_FILE
+    if not os.path.exists(path):
         return None
     mb = {}
-    for line in open(TRAFFIC_FILE):
+    for line in open(path):
         parts = line.split()
         if len(parts) >= 2 and parts[0].startswith("k_"):
             try:
@@ -1119,27 +1176,6 @@ def main_sparse(args):
         ms_step_native = e_0.elapsed_time(e_1) / args.steps
         native_sum[0] = False
         print("with flashlog_kernel.sum_sp_3d: %.3f ms/step" % ms_step_native, file=sys.stderr, flush=True)
-        # the reference's training batch for --batch_size 256: 2B queries (each
-        # triple forward and inverse), the same step otherwise
-        ref_batch = None
-        if train:
-            work.insert(0, workload(src2, tgt2, W2))
-            for _ in range(2):
-                step()
-            torch.cuda.synchronize()
-            e_0.record()
-            for _ in range(args.steps):
-                step()
-            e_1.record()
-            torch.cuda.synchronize()
-            ms_step_2b = e_0.elapsed_time(e_1) / args.steps
-            work.pop(0)
-            ref_batch = {"queries_per_step": 2 * B, "ms_per_step": ms_step_2b,
-                         "value": 2 * B / (ms_step_2b * 1e-3), "unit": "queries/s",
-                         "what": "the same training step on the %d queries the reference propagates for "
-                                 "--batch_size %d (each batch triple forward and inverse, "
-                                 "src/dataloader.py:114-122)" % (2 * B, B)}
-            print("reference batch (%d queries): %.3f ms/step" % (2 * B, ms_step_2b), file=sys.stderr, flush=True)
         _lib.prof_enable(True)
         for _ in range(args.profile_steps):
             step()
@@ -1168,6 +1204,28 @@ def main_sparse(args):
         torch.cuda.synchronize()
         plans = fk.plan_log
         fk.plan_log = None
+        # the reference's training batch for --batch_size 256: 2B queries (each
+        # triple forward and inverse), the same step otherwise; run last, so
+        # that in a kernel trace the default batch's launches come first
+        ref_batch = None
+        if train:
+            work.insert(0, workload(src2, tgt2, W2))
+            for _ in range(2):
+                step()
+            torch.cuda.synchronize()
+            e_0.record()
+            for _ in range(args.steps):
+                step()
+            e_1.record()
+            torch.cuda.synchronize()
+            ms_step_2b = e_0.elapsed_time(e_1) / args.steps
+            work.pop(0)
+            ref_batch = {"queries_per_step": 2 * B, "ms_per_step": ms_step_2b,
+                         "value": 2 * B / (ms_step_2b * 1e-3), "unit": "queries/s",
+                         "what": "the same training step on the %d queries the reference propagates for "
+                                 "--batch_size %d (each batch triple forward and inverse, "
+                                 "src/dataloader.py:114-122)" % (2 * B, B)}
+            print("reference batch (%d queries): %.3f ms/step" % (2 * B, ms_step_2b), file=sys.stderr, flush=True)
     csr_np = [c.cpu().numpy() for c in csr]
     cpu = (cpu_baseline_sparse(args, csr_np, L, E, R, K, c1, src, tgt, W.cpu(), T, train)
            if args.cpu_seconds > 0 else None)

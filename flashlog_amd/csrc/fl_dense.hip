@@ -947,7 +947,8 @@ __global__ __launch_bounds__(PULL_NT) void k_heavy_max(fl_side ori, fl_side inv,
 //                   gw[row, n-1] = sum_e g_ind * A (fixed tree order).
 //   (frontier)      the forward's k_col_count / k_frontier / k_c2_hard on the
 //                   same A and w give the same admitted edges.
-//   k_row_list      per row, its active sources in ascending order.
+//   k_row_count, k_row_fill  per row, its active sources in ascending order
+//                   (per chunk of sources and 32-row word: counts, then ranks).
 //   k_bwd_pairs     one wave per active (source, row): the ORI then INV row
 //                   walk of the reference, adding (go*w)*m onto the identity
 //                   term in CSR order (bit-exact gA), and per relation group
@@ -1031,26 +1032,75 @@ static void bwd_identity(hipStream_t st, const float *g_ind, const float *A, con
                        (int)nsl, wot_i, gw);
 }
 
-constexpr int RL_NT = 1024;
+constexpr int RL_NT = 1024;  // sources per row-list chunk, one per thread
 
-// Ordered compaction of the row's active sources (bit bl of BM[bl/32][src]).
-__global__ __launch_bounds__(RL_NT) void k_row_list(const uint32_t *__restrict__ BM, int64_t E,
-                                                    int32_t *__restrict__ rowlist, int32_t *__restrict__ rowcnt) {
-    __shared__ int lds_scan[RL_NT / FL_WAVE + 1];
-    const int64_t bl = blockIdx.x;
-    const uint32_t *bm = BM + (bl >> 5) * E;
-    const uint32_t bit = 1u << (bl & 31);
-    int32_t *out = rowlist + bl * E;
-    int run = 0;
-    for (int64_t base = 0; base < E; base += RL_NT) {
-        const int64_t e = base + threadIdx.x;
-        const int f = (e < E && (bm[e] & bit)) ? 1 : 0;
-        int tot;
-        const int ex = fl_block_excl_scan<RL_NT>(f, lds_scan, &tot);
-        if (f) out[run + ex] = (int32_t)e;
-        run += tot;
+__device__ __forceinline__ uint32_t sp_lanes_below_u64(unsigned long long m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Row lists (each row's active sources in ascending order) in two passes
+// over (chunk of RL_NT sources, 32-row word) workgroups.  k_row_count: per
+// row of the word, the chunk's active sources (a ballot per row and wave).
+__global__ __launch_bounds__(RL_NT) void k_row_count(const uint32_t *__restrict__ BM, int64_t BL, int64_t E,
+                                                     int64_t nch, int32_t *__restrict__ ccnt) {
+    __shared__ int wc[RL_NT / FL_WAVE][32];
+    const int64_t c = blockIdx.x, wi = blockIdx.y;
+    const int64_t src = c * RL_NT + threadIdx.x;
+    const uint32_t bits = src < E ? BM[wi * E + src] : 0u;
+    const int lane = fl_lane(), w = fl_wave_id();
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+        const unsigned long long m = __ballot((bits >> r) & 1u);
+        if (lane == 0) wc[w][r] = __popcll(m);
     }
-    if (threadIdx.x == 0) rowcnt[bl] = run;
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        const int64_t bl = wi * 32 + threadIdx.x;
+        int tot = 0;
+        for (int q = 0; q < RL_NT / FL_WAVE; ++q) tot += wc[q][threadIdx.x];
+        if (bl < BL) ccnt[bl * nch + c] = tot;
+    }
+}
+
+// k_row_fill: each active source's rank in its row = the row's active
+// sources in earlier chunks + in earlier waves of this chunk + in lower
+// lanes; the last chunk also stores the row's count.
+__global__ __launch_bounds__(RL_NT) void k_row_fill(const uint32_t *__restrict__ BM, int64_t BL, int64_t E,
+                                                    int64_t nch, const int32_t *__restrict__ ccnt,
+                                                    int32_t *__restrict__ rowlist, int32_t *__restrict__ rowcnt) {
+    __shared__ int wc[RL_NT / FL_WAVE][32];
+    const int64_t c = blockIdx.x, wi = blockIdx.y;
+    const int64_t src = c * RL_NT + threadIdx.x;
+    const uint32_t bits = src < E ? BM[wi * E + src] : 0u;
+    const int lane = fl_lane(), w = fl_wave_id();
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+        const unsigned long long m = __ballot((bits >> r) & 1u);
+        if (lane == 0) wc[w][r] = __popcll(m);
+    }
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        // wave prefixes in place, the chunk's offset in the row added
+        const int64_t bl = wi * 32 + threadIdx.x;
+        int run = 0;
+        if (bl < BL)
+            for (int64_t q = 0; q < c; ++q) run += ccnt[bl * nch + q];
+        for (int q = 0; q < RL_NT / FL_WAVE; ++q) {
+            const int x = wc[q][threadIdx.x];
+            wc[q][threadIdx.x] = run;
+            run += x;
+        }
+        if (bl < BL && c == nch - 1) rowcnt[bl] = run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 32; ++r) {
+        const unsigned long long m = __ballot((bits >> r) & 1u);
+        if ((bits >> r) & 1u) {
+            const int64_t bl = wi * 32 + r;  // set bits are rows < BL
+            rowlist[bl * E + wc[w][r] + (int)sp_lanes_below_u64(m)] = (int32_t)src;
+        }
+    }
 }
 
 // One side of an active (source, row) pair, by one wave: the kept positions
@@ -1131,7 +1181,7 @@ __device__ __forceinline__ float bwd_side(const fl_side &s, int64_t src, int64_t
 }
 
 // One wave per active (source, row) pair, pairs in row-major order (the
-// row's sources ascending, from k_row_list): gA[row, src] = the identity
+// row's sources ascending, from k_row_fill): gA[row, src] = the identity
 // term written by k_bwd_identity plus the ORI then INV walks, and the pair's
 // row of PG (relation partials, 0 where no edge of the relation is kept).
 constexpr int BWDP_WAVES = BWD_NT / FL_WAVE;
@@ -1406,9 +1456,11 @@ int fl_dense_sum_forward(void *stream, const fl_side *ori, const fl_side *inv, c
 
 size_t fl_dense_backward_workspace_bytes(const fl_side *ori, const fl_side *inv, int64_t BL, int64_t E) {
     if (BL <= 0 || E <= 0 || !ori || !inv) return 256;
-    // the forward's frontier arrays plus the row lists
+    // the forward's frontier arrays plus the row lists and their chunk counts
+    const int64_t nch = (E + RL_NT - 1) / RL_NT;
     return dense_ws_layout(BL, E, ori, inv, nullptr).bytes + align256(sizeof(int32_t) * (size_t)(BL * E)) +
-           align256(sizeof(int32_t) * (size_t)BL) + align256(sizeof(int64_t) * (size_t)(BL + 1));
+           align256(sizeof(int32_t) * (size_t)BL) + align256(sizeof(int64_t) * (size_t)(BL + 1)) +
+           align256(sizeof(int32_t) * (size_t)(BL * nch));
 }
 
 }  // extern "C"
@@ -1456,7 +1508,12 @@ int dense_backward_impl(const char *name, void *stream, const fl_side *ori, cons
     if (do_topk)
         FL_LAUNCH("k_c2_hard", k_c2_hard, dim3(1024), dim3(C2_NT), 0, st, *ori, *inv, w, BL, E, n, r_size, K,
                   ws.hard_count, ws.hard, ws.pk, ws.cut);
-    FL_LAUNCH("k_row_list", k_row_list, dim3((unsigned)BL), dim3(RL_NT), 0, st, ws.bm, E, rowlist, rowcnt);
+    const int64_t nch = (E + RL_NT - 1) / RL_NT;
+    int32_t *ccnt = (int32_t *)((char *)rowoff + align256(sizeof(int64_t) * (size_t)(BL + 1)));
+    FL_LAUNCH("k_row_count", k_row_count, dim3((unsigned)nch, (unsigned)nw), dim3(RL_NT), 0, st, ws.bm, BL, E, nch,
+              ccnt);
+    FL_LAUNCH("k_row_fill", k_row_fill, dim3((unsigned)nch, (unsigned)nw), dim3(RL_NT), 0, st, ws.bm, BL, E, nch, ccnt,
+              rowlist, rowcnt);
     FL_LAUNCH("k_row_offsets", k_row_offsets, dim3(1), dim3(64), 0, st, rowcnt, BL, rowoff);
     if (pg_pairs > 0) {
         // a wave per pair: the host's pair count bounds the grid (pairs past

@@ -11,7 +11,7 @@ kernels compute it (fl_mul / fl_add), so the replayed grad_A can also be
 compared bit for bit with the CPU oracle of flashlog.cpp:216-278.
 
 The sequence is k_bwd_identity (+ k_bwd_identity_fin) -> k_col_count with a
-null out_ind -> k_frontier -> k_c2_hard -> k_row_list -> k_row_offsets ->
+null out_ind -> k_frontier -> k_c2_hard -> k_row_count -> k_row_fill -> k_row_offsets ->
 k_bwd_pairs -> k_bwd_gw, on the inputs of tests/test_gpu_dense.py's
 test_dense_sum_backward.  An earlier k_col_count stored the identity output
 without testing out_ind; the replay of that form stores through the null
@@ -270,19 +270,32 @@ def k_c2_hard(ori, inv, w, BL, E, n, r_size, K, hard_count, hard_e, hard_bl, PKt
                 CUT[at] = c2
 
 
-def k_row_list(BM, BL, E, rowlist, rowcnt):
-    for bl in range(BL):
-        run = 0
-        for base in range(0, E, RL_NT):
-            flags = [1 if (base + t < E and int(BM[(bl >> 5) * E + base + t]) & (1 << (bl & 31))) else 0
-                     for t in range(RL_NT)]
-            ex = 0
-            for t in range(RL_NT):
-                if flags[t]:
-                    rowlist[bl * E + run + ex] = base + t
-                ex += flags[t]
-            run += ex
-        rowcnt[bl] = run
+def k_row_count(BM, BL, E, nch, ccnt):
+    nw = (BL + 31) // 32
+    for wi in range(nw):
+        for c in range(nch):  # workgroup (chunk, word): thread t holds source c * RL_NT + t
+            bits = [int(BM[wi * E + c * RL_NT + t]) if c * RL_NT + t < E else 0 for t in range(RL_NT)]
+            for r in range(32):
+                bl = wi * 32 + r
+                if bl < BL:
+                    ccnt[bl * nch + c] = sum((b >> r) & 1 for b in bits)
+
+
+def k_row_fill(BM, BL, E, nch, ccnt, rowlist, rowcnt):
+    nw = (BL + 31) // 32
+    for wi in range(nw):
+        for c in range(nch):
+            bits = [int(BM[wi * E + c * RL_NT + t]) if c * RL_NT + t < E else 0 for t in range(RL_NT)]
+            for r in range(32):
+                bl = wi * 32 + r
+                run = sum(int(ccnt[bl * nch + q]) for q in range(c)) if bl < BL else 0
+                for t in range(RL_NT):  # waves in order, lanes in order
+                    if (bits[t] >> r) & 1:
+                        assert bl < BL
+                        rowlist[bl * E + run] = c * RL_NT + t
+                        run += 1
+                if bl < BL and c == nch - 1:
+                    rowcnt[bl] = run
 
 
 def k_row_offsets(rowcnt, BL, rowoff):
@@ -435,13 +448,16 @@ def replay(A, w, g, csr, masks, R, wot_i, K, guard_out_ind=True):
     rowlist = Buf("rowlist", cap, np.int32, tracked=True)
     rowcnt = Buf("rowcnt", BL, np.int32, tracked=True)
     rowoff = Buf("rowoff", BL + 1, np.int64, tracked=True)
+    nch = (E + RL_NT - 1) // RL_NT
+    ccnt = Buf("row chunk counts", BL * nch, np.int32, tracked=True)
 
     bwd_identity(gi, Ab, wb, BL, E, n, wot_i, 1, gA, gw)
     k_col_count(Ab, wb, BL, E, n, wot_i, None, BM, hard_count, guard_out_ind)
     k_frontier(ori, inv, Ab, BL, E, K, do_topk, BM, PKa, PKt, hard_count, hard_e, hard_bl)
     if do_topk:
         k_c2_hard(ori, inv, wb, BL, E, n, R, K, hard_count, hard_e, hard_bl, PKt, CUT)
-    k_row_list(BM, BL, E, rowlist, rowcnt)
+    k_row_count(BM, BL, E, nch, ccnt)
+    k_row_fill(BM, BL, E, nch, ccnt, rowlist, rowcnt)
     k_row_offsets(rowcnt, BL, rowoff)
     if pairs > 0:
         k_bwd_pairs(ori, inv, Ab, wb, go, gv, BL, E, n, R, PKt, CUT, rowlist, rowcnt, rowoff, pairs, gA, PG)
