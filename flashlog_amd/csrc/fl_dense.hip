@@ -658,6 +658,35 @@ constexpr int FOLD_NT = 256;
 constexpr int FOLD_ROWS = 16;
 constexpr int FOLD_CHUNK = 4 * FOLD_NT;
 
+// a + v[0] + v[1] + ... + v[lim-1], left to right, from a 16-byte aligned
+// LDS row: the values are read 32 at a time with 16-byte loads, so the
+// chain of additions waits on one LDS round trip per 32 of them.
+__device__ __forceinline__ float fold_lds(float a, const float *v, int lim) {
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    int q = 0;
+    for (; q + 32 <= lim; q += 32) {
+        float4 x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = v4[(q >> 2) + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            a = fl_add(a, x[u].x);
+            a = fl_add(a, x[u].y);
+            a = fl_add(a, x[u].z);
+            a = fl_add(a, x[u].w);
+        }
+    }
+    for (; q + 4 <= lim; q += 4) {
+        const float4 x = v4[q >> 2];
+        a = fl_add(a, x.x);
+        a = fl_add(a, x.y);
+        a = fl_add(a, x.z);
+        a = fl_add(a, x.w);
+    }
+    for (; q < lim; ++q) a = fl_add(a, v[q]);
+    return a;
+}
+
 __global__ __launch_bounds__(FOLD_NT) void k_fold_heavy(
     fl_side ori, fl_side inv, int64_t BL, int64_t E, const float *__restrict__ region_ori,
     const float *__restrict__ region_inv, const int32_t *__restrict__ tot_ori, const int32_t *__restrict__ tot_inv,
@@ -689,9 +718,8 @@ __global__ __launch_bounds__(FOLD_NT) void k_fold_heavy(
         for (int r = 0; r < FOLD_ROWS; ++r) stage[r][t] = x[r];
         __syncthreads();
         if (t < FOLD_ROWS && rb + t < BL) {
-            const int64_t lim = (s_tot[t] - c0 < FOLD_CHUNK) ? s_tot[t] - c0 : FOLD_CHUNK;
-            const float *row = (const float *)stage[t];
-            for (int64_t k = 0; k < lim; ++k) acc = fl_add(acc, row[k]);
+            const int lim = (int)((s_tot[t] - c0 < FOLD_CHUNK) ? s_tot[t] - c0 : FOLD_CHUNK);
+            acc = fold_lds(acc, (const float *)stage[t], lim);
         }
         __syncthreads();
     }
