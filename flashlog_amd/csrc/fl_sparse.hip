@@ -170,6 +170,47 @@ struct SpQuota {
     long long cap, target, residual, spare;
 };
 
+// A side's groups, U windows of 64 at a time (the loads of a batch in
+// flight together; one window for sides that have no more groups, so that
+// they issue no work for empty windows), each lane visiting its groups in
+// order: fn(w, count) for every eligible group (w > 0, count > 0).  Loads at
+// clamped indices (every one issued, none behind a branch); groups past the
+// side's end are zeroed.
+template <int U, typename F>
+__device__ __forceinline__ void sp_quota_windows(const int16_t *__restrict__ grel, const int32_t *__restrict__ gcnt,
+                                                 uint32_t ng, const float *wr, F &&fn) {
+    const int lane = fl_lane();
+    for (uint32_t gb = 0; gb < ng; gb += U * FL_WAVE) {
+        int rl[U];
+        int32_t cl[U];
+        float wl[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t g = gb + u * FL_WAVE + (uint32_t)lane;
+            const uint32_t gc = g < ng ? g : ng - 1;
+            rl[u] = fl_ld32(grel, gc);
+            cl[u] = fl_ld32(gcnt, gc);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool in = gb + u * FL_WAVE + (uint32_t)lane < ng;
+            const float wraw = fl_ld32(wr, (uint32_t)rl[u]);
+            wl[u] = in ? wraw : 0.0f;
+            cl[u] = in ? cl[u] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (wl[u] > 0.0f && cl[u] > 0) fn(wl[u], cl[u]);
+    }
+}
+
+template <typename F>
+__device__ __forceinline__ void sp_quota_groups(const int16_t *__restrict__ grel, const int32_t *__restrict__ gcnt,
+                                                uint32_t ng, const float *wr, F &&fn) {
+    if (ng <= FL_WAVE) sp_quota_windows<1>(grel, gcnt, ng, wr, fn);
+    else sp_quota_windows<4>(grel, gcnt, ng, wr, fn);
+}
+
 __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int64_t K) {
     const int lane = fl_lane();
     // 32-bit offsets from the side's first group (a wave-uniform base)
@@ -179,42 +220,14 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     double ws = 0.0;
     long long cap = 0, nel = 0;
     int emin = 1 << 20, emax = -(1 << 20);
-    // groups 4 windows at a time (the loads of a batch in flight together);
-    // each lane still visits its groups in order
-    for (uint32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
-        int rl[4];
-        int32_t cl[4];
-        float wl[4];
-        // loads at clamped indices (every one issued, none behind a branch);
-        // groups past the side's end are zeroed
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t g = gb + u * FL_WAVE + (uint32_t)lane;
-            const uint32_t gc = g < ng ? g : ng - 1;
-            rl[u] = fl_ld32(grel, gc);
-            cl[u] = fl_ld32(gcnt, gc);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const bool in = gb + u * FL_WAVE + (uint32_t)lane < ng;
-            const float wraw = fl_ld32(wr, (uint32_t)rl[u]);
-            wl[u] = in ? wraw : 0.0f;
-            cl[u] = in ? cl[u] : 0;
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const float wv = wl[u];
-            const int32_t c = cl[u];
-            if (wv > 0.0f && c > 0) {
-                cap += c;
-                ++nel;
-                ws = __dadd_rn(ws, (double)wv);
-                const int lo = sp_lsb_exp(wv), hi = (int)((__float_as_uint(wv) >> 23) & 0xFF) - 127;
-                emin = lo < emin ? lo : emin;
-                emax = hi > emax ? hi : emax;
-            }
-        }
-    }
+    sp_quota_groups(grel, gcnt, ng, wr, [&](float wv, int32_t c) {
+        cap += c;
+        ++nel;
+        ws = __dadd_rn(ws, (double)wv);
+        const int lo = sp_lsb_exp(wv), hi = (int)((__float_as_uint(wv) >> 23) & 0xFF) - 127;
+        emin = lo < emin ? lo : emin;
+        emax = hi > emax ? hi : emax;
+    });
     cap = fl_wave_sum_i64(cap);
     nel = fl_wave_sum_i64(nel);
 #pragma unroll
@@ -255,30 +268,7 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     tk.wsum_r = __ddiv_rn(1.0, tk.wsum);
     tk.target = (int32_t)q.target;
     long long alloc = 0;
-    for (uint32_t gb = 0; gb < ng; gb += 4 * FL_WAVE) {
-        int rl[4];
-        int32_t cl[4];
-        float wl[4];
-        // loads at clamped indices (every one issued, none behind a branch);
-        // groups past the side's end are zeroed
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint32_t g = gb + u * FL_WAVE + (uint32_t)lane;
-            const uint32_t gc = g < ng ? g : ng - 1;
-            rl[u] = fl_ld32(grel, gc);
-            cl[u] = fl_ld32(gcnt, gc);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const bool in = gb + u * FL_WAVE + (uint32_t)lane < ng;
-            const float wraw = fl_ld32(wr, (uint32_t)rl[u]);
-            wl[u] = in ? wraw : 0.0f;
-            cl[u] = in ? cl[u] : 0;
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (wl[u] > 0.0f && cl[u] > 0) alloc += sp_quota_base(tk, wl[u], cl[u]);
-    }
+    sp_quota_groups(grel, gcnt, ng, wr, [&](float wv, int32_t c) { alloc += sp_quota_base(tk, wv, c); });
     alloc = fl_wave_sum_i64(alloc);
     q.residual = q.target - alloc;
     q.spare = cap - alloc;
