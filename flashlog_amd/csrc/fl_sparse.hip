@@ -322,73 +322,84 @@ __device__ __forceinline__ int32_t sp_quota_window(SpTake &tk, float wv, int32_t
 // every edge, or the quota window); fn(take, start, rel, wv, ex) is called
 // by every lane for each window that keeps an item, with ex = the lane's
 // first item index within the side (a wave prefix sum of the takes).
-// Returns the side's item count.  Q: quotas possible.
-template <bool Q, typename F>
-__device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, int64_t g1, const float *wr,
-                                                SpTake &tk, F &&fn) {
+// Returns the side's item count.  KIND: the side's take rule.
+template <int KIND, typename F>
+__device__ __forceinline__ int64_t sp_side_runs_k(const fl_side &s, int64_t g0, int64_t g1, const float *wr,
+                                                  SpTake &tk, F &&fn) {
     const int lane = fl_lane();
     int64_t base = 0;
     // software pipeline over the windows: the records two windows ahead and
     // the weights one window ahead are requested before this window's takes
-    // are computed; records at clamped indices (loads issued
-    // unconditionally), groups past the end zeroed.  32-bit offsets from the
-    // side's first group (a wave-uniform base; a side has at most 32767
-    // groups, one per relation).
+    // are computed; records at clamped indices, groups past the end zeroed.
+    // The windows' registers rotate through three sets (the loop body holds
+    // three windows), so that no register copy waits on a load in flight.
+    // 32-bit offsets from the side's first group (a wave-uniform base; a side
+    // has at most 32767 groups, one per relation).
     const uint32_t ng = (uint32_t)(g1 - g0);
+    if (ng == 0) return 0;
     const int16_t *__restrict__ grel = s.group_rel + g0;
     const int32_t *__restrict__ gsta = s.group_start + g0;
     const int32_t *__restrict__ gcnt = s.group_count + g0;
     const uint32_t glast = ng - 1;
     const uint32_t ul = (uint32_t)lane;
-    int rel = 0, rel1 = 0;
-    int32_t start = 0, cnt = 0, start1 = 0, cnt1 = 0;
-    float wraw = 0.0f;
-    if (ng > 0) {
-        const uint32_t gc = ul < ng ? ul : glast;
-        rel = fl_ld32(grel, gc);
-        start = fl_ld32(gsta, gc);
-        cnt = fl_ld32(gcnt, gc);
-        if (FL_WAVE < ng) {
-            const uint32_t gc1 = FL_WAVE + ul < ng ? FL_WAVE + ul : glast;
-            rel1 = fl_ld32(grel, gc1);
-            start1 = fl_ld32(gsta, gc1);
-            cnt1 = fl_ld32(gcnt, gc1);
-        }
-        wraw = fl_ld32(wr, (uint32_t)rel);
-    }
-    for (uint32_t gb = 0; gb < ng; gb += FL_WAVE) {
-        const uint32_t g = gb + ul;
-        int rel2 = 0;
-        int32_t start2 = 0, cnt2 = 0;
-        if (gb + 2 * FL_WAVE < ng) {
-            const uint32_t gn = g + 2 * FL_WAVE;
-            const uint32_t gc = gn < ng ? gn : glast;
-            rel2 = fl_ld32(grel, gc);
-            start2 = fl_ld32(gsta, gc);
-            cnt2 = fl_ld32(gcnt, gc);
-        }
-        const float wraw1 = gb + FL_WAVE < ng ? fl_ld32(wr, (uint32_t)rel1) : 0.0f;
-        const bool in = g < ng;
-        const float wv = in ? wraw : 0.0f;
-        if (!in) cnt = 0;
-        int32_t take = tk.kind == TAKE_ALL ? cnt : (tk.kind == TAKE_TH ? (int32_t)group_take(wv, tk.th, tk.cut, start, cnt) : 0);
-        if (Q && tk.kind == TAKE_QUOTA)
-            take = (int32_t)sp_quota_window(tk, wv, cnt, in);
+    struct Win {
+        int rel;
+        int32_t start, cnt;
+        float w;
+    };
+    auto load_rec = [&](Win &x, uint32_t gb) {
+        const uint32_t gn = gb + ul;
+        const uint32_t gc = min(gn, glast);
+        x.rel = fl_ld32(grel, gc);
+        x.start = fl_ld32(gsta, gc);
+        x.cnt = fl_ld32(gcnt, gc);
+    };
+    // Every load is issued, past the side's end at the clamped index, so
+    // that each window waits only for its own loads (a skipped load would
+    // make the wait count depend on the path and the waits cover every load).
+    Win A, B, C;
+    load_rec(A, 0);
+    load_rec(B, FL_WAVE);
+    A.w = fl_ld32(wr, (uint32_t)A.rel);
+    // window gb from cur; nxt holds window gb + 64 (its weights requested
+    // here), nx2 receives window gb + 128
+    auto step = [&](Win &cur, Win &nxt, Win &nx2, uint32_t gb) {
+        load_rec(nx2, gb + 2 * FL_WAVE);
+        nxt.w = fl_ld32(wr, (uint32_t)nxt.rel);
+        __builtin_amdgcn_sched_barrier(0);  // the loads issued before this window's work
+        const bool in = gb + ul < ng;
+        const float wv = in ? cur.w : 0.0f;
+        const int32_t cnt = in ? cur.cnt : 0;
+        int32_t take;
+        if (KIND == TAKE_ALL) take = cnt;
+        else if (KIND == TAKE_TH) take = (int32_t)group_take(wv, tk.th, tk.cut, cur.start, cnt);
+        else take = sp_quota_window(tk, wv, cnt, in);
         if (__ballot(take > 0) != 0) {
             // a window's takes add up to at most the source's edges (int32)
             const int32_t incl = fl_wave_incl_scan_i32(take);
-            fn((long long)take, (int64_t)start, rel, wv, (long long)(base + incl - take));
+            fn((long long)take, (int64_t)cur.start, cur.rel, wv, (long long)(base + incl - take));
             base += __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
         }
-        rel = rel1;
-        start = start1;
-        cnt = cnt1;
-        wraw = wraw1;
-        rel1 = rel2;
-        start1 = start2;
-        cnt1 = cnt2;
+    };
+    for (uint32_t gb = 0;;) {
+        step(A, B, C, gb);
+        if ((gb += FL_WAVE) >= ng) break;
+        step(B, C, A, gb);
+        if ((gb += FL_WAVE) >= ng) break;
+        step(C, A, B, gb);
+        if ((gb += FL_WAVE) >= ng) break;
     }
     return base;
+}
+
+// The walk above for the side's take rule (one code path per rule: no
+// per-window test of the rule).
+template <bool Q, typename F>
+__device__ __forceinline__ int64_t sp_side_runs(const fl_side &s, int64_t g0, int64_t g1, const float *wr,
+                                                SpTake &tk, F &&fn) {
+    if (Q && tk.kind == TAKE_QUOTA) return sp_side_runs_k<TAKE_QUOTA>(s, g0, g1, wr, tk, fn);
+    if (tk.kind == TAKE_ALL) return sp_side_runs_k<TAKE_ALL>(s, g0, g1, wr, tk, fn);
+    return sp_side_runs_k<TAKE_TH>(s, g0, g1, wr, tk, fn);
 }
 
 // Admission order of c2 per (row, side): the relations with a positive
@@ -912,6 +923,7 @@ __global__ __launch_bounds__(SP_ITEMS_NT) void k_sp_items(fl_side ori, fl_side i
 // runs starting inside the round marked in LDS, the owner of slot k the
 // number of marks at 1..k).  rcap: runs per wave the dynamic LDS holds.
 constexpr int64_t SP_FUSE_KMAX = 256;  // budgets whose runs fit the fused kernel's LDS
+constexpr int64_t SP_OFF32_EDGES = (int64_t)1 << 30;  // positions addressed with 32-bit byte offsets
 
 // A run in LDS, one 8-byte record (one LDS store and one load per run):
 // x = first item << 20 | side and identity flags (bits 19, 18) | column,
@@ -1014,14 +1026,37 @@ __global__ __launch_bounds__(SEL_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) 
         if (r0 + 1 < nr && (int32_t)((uint32_t)ru.rec[r0 + 1].x >> SP_LR_FIRST) <= q0 + SP_ICHUNK) ++r0;
         fl_wave_sync();  // marks read before the next round clears them
         const int32_t it = q0 + lane;
-        if (it >= (int32_t)nitems) continue;
-        const float awj = fl_mul(a, fl_ld32(wrow, mj & SP_RUN_COL));
+        const bool live = it < (int32_t)nitems;
+        // the sides of the round's edge items: one side but for the round
+        // that crosses from the ORI runs to the INV runs
+        const bool edge_it = live && !(mj & SP_RUN_ID);
+        const uint64_t inv_items = __ballot(edge_it && (mj & SP_RUN_INV));
+        const uint64_t ori_items = __ballot(edge_it && !(mj & SP_RUN_INV));
+        if (!live) continue;
+        const float wc = fl_ld32(wrow, mj & SP_RUN_COL);  // a * wc formed where it is used
         int32_t dst = -1, pp = -1;
         float val = 0.0f;
         uint32_t tie = SP_TIE_IDENTITY;
+        // an edge item of side s (wave-uniform: its arrays from scalar bases
+        // and 32-bit byte offsets, for sides of fewer than 2^30 positions)
+        auto side_item = [&](const fl_side &s, bool inv_side) {
+            if ((uint32_t)pj < (uint32_t)s.edges) {
+                const int32_t e = fl_ld32(s.col_ind, (uint32_t)pj);  // requested before the mask
+                const float m = s.mask_bits ? (((fl_ld32(s.mask_bits, (uint32_t)pj >> 5) >> (pj & 31)) & 1u) ? 1.0f : 0.0f)
+                                            : fl_ld32(s.mask, (uint32_t)pj);
+                dst = (!holes || m != 0.0f) ? e : -1;
+                val = fl_mul(fl_mul(a, wc), m);
+                if (MAXT) tie = (inv_side ? SP_TIE_INV : 0u) | (uint32_t)fl_ld32(s.order, (uint32_t)pj);
+                pp = pj;
+            }
+        };
         if (mj & SP_RUN_ID) {
             dst = pj;
-            val = awj;
+            val = fl_mul(a, wc);
+        } else if (inv_items == 0 && ori.edges < SP_OFF32_EDGES) {
+            side_item(ori, false);
+        } else if (ori_items == 0 && inv.edges < SP_OFF32_EDGES) {
+            side_item(inv, true);
         } else {
             const bool inv_side = (mj & SP_RUN_INV) != 0;
             const uint32_t edges = (uint32_t)(inv_side ? inv.edges : ori.edges);
@@ -1032,7 +1067,7 @@ __global__ __launch_bounds__(SEL_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) 
                 const float m = sp_mask_at(mb, mk, pj);
                 const int32_t e = ci[pj];
                 dst = (!holes || m != 0.0f) ? e : -1;
-                val = fl_mul(awj, m);
+                val = fl_mul(fl_mul(a, wc), m);
                 if (MAXT) tie = (inv_side ? SP_TIE_INV : 0u) | (uint32_t)(inv_side ? inv.order : ori.order)[pj];
                 pp = pj;
             }
