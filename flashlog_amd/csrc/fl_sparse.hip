@@ -217,25 +217,35 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     const uint32_t ng = (uint32_t)(g1 - g0);  // at most 32767: one group per relation
     const int16_t *__restrict__ grel = s.group_rel + g0;
     const int32_t *__restrict__ gcnt = s.group_count + g0;
+    // per lane: capacity and eligible groups in 32 bits (at most the
+    // source's edges on the side), and the smallest and largest eligible
+    // weight as bit patterns (positive floats order as their bits); the
+    // place value of the lowest mantissa bit and the exponent are both
+    // nondecreasing in the weight, so their extremes come from these two
     double ws = 0.0;
-    long long cap = 0, nel = 0;
-    int emin = 1 << 20, emax = -(1 << 20);
+    int32_t cap32 = 0, nel32 = 0;
+    uint32_t umin = 0xFFFFFFFFu, umax = 0u;
     sp_quota_groups(grel, gcnt, ng, wr, [&](float wv, int32_t c) {
-        cap += c;
-        ++nel;
+        cap32 += c;
+        ++nel32;
         ws = __dadd_rn(ws, (double)wv);
-        const int lo = sp_lsb_exp(wv), hi = (int)((__float_as_uint(wv) >> 23) & 0xFF) - 127;
-        emin = lo < emin ? lo : emin;
-        emax = hi > emax ? hi : emax;
+        const uint32_t u = __float_as_uint(wv);
+        umin = min(umin, u);
+        umax = max(umax, u);
     });
-    cap = fl_wave_sum_i64(cap);
-    nel = fl_wave_sum_i64(nel);
+    // wave totals in 32 bits: at most the source's edges on the side
+    const long long cap = fl_wave_sum_i32(cap32);
+    const long long nel = fl_wave_sum_i32(nel32);
 #pragma unroll
     for (int o = FL_WAVE / 2; o > 0; o >>= 1) {
         ws = __dadd_rn(ws, __shfl_xor(ws, o, FL_WAVE));
-        const int a = __shfl_xor(emin, o, FL_WAVE), c = __shfl_xor(emax, o, FL_WAVE);
-        emin = a < emin ? a : emin;
-        emax = c > emax ? c : emax;
+        umin = min(umin, (uint32_t)__shfl_xor((int)umin, o, FL_WAVE));
+        umax = max(umax, (uint32_t)__shfl_xor((int)umax, o, FL_WAVE));
+    }
+    int emin = 1 << 20, emax = -(1 << 20);
+    if (nel > 0) {
+        emin = sp_lsb_exp(__uint_as_float(umin));
+        emax = (int)((umax >> 23) & 0xFF) - 127;
     }
     int lg = 0;
     while ((1ll << lg) < nel) ++lg;
@@ -267,9 +277,9 @@ __device__ SpQuota sp_quota_setup(const fl_side &s, int64_t g0, int64_t g1, cons
     tk.wsum = fl_uniform_f64(ws);
     tk.wsum_r = __ddiv_rn(1.0, tk.wsum);
     tk.target = (int32_t)q.target;
-    long long alloc = 0;
-    sp_quota_groups(grel, gcnt, ng, wr, [&](float wv, int32_t c) { alloc += sp_quota_base(tk, wv, c); });
-    alloc = fl_wave_sum_i64(alloc);
+    int32_t alloc32 = 0;  // at most the lane's capacity
+    sp_quota_groups(grel, gcnt, ng, wr, [&](float wv, int32_t c) { alloc32 += sp_quota_base(tk, wv, c); });
+    const long long alloc = fl_wave_sum_i32(alloc32);
     q.residual = q.target - alloc;
     q.spare = cap - alloc;
     return q;
