@@ -2598,24 +2598,33 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
     const int64_t k0 = item_off[i], k1 = item_off[i + 1];
     const bool edge_grads = ori.grad_edge || inv.grad_edge;
     float gsp = 0.0f;
-    int32_t p = -1, loc = -1;
-    int col = -1;
     // without positions every kept item has mask 1 (the holes, the masked
-    // items, carry output index -1) and there are no edge factors
-    if (k0 + lane < k1) {
-        p = raw_pos ? raw_pos[k0 + lane] : -1;
-        col = raw_col[k0 + lane];
-        loc = raw_out[k0 + lane];
-    }
-    for (int64_t kb = k0; kb < k1; kb += FL_WAVE) {
-        const int64_t kn = kb + FL_WAVE + lane;
-        int32_t pn = -1, locn = -1;
-        int coln = -1;
-        if (kn < k1) {
-            pn = raw_pos ? raw_pos[kn] : -1;
-            coln = raw_col[kn];
-            locn = raw_out[kn];
-        }
+    // items, carry output index -1) and there are no edge factors.
+    //   The next round's records are requested before this round's gathers;
+    // the two rounds' registers alternate between two sets (the loop body
+    // holds two rounds) and every load is issued, past the entry's end at
+    // its last item, so that a round waits only for the loads issued a round
+    // earlier (lanes past the end take no part: -1 where the round uses them)
+    struct Rec {
+        int32_t p, loc;
+        int col;
+    };
+    // has_pos: raw_pos given (a compile-time branch, so that no load is
+    // conditional inside the loop)
+    auto load = [&](Rec &x, int64_t kb, auto has_pos) {
+        const int64_t k = kb + lane;
+        const int64_t kc = k < k1 ? k : k1 - 1;
+        if constexpr (decltype(has_pos)::value) x.p = raw_pos[kc];
+        else x.p = -1;
+        x.col = raw_col[kc];
+        x.loc = raw_out[kc];
+    };
+    auto do_round = [&](const Rec &cur, Rec &nxt, int64_t kb, auto has_pos) {
+        load(nxt, kb + FL_WAVE, has_pos);
+        __builtin_amdgcn_sched_barrier(0);  // the next round's loads issued first
+        const bool in = kb + lane < k1;
+        const int32_t p = in ? cur.p : -1, loc = in ? cur.loc : -1;
+        const int col = in ? cur.col : -1;
         float gwv = 0.0f;
         const bool iv = p >= 0 && col >= r_size;
         const float m =
@@ -2650,9 +2659,20 @@ __device__ __forceinline__ void sp_bwd_entry(fl_side ori, fl_side inv, const int
         const int next1 = fl_dpp<0x130>(col + 1);  // wave_shl:1, lane 63 receives 0
         const bool tail = next1 != col + 1;
         if (col >= 0 && tail) gdst[col] = fl_add(gdst[col], x);
-        p = pn;
-        col = coln;
-        loc = locn;
+    };
+    auto walk = [&](auto has_pos) {
+        Rec A, B;
+        load(A, k0, has_pos);
+        for (int64_t kb = k0;;) {
+            do_round(A, B, kb, has_pos);
+            if ((kb += FL_WAVE) >= k1) break;
+            do_round(B, A, kb, has_pos);
+            if ((kb += FL_WAVE) >= k1) break;
+        }
+    };
+    if (k0 < k1) {
+        if (raw_pos) walk(std::true_type{});
+        else walk(std::false_type{});
     }
     gsp = fl_wave_sum_f32(gsp);
     if (lane == 0) grad_v[i] = gsp;
