@@ -3631,8 +3631,17 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
     // value array (dead after the partition), mapped back by k_sp_local_to_out
     int32_t *acc_local = raw_local && NB > 1 ? reinterpret_cast<int32_t *>(x.raw_val) : raw_local;
     // hot buckets (more than one LDS chunk) are listed by the first kernel
-    // and taken by a persistent grid of the second
-    const unsigned hot_grid = (unsigned)(R * NB < SP_HOT_GRID ? R * NB : SP_HOT_GRID);
+    // and taken by a persistent grid of the second.  The persistent grids
+    // are no larger than their lists can be (a bucket holds at most the
+    // hop's items: at most items / (SP_CHUNK + 1) hot buckets and items /
+    // (SP_WB + 1) hot and mid ones), so that a small hop launches a few
+    // workgroups, not thousands that find nothing to claim
+    const int64_t hot_cap = h->items / (SP_CHUNK + 1) + 1, mid_cap = h->items / (SP_WB + 1) + 1;
+    int64_t hot_g = R * NB < SP_HOT_GRID ? R * NB : SP_HOT_GRID;
+    if (hot_g > hot_cap) hot_g = hot_cap;
+    int64_t mid_g = R * NB < SP_MID_GRID ? R * NB : SP_MID_GRID;
+    if (mid_g > mid_cap) mid_g = mid_cap;
+    const unsigned hot_grid = (unsigned)hot_g;
     if (R * NB > 0)
         FL_LAUNCH("k_fill_i32", k_fill_i32, dim3(1), dim3(64), 0, st, x.hot_count, (int64_t)8, 0);
     if (R * NB > 0 && mx) {
@@ -3647,10 +3656,10 @@ int fl_sparse_expand(void *stream, const fl_side *ori, const fl_side *inv, const
                   dst_arr, val_arr, acc_local, x.out_count, nslot, x.hot_list, x.mid_list, x.mid_fb, x.hot_count);
         // buckets of more than SP_WB items: few destinations here, the rest
         // on the fallback lists
-        FL_LAUNCH("k_sp_accum_few", k_sp_accum_few, dim3((unsigned)(nslot < SP_MID_GRID ? nslot : SP_MID_GRID)),
+        FL_LAUNCH("k_sp_accum_few", k_sp_accum_few, dim3((unsigned)mid_g),
                   dim3(SP_NT), 0, st, rows, x.base, dst_arr, val_arr, acc_local, x.out_count, x.hot_list,
                   x.mid_list, x.hot_fb, x.mid_fb, x.hot_count);
-        FL_LAUNCH("k_sp_accum_mid", k_sp_accum_mid, dim3((unsigned)(nslot < SP_MID_GRID ? nslot : SP_MID_GRID)),
+        FL_LAUNCH("k_sp_accum_mid", k_sp_accum_mid, dim3((unsigned)mid_g),
                   dim3(SP_NT), 0, st, rows, x.base, dst_arr, val_arr, acc_local, x.out_count, x.mid_fb,
                   x.hot_count + 6);
         FL_LAUNCH("k_sp_accum_hot", k_sp_accum_hot, dim3(hot_grid), dim3(SP_NT), 0, st, rows, x.base, dst_arr,
