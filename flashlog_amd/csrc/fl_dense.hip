@@ -863,16 +863,32 @@ __global__ __launch_bounds__(PULL_NT) void k_pull_max(
 // of one side, each segment's best key per row (max_slots over the
 // segments' slots -- segment j holds [seg_start, seg_start + FL_SEG) clipped
 // to its destination's end -- cell = segment within the chunk), stored to
-// sb[segment][row].
+// sb[segment][row].  STAGED: the chunk's slots -- source, position,
+// relation, mask, cell and the source's row words -- are first read into LDS
+// (one slot per thread, the loads of every slot in flight together), so a
+// task (slot, row word) reads only its rows' weights and records from
+// global memory.
 constexpr int SEGS_PER_WG = 8;
+constexpr int SEG_SLOTS = SEGS_PER_WG * FL_SEG;  // slots of one chunk, at most
 
+// Dynamic LDS of the staged k_seg_max: the cells and the slots' row words.
+inline size_t seg_max_lds_bytes(int64_t BL, bool staged) {
+    return sizeof(uint64_t) * SEGS_PER_WG * (size_t)BL +
+           (staged ? sizeof(uint32_t) * SEG_SLOTS * (size_t)((BL + 31) / 32) : 0);
+}
+
+template <bool STAGED>
 __global__ __launch_bounds__(PULL_NT) void k_seg_max(fl_side ori, fl_side inv, const float *__restrict__ w,
                                                      int64_t BL, int64_t E, int64_t n, int64_t r_size,
                                                      const uint32_t *__restrict__ BM, const float2 *__restrict__ PK,
                                                      const int32_t *__restrict__ CUT, uint64_t *__restrict__ sb_ori,
                                                      uint64_t *__restrict__ sb_inv) {
-    extern __shared__ uint64_t cells[];  // [SEGS_PER_WG][BL]
+    extern __shared__ uint64_t cells[];  // [SEGS_PER_WG][BL], then (STAGED) [SEG_SLOTS][nw] row words
     __shared__ int32_t first[SEGS_PER_WG], pre[SEGS_PER_WG + 1];
+    __shared__ int32_t st_src[STAGED ? SEG_SLOTS : 1], st_pos[STAGED ? SEG_SLOTS : 1];
+    __shared__ int16_t st_rel[STAGED ? SEG_SLOTS : 1];
+    __shared__ uint8_t st_c[STAGED ? SEG_SLOTS : 1];
+    __shared__ float st_m[STAGED ? SEG_SLOTS : 1];
     const int64_t nwg_ori = (ori.nseg + SEGS_PER_WG - 1) / SEGS_PER_WG;
     const int dir = (int64_t)blockIdx.x >= nwg_ori;
     const fl_side &s = dir ? inv : ori;
@@ -894,7 +910,7 @@ __global__ __launch_bounds__(PULL_NT) void k_seg_max(fl_side ori, fl_side inv, c
         if (j == 0) pre[0] = 0;
     }
     __syncthreads();
-    max_slots(s, pre[ns], dir, BL, E, n, dir ? r_size : 0, w, BM, PK, CUT, cells, [&](int64_t k, int32_t *sl, int *c) {
+    auto slot_of = [&](int64_t k, int32_t *sl, int *c) {
         int lo = 0, hi = ns;  // the segment: pre[lo] <= k < pre[lo + 1]
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
@@ -903,7 +919,67 @@ __global__ __launch_bounds__(PULL_NT) void k_seg_max(fl_side ori, fl_side inv, c
         }
         *sl = first[lo] + (int32_t)(k - pre[lo]);
         *c = lo;
-    });
+    };
+    if constexpr (!STAGED) {
+        max_slots(s, pre[ns], dir, BL, E, n, dir ? r_size : 0, w, BM, PK, CUT, cells, slot_of);
+    } else {
+        const int64_t nw = (BL + 31) / 32;
+        uint32_t *st_w = reinterpret_cast<uint32_t *>(cells + SEGS_PER_WG * BL);  // [SEG_SLOTS][nw]
+        const int nslot = pre[ns];  // at most SEG_SLOTS
+        for (int k = threadIdx.x; k < nslot; k += PULL_NT) {
+            int32_t sl;
+            int c;
+            slot_of(k, &sl, &c);
+            const int32_t src = s.pull_src[sl], pos = s.pull_pos[sl];
+            st_src[k] = src;
+            st_pos[k] = pos;
+            st_rel[k] = s.pull_rel[sl];
+            st_c[k] = (uint8_t)c;
+            st_m[k] = s.mask[pos];
+            for (int64_t wi = 0; wi < nw; ++wi) st_w[k * nw + wi] = BM[wi * E + src];
+        }
+        __syncthreads();
+        const int64_t plane = (int64_t)dir * E * BL;
+        const float *wb = w + (dir ? r_size : 0);
+        for (int64_t t = threadIdx.x; t < (int64_t)nslot * nw; t += PULL_NT) {
+            const int64_t k = t / nw, wi = t - k * nw;
+            uint32_t bits = st_w[t];  // = st_w[k * nw + wi]
+            if (!bits) continue;
+            const float m = st_m[k];
+            if (m == 0.0f) continue;
+            const int32_t src = st_src[k], pos = st_pos[k];
+            uint64_t *crow = cells + (int64_t)st_c[k] * BL;
+            const float *wc = wb + st_rel[k];
+            const int64_t at0 = plane + (int64_t)src * BL;
+            // the word's active rows 8 at a time (as max_slots)
+            while (bits) {
+                int64_t bl[8];
+                float wv[8];
+                float2 rc[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    bl[j] = -1;
+                    wv[j] = 0.0f;
+                    rc[j] = make_float2(0.0f, 0.0f);
+                    if (bits) {
+                        bl[j] = wi * 32 + __ffs(bits) - 1;
+                        bits &= bits - 1;
+                        wv[j] = wc[bl[j] * n];
+                        rc[j] = PK[at0 + bl[j]];
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (bl[j] < 0 || !(wv[j] > 0.0f)) continue;
+                    bool kept = wv[j] > rc[j].y;
+                    if (!kept && wv[j] == rc[j].y) kept = pos < CUT[at0 + bl[j]];
+                    if (kept)
+                        atomicMax((unsigned long long *)&crow[bl[j]],
+                                  (unsigned long long)max_key(fl_mul(fl_mul(rc[j].x, wv[j]), m), pos));
+                }
+            }
+        }
+    }
     __syncthreads();
     uint64_t *sb = (dir ? sb_inv : sb_ori) + seg0 * BL;
     for (int64_t i = threadIdx.x; i < (int64_t)ns * BL; i += PULL_NT) sb[i] = cells[i];
@@ -1628,8 +1704,11 @@ int fl_dense_max_forward(void *stream, const fl_side *ori, const fl_side *inv, c
     const int64_t nq_seg = (ori->nseg + inv->nseg) * BL;
     if (nq_seg > 0) {
         const int64_t nwg = (ori->nseg + SEGS_PER_WG - 1) / SEGS_PER_WG + (inv->nseg + SEGS_PER_WG - 1) / SEGS_PER_WG;
-        FL_LAUNCH("k_seg_max", k_seg_max, dim3((unsigned)nwg), dim3(PULL_NT), sizeof(uint64_t) * SEGS_PER_WG * BL,
-                  st, *ori, *inv, w, BL, E, n, r_size, ws.bm, ws.pk, ws.cut, sb_ori, sb_inv);
+        // the staged form while its LDS stays within 64 KiB (BL up to 640)
+        const bool staged = seg_max_lds_bytes(BL, true) + 4096 <= 65536;
+        FL_LAUNCH("k_seg_max", staged ? k_seg_max<true> : k_seg_max<false>, dim3((unsigned)nwg), dim3(PULL_NT),
+                  seg_max_lds_bytes(BL, staged), st, *ori, *inv, w, BL, E, n, r_size, ws.bm, ws.pk, ws.cut, sb_ori,
+                  sb_inv);
         const int64_t nq_sup = (ori->nsup + inv->nsup) * BL;
         if (nq_sup > 0)
             FL_LAUNCH("k_sup_max", k_sup_max, dim3((unsigned)((nq_sup + PULL_NT - 1) / PULL_NT)), dim3(PULL_NT), 0,
