@@ -485,10 +485,12 @@ __device__ __forceinline__ int64_t sp_find_group(const fl_side &s, int64_t g0, i
 }
 
 __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, const float *wr, int64_t K,
-                                      const int16_t *__restrict__ ord, int ne, int *cmap, float *thv_out,
-                                      int32_t *ct_out) {
+                                      const int16_t *__restrict__ ord, int ne, int *cmap, int64_t r_size,
+                                      float *thv_out, int32_t *ct_out) {
     const int lane = fl_lane();
     if (cmap) {
+        // four windows of group records in flight per round
+#pragma unroll 4
         for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) cmap[s.group_rel[g]] = s.group_count[g];
         fl_wave_sync();
     }
@@ -520,8 +522,9 @@ __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, 
         carry += __shfl(incl, FL_WAVE - 1, FL_WAVE);
     }
     if (cmap) {
+        // the whole map cleared from LDS alone (no second read of the records)
         fl_wave_sync();
-        for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) cmap[s.group_rel[g]] = 0;
+        for (int64_t q = lane; q < r_size; q += FL_WAVE) cmap[q] = 0;
         fl_wave_sync();
     }
     if (hit_rel >= 0) {
@@ -599,7 +602,8 @@ __global__ __launch_bounds__(SEL_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) 
                     c += wr[s.group_rel[g]] > 0.0f ? s.group_count[g] : 0;
             } else {
                 const int64_t ro = (sb[i] * L + sl[i]) * 2 + dir;
-                c = sp_select_lookup(s, g0, g1, wr, K, rel_order + ro * r_size, rel_nelig[ro], cmap, &thv, &ct);
+                c = sp_select_lookup(s, g0, g1, wr, K, rel_order + ro * r_size, rel_nelig[ro], cmap, r_size, &thv,
+                                     &ct);
             }
         } else {
             uint32_t key;
