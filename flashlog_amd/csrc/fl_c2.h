@@ -84,6 +84,79 @@ static __device__ bool c2_select(const fl_side &s, int64_t g0, int64_t g1, const
     return true;
 }
 
+// c2_select for a side of at most one window of groups: lane j reads group
+// g0 + j once and every pass (the total, the four radix passes and the cut)
+// works from registers.  Same threshold and cut as the general form.  (The
+// dense hard-case kernel takes it; in the sparse selection, whose sides
+// mostly stop at the total, it measured slower.)
+static __device__ bool c2_select_window(const fl_side &s, int64_t g0, int64_t g1, const float *wrow, int64_t K,
+                                        int *hist, uint32_t *th_key, int32_t *cut) {
+    const int lane = fl_lane();
+    const int64_t g = g0 + lane;
+    float wv = 0.0f;
+    int cnt = 0, st = 0;
+    if (g < g1) {
+        wv = wrow[s.group_rel[g]];
+        cnt = s.group_count[g];
+        st = s.group_start[g];
+    }
+    const bool el = wv > 0.0f;  // (groups past the end have wv 0)
+    const uint32_t k = __float_as_uint(wv);
+    const long long tot = fl_wave_sum_i64(el ? cnt : 0);
+    if (tot <= K) return false;
+    int need = (int)K;
+    uint32_t prefix = 0, pmask = 0;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[lane * 4 + 0] = 0; hist[lane * 4 + 1] = 0;
+        hist[lane * 4 + 2] = 0; hist[lane * 4 + 3] = 0;
+        __builtin_amdgcn_wave_barrier();
+        if (el && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255], cnt);
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const int owner = FL_WAVE - 1 - lane;
+        int h[4];
+        int v = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { h[q] = hist[owner * 4 + q]; v += h[q]; }
+        int incl = fl_wave_incl_scan_i32(v);
+        int above = incl - v;
+        int found = 0, digit = 0, nneed = 0;
+#pragma unroll
+        for (int q = 3; q >= 0; --q) {
+            if (!found && above < need && need <= above + h[q]) { found = 1; digit = owner * 4 + q; nneed = need - above; }
+            above += h[q];
+        }
+        unsigned long long bal = __ballot(found);
+        int src_lane = __ffsll((long long)bal) - 1;
+        digit = __shfl(digit, src_lane, FL_WAVE);
+        nneed = __shfl(nneed, src_lane, FL_WAVE);
+        prefix |= (uint32_t)digit << shift;
+        pmask |= 0xFFu << shift;
+        need = nneed;
+        __builtin_amdgcn_wave_barrier();
+    }
+    // cut: first tied group whose cumulative tie count passes `need`
+    const int tc = (el && k == prefix) ? cnt : 0;
+    const int incl = fl_wave_incl_scan_i32(tc);
+    const int before = incl - tc;
+    const unsigned long long bal = __ballot(tc > 0 && before + tc > need);
+    int32_t c = 0x7FFFFFFF;
+    if (bal) {
+        const int hl = __ffsll((long long)bal) - 1;
+        c = __shfl(st + (need - before), hl, FL_WAVE);
+    }
+    *th_key = prefix;
+    *cut = c;
+    return true;
+}
+
+// c2_select, with sides of at most one window from registers.
+static __device__ bool c2_select_fast(const fl_side &s, int64_t g0, int64_t g1, const float *wrow, int64_t K,
+                                      int *hist, uint32_t *th_key, int32_t *cut) {
+    if (g1 - g0 <= FL_WAVE) return c2_select_window(s, g0, g1, wrow, K, hist, th_key, cut);
+    return c2_select(s, g0, g1, wrow, K, hist, th_key, cut);
+}
+
 // Kept range of group g for (source, row): [start, start + take).
 __device__ __forceinline__ int64_t group_take(float wv, float th, int32_t cut, int64_t start, int64_t count) {
     if (!(wv > 0.0f)) return 0;

@@ -316,7 +316,7 @@ __global__ __launch_bounds__(C2_NT) void k_c2_hard(fl_side ori, fl_side inv, con
             const fl_side &s = dir ? inv : ori;
             const int64_t g0 = s.row_group_ptr[src], g1 = s.row_group_ptr[src + 1];
             uint32_t k2; int32_t c2;
-            if (c2_select(s, g0, g1, w + bl * n + (dir ? r_size : 0), K, hist, &k2, &c2) && lane == 0) {
+            if (c2_select_fast(s, g0, g1, w + bl * n + (dir ? r_size : 0), K, hist, &k2, &c2) && lane == 0) {
                 const int64_t at = ((int64_t)dir * E + src) * BL + bl;
                 PK[at].y = __uint_as_float(k2);
                 CUT[at] = c2;
