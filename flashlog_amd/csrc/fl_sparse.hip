@@ -494,13 +494,18 @@ __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, 
         for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) cmap[s.group_rel[g]] = s.group_count[g];
         fl_wave_sync();
     }
-    long long carry = 0;
+    // counts in 32 bits: the source's edges on the side (more than K here)
+    // are CSR positions; the next window of the order is requested before
+    // this one is counted (two alternating registers, every load issued at
+    // an index clamped to the order's end)
+    int32_t carry = 0;
     int hit_rel = -1;
-    long long hit_before = 0;
-    for (int k0 = 0; k0 < ne; k0 += FL_WAVE) {
-        const int kk = k0 + lane;
-        const int rel = kk < ne ? (int)ord[kk] : -1;
-        long long cnt = 0;
+    int32_t hit_before = 0;
+    const int32_t K32 = (int32_t)K;
+    auto ord_at = [&](int k0) { return ne > 0 ? (int)ord[min(k0 + lane, ne - 1)] : -1; };
+    auto window = [&](int k0, int rel_raw) {  // true: the K-th edge is in this window
+        const int rel = k0 + lane < ne ? rel_raw : -1;
+        int32_t cnt = 0;
         if (rel >= 0) {
             if (cmap) {
                 cnt = cmap[rel];
@@ -509,17 +514,27 @@ __device__ long long sp_select_lookup(const fl_side &s, int64_t g0, int64_t g1, 
                 cnt = g >= 0 ? s.group_count[g] : 0;
             }
         }
-        const long long incl = fl_wave_incl_scan_i64(cnt);
-        const long long before = carry + incl - cnt;
-        const bool hit = cnt > 0 && before < K && before + cnt >= K;
+        const int32_t incl = fl_wave_incl_scan_i32(cnt);
+        const int32_t before = carry + incl - cnt;
+        const bool hit = cnt > 0 && before < K32 && before + cnt >= K32;
         const unsigned long long bal = __ballot(hit);
         if (bal) {
             const int hl = __ffsll((long long)bal) - 1;
             hit_rel = __shfl(rel, hl, FL_WAVE);
             hit_before = __shfl(before, hl, FL_WAVE);
-            break;
+            return true;
         }
-        carry += __shfl(incl, FL_WAVE - 1, FL_WAVE);
+        carry += __builtin_amdgcn_readlane(incl, FL_WAVE - 1);
+        return false;
+    };
+    int ra = ord_at(0), rb = 0;
+    for (int k0 = 0; k0 < ne;) {
+        rb = ord_at(k0 + FL_WAVE);
+        if (window(k0, ra)) break;
+        if ((k0 += FL_WAVE) >= ne) break;
+        ra = ord_at(k0 + FL_WAVE);
+        if (window(k0, rb)) break;
+        k0 += FL_WAVE;
     }
     if (cmap) {
         // the whole map cleared from LDS alone (no second read of the records)
@@ -598,6 +613,7 @@ __global__ __launch_bounds__(SEL_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) 
             // has at most K, else the admission-order lookup
             const int64_t deg = (int64_t)s.group_start[g1 - 1] + s.group_count[g1 - 1] - s.group_start[g0];
             if (deg <= K) {
+#pragma unroll 4
                 for (int64_t g = g0 + lane; g < g1; g += FL_WAVE)
                     c += wr[s.group_rel[g]] > 0.0f ? s.group_count[g] : 0;
             } else {
