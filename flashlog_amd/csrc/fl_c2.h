@@ -157,6 +157,18 @@ static __device__ bool c2_select_fast(const fl_side &s, int64_t g0, int64_t g1, 
     return c2_select(s, g0, g1, wrow, K, hist, th_key, cut);
 }
 
+// group_take in 32 bits (CSR positions and group sizes are int32, so the
+// tie difference cut - start cannot overflow).
+__device__ __forceinline__ int32_t group_take32(float wv, float th, int32_t cut, int32_t start, int32_t count) {
+    if (!(wv > 0.0f)) return 0;
+    if (wv > th) return count;
+    if (wv == th) {
+        const int32_t t = cut - start;
+        return t <= 0 ? 0 : (t < count ? t : count);
+    }
+    return 0;
+}
+
 // Kept range of group g for (source, row): [start, start + take).
 __device__ __forceinline__ int64_t group_take(float wv, float th, int32_t cut, int64_t start, int64_t count) {
     if (!(wv > 0.0f)) return 0;

@@ -382,7 +382,7 @@ __device__ __forceinline__ int64_t sp_side_runs_k(const fl_side &s, int64_t g0, 
         const int32_t cnt = in ? cur.cnt : 0;
         int32_t take;
         if (KIND == TAKE_ALL) take = cnt;
-        else if (KIND == TAKE_TH) take = (int32_t)group_take(wv, tk.th, tk.cut, cur.start, cnt);
+        else if (KIND == TAKE_TH) take = group_take32(wv, tk.th, tk.cut, cur.start, cnt);
         else take = sp_quota_window(tk, wv, cnt, in);
         if (__ballot(take > 0) != 0) {
             // a window's takes add up to at most the source's edges (int32)
@@ -646,10 +646,8 @@ __global__ __launch_bounds__(SEL_NT) __attribute__((amdgpu_waves_per_eu(8, 8))) 
                 c = lane == 0 ? eligible : 0;
             } else {
                 // kept edges, masked ones included
-                for (int64_t g = g0 + lane; g < g1; g += FL_WAVE) {
-                    const int64_t start = s.group_start[g];
-                    c += group_take(wr[s.group_rel[g]], thv, ct, start, s.group_count[g]);
-                }
+                for (int64_t g = g0 + lane; g < g1; g += FL_WAVE)
+                    c += group_take32(wr[s.group_rel[g]], thv, ct, s.group_start[g], s.group_count[g]);
             }
         }
         c = fl_wave_sum_i64(c);
