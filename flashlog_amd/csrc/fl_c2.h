@@ -151,8 +151,8 @@ static __device__ bool c2_select_window(const fl_side &s, int64_t g0, int64_t g1
 }
 
 // c2_select, with sides of at most one window from registers.
-static __device__ bool c2_select_fast(const fl_side &s, int64_t g0, int64_t g1, const float *wrow, int64_t K,
-                                      int *hist, uint32_t *th_key, int32_t *cut) {
+static __device__ __forceinline__ bool c2_select_fast(const fl_side &s, int64_t g0, int64_t g1, const float *wrow,
+                                                      int64_t K, int *hist, uint32_t *th_key, int32_t *cut) {
     if (g1 - g0 <= FL_WAVE) return c2_select_window(s, g0, g1, wrow, K, hist, th_key, cut);
     return c2_select(s, g0, g1, wrow, K, hist, th_key, cut);
 }

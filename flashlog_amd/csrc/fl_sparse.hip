@@ -1207,7 +1207,6 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
     constexpr int TAB = SP_ND * (SPAN + 1);           // one buffer, padded
     constexpr int PER = SP_ND * SPAN / NT;            // scanned entries per thread
     const int t = threadIdx.x;
-    const int lane = fl_lane();
     const int w = fl_wave_id();
     uint16_t *tab = cnt, *nxt = TWO_TABLES ? cnt + TAB : cnt;
     for (int q = t; q < TAB; q += NT) tab[q] = 0;
@@ -1854,7 +1853,6 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
                                            const int32_t *slot_dl, uint16_t (*tab)[SP_FEW_TAB], float *sv,
                                            int *scan_lds) {
     const int t = threadIdx.x;
-    const int lane = fl_lane();
     const int w = fl_wave_id();
     for (int q = t; q < SP_FEW_TAB; q += SP_NT) tab[0][q] = 0;
     float acc = 0.0f;  // thread t < total: the sum of slot t
@@ -2336,7 +2334,7 @@ __global__ __launch_bounds__(SP_EMIT_WAVES * FL_WAVE) void k_sp_emit(SpRows rows
     for (int s_ = 0; s_ < SP_EMIT_SLOTS / SP_EMIT_WAVES; ++s_) {
     const int64_t slot = g * SP_EMIT_SLOTS + (int64_t)s_ * SP_EMIT_WAVES + fl_wave_id();
     if (slot >= nslot) return;
-    const int64_t r = slot / rows.NB, bk = slot - r * rows.NB;
+    const int64_t r = slot / rows.NB;
     const int64_t o0 = out_base[slot];
     const int64_t cnt = out_base[slot + 1] - o0;
     if (cnt == 0) continue;
