@@ -2388,10 +2388,12 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
     const int c = (int)((i1e - i0) < SP_TILE ? (i1e - i0) : SP_TILE);
     const int64_t *orow = out_base + r * rows.NB;
     // the row's bucket bases in LDS when they fit (one load each per tile)
-    __shared__ int64_t obase[SP_LTO_NB];
+    // (32-bit: output indices are below the item count, which the expand
+    // holds below 2^31 when a map is made)
+    __shared__ int32_t obase[SP_LTO_NB];
     const bool lds = rows.NB <= SP_LTO_NB;
     if (lds) {
-        for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) obase[q] = orow[q];
+        for (int64_t q = threadIdx.x; q < rows.NB; q += SP_NT) obase[q] = (int32_t)orow[q];
         __syncthreads();
     }
     // the tile's items from wave-uniform bases, 32-bit offsets
@@ -2417,7 +2419,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
         for (int j = 0; j < Q; ++j) {
             const uint32_t idx = (uint32_t)(j * SP_NT) + threadIdx.x;
             if (idx < (uint32_t)c)
-                fl_st32(tloc, idx, ll[j] >= 0 ? (int32_t)(obase[(uint32_t)qq[j] >> pos_bits] + ll[j]) : -1);
+                fl_st32(tloc, idx, ll[j] >= 0 ? obase[(uint32_t)qq[j] >> pos_bits] + ll[j] : -1);
         }
         return;
     }
@@ -2437,7 +2439,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
             const uint32_t idx = (uint32_t)(j * SP_NT) + threadIdx.x;
-            fl_st32(tloc, idx, qq[j] >= 0 ? (int32_t)(obase[dd[j] >> SP_S] + qq[j]) : -1);
+            fl_st32(tloc, idx, qq[j] >= 0 ? obase[dd[j] >> SP_S] + qq[j] : -1);
         }
         return;
     }
@@ -2450,7 +2452,7 @@ __global__ __launch_bounds__(SP_NT) void k_sp_local_to_out(int64_t R, SpRows row
             int32_t o = -1;
             if (d >= 0) {
                 const int32_t loc = part_local[fl_ld32(tinv, idx)];
-                if (loc >= 0) o = (int32_t)((lds ? obase[d >> SP_S] : orow[d >> SP_S]) + loc);
+                if (loc >= 0) o = (int32_t)((lds ? (int64_t)obase[d >> SP_S] : orow[d >> SP_S]) + loc);
             }
             fl_st32(tloc, idx, o);
         } else {
