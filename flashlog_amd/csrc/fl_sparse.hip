@@ -1303,14 +1303,19 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
     const int64_t i1e = rows.row_item0[r + 1];
     const int c = (int)((i1e - i0) < SP_TILE ? (i1e - i0) : SP_TILE);
     const int t = threadIdx.x;
+    // a tile holds at least one item (a row has ceil(items / SP_TILE) tiles),
+    // so every destination is requested at once at an index clamped to c - 1
+    int32_t dk[SP_PT_IPT];
 #pragma unroll
     for (int j = 0; j < SP_PT_IPT; ++j) {
-        const int idx = t * SP_PT_IPT + j;
+        const int idx = j * SP_PT_NT + t;
+        dk[j] = fl_ld32(raw_dst + i0, (uint32_t)(idx < c ? idx : c - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < SP_PT_IPT; ++j) {
+        const int idx = j * SP_PT_NT + t;
         uint32_t key = 0xFFFFF000u | (uint32_t)idx;  // padding and holes sort last
-        if (idx < c) {
-            const int32_t d = fl_ld32(raw_dst + i0, (uint32_t)idx);
-            if (d >= 0) key = ((uint32_t)(d >> SP_S) << 12) | (uint32_t)idx;
-        }
+        if (idx < c && dk[j] >= 0) key = ((uint32_t)(dk[j] >> SP_S) << 12) | (uint32_t)idx;
         kb[0][idx] = key;
     }
     __syncthreads();
@@ -1325,39 +1330,64 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
     int64_t *boff = reinterpret_cast<int64_t *>(sorted == kb[0] ? kb[1] : kb[0]);
     const bool table = rows.NB <= SP_TILE / 2;
     if (table) {
-#pragma unroll 4
+        // every bucket start of the thread's slots found first, then all
+        // their base loads issued together (index 0 where no bucket starts;
+        // the positions from c on hold hole or padding keys: the at most c
+        // items with a bucket sort first)
+        uint32_t key[SP_PT_IPT];
+        bool first[SP_PT_IPT];
+#pragma unroll
         for (int j = 0; j < SP_PT_IPT; ++j) {
             const int p = j * SP_PT_NT + t;
-            if (p >= c) continue;
-            const uint32_t bk = sorted[p] >> 12;
-            if (bk != 0xFFFFFu && (p == 0 || (sorted[p - 1] >> 12) != bk)) boff[bk] = bb[bk] + cp[bk] - p;
+            key[j] = sorted[p];
+            const uint32_t bk = key[j] >> 12;
+            first[j] = bk != 0xFFFFFu && (p == 0 || (sorted[p - 1] >> 12) != bk);
         }
-        __syncthreads();
-    }
-    if (table && part_inv) {
-        // the keys move to registers and the key buffer takes the inverse map
-        // (raw index -> partition position), stored to part_inv coalesced
-        // instead of one scattered store per item
-        uint32_t key[SP_PT_IPT];
+        int64_t b0[SP_PT_IPT];
+        int32_t c0[SP_PT_IPT];
 #pragma unroll
-        for (int j = 0; j < SP_PT_IPT; ++j) key[j] = sorted[j * SP_PT_NT + t];
+        for (int j = 0; j < SP_PT_IPT; ++j) {
+            const uint32_t bq = first[j] ? key[j] >> 12 : 0u;
+            b0[j] = bb[bq];
+            c0[j] = fl_ld32(cp, bq);
+        }
+#pragma unroll
+        for (int j = 0; j < SP_PT_IPT; ++j)
+            if (first[j]) boff[key[j] >> 12] = b0[j] + c0[j] - (j * SP_PT_NT + t);
         __syncthreads();
+        // every item's destination and value requested before the stores
+        // (raw index 0 for holes and padding)
+        int32_t dv[SP_PT_IPT];
+        float vv[SP_PT_IPT];
+#pragma unroll
+        for (int j = 0; j < SP_PT_IPT; ++j) {
+            const bool ok = j * SP_PT_NT + t < c && (key[j] >> 12) != 0xFFFFFu;
+            const uint32_t idx = ok ? key[j] & 4095u : 0u;
+            dv[j] = fl_ld32(raw_dst + i0, idx);
+            vv[j] = fl_ld32(raw_val + i0, idx);
+        }
+        if (!part_inv) {
+#pragma unroll
+            for (int j = 0; j < SP_PT_IPT; ++j) {
+                const int p = j * SP_PT_NT + t;  // striped: consecutive threads write consecutive slots
+                const uint32_t bk = key[j] >> 12;
+                if (p >= c || bk == 0xFFFFFu) continue;
+                const int64_t q = boff[bk] + p;
+                part_dst[q] = dv[j];
+                part_val[q] = vv[j];
+                if (part_tie) part_tie[q] = fl_ld32(raw_tie + i0, key[j] & 4095u);
+            }
+            return;
+        }
+        // the key buffer (every read of it precedes the barrier above) takes
+        // the inverse map (raw index -> partition position), stored to
+        // part_inv coalesced instead of one scattered store per item
         int32_t *inv_lds = reinterpret_cast<int32_t *>(const_cast<uint32_t *>(sorted));
         // rows of fewer than 2^pos_bits items store bucket << pos_bits | the
         // position within the row's partitioned items, so that the output
         // map needs no destination (sp_inv_encoded)
         const bool enc = sp_inv_encoded(rows, r, pos_bits);
         const int64_t rowpos0 = bb[0];
-        // every item's destination and value requested before the stores
-        int32_t dv[SP_PT_IPT];
-        float vv[SP_PT_IPT];
-#pragma unroll
-        for (int j = 0; j < SP_PT_IPT; ++j) {
-            const uint32_t idx = key[j] & 4095u;
-            const bool ok = j * SP_PT_NT + t < c && (key[j] >> 12) != 0xFFFFFu;
-            dv[j] = ok ? fl_ld32(raw_dst + i0, idx) : 0;
-            vv[j] = ok ? fl_ld32(raw_val + i0, idx) : 0.0f;
-        }
 #pragma unroll
         for (int j = 0; j < SP_PT_IPT; ++j) {
             const int p = j * SP_PT_NT + t;
@@ -1378,6 +1408,7 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
         for (uint32_t idx = (uint32_t)t; idx < (uint32_t)c; idx += SP_PT_NT) fl_st32(part_inv + i0, idx, inv_lds[idx]);
         return;
     }
+    // buckets beyond the table: each item's bucket start by binary search
 #pragma unroll 4
     for (int j = 0; j < SP_PT_IPT; ++j) {
         const int p = j * SP_PT_NT + t;  // striped: consecutive threads write consecutive slots
@@ -1385,18 +1416,13 @@ __global__ __launch_bounds__(SP_PT_NT) void k_sp_partition(int64_t R, SpRows row
         const uint32_t key = sorted[p];
         const uint32_t bk = key >> 12;
         if (bk == 0xFFFFFu) continue;  // hole
-        int64_t q;
-        if (table) {
-            q = boff[bk] + p;
-        } else {
-            int lo = 0, hi = p;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if ((sorted[mid] >> 12) < bk) lo = mid + 1;
-                else hi = mid;
-            }
-            q = bb[bk] + cp[bk] + (p - lo);
+        int lo = 0, hi = p;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if ((sorted[mid] >> 12) < bk) lo = mid + 1;
+            else hi = mid;
         }
+        const int64_t q = bb[bk] + cp[bk] + (p - lo);
         const uint32_t idx = key & 4095u;
         part_dst[q] = fl_ld32(raw_dst + i0, idx);
         part_val[q] = fl_ld32(raw_val + i0, idx);
