@@ -1194,8 +1194,22 @@ constexpr int SP_NWV = SP_NT / FL_WAVE;      // waves per workgroup
 constexpr int SP_SORT_IPT_MAX = 16;
 constexpr int SP_SORT_TAB = 2 * SP_ND * (SP_SORT_IPT_MAX * SP_NWV + 1);  // uint16 entries
 
-__device__ __forceinline__ uint32_t sp_lanes_below(unsigned long long m) {
-    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+// This lane's peers among the lanes set in m0: the lanes whose v agrees with
+// this lane's in bits [0, NBITS), as two 32-bit halves.  Per bit, sb = 0 or
+// -1 (the bit moved to the sign and shifted back) and the peers keep
+// ~(ballot ^ sb): five VALU operations per bit.
+template <int NBITS>
+__device__ __forceinline__ void sp_peers(uint32_t v, unsigned long long m0, uint32_t &mlo, uint32_t &mhi) {
+    static_assert(NBITS >= 1 && NBITS <= 32, "peer bits");
+    mlo = (uint32_t)m0;
+    mhi = (uint32_t)(m0 >> 32);
+#pragma unroll
+    for (int b = 0; b < NBITS; ++b) {
+        const int32_t sb = (int32_t)(v << (31 - b)) >> 31;
+        const unsigned long long bal = __builtin_amdgcn_ballot_w64(sb < 0);
+        mlo &= ~((uint32_t)bal ^ (uint32_t)sb);
+        mhi &= ~((uint32_t)(bal >> 32) ^ (uint32_t)sb);
+    }
 }
 
 template <int IPT, int NT = SP_NT, bool TWO_TABLES = true>
@@ -1222,17 +1236,14 @@ __device__ uint32_t *sp_block_sort(uint32_t *kin, uint32_t *kout, int lo_bit, in
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             key[j] = kin[j * NT + t];
-            const int d = (int)((key[j] >> shift) & (SP_ND - 1));
-            unsigned long long m = ~0ull;
-#pragma unroll
-            for (int b = 0; b < SP_RB; ++b) {
-                const unsigned long long bal = __ballot((d >> b) & 1);
-                m &= ((d >> b) & 1) ? bal : ~bal;
-            }
-            const uint32_t below = sp_lanes_below(m);
+            const uint32_t ks = key[j] >> shift;
+            uint32_t mlo, mhi;  // the lanes whose digit equals this lane's
+            sp_peers<SP_RB>(ks, ~0ull, mlo, mhi);
+            const int d = (int)(ks & (SP_ND - 1));
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
             dg[j] = (uint16_t)d;
             rk[j] = (uint16_t)below;
-            if (below == 0) tab[d * (SPAN + 1) + j * NWV + w] = (uint16_t)__popcll(m);
+            if (below == 0) tab[d * (SPAN + 1) + j * NWV + w] = (uint16_t)(__popc(mlo) + __popc(mhi));
         }
         __syncthreads();
         // exclusive scan in (digit, round, wave) order; the other buffer is cleared
@@ -1715,14 +1726,10 @@ __device__ __forceinline__ bool sp_wave_few(int64_t start, int64_t n, int32_t db
             const int x = d[j] & (SP_W - 1);
             sj = wpre[x >> 5] + __popc(bits[x >> 5] & ((1u << (x & 31)) - 1u));
         }
-        unsigned long long m = __ballot(valid);
-#pragma unroll
-        for (int b = 0; b < SP_WFEW_RB; ++b) {
-            const unsigned long long bal = __ballot((sj >> b) & 1);
-            m &= ((sj >> b) & 1) ? bal : ~bal;
-        }
-        const uint32_t below = sp_lanes_below(m);
-        if (valid && below == 0) tab[sj * (IPT + 1) + j] = (uint16_t)__popcll(m);
+        uint32_t mlo, mhi;
+        sp_peers<SP_WFEW_RB>((uint32_t)sj, __builtin_amdgcn_ballot_w64(valid), mlo, mhi);
+        const uint32_t below = __builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
+        if (valid && below == 0) tab[sj * (IPT + 1) + j] = (uint16_t)(__popc(mlo) + __popc(mhi));
         if (valid && raw_local) raw_local[start + (int64_t)j * FL_WAVE + lane] = sj;
         sl[j] = (uint8_t)sj;
         rk[j] = (uint8_t)below;
@@ -1911,14 +1918,11 @@ __device__ __forceinline__ void sp_few_one(int64_t start, int64_t n, int32_t dba
                 const int dl = pd[j] & (SP_W - 1);
                 sj = wpre[dl >> 5] + __popc(bits[dl >> 5] & ((1u << (dl & 31)) - 1u));
             }
-            unsigned long long m = __ballot(valid);
-#pragma unroll
-            for (int b = 0; b < SP_FEW_RB; ++b) {
-                const unsigned long long bal = __ballot((sj >> b) & 1);
-                m &= ((sj >> b) & 1) ? bal : ~bal;
-            }
-            const uint32_t below = sp_lanes_below(m);
-            if (valid && below == 0) tab[cur][sj * (SP_FEW_SPAN + 1) + j * SP_NWV + w] = (uint16_t)__popcll(m);
+            uint32_t mlo, mhi;
+            sp_peers<SP_FEW_RB>((uint32_t)sj, __builtin_amdgcn_ballot_w64(valid), mlo, mhi);
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(mhi, __builtin_amdgcn_mbcnt_lo(mlo, 0u));
+            if (valid && below == 0)
+                tab[cur][sj * (SP_FEW_SPAN + 1) + j * SP_NWV + w] = (uint16_t)(__popc(mlo) + __popc(mhi));
             if (valid && raw_local) fl_st32(raw_local + start, k, (int32_t)sj);
             sl[j] = (uint8_t)sj;
             rk[j] = (uint8_t)below;
