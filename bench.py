@@ -1236,14 +1236,15 @@ def main_sparse(args):
     achieved = step_bytes / (hop_ms * 1e-3) / 1e9 if hop_ms > 0 else 0.0
     warm_ms = sum(per_step[k] for k in HOP_KERNELS)
     warm = step_bytes / (warm_ms * 1e-3) / 1e9 if warm_ms > 0 else 0.0
-    traffic = measured_traffic(HOP_KERNELS)
+    # the committed counter summary is of the training step: no figure for eval
+    traffic = measured_traffic(HOP_KERNELS) if train else None
     kernel_rooflines = {}
     for k, b in item_kernel_bytes(plans).items():
         if cold_step.get(k, 0.0) > 0 and per_step.get(k, 0.0) > 0 and b > 0:
             a = b / (cold_step[k] * 1e-3) / 1e9
             aw = b / (per_step[k] * 1e-3) / 1e9
             kernel_rooflines[k] = {"achieved": a, "frac": a / HBM_PEAK_GBS, "algorithmic_bytes_per_step": b,
-                                   "ms_per_step": cold_step[k], "traffic": measured_traffic([k]),
+                                   "ms_per_step": cold_step[k], "traffic": measured_traffic([k]) if train else None,
                                    "warm": {"achieved": aw, "frac": aw / HBM_PEAK_GBS, "ms_per_step": per_step[k]}}
     dominant = max(per_step, key=lambda k: per_step[k])
     result = {
