@@ -38,6 +38,8 @@ def _torch_sum(b, e, v, B, E, dev):
     (16, 3, 5000, 20000, 1),
     (8, 1, 1000, 3000, 2),      # one channel: a copy
     (8, 5, 200, 6000, 3),       # dense: nearly every (b, e) in all channels
+    (4, 8, 400, 9000, 5),       # many channels: every entry ranked in seven other rows
+    (6, 10, 300, 12000, 6),
     (256, 3, 4_600_000, 3_000_000, 4),
 ])
 def test_channel_sum_bitexact(B, L, E, n, seed):
