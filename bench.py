@@ -129,17 +129,22 @@ def _pmc_counters(path):
         return sorted({row.get("Counter_Name") or row.get("Counter-Name") for row in csv.DictReader(f)})
 
 
-def counter_table(out_path, csvs):
-    """Per sparse hop kernel: dispatches and the mean over its dispatches
-    of every counter of the passes (a dispatch's value summed over its
-    rows), with two derived columns where their counters were collected:
-    LDS bank-conflict cycles per LDS-active cycle and VALU instructions per
-    wave."""
+def counter_table(out_path, csvs, config=5):
+    """Per hop kernel of the workload (C5: the sparse hop's; C2 / C4: every
+    kernel of this library in the run): dispatches and the mean over its
+    dispatches of every counter of the passes (a dispatch's value summed
+    over its rows), with two derived columns where their counters were
+    collected: LDS bank-conflict cycles per LDS-active cycle and VALU
+    instructions per wave."""
     cols = {}
     for path in csvs:
         for c in _pmc_counters(path):
             cols[c] = _pmc_per_kernel(path, c)
-    names = [k for k in SPARSE_KERNELS if any(k in per for per in cols.values())]
+    if config == 5:
+        names = [k for k in SPARSE_KERNELS if any(k in per for per in cols.values())]
+    else:
+        names = sorted({k for per in cols.values() for k in per if k.startswith("k_")})
+    title, run = PMC_WORKLOADS[config]
     counters = sorted(cols)
     head = ["kernel", "dispatches"] + counters
     derived = []
@@ -150,13 +155,14 @@ def counter_table(out_path, csvs):
     if "SQ_INSTS_VALU" in cols and "SQ_WAVES" in cols:
         derived.append(("VALU insts / wave", "SQ_INSTS_VALU", "SQ_WAVES"))
     head += [d[0] for d in derived]
-    lines = ["# Counters per dispatch of the sparse hop kernels, C5 sparse training step", "",
+    lines = ["# Counters per dispatch of the %s kernels, %s"
+             % ("sparse hop" if config == 5 else "dense hop", title), "",
              "One rocprofv3 pass per counter set over `--counter-steps` (from the repo root, on one MI355X), "
              "then this table:", ""]
     for i, path in enumerate(csvs):
         lines.append("    cd /tmp && rocprofv3 --pmc %s --output-format csv -d /tmp/p_%d -o run -- "
-                     "python3 <repo>/bench.py --counter-steps 3" % (" ".join(_pmc_counters(path)), i))
-    lines += ["    python3 <repo>/bench.py --counter-table <this file> "
+                     "python3 <repo>/bench.py %s--counter-steps 3" % (" ".join(_pmc_counters(path)), i, run))
+    lines += ["    python3 <repo>/bench.py %s--counter-table <this file> " % run
               + " ".join("<pass %d counter_collection.csv>" % i for i in range(len(csvs))), "",
               "Means over each kernel's dispatches (all hops of the run); a dispatch's value is summed "
               "over the counter's instances.", ""]
@@ -376,7 +382,7 @@ def main():
     if args.counter_table:
         if len(args.counter_table) < 2:
             sys.exit("--counter-table needs OUT and at least one CSV")
-        return counter_table(args.counter_table[0], args.counter_table[1:])
+        return counter_table(args.counter_table[0], args.counter_table[1:], args.config)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(every (query, channel) row is independent, so batches would shard by query)",

@@ -159,3 +159,37 @@ def test_stats_table_default_batch_means(tmp_path):
     assert "<the run's kernel_trace.csv> 2" in text
     bench.stats_table(str(out), str(tmp_path / "stats.csv"), "T", "cmd")
     assert "default batch" not in out.read_text()
+
+
+def test_counter_table_dense(tmp_path):
+    # two dispatches of k_seg_max, one of k_pull_max, a torch kernel left out;
+    # the derived columns are means of per-dispatch sums
+    def rows(per):
+        out, d = [], 1
+        for name, vals in per.items():
+            for counter, v in vals:
+                out.append({"Dispatch_Id": str(d), "Kernel_Name": name, "Counter_Name": counter,
+                            "Counter_Value": str(v)})
+                d += 1
+        return out
+    p0 = rows({"void fl::k_seg_max<true>(int*)": [("SQ_LDS_BANK_CONFLICT", 10.0), ("SQ_LDS_IDX_ACTIVE", 40.0)],
+               "void fl::k_seg_max<true>(long*)": [("SQ_LDS_BANK_CONFLICT", 30.0), ("SQ_LDS_IDX_ACTIVE", 40.0)],
+               "void at::native::reduce_kernel(int)": [("SQ_LDS_BANK_CONFLICT", 5.0), ("SQ_LDS_IDX_ACTIVE", 5.0)]})
+    p1 = rows({"void fl::k_pull_max(int*)": [("SQ_INSTS_VALU", 640.0), ("SQ_WAVES", 4.0)]})
+    _write_csv(tmp_path / "p0.csv", p0)
+    _write_csv(tmp_path / "p1.csv", p1)
+    out = tmp_path / "c.md"
+    bench.counter_table(str(out), [str(tmp_path / "p0.csv"), str(tmp_path / "p1.csv")], config=4)
+    text = out.read_text()
+    assert "dense hop kernels, C4 dense max step" in text
+    assert "bench.py --config 4 --counter-steps 3" in text
+    assert "reduce_kernel" not in text
+    rows_ = {ln.split("|")[1].strip(): [c.strip() for c in ln.split("|")[2:-1]]
+             for ln in text.splitlines() if ln.startswith("| k_")}
+    assert set(rows_) == {"k_seg_max", "k_pull_max"}
+    head = [c.strip() for c in [ln for ln in text.splitlines() if ln.startswith("| kernel")][0].split("|")[1:-1]]
+    seg = dict(zip(head[1:], rows_["k_seg_max"]))
+    assert seg["dispatches"] == "2" and seg["SQ_LDS_BANK_CONFLICT"] == "20"
+    assert seg["LDS conflict / SQ_LDS_IDX_ACTIVE"] == "0.500"
+    pull = dict(zip(head[1:], rows_["k_pull_max"]))
+    assert pull["VALU insts / wave"] == "160.000"
