@@ -30,7 +30,7 @@ __device__ __forceinline__ void topc_select(const int *hist, int need, int *lds_
 }
 
 // Loads of TOPC_U elements per thread are issued together before their use.
-constexpr int TOPC_U = 8;
+constexpr int TOPC_U = 16;
 
 #define TOPC_FOR_ROW(BODY)                                                        \
     for (int64_t base_ = 0; base_ < E; base_ += (int64_t)TOPC_NT * TOPC_U) {      \
