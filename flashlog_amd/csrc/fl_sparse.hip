@@ -2753,20 +2753,33 @@ __global__ void k_pack_bool_bits(const uint8_t *__restrict__ mask, int64_t n, ui
     if (lane == 32 && w0 + 1 < nw) bits[w0 + 1] = (uint32_t)(b >> 32);
 }
 
+// Wave per OB_U consecutive 64-position rounds: every round's order entry,
+// then every bitmap word, requested before the first is used.
+constexpr int OB_U = 4;
+
 __global__ void k_order_bits(const uint32_t *__restrict__ edge_bits, const int32_t *__restrict__ order, int64_t n,
                              uint32_t *__restrict__ bits) {
-    const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    bool on = false;
-    if (p < n) {
-        const int32_t e = order[p];
-        on = e >= 0 && e < n && ((edge_bits[e >> 5] >> (e & 31)) & 1u);
-    }
-    const uint64_t b = __ballot(on);
     const int lane = fl_lane();
-    const int64_t w0 = (p - lane) >> 5;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / FL_WAVE;
+    const int64_t p0 = wave * (OB_U * FL_WAVE) + lane;
+    int32_t e[OB_U];
+#pragma unroll
+    for (int u = 0; u < OB_U; ++u) {
+        const int64_t p = p0 + u * FL_WAVE;
+        e[u] = p < n ? order[p] : -1;
+    }
+    uint32_t wd[OB_U];
+#pragma unroll
+    for (int u = 0; u < OB_U; ++u) wd[u] = e[u] >= 0 && e[u] < n ? edge_bits[e[u] >> 5] : 0u;
     const int64_t nw = (n + 31) >> 5;
-    if (lane == 0 && w0 < nw) bits[w0] = (uint32_t)b;
-    if (lane == 32 && w0 + 1 < nw) bits[w0 + 1] = (uint32_t)(b >> 32);
+#pragma unroll
+    for (int u = 0; u < OB_U; ++u) {
+        const bool on = e[u] >= 0 && e[u] < n && ((wd[u] >> (e[u] & 31)) & 1u);
+        const uint64_t b = __ballot(on);
+        const int64_t w0 = (p0 + u * FL_WAVE - lane) >> 5;
+        if (lane == 0 && w0 < nw) bits[w0] = (uint32_t)b;
+        if (lane == 32 && w0 + 1 < nw) bits[w0 + 1] = (uint32_t)(b >> 32);
+    }
 }
 
 // Entry order validation: every entry visited exactly once (else error 1).
@@ -3880,7 +3893,8 @@ int fl_mask_order_bits(void *stream, const uint8_t *mask, const int32_t *order, 
     hipStream_t st = (hipStream_t)stream;
     const unsigned g = (unsigned)((n + 255) / 256);
     FL_LAUNCH("k_pack_bool_bits", k_pack_bool_bits, dim3(g), dim3(256), 0, st, mask, n, edge_bits);
-    FL_LAUNCH("k_order_bits", k_order_bits, dim3(g), dim3(256), 0, st, edge_bits, order, n, bits);
+    FL_LAUNCH("k_order_bits", k_order_bits, dim3((unsigned)((n + 256 * OB_U - 1) / (256 * OB_U))), dim3(256), 0, st,
+              edge_bits, order, n, bits);
     return fl_check_launch("mask_order_bits");
 }
 
